@@ -1,0 +1,171 @@
+"""Benchmark of the fused CD-SSM chunkwise delta-rule scan on one MI355X.
+
+Default workload (the metric's headline shape): forward
+scan, B=8 H=16 L=4096 D=Q=64 N=2, bf16 q/k/v/gates, fp32 state, synthetic
+inputs drawn as the configuration text specifies (seed 0), zero initial state.
+One step = one forward scan over the batch (three kernel launches).
+
+Prints ONE JSON line with the metric, the roofline of the scan against HBM
+and a CPU baseline: the fp32 CPU restatement of the reference algorithm
+(oracle/cdssm_oracle.py) timed on this host's cores on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "cayley-delta-state-space-model_amd")
+for _p in (ROOT, PKG_DIR):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor peak
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="C1", choices=["C1", "C3"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-batches", type=int, default=1)
+    return ap.parse_args()
+
+
+def cpu_baseline(cfg, x, batches):
+    """Time the fp32 oracle (CPU restatement of ops.py's R-mode scan) on
+    `batches` batch rows of the workload, all heads, full length."""
+    import torch
+    from oracle import cdssm_oracle as o
+
+    n = os.cpu_count() or 1
+    torch.set_num_threads(n)
+    sl = {k: (t[:batches].float() if isinstance(t, torch.Tensor) and t.dim() >= 3 else t)
+          for k, t in x.items()}
+    sl["alpha"], sl["omega"] = x["alpha"].float(), x["omega"].float()
+    h0 = None if x["h0"] is None else x["h0"][:batches].float()
+
+    def once():
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            o.fused_scan(sl["q"], sl["k"], sl["v"], sl["beta"], sl["sel_C"], sl["dt"], sl["r"],
+                         sl["alpha"], sl["omega"], x["c"], h0=h0)
+        return time.perf_counter() - t0
+
+    once()  # warm-up
+    times = [once() for _ in range(3)]
+    med = statistics.median(times)
+    tokens = batches * cfg.L
+    return {"value": tokens / med, "unit": "tokens/s", "cores": n, "kind": "port",
+            "sample": (f"oracle fp32 R-mode fused scan (torch CPU, {n} threads) on {batches} of "
+                       f"{cfg.B} batch rows x all {cfg.H} heads x L={cfg.L}; median of 3 after 1 warm-up; "
+                       f"{med:.3f} s per sample")}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+    from cdssm_hip.scan import PreparedForward
+    from cdssm_hip.workloads import CONFIGS, draw_inputs, scan_bytes
+
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    x = draw_inputs(cfg, seed=0)
+    g = {n: (t.to(dev) if isinstance(t, torch.Tensor) else t) for n, t in x.items()}
+    run = PreparedForward(g["q"], g["k"], g["v"], g["beta"], g["sel_C"], g["dt"], g["r"], g["alpha"],
+                          g["omega"], g["c"], h0=g["h0"])
+
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+
+    # timed region: exactly `steps` back-to-back forward scans
+    stream = torch.cuda.current_stream(dev)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        run()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    ms_per_step = gpu_ms / args.steps
+
+    # per-launch durations (events around each call on the launch stream)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(2 * 50)]
+    for i in range(50):
+        evs[2 * i].record(stream)
+        run()
+        evs[2 * i + 1].record(stream)
+    torch.cuda.synchronize()
+    per_call = sorted(evs[2 * i].elapsed_time(evs[2 * i + 1]) for i in range(50))
+    call_ms = statistics.median(per_call)
+
+    # cold: last-level cache (256 MB MALL) flushed before each call
+    flush = torch.empty(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+    cold = []
+    for i in range(10):
+        flush.fill_(float(i))
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        run()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        cold.append(e0.elapsed_time(e1))
+    cold_ms = statistics.median(cold)
+    del flush
+
+    tokens = cfg.B * cfg.L
+    alg = scan_bytes(cfg)["fwd"]
+    achieved = alg / (call_ms * 1e-3) / 1e9
+    out = {
+        "metric": "scan tokens/sec (fwd), B8 H16 L4096 D64 bf16" if args.config == "C1"
+                  else "scan tokens/sec (fwd), B1 H32 L65536 D64 bf16",
+        "value": tokens / (ms_per_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (BASELINE config draws, seed 0)",
+        "config": {"workload": f"{cfg.name} forward scan", "B": cfg.B, "H": cfg.H, "L": cfg.L,
+                   "D": cfg.D, "Q": cfg.D, "N": cfg.N, "inputs": "bf16", "state": "fp32",
+                   "h0": cfg.h0_std > 0, "global_batch": cfg.B, "seq_len": cfg.L},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "basis": (f"algorithmic {alg / 1e6:.2f} MB per scan call "
+                               f"(272 B per token-head) / median event-timed call {call_ms * 1e3:.2f} us; "
+                               f"one call = summary + carry + main kernels")},
+        "cold_ms_per_call": cold_ms,
+        "cold_frac": alg / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "wall_s_timed": wall,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(cfg, x, args.cpu_sample_batches)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,10 @@
+"""MI355X-native (gfx950 HIP) CD-SSM chunkwise delta-rule scan.
+
+Host side of the HIP library ``libcdssm_hip.so``: the fused scan op and the
+reference-compatible autograd Functions.  Importing this package does not
+touch the GPU; the library is loaded on first use and its absence is an error.
+"""
+
+from .scan import chunkwise_delta_scan, chunkwise_delta_scan_fwd  # noqa: F401
+
+__all__ = ["chunkwise_delta_scan", "chunkwise_delta_scan_fwd"]

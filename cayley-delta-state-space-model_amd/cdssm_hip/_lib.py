@@ -1,0 +1,81 @@
+"""ctypes binding of ``libcdssm_hip.so``, the C-ABI of the HIP kernels.
+
+The library is built in-tree (``__graft_entry__.build()``) next to this file.
+There is no fallback: if the library is missing or fails to load, every op
+raises ``RuntimeError`` naming the path it looked for.  Entry points take raw
+device pointers, int64 sizes, fp32 scalars and a ``hipStream_t``; they return
+0 on success and a negative status otherwise, with the message available from
+``cdssm_last_error()``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional
+
+import torch
+
+LIB_NAME = "libcdssm_hip.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int
+_F32 = ctypes.c_float
+
+# name -> (restype, argtypes).  Mirrors include/cdssm_hip.h.
+SIGNATURES = {
+    "cdssm_abi_version": (_I32, []),
+    "cdssm_last_error": (ctypes.c_char_p, []),
+    "cdssm_fused_scan_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _I64]),
+    "cdssm_fused_scan_fwd": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _P,
+                                    _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+}
+
+_lock = threading.Lock()
+_lib: Optional[ctypes.CDLL] = None
+_load_error: Optional[str] = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library once; raise RuntimeError if it is absent or broken."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            _load_error = (f"{LIB_PATH} not found: build it with "
+                           f"`python -c 'import __graft_entry__ as g; g.build()'` from the repo root")
+            raise RuntimeError(_load_error)
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    msg = load().cdssm_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(status: int, op: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"{op} failed (status {status}): {last_error()}")
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1}

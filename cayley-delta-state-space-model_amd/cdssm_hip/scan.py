@@ -1,0 +1,134 @@
+"""Fused chunkwise delta-rule scan (the metric op), host side.
+
+``chunkwise_delta_scan`` runs the scan-level CD-SSM path in one C-ABI call
+(``cdssm_fused_scan_fwd``): Cayley/gated dynamics from (dt, r, alpha, omega),
+VP-scaled values, the reference's three-pass R-mode scan (intra-chunk,
+inter-chunk carry, exact correction; ssd.py:39-111) and the sel_C-gated
+readout (block.py:208-211).  It validates on the host, allocates the outputs
+and the workspace with torch, and launches on torch's current stream.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+Tensor = torch.Tensor
+
+PER_TOKEN = ("q", "k", "v", "beta", "sel_C", "dt", "r")
+
+
+def _validate(q, k, v, beta, sel_C, dt, r, alpha, omega, h0, chunk_size):
+    named = dict(q=q, k=k, v=v, beta=beta, sel_C=sel_C, dt=dt, r=r, alpha=alpha, omega=omega)
+    for n, t in named.items():
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{n} must be a tensor")
+    dev = q.device
+    if dev.type != "cuda":
+        raise RuntimeError("chunkwise_delta_scan runs on the GPU only: inputs must be on a cuda device")
+    for n, t in named.items():
+        if t.device != dev:
+            raise RuntimeError(f"{n} is on {t.device}, expected {dev}")
+    if q.dim() != 4:
+        raise ValueError(f"q must be (B, L, H, D), got {tuple(q.shape)}")
+    B, L, H, D = q.shape
+    N = v.shape[-1] if v.dim() == 4 else -1
+    shapes = dict(q=(B, L, H, D), k=(B, L, H, D), v=(B, L, H, N), beta=(B, L, H), sel_C=(B, L, H),
+                  dt=(B, L, H), r=(B, L, H))
+    for n, shp in shapes.items():
+        if tuple(named[n].shape) != shp:
+            raise ValueError(f"{n} has shape {tuple(named[n].shape)}, expected {shp}")
+    dtype = q.dtype
+    if dtype not in _lib.DTYPE_CODE:
+        raise TypeError(f"inputs must be float32 or bfloat16, got {dtype}")
+    for n in PER_TOKEN:
+        if named[n].dtype != dtype:
+            raise TypeError(f"{n} has dtype {named[n].dtype}, expected {dtype} (same as q)")
+    for n in ("alpha", "omega"):
+        t = named[n]
+        if t.dtype != torch.float32 or tuple(t.shape) != (H,):
+            raise ValueError(f"{n} must be float32 of shape ({H},), got {t.dtype} {tuple(t.shape)}")
+    if N != 2:
+        raise ValueError(f"the fused scan supports N = 2 (one complex pair per head), got N = {N}")
+    if D not in (64, 128):
+        raise ValueError(f"head_dim D must be 64 or 128, got {D}")
+    Q = D if chunk_size is None else int(chunk_size)
+    if not 1 <= Q <= 128:
+        raise ValueError(f"chunk_size must be in [1, 128], got {Q}")
+    if h0 is not None:
+        if h0.dtype != torch.float32 or tuple(h0.shape) != (B, H, N, D) or h0.device != dev:
+            raise ValueError(f"h0 must be float32 ({B}, {H}, {N}, {D}) on {dev}")
+    return B, L, H, D, N, Q, dtype
+
+
+def chunkwise_delta_scan_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_C: Tensor, dt: Tensor,
+                             r: Tensor, alpha: Tensor, omega: Tensor, c: float,
+                             h0: Optional[Tensor] = None, chunk_size: Optional[int] = None
+                             ) -> Tuple[Tensor, Tensor, Tensor]:
+    """Forward only.  Returns (y (B,L,H,2), h_final (B,H,2,D) fp32, carry).
+
+    ``carry`` is the workspace: the complex fp32 state entering every chunk,
+    shape (B, NC, H, D, 2) followed by the per-chunk rotation products.
+    """
+    B, L, H, D, N, Q, dtype = _validate(q, k, v, beta, sel_C, dt, r, alpha, omega, h0, chunk_size)
+    lib = _lib.load()
+    ins = [t.contiguous() for t in (q, k, v, beta, sel_C, dt, r, alpha, omega)]
+    h0c = h0.contiguous() if h0 is not None else None
+    dev = q.device
+    y = torch.empty(B, L, H, N, dtype=dtype, device=dev)
+    h_final = torch.empty(B, H, N, D, dtype=torch.float32, device=dev)
+    nbytes = lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, N, Q)
+    if nbytes <= 0:
+        raise RuntimeError(f"cdssm_fused_scan_workspace_bytes rejected the shape ({nbytes})")
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    st = lib.cdssm_fused_scan_fwd(_lib.DTYPE_CODE[dtype], *[_lib.ptr(t) for t in ins[:7]],
+                                  _lib.ptr(ins[7]), _lib.ptr(ins[8]), float(c), _lib.ptr(h0c),
+                                  _lib.ptr(y), _lib.ptr(h_final), _lib.ptr(ws), B, L, H, D, N, Q,
+                                  _lib.stream_of(dev))
+    _lib.check(st, "cdssm_fused_scan_fwd")
+    return y, h_final, ws
+
+
+def chunkwise_delta_scan(q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0=None, chunk_size=None):
+    """y (B,L,H,2) and the final R-mode state (B,H,2,D) of the fused scan."""
+    y, h_final, _ = chunkwise_delta_scan_fwd(q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0, chunk_size)
+    return y, h_final
+
+
+class PreparedForward:
+    """A forward scan with inputs, outputs and workspace bound once.
+
+    Calling it re-launches the three kernels on torch's current stream with no
+    validation, allocation or tensor creation on the host: the launch path for
+    serving loops, graph capture and timing.  The bound tensors must stay alive
+    and keep their shapes.
+    """
+
+    def __init__(self, q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0=None, chunk_size=None):
+        B, L, H, D, N, Q, dtype = _validate(q, k, v, beta, sel_C, dt, r, alpha, omega, h0, chunk_size)
+        for n, t in dict(q=q, k=k, v=v, beta=beta, sel_C=sel_C, dt=dt, r=r, alpha=alpha, omega=omega).items():
+            if not t.is_contiguous():
+                raise ValueError(f"{n} must be contiguous for a prepared scan")
+        if h0 is not None and not h0.is_contiguous():
+            raise ValueError("h0 must be contiguous for a prepared scan")
+        self._lib = _lib.load()
+        dev = q.device
+        self.inputs = (q, k, v, beta, sel_C, dt, r, alpha, omega, h0)
+        self.y = torch.empty(B, L, H, N, dtype=dtype, device=dev)
+        self.h_final = torch.empty(B, H, N, D, dtype=torch.float32, device=dev)
+        nbytes = self._lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, N, Q)
+        self.workspace = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+        self.shape = (B, L, H, D, N, Q)
+        self.device = dev
+        self._args = (_lib.DTYPE_CODE[dtype], *[_lib.ptr(t) for t in self.inputs[:9]], float(c),
+                      _lib.ptr(h0), _lib.ptr(self.y), _lib.ptr(self.h_final), _lib.ptr(self.workspace),
+                      B, L, H, D, N, Q)
+
+    def __call__(self):
+        st = self._lib.cdssm_fused_scan_fwd(*self._args, _lib.stream_of(self.device))
+        if st != 0:
+            _lib.check(st, "cdssm_fused_scan_fwd")
+        return self.y, self.h_final

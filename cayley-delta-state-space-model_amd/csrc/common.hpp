@@ -1,0 +1,155 @@
+// Shared device helpers for the CD-SSM scan kernels (gfx950, wave64).
+//
+// Conventions used by every kernel in this library:
+//   * tensors are contiguous, token-major (B, L, H, ...), as in the reference's
+//     ops.py contracts;
+//   * bf16 values travel as raw 16-bit patterns (uint16_t) and are widened to
+//     fp32 by a shift; every state and every accumulation is fp32;
+//   * a complex pair (re, im) is stored interleaved, and the stored transition
+//     A_bar = conj(mu) * scale multiplies a state row pair as a complex scalar
+//     (reference: intra_chunk_scan.cu:151-162, cayley_math.cuh:20-24).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cdssm {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// bf16 <-> fp32
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_lo(uint32_t packed) { return __uint_as_float(packed << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t packed) { return __uint_as_float(packed & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t x) { return __uint_as_float(uint32_t(x) << 16); }
+
+// Round-to-nearest-even narrowing; NaN stays NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+// Element type tags: loads of one element and stores of one element.
+struct BF16 {
+  using raw = uint16_t;
+  static constexpr int bytes = 2;
+  __device__ __forceinline__ static float load(const raw* p) { return bf16_to_f32(*p); }
+  __device__ __forceinline__ static void store(raw* p, float v) { *p = f32_to_bf16(v); }
+};
+struct F32 {
+  using raw = float;
+  static constexpr int bytes = 4;
+  __device__ __forceinline__ static float load(const raw* p) { return *p; }
+  __device__ __forceinline__ static void store(raw* p, float v) { *p = v; }
+};
+
+// A 16-byte vector of DPL = 16 / bytes elements, loaded with one 128-bit load
+// and widened to fp32 on use.
+template <typename T> struct Vec16;
+template <> struct Vec16<BF16> {
+  static constexpr int n = 8;
+  __device__ __forceinline__ static void unpack(const uint4& r, float (&o)[8]) {
+    o[0] = bf16_lo(r.x); o[1] = bf16_hi(r.x);
+    o[2] = bf16_lo(r.y); o[3] = bf16_hi(r.y);
+    o[4] = bf16_lo(r.z); o[5] = bf16_hi(r.z);
+    o[6] = bf16_lo(r.w); o[7] = bf16_hi(r.w);
+  }
+};
+template <> struct Vec16<F32> {
+  static constexpr int n = 4;
+  __device__ __forceinline__ static void unpack(const uint4& r, float (&o)[4]) {
+    o[0] = __uint_as_float(r.x); o[1] = __uint_as_float(r.y);
+    o[2] = __uint_as_float(r.z); o[3] = __uint_as_float(r.w);
+  }
+};
+
+__device__ __forceinline__ uint4 ld16(const void* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+// ---------------------------------------------------------------------------
+// Lane-group all-reduce (sum) over G consecutive lanes, G in {1,2,4,...,64}.
+// DPP quad permutes and row mirrors stay inside a 16-lane row; the 32-lane
+// stage uses a ds_swizzle xor; the 64-lane stage combines the two halves
+// through readlane.  Every lane of the group ends with the group sum.
+// ---------------------------------------------------------------------------
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+template <int G>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "group size");
+  if constexpr (G >= 2) x += dpp<0xB1>(x);     // quad_perm [1,0,3,2]: lane ^ 1
+  if constexpr (G >= 4) x += dpp<0x4E>(x);     // quad_perm [2,3,0,1]: lane ^ 2
+  if constexpr (G >= 8) x += dpp<0x141>(x);    // row_half_mirror: other quad of the 8
+  if constexpr (G >= 16) x += dpp<0x140>(x);   // row_mirror: other half of the row
+  if constexpr (G >= 32) x += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));
+  if constexpr (G >= 64) {
+    const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+    const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+    x = lo + hi;
+  }
+  return x;
+}
+
+// ---------------------------------------------------------------------------
+// Scan-level Cayley dynamics for one eigenvalue pair (reference:
+// dynamics_fused.cu:109-131, cayley_math.cuh:51-99):
+//   tau = dt/2, ta = tau*max(alpha,0), tw = tau*omega,
+//   mu  = ((1 - ta^2 - tw^2) + i 2 tw) / ((1+ta)^2 + tw^2 + 1e-6),
+//   E   = max(((1-ta)^2 + tw^2) / ((1+ta)^2 + tw^2 + 1e-6), 1e-8),
+//   A   = conj(mu) * E^((c r - 1)/2),
+//   vp  = min(sqrt(max(1 - E^(c r), 1e-6)), 1).
+// Powers use the hardware base-2 log/exp (v_log_f32 / v_exp_f32); E >= 1e-8
+// keeps the log argument normal.
+// ---------------------------------------------------------------------------
+
+struct Transition {
+  float ar, ai, vp;
+};
+
+__device__ __forceinline__ Transition cayley_gated(float dt, float r, float alpha, float omega, float c) {
+  const float tau = 0.5f * dt;
+  const float ta = tau * fmaxf(alpha, 0.0f);
+  const float tw = tau * omega;
+  const float tw2 = tw * tw;
+  const float opa = 1.0f + ta;
+  const float oma = 1.0f - ta;
+  const float den = opa * opa + tw2 + 1e-6f;
+  const float inv = 1.0f / den;
+  const float mur = (1.0f - ta * ta - tw2) * inv;
+  const float mui = (2.0f * tw) * inv;
+  const float E = fmaxf((oma * oma + tw2) * inv, 1e-8f);
+  const float cr = c * r;
+  const float lE = __builtin_amdgcn_logf(E);
+  const float scale = __builtin_amdgcn_exp2f(0.5f * (cr - 1.0f) * lE);
+  const float eff = __builtin_amdgcn_exp2f(cr * lE);
+  Transition o;
+  o.ar = mur * scale;
+  o.ai = -mui * scale;
+  o.vp = fminf(sqrtf(fmaxf(1.0f - eff, 1e-6f)), 1.0f);
+  return o;
+}
+
+}  // namespace cdssm
+
+// ---------------------------------------------------------------------------
+// Host-side status plumbing shared by the C-ABI entry points.
+// ---------------------------------------------------------------------------
+
+namespace cdssm_host {
+void set_error(const char* fmt, ...);
+int check_launch(const char* op);
+}  // namespace cdssm_host
+
+// Status codes returned by every entry point.
+#define CDSSM_OK 0
+#define CDSSM_EINVAL (-1)
+#define CDSSM_EHIP (-2)

@@ -1,0 +1,84 @@
+"""The C-ABI library on the CPU host: it loads, exports every symbol the header
+declares, and its host-side argument checks reject bad calls before any GPU
+work (these calls launch nothing, so they run without a GPU)."""
+
+import os
+import re
+
+import pytest
+
+from cdssm_hip import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADERS = [os.path.join(ROOT, "include", f) for f in os.listdir(os.path.join(ROOT, "include"))
+           if f.endswith(".h")]
+
+
+def declared_functions():
+    names = set()
+    for h in HEADERS:
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b(cdssm_[a-z0-9_]+)\s*\(", text):
+            names.add(m.group(1))
+    return sorted(names)
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert "cdssm_fused_scan_fwd" in names and "cdssm_last_error" in names
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+    assert lib.cdssm_abi_version() >= 1
+
+
+def test_binding_signatures_cover_the_header():
+    assert set(declared_functions()) <= set(_lib.SIGNATURES), \
+        "every declared entry point needs a ctypes signature"
+
+
+def _fused_call(lib, **over):
+    args = dict(dtype=1, q=16, k=16, v=16, beta=16, sel_c=16, dt=16, r=16, alpha=16, omega=16, c=1.0,
+                h0=None, y=16, h_final=16, ws=16, B=1, L=64, H=2, D=64, N=2, chunk=64, stream=None)
+    args.update(over)
+    return lib.cdssm_fused_scan_fwd(*args.values())
+
+
+@pytest.mark.parametrize("bad,msg", [
+    (dict(dtype=7), "dtype"),
+    (dict(N=4), "state_dim"),
+    (dict(D=96), "head_dim"),
+    (dict(chunk=0), "chunk"),
+    (dict(chunk=256), "chunk"),
+    (dict(B=0), "positive"),
+    (dict(q=None), "null"),
+    (dict(k=8), "aligned"),
+])
+def test_fused_fwd_rejects_invalid_arguments_without_launching(bad, msg):
+    lib = _lib.load()
+    st = _fused_call(lib, **bad)
+    assert st == -1
+    assert msg in _lib.last_error()
+
+
+def test_workspace_size_formula():
+    lib = _lib.load()
+    B, L, H, D, N, Q = 8, 4096, 16, 64, 2, 64
+    NC = L // Q
+    assert lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, N, Q) == (B * NC * H * D + B * NC * H) * 8
+    assert lib.cdssm_fused_scan_workspace_bytes(B, 100, H, D, N, Q) == (B * 2 * H * D + B * 2 * H) * 8
+    assert lib.cdssm_fused_scan_workspace_bytes(0, L, H, D, N, Q) == -1
+
+
+def test_product_path_has_no_cpu_fallback():
+    """The scan raises on CPU tensors instead of computing anything on the host."""
+    import torch
+    from cdssm_hip import chunkwise_delta_scan
+    x = torch.zeros(1, 64, 2, 64)
+    s = torch.zeros(1, 64, 2)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        chunkwise_delta_scan(x, x, torch.zeros(1, 64, 2, 2), s, s, s, s, torch.zeros(2), torch.zeros(2), 1.0)
