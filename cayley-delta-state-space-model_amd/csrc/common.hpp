@@ -47,29 +47,43 @@ struct F32 {
   __device__ __forceinline__ static void store(raw* p, float v) { *p = v; }
 };
 
-// A 16-byte vector of DPL = 16 / bytes elements, loaded with one 128-bit load
-// and widened to fp32 on use.
-template <typename T> struct Vec16;
-template <> struct Vec16<BF16> {
-  static constexpr int n = 8;
-  __device__ __forceinline__ static void unpack(const uint4& r, float (&o)[8]) {
-    o[0] = bf16_lo(r.x); o[1] = bf16_hi(r.x);
-    o[2] = bf16_lo(r.y); o[3] = bf16_hi(r.y);
-    o[4] = bf16_lo(r.z); o[5] = bf16_hi(r.z);
-    o[6] = bf16_lo(r.w); o[7] = bf16_hi(r.w);
-  }
-};
-template <> struct Vec16<F32> {
-  static constexpr int n = 4;
-  __device__ __forceinline__ static void unpack(const uint4& r, float (&o)[4]) {
-    o[0] = __uint_as_float(r.x); o[1] = __uint_as_float(r.y);
-    o[2] = __uint_as_float(r.z); o[3] = __uint_as_float(r.w);
-  }
-};
+// A lane's slice of one row: DPL consecutive elements, loaded with a single
+// 8- or 16-byte load into W = DPL * bytes / 4 dwords and widened on use.
+template <typename T, int DPL>
+struct RowVec {
+  static constexpr int W = DPL * T::bytes / 4;
+  static_assert(W == 2 || W == 4, "a lane slice is one 8- or 16-byte load");
+  uint32_t u[W];
 
-__device__ __forceinline__ uint4 ld16(const void* p) {
-  return *reinterpret_cast<const uint4*>(p);
-}
+  __device__ __forceinline__ void load(const typename T::raw* p) {
+    if constexpr (W == 4) {
+      const uint4 v = *reinterpret_cast<const uint4*>(p);
+      u[0] = v.x; u[1] = v.y; u[2] = v.z; u[3] = v.w;
+    } else {
+      const uint2 v = *reinterpret_cast<const uint2*>(p);
+      u[0] = v.x; u[1] = v.y;
+    }
+  }
+  // Opaque copy: keeps the compiler from merging a prefetch ring's initial
+  // loads with the in-loop loads into one load at the loop head (which would
+  // undo the software pipelining).  Waits for this slice's load.
+  __device__ __forceinline__ void pin() {
+#pragma unroll
+    for (int i = 0; i < W; ++i) asm volatile("" : "+v"(u[i]));
+  }
+  __device__ __forceinline__ void unpack(float (&o)[DPL]) const {
+    if constexpr (T::bytes == 2) {
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        o[2 * i] = bf16_lo(u[i]);
+        o[2 * i + 1] = bf16_hi(u[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < W; ++i) o[i] = __uint_as_float(u[i]);
+    }
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Lane-group all-reduce (sum) over G consecutive lanes, G in {1,2,4,...,64}.

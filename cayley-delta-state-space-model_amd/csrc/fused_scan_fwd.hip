@@ -20,32 +20,40 @@
 // the complex scalar a_t commutes with the real projection I - beta k k^T.
 // That removes the per-element rotation from the correction update.
 //
-// Three launches, all on the caller's stream:
+// Four launches, all on the caller's stream:
 //   1. summary:  one pass over k, v, beta, dt, r per chunk -> (F_k = z_{Q-1}, G_k)
-//   2. carry:    per (b, h, d) scan of s_{k+1} = G_k s_k + F_k over chunks, in
-//                three phases (segment fold, segment prefix, segment replay) so
-//                the serial depth is ~2 NC/S + S instead of NC;
-//   3. main:     per chunk: z and c^ recurrences with the readout; writes y.
+//   2. fold:     per (b, h, segment of kSegLen chunks, d): compose the segment's
+//                carry maps -> (A_seg = prod G, X_seg = segment carry from 0)
+//   3. replay:   per (b, h, segment, d): state entering the segment from the
+//                earlier segments' (A, X), then replay the segment, writing the
+//                state entering every chunk over F_k, and the final state
+//   4. main:     per chunk: z and c^ recurrences with the readout; writes y.
 //
-// Work layout of passes 1 and 3: one wave64 holds HPW = 64/LPH heads of one
+// Work layout of passes 1 and 4: one wave64 holds HPW = 64/LPH heads of one
 // (b, chunk); each head is owned by LPH consecutive lanes, each lane holding
-// DPL = D/LPH consecutive state elements, so every q/k row is read with one
-// 16-byte load per lane and a head's 64..256-byte row is one contiguous
-// segment.  Dot products reduce over the LPH lanes with DPP.  The per-token
-// scalars (a, w, beta, sel_C) are computed once per token-head into LDS.
+// DPL = D/LPH consecutive state elements, so every q/k row slice is one 8- or
+// 16-byte load and a head's row is one contiguous segment.  Dot products
+// reduce over the LPH lanes with DPP.  The per-token scalars (a, w, beta,
+// sel_C) are computed once per token-head into LDS, one lane per token.
+// Row loads are unconditional (addresses clamped into the tile) and issued
+// kPrefetch tokens ahead, so the loop carries no branch and the memory waits
+// count only the oldest load.  Tokens past the end of a ragged last chunk are
+// inert steps (a = 1, w = 0, beta = 0).
 #include "common.hpp"
 
 namespace cdssm {
+
+constexpr int kPrefetch = 8;
+constexpr int kSegLen = 16;  // chunks per carry segment
 
 template <typename T, int D, int LPH>
 struct FusedCfg {
   static constexpr int DPL = D / LPH;
   static constexpr int HPW = kWave / LPH;
-  static_assert(DPL == Vec16<T>::n, "one 16-byte vector per lane per row");
   static_assert(HPW * LPH == kWave, "lane groups tile the wave");
 };
 
-constexpr int kPrefetch = 4;
+__host__ __device__ constexpr int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
 // Decode blockIdx.x -> (b, chunk, head group).
 struct ChunkTile {
@@ -67,10 +75,16 @@ __device__ __forceinline__ ChunkTile decode_tile(int L, int Q, int NC, int n_hg,
   return c;
 }
 
-// Stage per-token scalars of the tile into LDS.  Slot p = t*HPW + j.
-// Heads beyond H get an inert step (a = 1, w = 0, beta = 0).
-template <typename T, bool WITH_SELC>
-__device__ __forceinline__ void stage_scalars(const ChunkTile& tc, int H, int HPW,
+// Per-token scalars of the tile, one LDS array each, slot p = t*HPW + j.
+struct TileScalars {
+  float *ar, *ai, *wr, *wi, *b, *sc;
+};
+
+// Stage the tile's per-token scalars.  Lane = token; every lane first issues
+// all of its loads (addresses clamped into the tile), then computes.  Slots
+// for tokens in [nt, ntr) and heads >= H hold inert steps.
+template <typename T, int HPW, bool WITH_SELC>
+__device__ __forceinline__ void stage_scalars(const ChunkTile& tc, int H, int ntr,
                                               const typename T::raw* __restrict__ v,
                                               const typename T::raw* __restrict__ beta,
                                               const typename T::raw* __restrict__ sel_c,
@@ -78,30 +92,47 @@ __device__ __forceinline__ void stage_scalars(const ChunkTile& tc, int H, int HP
                                               const typename T::raw* __restrict__ r,
                                               const float* __restrict__ alpha,
                                               const float* __restrict__ omega, float c,
-                                              float* s_ar, float* s_ai, float* s_wr, float* s_wi,
-                                              float* s_b, float* s_sc) {
-  const int n = tc.nt * HPW;
-  for (int p = threadIdx.x; p < n; p += kWave) {
-    const int t = p / HPW;
-    const int hj = tc.hbase + (p - t * HPW);
-    float ar = 1.0f, ai = 0.0f, wr = 0.0f, wi = 0.0f, bb = 0.0f, sc = 0.0f;
-    if (hj < H) {
-      const int64_t e = (tc.row0 + t) * H + hj;
-      bb = T::load(beta + e);
-      const Transition tr = cayley_gated(T::load(dt + e), T::load(r + e), alpha[hj], omega[hj], c);
-      ar = tr.ar;
-      ai = tr.ai;
-      const float s = bb * tr.vp;
-      wr = s * T::load(v + 2 * e);
-      wi = s * T::load(v + 2 * e + 1);
-      if constexpr (WITH_SELC) sc = T::load(sel_c + e);
+                                              const TileScalars& s) {
+  for (int tl = 0; tl < ntr; tl += kWave) {
+    const int tt = tl + int(threadIdx.x);
+    const int t = min(tt, tc.nt - 1);
+    const int64_t rowe = (tc.row0 + t) * H;
+    float bb[HPW], dd[HPW], rr[HPW], v0[HPW], v1[HPW], sc[HPW];
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) {
+      const int64_t e = rowe + min(tc.hbase + j, H - 1);
+      bb[j] = T::load(beta + e);
+      dd[j] = T::load(dt + e);
+      rr[j] = T::load(r + e);
+      v0[j] = T::load(v + 2 * e);
+      v1[j] = T::load(v + 2 * e + 1);
+      sc[j] = WITH_SELC ? T::load(sel_c + e) : 0.0f;
     }
-    s_ar[p] = ar;
-    s_ai[p] = ai;
-    s_wr[p] = wr;
-    s_wi[p] = wi;
-    s_b[p] = bb;
-    if constexpr (WITH_SELC) s_sc[p] = sc;
+    if (tt < ntr) {
+      const bool real = tt < tc.nt;
+#pragma unroll
+      for (int j = 0; j < HPW; ++j) {
+        const int hj = tc.hbase + j;
+        float ar = 1.0f, ai = 0.0f, wr = 0.0f, wi = 0.0f, b = 0.0f, scv = 0.0f;
+        if (real && hj < H) {
+          const Transition tr = cayley_gated(dd[j], rr[j], alpha[hj], omega[hj], c);
+          ar = tr.ar;
+          ai = tr.ai;
+          b = bb[j];
+          const float f = b * tr.vp;
+          wr = f * v0[j];
+          wi = f * v1[j];
+          scv = sc[j];
+        }
+        const int p = tt * HPW + j;
+        s.ar[p] = ar;
+        s.ai[p] = ai;
+        s.wr[p] = wr;
+        s.wi[p] = wi;
+        s.b[p] = b;
+        if constexpr (WITH_SELC) s.sc[p] = scv;
+      }
+    }
   }
 }
 
@@ -116,7 +147,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
     const float* __restrict__ omega, float c, float2* __restrict__ summ, float2* __restrict__ gam,
     int L, int H, int Q, int NC, int n_hg) {
   using Cfg = FusedCfg<T, D, LPH>;
-  constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW;
+  constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch;
   extern __shared__ float smem[];
   const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
@@ -124,14 +155,11 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
   const int sub = lane % LPH;
   const int h = tc.hbase + hh;
   const bool hok = h < H;
+  const int ntr = round_up(tc.nt, PF);
+  const int slots = round_up(Q, PF) * HPW;
 
-  float* s_ar = smem;
-  float* s_ai = s_ar + Q * HPW;
-  float* s_wr = s_ai + Q * HPW;
-  float* s_wi = s_wr + Q * HPW;
-  float* s_b = s_wi + Q * HPW;
-  stage_scalars<T, false>(tc, H, HPW, v, beta, nullptr, dt, r, alpha, omega, c, s_ar, s_ai, s_wr,
-                          s_wi, s_b, nullptr);
+  TileScalars s{smem, smem + slots, smem + 2 * slots, smem + 3 * slots, smem + 4 * slots, nullptr};
+  stage_scalars<T, HPW, false>(tc, H, ntr, v, beta, nullptr, dt, r, alpha, omega, c, s);
   __syncthreads();
 
   float zr[DPL], zi[DPL];
@@ -140,47 +168,47 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
   float gr = 1.0f, gi = 0.0f;
 
   const int64_t stride = int64_t(H) * D;
-  const typename T::raw* kp = k + (tc.row0 * H + (hok ? h : 0)) * D + sub * DPL;
-  const uint4 zero4 = make_uint4(0, 0, 0, 0);
-  uint4 kb[kPrefetch];
+  const typename T::raw* kp = k + (tc.row0 * H + (hok ? h : H - 1)) * D + sub * DPL;
+  const int tlast = tc.nt - 1;
+  RowVec<T, DPL> kb[PF];
 #pragma unroll
-  for (int i = 0; i < kPrefetch; ++i) kb[i] = (hok && i < tc.nt) ? ld16(kp + i * stride) : zero4;
+  for (int i = 0; i < PF; ++i) kb[i].load(kp + min(i, tlast) * stride);
+#pragma unroll
+  for (int i = 0; i < PF; ++i) kb[i].pin();
 
-  for (int tb = 0; tb < tc.nt; tb += kPrefetch) {
+  for (int tb = 0; tb < ntr; tb += PF) {
 #pragma unroll
-    for (int i = 0; i < kPrefetch; ++i) {
+    for (int i = 0; i < PF; ++i) {
       const int t = tb + i;
-      if (t < tc.nt) {
-        float kk[DPL];
-        Vec16<T>::unpack(kb[i], kk);
-        kb[i] = (hok && t + kPrefetch < tc.nt) ? ld16(kp + (t + kPrefetch) * stride) : zero4;
-        float pr0 = 0.0f, pi0 = 0.0f, pr1 = 0.0f, pi1 = 0.0f;
+      float kk[DPL];
+      kb[i].unpack(kk);
+      kb[i].load(kp + min(t + PF, tlast) * stride);
+      float pr0 = 0.0f, pi0 = 0.0f, pr1 = 0.0f, pi1 = 0.0f;
 #pragma unroll
-        for (int j = 0; j < DPL; j += 2) {
-          pr0 = fmaf(zr[j], kk[j], pr0);
-          pi0 = fmaf(zi[j], kk[j], pi0);
-          pr1 = fmaf(zr[j + 1], kk[j + 1], pr1);
-          pi1 = fmaf(zi[j + 1], kk[j + 1], pi1);
-        }
-        const float pr = group_sum<LPH>(pr0 + pr1);
-        const float pi = group_sum<LPH>(pi0 + pi1);
-        const int s = t * HPW + hh;
-        const float ar = s_ar[s], ai = s_ai[s], wr = s_wr[s], wi = s_wi[s], bb = s_b[s];
-        const float bpr = bb * pr, bpi = bb * pi;
-        // z <- a (z - beta p k) + w k = a z + (w - a beta p) k
-        const float cr = wr - (ar * bpr - ai * bpi);
-        const float ci = wi - (ar * bpi + ai * bpr);
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-          const float nr = fmaf(ar, zr[j], fmaf(-ai, zi[j], cr * kk[j]));
-          const float ni = fmaf(ar, zi[j], fmaf(ai, zr[j], ci * kk[j]));
-          zr[j] = nr;
-          zi[j] = ni;
-        }
-        const float ngr = ar * gr - ai * gi;
-        gi = ar * gi + ai * gr;
-        gr = ngr;
+      for (int j = 0; j < DPL; j += 2) {
+        pr0 = fmaf(zr[j], kk[j], pr0);
+        pi0 = fmaf(zi[j], kk[j], pi0);
+        pr1 = fmaf(zr[j + 1], kk[j + 1], pr1);
+        pi1 = fmaf(zi[j + 1], kk[j + 1], pi1);
       }
+      const float pr = group_sum<LPH>(pr0 + pr1);
+      const float pi = group_sum<LPH>(pi0 + pi1);
+      const int p = t * HPW + hh;
+      const float ar = s.ar[p], ai = s.ai[p], wr = s.wr[p], wi = s.wi[p], bb = s.b[p];
+      const float bpr = bb * pr, bpi = bb * pi;
+      // z <- a (z - beta p k) + w k = a z + (w - a beta p) k
+      const float er = wr - (ar * bpr - ai * bpi);
+      const float ei = wi - (ar * bpi + ai * bpr);
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        const float nr = fmaf(ar, zr[j], fmaf(-ai, zi[j], er * kk[j]));
+        const float ni = fmaf(ar, zi[j], fmaf(ai, zr[j], ei * kk[j]));
+        zr[j] = nr;
+        zi[j] = ni;
+      }
+      const float ngr = ar * gr - ai * gi;
+      gi = ar * gi + ai * gr;
+      gr = ngr;
     }
   }
 
@@ -194,10 +222,9 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2: inter-chunk carry, s_{k+1} = G_k s_k + F_k (elementwise complex).
-// One block per (b, h) with D * S threads; thread (seg, d) owns chunks
-// [seg*len, (seg+1)*len).  Overwrites F_k with the entering state s_k and
-// writes the final state s_NC as (B, H, 2, D) fp32 (row 0 = re, row 1 = im).
+// Passes 2-3: inter-chunk carry, s_{k+1} = G_k s_k + F_k (elementwise complex),
+// split into segments of kSegLen chunks.  Loads are issued in groups of 8
+// with clamped indices so the serial chain waits on memory once per group.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float2 cmul(float2 a, float2 b) {
   return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
@@ -206,60 +233,109 @@ __device__ __forceinline__ float2 cfma(float2 a, float2 b, float2 c) {
   return make_float2(fmaf(a.x, b.x, fmaf(-a.y, b.y, c.x)), fmaf(a.x, b.y, fmaf(a.y, b.x, c.y)));
 }
 
-__global__ __launch_bounds__(1024) void fused_fwd_carry_kernel(float2* __restrict__ summ,
-                                                               const float2* __restrict__ gam,
-                                                               const float* __restrict__ h0,
-                                                               float* __restrict__ h_final, int NC,
-                                                               int H, int D, int S) {
-  extern __shared__ float2 csm[];  // [S] segment transitions, then [S][D] segment folds
-  float2* s_A = csm;
-  float2* s_X = csm + S;
-  const int b = blockIdx.x / H;
-  const int h = blockIdx.x % H;
-  const int d = threadIdx.x % D;
-  const int seg = threadIdx.x / D;
-  const int len = (NC + S - 1) / S;
-  const int c0 = min(NC, seg * len);
-  const int c1 = min(NC, c0 + len);
-  const int64_t base = (int64_t(b) * NC) * H + h;  // chunk ch -> base + ch*H
+struct CarryIdx {
+  int b, h, seg, d, c0, c1;
+  int64_t base;  // chunk ch of (b, h) is element base + ch * H
+};
 
-  // phase 1: fold the segment from zero
+__device__ __forceinline__ CarryIdx carry_index(int64_t tid, int NC, int H, int D, int S) {
+  CarryIdx x;
+  x.d = int(tid % D);
+  int64_t rest = tid / D;
+  x.seg = int(rest % S);
+  rest /= S;
+  x.h = int(rest % H);
+  x.b = int(rest / H);
+  x.c0 = min(NC, x.seg * kSegLen);
+  x.c1 = min(NC, x.c0 + kSegLen);
+  x.base = int64_t(x.b) * NC * H + x.h;
+  return x;
+}
+
+__global__ __launch_bounds__(256) void fused_fwd_fold_kernel(const float2* __restrict__ summ,
+                                                            const float2* __restrict__ gam,
+                                                            float2* __restrict__ segA,
+                                                            float2* __restrict__ segX, int B, int NC,
+                                                            int H, int D, int S) {
+  const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (tid >= int64_t(B) * H * S * D) return;
+  const CarryIdx x = carry_index(tid, NC, H, D, S);
   float2 A = make_float2(1.0f, 0.0f), X = make_float2(0.0f, 0.0f);
-  for (int ch = c0; ch < c1; ++ch) {
-    const int64_t e = base + int64_t(ch) * H;
-    const float2 G = gam[e];
-    X = cfma(G, X, summ[e * D + d]);
-    A = cmul(G, A);
+  const int last = max(x.c1 - 1, 0);
+  for (int cb = x.c0; cb < x.c1; cb += 8) {
+    float2 G[8], F[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t e = x.base + int64_t(min(cb + i, last)) * H;
+      G[i] = gam[e];
+      F[i] = summ[e * D + x.d];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (cb + i < x.c1) {
+        X = cfma(G[i], X, F[i]);
+        A = cmul(G[i], A);
+      }
+    }
   }
-  s_X[seg * D + d] = X;
-  if (d == 0) s_A[seg] = A;
-  __syncthreads();
+  const int64_t sidx = (int64_t(x.b) * H + x.h) * S + x.seg;
+  segX[sidx * D + x.d] = X;
+  if (x.d == 0) segA[sidx] = A;
+}
 
-  // phase 2: state entering the segment
+__global__ __launch_bounds__(256) void fused_fwd_replay_kernel(float2* __restrict__ summ,
+                                                              const float2* __restrict__ gam,
+                                                              const float2* __restrict__ segA,
+                                                              const float2* __restrict__ segX,
+                                                              const float* __restrict__ h0,
+                                                              float* __restrict__ h_final, int B,
+                                                              int NC, int H, int D, int S) {
+  const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (tid >= int64_t(B) * H * S * D) return;
+  const CarryIdx x = carry_index(tid, NC, H, D, S);
+  const int64_t sbase = (int64_t(x.b) * H + x.h) * S;
+  const int64_t hb = (int64_t(x.b) * H + x.h) * 2 * D;
   float2 s = make_float2(0.0f, 0.0f);
-  if (h0 != nullptr) {
-    const int64_t hb = (int64_t(b) * H + h) * 2 * D;
-    s = make_float2(h0[hb + d], h0[hb + D + d]);
+  if (h0 != nullptr) s = make_float2(h0[hb + x.d], h0[hb + D + x.d]);
+  // state entering the segment
+  for (int jb = 0; jb < x.seg; jb += 8) {
+    float2 A[8], X[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t j = sbase + min(jb + i, x.seg - 1);
+      A[i] = segA[j];
+      X[i] = segX[j * D + x.d];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (jb + i < x.seg) s = cfma(A[i], s, X[i]);
   }
-  for (int j = 0; j < seg; ++j) s = cfma(s_A[j], s, s_X[j * D + d]);
-
-  // phase 3: replay, writing entering states
-  for (int ch = c0; ch < c1; ++ch) {
-    const int64_t e = base + int64_t(ch) * H;
-    const float2 G = gam[e];
-    const float2 F = summ[e * D + d];
-    summ[e * D + d] = s;
-    s = cfma(G, s, F);
+  // replay the segment, writing the state entering each chunk over F
+  const int last = max(x.c1 - 1, 0);
+  for (int cb = x.c0; cb < x.c1; cb += 8) {
+    float2 G[8], F[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t e = x.base + int64_t(min(cb + i, last)) * H;
+      G[i] = gam[e];
+      F[i] = summ[e * D + x.d];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (cb + i < x.c1) {
+        summ[(x.base + int64_t(cb + i) * H) * D + x.d] = s;
+        s = cfma(G[i], s, F[i]);
+      }
+    }
   }
-  if (c0 < c1 && c1 == NC) {
-    const int64_t hb = (int64_t(b) * H + h) * 2 * D;
-    h_final[hb + d] = s.x;
-    h_final[hb + D + d] = s.y;
+  if (x.c0 < x.c1 && x.c1 == NC) {
+    h_final[hb + x.d] = s.x;
+    h_final[hb + D + x.d] = s.y;
   }
 }
 
 // ---------------------------------------------------------------------------
-// Pass 3: per chunk, local state z and decay-free correction c^ from s_k,
+// Pass 4: per chunk, local state z and decay-free correction c^ from s_k,
 // output y_t = sel_C_t ((z_t + g_{t-1} c^_t) . q_t).
 // ---------------------------------------------------------------------------
 template <typename T, int D, int LPH>
@@ -271,7 +347,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
     const float* __restrict__ omega, float c, const float2* __restrict__ states,
     typename T::raw* __restrict__ y, int L, int H, int Q, int NC, int n_hg) {
   using Cfg = FusedCfg<T, D, LPH>;
-  constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW;
+  constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch;
   extern __shared__ float smem[];
   const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
@@ -279,105 +355,103 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
   const int sub = lane % LPH;
   const int h = tc.hbase + hh;
   const bool hok = h < H;
+  const int ntr = round_up(tc.nt, PF);
+  const int slots = round_up(Q, PF) * HPW;
 
-  float* s_ar = smem;
-  float* s_ai = s_ar + Q * HPW;
-  float* s_wr = s_ai + Q * HPW;
-  float* s_wi = s_wr + Q * HPW;
-  float* s_b = s_wi + Q * HPW;
-  float* s_sc = s_b + Q * HPW;
-  float* s_yr = s_sc + Q * HPW;
-  float* s_yi = s_yr + Q * HPW;
-  stage_scalars<T, true>(tc, H, HPW, v, beta, sel_c, dt, r, alpha, omega, c, s_ar, s_ai, s_wr, s_wi,
-                         s_b, s_sc);
+  TileScalars s{smem, smem + slots, smem + 2 * slots, smem + 3 * slots, smem + 4 * slots,
+                smem + 5 * slots};
+  float* s_yr = smem + 6 * slots;
+  float* s_yi = smem + 7 * slots;
+  stage_scalars<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, alpha, omega, c, s);
 
   float zr[DPL], zi[DPL], cr[DPL], ci[DPL];
-#pragma unroll
-  for (int j = 0; j < DPL; ++j) zr[j] = zi[j] = cr[j] = ci[j] = 0.0f;
-  if (hok) {
-    const float2* sp = states + ((int64_t(tc.b) * NC + tc.chunk) * H + h) * D + sub * DPL;
+  {
+    const int hl = hok ? h : H - 1;
+    const float2* sp = states + ((int64_t(tc.b) * NC + tc.chunk) * H + hl) * D + sub * DPL;
 #pragma unroll
     for (int j = 0; j < DPL; ++j) {
       const float2 sv = sp[j];
-      cr[j] = sv.x;
-      ci[j] = sv.y;
+      zr[j] = zi[j] = 0.0f;
+      cr[j] = hok ? sv.x : 0.0f;
+      ci[j] = hok ? sv.y : 0.0f;
     }
   }
-  __syncthreads();
   float gr = 1.0f, gi = 0.0f;  // g_{t-1}
 
   const int64_t stride = int64_t(H) * D;
-  const int64_t off = (tc.row0 * H + (hok ? h : 0)) * D + sub * DPL;
+  const int64_t off = (tc.row0 * H + (hok ? h : H - 1)) * D + sub * DPL;
   const typename T::raw* kp = k + off;
   const typename T::raw* qp = q + off;
-  const uint4 zero4 = make_uint4(0, 0, 0, 0);
-  uint4 kb[kPrefetch], qb[kPrefetch];
+  const int tlast = tc.nt - 1;
+  RowVec<T, DPL> kb[PF], qb[PF];
 #pragma unroll
-  for (int i = 0; i < kPrefetch; ++i) {
-    const bool ld = hok && i < tc.nt;
-    kb[i] = ld ? ld16(kp + i * stride) : zero4;
-    qb[i] = ld ? ld16(qp + i * stride) : zero4;
+  for (int i = 0; i < PF; ++i) {
+    kb[i].load(kp + min(i, tlast) * stride);
+    qb[i].load(qp + min(i, tlast) * stride);
   }
-
-  for (int tb = 0; tb < tc.nt; tb += kPrefetch) {
 #pragma unroll
-    for (int i = 0; i < kPrefetch; ++i) {
+  for (int i = 0; i < PF; ++i) {
+    kb[i].pin();
+    qb[i].pin();
+  }
+  __syncthreads();
+
+  for (int tb = 0; tb < ntr; tb += PF) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
       const int t = tb + i;
-      if (t < tc.nt) {
-        float kk[DPL], qq[DPL];
-        Vec16<T>::unpack(kb[i], kk);
-        Vec16<T>::unpack(qb[i], qq);
-        const bool ld = hok && t + kPrefetch < tc.nt;
-        kb[i] = ld ? ld16(kp + (t + kPrefetch) * stride) : zero4;
-        qb[i] = ld ? ld16(qp + (t + kPrefetch) * stride) : zero4;
+      float kk[DPL], qq[DPL];
+      kb[i].unpack(kk);
+      qb[i].unpack(qq);
+      kb[i].load(kp + min(t + PF, tlast) * stride);
+      qb[i].load(qp + min(t + PF, tlast) * stride);
 
-        float pzr = 0.0f, pzi = 0.0f, pcr = 0.0f, pci = 0.0f, qcr = 0.0f, qci = 0.0f;
+      float pzr = 0.0f, pzi = 0.0f, pcr = 0.0f, pci = 0.0f, qcr = 0.0f, qci = 0.0f;
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-          pzr = fmaf(zr[j], kk[j], pzr);
-          pzi = fmaf(zi[j], kk[j], pzi);
-          pcr = fmaf(cr[j], kk[j], pcr);
-          pci = fmaf(ci[j], kk[j], pci);
-          qcr = fmaf(cr[j], qq[j], qcr);
-          qci = fmaf(ci[j], qq[j], qci);
-        }
-        pzr = group_sum<LPH>(pzr);
-        pzi = group_sum<LPH>(pzi);
-        pcr = group_sum<LPH>(pcr);
-        pci = group_sum<LPH>(pci);
-
-        const int s = t * HPW + hh;
-        const float ar = s_ar[s], ai = s_ai[s], wr = s_wr[s], wi = s_wi[s], bb = s_b[s];
-        const float bpr = bb * pzr, bpi = bb * pzi;
-        const float er = wr - (ar * bpr - ai * bpi);
-        const float ei = wi - (ar * bpi + ai * bpr);
-        const float ecr = bb * pcr, eci = bb * pci;
-        float qzr = 0.0f, qzi = 0.0f;
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-          const float nr = fmaf(ar, zr[j], fmaf(-ai, zi[j], er * kk[j]));
-          const float ni = fmaf(ar, zi[j], fmaf(ai, zr[j], ei * kk[j]));
-          zr[j] = nr;
-          zi[j] = ni;
-          qzr = fmaf(nr, qq[j], qzr);
-          qzi = fmaf(ni, qq[j], qzi);
-          cr[j] = fmaf(-ecr, kk[j], cr[j]);
-          ci[j] = fmaf(-eci, kk[j], ci[j]);
-        }
-        // readout partial: z_t.q + g_{t-1} (c^_t.q)
-        float Rr = qzr + (gr * qcr - gi * qci);
-        float Ri = qzi + (gr * qci + gi * qcr);
-        Rr = group_sum<LPH>(Rr);
-        Ri = group_sum<LPH>(Ri);
-        if (sub == 0) {
-          const float sc = s_sc[s];
-          s_yr[s] = sc * Rr;
-          s_yi[s] = sc * Ri;
-        }
-        const float ngr = ar * gr - ai * gi;
-        gi = ar * gi + ai * gr;
-        gr = ngr;
+      for (int j = 0; j < DPL; ++j) {
+        pzr = fmaf(zr[j], kk[j], pzr);
+        pzi = fmaf(zi[j], kk[j], pzi);
+        pcr = fmaf(cr[j], kk[j], pcr);
+        pci = fmaf(ci[j], kk[j], pci);
+        qcr = fmaf(cr[j], qq[j], qcr);
+        qci = fmaf(ci[j], qq[j], qci);
       }
+      pzr = group_sum<LPH>(pzr);
+      pzi = group_sum<LPH>(pzi);
+      pcr = group_sum<LPH>(pcr);
+      pci = group_sum<LPH>(pci);
+
+      const int p = t * HPW + hh;
+      const float ar = s.ar[p], ai = s.ai[p], wr = s.wr[p], wi = s.wi[p], bb = s.b[p];
+      const float bpr = bb * pzr, bpi = bb * pzi;
+      const float er = wr - (ar * bpr - ai * bpi);
+      const float ei = wi - (ar * bpi + ai * bpr);
+      const float ecr = bb * pcr, eci = bb * pci;
+      float qzr = 0.0f, qzi = 0.0f;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        const float nr = fmaf(ar, zr[j], fmaf(-ai, zi[j], er * kk[j]));
+        const float ni = fmaf(ar, zi[j], fmaf(ai, zr[j], ei * kk[j]));
+        zr[j] = nr;
+        zi[j] = ni;
+        qzr = fmaf(nr, qq[j], qzr);
+        qzi = fmaf(ni, qq[j], qzi);
+        cr[j] = fmaf(-ecr, kk[j], cr[j]);
+        ci[j] = fmaf(-eci, kk[j], ci[j]);
+      }
+      // readout partial: z_t.q + g_{t-1} (c^_t.q)
+      float Rr = qzr + (gr * qcr - gi * qci);
+      float Ri = qzi + (gr * qci + gi * qcr);
+      Rr = group_sum<LPH>(Rr);
+      Ri = group_sum<LPH>(Ri);
+      if (sub == 0) {
+        const float sc = s.sc[p];
+        s_yr[p] = sc * Rr;
+        s_yi[p] = sc * Ri;
+      }
+      const float ngr = ar * gr - ai * gi;
+      gi = ar * gi + ai * gr;
+      gr = ngr;
     }
   }
   __syncthreads();
@@ -404,10 +478,21 @@ namespace {
 
 using namespace cdssm;
 
-int carry_segments(int NC, int D) {
-  int S = 1024 / D;
-  while (S > 1 && S * 2 > NC) S >>= 1;  // no more segments than chunks (roughly)
-  return S;
+struct FwdLayout {
+  int NC, S;
+  int64_t n_summ, n_gam, n_segA, n_segX;  // float2 counts, in workspace order
+  int64_t total() const { return n_summ + n_gam + n_segA + n_segX; }
+};
+
+FwdLayout fwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) {
+  FwdLayout w;
+  w.NC = int((L + chunk - 1) / chunk);
+  w.S = (w.NC + kSegLen - 1) / kSegLen;
+  w.n_summ = B * w.NC * H * D;
+  w.n_gam = B * w.NC * H;
+  w.n_segA = B * H * w.S;
+  w.n_segX = B * H * w.S * D;
+  return w;
 }
 
 template <typename T, int D, int LPH>
@@ -417,35 +502,43 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
                      hipStream_t stream) {
   using raw = typename T::raw;
   constexpr int HPW = kWave / LPH;
-  const int NC = (L + Q - 1) / Q;
+  const FwdLayout w = fwd_layout(B, L, H, D, Q);
+  const int NC = w.NC, S = w.S;
   const int n_hg = (H + HPW - 1) / HPW;
   const int64_t tiles = int64_t(B) * NC * n_hg;
-  if (tiles > 0x7fffffff) {
-    cdssm_host::set_error("cdssm_fused_scan_fwd: too many chunk tiles (%lld)", (long long)tiles);
+  const int64_t carry_threads = int64_t(B) * H * S * D;
+  if (tiles > 0x7fffffff || carry_threads / 256 > 0x7fffffff) {
+    cdssm_host::set_error("cdssm_fused_scan_fwd: grid too large (%lld tiles)", (long long)tiles);
     return CDSSM_EINVAL;
   }
   float2* summ = reinterpret_cast<float2*>(ws);
-  float2* gam = summ + int64_t(B) * NC * H * D;
+  float2* gam = summ + w.n_summ;
+  float2* segA = gam + w.n_gam;
+  float2* segX = segA + w.n_segA;
+  const int slots = round_up(Q, kPrefetch) * HPW;
 
-  const size_t sm1 = size_t(5) * Q * HPW * sizeof(float);
-  hipLaunchKernelGGL((fused_fwd_summary_kernel<T, D, LPH>), dim3(unsigned(tiles)), dim3(kWave), sm1,
-                     stream, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)dt,
-                     (const raw*)r, alpha, omega, c, summ, gam, L, H, Q, NC, n_hg);
+  hipLaunchKernelGGL((fused_fwd_summary_kernel<T, D, LPH>), dim3(unsigned(tiles)), dim3(kWave),
+                     size_t(5) * slots * sizeof(float), stream, (const raw*)k, (const raw*)v,
+                     (const raw*)beta, (const raw*)dt, (const raw*)r, alpha, omega, c, summ, gam, L, H,
+                     Q, NC, n_hg);
   int st = cdssm_host::check_launch("cdssm_fused_scan_fwd/summary");
   if (st) return st;
 
-  const int S = carry_segments(NC, D);
-  const size_t sm2 = size_t(S) * (D + 1) * sizeof(float2);
-  hipLaunchKernelGGL(fused_fwd_carry_kernel, dim3(unsigned(B * H)), dim3(unsigned(S * D)), sm2, stream,
-                     summ, (const float2*)gam, h0, h_final, NC, H, D, S);
-  st = cdssm_host::check_launch("cdssm_fused_scan_fwd/carry");
+  const unsigned cblocks = unsigned((carry_threads + 255) / 256);
+  hipLaunchKernelGGL(fused_fwd_fold_kernel, dim3(cblocks), dim3(256), 0, stream, (const float2*)summ,
+                     (const float2*)gam, segA, segX, B, NC, H, D, S);
+  st = cdssm_host::check_launch("cdssm_fused_scan_fwd/fold");
+  if (st) return st;
+  hipLaunchKernelGGL(fused_fwd_replay_kernel, dim3(cblocks), dim3(256), 0, stream, summ,
+                     (const float2*)gam, (const float2*)segA, (const float2*)segX, h0, h_final, B, NC,
+                     H, D, S);
+  st = cdssm_host::check_launch("cdssm_fused_scan_fwd/replay");
   if (st) return st;
 
-  const size_t sm3 = size_t(8) * Q * HPW * sizeof(float);
-  hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH>), dim3(unsigned(tiles)), dim3(kWave), sm3, stream,
-                     (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,
-                     (const raw*)dt, (const raw*)r, alpha, omega, c, (const float2*)summ, (raw*)y, L, H,
-                     Q, NC, n_hg);
+  hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH>), dim3(unsigned(tiles)), dim3(kWave),
+                     size_t(8) * slots * sizeof(float), stream, (const raw*)q, (const raw*)k,
+                     (const raw*)v, (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r,
+                     alpha, omega, c, (const float2*)summ, (raw*)y, L, H, Q, NC, n_hg);
   return cdssm_host::check_launch("cdssm_fused_scan_fwd/main");
 }
 
@@ -455,9 +548,8 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 extern "C" int64_t cdssm_fused_scan_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t D,
                                                     int64_t N, int64_t chunk) {
-  if (B <= 0 || L <= 0 || H <= 0 || D <= 0 || N <= 0 || chunk <= 0) return -1;
-  const int64_t NC = (L + chunk - 1) / chunk;
-  return (B * NC * H * D * (N / 2) + B * NC * H * (N / 2)) * int64_t(sizeof(float2));
+  if (B <= 0 || L <= 0 || H <= 0 || D <= 0 || N != 2 || chunk <= 0) return -1;
+  return fwd_layout(B, L, H, D, chunk).total() * int64_t(sizeof(float2));
 }
 
 extern "C" int cdssm_fused_scan_fwd(int dtype, const void* q, const void* k, const void* v,

@@ -68,9 +68,13 @@ def test_fused_fwd_rejects_invalid_arguments_without_launching(bad, msg):
 def test_workspace_size_formula():
     lib = _lib.load()
     B, L, H, D, N, Q = 8, 4096, 16, 64, 2, 64
-    NC = L // Q
-    assert lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, N, Q) == (B * NC * H * D + B * NC * H) * 8
-    assert lib.cdssm_fused_scan_workspace_bytes(B, 100, H, D, N, Q) == (B * 2 * H * D + B * 2 * H) * 8
+
+    def expect(L):
+        NC = -(-L // Q)
+        S = -(-NC // 16)          # carry segments of 16 chunks
+        return (B * NC * H * D + B * NC * H + B * H * S * (D + 1)) * 8
+    assert lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, N, Q) == expect(L)
+    assert lib.cdssm_fused_scan_workspace_bytes(B, 100, H, D, N, Q) == expect(100)
     assert lib.cdssm_fused_scan_workspace_bytes(0, L, H, D, N, Q) == -1
 
 
