@@ -5,6 +5,8 @@ reference-compatible autograd Functions.  Importing this package does not
 touch the GPU; the library is loaded on first use and its absence is an error.
 """
 
-from .scan import chunkwise_delta_scan, chunkwise_delta_scan_fwd  # noqa: F401
+from .scan import (ChunkwiseDeltaScanFn, chunkwise_delta_scan, chunkwise_delta_scan_bwd,  # noqa: F401
+                   chunkwise_delta_scan_fwd, chunkwise_delta_scan_train)
 
-__all__ = ["chunkwise_delta_scan", "chunkwise_delta_scan_fwd"]
+__all__ = ["ChunkwiseDeltaScanFn", "chunkwise_delta_scan", "chunkwise_delta_scan_fwd",
+           "chunkwise_delta_scan_bwd", "chunkwise_delta_scan_train"]

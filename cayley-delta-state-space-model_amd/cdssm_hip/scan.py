@@ -132,3 +132,70 @@ class PreparedForward:
         if st != 0:
             _lib.check(st, "cdssm_fused_scan_fwd")
         return self.y, self.h_final
+
+
+def chunkwise_delta_scan_bwd(dy: Tensor, dh_final: Optional[Tensor], q, k, v, beta, sel_C, dt, r,
+                             alpha, omega, c, carry: Tensor, has_h0: bool, chunk_size: int):
+    """Backward of the fused scan (cdssm_fused_scan_bwd), reference-mode gradients.
+
+    Returns (dq, dk, dv, dbeta, dsel_C, ddt, dr, dalpha, domega, dh0); dh0 is
+    None when the forward had no initial state.
+    """
+    B, L, H, D = q.shape
+    N = v.shape[-1]
+    Q = int(chunk_size)
+    lib = _lib.load()
+    dev = q.device
+    dtype = q.dtype
+    dy = dy.to(dtype).contiguous()
+    dhf = None if dh_final is None else dh_final.float().contiguous()
+    outs = [torch.empty_like(t) for t in (q, k, v, beta, sel_C, dt, r)]
+    dalpha = torch.empty(H, dtype=torch.float32, device=dev)
+    domega = torch.empty(H, dtype=torch.float32, device=dev)
+    dh0 = torch.empty(B, H, N, D, dtype=torch.float32, device=dev) if has_h0 else None
+    nbytes = lib.cdssm_fused_scan_bwd_workspace_bytes(B, L, H, D, N, Q)
+    if nbytes <= 0:
+        raise RuntimeError(f"cdssm_fused_scan_bwd_workspace_bytes rejected the shape ({nbytes})")
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    st = lib.cdssm_fused_scan_bwd(_lib.DTYPE_CODE[dtype], *[_lib.ptr(t) for t in (q, k, v, beta, sel_C, dt, r)],
+                                  _lib.ptr(alpha), _lib.ptr(omega), float(c), _lib.ptr(dy), _lib.ptr(dhf),
+                                  _lib.ptr(carry), *[_lib.ptr(t) for t in outs], _lib.ptr(dalpha),
+                                  _lib.ptr(domega), _lib.ptr(dh0), _lib.ptr(ws), B, L, H, D, N, Q,
+                                  _lib.stream_of(dev))
+    _lib.check(st, "cdssm_fused_scan_bwd")
+    return (*outs, dalpha, domega, dh0)
+
+
+class ChunkwiseDeltaScanFn(torch.autograd.Function):
+    """Autograd Function of the fused scan: (q, k, v, beta, sel_C, dt, r, alpha,
+    omega, c, h0, chunk_size) -> (y, h_final).
+
+    Saves the inputs and the per-chunk entering states (no per-step state);
+    the backward recomputes chunk-local states and returns the gradients that
+    the reference ops.py path yields (exact for the readout, the intra-chunk
+    and inter-chunk passes; the reference's shifted gradient for the exact
+    correction pass, exact_correction.cu:213-382).
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0=None, chunk_size=None):
+        B, L, H, D, N, Q, _ = _validate(q, k, v, beta, sel_C, dt, r, alpha, omega, h0, chunk_size)
+        ins = [t.contiguous() for t in (q, k, v, beta, sel_C, dt, r, alpha, omega)]
+        y, h_final, ws = chunkwise_delta_scan_fwd(*ins, c, h0, Q)
+        ctx.save_for_backward(*ins, ws)
+        ctx.c = float(c)
+        ctx.Q = Q
+        ctx.has_h0 = h0 is not None
+        return y, h_final
+
+    @staticmethod
+    def backward(ctx, dy, dh_final):
+        *ins, ws = ctx.saved_tensors
+        g = chunkwise_delta_scan_bwd(dy, dh_final, *ins, ctx.c, ws, ctx.has_h0, ctx.Q)
+        dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0 = g
+        return dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, None, dh0, None
+
+
+def chunkwise_delta_scan_train(q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0=None, chunk_size=None):
+    """Differentiable fused scan: (y, h_final) with gradients for every tensor input."""
+    return ChunkwiseDeltaScanFn.apply(q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0, chunk_size)

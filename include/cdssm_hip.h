@@ -54,6 +54,31 @@ int cdssm_fused_scan_fwd(int dtype, const void* q, const void* k, const void* v,
                          float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
                          int64_t chunk, hipStream_t stream);
 
+/*
+ * Fused scan, backward.  Gradients are those the reference ops.py autograd
+ * path produces for the same forward: exact for the readout (block.py:208-211),
+ * for IntraChunkScanFn.backward (ops.py:123-135, intra_chunk_scan.cu:611-674)
+ * and for InterChunkScanFn.backward (ops.py:158-163, inter_chunk_scan.cu:236-275);
+ * for ExactCorrectionFn.backward (ops.py:189-195, exact_correction.cu:440-498)
+ * the reference's own rule, which treats grad_corrections[t] as the gradient
+ * of the state after step t; and the exact chain rule of the scan-level
+ * Cayley/gating formula for dt, r, alpha, omega.
+ * Inputs: the forward's inputs, dy (B,L,H,N) of `dtype`, dh_final (B,H,N,D)
+ * fp32 or NULL, and fwd_workspace as filled by cdssm_fused_scan_fwd.
+ * Outputs: dq, dk, dv, dbeta, dsel_c, ddt, dr (shapes/dtype of the inputs),
+ * dalpha, domega (H,) fp32, dh0 (B,H,N,D) fp32 or NULL.
+ * workspace: cdssm_fused_scan_bwd_workspace_bytes() bytes.
+ */
+int64_t cdssm_fused_scan_bwd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                             int64_t chunk);
+int cdssm_fused_scan_bwd(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                         const void* sel_c, const void* dt, const void* r, const float* alpha,
+                         const float* omega, float c, const void* dy, const float* dh_final,
+                         const float* fwd_workspace, void* dq, void* dk, void* dv, void* dbeta,
+                         void* dsel_c, void* ddt, void* dr, float* dalpha, float* domega, float* dh0,
+                         float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                         int64_t chunk, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
