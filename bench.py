@@ -37,7 +37,53 @@ def parse():
     ap.add_argument("--config", default="C1", choices=["C1", "C3"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-batches", type=int, default=1)
+    ap.add_argument("--no-fwd-bwd", action="store_true")
     return ap.parse_args()
+
+
+def time_fwd_bwd(cfg_name, steps, warmup):
+    """Forward + backward scan steps on one configuration (bf16, seeded draws,
+    cotangents dy ~ N(0,1) and dh_final ~ N(0,1)).  Returns tokens/s, ms/step,
+    the HBM roofline fraction of the algorithmic fwd+bwd bytes, and the
+    per-pass split."""
+    import torch
+    from cdssm_hip.scan import PreparedBackward, PreparedForward
+    from cdssm_hip.workloads import CONFIGS, draw_inputs, scan_bytes
+
+    cfg = CONFIGS[cfg_name]
+    dev = torch.device("cuda:0")
+    x = draw_inputs(cfg, seed=0)
+    g = {n: (t.to(dev) if isinstance(t, torch.Tensor) else t) for n, t in x.items()}
+    gen = torch.Generator().manual_seed(7)
+    dy = torch.randn(cfg.B, cfg.L, cfg.H, cfg.N, generator=gen).to(dev)
+    dhf = torch.randn(cfg.B, cfg.H, cfg.N, cfg.D, generator=gen).to(dev)
+    fwd = PreparedForward(g["q"], g["k"], g["v"], g["beta"], g["sel_C"], g["dt"], g["r"], g["alpha"],
+                          g["omega"], g["c"], h0=g["h0"])
+    bwd = PreparedBackward(fwd, dy, dhf)
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(warmup):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    tf = tb = 0.0
+    for _ in range(steps):
+        e[0].record(stream)
+        fwd()
+        e[1].record(stream)
+        bwd()
+        e[2].record(stream)
+        torch.cuda.synchronize()
+        tf += e[0].elapsed_time(e[1])
+        tb += e[1].elapsed_time(e[2])
+    ms = (tf + tb) / steps
+    by = scan_bytes(cfg, backward=True)
+    alg = by["fwd"] + by["bwd"]
+    return {"workload": f"{cfg.name} fwd+bwd B{cfg.B} H{cfg.H} L{cfg.L} D{cfg.D} bf16",
+            "tokens_per_s": cfg.B * cfg.L / (ms * 1e-3), "ms_per_step": ms,
+            "fwd_ms": tf / steps, "bwd_ms": tb / steps,
+            "hbm_frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "alg_bytes": alg}
 
 
 def cpu_baseline(cfg, x, batches):
@@ -162,6 +208,8 @@ def main():
         "cold_frac": alg / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "wall_s_timed": wall,
     }
+    if not args.no_fwd_bwd:
+        out["fwd_bwd"] = [time_fwd_bwd(n, 20, 3) for n in ("C1", "C2")]
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg, x, args.cpu_sample_batches)
     print(json.dumps(out), flush=True)

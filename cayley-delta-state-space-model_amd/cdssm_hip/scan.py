@@ -199,3 +199,39 @@ class ChunkwiseDeltaScanFn(torch.autograd.Function):
 def chunkwise_delta_scan_train(q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0=None, chunk_size=None):
     """Differentiable fused scan: (y, h_final) with gradients for every tensor input."""
     return ChunkwiseDeltaScanFn.apply(q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0, chunk_size)
+
+
+class PreparedBackward:
+    """The fused backward bound to a PreparedForward's inputs and workspace.
+
+    Gradient buffers and the backward workspace are allocated once; each call
+    re-launches the backward kernels for the bound cotangents on torch's
+    current stream.  Call the forward first: the backward reads the entering
+    states the forward left in its workspace.
+    """
+
+    def __init__(self, fwd: PreparedForward, dy: Tensor, dh_final: Optional[Tensor] = None, c: float = None):
+        q, k, v, beta, sel_C, dt, r, alpha, omega, h0 = fwd.inputs
+        B, L, H, D, N, Q = fwd.shape
+        self._lib = fwd._lib
+        dev = fwd.device
+        self.dy = dy.to(q.dtype).contiguous()
+        self.dh_final = None if dh_final is None else dh_final.float().contiguous()
+        self.grads = [torch.empty_like(t) for t in (q, k, v, beta, sel_C, dt, r)]
+        self.dalpha = torch.empty(H, dtype=torch.float32, device=dev)
+        self.domega = torch.empty(H, dtype=torch.float32, device=dev)
+        self.dh0 = torch.empty(B, H, N, D, dtype=torch.float32, device=dev) if h0 is not None else None
+        nbytes = self._lib.cdssm_fused_scan_bwd_workspace_bytes(B, L, H, D, N, Q)
+        self.workspace = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+        self.device = dev
+        cval = fwd._args[10] if c is None else float(c)
+        self._args = (_lib.DTYPE_CODE[q.dtype], *[_lib.ptr(t) for t in (q, k, v, beta, sel_C, dt, r)],
+                      _lib.ptr(alpha), _lib.ptr(omega), cval, _lib.ptr(self.dy), _lib.ptr(self.dh_final),
+                      _lib.ptr(fwd.workspace), *[_lib.ptr(t) for t in self.grads], _lib.ptr(self.dalpha),
+                      _lib.ptr(self.domega), _lib.ptr(self.dh0), _lib.ptr(self.workspace), B, L, H, D, N, Q)
+
+    def __call__(self):
+        st = self._lib.cdssm_fused_scan_bwd(*self._args, _lib.stream_of(self.device))
+        if st != 0:
+            _lib.check(st, "cdssm_fused_scan_bwd")
+        return self.grads
