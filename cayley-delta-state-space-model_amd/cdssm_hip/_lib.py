@@ -36,6 +36,17 @@ SIGNATURES = {
     "cdssm_fused_scan_bwd": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _P, _P, _P,
                                     _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                     _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "cdssm_intra_chunk_scan_fwd": (_I32, [_I32] + [_P] * 6 + [_I64] * 5 + [_P]),
+    "cdssm_intra_chunk_scan_bwd": (_I32, [_I32] + [_P] * 12 + [_I64] * 5 + [_P]),
+    "cdssm_inter_chunk_scan_fwd": (_I32, [_I32] + [_P] * 3 + [_I64] * 5 + [_P]),
+    "cdssm_inter_chunk_scan_bwd": (_I32, [_I32] + [_P] * 5 + [_I64] * 5 + [_P]),
+    "cdssm_exact_correction_fwd": (_I32, [_I32] + [_P] * 5 + [_I64] * 6 + [_P]),
+    "cdssm_exact_correction_bwd": (_I32, [_I32] + [_P] * 10 + [_I64] * 6 + [_P]),
+    "cdssm_dynamics_fused_fwd": (_I32, [_I32, _P, _P, _P] + [_F32] * 5 + [_P] * 4 + [_I64] * 4 + [_P]),
+    "cdssm_dynamics_fused_bwd_workspace_bytes": (_I64, [_I64] * 3),
+    "cdssm_dynamics_fused_bwd": (_I32, [_I32] + [_P] * 7 + [_F32] * 5 + [_P] * 3 + [_I64] * 4 + [_P]),
+    "cdssm_normalize_kq_fwd": (_I32, [_I32] + [_P] * 4 + [_I64] * 2 + [_P]),
+    "cdssm_normalize_kq_bwd": (_I32, [_I32] + [_P] * 6 + [_I64] * 2 + [_P]),
 }
 
 _lock = threading.Lock()

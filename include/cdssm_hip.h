@@ -79,6 +79,80 @@ int cdssm_fused_scan_bwd(int dtype, const void* q, const void* k, const void* v,
                          float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
                          int64_t chunk, hipStream_t stream);
 
+/*
+ * The reference's three scan passes as separate ops, same tensor contracts
+ * (all tensors `dtype`, contiguous; N even, N <= 32; D <= 128).
+ *
+ * Replaces intra_chunk_scan_fwd_cuda (intra_chunk_scan.cu:560-609; bound at
+ * binding.cpp:143, called by IntraChunkScanFn.forward, ops.py:107-121):
+ *   A (BNC,C,H,N), K (BNC,C,H,D), V (BNC,C,H,N), beta (BNC,C,H)
+ *   -> local_h (BNC,C,H,N,D) (state after each step), cum_A (BNC,C,H,N).
+ */
+int cdssm_intra_chunk_scan_fwd(int dtype, const void* A, const void* K, const void* V, const void* beta,
+                               void* local_h, void* cum_A, int64_t BNC, int64_t C, int64_t H, int64_t D,
+                               int64_t N, hipStream_t stream);
+/* Replaces intra_chunk_scan_bwd_cuda (intra_chunk_scan.cu:611-674; IntraChunkScanFn.backward,
+ * ops.py:123-135).  grad_beta is written in `dtype` (ops.py:134 casts it). */
+int cdssm_intra_chunk_scan_bwd(int dtype, const void* grad_local_h, const void* grad_cum_A, const void* A,
+                               const void* K, const void* V, const void* beta, const void* local_h,
+                               const void* cum_A, void* grad_A, void* grad_K, void* grad_V, void* grad_beta,
+                               int64_t BNC, int64_t C, int64_t H, int64_t D, int64_t N, hipStream_t stream);
+/* Replaces inter_chunk_scan_fwd_cuda (inter_chunk_scan.cu:201-234; InterChunkScanFn.forward,
+ * ops.py:146-155): total_A (B,NC,H,N), final_local_h (B,NC,H,N,D) -> chunk_states (B,NC,H,N,D). */
+int cdssm_inter_chunk_scan_fwd(int dtype, const void* total_A, const void* final_local_h,
+                               void* chunk_states, int64_t B, int64_t NC, int64_t H, int64_t D, int64_t N,
+                               hipStream_t stream);
+/* Replaces inter_chunk_scan_bwd_cuda (inter_chunk_scan.cu:236-275; InterChunkScanFn.backward,
+ * ops.py:158-163). */
+int cdssm_inter_chunk_scan_bwd(int dtype, const void* grad_chunk_states, const void* total_A,
+                               const void* chunk_states, void* grad_total_A, void* grad_final_local_h,
+                               int64_t B, int64_t NC, int64_t H, int64_t D, int64_t N, hipStream_t stream);
+/* Replaces exact_correction_fwd_cuda (exact_correction.cu:390-438; ExactCorrectionFn.forward,
+ * ops.py:173-186): A (B,NC,C,H,N), K (B,NC,C,H,D), beta (B,NC,C,H), chunk_states (B,NC,H,N,D)
+ * -> corrections (B,NC,C,H,N,D) (state before each step). */
+int cdssm_exact_correction_fwd(int dtype, const void* A_chunk, const void* K_chunk, const void* beta_chunk,
+                               const void* chunk_states, void* corrections, int64_t B, int64_t NC,
+                               int64_t C, int64_t H, int64_t D, int64_t N, hipStream_t stream);
+/* Replaces exact_correction_bwd_cuda (exact_correction.cu:440-498; ExactCorrectionFn.backward,
+ * ops.py:189-195), with the reference's rule (grad_corrections[t] applied to the state after
+ * step t).  chunk_states is accepted for signature parity; corrections holds every pre-step state. */
+int cdssm_exact_correction_bwd(int dtype, const void* grad_corrections, const void* A_chunk,
+                               const void* K_chunk, const void* beta_chunk, const void* chunk_states,
+                               const void* corrections, void* grad_A, void* grad_K, void* grad_beta,
+                               void* grad_states, int64_t B, int64_t NC, int64_t C, int64_t H, int64_t D,
+                               int64_t N, hipStream_t stream);
+
+/*
+ * Replaces dynamics_fused_fwd_cuda (dynamics_fused.cu:392-440; DynamicsFusedFn.forward,
+ * ops.py:39-66): gate_raw (B,L,(N+5)H) `dtype`; log_dt_scale, rope_freqs (H,) fp32
+ * -> A_bar (B,L,H,N), vp_scale (B,L,H,N/2), beta (B,L,H), sel_c (B,L,H), all `dtype`.
+ */
+int cdssm_dynamics_fused_fwd(int dtype, const void* gate_raw, const float* log_dt_scale,
+                             const float* rope_freqs, float gating_c, float omega_thresh, float adt_delta,
+                             float adt_smoothness, float adt_eps, void* A_bar, void* vp_scale, void* beta,
+                             void* sel_c, int64_t B, int64_t L, int64_t H, int64_t N, hipStream_t stream);
+/* Replaces dynamics_fused_bwd_cuda (dynamics_fused.cu:442-499; DynamicsFusedFn.backward,
+ * ops.py:68-81) with the reference's analytic rule; grad_log_dt_scale (H,) fp32 is a
+ * deterministic per-head sum.  workspace: cdssm_dynamics_fused_bwd_workspace_bytes() bytes. */
+int64_t cdssm_dynamics_fused_bwd_workspace_bytes(int64_t B, int64_t L, int64_t H);
+int cdssm_dynamics_fused_bwd(int dtype, const void* grad_A_bar, const void* grad_vp_scale,
+                             const void* grad_beta, const void* grad_sel_c, const void* gate_raw,
+                             const float* log_dt_scale, const float* rope_freqs, float gating_c,
+                             float omega_thresh, float adt_delta, float adt_smoothness, float adt_eps,
+                             void* grad_gate_raw, float* grad_log_dt_scale, float* workspace, int64_t B,
+                             int64_t L, int64_t H, int64_t N, hipStream_t stream);
+
+/*
+ * Replaces normalize_kq_fwd_cuda / normalize_kq_bwd_cuda (normalize_kq.cu:168-244;
+ * NormalizeKQFn, ops.py:84-97): rows of length D (any D <= 256; the reference kernel is
+ * correct only for D = 64), x_hat = x rsqrt(sum x^2 + 1e-6).
+ */
+int cdssm_normalize_kq_fwd(int dtype, const void* K, const void* Q, void* K_out, void* Q_out, int64_t rows,
+                           int64_t D, hipStream_t stream);
+int cdssm_normalize_kq_bwd(int dtype, const void* grad_K_out, const void* grad_Q_out, const void* K,
+                           const void* Q, void* grad_K, void* grad_Q, int64_t rows, int64_t D,
+                           hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
