@@ -18,7 +18,9 @@ from typing import Optional
 import torch
 
 LIB_NAME = "libcdssm_hip.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# CDSSM_HIP_LIB names another build of the same library (e.g. a variant
+# compiled with different launch parameters); default: the in-tree build.
+LIB_PATH = os.environ.get("CDSSM_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64

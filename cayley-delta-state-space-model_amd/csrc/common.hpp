@@ -48,20 +48,22 @@ struct F32 {
 };
 
 // A lane's slice of one row: DPL consecutive elements, loaded with a single
-// 8- or 16-byte load into W = DPL * bytes / 4 dwords and widened on use.
+// 4-, 8- or 16-byte load into W = DPL * bytes / 4 dwords and widened on use.
 template <typename T, int DPL>
 struct RowVec {
   static constexpr int W = DPL * T::bytes / 4;
-  static_assert(W == 2 || W == 4, "a lane slice is one 8- or 16-byte load");
+  static_assert(W == 1 || W == 2 || W == 4, "a lane slice is one 4-, 8- or 16-byte load");
   uint32_t u[W];
 
   __device__ __forceinline__ void load(const typename T::raw* p) {
     if constexpr (W == 4) {
       const uint4 v = *reinterpret_cast<const uint4*>(p);
       u[0] = v.x; u[1] = v.y; u[2] = v.z; u[3] = v.w;
-    } else {
+    } else if constexpr (W == 2) {
       const uint2 v = *reinterpret_cast<const uint2*>(p);
       u[0] = v.x; u[1] = v.y;
+    } else {
+      u[0] = *reinterpret_cast<const uint32_t*>(p);
     }
   }
   // Opaque copy: keeps the compiler from merging a prefetch ring's initial
@@ -92,9 +94,12 @@ struct RowVec {
 // through readlane.  Every lane of the group ends with the group sum.
 // ---------------------------------------------------------------------------
 
+// Full-row permutes only (every source lane valid), so bound_ctrl never
+// zeroes a lane; with it set the compiler folds the move into the add
+// (v_add_f32_dpp).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
 template <int G>

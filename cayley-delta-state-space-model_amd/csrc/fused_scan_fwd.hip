@@ -44,6 +44,12 @@
 namespace cdssm {
 
 constexpr int kPrefetch = 8;
+
+// Lanes per head of the bf16 D = 64 forward (8: one 16-byte row slice per
+// lane; 16 or 32: more waves per SIMD at smaller slices).
+#ifndef CDSSM_FWD_LPH_BF16_D64
+#define CDSSM_FWD_LPH_BF16_D64 8
+#endif
 constexpr int kSegLen = 16;  // chunks per carry segment
 
 template <typename T, int D, int LPH>
@@ -75,9 +81,11 @@ __device__ __forceinline__ ChunkTile decode_tile(int L, int Q, int NC, int n_hg,
   return c;
 }
 
-// Per-token scalars of the tile, one LDS array each, slot p = t*HPW + j.
+// Per-token scalars of the tile in LDS, slot p = t*HPW + j:
+//   s4[p] = (a_re, a_im, w_re, w_im), s2[p] = (beta, sel_C).
 struct TileScalars {
-  float *ar, *ai, *wr, *wi, *b, *sc;
+  float4* s4;
+  float2* s2;
 };
 
 // Stage the tile's per-token scalars.  Lane = token; every lane first issues
@@ -113,26 +121,66 @@ __device__ __forceinline__ void stage_scalars(const ChunkTile& tc, int H, int nt
 #pragma unroll
       for (int j = 0; j < HPW; ++j) {
         const int hj = tc.hbase + j;
-        float ar = 1.0f, ai = 0.0f, wr = 0.0f, wi = 0.0f, b = 0.0f, scv = 0.0f;
+        float4 q4 = make_float4(1.0f, 0.0f, 0.0f, 0.0f);
+        float2 q2 = make_float2(0.0f, 0.0f);
         if (real && hj < H) {
           const Transition tr = cayley_gated(dd[j], rr[j], alpha[hj], omega[hj], c);
-          ar = tr.ar;
-          ai = tr.ai;
-          b = bb[j];
-          const float f = b * tr.vp;
-          wr = f * v0[j];
-          wi = f * v1[j];
-          scv = sc[j];
+          const float f = bb[j] * tr.vp;
+          q4 = make_float4(tr.ar, tr.ai, f * v0[j], f * v1[j]);
+          q2 = make_float2(bb[j], sc[j]);
         }
         const int p = tt * HPW + j;
-        s.ar[p] = ar;
-        s.ai[p] = ai;
-        s.wr[p] = wr;
-        s.wi[p] = wi;
-        s.b[p] = b;
-        if constexpr (WITH_SELC) s.sc[p] = scv;
+        s.s4[p] = q4;
+        s.s2[p] = q2;
       }
     }
+  }
+}
+
+// Local state in a rescaled frame: z = f * zh (f complex, per head).  A step
+//   z_t = a (z_{t-1} - beta (z_{t-1}.k) k) + w k
+// becomes zh += (w/f_t - beta ph) k with f_t = a f_{t-1} and ph = zh.k: two
+// FMAs per element instead of a complex rotation.  When |f_t| would drop
+// below 2^-30 for any head of the wave (or a = 0), the wave takes the direct
+// step zh = mu zh + (w - mu beta ph) k with mu = f_t and resets f to 1, which
+// is exact for every head, so 1/f stays below 2^30.
+struct Frame {
+  float fr, fi;
+};
+
+// One local step for a lane's DPL elements.  Returns nothing; updates zh, f.
+template <int DPL>
+__device__ __forceinline__ void local_step(float (&zr)[DPL], float (&zi)[DPL], Frame& f, const float (&kk)[DPL],
+                                           float ar, float ai, float wr, float wi, float bb, float pr, float pi) {
+  const float nfr = ar * f.fr - ai * f.fi;
+  const float nfi = ar * f.fi + ai * f.fr;
+  const float m2 = nfr * nfr + nfi * nfi;
+  const bool slow = __builtin_amdgcn_ballot_w64(!(m2 >= 0x1p-60f)) != 0;  // also catches NaN / 0
+  const float bpr = bb * pr, bpi = bb * pi;
+  if (!slow) {
+    const float inv = __builtin_amdgcn_rcpf(m2);
+    // w / f_t = w conj(f_t) / |f_t|^2
+    const float er = (wr * nfr + wi * nfi) * inv - bpr;
+    const float ei = (wi * nfr - wr * nfi) * inv - bpi;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      zr[j] = fmaf(er, kk[j], zr[j]);
+      zi[j] = fmaf(ei, kk[j], zi[j]);
+    }
+    f.fr = nfr;
+    f.fi = nfi;
+  } else {
+    const float er = wr - (nfr * bpr - nfi * bpi);
+    const float ei = wi - (nfr * bpi + nfi * bpr);
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const float xr = fmaf(nfr, zr[j], fmaf(-nfi, zi[j], er * kk[j]));
+      const float xi = fmaf(nfr, zi[j], fmaf(nfi, zr[j], ei * kk[j]));
+      zr[j] = xr;
+      zi[j] = xi;
+    }
+    f.fr = 1.0f;
+    f.fi = 0.0f;
   }
 }
 
@@ -148,7 +196,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
     int L, int H, int Q, int NC, int n_hg) {
   using Cfg = FusedCfg<T, D, LPH>;
   constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch;
-  extern __shared__ float smem[];
+  extern __shared__ float4 smem4[];
   const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
   const int hh = lane / LPH;
@@ -158,13 +206,14 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
   const int ntr = round_up(tc.nt, PF);
   const int slots = round_up(Q, PF) * HPW;
 
-  TileScalars s{smem, smem + slots, smem + 2 * slots, smem + 3 * slots, smem + 4 * slots, nullptr};
+  TileScalars s{smem4, reinterpret_cast<float2*>(smem4 + slots)};
   stage_scalars<T, HPW, false>(tc, H, ntr, v, beta, nullptr, dt, r, alpha, omega, c, s);
   __syncthreads();
 
   float zr[DPL], zi[DPL];
 #pragma unroll
   for (int j = 0; j < DPL; ++j) zr[j] = zi[j] = 0.0f;
+  Frame f{1.0f, 0.0f};
   float gr = 1.0f, gi = 0.0f;
 
   const int64_t stride = int64_t(H) * D;
@@ -194,20 +243,11 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
       const float pr = group_sum<LPH>(pr0 + pr1);
       const float pi = group_sum<LPH>(pi0 + pi1);
       const int p = t * HPW + hh;
-      const float ar = s.ar[p], ai = s.ai[p], wr = s.wr[p], wi = s.wi[p], bb = s.b[p];
-      const float bpr = bb * pr, bpi = bb * pi;
-      // z <- a (z - beta p k) + w k = a z + (w - a beta p) k
-      const float er = wr - (ar * bpr - ai * bpi);
-      const float ei = wi - (ar * bpi + ai * bpr);
-#pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        const float nr = fmaf(ar, zr[j], fmaf(-ai, zi[j], er * kk[j]));
-        const float ni = fmaf(ar, zi[j], fmaf(ai, zr[j], ei * kk[j]));
-        zr[j] = nr;
-        zi[j] = ni;
-      }
-      const float ngr = ar * gr - ai * gi;
-      gi = ar * gi + ai * gr;
+      const float4 q4 = s.s4[p];
+      const float bb = s.s2[p].x;
+      local_step<DPL>(zr, zi, f, kk, q4.x, q4.y, q4.z, q4.w, bb, pr, pi);
+      const float ngr = q4.x * gr - q4.y * gi;
+      gi = q4.x * gi + q4.y * gr;
       gr = ngr;
     }
   }
@@ -216,7 +256,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
     const int64_t ch = (int64_t(tc.b) * NC + tc.chunk) * H + h;
     float2* sp = summ + ch * D + sub * DPL;
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) sp[j] = make_float2(zr[j], zi[j]);
+    for (int j = 0; j < DPL; ++j) sp[j] = make_float2(f.fr * zr[j] - f.fi * zi[j], f.fr * zi[j] + f.fi * zr[j]);
     if (sub == 0) gam[ch] = make_float2(gr, gi);
   }
 }
@@ -335,8 +375,8 @@ __global__ __launch_bounds__(256) void fused_fwd_replay_kernel(float2* __restric
 }
 
 // ---------------------------------------------------------------------------
-// Pass 4: per chunk, local state z and decay-free correction c^ from s_k,
-// output y_t = sel_C_t ((z_t + g_{t-1} c^_t) . q_t).
+// Pass 4: per chunk, local state z (rescaled frame) and decay-free correction
+// c^ from s_k; output y_t = sel_C_t ((z_t + g_{t-1} c^_t) . q_t).
 // ---------------------------------------------------------------------------
 template <typename T, int D, int LPH>
 __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
@@ -348,7 +388,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
     typename T::raw* __restrict__ y, int L, int H, int Q, int NC, int n_hg) {
   using Cfg = FusedCfg<T, D, LPH>;
   constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch;
-  extern __shared__ float smem[];
+  extern __shared__ float4 smem4[];
   const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
   const int hh = lane / LPH;
@@ -358,10 +398,8 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
   const int ntr = round_up(tc.nt, PF);
   const int slots = round_up(Q, PF) * HPW;
 
-  TileScalars s{smem, smem + slots, smem + 2 * slots, smem + 3 * slots, smem + 4 * slots,
-                smem + 5 * slots};
-  float* s_yr = smem + 6 * slots;
-  float* s_yi = smem + 7 * slots;
+  TileScalars s{smem4, reinterpret_cast<float2*>(smem4 + slots)};
+  float2* s_y = reinterpret_cast<float2*>(smem4 + slots) + slots;
   stage_scalars<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, alpha, omega, c, s);
 
   float zr[DPL], zi[DPL], cr[DPL], ci[DPL];
@@ -376,6 +414,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
       ci[j] = hok ? sv.y : 0.0f;
     }
   }
+  Frame f{1.0f, 0.0f};
   float gr = 1.0f, gi = 0.0f;  // g_{t-1}
 
   const int64_t stride = int64_t(H) * D;
@@ -422,33 +461,25 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
       pci = group_sum<LPH>(pci);
 
       const int p = t * HPW + hh;
-      const float ar = s.ar[p], ai = s.ai[p], wr = s.wr[p], wi = s.wi[p], bb = s.b[p];
-      const float bpr = bb * pzr, bpi = bb * pzi;
-      const float er = wr - (ar * bpr - ai * bpi);
-      const float ei = wi - (ar * bpi + ai * bpr);
+      const float4 q4 = s.s4[p];
+      const float2 q2 = s.s2[p];
+      const float ar = q4.x, ai = q4.y, bb = q2.x;
+      local_step<DPL>(zr, zi, f, kk, ar, ai, q4.z, q4.w, bb, pzr, pzi);
       const float ecr = bb * pcr, eci = bb * pci;
       float qzr = 0.0f, qzi = 0.0f;
 #pragma unroll
       for (int j = 0; j < DPL; ++j) {
-        const float nr = fmaf(ar, zr[j], fmaf(-ai, zi[j], er * kk[j]));
-        const float ni = fmaf(ar, zi[j], fmaf(ai, zr[j], ei * kk[j]));
-        zr[j] = nr;
-        zi[j] = ni;
-        qzr = fmaf(nr, qq[j], qzr);
-        qzi = fmaf(ni, qq[j], qzi);
+        qzr = fmaf(zr[j], qq[j], qzr);
+        qzi = fmaf(zi[j], qq[j], qzi);
         cr[j] = fmaf(-ecr, kk[j], cr[j]);
         ci[j] = fmaf(-eci, kk[j], ci[j]);
       }
-      // readout partial: z_t.q + g_{t-1} (c^_t.q)
-      float Rr = qzr + (gr * qcr - gi * qci);
-      float Ri = qzi + (gr * qci + gi * qcr);
+      // readout partial: f_t (zh_t.q) + g_{t-1} (c^_t.q)
+      float Rr = (f.fr * qzr - f.fi * qzi) + (gr * qcr - gi * qci);
+      float Ri = (f.fr * qzi + f.fi * qzr) + (gr * qci + gi * qcr);
       Rr = group_sum<LPH>(Rr);
       Ri = group_sum<LPH>(Ri);
-      if (sub == 0) {
-        const float sc = s.sc[p];
-        s_yr[p] = sc * Rr;
-        s_yi[p] = sc * Ri;
-      }
+      if (sub == 0) s_y[p] = make_float2(q2.y * Rr, q2.y * Ri);
       const float ngr = ar * gr - ai * gi;
       gi = ar * gi + ai * gr;
       gr = ngr;
@@ -463,8 +494,9 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
     const int hj = tc.hbase + (p - t * HPW);
     if (hj < H) {
       const int64_t e = ((tc.row0 + t) * H + hj) * 2;
-      T::store(y + e, s_yr[p]);
-      T::store(y + e + 1, s_yi[p]);
+      const float2 yv = s_y[p];
+      T::store(y + e, yv.x);
+      T::store(y + e + 1, yv.y);
     }
   }
 }
@@ -518,7 +550,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   const int slots = round_up(Q, kPrefetch) * HPW;
 
   hipLaunchKernelGGL((fused_fwd_summary_kernel<T, D, LPH>), dim3(unsigned(tiles)), dim3(kWave),
-                     size_t(5) * slots * sizeof(float), stream, (const raw*)k, (const raw*)v,
+                     size_t(slots) * (sizeof(float4) + sizeof(float2)), stream, (const raw*)k, (const raw*)v,
                      (const raw*)beta, (const raw*)dt, (const raw*)r, alpha, omega, c, summ, gam, L, H,
                      Q, NC, n_hg);
   int st = cdssm_host::check_launch("cdssm_fused_scan_fwd/summary");
@@ -536,7 +568,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   if (st) return st;
 
   hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH>), dim3(unsigned(tiles)), dim3(kWave),
-                     size_t(8) * slots * sizeof(float), stream, (const raw*)q, (const raw*)k,
+                     size_t(slots) * (sizeof(float4) + 2 * sizeof(float2)), stream, (const raw*)q, (const raw*)k,
                      (const raw*)v, (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r,
                      alpha, omega, c, (const float2*)summ, (raw*)y, L, H, Q, NC, n_hg);
   return cdssm_host::check_launch("cdssm_fused_scan_fwd/main");
@@ -596,7 +628,7 @@ extern "C" int cdssm_fused_scan_fwd(int dtype, const void* q, const void* k, con
   const int b = int(B), l = int(L), hh = int(H), qc = int(chunk);
   if (dtype == 1) {
     if (D == 64)
-      return launch_fused_fwd<BF16, 64, 8>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
+      return launch_fused_fwd<BF16, 64, CDSSM_FWD_LPH_BF16_D64>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
                                            workspace, b, l, hh, qc, stream);
     return launch_fused_fwd<BF16, 128, 16>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
                                            workspace, b, l, hh, qc, stream);
