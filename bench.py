@@ -38,7 +38,21 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-batches", type=int, default=1)
     ap.add_argument("--no-fwd-bwd", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="only run a device copy of this many MiB (read + write), 10 times, and exit: "
+                         "the reference kernel for scaling HBM byte counters")
     return ap.parse_args()
+
+
+def copy_probe(mib):
+    import torch
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(10):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read_per_call": n * 4, "bytes_written_per_call": n * 4, "calls": 10}))
 
 
 def time_fwd_bwd(cfg_name, steps, warmup):
@@ -123,6 +137,10 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+
+    if args.copy_probe_mib:
+        copy_probe(args.copy_probe_mib)
+        return
 
     import torch
     from cdssm_hip.scan import PreparedForward

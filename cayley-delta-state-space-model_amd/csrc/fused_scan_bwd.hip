@@ -25,15 +25,14 @@
 //   B2 rfold/rreplay: reverse carry over chunks,
 //               d s_k = conj(G_k) d s_{k+1} + lambda_0^(k),  d s_NC = d h_final,
 //               storing d s_{k+1} per chunk and d h0 = d s_0
-//   B3 main:    per chunk: forward recompute with checkpoints,
-//               then segment-wise reverse of both branches (checkpoint
-//               interval 16 / DPL steps), emitting dq, dk,
+//   B3 main:    per chunk: forward recompute (z checkpoints every 16 steps),
+//               then segment-wise reverse of both branches, emitting dq, dk,
 //               dv, dbeta, dsel_C, ddt, dr and per-chunk d alpha / d omega
 //   B4 heads:   deterministic sum of the per-chunk d alpha / d omega.
 //
 // Work layout of B1 and B3: one wave64 per (b, chunk, h); lane owns
-// DPL = D/64 state elements; per-token scalars live one token per lane
-// (two slots for 128-token chunks) and are broadcast with readlane.
+// DPL = D/64 state elements; per-token scalars are computed one token per
+// lane (two slots for 128-token chunks) and read back from LDS.
 #include "common.hpp"
 
 namespace cdssm {
@@ -43,19 +42,6 @@ constexpr int kBwdSeg = 16;
 __device__ __forceinline__ float rl(float x, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
-// Value of token t from a two-slot lane-per-token register pair.
-__device__ __forceinline__ float tok(const float (&s)[2], int t) {
-  return t < 64 ? rl(s[0], t) : rl(s[1], t - 64);
-}
-__device__ __forceinline__ void set_tok(float (&s)[2], int t, float v) {
-  const int lane = threadIdx.x;
-  if (t < 64) {
-    if (lane == t) s[0] = v;
-  } else {
-    if (lane == t - 64) s[1] = v;
-  }
-}
-
 // Full-wave sum, broadcast to every lane.
 __device__ __forceinline__ float wsum(float x) { return group_sum<64>(x); }
 
@@ -154,17 +140,51 @@ struct TokenInputs {
   }
 };
 
-// Load lane's DPL elements of row t (clamped into the tile).
+// A lane's DPL contiguous state columns d = lane*DPL + j of one row.
 template <typename T, int DPL>
-__device__ __forceinline__ void load_row(const typename T::raw* base, int64_t stride, int t, int tlast,
-                                         float (&o)[DPL]) {
-  const typename T::raw* p = base + int64_t(min(t, tlast)) * stride;
+struct Cols {
+  float x[DPL];
+  __device__ __forceinline__ void load(const typename T::raw* p) {
 #pragma unroll
-  for (int j = 0; j < DPL; ++j) o[j] = T::load(p + j);
+    for (int j = 0; j < DPL; ++j) x[j] = T::load(p + j);
+  }
+  // Opaque copy that keeps prefetched values in their registers (see RowVec::pin).
+  __device__ __forceinline__ void pin() {
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) asm volatile("" : "+v"(x[j]));
+  }
+};
+
+// Sum of NV <= 8 values over the 64 lanes of a one-wave block, returned to
+// every lane.  Transposes through LDS: lane l writes its NV partials, then
+// lane l adds 8 lanes' partials of value l%8, and three swizzle/permute
+// stages combine the 8 blocks.  scratch: 8*65 floats.
+template <int NV>
+__device__ __forceinline__ void wave_reduce(float (&v)[NV], float* scratch) {
+  static_assert(NV >= 1 && NV <= 8, "up to 8 values");
+  const int lane = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) scratch[i * 65 + lane] = v[i];
+  asm volatile("" ::: "memory");
+  const int vi = lane & 7, blk = lane >> 3;
+  float s = 0.0f;
+  if (vi < NV) {
+    const float* row = scratch + vi * 65 + blk * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += row[i];
+  }
+  s += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(s), 0x201F));  // lane ^ 8
+  s += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(s), 0x401F));  // lane ^ 16
+  s += __shfl_xor(s, 32, 64);
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = rl(s, i);
 }
 
 // ---------------------------------------------------------------------------
 // B1: correction-branch adjoint of the entering state, per chunk.
+//   lambda = 0; for t = n-1..0: lambda += conj(g_t) sel_t dy_t q_t;
+//   lambda <- lambda - beta_t (lambda.k_t) k_t.   Result: lambda_0 = d s_k.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
@@ -174,21 +194,25 @@ __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
     const typename T::raw* __restrict__ r, const float* __restrict__ alpha,
     const float* __restrict__ omega, float c, const typename T::raw* __restrict__ dy,
     float2* __restrict__ lam0, int L, int H, int Q, int NC) {
-  constexpr int DPL = D / kWave;
+  constexpr int DPL = D / kWave, PF = 8;
+  __shared__ float4 sh[128];  // (h_re, h_im, beta, 0) per token
   const BwdTile tc = bwd_tile(L, Q, NC, H);
   const int lane = threadIdx.x;
-  TokenInputs<T> in;
-  in.load(tc, H, v, beta, sel_c, dt, r, dy, alpha[tc.h], omega[tc.h], c);
-  float gr[2], gi[2], gpr[2], gpi[2];
-  prefix_prod(in.ar, in.ai, gr, gi, gpr, gpi);
-  // h_t = conj(g_t) * sel_t * dy_t
-  float hr[2], hi[2];
+  {
+    TokenInputs<T> in;
+    in.load(tc, H, v, beta, sel_c, dt, r, dy, alpha[tc.h], omega[tc.h], c);
+    float gr[2], gi[2], gpr[2], gpi[2];
+    prefix_prod(in.ar, in.ai, gr, gi, gpr, gpi);
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const float fr = in.sel[s] * in.dyr[s], fi = in.sel[s] * in.dyi[s];
-    hr[s] = gr[s] * fr + gi[s] * fi;
-    hi[s] = gr[s] * fi - gi[s] * fr;
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int t = lane + 64 * s2;
+      if (t < Q) {
+        const float fr = in.sel[s2] * in.dyr[s2], fi = in.sel[s2] * in.dyi[s2];
+        sh[t] = make_float4(gr[s2] * fr + gi[s2] * fi, gr[s2] * fi - gi[s2] * fr, in.b[s2], 0.0f);
+      }
+    }
   }
+  __syncthreads();
 
   const int64_t stride = int64_t(H) * D;
   const int64_t off = (tc.row0 * H + tc.h) * D + lane * DPL;
@@ -198,26 +222,49 @@ __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
   float lr[DPL], li[DPL];
 #pragma unroll
   for (int j = 0; j < DPL; ++j) lr[j] = li[j] = 0.0f;
-
-  for (int t = tc.nt - 1; t >= 0; --t) {
-    float kk[DPL], qq[DPL];
-    load_row<T, DPL>(kp, stride, t, tlast, kk);
-    load_row<T, DPL>(qp, stride, t, tlast, qq);
-    const float h_r = tok(hr, t), h_i = tok(hi, t), bb = tok(in.b, t);
-    float sr = 0.0f, si = 0.0f;
+  // reverse order, rows prefetched PF tokens ahead
+  Cols<T, DPL> kb[PF], qb[PF];
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      lr[j] = fmaf(h_r, qq[j], lr[j]);
-      li[j] = fmaf(h_i, qq[j], li[j]);
-      sr = fmaf(lr[j], kk[j], sr);
-      si = fmaf(li[j], kk[j], si);
-    }
-    sr = wsum(sr);
-    si = wsum(si);
+  for (int i = 0; i < PF; ++i) {
+    const int t = max(tlast - i, 0);
+    kb[i].load(kp + t * stride);
+    qb[i].load(qp + t * stride);
+  }
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      lr[j] = fmaf(-bb * sr, kk[j], lr[j]);
-      li[j] = fmaf(-bb * si, kk[j], li[j]);
+  for (int i = 0; i < PF; ++i) {
+    kb[i].pin();
+    qb[i].pin();
+  }
+  const int nr = (tc.nt + PF - 1) / PF * PF;
+  for (int ib = 0; ib < nr; ib += PF) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int t = tlast - (ib + i);  // may go negative: inert (h = 0, beta = 0)
+      float kk[DPL], qq[DPL];
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        kk[j] = kb[i].x[j];
+        qq[j] = qb[i].x[j];
+      }
+      const int tn = max(t - PF, 0);
+      kb[i].load(kp + tn * stride);
+      qb[i].load(qp + tn * stride);
+      const float4 hv = t >= 0 ? sh[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      float sr = 0.0f, si = 0.0f;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        lr[j] = fmaf(hv.x, qq[j], lr[j]);
+        li[j] = fmaf(hv.y, qq[j], li[j]);
+        sr = fmaf(lr[j], kk[j], sr);
+        si = fmaf(li[j], kk[j], si);
+      }
+      sr = wsum(sr);
+      si = wsum(si);
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        lr[j] = fmaf(-hv.z * sr, kk[j], lr[j]);
+        li[j] = fmaf(-hv.z * si, kk[j], li[j]);
+      }
     }
   }
   float2* o = lam0 + tc.tile * D + lane * DPL;
@@ -361,8 +408,31 @@ __device__ __forceinline__ DynGrad cayley_gated_bwd(float dt, float r, float alp
 }
 
 // ---------------------------------------------------------------------------
-// B3: per-chunk backward of both branches with checkpointed recompute.
+// B3: per-chunk backward of both branches.
+//   forward pass: z and c^ from (0, s_k); per token keeps p_t = z_{t-1}.k_t,
+//     pc_t = c^_t.k_t, Y_t.q_t and the correction's delta g_t in LDS, emits dq,
+//     and stores z every CK tokens;
+//   reverse pass, CK tokens at a time: z of the segment is recomputed from its
+//     checkpoint with the stored p_t (no reductions); c^_t is rebuilt backward,
+//     exactly, as c^_t = c^_{t+1} + beta_t pc_t k_t; the local adjoint mu and
+//     the correction adjoint lambda step back and dk is emitted;
+//   epilogue, one token per lane: dynamics chain rule, dv, dbeta, dsel, ddt,
+//     dr, and the chunk's d alpha / d omega partial.
+// LDS (float4 per token unless noted): S0 (a, w), S1 (beta, f = sel dy),
+// S2 (h = conj(g_t) f, g_{t-1}), P (p, pc), G (delta g, Y.q), R (da, dw),
+// RB (dbeta from the erasures, float), z checkpoints, reduction scratch.
 // ---------------------------------------------------------------------------
+template <int D>
+struct BwdSmem {
+  static constexpr int DPL = D / kWave;
+  static constexpr int CK = 16;
+  static constexpr int QMAX = 128;
+  float4 S0[QMAX], S1[QMAX], S2[QMAX], P[QMAX], G[QMAX], R[QMAX];
+  float RB[QMAX];
+  float2 ck[QMAX / CK][kWave * DPL];
+  float red[8 * 65];
+};
+
 template <typename T, int D>
 __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
     const typename T::raw* __restrict__ q, const typename T::raw* __restrict__ k,
@@ -375,32 +445,41 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
     typename T::raw* __restrict__ dbeta, typename T::raw* __restrict__ dsel,
     typename T::raw* __restrict__ ddt, typename T::raw* __restrict__ dr,
     float2* __restrict__ dhead_parts, int L, int H, int Q, int NC) {
-  constexpr int DPL = D / kWave;
-  constexpr int kCk = 16 / DPL;  // checkpoint interval of the recompute
-  extern __shared__ float4 ck[];  // [Q/kCk][64*DPL] checkpoints (zr, zi, cr, ci)
+  using SM = BwdSmem<D>;
+  constexpr int DPL = SM::DPL, CK = SM::CK, PF = 8;
+  __shared__ SM sm;
   const BwdTile tc = bwd_tile(L, Q, NC, H);
   const int lane = threadIdx.x;
   const float al = alpha[tc.h], om = omega[tc.h];
+
+  // ---- per-token scalars (lane = token, two slots) ----
   TokenInputs<T> in;
   in.load(tc, H, v, beta, sel_c, dt, r, dy, al, om, c);
-  float gr[2], gi[2], gpr[2], gpi[2];
-  prefix_prod(in.ar, in.ai, gr, gi, gpr, gpi);
-  float wr[2], wi[2];
+  {
+    float gr[2], gi[2], gpr[2], gpi[2];
+    prefix_prod(in.ar, in.ai, gr, gi, gpr, gpi);
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const float f = in.b[s] * in.vp[s];
-    wr[s] = f * in.vr[s];
-    wi[s] = f * in.vi[s];
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int t = lane + 64 * s2;
+      if (t < Q) {
+        const float f = in.b[s2] * in.vp[s2];
+        const float fr = in.sel[s2] * in.dyr[s2], fi = in.sel[s2] * in.dyi[s2];
+        sm.S0[t] = make_float4(in.ar[s2], in.ai[s2], f * in.vr[s2], f * in.vi[s2]);
+        sm.S1[t] = make_float4(in.b[s2], fr, fi, 0.0f);
+        sm.S2[t] = make_float4(gr[s2] * fr + gi[s2] * fi, gr[s2] * fi - gi[s2] * fr, gpr[s2], gpi[s2]);
+      }
+    }
   }
+  __syncthreads();
 
   const int64_t stride = int64_t(H) * D;
   const int64_t off = (tc.row0 * H + tc.h) * D + lane * DPL;
   const typename T::raw* kp = k + off;
   const typename T::raw* qp = q + off;
   const int tlast = tc.nt - 1;
-  const int ntr = (tc.nt + kCk - 1) / kCk * kCk;
+  const int ntr = (tc.nt + CK - 1) / CK * CK;
 
-  // ---- forward recompute with checkpoints; per-token dots kept per lane ----
+  // ---- forward pass ----
   float zr[DPL], zi[DPL], cr[DPL], ci[DPL];
   const float2* sp = states + tc.tile * D + lane * DPL;
 #pragma unroll
@@ -409,232 +488,226 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
     cr[j] = sp[j].x;
     ci[j] = sp[j].y;
   }
-  float p_r[2] = {0, 0}, p_i[2] = {0, 0}, pc_r[2] = {0, 0}, pc_i[2] = {0, 0};
-  float zq_r[2] = {0, 0}, zq_i[2] = {0, 0}, cq_r[2] = {0, 0}, cq_i[2] = {0, 0}, kq[2] = {0, 0};
-  for (int t = 0; t < ntr; ++t) {
-    if (t % kCk == 0) {
+  {
+    Cols<T, DPL> kb[PF], qb[PF];
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) ck[(t / kCk) * (64 * DPL) + lane * DPL + j] = make_float4(zr[j], zi[j], cr[j], ci[j]);
-    }
-    float kk[DPL], qq[DPL];
-    load_row<T, DPL>(kp, stride, t, tlast, kk);
-    load_row<T, DPL>(qp, stride, t, tlast, qq);
-    const bool real = t < tc.nt;
-    float s0 = 0, s1 = 0, s2 = 0, s3 = 0, s4 = 0, s5 = 0, s6 = 0, s7 = 0, s8 = 0;
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      s0 = fmaf(zr[j], kk[j], s0);
-      s1 = fmaf(zi[j], kk[j], s1);
-      s2 = fmaf(cr[j], kk[j], s2);
-      s3 = fmaf(ci[j], kk[j], s3);
-      s4 = fmaf(zr[j], qq[j], s4);
-      s5 = fmaf(zi[j], qq[j], s5);
-      s6 = fmaf(cr[j], qq[j], s6);
-      s7 = fmaf(ci[j], qq[j], s7);
-      s8 = fmaf(kk[j], qq[j], s8);
-    }
-    s0 = wsum(s0); s1 = wsum(s1); s2 = wsum(s2); s3 = wsum(s3);
-    s4 = wsum(s4); s5 = wsum(s5); s6 = wsum(s6); s7 = wsum(s7); s8 = wsum(s8);
-    const float ar = tok(in.ar, t), ai = tok(in.ai, t), bb = tok(in.b, t);
-    const float w_r = tok(wr, t), w_i = tok(wi, t);
-    const float bpr = bb * s0, bpi = bb * s1;
-    const float er = w_r - (ar * bpr - ai * bpi);
-    const float ei = w_i - (ar * bpi + ai * bpr);
-    // z_t . q = a (z_{t-1}.q) + e (k.q)
-    const float zqr = ar * s4 - ai * s5 + er * s8;
-    const float zqi = ar * s5 + ai * s4 + ei * s8;
-    set_tok(p_r, t, real ? s0 : 0.0f);
-    set_tok(p_i, t, real ? s1 : 0.0f);
-    set_tok(pc_r, t, real ? s2 : 0.0f);
-    set_tok(pc_i, t, real ? s3 : 0.0f);
-    set_tok(zq_r, t, zqr);
-    set_tok(zq_i, t, zqi);
-    set_tok(cq_r, t, s6);
-    set_tok(cq_i, t, s7);
-    set_tok(kq, t, s8);
-    const float ecr = bb * s2, eci = bb * s3;
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const float nr = fmaf(ar, zr[j], fmaf(-ai, zi[j], er * kk[j]));
-      const float ni = fmaf(ar, zi[j], fmaf(ai, zr[j], ei * kk[j]));
-      zr[j] = nr;
-      zi[j] = ni;
-      cr[j] = fmaf(-ecr, kk[j], cr[j]);
-      ci[j] = fmaf(-eci, kk[j], ci[j]);
-    }
-  }
-
-  // ---- reverse ----
-  // local adjoint mu starts at d s_{k+1}; delta G = sum_d ds_{k+1} conj(s_k)
-  float mr[DPL], mi[DPL], lr[DPL], li[DPL];
-  const float2* dp = dsn + tc.tile * D + lane * DPL;
-  float dGr = 0.0f, dGi = 0.0f;
-#pragma unroll
-  for (int j = 0; j < DPL; ++j) {
-    const float2 ds = dp[j];
-    const float2 s0 = sp[j];
-    mr[j] = ds.x;
-    mi[j] = ds.y;
-    lr[j] = li[j] = 0.0f;
-    dGr = fmaf(ds.x, s0.x, fmaf(ds.y, s0.y, dGr));
-    dGi = fmaf(ds.y, s0.x, fmaf(-ds.x, s0.y, dGi));
-  }
-  dGr = wsum(dGr);
-  dGi = wsum(dGi);
-
-  // per-token gradient scalars (lane = token)
-  float da_r[2] = {0, 0}, da_i[2] = {0, 0}, dw_r[2] = {0, 0}, dw_i[2] = {0, 0}, db_e[2] = {0, 0},
-        dsl[2] = {0, 0};
-  float psr = 0.0f, psi = 0.0f;    // psi_{t+1}
-  float anr = 1.0f, ani = 0.0f;    // a_{t+1}
-  const int64_t doff = off;
-  for (int seg = ntr / kCk - 1; seg >= 0; --seg) {
-    const int tb = seg * kCk;
-    // recompute the segment's states: zb[i] = z_{tb+i-1}, cb[i] = c^_{tb+i}
-    float zbr[kCk + 1][DPL], zbi[kCk + 1][DPL], cbr[kCk][DPL], cbi[kCk][DPL];
-    float kseg[kCk][DPL], qseg[kCk][DPL];
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const float4 cv = ck[seg * (64 * DPL) + lane * DPL + j];
-      zbr[0][j] = cv.x;
-      zbi[0][j] = cv.y;
-      cbr[0][j] = cv.z;
-      cbi[0][j] = cv.w;
+    for (int i = 0; i < PF; ++i) {
+      kb[i].load(kp + min(i, tlast) * stride);
+      qb[i].load(qp + min(i, tlast) * stride);
     }
 #pragma unroll
-    for (int i = 0; i < kCk; ++i) {
-      load_row<T, DPL>(kp, stride, tb + i, tlast, kseg[i]);
-      load_row<T, DPL>(qp, stride, tb + i, tlast, qseg[i]);
+    for (int i = 0; i < PF; ++i) {
+      kb[i].pin();
+      qb[i].pin();
     }
+    for (int tb = 0; tb < ntr; tb += PF) {
 #pragma unroll
-    for (int i = 0; i < kCk; ++i) {
-      const int t = tb + i;
-      const float ar = tok(in.ar, t), ai = tok(in.ai, t), bb = tok(in.b, t);
-      const float w_r = tok(wr, t), w_i = tok(wi, t);
-      const float pr = tok(p_r, t), pi = tok(p_i, t), pcr = tok(pc_r, t), pci = tok(pc_i, t);
-      const float bpr = bb * pr, bpi = bb * pi;
-      const float er = w_r - (ar * bpr - ai * bpi);
-      const float ei = w_i - (ar * bpi + ai * bpr);
-#pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        zbr[i + 1][j] = fmaf(ar, zbr[i][j], fmaf(-ai, zbi[i][j], er * kseg[i][j]));
-        zbi[i + 1][j] = fmaf(ar, zbi[i][j], fmaf(ai, zbr[i][j], ei * kseg[i][j]));
-        if (i + 1 < kCk) {
-          cbr[i + 1][j] = fmaf(-bb * pcr, kseg[i][j], cbr[i][j]);
-          cbi[i + 1][j] = fmaf(-bb * pci, kseg[i][j], cbi[i][j]);
-        }
-      }
-    }
-#pragma unroll
-    for (int i = kCk - 1; i >= 0; --i) {
-      const int t = tb + i;
-      const bool real = t < tc.nt;
-      const float ar = tok(in.ar, t), ai = tok(in.ai, t), bb = tok(in.b, t);
-      const float w_r = tok(wr, t), w_i = tok(wi, t);
-      const float pr = tok(p_r, t), pi = tok(p_i, t), pcr = tok(pc_r, t), pci = tok(pc_i, t);
-      const float sel = tok(in.sel, t), dyr = tok(in.dyr, t), dyi = tok(in.dyi, t);
-      const float g_r = tok(gr, t), g_i = tok(gi, t), gp_r = tok(gpr, t), gp_i = tok(gpi, t);
-      const float fr = sel * dyr, fi = sel * dyi;
-      // conj(g_t) f
-      const float hr = g_r * fr + g_i * fi, hi = g_r * fi - g_i * fr;
-      float sk0 = 0, sk1 = 0, sz0 = 0, sz1 = 0, sl0 = 0, sl1 = 0;
-      float dqv[DPL];
-#pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        const float qv = qseg[i][j], kv = kseg[i][j];
-        // Y_t = z_t + g_{t-1} c^_t
-        const float Yr = zbr[i + 1][j] + gp_r * cbr[i][j] - gp_i * cbi[i][j];
-        const float Yi = zbi[i + 1][j] + gp_r * cbi[i][j] + gp_i * cbr[i][j];
-        dqv[j] = sel * (Yr * dyr + Yi * dyi);
-        mr[j] = fmaf(fr, qv, mr[j]);
-        mi[j] = fmaf(fi, qv, mi[j]);
-        lr[j] = fmaf(hr, qv, lr[j]);
-        li[j] = fmaf(hi, qv, li[j]);
-        sk0 = fmaf(mr[j], kv, sk0);
-        sk1 = fmaf(mi[j], kv, sk1);
-        sz0 = fmaf(mr[j], zbr[i][j], fmaf(mi[j], zbi[i][j], sz0));
-        sz1 = fmaf(mi[j], zbr[i][j], fmaf(-mr[j], zbi[i][j], sz1));
-        sl0 = fmaf(lr[j], kv, sl0);
-        sl1 = fmaf(li[j], kv, sl1);
-      }
-      sk0 = wsum(sk0); sk1 = wsum(sk1); sz0 = wsum(sz0); sz1 = wsum(sz1); sl0 = wsum(sl0); sl1 = wsum(sl1);
-      // dw = mu.k; mk = conj(a) dw
-      const float dwr = sk0, dwi = sk1;
-      const float mkr = ar * dwr + ai * dwi, mki = ar * dwi - ai * dwr;
-      // da (local) = mu.conj(z_{t-1}) - beta conj(p) dw
-      float dar = sz0 - bb * (pr * dwr + pi * dwi);
-      float dai = sz1 - bb * (pr * dwi - pi * dwr);
-      const float dbe = -(pr * mkr + pi * mki) - (pcr * sl0 + pci * sl1);
-      // delta g_t from the correction branch: f conj(c^_{t+1}.q)
-      const float cnr = tok(cq_r, t) - bb * pcr * tok(kq, t);
-      const float cni = tok(cq_i, t) - bb * pci * tok(kq, t);
-      float dgr = fr * cnr + fi * cni, dgi = fi * cnr - fr * cni;
-      if (t == tc.nt - 1) {
-        dgr += dGr;
-        dgi += dGi;
-      }
-      // psi_t = dg_t + conj(a_{t+1}) psi_{t+1}
-      const float npr = dgr + anr * psr + ani * psi;
-      const float npi = dgi + anr * psi - ani * psr;
-      psr = npr;
-      psi = npi;
-      anr = ar;
-      ani = ai;
-      // da += conj(g_{t-1}) psi_t
-      dar += gp_r * psr + gp_i * psi;
-      dai += gp_r * psi - gp_i * psr;
-      // dsel_t = dy . (Y . q)
-      const float yqr = tok(zq_r, t) + gp_r * tok(cq_r, t) - gp_i * tok(cq_i, t);
-      const float yqi = tok(zq_i, t) + gp_r * tok(cq_i, t) + gp_i * tok(cq_r, t);
-      const float dsv = dyr * yqr + dyi * yqi;
-      float dkv[DPL];
-#pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        const float kv = kseg[i][j];
-        // m = conj(a) mu
-        const float m_r = ar * mr[j] + ai * mi[j], m_i = ar * mi[j] - ai * mr[j];
-        dkv[j] = mr[j] * w_r + mi[j] * w_i
-                 - bb * (zbr[i][j] * mkr + zbi[i][j] * mki + m_r * pr + m_i * pi)
-                 - bb * (cbr[i][j] * sl0 + cbi[i][j] * sl1 + lr[j] * pcr + li[j] * pci);
-        // mu <- P_t m ; lambda <- P_t lambda
-        mr[j] = fmaf(-bb * mkr, kv, m_r);
-        mi[j] = fmaf(-bb * mki, kv, m_i);
-        lr[j] = fmaf(-bb * sl0, kv, lr[j]);
-        li[j] = fmaf(-bb * sl1, kv, li[j]);
-      }
-      if (real) {
-        const int64_t o = doff + int64_t(t) * stride;
+      for (int i = 0; i < PF; ++i) {
+        const int t = tb + i;
+        float kk[DPL], qq[DPL];
 #pragma unroll
         for (int j = 0; j < DPL; ++j) {
-          T::store(dq + o + j, dqv[j]);
-          T::store(dk + o + j, dkv[j]);
+          kk[j] = kb[i].x[j];
+          qq[j] = qb[i].x[j];
+        }
+        kb[i].load(kp + min(t + PF, tlast) * stride);
+        qb[i].load(qp + min(t + PF, tlast) * stride);
+        if (t % CK == 0) {
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) sm.ck[t / CK][lane * DPL + j] = make_float2(zr[j], zi[j]);
+        }
+        if (t < tc.nt) {
+          const float4 s0 = sm.S0[t], s1 = sm.S1[t], s2 = sm.S2[t];
+          float red[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) {
+            red[0] = fmaf(zr[j], kk[j], red[0]);
+            red[1] = fmaf(zi[j], kk[j], red[1]);
+            red[2] = fmaf(cr[j], kk[j], red[2]);
+            red[3] = fmaf(ci[j], kk[j], red[3]);
+          }
+          wave_reduce<4>(red, sm.red);
+          const float pr = red[0], pi = red[1], pcr = red[2], pci = red[3];
+          const float ar = s0.x, ai = s0.y, bb = s1.x;
+          const float bpr = bb * pr, bpi = bb * pi;
+          const float er = s0.z - (ar * bpr - ai * bpi);
+          const float ei = s0.w - (ar * bpi + ai * bpr);
+          const float ecr = bb * pcr, eci = bb * pci;
+          float o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+          float dqv[DPL];
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) {
+            const float nr = fmaf(ar, zr[j], fmaf(-ai, zi[j], er * kk[j]));
+            const float ni = fmaf(ar, zi[j], fmaf(ai, zr[j], ei * kk[j]));
+            // Y_t = z_t + g_{t-1} c^_t
+            const float Yr = nr + s2.z * cr[j] - s2.w * ci[j];
+            const float Yi = ni + s2.z * ci[j] + s2.w * cr[j];
+            dqv[j] = Yr * s1.y + Yi * s1.z;
+            o4[0] = fmaf(Yr, qq[j], o4[0]);
+            o4[1] = fmaf(Yi, qq[j], o4[1]);
+            zr[j] = nr;
+            zi[j] = ni;
+            cr[j] = fmaf(-ecr, kk[j], cr[j]);
+            ci[j] = fmaf(-eci, kk[j], ci[j]);
+            o4[2] = fmaf(cr[j], qq[j], o4[2]);
+            o4[3] = fmaf(ci[j], qq[j], o4[3]);
+          }
+          const int64_t o = off + int64_t(t) * stride;
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) T::store(dq + o + j, dqv[j]);
+          wave_reduce<4>(o4, sm.red);
+          if (lane == 0) {
+            // delta g_t = f conj(c^_{t+1}.q)
+            sm.P[t] = make_float4(pr, pi, pcr, pci);
+            sm.G[t] = make_float4(s1.y * o4[2] + s1.z * o4[3], s1.z * o4[2] - s1.y * o4[3], o4[0], o4[1]);
+          }
         }
       }
-      set_tok(da_r, t, dar);
-      set_tok(da_i, t, dai);
-      set_tok(dw_r, t, dwr);
-      set_tok(dw_i, t, dwi);
-      set_tok(db_e, t, dbe);
-      set_tok(dsl, t, dsv);
     }
   }
+  __syncthreads();
+
+  // ---- reverse pass ----
+  float mr[DPL], mi[DPL], lr[DPL], li[DPL];
+  float dG[2] = {0.0f, 0.0f};
+  {
+    const float2* dp = dsn + tc.tile * D + lane * DPL;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const float2 ds = dp[j];
+      const float2 s0 = sp[j];
+      mr[j] = ds.x;
+      mi[j] = ds.y;
+      lr[j] = li[j] = 0.0f;
+      dG[0] = fmaf(ds.x, s0.x, fmaf(ds.y, s0.y, dG[0]));
+      dG[1] = fmaf(ds.y, s0.x, fmaf(-ds.x, s0.y, dG[1]));
+    }
+    wave_reduce<2>(dG, sm.red);
+  }
+  float psr = 0.0f, psi = 0.0f;  // psi_{t+1}
+  float anr = 1.0f, ani = 0.0f;  // a_{t+1}
+  for (int seg = ntr / CK - 1; seg >= 0; --seg) {
+    const int tb = seg * CK;
+    Cols<T, DPL> ks[CK], qs[CK];
+#pragma unroll
+    for (int i = 0; i < CK; ++i) {
+      ks[i].load(kp + min(tb + i, tlast) * stride);
+      qs[i].load(qp + min(tb + i, tlast) * stride);
+    }
+    // z_{tb-1+i} for i = 0..CK (recomputed with the stored p_t)
+    float zbr[CK + 1][DPL], zbi[CK + 1][DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const float2 z0 = sm.ck[seg][lane * DPL + j];
+      zbr[0][j] = z0.x;
+      zbi[0][j] = z0.y;
+    }
+#pragma unroll
+    for (int i = 0; i < CK; ++i) {
+      const int t = tb + i;
+      // steps past the chunk's last token are inert (their LDS slots may be unset)
+      const bool real = t < tc.nt;
+      const float4 s0 = sm.S0[t];
+      const float4 pv = sm.P[t];
+      const float bb = sm.S1[t].x;
+      const float ar = real ? s0.x : 1.0f, ai = real ? s0.y : 0.0f;
+      const float wr = real ? s0.z : 0.0f, wi = real ? s0.w : 0.0f;
+      const float bpr = real ? bb * pv.x : 0.0f, bpi = real ? bb * pv.y : 0.0f;
+      const float er = wr - (ar * bpr - ai * bpi);
+      const float ei = wi - (ar * bpi + ai * bpr);
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        zbr[i + 1][j] = fmaf(ar, zbr[i][j], fmaf(-ai, zbi[i][j], er * ks[i].x[j]));
+        zbi[i + 1][j] = fmaf(ar, zbi[i][j], fmaf(ai, zbr[i][j], ei * ks[i].x[j]));
+      }
+    }
+#pragma unroll
+    for (int i = CK - 1; i >= 0; --i) {
+      const int t = tb + i;
+      if (t < tc.nt) {
+        const float4 s0 = sm.S0[t], s1 = sm.S1[t], s2 = sm.S2[t], pv = sm.P[t], gv = sm.G[t];
+        const float ar = s0.x, ai = s0.y, wr = s0.z, wi = s0.w, bb = s1.x;
+        const float pr = pv.x, pi = pv.y, pcr = pv.z, pci = pv.w;
+        float red[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          const float kv = ks[i].x[j], qv = qs[i].x[j];
+          // c^_t = c^_{t+1} + beta pc k
+          cr[j] = fmaf(bb * pcr, kv, cr[j]);
+          ci[j] = fmaf(bb * pci, kv, ci[j]);
+          mr[j] = fmaf(s1.y, qv, mr[j]);
+          mi[j] = fmaf(s1.z, qv, mi[j]);
+          lr[j] = fmaf(s2.x, qv, lr[j]);
+          li[j] = fmaf(s2.y, qv, li[j]);
+          red[0] = fmaf(mr[j], kv, red[0]);
+          red[1] = fmaf(mi[j], kv, red[1]);
+          red[2] = fmaf(mr[j], zbr[i][j], fmaf(mi[j], zbi[i][j], red[2]));
+          red[3] = fmaf(mi[j], zbr[i][j], fmaf(-mr[j], zbi[i][j], red[3]));
+          red[4] = fmaf(lr[j], kv, red[4]);
+          red[5] = fmaf(li[j], kv, red[5]);
+        }
+        wave_reduce<6>(red, sm.red);
+        const float dwr = red[0], dwi = red[1], slr = red[4], sli = red[5];
+        const float mkr = ar * dwr + ai * dwi, mki = ar * dwi - ai * dwr;
+        float dar = red[2] - bb * (pr * dwr + pi * dwi);
+        float dai = red[3] - bb * (pr * dwi - pi * dwr);
+        const float dbe = -(pr * mkr + pi * mki) - (pcr * slr + pci * sli);
+        float dgr = gv.x, dgi = gv.y;
+        if (t == tc.nt - 1) {
+          dgr += dG[0];
+          dgi += dG[1];
+        }
+        const float npr = dgr + anr * psr + ani * psi;
+        const float npi = dgi + anr * psi - ani * psr;
+        psr = npr;
+        psi = npi;
+        anr = ar;
+        ani = ai;
+        dar += s2.z * psr + s2.w * psi;
+        dai += s2.z * psi - s2.w * psr;
+        float dkv[DPL];
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          const float kv = ks[i].x[j];
+          const float m_r = ar * mr[j] + ai * mi[j], m_i = ar * mi[j] - ai * mr[j];
+          dkv[j] = mr[j] * wr + mi[j] * wi -
+                   bb * (zbr[i][j] * mkr + zbi[i][j] * mki + m_r * pr + m_i * pi) -
+                   bb * (cr[j] * slr + ci[j] * sli + lr[j] * pcr + li[j] * pci);
+          mr[j] = fmaf(-bb * mkr, kv, m_r);
+          mi[j] = fmaf(-bb * mki, kv, m_i);
+          lr[j] = fmaf(-bb * slr, kv, lr[j]);
+          li[j] = fmaf(-bb * sli, kv, li[j]);
+        }
+        const int64_t o = off + int64_t(t) * stride;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) T::store(dk + o + j, dkv[j]);
+        if (lane == 0) {
+          sm.R[t] = make_float4(dar, dai, dwr, dwi);
+          sm.RB[t] = dbe;
+        }
+      }
+    }
+  }
+  __syncthreads();
 
   // ---- per-token dynamics backward (lane = token) ----
   float dal = 0.0f, dom = 0.0f;
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const int t = lane + 64 * s;
+  for (int s2 = 0; s2 < 2; ++s2) {
+    const int t = lane + 64 * s2;
     if (t < tc.nt) {
-      const float bb = in.b[s], vp = in.vp[s], vr = in.vr[s], vi = in.vi[s];
-      const float dwv = dw_r[s] * vr + dw_i[s] * vi;
-      const float dbeta_t = db_e[s] + vp * dwv;
+      const float4 rv = sm.R[t];
+      const float4 gv = sm.G[t];
+      const float bb = in.b[s2], vp = in.vp[s2], vr = in.vr[s2], vi = in.vi[s2];
+      const float dwv = rv.z * vr + rv.w * vi;
+      const float dbeta_t = sm.RB[t] + vp * dwv;
       const float dvp = bb * dwv;
-      const DynGrad g = cayley_gated_bwd(in.dt[s], in.r[s], al, om, c, da_r[s], da_i[s], dvp);
+      const DynGrad g = cayley_gated_bwd(in.dt[s2], in.r[s2], al, om, c, rv.x, rv.y, dvp);
       const int64_t e = (tc.row0 + t) * H + tc.h;
-      T::store(dv + 2 * e, bb * vp * dw_r[s]);
-      T::store(dv + 2 * e + 1, bb * vp * dw_i[s]);
+      T::store(dv + 2 * e, bb * vp * rv.z);
+      T::store(dv + 2 * e + 1, bb * vp * rv.w);
       T::store(dbeta + e, dbeta_t);
-      T::store(dsel + e, dsl[s]);
+      T::store(dsel + e, in.dyr[s2] * gv.z + in.dyi[s2] * gv.w);
       T::store(ddt + e, g.ddt);
       T::store(dr + e, g.dr);
       dal += g.dalpha;
@@ -740,9 +813,7 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
                      gam, (const float2*)segA, (const float2*)segX, dh_final, dsn, dh0, B, NC, H, D, S);
   st = cdssm_host::check_launch("cdssm_fused_scan_bwd/rreplay");
   if (st) return st;
-  constexpr int kCk = 16 / (D / kWave);
-  const size_t ck_bytes = size_t((Q + kCk - 1) / kCk) * 64 * (D / kWave) * sizeof(float4);
-  hipLaunchKernelGGL((fused_bwd_main_kernel<T, D>), dim3(unsigned(tiles)), dim3(kWave), ck_bytes, stream,
+  hipLaunchKernelGGL((fused_bwd_main_kernel<T, D>), dim3(unsigned(tiles)), dim3(kWave), 0, stream,
                      (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,
                      (const raw*)dt, (const raw*)r, alpha, omega, c, (const raw*)dy, states,
                      (const float2*)dsn, (raw*)dq, (raw*)dk, (raw*)dv, (raw*)dbeta, (raw*)dsel, (raw*)ddt,
