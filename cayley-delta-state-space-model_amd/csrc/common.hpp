@@ -73,6 +73,15 @@ struct RowVec {
 #pragma unroll
     for (int i = 0; i < W; ++i) asm volatile("" : "+v"(u[i]));
   }
+  // Unpack, then order the caller's next load of this slice after the unpack:
+  // without the barrier the scheduler may hoist that load above the unpack,
+  // the old and new slice overlap, and the register allocator copies the ring
+  // at the loop latch, which waits for every outstanding load.
+  __device__ __forceinline__ void unpack_then_reload(float (&o)[DPL]) const {
+    unpack(o);
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) asm volatile("" ::"v"(o[i]) : "memory");
+  }
   __device__ __forceinline__ void unpack(float (&o)[DPL]) const {
     if constexpr (T::bytes == 2) {
 #pragma unroll
@@ -142,7 +151,7 @@ __device__ __forceinline__ Transition cayley_gated(float dt, float r, float alph
   const float opa = 1.0f + ta;
   const float oma = 1.0f - ta;
   const float den = opa * opa + tw2 + 1e-6f;
-  const float inv = 1.0f / den;
+  const float inv = __builtin_amdgcn_rcpf(den);  // den >= 1
   const float mur = (1.0f - ta * ta - tw2) * inv;
   const float mui = (2.0f * tw) * inv;
   const float E = fmaxf((oma * oma + tw2) * inv, 1e-8f);
@@ -153,7 +162,7 @@ __device__ __forceinline__ Transition cayley_gated(float dt, float r, float alph
   Transition o;
   o.ar = mur * scale;
   o.ai = -mui * scale;
-  o.vp = fminf(sqrtf(fmaxf(1.0f - eff, 1e-6f)), 1.0f);
+  o.vp = fminf(__builtin_amdgcn_sqrtf(fmaxf(1.0f - eff, 1e-6f)), 1.0f);
   return o;
 }
 

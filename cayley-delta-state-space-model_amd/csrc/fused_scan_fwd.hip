@@ -81,106 +81,279 @@ __device__ __forceinline__ ChunkTile decode_tile(int L, int Q, int NC, int n_hg,
   return c;
 }
 
-// Per-token scalars of the tile in LDS, slot p = t*HPW + j:
-//   s4[p] = (a_re, a_im, w_re, w_im), s2[p] = (beta, sel_C).
+// Per-token scalars of the tile in LDS, slot p = t*HPW + j (token t, head j):
+//   A[p] = (e_re, e_im, beta, sel_C)   the step's write coefficient: w/f_t, or w
+//                                       at a frame reset
+//   B[p] = (f_re, f_im, gp_re, gp_im)  the local frame f_t and g_{t-1}
+//   M[p] = (m_re, m_im)                 1, or f_{t-1} a_t at a frame reset
 struct TileScalars {
-  float4* s4;
-  float2* s2;
+  float4* A;
+  float4* B;
+  float2* M;
 };
 
-// Stage the tile's per-token scalars.  Lane = token; every lane first issues
-// all of its loads (addresses clamped into the tile), then computes.  Slots
-// for tokens in [nt, ntr) and heads >= H hold inert steps.
-template <typename T, int HPW, bool WITH_SELC>
-__device__ __forceinline__ void stage_scalars(const ChunkTile& tc, int H, int ntr,
-                                              const typename T::raw* __restrict__ v,
-                                              const typename T::raw* __restrict__ beta,
-                                              const typename T::raw* __restrict__ sel_c,
-                                              const typename T::raw* __restrict__ dt,
-                                              const typename T::raw* __restrict__ r,
-                                              const float* __restrict__ alpha,
-                                              const float* __restrict__ omega, float c,
-                                              const TileScalars& s) {
-  for (int tl = 0; tl < ntr; tl += kWave) {
-    const int tt = tl + int(threadIdx.x);
-    const int t = min(tt, tc.nt - 1);
-    const int64_t rowe = (tc.row0 + t) * H;
-    float bb[HPW], dd[HPW], rr[HPW], v0[HPW], v1[HPW], sc[HPW];
-#pragma unroll
-    for (int j = 0; j < HPW; ++j) {
-      const int64_t e = rowe + min(tc.hbase + j, H - 1);
-      bb[j] = T::load(beta + e);
-      dd[j] = T::load(dt + e);
-      rr[j] = T::load(r + e);
-      v0[j] = T::load(v + 2 * e);
-      v1[j] = T::load(v + 2 * e + 1);
-      sc[j] = WITH_SELC ? T::load(sel_c + e) : 0.0f;
-    }
-    if (tt < ntr) {
-      const bool real = tt < tc.nt;
-#pragma unroll
-      for (int j = 0; j < HPW; ++j) {
-        const int hj = tc.hbase + j;
-        float4 q4 = make_float4(1.0f, 0.0f, 0.0f, 0.0f);
-        float2 q2 = make_float2(0.0f, 0.0f);
-        if (real && hj < H) {
-          const Transition tr = cayley_gated(dd[j], rr[j], alpha[hj], omega[hj], c);
-          const float f = bb[j] * tr.vp;
-          q4 = make_float4(tr.ar, tr.ai, f * v0[j], f * v1[j]);
-          q2 = make_float2(bb[j], sc[j]);
-        }
-        const int p = tt * HPW + j;
-        s.s4[p] = q4;
-        s.s2[p] = q2;
-      }
-    }
+// Bit t%64 of m0 (t < 64) or m1: some head of the wave resets its frame at
+// token t.  Two named words, not an array, so they stay in scalar registers.
+struct ResetMask {
+  uint64_t m0, m1;
+  __device__ __forceinline__ bool test(int t) const {
+    const uint64_t w = t < 64 ? m0 : m1;
+    // wave-uniform by construction (ballots); readfirstlane makes the branch scalar
+    return __builtin_amdgcn_readfirstlane(int((w >> (t & 63)) & 1ull)) != 0;
   }
+};
+
+// The local state is kept in a rescaled frame, z_t = f_t zh_t (f complex, per
+// head).  A step z_t = a (z_{t-1} - beta (z_{t-1}.k) k) + w k becomes
+//   zh_t = zh_{t-1} + (w/f_t - beta ph) k,   f_t = f_{t-1} a_t,   ph = zh_{t-1}.k
+// (two FMAs per element), or, at a frame reset, the direct step
+//   zh_t = m zh_{t-1} + (w - m beta ph) k,   m = f_{t-1} a_t,   f_t = 1.
+// Resets are placed where log2 |g_t|^2 (g_t = prod_{u<=t} a_u) crosses a
+// multiple of -kBand, and at every token with |a_t|^2 < 2^-kBandStep; the
+// decay between two resets then stays above 2^-kBand, so |f|^2 > 2^-kBand and
+// 1/f is finite.  The positions depend only on the a_t, so they are found
+// here, in parallel over tokens (prefix sums), and the loops branch on a
+// wave-uniform mask instead of testing |f| every step.
+constexpr float kBand = 120.0f;
+constexpr float kBandStep = 60.0f;
+
+__device__ __forceinline__ void cmul_acc(float& xr, float& xi, float yr, float yi) {
+  const float nr = xr * yr - xi * yi;
+  xi = xr * yi + xi * yr;
+  xr = nr;
 }
 
-// Local state in a rescaled frame: z = f * zh (f complex, per head).  A step
-//   z_t = a (z_{t-1} - beta (z_{t-1}.k) k) + w k
-// becomes zh += (w/f_t - beta ph) k with f_t = a f_{t-1} and ph = zh.k: two
-// FMAs per element instead of a complex rotation.  When |f_t| would drop
-// below 2^-30 for any head of the wave (or a = 0), the wave takes the direct
-// step zh = mu zh + (w - mu beta ph) k with mu = f_t and resets f to 1, which
-// is exact for every head, so 1/f stays below 2^30.
-struct Frame {
-  float fr, fi;
-};
+// Spread the low 8 bits of x to bit positions 0, 8, ..., 56.
+__device__ __forceinline__ uint64_t spread8(uint64_t x) {
+  x = (x | (x << 28)) & 0x0000000F0000000Full;
+  x = (x | (x << 14)) & 0x0003000300030003ull;
+  x = (x | (x << 7)) & 0x0101010101010101ull;
+  return x;
+}
 
-// One local step for a lane's DPL elements.  Returns nothing; updates zh, f.
+// Stage the tile's per-token scalars.  Work layout: lane = (head j, block of
+// TPB = HPW consecutive tokens of a 64-token slab), NB = 64/HPW blocks per
+// head.  Each lane first issues all of its loads (addresses clamped into the
+// tile), computes its tokens' dynamics, runs the three prefix scans (log2|g|^2
+// for the reset bands, the segmented frame product f, the plain product g)
+// sequentially over its own tokens, and joins them across the head's NB
+// lanes with log2(NB) shuffle steps.  Slots past the last token and heads
+// >= H hold inert steps (a = 1, w = 0, beta = 0).  Summary pass (MAIN false):
+// writes G_k = g over the chunk to gam and the last frame f to B[j].
+template <typename T, int HPW, bool MAIN>
+__device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, int ntr,
+                                                   const typename T::raw* __restrict__ v,
+                                                   const typename T::raw* __restrict__ beta,
+                                                   const typename T::raw* __restrict__ sel_c,
+                                                   const typename T::raw* __restrict__ dt,
+                                                   const typename T::raw* __restrict__ r,
+                                                   const float* __restrict__ alpha,
+                                                   const float* __restrict__ omega, float c,
+                                                   const TileScalars& s, float2* __restrict__ gam,
+                                                   int64_t gam_base) {
+  constexpr int NB = kWave / HPW;
+  constexpr int TPB = HPW;
+  static_assert(NB * TPB == kWave, "blocks tile the slab");
+  const int lane = threadIdx.x;
+  const int j = lane / NB;
+  const int blk = lane % NB;
+  const int hj = tc.hbase + j;
+  const bool hok = hj < H;
+  const int hl = hok ? hj : H - 1;
+  const float al = alpha[hl], om = omega[hl];
+  const int glast = j * NB + NB - 1;  // the head's last lane
+
+  ResetMask rm{0ull, 0ull};
+  float cL = 0.0f, cfr = 1.0f, cfi = 0.0f, cgr = 1.0f, cgi = 0.0f;  // carries from earlier slabs
+  for (int tl = 0; tl < ntr; tl += kWave) {
+    const int t0 = tl + blk * TPB;
+    float bb[TPB], dd[TPB], rr[TPB], v0[TPB], v1[TPB], sc[TPB];
+#pragma unroll
+    for (int i = 0; i < TPB; ++i) {
+      const int t = min(t0 + i, tc.nt - 1);
+      const int64_t e = (tc.row0 + t) * H + hl;
+      bb[i] = T::load(beta + e);
+      dd[i] = T::load(dt + e);
+      rr[i] = T::load(r + e);
+      v0[i] = T::load(v + 2 * e);
+      v1[i] = T::load(v + 2 * e + 1);
+      sc[i] = MAIN ? T::load(sel_c + e) : 0.0f;
+    }
+    // dynamics and local (in-block) prefixes; computed for every slot (the
+    // clamped loads hold valid numbers) and replaced by an inert step where
+    // the slot is not a real token, so the tokens interleave without branches
+    float ar[TPB], ai[TPB], wr[TPB], wi[TPB], Ls[TPB], Gr[TPB], Gi[TPB];
+    bool forced[TPB];
+    float lsum = 0.0f, gpr = 1.0f, gpi = 0.0f;
+#pragma unroll
+    for (int i = 0; i < TPB; ++i) {
+      const bool real = hok && t0 + i < tc.nt;
+      const Transition tr = cayley_gated(dd[i], rr[i], al, om, c);
+      const float f = bb[i] * tr.vp;
+      ar[i] = real ? tr.ar : 1.0f;
+      ai[i] = real ? tr.ai : 0.0f;
+      wr[i] = real ? f * v0[i] : 0.0f;
+      wi[i] = real ? f * v1[i] : 0.0f;
+      bb[i] = real ? bb[i] : 0.0f;
+      sc[i] = real ? sc[i] : 0.0f;
+      const float m2 = ar[i] * ar[i] + ai[i] * ai[i];
+      forced[i] = !(m2 >= 0x1p-60f);  // also NaN
+      lsum += forced[i] ? -kBandStep : __builtin_amdgcn_logf(m2);
+      Ls[i] = lsum;
+      cmul_acc(gpr, gpi, ar[i], ai[i]);
+      Gr[i] = gpr;
+      Gi[i] = gpi;
+    }
+    // exclusive prefix over the head's blocks: sum of log2|a|^2, product of a
+    float xL = lsum, xgr = gpr, xgi = gpi;
+#pragma unroll
+    for (int off = 1; off < NB; off <<= 1) {
+      const float yL = __shfl_up(xL, off, NB), ygr = __shfl_up(xgr, off, NB), ygi = __shfl_up(xgi, off, NB);
+      if (blk >= off) {
+        xL += yL;
+        cmul_acc(xgr, xgi, ygr, ygi);
+      }
+    }
+    float eL = __shfl_up(xL, 1, NB), egr = __shfl_up(xgr, 1, NB), egi = __shfl_up(xgi, 1, NB);
+    if (blk == 0) {
+      eL = 0.0f;
+      egr = 1.0f;
+      egi = 0.0f;
+    }
+    eL += cL;
+    cmul_acc(egr, egi, cgr, cgi);  // g entering the block
+    // reset positions and the in-block segmented frame product
+    bool reset[TPB];
+    float Fr[TPB], Fi[TPB];
+    bool anyr = false;
+    {
+      float bprev = floorf(eL * (-1.0f / kBand));
+      float fr = 1.0f, fi = 0.0f;
+#pragma unroll
+      for (int i = 0; i < TPB; ++i) {
+        const float band = floorf((eL + Ls[i]) * (-1.0f / kBand));
+        reset[i] = forced[i] || band != bprev;
+        bprev = band;
+        const float nr = fr * ar[i] - fi * ai[i];
+        const float ni = fr * ai[i] + fi * ar[i];
+        fr = reset[i] ? 1.0f : nr;
+        fi = reset[i] ? 0.0f : ni;
+        anyr = anyr || reset[i];
+        Fr[i] = fr;
+        Fi[i] = fi;
+      }
+    }
+    // frame entering the block: segmented exclusive scan over blocks, seeded
+    // with the carry (which acts as a reset element)
+    float xfr = Fr[TPB - 1], xfi = Fi[TPB - 1];
+    int xfl = anyr;
+#pragma unroll
+    for (int off = 1; off < NB; off <<= 1) {
+      const float yr = __shfl_up(xfr, off, NB), yi = __shfl_up(xfi, off, NB);
+      const int yf = __shfl_up(xfl, off, NB);
+      if (blk >= off && !xfl) {
+        cmul_acc(xfr, xfi, yr, yi);
+        xfl = yf;
+      }
+    }
+    float efr = __shfl_up(xfr, 1, NB), efi = __shfl_up(xfi, 1, NB);
+    int efl = __shfl_up(xfl, 1, NB);
+    if (blk == 0) {
+      efr = 1.0f;
+      efi = 0.0f;
+      efl = 0;
+    }
+    if (!efl) cmul_acc(efr, efi, cfr, cfi);
+    // per token outputs (every slot of the slab: LDS holds whole slabs)
+    float fpr = efr, fpi = efi;  // f_{t-1}
+    float lfr = efr, lfi = efi;  // f_t
+    bool seen = false;           // a reset at or before this token in the block
+#pragma unroll
+    for (int i = 0; i < TPB; ++i) {
+      seen = seen || reset[i];
+      lfr = seen ? Fr[i] : Fr[i] * efr - Fi[i] * efi;
+      lfi = seen ? Fi[i] : Fr[i] * efi + Fi[i] * efr;
+      const int t = t0 + i;
+      const int p = t * HPW + j;
+      const float inv = __builtin_amdgcn_rcpf(lfr * lfr + lfi * lfi);
+      const float er = reset[i] ? wr[i] : (wr[i] * lfr + wi[i] * lfi) * inv;
+      const float ei = reset[i] ? wi[i] : (wi[i] * lfr - wr[i] * lfi) * inv;
+      s.A[p] = make_float4(er, ei, bb[i], sc[i]);
+      if (MAIN) {
+        // g_{t-1} = g entering the block times the in-block product before t
+        float gr = egr, gi = egi;
+        if (i > 0) cmul_acc(gr, gi, Gr[i - 1], Gi[i - 1]);
+        s.B[p] = make_float4(lfr, lfi, gr, gi);
+      }
+      const float mr = fpr * ar[i] - fpi * ai[i], mi = fpr * ai[i] + fpi * ar[i];
+      s.M[p] = reset[i] ? make_float2(mr, mi) : make_float2(1.0f, 0.0f);
+      fpr = lfr;
+      fpi = lfi;
+      // tokens of this slab where some head resets: OR over the heads' lanes
+      uint64_t bal = __builtin_amdgcn_ballot_w64(reset[i]);
+#pragma unroll
+      for (int sh = NB; sh < kWave; sh <<= 1) bal |= bal >> sh;
+      bal &= (NB == 64 ? ~0ull : ((1ull << NB) - 1));
+      uint64_t tokbits = 0;
+      if constexpr (NB == 8) {
+        tokbits = spread8(bal) << i;
+      } else {
+#pragma unroll
+        for (int b2 = 0; b2 < NB; ++b2)
+          if ((bal >> b2) & 1ull) tokbits |= 1ull << (b2 * TPB + i);
+      }
+      if (tl == 0)
+        rm.m0 |= tokbits;
+      else
+        rm.m1 |= tokbits;
+    }
+    // carries to the next slab, from the head's last lane
+    float gtr = egr, gti = egi;
+    cmul_acc(gtr, gti, gpr, gpi);
+    cL = __shfl(eL + lsum, glast, kWave);
+    cfr = __shfl(lfr, glast, kWave);
+    cfi = __shfl(lfi, glast, kWave);
+    cgr = __shfl(gtr, glast, kWave);
+    cgi = __shfl(gti, glast, kWave);
+  }
+  if (!MAIN && blk == 0) {
+    // G_k = g over the whole (padded) chunk and the frame after its last step
+    // (inert steps have a = 1)
+    if (hok) gam[gam_base + j] = make_float2(cgr, cgi);
+    s.B[j] = make_float4(cfr, cfi, 0.0f, 0.0f);
+  }
+  rm.m0 = __builtin_amdgcn_readfirstlane(uint32_t(rm.m0)) |
+          (uint64_t(__builtin_amdgcn_readfirstlane(uint32_t(rm.m0 >> 32))) << 32);
+  rm.m1 = __builtin_amdgcn_readfirstlane(uint32_t(rm.m1)) |
+          (uint64_t(__builtin_amdgcn_readfirstlane(uint32_t(rm.m1 >> 32))) << 32);
+  return rm;
+}
+
+// One local step for a lane's DPL elements (see the frame rule above).  At a
+// token where some head of the wave resets, zh is first scaled in place by m
+// (m = 1 for the other heads), then every head takes the common update.
 template <int DPL>
-__device__ __forceinline__ void local_step(float (&zr)[DPL], float (&zi)[DPL], Frame& f, const float (&kk)[DPL],
-                                           float ar, float ai, float wr, float wi, float bb, float pr, float pi) {
-  const float nfr = ar * f.fr - ai * f.fi;
-  const float nfi = ar * f.fi + ai * f.fr;
-  const float m2 = nfr * nfr + nfi * nfi;
-  const bool slow = __builtin_amdgcn_ballot_w64(!(m2 >= 0x1p-60f)) != 0;  // also catches NaN / 0
-  const float bpr = bb * pr, bpi = bb * pi;
-  if (!slow) {
-    const float inv = __builtin_amdgcn_rcpf(m2);
-    // w / f_t = w conj(f_t) / |f_t|^2
-    const float er = (wr * nfr + wi * nfi) * inv - bpr;
-    const float ei = (wi * nfr - wr * nfi) * inv - bpi;
+__device__ __forceinline__ void local_step(float (&zr)[DPL], float (&zi)[DPL], const float (&kk)[DPL],
+                                           bool reset_any, const float2* mslot, float er0, float ei0,
+                                           float bb, float pr, float pi) {
+  float bpr = bb * pr, bpi = bb * pi;
+  if (reset_any) {
+    const float2 m = *mslot;
 #pragma unroll
     for (int j = 0; j < DPL; ++j) {
-      zr[j] = fmaf(er, kk[j], zr[j]);
-      zi[j] = fmaf(ei, kk[j], zi[j]);
-    }
-    f.fr = nfr;
-    f.fi = nfi;
-  } else {
-    const float er = wr - (nfr * bpr - nfi * bpi);
-    const float ei = wi - (nfr * bpi + nfi * bpr);
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const float xr = fmaf(nfr, zr[j], fmaf(-nfi, zi[j], er * kk[j]));
-      const float xi = fmaf(nfr, zi[j], fmaf(nfi, zr[j], ei * kk[j]));
+      const float xr = m.x * zr[j] - m.y * zi[j];
+      zi[j] = m.x * zi[j] + m.y * zr[j];
       zr[j] = xr;
-      zi[j] = xi;
     }
-    f.fr = 1.0f;
-    f.fi = 0.0f;
+    const float nr = m.x * bpr - m.y * bpi;
+    bpi = m.x * bpi + m.y * bpr;
+    bpr = nr;
+  }
+  const float er = er0 - bpr, ei = ei0 - bpi;
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) {
+    zr[j] = fmaf(er, kk[j], zr[j]);
+    zi[j] = fmaf(ei, kk[j], zi[j]);
   }
 }
 
@@ -204,17 +377,8 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
   const int h = tc.hbase + hh;
   const bool hok = h < H;
   const int ntr = round_up(tc.nt, PF);
-  const int slots = round_up(Q, PF) * HPW;
-
-  TileScalars s{smem4, reinterpret_cast<float2*>(smem4 + slots)};
-  stage_scalars<T, HPW, false>(tc, H, ntr, v, beta, nullptr, dt, r, alpha, omega, c, s);
-  __syncthreads();
-
-  float zr[DPL], zi[DPL];
-#pragma unroll
-  for (int j = 0; j < DPL; ++j) zr[j] = zi[j] = 0.0f;
-  Frame f{1.0f, 0.0f};
-  float gr = 1.0f, gi = 0.0f;
+  const int slots = round_up(Q, kWave) * HPW;
+  const int64_t ch0 = (int64_t(tc.b) * NC + tc.chunk) * H + tc.hbase;
 
   const int64_t stride = int64_t(H) * D;
   const typename T::raw* kp = k + (tc.row0 * H + (hok ? h : H - 1)) * D + sub * DPL;
@@ -222,15 +386,27 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
   RowVec<T, DPL> kb[PF];
 #pragma unroll
   for (int i = 0; i < PF; ++i) kb[i].load(kp + min(i, tlast) * stride);
+
+  TileScalars s{smem4, smem4 + slots, reinterpret_cast<float2*>(smem4 + slots + HPW)};
+  const ResetMask rm = stage_scalars<T, HPW, false>(tc, H, ntr, v, beta, nullptr, dt, r, alpha, omega, c, s,
+                                                    gam, ch0);
 #pragma unroll
   for (int i = 0; i < PF; ++i) kb[i].pin();
+  __syncthreads();
+
+  float zr[DPL], zi[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) zr[j] = zi[j] = 0.0f;
 
   for (int tb = 0; tb < ntr; tb += PF) {
+    float4 sa[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) sa[i] = s.A[(tb + i) * HPW + hh];
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int t = tb + i;
       float kk[DPL];
-      kb[i].unpack(kk);
+      kb[i].unpack_then_reload(kk);
       kb[i].load(kp + min(t + PF, tlast) * stride);
       float pr0 = 0.0f, pi0 = 0.0f, pr1 = 0.0f, pi1 = 0.0f;
 #pragma unroll
@@ -242,22 +418,15 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
       }
       const float pr = group_sum<LPH>(pr0 + pr1);
       const float pi = group_sum<LPH>(pi0 + pi1);
-      const int p = t * HPW + hh;
-      const float4 q4 = s.s4[p];
-      const float bb = s.s2[p].x;
-      local_step<DPL>(zr, zi, f, kk, q4.x, q4.y, q4.z, q4.w, bb, pr, pi);
-      const float ngr = q4.x * gr - q4.y * gi;
-      gi = q4.x * gi + q4.y * gr;
-      gr = ngr;
+      local_step<DPL>(zr, zi, kk, rm.test(t), s.M + t * HPW + hh, sa[i].x, sa[i].y, sa[i].z, pr, pi);
     }
   }
 
   if (hok) {
-    const int64_t ch = (int64_t(tc.b) * NC + tc.chunk) * H + h;
-    float2* sp = summ + ch * D + sub * DPL;
+    const float4 fe = s.B[hh];
+    float2* sp = summ + (ch0 + hh) * D + sub * DPL;
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) sp[j] = make_float2(f.fr * zr[j] - f.fi * zi[j], f.fr * zi[j] + f.fi * zr[j]);
-    if (sub == 0) gam[ch] = make_float2(gr, gi);
+    for (int j = 0; j < DPL; ++j) sp[j] = make_float2(fe.x * zr[j] - fe.y * zi[j], fe.x * zi[j] + fe.y * zr[j]);
   }
 }
 
@@ -376,7 +545,7 @@ __global__ __launch_bounds__(256) void fused_fwd_replay_kernel(float2* __restric
 
 // ---------------------------------------------------------------------------
 // Pass 4: per chunk, local state z (rescaled frame) and decay-free correction
-// c^ from s_k; output y_t = sel_C_t ((z_t + g_{t-1} c^_t) . q_t).
+// c^ from s_k; output y_t = sel_C_t (f_t (zh_t . q_t) + g_{t-1} (c^_t . q_t)).
 // ---------------------------------------------------------------------------
 template <typename T, int D, int LPH>
 __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
@@ -396,26 +565,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
   const int h = tc.hbase + hh;
   const bool hok = h < H;
   const int ntr = round_up(tc.nt, PF);
-  const int slots = round_up(Q, PF) * HPW;
-
-  TileScalars s{smem4, reinterpret_cast<float2*>(smem4 + slots)};
-  float2* s_y = reinterpret_cast<float2*>(smem4 + slots) + slots;
-  stage_scalars<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, alpha, omega, c, s);
-
-  float zr[DPL], zi[DPL], cr[DPL], ci[DPL];
-  {
-    const int hl = hok ? h : H - 1;
-    const float2* sp = states + ((int64_t(tc.b) * NC + tc.chunk) * H + hl) * D + sub * DPL;
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const float2 sv = sp[j];
-      zr[j] = zi[j] = 0.0f;
-      cr[j] = hok ? sv.x : 0.0f;
-      ci[j] = hok ? sv.y : 0.0f;
-    }
-  }
-  Frame f{1.0f, 0.0f};
-  float gr = 1.0f, gi = 0.0f;  // g_{t-1}
+  const int slots = round_up(Q, kWave) * HPW;
 
   const int64_t stride = int64_t(H) * D;
   const int64_t off = (tc.row0 * H + (hok ? h : H - 1)) * D + sub * DPL;
@@ -428,6 +578,23 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
     kb[i].load(kp + min(i, tlast) * stride);
     qb[i].load(qp + min(i, tlast) * stride);
   }
+  float zr[DPL], zi[DPL], cr[DPL], ci[DPL];
+  {
+    const int hl = hok ? h : H - 1;
+    const float2* sp = states + ((int64_t(tc.b) * NC + tc.chunk) * H + hl) * D + sub * DPL;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const float2 sv = sp[j];
+      zr[j] = zi[j] = 0.0f;
+      cr[j] = hok ? sv.x : 0.0f;
+      ci[j] = hok ? sv.y : 0.0f;
+    }
+  }
+
+  TileScalars s{smem4, smem4 + slots, reinterpret_cast<float2*>(smem4 + 2 * slots)};
+  float2* s_y = s.M + slots;
+  const ResetMask rm = stage_scalars<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, alpha, omega, c, s,
+                                                   nullptr, 0);
 #pragma unroll
   for (int i = 0; i < PF; ++i) {
     kb[i].pin();
@@ -436,12 +603,19 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
   __syncthreads();
 
   for (int tb = 0; tb < ntr; tb += PF) {
+    float4 sa[PF], sb[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      sa[i] = s.A[(tb + i) * HPW + hh];
+      sb[i] = s.B[(tb + i) * HPW + hh];
+    }
+    float yr[PF], yi[PF];
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int t = tb + i;
       float kk[DPL], qq[DPL];
-      kb[i].unpack(kk);
-      qb[i].unpack(qq);
+      kb[i].unpack_then_reload(kk);
+      qb[i].unpack_then_reload(qq);
       kb[i].load(kp + min(t + PF, tlast) * stride);
       qb[i].load(qp + min(t + PF, tlast) * stride);
 
@@ -460,11 +634,8 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
       pcr = group_sum<LPH>(pcr);
       pci = group_sum<LPH>(pci);
 
-      const int p = t * HPW + hh;
-      const float4 q4 = s.s4[p];
-      const float2 q2 = s.s2[p];
-      const float ar = q4.x, ai = q4.y, bb = q2.x;
-      local_step<DPL>(zr, zi, f, kk, ar, ai, q4.z, q4.w, bb, pzr, pzi);
+      const float bb = sa[i].z;
+      local_step<DPL>(zr, zi, kk, rm.test(t), s.M + t * HPW + hh, sa[i].x, sa[i].y, bb, pzr, pzi);
       const float ecr = bb * pcr, eci = bb * pci;
       float qzr = 0.0f, qzi = 0.0f;
 #pragma unroll
@@ -475,14 +646,15 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
         ci[j] = fmaf(-eci, kk[j], ci[j]);
       }
       // readout partial: f_t (zh_t.q) + g_{t-1} (c^_t.q)
-      float Rr = (f.fr * qzr - f.fi * qzi) + (gr * qcr - gi * qci);
-      float Ri = (f.fr * qzi + f.fi * qzr) + (gr * qci + gi * qcr);
-      Rr = group_sum<LPH>(Rr);
-      Ri = group_sum<LPH>(Ri);
-      if (sub == 0) s_y[p] = make_float2(q2.y * Rr, q2.y * Ri);
-      const float ngr = ar * gr - ai * gi;
-      gi = ar * gi + ai * gr;
-      gr = ngr;
+      const float4 fb = sb[i];
+      float Rr = (fb.x * qzr - fb.y * qzi) + (fb.z * qcr - fb.w * qci);
+      float Ri = (fb.x * qzi + fb.y * qzr) + (fb.z * qci + fb.w * qcr);
+      yr[i] = sa[i].w * group_sum<LPH>(Rr);
+      yi[i] = sa[i].w * group_sum<LPH>(Ri);
+    }
+    if (sub == 0) {
+#pragma unroll
+      for (int i = 0; i < PF; ++i) s_y[(tb + i) * HPW + hh] = make_float2(yr[i], yi[i]);
     }
   }
   __syncthreads();
@@ -547,12 +719,12 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   float2* gam = summ + w.n_summ;
   float2* segA = gam + w.n_gam;
   float2* segX = segA + w.n_segA;
-  const int slots = round_up(Q, kPrefetch) * HPW;
+  const int slots = round_up(Q, kWave) * HPW;
 
   hipLaunchKernelGGL((fused_fwd_summary_kernel<T, D, LPH>), dim3(unsigned(tiles)), dim3(kWave),
-                     size_t(slots) * (sizeof(float4) + sizeof(float2)), stream, (const raw*)k, (const raw*)v,
-                     (const raw*)beta, (const raw*)dt, (const raw*)r, alpha, omega, c, summ, gam, L, H,
-                     Q, NC, n_hg);
+                     size_t(slots) * (sizeof(float4) + sizeof(float2)) + HPW * sizeof(float4), stream,
+                     (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)dt, (const raw*)r, alpha,
+                     omega, c, summ, gam, L, H, Q, NC, n_hg);
   int st = cdssm_host::check_launch("cdssm_fused_scan_fwd/summary");
   if (st) return st;
 
@@ -568,9 +740,9 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   if (st) return st;
 
   hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH>), dim3(unsigned(tiles)), dim3(kWave),
-                     size_t(slots) * (sizeof(float4) + 2 * sizeof(float2)), stream, (const raw*)q, (const raw*)k,
-                     (const raw*)v, (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r,
-                     alpha, omega, c, (const float2*)summ, (raw*)y, L, H, Q, NC, n_hg);
+                     size_t(slots) * (2 * sizeof(float4) + 2 * sizeof(float2)), stream, (const raw*)q,
+                     (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c, (const raw*)dt,
+                     (const raw*)r, alpha, omega, c, (const float2*)summ, (raw*)y, L, H, Q, NC, n_hg);
   return cdssm_host::check_launch("cdssm_fused_scan_fwd/main");
 }
 
