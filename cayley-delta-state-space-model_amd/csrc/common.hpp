@@ -52,11 +52,16 @@ struct F32 {
 template <typename T, int DPL>
 struct RowVec {
   static constexpr int W = DPL * T::bytes / 4;
-  static_assert(W == 1 || W == 2 || W == 4, "a lane slice is one 4-, 8- or 16-byte load");
+  static_assert(W == 1 || W == 2 || W == 4 || W == 8, "a lane slice is 4, 8, 16 or 32 bytes");
   uint32_t u[W];
 
   __device__ __forceinline__ void load(const typename T::raw* p) {
-    if constexpr (W == 4) {
+    if constexpr (W == 8) {
+      const uint4 v0 = reinterpret_cast<const uint4*>(p)[0];
+      const uint4 v1 = reinterpret_cast<const uint4*>(p)[1];
+      u[0] = v0.x; u[1] = v0.y; u[2] = v0.z; u[3] = v0.w;
+      u[4] = v1.x; u[5] = v1.y; u[6] = v1.z; u[7] = v1.w;
+    } else if constexpr (W == 4) {
       const uint4 v = *reinterpret_cast<const uint4*>(p);
       u[0] = v.x; u[1] = v.y; u[2] = v.z; u[3] = v.w;
     } else if constexpr (W == 2) {
@@ -98,9 +103,9 @@ struct RowVec {
 
 // ---------------------------------------------------------------------------
 // Lane-group all-reduce (sum) over G consecutive lanes, G in {1,2,4,...,64}.
-// DPP quad permutes and row mirrors stay inside a 16-lane row; the 32-lane
-// stage uses a ds_swizzle xor; the 64-lane stage combines the two halves
-// through readlane.  Every lane of the group ends with the group sum.
+// DPP quad permutes and row mirrors stay inside a 16-lane row; the 32- and
+// 64-lane stages use the gfx950 row / half-wave swaps.  All stages are VALU
+// (no LDS round trip).  Every lane of the group ends with the group sum.
 // ---------------------------------------------------------------------------
 
 // Full-row permutes only (every source lane valid), so bound_ctrl never
@@ -118,13 +123,50 @@ __device__ __forceinline__ float group_sum(float x) {
   if constexpr (G >= 4) x += dpp<0x4E>(x);     // quad_perm [2,3,0,1]: lane ^ 2
   if constexpr (G >= 8) x += dpp<0x141>(x);    // row_half_mirror: other quad of the 8
   if constexpr (G >= 16) x += dpp<0x140>(x);   // row_mirror: other half of the row
-  if constexpr (G >= 32) x += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));
+  if constexpr (G >= 32) {
+    // v_permlane16_swap: each row meets its neighbour row (lane ^ 16)
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
   if constexpr (G >= 64) {
-    const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
-    const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
-    x = lo + hi;
+    // v_permlane32_swap: the two halves of the wave meet (lane ^ 32)
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
   }
   return x;
+}
+
+// ---------------------------------------------------------------------------
+// Tiles of the fused scan: one wave per (b, chunk, group of HPW heads).
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+// Decode blockIdx.x -> (b, chunk, head group).
+struct ChunkTile {
+  int b, chunk, hbase, t0, nt;
+  int64_t row0;
+};
+
+__device__ __forceinline__ ChunkTile decode_tile(int L, int Q, int NC, int n_hg, int HPW) {
+  ChunkTile c;
+  int g = blockIdx.x;
+  const int hg = g % n_hg;
+  g /= n_hg;
+  c.chunk = g % NC;
+  c.b = g / NC;
+  c.hbase = hg * HPW;
+  c.t0 = c.chunk * Q;
+  c.nt = min(Q, L - c.t0);
+  c.row0 = int64_t(c.b) * L + c.t0;
+  return c;
+}
+
+
+// x *= y (complex)
+__device__ __forceinline__ void cmul_acc(float& xr, float& xi, float yr, float yi) {
+  const float nr = xr * yr - xi * yi;
+  xi = xr * yi + xi * yr;
+  xr = nr;
 }
 
 // ---------------------------------------------------------------------------

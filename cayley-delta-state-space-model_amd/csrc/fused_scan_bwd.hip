@@ -30,155 +30,148 @@
 //               dv, dbeta, dsel_C, ddt, dr and per-chunk d alpha / d omega
 //   B4 heads:   deterministic sum of the per-chunk d alpha / d omega.
 //
-// Work layout of B1 and B3: one wave64 per (b, chunk, h); lane owns
-// DPL = D/64 state elements; per-token scalars are computed one token per
-// lane (two slots for 128-token chunks) and read back from LDS.
+// Work layout of B1 and B3: one wave64 per (b, chunk, group of HPW heads);
+// each head is owned by LPH = D/4 consecutive lanes, each lane holding 4
+// consecutive state elements (HPW = 4 for D = 64, 2 for D = 128); dot
+// products reduce over the head's lanes with DPP and row swaps.  Per-token
+// scalars are staged in LDS, one slot per (token, head), by lanes that each
+// own a block of tokens of one head.
 #include "common.hpp"
 
 namespace cdssm {
 
-constexpr int kBwdSeg = 16;
+constexpr int kBwdSeg = 16;   // chunks per reverse-carry segment
+// lanes per head: D/4, so every lane holds DPL = 4 state elements
+template <int D>
+struct BwdCfg {
+  static constexpr int LPH = D / 4;
+  static constexpr int HPW = kWave / LPH;
+  static constexpr int DPL = 4;
+};
+constexpr int kBwdMaxHPW = 4;
+constexpr int kBwdCK = 8;     // z checkpoint interval of the main pass
+constexpr int kBwdPF = 8;     // row prefetch depth
 
-__device__ __forceinline__ float rl(float x, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
-}
-// Full-wave sum, broadcast to every lane.
-__device__ __forceinline__ float wsum(float x) { return group_sum<64>(x); }
-
-struct BwdTile {
-  int b, chunk, h, t0, nt;
-  int64_t row0, tile;
+// Per-token scalars of a backward tile in LDS, slot p = t*HPW + j:
+//   S0 = (a_re, a_im, w_re, w_im)       transition and write (w = beta vp v)
+//   S1 = (beta, f_re, f_im, 0)          f = sel_C dy
+//   S2 = (h_re, h_im, gp_re, gp_im)     h = conj(g_t) f, gp = g_{t-1}
+struct BwdScalars {
+  float4 *S0, *S1, *S2;
 };
 
-__device__ __forceinline__ BwdTile bwd_tile(int L, int Q, int NC, int H) {
-  BwdTile c;
-  const int g = blockIdx.x;
-  c.tile = g;  // (b*NC + chunk)*H + h
-  c.h = g % H;
-  const int bc = g / H;
-  c.chunk = bc % NC;
-  c.b = bc / NC;
-  c.t0 = c.chunk * Q;
-  c.nt = min(Q, L - c.t0);
-  c.row0 = int64_t(c.b) * L + c.t0;
-  return c;
-}
-
-// Exclusive/inclusive complex prefix product over the tokens held one per
-// lane in two slots.  Returns inclusive g_t and exclusive g_{t-1} (g_{-1}=1).
-__device__ __forceinline__ void prefix_prod(const float (&ar)[2], const float (&ai)[2], float (&gr)[2],
-                                            float (&gi)[2], float (&gpr)[2], float (&gpi)[2]) {
+// Stage the per-token scalars of a tile, every slot of the slabs covering
+// [0, ntr).  Lane = (head j, block of TPB tokens); each lane loads and computes
+// its own tokens, runs g = prod a sequentially over them and joins the blocks
+// of its head with log2(NB) shuffle steps.  Slots past the last token and
+// heads >= H hold inert steps (a = 1, w = 0, beta = 0, f = 0).
+template <typename T, int HPW, bool WITH_W>
+__device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
+                                          const typename T::raw* __restrict__ v,
+                                          const typename T::raw* __restrict__ beta,
+                                          const typename T::raw* __restrict__ sel_c,
+                                          const typename T::raw* __restrict__ dt,
+                                          const typename T::raw* __restrict__ r,
+                                          const typename T::raw* __restrict__ dy, float al, float om,
+                                          float c, const BwdScalars& s) {
+  constexpr int NB = kWave / HPW, TPB = HPW;
   const int lane = threadIdx.x;
+  const int j = lane / NB;
+  const int blk = lane % NB;
+  const int hj = tc.hbase + j;
+  const bool hok = hj < H;
+  const int hl = hok ? hj : H - 1;
+  float cgr = 1.0f, cgi = 0.0f;  // g carried in from earlier slabs
+  for (int tl = 0; tl < ntr; tl += kWave) {
+    const int t0 = tl + blk * TPB;
+    float bb[TPB], dd[TPB], rr[TPB], v0[TPB], v1[TPB], sc[TPB], g0[TPB], g1[TPB];
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    float xr = ar[s], xi = ai[s];
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float yr = __shfl_up(xr, off, 64);
-      const float yi = __shfl_up(xi, off, 64);
-      if (lane >= off) {
-        const float nr = xr * yr - xi * yi;
-        xi = xr * yi + xi * yr;
-        xr = nr;
-      }
+    for (int i = 0; i < TPB; ++i) {
+      const int t = min(t0 + i, tc.nt - 1);
+      const int64_t e = (tc.row0 + t) * H + hl;
+      bb[i] = T::load(beta + e);
+      dd[i] = T::load(dt + e);
+      rr[i] = T::load(r + e);
+      v0[i] = WITH_W ? T::load(v + 2 * e) : 0.0f;
+      v1[i] = WITH_W ? T::load(v + 2 * e + 1) : 0.0f;
+      sc[i] = T::load(sel_c + e);
+      g0[i] = T::load(dy + 2 * e);
+      g1[i] = T::load(dy + 2 * e + 1);
     }
-    gr[s] = xr;
-    gi[s] = xi;
-  }
-  // slot 1 continues after slot 0's total
-  const float tr = rl(gr[0], 63), ti = rl(gi[0], 63);
-  {
-    const float nr = gr[1] * tr - gi[1] * ti;
-    gi[1] = gr[1] * ti + gi[1] * tr;
-    gr[1] = nr;
-  }
+    float ar[TPB], ai[TPB], Gr[TPB], Gi[TPB];
+    float gpr = 1.0f, gpi = 0.0f;
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    float er = __shfl_up(gr[s], 1, 64), ei = __shfl_up(gi[s], 1, 64);
-    if (lane == 0) {
-      er = s == 0 ? 1.0f : tr;
-      ei = s == 0 ? 0.0f : ti;
+    for (int i = 0; i < TPB; ++i) {
+      const bool real = hok && t0 + i < tc.nt;
+      const Transition tr = cayley_gated(dd[i], rr[i], al, om, c);
+      ar[i] = real ? tr.ar : 1.0f;
+      ai[i] = real ? tr.ai : 0.0f;
+      const float f = bb[i] * tr.vp;
+      v0[i] = real ? f * v0[i] : 0.0f;  // w
+      v1[i] = real ? f * v1[i] : 0.0f;
+      bb[i] = real ? bb[i] : 0.0f;
+      g0[i] = real ? sc[i] * g0[i] : 0.0f;  // f = sel dy
+      g1[i] = real ? sc[i] * g1[i] : 0.0f;
+      cmul_acc(gpr, gpi, ar[i], ai[i]);
+      Gr[i] = gpr;
+      Gi[i] = gpi;
     }
-    gpr[s] = er;
-    gpi[s] = ei;
+    // g entering the block: exclusive product over the head's earlier blocks
+    float xgr = gpr, xgi = gpi;
+#pragma unroll
+    for (int off = 1; off < NB; off <<= 1) {
+      const float ygr = __shfl_up(xgr, off, NB), ygi = __shfl_up(xgi, off, NB);
+      if (blk >= off) cmul_acc(xgr, xgi, ygr, ygi);
+    }
+    float egr = __shfl_up(xgr, 1, NB), egi = __shfl_up(xgi, 1, NB);
+    if (blk == 0) {
+      egr = 1.0f;
+      egi = 0.0f;
+    }
+    cmul_acc(egr, egi, cgr, cgi);
+#pragma unroll
+    for (int i = 0; i < TPB; ++i) {
+      const int p = (t0 + i) * HPW + j;
+      float gr = egr, gi = egi;  // g_t
+      cmul_acc(gr, gi, Gr[i], Gi[i]);
+      float pr = egr, pi = egi;  // g_{t-1}
+      if (i > 0) cmul_acc(pr, pi, Gr[i - 1], Gi[i - 1]);
+      if (WITH_W) s.S0[p] = make_float4(ar[i], ai[i], v0[i], v1[i]);
+      s.S1[p] = make_float4(bb[i], g0[i], g1[i], 0.0f);
+      s.S2[p] = make_float4(gr * g0[i] + gi * g1[i], gr * g1[i] - gi * g0[i], pr, pi);
+    }
+    float gtr = egr, gti = egi;
+    cmul_acc(gtr, gti, gpr, gpi);
+    cgr = __shfl(gtr, j * NB + NB - 1, kWave);
+    cgi = __shfl(gti, j * NB + NB - 1, kWave);
   }
 }
 
-// Per-token inputs of a chunk tile, one token per lane (two slots).
-template <typename T>
-struct TokenInputs {
-  float ar[2], ai[2], vp[2], vr[2], vi[2], b[2], sel[2], dyr[2], dyi[2], dt[2], r[2];
-
-  __device__ __forceinline__ void load(const BwdTile& tc, int H, const typename T::raw* v,
-                                       const typename T::raw* beta, const typename T::raw* sel_c,
-                                       const typename T::raw* dtp, const typename T::raw* rp,
-                                       const typename T::raw* dy, float alpha, float omega, float c) {
-    const int lane = threadIdx.x;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int t = lane + 64 * s;
-      const int tcl = min(t, tc.nt - 1);
-      const int64_t e = (tc.row0 + tcl) * H + tc.h;
-      const float bb = T::load(beta + e), d = T::load(dtp + e), rr = T::load(rp + e);
-      const float v0 = T::load(v + 2 * e), v1 = T::load(v + 2 * e + 1);
-      const float sc = T::load(sel_c + e);
-      const float g0 = T::load(dy + 2 * e), g1 = T::load(dy + 2 * e + 1);
-      const bool real = t < tc.nt;
-      const Transition tr = cayley_gated(d, rr, alpha, omega, c);
-      ar[s] = real ? tr.ar : 1.0f;
-      ai[s] = real ? tr.ai : 0.0f;
-      vp[s] = real ? tr.vp : 0.0f;
-      vr[s] = real ? v0 : 0.0f;
-      vi[s] = real ? v1 : 0.0f;
-      b[s] = real ? bb : 0.0f;
-      sel[s] = real ? sc : 0.0f;
-      dyr[s] = real ? g0 : 0.0f;
-      dyi[s] = real ? g1 : 0.0f;
-      dt[s] = d;
-      r[s] = rr;
-    }
-  }
-};
-
-// A lane's DPL contiguous state columns d = lane*DPL + j of one row.
+// Store a lane's DPL consecutive elements (bf16 pairs packed into dwords).
 template <typename T, int DPL>
-struct Cols {
-  float x[DPL];
-  __device__ __forceinline__ void load(const typename T::raw* p) {
+__device__ __forceinline__ void store_row(typename T::raw* p, const float (&x)[DPL]) {
+  if constexpr (T::bytes == 2) {
+    uint32_t u[DPL / 2];
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) x[j] = T::load(p + j);
+    for (int i = 0; i < DPL / 2; ++i) u[i] = uint32_t(f32_to_bf16(x[2 * i])) | (uint32_t(f32_to_bf16(x[2 * i + 1])) << 16);
+    if constexpr (DPL == 8) {
+      *reinterpret_cast<uint4*>(p) = make_uint4(u[0], u[1], u[2], u[3]);
+    } else if constexpr (DPL == 4) {
+      *reinterpret_cast<uint2*>(p) = make_uint2(u[0], u[1]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < DPL / 2; ++i) reinterpret_cast<uint32_t*>(p)[i] = u[i];
+    }
+  } else {
+    if constexpr (DPL % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < DPL / 4; ++i)
+        reinterpret_cast<float4*>(p)[i] = make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) p[i] = x[i];
+    }
   }
-  // Opaque copy that keeps prefetched values in their registers (see RowVec::pin).
-  __device__ __forceinline__ void pin() {
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) asm volatile("" : "+v"(x[j]));
-  }
-};
-
-// Sum of NV <= 8 values over the 64 lanes of a one-wave block, returned to
-// every lane.  Transposes through LDS: lane l writes its NV partials, then
-// lane l adds 8 lanes' partials of value l%8, and three swizzle/permute
-// stages combine the 8 blocks.  scratch: 8*65 floats.
-template <int NV>
-__device__ __forceinline__ void wave_reduce(float (&v)[NV], float* scratch) {
-  static_assert(NV >= 1 && NV <= 8, "up to 8 values");
-  const int lane = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) scratch[i * 65 + lane] = v[i];
-  asm volatile("" ::: "memory");
-  const int vi = lane & 7, blk = lane >> 3;
-  float s = 0.0f;
-  if (vi < NV) {
-    const float* row = scratch + vi * 65 + blk * 8;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s += row[i];
-  }
-  s += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(s), 0x201F));  // lane ^ 8
-  s += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(s), 0x401F));  // lane ^ 16
-  s += __shfl_xor(s, 32, 64);
-  asm volatile("" ::: "memory");
-#pragma unroll
-  for (int i = 0; i < NV; ++i) v[i] = rl(s, i);
 }
 
 // ---------------------------------------------------------------------------
@@ -189,87 +182,86 @@ __device__ __forceinline__ void wave_reduce(float (&v)[NV], float* scratch) {
 template <typename T, int D>
 __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
     const typename T::raw* __restrict__ q, const typename T::raw* __restrict__ k,
-    const typename T::raw* __restrict__ v, const typename T::raw* __restrict__ beta,
-    const typename T::raw* __restrict__ sel_c, const typename T::raw* __restrict__ dt,
-    const typename T::raw* __restrict__ r, const float* __restrict__ alpha,
-    const float* __restrict__ omega, float c, const typename T::raw* __restrict__ dy,
-    float2* __restrict__ lam0, int L, int H, int Q, int NC) {
-  constexpr int DPL = D / kWave, PF = 8;
-  __shared__ float4 sh[128];  // (h_re, h_im, beta, 0) per token
-  const BwdTile tc = bwd_tile(L, Q, NC, H);
+    const typename T::raw* __restrict__ beta, const typename T::raw* __restrict__ sel_c,
+    const typename T::raw* __restrict__ dt, const typename T::raw* __restrict__ r,
+    const float* __restrict__ alpha, const float* __restrict__ omega, float c,
+    const typename T::raw* __restrict__ dy, float2* __restrict__ lam0, int L, int H, int Q, int NC,
+    int n_hg) {
+  constexpr int LPH = BwdCfg<D>::LPH, HPW = BwdCfg<D>::HPW, DPL = BwdCfg<D>::DPL, PF = kBwdPF;
+  extern __shared__ float4 smem4[];
+  const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
-  {
-    TokenInputs<T> in;
-    in.load(tc, H, v, beta, sel_c, dt, r, dy, alpha[tc.h], omega[tc.h], c);
-    float gr[2], gi[2], gpr[2], gpi[2];
-    prefix_prod(in.ar, in.ai, gr, gi, gpr, gpi);
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      const int t = lane + 64 * s2;
-      if (t < Q) {
-        const float fr = in.sel[s2] * in.dyr[s2], fi = in.sel[s2] * in.dyi[s2];
-        sh[t] = make_float4(gr[s2] * fr + gi[s2] * fi, gr[s2] * fi - gi[s2] * fr, in.b[s2], 0.0f);
-      }
-    }
-  }
-  __syncthreads();
+  const int hh = lane / LPH, sub = lane % LPH;
+  const int h = tc.hbase + hh;
+  const bool hok = h < H;
+  const int hl = hok ? h : H - 1;
+  const int slots = round_up(Q, kWave) * HPW;
+  const int ntr = round_up(tc.nt, PF);
 
   const int64_t stride = int64_t(H) * D;
-  const int64_t off = (tc.row0 * H + tc.h) * D + lane * DPL;
+  const int64_t off = (tc.row0 * H + hl) * D + sub * DPL;
   const typename T::raw* kp = k + off;
   const typename T::raw* qp = q + off;
   const int tlast = tc.nt - 1;
-  float lr[DPL], li[DPL];
-#pragma unroll
-  for (int j = 0; j < DPL; ++j) lr[j] = li[j] = 0.0f;
-  // reverse order, rows prefetched PF tokens ahead
-  Cols<T, DPL> kb[PF], qb[PF];
+  // reverse ring: slot i holds token ntr-1-(tb+i)
+  RowVec<T, DPL> kb[PF], qb[PF];
 #pragma unroll
   for (int i = 0; i < PF; ++i) {
-    const int t = max(tlast - i, 0);
-    kb[i].load(kp + t * stride);
-    qb[i].load(qp + t * stride);
+    kb[i].load(kp + min(ntr - 1 - i, tlast) * stride);
+    qb[i].load(qp + min(ntr - 1 - i, tlast) * stride);
   }
+  BwdScalars s{nullptr, smem4, smem4 + slots};
+  stage_bwd<T, HPW, false>(tc, H, ntr, nullptr, beta, sel_c, dt, r, dy, alpha[hl], omega[hl], c, s);
 #pragma unroll
   for (int i = 0; i < PF; ++i) {
     kb[i].pin();
     qb[i].pin();
   }
-  const int nr = (tc.nt + PF - 1) / PF * PF;
-  for (int ib = 0; ib < nr; ib += PF) {
+  __syncthreads();
+
+  float lr[DPL], li[DPL];
+#pragma unroll
+  for (int jj = 0; jj < DPL; ++jj) lr[jj] = li[jj] = 0.0f;
+  for (int tb = 0; tb < ntr; tb += PF) {
+    float4 s1[PF], s2[PF];
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      const int t = tlast - (ib + i);  // may go negative: inert (h = 0, beta = 0)
-      float kk[DPL], qq[DPL];
+      const int p = (ntr - 1 - (tb + i)) * HPW + hh;
+      s1[i] = s.S1[p];
+      s2[i] = s.S2[p];
+    }
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        kk[j] = kb[i].x[j];
-        qq[j] = qb[i].x[j];
-      }
-      const int tn = max(t - PF, 0);
-      kb[i].load(kp + tn * stride);
-      qb[i].load(qp + tn * stride);
-      const float4 hv = t >= 0 ? sh[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int i = 0; i < PF; ++i) {
+      const int t = ntr - 1 - (tb + i);
+      float kk[DPL], qq[DPL];
+      kb[i].unpack_then_reload(kk);
+      qb[i].unpack_then_reload(qq);
+      kb[i].load(kp + max(min(t - PF, tlast), 0) * stride);
+      qb[i].load(qp + max(min(t - PF, tlast), 0) * stride);
+      // padded steps have h = 0 and beta = 0
       float sr = 0.0f, si = 0.0f;
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        lr[j] = fmaf(hv.x, qq[j], lr[j]);
-        li[j] = fmaf(hv.y, qq[j], li[j]);
-        sr = fmaf(lr[j], kk[j], sr);
-        si = fmaf(li[j], kk[j], si);
+      for (int jj = 0; jj < DPL; ++jj) {
+        lr[jj] = fmaf(s2[i].x, qq[jj], lr[jj]);
+        li[jj] = fmaf(s2[i].y, qq[jj], li[jj]);
+        sr = fmaf(lr[jj], kk[jj], sr);
+        si = fmaf(li[jj], kk[jj], si);
       }
-      sr = wsum(sr);
-      si = wsum(si);
+      sr = group_sum<LPH>(sr);
+      si = group_sum<LPH>(si);
+      const float br = s1[i].x * sr, bi = s1[i].x * si;
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        lr[j] = fmaf(-hv.z * sr, kk[j], lr[j]);
-        li[j] = fmaf(-hv.z * si, kk[j], li[j]);
+      for (int jj = 0; jj < DPL; ++jj) {
+        lr[jj] = fmaf(-br, kk[jj], lr[jj]);
+        li[jj] = fmaf(-bi, kk[jj], li[jj]);
       }
     }
   }
-  float2* o = lam0 + tc.tile * D + lane * DPL;
+  if (hok) {
+    float2* lp = lam0 + ((int64_t(tc.b) * NC + tc.chunk) * H + h) * D + sub * DPL;
 #pragma unroll
-  for (int j = 0; j < DPL; ++j) o[j] = make_float2(lr[j], li[j]);
+    for (int jj = 0; jj < DPL; ++jj) lp[jj] = make_float2(lr[jj], li[jj]);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -411,28 +403,17 @@ __device__ __forceinline__ DynGrad cayley_gated_bwd(float dt, float r, float alp
 // B3: per-chunk backward of both branches.
 //   forward pass: z and c^ from (0, s_k); per token keeps p_t = z_{t-1}.k_t,
 //     pc_t = c^_t.k_t, Y_t.q_t and the correction's delta g_t in LDS, emits dq,
-//     and stores z every CK tokens;
-//   reverse pass, CK tokens at a time: z of the segment is recomputed from its
-//     checkpoint with the stored p_t (no reductions); c^_t is rebuilt backward,
-//     exactly, as c^_t = c^_{t+1} + beta_t pc_t k_t; the local adjoint mu and
-//     the correction adjoint lambda step back and dk is emitted;
-//   epilogue, one token per lane: dynamics chain rule, dv, dbeta, dsel, ddt,
-//     dr, and the chunk's d alpha / d omega partial.
-// LDS (float4 per token unless noted): S0 (a, w), S1 (beta, f = sel dy),
-// S2 (h = conj(g_t) f, g_{t-1}), P (p, pc), G (delta g, Y.q), R (da, dw),
-// RB (dbeta from the erasures, float), z checkpoints, reduction scratch.
+//     and stores z every kBwdCK tokens in the checkpoint workspace;
+//   reverse pass, kBwdCK tokens at a time: z of the segment is recomputed
+//     from its checkpoint with the stored p_t (no reductions); c^_t is rebuilt
+//     backward, exactly, as c^_t = c^_{t+1} + beta_t pc_t k_t; the local adjoint
+//     mu and the correction adjoint lambda step back and dk is emitted;
+//   epilogue, lanes owning blocks of tokens: dynamics chain rule, dv, dbeta,
+//     dsel, ddt, dr, and the chunk's d alpha / d omega per head.
+// LDS (float4 per (token, head) slot): S0, S1, S2 (staged scalars), P = (p,
+// pc), then (da, dw) after the reverse pass, G = (delta g, Y.q), then
+// (dbeta_erase, 0, Y.q).
 // ---------------------------------------------------------------------------
-template <int D>
-struct BwdSmem {
-  static constexpr int DPL = D / kWave;
-  static constexpr int CK = 16;
-  static constexpr int QMAX = 128;
-  float4 S0[QMAX], S1[QMAX], S2[QMAX], P[QMAX], G[QMAX], R[QMAX];
-  float RB[QMAX];
-  float2 ck[QMAX / CK][kWave * DPL];
-  float red[8 * 65];
-};
-
 template <typename T, int D>
 __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
     const typename T::raw* __restrict__ q, const typename T::raw* __restrict__ k,
@@ -440,128 +421,127 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
     const typename T::raw* __restrict__ sel_c, const typename T::raw* __restrict__ dt,
     const typename T::raw* __restrict__ r, const float* __restrict__ alpha,
     const float* __restrict__ omega, float c, const typename T::raw* __restrict__ dy,
-    const float2* __restrict__ states, const float2* __restrict__ dsn, typename T::raw* __restrict__ dq,
-    typename T::raw* __restrict__ dk, typename T::raw* __restrict__ dv,
+    const float2* __restrict__ states, const float2* __restrict__ dsn, float2* __restrict__ ckpt,
+    typename T::raw* __restrict__ dq, typename T::raw* __restrict__ dk, typename T::raw* __restrict__ dv,
     typename T::raw* __restrict__ dbeta, typename T::raw* __restrict__ dsel,
-    typename T::raw* __restrict__ ddt, typename T::raw* __restrict__ dr,
-    float2* __restrict__ dhead_parts, int L, int H, int Q, int NC) {
-  using SM = BwdSmem<D>;
-  constexpr int DPL = SM::DPL, CK = SM::CK, PF = 8;
-  __shared__ SM sm;
-  const BwdTile tc = bwd_tile(L, Q, NC, H);
+    typename T::raw* __restrict__ ddt, typename T::raw* __restrict__ dr, float2* __restrict__ dhead_parts,
+    int L, int H, int Q, int NC, int n_hg) {
+  constexpr int LPH = BwdCfg<D>::LPH, HPW = BwdCfg<D>::HPW, DPL = BwdCfg<D>::DPL, PF = kBwdPF, CK = kBwdCK;
+  static_assert(PF == CK, "checkpoints fall on prefetch-group starts");
+  extern __shared__ float4 smem4[];
+  const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
-  const float al = alpha[tc.h], om = omega[tc.h];
-
-  // ---- per-token scalars (lane = token, two slots) ----
-  TokenInputs<T> in;
-  in.load(tc, H, v, beta, sel_c, dt, r, dy, al, om, c);
-  {
-    float gr[2], gi[2], gpr[2], gpi[2];
-    prefix_prod(in.ar, in.ai, gr, gi, gpr, gpi);
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      const int t = lane + 64 * s2;
-      if (t < Q) {
-        const float f = in.b[s2] * in.vp[s2];
-        const float fr = in.sel[s2] * in.dyr[s2], fi = in.sel[s2] * in.dyi[s2];
-        sm.S0[t] = make_float4(in.ar[s2], in.ai[s2], f * in.vr[s2], f * in.vi[s2]);
-        sm.S1[t] = make_float4(in.b[s2], fr, fi, 0.0f);
-        sm.S2[t] = make_float4(gr[s2] * fr + gi[s2] * fi, gr[s2] * fi - gi[s2] * fr, gpr[s2], gpi[s2]);
-      }
-    }
-  }
-  __syncthreads();
+  const int hh = lane / LPH, sub = lane % LPH;
+  const int h = tc.hbase + hh;
+  const bool hok = h < H;
+  const int hl = hok ? h : H - 1;
+  const int slots = round_up(Q, kWave) * HPW;
+  const int ntr = round_up(tc.nt, PF);
+  const int nseg = round_up(Q, CK) / CK;
+  const float al = alpha[hl], om = omega[hl];
 
   const int64_t stride = int64_t(H) * D;
-  const int64_t off = (tc.row0 * H + tc.h) * D + lane * DPL;
+  const int64_t off = (tc.row0 * H + hl) * D + sub * DPL;
   const typename T::raw* kp = k + off;
   const typename T::raw* qp = q + off;
   const int tlast = tc.nt - 1;
-  const int ntr = (tc.nt + CK - 1) / CK * CK;
+  const int64_t chh = (int64_t(tc.b) * NC + tc.chunk) * H + hl;  // (b, chunk, head) index
+  float2* ck = ckpt + ((int64_t(blockIdx.x) * HPW + hh) * nseg) * D + sub * DPL;
+
+  RowVec<T, DPL> kb[PF], qb[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) {
+    kb[i].load(kp + min(i, tlast) * stride);
+    qb[i].load(qp + min(i, tlast) * stride);
+  }
+  float zr[DPL], zi[DPL], cr[DPL], ci[DPL];
+  const float2* sp = states + chh * D + sub * DPL;
+#pragma unroll
+  for (int jj = 0; jj < DPL; ++jj) {
+    const float2 sv = sp[jj];
+    zr[jj] = zi[jj] = 0.0f;
+    cr[jj] = hok ? sv.x : 0.0f;
+    ci[jj] = hok ? sv.y : 0.0f;
+  }
+  BwdScalars s{smem4, smem4 + slots, smem4 + 2 * slots};
+  float4* sP = smem4 + 3 * slots;
+  float4* sG = smem4 + 4 * slots;
+  stage_bwd<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, dy, al, om, c, s);
+#pragma unroll
+  for (int i = 0; i < PF; ++i) {
+    kb[i].pin();
+    qb[i].pin();
+  }
+  __syncthreads();
 
   // ---- forward pass ----
-  float zr[DPL], zi[DPL], cr[DPL], ci[DPL];
-  const float2* sp = states + tc.tile * D + lane * DPL;
+  for (int tb = 0; tb < ntr; tb += PF) {
+    // checkpoint z_{tb-1}
 #pragma unroll
-  for (int j = 0; j < DPL; ++j) {
-    zr[j] = zi[j] = 0.0f;
-    cr[j] = sp[j].x;
-    ci[j] = sp[j].y;
-  }
-  {
-    Cols<T, DPL> kb[PF], qb[PF];
+    for (int jj = 0; jj < DPL; ++jj) ck[(tb / CK) * D + jj] = make_float2(zr[jj], zi[jj]);
+    float4 s0[PF], s1[PF], s2[PF];
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      kb[i].load(kp + min(i, tlast) * stride);
-      qb[i].load(qp + min(i, tlast) * stride);
+      const int p = (tb + i) * HPW + hh;
+      s0[i] = s.S0[p];
+      s1[i] = s.S1[p];
+      s2[i] = s.S2[p];
     }
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      kb[i].pin();
-      qb[i].pin();
-    }
-    for (int tb = 0; tb < ntr; tb += PF) {
+      const int t = tb + i;
+      float kk[DPL], qq[DPL];
+      kb[i].unpack_then_reload(kk);
+      qb[i].unpack_then_reload(qq);
+      kb[i].load(kp + min(t + PF, tlast) * stride);
+      qb[i].load(qp + min(t + PF, tlast) * stride);
+      float pr = 0.0f, pi = 0.0f, pcr = 0.0f, pci = 0.0f;
 #pragma unroll
-      for (int i = 0; i < PF; ++i) {
-        const int t = tb + i;
-        float kk[DPL], qq[DPL];
+      for (int jj = 0; jj < DPL; ++jj) {
+        pr = fmaf(zr[jj], kk[jj], pr);
+        pi = fmaf(zi[jj], kk[jj], pi);
+        pcr = fmaf(cr[jj], kk[jj], pcr);
+        pci = fmaf(ci[jj], kk[jj], pci);
+      }
+      pr = group_sum<LPH>(pr);
+      pi = group_sum<LPH>(pi);
+      pcr = group_sum<LPH>(pcr);
+      pci = group_sum<LPH>(pci);
+      const float ar = s0[i].x, ai = s0[i].y, bb = s1[i].x, fr = s1[i].y, fi = s1[i].z;
+      const float gpr = s2[i].z, gpi = s2[i].w;
+      const float bpr = bb * pr, bpi = bb * pi;
+      const float er = s0[i].z - (ar * bpr - ai * bpi);
+      const float ei = s0[i].w - (ar * bpi + ai * bpr);
+      const float ecr = bb * pcr, eci = bb * pci;
+      float yqr = 0.0f, yqi = 0.0f, cqr = 0.0f, cqi = 0.0f;
+      float dqv[DPL];
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-          kk[j] = kb[i].x[j];
-          qq[j] = qb[i].x[j];
-        }
-        kb[i].load(kp + min(t + PF, tlast) * stride);
-        qb[i].load(qp + min(t + PF, tlast) * stride);
-        if (t % CK == 0) {
-#pragma unroll
-          for (int j = 0; j < DPL; ++j) sm.ck[t / CK][lane * DPL + j] = make_float2(zr[j], zi[j]);
-        }
-        if (t < tc.nt) {
-          const float4 s0 = sm.S0[t], s1 = sm.S1[t], s2 = sm.S2[t];
-          float red[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-          for (int j = 0; j < DPL; ++j) {
-            red[0] = fmaf(zr[j], kk[j], red[0]);
-            red[1] = fmaf(zi[j], kk[j], red[1]);
-            red[2] = fmaf(cr[j], kk[j], red[2]);
-            red[3] = fmaf(ci[j], kk[j], red[3]);
-          }
-          wave_reduce<4>(red, sm.red);
-          const float pr = red[0], pi = red[1], pcr = red[2], pci = red[3];
-          const float ar = s0.x, ai = s0.y, bb = s1.x;
-          const float bpr = bb * pr, bpi = bb * pi;
-          const float er = s0.z - (ar * bpr - ai * bpi);
-          const float ei = s0.w - (ar * bpi + ai * bpr);
-          const float ecr = bb * pcr, eci = bb * pci;
-          float o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-          float dqv[DPL];
-#pragma unroll
-          for (int j = 0; j < DPL; ++j) {
-            const float nr = fmaf(ar, zr[j], fmaf(-ai, zi[j], er * kk[j]));
-            const float ni = fmaf(ar, zi[j], fmaf(ai, zr[j], ei * kk[j]));
-            // Y_t = z_t + g_{t-1} c^_t
-            const float Yr = nr + s2.z * cr[j] - s2.w * ci[j];
-            const float Yi = ni + s2.z * ci[j] + s2.w * cr[j];
-            dqv[j] = Yr * s1.y + Yi * s1.z;
-            o4[0] = fmaf(Yr, qq[j], o4[0]);
-            o4[1] = fmaf(Yi, qq[j], o4[1]);
-            zr[j] = nr;
-            zi[j] = ni;
-            cr[j] = fmaf(-ecr, kk[j], cr[j]);
-            ci[j] = fmaf(-eci, kk[j], ci[j]);
-            o4[2] = fmaf(cr[j], qq[j], o4[2]);
-            o4[3] = fmaf(ci[j], qq[j], o4[3]);
-          }
-          const int64_t o = off + int64_t(t) * stride;
-#pragma unroll
-          for (int j = 0; j < DPL; ++j) T::store(dq + o + j, dqv[j]);
-          wave_reduce<4>(o4, sm.red);
-          if (lane == 0) {
-            // delta g_t = f conj(c^_{t+1}.q)
-            sm.P[t] = make_float4(pr, pi, pcr, pci);
-            sm.G[t] = make_float4(s1.y * o4[2] + s1.z * o4[3], s1.z * o4[2] - s1.y * o4[3], o4[0], o4[1]);
-          }
-        }
+      for (int jj = 0; jj < DPL; ++jj) {
+        const float nr = fmaf(ar, zr[jj], fmaf(-ai, zi[jj], er * kk[jj]));
+        const float ni = fmaf(ar, zi[jj], fmaf(ai, zr[jj], ei * kk[jj]));
+        // Y_t = z_t + g_{t-1} c^_t
+        const float Yr = nr + gpr * cr[jj] - gpi * ci[jj];
+        const float Yi = ni + gpr * ci[jj] + gpi * cr[jj];
+        dqv[jj] = Yr * fr + Yi * fi;
+        yqr = fmaf(Yr, qq[jj], yqr);
+        yqi = fmaf(Yi, qq[jj], yqi);
+        zr[jj] = nr;
+        zi[jj] = ni;
+        cr[jj] = fmaf(-ecr, kk[jj], cr[jj]);
+        ci[jj] = fmaf(-eci, kk[jj], ci[jj]);
+        cqr = fmaf(cr[jj], qq[jj], cqr);
+        cqi = fmaf(ci[jj], qq[jj], cqi);
+      }
+      if (t < tc.nt && hok) store_row<T, DPL>(dq + off + int64_t(t) * stride, dqv);
+      yqr = group_sum<LPH>(yqr);
+      yqi = group_sum<LPH>(yqi);
+      cqr = group_sum<LPH>(cqr);
+      cqi = group_sum<LPH>(cqi);
+      if (sub == 0) {
+        const int p = t * HPW + hh;
+        sP[p] = make_float4(pr, pi, pcr, pci);
+        // delta g_t = f conj(c^_{t+1}.q)
+        sG[p] = make_float4(fr * cqr + fi * cqi, fi * cqr - fr * cqi, yqr, yqi);
       }
     }
   }
@@ -569,84 +549,88 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
 
   // ---- reverse pass ----
   float mr[DPL], mi[DPL], lr[DPL], li[DPL];
-  float dG[2] = {0.0f, 0.0f};
+  float dGr = 0.0f, dGi = 0.0f;
   {
-    const float2* dp = dsn + tc.tile * D + lane * DPL;
+    const float2* dp = dsn + chh * D + sub * DPL;
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const float2 ds = dp[j];
-      const float2 s0 = sp[j];
-      mr[j] = ds.x;
-      mi[j] = ds.y;
-      lr[j] = li[j] = 0.0f;
-      dG[0] = fmaf(ds.x, s0.x, fmaf(ds.y, s0.y, dG[0]));
-      dG[1] = fmaf(ds.y, s0.x, fmaf(-ds.x, s0.y, dG[1]));
+    for (int jj = 0; jj < DPL; ++jj) {
+      const float2 ds = dp[jj];
+      const float2 s0 = sp[jj];
+      mr[jj] = ds.x;
+      mi[jj] = ds.y;
+      lr[jj] = li[jj] = 0.0f;
+      dGr = fmaf(ds.x, s0.x, fmaf(ds.y, s0.y, dGr));
+      dGi = fmaf(ds.y, s0.x, fmaf(-ds.x, s0.y, dGi));
     }
-    wave_reduce<2>(dG, sm.red);
+    dGr = group_sum<LPH>(dGr);
+    dGi = group_sum<LPH>(dGi);
   }
   float psr = 0.0f, psi = 0.0f;  // psi_{t+1}
   float anr = 1.0f, ani = 0.0f;  // a_{t+1}
   for (int seg = ntr / CK - 1; seg >= 0; --seg) {
     const int tb = seg * CK;
-    Cols<T, DPL> ks[CK], qs[CK];
+    RowVec<T, DPL> ks[CK], qs[CK];
 #pragma unroll
     for (int i = 0; i < CK; ++i) {
       ks[i].load(kp + min(tb + i, tlast) * stride);
       qs[i].load(qp + min(tb + i, tlast) * stride);
     }
-    // z_{tb-1+i} for i = 0..CK (recomputed with the stored p_t)
+    // z_{tb-1+i} for i = 0..CK, recomputed with the stored p_t
     float zbr[CK + 1][DPL], zbi[CK + 1][DPL];
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const float2 z0 = sm.ck[seg][lane * DPL + j];
-      zbr[0][j] = z0.x;
-      zbi[0][j] = z0.y;
+    for (int jj = 0; jj < DPL; ++jj) {
+      const float2 z0 = ck[seg * D + jj];
+      zbr[0][jj] = z0.x;
+      zbi[0][jj] = z0.y;
     }
 #pragma unroll
     for (int i = 0; i < CK; ++i) {
-      const int t = tb + i;
-      // steps past the chunk's last token are inert (their LDS slots may be unset)
-      const bool real = t < tc.nt;
-      const float4 s0 = sm.S0[t];
-      const float4 pv = sm.P[t];
-      const float bb = sm.S1[t].x;
-      const float ar = real ? s0.x : 1.0f, ai = real ? s0.y : 0.0f;
-      const float wr = real ? s0.z : 0.0f, wi = real ? s0.w : 0.0f;
-      const float bpr = real ? bb * pv.x : 0.0f, bpi = real ? bb * pv.y : 0.0f;
-      const float er = wr - (ar * bpr - ai * bpi);
-      const float ei = wi - (ar * bpi + ai * bpr);
+      const int p = (tb + i) * HPW + hh;
+      const float4 s0 = s.S0[p];
+      const float bb = s.S1[p].x;
+      const float4 pv = sP[p];
+      // slots past the last token are inert: a = 1, w = 0, beta = 0 (p may be stale)
+      const float bpr = bb * pv.x, bpi = bb * pv.y;
+      const float er = s0.z - (s0.x * bpr - s0.y * bpi);
+      const float ei = s0.w - (s0.x * bpi + s0.y * bpr);
+      float kk[DPL];
+      ks[i].unpack(kk);
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        zbr[i + 1][j] = fmaf(ar, zbr[i][j], fmaf(-ai, zbi[i][j], er * ks[i].x[j]));
-        zbi[i + 1][j] = fmaf(ar, zbi[i][j], fmaf(ai, zbr[i][j], ei * ks[i].x[j]));
+      for (int jj = 0; jj < DPL; ++jj) {
+        zbr[i + 1][jj] = fmaf(s0.x, zbr[i][jj], fmaf(-s0.y, zbi[i][jj], er * kk[jj]));
+        zbi[i + 1][jj] = fmaf(s0.x, zbi[i][jj], fmaf(s0.y, zbr[i][jj], ei * kk[jj]));
       }
     }
 #pragma unroll
     for (int i = CK - 1; i >= 0; --i) {
       const int t = tb + i;
       if (t < tc.nt) {
-        const float4 s0 = sm.S0[t], s1 = sm.S1[t], s2 = sm.S2[t], pv = sm.P[t], gv = sm.G[t];
+        const int p = t * HPW + hh;
+        const float4 s0 = s.S0[p], s1 = s.S1[p], s2 = s.S2[p], pv = sP[p], gv = sG[p];
         const float ar = s0.x, ai = s0.y, wr = s0.z, wi = s0.w, bb = s1.x;
         const float pr = pv.x, pi = pv.y, pcr = pv.z, pci = pv.w;
+        float kk[DPL], qq[DPL];
+        ks[i].unpack(kk);
+        qs[i].unpack(qq);
         float red[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-          const float kv = ks[i].x[j], qv = qs[i].x[j];
+        for (int jj = 0; jj < DPL; ++jj) {
           // c^_t = c^_{t+1} + beta pc k
-          cr[j] = fmaf(bb * pcr, kv, cr[j]);
-          ci[j] = fmaf(bb * pci, kv, ci[j]);
-          mr[j] = fmaf(s1.y, qv, mr[j]);
-          mi[j] = fmaf(s1.z, qv, mi[j]);
-          lr[j] = fmaf(s2.x, qv, lr[j]);
-          li[j] = fmaf(s2.y, qv, li[j]);
-          red[0] = fmaf(mr[j], kv, red[0]);
-          red[1] = fmaf(mi[j], kv, red[1]);
-          red[2] = fmaf(mr[j], zbr[i][j], fmaf(mi[j], zbi[i][j], red[2]));
-          red[3] = fmaf(mi[j], zbr[i][j], fmaf(-mr[j], zbi[i][j], red[3]));
-          red[4] = fmaf(lr[j], kv, red[4]);
-          red[5] = fmaf(li[j], kv, red[5]);
+          cr[jj] = fmaf(bb * pcr, kk[jj], cr[jj]);
+          ci[jj] = fmaf(bb * pci, kk[jj], ci[jj]);
+          mr[jj] = fmaf(s1.y, qq[jj], mr[jj]);
+          mi[jj] = fmaf(s1.z, qq[jj], mi[jj]);
+          lr[jj] = fmaf(s2.x, qq[jj], lr[jj]);
+          li[jj] = fmaf(s2.y, qq[jj], li[jj]);
+          red[0] = fmaf(mr[jj], kk[jj], red[0]);
+          red[1] = fmaf(mi[jj], kk[jj], red[1]);
+          red[2] = fmaf(mr[jj], zbr[i][jj], fmaf(mi[jj], zbi[i][jj], red[2]));
+          red[3] = fmaf(mi[jj], zbr[i][jj], fmaf(-mr[jj], zbi[i][jj], red[3]));
+          red[4] = fmaf(lr[jj], kk[jj], red[4]);
+          red[5] = fmaf(li[jj], kk[jj], red[5]);
         }
-        wave_reduce<6>(red, sm.red);
+#pragma unroll
+        for (int x = 0; x < 6; ++x) red[x] = group_sum<LPH>(red[x]);
         const float dwr = red[0], dwi = red[1], slr = red[4], sli = red[5];
         const float mkr = ar * dwr + ai * dwi, mki = ar * dwi - ai * dwr;
         float dar = red[2] - bb * (pr * dwr + pi * dwi);
@@ -654,8 +638,8 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
         const float dbe = -(pr * mkr + pi * mki) - (pcr * slr + pci * sli);
         float dgr = gv.x, dgi = gv.y;
         if (t == tc.nt - 1) {
-          dgr += dG[0];
-          dgi += dG[1];
+          dgr += dGr;
+          dgi += dGi;
         }
         const float npr = dgr + anr * psr + ani * psi;
         const float npi = dgi + anr * psi - ani * psr;
@@ -667,56 +651,64 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
         dai += s2.z * psi - s2.w * psr;
         float dkv[DPL];
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-          const float kv = ks[i].x[j];
-          const float m_r = ar * mr[j] + ai * mi[j], m_i = ar * mi[j] - ai * mr[j];
-          dkv[j] = mr[j] * wr + mi[j] * wi -
-                   bb * (zbr[i][j] * mkr + zbi[i][j] * mki + m_r * pr + m_i * pi) -
-                   bb * (cr[j] * slr + ci[j] * sli + lr[j] * pcr + li[j] * pci);
-          mr[j] = fmaf(-bb * mkr, kv, m_r);
-          mi[j] = fmaf(-bb * mki, kv, m_i);
-          lr[j] = fmaf(-bb * slr, kv, lr[j]);
-          li[j] = fmaf(-bb * sli, kv, li[j]);
+        for (int jj = 0; jj < DPL; ++jj) {
+          const float m_r = ar * mr[jj] + ai * mi[jj], m_i = ar * mi[jj] - ai * mr[jj];
+          dkv[jj] = mr[jj] * wr + mi[jj] * wi -
+                    bb * (zbr[i][jj] * mkr + zbi[i][jj] * mki + m_r * pr + m_i * pi) -
+                    bb * (cr[jj] * slr + ci[jj] * sli + lr[jj] * pcr + li[jj] * pci);
+          mr[jj] = fmaf(-bb * mkr, kk[jj], m_r);
+          mi[jj] = fmaf(-bb * mki, kk[jj], m_i);
+          lr[jj] = fmaf(-bb * slr, kk[jj], lr[jj]);
+          li[jj] = fmaf(-bb * sli, kk[jj], li[jj]);
         }
-        const int64_t o = off + int64_t(t) * stride;
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) T::store(dk + o + j, dkv[j]);
-        if (lane == 0) {
-          sm.R[t] = make_float4(dar, dai, dwr, dwi);
-          sm.RB[t] = dbe;
+        if (hok) store_row<T, DPL>(dk + off + int64_t(t) * stride, dkv);
+        if (sub == 0) {
+          sP[p] = make_float4(dar, dai, dwr, dwi);
+          sG[p] = make_float4(dbe, 0.0f, gv.z, gv.w);
         }
       }
     }
   }
   __syncthreads();
 
-  // ---- per-token dynamics backward (lane = token) ----
-  float dal = 0.0f, dom = 0.0f;
+  // ---- per-token dynamics backward: lane = (head j, block of TPB tokens) ----
+  {
+    constexpr int NB = kWave / HPW, TPB = HPW;
+    const int j = lane / NB, blk = lane % NB;
+    const int hj = tc.hbase + j;
+    const bool jok = hj < H;
+    const int hjl = jok ? hj : H - 1;
+    const float alj = alpha[hjl], omj = omega[hjl];
+    float dal = 0.0f, dom = 0.0f;
+    for (int tl = 0; tl < ntr; tl += kWave) {
 #pragma unroll
-  for (int s2 = 0; s2 < 2; ++s2) {
-    const int t = lane + 64 * s2;
-    if (t < tc.nt) {
-      const float4 rv = sm.R[t];
-      const float4 gv = sm.G[t];
-      const float bb = in.b[s2], vp = in.vp[s2], vr = in.vr[s2], vi = in.vi[s2];
-      const float dwv = rv.z * vr + rv.w * vi;
-      const float dbeta_t = sm.RB[t] + vp * dwv;
-      const float dvp = bb * dwv;
-      const DynGrad g = cayley_gated_bwd(in.dt[s2], in.r[s2], al, om, c, rv.x, rv.y, dvp);
-      const int64_t e = (tc.row0 + t) * H + tc.h;
-      T::store(dv + 2 * e, bb * vp * rv.z);
-      T::store(dv + 2 * e + 1, bb * vp * rv.w);
-      T::store(dbeta + e, dbeta_t);
-      T::store(dsel + e, in.dyr[s2] * gv.z + in.dyi[s2] * gv.w);
-      T::store(ddt + e, g.ddt);
-      T::store(dr + e, g.dr);
-      dal += g.dalpha;
-      dom += g.domega;
+      for (int i = 0; i < TPB; ++i) {
+        const int t = tl + blk * TPB + i;
+        if (t < tc.nt && jok) {
+          const int64_t e = (tc.row0 + t) * H + hj;
+          const int p = t * HPW + j;
+          const float4 rv = sP[p], gv = sG[p];
+          const float bb = T::load(beta + e), v0 = T::load(v + 2 * e), v1 = T::load(v + 2 * e + 1);
+          const float dtv = T::load(dt + e), rrv = T::load(r + e);
+          const float g0 = T::load(dy + 2 * e), g1 = T::load(dy + 2 * e + 1);
+          const Transition tr = cayley_gated(dtv, rrv, alj, omj, c);
+          const float dwv = rv.z * v0 + rv.w * v1;
+          const DynGrad g = cayley_gated_bwd(dtv, rrv, alj, omj, c, rv.x, rv.y, bb * dwv);
+          T::store(dv + 2 * e, bb * tr.vp * rv.z);
+          T::store(dv + 2 * e + 1, bb * tr.vp * rv.w);
+          T::store(dbeta + e, gv.x + tr.vp * dwv);
+          T::store(dsel + e, g0 * gv.z + g1 * gv.w);
+          T::store(ddt + e, g.ddt);
+          T::store(dr + e, g.dr);
+          dal += g.dalpha;
+          dom += g.domega;
+        }
+      }
     }
+    dal = group_sum<NB>(dal);
+    dom = group_sum<NB>(dom);
+    if (blk == 0 && jok) dhead_parts[(int64_t(tc.b) * NC + tc.chunk) * H + hj] = make_float2(dal, dom);
   }
-  dal = wsum(dal);
-  dom = wsum(dom);
-  if (lane == 0) dhead_parts[tc.tile] = make_float2(dal, dom);
 }
 
 // ---------------------------------------------------------------------------
@@ -759,8 +751,8 @@ using namespace cdssm;
 
 struct BwdLayout {
   int NC, S;
-  int64_t n_lam, n_dsn, n_segA, n_segX, n_parts;  // float2 counts
-  int64_t total() const { return n_lam + n_dsn + n_segA + n_segX + n_parts; }
+  int64_t n_lam, n_dsn, n_segA, n_segX, n_parts, n_ck;  // float2 counts
+  int64_t total() const { return n_lam + n_dsn + n_segA + n_segX + n_parts + n_ck; }
 };
 
 BwdLayout bwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) {
@@ -772,6 +764,8 @@ BwdLayout bwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) 
   w.n_segA = B * H * w.S;
   w.n_segX = B * H * w.S * D;
   w.n_parts = B * w.NC * H;
+  // z checkpoints of the main pass: per (tile, head slot, segment) one D-vector
+  w.n_ck = B * w.NC * ((H + kBwdMaxHPW - 1) / kBwdMaxHPW) * kBwdMaxHPW * ((chunk + kBwdCK - 1) / kBwdCK) * D;
   return w;
 }
 
@@ -785,7 +779,9 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
   using raw = typename T::raw;
   const BwdLayout w = bwd_layout(B, L, H, D, Q);
   const int NC = w.NC, S = w.S;
-  const int64_t tiles = int64_t(B) * NC * H;
+  constexpr int HPW = BwdCfg<D>::HPW;
+  const int n_hg = (H + HPW - 1) / HPW;
+  const int64_t tiles = int64_t(B) * NC * n_hg;
   const int64_t carry_threads = int64_t(B) * H * S * D;
   if (tiles > 0x7fffffff || carry_threads / 256 > 0x7fffffff) {
     cdssm_host::set_error("cdssm_fused_scan_bwd: grid too large");
@@ -798,10 +794,13 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
   float2* segA = dsn + w.n_dsn;
   float2* segX = segA + w.n_segA;
   float2* parts = segX + w.n_segX;
+  float2* ckpt = parts + w.n_parts;
+  const int slots = round_up(Q, kWave) * HPW;
 
-  hipLaunchKernelGGL((fused_bwd_corr_kernel<T, D>), dim3(unsigned(tiles)), dim3(kWave), 0, stream,
-                     (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,
-                     (const raw*)dt, (const raw*)r, alpha, omega, c, (const raw*)dy, lam0, L, H, Q, NC);
+  hipLaunchKernelGGL((fused_bwd_corr_kernel<T, D>), dim3(unsigned(tiles)), dim3(kWave),
+                     size_t(slots) * 2 * sizeof(float4), stream, (const raw*)q, (const raw*)k,
+                     (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c,
+                     (const raw*)dy, lam0, L, H, Q, NC, n_hg);
   int st = cdssm_host::check_launch("cdssm_fused_scan_bwd/corr");
   if (st) return st;
   const unsigned cblocks = unsigned((carry_threads + 255) / 256);
@@ -813,11 +812,11 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
                      gam, (const float2*)segA, (const float2*)segX, dh_final, dsn, dh0, B, NC, H, D, S);
   st = cdssm_host::check_launch("cdssm_fused_scan_bwd/rreplay");
   if (st) return st;
-  hipLaunchKernelGGL((fused_bwd_main_kernel<T, D>), dim3(unsigned(tiles)), dim3(kWave), 0, stream,
-                     (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,
-                     (const raw*)dt, (const raw*)r, alpha, omega, c, (const raw*)dy, states,
-                     (const float2*)dsn, (raw*)dq, (raw*)dk, (raw*)dv, (raw*)dbeta, (raw*)dsel, (raw*)ddt,
-                     (raw*)dr, parts, L, H, Q, NC);
+  hipLaunchKernelGGL((fused_bwd_main_kernel<T, D>), dim3(unsigned(tiles)), dim3(kWave),
+                     size_t(slots) * 5 * sizeof(float4), stream, (const raw*)q, (const raw*)k, (const raw*)v,
+                     (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c,
+                     (const raw*)dy, states, (const float2*)dsn, ckpt, (raw*)dq, (raw*)dk, (raw*)dv,
+                     (raw*)dbeta, (raw*)dsel, (raw*)ddt, (raw*)dr, parts, L, H, Q, NC, n_hg);
   st = cdssm_host::check_launch("cdssm_fused_scan_bwd/main");
   if (st) return st;
   hipLaunchKernelGGL(fused_bwd_heads_kernel, dim3(unsigned(H)), dim3(256), 0, stream,

@@ -59,28 +59,6 @@ struct FusedCfg {
   static_assert(HPW * LPH == kWave, "lane groups tile the wave");
 };
 
-__host__ __device__ constexpr int round_up(int x, int m) { return (x + m - 1) / m * m; }
-
-// Decode blockIdx.x -> (b, chunk, head group).
-struct ChunkTile {
-  int b, chunk, hbase, t0, nt;
-  int64_t row0;
-};
-
-__device__ __forceinline__ ChunkTile decode_tile(int L, int Q, int NC, int n_hg, int HPW) {
-  ChunkTile c;
-  int g = blockIdx.x;
-  const int hg = g % n_hg;
-  g /= n_hg;
-  c.chunk = g % NC;
-  c.b = g / NC;
-  c.hbase = hg * HPW;
-  c.t0 = c.chunk * Q;
-  c.nt = min(Q, L - c.t0);
-  c.row0 = int64_t(c.b) * L + c.t0;
-  return c;
-}
-
 // Per-token scalars of the tile in LDS, slot p = t*HPW + j (token t, head j):
 //   A[p] = (e_re, e_im, beta, sel_C)   the step's write coefficient: w/f_t, or w
 //                                       at a frame reset
@@ -116,12 +94,6 @@ struct ResetMask {
 // wave-uniform mask instead of testing |f| every step.
 constexpr float kBand = 120.0f;
 constexpr float kBandStep = 60.0f;
-
-__device__ __forceinline__ void cmul_acc(float& xr, float& xi, float yr, float yi) {
-  const float nr = xr * yr - xi * yi;
-  xi = xr * yi + xi * yr;
-  xr = nr;
-}
 
 // Spread the low 8 bits of x to bit positions 0, 8, ..., 56.
 __device__ __forceinline__ uint64_t spread8(uint64_t x) {
