@@ -153,7 +153,7 @@ __device__ __forceinline__ void store_row(typename T::raw* p, const float (&x)[D
   if constexpr (T::bytes == 2) {
     uint32_t u[DPL / 2];
 #pragma unroll
-    for (int i = 0; i < DPL / 2; ++i) u[i] = uint32_t(f32_to_bf16(x[2 * i])) | (uint32_t(f32_to_bf16(x[2 * i + 1])) << 16);
+    for (int i = 0; i < DPL / 2; ++i) u[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
     if constexpr (DPL == 8) {
       *reinterpret_cast<uint4*>(p) = make_uint4(u[0], u[1], u[2], u[3]);
     } else if constexpr (DPL == 4) {
