@@ -10,6 +10,8 @@ and the workspace with torch, and launches on torch's current stream.
 
 from __future__ import annotations
 
+import ctypes
+
 from typing import Optional, Tuple
 
 import torch
@@ -133,6 +135,17 @@ class PreparedForward:
             _lib.check(st, "cdssm_fused_scan_fwd")
         return self.y, self.h_final
 
+    PHASES = ("summary", "carry_fold", "carry_replay", "main")
+
+    def profile(self, iters: int) -> dict:
+        """Average milliseconds of each kernel launch over `iters` calls, from HIP
+        events recorded on the launch stream between the launches."""
+        out = (ctypes.c_float * len(self.PHASES))()
+        st = self._lib.cdssm_fused_scan_fwd_profile(*self._args, _lib.stream_of(self.device), int(iters), out)
+        if st != 0:
+            _lib.check(st, "cdssm_fused_scan_fwd_profile")
+        return dict(zip(self.PHASES, list(out)))
+
 
 def chunkwise_delta_scan_bwd(dy: Tensor, dh_final: Optional[Tensor], q, k, v, beta, sel_C, dt, r,
                              alpha, omega, c, carry: Tensor, has_h0: bool, chunk_size: int):
@@ -235,3 +248,13 @@ class PreparedBackward:
         if st != 0:
             _lib.check(st, "cdssm_fused_scan_bwd")
         return self.grads
+
+    PHASES = ("corr_adjoint", "rcarry_fold", "rcarry_replay", "main", "heads")
+
+    def profile(self, iters: int) -> dict:
+        """Average milliseconds of each backward kernel launch over `iters` calls."""
+        out = (ctypes.c_float * len(self.PHASES))()
+        st = self._lib.cdssm_fused_scan_bwd_profile(*self._args, _lib.stream_of(self.device), int(iters), out)
+        if st != 0:
+            _lib.check(st, "cdssm_fused_scan_bwd_profile")
+        return dict(zip(self.PHASES, list(out)))

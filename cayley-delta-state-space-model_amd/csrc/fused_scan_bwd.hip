@@ -775,7 +775,7 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
                      const void* dy, const float* dh_final, const float* fwd_ws, void* dq, void* dk,
                      void* dv, void* dbeta, void* dsel, void* ddt, void* dr, float* dalpha,
                      float* domega, float* dh0, float* ws, int B, int L, int H, int Q,
-                     hipStream_t stream) {
+                     hipStream_t stream, hipEvent_t* ev) {
   using raw = typename T::raw;
   const BwdLayout w = bwd_layout(B, L, H, D, Q);
   const int NC = w.NC, S = w.S;
@@ -797,21 +797,25 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
   float2* ckpt = parts + w.n_parts;
   const int slots = round_up(Q, kWave) * HPW;
 
+  if (ev) (void)hipEventRecord(ev[0], stream);
   hipLaunchKernelGGL((fused_bwd_corr_kernel<T, D>), dim3(unsigned(tiles)), dim3(kWave),
                      size_t(slots) * 2 * sizeof(float4), stream, (const raw*)q, (const raw*)k,
                      (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c,
                      (const raw*)dy, lam0, L, H, Q, NC, n_hg);
   int st = cdssm_host::check_launch("cdssm_fused_scan_bwd/corr");
   if (st) return st;
+  if (ev) (void)hipEventRecord(ev[1], stream);
   const unsigned cblocks = unsigned((carry_threads + 255) / 256);
   hipLaunchKernelGGL(fused_bwd_rfold_kernel, dim3(cblocks), dim3(256), 0, stream, (const float2*)lam0,
                      gam, segA, segX, B, NC, H, D, S);
   st = cdssm_host::check_launch("cdssm_fused_scan_bwd/rfold");
   if (st) return st;
+  if (ev) (void)hipEventRecord(ev[2], stream);
   hipLaunchKernelGGL(fused_bwd_rreplay_kernel, dim3(cblocks), dim3(256), 0, stream, (const float2*)lam0,
                      gam, (const float2*)segA, (const float2*)segX, dh_final, dsn, dh0, B, NC, H, D, S);
   st = cdssm_host::check_launch("cdssm_fused_scan_bwd/rreplay");
   if (st) return st;
+  if (ev) (void)hipEventRecord(ev[3], stream);
   hipLaunchKernelGGL((fused_bwd_main_kernel<T, D>), dim3(unsigned(tiles)), dim3(kWave),
                      size_t(slots) * 5 * sizeof(float4), stream, (const raw*)q, (const raw*)k, (const raw*)v,
                      (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c,
@@ -819,9 +823,12 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
                      (raw*)dbeta, (raw*)dsel, (raw*)ddt, (raw*)dr, parts, L, H, Q, NC, n_hg);
   st = cdssm_host::check_launch("cdssm_fused_scan_bwd/main");
   if (st) return st;
+  if (ev) (void)hipEventRecord(ev[4], stream);
   hipLaunchKernelGGL(fused_bwd_heads_kernel, dim3(unsigned(H)), dim3(256), 0, stream,
                      (const float2*)parts, dalpha, domega, B * NC, H);
-  return cdssm_host::check_launch("cdssm_fused_scan_bwd/heads");
+  st = cdssm_host::check_launch("cdssm_fused_scan_bwd/heads");
+  if (ev) (void)hipEventRecord(ev[5], stream);
+  return st;
 }
 
 }  // namespace
@@ -832,14 +839,14 @@ extern "C" int64_t cdssm_fused_scan_bwd_workspace_bytes(int64_t B, int64_t L, in
   return bwd_layout(B, L, H, D, chunk).total() * int64_t(sizeof(float2));
 }
 
-extern "C" int cdssm_fused_scan_bwd(int dtype, const void* q, const void* k, const void* v,
-                                    const void* beta, const void* sel_c, const void* dt,
-                                    const void* r, const float* alpha, const float* omega, float c,
-                                    const void* dy, const float* dh_final, const float* fwd_workspace,
-                                    void* dq, void* dk, void* dv, void* dbeta, void* dsel, void* ddt,
-                                    void* dr, float* dalpha, float* domega, float* dh0, float* workspace,
-                                    int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
-                                    int64_t chunk, hipStream_t stream) {
+namespace {
+int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                    const void* sel_c, const void* dt, const void* r, const float* alpha,
+                    const float* omega, float c, const void* dy, const float* dh_final,
+                    const float* fwd_workspace, void* dq, void* dk, void* dv, void* dbeta, void* dsel,
+                    void* ddt, void* dr, float* dalpha, float* domega, float* dh0, float* workspace,
+                    int64_t B, int64_t L, int64_t H, int64_t D, int64_t N, int64_t chunk,
+                    hipStream_t stream, hipEvent_t* ev) {
   const char* op = "cdssm_fused_scan_bwd";
   if (dtype != 0 && dtype != 1) {
     cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
@@ -875,16 +882,72 @@ extern "C" int cdssm_fused_scan_bwd(int dtype, const void* q, const void* k, con
     if (D == 64)
       return launch_fused_bwd<BF16, 64>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final,
                                         fwd_workspace, dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega,
-                                        dh0, workspace, b, l, hh, qc, stream);
+                                        dh0, workspace, b, l, hh, qc, stream, ev);
     return launch_fused_bwd<BF16, 128>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final,
                                        fwd_workspace, dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega,
-                                       dh0, workspace, b, l, hh, qc, stream);
+                                       dh0, workspace, b, l, hh, qc, stream, ev);
   }
   if (D == 64)
     return launch_fused_bwd<F32, 64>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final,
                                      fwd_workspace, dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0,
-                                     workspace, b, l, hh, qc, stream);
+                                     workspace, b, l, hh, qc, stream, ev);
   return launch_fused_bwd<F32, 128>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final,
                                     fwd_workspace, dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0,
-                                    workspace, b, l, hh, qc, stream);
+                                    workspace, b, l, hh, qc, stream, ev);
+}
+}  // namespace
+
+extern "C" int cdssm_fused_scan_bwd(int dtype, const void* q, const void* k, const void* v,
+                                    const void* beta, const void* sel_c, const void* dt,
+                                    const void* r, const float* alpha, const float* omega, float c,
+                                    const void* dy, const float* dh_final, const float* fwd_workspace,
+                                    void* dq, void* dk, void* dv, void* dbeta, void* dsel, void* ddt,
+                                    void* dr, float* dalpha, float* domega, float* dh0, float* workspace,
+                                    int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                    int64_t chunk, hipStream_t stream) {
+  return fused_bwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final, fwd_workspace,
+                         dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0, workspace, B, L, H, D, N,
+                         chunk, stream, nullptr);
+}
+
+extern "C" int cdssm_fused_scan_bwd_profile(int dtype, const void* q, const void* k, const void* v,
+                                            const void* beta, const void* sel_c, const void* dt,
+                                            const void* r, const float* alpha, const float* omega,
+                                            float c, const void* dy, const float* dh_final,
+                                            const float* fwd_workspace, void* dq, void* dk, void* dv,
+                                            void* dbeta, void* dsel, void* ddt, void* dr, float* dalpha,
+                                            float* domega, float* dh0, float* workspace, int64_t B,
+                                            int64_t L, int64_t H, int64_t D, int64_t N, int64_t chunk,
+                                            hipStream_t stream, int iters, float* phase_ms) {
+  if (iters < 1 || !phase_ms) {
+    cdssm_host::set_error("cdssm_fused_scan_bwd_profile: iters >= 1 and phase_ms required");
+    return CDSSM_EINVAL;
+  }
+  hipEvent_t ev[6];
+  for (int i = 0; i < 6; ++i)
+    if (hipEventCreate(&ev[i]) != hipSuccess) {
+      for (int j = 0; j < i; ++j) (void)hipEventDestroy(ev[j]);
+      cdssm_host::set_error("cdssm_fused_scan_bwd_profile: hipEventCreate failed");
+      return CDSSM_EHIP;
+    }
+  for (int p = 0; p < 5; ++p) phase_ms[p] = 0.0f;
+  int st = CDSSM_OK;
+  for (int it = 0; it < iters; ++it) {
+    st = fused_bwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final, fwd_workspace,
+                         dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0, workspace, B, L, H, D, N,
+                         chunk, stream, ev);
+    if (st != CDSSM_OK) break;
+    if (hipEventSynchronize(ev[5]) != hipSuccess) {
+      cdssm_host::set_error("cdssm_fused_scan_bwd_profile: hipEventSynchronize failed");
+      st = CDSSM_EHIP;
+      break;
+    }
+    for (int p = 0; p < 5; ++p) {
+      float ms = 0.0f;
+      (void)hipEventElapsedTime(&ms, ev[p], ev[p + 1]);
+      phase_ms[p] += ms / float(iters);
+    }
+  }
+  for (int i = 0; i < 6; ++i) (void)hipEventDestroy(ev[i]);
+  return st;
 }

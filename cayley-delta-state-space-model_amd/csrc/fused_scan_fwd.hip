@@ -675,7 +675,7 @@ template <typename T, int D, int LPH>
 int launch_fused_fwd(const void* q, const void* k, const void* v, const void* beta, const void* sel_c,
                      const void* dt, const void* r, const float* alpha, const float* omega, float c,
                      const float* h0, void* y, float* h_final, float* ws, int B, int L, int H, int Q,
-                     hipStream_t stream) {
+                     hipStream_t stream, hipEvent_t* ev) {
   using raw = typename T::raw;
   constexpr int HPW = kWave / LPH;
   const FwdLayout w = fwd_layout(B, L, H, D, Q);
@@ -693,6 +693,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   float2* segX = segA + w.n_segA;
   const int slots = round_up(Q, kWave) * HPW;
 
+  if (ev) (void)hipEventRecord(ev[0], stream);
   hipLaunchKernelGGL((fused_fwd_summary_kernel<T, D, LPH>), dim3(unsigned(tiles)), dim3(kWave),
                      size_t(slots) * (sizeof(float4) + sizeof(float2)) + HPW * sizeof(float4), stream,
                      (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)dt, (const raw*)r, alpha,
@@ -700,22 +701,27 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   int st = cdssm_host::check_launch("cdssm_fused_scan_fwd/summary");
   if (st) return st;
 
+  if (ev) (void)hipEventRecord(ev[1], stream);
   const unsigned cblocks = unsigned((carry_threads + 255) / 256);
   hipLaunchKernelGGL(fused_fwd_fold_kernel, dim3(cblocks), dim3(256), 0, stream, (const float2*)summ,
                      (const float2*)gam, segA, segX, B, NC, H, D, S);
   st = cdssm_host::check_launch("cdssm_fused_scan_fwd/fold");
   if (st) return st;
+  if (ev) (void)hipEventRecord(ev[2], stream);
   hipLaunchKernelGGL(fused_fwd_replay_kernel, dim3(cblocks), dim3(256), 0, stream, summ,
                      (const float2*)gam, (const float2*)segA, (const float2*)segX, h0, h_final, B, NC,
                      H, D, S);
   st = cdssm_host::check_launch("cdssm_fused_scan_fwd/replay");
   if (st) return st;
+  if (ev) (void)hipEventRecord(ev[3], stream);
 
   hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH>), dim3(unsigned(tiles)), dim3(kWave),
                      size_t(slots) * (2 * sizeof(float4) + 2 * sizeof(float2)), stream, (const raw*)q,
                      (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c, (const raw*)dt,
                      (const raw*)r, alpha, omega, c, (const float2*)summ, (raw*)y, L, H, Q, NC, n_hg);
-  return cdssm_host::check_launch("cdssm_fused_scan_fwd/main");
+  st = cdssm_host::check_launch("cdssm_fused_scan_fwd/main");
+  if (ev) (void)hipEventRecord(ev[4], stream);
+  return st;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -728,12 +734,12 @@ extern "C" int64_t cdssm_fused_scan_workspace_bytes(int64_t B, int64_t L, int64_
   return fwd_layout(B, L, H, D, chunk).total() * int64_t(sizeof(float2));
 }
 
-extern "C" int cdssm_fused_scan_fwd(int dtype, const void* q, const void* k, const void* v,
-                                    const void* beta, const void* sel_c, const void* dt,
-                                    const void* r, const float* alpha, const float* omega, float c,
-                                    const float* h0, void* y, float* h_final, float* workspace,
-                                    int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
-                                    int64_t chunk, hipStream_t stream) {
+namespace {
+int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                    const void* sel_c, const void* dt, const void* r, const float* alpha,
+                    const float* omega, float c, const float* h0, void* y, float* h_final,
+                    float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                    int64_t chunk, hipStream_t stream, hipEvent_t* ev) {
   const char* op = "cdssm_fused_scan_fwd";
   if (dtype != 0 && dtype != 1) {
     cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
@@ -773,13 +779,63 @@ extern "C" int cdssm_fused_scan_fwd(int dtype, const void* q, const void* k, con
   if (dtype == 1) {
     if (D == 64)
       return launch_fused_fwd<BF16, 64, CDSSM_FWD_LPH_BF16_D64>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                           workspace, b, l, hh, qc, stream);
+                                           workspace, b, l, hh, qc, stream, ev);
     return launch_fused_fwd<BF16, 128, 16>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                           workspace, b, l, hh, qc, stream);
+                                           workspace, b, l, hh, qc, stream, ev);
   }
   if (D == 64)
     return launch_fused_fwd<F32, 64, 16>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                         workspace, b, l, hh, qc, stream);
+                                         workspace, b, l, hh, qc, stream, ev);
   return launch_fused_fwd<F32, 128, 32>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                        workspace, b, l, hh, qc, stream);
+                                        workspace, b, l, hh, qc, stream, ev);
+}
+}  // namespace
+
+extern "C" int cdssm_fused_scan_fwd(int dtype, const void* q, const void* k, const void* v,
+                                    const void* beta, const void* sel_c, const void* dt,
+                                    const void* r, const float* alpha, const float* omega, float c,
+                                    const float* h0, void* y, float* h_final, float* workspace,
+                                    int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                    int64_t chunk, hipStream_t stream) {
+  return fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace,
+                         B, L, H, D, N, chunk, stream, nullptr);
+}
+
+extern "C" int cdssm_fused_scan_fwd_profile(int dtype, const void* q, const void* k, const void* v,
+                                            const void* beta, const void* sel_c, const void* dt,
+                                            const void* r, const float* alpha, const float* omega,
+                                            float c, const float* h0, void* y, float* h_final,
+                                            float* workspace, int64_t B, int64_t L, int64_t H,
+                                            int64_t D, int64_t N, int64_t chunk, hipStream_t stream,
+                                            int iters, float* phase_ms) {
+  if (iters < 1 || !phase_ms) {
+    cdssm_host::set_error("cdssm_fused_scan_fwd_profile: iters >= 1 and phase_ms required");
+    return CDSSM_EINVAL;
+  }
+  hipEvent_t ev[5];
+  for (int i = 0; i < 5; ++i)
+    if (hipEventCreate(&ev[i]) != hipSuccess) {
+      for (int j = 0; j < i; ++j) (void)hipEventDestroy(ev[j]);
+      cdssm_host::set_error("cdssm_fused_scan_fwd_profile: hipEventCreate failed");
+      return CDSSM_EHIP;
+    }
+  for (int p = 0; p < 4; ++p) phase_ms[p] = 0.0f;
+  int st = CDSSM_OK;
+  for (int it = 0; it < iters && st == CDSSM_OK; ++it) {
+    st = fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace, B,
+                         L, H, D, N, chunk, stream, ev);
+    if (st != CDSSM_OK) break;
+    if (hipEventSynchronize(ev[4]) != hipSuccess) {
+      cdssm_host::set_error("cdssm_fused_scan_fwd_profile: hipEventSynchronize failed");
+      st = CDSSM_EHIP;
+      break;
+    }
+    for (int p = 0; p < 4; ++p) {
+      float ms = 0.0f;
+      (void)hipEventElapsedTime(&ms, ev[p], ev[p + 1]);
+      phase_ms[p] += ms / float(iters);
+    }
+  }
+  for (int i = 0; i < 5; ++i) (void)hipEventDestroy(ev[i]);
+  return st;
 }

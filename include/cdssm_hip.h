@@ -80,6 +80,29 @@ int cdssm_fused_scan_bwd(int dtype, const void* q, const void* k, const void* v,
                          int64_t chunk, hipStream_t stream);
 
 /*
+ * Instrumentation (no counterpart in the reference; for benchmarks and
+ * profilers): run the fused forward / backward `iters` times on `stream` with
+ * HIP events recorded between its kernel launches, synchronise, and return in
+ * phase_ms the average milliseconds of each launch:
+ *   forward  phase_ms[4]: chunk summaries, carry fold, carry replay, main pass;
+ *   backward phase_ms[5]: correction adjoint, reverse-carry fold, reverse-carry
+ *            replay, main pass, per-head reduction.
+ * Arguments otherwise as cdssm_fused_scan_fwd / cdssm_fused_scan_bwd.
+ */
+int cdssm_fused_scan_fwd_profile(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                                 const void* sel_c, const void* dt, const void* r, const float* alpha,
+                                 const float* omega, float c, const float* h0, void* y, float* h_final,
+                                 float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                 int64_t chunk, hipStream_t stream, int iters, float* phase_ms);
+int cdssm_fused_scan_bwd_profile(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                                 const void* sel_c, const void* dt, const void* r, const float* alpha,
+                                 const float* omega, float c, const void* dy, const float* dh_final,
+                                 const float* fwd_workspace, void* dq, void* dk, void* dv, void* dbeta,
+                                 void* dsel_c, void* ddt, void* dr, float* dalpha, float* domega,
+                                 float* dh0, float* workspace, int64_t B, int64_t L, int64_t H, int64_t D,
+                                 int64_t N, int64_t chunk, hipStream_t stream, int iters, float* phase_ms);
+
+/*
  * The reference's three scan passes as separate ops, same tensor contracts
  * (all tensors `dtype`, contiguous; N even, N <= 32; D <= 128).
  *
