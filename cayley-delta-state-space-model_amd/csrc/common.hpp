@@ -33,6 +33,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return uint16_t(u >> 16);
 }
 
+// A copy of x in a new register (an explicit v_mov the compiler cannot fold
+// away): lets a prefetch ring slot be reloaded while its old value is in use.
+__device__ __forceinline__ float fresh(float x) {
+  float r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
 // Two fp32 -> packed bf16 pair (lo = a), round-to-nearest-even in one
 // v_cvt_pk_bf16_f32.
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));

@@ -41,15 +41,25 @@
 namespace cdssm {
 
 constexpr int kBwdSeg = 16;   // chunks per reverse-carry segment
-// lanes per head: D/4, so every lane holds DPL = 4 state elements
+// lanes per head and state elements per lane (LPH * DPL = D)
+#ifndef CDSSM_BWD_LPH_D128
+#define CDSSM_BWD_LPH_D128 32
+#endif
 template <int D>
 struct BwdCfg {
-  static constexpr int LPH = D / 4;
+  static constexpr int LPH = D == 64 ? 16 : CDSSM_BWD_LPH_D128;
   static constexpr int HPW = kWave / LPH;
-  static constexpr int DPL = 4;
+  static constexpr int DPL = D / LPH;
+};
+// the correction-adjoint pass is light on registers: 16 lanes per head for both D
+template <int D>
+struct BwdCorrCfg {
+  static constexpr int LPH = 16;
+  static constexpr int HPW = kWave / LPH;
+  static constexpr int DPL = D / LPH;
 };
 constexpr int kBwdMaxHPW = 4;
-constexpr int kBwdCK = 8;     // z checkpoint interval of the main pass
+constexpr int kBwdCK = 4;     // z checkpoint interval of the main pass
 constexpr int kBwdPF = 8;     // row prefetch depth
 
 // Per-token scalars of a backward tile in LDS, slot p = t*HPW + j:
@@ -187,7 +197,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
     const float* __restrict__ alpha, const float* __restrict__ omega, float c,
     const typename T::raw* __restrict__ dy, float2* __restrict__ lam0, int L, int H, int Q, int NC,
     int n_hg) {
-  constexpr int LPH = BwdCfg<D>::LPH, HPW = BwdCfg<D>::HPW, DPL = BwdCfg<D>::DPL, PF = kBwdPF;
+  constexpr int LPH = BwdCorrCfg<D>::LPH, HPW = BwdCorrCfg<D>::HPW, DPL = BwdCorrCfg<D>::DPL, PF = kBwdPF;
   extern __shared__ float4 smem4[];
   const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
@@ -238,6 +248,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
       qb[i].unpack_then_reload(qq);
       kb[i].load(kp + max(min(t - PF, tlast), 0) * stride);
       qb[i].load(qp + max(min(t - PF, tlast), 0) * stride);
+      __builtin_amdgcn_sched_barrier(0);  // issue the reloads here, not sunk below later tokens
       // padded steps have h = 0 and beta = 0
       float sr = 0.0f, si = 0.0f;
 #pragma unroll
@@ -301,13 +312,21 @@ __global__ __launch_bounds__(256) void fused_bwd_rfold_kernel(const float2* __re
   const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (tid >= int64_t(B) * H * S * D) return;
   const RCarry x = rcarry_index(tid, NC, H, D, S);
-  // map: ds_{c0} = A ds_{c1} + X
+  // map: ds_{c0} = A ds_{c1} + X; all loads of the segment issued first
+  float2 G[kBwdSeg], Lm[kBwdSeg];
+#pragma unroll
+  for (int i = 0; i < kBwdSeg; ++i) {
+    const int64_t e = x.base + int64_t(min(x.c0 + i, x.c1 - 1)) * H;
+    G[i] = gam[e];
+    Lm[i] = lam0[e * D + x.d];
+  }
   float2 A = make_float2(1.0f, 0.0f), X = make_float2(0.0f, 0.0f);
-  for (int ch = x.c1 - 1; ch >= x.c0; --ch) {
-    const int64_t e = x.base + int64_t(ch) * H;
-    const float2 G = gam[e];
-    X = cfma_conj(G, X, lam0[e * D + x.d]);
-    A = cmul_conj(G, A);
+#pragma unroll
+  for (int i = kBwdSeg - 1; i >= 0; --i) {
+    if (x.c0 + i < x.c1) {
+      X = cfma_conj(G[i], X, Lm[i]);
+      A = cmul_conj(G[i], A);
+    }
   }
   const int64_t sidx = (int64_t(x.b) * H + x.h) * S + x.seg;
   segX[sidx * D + x.d] = X;
@@ -325,15 +344,33 @@ __global__ __launch_bounds__(256) void fused_bwd_rreplay_kernel(
   const int64_t hb = (int64_t(x.b) * H + x.h) * 2 * D;
   float2 ds = make_float2(0.0f, 0.0f);
   if (dh_final != nullptr) ds = make_float2(dh_final[hb + x.d], dh_final[hb + D + x.d]);
-  for (int j = S - 1; j > x.seg; --j) {
-    const float2 A = segA[sbase + j];
-    const float2 X = segX[(sbase + j) * D + x.d];
-    ds = make_float2(A.x * ds.x - A.y * ds.y + X.x, A.x * ds.y + A.y * ds.x + X.y);
+  // the segment's own loads first, then the later segments' maps (in groups of 8)
+  float2 G[kBwdSeg], Lm[kBwdSeg];
+#pragma unroll
+  for (int i = 0; i < kBwdSeg; ++i) {
+    const int64_t e = x.base + int64_t(min(x.c0 + i, max(x.c1 - 1, 0))) * H;
+    G[i] = gam[e];
+    Lm[i] = lam0[e * D + x.d];
   }
-  for (int ch = x.c1 - 1; ch >= x.c0; --ch) {
-    const int64_t e = x.base + int64_t(ch) * H;
-    dsn[e * D + x.d] = ds;
-    ds = cfma_conj(gam[e], ds, lam0[e * D + x.d]);
+  for (int jb = S - 1; jb > x.seg; jb -= 8) {
+    float2 A[8], X[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t j = sbase + max(jb - i, x.seg + 1);
+      A[i] = segA[j];
+      X[i] = segX[j * D + x.d];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (jb - i > x.seg)
+        ds = make_float2(A[i].x * ds.x - A[i].y * ds.y + X[i].x, A[i].x * ds.y + A[i].y * ds.x + X[i].y);
+  }
+#pragma unroll
+  for (int i = kBwdSeg - 1; i >= 0; --i) {
+    if (x.c0 + i < x.c1) {
+      dsn[(x.base + int64_t(x.c0 + i) * H) * D + x.d] = ds;
+      ds = cfma_conj(G[i], ds, Lm[i]);
+    }
   }
   if (x.seg == 0 && dh0 != nullptr) {
     dh0[hb + x.d] = ds.x;
@@ -427,7 +464,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
     typename T::raw* __restrict__ ddt, typename T::raw* __restrict__ dr, float2* __restrict__ dhead_parts,
     int L, int H, int Q, int NC, int n_hg) {
   constexpr int LPH = BwdCfg<D>::LPH, HPW = BwdCfg<D>::HPW, DPL = BwdCfg<D>::DPL, PF = kBwdPF, CK = kBwdCK;
-  static_assert(PF == CK, "checkpoints fall on prefetch-group starts");
+  static_assert(PF % CK == 0, "checkpoints fall inside prefetch groups at fixed positions");
   extern __shared__ float4 smem4[];
   const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
@@ -476,9 +513,6 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
 
   // ---- forward pass ----
   for (int tb = 0; tb < ntr; tb += PF) {
-    // checkpoint z_{tb-1}
-#pragma unroll
-    for (int jj = 0; jj < DPL; ++jj) ck[(tb / CK) * D + jj] = make_float2(zr[jj], zi[jj]);
     float4 s0[PF], s1[PF], s2[PF];
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
@@ -490,11 +524,17 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int t = tb + i;
+      if (i % CK == 0) {
+        // checkpoint z_{t-1}
+#pragma unroll
+        for (int jj = 0; jj < DPL; ++jj) ck[(t / CK) * D + jj] = make_float2(zr[jj], zi[jj]);
+      }
       float kk[DPL], qq[DPL];
       kb[i].unpack_then_reload(kk);
       qb[i].unpack_then_reload(qq);
       kb[i].load(kp + min(t + PF, tlast) * stride);
       qb[i].load(qp + min(t + PF, tlast) * stride);
+      __builtin_amdgcn_sched_barrier(0);  // issue the reloads here, not sunk below later tokens
       float pr = 0.0f, pi = 0.0f, pcr = 0.0f, pci = 0.0f;
 #pragma unroll
       for (int jj = 0; jj < DPL; ++jj) {
@@ -567,21 +607,30 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   }
   float psr = 0.0f, psi = 0.0f;  // psi_{t+1}
   float anr = 1.0f, ani = 0.0f;  // a_{t+1}
-  for (int seg = ntr / CK - 1; seg >= 0; --seg) {
+  // Segments run last to first; the next segment's k / q rows and z checkpoint
+  // are loaded while the current one is processed (two buffers, alternating).
+  struct SegBuf {
+    RowVec<T, DPL> k[CK], q[CK];
+    float2 z0[DPL];
+  };
+  auto load_seg = [&](SegBuf& R, int seg) {
     const int tb = seg * CK;
-    RowVec<T, DPL> ks[CK], qs[CK];
 #pragma unroll
     for (int i = 0; i < CK; ++i) {
-      ks[i].load(kp + min(tb + i, tlast) * stride);
-      qs[i].load(qp + min(tb + i, tlast) * stride);
+      R.k[i].load(kp + min(tb + i, tlast) * stride);
+      R.q[i].load(qp + min(tb + i, tlast) * stride);
     }
+#pragma unroll
+    for (int jj = 0; jj < DPL; ++jj) R.z0[jj] = ck[seg * D + jj];
+  };
+  auto run_seg = [&](const SegBuf& R, int seg) {
+    const int tb = seg * CK;
     // z_{tb-1+i} for i = 0..CK, recomputed with the stored p_t
     float zbr[CK + 1][DPL], zbi[CK + 1][DPL];
 #pragma unroll
     for (int jj = 0; jj < DPL; ++jj) {
-      const float2 z0 = ck[seg * D + jj];
-      zbr[0][jj] = z0.x;
-      zbi[0][jj] = z0.y;
+      zbr[0][jj] = R.z0[jj].x;
+      zbi[0][jj] = R.z0[jj].y;
     }
 #pragma unroll
     for (int i = 0; i < CK; ++i) {
@@ -594,7 +643,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
       const float er = s0.z - (s0.x * bpr - s0.y * bpi);
       const float ei = s0.w - (s0.x * bpi + s0.y * bpr);
       float kk[DPL];
-      ks[i].unpack(kk);
+      R.k[i].unpack(kk);
 #pragma unroll
       for (int jj = 0; jj < DPL; ++jj) {
         zbr[i + 1][jj] = fmaf(s0.x, zbr[i][jj], fmaf(-s0.y, zbi[i][jj], er * kk[jj]));
@@ -607,11 +656,11 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
       if (t < tc.nt) {
         const int p = t * HPW + hh;
         const float4 s0 = s.S0[p], s1 = s.S1[p], s2 = s.S2[p], pv = sP[p], gv = sG[p];
-        const float ar = s0.x, ai = s0.y, wr = s0.z, wi = s0.w, bb = s1.x;
+        const float ar = s0.x, ai = s0.y, bb = s1.x;
         const float pr = pv.x, pi = pv.y, pcr = pv.z, pci = pv.w;
         float kk[DPL], qq[DPL];
-        ks[i].unpack(kk);
-        qs[i].unpack(qq);
+        R.k[i].unpack(kk);
+        R.q[i].unpack(qq);
         float red[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int jj = 0; jj < DPL; ++jj) {
@@ -649,17 +698,29 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
         ani = ai;
         dar += s2.z * psr + s2.w * psi;
         dai += s2.z * psi - s2.w * psr;
+        // dk = mu.e - beta (z_{t-1}.mk + c^_t.(lambda.k) + lambda.pc), e = w - beta a p:
+        // the mu.w and conj(a) mu . p terms combine into mu.e
+        const float bpr = bb * pr, bpi = bb * pi;
+        const float er = s0.z - (ar * bpr - ai * bpi);
+        const float ei = s0.w - (ar * bpi + ai * bpr);
+        const float bmkr = bb * mkr, bmki = bb * mki, bslr = bb * slr, bsli = bb * sli;
+        const float bpcr = bb * pcr, bpci = bb * pci;
         float dkv[DPL];
 #pragma unroll
         for (int jj = 0; jj < DPL; ++jj) {
+          float acc = mr[jj] * er;
+          acc = fmaf(mi[jj], ei, acc);
+          acc = fmaf(-zbr[i][jj], bmkr, acc);
+          acc = fmaf(-zbi[i][jj], bmki, acc);
+          acc = fmaf(-cr[jj], bslr, acc);
+          acc = fmaf(-ci[jj], bsli, acc);
+          acc = fmaf(-lr[jj], bpcr, acc);
+          dkv[jj] = fmaf(-li[jj], bpci, acc);
           const float m_r = ar * mr[jj] + ai * mi[jj], m_i = ar * mi[jj] - ai * mr[jj];
-          dkv[jj] = mr[jj] * wr + mi[jj] * wi -
-                    bb * (zbr[i][jj] * mkr + zbi[i][jj] * mki + m_r * pr + m_i * pi) -
-                    bb * (cr[jj] * slr + ci[jj] * sli + lr[jj] * pcr + li[jj] * pci);
-          mr[jj] = fmaf(-bb * mkr, kk[jj], m_r);
-          mi[jj] = fmaf(-bb * mki, kk[jj], m_i);
-          lr[jj] = fmaf(-bb * slr, kk[jj], lr[jj]);
-          li[jj] = fmaf(-bb * sli, kk[jj], li[jj]);
+          mr[jj] = fmaf(-bmkr, kk[jj], m_r);
+          mi[jj] = fmaf(-bmki, kk[jj], m_i);
+          lr[jj] = fmaf(-bslr, kk[jj], lr[jj]);
+          li[jj] = fmaf(-bsli, kk[jj], li[jj]);
         }
         if (hok) store_row<T, DPL>(dk + off + int64_t(t) * stride, dkv);
         if (sub == 0) {
@@ -667,6 +728,21 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
           sG[p] = make_float4(dbe, 0.0f, gv.z, gv.w);
         }
       }
+    }
+  };
+  {
+    SegBuf bufA, bufB;
+    int seg = ntr / CK - 1;
+    load_seg(bufA, seg);
+    while (true) {
+      load_seg(bufB, max(seg - 1, 0));  // unconditional: a clamped reload past segment 0 is harmless
+      __builtin_amdgcn_sched_barrier(0);
+      run_seg(bufA, seg);
+      if (--seg < 0) break;
+      load_seg(bufA, max(seg - 1, 0));
+      __builtin_amdgcn_sched_barrier(0);
+      run_seg(bufB, seg);
+      if (--seg < 0) break;
     }
   }
   __syncthreads();
@@ -779,11 +855,11 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
   using raw = typename T::raw;
   const BwdLayout w = bwd_layout(B, L, H, D, Q);
   const int NC = w.NC, S = w.S;
-  constexpr int HPW = BwdCfg<D>::HPW;
-  const int n_hg = (H + HPW - 1) / HPW;
-  const int64_t tiles = int64_t(B) * NC * n_hg;
+  constexpr int HPW = BwdCfg<D>::HPW, HPWC = BwdCorrCfg<D>::HPW;
+  const int n_hg = (H + HPW - 1) / HPW, n_hgc = (H + HPWC - 1) / HPWC;
+  const int64_t tiles = int64_t(B) * NC * n_hg, tiles_c = int64_t(B) * NC * n_hgc;
   const int64_t carry_threads = int64_t(B) * H * S * D;
-  if (tiles > 0x7fffffff || carry_threads / 256 > 0x7fffffff) {
+  if (tiles > 0x7fffffff || tiles_c > 0x7fffffff || carry_threads / 256 > 0x7fffffff) {
     cdssm_host::set_error("cdssm_fused_scan_bwd: grid too large");
     return CDSSM_EINVAL;
   }
@@ -795,13 +871,13 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
   float2* segX = segA + w.n_segA;
   float2* parts = segX + w.n_segX;
   float2* ckpt = parts + w.n_parts;
-  const int slots = round_up(Q, kWave) * HPW;
+  const int slots = round_up(Q, kWave) * HPW, slots_c = round_up(Q, kWave) * HPWC;
 
   if (ev) (void)hipEventRecord(ev[0], stream);
-  hipLaunchKernelGGL((fused_bwd_corr_kernel<T, D>), dim3(unsigned(tiles)), dim3(kWave),
-                     size_t(slots) * 2 * sizeof(float4), stream, (const raw*)q, (const raw*)k,
+  hipLaunchKernelGGL((fused_bwd_corr_kernel<T, D>), dim3(unsigned(tiles_c)), dim3(kWave),
+                     size_t(slots_c) * 2 * sizeof(float4), stream, (const raw*)q, (const raw*)k,
                      (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c,
-                     (const raw*)dy, lam0, L, H, Q, NC, n_hg);
+                     (const raw*)dy, lam0, L, H, Q, NC, n_hgc);
   int st = cdssm_host::check_launch("cdssm_fused_scan_bwd/corr");
   if (st) return st;
   if (ev) (void)hipEventRecord(ev[1], stream);

@@ -50,6 +50,12 @@ constexpr int kPrefetch = 8;
 #ifndef CDSSM_FWD_LPH_BF16_D64
 #define CDSSM_FWD_LPH_BF16_D64 8
 #endif
+#ifndef CDSSM_FWD_LPHS_BF16_D64
+#define CDSSM_FWD_LPHS_BF16_D64 8
+#endif
+#ifndef CDSSM_FWD_LPHS_BF16_D128
+#define CDSSM_FWD_LPHS_BF16_D128 16
+#endif
 constexpr int kSegLen = 16;  // chunks per carry segment
 
 template <typename T, int D, int LPH>
@@ -671,19 +677,21 @@ FwdLayout fwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) 
   return w;
 }
 
-template <typename T, int D, int LPH>
+// LPH: lanes per head of the main pass; LPHS: of the summary pass (its own
+// tile grid, so the lighter summary can run with more waves).
+template <typename T, int D, int LPH, int LPHS>
 int launch_fused_fwd(const void* q, const void* k, const void* v, const void* beta, const void* sel_c,
                      const void* dt, const void* r, const float* alpha, const float* omega, float c,
                      const float* h0, void* y, float* h_final, float* ws, int B, int L, int H, int Q,
                      hipStream_t stream, hipEvent_t* ev) {
   using raw = typename T::raw;
-  constexpr int HPW = kWave / LPH;
+  constexpr int HPW = kWave / LPH, HPWS = kWave / LPHS;
   const FwdLayout w = fwd_layout(B, L, H, D, Q);
   const int NC = w.NC, S = w.S;
-  const int n_hg = (H + HPW - 1) / HPW;
-  const int64_t tiles = int64_t(B) * NC * n_hg;
+  const int n_hg = (H + HPW - 1) / HPW, n_hgs = (H + HPWS - 1) / HPWS;
+  const int64_t tiles = int64_t(B) * NC * n_hg, tiles_s = int64_t(B) * NC * n_hgs;
   const int64_t carry_threads = int64_t(B) * H * S * D;
-  if (tiles > 0x7fffffff || carry_threads / 256 > 0x7fffffff) {
+  if (tiles_s > 0x7fffffff || carry_threads / 256 > 0x7fffffff) {
     cdssm_host::set_error("cdssm_fused_scan_fwd: grid too large (%lld tiles)", (long long)tiles);
     return CDSSM_EINVAL;
   }
@@ -691,13 +699,13 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   float2* gam = summ + w.n_summ;
   float2* segA = gam + w.n_gam;
   float2* segX = segA + w.n_segA;
-  const int slots = round_up(Q, kWave) * HPW;
+  const int slots = round_up(Q, kWave) * HPW, slots_s = round_up(Q, kWave) * HPWS;
 
   if (ev) (void)hipEventRecord(ev[0], stream);
-  hipLaunchKernelGGL((fused_fwd_summary_kernel<T, D, LPH>), dim3(unsigned(tiles)), dim3(kWave),
-                     size_t(slots) * (sizeof(float4) + sizeof(float2)) + HPW * sizeof(float4), stream,
+  hipLaunchKernelGGL((fused_fwd_summary_kernel<T, D, LPHS>), dim3(unsigned(tiles_s)), dim3(kWave),
+                     size_t(slots_s) * (sizeof(float4) + sizeof(float2)) + HPWS * sizeof(float4), stream,
                      (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)dt, (const raw*)r, alpha,
-                     omega, c, summ, gam, L, H, Q, NC, n_hg);
+                     omega, c, summ, gam, L, H, Q, NC, n_hgs);
   int st = cdssm_host::check_launch("cdssm_fused_scan_fwd/summary");
   if (st) return st;
 
@@ -778,15 +786,15 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
   const int b = int(B), l = int(L), hh = int(H), qc = int(chunk);
   if (dtype == 1) {
     if (D == 64)
-      return launch_fused_fwd<BF16, 64, CDSSM_FWD_LPH_BF16_D64>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
+      return launch_fused_fwd<BF16, 64, CDSSM_FWD_LPH_BF16_D64, CDSSM_FWD_LPHS_BF16_D64>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
                                            workspace, b, l, hh, qc, stream, ev);
-    return launch_fused_fwd<BF16, 128, 16>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
+    return launch_fused_fwd<BF16, 128, 16, CDSSM_FWD_LPHS_BF16_D128>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
                                            workspace, b, l, hh, qc, stream, ev);
   }
   if (D == 64)
-    return launch_fused_fwd<F32, 64, 16>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
+    return launch_fused_fwd<F32, 64, 16, 16>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
                                          workspace, b, l, hh, qc, stream, ev);
-  return launch_fused_fwd<F32, 128, 32>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
+  return launch_fused_fwd<F32, 128, 32, 32>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
                                         workspace, b, l, hh, qc, stream, ev);
 }
 }  // namespace
