@@ -312,11 +312,10 @@ __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, i
 // (m = 1 for the other heads), then every head takes the common update.
 template <int DPL>
 __device__ __forceinline__ void local_step(float (&zr)[DPL], float (&zi)[DPL], const float (&kk)[DPL],
-                                           bool reset_any, const float2* mslot, float er0, float ei0,
+                                           bool reset_any, float2 m, float er0, float ei0,
                                            float bb, float pr, float pi) {
   float bpr = bb * pr, bpi = bb * pi;
   if (reset_any) {
-    const float2 m = *mslot;
 #pragma unroll
     for (int j = 0; j < DPL; ++j) {
       const float xr = m.x * zr[j] - m.y * zi[j];
@@ -378,8 +377,12 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
 
   for (int tb = 0; tb < ntr; tb += PF) {
     float4 sa[PF];
+    float2 sm[PF];
 #pragma unroll
-    for (int i = 0; i < PF; ++i) sa[i] = s.A[(tb + i) * HPW + hh];
+    for (int i = 0; i < PF; ++i) {
+      sa[i] = s.A[(tb + i) * HPW + hh];
+      sm[i] = s.M[(tb + i) * HPW + hh];
+    }
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int t = tb + i;
@@ -396,7 +399,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
       }
       const float pr = group_sum<LPH>(pr0 + pr1);
       const float pi = group_sum<LPH>(pi0 + pi1);
-      local_step<DPL>(zr, zi, kk, rm.test(t), s.M + t * HPW + hh, sa[i].x, sa[i].y, sa[i].z, pr, pi);
+      local_step<DPL>(zr, zi, kk, rm.test(t), sm[i], sa[i].x, sa[i].y, sa[i].z, pr, pi);
     }
   }
 
@@ -582,10 +585,12 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
 
   for (int tb = 0; tb < ntr; tb += PF) {
     float4 sa[PF], sb[PF];
+    float2 sm[PF];
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       sa[i] = s.A[(tb + i) * HPW + hh];
       sb[i] = s.B[(tb + i) * HPW + hh];
+      sm[i] = s.M[(tb + i) * HPW + hh];
     }
     float yr[PF], yi[PF];
 #pragma unroll
@@ -613,7 +618,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
       pci = group_sum<LPH>(pci);
 
       const float bb = sa[i].z;
-      local_step<DPL>(zr, zi, kk, rm.test(t), s.M + t * HPW + hh, sa[i].x, sa[i].y, bb, pzr, pzi);
+      local_step<DPL>(zr, zi, kk, rm.test(t), sm[i], sa[i].x, sa[i].y, bb, pzr, pzi);
       const float ecr = bb * pcr, eci = bb * pci;
       float qzr = 0.0f, qzi = 0.0f;
 #pragma unroll
