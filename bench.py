@@ -92,7 +92,7 @@ def time_fwd_bwd(cfg_name, steps, warmup):
     dy = torch.randn(cfg.B, cfg.L, cfg.H, cfg.N, generator=gen).to(dev)
     dhf = torch.randn(cfg.B, cfg.H, cfg.N, cfg.D, generator=gen).to(dev)
     fwd = PreparedForward(g["q"], g["k"], g["v"], g["beta"], g["sel_C"], g["dt"], g["r"], g["alpha"],
-                          g["omega"], g["c"], h0=g["h0"])
+                          g["omega"], g["c"], h0=g["h0"], train=True)
     bwd = PreparedBackward(fwd, dy, dhf)
     fwd()
     stream = torch.cuda.current_stream(dev)

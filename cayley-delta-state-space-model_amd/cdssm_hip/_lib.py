@@ -38,8 +38,11 @@ SIGNATURES = {
     "cdssm_fused_scan_bwd": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _P, _P, _P,
                                     _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                     _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "cdssm_fused_scan_fwd_train": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _P,
+                                          _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "cdssm_fused_scan_fwd_profile": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _P,
-                                            _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P]),
+                                            _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I32, _I32,
+                                            _P]),
     "cdssm_fused_scan_bwd_profile": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _P, _P, _P,
                                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                             _I64, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P]),

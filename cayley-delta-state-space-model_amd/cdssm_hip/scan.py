@@ -68,12 +68,14 @@ def _validate(q, k, v, beta, sel_C, dt, r, alpha, omega, h0, chunk_size):
 
 def chunkwise_delta_scan_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_C: Tensor, dt: Tensor,
                              r: Tensor, alpha: Tensor, omega: Tensor, c: float,
-                             h0: Optional[Tensor] = None, chunk_size: Optional[int] = None
-                             ) -> Tuple[Tensor, Tensor, Tensor]:
+                             h0: Optional[Tensor] = None, chunk_size: Optional[int] = None,
+                             train: bool = False) -> Tuple[Tensor, Tensor, Tensor]:
     """Forward only.  Returns (y (B,L,H,2), h_final (B,H,2,D) fp32, carry).
 
     ``carry`` is the workspace: the complex fp32 state entering every chunk,
-    shape (B, NC, H, D, 2) followed by the per-chunk rotation products.
+    shape (B, NC, H, D, 2), the per-chunk rotation products and, with
+    ``train=True`` (cdssm_fused_scan_fwd_train), the per-token dot products the
+    backward consumes.
     """
     B, L, H, D, N, Q, dtype = _validate(q, k, v, beta, sel_C, dt, r, alpha, omega, h0, chunk_size)
     lib = _lib.load()
@@ -86,11 +88,11 @@ def chunkwise_delta_scan_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_
     if nbytes <= 0:
         raise RuntimeError(f"cdssm_fused_scan_workspace_bytes rejected the shape ({nbytes})")
     ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
-    st = lib.cdssm_fused_scan_fwd(_lib.DTYPE_CODE[dtype], *[_lib.ptr(t) for t in ins[:7]],
-                                  _lib.ptr(ins[7]), _lib.ptr(ins[8]), float(c), _lib.ptr(h0c),
-                                  _lib.ptr(y), _lib.ptr(h_final), _lib.ptr(ws), B, L, H, D, N, Q,
-                                  _lib.stream_of(dev))
-    _lib.check(st, "cdssm_fused_scan_fwd")
+    fn = lib.cdssm_fused_scan_fwd_train if train else lib.cdssm_fused_scan_fwd
+    st = fn(_lib.DTYPE_CODE[dtype], *[_lib.ptr(t) for t in ins[:7]], _lib.ptr(ins[7]), _lib.ptr(ins[8]),
+            float(c), _lib.ptr(h0c), _lib.ptr(y), _lib.ptr(h_final), _lib.ptr(ws), B, L, H, D, N, Q,
+            _lib.stream_of(dev))
+    _lib.check(st, "cdssm_fused_scan_fwd_train" if train else "cdssm_fused_scan_fwd")
     return y, h_final, ws
 
 
@@ -109,8 +111,10 @@ class PreparedForward:
     and keep their shapes.
     """
 
-    def __init__(self, q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0=None, chunk_size=None):
+    def __init__(self, q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0=None, chunk_size=None,
+                 train: bool = False):
         B, L, H, D, N, Q, dtype = _validate(q, k, v, beta, sel_C, dt, r, alpha, omega, h0, chunk_size)
+        self.train = bool(train)
         for n, t in dict(q=q, k=k, v=v, beta=beta, sel_C=sel_C, dt=dt, r=r, alpha=alpha, omega=omega).items():
             if not t.is_contiguous():
                 raise ValueError(f"{n} must be contiguous for a prepared scan")
@@ -130,7 +134,8 @@ class PreparedForward:
                       B, L, H, D, N, Q)
 
     def __call__(self):
-        st = self._lib.cdssm_fused_scan_fwd(*self._args, _lib.stream_of(self.device))
+        fn = self._lib.cdssm_fused_scan_fwd_train if self.train else self._lib.cdssm_fused_scan_fwd
+        st = fn(*self._args, _lib.stream_of(self.device))
         if st != 0:
             _lib.check(st, "cdssm_fused_scan_fwd")
         return self.y, self.h_final
@@ -141,7 +146,8 @@ class PreparedForward:
         """Average milliseconds of each kernel launch over `iters` calls, from HIP
         events recorded on the launch stream between the launches."""
         out = (ctypes.c_float * len(self.PHASES))()
-        st = self._lib.cdssm_fused_scan_fwd_profile(*self._args, _lib.stream_of(self.device), int(iters), out)
+        st = self._lib.cdssm_fused_scan_fwd_profile(*self._args, _lib.stream_of(self.device), int(self.train),
+                                                    int(iters), out)
         if st != 0:
             _lib.check(st, "cdssm_fused_scan_fwd_profile")
         return dict(zip(self.PHASES, list(out)))
@@ -194,7 +200,7 @@ class ChunkwiseDeltaScanFn(torch.autograd.Function):
     def forward(ctx, q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0=None, chunk_size=None):
         B, L, H, D, N, Q, _ = _validate(q, k, v, beta, sel_C, dt, r, alpha, omega, h0, chunk_size)
         ins = [t.contiguous() for t in (q, k, v, beta, sel_C, dt, r, alpha, omega)]
-        y, h_final, ws = chunkwise_delta_scan_fwd(*ins, c, h0, Q)
+        y, h_final, ws = chunkwise_delta_scan_fwd(*ins, c, h0, Q, train=True)
         ctx.save_for_backward(*ins, ws)
         ctx.c = float(c)
         ctx.Q = Q
@@ -224,6 +230,9 @@ class PreparedBackward:
     """
 
     def __init__(self, fwd: PreparedForward, dy: Tensor, dh_final: Optional[Tensor] = None, c: float = None):
+        if not fwd.train:
+            raise ValueError("PreparedBackward needs a PreparedForward(..., train=True): the backward reads the "
+                             "per-token records the training forward keeps")
         q, k, v, beta, sel_C, dt, r, alpha, omega, h0 = fwd.inputs
         B, L, H, D, N, Q = fwd.shape
         self._lib = fwd._lib

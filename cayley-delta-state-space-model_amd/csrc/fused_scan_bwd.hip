@@ -51,10 +51,13 @@ struct BwdCfg {
   static constexpr int HPW = kWave / LPH;
   static constexpr int DPL = D / LPH;
 };
-// the correction-adjoint pass is light on registers: 16 lanes per head for both D
+// the correction-adjoint pass is light on registers and latency-bound
+#ifndef CDSSM_BWD_CORR_LPH
+#define CDSSM_BWD_CORR_LPH 16
+#endif
 template <int D>
 struct BwdCorrCfg {
-  static constexpr int LPH = 16;
+  static constexpr int LPH = CDSSM_BWD_CORR_LPH;
   static constexpr int HPW = kWave / LPH;
   static constexpr int DPL = D / LPH;
 };
@@ -83,7 +86,9 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
                                           const typename T::raw* __restrict__ dt,
                                           const typename T::raw* __restrict__ r,
                                           const typename T::raw* __restrict__ dy, float al, float om,
-                                          float c, const BwdScalars& s) {
+                                          float c, const BwdScalars& s,
+                                          const float4* __restrict__ saved = nullptr,
+                                          float4* __restrict__ sP = nullptr, float4* __restrict__ sG = nullptr) {
   constexpr int NB = kWave / HPW, TPB = HPW;
   const int lane = threadIdx.x;
   const int j = lane / NB;
@@ -107,6 +112,17 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
       sc[i] = T::load(sel_c + e);
       g0[i] = T::load(dy + 2 * e);
       g1[i] = T::load(dy + 2 * e + 1);
+    }
+    // the training forward's records: (p, pc), (c^_{t+1}.q, Y.q)
+    float4 rp[TPB], rq[TPB];
+    if constexpr (WITH_W) {
+#pragma unroll
+      for (int i = 0; i < TPB; ++i) {
+        const int t = min(t0 + i, tc.nt - 1);
+        const int64_t e = (tc.row0 + t) * H + hl;
+        rp[i] = saved[2 * e];
+        rq[i] = saved[2 * e + 1];
+      }
     }
     float ar[TPB], ai[TPB], Gr[TPB], Gi[TPB];
     float gpr = 1.0f, gpi = 0.0f;
@@ -146,9 +162,18 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
       cmul_acc(gr, gi, Gr[i], Gi[i]);
       float pr = egr, pi = egi;  // g_{t-1}
       if (i > 0) cmul_acc(pr, pi, Gr[i - 1], Gi[i - 1]);
-      if (WITH_W) s.S0[p] = make_float4(ar[i], ai[i], v0[i], v1[i]);
       s.S1[p] = make_float4(bb[i], g0[i], g1[i], 0.0f);
       s.S2[p] = make_float4(gr * g0[i] + gi * g1[i], gr * g1[i] - gi * g0[i], pr, pi);
+      if constexpr (WITH_W) {
+        s.S0[p] = make_float4(ar[i], ai[i], v0[i], v1[i]);
+        // past the last token: p = pc = 0 (inert), delta g = 0, Y.q = 0
+        const bool real = hok && t0 + i < tc.nt;
+        const float4 pp = real ? rp[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float4 qq = real ? rq[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        sP[p] = pp;
+        // delta g_t = f conj(c^_{t+1}.q), f = sel dy
+        sG[p] = make_float4(g0[i] * qq.x + g1[i] * qq.y, g1[i] * qq.x - g0[i] * qq.y, qq.z, qq.w);
+      }
     }
     float gtr = egr, gti = egi;
     cmul_acc(gtr, gti, gpr, gpi);
@@ -458,8 +483,9 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
     const typename T::raw* __restrict__ sel_c, const typename T::raw* __restrict__ dt,
     const typename T::raw* __restrict__ r, const float* __restrict__ alpha,
     const float* __restrict__ omega, float c, const typename T::raw* __restrict__ dy,
-    const float2* __restrict__ states, const float2* __restrict__ dsn, float2* __restrict__ ckpt,
-    typename T::raw* __restrict__ dq, typename T::raw* __restrict__ dk, typename T::raw* __restrict__ dv,
+    const float2* __restrict__ states, const float4* __restrict__ saved, const float2* __restrict__ dsn,
+    float2* __restrict__ ckpt, typename T::raw* __restrict__ dq, typename T::raw* __restrict__ dk,
+    typename T::raw* __restrict__ dv,
     typename T::raw* __restrict__ dbeta, typename T::raw* __restrict__ dsel,
     typename T::raw* __restrict__ ddt, typename T::raw* __restrict__ dr, float2* __restrict__ dhead_parts,
     int L, int H, int Q, int NC, int n_hg) {
@@ -485,12 +511,9 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   const int64_t chh = (int64_t(tc.b) * NC + tc.chunk) * H + hl;  // (b, chunk, head) index
   float2* ck = ckpt + ((int64_t(blockIdx.x) * HPW + hh) * nseg) * D + sub * DPL;
 
-  RowVec<T, DPL> kb[PF], qb[PF];
+  RowVec<T, DPL> kb[PF];
 #pragma unroll
-  for (int i = 0; i < PF; ++i) {
-    kb[i].load(kp + min(i, tlast) * stride);
-    qb[i].load(qp + min(i, tlast) * stride);
-  }
+  for (int i = 0; i < PF; ++i) kb[i].load(kp + min(i, tlast) * stride);
   float zr[DPL], zi[DPL], cr[DPL], ci[DPL];
   const float2* sp = states + chh * D + sub * DPL;
 #pragma unroll
@@ -503,23 +526,21 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   BwdScalars s{smem4, smem4 + slots, smem4 + 2 * slots};
   float4* sP = smem4 + 3 * slots;
   float4* sG = smem4 + 4 * slots;
-  stage_bwd<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, dy, al, om, c, s);
+  stage_bwd<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, dy, al, om, c, s, saved, sP, sG);
 #pragma unroll
-  for (int i = 0; i < PF; ++i) {
-    kb[i].pin();
-    qb[i].pin();
-  }
+  for (int i = 0; i < PF; ++i) kb[i].pin();
   __syncthreads();
 
-  // ---- forward pass ----
+  // ---- forward pass: z and c^ with the saved p_t, pc_t (no reductions) ----
   for (int tb = 0; tb < ntr; tb += PF) {
-    float4 s0[PF], s1[PF], s2[PF];
+    float4 s0[PF], pv[PF];
+    float bbv[PF];
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int p = (tb + i) * HPW + hh;
       s0[i] = s.S0[p];
-      s1[i] = s.S1[p];
-      s2[i] = s.S2[p];
+      bbv[i] = s.S1[p].x;
+      pv[i] = sP[p];
     }
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
@@ -529,59 +550,23 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
 #pragma unroll
         for (int jj = 0; jj < DPL; ++jj) ck[(t / CK) * D + jj] = make_float2(zr[jj], zi[jj]);
       }
-      float kk[DPL], qq[DPL];
+      float kk[DPL];
       kb[i].unpack_then_reload(kk);
-      qb[i].unpack_then_reload(qq);
       kb[i].load(kp + min(t + PF, tlast) * stride);
-      qb[i].load(qp + min(t + PF, tlast) * stride);
-      __builtin_amdgcn_sched_barrier(0);  // issue the reloads here, not sunk below later tokens
-      float pr = 0.0f, pi = 0.0f, pcr = 0.0f, pci = 0.0f;
-#pragma unroll
-      for (int jj = 0; jj < DPL; ++jj) {
-        pr = fmaf(zr[jj], kk[jj], pr);
-        pi = fmaf(zi[jj], kk[jj], pi);
-        pcr = fmaf(cr[jj], kk[jj], pcr);
-        pci = fmaf(ci[jj], kk[jj], pci);
-      }
-      pr = group_sum<LPH>(pr);
-      pi = group_sum<LPH>(pi);
-      pcr = group_sum<LPH>(pcr);
-      pci = group_sum<LPH>(pci);
-      const float ar = s0[i].x, ai = s0[i].y, bb = s1[i].x, fr = s1[i].y, fi = s1[i].z;
-      const float gpr = s2[i].z, gpi = s2[i].w;
-      const float bpr = bb * pr, bpi = bb * pi;
+      __builtin_amdgcn_sched_barrier(0);  // issue the reload here, not sunk below later tokens
+      const float ar = s0[i].x, ai = s0[i].y, bb = bbv[i];
+      const float bpr = bb * pv[i].x, bpi = bb * pv[i].y;
       const float er = s0[i].z - (ar * bpr - ai * bpi);
       const float ei = s0[i].w - (ar * bpi + ai * bpr);
-      const float ecr = bb * pcr, eci = bb * pci;
-      float yqr = 0.0f, yqi = 0.0f, cqr = 0.0f, cqi = 0.0f;
-      float dqv[DPL];
+      const float ecr = bb * pv[i].z, eci = bb * pv[i].w;
 #pragma unroll
       for (int jj = 0; jj < DPL; ++jj) {
         const float nr = fmaf(ar, zr[jj], fmaf(-ai, zi[jj], er * kk[jj]));
         const float ni = fmaf(ar, zi[jj], fmaf(ai, zr[jj], ei * kk[jj]));
-        // Y_t = z_t + g_{t-1} c^_t
-        const float Yr = nr + gpr * cr[jj] - gpi * ci[jj];
-        const float Yi = ni + gpr * ci[jj] + gpi * cr[jj];
-        dqv[jj] = Yr * fr + Yi * fi;
-        yqr = fmaf(Yr, qq[jj], yqr);
-        yqi = fmaf(Yi, qq[jj], yqi);
         zr[jj] = nr;
         zi[jj] = ni;
         cr[jj] = fmaf(-ecr, kk[jj], cr[jj]);
         ci[jj] = fmaf(-eci, kk[jj], ci[jj]);
-        cqr = fmaf(cr[jj], qq[jj], cqr);
-        cqi = fmaf(ci[jj], qq[jj], cqi);
-      }
-      if (t < tc.nt && hok) store_row<T, DPL>(dq + off + int64_t(t) * stride, dqv);
-      yqr = group_sum<LPH>(yqr);
-      yqi = group_sum<LPH>(yqi);
-      cqr = group_sum<LPH>(cqr);
-      cqi = group_sum<LPH>(cqi);
-      if (sub == 0) {
-        const int p = t * HPW + hh;
-        sP[p] = make_float4(pr, pi, pcr, pci);
-        // delta g_t = f conj(c^_{t+1}.q)
-        sG[p] = make_float4(fr * cqr + fi * cqi, fi * cqr - fr * cqi, yqr, yqi);
       }
     }
   }
@@ -662,11 +647,16 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
         R.k[i].unpack(kk);
         R.q[i].unpack(qq);
         float red[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        float dqv[DPL];
 #pragma unroll
         for (int jj = 0; jj < DPL; ++jj) {
           // c^_t = c^_{t+1} + beta pc k
           cr[jj] = fmaf(bb * pcr, kk[jj], cr[jj]);
           ci[jj] = fmaf(bb * pci, kk[jj], ci[jj]);
+          // dq = Re(conj(f) Y_t), Y_t = z_t + g_{t-1} c^_t
+          const float Yr = zbr[i + 1][jj] + s2.z * cr[jj] - s2.w * ci[jj];
+          const float Yi = zbi[i + 1][jj] + s2.z * ci[jj] + s2.w * cr[jj];
+          dqv[jj] = Yr * s1.y + Yi * s1.z;
           mr[jj] = fmaf(s1.y, qq[jj], mr[jj]);
           mi[jj] = fmaf(s1.z, qq[jj], mi[jj]);
           lr[jj] = fmaf(s2.x, qq[jj], lr[jj]);
@@ -722,7 +712,10 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
           lr[jj] = fmaf(-bslr, kk[jj], lr[jj]);
           li[jj] = fmaf(-bsli, kk[jj], li[jj]);
         }
-        if (hok) store_row<T, DPL>(dk + off + int64_t(t) * stride, dkv);
+        if (hok) {
+          store_row<T, DPL>(dk + off + int64_t(t) * stride, dkv);
+          store_row<T, DPL>(dq + off + int64_t(t) * stride, dqv);
+        }
         if (sub == 0) {
           sP[p] = make_float4(dar, dai, dwr, dwi);
           sG[p] = make_float4(dbe, 0.0f, gv.z, gv.w);
@@ -865,6 +858,7 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
   }
   const float2* states = reinterpret_cast<const float2*>(fwd_ws);
   const float2* gam = states + int64_t(B) * NC * H * D;
+  const float4* saved = reinterpret_cast<const float4*>(states + fwd_layout(B, L, H, D, Q).saved_offset());
   float2* lam0 = reinterpret_cast<float2*>(ws);
   float2* dsn = lam0 + w.n_lam;
   float2* segA = dsn + w.n_dsn;
@@ -895,7 +889,7 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
   hipLaunchKernelGGL((fused_bwd_main_kernel<T, D>), dim3(unsigned(tiles)), dim3(kWave),
                      size_t(slots) * 5 * sizeof(float4), stream, (const raw*)q, (const raw*)k, (const raw*)v,
                      (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c,
-                     (const raw*)dy, states, (const float2*)dsn, ckpt, (raw*)dq, (raw*)dk, (raw*)dv,
+                     (const raw*)dy, states, saved, (const float2*)dsn, ckpt, (raw*)dq, (raw*)dk, (raw*)dv,
                      (raw*)dbeta, (raw*)dsel, (raw*)ddt, (raw*)dr, parts, L, H, Q, NC, n_hg);
   st = cdssm_host::check_launch("cdssm_fused_scan_bwd/main");
   if (st) return st;

@@ -56,7 +56,6 @@ constexpr int kPrefetch = 8;
 #ifndef CDSSM_FWD_LPHS_BF16_D128
 #define CDSSM_FWD_LPHS_BF16_D128 16
 #endif
-constexpr int kSegLen = 16;  // chunks per carry segment
 
 template <typename T, int D, int LPH>
 struct FusedCfg {
@@ -527,15 +526,19 @@ __global__ __launch_bounds__(256) void fused_fwd_replay_kernel(float2* __restric
 // ---------------------------------------------------------------------------
 // Pass 4: per chunk, local state z (rescaled frame) and decay-free correction
 // c^ from s_k; output y_t = sel_C_t (f_t (zh_t . q_t) + g_{t-1} (c^_t . q_t)).
+// SAVE (training forward): also keeps, per (token, head), the dot products the
+// backward needs, saved[2 e] = (p_t, pc_t), saved[2 e + 1] = (c^_{t+1}.q_t,
+// Y_t.q_t), with p_t = z_{t-1}.k_t in true units and pc_t = c^_t.k_t, so the
+// backward recomputes the chunk states without any reduction.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int LPH>
+template <typename T, int D, int LPH, bool SAVE>
 __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
     const typename T::raw* __restrict__ q, const typename T::raw* __restrict__ k,
     const typename T::raw* __restrict__ v, const typename T::raw* __restrict__ beta,
     const typename T::raw* __restrict__ sel_c, const typename T::raw* __restrict__ dt,
     const typename T::raw* __restrict__ r, const float* __restrict__ alpha,
     const float* __restrict__ omega, float c, const float2* __restrict__ states,
-    typename T::raw* __restrict__ y, int L, int H, int Q, int NC, int n_hg) {
+    typename T::raw* __restrict__ y, float4* __restrict__ saved, int L, int H, int Q, int NC, int n_hg) {
   using Cfg = FusedCfg<T, D, LPH>;
   constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch;
   extern __shared__ float4 smem4[];
@@ -583,6 +586,9 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
   }
   __syncthreads();
 
+  float fpr = 1.0f, fpi = 0.0f;  // frame f_{t-1}
+  float4* svp = SAVE ? saved + 2 * ((tc.row0 * H) + (hok ? h : H - 1)) : nullptr;
+
   for (int tb = 0; tb < ntr; tb += PF) {
     float4 sa[PF], sb[PF];
     float2 sm[PF];
@@ -620,20 +626,36 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
       const float bb = sa[i].z;
       local_step<DPL>(zr, zi, kk, rm.test(t), sm[i], sa[i].x, sa[i].y, bb, pzr, pzi);
       const float ecr = bb * pcr, eci = bb * pci;
-      float qzr = 0.0f, qzi = 0.0f;
+      float qzr = 0.0f, qzi = 0.0f, cnr = 0.0f, cni = 0.0f;
 #pragma unroll
       for (int j = 0; j < DPL; ++j) {
         qzr = fmaf(zr[j], qq[j], qzr);
         qzi = fmaf(zi[j], qq[j], qzi);
         cr[j] = fmaf(-ecr, kk[j], cr[j]);
         ci[j] = fmaf(-eci, kk[j], ci[j]);
+        if (SAVE) {
+          cnr = fmaf(cr[j], qq[j], cnr);  // c^_{t+1}.q
+          cni = fmaf(ci[j], qq[j], cni);
+        }
       }
       // readout partial: f_t (zh_t.q) + g_{t-1} (c^_t.q)
       const float4 fb = sb[i];
       float Rr = (fb.x * qzr - fb.y * qzi) + (fb.z * qcr - fb.w * qci);
       float Ri = (fb.x * qzi + fb.y * qzr) + (fb.z * qci + fb.w * qcr);
-      yr[i] = sa[i].w * group_sum<LPH>(Rr);
-      yi[i] = sa[i].w * group_sum<LPH>(Ri);
+      Rr = group_sum<LPH>(Rr);
+      Ri = group_sum<LPH>(Ri);
+      yr[i] = sa[i].w * Rr;
+      yi[i] = sa[i].w * Ri;
+      if (SAVE) {
+        const float cqr = group_sum<LPH>(cnr), cqi = group_sum<LPH>(cni);
+        if (sub == 0 && hok && t < tc.nt) {
+          // p_t = f_{t-1} (zh_{t-1}.k_t)
+          svp[2 * int64_t(t) * H] = make_float4(fpr * pzr - fpi * pzi, fpr * pzi + fpi * pzr, pcr, pci);
+          svp[2 * int64_t(t) * H + 1] = make_float4(cqr, cqi, Rr, Ri);
+        }
+        fpr = fb.x;
+        fpi = fb.y;
+      }
     }
     if (sub == 0) {
 #pragma unroll
@@ -665,30 +687,11 @@ namespace {
 
 using namespace cdssm;
 
-struct FwdLayout {
-  int NC, S;
-  int64_t n_summ, n_gam, n_segA, n_segX;  // float2 counts, in workspace order
-  int64_t total() const { return n_summ + n_gam + n_segA + n_segX; }
-};
-
-FwdLayout fwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) {
-  FwdLayout w;
-  w.NC = int((L + chunk - 1) / chunk);
-  w.S = (w.NC + kSegLen - 1) / kSegLen;
-  w.n_summ = B * w.NC * H * D;
-  w.n_gam = B * w.NC * H;
-  w.n_segA = B * H * w.S;
-  w.n_segX = B * H * w.S * D;
-  return w;
-}
-
-// LPH: lanes per head of the main pass; LPHS: of the summary pass (its own
-// tile grid, so the lighter summary can run with more waves).
 template <typename T, int D, int LPH, int LPHS>
 int launch_fused_fwd(const void* q, const void* k, const void* v, const void* beta, const void* sel_c,
                      const void* dt, const void* r, const float* alpha, const float* omega, float c,
                      const float* h0, void* y, float* h_final, float* ws, int B, int L, int H, int Q,
-                     hipStream_t stream, hipEvent_t* ev) {
+                     hipStream_t stream, hipEvent_t* ev, bool save) {
   using raw = typename T::raw;
   constexpr int HPW = kWave / LPH, HPWS = kWave / LPHS;
   const FwdLayout w = fwd_layout(B, L, H, D, Q);
@@ -704,6 +707,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   float2* gam = summ + w.n_summ;
   float2* segA = gam + w.n_gam;
   float2* segX = segA + w.n_segA;
+  float4* saved = reinterpret_cast<float4*>(segX + w.n_segX + w.n_pad);
   const int slots = round_up(Q, kWave) * HPW, slots_s = round_up(Q, kWave) * HPWS;
 
   if (ev) (void)hipEventRecord(ev[0], stream);
@@ -728,10 +732,17 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   if (st) return st;
   if (ev) (void)hipEventRecord(ev[3], stream);
 
-  hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH>), dim3(unsigned(tiles)), dim3(kWave),
-                     size_t(slots) * (2 * sizeof(float4) + 2 * sizeof(float2)), stream, (const raw*)q,
-                     (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c, (const raw*)dt,
-                     (const raw*)r, alpha, omega, c, (const float2*)summ, (raw*)y, L, H, Q, NC, n_hg);
+  const size_t lds_main = size_t(slots) * (2 * sizeof(float4) + 2 * sizeof(float2));
+  if (save)
+    hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH, true>), dim3(unsigned(tiles)), dim3(kWave), lds_main,
+                       stream, (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,
+                       (const raw*)dt, (const raw*)r, alpha, omega, c, (const float2*)summ, (raw*)y, saved, L,
+                       H, Q, NC, n_hg);
+  else
+    hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH, false>), dim3(unsigned(tiles)), dim3(kWave), lds_main,
+                       stream, (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,
+                       (const raw*)dt, (const raw*)r, alpha, omega, c, (const float2*)summ, (raw*)y, nullptr,
+                       L, H, Q, NC, n_hg);
   st = cdssm_host::check_launch("cdssm_fused_scan_fwd/main");
   if (ev) (void)hipEventRecord(ev[4], stream);
   return st;
@@ -752,7 +763,7 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
                     const void* sel_c, const void* dt, const void* r, const float* alpha,
                     const float* omega, float c, const float* h0, void* y, float* h_final,
                     float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
-                    int64_t chunk, hipStream_t stream, hipEvent_t* ev) {
+                    int64_t chunk, hipStream_t stream, hipEvent_t* ev, bool save) {
   const char* op = "cdssm_fused_scan_fwd";
   if (dtype != 0 && dtype != 1) {
     cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
@@ -792,15 +803,15 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
   if (dtype == 1) {
     if (D == 64)
       return launch_fused_fwd<BF16, 64, CDSSM_FWD_LPH_BF16_D64, CDSSM_FWD_LPHS_BF16_D64>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                           workspace, b, l, hh, qc, stream, ev);
+                                           workspace, b, l, hh, qc, stream, ev, save);
     return launch_fused_fwd<BF16, 128, 16, CDSSM_FWD_LPHS_BF16_D128>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                           workspace, b, l, hh, qc, stream, ev);
+                                           workspace, b, l, hh, qc, stream, ev, save);
   }
   if (D == 64)
     return launch_fused_fwd<F32, 64, 16, 16>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                         workspace, b, l, hh, qc, stream, ev);
+                                         workspace, b, l, hh, qc, stream, ev, save);
   return launch_fused_fwd<F32, 128, 32, 32>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                        workspace, b, l, hh, qc, stream, ev);
+                                        workspace, b, l, hh, qc, stream, ev, save);
 }
 }  // namespace
 
@@ -811,7 +822,17 @@ extern "C" int cdssm_fused_scan_fwd(int dtype, const void* q, const void* k, con
                                     int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
                                     int64_t chunk, hipStream_t stream) {
   return fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace,
-                         B, L, H, D, N, chunk, stream, nullptr);
+                         B, L, H, D, N, chunk, stream, nullptr, false);
+}
+
+extern "C" int cdssm_fused_scan_fwd_train(int dtype, const void* q, const void* k, const void* v,
+                                          const void* beta, const void* sel_c, const void* dt,
+                                          const void* r, const float* alpha, const float* omega, float c,
+                                          const float* h0, void* y, float* h_final, float* workspace,
+                                          int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                          int64_t chunk, hipStream_t stream) {
+  return fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace,
+                         B, L, H, D, N, chunk, stream, nullptr, true);
 }
 
 extern "C" int cdssm_fused_scan_fwd_profile(int dtype, const void* q, const void* k, const void* v,
@@ -820,7 +841,7 @@ extern "C" int cdssm_fused_scan_fwd_profile(int dtype, const void* q, const void
                                             float c, const float* h0, void* y, float* h_final,
                                             float* workspace, int64_t B, int64_t L, int64_t H,
                                             int64_t D, int64_t N, int64_t chunk, hipStream_t stream,
-                                            int iters, float* phase_ms) {
+                                            int train, int iters, float* phase_ms) {
   if (iters < 1 || !phase_ms) {
     cdssm_host::set_error("cdssm_fused_scan_fwd_profile: iters >= 1 and phase_ms required");
     return CDSSM_EINVAL;
@@ -836,7 +857,7 @@ extern "C" int cdssm_fused_scan_fwd_profile(int dtype, const void* q, const void
   int st = CDSSM_OK;
   for (int it = 0; it < iters && st == CDSSM_OK; ++it) {
     st = fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace, B,
-                         L, H, D, N, chunk, stream, ev);
+                         L, H, D, N, chunk, stream, ev, train != 0);
     if (st != CDSSM_OK) break;
     if (hipEventSynchronize(ev[4]) != hipSuccess) {
       cdssm_host::set_error("cdssm_fused_scan_fwd_profile: hipEventSynchronize failed");

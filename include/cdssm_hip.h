@@ -55,6 +55,20 @@ int cdssm_fused_scan_fwd(int dtype, const void* q, const void* k, const void* v,
                          int64_t chunk, hipStream_t stream);
 
 /*
+ * Training forward (no counterpart in the reference; the reference keeps its
+ * passes' full outputs for backward instead): the forward above, which also
+ * stores in the workspace, per (token, head), the dot products of the chunk
+ * recurrences (p_t = z_{t-1}.k_t, c^_t.k_t, c^_{t+1}.q_t, Y_t.q_t; 32 bytes)
+ * so that the backward recomputes the chunk states without reductions.  Same
+ * arguments and workspace size as cdssm_fused_scan_fwd.
+ */
+int cdssm_fused_scan_fwd_train(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                               const void* sel_c, const void* dt, const void* r, const float* alpha,
+                               const float* omega, float c, const float* h0, void* y, float* h_final,
+                               float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                               int64_t chunk, hipStream_t stream);
+
+/*
  * Fused scan, backward.  Gradients are those the reference ops.py autograd
  * path produces for the same forward: exact for the readout (block.py:208-211),
  * for IntraChunkScanFn.backward (ops.py:123-135, intra_chunk_scan.cu:611-674)
@@ -64,7 +78,7 @@ int cdssm_fused_scan_fwd(int dtype, const void* q, const void* k, const void* v,
  * of the state after step t; and the exact chain rule of the scan-level
  * Cayley/gating formula for dt, r, alpha, omega.
  * Inputs: the forward's inputs, dy (B,L,H,N) of `dtype`, dh_final (B,H,N,D)
- * fp32 or NULL, and fwd_workspace as filled by cdssm_fused_scan_fwd.
+ * fp32 or NULL, and fwd_workspace as filled by cdssm_fused_scan_fwd_train.
  * Outputs: dq, dk, dv, dbeta, dsel_c, ddt, dr (shapes/dtype of the inputs),
  * dalpha, domega (H,) fp32, dh0 (B,H,N,D) fp32 or NULL.
  * workspace: cdssm_fused_scan_bwd_workspace_bytes() bytes.
@@ -87,13 +101,14 @@ int cdssm_fused_scan_bwd(int dtype, const void* q, const void* k, const void* v,
  *   forward  phase_ms[4]: chunk summaries, carry fold, carry replay, main pass;
  *   backward phase_ms[5]: correction adjoint, reverse-carry fold, reverse-carry
  *            replay, main pass, per-head reduction.
- * Arguments otherwise as cdssm_fused_scan_fwd / cdssm_fused_scan_bwd.
+ * `train` != 0 profiles cdssm_fused_scan_fwd_train.  Arguments otherwise as
+ * cdssm_fused_scan_fwd / cdssm_fused_scan_bwd.
  */
 int cdssm_fused_scan_fwd_profile(int dtype, const void* q, const void* k, const void* v, const void* beta,
                                  const void* sel_c, const void* dt, const void* r, const float* alpha,
                                  const float* omega, float c, const float* h0, void* y, float* h_final,
                                  float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
-                                 int64_t chunk, hipStream_t stream, int iters, float* phase_ms);
+                                 int64_t chunk, hipStream_t stream, int train, int iters, float* phase_ms);
 int cdssm_fused_scan_bwd_profile(int dtype, const void* q, const void* k, const void* v, const void* beta,
                                  const void* sel_c, const void* dt, const void* r, const float* alpha,
                                  const float* omega, float c, const void* dy, const float* dh_final,
