@@ -63,7 +63,11 @@ struct BwdCorrCfg {
 };
 constexpr int kBwdMaxHPW = 4;
 constexpr int kBwdCK = 4;     // z checkpoint interval of the main pass
-constexpr int kBwdPF = 8;     // row prefetch depth
+constexpr int kBwdPF = 8;     // row prefetch depth (main pass)
+#ifndef CDSSM_BWD_CORR_PF
+#define CDSSM_BWD_CORR_PF 8
+#endif
+constexpr int kBwdCorrPF = CDSSM_BWD_CORR_PF;  // row prefetch depth (correction-adjoint pass)
 
 // Per-token scalars of a backward tile in LDS, slot p = t*HPW + j:
 //   S0 = (a_re, a_im, w_re, w_im)       transition and write (w = beta vp v)
@@ -182,6 +186,47 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
   }
 }
 
+// Per-token scalars of the correction-adjoint pass: S1 = (beta, 0, 0, 0),
+// S2 = (h, 0, 0) with h = conj(g_t) sel_C dy, g_t read from the training
+// forward's records.  Slots past the last token and heads >= H are inert.
+template <typename T, int HPW>
+__device__ __forceinline__ void stage_corr(const ChunkTile& tc, int H, int ntr,
+                                           const typename T::raw* __restrict__ beta,
+                                           const typename T::raw* __restrict__ sel_c,
+                                           const typename T::raw* __restrict__ dy,
+                                           const float2* __restrict__ gsaved, const BwdScalars& s) {
+  constexpr int NB = kWave / HPW, TPB = HPW;
+  const int lane = threadIdx.x;
+  const int j = lane / NB;
+  const int blk = lane % NB;
+  const int hj = tc.hbase + j;
+  const bool hok = hj < H;
+  const int hl = hok ? hj : H - 1;
+  for (int tl = 0; tl < ntr; tl += kWave) {
+    const int t0 = tl + blk * TPB;
+    float bb[TPB], sc[TPB], g0[TPB], g1[TPB];
+    float2 gg[TPB];
+#pragma unroll
+    for (int i = 0; i < TPB; ++i) {
+      const int t = min(t0 + i, tc.nt - 1);
+      const int64_t e = (tc.row0 + t) * H + hl;
+      bb[i] = T::load(beta + e);
+      sc[i] = T::load(sel_c + e);
+      g0[i] = T::load(dy + 2 * e);
+      g1[i] = T::load(dy + 2 * e + 1);
+      gg[i] = gsaved[e];
+    }
+#pragma unroll
+    for (int i = 0; i < TPB; ++i) {
+      const bool real = hok && t0 + i < tc.nt;
+      const float fr = real ? sc[i] * g0[i] : 0.0f, fi = real ? sc[i] * g1[i] : 0.0f;
+      const int p = (t0 + i) * HPW + j;
+      s.S1[p] = make_float4(real ? bb[i] : 0.0f, 0.0f, 0.0f, 0.0f);
+      s.S2[p] = make_float4(gg[i].x * fr + gg[i].y * fi, gg[i].x * fi - gg[i].y * fr, 0.0f, 0.0f);
+    }
+  }
+}
+
 // Store a lane's DPL consecutive elements (bf16 pairs packed into dwords).
 template <typename T, int DPL>
 __device__ __forceinline__ void store_row(typename T::raw* p, const float (&x)[DPL]) {
@@ -218,11 +263,9 @@ template <typename T, int D>
 __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
     const typename T::raw* __restrict__ q, const typename T::raw* __restrict__ k,
     const typename T::raw* __restrict__ beta, const typename T::raw* __restrict__ sel_c,
-    const typename T::raw* __restrict__ dt, const typename T::raw* __restrict__ r,
-    const float* __restrict__ alpha, const float* __restrict__ omega, float c,
-    const typename T::raw* __restrict__ dy, float2* __restrict__ lam0, int L, int H, int Q, int NC,
-    int n_hg) {
-  constexpr int LPH = BwdCorrCfg<D>::LPH, HPW = BwdCorrCfg<D>::HPW, DPL = BwdCorrCfg<D>::DPL, PF = kBwdPF;
+    const typename T::raw* __restrict__ dy, const float2* __restrict__ gsaved, float2* __restrict__ lam0,
+    int L, int H, int Q, int NC, int n_hg) {
+  constexpr int LPH = BwdCorrCfg<D>::LPH, HPW = BwdCorrCfg<D>::HPW, DPL = BwdCorrCfg<D>::DPL, PF = kBwdCorrPF;
   extern __shared__ float4 smem4[];
   const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
@@ -246,7 +289,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
     qb[i].load(qp + min(ntr - 1 - i, tlast) * stride);
   }
   BwdScalars s{nullptr, smem4, smem4 + slots};
-  stage_bwd<T, HPW, false>(tc, H, ntr, nullptr, beta, sel_c, dt, r, dy, alpha[hl], omega[hl], c, s);
+  stage_corr<T, HPW>(tc, H, ntr, beta, sel_c, dy, gsaved, s);
 #pragma unroll
   for (int i = 0; i < PF; ++i) {
     kb[i].pin();
@@ -858,7 +901,9 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
   }
   const float2* states = reinterpret_cast<const float2*>(fwd_ws);
   const float2* gam = states + int64_t(B) * NC * H * D;
-  const float4* saved = reinterpret_cast<const float4*>(states + fwd_layout(B, L, H, D, Q).saved_offset());
+  const FwdLayout fw = fwd_layout(B, L, H, D, Q);
+  const float4* saved = reinterpret_cast<const float4*>(states + fw.saved_offset());
+  const float2* gsaved = states + fw.gsaved_offset();
   float2* lam0 = reinterpret_cast<float2*>(ws);
   float2* dsn = lam0 + w.n_lam;
   float2* segA = dsn + w.n_dsn;
@@ -870,8 +915,7 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
   if (ev) (void)hipEventRecord(ev[0], stream);
   hipLaunchKernelGGL((fused_bwd_corr_kernel<T, D>), dim3(unsigned(tiles_c)), dim3(kWave),
                      size_t(slots_c) * 2 * sizeof(float4), stream, (const raw*)q, (const raw*)k,
-                     (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c,
-                     (const raw*)dy, lam0, L, H, Q, NC, n_hgc);
+                     (const raw*)beta, (const raw*)sel_c, (const raw*)dy, gsaved, lam0, L, H, Q, NC, n_hgc);
   int st = cdssm_host::check_launch("cdssm_fused_scan_bwd/corr");
   if (st) return st;
   if (ev) (void)hipEventRecord(ev[1], stream);

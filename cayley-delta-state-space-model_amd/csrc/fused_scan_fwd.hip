@@ -127,7 +127,7 @@ __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, i
                                                    const float* __restrict__ alpha,
                                                    const float* __restrict__ omega, float c,
                                                    const TileScalars& s, float2* __restrict__ gam,
-                                                   int64_t gam_base) {
+                                                   int64_t gam_base, float2* __restrict__ gsv = nullptr) {
   constexpr int NB = kWave / HPW;
   constexpr int TPB = HPW;
   static_assert(NB * TPB == kWave, "blocks tile the slab");
@@ -261,6 +261,11 @@ __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, i
         float gr = egr, gi = egi;
         if (i > 0) cmul_acc(gr, gi, Gr[i - 1], Gi[i - 1]);
         s.B[p] = make_float4(lfr, lfi, gr, gi);
+        if (gsv && hok && t < tc.nt) {
+          // training forward: keep g_t for the backward's correction adjoint
+          cmul_acc(gr, gi, ar[i], ai[i]);
+          gsv[(tc.row0 + t) * H + hj] = make_float2(gr, gi);
+        }
       }
       const float mr = fpr * ar[i] - fpi * ai[i], mi = fpr * ai[i] + fpi * ar[i];
       s.M[p] = reset[i] ? make_float2(mr, mi) : make_float2(1.0f, 0.0f);
@@ -529,7 +534,8 @@ __global__ __launch_bounds__(256) void fused_fwd_replay_kernel(float2* __restric
 // SAVE (training forward): also keeps, per (token, head), the dot products the
 // backward needs, saved[2 e] = (p_t, pc_t), saved[2 e + 1] = (c^_{t+1}.q_t,
 // Y_t.q_t), with p_t = z_{t-1}.k_t in true units and pc_t = c^_t.k_t, so the
-// backward recomputes the chunk states without any reduction.
+// backward recomputes the chunk states without any reduction, and gsaved[e] =
+// g_t (the in-chunk decay product the correction adjoint needs).
 // ---------------------------------------------------------------------------
 template <typename T, int D, int LPH, bool SAVE>
 __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
@@ -538,7 +544,8 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
     const typename T::raw* __restrict__ sel_c, const typename T::raw* __restrict__ dt,
     const typename T::raw* __restrict__ r, const float* __restrict__ alpha,
     const float* __restrict__ omega, float c, const float2* __restrict__ states,
-    typename T::raw* __restrict__ y, float4* __restrict__ saved, int L, int H, int Q, int NC, int n_hg) {
+    typename T::raw* __restrict__ y, float4* __restrict__ saved, float2* __restrict__ gsaved, int L, int H,
+    int Q, int NC, int n_hg) {
   using Cfg = FusedCfg<T, D, LPH>;
   constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch;
   extern __shared__ float4 smem4[];
@@ -578,7 +585,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
   TileScalars s{smem4, smem4 + slots, reinterpret_cast<float2*>(smem4 + 2 * slots)};
   float2* s_y = s.M + slots;
   const ResetMask rm = stage_scalars<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, alpha, omega, c, s,
-                                                   nullptr, 0);
+                                                   nullptr, 0, SAVE ? gsaved : nullptr);
 #pragma unroll
   for (int i = 0; i < PF; ++i) {
     kb[i].pin();
@@ -708,6 +715,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   float2* segA = gam + w.n_gam;
   float2* segX = segA + w.n_segA;
   float4* saved = reinterpret_cast<float4*>(segX + w.n_segX + w.n_pad);
+  float2* gsaved = reinterpret_cast<float2*>(ws) + w.gsaved_offset();
   const int slots = round_up(Q, kWave) * HPW, slots_s = round_up(Q, kWave) * HPWS;
 
   if (ev) (void)hipEventRecord(ev[0], stream);
@@ -736,13 +744,13 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   if (save)
     hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH, true>), dim3(unsigned(tiles)), dim3(kWave), lds_main,
                        stream, (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,
-                       (const raw*)dt, (const raw*)r, alpha, omega, c, (const float2*)summ, (raw*)y, saved, L,
-                       H, Q, NC, n_hg);
+                       (const raw*)dt, (const raw*)r, alpha, omega, c, (const float2*)summ, (raw*)y, saved,
+                       gsaved, L, H, Q, NC, n_hg);
   else
     hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH, false>), dim3(unsigned(tiles)), dim3(kWave), lds_main,
                        stream, (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,
                        (const raw*)dt, (const raw*)r, alpha, omega, c, (const float2*)summ, (raw*)y, nullptr,
-                       L, H, Q, NC, n_hg);
+                       nullptr, L, H, Q, NC, n_hg);
   st = cdssm_host::check_launch("cdssm_fused_scan_fwd/main");
   if (ev) (void)hipEventRecord(ev[4], stream);
   return st;

@@ -75,7 +75,8 @@ def test_workspace_size_formula():
         carry = B * NC * H * D + B * NC * H + B * H * S * (D + 1)   # float2 counts
         pad = carry & 1               # the training records start 16-byte aligned
         saved = 4 * B * L * H         # (p, pc), (c.q, Y.q) per token-head: 2 float4
-        return (carry + pad + saved) * 8
+        gsaved = B * L * H            # g_t per token-head: float2
+        return (carry + pad + saved + gsaved) * 8
     assert lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, N, Q) == expect(L)
     assert lib.cdssm_fused_scan_workspace_bytes(B, 100, H, D, N, Q) == expect(100)
     assert lib.cdssm_fused_scan_workspace_bytes(0, L, H, D, N, Q) == -1
