@@ -3,17 +3,20 @@
 Default workload (the metric's headline shape): forward
 scan, B=8 H=16 L=4096 D=Q=64 N=2, bf16 q/k/v/gates, fp32 state, synthetic
 inputs drawn as the configuration text specifies (seed 0), zero initial state.
-One step = one forward scan over the batch (four kernel launches: chunk
-summaries, carry fold, carry replay, main pass).
+One step = one forward scan over the batch: at C1 one launch of the one-pass
+kernel (chunk scans, look-back carry and correction in one kernel); shapes it
+cannot take run as four launches (chunk summaries, carry fold, carry replay,
+main pass).
 
 Prints ONE JSON line with the metric, the roofline of the dominant kernel (the
-main pass, which reads every algorithmic byte: q, k, v, beta, sel_C, dt, r and
-writes y) against HBM, and a CPU baseline: the fp32 CPU restatement of the
-reference algorithm (oracle/cdssm_oracle.py) timed on this host's cores on a
-bounded sample.  Kernel durations come from HIP events recorded on the launch
-stream between the launches (cdssm_fused_scan_fwd_profile).  `traffic` is the
-HBM bytes per main-pass launch measured by rocprofv3 counters and recorded in
-profiles/ (see the file named below), or null when that file is absent.
+one-pass kernel, or the four-launch scan's main pass; either reads every
+algorithmic byte: q, k, v, beta, sel_C, dt, r, and writes y) against HBM, and a
+CPU baseline: the fp32 CPU restatement of the reference algorithm
+(oracle/cdssm_oracle.py) timed on this host's cores on a bounded sample.
+Kernel durations come from HIP events recorded on the launch stream around the
+launches (cdssm_fused_scan_fwd_profile).  `traffic` is the HBM bytes per launch
+of that kernel measured by rocprofv3 counters and recorded in profiles/ (the
+file named below), or null when that file is absent.
 """
 
 from __future__ import annotations
@@ -33,14 +36,17 @@ for _p in (ROOT, PKG_DIR):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor peak
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fused_fwd_main_C1_hbm_traffic.txt")
+TRAFFIC_FILES = {
+    "fused_fwd_onepass_kernel": os.path.join(ROOT, "profiles", "fused_fwd_onepass_C1_hbm_traffic.txt"),
+    "fused_fwd_main_kernel": os.path.join(ROOT, "profiles", "fused_fwd_main_C1_hbm_traffic.txt"),
+}
 
 
-def recorded_traffic():
-    """Bytes per main-pass launch from the committed counter summary
+def recorded_traffic(path):
+    """Bytes per launch from a committed counter summary
     (`traffic_bytes_per_launch: N` line), or None."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
                     return float(line.split(":", 1)[1])
@@ -227,11 +233,14 @@ def main():
     # per-kernel durations, HIP events between the launches on the launch stream
     phases = run.profile(args.steps)
     main_ms = phases["main"]
+    one_pass = all(phases[k] == 0.0 for k in ("summary", "carry_fold", "carry_replay"))
+    kernel = "fused_fwd_onepass_kernel" if one_pass else "fused_fwd_main_kernel"
+    traffic_file = TRAFFIC_FILES[kernel]
 
     tokens = cfg.B * cfg.L
     alg = scan_bytes(cfg)["fwd"]
     achieved = alg / (main_ms * 1e-3) / 1e9
-    traffic = recorded_traffic() if args.config == "C1" else None
+    traffic = recorded_traffic(traffic_file) if args.config == "C1" else None
     out = {
         "metric": "scan tokens/sec (fwd), B8 H16 L4096 D64 bf16" if args.config == "C1"
                   else "scan tokens/sec (fwd), B1 H32 L65536 D64 bf16",
@@ -251,14 +260,15 @@ def main():
                    "h0": cfg.h0_std > 0, "global_batch": cfg.B, "seq_len": cfg.L},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "fused_fwd_main_kernel",
+                     "kernel": kernel,
                      "basis": (f"algorithmic {alg / 1e6:.2f} MB per launch (272 B per token-head: q, k, v, "
-                               f"beta, sel_C, dt, r read, y written) / main-pass launch {main_ms * 1e3:.2f} us "
+                               f"beta, sel_C, dt, r read, y written) / {kernel} launch {main_ms * 1e3:.2f} us "
                                f"(HIP events, mean of {args.steps})"),
-                     "traffic_source": (os.path.relpath(TRAFFIC_FILE, ROOT) if traffic is not None else None)},
+                     "traffic_source": (os.path.relpath(traffic_file, ROOT) if traffic is not None else None)},
         "whole_call": {"ms": call_ms, "achieved_GBs": alg / (call_ms * 1e-3) / 1e9,
                        "frac": alg / (call_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                       "note": "all four launches of one scan call, median of 50 event-timed calls"},
+                       "note": ("one launch" if one_pass else "all four launches") +
+                               " of one scan call, median of 50 event-timed calls"},
         "phase_ms": phases,
         "cold_ms_per_call": cold_ms,
         "cold_frac": alg / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,

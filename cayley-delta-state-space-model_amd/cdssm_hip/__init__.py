@@ -6,7 +6,7 @@ touch the GPU; the library is loaded on first use and its absence is an error.
 """
 
 from .scan import (ChunkwiseDeltaScanFn, chunkwise_delta_scan, chunkwise_delta_scan_bwd,  # noqa: F401
-                   chunkwise_delta_scan_fwd, chunkwise_delta_scan_train)
+                   chunkwise_delta_scan_fwd, chunkwise_delta_scan_train, set_forward_path)
 
 from .ops import (DynamicsFusedFn, ExactCorrectionFn, InterChunkScanFn,  # noqa: F401
                   IntraChunkScanFn, NormalizeKQFn)
@@ -14,4 +14,4 @@ from .ssd import SSDChunkwiseScan  # noqa: F401
 
 __all__ = ["DynamicsFusedFn", "NormalizeKQFn", "IntraChunkScanFn", "InterChunkScanFn", "ExactCorrectionFn",
            "SSDChunkwiseScan", "ChunkwiseDeltaScanFn", "chunkwise_delta_scan", "chunkwise_delta_scan_fwd",
-           "chunkwise_delta_scan_bwd", "chunkwise_delta_scan_train"]
+           "chunkwise_delta_scan_bwd", "chunkwise_delta_scan_train", "set_forward_path"]

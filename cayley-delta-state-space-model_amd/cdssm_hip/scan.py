@@ -96,6 +96,26 @@ def chunkwise_delta_scan_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_
     return y, h_final, ws
 
 
+FORWARD_PATHS = {"auto": 0, "four_launch": 1, "one_pass": 2}
+
+
+def set_forward_path(path: str) -> str:
+    """Select how the inference forward is launched; returns the previous setting.
+
+    "auto" (default) takes the one-pass kernel wherever its whole grid is
+    resident at once and a sequence has at most 64 segments of 4 chunks, else
+    the four-launch scan; "four_launch" always takes the four-launch scan;
+    "one_pass" requires the one-pass kernel (calls it cannot serve raise).
+    Process-wide; the training forward always takes the four-launch scan.
+    """
+    if path not in FORWARD_PATHS:
+        raise ValueError(f"path must be one of {sorted(FORWARD_PATHS)}, got {path!r}")
+    prev = _lib.load().cdssm_fused_scan_fwd_set_path(FORWARD_PATHS[path])
+    if prev < 0:
+        _lib.check(prev, "cdssm_fused_scan_fwd_set_path")
+    return {v: n for n, v in FORWARD_PATHS.items()}[prev]
+
+
 def chunkwise_delta_scan(q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0=None, chunk_size=None):
     """y (B,L,H,2) and the final R-mode state (B,H,2,D) of the fused scan."""
     y, h_final, _ = chunkwise_delta_scan_fwd(q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0, chunk_size)
@@ -105,7 +125,7 @@ def chunkwise_delta_scan(q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0=None, 
 class PreparedForward:
     """A forward scan with inputs, outputs and workspace bound once.
 
-    Calling it re-launches the three kernels on torch's current stream with no
+    Calling it re-launches the scan's kernels on torch's current stream with no
     validation, allocation or tensor creation on the host: the launch path for
     serving loops, graph capture and timing.  The bound tensors must stay alive
     and keep their shapes.
@@ -144,7 +164,8 @@ class PreparedForward:
 
     def profile(self, iters: int) -> dict:
         """Average milliseconds of each kernel launch over `iters` calls, from HIP
-        events recorded on the launch stream between the launches."""
+        events recorded on the launch stream between the launches.  A call that
+        takes the one-pass kernel reports it as "main" and 0 for the others."""
         out = (ctypes.c_float * len(self.PHASES))()
         st = self._lib.cdssm_fused_scan_fwd_profile(*self._args, _lib.stream_of(self.device), int(self.train),
                                                     int(iters), out)

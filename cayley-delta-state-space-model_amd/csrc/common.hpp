@@ -189,17 +189,22 @@ __device__ __forceinline__ void cmul_acc(float& xr, float& xi, float yr, float y
 // ---------------------------------------------------------------------------
 // Forward workspace layout shared by the forward and the backward (float2
 // units): entering states (B, NC, H, D), chunk rotations (B, NC, H), carry
-// segment maps (B, H, S) and (B, H, S, D), a pad to 16 bytes, then the
-// training forward's per-token records (B, L, H, 2) float4 and (B, L, H) float2.
+// segment maps (B, H, S) and (B, H, S, D), a pad to 16 bytes, the training
+// forward's per-token records (B, L, H, 2) float4 and (B, L, H) float2, then
+// the one-pass forward's look-back area over segments of kOnePassW chunks:
+// segment maps (B, NSEG, H, D), leaving states (B, NSEG, H, D), segment
+// rotations (B, NSEG, H) and flags (B, NSEG, H) (8-byte words).
 // ---------------------------------------------------------------------------
-constexpr int kSegLen = 16;  // chunks per forward carry segment
+constexpr int kSegLen = 16;   // chunks per forward carry segment
+constexpr int kOnePassW = 4;  // chunks (waves) per workgroup of the one-pass forward
 
 struct FwdLayout {
-  int NC, S;
-  int64_t n_summ, n_gam, n_segA, n_segX, n_pad, n_saved, n_gsaved;
-  int64_t total() const { return n_summ + n_gam + n_segA + n_segX + n_pad + n_saved + n_gsaved; }
+  int NC, S, NSEG;
+  int64_t n_summ, n_gam, n_segA, n_segX, n_pad, n_saved, n_gsaved, n_op;
+  int64_t total() const { return n_summ + n_gam + n_segA + n_segX + n_pad + n_saved + n_gsaved + n_op; }
   int64_t saved_offset() const { return n_summ + n_gam + n_segA + n_segX + n_pad; }
   int64_t gsaved_offset() const { return saved_offset() + n_saved; }
+  int64_t onepass_offset() const { return gsaved_offset() + n_gsaved; }
 };
 
 inline FwdLayout fwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) {
@@ -213,6 +218,8 @@ inline FwdLayout fwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t 
   w.n_pad = (w.n_summ + w.n_gam + w.n_segA + w.n_segX) & 1;
   w.n_saved = 4 * B * L * H;
   w.n_gsaved = B * L * H;
+  w.NSEG = (w.NC + kOnePassW - 1) / kOnePassW;
+  w.n_op = B * w.NSEG * H * (2 * D + 2);
   return w;
 }
 

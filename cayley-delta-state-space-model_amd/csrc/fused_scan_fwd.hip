@@ -39,6 +39,10 @@
 // kPrefetch tokens ahead, so the loop carries no branch and the memory waits
 // count only the oldest load.  Tokens past the end of a ragged last chunk are
 // inert steps (a = 1, w = 0, beta = 0).
+#include <atomic>
+#include <chrono>
+#include <mutex>
+
 #include "common.hpp"
 
 namespace cdssm {
@@ -116,7 +120,8 @@ __device__ __forceinline__ uint64_t spread8(uint64_t x) {
 // sequentially over its own tokens, and joins them across the head's NB
 // lanes with log2(NB) shuffle steps.  Slots past the last token and heads
 // >= H hold inert steps (a = 1, w = 0, beta = 0).  Summary pass (MAIN false):
-// writes G_k = g over the chunk to gam and the last frame f to B[j].
+// writes G_k = g over the chunk to gam and the last frame f to B[j]; with
+// cend (MAIN true) the same pair goes to cend[j].
 template <typename T, int HPW, bool MAIN>
 __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, int ntr,
                                                    const typename T::raw* __restrict__ v,
@@ -127,11 +132,12 @@ __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, i
                                                    const float* __restrict__ alpha,
                                                    const float* __restrict__ omega, float c,
                                                    const TileScalars& s, float2* __restrict__ gam,
-                                                   int64_t gam_base, float2* __restrict__ gsv = nullptr) {
+                                                   int64_t gam_base, float2* __restrict__ gsv = nullptr,
+                                                   float4* __restrict__ cend = nullptr) {
   constexpr int NB = kWave / HPW;
   constexpr int TPB = HPW;
   static_assert(NB * TPB == kWave, "blocks tile the slab");
-  const int lane = threadIdx.x;
+  const int lane = int(threadIdx.x) % kWave;  // lane in the wave (the one-pass workgroup has several)
   const int j = lane / NB;
   const int blk = lane % NB;
   const int hj = tc.hbase + j;
@@ -304,6 +310,8 @@ __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, i
     if (hok) gam[gam_base + j] = make_float2(cgr, cgi);
     s.B[j] = make_float4(cfr, cfi, 0.0f, 0.0f);
   }
+  // one-pass forward: (G_k, frame after the last step) per head of the tile
+  if (MAIN && cend && blk == 0) cend[j] = make_float4(cgr, cgi, cfr, cfi);
   rm.m0 = __builtin_amdgcn_readfirstlane(uint32_t(rm.m0)) |
           (uint64_t(__builtin_amdgcn_readfirstlane(uint32_t(rm.m0 >> 32))) << 32);
   rm.m1 = __builtin_amdgcn_readfirstlane(uint32_t(rm.m1)) |
@@ -685,6 +693,424 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// One-pass forward (inference): the four passes above in one launch.
+// A workgroup of kOnePassW waves takes kOnePassW consecutive chunks (a
+// segment) of one (b, head group); wave w owns chunk seg * kOnePassW + w.
+//   1. each wave stages its chunk's scalars and runs the local recurrence
+//      (rescaled frame), keeping the local readout f_t (zh_t . q_t) in LDS;
+//      its chunk map is (G_k, F_k = z_{Q-1});
+//   2. the segment's chunk maps are composed through LDS into the segment
+//      map, which is published; the state entering the segment is found by a
+//      decoupled look-back over the earlier segments of the same (b, head
+//      group): published maps are composed, nearest first, until a published
+//      leaving state is met (segment 0 starts from h0).  The state leaving the
+//      segment is then published for the later segments;
+//   3. each wave derives the state entering its chunk and runs the decay-free
+//      correction with the full readout; y is written coalesced.
+// Look-back flags hold epoch << 2 | state (1: map, 2: leaving state) with a
+// per-call epoch, so the workspace needs no clearing between calls.  Published
+// data and flags are written and read with agent-scope atomics (stores written
+// through to the device-coherent level, loads served from it), so no cache
+// maintenance is needed: a writer waits until its data stores are acknowledged
+// before the flag is stored, and a reader issues its data loads only after it
+// has seen the flag (agent-scope release / acquire fences would write back or
+// invalidate the whole L2 instead, microseconds per publish and the k, q rows
+// the correction pass re-reads).  A workgroup waits only on
+// workgroups of lower index, and the launcher takes this path only when the
+// whole grid is resident at once; a bounded wait turns a missing flag into NaN
+// output instead of a hang.
+// ---------------------------------------------------------------------------
+constexpr int kLookbackBatch = 8;
+constexpr int kOnePassMaxSeg = 64;
+constexpr uint64_t kSpinTicks = 5000000;  // look-back wait bound: 50 ms of the 100 MHz real-time counter
+
+struct OnePassBufs {
+  float2* seg_f;             // (B, NSEG, H, D) segment map F: state at the segment's end from zero
+  float2* seg_s;             // (B, NSEG, H, D) state leaving the segment
+  float2* seg_g;             // (B, NSEG, H)    segment rotation product
+  unsigned long long* flag;  // (B, NSEG, H); entry hbase serves the head group
+};
+
+// Wait until this wave's earlier stores are acknowledged; also a compiler
+// barrier, so no memory access moves across it.
+__device__ __forceinline__ void wait_stores_acked() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ void st_agent(float2* p, float2 v) {
+  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), __builtin_bit_cast(unsigned long long, v),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 ld_agent(const float2* p) {
+  const unsigned long long x = __hip_atomic_load(
+      reinterpret_cast<unsigned long long*>(const_cast<float2*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __builtin_bit_cast(float2, x);
+}
+
+template <typename T, int D, int LPH>
+__global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(
+    const typename T::raw* __restrict__ q, const typename T::raw* __restrict__ k,
+    const typename T::raw* __restrict__ v, const typename T::raw* __restrict__ beta,
+    const typename T::raw* __restrict__ sel_c, const typename T::raw* __restrict__ dt,
+    const typename T::raw* __restrict__ r, const float* __restrict__ alpha,
+    const float* __restrict__ omega, float c, const float* __restrict__ h0, typename T::raw* __restrict__ y,
+    float* __restrict__ h_final, OnePassBufs ob, unsigned long long epoch, int L, int H, int Q, int NC,
+    int NSEG, int n_hg) {
+  using Cfg = FusedCfg<T, D, LPH>;
+  constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch, W = kOnePassW;
+  constexpr int SEGN = HPW * D;  // complex elements of a head group's state
+  constexpr int EPT = DPL / W;   // of which each thread of the workgroup composes EPT
+  static_assert(EPT * W == DPL && EPT * kWave * W == SEGN, "segment state tiles the workgroup");
+  extern __shared__ float4 smem4[];
+
+  // wave index made wave-uniform, so the tile's fields live in scalar registers
+  const int wv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+  const int lane = int(threadIdx.x) % kWave;
+  const int n_chain = int(gridDim.x) / NSEG;
+  const int chain = int(blockIdx.x) % n_chain;
+  const int seg = int(blockIdx.x) / n_chain;
+  const int bi = chain / n_hg;
+  const int hbase = (chain % n_hg) * HPW;
+  const int n_live = min(W, NC - seg * W);  // chunks in this segment
+  const bool live = wv < n_live;
+
+  ChunkTile tc;
+  tc.b = bi;
+  tc.chunk = min(seg * W + wv, NC - 1);
+  tc.hbase = hbase;
+  tc.t0 = tc.chunk * Q;
+  tc.nt = min(Q, L - tc.t0);
+  tc.row0 = int64_t(bi) * L + tc.t0;
+
+  const int hh = lane / LPH;
+  const int sub = lane % LPH;
+  const int h = hbase + hh;
+  const bool hok = h < H;
+  const int ntr = round_up(tc.nt, PF);
+  const int slots = round_up(Q, kWave) * HPW;
+
+  // LDS: per wave the A, B (float4) and M, Y (float2) token slots; then the
+  // segment's chunk maps (F per wave, (G, last frame) per wave and head), the
+  // state entering the segment and the look-back result
+  float4* wbase = smem4 + size_t(wv) * 3 * slots;
+  TileScalars s{wbase, wbase + slots, reinterpret_cast<float2*>(wbase + 2 * slots)};
+  float2* s_y = s.M + slots;
+  float2* Fx = reinterpret_cast<float2*>(smem4 + size_t(W) * 3 * slots);
+  float4* GF = reinterpret_cast<float4*>(Fx + W * SEGN);
+  float2* Sx = reinterpret_cast<float2*>(GF + W * HPW);
+  int* ctrl = reinterpret_cast<int*>(Sx + SEGN);
+
+  const int64_t stride = int64_t(H) * D;
+  const int64_t off = (tc.row0 * H + (hok ? h : H - 1)) * D + sub * DPL;
+  const typename T::raw* kp = k + off;
+  const typename T::raw* qp = q + off;
+  const int tlast = tc.nt - 1;
+  RowVec<T, DPL> kb[PF], qb[PF];
+  float zr[DPL], zi[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) zr[j] = zi[j] = 0.0f;
+  ResetMask rm{0ull, 0ull};
+
+  if (live) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      kb[i].load(kp + min(i, tlast) * stride);
+      qb[i].load(qp + min(i, tlast) * stride);
+    }
+    rm = stage_scalars<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, alpha, omega, c, s, nullptr, 0,
+                                     nullptr, GF + wv * HPW);
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      kb[i].pin();
+      qb[i].pin();
+    }
+  }
+  __syncthreads();
+
+  // 1. local recurrence with the local readout f_t (zh_t . q_t); in the last
+  // PF steps the prefetch wraps to the first tokens, for the correction pass
+  if (live) {
+    for (int tb = 0; tb < ntr; tb += PF) {
+      float4 sa[PF], sb[PF];
+      float2 sm[PF];
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        sa[i] = s.A[(tb + i) * HPW + hh];
+        sb[i] = s.B[(tb + i) * HPW + hh];
+        sm[i] = s.M[(tb + i) * HPW + hh];
+      }
+      float yr[PF], yi[PF];
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        const int t = tb + i;
+        float kk[DPL], qq[DPL];
+        kb[i].unpack_then_reload(kk);
+        qb[i].unpack_then_reload(qq);
+        int tn = t + PF;
+        tn = tn < ntr ? tn : tn - ntr;
+        kb[i].load(kp + min(tn, tlast) * stride);
+        qb[i].load(qp + min(tn, tlast) * stride);
+        float pr0 = 0.0f, pi0 = 0.0f, pr1 = 0.0f, pi1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < DPL; j += 2) {
+          pr0 = fmaf(zr[j], kk[j], pr0);
+          pi0 = fmaf(zi[j], kk[j], pi0);
+          pr1 = fmaf(zr[j + 1], kk[j + 1], pr1);
+          pi1 = fmaf(zi[j + 1], kk[j + 1], pi1);
+        }
+        const float pr = group_sum<LPH>(pr0 + pr1);
+        const float pi = group_sum<LPH>(pi0 + pi1);
+        local_step<DPL>(zr, zi, kk, rm.test(t), sm[i], sa[i].x, sa[i].y, sa[i].z, pr, pi);
+        float qzr = 0.0f, qzi = 0.0f;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          qzr = fmaf(zr[j], qq[j], qzr);
+          qzi = fmaf(zi[j], qq[j], qzi);
+        }
+        const float4 fb = sb[i];
+        yr[i] = group_sum<LPH>(fb.x * qzr - fb.y * qzi);
+        yi[i] = group_sum<LPH>(fb.x * qzi + fb.y * qzr);
+      }
+      if (sub == 0) {
+#pragma unroll
+        for (int i = 0; i < PF; ++i) s_y[(tb + i) * HPW + hh] = make_float2(yr[i], yi[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      kb[i].pin();
+      qb[i].pin();
+    }
+    // chunk map F = f_end zh (zero for heads >= H: their steps are inert)
+    const float4 ge = GF[wv * HPW + hh];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j)
+      Fx[wv * SEGN + hh * D + sub * DPL + j] =
+          make_float2(ge.z * zr[j] - ge.w * zi[j], ge.z * zi[j] + ge.w * zr[j]);
+  }
+  __syncthreads();
+
+  // 2. segment map over the live chunks; thread x composes elements
+  // e = x * EPT + i of the head group's state (head e / D, element e % D)
+  const int e0 = int(threadIdx.x) * EPT;
+  const int ej = e0 / D;
+  const int ed = e0 % D;
+  const int eh = hbase + ej;
+  const bool ehok = eh < H;
+  float2 segF[EPT];
+  float2 segG = make_float2(1.0f, 0.0f);
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) segF[i] = make_float2(0.0f, 0.0f);
+  for (int u = 0; u < n_live; ++u) {
+    const float4 g = GF[u * HPW + ej];
+    const float2 gu = make_float2(g.x, g.y);
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const float2 f = Fx[u * SEGN + e0 + i];
+      segF[i] = make_float2(gu.x * segF[i].x - gu.y * segF[i].y + f.x, gu.x * segF[i].y + gu.y * segF[i].x + f.y);
+    }
+    segG = make_float2(gu.x * segG.x - gu.y * segG.y, gu.x * segG.y + gu.y * segG.x);
+  }
+  const int64_t sb0 = (int64_t(bi) * NSEG + seg) * H;  // (b, seg, head 0)
+  unsigned long long* flag = ob.flag + sb0 + hbase;
+
+  float2 Sin[EPT];  // state entering the segment
+  if (seg == 0) {
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      Sin[i] = make_float2(0.0f, 0.0f);
+      if (h0 && ehok) {
+        const int64_t hb = (int64_t(bi) * H + eh) * 2 * D;
+        Sin[i] = make_float2(h0[hb + ed + i], h0[hb + D + ed + i]);
+      }
+    }
+  } else {
+    // publish the segment map, then look back
+    if (ehok) {
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) st_agent(ob.seg_f + (sb0 + eh) * D + ed + i, segF[i]);
+      if (ed == 0) st_agent(ob.seg_g + sb0 + eh, segG);
+    }
+    wait_stores_acked();
+    __syncthreads();
+    if (threadIdx.x == 0)
+      __hip_atomic_store(flag, (epoch << 2) | 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (wv == 0) {
+      // lane i watches segment seg - 1 - i; wait until the nearest published
+      // leaving state i0 is known and every segment between has its map
+      const unsigned long long* f0 = ob.flag + (int64_t(bi) * NSEG) * H + hbase;
+      int found = -1;
+      const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
+      for (;;) {
+        int st = 0;
+        if (lane < seg) {
+          const unsigned long long fv = __hip_atomic_load(
+              const_cast<unsigned long long*>(f0 + int64_t(seg - 1 - lane) * H), __ATOMIC_RELAXED,
+              __HIP_MEMORY_SCOPE_AGENT);
+          st = (fv >> 2) == epoch ? int(fv & 3ull) : 0;
+        }
+        const uint64_t m2 = __builtin_amdgcn_ballot_w64(st == 2);
+        const uint64_t m1 = __builtin_amdgcn_ballot_w64(st >= 1);
+        if (m2) {
+          const int i0 = __builtin_ctzll(m2);
+          const uint64_t need = i0 == 63 ? ~0ull : ((1ull << (i0 + 1)) - 1ull);
+          if ((m1 & need) == need) {
+            found = i0;
+            break;
+          }
+        }
+        if (__builtin_amdgcn_s_memrealtime() - t_start > kSpinTicks) break;
+        __builtin_amdgcn_s_sleep(2);
+      }
+      if (lane == 0) ctrl[0] = found;
+    }
+    __syncthreads();
+    const int i0 = ctrl[0];
+    // compose: leaving state of segment seg - 1 - i0, then the maps of the
+    // segments after it, oldest first
+    const int jl = seg - 1 - max(i0, 0);
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) Sin[i] = make_float2(0.0f, 0.0f);
+    if (ehok) {
+      const int64_t base = int64_t(bi) * NSEG * H + eh;
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) Sin[i] = ld_agent(ob.seg_s + (base + int64_t(jl) * H) * D + ed + i);
+      for (int jb = jl + 1; jb < seg; jb += kLookbackBatch) {
+        float2 G[kLookbackBatch], F[kLookbackBatch][EPT];
+#pragma unroll
+        for (int u = 0; u < kLookbackBatch; ++u) {
+          const int js = min(jb + u, seg - 1);
+          G[u] = ld_agent(ob.seg_g + base + int64_t(js) * H);
+#pragma unroll
+          for (int i = 0; i < EPT; ++i) F[u][i] = ld_agent(ob.seg_f + (base + int64_t(js) * H) * D + ed + i);
+        }
+#pragma unroll
+        for (int u = 0; u < kLookbackBatch; ++u) {
+          if (jb + u < seg) {
+#pragma unroll
+            for (int i = 0; i < EPT; ++i)
+              Sin[i] = make_float2(G[u].x * Sin[i].x - G[u].y * Sin[i].y + F[u][i].x,
+                                   G[u].x * Sin[i].y + G[u].y * Sin[i].x + F[u][i].y);
+          }
+        }
+      }
+      if (i0 < 0) {
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) Sin[i] = make_float2(__builtin_nanf(""), __builtin_nanf(""));
+      }
+    }
+  }
+  // publish the state leaving the segment; the last segment's is h_final
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) Sx[e0 + i] = Sin[i];
+  if (ehok) {
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const float2 so = make_float2(segG.x * Sin[i].x - segG.y * Sin[i].y + segF[i].x,
+                                    segG.x * Sin[i].y + segG.y * Sin[i].x + segF[i].y);
+      if (seg + 1 < NSEG) {
+        st_agent(ob.seg_s + (sb0 + eh) * D + ed + i, so);
+      } else {
+        const int64_t hb = (int64_t(bi) * H + eh) * 2 * D;
+        h_final[hb + ed + i] = so.x;
+        h_final[hb + D + ed + i] = so.y;
+      }
+    }
+  }
+  if (seg + 1 < NSEG) wait_stores_acked();
+  __syncthreads();
+  if (seg + 1 < NSEG && threadIdx.x == 0)
+    __hip_atomic_store(flag, (epoch << 2) | 2ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // 3. state entering this wave's chunk, then the correction with the readout
+  if (live) {
+    float cr[DPL], ci[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const float2 sv = Sx[hh * D + sub * DPL + j];
+      cr[j] = sv.x;
+      ci[j] = sv.y;
+    }
+    for (int u = 0; u < wv; ++u) {
+      const float4 g = GF[u * HPW + hh];
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        const float2 f = Fx[u * SEGN + hh * D + sub * DPL + j];
+        const float nr = g.x * cr[j] - g.y * ci[j] + f.x;
+        ci[j] = g.x * ci[j] + g.y * cr[j] + f.y;
+        cr[j] = nr;
+      }
+    }
+    if (!hok) {
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) cr[j] = ci[j] = 0.0f;
+    }
+
+    for (int tb = 0; tb < ntr; tb += PF) {
+      float4 sa[PF], sb[PF];
+      float2 sl[PF];
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        sa[i] = s.A[(tb + i) * HPW + hh];
+        sb[i] = s.B[(tb + i) * HPW + hh];
+        sl[i] = s_y[(tb + i) * HPW + hh];
+      }
+      float yr[PF], yi[PF];
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        const int t = tb + i;
+        float kk[DPL], qq[DPL];
+        kb[i].unpack_then_reload(kk);
+        qb[i].unpack_then_reload(qq);
+        kb[i].load(kp + min(t + PF, tlast) * stride);
+        qb[i].load(qp + min(t + PF, tlast) * stride);
+        float pcr = 0.0f, pci = 0.0f, qcr = 0.0f, qci = 0.0f;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          pcr = fmaf(cr[j], kk[j], pcr);
+          pci = fmaf(ci[j], kk[j], pci);
+          qcr = fmaf(cr[j], qq[j], qcr);
+          qci = fmaf(ci[j], qq[j], qci);
+        }
+        pcr = group_sum<LPH>(pcr);
+        pci = group_sum<LPH>(pci);
+        qcr = group_sum<LPH>(qcr);
+        qci = group_sum<LPH>(qci);
+        const float bb = sa[i].z;
+        const float ecr = bb * pcr, eci = bb * pci;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          cr[j] = fmaf(-ecr, kk[j], cr[j]);
+          ci[j] = fmaf(-eci, kk[j], ci[j]);
+        }
+        // y_t = sel_C (f_t (zh_t.q_t) + g_{t-1} (c^_t.q_t))
+        const float4 fb = sb[i];
+        yr[i] = sa[i].w * (sl[i].x + fb.z * qcr - fb.w * qci);
+        yi[i] = sa[i].w * (sl[i].y + fb.z * qci + fb.w * qcr);
+      }
+      if (sub == 0) {
+#pragma unroll
+        for (int i = 0; i < PF; ++i) s_y[(tb + i) * HPW + hh] = make_float2(yr[i], yi[i]);
+      }
+    }
+  }
+  __syncthreads();
+
+  // coalesced write of y (B, L, H, 2) for the wave's tile
+  if (live) {
+    const int n = tc.nt * HPW;
+    for (int p = lane; p < n; p += kWave) {
+      const int t = p / HPW;
+      const int hj = hbase + (p - t * HPW);
+      if (hj < H) {
+        const int64_t e = ((tc.row0 + t) * H + hj) * 2;
+        const float2 yv = s_y[p];
+        T::store(y + e, yv.x);
+        T::store(y + e + 1, yv.y);
+      }
+    }
+  }
+}
+
 }  // namespace cdssm
 
 // ---------------------------------------------------------------------------
@@ -694,11 +1120,70 @@ namespace {
 
 using namespace cdssm;
 
+// Forward path selection: auto (one-pass where it applies), always four
+// launches, or one-pass required (calls it cannot serve fail).
+enum { kPathAuto = 0, kPathFour = 1, kPathOne = 2 };
+std::atomic<int> g_fwd_path{kPathAuto};
+
+// Look-back epochs: distinct per call and process, started from a clock-mixed
+// value so flag words left in a reused buffer never match by accident.
+unsigned long long next_epoch() {
+  static std::atomic<unsigned long long> ctr{
+      (unsigned long long)(std::chrono::steady_clock::now().time_since_epoch().count()) * 0x9E3779B97F4A7C15ull};
+  unsigned long long e;
+  do {
+    e = ctr.fetch_add(1, std::memory_order_relaxed) & ((1ull << 62) - 1);
+  } while (e == 0);
+  return e;
+}
+
+template <int D, int LPH>
+size_t onepass_lds(int Q) {
+  constexpr int HPW = kWave / LPH;
+  const size_t slots = size_t(round_up(Q, kWave)) * HPW;
+  return size_t(kOnePassW) * 3 * slots * sizeof(float4) + size_t(kOnePassW) * HPW * D * sizeof(float2) +
+         size_t(kOnePassW) * HPW * sizeof(float4) + size_t(HPW) * D * sizeof(float2) + 16;
+}
+
+// The one-pass grid must be resident at once (a workgroup may wait on any
+// earlier one): check the per-block LDS limit and occupancy x CUs, cached per
+// device and LDS size.
+template <typename T, int D, int LPH>
+bool onepass_fits(int grid, size_t lds, int nseg) {
+  if (nseg > kOnePassMaxSeg) return false;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  struct Entry {
+    int dev;
+    size_t lds;
+    int capacity;
+  };
+  static std::mutex mu;
+  static Entry cache[16];
+  static int n_cache = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < n_cache; ++i)
+    if (cache[i].dev == dev && cache[i].lds == lds) return grid <= cache[i].capacity;
+  int max_lds = 0, n_cu = 0, per_cu = 0;
+  int capacity = 0;
+  const void* fn = reinterpret_cast<const void*>(&fused_fwd_onepass_kernel<T, D, LPH>);
+  if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+      hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      lds <= size_t(max_lds)) {
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kWave * kOnePassW, lds) == hipSuccess)
+      capacity = per_cu * n_cu;
+  }
+  (void)hipGetLastError();
+  if (n_cache < 16) cache[n_cache++] = Entry{dev, lds, capacity};
+  return grid <= capacity;
+}
+
 template <typename T, int D, int LPH, int LPHS>
 int launch_fused_fwd(const void* q, const void* k, const void* v, const void* beta, const void* sel_c,
                      const void* dt, const void* r, const float* alpha, const float* omega, float c,
                      const float* h0, void* y, float* h_final, float* ws, int B, int L, int H, int Q,
-                     hipStream_t stream, hipEvent_t* ev, bool save) {
+                     hipStream_t stream, hipEvent_t* ev, bool save, int* path) {
   using raw = typename T::raw;
   constexpr int HPW = kWave / LPH, HPWS = kWave / LPHS;
   const FwdLayout w = fwd_layout(B, L, H, D, Q);
@@ -718,6 +1203,34 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   float2* gsaved = reinterpret_cast<float2*>(ws) + w.gsaved_offset();
   const int slots = round_up(Q, kWave) * HPW, slots_s = round_up(Q, kWave) * HPWS;
 
+  if (!save && g_fwd_path.load(std::memory_order_relaxed) != kPathFour) {
+    const int grid = w.NSEG * B * n_hg;
+    const size_t lds = onepass_lds<D, LPH>(Q);
+    if (onepass_fits<T, D, LPH>(grid, lds, w.NSEG)) {
+      const int64_t op = w.onepass_offset();
+      float2* base = reinterpret_cast<float2*>(ws) + op;
+      const int64_t nsd = int64_t(B) * w.NSEG * H * D, nsh = int64_t(B) * w.NSEG * H;
+      const OnePassBufs ob{base, base + nsd, base + 2 * nsd, reinterpret_cast<unsigned long long*>(base + 2 * nsd + nsh)};
+      const unsigned long long epoch = next_epoch();
+      if (path) *path = kPathOne;
+      if (ev)
+        for (int i = 0; i < 4; ++i) (void)hipEventRecord(ev[i], stream);
+      hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH>), dim3(unsigned(grid)), dim3(kWave * kOnePassW), lds,
+                         stream, (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,
+                         (const raw*)dt, (const raw*)r, alpha, omega, c, h0, (raw*)y, h_final, ob, epoch, L, H, Q,
+                         NC, w.NSEG, n_hg);
+      const int st = cdssm_host::check_launch("cdssm_fused_scan_fwd/onepass");
+      if (ev) (void)hipEventRecord(ev[4], stream);
+      return st;
+    }
+    if (g_fwd_path.load(std::memory_order_relaxed) == kPathOne) {
+      cdssm_host::set_error("cdssm_fused_scan_fwd: one-pass path required but not possible for this shape "
+                            "(%d workgroups, %d segments per sequence, %zu bytes of LDS)", grid, w.NSEG, lds);
+      return CDSSM_EINVAL;
+    }
+  }
+
+  if (path) *path = kPathFour;
   if (ev) (void)hipEventRecord(ev[0], stream);
   hipLaunchKernelGGL((fused_fwd_summary_kernel<T, D, LPHS>), dim3(unsigned(tiles_s)), dim3(kWave),
                      size_t(slots_s) * (sizeof(float4) + sizeof(float2)) + HPWS * sizeof(float4), stream,
@@ -771,7 +1284,7 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
                     const void* sel_c, const void* dt, const void* r, const float* alpha,
                     const float* omega, float c, const float* h0, void* y, float* h_final,
                     float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
-                    int64_t chunk, hipStream_t stream, hipEvent_t* ev, bool save) {
+                    int64_t chunk, hipStream_t stream, hipEvent_t* ev, bool save, int* path = nullptr) {
   const char* op = "cdssm_fused_scan_fwd";
   if (dtype != 0 && dtype != 1) {
     cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
@@ -811,15 +1324,15 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
   if (dtype == 1) {
     if (D == 64)
       return launch_fused_fwd<BF16, 64, CDSSM_FWD_LPH_BF16_D64, CDSSM_FWD_LPHS_BF16_D64>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                           workspace, b, l, hh, qc, stream, ev, save);
+                                           workspace, b, l, hh, qc, stream, ev, save, path);
     return launch_fused_fwd<BF16, 128, 16, CDSSM_FWD_LPHS_BF16_D128>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                           workspace, b, l, hh, qc, stream, ev, save);
+                                           workspace, b, l, hh, qc, stream, ev, save, path);
   }
   if (D == 64)
     return launch_fused_fwd<F32, 64, 16, 16>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                         workspace, b, l, hh, qc, stream, ev, save);
+                                         workspace, b, l, hh, qc, stream, ev, save, path);
   return launch_fused_fwd<F32, 128, 32, 32>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                        workspace, b, l, hh, qc, stream, ev, save);
+                                        workspace, b, l, hh, qc, stream, ev, save, path);
 }
 }  // namespace
 
@@ -864,15 +1377,17 @@ extern "C" int cdssm_fused_scan_fwd_profile(int dtype, const void* q, const void
   for (int p = 0; p < 4; ++p) phase_ms[p] = 0.0f;
   int st = CDSSM_OK;
   for (int it = 0; it < iters && st == CDSSM_OK; ++it) {
+    int path = kPathFour;
     st = fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace, B,
-                         L, H, D, N, chunk, stream, ev, train != 0);
+                         L, H, D, N, chunk, stream, ev, train != 0, &path);
     if (st != CDSSM_OK) break;
     if (hipEventSynchronize(ev[4]) != hipSuccess) {
       cdssm_host::set_error("cdssm_fused_scan_fwd_profile: hipEventSynchronize failed");
       st = CDSSM_EHIP;
       break;
     }
-    for (int p = 0; p < 4; ++p) {
+    // a one-pass call is one launch: reported as the main pass, 0 for the others
+    for (int p = path == kPathOne ? 3 : 0; p < 4; ++p) {
       float ms = 0.0f;
       (void)hipEventElapsedTime(&ms, ev[p], ev[p + 1]);
       phase_ms[p] += ms / float(iters);
@@ -880,4 +1395,13 @@ extern "C" int cdssm_fused_scan_fwd_profile(int dtype, const void* q, const void
   }
   for (int i = 0; i < 5; ++i) (void)hipEventDestroy(ev[i]);
   return st;
+}
+
+extern "C" int cdssm_fused_scan_fwd_set_path(int mode) {
+  if (mode < kPathAuto || mode > kPathOne) {
+    cdssm_host::set_error("cdssm_fused_scan_fwd_set_path: mode must be 0 (auto), 1 (four launches) or 2 "
+                          "(one pass required), got %d", mode);
+    return CDSSM_EINVAL;
+  }
+  return g_fwd_path.exchange(mode);
 }

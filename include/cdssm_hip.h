@@ -42,9 +42,13 @@ const char* cdssm_last_error(void);
  * `dtype`; alpha, omega (H,) fp32; h0 (B,H,N,D) fp32 or NULL (zero state);
  * outputs y (B,L,H,N) of `dtype`, h_final (B,H,N,D) fp32 (the R-mode carry
  * after the last token; an extension -- the reference has no state output).
- * workspace: cdssm_fused_scan_workspace_bytes() bytes; on return it holds the
- * state entering every chunk, (B, L/chunk, H, D) complex fp32, which the
- * backward consumes.  Supported: N = 2, D in {64, 128}, 1 <= chunk <= 128.
+ * workspace: cdssm_fused_scan_workspace_bytes() bytes of device memory, any
+ * contents (scratch for this call; the backward takes the workspace of
+ * cdssm_fused_scan_fwd_train instead).  Supported: N = 2, D in {64, 128},
+ * 1 <= chunk <= 128.  Where the whole grid fits on the device at once and a
+ * sequence has at most 64 segments of 4 chunks, the scan runs as one launch
+ * (chunk maps composed by a look-back between workgroups); otherwise as four
+ * (chunk summaries, carry fold, carry replay, main pass).
  */
 int64_t cdssm_fused_scan_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
                                          int64_t chunk);
@@ -116,6 +120,16 @@ int cdssm_fused_scan_bwd_profile(int dtype, const void* q, const void* k, const 
                                  void* dsel_c, void* ddt, void* dr, float* dalpha, float* domega,
                                  float* dh0, float* workspace, int64_t B, int64_t L, int64_t H, int64_t D,
                                  int64_t N, int64_t chunk, hipStream_t stream, int iters, float* phase_ms);
+
+/*
+ * Forward path selection (no counterpart in the reference; for tests and
+ * benchmarks): 0 = automatic (default), 1 = always the four-launch scan,
+ * 2 = the one-pass scan required (calls it cannot serve return -1).
+ * Process-wide; returns the previous mode, or -1 for an invalid mode.  The
+ * training forward always runs the four-launch scan.  A one-pass call reports
+ * its single launch as the main pass in cdssm_fused_scan_fwd_profile.
+ */
+int cdssm_fused_scan_fwd_set_path(int mode);
 
 /*
  * The reference's three scan passes as separate ops, same tensor contracts

@@ -76,7 +76,9 @@ def test_workspace_size_formula():
         pad = carry & 1               # the training records start 16-byte aligned
         saved = 4 * B * L * H         # (p, pc), (c.q, Y.q) per token-head: 2 float4
         gsaved = B * L * H            # g_t per token-head: float2
-        return (carry + pad + saved + gsaved) * 8
+        NSEG = -(-NC // 4)            # one-pass look-back segments of 4 chunks
+        onepass = B * NSEG * H * (2 * D + 2)   # maps, leaving states, rotations, flags
+        return (carry + pad + saved + gsaved + onepass) * 8
     assert lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, N, Q) == expect(L)
     assert lib.cdssm_fused_scan_workspace_bytes(B, 100, H, D, N, Q) == expect(100)
     assert lib.cdssm_fused_scan_workspace_bytes(0, L, H, D, N, Q) == -1

@@ -6,12 +6,25 @@ Tolerances (from the task's stated bar, measured normwise max|x-ref|/max|ref|):
 The oracle is fed the same (bf16-rounded) inputs and computes in fp64.
 """
 
+import contextlib
+
 import pytest
 import torch
 
 from _gpu_util import DEV, ScanConfig, draw_inputs, log, oracle_fwd, rel, select, state_norm_rel, to_dev
 
 pytestmark = pytest.mark.gpu
+
+
+@contextlib.contextmanager
+def forward_path(path):
+    """Run the block with the forward launched as `path` ("four_launch", "one_pass", "auto")."""
+    from cdssm_hip import set_forward_path
+    prev = set_forward_path(path)
+    try:
+        yield
+    finally:
+        set_forward_path(prev)
 
 
 def run_fused(x, chunk_size=None):
@@ -36,11 +49,13 @@ SMALL = [
 ]
 
 
+@pytest.mark.parametrize("path", ["four_launch", "one_pass"])
 @pytest.mark.parametrize("name,cfg,chunk", SMALL, ids=[s[0] for s in SMALL])
-def test_fused_fwd_matches_oracle(name, cfg, chunk):
-    log(f"[fused fwd] {name}: B{cfg.B} H{cfg.H} L{cfg.L} D{cfg.D} {cfg.dtype} chunk={chunk or cfg.D}")
+def test_fused_fwd_matches_oracle(name, cfg, chunk, path):
+    log(f"[fused fwd] {name} ({path}): B{cfg.B} H{cfg.H} L{cfg.L} D{cfg.D} {cfg.dtype} chunk={chunk or cfg.D}")
     x = draw_inputs(cfg, seed=0)
-    y, hf = run_fused(x, chunk)
+    with forward_path(path):
+        y, hf = run_fused(x, chunk)
     yr, hr = oracle_fwd(x, chunk_size=chunk)
     ey, eh, en = rel(y, yr), rel(hf, hr), state_norm_rel(hf, hr)
     log(f"   rel err y {ey:.2e}  h_final {eh:.2e}  state-norm {en:.2e}")
@@ -125,3 +140,79 @@ def test_fused_fwd_rejects_bad_arguments():
         chunkwise_delta_scan(a[0].float(), *a[1:], g["alpha"], g["omega"], g["c"])
     with pytest.raises(ValueError):
         chunkwise_delta_scan(a[0][..., :32].contiguous(), *a[1:], g["alpha"], g["omega"], g["c"])
+
+
+def test_one_pass_matches_four_launch_full_c1():
+    """At the C1 shape the one-pass kernel (look-back carry) and the four-launch
+    scan (segmented fold / replay carry) agree on every output; they differ only
+    in the order the chunk maps are composed (fp32 rounding)."""
+    cfg = ScanConfig("C1", B=8, H=16, L=4096, D=64, h0_std=0.1)
+    log("[fused fwd] C1 one-pass vs four-launch, bf16 with h0")
+    x = draw_inputs(cfg, seed=4)
+    with forward_path("one_pass"):
+        y1, h1 = run_fused(x)
+    with forward_path("four_launch"):
+        y4, h4 = run_fused(x)
+    ey, eh = rel(y1, y4), rel(h1, h4)
+    log(f"   rel diff y {ey:.2e}  h_final {eh:.2e}")
+    assert ey <= 1e-2 and eh <= 1e-5
+
+
+def test_one_pass_longest_look_back_matches_oracle():
+    """64 segments of 4 chunks per sequence, the most the one-pass kernel takes:
+    the last workgroup composes up to 63 published segment maps."""
+    cfg = ScanConfig("t", B=1, H=8, L=64 * 4 * 64, D=64, omega_std=3.0, h0_std=0.1)
+    log("[fused fwd] one-pass, 64 segments: B1 H8 L16384 D64 bf16")
+    x = draw_inputs(cfg, seed=5)
+    with forward_path("one_pass"):
+        y, hf = run_fused(x)
+    heads = [0, 7]
+    yr, hr = oracle_fwd(select(x, [0], heads))
+    ys = y.index_select(2, torch.as_tensor(heads))
+    hs = hf.index_select(1, torch.as_tensor(heads))
+    ey, en = rel(ys, yr), state_norm_rel(hs, hr)
+    log(f"   rel err y {ey:.2e}  state-norm {en:.2e}")
+    assert ey <= 2e-2 and en <= 1e-3
+
+
+def test_one_pass_refuses_more_than_64_segments():
+    from cdssm_hip import chunkwise_delta_scan
+    cfg = ScanConfig("t", B=1, H=8, L=64 * 4 * 64 + 1, D=64)
+    g = to_dev(draw_inputs(cfg, seed=0))
+    a = [g[n] for n in ("q", "k", "v", "beta", "sel_C", "dt", "r")]
+    with forward_path("one_pass"):
+        with pytest.raises(Exception, match="one-pass"):
+            chunkwise_delta_scan(*a, g["alpha"], g["omega"], g["c"])
+    with forward_path("auto"):
+        y, _ = chunkwise_delta_scan(*a, g["alpha"], g["omega"], g["c"])
+        torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all()
+
+
+def test_one_pass_reused_workspace_sees_only_its_own_call():
+    """Back-to-back one-pass calls on one workspace: flags left by the previous
+    call (other epoch) must not be taken for this call's, so changing the inputs
+    in place between calls gives the fresh result every time."""
+    from cdssm_hip.scan import PreparedForward
+    cfg = ScanConfig("t", B=2, H=16, L=4096, D=64, h0_std=0.1)
+    log("[fused fwd] one-pass, reused workspace over three calls")
+    xa, xb = to_dev(draw_inputs(cfg, seed=6)), to_dev(draw_inputs(cfg, seed=7))
+    xb["alpha"], xb["omega"] = xa["alpha"], xa["omega"]  # per-head parameters stay bound
+    names = ("q", "k", "v", "beta", "sel_C", "dt", "r")
+    bufs = {n: xa[n].clone() for n in names}
+    h0 = xa["h0"].clone()
+    with forward_path("one_pass"):
+        run = PreparedForward(*[bufs[n] for n in names], xa["alpha"], xa["omega"], xa["c"], h0=h0)
+        outs = []
+        for src in (xa, xb, xa):
+            for n in names:
+                bufs[n].copy_(src[n])
+            h0.copy_(src["h0"])
+            y, hf = run()
+            torch.cuda.synchronize()
+            outs.append((y.clone().cpu(), hf.clone().cpu()))
+    with forward_path("four_launch"):
+        ref_a, ref_b = run_fused(xa), run_fused(xb)
+    for (y, hf), (yr, hr) in zip(outs, (ref_a, ref_b, ref_a)):
+        assert rel(y, yr) <= 1e-2 and rel(hf, hr) <= 1e-5
+    assert rel(outs[0][0], outs[2][0]) == 0.0 and rel(outs[0][1], outs[2][1]) == 0.0
