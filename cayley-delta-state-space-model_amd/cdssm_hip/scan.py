@@ -106,7 +106,7 @@ def set_forward_path(path: str) -> str:
     resident at once and a sequence has at most 64 segments of 4 chunks, else
     the four-launch scan; "four_launch" always takes the four-launch scan;
     "one_pass" requires the one-pass kernel (calls it cannot serve raise).
-    Process-wide; the training forward always takes the four-launch scan.
+    Process-wide; applies to the inference and the training forward alike.
     """
     if path not in FORWARD_PATHS:
         raise ValueError(f"path must be one of {sorted(FORWARD_PATHS)}, got {path!r}")

@@ -708,6 +708,9 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
 //      segment is then published for the later segments;
 //   3. each wave derives the state entering its chunk and runs the decay-free
 //      correction with the full readout; y is written coalesced.
+// SAVE (training forward) also writes what the backward reads: the state
+// entering every chunk and G_k (the four-launch layout), the per-token records
+// (p_t, pc_t), (c^_{t+1}.q_t, Y_t.q_t) and g_t, as the main pass does.
 // Look-back flags hold epoch << 2 | state (1: map, 2: leaving state) with a
 // per-call epoch, so the workspace needs no clearing between calls.  Published
 // data and flags are written and read with agent-scope atomics (stores written
@@ -746,15 +749,16 @@ __device__ __forceinline__ float2 ld_agent(const float2* p) {
   return __builtin_bit_cast(float2, x);
 }
 
-template <typename T, int D, int LPH>
+template <typename T, int D, int LPH, bool SAVE>
 __global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(
     const typename T::raw* __restrict__ q, const typename T::raw* __restrict__ k,
     const typename T::raw* __restrict__ v, const typename T::raw* __restrict__ beta,
     const typename T::raw* __restrict__ sel_c, const typename T::raw* __restrict__ dt,
     const typename T::raw* __restrict__ r, const float* __restrict__ alpha,
     const float* __restrict__ omega, float c, const float* __restrict__ h0, typename T::raw* __restrict__ y,
-    float* __restrict__ h_final, OnePassBufs ob, unsigned long long epoch, int L, int H, int Q, int NC,
-    int NSEG, int n_hg) {
+    float* __restrict__ h_final, OnePassBufs ob, float2* __restrict__ states, float2* __restrict__ gam,
+    float4* __restrict__ saved, float2* __restrict__ gsaved, unsigned long long epoch, int L, int H, int Q,
+    int NC, int NSEG, int n_hg) {
   using Cfg = FusedCfg<T, D, LPH>;
   constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch, W = kOnePassW;
   constexpr int SEGN = HPW * D;  // complex elements of a head group's state
@@ -817,7 +821,7 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(
       qb[i].load(qp + min(i, tlast) * stride);
     }
     rm = stage_scalars<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, alpha, omega, c, s, nullptr, 0,
-                                     nullptr, GF + wv * HPW);
+                                     SAVE ? gsaved : nullptr, GF + wv * HPW);
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       kb[i].pin();
@@ -826,9 +830,14 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(
   }
   __syncthreads();
 
+  const int64_t tile_h = (int64_t(bi) * NC + tc.chunk) * H + (hok ? h : H - 1);  // (b, chunk, h)
+  float4* svp = SAVE ? saved + 2 * ((tc.row0 * H) + (hok ? h : H - 1)) : nullptr;
+
   // 1. local recurrence with the local readout f_t (zh_t . q_t); in the last
   // PF steps the prefetch wraps to the first tokens, for the correction pass
   if (live) {
+    if (SAVE && sub == 0 && hok) gam[tile_h] = make_float2(GF[wv * HPW + hh].x, GF[wv * HPW + hh].y);
+    float fpr = 1.0f, fpi = 0.0f;  // frame f_{t-1} (SAVE)
     for (int tb = 0; tb < ntr; tb += PF) {
       float4 sa[PF], sb[PF];
       float2 sm[PF];
@@ -869,6 +878,14 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(
         const float4 fb = sb[i];
         yr[i] = group_sum<LPH>(fb.x * qzr - fb.y * qzi);
         yi[i] = group_sum<LPH>(fb.x * qzi + fb.y * qzr);
+        if (SAVE) {
+          // p_t = f_{t-1} (zh_{t-1}.k_t), the first half of the token's first record
+          if (sub == 0 && hok && t < tc.nt)
+            reinterpret_cast<float2*>(svp + 2 * int64_t(t) * H)[0] =
+                make_float2(fpr * pr - fpi * pi, fpr * pi + fpi * pr);
+          fpr = fb.x;
+          fpi = fb.y;
+        }
       }
       if (sub == 0) {
 #pragma unroll
@@ -1043,6 +1060,9 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(
     if (!hok) {
 #pragma unroll
       for (int j = 0; j < DPL; ++j) cr[j] = ci[j] = 0.0f;
+    } else if (SAVE) {
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) states[tile_h * D + sub * DPL + j] = make_float2(cr[j], ci[j]);
     }
 
     for (int tb = 0; tb < ntr; tb += PF) {
@@ -1077,15 +1097,30 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(
         qci = group_sum<LPH>(qci);
         const float bb = sa[i].z;
         const float ecr = bb * pcr, eci = bb * pci;
+        float cnr = 0.0f, cni = 0.0f;
 #pragma unroll
         for (int j = 0; j < DPL; ++j) {
           cr[j] = fmaf(-ecr, kk[j], cr[j]);
           ci[j] = fmaf(-eci, kk[j], ci[j]);
+          if (SAVE) {
+            cnr = fmaf(cr[j], qq[j], cnr);  // c^_{t+1}.q
+            cni = fmaf(ci[j], qq[j], cni);
+          }
         }
         // y_t = sel_C (f_t (zh_t.q_t) + g_{t-1} (c^_t.q_t))
         const float4 fb = sb[i];
-        yr[i] = sa[i].w * (sl[i].x + fb.z * qcr - fb.w * qci);
-        yi[i] = sa[i].w * (sl[i].y + fb.z * qci + fb.w * qcr);
+        const float Rr = sl[i].x + fb.z * qcr - fb.w * qci;
+        const float Ri = sl[i].y + fb.z * qci + fb.w * qcr;
+        yr[i] = sa[i].w * Rr;
+        yi[i] = sa[i].w * Ri;
+        if (SAVE) {
+          const float cqr = group_sum<LPH>(cnr), cqi = group_sum<LPH>(cni);
+          if (sub == 0 && hok && t < tc.nt) {
+            float4* rec = svp + 2 * int64_t(t) * H;
+            reinterpret_cast<float2*>(rec)[1] = make_float2(pcr, pci);
+            rec[1] = make_float4(cqr, cqi, Rr, Ri);
+          }
+        }
       }
       if (sub == 0) {
 #pragma unroll
@@ -1148,7 +1183,7 @@ size_t onepass_lds(int Q) {
 // The one-pass grid must be resident at once (a workgroup may wait on any
 // earlier one): check the per-block LDS limit and occupancy x CUs, cached per
 // device and LDS size.
-template <typename T, int D, int LPH>
+template <typename T, int D, int LPH, bool SAVE>
 bool onepass_fits(int grid, size_t lds, int nseg) {
   if (nseg > kOnePassMaxSeg) return false;
   int dev = 0;
@@ -1166,7 +1201,7 @@ bool onepass_fits(int grid, size_t lds, int nseg) {
     if (cache[i].dev == dev && cache[i].lds == lds) return grid <= cache[i].capacity;
   int max_lds = 0, n_cu = 0, per_cu = 0;
   int capacity = 0;
-  const void* fn = reinterpret_cast<const void*>(&fused_fwd_onepass_kernel<T, D, LPH>);
+  const void* fn = reinterpret_cast<const void*>(&fused_fwd_onepass_kernel<T, D, LPH, SAVE>);
   if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
       hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
       lds <= size_t(max_lds)) {
@@ -1203,10 +1238,10 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   float2* gsaved = reinterpret_cast<float2*>(ws) + w.gsaved_offset();
   const int slots = round_up(Q, kWave) * HPW, slots_s = round_up(Q, kWave) * HPWS;
 
-  if (!save && g_fwd_path.load(std::memory_order_relaxed) != kPathFour) {
+  if (g_fwd_path.load(std::memory_order_relaxed) != kPathFour) {
     const int grid = w.NSEG * B * n_hg;
     const size_t lds = onepass_lds<D, LPH>(Q);
-    if (onepass_fits<T, D, LPH>(grid, lds, w.NSEG)) {
+    if (save ? onepass_fits<T, D, LPH, true>(grid, lds, w.NSEG) : onepass_fits<T, D, LPH, false>(grid, lds, w.NSEG)) {
       const int64_t op = w.onepass_offset();
       float2* base = reinterpret_cast<float2*>(ws) + op;
       const int64_t nsd = int64_t(B) * w.NSEG * H * D, nsh = int64_t(B) * w.NSEG * H;
@@ -1215,10 +1250,21 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
       if (path) *path = kPathOne;
       if (ev)
         for (int i = 0; i < 4; ++i) (void)hipEventRecord(ev[i], stream);
-      hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH>), dim3(unsigned(grid)), dim3(kWave * kOnePassW), lds,
-                         stream, (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,
-                         (const raw*)dt, (const raw*)r, alpha, omega, c, h0, (raw*)y, h_final, ob, epoch, L, H, Q,
-                         NC, w.NSEG, n_hg);
+      float2* summ = reinterpret_cast<float2*>(ws);
+      float2* gam = summ + w.n_summ;
+      float4* saved = reinterpret_cast<float4*>(reinterpret_cast<float2*>(ws) + w.saved_offset());
+      float2* gsaved = reinterpret_cast<float2*>(ws) + w.gsaved_offset();
+      if (save)
+        hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, true>), dim3(unsigned(grid)),
+                           dim3(kWave * kOnePassW), lds, stream, (const raw*)q, (const raw*)k, (const raw*)v,
+                           (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c, h0,
+                           (raw*)y, h_final, ob, summ, gam, saved, gsaved, epoch, L, H, Q, NC, w.NSEG, n_hg);
+      else
+        hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, false>), dim3(unsigned(grid)),
+                           dim3(kWave * kOnePassW), lds, stream, (const raw*)q, (const raw*)k, (const raw*)v,
+                           (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c, h0,
+                           (raw*)y, h_final, ob, nullptr, nullptr, nullptr, nullptr, epoch, L, H, Q, NC, w.NSEG,
+                           n_hg);
       const int st = cdssm_host::check_launch("cdssm_fused_scan_fwd/onepass");
       if (ev) (void)hipEventRecord(ev[4], stream);
       return st;

@@ -125,8 +125,8 @@ int cdssm_fused_scan_bwd_profile(int dtype, const void* q, const void* k, const 
  * Forward path selection (no counterpart in the reference; for tests and
  * benchmarks): 0 = automatic (default), 1 = always the four-launch scan,
  * 2 = the one-pass scan required (calls it cannot serve return -1).
- * Process-wide; returns the previous mode, or -1 for an invalid mode.  The
- * training forward always runs the four-launch scan.  A one-pass call reports
+ * Process-wide (inference and training forward alike); returns the previous
+ * mode, or -1 for an invalid mode.  A one-pass call reports
  * its single launch as the main pass in cdssm_fused_scan_fwd_profile.
  */
 int cdssm_fused_scan_fwd_set_path(int mode);

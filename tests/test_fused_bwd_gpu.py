@@ -7,6 +7,7 @@ Tolerances per gradient tensor, normwise max|g-ref|/max|ref|:
 fp32 inputs <= 1e-4, bf16 inputs <= 2e-2.
 """
 
+import contextlib
 import math
 
 import pytest
@@ -70,13 +71,27 @@ CASES = [
 ]
 
 
+@contextlib.contextmanager
+def forward_path(path):
+    from cdssm_hip import set_forward_path
+    prev = set_forward_path(path)
+    try:
+        yield
+    finally:
+        set_forward_path(prev)
+
+
+@pytest.mark.parametrize("path", ["four_launch", "one_pass"])
 @pytest.mark.parametrize("name,cfg,chunk", CASES, ids=[c[0] for c in CASES])
-def test_fused_bwd_matches_oracle(name, cfg, chunk):
-    log(f"[fused bwd] {name}: B{cfg.B} H{cfg.H} L{cfg.L} D{cfg.D} {cfg.dtype} chunk={chunk or cfg.D}")
+def test_fused_bwd_matches_oracle(name, cfg, chunk, path):
+    """Backward from the training forward's workspace, as written by either forward path."""
+    log(f"[fused bwd] {name} (forward {path}): B{cfg.B} H{cfg.H} L{cfg.L} D{cfg.D} {cfg.dtype} "
+        f"chunk={chunk or cfg.D}")
     x = draw_inputs(cfg, seed=0)
     gy, gh = cotangents(cfg)
     ref = oracle_grads(x, gy, gh, chunk)
-    got = hip_grads(x, gy, gh, chunk)
+    with forward_path(path):
+        got = hip_grads(x, gy, gh, chunk)
     tol = 1e-4 if cfg.dtype == "fp32" else 2e-2
     errs = {n: rel(got[n], ref[n]) for n in ref}
     log("   " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
@@ -109,3 +124,36 @@ def test_fused_bwd_full_c2_sequences_match_oracle():
         errs[n] = rel(gsel, ref[n])
     log("   " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
     assert all(e <= 2e-2 for e in errs.values()), errs
+
+
+def test_one_pass_training_forward_writes_the_four_launch_records():
+    """The training forward's workspace (entering state of every chunk, chunk
+    rotations, per-token records, g_t) is the backward's input: the one-pass
+    kernel must leave the same values there as the four-launch scan (fp32,
+    several look-back segments, ragged last chunk, h0)."""
+    from cdssm_hip.scan import chunkwise_delta_scan_fwd
+    cfg = ScanConfig("t", B=2, H=5, L=64 * 4 * 5 + 37, D=64, dtype="fp32", h0_std=0.1)
+    log("[fused fwd train] one-pass vs four-launch workspace: B2 H5 L1317 D64 fp32")
+    g = to_dev(draw_inputs(cfg, seed=8))
+    a = [g[n] for n in ("q", "k", "v", "beta", "sel_C", "dt", "r")]
+    outs = {}
+    for path in ("one_pass", "four_launch"):
+        with forward_path(path):
+            y, hf, ws = chunkwise_delta_scan_fwd(*a, g["alpha"], g["omega"], g["c"], h0=g["h0"], train=True)
+            torch.cuda.synchronize()
+        outs[path] = (y.cpu(), hf.cpu(), ws.view(-1, 2).cpu())
+    B, L, H, D, Q = cfg.B, cfg.L, cfg.H, cfg.D, cfg.D
+    NC = -(-L // Q)
+    S = -(-NC // 16)
+    n_states, n_gam = B * NC * H * D, B * NC * H
+    carry = n_states + n_gam + B * H * S * (D + 1)
+    off_saved = carry + (carry & 1)
+    regions = {"states": (0, n_states), "gam": (n_states, n_states + n_gam),
+               "saved": (off_saved, off_saved + 4 * B * L * H),
+               "gsaved": (off_saved + 4 * B * L * H, off_saved + 5 * B * L * H)}
+    (y1, h1, w1), (y4, h4, w4) = outs["one_pass"], outs["four_launch"]
+    assert rel(y1, y4) <= 1e-5 and rel(h1, h4) <= 1e-5
+    for name, (lo, hi) in regions.items():
+        e = rel(w1[lo:hi], w4[lo:hi])
+        log(f"   {name}: rel diff {e:.1e}")
+        assert e <= 1e-5, name
