@@ -118,11 +118,16 @@ __device__ __forceinline__ uint64_t spread8(uint64_t x) {
 // tile), computes its tokens' dynamics, runs the three prefix scans (log2|g|^2
 // for the reset bands, the segmented frame product f, the plain product g)
 // sequentially over its own tokens, and joins them across the head's NB
-// lanes with log2(NB) shuffle steps.  Slots past the last token and heads
+// lanes with log2(NB) shuffle steps.  `pre` (the caller's row prefetch) is
+// issued right after the first slab's loads.  Slots past the last token and heads
 // >= H hold inert steps (a = 1, w = 0, beta = 0).  Summary pass (MAIN false):
 // writes G_k = g over the chunk to gam and the last frame f to B[j]; with
 // cend (MAIN true) the same pair goes to cend[j].
-template <typename T, int HPW, bool MAIN>
+struct NoPrefetch {
+  __device__ void operator()() const {}
+};
+
+template <typename T, int HPW, bool MAIN, typename Pre = NoPrefetch>
 __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, int ntr,
                                                    const typename T::raw* __restrict__ v,
                                                    const typename T::raw* __restrict__ beta,
@@ -133,7 +138,7 @@ __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, i
                                                    const float* __restrict__ omega, float c,
                                                    const TileScalars& s, float2* __restrict__ gam,
                                                    int64_t gam_base, float2* __restrict__ gsv = nullptr,
-                                                   float4* __restrict__ cend = nullptr) {
+                                                   float4* __restrict__ cend = nullptr, Pre pre = Pre{}) {
   constexpr int NB = kWave / HPW;
   constexpr int TPB = HPW;
   static_assert(NB * TPB == kWave, "blocks tile the slab");
@@ -162,6 +167,9 @@ __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, i
       v1[i] = T::load(v + 2 * e + 1);
       sc[i] = MAIN ? T::load(sel_c + e) : 0.0f;
     }
+    // the caller's row prefetch goes after these small loads, so waiting for
+    // them does not wait for the rows
+    if (tl == 0) pre();
     // dynamics and local (in-block) prefixes; computed for every slot (the
     // clamped loads hold valid numbers) and replaced by an inert step where
     // the slot is not a real token, so the tokens interleave without branches
@@ -373,12 +381,13 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
   const typename T::raw* kp = k + (tc.row0 * H + (hok ? h : H - 1)) * D + sub * DPL;
   const int tlast = tc.nt - 1;
   RowVec<T, DPL> kb[PF];
-#pragma unroll
-  for (int i = 0; i < PF; ++i) kb[i].load(kp + min(i, tlast) * stride);
-
   TileScalars s{smem4, smem4 + slots, reinterpret_cast<float2*>(smem4 + slots + HPW)};
   const ResetMask rm = stage_scalars<T, HPW, false>(tc, H, ntr, v, beta, nullptr, dt, r, alpha, omega, c, s,
-                                                    gam, ch0);
+                                                    gam, ch0, nullptr, nullptr, [&] {
+#pragma unroll
+                                                      for (int i = 0; i < PF; ++i)
+                                                        kb[i].load(kp + min(i, tlast) * stride);
+                                                    });
 #pragma unroll
   for (int i = 0; i < PF; ++i) kb[i].pin();
   __syncthreads();
@@ -572,11 +581,6 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
   const typename T::raw* qp = q + off;
   const int tlast = tc.nt - 1;
   RowVec<T, DPL> kb[PF], qb[PF];
-#pragma unroll
-  for (int i = 0; i < PF; ++i) {
-    kb[i].load(kp + min(i, tlast) * stride);
-    qb[i].load(qp + min(i, tlast) * stride);
-  }
   float zr[DPL], zi[DPL], cr[DPL], ci[DPL];
   {
     const int hl = hok ? h : H - 1;
@@ -593,7 +597,13 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
   TileScalars s{smem4, smem4 + slots, reinterpret_cast<float2*>(smem4 + 2 * slots)};
   float2* s_y = s.M + slots;
   const ResetMask rm = stage_scalars<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, alpha, omega, c, s,
-                                                   nullptr, 0, SAVE ? gsaved : nullptr);
+                                                   nullptr, 0, SAVE ? gsaved : nullptr, nullptr, [&] {
+#pragma unroll
+                                                     for (int i = 0; i < PF; ++i) {
+                                                       kb[i].load(kp + min(i, tlast) * stride);
+                                                       qb[i].load(qp + min(i, tlast) * stride);
+                                                     }
+                                                   });
 #pragma unroll
   for (int i = 0; i < PF; ++i) {
     kb[i].pin();
@@ -815,13 +825,14 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(
   ResetMask rm{0ull, 0ull};
 
   if (live) {
-#pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      kb[i].load(kp + min(i, tlast) * stride);
-      qb[i].load(qp + min(i, tlast) * stride);
-    }
     rm = stage_scalars<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, alpha, omega, c, s, nullptr, 0,
-                                     SAVE ? gsaved : nullptr, GF + wv * HPW);
+                                     SAVE ? gsaved : nullptr, GF + wv * HPW, [&] {
+#pragma unroll
+                                       for (int i = 0; i < PF; ++i) {
+                                         kb[i].load(kp + min(i, tlast) * stride);
+                                         qb[i].load(qp + min(i, tlast) * stride);
+                                       }
+                                     });
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       kb[i].pin();
