@@ -711,17 +711,18 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
 //      (rescaled frame), keeping the local readout f_t (zh_t . q_t) in LDS;
 //      its chunk map is (G_k, F_k = z_{Q-1});
 //   2. the segment's chunk maps are composed through LDS into the segment
-//      map, which is published; the state entering the segment is found by a
-//      decoupled look-back over the earlier segments of the same (b, head
-//      group): published maps are composed, nearest first, until a published
-//      leaving state is met (segment 0 starts from h0).  The state leaving the
-//      segment is then published for the later segments;
+//      map, which is published.  The state entering the segment is the
+//      composition, oldest first, of the maps of the segments since its
+//      anchor (segment kAnchor * floor((seg - 1) / kAnchor)) applied to the
+//      anchor state (h0, or the published state leaving the segment before the
+//      anchor): a fixed order, so the results do not depend on timing.  Anchor
+//      ends publish their leaving state for the next kAnchor segments;
 //   3. each wave derives the state entering its chunk and runs the decay-free
 //      correction with the full readout; y is written coalesced.
 // SAVE (training forward) also writes what the backward reads: the state
 // entering every chunk and G_k (the four-launch layout), the per-token records
 // (p_t, pc_t), (c^_{t+1}.q_t, Y_t.q_t) and g_t, as the main pass does.
-// Look-back flags hold epoch << 2 | state (1: map, 2: leaving state) with a
+// Flags hold epoch << 2 | state (1: map, 2: map and leaving state) with a
 // per-call epoch, so the workspace needs no clearing between calls.  Published
 // data and flags are written and read with agent-scope atomics (stores written
 // through to the device-coherent level, loads served from it), so no cache
@@ -729,13 +730,13 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
 // before the flag is stored, and a reader issues its data loads only after it
 // has seen the flag (agent-scope release / acquire fences would write back or
 // invalidate the whole L2 instead, microseconds per publish and the k, q rows
-// the correction pass re-reads).  A workgroup waits only on
-// workgroups of lower index, and the launcher takes this path only when the
-// whole grid is resident at once; a bounded wait turns a missing flag into NaN
-// output instead of a hang.
+// the correction pass re-reads).  A workgroup waits only on segments of lower
+// index; the launcher sizes the grid to the workgroups resident at once (one
+// per segment, or fewer that take the segments in order), and a bounded wait
+// turns a missing flag into NaN output instead of a hang.
 // ---------------------------------------------------------------------------
 constexpr int kLookbackBatch = 8;
-constexpr int kOnePassMaxSeg = 64;
+constexpr int kAnchor = 63;  // segments folded from one anchor state (<= 63: one watch window)
 constexpr uint64_t kSpinTicks = 5000000;  // look-back wait bound: 50 ms of the 100 MHz real-time counter
 
 struct OnePassBufs {
@@ -759,16 +760,46 @@ __device__ __forceinline__ float2 ld_agent(const float2* p) {
   return __builtin_bit_cast(float2, x);
 }
 
+template <typename T>
+struct OnePassArgs {
+  const typename T::raw *q, *k, *v, *beta, *sel_c, *dt, *r;
+  const float *alpha, *omega;
+  float c;
+  const float* h0;
+  typename T::raw* y;
+  float* h_final;
+  OnePassBufs ob;
+  float2* states;  // SAVE: state entering every chunk (B, NC, H, D)
+  float2* gam;     // SAVE: G_k (B, NC, H)
+  float4* saved;   // SAVE: per-token records (B, L, H, 2)
+  float2* gsaved;  // SAVE: g_t (B, L, H)
+  unsigned long long epoch;
+  int L, H, Q, NC, NSEG, n_hg, n_chain, n_items;
+};
+
+// One segment (work item): item = seg * n_chain + chain.
 template <typename T, int D, int LPH, bool SAVE>
-__global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(
-    const typename T::raw* __restrict__ q, const typename T::raw* __restrict__ k,
-    const typename T::raw* __restrict__ v, const typename T::raw* __restrict__ beta,
-    const typename T::raw* __restrict__ sel_c, const typename T::raw* __restrict__ dt,
-    const typename T::raw* __restrict__ r, const float* __restrict__ alpha,
-    const float* __restrict__ omega, float c, const float* __restrict__ h0, typename T::raw* __restrict__ y,
-    float* __restrict__ h_final, OnePassBufs ob, float2* __restrict__ states, float2* __restrict__ gam,
-    float4* __restrict__ saved, float2* __restrict__ gsaved, unsigned long long epoch, int L, int H, int Q,
-    int NC, int NSEG, int n_hg) {
+__device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int item) {
+  const typename T::raw* __restrict__ q = a.q;
+  const typename T::raw* __restrict__ k = a.k;
+  const typename T::raw* __restrict__ v = a.v;
+  const typename T::raw* __restrict__ beta = a.beta;
+  const typename T::raw* __restrict__ sel_c = a.sel_c;
+  const typename T::raw* __restrict__ dt = a.dt;
+  const typename T::raw* __restrict__ r = a.r;
+  const float* __restrict__ alpha = a.alpha;
+  const float* __restrict__ omega = a.omega;
+  const float c = a.c;
+  const float* __restrict__ h0 = a.h0;
+  typename T::raw* __restrict__ y = a.y;
+  float* __restrict__ h_final = a.h_final;
+  const OnePassBufs& ob = a.ob;
+  float2* __restrict__ states = a.states;
+  float2* __restrict__ gam = a.gam;
+  float4* __restrict__ saved = a.saved;
+  float2* __restrict__ gsaved = a.gsaved;
+  const unsigned long long epoch = a.epoch;
+  const int L = a.L, H = a.H, Q = a.Q, NC = a.NC, NSEG = a.NSEG, n_hg = a.n_hg;
   using Cfg = FusedCfg<T, D, LPH>;
   constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch, W = kOnePassW;
   constexpr int SEGN = HPW * D;  // complex elements of a head group's state
@@ -779,9 +810,8 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(
   // wave index made wave-uniform, so the tile's fields live in scalar registers
   const int wv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
   const int lane = int(threadIdx.x) % kWave;
-  const int n_chain = int(gridDim.x) / NSEG;
-  const int chain = int(blockIdx.x) % n_chain;
-  const int seg = int(blockIdx.x) / n_chain;
+  const int chain = item % a.n_chain;
+  const int seg = item / a.n_chain;
   const int bi = chain / n_hg;
   const int hbase = (chain % n_hg) * HPW;
   const int n_live = min(W, NC - seg * W);  // chunks in this segment
@@ -941,101 +971,101 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(
   const int64_t sb0 = (int64_t(bi) * NSEG + seg) * H;  // (b, seg, head 0)
   unsigned long long* flag = ob.flag + sb0 + hbase;
 
-  float2 Sin[EPT];  // state entering the segment
-  if (seg == 0) {
+  // publish the segment map (every segment: later ones fold it in)
+  if (ehok) {
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-      Sin[i] = make_float2(0.0f, 0.0f);
-      if (h0 && ehok) {
-        const int64_t hb = (int64_t(bi) * H + eh) * 2 * D;
-        Sin[i] = make_float2(h0[hb + ed + i], h0[hb + D + ed + i]);
-      }
-    }
-  } else {
-    // publish the segment map, then look back
-    if (ehok) {
-#pragma unroll
-      for (int i = 0; i < EPT; ++i) st_agent(ob.seg_f + (sb0 + eh) * D + ed + i, segF[i]);
-      if (ed == 0) st_agent(ob.seg_g + sb0 + eh, segG);
-    }
-    wait_stores_acked();
-    __syncthreads();
-    if (threadIdx.x == 0)
-      __hip_atomic_store(flag, (epoch << 2) | 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = 0; i < EPT; ++i) st_agent(ob.seg_f + (sb0 + eh) * D + ed + i, segF[i]);
+    if (ed == 0) st_agent(ob.seg_g + sb0 + eh, segG);
+  }
+  wait_stores_acked();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_store(flag, (epoch << 2) | 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // state entering the segment, in a fixed order (so results do not depend on
+  // timing): from the anchor a = kAnchor * floor((seg - 1) / kAnchor) -- h0
+  // for a = 0, else the published state leaving segment a - 1 -- fold the
+  // maps of segments a .. seg - 1, oldest first.  Wave 0 waits until they are
+  // published (lane i: map of segment a + i; lane 63: the anchor state).
+  const int anc = seg == 0 ? 0 : kAnchor * ((seg - 1) / kAnchor);
+  const int nmap = seg - anc;
+  int ok = 1;
+  if (seg > 0) {
     if (wv == 0) {
-      // lane i watches segment seg - 1 - i; wait until the nearest published
-      // leaving state i0 is known and every segment between has its map
       const unsigned long long* f0 = ob.flag + (int64_t(bi) * NSEG) * H + hbase;
-      int found = -1;
+      int got = 0;
       const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
       for (;;) {
-        int st = 0;
-        if (lane < seg) {
-          const unsigned long long fv = __hip_atomic_load(
-              const_cast<unsigned long long*>(f0 + int64_t(seg - 1 - lane) * H), __ATOMIC_RELAXED,
-              __HIP_MEMORY_SCOPE_AGENT);
+        int st = 3;  // lanes with nothing to watch count as ready
+        const int js = lane < nmap ? anc + lane : (lane == kWave - 1 && anc > 0 ? anc - 1 : -1);
+        if (js >= 0) {
+          const unsigned long long fv = __hip_atomic_load(const_cast<unsigned long long*>(f0 + int64_t(js) * H),
+                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           st = (fv >> 2) == epoch ? int(fv & 3ull) : 0;
         }
-        const uint64_t m2 = __builtin_amdgcn_ballot_w64(st == 2);
-        const uint64_t m1 = __builtin_amdgcn_ballot_w64(st >= 1);
-        if (m2) {
-          const int i0 = __builtin_ctzll(m2);
-          const uint64_t need = i0 == 63 ? ~0ull : ((1ull << (i0 + 1)) - 1ull);
-          if ((m1 & need) == need) {
-            found = i0;
-            break;
-          }
+        const bool ready = lane < nmap ? st >= 1 : (lane == kWave - 1 && anc > 0 ? st == 2 : true);
+        if (__builtin_amdgcn_ballot_w64(!ready) == 0ull) {
+          got = 1;
+          break;
         }
         if (__builtin_amdgcn_s_memrealtime() - t_start > kSpinTicks) break;
         __builtin_amdgcn_s_sleep(2);
       }
-      if (lane == 0) ctrl[0] = found;
+      if (lane == 0) ctrl[0] = got;
     }
     __syncthreads();
-    const int i0 = ctrl[0];
-    // compose: leaving state of segment seg - 1 - i0, then the maps of the
-    // segments after it, oldest first
-    const int jl = seg - 1 - max(i0, 0);
+    ok = ctrl[0];
+  }
+  float2 Sin[EPT];
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) Sin[i] = make_float2(0.0f, 0.0f);
-    if (ehok) {
-      const int64_t base = int64_t(bi) * NSEG * H + eh;
+  for (int i = 0; i < EPT; ++i) Sin[i] = make_float2(0.0f, 0.0f);
+  if (ehok) {
+    const int64_t lb = int64_t(bi) * NSEG * H + eh;  // (b, segment 0, head eh)
+    if (anc == 0) {
+      if (h0) {
+        const int64_t hb = (int64_t(bi) * H + eh) * 2 * D;
 #pragma unroll
-      for (int i = 0; i < EPT; ++i) Sin[i] = ld_agent(ob.seg_s + (base + int64_t(jl) * H) * D + ed + i);
-      for (int jb = jl + 1; jb < seg; jb += kLookbackBatch) {
-        float2 G[kLookbackBatch], F[kLookbackBatch][EPT];
-#pragma unroll
-        for (int u = 0; u < kLookbackBatch; ++u) {
-          const int js = min(jb + u, seg - 1);
-          G[u] = ld_agent(ob.seg_g + base + int64_t(js) * H);
-#pragma unroll
-          for (int i = 0; i < EPT; ++i) F[u][i] = ld_agent(ob.seg_f + (base + int64_t(js) * H) * D + ed + i);
-        }
-#pragma unroll
-        for (int u = 0; u < kLookbackBatch; ++u) {
-          if (jb + u < seg) {
-#pragma unroll
-            for (int i = 0; i < EPT; ++i)
-              Sin[i] = make_float2(G[u].x * Sin[i].x - G[u].y * Sin[i].y + F[u][i].x,
-                                   G[u].x * Sin[i].y + G[u].y * Sin[i].x + F[u][i].y);
-          }
-        }
+        for (int i = 0; i < EPT; ++i) Sin[i] = make_float2(h0[hb + ed + i], h0[hb + D + ed + i]);
       }
-      if (i0 < 0) {
+    } else {
 #pragma unroll
-        for (int i = 0; i < EPT; ++i) Sin[i] = make_float2(__builtin_nanf(""), __builtin_nanf(""));
+      for (int i = 0; i < EPT; ++i) Sin[i] = ld_agent(ob.seg_s + (lb + int64_t(anc - 1) * H) * D + ed + i);
+    }
+    for (int jb = 0; jb < nmap; jb += kLookbackBatch) {
+      float2 G[kLookbackBatch], F[kLookbackBatch][EPT];
+#pragma unroll
+      for (int u = 0; u < kLookbackBatch; ++u) {
+        const int js = anc + min(jb + u, nmap - 1);
+        G[u] = ld_agent(ob.seg_g + lb + int64_t(js) * H);
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) F[u][i] = ld_agent(ob.seg_f + (lb + int64_t(js) * H) * D + ed + i);
+      }
+#pragma unroll
+      for (int u = 0; u < kLookbackBatch; ++u) {
+        if (jb + u < nmap) {
+#pragma unroll
+          for (int i = 0; i < EPT; ++i)
+            Sin[i] = make_float2(G[u].x * Sin[i].x - G[u].y * Sin[i].y + F[u][i].x,
+                                 G[u].x * Sin[i].y + G[u].y * Sin[i].x + F[u][i].y);
+        }
       }
     }
+    if (!ok) {
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) Sin[i] = make_float2(__builtin_nanf(""), __builtin_nanf(""));
+    }
   }
-  // publish the state leaving the segment; the last segment's is h_final
+  // the state leaving the segment: h_final for the last segment; published
+  // for the segments that start from it (anchor ends, (seg + 1) % kAnchor == 0)
+  const bool anchor_end = seg + 1 < NSEG && (seg + 1) % kAnchor == 0;
 #pragma unroll
   for (int i = 0; i < EPT; ++i) Sx[e0 + i] = Sin[i];
-  if (ehok) {
+  if (ehok && (anchor_end || seg + 1 == NSEG)) {
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
       const float2 so = make_float2(segG.x * Sin[i].x - segG.y * Sin[i].y + segF[i].x,
                                     segG.x * Sin[i].y + segG.y * Sin[i].x + segF[i].y);
-      if (seg + 1 < NSEG) {
+      if (anchor_end) {
         st_agent(ob.seg_s + (sb0 + eh) * D + ed + i, so);
       } else {
         const int64_t hb = (int64_t(bi) * H + eh) * 2 * D;
@@ -1044,9 +1074,9 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(
       }
     }
   }
-  if (seg + 1 < NSEG) wait_stores_acked();
+  if (anchor_end) wait_stores_acked();
   __syncthreads();
-  if (seg + 1 < NSEG && threadIdx.x == 0)
+  if (anchor_end && threadIdx.x == 0)
     __hip_atomic_store(flag, (epoch << 2) | 2ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // 3. state entering this wave's chunk, then the correction with the readout
@@ -1157,6 +1187,22 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(
   }
 }
 
+// PERSIST false: one workgroup per segment (grid = segments, all resident).
+// PERSIST true: the grid is resident at once and takes the segments in order,
+// so the lowest unfinished segment is always running and waits only on
+// finished ones.
+template <typename T, int D, int LPH, bool SAVE, bool PERSIST>
+__global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(OnePassArgs<T> a) {
+  if (!PERSIST) {
+    onepass_segment<T, D, LPH, SAVE>(a, int(blockIdx.x));
+    return;
+  }
+  for (int item = int(blockIdx.x); item < a.n_items; item += int(gridDim.x)) {
+    onepass_segment<T, D, LPH, SAVE>(a, item);
+    __syncthreads();  // LDS is reused by the next segment
+  }
+}
+
 }  // namespace cdssm
 
 // ---------------------------------------------------------------------------
@@ -1191,14 +1237,13 @@ size_t onepass_lds(int Q) {
          size_t(kOnePassW) * HPW * sizeof(float4) + size_t(HPW) * D * sizeof(float2) + 16;
 }
 
-// The one-pass grid must be resident at once (a workgroup may wait on any
-// earlier one): check the per-block LDS limit and occupancy x CUs, cached per
-// device and LDS size.
-template <typename T, int D, int LPH, bool SAVE>
-bool onepass_fits(int grid, size_t lds, int nseg) {
-  if (nseg > kOnePassMaxSeg) return false;
+// Workgroups of the one-pass kernel resident at once (its grid: a workgroup
+// may wait on any earlier segment), from the per-block LDS limit and the
+// occupancy x CUs; 0 if it cannot run.  Cached per device and LDS size.
+template <typename T, int D, int LPH, bool SAVE, bool PERSIST>
+int onepass_capacity(size_t lds) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return false;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
   struct Entry {
     int dev;
     size_t lds;
@@ -1209,10 +1254,10 @@ bool onepass_fits(int grid, size_t lds, int nseg) {
   static int n_cache = 0;
   std::lock_guard<std::mutex> lock(mu);
   for (int i = 0; i < n_cache; ++i)
-    if (cache[i].dev == dev && cache[i].lds == lds) return grid <= cache[i].capacity;
+    if (cache[i].dev == dev && cache[i].lds == lds) return cache[i].capacity;
   int max_lds = 0, n_cu = 0, per_cu = 0;
   int capacity = 0;
-  const void* fn = reinterpret_cast<const void*>(&fused_fwd_onepass_kernel<T, D, LPH, SAVE>);
+  const void* fn = reinterpret_cast<const void*>(&fused_fwd_onepass_kernel<T, D, LPH, SAVE, PERSIST>);
   if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
       hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
       lds <= size_t(max_lds)) {
@@ -1222,7 +1267,7 @@ bool onepass_fits(int grid, size_t lds, int nseg) {
   }
   (void)hipGetLastError();
   if (n_cache < 16) cache[n_cache++] = Entry{dev, lds, capacity};
-  return grid <= capacity;
+  return capacity;
 }
 
 template <typename T, int D, int LPH, int LPHS>
@@ -1250,39 +1295,73 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   const int slots = round_up(Q, kWave) * HPW, slots_s = round_up(Q, kWave) * HPWS;
 
   if (g_fwd_path.load(std::memory_order_relaxed) != kPathFour) {
-    const int grid = w.NSEG * B * n_hg;
+    const int64_t items = int64_t(w.NSEG) * B * n_hg;
     const size_t lds = onepass_lds<D, LPH>(Q);
-    if (save ? onepass_fits<T, D, LPH, true>(grid, lds, w.NSEG) : onepass_fits<T, D, LPH, false>(grid, lds, w.NSEG)) {
-      const int64_t op = w.onepass_offset();
-      float2* base = reinterpret_cast<float2*>(ws) + op;
+    // one round of resident workgroups takes every segment: one-pass.  More
+    // segments than that: the persistent one-pass only for inference with
+    // full rounds (measured on MI355X: faster than four launches at C3,
+    // slower at C2's 1.5 rounds and for the training forward's records)
+    const int cap1 = save ? onepass_capacity<T, D, LPH, true, false>(lds)
+                          : onepass_capacity<T, D, LPH, false, false>(lds);
+    const int capp = save ? onepass_capacity<T, D, LPH, true, true>(lds)
+                          : onepass_capacity<T, D, LPH, false, true>(lds);
+    const bool single = cap1 > 0 && items <= cap1;
+    const bool forced = g_fwd_path.load(std::memory_order_relaxed) == kPathOne;
+    const int64_t rounds = capp > 0 ? (items + capp - 1) / capp : 0;
+    const bool persist = !single && capp > 0 && items <= 0x7fffffff &&
+                         (forced || (!save && items * 10 >= rounds * capp * 9));
+    if (single || persist) {
+      const int grid = single ? int(items) : capp;
+      float2* base = reinterpret_cast<float2*>(ws) + w.onepass_offset();
       const int64_t nsd = int64_t(B) * w.NSEG * H * D, nsh = int64_t(B) * w.NSEG * H;
-      const OnePassBufs ob{base, base + nsd, base + 2 * nsd, reinterpret_cast<unsigned long long*>(base + 2 * nsd + nsh)};
-      const unsigned long long epoch = next_epoch();
+      OnePassArgs<T> a;
+      a.q = (const raw*)q;
+      a.k = (const raw*)k;
+      a.v = (const raw*)v;
+      a.beta = (const raw*)beta;
+      a.sel_c = (const raw*)sel_c;
+      a.dt = (const raw*)dt;
+      a.r = (const raw*)r;
+      a.alpha = alpha;
+      a.omega = omega;
+      a.c = c;
+      a.h0 = h0;
+      a.y = (raw*)y;
+      a.h_final = h_final;
+      a.ob = OnePassBufs{base, base + nsd, base + 2 * nsd,
+                         reinterpret_cast<unsigned long long*>(base + 2 * nsd + nsh)};
+      a.states = save ? summ : nullptr;
+      a.gam = save ? gam : nullptr;
+      a.saved = save ? saved : nullptr;
+      a.gsaved = save ? gsaved : nullptr;
+      a.epoch = next_epoch();
+      a.L = L;
+      a.H = H;
+      a.Q = Q;
+      a.NC = NC;
+      a.NSEG = w.NSEG;
+      a.n_hg = n_hg;
+      a.n_chain = B * n_hg;
+      a.n_items = int(items);
       if (path) *path = kPathOne;
       if (ev)
         for (int i = 0; i < 4; ++i) (void)hipEventRecord(ev[i], stream);
-      float2* summ = reinterpret_cast<float2*>(ws);
-      float2* gam = summ + w.n_summ;
-      float4* saved = reinterpret_cast<float4*>(reinterpret_cast<float2*>(ws) + w.saved_offset());
-      float2* gsaved = reinterpret_cast<float2*>(ws) + w.gsaved_offset();
-      if (save)
-        hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, true>), dim3(unsigned(grid)),
-                           dim3(kWave * kOnePassW), lds, stream, (const raw*)q, (const raw*)k, (const raw*)v,
-                           (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c, h0,
-                           (raw*)y, h_final, ob, summ, gam, saved, gsaved, epoch, L, H, Q, NC, w.NSEG, n_hg);
+      const dim3 gd = dim3(unsigned(grid)), bd = dim3(kWave * kOnePassW);
+      if (save && single)
+        hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, true, false>), gd, bd, lds, stream, a);
+      else if (save)
+        hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, true, true>), gd, bd, lds, stream, a);
+      else if (single)
+        hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, false, false>), gd, bd, lds, stream, a);
       else
-        hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, false>), dim3(unsigned(grid)),
-                           dim3(kWave * kOnePassW), lds, stream, (const raw*)q, (const raw*)k, (const raw*)v,
-                           (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c, h0,
-                           (raw*)y, h_final, ob, nullptr, nullptr, nullptr, nullptr, epoch, L, H, Q, NC, w.NSEG,
-                           n_hg);
+        hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, false, true>), gd, bd, lds, stream, a);
       const int st = cdssm_host::check_launch("cdssm_fused_scan_fwd/onepass");
       if (ev) (void)hipEventRecord(ev[4], stream);
       return st;
     }
-    if (g_fwd_path.load(std::memory_order_relaxed) == kPathOne) {
+    if (forced) {
       cdssm_host::set_error("cdssm_fused_scan_fwd: one-pass path required but not possible for this shape "
-                            "(%d workgroups, %d segments per sequence, %zu bytes of LDS)", grid, w.NSEG, lds);
+                            "(%zu bytes of LDS per workgroup)", lds);
       return CDSSM_EINVAL;
     }
   }
