@@ -64,6 +64,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-batches", type=int, default=1)
     ap.add_argument("--no-fwd-bwd", action="store_true")
+    ap.add_argument("--forward-path", default="auto", choices=["auto", "four_launch", "one_pass"],
+                    help="how the forward is launched (default: the library's own choice)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a device copy of this many MiB (read + write), 10 times, and exit: "
                          "the reference kernel for scaling HBM byte counters")
@@ -176,8 +178,10 @@ def main():
         return
 
     import torch
-    from cdssm_hip.scan import PreparedForward
+    from cdssm_hip.scan import PreparedForward, set_forward_path
     from cdssm_hip.workloads import CONFIGS, draw_inputs, scan_bytes
+
+    set_forward_path(args.forward_path)
 
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
