@@ -543,7 +543,9 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   const int hl = hok ? h : H - 1;
   const int slots = round_up(Q, kWave) * HPW;
   const int ntr = round_up(tc.nt, PF);
-  const int nseg = round_up(Q, CK) / CK;
+  // checkpoints at t = 0, CK, ... < ntr <= round_up(Q, PF): per tile and head
+  // slot round_up(Q, PF) / CK of them (not round_up(Q, CK) / CK: Q = 20 runs to t = 20)
+  const int nseg = round_up(Q, PF) / CK;
   const float al = alpha[hl], om = omega[hl];
 
   const int64_t stride = int64_t(H) * D;
@@ -877,7 +879,8 @@ BwdLayout bwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) 
   w.n_segX = B * H * w.S * D;
   w.n_parts = B * w.NC * H;
   // z checkpoints of the main pass: per (tile, head slot, segment) one D-vector
-  w.n_ck = B * w.NC * ((H + kBwdMaxHPW - 1) / kBwdMaxHPW) * kBwdMaxHPW * ((chunk + kBwdCK - 1) / kBwdCK) * D;
+  w.n_ck = B * w.NC * ((H + kBwdMaxHPW - 1) / kBwdMaxHPW) * kBwdMaxHPW *
+           (((chunk + kBwdPF - 1) / kBwdPF) * kBwdPF / kBwdCK) * D;
   return w;
 }
 

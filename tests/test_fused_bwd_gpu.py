@@ -66,6 +66,9 @@ CASES = [
     ("fp32_h0_ragged", ScanConfig("t", B=2, H=3, L=300, D=64, dtype="fp32", h0_std=0.1), None),
     ("fp32_D128_h0", ScanConfig("t", B=1, H=2, L=333, D=128, dtype="fp32", h0_std=0.1), None),
     ("fp32_chunk32", ScanConfig("t", B=1, H=2, L=200, D=64, dtype="fp32", h0_std=0.1), 32),
+    # chunk % 8 in 1..4: the main pass's token loop runs past round_up(chunk, 4)
+    ("fp32_chunk20", ScanConfig("t", B=1, H=5, L=230, D=64, dtype="fp32", h0_std=0.1), 20),
+    ("bf16_D128_chunk100", ScanConfig("t", B=1, H=3, L=300, D=128, h0_std=0.1), 100),
     ("bf16_D64", ScanConfig("t", B=2, H=4, L=640, D=64), None),
     ("bf16_D128", ScanConfig("t", B=1, H=3, L=512, D=128, h0_std=0.1), None),
 ]

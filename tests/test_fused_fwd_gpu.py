@@ -42,6 +42,7 @@ SMALL = [
     ("fp32_h0_ragged", ScanConfig("t", B=2, H=5, L=300, D=64, dtype="fp32", h0_std=0.1), None),
     ("fp32_D128", ScanConfig("t", B=1, H=3, L=260, D=128, dtype="fp32", h0_std=0.1), None),
     ("fp32_chunk32", ScanConfig("t", B=1, H=4, L=200, D=64, dtype="fp32", h0_std=0.1), 32),
+    ("fp32_chunk20", ScanConfig("t", B=1, H=5, L=230, D=64, dtype="fp32", h0_std=0.1), 20),
     ("fp32_one_token", ScanConfig("t", B=2, H=3, L=1, D=64, dtype="fp32", h0_std=0.1), None),
     ("bf16_D64", ScanConfig("t", B=2, H=16, L=640, D=64), None),
     ("bf16_D128_ragged", ScanConfig("t", B=1, H=24, L=333, D=128, h0_std=0.1), None),
