@@ -193,18 +193,65 @@ __device__ __forceinline__ void cmul_acc(float& xr, float& xi, float yr, float y
 // forward's per-token records (B, L, H, 2) float4 and (B, L, H) float2, then
 // the one-pass forward's look-back area over segments of kOnePassW chunks:
 // segment maps (B, NSEG, H, D), leaving states (B, NSEG, H, D), segment
-// rotations (B, NSEG, H) and flags (B, NSEG, H) (8-byte words).
+// rotations (B, NSEG, H) and flags (B, NSEG, H) (8-byte words); then, written
+// by the training forward for the backward, the local state z_{t-1} at every
+// kZck-th token t of each chunk (B, NC, H, NCK, D) and the decay-free
+// correction state after each chunk's last step (B, NC, H, D).
 // ---------------------------------------------------------------------------
+// Complex rows of the z checkpoints, element idx = ((b, chunk, h) * NCK +
+// slot) * D + d: fp32 pairs for fp32 inputs; for bf16 inputs bf16 pairs, (re,
+// im) in one dword, in the first half of the region -- the precision the
+// reference keeps its saved local states in (intra_chunk_scan.cu:588-589).
+template <typename T, int N>
+__device__ __forceinline__ void store_zck(float2* base, int64_t idx, const float (&re)[N], const float (&im)[N]) {
+  if constexpr (T::bytes == 2) {
+    uint32_t* p = reinterpret_cast<uint32_t*>(base) + idx;
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+      for (int j = 0; j < N; j += 4)
+        *reinterpret_cast<uint4*>(p + j) = make_uint4(pack_bf16x2(re[j], im[j]), pack_bf16x2(re[j + 1], im[j + 1]),
+                                                      pack_bf16x2(re[j + 2], im[j + 2]),
+                                                      pack_bf16x2(re[j + 3], im[j + 3]));
+    } else {
+#pragma unroll
+      for (int j = 0; j < N; ++j) p[j] = pack_bf16x2(re[j], im[j]);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) base[idx + j] = make_float2(re[j], im[j]);
+  }
+}
+template <typename T, int N>
+__device__ __forceinline__ void load_zck(const float2* base, int64_t idx, float2 (&out)[N]) {
+  if constexpr (T::bytes == 2) {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(base) + idx;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const uint32_t u = p[j];
+      out[j] = make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) out[j] = base[idx + j];
+  }
+}
+
 constexpr int kSegLen = 16;   // chunks per forward carry segment
 constexpr int kOnePassW = 4;  // chunks (waves) per workgroup of the one-pass forward
+constexpr int kZck = 4;       // token interval of the z checkpoints
+constexpr int kTokRound = 8;  // token loops run to round_up(tokens, kTokRound)
 
 struct FwdLayout {
-  int NC, S, NSEG;
-  int64_t n_summ, n_gam, n_segA, n_segX, n_pad, n_saved, n_gsaved, n_op;
-  int64_t total() const { return n_summ + n_gam + n_segA + n_segX + n_pad + n_saved + n_gsaved + n_op; }
+  int NC, S, NSEG, NCK;
+  int64_t n_summ, n_gam, n_segA, n_segX, n_pad, n_saved, n_gsaved, n_op, n_zck, n_cend;
+  int64_t total() const {
+    return n_summ + n_gam + n_segA + n_segX + n_pad + n_saved + n_gsaved + n_op + n_zck + n_cend;
+  }
   int64_t saved_offset() const { return n_summ + n_gam + n_segA + n_segX + n_pad; }
   int64_t gsaved_offset() const { return saved_offset() + n_saved; }
   int64_t onepass_offset() const { return gsaved_offset() + n_gsaved; }
+  int64_t zck_offset() const { return onepass_offset() + n_op; }
+  int64_t cend_offset() const { return zck_offset() + n_zck; }
 };
 
 inline FwdLayout fwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) {
@@ -220,6 +267,10 @@ inline FwdLayout fwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t 
   w.n_gsaved = B * L * H;
   w.NSEG = (w.NC + kOnePassW - 1) / kOnePassW;
   w.n_op = B * w.NSEG * H * (2 * D + 2);
+  // checkpoints at t = 0, kZck, ... < round_up(chunk, kTokRound)
+  w.NCK = int((chunk + kTokRound - 1) / kTokRound * kTokRound / kZck);
+  w.n_zck = B * w.NC * H * int64_t(w.NCK) * D;
+  w.n_cend = B * w.NC * H * D;
   return w;
 }
 

@@ -25,9 +25,9 @@
 //   B2 rfold/rreplay: reverse carry over chunks,
 //               d s_k = conj(G_k) d s_{k+1} + lambda_0^(k),  d s_NC = d h_final,
 //               storing d s_{k+1} per chunk and d h0 = d s_0
-//   B3 main:    per chunk: forward recompute (z checkpoints every 16 steps),
-//               then segment-wise reverse of both branches, emitting dq, dk,
-//               dv, dbeta, dsel_C, ddt, dr and per-chunk d alpha / d omega
+//   B3 main:    per chunk: segment-wise reverse of both branches from the
+//               training forward's z checkpoints and records, emitting dq,
+//               dk, dv, dbeta, dsel_C, ddt, dr and per-chunk d alpha / d omega
 //   B4 heads:   deterministic sum of the per-chunk d alpha / d omega.
 //
 // Work layout of B1 and B3: one wave64 per (b, chunk, group of HPW heads);
@@ -61,8 +61,7 @@ struct BwdCorrCfg {
   static constexpr int HPW = kWave / LPH;
   static constexpr int DPL = D / LPH;
 };
-constexpr int kBwdMaxHPW = 4;
-constexpr int kBwdCK = 4;     // z checkpoint interval of the main pass
+constexpr int kBwdCK = 4;     // z checkpoint interval (the training forward writes them)
 constexpr int kBwdPF = 8;     // row prefetch depth (main pass)
 #ifndef CDSSM_BWD_CORR_PF
 #define CDSSM_BWD_CORR_PF 8
@@ -505,10 +504,10 @@ __device__ __forceinline__ DynGrad cayley_gated_bwd(float dt, float r, float alp
 }
 
 // ---------------------------------------------------------------------------
-// B3: per-chunk backward of both branches.
-//   forward pass: z and c^ from (0, s_k); per token keeps p_t = z_{t-1}.k_t,
-//     pc_t = c^_t.k_t, Y_t.q_t and the correction's delta g_t in LDS, emits dq,
-//     and stores z every kBwdCK tokens in the checkpoint workspace;
+// B3: per-chunk backward of both branches, from the training forward's
+//   workspace: z_{t-1} every kBwdCK tokens, c^ after the chunk's last step,
+//   and per token p_t = z_{t-1}.k_t, pc_t = c^_t.k_t, c^_{t+1}.q_t, Y_t.q_t
+//   (staged in LDS with the correction's delta g_t);
 //   reverse pass, kBwdCK tokens at a time: z of the segment is recomputed
 //     from its checkpoint with the stored p_t (no reductions); c^_t is rebuilt
 //     backward, exactly, as c^_t = c^_{t+1} + beta_t pc_t k_t; the local adjoint
@@ -527,13 +526,14 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
     const typename T::raw* __restrict__ r, const float* __restrict__ alpha,
     const float* __restrict__ omega, float c, const typename T::raw* __restrict__ dy,
     const float2* __restrict__ states, const float4* __restrict__ saved, const float2* __restrict__ dsn,
-    float2* __restrict__ ckpt, typename T::raw* __restrict__ dq, typename T::raw* __restrict__ dk,
+    const float2* __restrict__ zck, const float2* __restrict__ cend, typename T::raw* __restrict__ dq,
+    typename T::raw* __restrict__ dk,
     typename T::raw* __restrict__ dv,
     typename T::raw* __restrict__ dbeta, typename T::raw* __restrict__ dsel,
     typename T::raw* __restrict__ ddt, typename T::raw* __restrict__ dr, float2* __restrict__ dhead_parts,
-    int L, int H, int Q, int NC, int n_hg) {
+    int L, int H, int Q, int NC, int NCK, int n_hg) {
   constexpr int LPH = BwdCfg<D>::LPH, HPW = BwdCfg<D>::HPW, DPL = BwdCfg<D>::DPL, PF = kBwdPF, CK = kBwdCK;
-  static_assert(PF % CK == 0, "checkpoints fall inside prefetch groups at fixed positions");
+  static_assert(CK == kZck && PF == kTokRound, "the training forward's z checkpoints: every CK tokens");
   extern __shared__ float4 smem4[];
   const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
@@ -543,9 +543,6 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   const int hl = hok ? h : H - 1;
   const int slots = round_up(Q, kWave) * HPW;
   const int ntr = round_up(tc.nt, PF);
-  // checkpoints at t = 0, CK, ... < ntr <= round_up(Q, PF): per tile and head
-  // slot round_up(Q, PF) / CK of them (not round_up(Q, CK) / CK: Q = 20 runs to t = 20)
-  const int nseg = round_up(Q, PF) / CK;
   const float al = alpha[hl], om = omega[hl];
 
   const int64_t stride = int64_t(H) * D;
@@ -554,67 +551,25 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   const typename T::raw* qp = q + off;
   const int tlast = tc.nt - 1;
   const int64_t chh = (int64_t(tc.b) * NC + tc.chunk) * H + hl;  // (b, chunk, head) index
-  float2* ck = ckpt + ((int64_t(blockIdx.x) * HPW + hh) * nseg) * D + sub * DPL;
+  // the training forward's z checkpoints of this (chunk, head): z_{t-1} at t = CK * seg
+  const int64_t ck0 = chh * NCK * D + sub * DPL;
 
-  RowVec<T, DPL> kb[PF];
-#pragma unroll
-  for (int i = 0; i < PF; ++i) kb[i].load(kp + min(i, tlast) * stride);
-  float zr[DPL], zi[DPL], cr[DPL], ci[DPL];
+  // c^ after the chunk's last step (the reverse pass rebuilds it backward)
+  float cr[DPL], ci[DPL];
   const float2* sp = states + chh * D + sub * DPL;
+  {
+    const float2* ce = cend + chh * D + sub * DPL;
 #pragma unroll
-  for (int jj = 0; jj < DPL; ++jj) {
-    const float2 sv = sp[jj];
-    zr[jj] = zi[jj] = 0.0f;
-    cr[jj] = hok ? sv.x : 0.0f;
-    ci[jj] = hok ? sv.y : 0.0f;
+    for (int jj = 0; jj < DPL; ++jj) {
+      const float2 cv = ce[jj];
+      cr[jj] = hok ? cv.x : 0.0f;
+      ci[jj] = hok ? cv.y : 0.0f;
+    }
   }
   BwdScalars s{smem4, smem4 + slots, smem4 + 2 * slots};
   float4* sP = smem4 + 3 * slots;
   float4* sG = smem4 + 4 * slots;
   stage_bwd<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, dy, al, om, c, s, saved, sP, sG);
-#pragma unroll
-  for (int i = 0; i < PF; ++i) kb[i].pin();
-  __syncthreads();
-
-  // ---- forward pass: z and c^ with the saved p_t, pc_t (no reductions) ----
-  for (int tb = 0; tb < ntr; tb += PF) {
-    float4 s0[PF], pv[PF];
-    float bbv[PF];
-#pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      const int p = (tb + i) * HPW + hh;
-      s0[i] = s.S0[p];
-      bbv[i] = s.S1[p].x;
-      pv[i] = sP[p];
-    }
-#pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      const int t = tb + i;
-      if (i % CK == 0) {
-        // checkpoint z_{t-1}
-#pragma unroll
-        for (int jj = 0; jj < DPL; ++jj) ck[(t / CK) * D + jj] = make_float2(zr[jj], zi[jj]);
-      }
-      float kk[DPL];
-      kb[i].unpack_then_reload(kk);
-      kb[i].load(kp + min(t + PF, tlast) * stride);
-      __builtin_amdgcn_sched_barrier(0);  // issue the reload here, not sunk below later tokens
-      const float ar = s0[i].x, ai = s0[i].y, bb = bbv[i];
-      const float bpr = bb * pv[i].x, bpi = bb * pv[i].y;
-      const float er = s0[i].z - (ar * bpr - ai * bpi);
-      const float ei = s0[i].w - (ar * bpi + ai * bpr);
-      const float ecr = bb * pv[i].z, eci = bb * pv[i].w;
-#pragma unroll
-      for (int jj = 0; jj < DPL; ++jj) {
-        const float nr = fmaf(ar, zr[jj], fmaf(-ai, zi[jj], er * kk[jj]));
-        const float ni = fmaf(ar, zi[jj], fmaf(ai, zr[jj], ei * kk[jj]));
-        zr[jj] = nr;
-        zi[jj] = ni;
-        cr[jj] = fmaf(-ecr, kk[jj], cr[jj]);
-        ci[jj] = fmaf(-eci, kk[jj], ci[jj]);
-      }
-    }
-  }
   __syncthreads();
 
   // ---- reverse pass ----
@@ -650,8 +605,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
       R.k[i].load(kp + min(tb + i, tlast) * stride);
       R.q[i].load(qp + min(tb + i, tlast) * stride);
     }
-#pragma unroll
-    for (int jj = 0; jj < DPL; ++jj) R.z0[jj] = ck[seg * D + jj];
+    load_zck<T, DPL>(zck, ck0 + int64_t(seg) * D, R.z0);
   };
   auto run_seg = [&](const SegBuf& R, int seg) {
     const int tb = seg * CK;
@@ -865,8 +819,8 @@ using namespace cdssm;
 
 struct BwdLayout {
   int NC, S;
-  int64_t n_lam, n_dsn, n_segA, n_segX, n_parts, n_ck;  // float2 counts
-  int64_t total() const { return n_lam + n_dsn + n_segA + n_segX + n_parts + n_ck; }
+  int64_t n_lam, n_dsn, n_segA, n_segX, n_parts;  // float2 counts
+  int64_t total() const { return n_lam + n_dsn + n_segA + n_segX + n_parts; }
 };
 
 BwdLayout bwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) {
@@ -878,9 +832,6 @@ BwdLayout bwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) 
   w.n_segA = B * H * w.S;
   w.n_segX = B * H * w.S * D;
   w.n_parts = B * w.NC * H;
-  // z checkpoints of the main pass: per (tile, head slot, segment) one D-vector
-  w.n_ck = B * w.NC * ((H + kBwdMaxHPW - 1) / kBwdMaxHPW) * kBwdMaxHPW *
-           (((chunk + kBwdPF - 1) / kBwdPF) * kBwdPF / kBwdCK) * D;
   return w;
 }
 
@@ -912,7 +863,8 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
   float2* segA = dsn + w.n_dsn;
   float2* segX = segA + w.n_segA;
   float2* parts = segX + w.n_segX;
-  float2* ckpt = parts + w.n_parts;
+  const float2* zck = states + fw.zck_offset();
+  const float2* cend = states + fw.cend_offset();
   const int slots = round_up(Q, kWave) * HPW, slots_c = round_up(Q, kWave) * HPWC;
 
   if (ev) (void)hipEventRecord(ev[0], stream);
@@ -936,8 +888,8 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
   hipLaunchKernelGGL((fused_bwd_main_kernel<T, D>), dim3(unsigned(tiles)), dim3(kWave),
                      size_t(slots) * 5 * sizeof(float4), stream, (const raw*)q, (const raw*)k, (const raw*)v,
                      (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c,
-                     (const raw*)dy, states, saved, (const float2*)dsn, ckpt, (raw*)dq, (raw*)dk, (raw*)dv,
-                     (raw*)dbeta, (raw*)dsel, (raw*)ddt, (raw*)dr, parts, L, H, Q, NC, n_hg);
+                     (const raw*)dy, states, saved, (const float2*)dsn, zck, cend, (raw*)dq, (raw*)dk, (raw*)dv,
+                     (raw*)dbeta, (raw*)dsel, (raw*)ddt, (raw*)dr, parts, L, H, Q, NC, fw.NCK, n_hg);
   st = cdssm_host::check_launch("cdssm_fused_scan_bwd/main");
   if (st) return st;
   if (ev) (void)hipEventRecord(ev[4], stream);

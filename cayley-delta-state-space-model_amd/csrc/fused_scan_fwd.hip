@@ -551,8 +551,9 @@ __global__ __launch_bounds__(256) void fused_fwd_replay_kernel(float2* __restric
 // SAVE (training forward): also keeps, per (token, head), the dot products the
 // backward needs, saved[2 e] = (p_t, pc_t), saved[2 e + 1] = (c^_{t+1}.q_t,
 // Y_t.q_t), with p_t = z_{t-1}.k_t in true units and pc_t = c^_t.k_t, so the
-// backward recomputes the chunk states without any reduction, and gsaved[e] =
-// g_t (the in-chunk decay product the correction adjoint needs).
+// backward recomputes the chunk states without any reduction, gsaved[e] =
+// g_t (the in-chunk decay product the correction adjoint needs), the z
+// checkpoints z_{t-1} at t % kZck == 0 and c^ after the chunk's last step.
 // ---------------------------------------------------------------------------
 template <typename T, int D, int LPH, bool SAVE>
 __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
@@ -561,10 +562,11 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
     const typename T::raw* __restrict__ sel_c, const typename T::raw* __restrict__ dt,
     const typename T::raw* __restrict__ r, const float* __restrict__ alpha,
     const float* __restrict__ omega, float c, const float2* __restrict__ states,
-    typename T::raw* __restrict__ y, float4* __restrict__ saved, float2* __restrict__ gsaved, int L, int H,
-    int Q, int NC, int n_hg) {
+    typename T::raw* __restrict__ y, float4* __restrict__ saved, float2* __restrict__ gsaved,
+    float2* __restrict__ zck, float2* __restrict__ cend, int L, int H, int Q, int NC, int NCK, int n_hg) {
   using Cfg = FusedCfg<T, D, LPH>;
   constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch;
+  static_assert(PF == kTokRound && PF % kZck == 0, "z checkpoints fall at fixed positions of a prefetch group");
   extern __shared__ float4 smem4[];
   const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
@@ -613,6 +615,8 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
 
   float fpr = 1.0f, fpi = 0.0f;  // frame f_{t-1}
   float4* svp = SAVE ? saved + 2 * ((tc.row0 * H) + (hok ? h : H - 1)) : nullptr;
+  const int64_t tile_h = (int64_t(tc.b) * NC + tc.chunk) * H + (hok ? h : H - 1);  // (b, chunk, h)
+  const int64_t zc0 = tile_h * NCK * D + sub * DPL;  // this lane's z checkpoint row, slot 0
 
   for (int tb = 0; tb < ntr; tb += PF) {
     float4 sa[PF], sb[PF];
@@ -627,6 +631,16 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int t = tb + i;
+      if (SAVE && i % kZck == 0 && hok) {
+        // z_{t-1} = f_{t-1} zh_{t-1}
+        float xr[DPL], xi[DPL];
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          xr[j] = fpr * zr[j] - fpi * zi[j];
+          xi[j] = fpr * zi[j] + fpi * zr[j];
+        }
+        store_zck<T, DPL>(zck, zc0 + (t / kZck) * D, xr, xi);
+      }
       float kk[DPL], qq[DPL];
       kb[i].unpack_then_reload(kk);
       qb[i].unpack_then_reload(qq);
@@ -686,6 +700,10 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
 #pragma unroll
       for (int i = 0; i < PF; ++i) s_y[(tb + i) * HPW + hh] = make_float2(yr[i], yi[i]);
     }
+  }
+  if (SAVE && hok) {
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) cend[tile_h * D + sub * DPL + j] = make_float2(cr[j], ci[j]);
   }
   __syncthreads();
 
@@ -773,8 +791,10 @@ struct OnePassArgs {
   float2* gam;     // SAVE: G_k (B, NC, H)
   float4* saved;   // SAVE: per-token records (B, L, H, 2)
   float2* gsaved;  // SAVE: g_t (B, L, H)
+  float2* zck;     // SAVE: z_{t-1} at t % kZck == 0 (B, NC, H, NCK, D)
+  float2* cend;    // SAVE: c^ after the chunk's last step (B, NC, H, D)
   unsigned long long epoch;
-  int L, H, Q, NC, NSEG, n_hg, n_chain, n_items;
+  int L, H, Q, NC, NSEG, NCK, n_hg, n_chain, n_items;
 };
 
 // One segment (work item): item = seg * n_chain + chain.
@@ -798,6 +818,8 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   float2* __restrict__ gam = a.gam;
   float4* __restrict__ saved = a.saved;
   float2* __restrict__ gsaved = a.gsaved;
+  float2* __restrict__ zck = a.zck;
+  float2* __restrict__ cend = a.cend;
   const unsigned long long epoch = a.epoch;
   const int L = a.L, H = a.H, Q = a.Q, NC = a.NC, NSEG = a.NSEG, n_hg = a.n_hg;
   using Cfg = FusedCfg<T, D, LPH>;
@@ -805,6 +827,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   constexpr int SEGN = HPW * D;  // complex elements of a head group's state
   constexpr int EPT = DPL / W;   // of which each thread of the workgroup composes EPT
   static_assert(EPT * W == DPL && EPT * kWave * W == SEGN, "segment state tiles the workgroup");
+  static_assert(PF == kTokRound && PF % kZck == 0, "z checkpoints fall at fixed positions of a prefetch group");
   extern __shared__ float4 smem4[];
 
   // wave index made wave-uniform, so the tile's fields live in scalar registers
@@ -873,6 +896,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
 
   const int64_t tile_h = (int64_t(bi) * NC + tc.chunk) * H + (hok ? h : H - 1);  // (b, chunk, h)
   float4* svp = SAVE ? saved + 2 * ((tc.row0 * H) + (hok ? h : H - 1)) : nullptr;
+  const int64_t zc0 = tile_h * a.NCK * D + sub * DPL;  // this lane's z checkpoint row, slot 0
 
   // 1. local recurrence with the local readout f_t (zh_t . q_t); in the last
   // PF steps the prefetch wraps to the first tokens, for the correction pass
@@ -892,6 +916,16 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
 #pragma unroll
       for (int i = 0; i < PF; ++i) {
         const int t = tb + i;
+        if (SAVE && i % kZck == 0 && hok) {
+          // z_{t-1} = f_{t-1} zh_{t-1}
+          float xr[DPL], xi[DPL];
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) {
+            xr[j] = fpr * zr[j] - fpi * zi[j];
+            xi[j] = fpr * zi[j] + fpi * zr[j];
+          }
+          store_zck<T, DPL>(zck, zc0 + (t / kZck) * D, xr, xi);
+        }
         float kk[DPL], qq[DPL];
         kb[i].unpack_then_reload(kk);
         qb[i].unpack_then_reload(qq);
@@ -1168,6 +1202,10 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
         for (int i = 0; i < PF; ++i) s_y[(tb + i) * HPW + hh] = make_float2(yr[i], yi[i]);
       }
     }
+    if (SAVE && hok) {
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) cend[tile_h * D + sub * DPL + j] = make_float2(cr[j], ci[j]);
+    }
   }
   __syncthreads();
 
@@ -1292,6 +1330,8 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   float2* segX = segA + w.n_segA;
   float4* saved = reinterpret_cast<float4*>(segX + w.n_segX + w.n_pad);
   float2* gsaved = reinterpret_cast<float2*>(ws) + w.gsaved_offset();
+  float2* zck = reinterpret_cast<float2*>(ws) + w.zck_offset();
+  float2* cend = reinterpret_cast<float2*>(ws) + w.cend_offset();
   const int slots = round_up(Q, kWave) * HPW, slots_s = round_up(Q, kWave) * HPWS;
 
   if (g_fwd_path.load(std::memory_order_relaxed) != kPathFour) {
@@ -1334,12 +1374,15 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
       a.gam = save ? gam : nullptr;
       a.saved = save ? saved : nullptr;
       a.gsaved = save ? gsaved : nullptr;
+      a.zck = save ? zck : nullptr;
+      a.cend = save ? cend : nullptr;
       a.epoch = next_epoch();
       a.L = L;
       a.H = H;
       a.Q = Q;
       a.NC = NC;
       a.NSEG = w.NSEG;
+      a.NCK = w.NCK;
       a.n_hg = n_hg;
       a.n_chain = B * n_hg;
       a.n_items = int(items);
@@ -1394,12 +1437,12 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
     hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH, true>), dim3(unsigned(tiles)), dim3(kWave), lds_main,
                        stream, (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,
                        (const raw*)dt, (const raw*)r, alpha, omega, c, (const float2*)summ, (raw*)y, saved,
-                       gsaved, L, H, Q, NC, n_hg);
+                       gsaved, zck, cend, L, H, Q, NC, w.NCK, n_hg);
   else
     hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH, false>), dim3(unsigned(tiles)), dim3(kWave), lds_main,
                        stream, (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,
                        (const raw*)dt, (const raw*)r, alpha, omega, c, (const float2*)summ, (raw*)y, nullptr,
-                       nullptr, L, H, Q, NC, n_hg);
+                       nullptr, nullptr, nullptr, L, H, Q, NC, w.NCK, n_hg);
   st = cdssm_host::check_launch("cdssm_fused_scan_fwd/main");
   if (ev) (void)hipEventRecord(ev[4], stream);
   return st;

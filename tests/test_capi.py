@@ -78,7 +78,10 @@ def test_workspace_size_formula():
         gsaved = B * L * H            # g_t per token-head: float2
         NSEG = -(-NC // 4)            # one-pass look-back segments of 4 chunks
         onepass = B * NSEG * H * (2 * D + 2)   # maps, leaving states, rotations, flags
-        return (carry + pad + saved + gsaved + onepass) * 8
+        NCK = -(-Q // 8) * 8 // 4     # z checkpoints per chunk (every 4 tokens of the 8-rounded loop)
+        zck = B * NC * H * NCK * D
+        cend = B * NC * H * D         # correction state after each chunk
+        return (carry + pad + saved + gsaved + onepass + zck + cend) * 8
     assert lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, N, Q) == expect(L)
     assert lib.cdssm_fused_scan_workspace_bytes(B, 100, H, D, N, Q) == expect(100)
     assert lib.cdssm_fused_scan_workspace_bytes(0, L, H, D, N, Q) == -1

@@ -131,7 +131,8 @@ def test_fused_bwd_full_c2_sequences_match_oracle():
 
 def test_one_pass_training_forward_writes_the_four_launch_records():
     """The training forward's workspace (entering state of every chunk, chunk
-    rotations, per-token records, g_t) is the backward's input: the one-pass
+    rotations, per-token records, g_t, z checkpoints, correction state at chunk
+    ends) is the backward's input: the one-pass
     kernel must leave the same values there as the four-launch scan (fp32,
     several look-back segments, ragged last chunk, h0)."""
     from cdssm_hip.scan import chunkwise_delta_scan_fwd
@@ -151,12 +152,24 @@ def test_one_pass_training_forward_writes_the_four_launch_records():
     n_states, n_gam = B * NC * H * D, B * NC * H
     carry = n_states + n_gam + B * H * S * (D + 1)
     off_saved = carry + (carry & 1)
+    NSEG, NCK = -(-NC // 4), -(-Q // 8) * 8 // 4
+    off_zck = off_saved + 5 * B * L * H + B * NSEG * H * (2 * D + 2)
+    n_zck = B * NC * H * NCK * D
     regions = {"states": (0, n_states), "gam": (n_states, n_states + n_gam),
                "saved": (off_saved, off_saved + 4 * B * L * H),
-               "gsaved": (off_saved + 4 * B * L * H, off_saved + 5 * B * L * H)}
+               "gsaved": (off_saved + 4 * B * L * H, off_saved + 5 * B * L * H),
+               "z checkpoints": (off_zck, off_zck + n_zck),
+               "c^ at chunk ends": (off_zck + n_zck, off_zck + n_zck + B * NC * H * D)}
     (y1, h1, w1), (y4, h4, w4) = outs["one_pass"], outs["four_launch"]
     assert rel(y1, y4) <= 1e-5 and rel(h1, h4) <= 1e-5
+    # checkpoint slots past a ragged last chunk's token loop are not written
+    nt_last = L - (NC - 1) * Q
+    ck_used = torch.ones(B, NC, H, NCK, D, 2, dtype=torch.bool)
+    ck_used[:, NC - 1, :, -(-nt_last // 8) * 8 // 4:] = False
     for name, (lo, hi) in regions.items():
-        e = rel(w1[lo:hi], w4[lo:hi])
+        a1, a4 = w1[lo:hi], w4[lo:hi]
+        if name == "z checkpoints":
+            a1, a4 = a1.reshape(ck_used.shape)[ck_used], a4.reshape(ck_used.shape)[ck_used]
+        e = rel(a1, a4)
         log(f"   {name}: rel diff {e:.1e}")
         assert e <= 1e-5, name
