@@ -108,18 +108,25 @@ def time_fwd_bwd(cfg_name, steps, warmup):
         fwd()
         bwd()
     torch.cuda.synchronize()
-    e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-    tf = tb = 0.0
-    for _ in range(steps):
-        e[0].record(stream)
-        fwd()
-        e[1].record(stream)
-        bwd()
-        e[2].record(stream)
+
+    def timed(fn):
+        # `steps` back-to-back calls between two events on the launch stream
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        tf += e[0].elapsed_time(e[1])
-        tb += e[1].elapsed_time(e[2])
-    ms = (tf + tb) / steps
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    def step():
+        fwd()
+        bwd()
+    ms = timed(step) / steps
+    tf = timed(fwd)
+    fwd()  # the backward reads this forward's workspace
+    tb = timed(bwd)
     by = scan_bytes(cfg, backward=True)
     alg = by["fwd"] + by["bwd"]
     fwd()

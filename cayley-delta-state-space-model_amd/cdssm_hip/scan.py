@@ -102,11 +102,12 @@ FORWARD_PATHS = {"auto": 0, "four_launch": 1, "one_pass": 2}
 def set_forward_path(path: str) -> str:
     """Select how the inference forward is launched; returns the previous setting.
 
-    "auto" (default) takes the one-pass kernel wherever its whole grid is
-    resident at once and a sequence has at most 64 segments of 4 chunks, else
-    the four-launch scan; "four_launch" always takes the four-launch scan;
-    "one_pass" requires the one-pass kernel (calls it cannot serve raise).
-    Process-wide; applies to the inference and the training forward alike.
+    "auto" (default) takes the one-pass forward where one round of resident
+    workgroups holds every segment of 4 chunks (and, for inference, where the
+    persistent one-pass fills whole rounds), else the four-launch scan;
+    "four_launch" always takes the multi-launch passes; "one_pass" requires
+    the one-launch passes (calls they cannot serve raise).  Process-wide; the
+    same choice applies to the backward's correction adjoint + reverse carry.
     """
     if path not in FORWARD_PATHS:
         raise ValueError(f"path must be one of {sorted(FORWARD_PATHS)}, got {path!r}")

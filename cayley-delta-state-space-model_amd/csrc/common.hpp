@@ -313,6 +313,36 @@ __device__ __forceinline__ Transition cayley_gated(float dt, float r, float alph
   return o;
 }
 
+// ---------------------------------------------------------------------------
+// Segment look-back between the workgroups of a one-launch pass.
+// ---------------------------------------------------------------------------
+constexpr int kLookbackBatch = 8;
+constexpr int kAnchor = 63;  // segments folded from one anchor state (<= 63: one watch window)
+constexpr uint64_t kSpinTicks = 5000000;  // look-back wait bound: 50 ms of the 100 MHz real-time counter
+
+// Look-back area of a one-launch pass: per (b, segment, head) a map (D
+// complex + one complex scalar), a state (D complex) and an 8-byte flag.
+struct OnePassBufs {
+  float2* seg_f;             // (B, NSEG, H, D) segment map F: state at the segment's end from zero
+  float2* seg_s;             // (B, NSEG, H, D) state leaving the segment
+  float2* seg_g;             // (B, NSEG, H)    segment rotation product
+  unsigned long long* flag;  // (B, NSEG, H); entry hbase serves the head group
+};
+
+// Wait until this wave's earlier stores are acknowledged; also a compiler
+// barrier, so no memory access moves across it.
+__device__ __forceinline__ void wait_stores_acked() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ void st_agent(float2* p, float2 v) {
+  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), __builtin_bit_cast(unsigned long long, v),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 ld_agent(const float2* p) {
+  const unsigned long long x = __hip_atomic_load(
+      reinterpret_cast<unsigned long long*>(const_cast<float2*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __builtin_bit_cast(float2, x);
+}
+
 }  // namespace cdssm
 
 // ---------------------------------------------------------------------------
@@ -322,6 +352,16 @@ __device__ __forceinline__ Transition cayley_gated(float dt, float r, float alph
 namespace cdssm_host {
 void set_error(const char* fmt, ...);
 int check_launch(const char* op);
+// Look-back epochs: distinct per call and process (62 bits, never 0), started
+// from a clock-mixed value so flag words left in a reused buffer never match.
+unsigned long long next_epoch();
+// Workgroups of kernel `fn` (block threads, lds bytes of dynamic LDS) resident
+// on the current device at once; 0 if it cannot run.  Cached.
+int resident_capacity(const void* fn, int block, size_t lds);
+// Launch-path selection of the fused scan (forward and backward carry):
+// automatic, always the multi-launch passes, or one launch required.
+enum { kPathAuto = 0, kPathFour = 1, kPathOne = 2 };
+int scan_path();
 }  // namespace cdssm_host
 
 // Status codes returned by every entry point.

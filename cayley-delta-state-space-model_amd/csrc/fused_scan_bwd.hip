@@ -93,7 +93,7 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
                                           const float4* __restrict__ saved = nullptr,
                                           float4* __restrict__ sP = nullptr, float4* __restrict__ sG = nullptr) {
   constexpr int NB = kWave / HPW, TPB = HPW;
-  const int lane = threadIdx.x;
+  const int lane = int(threadIdx.x) % kWave;  // lane in the wave (one-launch workgroups have several)
   const int j = lane / NB;
   const int blk = lane % NB;
   const int hj = tc.hbase + j;
@@ -195,7 +195,7 @@ __device__ __forceinline__ void stage_corr(const ChunkTile& tc, int H, int ntr,
                                            const typename T::raw* __restrict__ dy,
                                            const float2* __restrict__ gsaved, const BwdScalars& s) {
   constexpr int NB = kWave / HPW, TPB = HPW;
-  const int lane = threadIdx.x;
+  const int lane = int(threadIdx.x) % kWave;  // lane in the wave (one-launch workgroups have several)
   const int j = lane / NB;
   const int blk = lane % NB;
   const int hj = tc.hbase + j;
@@ -442,6 +442,297 @@ __global__ __launch_bounds__(256) void fused_bwd_rreplay_kernel(
   if (x.seg == 0 && dh0 != nullptr) {
     dh0[hb + x.d] = ds.x;
     dh0[hb + D + x.d] = ds.y;
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// B1 + B2 in one launch (when one round of resident workgroups holds every
+// segment).  A workgroup of kOnePassW waves takes kOnePassW consecutive chunks
+// (a segment) of one (b, head group), segments taken from the last: wave w
+// runs B1 for chunk kOnePassW * seg + w; the segment's reverse map
+// d s_{k0} = A d s_{k0+n} + X (A = prod conj(G_k), X from the chunks' lambda_0)
+// is composed through LDS and published; the carry adjoint at the segment's
+// right end is the composition, in a fixed order, of the maps of the segments
+// since its anchor (kAnchor segments, counted from the right) applied to the
+// anchor state (d h_final, or the published left-end state of the segment
+// right of the anchor); each wave then writes d s_{k+1} of its chunk, and the
+// first segment writes d h0.  Flags and ordering as in the one-pass forward.
+// ---------------------------------------------------------------------------
+template <typename T>
+struct CorrCarryArgs {
+  const typename T::raw *q, *k, *beta, *sel_c, *dy;
+  const float2* gsaved;   // the training forward's g_t (B, L, H)
+  const float2* gam;      // the training forward's G_k (B, NC, H)
+  const float* dh_final;  // (B, H, 2, D) or null
+  float2* dsn;            // out: d s_{k+1} per chunk (B, NC, H, D)
+  float* dh0;             // out: (B, H, 2, D) or null
+  OnePassBufs ob;         // X in seg_f, A in seg_g, left-end states in seg_s
+  unsigned long long epoch;
+  int L, H, Q, NC, NSEG, n_hg, n_chain;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(CorrCarryArgs<T> a) {
+  constexpr int LPH = BwdCorrCfg<D>::LPH, HPW = BwdCorrCfg<D>::HPW, DPL = BwdCorrCfg<D>::DPL, PF = kBwdCorrPF;
+  constexpr int W = kOnePassW;
+  constexpr int SEGN = HPW * D;             // complex elements of a head group's state
+  constexpr int EPT = SEGN / (kWave * W);   // composed by each thread of the workgroup
+  static_assert(EPT >= 1 && EPT * kWave * W == SEGN && D % EPT == 0, "segment state tiles the workgroup");
+  extern __shared__ float4 smem4[];
+  const int L = a.L, H = a.H, Q = a.Q, NC = a.NC, NSEG = a.NSEG;
+  const unsigned long long epoch = a.epoch;
+
+  const int wv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+  const int lane = int(threadIdx.x) % kWave;
+  const int chain = int(blockIdx.x) % a.n_chain;
+  const int rs = int(blockIdx.x) / a.n_chain;  // segments counted from the right
+  const int seg = NSEG - 1 - rs;
+  const int bi = chain / a.n_hg;
+  const int hbase = (chain % a.n_hg) * HPW;
+  const int n_live = min(W, NC - seg * W);
+  const bool live = wv < n_live;
+
+  ChunkTile tc;
+  tc.b = bi;
+  tc.chunk = min(seg * W + wv, NC - 1);
+  tc.hbase = hbase;
+  tc.t0 = tc.chunk * Q;
+  tc.nt = min(Q, L - tc.t0);
+  tc.row0 = int64_t(bi) * L + tc.t0;
+  const int hh = lane / LPH, sub = lane % LPH;
+  const int h = hbase + hh;
+  const bool hok = h < H;
+  const int hl = hok ? h : H - 1;
+  const int slots = round_up(Q, kWave) * HPW;
+  const int ntr = round_up(tc.nt, PF);
+
+  // LDS: per wave S1, S2 (float4 token slots), which after the wave's lambda
+  // pass hold its lambda_0 (SEGN float2 <= 2 * slots float4); G per (wave,
+  // head); the carry adjoint at the segment's right end
+  BwdScalars s{nullptr, smem4 + size_t(wv) * 2 * slots, smem4 + size_t(wv) * 2 * slots + slots};
+  auto Lw = [&](int u) { return reinterpret_cast<float2*>(smem4 + size_t(u) * 2 * slots); };
+  float2* Gx = reinterpret_cast<float2*>(smem4 + size_t(W) * 2 * slots);
+  float2* Sx = Gx + W * HPW;
+  int* ctrl = reinterpret_cast<int*>(Sx + SEGN);
+
+  // ---- B1 for this wave's chunk: lambda backward through the chunk ----
+  float lr[DPL], li[DPL];
+#pragma unroll
+  for (int jj = 0; jj < DPL; ++jj) lr[jj] = li[jj] = 0.0f;
+  const int64_t stride = int64_t(H) * D;
+  const int64_t off = (tc.row0 * H + hl) * D + sub * DPL;
+  const typename T::raw* kp = a.k + off;
+  const typename T::raw* qp = a.q + off;
+  const int tlast = tc.nt - 1;
+  RowVec<T, DPL> kb[PF], qb[PF];
+  if (live) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      kb[i].load(kp + min(ntr - 1 - i, tlast) * stride);
+      qb[i].load(qp + min(ntr - 1 - i, tlast) * stride);
+    }
+    stage_corr<T, HPW>(tc, H, ntr, a.beta, a.sel_c, a.dy, a.gsaved, s);
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      kb[i].pin();
+      qb[i].pin();
+    }
+  }
+  __syncthreads();  // every wave reaches every barrier of this kernel
+  if (live) {
+    for (int tb = 0; tb < ntr; tb += PF) {
+      float4 s1[PF], s2[PF];
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        const int p = (ntr - 1 - (tb + i)) * HPW + hh;
+        s1[i] = s.S1[p];
+        s2[i] = s.S2[p];
+      }
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        const int t = ntr - 1 - (tb + i);
+        float kk[DPL], qq[DPL];
+        kb[i].unpack_then_reload(kk);
+        qb[i].unpack_then_reload(qq);
+        kb[i].load(kp + max(min(t - PF, tlast), 0) * stride);
+        qb[i].load(qp + max(min(t - PF, tlast), 0) * stride);
+        __builtin_amdgcn_sched_barrier(0);
+        float sr = 0.0f, si = 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < DPL; ++jj) {
+          lr[jj] = fmaf(s2[i].x, qq[jj], lr[jj]);
+          li[jj] = fmaf(s2[i].y, qq[jj], li[jj]);
+          sr = fmaf(lr[jj], kk[jj], sr);
+          si = fmaf(li[jj], kk[jj], si);
+        }
+        sr = group_sum<LPH>(sr);
+        si = group_sum<LPH>(si);
+        const float br = s1[i].x * sr, bi2 = s1[i].x * si;
+#pragma unroll
+        for (int jj = 0; jj < DPL; ++jj) {
+          lr[jj] = fmaf(-br, kk[jj], lr[jj]);
+          li[jj] = fmaf(-bi2, kk[jj], li[jj]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      kb[i].pin();
+      qb[i].pin();
+    }
+    // lambda_0 and G_k of the chunk (heads >= H: zero map)
+#pragma unroll
+    for (int jj = 0; jj < DPL; ++jj)
+      Lw(wv)[hh * D + sub * DPL + jj] = hok ? make_float2(lr[jj], li[jj]) : make_float2(0.0f, 0.0f);
+    if (sub == 0)
+      Gx[wv * HPW + hh] = hok ? a.gam[(int64_t(bi) * NC + tc.chunk) * H + h] : make_float2(1.0f, 0.0f);
+  }
+  __syncthreads();
+
+  // ---- the segment's reverse map over its live chunks ----
+  const int e0 = int(threadIdx.x) * EPT;
+  const int ej = e0 / D, ed = e0 % D;
+  const int eh = hbase + ej;
+  const bool ehok = eh < H;
+  float2 X[EPT];
+  float2 A = make_float2(1.0f, 0.0f);
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) X[i] = make_float2(0.0f, 0.0f);
+  for (int u = n_live - 1; u >= 0; --u) {
+    const float2 g = Gx[u * HPW + ej];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const float2 l = Lw(u)[e0 + i];
+      X[i] = make_float2(g.x * X[i].x + g.y * X[i].y + l.x, g.x * X[i].y - g.y * X[i].x + l.y);
+    }
+    A = make_float2(g.x * A.x + g.y * A.y, g.x * A.y - g.y * A.x);
+  }
+  const OnePassBufs& ob = a.ob;
+  const int64_t sb0 = (int64_t(bi) * NSEG + seg) * H;  // (b, seg, head 0)
+  unsigned long long* flag = ob.flag + sb0 + hbase;
+  if (ehok) {
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) st_agent(ob.seg_f + (sb0 + eh) * D + ed + i, X[i]);
+    if (ed == 0) st_agent(ob.seg_g + sb0 + eh, A);
+  }
+  wait_stores_acked();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_store(flag, (epoch << 2) | 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // ---- carry adjoint at the segment's right end, from its anchor ----
+  const int anc = rs == 0 ? 0 : kAnchor * ((rs - 1) / kAnchor);  // counted from the right
+  const int nmap = rs - anc;
+  int ok = 1;
+  if (rs > 0) {
+    if (wv == 0) {
+      const unsigned long long* f0 = ob.flag + (int64_t(bi) * NSEG) * H + hbase;
+      int got = 0;
+      const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
+      for (;;) {
+        int st = 3;
+        // lane i: map of the segment anc + i from the right; lane 63: the anchor state
+        const int jr = lane < nmap ? anc + lane : (lane == kWave - 1 && anc > 0 ? anc - 1 : -1);
+        if (jr >= 0) {
+          const unsigned long long fv =
+              __hip_atomic_load(const_cast<unsigned long long*>(f0 + int64_t(NSEG - 1 - jr) * H), __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+          st = (fv >> 2) == epoch ? int(fv & 3ull) : 0;
+        }
+        const bool ready = lane < nmap ? st >= 1 : (lane == kWave - 1 && anc > 0 ? st == 2 : true);
+        if (__builtin_amdgcn_ballot_w64(!ready) == 0ull) {
+          got = 1;
+          break;
+        }
+        if (__builtin_amdgcn_s_memrealtime() - t_start > kSpinTicks) break;
+        __builtin_amdgcn_s_sleep(2);
+      }
+      if (lane == 0) ctrl[0] = got;
+    }
+    __syncthreads();
+    ok = ctrl[0];
+  }
+  float2 Sin[EPT];
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) Sin[i] = make_float2(0.0f, 0.0f);
+  if (ehok) {
+    const int64_t lb = int64_t(bi) * NSEG * H + eh;  // (b, segment 0, head eh)
+    if (anc == 0) {
+      if (a.dh_final) {
+        const int64_t hb = (int64_t(bi) * H + eh) * 2 * D;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) Sin[i] = make_float2(a.dh_final[hb + ed + i], a.dh_final[hb + D + ed + i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < EPT; ++i)
+        Sin[i] = ld_agent(ob.seg_s + (lb + int64_t(NSEG - anc) * H) * D + ed + i);
+    }
+    for (int jb = 0; jb < nmap; jb += kLookbackBatch) {
+      float2 G[kLookbackBatch], F[kLookbackBatch][EPT];
+#pragma unroll
+      for (int u = 0; u < kLookbackBatch; ++u) {
+        const int js = NSEG - 1 - (anc + min(jb + u, nmap - 1));
+        G[u] = ld_agent(ob.seg_g + lb + int64_t(js) * H);
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) F[u][i] = ld_agent(ob.seg_f + (lb + int64_t(js) * H) * D + ed + i);
+      }
+#pragma unroll
+      for (int u = 0; u < kLookbackBatch; ++u) {
+        if (jb + u < nmap) {
+#pragma unroll
+          for (int i = 0; i < EPT; ++i)
+            Sin[i] = make_float2(G[u].x * Sin[i].x - G[u].y * Sin[i].y + F[u][i].x,
+                                 G[u].x * Sin[i].y + G[u].y * Sin[i].x + F[u][i].y);
+        }
+      }
+    }
+    if (!ok) {
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) Sin[i] = make_float2(__builtin_nanf(""), __builtin_nanf(""));
+    }
+  }
+  // the segment's left-end state: published for the segments that start from
+  // it, and d h0 for the first segment
+  const bool anchor_end = rs + 1 < NSEG && (rs + 1) % kAnchor == 0;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) Sx[e0 + i] = Sin[i];
+  if (ehok && (anchor_end || (seg == 0 && a.dh0))) {
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const float2 so = make_float2(A.x * Sin[i].x - A.y * Sin[i].y + X[i].x, A.x * Sin[i].y + A.y * Sin[i].x + X[i].y);
+      if (anchor_end) {
+        st_agent(ob.seg_s + (sb0 + eh) * D + ed + i, so);
+      } else {
+        const int64_t hb = (int64_t(bi) * H + eh) * 2 * D;
+        a.dh0[hb + ed + i] = so.x;
+        a.dh0[hb + D + ed + i] = so.y;
+      }
+    }
+  }
+  if (anchor_end) wait_stores_acked();
+  __syncthreads();
+  if (anchor_end && threadIdx.x == 0)
+    __hip_atomic_store(flag, (epoch << 2) | 2ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // ---- d s_{k+1} of this wave's chunk: the maps of the later chunks of the
+  // segment applied to the right-end state ----
+  if (live && hok) {
+    float2 acc[DPL];
+#pragma unroll
+    for (int jj = 0; jj < DPL; ++jj) acc[jj] = Sx[hh * D + sub * DPL + jj];
+    for (int u = n_live - 1; u > wv; --u) {
+      const float2 g = Gx[u * HPW + hh];
+#pragma unroll
+      for (int jj = 0; jj < DPL; ++jj) {
+        const float2 l = Lw(u)[hh * D + sub * DPL + jj];
+        acc[jj] = make_float2(g.x * acc[jj].x + g.y * acc[jj].y + l.x, g.x * acc[jj].y - g.y * acc[jj].x + l.y);
+      }
+    }
+    float2* dp = a.dsn + ((int64_t(bi) * NC + tc.chunk) * H + h) * D + sub * DPL;
+#pragma unroll
+    for (int jj = 0; jj < DPL; ++jj) dp[jj] = acc[jj];
   }
 }
 
@@ -818,9 +1109,9 @@ namespace {
 using namespace cdssm;
 
 struct BwdLayout {
-  int NC, S;
-  int64_t n_lam, n_dsn, n_segA, n_segX, n_parts;  // float2 counts
-  int64_t total() const { return n_lam + n_dsn + n_segA + n_segX + n_parts; }
+  int NC, S, NSEG;
+  int64_t n_lam, n_dsn, n_segA, n_segX, n_parts, n_cc;  // float2 counts
+  int64_t total() const { return n_lam + n_dsn + n_segA + n_segX + n_parts + n_cc; }
 };
 
 BwdLayout bwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) {
@@ -832,6 +1123,10 @@ BwdLayout bwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) 
   w.n_segA = B * H * w.S;
   w.n_segX = B * H * w.S * D;
   w.n_parts = B * w.NC * H;
+  // one-launch correction adjoint + reverse carry: look-back area per (b,
+  // segment of kOnePassW chunks, h): map X (D), left-end state (D), A, flag
+  w.NSEG = (w.NC + kOnePassW - 1) / kOnePassW;
+  w.n_cc = B * w.NSEG * H * (2 * D + 2);
   return w;
 }
 
@@ -841,7 +1136,7 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
                      const void* dy, const float* dh_final, const float* fwd_ws, void* dq, void* dk,
                      void* dv, void* dbeta, void* dsel, void* ddt, void* dr, float* dalpha,
                      float* domega, float* dh0, float* ws, int B, int L, int H, int Q,
-                     hipStream_t stream, hipEvent_t* ev) {
+                     hipStream_t stream, hipEvent_t* ev, int* carry_fused) {
   using raw = typename T::raw;
   const BwdLayout w = bwd_layout(B, L, H, D, Q);
   const int NC = w.NC, S = w.S;
@@ -867,24 +1162,76 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
   const float2* cend = states + fw.cend_offset();
   const int slots = round_up(Q, kWave) * HPW, slots_c = round_up(Q, kWave) * HPWC;
 
-  if (ev) (void)hipEventRecord(ev[0], stream);
-  hipLaunchKernelGGL((fused_bwd_corr_kernel<T, D>), dim3(unsigned(tiles_c)), dim3(kWave),
-                     size_t(slots_c) * 2 * sizeof(float4), stream, (const raw*)q, (const raw*)k,
-                     (const raw*)beta, (const raw*)sel_c, (const raw*)dy, gsaved, lam0, L, H, Q, NC, n_hgc);
-  int st = cdssm_host::check_launch("cdssm_fused_scan_bwd/corr");
-  if (st) return st;
-  if (ev) (void)hipEventRecord(ev[1], stream);
-  const unsigned cblocks = unsigned((carry_threads + 255) / 256);
-  hipLaunchKernelGGL(fused_bwd_rfold_kernel, dim3(cblocks), dim3(256), 0, stream, (const float2*)lam0,
-                     gam, segA, segX, B, NC, H, D, S);
-  st = cdssm_host::check_launch("cdssm_fused_scan_bwd/rfold");
-  if (st) return st;
-  if (ev) (void)hipEventRecord(ev[2], stream);
-  hipLaunchKernelGGL(fused_bwd_rreplay_kernel, dim3(cblocks), dim3(256), 0, stream, (const float2*)lam0,
-                     gam, (const float2*)segA, (const float2*)segX, dh_final, dsn, dh0, B, NC, H, D, S);
-  st = cdssm_host::check_launch("cdssm_fused_scan_bwd/rreplay");
-  if (st) return st;
-  if (ev) (void)hipEventRecord(ev[3], stream);
+  // correction adjoint + reverse carry: one launch when one round of resident
+  // workgroups holds every segment, else three (B1, fold, replay)
+  int st = CDSSM_OK;
+  bool fused = false;
+  if (cdssm_host::scan_path() != cdssm_host::kPathFour) {
+    constexpr int SEGN = HPWC * D;
+    const int64_t items = int64_t(w.NSEG) * B * n_hgc;
+    static_assert(SEGN * sizeof(float2) <= 2 * kWave * HPWC * sizeof(float4), "lambda_0 fits a wave's slots");
+    const size_t lds = size_t(kOnePassW) * 2 * slots_c * sizeof(float4) + size_t(kOnePassW) * HPWC * sizeof(float2) +
+                       size_t(SEGN) * sizeof(float2) + 16;
+    const int cap = cdssm_host::resident_capacity(reinterpret_cast<const void*>(&fused_bwd_corrcarry_kernel<T, D>),
+                                                  kWave * kOnePassW, lds);
+    if (cap > 0 && items <= cap) {
+      float2* base = parts + w.n_parts;
+      const int64_t nsd = int64_t(B) * w.NSEG * H * D, nsh = int64_t(B) * w.NSEG * H;
+      CorrCarryArgs<T> a;
+      a.q = (const raw*)q;
+      a.k = (const raw*)k;
+      a.beta = (const raw*)beta;
+      a.sel_c = (const raw*)sel_c;
+      a.dy = (const raw*)dy;
+      a.gsaved = gsaved;
+      a.gam = gam;
+      a.dh_final = dh_final;
+      a.dsn = dsn;
+      a.dh0 = dh0;
+      a.ob = OnePassBufs{base, base + nsd, base + 2 * nsd, reinterpret_cast<unsigned long long*>(base + 2 * nsd + nsh)};
+      a.epoch = cdssm_host::next_epoch();
+      a.L = L;
+      a.H = H;
+      a.Q = Q;
+      a.NC = NC;
+      a.NSEG = w.NSEG;
+      a.n_hg = n_hgc;
+      a.n_chain = B * n_hgc;
+      if (ev) (void)hipEventRecord(ev[0], stream);
+      hipLaunchKernelGGL((fused_bwd_corrcarry_kernel<T, D>), dim3(unsigned(items)), dim3(kWave * kOnePassW), lds,
+                         stream, a);
+      st = cdssm_host::check_launch("cdssm_fused_scan_bwd/corrcarry");
+      if (st) return st;
+      if (ev)
+        for (int i = 1; i < 4; ++i) (void)hipEventRecord(ev[i], stream);
+      fused = true;
+    } else if (cdssm_host::scan_path() == cdssm_host::kPathOne) {
+      cdssm_host::set_error("cdssm_fused_scan_bwd: one-launch carry required but %lld segments exceed the %d "
+                            "resident workgroups", (long long)items, cap);
+      return CDSSM_EINVAL;
+    }
+  }
+  if (carry_fused) *carry_fused = fused;
+  if (!fused) {
+    if (ev) (void)hipEventRecord(ev[0], stream);
+    hipLaunchKernelGGL((fused_bwd_corr_kernel<T, D>), dim3(unsigned(tiles_c)), dim3(kWave),
+                       size_t(slots_c) * 2 * sizeof(float4), stream, (const raw*)q, (const raw*)k,
+                       (const raw*)beta, (const raw*)sel_c, (const raw*)dy, gsaved, lam0, L, H, Q, NC, n_hgc);
+    st = cdssm_host::check_launch("cdssm_fused_scan_bwd/corr");
+    if (st) return st;
+    if (ev) (void)hipEventRecord(ev[1], stream);
+    const unsigned cblocks = unsigned((carry_threads + 255) / 256);
+    hipLaunchKernelGGL(fused_bwd_rfold_kernel, dim3(cblocks), dim3(256), 0, stream, (const float2*)lam0,
+                       gam, segA, segX, B, NC, H, D, S);
+    st = cdssm_host::check_launch("cdssm_fused_scan_bwd/rfold");
+    if (st) return st;
+    if (ev) (void)hipEventRecord(ev[2], stream);
+    hipLaunchKernelGGL(fused_bwd_rreplay_kernel, dim3(cblocks), dim3(256), 0, stream, (const float2*)lam0,
+                       gam, (const float2*)segA, (const float2*)segX, dh_final, dsn, dh0, B, NC, H, D, S);
+    st = cdssm_host::check_launch("cdssm_fused_scan_bwd/rreplay");
+    if (st) return st;
+    if (ev) (void)hipEventRecord(ev[3], stream);
+  }
   hipLaunchKernelGGL((fused_bwd_main_kernel<T, D>), dim3(unsigned(tiles)), dim3(kWave),
                      size_t(slots) * 5 * sizeof(float4), stream, (const raw*)q, (const raw*)k, (const raw*)v,
                      (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c,
@@ -915,7 +1262,7 @@ int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, cons
                     const float* fwd_workspace, void* dq, void* dk, void* dv, void* dbeta, void* dsel,
                     void* ddt, void* dr, float* dalpha, float* domega, float* dh0, float* workspace,
                     int64_t B, int64_t L, int64_t H, int64_t D, int64_t N, int64_t chunk,
-                    hipStream_t stream, hipEvent_t* ev) {
+                    hipStream_t stream, hipEvent_t* ev, int* carry_fused = nullptr) {
   const char* op = "cdssm_fused_scan_bwd";
   if (dtype != 0 && dtype != 1) {
     cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
@@ -951,18 +1298,18 @@ int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, cons
     if (D == 64)
       return launch_fused_bwd<BF16, 64>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final,
                                         fwd_workspace, dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega,
-                                        dh0, workspace, b, l, hh, qc, stream, ev);
+                                        dh0, workspace, b, l, hh, qc, stream, ev, carry_fused);
     return launch_fused_bwd<BF16, 128>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final,
                                        fwd_workspace, dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega,
-                                       dh0, workspace, b, l, hh, qc, stream, ev);
+                                       dh0, workspace, b, l, hh, qc, stream, ev, carry_fused);
   }
   if (D == 64)
     return launch_fused_bwd<F32, 64>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final,
                                      fwd_workspace, dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0,
-                                     workspace, b, l, hh, qc, stream, ev);
+                                     workspace, b, l, hh, qc, stream, ev, carry_fused);
   return launch_fused_bwd<F32, 128>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final,
                                     fwd_workspace, dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0,
-                                    workspace, b, l, hh, qc, stream, ev);
+                                    workspace, b, l, hh, qc, stream, ev, carry_fused);
 }
 }  // namespace
 
@@ -1002,9 +1349,10 @@ extern "C" int cdssm_fused_scan_bwd_profile(int dtype, const void* q, const void
   for (int p = 0; p < 5; ++p) phase_ms[p] = 0.0f;
   int st = CDSSM_OK;
   for (int it = 0; it < iters; ++it) {
+    int fusedc = 0;
     st = fused_bwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final, fwd_workspace,
                          dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0, workspace, B, L, H, D, N,
-                         chunk, stream, ev);
+                         chunk, stream, ev, &fusedc);
     if (st != CDSSM_OK) break;
     if (hipEventSynchronize(ev[5]) != hipSuccess) {
       cdssm_host::set_error("cdssm_fused_scan_bwd_profile: hipEventSynchronize failed");
@@ -1012,6 +1360,8 @@ extern "C" int cdssm_fused_scan_bwd_profile(int dtype, const void* q, const void
       break;
     }
     for (int p = 0; p < 5; ++p) {
+      // a one-launch correction adjoint + carry is reported as the first phase
+      if (fusedc && (p == 1 || p == 2)) continue;
       float ms = 0.0f;
       (void)hipEventElapsedTime(&ms, ev[p], ev[p + 1]);
       phase_ms[p] += ms / float(iters);

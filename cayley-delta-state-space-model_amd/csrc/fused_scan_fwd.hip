@@ -40,8 +40,6 @@
 // count only the oldest load.  Tokens past the end of a ragged last chunk are
 // inert steps (a = 1, w = 0, beta = 0).
 #include <atomic>
-#include <chrono>
-#include <mutex>
 
 #include "common.hpp"
 
@@ -753,31 +751,6 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
 // per segment, or fewer that take the segments in order), and a bounded wait
 // turns a missing flag into NaN output instead of a hang.
 // ---------------------------------------------------------------------------
-constexpr int kLookbackBatch = 8;
-constexpr int kAnchor = 63;  // segments folded from one anchor state (<= 63: one watch window)
-constexpr uint64_t kSpinTicks = 5000000;  // look-back wait bound: 50 ms of the 100 MHz real-time counter
-
-struct OnePassBufs {
-  float2* seg_f;             // (B, NSEG, H, D) segment map F: state at the segment's end from zero
-  float2* seg_s;             // (B, NSEG, H, D) state leaving the segment
-  float2* seg_g;             // (B, NSEG, H)    segment rotation product
-  unsigned long long* flag;  // (B, NSEG, H); entry hbase serves the head group
-};
-
-// Wait until this wave's earlier stores are acknowledged; also a compiler
-// barrier, so no memory access moves across it.
-__device__ __forceinline__ void wait_stores_acked() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-__device__ __forceinline__ void st_agent(float2* p, float2 v) {
-  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), __builtin_bit_cast(unsigned long long, v),
-                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float2 ld_agent(const float2* p) {
-  const unsigned long long x = __hip_atomic_load(
-      reinterpret_cast<unsigned long long*>(const_cast<float2*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return __builtin_bit_cast(float2, x);
-}
-
 template <typename T>
 struct OnePassArgs {
   const typename T::raw *q, *k, *v, *beta, *sel_c, *dt, *r;
@@ -1250,22 +1223,6 @@ namespace {
 
 using namespace cdssm;
 
-// Forward path selection: auto (one-pass where it applies), always four
-// launches, or one-pass required (calls it cannot serve fail).
-enum { kPathAuto = 0, kPathFour = 1, kPathOne = 2 };
-std::atomic<int> g_fwd_path{kPathAuto};
-
-// Look-back epochs: distinct per call and process, started from a clock-mixed
-// value so flag words left in a reused buffer never match by accident.
-unsigned long long next_epoch() {
-  static std::atomic<unsigned long long> ctr{
-      (unsigned long long)(std::chrono::steady_clock::now().time_since_epoch().count()) * 0x9E3779B97F4A7C15ull};
-  unsigned long long e;
-  do {
-    e = ctr.fetch_add(1, std::memory_order_relaxed) & ((1ull << 62) - 1);
-  } while (e == 0);
-  return e;
-}
 
 template <int D, int LPH>
 size_t onepass_lds(int Q) {
@@ -1276,36 +1233,11 @@ size_t onepass_lds(int Q) {
 }
 
 // Workgroups of the one-pass kernel resident at once (its grid: a workgroup
-// may wait on any earlier segment), from the per-block LDS limit and the
-// occupancy x CUs; 0 if it cannot run.  Cached per device and LDS size.
+// may wait on any earlier segment); 0 if it cannot run.
 template <typename T, int D, int LPH, bool SAVE, bool PERSIST>
 int onepass_capacity(size_t lds) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  struct Entry {
-    int dev;
-    size_t lds;
-    int capacity;
-  };
-  static std::mutex mu;
-  static Entry cache[16];
-  static int n_cache = 0;
-  std::lock_guard<std::mutex> lock(mu);
-  for (int i = 0; i < n_cache; ++i)
-    if (cache[i].dev == dev && cache[i].lds == lds) return cache[i].capacity;
-  int max_lds = 0, n_cu = 0, per_cu = 0;
-  int capacity = 0;
-  const void* fn = reinterpret_cast<const void*>(&fused_fwd_onepass_kernel<T, D, LPH, SAVE, PERSIST>);
-  if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
-      hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-      lds <= size_t(max_lds)) {
-    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kWave * kOnePassW, lds) == hipSuccess)
-      capacity = per_cu * n_cu;
-  }
-  (void)hipGetLastError();
-  if (n_cache < 16) cache[n_cache++] = Entry{dev, lds, capacity};
-  return capacity;
+  return cdssm_host::resident_capacity(
+      reinterpret_cast<const void*>(&fused_fwd_onepass_kernel<T, D, LPH, SAVE, PERSIST>), kWave * kOnePassW, lds);
 }
 
 template <typename T, int D, int LPH, int LPHS>
@@ -1334,7 +1266,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   float2* cend = reinterpret_cast<float2*>(ws) + w.cend_offset();
   const int slots = round_up(Q, kWave) * HPW, slots_s = round_up(Q, kWave) * HPWS;
 
-  if (g_fwd_path.load(std::memory_order_relaxed) != kPathFour) {
+  if (cdssm_host::scan_path() != cdssm_host::kPathFour) {
     const int64_t items = int64_t(w.NSEG) * B * n_hg;
     const size_t lds = onepass_lds<D, LPH>(Q);
     // one round of resident workgroups takes every segment: one-pass.  More
@@ -1346,7 +1278,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
     const int capp = save ? onepass_capacity<T, D, LPH, true, true>(lds)
                           : onepass_capacity<T, D, LPH, false, true>(lds);
     const bool single = cap1 > 0 && items <= cap1;
-    const bool forced = g_fwd_path.load(std::memory_order_relaxed) == kPathOne;
+    const bool forced = cdssm_host::scan_path() == cdssm_host::kPathOne;
     const int64_t rounds = capp > 0 ? (items + capp - 1) / capp : 0;
     const bool persist = !single && capp > 0 && items <= 0x7fffffff &&
                          (forced || (!save && items * 10 >= rounds * capp * 9));
@@ -1376,7 +1308,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
       a.gsaved = save ? gsaved : nullptr;
       a.zck = save ? zck : nullptr;
       a.cend = save ? cend : nullptr;
-      a.epoch = next_epoch();
+      a.epoch = cdssm_host::next_epoch();
       a.L = L;
       a.H = H;
       a.Q = Q;
@@ -1386,7 +1318,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
       a.n_hg = n_hg;
       a.n_chain = B * n_hg;
       a.n_items = int(items);
-      if (path) *path = kPathOne;
+      if (path) *path = cdssm_host::kPathOne;
       if (ev)
         for (int i = 0; i < 4; ++i) (void)hipEventRecord(ev[i], stream);
       const dim3 gd = dim3(unsigned(grid)), bd = dim3(kWave * kOnePassW);
@@ -1409,7 +1341,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
     }
   }
 
-  if (path) *path = kPathFour;
+  if (path) *path = cdssm_host::kPathFour;
   if (ev) (void)hipEventRecord(ev[0], stream);
   hipLaunchKernelGGL((fused_fwd_summary_kernel<T, D, LPHS>), dim3(unsigned(tiles_s)), dim3(kWave),
                      size_t(slots_s) * (sizeof(float4) + sizeof(float2)) + HPWS * sizeof(float4), stream,
@@ -1556,7 +1488,7 @@ extern "C" int cdssm_fused_scan_fwd_profile(int dtype, const void* q, const void
   for (int p = 0; p < 4; ++p) phase_ms[p] = 0.0f;
   int st = CDSSM_OK;
   for (int it = 0; it < iters && st == CDSSM_OK; ++it) {
-    int path = kPathFour;
+    int path = cdssm_host::kPathFour;
     st = fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace, B,
                          L, H, D, N, chunk, stream, ev, train != 0, &path);
     if (st != CDSSM_OK) break;
@@ -1566,7 +1498,7 @@ extern "C" int cdssm_fused_scan_fwd_profile(int dtype, const void* q, const void
       break;
     }
     // a one-pass call is one launch: reported as the main pass, 0 for the others
-    for (int p = path == kPathOne ? 3 : 0; p < 4; ++p) {
+    for (int p = path == cdssm_host::kPathOne ? 3 : 0; p < 4; ++p) {
       float ms = 0.0f;
       (void)hipEventElapsedTime(&ms, ev[p], ev[p + 1]);
       phase_ms[p] += ms / float(iters);
@@ -1576,11 +1508,3 @@ extern "C" int cdssm_fused_scan_fwd_profile(int dtype, const void* q, const void
   return st;
 }
 
-extern "C" int cdssm_fused_scan_fwd_set_path(int mode) {
-  if (mode < kPathAuto || mode > kPathOne) {
-    cdssm_host::set_error("cdssm_fused_scan_fwd_set_path: mode must be 0 (auto), 1 (four launches) or 2 "
-                          "(one pass required), got %d", mode);
-    return CDSSM_EINVAL;
-  }
-  return g_fwd_path.exchange(mode);
-}

@@ -3,6 +3,10 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+#include <chrono>
+#include <mutex>
+
 #include "common.hpp"
 
 namespace {
@@ -27,7 +31,60 @@ int check_launch(const char* op) {
   return CDSSM_OK;
 }
 
+unsigned long long next_epoch() {
+  static std::atomic<unsigned long long> ctr{
+      (unsigned long long)(std::chrono::steady_clock::now().time_since_epoch().count()) * 0x9E3779B97F4A7C15ull};
+  unsigned long long e;
+  do {
+    e = ctr.fetch_add(1, std::memory_order_relaxed) & ((1ull << 62) - 1);
+  } while (e == 0);
+  return e;
+}
+
+int resident_capacity(const void* fn, int block, size_t lds) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  struct Entry {
+    const void* fn;
+    int dev, block;
+    size_t lds;
+    int capacity;
+  };
+  static std::mutex mu;
+  static Entry cache[64];
+  static int n_cache = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < n_cache; ++i)
+    if (cache[i].fn == fn && cache[i].dev == dev && cache[i].block == block && cache[i].lds == lds)
+      return cache[i].capacity;
+  int max_lds = 0, n_cu = 0, per_cu = 0, capacity = 0;
+  if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+      hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      lds <= size_t(max_lds)) {
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, block, lds) == hipSuccess) capacity = per_cu * n_cu;
+  }
+  (void)hipGetLastError();
+  if (n_cache < 64) cache[n_cache++] = Entry{fn, dev, block, lds, capacity};
+  return capacity;
+}
+
+namespace {
+std::atomic<int> g_scan_path{kPathAuto};
+}
+
+int scan_path() { return g_scan_path.load(std::memory_order_relaxed); }
+
 }  // namespace cdssm_host
+
+extern "C" int cdssm_fused_scan_fwd_set_path(int mode) {
+  if (mode < cdssm_host::kPathAuto || mode > cdssm_host::kPathOne) {
+    cdssm_host::set_error("cdssm_fused_scan_fwd_set_path: mode must be 0 (auto), 1 (four launches) or 2 "
+                          "(one pass required), got %d", mode);
+    return CDSSM_EINVAL;
+  }
+  return cdssm_host::g_scan_path.exchange(mode);
+}
 
 extern "C" const char* cdssm_last_error(void) { return g_err; }
 

@@ -122,12 +122,15 @@ int cdssm_fused_scan_bwd_profile(int dtype, const void* q, const void* k, const 
                                  int64_t N, int64_t chunk, hipStream_t stream, int iters, float* phase_ms);
 
 /*
- * Forward path selection (no counterpart in the reference; for tests and
- * benchmarks): 0 = automatic (default), 1 = always the four-launch scan,
- * 2 = the one-pass scan required (calls it cannot serve return -1).
- * Process-wide (inference and training forward alike); returns the previous
- * mode, or -1 for an invalid mode.  A one-pass call reports
- * its single launch as the main pass in cdssm_fused_scan_fwd_profile.
+ * Launch-path selection (no counterpart in the reference; for tests and
+ * benchmarks): 0 = automatic (default), 1 = always the multi-launch passes,
+ * 2 = one launch required (calls it cannot serve return -1).  Applies to the
+ * forward (one-pass scan vs four launches) and to the backward's correction
+ * adjoint + reverse carry (one launch vs three).  Process-wide; returns the
+ * previous mode, or -1 for an invalid mode.  A one-launch forward is reported
+ * as the main pass in cdssm_fused_scan_fwd_profile, a one-launch correction
+ * adjoint + carry as its first phase (0 for the fold and replay phases) in
+ * cdssm_fused_scan_bwd_profile.
  */
 int cdssm_fused_scan_fwd_set_path(int mode);
 
