@@ -325,21 +325,28 @@ __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, i
   return rm;
 }
 
+// zh *= m (complex, in place)
+template <int DPL>
+__device__ __forceinline__ void zscale(float (&zr)[DPL], float (&zi)[DPL], float2 m) {
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) {
+    const float xr = m.x * zr[j] - m.y * zi[j];
+    zi[j] = m.x * zi[j] + m.y * zr[j];
+    zr[j] = xr;
+  }
+}
+
 // One local step for a lane's DPL elements (see the frame rule above).  At a
 // token where some head of the wave resets, zh is first scaled in place by m
-// (m = 1 for the other heads), then every head takes the common update.
+// (m = 1 for the other heads), then every head takes the common update
+// zh += e k; returns e, which replays the step without the dot product.
 template <int DPL>
-__device__ __forceinline__ void local_step(float (&zr)[DPL], float (&zi)[DPL], const float (&kk)[DPL],
-                                           bool reset_any, float2 m, float er0, float ei0,
-                                           float bb, float pr, float pi) {
+__device__ __forceinline__ float2 local_step(float (&zr)[DPL], float (&zi)[DPL], const float (&kk)[DPL],
+                                             bool reset_any, float2 m, float er0, float ei0,
+                                             float bb, float pr, float pi) {
   float bpr = bb * pr, bpi = bb * pi;
   if (reset_any) {
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const float xr = m.x * zr[j] - m.y * zi[j];
-      zi[j] = m.x * zi[j] + m.y * zr[j];
-      zr[j] = xr;
-    }
+    zscale<DPL>(zr, zi, m);
     const float nr = m.x * bpr - m.y * bpi;
     bpi = m.x * bpi + m.y * bpr;
     bpr = nr;
@@ -350,6 +357,7 @@ __device__ __forceinline__ void local_step(float (&zr)[DPL], float (&zi)[DPL], c
     zr[j] = fmaf(er, kk[j], zr[j]);
     zi[j] = fmaf(ei, kk[j], zi[j]);
   }
+  return make_float2(er, ei);
 }
 
 // ---------------------------------------------------------------------------
@@ -724,8 +732,8 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
 // A workgroup of kOnePassW waves takes kOnePassW consecutive chunks (a
 // segment) of one (b, head group); wave w owns chunk seg * kOnePassW + w.
 //   1. each wave stages its chunk's scalars and runs the local recurrence
-//      (rescaled frame), keeping the local readout f_t (zh_t . q_t) in LDS;
-//      its chunk map is (G_k, F_k = z_{Q-1});
+//      (rescaled frame) over the k rows, keeping each step's update
+//      coefficient in LDS; its chunk map is (G_k, F_k = z_{Q-1});
 //   2. the segment's chunk maps are composed through LDS into the segment
 //      map, which is published.  The state entering the segment is the
 //      composition, oldest first, of the maps of the segments since its
@@ -734,7 +742,9 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
 //      anchor): a fixed order, so the results do not depend on timing.  Anchor
 //      ends publish their leaving state for the next kAnchor segments;
 //   3. each wave derives the state entering its chunk and runs the decay-free
-//      correction with the full readout; y is written coalesced.
+//      correction, replaying the local state from the stored coefficients,
+//      with the full readout f_t (zh_t.q_t) + g_{t-1} (c^_t.q_t) reduced once;
+//      y is written coalesced.  q is read once, k twice.
 // SAVE (training forward) also writes what the backward reads: the state
 // entering every chunk and G_k (the four-launch layout), the per-token records
 // (p_t, pc_t), (c^_{t+1}.q_t, Y_t.q_t) and g_t, as the main pass does.
@@ -871,8 +881,10 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   float4* svp = SAVE ? saved + 2 * ((tc.row0 * H) + (hok ? h : H - 1)) : nullptr;
   const int64_t zc0 = tile_h * a.NCK * D + sub * DPL;  // this lane's z checkpoint row, slot 0
 
-  // 1. local recurrence with the local readout f_t (zh_t . q_t); in the last
-  // PF steps the prefetch wraps to the first tokens, for the correction pass
+  // 1. local recurrence (k rows only); each step's update coefficient e_t is
+  // kept in LDS, so the correction pass replays zh without dot products.  In
+  // the last PF steps the k prefetch wraps to the first tokens; the q ring
+  // still holds the first tokens from the staging prefetch.
   if (live) {
     if (SAVE && sub == 0 && hok) gam[tile_h] = make_float2(GF[wv * HPW + hh].x, GF[wv * HPW + hh].y);
     float fpr = 1.0f, fpi = 0.0f;  // frame f_{t-1} (SAVE)
@@ -885,7 +897,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
         sb[i] = s.B[(tb + i) * HPW + hh];
         sm[i] = s.M[(tb + i) * HPW + hh];
       }
-      float yr[PF], yi[PF];
+      float2 ec[PF];
 #pragma unroll
       for (int i = 0; i < PF; ++i) {
         const int t = tb + i;
@@ -899,13 +911,11 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
           }
           store_zck<T, DPL>(zck, zc0 + (t / kZck) * D, xr, xi);
         }
-        float kk[DPL], qq[DPL];
+        float kk[DPL];
         kb[i].unpack_then_reload(kk);
-        qb[i].unpack_then_reload(qq);
         int tn = t + PF;
         tn = tn < ntr ? tn : tn - ntr;
         kb[i].load(kp + min(tn, tlast) * stride);
-        qb[i].load(qp + min(tn, tlast) * stride);
         float pr0 = 0.0f, pi0 = 0.0f, pr1 = 0.0f, pi1 = 0.0f;
 #pragma unroll
         for (int j = 0; j < DPL; j += 2) {
@@ -916,17 +926,9 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
         }
         const float pr = group_sum<LPH>(pr0 + pr1);
         const float pi = group_sum<LPH>(pi0 + pi1);
-        local_step<DPL>(zr, zi, kk, rm.test(t), sm[i], sa[i].x, sa[i].y, sa[i].z, pr, pi);
-        float qzr = 0.0f, qzi = 0.0f;
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-          qzr = fmaf(zr[j], qq[j], qzr);
-          qzi = fmaf(zi[j], qq[j], qzi);
-        }
-        const float4 fb = sb[i];
-        yr[i] = group_sum<LPH>(fb.x * qzr - fb.y * qzi);
-        yi[i] = group_sum<LPH>(fb.x * qzi + fb.y * qzr);
+        ec[i] = local_step<DPL>(zr, zi, kk, rm.test(t), sm[i], sa[i].x, sa[i].y, sa[i].z, pr, pi);
         if (SAVE) {
+          const float4 fb = sb[i];
           // p_t = f_{t-1} (zh_{t-1}.k_t), the first half of the token's first record
           if (sub == 0 && hok && t < tc.nt)
             reinterpret_cast<float2*>(svp + 2 * int64_t(t) * H)[0] =
@@ -937,7 +939,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
       }
       if (sub == 0) {
 #pragma unroll
-        for (int i = 0; i < PF; ++i) s_y[(tb + i) * HPW + hh] = make_float2(yr[i], yi[i]);
+        for (int i = 0; i < PF; ++i) s_y[(tb + i) * HPW + hh] = ec[i];
       }
     }
 #pragma unroll
@@ -1113,14 +1115,18 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
       for (int j = 0; j < DPL; ++j) states[tile_h * D + sub * DPL + j] = make_float2(cr[j], ci[j]);
     }
 
+    // the local state is replayed from its update coefficients
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) zr[j] = zi[j] = 0.0f;
     for (int tb = 0; tb < ntr; tb += PF) {
       float4 sa[PF], sb[PF];
-      float2 sl[PF];
+      float2 se[PF], sm[PF];
 #pragma unroll
       for (int i = 0; i < PF; ++i) {
         sa[i] = s.A[(tb + i) * HPW + hh];
         sb[i] = s.B[(tb + i) * HPW + hh];
-        sl[i] = s_y[(tb + i) * HPW + hh];
+        se[i] = s_y[(tb + i) * HPW + hh];
+        sm[i] = s.M[(tb + i) * HPW + hh];
       }
       float yr[PF], yi[PF];
 #pragma unroll
@@ -1131,18 +1137,22 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
         qb[i].unpack_then_reload(qq);
         kb[i].load(kp + min(t + PF, tlast) * stride);
         qb[i].load(qp + min(t + PF, tlast) * stride);
-        float pcr = 0.0f, pci = 0.0f, qcr = 0.0f, qci = 0.0f;
+        // zh_t = (m_t zh_{t-1} at a frame reset) + e_t k_t
+        if (rm.test(t)) zscale<DPL>(zr, zi, sm[i]);
+        float pcr = 0.0f, pci = 0.0f, zqr = 0.0f, zqi = 0.0f, qcr = 0.0f, qci = 0.0f;
 #pragma unroll
         for (int j = 0; j < DPL; ++j) {
+          zr[j] = fmaf(se[i].x, kk[j], zr[j]);
+          zi[j] = fmaf(se[i].y, kk[j], zi[j]);
           pcr = fmaf(cr[j], kk[j], pcr);
           pci = fmaf(ci[j], kk[j], pci);
+          zqr = fmaf(zr[j], qq[j], zqr);
+          zqi = fmaf(zi[j], qq[j], zqi);
           qcr = fmaf(cr[j], qq[j], qcr);
           qci = fmaf(ci[j], qq[j], qci);
         }
         pcr = group_sum<LPH>(pcr);
         pci = group_sum<LPH>(pci);
-        qcr = group_sum<LPH>(qcr);
-        qci = group_sum<LPH>(qci);
         const float bb = sa[i].z;
         const float ecr = bb * pcr, eci = bb * pci;
         float cnr = 0.0f, cni = 0.0f;
@@ -1155,10 +1165,10 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
             cni = fmaf(ci[j], qq[j], cni);
           }
         }
-        // y_t = sel_C (f_t (zh_t.q_t) + g_{t-1} (c^_t.q_t))
+        // y_t = sel_C (f_t (zh_t.q_t) + g_{t-1} (c^_t.q_t)), reduced once
         const float4 fb = sb[i];
-        const float Rr = sl[i].x + fb.z * qcr - fb.w * qci;
-        const float Ri = sl[i].y + fb.z * qci + fb.w * qcr;
+        const float Rr = group_sum<LPH>((fb.x * zqr - fb.y * zqi) + (fb.z * qcr - fb.w * qci));
+        const float Ri = group_sum<LPH>((fb.x * zqi + fb.y * zqr) + (fb.z * qci + fb.w * qcr));
         yr[i] = sa[i].w * Rr;
         yi[i] = sa[i].w * Ri;
         if (SAVE) {
