@@ -13,6 +13,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace cdssm {
 
 constexpr int kWave = 64;
@@ -131,6 +133,33 @@ struct RowVec {
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// x from lane (lane - OFF) of the same NB-lane segment: a DPP row shift when
+// the segments fit the 16-lane DPP rows (a few cycles), else a lane shuffle
+// (an LDS-crossbar permute).  Lanes whose offset in the segment is below OFF
+// get an unspecified value; callers mask them.
+template <int NB, int OFF, typename V>
+__device__ __forceinline__ V seg_shift_up(V x) {
+  static_assert(sizeof(V) == 4 && OFF >= 1 && OFF < NB, "32-bit values, shift inside the segment");
+  if constexpr (NB <= 16) {
+    const int u = __builtin_bit_cast(int, x);
+    return __builtin_bit_cast(V, __builtin_amdgcn_update_dpp(u, u, 0x110 + OFF, 0xF, 0xF, false));
+  } else {
+    return __shfl_up(x, OFF, NB);
+  }
+}
+
+// f(std::integral_constant<int, s>) for s = 1, 2, 4, ... < NB (the steps of a
+// segmented Hillis-Steele scan over NB lanes)
+template <int NB, typename F>
+__device__ __forceinline__ void for_shifts(F&& f) {
+  if constexpr (NB > 1) f(std::integral_constant<int, 1>{});
+  if constexpr (NB > 2) f(std::integral_constant<int, 2>{});
+  if constexpr (NB > 4) f(std::integral_constant<int, 4>{});
+  if constexpr (NB > 8) f(std::integral_constant<int, 8>{});
+  if constexpr (NB > 16) f(std::integral_constant<int, 16>{});
+  if constexpr (NB > 32) f(std::integral_constant<int, 32>{});
 }
 
 template <int G>

@@ -147,12 +147,12 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
     }
     // g entering the block: exclusive product over the head's earlier blocks
     float xgr = gpr, xgi = gpi;
-#pragma unroll
-    for (int off = 1; off < NB; off <<= 1) {
-      const float ygr = __shfl_up(xgr, off, NB), ygi = __shfl_up(xgi, off, NB);
+    for_shifts<NB>([&](auto offc) {
+      constexpr int off = decltype(offc)::value;
+      const float ygr = seg_shift_up<NB, off>(xgr), ygi = seg_shift_up<NB, off>(xgi);
       if (blk >= off) cmul_acc(xgr, xgi, ygr, ygi);
-    }
-    float egr = __shfl_up(xgr, 1, NB), egi = __shfl_up(xgi, 1, NB);
+    });
+    float egr = seg_shift_up<NB, 1>(xgr), egi = seg_shift_up<NB, 1>(xgi);
     if (blk == 0) {
       egr = 1.0f;
       egi = 0.0f;

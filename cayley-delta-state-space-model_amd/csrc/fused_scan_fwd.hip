@@ -195,15 +195,16 @@ __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, i
     }
     // exclusive prefix over the head's blocks: sum of log2|a|^2, product of a
     float xL = lsum, xgr = gpr, xgi = gpi;
-#pragma unroll
-    for (int off = 1; off < NB; off <<= 1) {
-      const float yL = __shfl_up(xL, off, NB), ygr = __shfl_up(xgr, off, NB), ygi = __shfl_up(xgi, off, NB);
+    for_shifts<NB>([&](auto offc) {
+      constexpr int off = decltype(offc)::value;
+      const float yL = seg_shift_up<NB, off>(xL), ygr = seg_shift_up<NB, off>(xgr),
+                  ygi = seg_shift_up<NB, off>(xgi);
       if (blk >= off) {
         xL += yL;
         cmul_acc(xgr, xgi, ygr, ygi);
       }
-    }
-    float eL = __shfl_up(xL, 1, NB), egr = __shfl_up(xgr, 1, NB), egi = __shfl_up(xgi, 1, NB);
+    });
+    float eL = seg_shift_up<NB, 1>(xL), egr = seg_shift_up<NB, 1>(xgr), egi = seg_shift_up<NB, 1>(xgi);
     if (blk == 0) {
       eL = 0.0f;
       egr = 1.0f;
@@ -236,17 +237,17 @@ __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, i
     // with the carry (which acts as a reset element)
     float xfr = Fr[TPB - 1], xfi = Fi[TPB - 1];
     int xfl = anyr;
-#pragma unroll
-    for (int off = 1; off < NB; off <<= 1) {
-      const float yr = __shfl_up(xfr, off, NB), yi = __shfl_up(xfi, off, NB);
-      const int yf = __shfl_up(xfl, off, NB);
+    for_shifts<NB>([&](auto offc) {
+      constexpr int off = decltype(offc)::value;
+      const float yr = seg_shift_up<NB, off>(xfr), yi = seg_shift_up<NB, off>(xfi);
+      const int yf = seg_shift_up<NB, off>(xfl);
       if (blk >= off && !xfl) {
         cmul_acc(xfr, xfi, yr, yi);
         xfl = yf;
       }
-    }
-    float efr = __shfl_up(xfr, 1, NB), efi = __shfl_up(xfi, 1, NB);
-    int efl = __shfl_up(xfl, 1, NB);
+    });
+    float efr = seg_shift_up<NB, 1>(xfr), efi = seg_shift_up<NB, 1>(xfi);
+    int efl = seg_shift_up<NB, 1>(xfl);
     if (blk == 0) {
       efr = 1.0f;
       efi = 0.0f;
