@@ -66,6 +66,25 @@ struct F32 {
   __device__ __forceinline__ static void store(raw* p, float v) { *p = v; }
 };
 
+// A wave's (chunk, head group) tile of a (B, L, H, D) tensor as a buffer
+// resource: the base (wave-uniform, scalar registers) is the tile's first row
+// at its first head, each lane adds its constant byte offset (head, slice),
+// and a token is selected by a scalar byte offset, so a row load costs one
+// scalar add instead of a 64-bit address computation.  num_records covers
+// the tensor's bytes from the base (clamped to 32 bits); every access the
+// kernels make is in range by construction.
+struct RowStream {
+  __amdgpu_buffer_rsrc_t rs;
+  int voff;
+};
+
+__device__ __forceinline__ RowStream make_row_stream(const void* base, int64_t bytes_from_base, int lane_off_bytes) {
+  const uint64_t n = bytes_from_base > 0 ? uint64_t(bytes_from_base) : 0ull;
+  const int nrec = int(uint32_t(n > 0xffffffffull ? 0xffffffffull : n));
+  return RowStream{__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), short(0), nrec, 0x00020000),
+                   lane_off_bytes};
+}
+
 // A lane's slice of one row: DPL consecutive elements, loaded with a single
 // 4-, 8- or 16-byte load into W = DPL * bytes / 4 dwords and widened on use.
 template <typename T, int DPL>
@@ -73,6 +92,24 @@ struct RowVec {
   static constexpr int W = DPL * T::bytes / 4;
   static_assert(W == 1 || W == 2 || W == 4 || W == 8, "a lane slice is 4, 8, 16 or 32 bytes");
   uint32_t u[W];
+
+  // The slice at scalar byte offset soff of a row stream.
+  __device__ __forceinline__ void load(const RowStream& s, int soff) {
+    if constexpr (W == 8) {
+      const auto v0 = __builtin_amdgcn_raw_buffer_load_b128(s.rs, s.voff, soff, 0);
+      const auto v1 = __builtin_amdgcn_raw_buffer_load_b128(s.rs, s.voff + 16, soff, 0);
+      u[0] = v0[0]; u[1] = v0[1]; u[2] = v0[2]; u[3] = v0[3];
+      u[4] = v1[0]; u[5] = v1[1]; u[6] = v1[2]; u[7] = v1[3];
+    } else if constexpr (W == 4) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(s.rs, s.voff, soff, 0);
+      u[0] = v[0]; u[1] = v[1]; u[2] = v[2]; u[3] = v[3];
+    } else if constexpr (W == 2) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(s.rs, s.voff, soff, 0);
+      u[0] = v[0]; u[1] = v[1];
+    } else {
+      u[0] = __builtin_amdgcn_raw_buffer_load_b32(s.rs, s.voff, soff, 0);
+    }
+  }
 
   __device__ __forceinline__ void load(const typename T::raw* p) {
     if constexpr (W == 8) {

@@ -86,7 +86,24 @@ struct ResetMask {
     // wave-uniform by construction (ballots); readfirstlane makes the branch scalar
     return __builtin_amdgcn_readfirstlane(int((w >> (t & 63)) & 1ull)) != 0;
   }
+  // Bits of the 8 tokens tb .. tb + 7 (tb a multiple of 8), bit i for token
+  // tb + i: one scalar word per token group, tested per token with one bit test.
+  __device__ __forceinline__ uint32_t group8(int tb) const {
+    const uint64_t w = tb < 64 ? m0 : m1;
+    return __builtin_amdgcn_readfirstlane(uint32_t(w >> (tb & 63)) & 0xffu);
+  }
 };
+
+// Row streams of a (B, L, H, D) tensor for the lane's head of a chunk tile:
+// base at (row0, hbase), lane offset (head of the lane, or H - 1 past the
+// last head; element slice), token stride H * D elements.
+template <typename T>
+__device__ __forceinline__ RowStream tile_stream(const typename T::raw* x, const ChunkTile& tc, int H, int D,
+                                                 int64_t n_rows, int hh, int sub_off) {
+  const int64_t base = (tc.row0 * H + tc.hbase) * D;
+  const int hl = tc.hbase + hh < H ? hh : H - 1 - tc.hbase;
+  return make_row_stream(x + base, (n_rows * H * D - base) * T::bytes, (hl * D + sub_off) * T::bytes);
+}
 
 // The local state is kept in a rescaled frame, z_t = f_t zh_t (f complex, per
 // head).  A step z_t = a (z_{t-1} - beta (z_{t-1}.k) k) + w k becomes
@@ -850,11 +867,12 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   float2* Sx = reinterpret_cast<float2*>(GF + W * HPW);
   int* ctrl = reinterpret_cast<int*>(Sx + SEGN);
 
-  const int64_t stride = int64_t(H) * D;
-  const int64_t off = (tc.row0 * H + (hok ? h : H - 1)) * D + sub * DPL;
-  const typename T::raw* kp = k + off;
-  const typename T::raw* qp = q + off;
+  const int64_t n_rows = int64_t(a.n_chain / n_hg) * L;  // B * L
+  const RowStream ks = tile_stream<T>(k, tc, H, D, n_rows, hh, sub * DPL);
+  const RowStream qs = tile_stream<T>(q, tc, H, D, n_rows, hh, sub * DPL);
+  const int rowb = H * D * T::bytes;  // token stride in bytes
   const int tlast = tc.nt - 1;
+  const int slim = tlast * rowb;
   RowVec<T, DPL> kb[PF], qb[PF];
   float zr[DPL], zi[DPL];
 #pragma unroll
@@ -866,8 +884,8 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
                                      SAVE ? gsaved : nullptr, GF + wv * HPW, [&] {
 #pragma unroll
                                        for (int i = 0; i < PF; ++i) {
-                                         kb[i].load(kp + min(i, tlast) * stride);
-                                         qb[i].load(qp + min(i, tlast) * stride);
+                                         kb[i].load(ks, min(i * rowb, slim));
+                                         qb[i].load(qs, min(i * rowb, slim));
                                        }
                                      });
 #pragma unroll
@@ -899,6 +917,9 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
         sm[i] = s.M[(tb + i) * HPW + hh];
       }
       float2 ec[PF];
+      // prefetch targets of this group: tokens tb + PF .., or the first tokens
+      const int nb = (tb + PF < ntr ? tb + PF : 0) * rowb;
+      const uint32_t rg = rm.group8(tb);
 #pragma unroll
       for (int i = 0; i < PF; ++i) {
         const int t = tb + i;
@@ -914,9 +935,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
         }
         float kk[DPL];
         kb[i].unpack_then_reload(kk);
-        int tn = t + PF;
-        tn = tn < ntr ? tn : tn - ntr;
-        kb[i].load(kp + min(tn, tlast) * stride);
+        kb[i].load(ks, min(nb + i * rowb, slim));
         float pr0 = 0.0f, pi0 = 0.0f, pr1 = 0.0f, pi1 = 0.0f;
 #pragma unroll
         for (int j = 0; j < DPL; j += 2) {
@@ -927,7 +946,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
         }
         const float pr = group_sum<LPH>(pr0 + pr1);
         const float pi = group_sum<LPH>(pi0 + pi1);
-        ec[i] = local_step<DPL>(zr, zi, kk, rm.test(t), sm[i], sa[i].x, sa[i].y, sa[i].z, pr, pi);
+        ec[i] = local_step<DPL>(zr, zi, kk, (rg >> i) & 1u, sm[i], sa[i].x, sa[i].y, sa[i].z, pr, pi);
         if (SAVE) {
           const float4 fb = sb[i];
           // p_t = f_{t-1} (zh_{t-1}.k_t), the first half of the token's first record
@@ -1130,16 +1149,18 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
         sm[i] = s.M[(tb + i) * HPW + hh];
       }
       float yr[PF], yi[PF];
+      const int nb = (tb + PF) * rowb;
+      const uint32_t rg = rm.group8(tb);
 #pragma unroll
       for (int i = 0; i < PF; ++i) {
         const int t = tb + i;
         float kk[DPL], qq[DPL];
         kb[i].unpack_then_reload(kk);
         qb[i].unpack_then_reload(qq);
-        kb[i].load(kp + min(t + PF, tlast) * stride);
-        qb[i].load(qp + min(t + PF, tlast) * stride);
+        kb[i].load(ks, min(nb + i * rowb, slim));
+        qb[i].load(qs, min(nb + i * rowb, slim));
         // zh_t = (m_t zh_{t-1} at a frame reset) + e_t k_t
-        if (rm.test(t)) zscale<DPL>(zr, zi, sm[i]);
+        if ((rg >> i) & 1u) zscale<DPL>(zr, zi, sm[i]);
         float pcr = 0.0f, pci = 0.0f, zqr = 0.0f, zqi = 0.0f, qcr = 0.0f, qci = 0.0f;
 #pragma unroll
         for (int j = 0; j < DPL; ++j) {
@@ -1431,6 +1452,12 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
   }
   if (B * H > 0x7fffffffLL || L > 0x7fffffffLL || B * L * H * D > (int64_t(1) << 46)) {
     cdssm_host::set_error("%s: problem too large", op);
+    return CDSSM_EINVAL;
+  }
+  // q/k rows of a chunk tile are addressed by 32-bit byte offsets
+  if ((chunk + 16) * H * D * 4 > 0x7fffffffLL) {
+    cdssm_host::set_error("%s: H * D too large for 32-bit row offsets (H=%lld D=%lld)", op, (long long)H,
+                          (long long)D);
     return CDSSM_EINVAL;
   }
   if (!q || !k || !v || !beta || !sel_c || !dt || !r || !alpha || !omega || !y || !h_final ||
