@@ -230,6 +230,19 @@ struct ChunkTile {
   int64_t row0;
 };
 
+// Row streams of a (B, L, H, D) tensor for the lane's head of a chunk tile:
+// base at (row0, hbase), lane offset (head of the lane, or H - 1 past the
+// last head; element slice), token stride H * D elements; the range is the
+// rest of the tile's batch row.
+template <typename T>
+__device__ __forceinline__ RowStream tile_stream(const typename T::raw* x, const ChunkTile& tc, int L, int H,
+                                                 int D, int hh, int sub_off) {
+  const int64_t base = (tc.row0 * H + tc.hbase) * D;
+  const int hl = tc.hbase + hh < H ? hh : H - 1 - tc.hbase;
+  return make_row_stream(x + base, (int64_t(L - tc.t0) * H - tc.hbase) * D * T::bytes,
+                         (hl * D + sub_off) * T::bytes);
+}
+
 __device__ __forceinline__ ChunkTile decode_tile(int L, int Q, int NC, int n_hg, int HPW) {
   ChunkTile c;
   int g = blockIdx.x;

@@ -253,6 +253,34 @@ __device__ __forceinline__ void store_row(typename T::raw* p, const float (&x)[D
   }
 }
 
+// The same slice stored through a row stream at scalar byte offset soff.
+template <typename T, int DPL>
+__device__ __forceinline__ void store_row(const RowStream& s, int soff, const float (&x)[DPL]) {
+  using u32x4 = __attribute__((ext_vector_type(4))) unsigned int;
+  using u32x2 = __attribute__((ext_vector_type(2))) unsigned int;
+  if constexpr (T::bytes == 2) {
+    uint32_t u[DPL / 2];
+#pragma unroll
+    for (int i = 0; i < DPL / 2; ++i) u[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+    if constexpr (DPL == 8) {
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{u[0], u[1], u[2], u[3]}, s.rs, s.voff, soff, 0);
+    } else if constexpr (DPL == 4) {
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2{u[0], u[1]}, s.rs, s.voff, soff, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < DPL / 2; ++i) __builtin_amdgcn_raw_buffer_store_b32(u[i], s.rs, s.voff + 4 * i, soff, 0);
+    }
+  } else {
+    static_assert(DPL % 4 == 0, "fp32 slices are whole 16-byte vectors");
+#pragma unroll
+    for (int i = 0; i < DPL / 4; ++i)
+      __builtin_amdgcn_raw_buffer_store_b128(
+          u32x4{__float_as_uint(x[4 * i]), __float_as_uint(x[4 * i + 1]), __float_as_uint(x[4 * i + 2]),
+                __float_as_uint(x[4 * i + 3])},
+          s.rs, s.voff + 16 * i, soff, 0);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // B1: correction-branch adjoint of the entering state, per chunk.
 //   lambda = 0; for t = n-1..0: lambda += conj(g_t) sel_t dy_t q_t;
@@ -275,17 +303,17 @@ __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
   const int slots = round_up(Q, kWave) * HPW;
   const int ntr = round_up(tc.nt, PF);
 
-  const int64_t stride = int64_t(H) * D;
-  const int64_t off = (tc.row0 * H + hl) * D + sub * DPL;
-  const typename T::raw* kp = k + off;
-  const typename T::raw* qp = q + off;
+  const RowStream ks = tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
+  const RowStream qs = tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
+  const int rowb = H * D * T::bytes;  // token stride in bytes
   const int tlast = tc.nt - 1;
+  const int slim = tlast * rowb;
   // reverse ring: slot i holds token ntr-1-(tb+i)
   RowVec<T, DPL> kb[PF], qb[PF];
 #pragma unroll
   for (int i = 0; i < PF; ++i) {
-    kb[i].load(kp + min(ntr - 1 - i, tlast) * stride);
-    qb[i].load(qp + min(ntr - 1 - i, tlast) * stride);
+    kb[i].load(ks, min((ntr - 1 - i) * rowb, slim));
+    qb[i].load(qs, min((ntr - 1 - i) * rowb, slim));
   }
   BwdScalars s{nullptr, smem4, smem4 + slots};
   stage_corr<T, HPW>(tc, H, ntr, beta, sel_c, dy, gsaved, s);
@@ -307,14 +335,14 @@ __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
       s1[i] = s.S1[p];
       s2[i] = s.S2[p];
     }
+    const int nb = (ntr - 1 - tb - PF) * rowb;  // row offset of the reload for slot 0
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      const int t = ntr - 1 - (tb + i);
       float kk[DPL], qq[DPL];
       kb[i].unpack_then_reload(kk);
       qb[i].unpack_then_reload(qq);
-      kb[i].load(kp + max(min(t - PF, tlast), 0) * stride);
-      qb[i].load(qp + max(min(t - PF, tlast), 0) * stride);
+      kb[i].load(ks, max(min(nb - i * rowb, slim), 0));
+      qb[i].load(qs, max(min(nb - i * rowb, slim), 0));
       __builtin_amdgcn_sched_barrier(0);  // issue the reloads here, not sunk below later tokens
       // padded steps have h = 0 and beta = 0
       float sr = 0.0f, si = 0.0f;
@@ -520,17 +548,17 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
   float lr[DPL], li[DPL];
 #pragma unroll
   for (int jj = 0; jj < DPL; ++jj) lr[jj] = li[jj] = 0.0f;
-  const int64_t stride = int64_t(H) * D;
-  const int64_t off = (tc.row0 * H + hl) * D + sub * DPL;
-  const typename T::raw* kp = a.k + off;
-  const typename T::raw* qp = a.q + off;
+  const RowStream ks = tile_stream<T>(a.k, tc, L, H, D, hh, sub * DPL);
+  const RowStream qs = tile_stream<T>(a.q, tc, L, H, D, hh, sub * DPL);
+  const int rowb = H * D * T::bytes;  // token stride in bytes
   const int tlast = tc.nt - 1;
+  const int slim = tlast * rowb;
   RowVec<T, DPL> kb[PF], qb[PF];
   if (live) {
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      kb[i].load(kp + min(ntr - 1 - i, tlast) * stride);
-      qb[i].load(qp + min(ntr - 1 - i, tlast) * stride);
+      kb[i].load(ks, min((ntr - 1 - i) * rowb, slim));
+      qb[i].load(qs, min((ntr - 1 - i) * rowb, slim));
     }
     stage_corr<T, HPW>(tc, H, ntr, a.beta, a.sel_c, a.dy, a.gsaved, s);
 #pragma unroll
@@ -549,14 +577,14 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
         s1[i] = s.S1[p];
         s2[i] = s.S2[p];
       }
+      const int nb = (ntr - 1 - tb - PF) * rowb;  // row offset of the reload for slot 0
 #pragma unroll
       for (int i = 0; i < PF; ++i) {
-        const int t = ntr - 1 - (tb + i);
         float kk[DPL], qq[DPL];
         kb[i].unpack_then_reload(kk);
         qb[i].unpack_then_reload(qq);
-        kb[i].load(kp + max(min(t - PF, tlast), 0) * stride);
-        qb[i].load(qp + max(min(t - PF, tlast), 0) * stride);
+        kb[i].load(ks, max(min(nb - i * rowb, slim), 0));
+        qb[i].load(qs, max(min(nb - i * rowb, slim), 0));
         __builtin_amdgcn_sched_barrier(0);
         float sr = 0.0f, si = 0.0f;
 #pragma unroll
@@ -836,11 +864,13 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   const int ntr = round_up(tc.nt, PF);
   const float al = alpha[hl], om = omega[hl];
 
-  const int64_t stride = int64_t(H) * D;
-  const int64_t off = (tc.row0 * H + hl) * D + sub * DPL;
-  const typename T::raw* kp = k + off;
-  const typename T::raw* qp = q + off;
+  const RowStream ks = tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
+  const RowStream qs = tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
+  const RowStream dks = tile_stream<T>(dk, tc, L, H, D, hh, sub * DPL);
+  const RowStream dqs = tile_stream<T>(dq, tc, L, H, D, hh, sub * DPL);
+  const int rowb = H * D * T::bytes;  // token stride in bytes
   const int tlast = tc.nt - 1;
+  const int slim = tlast * rowb;
   const int64_t chh = (int64_t(tc.b) * NC + tc.chunk) * H + hl;  // (b, chunk, head) index
   // the training forward's z checkpoints of this (chunk, head): z_{t-1} at t = CK * seg
   const int64_t ck0 = chh * NCK * D + sub * DPL;
@@ -893,8 +923,8 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
     const int tb = seg * CK;
 #pragma unroll
     for (int i = 0; i < CK; ++i) {
-      R.k[i].load(kp + min(tb + i, tlast) * stride);
-      R.q[i].load(qp + min(tb + i, tlast) * stride);
+      R.k[i].load(ks, min((tb + i) * rowb, slim));
+      R.q[i].load(qs, min((tb + i) * rowb, slim));
     }
     load_zck<T, DPL>(zck, ck0 + int64_t(seg) * D, R.z0);
   };
@@ -1003,8 +1033,8 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
           li[jj] = fmaf(-bsli, kk[jj], li[jj]);
         }
         if (hok) {
-          store_row<T, DPL>(dk + off + int64_t(t) * stride, dkv);
-          store_row<T, DPL>(dq + off + int64_t(t) * stride, dqv);
+          store_row<T, DPL>(dks, t * rowb, dkv);
+          store_row<T, DPL>(dqs, t * rowb, dqv);
         }
         if (sub == 0) {
           sP[p] = make_float4(dar, dai, dwr, dwi);

@@ -94,17 +94,6 @@ struct ResetMask {
   }
 };
 
-// Row streams of a (B, L, H, D) tensor for the lane's head of a chunk tile:
-// base at (row0, hbase), lane offset (head of the lane, or H - 1 past the
-// last head; element slice), token stride H * D elements.
-template <typename T>
-__device__ __forceinline__ RowStream tile_stream(const typename T::raw* x, const ChunkTile& tc, int H, int D,
-                                                 int64_t n_rows, int hh, int sub_off) {
-  const int64_t base = (tc.row0 * H + tc.hbase) * D;
-  const int hl = tc.hbase + hh < H ? hh : H - 1 - tc.hbase;
-  return make_row_stream(x + base, (n_rows * H * D - base) * T::bytes, (hl * D + sub_off) * T::bytes);
-}
-
 // The local state is kept in a rescaled frame, z_t = f_t zh_t (f complex, per
 // head).  A step z_t = a (z_{t-1} - beta (z_{t-1}.k) k) + w k becomes
 //   zh_t = zh_{t-1} + (w/f_t - beta ph) k,   f_t = f_{t-1} a_t,   ph = zh_{t-1}.k
@@ -401,16 +390,17 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
   const int slots = round_up(Q, kWave) * HPW;
   const int64_t ch0 = (int64_t(tc.b) * NC + tc.chunk) * H + tc.hbase;
 
-  const int64_t stride = int64_t(H) * D;
-  const typename T::raw* kp = k + (tc.row0 * H + (hok ? h : H - 1)) * D + sub * DPL;
+  const RowStream ks = tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
+  const int rowb = H * D * T::bytes;  // token stride in bytes
   const int tlast = tc.nt - 1;
+  const int slim = tlast * rowb;
   RowVec<T, DPL> kb[PF];
   TileScalars s{smem4, smem4 + slots, reinterpret_cast<float2*>(smem4 + slots + HPW)};
   const ResetMask rm = stage_scalars<T, HPW, false>(tc, H, ntr, v, beta, nullptr, dt, r, alpha, omega, c, s,
                                                     gam, ch0, nullptr, nullptr, [&] {
 #pragma unroll
                                                       for (int i = 0; i < PF; ++i)
-                                                        kb[i].load(kp + min(i, tlast) * stride);
+                                                        kb[i].load(ks, min(i * rowb, slim));
                                                     });
 #pragma unroll
   for (int i = 0; i < PF; ++i) kb[i].pin();
@@ -428,12 +418,13 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
       sa[i] = s.A[(tb + i) * HPW + hh];
       sm[i] = s.M[(tb + i) * HPW + hh];
     }
+    const int nb = (tb + PF) * rowb;
+    const uint32_t rg = rm.group8(tb);
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      const int t = tb + i;
       float kk[DPL];
       kb[i].unpack_then_reload(kk);
-      kb[i].load(kp + min(t + PF, tlast) * stride);
+      kb[i].load(ks, min(nb + i * rowb, slim));
       float pr0 = 0.0f, pi0 = 0.0f, pr1 = 0.0f, pi1 = 0.0f;
 #pragma unroll
       for (int j = 0; j < DPL; j += 2) {
@@ -444,7 +435,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
       }
       const float pr = group_sum<LPH>(pr0 + pr1);
       const float pi = group_sum<LPH>(pi0 + pi1);
-      local_step<DPL>(zr, zi, kk, rm.test(t), sm[i], sa[i].x, sa[i].y, sa[i].z, pr, pi);
+      local_step<DPL>(zr, zi, kk, (rg >> i) & 1u, sm[i], sa[i].x, sa[i].y, sa[i].z, pr, pi);
     }
   }
 
@@ -601,11 +592,11 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
   const int ntr = round_up(tc.nt, PF);
   const int slots = round_up(Q, kWave) * HPW;
 
-  const int64_t stride = int64_t(H) * D;
-  const int64_t off = (tc.row0 * H + (hok ? h : H - 1)) * D + sub * DPL;
-  const typename T::raw* kp = k + off;
-  const typename T::raw* qp = q + off;
+  const RowStream ks = tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
+  const RowStream qs = tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
+  const int rowb = H * D * T::bytes;  // token stride in bytes
   const int tlast = tc.nt - 1;
+  const int slim = tlast * rowb;
   RowVec<T, DPL> kb[PF], qb[PF];
   float zr[DPL], zi[DPL], cr[DPL], ci[DPL];
   {
@@ -626,8 +617,8 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
                                                    nullptr, 0, SAVE ? gsaved : nullptr, nullptr, [&] {
 #pragma unroll
                                                      for (int i = 0; i < PF; ++i) {
-                                                       kb[i].load(kp + min(i, tlast) * stride);
-                                                       qb[i].load(qp + min(i, tlast) * stride);
+                                                       kb[i].load(ks, min(i * rowb, slim));
+                                                       qb[i].load(qs, min(i * rowb, slim));
                                                      }
                                                    });
 #pragma unroll
@@ -652,6 +643,8 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
       sm[i] = s.M[(tb + i) * HPW + hh];
     }
     float yr[PF], yi[PF];
+    const int nb = (tb + PF) * rowb;
+    const uint32_t rg = rm.group8(tb);
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int t = tb + i;
@@ -668,8 +661,8 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
       float kk[DPL], qq[DPL];
       kb[i].unpack_then_reload(kk);
       qb[i].unpack_then_reload(qq);
-      kb[i].load(kp + min(t + PF, tlast) * stride);
-      qb[i].load(qp + min(t + PF, tlast) * stride);
+      kb[i].load(ks, min(nb + i * rowb, slim));
+      qb[i].load(qs, min(nb + i * rowb, slim));
 
       float pzr = 0.0f, pzi = 0.0f, pcr = 0.0f, pci = 0.0f, qcr = 0.0f, qci = 0.0f;
 #pragma unroll
@@ -687,7 +680,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
       pci = group_sum<LPH>(pci);
 
       const float bb = sa[i].z;
-      local_step<DPL>(zr, zi, kk, rm.test(t), sm[i], sa[i].x, sa[i].y, bb, pzr, pzi);
+      local_step<DPL>(zr, zi, kk, (rg >> i) & 1u, sm[i], sa[i].x, sa[i].y, bb, pzr, pzi);
       const float ecr = bb * pcr, eci = bb * pci;
       float qzr = 0.0f, qzi = 0.0f, cnr = 0.0f, cni = 0.0f;
 #pragma unroll
@@ -867,9 +860,8 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   float2* Sx = reinterpret_cast<float2*>(GF + W * HPW);
   int* ctrl = reinterpret_cast<int*>(Sx + SEGN);
 
-  const int64_t n_rows = int64_t(a.n_chain / n_hg) * L;  // B * L
-  const RowStream ks = tile_stream<T>(k, tc, H, D, n_rows, hh, sub * DPL);
-  const RowStream qs = tile_stream<T>(q, tc, H, D, n_rows, hh, sub * DPL);
+  const RowStream ks = tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
+  const RowStream qs = tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
   const int rowb = H * D * T::bytes;  // token stride in bytes
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb;
