@@ -11,7 +11,9 @@ from .scan import (ChunkwiseDeltaScanFn, chunkwise_delta_scan, chunkwise_delta_s
 from .ops import (DynamicsFusedFn, ExactCorrectionFn, InterChunkScanFn,  # noqa: F401
                   IntraChunkScanFn, NormalizeKQFn)
 from .ssd import SSDChunkwiseScan  # noqa: F401
+from .decode import DecodeState, decode_step, prefill  # noqa: F401
 
 __all__ = ["DynamicsFusedFn", "NormalizeKQFn", "IntraChunkScanFn", "InterChunkScanFn", "ExactCorrectionFn",
            "SSDChunkwiseScan", "ChunkwiseDeltaScanFn", "chunkwise_delta_scan", "chunkwise_delta_scan_fwd",
-           "chunkwise_delta_scan_bwd", "chunkwise_delta_scan_train", "set_forward_path"]
+           "chunkwise_delta_scan_bwd", "chunkwise_delta_scan_train", "set_forward_path", "DecodeState",
+           "decode_step", "prefill"]

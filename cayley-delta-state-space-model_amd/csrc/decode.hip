@@ -1,0 +1,265 @@
+// Recurrent decode step of the CD-SSM scan: one new token per (b, h), with the
+// R-mode state carried between calls, so that generating after a prefill
+// needs no re-forward of the sequence.
+//
+// The reference generates by re-running the whole forward for every new
+// token (predict.py:53-67); its outputs are those of the chunked R-mode scan
+// (ssd.py:39-111).  The decode step reproduces that scan one token at a time
+// (same chunk boundaries, chunk size Q):
+//   state entering token t, local index j = t mod Q of chunk k:
+//     z     local state of chunk k after token t-1 (z = 0 at j = 0)
+//     c^    decay-free correction state, c^_j (c^_0 = s_k)
+//     s     s_k, the carry entering chunk k
+//     g     g_{j-1} = prod_{u<j} a_u within the chunk (g = 1 at j = 0)
+//   step:   z' = a (z - beta (z.k) k) + w k              (intra_chunk_scan.cu:146-167)
+//           y  = sel_C ((z' + g c^) . q)                 (ssd.py:102, block.py:208-211;
+//                                                         c_j = g_{j-1} c^_j, exact_correction.cu:89-94)
+//           c^' = c^ - beta (c^.k) k,  g' = g a
+//   chunk end (j = Q - 1): s' = g' s + z' (inter_chunk_scan.cu:73-83); then
+//           z = 0, c^ = s', s = s', g = 1.
+// g' s + z' is also the R-mode carry after the token (the fused scan's
+// h_final for a sequence ending there).
+//
+// State layout (fp32, caller-owned): state (B, H, 3, 2, D) = rows z_re, z_im,
+// c^_re, c^_im, s_re, s_im; gam (B, H, 2) = g; pos (B, H) int32 = j.
+// Work layout: one wave per (b, group of HPW heads), LPH lanes per head, each
+// lane DPL consecutive state elements (as the fused scan's main pass).
+#include "common.hpp"
+
+namespace cdssm {
+
+template <typename T, int D, int LPH>
+__global__ __launch_bounds__(kWave) void decode_step_kernel(
+    const typename T::raw* __restrict__ q, const typename T::raw* __restrict__ k,
+    const typename T::raw* __restrict__ v, const typename T::raw* __restrict__ beta,
+    const typename T::raw* __restrict__ sel_c, const typename T::raw* __restrict__ dt,
+    const typename T::raw* __restrict__ r, const float* __restrict__ alpha, const float* __restrict__ omega,
+    float c, float* __restrict__ state, float2* __restrict__ gam, int* __restrict__ pos,
+    typename T::raw* __restrict__ y, float* __restrict__ h_out, int H, int Q, int n_hg) {
+  constexpr int DPL = D / LPH, HPW = kWave / LPH;
+  static_assert(DPL % 4 == 0, "state slices are whole float4s");
+  const int bi = int(blockIdx.x) / n_hg;
+  const int hbase = (int(blockIdx.x) % n_hg) * HPW;
+  const int lane = int(threadIdx.x);
+  const int hh = lane / LPH, sub = lane % LPH;
+  const int h = hbase + hh;
+  const bool hok = h < H;
+  const int hl = hok ? h : H - 1;
+  const int64_t bh = int64_t(bi) * H + hl;  // (b, h); the token is (b, 0, h)
+
+  // per-token scalars and dynamics (every lane of the head computes them)
+  const float bb = T::load(beta + bh), sc = T::load(sel_c + bh);
+  const Transition tr = cayley_gated(T::load(dt + bh), T::load(r + bh), alpha[hl], omega[hl], c);
+  const float wr = bb * tr.vp * T::load(v + 2 * bh), wi = bb * tr.vp * T::load(v + 2 * bh + 1);
+
+  float kk[DPL], qq[DPL];
+  {
+    RowVec<T, DPL> kv, qv;
+    kv.load(k + bh * D + sub * DPL);
+    qv.load(q + bh * D + sub * DPL);
+    kv.unpack(kk);
+    qv.unpack(qq);
+  }
+  float* st = state + bh * 6 * D + sub * DPL;
+  float zr[DPL], zi[DPL], cr[DPL], ci[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; j += 4) {
+    const float4 a0 = *reinterpret_cast<const float4*>(st + j);
+    const float4 a1 = *reinterpret_cast<const float4*>(st + D + j);
+    const float4 a2 = *reinterpret_cast<const float4*>(st + 2 * D + j);
+    const float4 a3 = *reinterpret_cast<const float4*>(st + 3 * D + j);
+    zr[j] = a0.x; zr[j + 1] = a0.y; zr[j + 2] = a0.z; zr[j + 3] = a0.w;
+    zi[j] = a1.x; zi[j + 1] = a1.y; zi[j + 2] = a1.z; zi[j + 3] = a1.w;
+    cr[j] = a2.x; cr[j + 1] = a2.y; cr[j + 2] = a2.z; cr[j + 3] = a2.w;
+    ci[j] = a3.x; ci[j + 1] = a3.y; ci[j + 2] = a3.z; ci[j + 3] = a3.w;
+  }
+  const float2 g = gam[bh];
+  const int jpos = pos[bh];
+
+  // z.k, c^.k, c^.q (c^ before its step: the correction is read before token t)
+  float pzr = 0.0f, pzi = 0.0f, pcr = 0.0f, pci = 0.0f, cqr = 0.0f, cqi = 0.0f;
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) {
+    pzr = fmaf(zr[j], kk[j], pzr);
+    pzi = fmaf(zi[j], kk[j], pzi);
+    pcr = fmaf(cr[j], kk[j], pcr);
+    pci = fmaf(ci[j], kk[j], pci);
+    cqr = fmaf(cr[j], qq[j], cqr);
+    cqi = fmaf(ci[j], qq[j], cqi);
+  }
+  pzr = group_sum<LPH>(pzr);
+  pzi = group_sum<LPH>(pzi);
+  pcr = group_sum<LPH>(pcr);
+  pci = group_sum<LPH>(pci);
+  cqr = group_sum<LPH>(cqr);
+  cqi = group_sum<LPH>(cqi);
+
+  // z' = a (z - beta (z.k) k) + w k ; c^' = c^ - beta (c^.k) k ; z'.q
+  float zqr = 0.0f, zqi = 0.0f;
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) {
+    const float ur = fmaf(-bb * pzr, kk[j], zr[j]);
+    const float ui = fmaf(-bb * pzi, kk[j], zi[j]);
+    zr[j] = fmaf(tr.ar, ur, fmaf(-tr.ai, ui, wr * kk[j]));
+    zi[j] = fmaf(tr.ar, ui, fmaf(tr.ai, ur, wi * kk[j]));
+    cr[j] = fmaf(-bb * pcr, kk[j], cr[j]);
+    ci[j] = fmaf(-bb * pci, kk[j], ci[j]);
+    zqr = fmaf(zr[j], qq[j], zqr);
+    zqi = fmaf(zi[j], qq[j], zqi);
+  }
+  zqr = group_sum<LPH>(zqr);
+  zqi = group_sum<LPH>(zqi);
+  const float yr = sc * (zqr + (g.x * cqr - g.y * cqi));
+  const float yi = sc * (zqi + (g.x * cqi + g.y * cqr));
+  const float2 gn = make_float2(g.x * tr.ar - g.y * tr.ai, g.x * tr.ai + g.y * tr.ar);
+
+  if (!hok) return;  // nothing below reduces across lanes
+  if (sub == 0) {
+    T::store(y + 2 * bh, yr);
+    T::store(y + 2 * bh + 1, yi);
+  }
+  // carry after the token: g' s + z' (also the next chunk's start at a chunk end)
+  const bool chunk_end = jpos + 1 >= Q;
+  if (chunk_end || h_out) {
+    float sr[DPL], si[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; j += 4) {
+      const float4 a4 = *reinterpret_cast<const float4*>(st + 4 * D + j);
+      const float4 a5 = *reinterpret_cast<const float4*>(st + 5 * D + j);
+      sr[j] = a4.x; sr[j + 1] = a4.y; sr[j + 2] = a4.z; sr[j + 3] = a4.w;
+      si[j] = a5.x; si[j + 1] = a5.y; si[j + 2] = a5.z; si[j + 3] = a5.w;
+    }
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const float nr = fmaf(gn.x, sr[j], fmaf(-gn.y, si[j], zr[j]));
+      si[j] = fmaf(gn.x, si[j], fmaf(gn.y, sr[j], zi[j]));
+      sr[j] = nr;
+    }
+    if (h_out) {
+      float* ho = h_out + bh * 2 * D + sub * DPL;
+#pragma unroll
+      for (int j = 0; j < DPL; j += 4) {
+        *reinterpret_cast<float4*>(ho + j) = make_float4(sr[j], sr[j + 1], sr[j + 2], sr[j + 3]);
+        *reinterpret_cast<float4*>(ho + D + j) = make_float4(si[j], si[j + 1], si[j + 2], si[j + 3]);
+      }
+    }
+    if (chunk_end) {
+      // next chunk: z = 0, c^ = s = s', g = 1
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        zr[j] = zi[j] = 0.0f;
+        cr[j] = sr[j];
+        ci[j] = si[j];
+      }
+#pragma unroll
+      for (int j = 0; j < DPL; j += 4) {
+        *reinterpret_cast<float4*>(st + 4 * D + j) = make_float4(sr[j], sr[j + 1], sr[j + 2], sr[j + 3]);
+        *reinterpret_cast<float4*>(st + 5 * D + j) = make_float4(si[j], si[j + 1], si[j + 2], si[j + 3]);
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < DPL; j += 4) {
+    *reinterpret_cast<float4*>(st + j) = make_float4(zr[j], zr[j + 1], zr[j + 2], zr[j + 3]);
+    *reinterpret_cast<float4*>(st + D + j) = make_float4(zi[j], zi[j + 1], zi[j + 2], zi[j + 3]);
+    *reinterpret_cast<float4*>(st + 2 * D + j) = make_float4(cr[j], cr[j + 1], cr[j + 2], cr[j + 3]);
+    *reinterpret_cast<float4*>(st + 3 * D + j) = make_float4(ci[j], ci[j + 1], ci[j + 2], ci[j + 3]);
+  }
+  if (sub == 0) {
+    gam[bh] = chunk_end ? make_float2(1.0f, 0.0f) : gn;
+    pos[bh] = chunk_end ? 0 : jpos + 1;
+  }
+}
+
+// state = (0, h, h) per (b, h) (h = 0 if null), g = 1, j = 0: the decode state
+// at a chunk boundary with carry h (the fused scan's h_final there).
+__global__ __launch_bounds__(256) void decode_init_kernel(const float* __restrict__ h, float* __restrict__ state,
+                                                          float2* __restrict__ gam, int* __restrict__ pos,
+                                                          int64_t BH, int D) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;  // (b, h, element of 2D)
+  if (i >= BH * 2 * D) return;
+  const int64_t bh = i / (2 * D);
+  const int e = int(i % (2 * D));  // row re (e < D) or im, element e % D
+  const float hv = h ? h[i] : 0.0f;
+  float* st = state + bh * 6 * D;
+  st[e] = 0.0f;          // z
+  st[2 * D + e] = hv;    // c^
+  st[4 * D + e] = hv;    // s
+  if (e == 0) {
+    gam[bh] = make_float2(1.0f, 0.0f);
+    pos[bh] = 0;
+  }
+}
+
+template <typename T, int D, int LPH>
+int launch_decode(const void* q, const void* k, const void* v, const void* beta, const void* sel_c,
+                  const void* dt, const void* r, const float* alpha, const float* omega, float c, float* state,
+                  float* gam, int* pos, void* y, float* h_out, int B, int H, int Q, hipStream_t stream) {
+  using raw = typename T::raw;
+  constexpr int HPW = kWave / LPH;
+  const int n_hg = (H + HPW - 1) / HPW;
+  hipLaunchKernelGGL((decode_step_kernel<T, D, LPH>), dim3(unsigned(int64_t(B) * n_hg)), dim3(kWave), 0, stream,
+                     static_cast<const raw*>(q), static_cast<const raw*>(k), static_cast<const raw*>(v),
+                     static_cast<const raw*>(beta), static_cast<const raw*>(sel_c), static_cast<const raw*>(dt),
+                     static_cast<const raw*>(r), alpha, omega, c, state, reinterpret_cast<float2*>(gam), pos,
+                     static_cast<raw*>(y), h_out, H, Q, n_hg);
+  return cdssm_host::check_launch("cdssm_decode_step");
+}
+
+}  // namespace cdssm
+
+using namespace cdssm;
+
+extern "C" int cdssm_decode_init(const float* h, float* state, float* gam, int* pos, int64_t B, int64_t H,
+                                 int64_t D, int64_t N, hipStream_t stream) {
+  const char* op = "cdssm_decode_init";
+  if (B <= 0 || H <= 0 || B * H > 0x7fffffffLL || N != 2 || (D != 64 && D != 128)) {
+    cdssm_host::set_error("%s: need B, H > 0, N = 2, D in {64, 128} (B=%lld H=%lld D=%lld N=%lld)", op,
+                          (long long)B, (long long)H, (long long)D, (long long)N);
+    return CDSSM_EINVAL;
+  }
+  if (!state || !gam || !pos) {
+    cdssm_host::set_error("%s: null pointer argument", op);
+    return CDSSM_EINVAL;
+  }
+  const int64_t n = B * H * 2 * D;
+  hipLaunchKernelGGL(decode_init_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, h, state,
+                     reinterpret_cast<float2*>(gam), pos, B * H, int(D));
+  return cdssm_host::check_launch(op);
+}
+
+extern "C" int cdssm_decode_step(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                                 const void* sel_c, const void* dt, const void* r, const float* alpha,
+                                 const float* omega, float c, float* state, float* gam, int* pos, void* y,
+                                 float* h_out, int64_t B, int64_t H, int64_t D, int64_t N, int64_t chunk,
+                                 hipStream_t stream) {
+  const char* op = "cdssm_decode_step";
+  if (dtype != 0 && dtype != 1) {
+    cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
+    return CDSSM_EINVAL;
+  }
+  if (B <= 0 || H <= 0 || B * H > 0x7fffffffLL || N != 2 || (D != 64 && D != 128) || chunk < 1 ||
+      chunk > 128) {
+    cdssm_host::set_error("%s: need B, H > 0, N = 2, D in {64, 128}, 1 <= chunk <= 128 "
+                          "(B=%lld H=%lld D=%lld N=%lld chunk=%lld)",
+                          op, (long long)B, (long long)H, (long long)D, (long long)N, (long long)chunk);
+    return CDSSM_EINVAL;
+  }
+  if (!q || !k || !v || !beta || !sel_c || !dt || !r || !alpha || !omega || !state || !gam || !pos || !y) {
+    cdssm_host::set_error("%s: null pointer argument", op);
+    return CDSSM_EINVAL;
+  }
+  const int b = int(B), hh = int(H), qc = int(chunk);
+  if (dtype == 1) {
+    if (D == 64)
+      return launch_decode<BF16, 64, 8>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, state, gam, pos, y, h_out, b,
+                                        hh, qc, stream);
+    return launch_decode<BF16, 128, 16>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, state, gam, pos, y, h_out, b,
+                                        hh, qc, stream);
+  }
+  if (D == 64)
+    return launch_decode<F32, 64, 16>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, state, gam, pos, y, h_out, b,
+                                      hh, qc, stream);
+  return launch_decode<F32, 128, 32>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, state, gam, pos, y, h_out, b,
+                                     hh, qc, stream);
+}

@@ -135,6 +135,33 @@ int cdssm_fused_scan_bwd_profile(int dtype, const void* q, const void* k, const 
 int cdssm_fused_scan_fwd_set_path(int mode);
 
 /*
+ * Recurrent decode: one new token per (b, h) with the R-mode state carried
+ * between calls.  No reference counterpart: the reference generates by
+ * re-running the whole forward for every new token (predict.py:53-67, through
+ * SSDChunkwiseScan.forward, ssd.py:39-111); the step gives the same outputs as
+ * that chunked scan over the longer sequence (same chunk boundaries).
+ * State (fp32, caller-owned, contiguous): state (B,H,3,N,D) = local state z,
+ * decay-free correction c^ and the carry s entering the current chunk;
+ * gam (B,H,N) = rotation product of the chunk so far; pos (B,H) int32 =
+ * position in the chunk.
+ * cdssm_decode_init: the state at a chunk boundary with carry h (B,H,N,D) fp32
+ * (the fused forward's h_final after a multiple of `chunk` tokens), or the
+ * zero state for h = NULL.
+ * cdssm_decode_step: token tensors q, k (B,H,D), v (B,H,N), beta, sel_c, dt,
+ * r (B,H) of `dtype` (a (B,1,H,.) slice of the scan inputs), alpha, omega (H,)
+ * fp32; writes y (B,H,N) of `dtype`, advances the state, and, if h_out is not
+ * NULL, writes the R-mode carry after the token to h_out (B,H,N,D) fp32 (what
+ * the fused forward returns as h_final for a sequence ending there).
+ * Supported: N = 2, D in {64, 128}, 1 <= chunk <= 128.
+ */
+int cdssm_decode_init(const float* h, float* state, float* gam, int* pos, int64_t B, int64_t H, int64_t D,
+                      int64_t N, hipStream_t stream);
+int cdssm_decode_step(int dtype, const void* q, const void* k, const void* v, const void* beta, const void* sel_c,
+                      const void* dt, const void* r, const float* alpha, const float* omega, float c,
+                      float* state, float* gam, int* pos, void* y, float* h_out, int64_t B, int64_t H, int64_t D,
+                      int64_t N, int64_t chunk, hipStream_t stream);
+
+/*
  * The reference's three scan passes as separate ops, same tensor contracts
  * (all tensors `dtype`, contiguous; N even, N <= 32; D <= 128).
  *

@@ -65,6 +65,35 @@ def test_fused_fwd_rejects_invalid_arguments_without_launching(bad, msg):
     assert msg in _lib.last_error()
 
 
+def _decode_call(lib, **over):
+    args = dict(dtype=1, q=16, k=16, v=16, beta=16, sel_c=16, dt=16, r=16, alpha=16, omega=16, c=1.0,
+                state=16, gam=16, pos=16, y=16, h_out=None, B=2, H=3, D=64, N=2, chunk=64, stream=None)
+    args.update(over)
+    return lib.cdssm_decode_step(*args.values())
+
+
+@pytest.mark.parametrize("bad,msg", [
+    (dict(dtype=3), "dtype"),
+    (dict(N=4), "N = 2"),
+    (dict(D=32), "D in"),
+    (dict(chunk=0), "chunk"),
+    (dict(B=0), "B, H > 0"),
+    (dict(state=None), "null"),
+])
+def test_decode_step_rejects_invalid_arguments_without_launching(bad, msg):
+    lib = _lib.load()
+    assert _decode_call(lib, **bad) == -1
+    assert msg in _lib.last_error()
+
+
+def test_decode_init_rejects_invalid_arguments_without_launching():
+    lib = _lib.load()
+    assert lib.cdssm_decode_init(None, 16, 16, 16, 1, 2, 96, 2, None) == -1
+    assert "D in" in _lib.last_error()
+    assert lib.cdssm_decode_init(None, None, 16, 16, 1, 2, 64, 2, None) == -1
+    assert "null" in _lib.last_error()
+
+
 def test_workspace_size_formula():
     lib = _lib.load()
     B, L, H, D, N, Q = 8, 4096, 16, 64, 2, 64
