@@ -139,6 +139,62 @@ def time_fwd_bwd(cfg_name, steps, warmup):
             "alg_bytes": alg, "phase_ms": phases}
 
 
+def time_decode(steps, warmup, B=64, H=16, D=64, prompt=2048):
+    """Recurrent decode at the config-4 decode shape, one layer: B64 H16 D64 bf16
+    from a 2048-token prompt (fused scan over the prompt, then decode steps).
+    `steps` back-to-back cdssm_decode_step calls between two events on the launch
+    stream; the token inputs are those of position `prompt` (synthetic)."""
+    import ctypes
+    import torch
+    from cdssm_hip import _lib
+    from cdssm_hip.decode import DecodeState
+    from cdssm_hip.scan import chunkwise_delta_scan
+    from cdssm_hip.workloads import ScanConfig, draw_inputs
+
+    cfg = ScanConfig("decode", B=B, H=H, L=prompt + 1, D=D)
+    dev = torch.device("cuda:0")
+    x = draw_inputs(cfg, seed=0)
+    g = {n: (t.to(dev) if isinstance(t, torch.Tensor) else t) for n, t in x.items()}
+    keys = ("q", "k", "v", "beta", "sel_C", "dt", "r")
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    pre = [g[n][:, :prompt].contiguous() for n in keys]
+    _, h = chunkwise_delta_scan(*pre, g["alpha"], g["omega"], g["c"])
+    e0.record(stream)
+    _, h = chunkwise_delta_scan(*pre, g["alpha"], g["omega"], g["c"])  # warm: the prompt's fused scan
+    e1.record(stream)
+    torch.cuda.synchronize()
+    prefill_ms = e0.elapsed_time(e1)
+    del pre
+    st = DecodeState.at_boundary(h, B, H, D, D, dev)
+    tok = [g[n][:, prompt].contiguous() for n in keys]
+    y = torch.empty(B, H, 2, dtype=torch.bfloat16, device=dev)
+    lib = _lib.load()
+    fn = lib.cdssm_decode_step
+    args = [1] + [_lib.ptr(t) for t in tok] + [_lib.ptr(g["alpha"]), _lib.ptr(g["omega"]), ctypes.c_float(g["c"]),
+                                                _lib.ptr(st.state), _lib.ptr(st.gam), _lib.ptr(st.pos), _lib.ptr(y),
+                                                None, B, H, D, 2, D, _lib.stream_of(dev)]
+    for _ in range(warmup):
+        _lib.check(fn(*args), "cdssm_decode_step")
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        fn(*args)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    # per (b, h): z and c^ read and written (4 D fp32 each way), q and k (2 D bf16),
+    # v, beta, sel_C, dt, r (6 bf16), y (2 bf16); the carry s at chunk ends only (1/Q)
+    Q = D
+    per_bh = 16 * D + 16 * D + 4 * D + 12 + 4 + 16 * D / Q
+    alg = B * H * per_bh
+    return {"workload": f"decode B{B} H{H} D{D} bf16, one layer, from a {prompt}-token prompt",
+            "us_per_step": us, "tokens_per_s": B / (us * 1e-6), "alg_bytes_per_step": alg,
+            "achieved_GBs": alg / (us * 1e-6) / 1e9, "hbm_frac": alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "prefill_ms": prefill_ms, "prefill_note": "fused scan over the prompt (one call, warm)",
+            "note": "steps launched back to back from Python through ctypes; per-step time includes the launch"}
+
+
 def cpu_baseline(cfg, x, batches, min_seconds=10.0):
     """Time the fp32 oracle (CPU restatement of ops.py's R-mode scan) on
     `batches` batch rows of the workload, all heads, full length, repeated
@@ -287,6 +343,7 @@ def main():
     }
     if not args.no_fwd_bwd:
         out["fwd_bwd"] = [time_fwd_bwd(n, 20, 3) for n in ("C1", "C2")]
+        out["decode"] = time_decode(200, 20)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg, x, args.cpu_sample_batches)
     print(json.dumps(out), flush=True)
