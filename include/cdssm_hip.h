@@ -45,10 +45,11 @@ const char* cdssm_last_error(void);
  * workspace: cdssm_fused_scan_workspace_bytes() bytes of device memory, any
  * contents (scratch for this call; the backward takes the workspace of
  * cdssm_fused_scan_fwd_train instead).  Supported: N = 2, D in {64, 128},
- * 1 <= chunk <= 128.  Where the whole grid fits on the device at once and a
- * sequence has at most 64 segments of 4 chunks, the scan runs as one launch
- * (chunk maps composed by a look-back between workgroups); otherwise as four
- * (chunk summaries, carry fold, carry replay, main pass).
+ * 1 <= chunk <= 128.  Where every segment of 4 chunks fits in one round of
+ * resident workgroups (or, for this inference forward, the segments fill
+ * whole rounds of a persistent grid), the scan runs as one launch (chunk maps
+ * composed by a look-back between workgroups); otherwise as four (chunk
+ * summaries, carry fold, carry replay, main pass).
  */
 int64_t cdssm_fused_scan_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
                                          int64_t chunk);
@@ -61,10 +62,12 @@ int cdssm_fused_scan_fwd(int dtype, const void* q, const void* k, const void* v,
 /*
  * Training forward (no counterpart in the reference; the reference keeps its
  * passes' full outputs for backward instead): the forward above, which also
- * stores in the workspace, per (token, head), the dot products of the chunk
- * recurrences (p_t = z_{t-1}.k_t, c^_t.k_t, c^_{t+1}.q_t, Y_t.q_t; 32 bytes)
- * so that the backward recomputes the chunk states without reductions.  Same
- * arguments and workspace size as cdssm_fused_scan_fwd.
+ * stores in the workspace what the backward reads: per (token, head) the dot
+ * products of the chunk recurrences (p_t = z_{t-1}.k_t, c^_t.k_t,
+ * c^_{t+1}.q_t, Y_t.q_t; 32 bytes) and g_t, the local state every 4 tokens and
+ * the correction state after every chunk, so that the backward rebuilds the
+ * chunk states without reductions or a forward recompute.  Same arguments and
+ * workspace size as cdssm_fused_scan_fwd.
  */
 int cdssm_fused_scan_fwd_train(int dtype, const void* q, const void* k, const void* v, const void* beta,
                                const void* sel_c, const void* dt, const void* r, const float* alpha,
