@@ -1324,6 +1324,12 @@ int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, cons
     cdssm_host::set_error("%s: problem too large", op);
     return CDSSM_EINVAL;
   }
+  // q/k/dq/dk rows of a chunk tile are addressed by 32-bit byte offsets
+  if ((chunk + 16) * H * D * 4 > 0x7fffffffLL) {
+    cdssm_host::set_error("%s: H * D too large for 32-bit row offsets (H=%lld D=%lld)", op, (long long)H,
+                          (long long)D);
+    return CDSSM_EINVAL;
+  }
   if (!q || !k || !v || !beta || !sel_c || !dt || !r || !alpha || !omega || !dy || !fwd_workspace ||
       !dq || !dk || !dv || !dbeta || !dsel || !ddt || !dr || !dalpha || !domega || !workspace) {
     cdssm_host::set_error("%s: null pointer argument", op);

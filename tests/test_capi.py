@@ -57,12 +57,22 @@ def _fused_call(lib, **over):
     (dict(B=0), "positive"),
     (dict(q=None), "null"),
     (dict(k=8), "aligned"),
+    (dict(H=1 << 19, D=128), "32-bit row offsets"),
 ])
 def test_fused_fwd_rejects_invalid_arguments_without_launching(bad, msg):
     lib = _lib.load()
     st = _fused_call(lib, **bad)
     assert st == -1
     assert msg in _lib.last_error()
+
+
+def test_fused_bwd_rejects_rows_beyond_32_bit_offsets_without_launching():
+    lib = _lib.load()
+    ptrs = [16] * 9
+    st = lib.cdssm_fused_scan_bwd(1, *ptrs, 1.0, 16, None, 16, *([16] * 9), None, 16,
+                                  1, 64, 1 << 19, 128, 2, 64, None)
+    assert st == -1
+    assert "32-bit row offsets" in _lib.last_error()
 
 
 def _decode_call(lib, **over):
