@@ -974,15 +974,15 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
         R.q[i].unpack(qq);
         float red[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
         float dqv[DPL];
+        // dq = Re(conj(f) Y_t), Y_t = z_t + g_{t-1} c^_t, f = (s1.y, -s1.z), g_{t-1} = (s2.z, s2.w):
+        // the c^ part's weight conj(f) g_{t-1} is formed once per token
+        const float wcr = s2.z * s1.y + s2.w * s1.z, wci = s2.z * s1.z - s2.w * s1.y;
 #pragma unroll
         for (int jj = 0; jj < DPL; ++jj) {
           // c^_t = c^_{t+1} + beta pc k
           cr[jj] = fmaf(bb * pcr, kk[jj], cr[jj]);
           ci[jj] = fmaf(bb * pci, kk[jj], ci[jj]);
-          // dq = Re(conj(f) Y_t), Y_t = z_t + g_{t-1} c^_t
-          const float Yr = zbr[i + 1][jj] + s2.z * cr[jj] - s2.w * ci[jj];
-          const float Yi = zbi[i + 1][jj] + s2.z * ci[jj] + s2.w * cr[jj];
-          dqv[jj] = Yr * s1.y + Yi * s1.z;
+          dqv[jj] = fmaf(zbr[i + 1][jj], s1.y, fmaf(zbi[i + 1][jj], s1.z, fmaf(cr[jj], wcr, ci[jj] * wci)));
           mr[jj] = fmaf(s1.y, qq[jj], mr[jj]);
           mi[jj] = fmaf(s1.z, qq[jj], mi[jj]);
           lr[jj] = fmaf(s2.x, qq[jj], lr[jj]);
