@@ -47,6 +47,7 @@ SIGNATURES = {
     "cdssm_fused_scan_bwd_profile": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _P, _P, _P,
                                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                             _I64, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P]),
+    "cdssm_fused_scan_fwd_abar": (_I32, [_I32] + [_P] * 11 + [_I64] * 6 + [_P]),
     "cdssm_decode_init": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "cdssm_decode_step": (_I32, [_I32] + [_P] * 9 + [_F32] + [_P] * 5 + [_I64] * 5 + [_P]),
     "cdssm_intra_chunk_scan_fwd": (_I32, [_I32] + [_P] * 6 + [_I64] * 5 + [_P]),

@@ -96,6 +96,42 @@ def chunkwise_delta_scan_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_
     return y, h_final, ws
 
 
+def chunkwise_delta_scan_abar(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_C: Tensor, A_bar: Tensor,
+                              vp: Tensor, h0: Optional[Tensor] = None,
+                              chunk_size: Optional[int] = None) -> Tuple[Tensor, Tensor]:
+    """The fused scan on gate-level inputs (cdssm_fused_scan_fwd_abar), inference only.
+
+    ``A_bar`` (B,L,H,2) and ``vp`` (B,L,H,1) are DynamicsFusedFn's outputs; the result is
+    ``sel_C * einsum('blhsd,blhd->blhs', SSDChunkwiseScan(Q, 2)(A_bar, k, v * vp, beta), q)``
+    (block.py:194-211 without the shortcut) and the final R-mode state (B,H,2,D) fp32.
+    """
+    if not isinstance(A_bar, torch.Tensor) or not isinstance(vp, torch.Tensor):
+        raise TypeError("A_bar and vp must be tensors")
+    B, L, H, D = q.shape
+    if tuple(A_bar.shape) != (B, L, H, 2) or tuple(vp.shape) != (B, L, H, 1):
+        raise ValueError(f"A_bar must be ({B}, {L}, {H}, 2) and vp ({B}, {L}, {H}, 1), got "
+                         f"{tuple(A_bar.shape)} and {tuple(vp.shape)}")
+    if A_bar.dtype != q.dtype or vp.dtype != q.dtype or A_bar.device != q.device or vp.device != q.device:
+        raise TypeError("A_bar and vp must have q's dtype and device")
+    # shape/dtype checks of the other inputs (A_bar and vp stand in for dt and r there)
+    ones = torch.empty(H, dtype=torch.float32, device=q.device)
+    _, _, _, _, N, Q, dtype = _validate(q, k, v, beta, sel_C, beta, beta, ones, ones, h0, chunk_size)
+    lib = _lib.load()
+    ins = [t.contiguous() for t in (q, k, v, beta, sel_C, A_bar, vp)]
+    h0c = h0.contiguous() if h0 is not None else None
+    y = torch.empty(B, L, H, N, dtype=dtype, device=q.device)
+    h_final = torch.empty(B, H, N, D, dtype=torch.float32, device=q.device)
+    nbytes = lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, N, Q)
+    if nbytes <= 0:
+        raise RuntimeError(f"cdssm_fused_scan_workspace_bytes rejected the shape ({nbytes})")
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=q.device)
+    st = lib.cdssm_fused_scan_fwd_abar(_lib.DTYPE_CODE[dtype], *[_lib.ptr(t) for t in ins], _lib.ptr(h0c),
+                                       _lib.ptr(y), _lib.ptr(h_final), _lib.ptr(ws), B, L, H, D, N, Q,
+                                       _lib.stream_of(q.device))
+    _lib.check(st, "cdssm_fused_scan_fwd_abar")
+    return y, h_final
+
+
 FORWARD_PATHS = {"auto": 0, "four_launch": 1, "one_pass": 2}
 
 

@@ -66,6 +66,21 @@ struct F32 {
   __device__ __forceinline__ static void store(raw* p, float v) { *p = v; }
 };
 
+// Input form of the fused forward: ABar<T> (elements of type T) takes the
+// per-token transition a_t (B,L,H,2) and VP scale (B,L,H,1) as computed by the
+// gate-level dynamics (in place of dt and r), instead of the scan-level
+// (dt, r, alpha, omega, c) from which the kernels compute them.
+template <typename Base>
+struct ABar : Base {};
+template <typename T>
+struct IsABar {
+  static constexpr bool value = false;
+};
+template <typename Base>
+struct IsABar<ABar<Base>> {
+  static constexpr bool value = true;
+};
+
 // A wave's (chunk, head group) tile of a (B, L, H, D) tensor as a buffer
 // resource: the base (wave-uniform, scalar registers) is the tile's first row
 // at its first head, each lane adds its constant byte offset (head, slice),

@@ -152,21 +152,29 @@ __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, i
   const int hj = tc.hbase + j;
   const bool hok = hj < H;
   const int hl = hok ? hj : H - 1;
-  const float al = alpha[hl], om = omega[hl];
+  constexpr bool kAbar = IsABar<T>::value;  // a_t and vp_t given (dt -> a (B,L,H,2), r -> vp)
+  const float al = kAbar ? 0.0f : alpha[hl], om = kAbar ? 0.0f : omega[hl];
   const int glast = j * NB + NB - 1;  // the head's last lane
 
   ResetMask rm{0ull, 0ull};
   float cL = 0.0f, cfr = 1.0f, cfi = 0.0f, cgr = 1.0f, cgi = 0.0f;  // carries from earlier slabs
   for (int tl = 0; tl < ntr; tl += kWave) {
     const int t0 = tl + blk * TPB;
-    float bb[TPB], dd[TPB], rr[TPB], v0[TPB], v1[TPB], sc[TPB];
+    float bb[TPB], dd[TPB], rr[TPB], v0[TPB], v1[TPB], sc[TPB], vq[TPB];
 #pragma unroll
     for (int i = 0; i < TPB; ++i) {
       const int t = min(t0 + i, tc.nt - 1);
       const int64_t e = (tc.row0 + t) * H + hl;
       bb[i] = T::load(beta + e);
-      dd[i] = T::load(dt + e);
-      rr[i] = T::load(r + e);
+      if constexpr (kAbar) {
+        dd[i] = T::load(dt + 2 * e);  // a_t re, im
+        rr[i] = T::load(dt + 2 * e + 1);
+        vq[i] = T::load(r + e);  // vp_t
+      } else {
+        dd[i] = T::load(dt + e);
+        rr[i] = T::load(r + e);
+        vq[i] = 0.0f;
+      }
       v0[i] = T::load(v + 2 * e);
       v1[i] = T::load(v + 2 * e + 1);
       sc[i] = MAIN ? T::load(sel_c + e) : 0.0f;
@@ -183,7 +191,7 @@ __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, i
 #pragma unroll
     for (int i = 0; i < TPB; ++i) {
       const bool real = hok && t0 + i < tc.nt;
-      const Transition tr = cayley_gated(dd[i], rr[i], al, om, c);
+      const Transition tr = kAbar ? Transition{dd[i], rr[i], vq[i]} : cayley_gated(dd[i], rr[i], al, om, c);
       const float f = bb[i] * tr.vp;
       ar[i] = real ? tr.ar : 1.0f;
       ai[i] = real ? tr.ai : 0.0f;
@@ -1271,6 +1279,9 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
                      hipStream_t stream, hipEvent_t* ev, bool save, int* path) {
   using raw = typename T::raw;
   constexpr int HPW = kWave / LPH, HPWS = kWave / LPHS;
+  // the a_t input form is inference-only: its training branches name the
+  // inference kernels (never taken: save is false for it)
+  constexpr bool kSv = !IsABar<T>::value;
   const FwdLayout w = fwd_layout(B, L, H, D, Q);
   const int NC = w.NC, S = w.S;
   const int n_hg = (H + HPW - 1) / HPW, n_hgs = (H + HPWS - 1) / HPWS;
@@ -1297,9 +1308,9 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
     // segments than that: the persistent one-pass only for inference with
     // full rounds (measured on MI355X: faster than four launches at C3,
     // slower at C2's 1.5 rounds and for the training forward's records)
-    const int cap1 = save ? onepass_capacity<T, D, LPH, true, false>(lds)
+    const int cap1 = save ? onepass_capacity<T, D, LPH, kSv, false>(lds)
                           : onepass_capacity<T, D, LPH, false, false>(lds);
-    const int capp = save ? onepass_capacity<T, D, LPH, true, true>(lds)
+    const int capp = save ? onepass_capacity<T, D, LPH, kSv, true>(lds)
                           : onepass_capacity<T, D, LPH, false, true>(lds);
     const bool single = cap1 > 0 && items <= cap1;
     const bool forced = cdssm_host::scan_path() == cdssm_host::kPathOne;
@@ -1347,9 +1358,9 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
         for (int i = 0; i < 4; ++i) (void)hipEventRecord(ev[i], stream);
       const dim3 gd = dim3(unsigned(grid)), bd = dim3(kWave * kOnePassW);
       if (save && single)
-        hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, true, false>), gd, bd, lds, stream, a);
+        hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, kSv, false>), gd, bd, lds, stream, a);
       else if (save)
-        hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, true, true>), gd, bd, lds, stream, a);
+        hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, kSv, true>), gd, bd, lds, stream, a);
       else if (single)
         hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, false, false>), gd, bd, lds, stream, a);
       else
@@ -1390,7 +1401,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
 
   const size_t lds_main = size_t(slots) * (2 * sizeof(float4) + 2 * sizeof(float2));
   if (save)
-    hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH, true>), dim3(unsigned(tiles)), dim3(kWave), lds_main,
+    hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH, kSv>), dim3(unsigned(tiles)), dim3(kWave), lds_main,
                        stream, (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,
                        (const raw*)dt, (const raw*)r, alpha, omega, c, (const float2*)summ, (raw*)y, saved,
                        gsaved, zck, cend, L, H, Q, NC, w.NCK, n_hg);
@@ -1419,8 +1430,9 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
                     const void* sel_c, const void* dt, const void* r, const float* alpha,
                     const float* omega, float c, const float* h0, void* y, float* h_final,
                     float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
-                    int64_t chunk, hipStream_t stream, hipEvent_t* ev, bool save, int* path = nullptr) {
-  const char* op = "cdssm_fused_scan_fwd";
+                    int64_t chunk, hipStream_t stream, hipEvent_t* ev, bool save, int* path = nullptr,
+                    bool abar = false) {
+  const char* op = abar ? "cdssm_fused_scan_fwd_abar" : "cdssm_fused_scan_fwd";
   if (dtype != 0 && dtype != 1) {
     cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
     return CDSSM_EINVAL;
@@ -1452,7 +1464,7 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
                           (long long)D);
     return CDSSM_EINVAL;
   }
-  if (!q || !k || !v || !beta || !sel_c || !dt || !r || !alpha || !omega || !y || !h_final ||
+  if (!q || !k || !v || !beta || !sel_c || !dt || !r || (!abar && (!alpha || !omega)) || !y || !h_final ||
       !workspace) {
     cdssm_host::set_error("%s: null pointer argument", op);
     return CDSSM_EINVAL;
@@ -1462,18 +1474,29 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
     return CDSSM_EINVAL;
   }
   const int b = int(B), l = int(L), hh = int(H), qc = int(chunk);
+#define CDSSM_FWD_ARGS q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace, b, l, hh, qc, stream, \
+                       ev, save, path
+  if (abar) {
+    if (save) {
+      cdssm_host::set_error("%s: the a_t input form has no training forward", op);
+      return CDSSM_EINVAL;
+    }
+    if (dtype == 1) {
+      if (D == 64)
+        return launch_fused_fwd<ABar<BF16>, 64, CDSSM_FWD_LPH_BF16_D64, CDSSM_FWD_LPHS_BF16_D64>(CDSSM_FWD_ARGS);
+      return launch_fused_fwd<ABar<BF16>, 128, 16, CDSSM_FWD_LPHS_BF16_D128>(CDSSM_FWD_ARGS);
+    }
+    if (D == 64) return launch_fused_fwd<ABar<F32>, 64, 16, 16>(CDSSM_FWD_ARGS);
+    return launch_fused_fwd<ABar<F32>, 128, 32, 32>(CDSSM_FWD_ARGS);
+  }
   if (dtype == 1) {
     if (D == 64)
-      return launch_fused_fwd<BF16, 64, CDSSM_FWD_LPH_BF16_D64, CDSSM_FWD_LPHS_BF16_D64>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                           workspace, b, l, hh, qc, stream, ev, save, path);
-    return launch_fused_fwd<BF16, 128, 16, CDSSM_FWD_LPHS_BF16_D128>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                           workspace, b, l, hh, qc, stream, ev, save, path);
+      return launch_fused_fwd<BF16, 64, CDSSM_FWD_LPH_BF16_D64, CDSSM_FWD_LPHS_BF16_D64>(CDSSM_FWD_ARGS);
+    return launch_fused_fwd<BF16, 128, 16, CDSSM_FWD_LPHS_BF16_D128>(CDSSM_FWD_ARGS);
   }
-  if (D == 64)
-    return launch_fused_fwd<F32, 64, 16, 16>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                         workspace, b, l, hh, qc, stream, ev, save, path);
-  return launch_fused_fwd<F32, 128, 32, 32>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final,
-                                        workspace, b, l, hh, qc, stream, ev, save, path);
+  if (D == 64) return launch_fused_fwd<F32, 64, 16, 16>(CDSSM_FWD_ARGS);
+  return launch_fused_fwd<F32, 128, 32, 32>(CDSSM_FWD_ARGS);
+#undef CDSSM_FWD_ARGS
 }
 }  // namespace
 
@@ -1485,6 +1508,18 @@ extern "C" int cdssm_fused_scan_fwd(int dtype, const void* q, const void* k, con
                                     int64_t chunk, hipStream_t stream) {
   return fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace,
                          B, L, H, D, N, chunk, stream, nullptr, false);
+}
+
+// The fused forward on gate-level inputs: a_t (B,L,H,2) and vp_t (B,L,H,1) of
+// `dtype` (DynamicsFusedFn's A_bar and vp_scale) in place of dt, r, alpha,
+// omega and c.
+extern "C" int cdssm_fused_scan_fwd_abar(int dtype, const void* q, const void* k, const void* v,
+                                         const void* beta, const void* sel_c, const void* a_bar,
+                                         const void* vp, const float* h0, void* y, float* h_final,
+                                         float* workspace, int64_t B, int64_t L, int64_t H, int64_t D,
+                                         int64_t N, int64_t chunk, hipStream_t stream) {
+  return fused_fwd_entry(dtype, q, k, v, beta, sel_c, a_bar, vp, nullptr, nullptr, 0.0f, h0, y, h_final, workspace,
+                         B, L, H, D, N, chunk, stream, nullptr, false, nullptr, true);
 }
 
 extern "C" int cdssm_fused_scan_fwd_train(int dtype, const void* q, const void* k, const void* v,

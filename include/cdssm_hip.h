@@ -60,6 +60,20 @@ int cdssm_fused_scan_fwd(int dtype, const void* q, const void* k, const void* v,
                          int64_t chunk, hipStream_t stream);
 
 /*
+ * The fused forward on gate-level inputs, for the model's block
+ * (block.py:177-211): instead of the scan-level dt, r, alpha, omega, c it takes
+ * the transition a_bar (B,L,H,N) and VP scale vp (B,L,H,N/2), both of `dtype`,
+ * as DynamicsFusedFn produces them (ops.py:39-66, dynamics_fused.cu:35-140),
+ * and computes SSDChunkwiseScan(A_bar, K, V * vp, beta) (ssd.py:39-111) with the
+ * readout y = sel_C (Y . q) (block.py:194-211, shortcut excluded).  Other
+ * arguments, workspace and limits as cdssm_fused_scan_fwd.  Inference only.
+ */
+int cdssm_fused_scan_fwd_abar(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                              const void* sel_c, const void* a_bar, const void* vp, const float* h0, void* y,
+                              float* h_final, float* workspace, int64_t B, int64_t L, int64_t H, int64_t D,
+                              int64_t N, int64_t chunk, hipStream_t stream);
+
+/*
  * Training forward (no counterpart in the reference; the reference keeps its
  * passes' full outputs for backward instead): the forward above, which also
  * stores in the workspace what the backward reads: per (token, head) the dot
