@@ -48,6 +48,7 @@ SIGNATURES = {
                                             _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                             _I64, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P]),
     "cdssm_fused_scan_fwd_abar": (_I32, [_I32] + [_P] * 11 + [_I64] * 6 + [_P]),
+    "cdssm_conv1d_silu_fwd": (_I32, [_I32] + [_P] * 4 + [_I64] * 4 + [_P]),
     "cdssm_decode_init": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "cdssm_decode_step": (_I32, [_I32] + [_P] * 9 + [_F32] + [_P] * 5 + [_I64] * 5 + [_P]),
     "cdssm_intra_chunk_scan_fwd": (_I32, [_I32] + [_P] * 6 + [_I64] * 5 + [_P]),

@@ -1,0 +1,294 @@
+"""CD-SSM language model forward on the MI355X kernels (the scan's caller).
+
+Mirrors the reference model (model.py:12-51, block.py:14-229, modules.py:14-53,
+init.py:13-126, config/model.py:38-178) with the same module and parameter
+names, so a reference ``state_dict`` loads unchanged.  Per block:
+RMSNorm -> in_proj -> value residual -> conv1d+SiLU (HIP) -> gate_proj ->
+DynamicsFusedFn (HIP) -> NormalizeKQFn (HIP) -> fused scan with the sel_C
+readout on the gate-level A_bar / vp (HIP, ``cdssm_fused_scan_fwd_abar``) ->
+current-token shortcut -> readout_proj -> fp32 GroupNorm -> * silu(z) -> + D x
+-> out_proj -> residual.  Dense projections, norms and the embedding are
+PyTorch (hipBLASLt GEMMs).  Forward only: the conv and the a_t-input scan have
+no backward here.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib
+from .ops import DynamicsFusedFn, NormalizeKQFn
+from .scan import chunkwise_delta_scan_abar
+
+Tensor = torch.Tensor
+
+_BF16_EPS = 2.0 ** -7  # torch.finfo(torch.bfloat16).eps
+
+
+@dataclass
+class CDSSMConfig:
+    """The reference's config surface and derived constants (config/model.py:38-178).
+
+    ``d_inner`` defaults to the reference's 2 * d_model (config/model.py:57);
+    pass it explicitly for other widths (the config-4 workload states
+    16 heads x 64 = 1024 = d_model).
+    """
+
+    d_model: int = 768
+    n_layers: int = 12
+    context_length: int = 8192
+    vocab_size: int = 50257
+    state_dim: int = 16
+    d_inner: Optional[int] = None
+    head_dim: int = 64
+    n_heads: int = field(init=False)
+    chunk_size: int = field(init=False)
+    ssm_norm_groups: int = field(init=False)
+    conv_kernel_size: int = field(init=False)
+    rope_base: float = field(init=False)
+    gating_c: float = field(init=False)
+    spectral_band_fraction: float = field(init=False)
+    eps_norm: float = field(init=False)
+    eps_log_argument: float = field(init=False)
+    eps_adaptive_dt: float = field(init=False)
+    init_biases: dict = field(init=False)
+    bf16_omega_thresh: float = field(init=False)
+    bf16_delta: float = field(init=False)
+    bf16_smoothness: float = field(init=False)
+
+    def __post_init__(self):
+        if self.state_dim % 2:
+            raise ValueError("state_dim must be even (complex pairs)")
+        if self.d_inner is None:
+            self.d_inner = 2 * self.d_model
+        if self.d_inner % self.head_dim:
+            raise ValueError("d_inner must be a multiple of head_dim")
+        self.n_heads = self.d_inner // self.head_dim
+        self.chunk_size = self.head_dim
+        self.ssm_norm_groups = 32
+        self.conv_kernel_size = max(2, self.head_dim // 16)
+        self.rope_base = float(self.context_length)
+        self.gating_c = math.log(self.context_length)
+        self.spectral_band_fraction = 2.0 / (self.n_layers + 1)
+        self.eps_norm = _BF16_EPS ** 2
+        self.eps_log_argument = _BF16_EPS ** 2
+        self.eps_adaptive_dt = 1.0
+        ln2 = math.log(2.0)
+        self.init_biases = {"sel_B_bias": ln2, "sel_C_bias": ln2, "r_gate_bias": ln2,
+                            "beta_bias": 0.0, "sel_dt_bias": 0.0}
+        self.bf16_omega_thresh = math.sqrt(_BF16_EPS)
+        self.bf16_delta = 16.0 * _BF16_EPS
+        self.bf16_smoothness = self.bf16_omega_thresh / 5.0
+
+
+def layer_stds(d_model: int, d_inner: int, n_layers: int) -> dict:
+    """T-Fixup depth-scaled init stds (init.py:13-41)."""
+    depth = 1.0 / math.sqrt(2 * n_layers)
+    return {
+        "embedding": math.sqrt(1.0 / d_model),
+        "in_proj": math.sqrt(2.0 / (d_model + d_inner)) * depth,
+        "dynamics_proj": math.sqrt(2.0 / (2 * d_inner)) * depth / math.sqrt(n_layers),
+        "out_proj": math.sqrt(2.0 / (d_model + d_inner)) * depth,
+    }
+
+
+def spectral_biases(cfg: CDSSMConfig, layer_idx: int):
+    """Per-pair alpha / omega gate biases of a layer (init.py:44-126): log-spaced
+    timescales in a band that slides from short to long with depth; alpha = 1/tau
+    through an inverse softplus, omega log-spaced between the band's frequencies."""
+    H, nh = cfg.n_heads, cfg.state_dim // 2
+    lo, hi = 0.0, math.log(float(cfg.context_length))
+    width = cfg.spectral_band_fraction * (hi - lo)
+    start = lo + layer_idx / max(cfg.n_layers - 1, 1) * (hi - lo - width)
+    step = width / max(nh, 1)
+    alphas, omegas = [], []
+    for j in range(nh):
+        j0 = start + j * step / nh
+        j1 = j0 + width
+        tau = torch.exp(torch.linspace(j0, j1, H))
+        a = 1.0 / tau
+        alphas.append(torch.log(torch.exp(a) - 1 + cfg.eps_log_argument))
+        f_lo = max(1.0 / math.exp(j1), cfg.eps_log_argument)
+        f_hi = min(0.5, 1.0 / math.exp(j0))
+        omegas.append(torch.exp(torch.linspace(math.log(f_lo), math.log(f_hi), H)))
+    return alphas, omegas
+
+
+class _Conv1dSiLUFn(torch.autograd.Function):
+    """CUDAConv1dSiLUOp (ops.py:13-28) forward through cdssm_conv1d_silu_fwd."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
+        return conv1d_silu(x, weight, bias)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        raise NotImplementedError("conv1d+SiLU backward is not part of this build (forward-only model path)")
+
+
+def conv1d_silu(x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
+    """silu(causal depthwise conv1d(x) + bias); x (B, L, C), weight (C, 1, K) or (C, K), bias (C)."""
+    if x.device.type != "cuda":
+        raise RuntimeError("conv1d_silu runs on the GPU only")
+    if x.dtype not in _lib.DTYPE_CODE:
+        raise TypeError(f"x must be float32 or bfloat16, got {x.dtype}")
+    B, L, C = x.shape
+    K = weight.shape[-1]
+    if weight.numel() != C * K or tuple(bias.shape) != (C,):
+        raise ValueError(f"weight must be ({C}, 1, K) and bias ({C},), got {tuple(weight.shape)}, {tuple(bias.shape)}")
+    xc = x.contiguous()
+    wc = weight.to(x.dtype).contiguous()
+    bc = bias.to(x.dtype).contiguous()
+    y = torch.empty_like(xc)
+    st = _lib.load().cdssm_conv1d_silu_fwd(_lib.DTYPE_CODE[x.dtype], _lib.ptr(xc), _lib.ptr(wc), _lib.ptr(bc),
+                                          _lib.ptr(y), B, L, C, K, _lib.stream_of(x.device))
+    _lib.check(st, "cdssm_conv1d_silu_fwd")
+    return y
+
+
+class Conv1dSiLU(nn.Module):
+    """Depthwise causal conv1d + SiLU (modules.py:14-35); weight (C, 1, K), bias (C)."""
+
+    def __init__(self, d_inner: int, kernel_size: int = 4):
+        super().__init__()
+        self.d_inner = d_inner
+        self.kernel_size = kernel_size
+        self.weight = nn.Parameter(torch.empty(d_inner, 1, kernel_size))
+        self.bias = nn.Parameter(torch.zeros(d_inner))
+        with torch.no_grad():
+            nn.init.normal_(self.weight, std=1.0 / math.sqrt(kernel_size))
+
+    def forward(self, x: Tensor) -> Tensor:
+        return _Conv1dSiLUFn.apply(x, self.weight, self.bias)
+
+
+class RMSNorm(nn.Module):
+    """x * rsqrt(mean(x^2) + eps) in fp32, cast back, times weight (modules.py:38-53)."""
+
+    def __init__(self, d_model: int, eps: float = _BF16_EPS ** 2):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(d_model))
+
+    def forward(self, x: Tensor) -> Tensor:
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)).to(x.dtype) * self.weight
+
+
+class CDSSMBlock(nn.Module):
+    """One CD-SSM block (block.py:14-229), forward on the HIP kernels."""
+
+    def __init__(self, config: CDSSMConfig, layer_idx: int = 0):
+        super().__init__()
+        self.config = config
+        N, H, Di = config.state_dim, config.n_heads, config.d_inner
+        G = N + 5
+        self.in_proj = nn.Linear(config.d_model, 3 * Di + H * N, bias=True)
+        self.conv = Conv1dSiLU(Di, kernel_size=config.conv_kernel_size)
+        self.gate_proj = nn.Linear(Di, H * G, bias=True)
+        self.log_dt_scale = nn.Parameter(torch.zeros(H))
+        freqs = 1.0 / (config.rope_base ** (torch.arange(0, H, dtype=torch.float32) / H))
+        self.register_buffer("rope_freqs", freqs, persistent=False)
+        self.Q_proj = nn.Linear(Di, Di, bias=False)
+        self.readout_proj = nn.Linear(H * N, Di, bias=False)
+        self.out_proj = nn.Linear(Di, config.d_model, bias=False)
+        self.norm = RMSNorm(config.d_model, eps=config.eps_norm)
+        self.ssm_norm = nn.GroupNorm(config.ssm_norm_groups, Di)
+        self.D = nn.Parameter(torch.zeros(Di))
+        self.v_residual_gate = nn.Parameter(torch.zeros(H))
+        self.shortcut_scale = nn.Parameter(torch.zeros(1))
+        self._init_weights(layer_idx)
+
+    @torch.no_grad()
+    def _init_weights(self, layer_idx: int) -> None:
+        """Variance-preserving init (block.py:90-138) and spectral init (init.py:44-126)."""
+        cfg = self.config
+        N, H, Di = cfg.state_dim, cfg.n_heads, cfg.d_inner
+        std = layer_stds(cfg.d_model, Di, cfg.n_layers)
+        nn.init.normal_(self.in_proj.weight, std=std["in_proj"])
+        nn.init.zeros_(self.in_proj.bias)
+        v0 = 3 * Di
+        self.in_proj.weight[v0:v0 + H * N].normal_(std=std["in_proj"] / math.sqrt(cfg.head_dim))
+        nn.init.normal_(self.gate_proj.weight[:N * H], std=std["dynamics_proj"])
+        nn.init.normal_(self.gate_proj.weight[N * H:], std=1.0 / math.sqrt(Di))
+        b = self.gate_proj.bias
+        b.zero_()
+        ib = cfg.init_biases
+        for seg, key in enumerate(("sel_B_bias", "sel_C_bias", "sel_dt_bias", "beta_bias", "r_gate_bias")):
+            b[(N + seg) * H:(N + seg + 1) * H] = ib[key]
+        alphas, omegas = spectral_biases(cfg, layer_idx)
+        nh = N // 2
+        for j in range(nh):
+            b[j * H:(j + 1) * H] = alphas[j]
+            b[(nh + j) * H:(nh + j + 1) * H] = omegas[j]
+        nn.init.eye_(self.Q_proj.weight)
+        nn.init.normal_(self.readout_proj.weight, std=1.0 / math.sqrt(H * N))
+        nn.init.normal_(self.out_proj.weight, std=std["out_proj"])
+        nn.init.zeros_(self.D)
+
+    def forward(self, x: Tensor, v_first: Optional[Tensor] = None):
+        cfg = self.config
+        N, H, D, Di = cfg.state_dim, cfg.n_heads, cfg.head_dim, cfg.d_inner
+        if N != 2:
+            raise ValueError("the fused scan of this build supports state_dim = 2")
+        B, L, _ = x.shape
+        residual = x
+        proj = self.in_proj(self.norm(x))
+        z, x_gate, K, V = proj.split([Di, Di, Di, H * N], dim=-1)
+        K = K.reshape(B, L, H, D)
+        V = V.reshape(B, L, H, N)
+        if v_first is None:
+            v_first = V.detach()
+        else:
+            V = torch.lerp(v_first, V, torch.sigmoid(self.v_residual_gate)[None, None, :, None].to(V.dtype))
+        x_conv = self.conv(x_gate).to(self.gate_proj.weight.dtype)
+        gates = self.gate_proj(x_conv)
+        A_bar, vp, beta, sel_C = DynamicsFusedFn.apply(
+            gates.contiguous(), self.log_dt_scale.float(), self.rope_freqs, cfg.gating_c, cfg.bf16_omega_thresh,
+            cfg.bf16_delta, cfg.bf16_smoothness, cfg.eps_adaptive_dt, H, N)
+        Q = self.Q_proj(x_conv).reshape(B, L, H, D)
+        K, Q = NormalizeKQFn.apply(K.contiguous(), Q.contiguous())
+        V = V.contiguous()
+        retrieved, _ = chunkwise_delta_scan_abar(Q, K, V, beta, sel_C, A_bar, vp, chunk_size=cfg.chunk_size)
+        # current-token shortcut (block.py:202-205) through the readout: sel_C s (q.k)^2 V vp
+        qk = (Q.float() * K.float()).sum(-1)
+        v_gated = V.float() * vp.float().repeat_interleave(2, dim=-1)
+        retrieved = (retrieved.float() + (self.shortcut_scale.float() * qk.square() * sel_C.float())[..., None]
+                     * v_gated).to(retrieved.dtype)
+        y = self.readout_proj(retrieved.reshape(B, L, H * N))
+        yf = F.group_norm(y.float().transpose(1, 2), self.ssm_norm.num_groups, self.ssm_norm.weight.float(),
+                          self.ssm_norm.bias.float(), self.ssm_norm.eps)
+        y = yf.to(y.dtype).transpose(1, 2)
+        y = y * F.silu(z)
+        y = y + self.D * x_conv
+        out = self.out_proj(y.to(self.out_proj.weight.dtype))
+        return residual + out, v_first
+
+
+class CDSSMLMHeadModel(nn.Module):
+    """Embedding -> blocks -> RMSNorm -> tied LM head (model.py:12-51)."""
+
+    def __init__(self, config: CDSSMConfig):
+        super().__init__()
+        self.config = config
+        self.embedding = nn.Embedding(config.vocab_size, config.d_model)
+        self.blocks = nn.ModuleList(CDSSMBlock(config, layer_idx=i) for i in range(config.n_layers))
+        self.final_norm = RMSNorm(config.d_model)
+        self.lm_head = nn.Linear(config.d_model, config.vocab_size, bias=False)
+        self.lm_head.weight = self.embedding.weight
+        with torch.no_grad():
+            nn.init.normal_(self.embedding.weight,
+                            std=layer_stds(config.d_model, config.d_inner, config.n_layers)["embedding"])
+
+    def forward(self, input_ids: Tensor) -> Tensor:
+        x = self.embedding(input_ids)
+        v_first = None
+        for blk in self.blocks:
+            x, v_first = blk(x, v_first=v_first)
+        return self.lm_head(self.final_norm(x))

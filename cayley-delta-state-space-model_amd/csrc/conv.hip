@@ -1,0 +1,181 @@
+// Causal depthwise conv1d + SiLU on the block's gate pathway
+// (conv1d_silu.cu:25-90, CUDAConv1dSiLUOp.forward ops.py:13-21, Conv1dSiLU
+// modules.py:14-35):
+//   y[b, t, c] = silu(bias[c] + sum_{j<K} w[c, j] x[b, t - (K-1) + j, c]),
+//   x[b, s, c] = 0 for s < 0,  silu(u) = u sigmoid(u).
+// Layouts as the reference: x, y (B, L, C) token-major, weight (C, 1, K) ->
+// (C, K), bias (C); all of one dtype.
+//
+// Work layout: a thread owns VEC consecutive channels (one 16-byte load per
+// token) over TB consecutive tokens, sliding a K-token window in registers,
+// so each input element is read once per token block (plus K-1 halo rows).
+// Consecutive threads take consecutive channel vectors of the same token:
+// every load and store of a wave is one contiguous segment.
+#include "common.hpp"
+
+namespace cdssm {
+
+constexpr int kConvTB = 16;  // tokens per thread
+
+__device__ __forceinline__ float silu_f(float u) { return u / (1.0f + __expf(-u)); }
+
+template <typename T, int VEC>
+struct ChanVec {
+  static constexpr int W = VEC * T::bytes / 4;
+  uint32_t u[W > 0 ? W : 1];
+  __device__ __forceinline__ void load(const typename T::raw* p) {
+    if constexpr (T::bytes * VEC == 16) {
+      const uint4 v = *reinterpret_cast<const uint4*>(p);
+      u[0] = v.x; u[1] = v.y; u[2] = v.z; u[3] = v.w;
+    } else {
+      static_assert(VEC == 1, "scalar or 16-byte channel vectors");
+    }
+  }
+};
+
+template <typename T, int VEC>
+__device__ __forceinline__ void load_vec(const typename T::raw* p, float (&o)[VEC]) {
+  if constexpr (VEC == 1) {
+    o[0] = T::load(p);
+  } else {
+    ChanVec<T, VEC> cv;
+    cv.load(p);
+    if constexpr (T::bytes == 2) {
+#pragma unroll
+      for (int i = 0; i < VEC / 2; ++i) {
+        o[2 * i] = bf16_lo(cv.u[i]);
+        o[2 * i + 1] = bf16_hi(cv.u[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) o[i] = __uint_as_float(cv.u[i]);
+    }
+  }
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void store_vec(typename T::raw* p, const float (&x)[VEC]) {
+  if constexpr (VEC == 1) {
+    T::store(p, x[0]);
+  } else if constexpr (T::bytes == 2) {
+    uint32_t u[VEC / 2];
+#pragma unroll
+    for (int i = 0; i < VEC / 2; ++i) u[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+    *reinterpret_cast<uint4*>(p) = make_uint4(u[0], u[1], u[2], u[3]);
+  } else {
+    *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+  }
+}
+
+template <typename T, int VEC, int K>
+__global__ __launch_bounds__(256) void conv1d_silu_fwd_kernel(const typename T::raw* __restrict__ x,
+                                                              const typename T::raw* __restrict__ w,
+                                                              const typename T::raw* __restrict__ bias,
+                                                              typename T::raw* __restrict__ y, int L, int C,
+                                                              int ntb, int64_t n_threads) {
+  const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (gid >= n_threads) return;
+  const int ncv = C / VEC;
+  const int cv = int(gid % ncv);
+  const int64_t rest = gid / ncv;
+  const int tb = int(rest % ntb);
+  const int b = int(rest / ntb);
+  const int c0 = cv * VEC;
+
+  float wt[K][VEC], bs[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    bs[i] = T::load(bias + c0 + i);
+#pragma unroll
+    for (int j = 0; j < K; ++j) wt[j][i] = T::load(w + int64_t(c0 + i) * K + j);
+  }
+  const int t0 = tb * kConvTB;
+  const typename T::raw* xb = x + int64_t(b) * L * C + c0;
+  typename T::raw* yb = y + int64_t(b) * L * C + c0;
+  // window: win[j] holds x[t - (K-1) + j]
+  float win[K][VEC];
+#pragma unroll
+  for (int j = 0; j < K - 1; ++j) {
+    const int s = t0 - (K - 1) + j;
+    if (s >= 0) {
+      load_vec<T, VEC>(xb + int64_t(s) * C, win[j + 1]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) win[j + 1][i] = 0.0f;
+    }
+  }
+  const int t1 = min(t0 + kConvTB, L);
+  for (int t = t0; t < t1; ++t) {
+#pragma unroll
+    for (int j = 0; j < K - 1; ++j)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) win[j][i] = win[j + 1][i];
+    load_vec<T, VEC>(xb + int64_t(t) * C, win[K - 1]);
+    float o[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      float u = bs[i];
+#pragma unroll
+      for (int j = 0; j < K; ++j) u = fmaf(wt[j][i], win[j][i], u);
+      o[i] = silu_f(u);
+    }
+    store_vec<T, VEC>(yb + int64_t(t) * C, o);
+  }
+}
+
+template <typename T, int VEC, int K>
+int launch_conv(const void* x, const void* w, const void* bias, void* y, int64_t B, int64_t L, int64_t C,
+                hipStream_t stream) {
+  using raw = typename T::raw;
+  const int ntb = int((L + kConvTB - 1) / kConvTB);
+  const int64_t n = B * ntb * (C / VEC);
+  hipLaunchKernelGGL((conv1d_silu_fwd_kernel<T, VEC, K>), dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const raw*>(x), static_cast<const raw*>(w), static_cast<const raw*>(bias),
+                     static_cast<raw*>(y), int(L), int(C), ntb, n);
+  return cdssm_host::check_launch("cdssm_conv1d_silu_fwd");
+}
+
+template <typename T, int VEC>
+int dispatch_k(const void* x, const void* w, const void* bias, void* y, int64_t B, int64_t L, int64_t C, int64_t K,
+               hipStream_t stream) {
+  switch (K) {
+    case 1: return launch_conv<T, VEC, 1>(x, w, bias, y, B, L, C, stream);
+    case 2: return launch_conv<T, VEC, 2>(x, w, bias, y, B, L, C, stream);
+    case 3: return launch_conv<T, VEC, 3>(x, w, bias, y, B, L, C, stream);
+    case 4: return launch_conv<T, VEC, 4>(x, w, bias, y, B, L, C, stream);
+    case 5: return launch_conv<T, VEC, 5>(x, w, bias, y, B, L, C, stream);
+    case 6: return launch_conv<T, VEC, 6>(x, w, bias, y, B, L, C, stream);
+    case 7: return launch_conv<T, VEC, 7>(x, w, bias, y, B, L, C, stream);
+    default: return launch_conv<T, VEC, 8>(x, w, bias, y, B, L, C, stream);
+  }
+}
+
+}  // namespace cdssm
+
+using namespace cdssm;
+
+extern "C" int cdssm_conv1d_silu_fwd(int dtype, const void* x, const void* weight, const void* bias, void* y,
+                                     int64_t B, int64_t L, int64_t C, int64_t K, hipStream_t stream) {
+  const char* op = "cdssm_conv1d_silu_fwd";
+  if (dtype != 0 && dtype != 1) {
+    cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
+    return CDSSM_EINVAL;
+  }
+  if (B <= 0 || L <= 0 || C <= 0 || K < 1 || K > 8 || L > 0x7fffffffLL || C > 0x7fffffffLL ||
+      B * ((L + kConvTB - 1) / kConvTB) * C > (int64_t(1) << 40)) {
+    cdssm_host::set_error("%s: need B, L, C > 0 and 1 <= kernel_size <= 8 (B=%lld L=%lld C=%lld K=%lld)", op,
+                          (long long)B, (long long)L, (long long)C, (long long)K);
+    return CDSSM_EINVAL;
+  }
+  if (!x || !weight || !bias || !y) {
+    cdssm_host::set_error("%s: null pointer argument", op);
+    return CDSSM_EINVAL;
+  }
+  const bool vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);
+  if (dtype == 1) {
+    if (vec && C % 8 == 0) return dispatch_k<BF16, 8>(x, weight, bias, y, B, L, C, K, stream);
+    return dispatch_k<BF16, 1>(x, weight, bias, y, B, L, C, K, stream);
+  }
+  if (vec && C % 4 == 0) return dispatch_k<F32, 4>(x, weight, bias, y, B, L, C, K, stream);
+  return dispatch_k<F32, 1>(x, weight, bias, y, B, L, C, K, stream);
+}
