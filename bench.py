@@ -195,6 +195,39 @@ def time_decode(steps, warmup, B=64, H=16, D=64, prompt=2048):
             "note": "steps launched back to back from Python through ctypes; per-step time includes the launch"}
 
 
+def time_lm_forward(steps=5, warmup=2):
+    """Config-4 LM forward: B8 L2048, d_model 1024, 24 layers, 16 heads x 64 (d_inner = 1024,
+    as the config states), state_dim 2, vocab 32000, bf16, random init (the reference's
+    init scheme), uniform random tokens.  Tokens/s of the whole forward (logits included)."""
+    import torch
+    from cdssm_hip.lm import CDSSMConfig, CDSSMLMHeadModel
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    cfg = CDSSMConfig(d_model=1024, n_layers=24, context_length=2048, vocab_size=32000, state_dim=2, d_inner=1024)
+    m = CDSSMLMHeadModel(cfg).to(torch.bfloat16).to(dev).eval()
+    B, L = 8, 2048
+    ids = torch.randint(0, cfg.vocab_size, (B, L), generator=torch.Generator().manual_seed(1)).to(dev)
+    stream = torch.cuda.current_stream(dev)
+    with torch.no_grad():
+        for _ in range(warmup):
+            m(ids)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            m(ids)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    n_params = sum(p.numel() for p in m.parameters())
+    flops = 2.0 * n_params * B * L  # dense GEMM work; the scan adds O(L D) per head
+    return {"workload": "config 4: LM forward B8 L2048 d_model 1024 24 layers 16x64 heads N=2 vocab 32000 bf16",
+            "ms_per_step": ms, "tokens_per_s": B * L / (ms * 1e-3), "params": n_params,
+            "gemm_tflops": flops / (ms * 1e-3) / 1e12,
+            "note": "GEMMs through torch (hipBLASLt); conv1d+SiLU, dynamics, K/Q norm, scan on the HIP kernels"}
+
+
 def cpu_baseline(cfg, x, batches, min_seconds=10.0):
     """Time the fp32 oracle (CPU restatement of ops.py's R-mode scan) on
     `batches` batch rows of the workload, all heads, full length, repeated
@@ -344,6 +377,7 @@ def main():
     if not args.no_fwd_bwd:
         out["fwd_bwd"] = [time_fwd_bwd(n, 20, 3) for n in ("C1", "C2")]
         out["decode"] = time_decode(200, 20)
+        out["lm_forward"] = time_lm_forward()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg, x, args.cpu_sample_batches)
     print(json.dumps(out), flush=True)

@@ -256,8 +256,9 @@ class CDSSMBlock(nn.Module):
         K, Q = NormalizeKQFn.apply(K.contiguous(), Q.contiguous())
         V = V.contiguous()
         retrieved, _ = chunkwise_delta_scan_abar(Q, K, V, beta, sel_C, A_bar, vp, chunk_size=cfg.chunk_size)
-        # current-token shortcut (block.py:202-205) through the readout: sel_C s (q.k)^2 V vp
-        qk = (Q.float() * K.float()).sum(-1)
+        # current-token shortcut (block.py:202-205) through the readout: sel_C s (q.k)^2 V vp,
+        # with q.k in the model dtype as the reference's einsum (fp32 accumulation)
+        qk = (Q * K).sum(-1, dtype=torch.float32)
         v_gated = V.float() * vp.float().repeat_interleave(2, dim=-1)
         retrieved = (retrieved.float() + (self.shortcut_scale.float() * qk.square() * sel_C.float())[..., None]
                      * v_gated).to(retrieved.dtype)
