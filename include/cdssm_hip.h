@@ -242,6 +242,17 @@ int cdssm_dynamics_fused_bwd(int dtype, const void* grad_A_bar, const void* grad
                              int64_t L, int64_t H, int64_t N, hipStream_t stream);
 
 /*
+ * Replaces conv1d_silu_fwd_cuda (conv1d_silu.cu:25-90 and its launcher :223-274;
+ * bound at binding.cpp:134, called by CUDAConv1dSiLUOp.forward, ops.py:13-21, for
+ * Conv1dSiLU, modules.py:14-35): causal depthwise conv + SiLU,
+ *   y[b,t,c] = silu(bias[c] + sum_{j<K} w[c,j] x[b, t-(K-1)+j, c]), x = 0 before t = 0.
+ * x, y (B,L,C); weight (C,1,K); bias (C); all `dtype` (the reference: bf16,
+ * K = 4 only).  Supported: 1 <= K <= 8.  Forward only.
+ */
+int cdssm_conv1d_silu_fwd(int dtype, const void* x, const void* weight, const void* bias, void* y, int64_t B,
+                          int64_t L, int64_t C, int64_t K, hipStream_t stream);
+
+/*
  * Replaces normalize_kq_fwd_cuda / normalize_kq_bwd_cuda (normalize_kq.cu:168-244;
  * NormalizeKQFn, ops.py:84-97): rows of length D (any D <= 256; the reference kernel is
  * correct only for D = 64), x_hat = x rsqrt(sum x^2 + 1e-6).
