@@ -64,6 +64,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-batches", type=int, default=1)
     ap.add_argument("--no-fwd-bwd", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the decode and config-4 LM timings (profiling runs)")
     ap.add_argument("--forward-path", default="auto", choices=["auto", "four_launch", "one_pass"],
                     help="how the forward is launched (default: the library's own choice)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -376,8 +378,9 @@ def main():
     }
     if not args.no_fwd_bwd:
         out["fwd_bwd"] = [time_fwd_bwd(n, 20, 3) for n in ("C1", "C2")]
-        out["decode"] = time_decode(200, 20)
-        out["lm_forward"] = time_lm_forward()
+        if not args.no_extras:
+            out["decode"] = time_decode(200, 20)
+            out["lm_forward"] = time_lm_forward()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg, x, args.cpu_sample_batches)
     print(json.dumps(out), flush=True)
