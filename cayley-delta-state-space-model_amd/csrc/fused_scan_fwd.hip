@@ -883,16 +883,10 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
     rm = stage_scalars<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, alpha, omega, c, s, nullptr, 0,
                                      SAVE ? gsaved : nullptr, GF + wv * HPW, [&] {
 #pragma unroll
-                                       for (int i = 0; i < PF; ++i) {
-                                         kb[i].load(ks, min(i * rowb, slim));
-                                         qb[i].load(qs, min(i * rowb, slim));
-                                       }
+                                       for (int i = 0; i < PF; ++i) kb[i].load(ks, min(i * rowb, slim));
                                      });
 #pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      kb[i].pin();
-      qb[i].pin();
-    }
+    for (int i = 0; i < PF; ++i) kb[i].pin();
   }
   __syncthreads();
 
@@ -902,8 +896,9 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
 
   // 1. local recurrence (k rows only); each step's update coefficient e_t is
   // kept in LDS, so the correction pass replays zh without dot products.  In
-  // the last PF steps the k prefetch wraps to the first tokens; the q ring
-  // still holds the first tokens from the staging prefetch.
+  // the last PF steps the k prefetch wraps to the first tokens; the q ring is
+  // loaded after the loop (the carry hand-off hides its latency), which keeps
+  // it out of the load burst at the start of the kernel.
   if (live) {
     if (SAVE && sub == 0 && hok) gam[tile_h] = make_float2(GF[wv * HPW + hh].x, GF[wv * HPW + hh].y);
     float fpr = 1.0f, fpi = 0.0f;  // frame f_{t-1} (SAVE)
@@ -963,10 +958,9 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
       }
     }
 #pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      kb[i].pin();
-      qb[i].pin();
-    }
+    for (int i = 0; i < PF; ++i) qb[i].load(qs, min(i * rowb, slim));
+#pragma unroll
+    for (int i = 0; i < PF; ++i) kb[i].pin();
     // chunk map F = f_end zh (zero for heads >= H: their steps are inert)
     const float4 ge = GF[wv * HPW + hh];
 #pragma unroll
@@ -1138,6 +1132,8 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
     // the local state is replayed from its update coefficients
 #pragma unroll
     for (int j = 0; j < DPL; ++j) zr[j] = zi[j] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PF; ++i) qb[i].pin();  // loaded after the local pass
     for (int tb = 0; tb < ntr; tb += PF) {
       float4 sa[PF], sb[PF];
       float2 se[PF], sm[PF];
