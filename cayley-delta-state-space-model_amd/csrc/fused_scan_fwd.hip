@@ -77,20 +77,23 @@ struct TileScalars {
   float2* M;
 };
 
-// Bit t%64 of m0 (t < 64) or m1: some head of the wave resets its frame at
-// token t.  Two named words, not an array, so they stay in scalar registers.
+// Tokens where some head of the wave resets its frame.  The staging lanes own
+// (head, block of TPB tokens) of a 64-token slab; after staging, every lane
+// holds in v0 (slab 0) / v1 (slab 1) the OR over the wave's heads of its
+// block's TPB flags (bit i: token block * TPB + i), so lane b holds block b's.
+template <int TPB>
 struct ResetMask {
-  uint64_t m0, m1;
-  __device__ __forceinline__ bool test(int t) const {
-    const uint64_t w = t < 64 ? m0 : m1;
-    // wave-uniform by construction (ballots); readfirstlane makes the branch scalar
-    return __builtin_amdgcn_readfirstlane(int((w >> (t & 63)) & 1ull)) != 0;
-  }
+  static_assert(TPB >= 1 && TPB <= 8 && 8 % TPB == 0, "blocks tile an 8-token group");
+  uint32_t v0, v1;
   // Bits of the 8 tokens tb .. tb + 7 (tb a multiple of 8), bit i for token
-  // tb + i: one scalar word per token group, tested per token with one bit test.
+  // tb + i, as a scalar: 8 / TPB lane reads, once per token group.
   __device__ __forceinline__ uint32_t group8(int tb) const {
-    const uint64_t w = tb < 64 ? m0 : m1;
-    return __builtin_amdgcn_readfirstlane(uint32_t(w >> (tb & 63)) & 0xffu);
+    const int src = int(tb < 64 ? v0 : v1);
+    const int b0 = (tb & 63) / TPB;
+    uint32_t g = 0;
+#pragma unroll
+    for (int u = 0; u < 8 / TPB; ++u) g |= uint32_t(__builtin_amdgcn_readlane(src, b0 + u)) << (u * TPB);
+    return g;
   }
 };
 
@@ -108,14 +111,6 @@ struct ResetMask {
 constexpr float kBand = 120.0f;
 constexpr float kBandStep = 60.0f;
 
-// Spread the low 8 bits of x to bit positions 0, 8, ..., 56.
-__device__ __forceinline__ uint64_t spread8(uint64_t x) {
-  x = (x | (x << 28)) & 0x0000000F0000000Full;
-  x = (x | (x << 14)) & 0x0003000300030003ull;
-  x = (x | (x << 7)) & 0x0101010101010101ull;
-  return x;
-}
-
 // Stage the tile's per-token scalars.  Work layout: lane = (head j, block of
 // TPB = HPW consecutive tokens of a 64-token slab), NB = 64/HPW blocks per
 // head.  Each lane first issues all of its loads (addresses clamped into the
@@ -132,7 +127,7 @@ struct NoPrefetch {
 };
 
 template <typename T, int HPW, bool MAIN, typename Pre = NoPrefetch>
-__device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, int ntr,
+__device__ __forceinline__ ResetMask<HPW> stage_scalars(const ChunkTile& tc, int H, int ntr,
                                                    const typename T::raw* __restrict__ v,
                                                    const typename T::raw* __restrict__ beta,
                                                    const typename T::raw* __restrict__ sel_c,
@@ -156,7 +151,7 @@ __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, i
   const float al = kAbar ? 0.0f : alpha[hl], om = kAbar ? 0.0f : omega[hl];
   const int glast = j * NB + NB - 1;  // the head's last lane
 
-  ResetMask rm{0ull, 0ull};
+  ResetMask<HPW> rm{0u, 0u};
   float cL = 0.0f, cfr = 1.0f, cfi = 0.0f, cgr = 1.0f, cgi = 0.0f;  // carries from earlier slabs
   for (int tl = 0; tl < ntr; tl += kWave) {
     const int t0 = tl + blk * TPB;
@@ -298,24 +293,17 @@ __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, i
       s.M[p] = reset[i] ? make_float2(mr, mi) : make_float2(1.0f, 0.0f);
       fpr = lfr;
       fpi = lfi;
-      // tokens of this slab where some head resets: OR over the heads' lanes
-      uint64_t bal = __builtin_amdgcn_ballot_w64(reset[i]);
-#pragma unroll
-      for (int sh = NB; sh < kWave; sh <<= 1) bal |= bal >> sh;
-      bal &= (NB == 64 ? ~0ull : ((1ull << NB) - 1));
-      uint64_t tokbits = 0;
-      if constexpr (NB == 8) {
-        tokbits = spread8(bal) << i;
-      } else {
-#pragma unroll
-        for (int b2 = 0; b2 < NB; ++b2)
-          if ((bal >> b2) & 1ull) tokbits |= 1ull << (b2 * TPB + i);
-      }
-      if (tl == 0)
-        rm.m0 |= tokbits;
-      else
-        rm.m1 |= tokbits;
     }
+    // this lane's block flags, then OR over the heads (lanes NB apart)
+    uint32_t r8 = 0;
+#pragma unroll
+    for (int i = 0; i < TPB; ++i) r8 |= reset[i] ? (1u << i) : 0u;
+#pragma unroll
+    for (int sh = NB; sh < kWave; sh <<= 1) r8 |= uint32_t(__shfl_xor(int(r8), sh, kWave));
+    if (tl == 0)
+      rm.v0 = r8;
+    else
+      rm.v1 = r8;
     // carries to the next slab, from the head's last lane
     float gtr = egr, gti = egi;
     cmul_acc(gtr, gti, gpr, gpi);
@@ -333,10 +321,6 @@ __device__ __forceinline__ ResetMask stage_scalars(const ChunkTile& tc, int H, i
   }
   // one-pass forward: (G_k, frame after the last step) per head of the tile
   if (MAIN && cend && blk == 0) cend[j] = make_float4(cgr, cgi, cfr, cfi);
-  rm.m0 = __builtin_amdgcn_readfirstlane(uint32_t(rm.m0)) |
-          (uint64_t(__builtin_amdgcn_readfirstlane(uint32_t(rm.m0 >> 32))) << 32);
-  rm.m1 = __builtin_amdgcn_readfirstlane(uint32_t(rm.m1)) |
-          (uint64_t(__builtin_amdgcn_readfirstlane(uint32_t(rm.m1 >> 32))) << 32);
   return rm;
 }
 
@@ -404,7 +388,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
   const int slim = tlast * rowb;
   RowVec<T, DPL> kb[PF];
   TileScalars s{smem4, smem4 + slots, reinterpret_cast<float2*>(smem4 + slots + HPW)};
-  const ResetMask rm = stage_scalars<T, HPW, false>(tc, H, ntr, v, beta, nullptr, dt, r, alpha, omega, c, s,
+  const auto rm = stage_scalars<T, HPW, false>(tc, H, ntr, v, beta, nullptr, dt, r, alpha, omega, c, s,
                                                     gam, ch0, nullptr, nullptr, [&] {
 #pragma unroll
                                                       for (int i = 0; i < PF; ++i)
@@ -621,7 +605,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
 
   TileScalars s{smem4, smem4 + slots, reinterpret_cast<float2*>(smem4 + 2 * slots)};
   float2* s_y = s.M + slots;
-  const ResetMask rm = stage_scalars<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, alpha, omega, c, s,
+  const auto rm = stage_scalars<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, alpha, omega, c, s,
                                                    nullptr, 0, SAVE ? gsaved : nullptr, nullptr, [&] {
 #pragma unroll
                                                      for (int i = 0; i < PF; ++i) {
@@ -877,7 +861,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   float zr[DPL], zi[DPL];
 #pragma unroll
   for (int j = 0; j < DPL; ++j) zr[j] = zi[j] = 0.0f;
-  ResetMask rm{0ull, 0ull};
+  ResetMask<HPW> rm{0u, 0u};
 
   if (live) {
     rm = stage_scalars<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, alpha, omega, c, s, nullptr, 0,
