@@ -227,7 +227,8 @@ def time_lm_forward(steps=5, warmup=2):
     return {"workload": "config 4: LM forward B8 L2048 d_model 1024 24 layers 16x64 heads N=2 vocab 32000 bf16",
             "ms_per_step": ms, "tokens_per_s": B * L / (ms * 1e-3), "params": n_params,
             "gemm_tflops": flops / (ms * 1e-3) / 1e12,
-            "note": "GEMMs through torch (hipBLASLt); conv1d+SiLU, dynamics, K/Q norm, scan on the HIP kernels"}
+            "note": "GEMMs through torch (hipBLASLt); RMSNorm, conv1d+SiLU, dynamics, K/Q norm + q.k, scan, shortcut, "
+                    "GroupNorm + gate on the HIP kernels"}
 
 
 def cpu_baseline(cfg, x, batches, min_seconds=10.0):

@@ -3,13 +3,13 @@
 Mirrors the reference model (model.py:12-51, block.py:14-229, modules.py:14-53,
 init.py:13-126, config/model.py:38-178) with the same module and parameter
 names, so a reference ``state_dict`` loads unchanged.  Per block:
-RMSNorm -> in_proj -> value residual -> conv1d+SiLU (HIP) -> gate_proj ->
-DynamicsFusedFn (HIP) -> NormalizeKQFn (HIP) -> fused scan with the sel_C
-readout on the gate-level A_bar / vp (HIP, ``cdssm_fused_scan_fwd_abar``) ->
-current-token shortcut -> readout_proj -> fp32 GroupNorm -> * silu(z) -> + D x
--> out_proj -> residual.  Dense projections, norms and the embedding are
-PyTorch (hipBLASLt GEMMs).  Forward only: the conv and the a_t-input scan have
-no backward here.
+RMSNorm (HIP) -> in_proj -> value residual -> conv1d+SiLU on the in_proj
+column slice (HIP) -> gate_proj -> DynamicsFusedFn (HIP) -> K/Q normalisation
+with q.k (HIP) -> fused scan with the sel_C readout on the gate-level A_bar /
+vp (HIP, ``cdssm_fused_scan_fwd_abar``) -> current-token shortcut (HIP) ->
+readout_proj -> fp32 GroupNorm, * silu(z), + D x (HIP) -> out_proj with the
+residual in the GEMM epilogue.  Dense projections and the embedding are
+PyTorch (hipBLASLt GEMMs).  Forward only: these kernels have no backward here.
 """
 
 from __future__ import annotations
@@ -20,10 +20,9 @@ from typing import Optional
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from . import _lib
-from .ops import DynamicsFusedFn, NormalizeKQFn
+from .ops import DynamicsFusedFn
 from .scan import chunkwise_delta_scan_abar
 
 Tensor = torch.Tensor
@@ -132,24 +131,136 @@ class _Conv1dSiLUFn(torch.autograd.Function):
         raise NotImplementedError("conv1d+SiLU backward is not part of this build (forward-only model path)")
 
 
+def _check_gpu(op: str, *ts: Tensor) -> torch.dtype:
+    dt = ts[0].dtype
+    for t in ts:
+        if t.device.type != "cuda":
+            raise RuntimeError(f"{op} runs on the GPU only")
+        if t.dtype != dt:
+            raise TypeError(f"{op}: all tensors must share one dtype, got {dt} and {t.dtype}")
+    if dt not in _lib.DTYPE_CODE:
+        raise TypeError(f"{op}: dtype must be float32 or bfloat16, got {dt}")
+    return dt
+
+
+def _token_view(x: Tensor, width: int) -> int:
+    """Token stride (elements) of a (B, L, width) view whose rows are dense; raises otherwise."""
+    B, L = x.shape[0], x.shape[1]
+    if x.stride(-1) != 1 or (L > 1 and B > 1 and x.stride(0) != L * x.stride(1)):
+        raise ValueError("expected a (B, L, C) view with dense channels and a uniform token stride")
+    return x.stride(1) if L > 1 else (x.stride(0) if B > 1 else width)
+
+
 def conv1d_silu(x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
-    """silu(causal depthwise conv1d(x) + bias); x (B, L, C), weight (C, 1, K) or (C, K), bias (C)."""
-    if x.device.type != "cuda":
-        raise RuntimeError("conv1d_silu runs on the GPU only")
-    if x.dtype not in _lib.DTYPE_CODE:
-        raise TypeError(f"x must be float32 or bfloat16, got {x.dtype}")
+    """silu(causal depthwise conv1d(x) + bias); x (B, L, C) (dense channels, any token stride, e.g. a
+    column slice of a projection output), weight (C, 1, K) or (C, K), bias (C)."""
+    _check_gpu("conv1d_silu", x)
     B, L, C = x.shape
     K = weight.shape[-1]
     if weight.numel() != C * K or tuple(bias.shape) != (C,):
         raise ValueError(f"weight must be ({C}, 1, K) and bias ({C},), got {tuple(weight.shape)}, {tuple(bias.shape)}")
-    xc = x.contiguous()
+    try:
+        xs = _token_view(x, C)
+    except ValueError:
+        x = x.contiguous()
+        xs = C
     wc = weight.to(x.dtype).contiguous()
     bc = bias.to(x.dtype).contiguous()
-    y = torch.empty_like(xc)
-    st = _lib.load().cdssm_conv1d_silu_fwd(_lib.DTYPE_CODE[x.dtype], _lib.ptr(xc), _lib.ptr(wc), _lib.ptr(bc),
-                                          _lib.ptr(y), B, L, C, K, _lib.stream_of(x.device))
-    _lib.check(st, "cdssm_conv1d_silu_fwd")
+    y = torch.empty((B, L, C), dtype=x.dtype, device=x.device)
+    st = _lib.load().cdssm_conv1d_silu_fwd_strided(_lib.DTYPE_CODE[x.dtype], _lib.ptr(x), xs, _lib.ptr(wc),
+                                                  _lib.ptr(bc), _lib.ptr(y), B, L, C, K, _lib.stream_of(x.device))
+    _lib.check(st, "cdssm_conv1d_silu_fwd_strided")
     return y
+
+
+def rms_norm(x: Tensor, weight: Tensor, eps: float) -> Tensor:
+    """(x * rsqrt(mean(x^2) + eps)).to(x.dtype) * weight over the last dim (modules.py:49-53)."""
+    w = weight.to(x.dtype).contiguous()
+    _check_gpu("rms_norm", x, w)
+    xc = x.contiguous()
+    C = x.shape[-1]
+    y = torch.empty_like(xc)
+    st = _lib.load().cdssm_rms_norm_fwd(_lib.DTYPE_CODE[x.dtype], _lib.ptr(xc), _lib.ptr(w), _lib.ptr(y),
+                                       xc.numel() // C, C, float(eps), _lib.stream_of(x.device))
+    _lib.check(st, "cdssm_rms_norm_fwd")
+    return y
+
+
+def normalize_kq_qk(K: Tensor, Q: Tensor) -> tuple:
+    """K^, Q^ = x * rsqrt(sum_d x^2 + 1e-6) per (token, head) and qk = K^.Q^ (fp32), in one pass.
+
+    K, Q (B, L, H, D) with dense (H, D) blocks per token and any token stride (K may be a column slice
+    of the in_proj output); returns dense K^, Q^ and qk (B, L, H) fp32 (normalize_kq.cu:75-79,
+    block.py:191-192, 202)."""
+    dt = _check_gpu("normalize_kq_qk", K, Q)
+    B, L, H, D = K.shape
+    if tuple(Q.shape) != (B, L, H, D):
+        raise ValueError(f"K and Q shapes differ: {tuple(K.shape)} vs {tuple(Q.shape)}")
+    strides, dense = [], []
+    for t in (K, Q):
+        ts = t.stride(1) if L > 1 else H * D
+        # read in place when the rows are dense and 16-byte aligned, else from a dense copy
+        if (t.stride(3) != 1 or t.stride(2) != D or (L > 1 and t.stride(0) != L * t.stride(1))
+                or t.data_ptr() % 16 or (ts * t.element_size()) % 16):
+            t, ts = t.contiguous(), H * D
+        strides.append(ts)
+        dense.append(t)
+    K, Q = dense
+    Ko = torch.empty((B, L, H, D), dtype=dt, device=K.device)
+    Qo = torch.empty_like(Ko)
+    qk = torch.empty((B, L, H), dtype=torch.float32, device=K.device)
+    st = _lib.load().cdssm_normalize_kq_qk_fwd(_lib.DTYPE_CODE[dt], _lib.ptr(K), strides[0], _lib.ptr(Q), strides[1],
+                                              _lib.ptr(Ko), _lib.ptr(Qo), _lib.ptr(qk), B * L, H, D,
+                                              _lib.stream_of(K.device))
+    _lib.check(st, "cdssm_normalize_kq_qk_fwd")
+    return Ko, Qo, qk
+
+
+def shortcut_readout_(retrieved: Tensor, qk: Tensor, V: Tensor, vp: Tensor, sel_C: Tensor, scale: Tensor) -> Tensor:
+    """In place: retrieved += sel_C * scale * qk^2 * vp * V (the shortcut of block.py:202-205 through the
+    readout of block.py:208-211).  retrieved, V (B, L, H, 2); vp (B, L, H, 1); sel_C (B, L, H); qk fp32."""
+    dt = _check_gpu("shortcut_readout", retrieved, V, vp, sel_C)
+    for n, t in dict(retrieved=retrieved, V=V, vp=vp, sel_C=sel_C, qk=qk).items():
+        if not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous")
+    n = sel_C.numel()
+    if retrieved.numel() != 2 * n or V.numel() != 2 * n or vp.numel() != n or qk.numel() != n:
+        raise ValueError("retrieved, V (n, 2), vp, sel_C, qk (n) with n = B*L*H")
+    sc = scale.detach().reshape(1).to(device=retrieved.device, dtype=torch.float32).contiguous()
+    st = _lib.load().cdssm_shortcut_readout_fwd(_lib.DTYPE_CODE[dt], _lib.ptr(retrieved), _lib.ptr(qk), _lib.ptr(V),
+                                               _lib.ptr(vp), _lib.ptr(sel_C), _lib.ptr(sc), n,
+                                               _lib.stream_of(retrieved.device))
+    _lib.check(st, "cdssm_shortcut_readout_fwd")
+    return retrieved
+
+
+def group_norm_gate(y: Tensor, num_groups: int, gamma: Tensor, beta: Tensor, eps: float, z: Tensor,
+                    x_conv: Tensor, D: Tensor) -> Tensor:
+    """GroupNorm over (channels of a group, all L) in fp32, cast to y's dtype, * silu(z) + D * x_conv
+    (block.py:215-225).  y, x_conv (B, L, C) dense; z (B, L, C) with any token stride."""
+    Dp = D.to(y.dtype).contiguous()
+    dt = _check_gpu("group_norm_gate", y, z, x_conv, Dp)
+    B, L, C = y.shape
+    if tuple(z.shape) != (B, L, C) or tuple(x_conv.shape) != (B, L, C):
+        raise ValueError("y, z and x_conv must all be (B, L, C)")
+    yc, xc = y.contiguous(), x_conv.contiguous()
+    zs = _token_view(z, C)
+    # the affine parameters are read in their own dtype (bf16 or fp32) and widened exactly in the kernel
+    pdt = gamma.dtype if gamma.dtype in _lib.DTYPE_CODE else torch.float32
+    g = gamma.detach().to(device=y.device, dtype=pdt).contiguous()
+    b = beta.detach().to(device=y.device, dtype=pdt).contiguous()
+    lib = _lib.load()
+    nb = lib.cdssm_group_norm_workspace_bytes(B, num_groups, L)
+    if nb < 0:
+        raise ValueError(f"invalid group norm shape B={B} G={num_groups} L={L}")
+    ws = torch.empty(max(1, nb // 4), dtype=torch.float32, device=y.device)
+    out = torch.empty_like(yc)
+    st = lib.cdssm_group_norm_gate_fwd(_lib.DTYPE_CODE[dt], _lib.DTYPE_CODE[pdt], _lib.ptr(yc), _lib.ptr(g),
+                                       _lib.ptr(b), _lib.ptr(z), zs,
+                                       _lib.ptr(xc), _lib.ptr(Dp), _lib.ptr(out), _lib.ptr(ws), B, L, C, num_groups,
+                                       float(eps), _lib.stream_of(y.device))
+    _lib.check(st, "cdssm_group_norm_gate_fwd")
+    return out
 
 
 class Conv1dSiLU(nn.Module):
@@ -177,8 +288,7 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(d_model))
 
     def forward(self, x: Tensor) -> Tensor:
-        xf = x.float()
-        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)).to(x.dtype) * self.weight
+        return rms_norm(x, self.weight, self.eps)
 
 
 class CDSSMBlock(nn.Module):
@@ -239,7 +349,7 @@ class CDSSMBlock(nn.Module):
             raise ValueError("the fused scan of this build supports state_dim = 2")
         B, L, _ = x.shape
         residual = x
-        proj = self.in_proj(self.norm(x))
+        proj = self.in_proj(self.norm(x))  # (B, L, 3 Di + H N); z, x_gate and K are read in place
         z, x_gate, K, V = proj.split([Di, Di, Di, H * N], dim=-1)
         K = K.reshape(B, L, H, D)
         V = V.reshape(B, L, H, N)
@@ -247,29 +357,23 @@ class CDSSMBlock(nn.Module):
             v_first = V.detach()
         else:
             V = torch.lerp(v_first, V, torch.sigmoid(self.v_residual_gate)[None, None, :, None].to(V.dtype))
-        x_conv = self.conv(x_gate).to(self.gate_proj.weight.dtype)
+        x_conv = self.conv(x_gate)
         gates = self.gate_proj(x_conv)
         A_bar, vp, beta, sel_C = DynamicsFusedFn.apply(
             gates.contiguous(), self.log_dt_scale.float(), self.rope_freqs, cfg.gating_c, cfg.bf16_omega_thresh,
             cfg.bf16_delta, cfg.bf16_smoothness, cfg.eps_adaptive_dt, H, N)
         Q = self.Q_proj(x_conv).reshape(B, L, H, D)
-        K, Q = NormalizeKQFn.apply(K.contiguous(), Q.contiguous())
+        K, Q, qk = normalize_kq_qk(K, Q)
         V = V.contiguous()
         retrieved, _ = chunkwise_delta_scan_abar(Q, K, V, beta, sel_C, A_bar, vp, chunk_size=cfg.chunk_size)
-        # current-token shortcut (block.py:202-205) through the readout: sel_C s (q.k)^2 V vp,
-        # with q.k in the model dtype as the reference's einsum (fp32 accumulation)
-        qk = (Q * K).sum(-1, dtype=torch.float32)
-        v_gated = V.float() * vp.float().repeat_interleave(2, dim=-1)
-        retrieved = (retrieved.float() + (self.shortcut_scale.float() * qk.square() * sel_C.float())[..., None]
-                     * v_gated).to(retrieved.dtype)
+        # current-token shortcut (block.py:202-205) through the readout: sel_C s (q.k)^2 V vp
+        shortcut_readout_(retrieved, qk, V, vp, sel_C, self.shortcut_scale)
         y = self.readout_proj(retrieved.reshape(B, L, H * N))
-        yf = F.group_norm(y.float().transpose(1, 2), self.ssm_norm.num_groups, self.ssm_norm.weight.float(),
-                          self.ssm_norm.bias.float(), self.ssm_norm.eps)
-        y = yf.to(y.dtype).transpose(1, 2)
-        y = y * F.silu(z)
-        y = y + self.D * x_conv
-        out = self.out_proj(y.to(self.out_proj.weight.dtype))
-        return residual + out, v_first
+        y = group_norm_gate(y, self.ssm_norm.num_groups, self.ssm_norm.weight, self.ssm_norm.bias,
+                            self.ssm_norm.eps, z, x_conv, self.D)
+        # out_proj with the residual added in the GEMM epilogue
+        out = torch.addmm(residual.reshape(B * L, -1), y.reshape(B * L, Di), self.out_proj.weight.t())
+        return out.reshape(residual.shape), v_first
 
 
 class CDSSMLMHeadModel(nn.Module):

@@ -17,7 +17,8 @@ namespace cdssm {
 
 constexpr int kConvTB = 16;  // tokens per thread
 
-__device__ __forceinline__ float silu_f(float u) { return u / (1.0f + __expf(-u)); }
+// silu(u) = u sigmoid(u), with the hardware reciprocal (about 1 ulp)
+__device__ __forceinline__ float silu_f(float u) { return u * __builtin_amdgcn_rcpf(1.0f + __expf(-u)); }
 
 template <typename T, int VEC>
 struct ChanVec {
@@ -72,14 +73,14 @@ __global__ __launch_bounds__(256) void conv1d_silu_fwd_kernel(const typename T::
                                                               const typename T::raw* __restrict__ w,
                                                               const typename T::raw* __restrict__ bias,
                                                               typename T::raw* __restrict__ y, int L, int C,
-                                                              int ntb, int64_t n_threads) {
-  const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+                                                              int64_t x_ts, int ntb, int n_threads) {
+  const int gid = int(blockIdx.x) * int(blockDim.x) + int(threadIdx.x);  // n_threads < 2^31 (host check)
   if (gid >= n_threads) return;
   const int ncv = C / VEC;
-  const int cv = int(gid % ncv);
-  const int64_t rest = gid / ncv;
-  const int tb = int(rest % ntb);
-  const int b = int(rest / ntb);
+  const int rest = gid / ncv;
+  const int cv = gid - rest * ncv;
+  const int b = rest / ntb;
+  const int tb = rest - b * ntb;
   const int c0 = cv * VEC;
 
   float wt[K][VEC], bs[VEC];
@@ -90,7 +91,7 @@ __global__ __launch_bounds__(256) void conv1d_silu_fwd_kernel(const typename T::
     for (int j = 0; j < K; ++j) wt[j][i] = T::load(w + int64_t(c0 + i) * K + j);
   }
   const int t0 = tb * kConvTB;
-  const typename T::raw* xb = x + int64_t(b) * L * C + c0;
+  const typename T::raw* xb = x + int64_t(b) * L * x_ts + c0;
   typename T::raw* yb = y + int64_t(b) * L * C + c0;
   // window: win[j] holds x[t - (K-1) + j]
   float win[K][VEC];
@@ -98,7 +99,7 @@ __global__ __launch_bounds__(256) void conv1d_silu_fwd_kernel(const typename T::
   for (int j = 0; j < K - 1; ++j) {
     const int s = t0 - (K - 1) + j;
     if (s >= 0) {
-      load_vec<T, VEC>(xb + int64_t(s) * C, win[j + 1]);
+      load_vec<T, VEC>(xb + int64_t(s) * x_ts, win[j + 1]);
     } else {
 #pragma unroll
       for (int i = 0; i < VEC; ++i) win[j + 1][i] = 0.0f;
@@ -110,7 +111,7 @@ __global__ __launch_bounds__(256) void conv1d_silu_fwd_kernel(const typename T::
     for (int j = 0; j < K - 1; ++j)
 #pragma unroll
       for (int i = 0; i < VEC; ++i) win[j][i] = win[j + 1][i];
-    load_vec<T, VEC>(xb + int64_t(t) * C, win[K - 1]);
+    load_vec<T, VEC>(xb + int64_t(t) * x_ts, win[K - 1]);
     float o[VEC];
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
@@ -124,29 +125,29 @@ __global__ __launch_bounds__(256) void conv1d_silu_fwd_kernel(const typename T::
 }
 
 template <typename T, int VEC, int K>
-int launch_conv(const void* x, const void* w, const void* bias, void* y, int64_t B, int64_t L, int64_t C,
-                hipStream_t stream) {
+int launch_conv(const void* x, int64_t x_ts, const void* w, const void* bias, void* y, int64_t B, int64_t L,
+                int64_t C, hipStream_t stream) {
   using raw = typename T::raw;
   const int ntb = int((L + kConvTB - 1) / kConvTB);
   const int64_t n = B * ntb * (C / VEC);
   hipLaunchKernelGGL((conv1d_silu_fwd_kernel<T, VEC, K>), dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream,
                      static_cast<const raw*>(x), static_cast<const raw*>(w), static_cast<const raw*>(bias),
-                     static_cast<raw*>(y), int(L), int(C), ntb, n);
+                     static_cast<raw*>(y), int(L), int(C), x_ts, ntb, int(n));
   return cdssm_host::check_launch("cdssm_conv1d_silu_fwd");
 }
 
 template <typename T, int VEC>
-int dispatch_k(const void* x, const void* w, const void* bias, void* y, int64_t B, int64_t L, int64_t C, int64_t K,
-               hipStream_t stream) {
+int dispatch_k(const void* x, int64_t x_ts, const void* w, const void* bias, void* y, int64_t B, int64_t L,
+               int64_t C, int64_t K, hipStream_t stream) {
   switch (K) {
-    case 1: return launch_conv<T, VEC, 1>(x, w, bias, y, B, L, C, stream);
-    case 2: return launch_conv<T, VEC, 2>(x, w, bias, y, B, L, C, stream);
-    case 3: return launch_conv<T, VEC, 3>(x, w, bias, y, B, L, C, stream);
-    case 4: return launch_conv<T, VEC, 4>(x, w, bias, y, B, L, C, stream);
-    case 5: return launch_conv<T, VEC, 5>(x, w, bias, y, B, L, C, stream);
-    case 6: return launch_conv<T, VEC, 6>(x, w, bias, y, B, L, C, stream);
-    case 7: return launch_conv<T, VEC, 7>(x, w, bias, y, B, L, C, stream);
-    default: return launch_conv<T, VEC, 8>(x, w, bias, y, B, L, C, stream);
+    case 1: return launch_conv<T, VEC, 1>(x, x_ts, w, bias, y, B, L, C, stream);
+    case 2: return launch_conv<T, VEC, 2>(x, x_ts, w, bias, y, B, L, C, stream);
+    case 3: return launch_conv<T, VEC, 3>(x, x_ts, w, bias, y, B, L, C, stream);
+    case 4: return launch_conv<T, VEC, 4>(x, x_ts, w, bias, y, B, L, C, stream);
+    case 5: return launch_conv<T, VEC, 5>(x, x_ts, w, bias, y, B, L, C, stream);
+    case 6: return launch_conv<T, VEC, 6>(x, x_ts, w, bias, y, B, L, C, stream);
+    case 7: return launch_conv<T, VEC, 7>(x, x_ts, w, bias, y, B, L, C, stream);
+    default: return launch_conv<T, VEC, 8>(x, x_ts, w, bias, y, B, L, C, stream);
   }
 }
 
@@ -154,16 +155,18 @@ int dispatch_k(const void* x, const void* w, const void* bias, void* y, int64_t 
 
 using namespace cdssm;
 
-extern "C" int cdssm_conv1d_silu_fwd(int dtype, const void* x, const void* weight, const void* bias, void* y,
-                                     int64_t B, int64_t L, int64_t C, int64_t K, hipStream_t stream) {
+extern "C" int cdssm_conv1d_silu_fwd_strided(int dtype, const void* x, int64_t x_token_stride, const void* weight,
+                                             const void* bias, void* y, int64_t B, int64_t L, int64_t C, int64_t K,
+                                             hipStream_t stream) {
   const char* op = "cdssm_conv1d_silu_fwd";
   if (dtype != 0 && dtype != 1) {
     cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
     return CDSSM_EINVAL;
   }
   if (B <= 0 || L <= 0 || C <= 0 || K < 1 || K > 8 || L > 0x7fffffffLL || C > 0x7fffffffLL ||
-      B * ((L + kConvTB - 1) / kConvTB) * C > (int64_t(1) << 40)) {
-    cdssm_host::set_error("%s: need B, L, C > 0 and 1 <= kernel_size <= 8 (B=%lld L=%lld C=%lld K=%lld)", op,
+      B * ((L + kConvTB - 1) / kConvTB) * C >= (int64_t(1) << 31)) {
+    cdssm_host::set_error("%s: need B, L, C > 0, B * ceil(L/16) * C < 2^31 and 1 <= kernel_size <= 8 "
+                          "(B=%lld L=%lld C=%lld K=%lld)", op,
                           (long long)B, (long long)L, (long long)C, (long long)K);
     return CDSSM_EINVAL;
   }
@@ -171,11 +174,22 @@ extern "C" int cdssm_conv1d_silu_fwd(int dtype, const void* x, const void* weigh
     cdssm_host::set_error("%s: null pointer argument", op);
     return CDSSM_EINVAL;
   }
-  const bool vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0);
-  if (dtype == 1) {
-    if (vec && C % 8 == 0) return dispatch_k<BF16, 8>(x, weight, bias, y, B, L, C, K, stream);
-    return dispatch_k<BF16, 1>(x, weight, bias, y, B, L, C, K, stream);
+  if (x_token_stride < C) {
+    cdssm_host::set_error("%s: x token stride %lld below C = %lld", op, (long long)x_token_stride, (long long)C);
+    return CDSSM_EINVAL;
   }
-  if (vec && C % 4 == 0) return dispatch_k<F32, 4>(x, weight, bias, y, B, L, C, K, stream);
-  return dispatch_k<F32, 1>(x, weight, bias, y, B, L, C, K, stream);
+  const int64_t eb = dtype == 1 ? 2 : 4;
+  const bool vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (reinterpret_cast<uintptr_t>(y) % 16 == 0) &&
+                   (x_token_stride * eb) % 16 == 0;
+  if (dtype == 1) {
+    if (vec && C % 8 == 0) return dispatch_k<BF16, 8>(x, x_token_stride, weight, bias, y, B, L, C, K, stream);
+    return dispatch_k<BF16, 1>(x, x_token_stride, weight, bias, y, B, L, C, K, stream);
+  }
+  if (vec && C % 4 == 0) return dispatch_k<F32, 4>(x, x_token_stride, weight, bias, y, B, L, C, K, stream);
+  return dispatch_k<F32, 1>(x, x_token_stride, weight, bias, y, B, L, C, K, stream);
+}
+
+extern "C" int cdssm_conv1d_silu_fwd(int dtype, const void* x, const void* weight, const void* bias, void* y,
+                                     int64_t B, int64_t L, int64_t C, int64_t K, hipStream_t stream) {
+  return cdssm_conv1d_silu_fwd_strided(dtype, x, C, weight, bias, y, B, L, C, K, stream);
 }

@@ -1,0 +1,488 @@
+// Fused elementwise and normalisation kernels of the CD-SSM block around the
+// scan (the scan's callers in block.py:140-229 and model.py:38-51), each one
+// pass over HBM with 16-byte vector loads:
+//   * RMSNorm               (x * rsqrt(mean(x^2) + eps)).to(dtype) * weight   modules.py:49-53
+//   * K/Q normalisation     x * rsqrt(sum x^2 + 1e-6) of K (a strided view of
+//                           the block's in_proj output) and Q, plus q.k per
+//                           (token, head) for the current-token shortcut      normalize_kq.cu:75-79,
+//                                                                             block.py:191-192, 202
+//   * shortcut readout      retrieved += sel_C s (q.k)^2 V vp                 block.py:202-211
+//   * GroupNorm statistics  mean and rstd per (batch row, group) over the
+//                           group's channels and all L positions              block.py:215-223
+//   * GroupNorm + gate      ((y - mean) rstd gamma + beta).to(dtype) * silu(z)
+//                           + D x_conv                                        block.py:216-225
+// Roundings to the model dtype happen where the reference's torch ops round
+// (each op's output), so a bf16 model keeps the reference's rounding points.
+#include "common.hpp"
+
+namespace cdssm {
+namespace lm {
+
+// Round to the element type (identity for fp32).
+template <typename T>
+__device__ __forceinline__ float rnd(float x) {
+  if constexpr (T::bytes == 2)
+    return bf16_to_f32(f32_to_bf16(x));
+  else
+    return x;
+}
+
+// Round a pair to the element type with one packed conversion (identity for fp32).
+template <typename T>
+__device__ __forceinline__ void rnd2(float& a, float& b) {
+  if constexpr (T::bytes == 2) {
+    const uint32_t p = pack_bf16x2(a, b);
+    a = bf16_lo(p);
+    b = bf16_hi(p);
+  }
+}
+
+// silu(u) = u sigmoid(u) with the hardware reciprocal (about 1 ulp)
+__device__ __forceinline__ float silu_fast(float u) { return u * __builtin_amdgcn_rcpf(1.0f + __expf(-u)); }
+
+// NV elements in registers: one 16-byte access (NV = 16 / element bytes, 8
+// bf16 or 4 fp32) or a single element (NV = 1).
+template <typename T, int NV = 16 / T::bytes>
+struct Vec16 {
+  static constexpr int N = NV;
+  static_assert(NV == 1 || NV * T::bytes == 16, "one element or 16 bytes");
+  float v[N];
+  __device__ __forceinline__ void load(const typename T::raw* p) {
+    if constexpr (NV == 1) {
+      v[0] = T::load(p);
+      return;
+    }
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    if constexpr (T::bytes == 2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = bf16_lo(w[i]);
+        v[2 * i + 1] = bf16_hi(w[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(w[i]);
+    }
+  }
+  __device__ __forceinline__ void store(typename T::raw* p) const {
+    if constexpr (NV == 1) {
+      T::store(p, v[0]);
+      return;
+    }
+    uint32_t w[4];
+    if constexpr (T::bytes == 2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = __float_as_uint(v[i]);
+    }
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// RMSNorm: one wave per row of C elements, N elements per access.
+// ---------------------------------------------------------------------------
+template <typename T, int N>
+__global__ __launch_bounds__(256) void rms_norm_kernel(const typename T::raw* __restrict__ x,
+                                                       const typename T::raw* __restrict__ w,
+                                                       typename T::raw* __restrict__ y, int64_t rows, int C,
+                                                       float eps) {
+  const int64_t row = int64_t(blockIdx.x) * 4 + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (row >= rows) return;  // whole waves: the reduction below stays inside one wave
+  const typename T::raw* xr = x + row * C;
+  float s = 0.0f;
+  for (int c = lane * N; c < C; c += kWave * N) {
+    Vec16<T, N> a;
+    a.load(xr + c);
+#pragma unroll
+    for (int i = 0; i < N; ++i) s = fmaf(a.v[i], a.v[i], s);
+  }
+  s = group_sum<kWave>(s);
+  const float r = rsqrtf(s / float(C) + eps);
+  for (int c = lane * N; c < C; c += kWave * N) {
+    Vec16<T, N> a, g;
+    a.load(xr + c);
+    g.load(w + c);
+#pragma unroll
+    for (int i = 0; i < N; ++i) a.v[i] = rnd<T>(a.v[i] * r) * g.v[i];
+    a.store(y + row * C + c);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// K/Q normalisation and q.k: LPR lanes per (token, head) row of D elements,
+// one 16-byte vector each (D = LPR * vector width).  K and Q rows are read
+// through a token stride (elements), so K may be a column slice of a wider
+// projection output; K^, Q^ (B, L, H, D) and qk (B, L, H) fp32 are dense.
+// ---------------------------------------------------------------------------
+template <typename T, int LPR>
+__global__ __launch_bounds__(256) void normalize_qk_kernel(const typename T::raw* __restrict__ k, int64_t k_ts,
+                                                           const typename T::raw* __restrict__ q, int64_t q_ts,
+                                                           typename T::raw* __restrict__ ko,
+                                                           typename T::raw* __restrict__ qo, float* __restrict__ qk,
+                                                           int64_t rows, int H) {
+  constexpr int N = Vec16<T>::N, D = LPR * N;
+  const int r = int((int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / LPR);  // rows < 2^31 (host check)
+  const int sub = threadIdx.x % LPR;
+  const bool ok = r < rows;
+  const int rr = ok ? r : int(rows) - 1;  // clamped row: every lane takes part in the reductions
+  const int tok = rr / H;
+  const int h = rr - tok * H;
+  Vec16<T> a, b;
+  a.load(k + int64_t(tok) * k_ts + h * D + sub * N);
+  b.load(q + int64_t(tok) * q_ts + h * D + sub * N);
+  float sk = 0.0f, sq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    sk = fmaf(a.v[i], a.v[i], sk);
+    sq = fmaf(b.v[i], b.v[i], sq);
+  }
+  sk = group_sum<LPR>(sk);
+  sq = group_sum<LPR>(sq);
+  const float ik = rsqrtf(sk + 1e-6f), iq = rsqrtf(sq + 1e-6f);
+  float d = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    a.v[i] = rnd<T>(a.v[i] * ik);
+    b.v[i] = rnd<T>(b.v[i] * iq);
+    d = fmaf(a.v[i], b.v[i], d);
+  }
+  d = group_sum<LPR>(d);
+  if (!ok) return;
+  a.store(ko + int64_t(r) * D + sub * N);
+  b.store(qo + int64_t(r) * D + sub * N);
+  if (sub == 0) qk[r] = d;
+}
+
+// ---------------------------------------------------------------------------
+// Current-token shortcut through the readout, per (token, head):
+//   retrieved[j] += scale * (q.k)^2 * sel_C * vp * V[j],  j = re, im.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void shortcut_kernel(typename T::raw* __restrict__ ret,
+                                                       const float* __restrict__ qk,
+                                                       const typename T::raw* __restrict__ v,
+                                                       const typename T::raw* __restrict__ vp,
+                                                       const typename T::raw* __restrict__ sel,
+                                                       const float* __restrict__ scale, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float x = qk[i];
+  const float c = scale[0] * x * x * T::load(sel + i) * T::load(vp + i);
+  T::store(ret + 2 * i, T::load(ret + 2 * i) + c * T::load(v + 2 * i));
+  T::store(ret + 2 * i + 1, T::load(ret + 2 * i + 1) + c * T::load(v + 2 * i + 1));
+}
+
+// ---------------------------------------------------------------------------
+// GroupNorm statistics over (L positions x Cg channels) per (b, g), Cg = C/G.
+// Sums of (x - K) and (x - K)^2 with a shift K = y[b, 0, g Cg] (the first
+// element of the group), which keeps the variance free of cancellation when
+// the mean is far from zero.  Partial sums per (b, g, split) in a fixed order,
+// then one thread per (b, g) adds the splits in order: deterministic.
+// ---------------------------------------------------------------------------
+constexpr int kGnThreads = 256;
+
+template <typename T, int N>
+__global__ __launch_bounds__(kGnThreads) void gn_partial_kernel(const typename T::raw* __restrict__ y,
+                                                                float2* __restrict__ part, int L, int C, int G,
+                                                                int S) {
+  __shared__ float2 red[kGnThreads / kWave];
+  const int sp = blockIdx.x % S;
+  const int bg = blockIdx.x / S;
+  const int g = bg % G, b = bg / G;
+  const int Cg = C / G, vpt = Cg / N;  // vectors per token of the group
+  const int ls = (L + S - 1) / S;
+  const int t0 = sp * ls, t1 = min(L, t0 + ls);
+  const typename T::raw* base = y + int64_t(b) * L * C + int64_t(g) * Cg;
+  const float K = T::load(base);
+  float s1 = 0.0f, s2 = 0.0f;
+  const int nv = max(0, t1 - t0) * vpt;
+  for (int i = threadIdx.x; i < nv; i += kGnThreads) {
+    const int t = t0 + i / vpt;
+    const int c = (i % vpt) * N;
+    Vec16<T, N> a;
+    a.load(base + int64_t(t) * C + c);
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const float d = a.v[j] - K;
+      s1 += d;
+      s2 = fmaf(d, d, s2);
+    }
+  }
+  s1 = group_sum<kWave>(s1);
+  s2 = group_sum<kWave>(s2);
+  const int wv = threadIdx.x / kWave;
+  if (threadIdx.x % kWave == 0) red[wv] = make_float2(s1, s2);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float2 acc = red[0];
+#pragma unroll
+    for (int u = 1; u < kGnThreads / kWave; ++u) {
+      acc.x += red[u].x;
+      acc.y += red[u].y;
+    }
+    part[blockIdx.x] = acc;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void gn_finalize_kernel(const typename T::raw* __restrict__ y,
+                                                          const float2* __restrict__ part,
+                                                          float2* __restrict__ stats, int BG, int L, int C, int G,
+                                                          int S, float eps) {
+  const int bg = int(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (bg >= BG) return;
+  const int g = bg % G, b = bg / G;
+  const int Cg = C / G;
+  const float K = T::load(y + int64_t(b) * L * C + int64_t(g) * Cg);
+  float s1 = 0.0f, s2 = 0.0f;
+  for (int sp = 0; sp < S; ++sp) {
+    s1 += part[int64_t(bg) * S + sp].x;
+    s2 += part[int64_t(bg) * S + sp].y;
+  }
+  const float n = float(L) * float(Cg);
+  const float m = s1 / n;
+  const float var = fmaxf(s2 / n - m * m, 0.0f);
+  stats[bg] = make_float2(K + m, rsqrtf(var + eps));
+}
+
+// ---------------------------------------------------------------------------
+// GroupNorm apply + gate + skip, one 16-byte vector of channels per thread:
+//   a = rnd(((y - mean) rstd) gamma + beta);  s = rnd(silu(z));
+//   out = rnd(rnd(a s) + rnd(D x_conv))
+// z is read through a token stride (a column slice of the projection output).
+// ---------------------------------------------------------------------------
+template <typename T, typename P, int N>
+__global__ __launch_bounds__(256) void gn_gate_kernel(const typename T::raw* __restrict__ y,
+                                                      const float2* __restrict__ stats,
+                                                      const typename P::raw* __restrict__ gamma,
+                                                      const typename P::raw* __restrict__ beta,
+                                                      const typename T::raw* __restrict__ z, int64_t z_ts,
+                                                      const typename T::raw* __restrict__ xc,
+                                                      const typename T::raw* __restrict__ Dp,
+                                                      typename T::raw* __restrict__ out, int BL, int L, int C, int G) {
+  // block: 4 tokens x 64 channel vectors; grid (tokens / 4, vectors per row / 64)
+  const int tok = int(blockIdx.x) * 4 + int(threadIdx.x) / kWave;
+  const int c = (int(blockIdx.y) * kWave + int(threadIdx.x) % kWave) * N;
+  if (tok >= BL || c >= C) return;
+  const int b = tok / L;
+  const float2 st = stats[b * G + c / (C / G)];
+  Vec16<T, N> a, zz, xv, dv;
+  a.load(y + int64_t(tok) * C + c);
+  zz.load(z + int64_t(tok) * z_ts + c);
+  xv.load(xc + int64_t(tok) * C + c);
+  dv.load(Dp + c);
+  // the affine parameters in 16-byte pieces of their own type (or one at a time)
+  constexpr int M = 16 / P::bytes <= N ? 16 / P::bytes : 1;
+  float ga[N], be[N];
+#pragma unroll
+  for (int h = 0; h < N; h += M) {
+    Vec16<P, M> g, bb;
+    g.load(gamma + c + h);
+    bb.load(beta + c + h);
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+      ga[h + j] = g.v[j];
+      be[h + j] = bb.v[j];
+    }
+  }
+  float gn[N], s[N], p[N], d[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    gn[j] = fmaf((a.v[j] - st.x) * st.y, ga[j], be[j]);
+    s[j] = silu_fast(zz.v[j]);
+    d[j] = dv.v[j] * xv.v[j];
+  }
+  if constexpr (N == 1) {
+    gn[0] = rnd<T>(gn[0]);
+    s[0] = rnd<T>(s[0]);
+    d[0] = rnd<T>(d[0]);
+    p[0] = rnd<T>(gn[0] * s[0]);
+    a.v[0] = rnd<T>(p[0] + d[0]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; j += 2) {
+      rnd2<T>(gn[j], gn[j + 1]);
+      rnd2<T>(s[j], s[j + 1]);
+      rnd2<T>(d[j], d[j + 1]);
+      p[j] = gn[j] * s[j];
+      p[j + 1] = gn[j + 1] * s[j + 1];
+      rnd2<T>(p[j], p[j + 1]);
+      a.v[j] = p[j] + d[j];
+      a.v[j + 1] = p[j + 1] + d[j + 1];
+    }
+  }
+  a.store(out + int64_t(tok) * C + c);  // the store rounds the sum
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <typename F>
+int by_dtype(int dtype, const char* op, F&& f) {
+  if (dtype == 1) return f(BF16{});
+  if (dtype == 0) return f(F32{});
+  cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
+  return CDSSM_EINVAL;
+}
+
+}  // namespace lm
+}  // namespace cdssm
+
+using namespace cdssm;
+using namespace cdssm::lm;
+
+extern "C" int cdssm_rms_norm_fwd(int dtype, const void* x, const void* weight, void* y, int64_t rows, int64_t C,
+                                  float eps, hipStream_t stream) {
+  const char* op = "cdssm_rms_norm_fwd";
+  return by_dtype(dtype, op, [&](auto t) -> int {
+    using T = decltype(t);
+    if (rows <= 0 || C <= 0 || C > (1 << 24) || rows > (int64_t(1) << 31)) {
+      cdssm_host::set_error("%s: need rows > 0 and 0 < C <= 2^24 (rows=%lld C=%lld)", op, (long long)rows,
+                            (long long)C);
+      return CDSSM_EINVAL;
+    }
+    if (!x || !weight || !y) {
+      cdssm_host::set_error("%s: null pointer argument", op);
+      return CDSSM_EINVAL;
+    }
+    using raw = typename T::raw;
+    constexpr int NV = 16 / T::bytes;
+    const bool vec = C % NV == 0 && aligned16(x) && aligned16(weight) && aligned16(y);
+    auto go = [&](auto nc) {
+      constexpr int N = decltype(nc)::value;
+      hipLaunchKernelGGL((rms_norm_kernel<T, N>), dim3(unsigned((rows + 3) / 4)), dim3(256), 0, stream,
+                         static_cast<const raw*>(x), static_cast<const raw*>(weight), static_cast<raw*>(y), rows,
+                         int(C), eps);
+    };
+    if (vec)
+      go(std::integral_constant<int, NV>{});
+    else
+      go(std::integral_constant<int, 1>{});
+    return cdssm_host::check_launch(op);
+  });
+}
+
+extern "C" int cdssm_normalize_kq_qk_fwd(int dtype, const void* K, int64_t k_token_stride, const void* Q,
+                                         int64_t q_token_stride, void* K_out, void* Q_out, float* qk, int64_t BL,
+                                         int64_t H, int64_t D, hipStream_t stream) {
+  const char* op = "cdssm_normalize_kq_qk_fwd";
+  return by_dtype(dtype, op, [&](auto t) -> int {
+    using T = decltype(t);
+    using raw = typename T::raw;
+    constexpr int N = Vec16<T>::N;
+    const int64_t lpr = D / N;
+    if (BL <= 0 || H <= 0 || D % N != 0 || !(lpr == 4 || lpr == 8 || lpr == 16 || lpr == 32) ||
+        k_token_stride < H * D || q_token_stride < H * D || BL * H >= (int64_t(1) << 31)) {
+      cdssm_host::set_error("%s: need D in {%d, %d, %d, %d} and token strides >= H*D (BL=%lld H=%lld D=%lld)", op,
+                            4 * N, 8 * N, 16 * N, 32 * N, (long long)BL, (long long)H, (long long)D);
+      return CDSSM_EINVAL;
+    }
+    if (!K || !Q || !K_out || !Q_out || !qk || !aligned16(K) || !aligned16(Q) || !aligned16(K_out) ||
+        !aligned16(Q_out) || (k_token_stride * T::bytes) % 16 != 0 || (q_token_stride * T::bytes) % 16 != 0) {
+      cdssm_host::set_error("%s: pointers must be non-null and 16-byte aligned, token strides whole 16 bytes", op);
+      return CDSSM_EINVAL;
+    }
+    const int64_t rows = BL * H;
+    const unsigned grid = unsigned((rows * lpr + 255) / 256);
+    auto go = [&](auto lc) {
+      constexpr int LPR = decltype(lc)::value;
+      hipLaunchKernelGGL((normalize_qk_kernel<T, LPR>), dim3(grid), dim3(256), 0, stream,
+                         static_cast<const raw*>(K), k_token_stride, static_cast<const raw*>(Q), q_token_stride,
+                         static_cast<raw*>(K_out), static_cast<raw*>(Q_out), qk, rows, int(H));
+    };
+    if (lpr == 4) go(std::integral_constant<int, 4>{});
+    else if (lpr == 8) go(std::integral_constant<int, 8>{});
+    else if (lpr == 16) go(std::integral_constant<int, 16>{});
+    else go(std::integral_constant<int, 32>{});
+    return cdssm_host::check_launch(op);
+  });
+}
+
+extern "C" int cdssm_shortcut_readout_fwd(int dtype, void* retrieved, const float* qk, const void* V,
+                                          const void* vp, const void* sel_c, const float* scale, int64_t n,
+                                          hipStream_t stream) {
+  const char* op = "cdssm_shortcut_readout_fwd";
+  return by_dtype(dtype, op, [&](auto t) -> int {
+    using T = decltype(t);
+    using raw = typename T::raw;
+    if (n <= 0 || n > (int64_t(1) << 38)) {
+      cdssm_host::set_error("%s: need n > 0 (n=%lld)", op, (long long)n);
+      return CDSSM_EINVAL;
+    }
+    if (!retrieved || !qk || !V || !vp || !sel_c || !scale) {
+      cdssm_host::set_error("%s: null pointer argument", op);
+      return CDSSM_EINVAL;
+    }
+    hipLaunchKernelGGL(shortcut_kernel<T>, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<raw*>(retrieved), qk, static_cast<const raw*>(V), static_cast<const raw*>(vp),
+                       static_cast<const raw*>(sel_c), scale, n);
+    return cdssm_host::check_launch(op);
+  });
+}
+
+extern "C" int64_t cdssm_group_norm_workspace_bytes(int64_t B, int64_t G, int64_t L) {
+  if (B <= 0 || G <= 0 || L <= 0) return -1;
+  const int64_t S = std::min<int64_t>(16, std::max<int64_t>(1, L / 256));
+  return (B * G * S + B * G) * int64_t(sizeof(float2));
+}
+
+extern "C" int cdssm_group_norm_gate_fwd(int dtype, int param_dtype, const void* y, const void* gamma, const void* beta,
+                                         const void* z, int64_t z_token_stride, const void* x_conv, const void* Dp,
+                                         void* out, float* workspace, int64_t B, int64_t L, int64_t C, int64_t G,
+                                         float eps, hipStream_t stream) {
+  const char* op = "cdssm_group_norm_gate_fwd";
+  return by_dtype(dtype, op, [&](auto t) -> int {
+    using T = decltype(t);
+    using raw = typename T::raw;
+    if (param_dtype != 0 && param_dtype != 1) {
+      cdssm_host::set_error("%s: param_dtype must be 0 (fp32) or 1 (bf16), got %d", op, param_dtype);
+      return CDSSM_EINVAL;
+    }
+    if (B <= 0 || L <= 0 || C <= 0 || G <= 0 || C % G != 0 || z_token_stride < C || B * L >= (int64_t(1) << 31) ||
+        C >= (int64_t(1) << 24) || B * G * C > 0x7fffffffLL) {
+      cdssm_host::set_error("%s: need C divisible by G and a z token stride >= C (B=%lld L=%lld C=%lld G=%lld)",
+                            op, (long long)B, (long long)L, (long long)C, (long long)G);
+      return CDSSM_EINVAL;
+    }
+    if (!y || !gamma || !beta || !z || !x_conv || !Dp || !out || !workspace) {
+      cdssm_host::set_error("%s: null pointer argument", op);
+      return CDSSM_EINVAL;
+    }
+    // 16-byte vectors where every access stays aligned, else one element per access
+    constexpr int NV = 16 / T::bytes;
+    const bool vec = (C / G) % NV == 0 && aligned16(y) && aligned16(z) && aligned16(x_conv) && aligned16(Dp) &&
+                     aligned16(out) && aligned16(gamma) && aligned16(beta) && (z_token_stride * T::bytes) % 16 == 0;
+    const int S = int(std::min<int64_t>(16, std::max<int64_t>(1, L / 256)));
+    const int BG = int(B * G);
+    float2* part = reinterpret_cast<float2*>(workspace);
+    float2* stats = part + int64_t(BG) * S;
+    auto go = [&](auto nc, auto pt) {
+      constexpr int N = decltype(nc)::value;
+      using P = decltype(pt);
+      using praw = typename P::raw;
+      hipLaunchKernelGGL((gn_partial_kernel<T, N>), dim3(unsigned(BG * S)), dim3(kGnThreads), 0, stream,
+                         static_cast<const raw*>(y), part, int(L), int(C), int(G), S);
+      hipLaunchKernelGGL(gn_finalize_kernel<T>, dim3(unsigned((BG + 255) / 256)), dim3(256), 0, stream,
+                         static_cast<const raw*>(y), part, stats, BG, int(L), int(C), int(G), S, eps);
+      const int vpr = int(C) / N;
+      const dim3 grid(unsigned((B * L + 3) / 4), unsigned((vpr + kWave - 1) / kWave));
+      hipLaunchKernelGGL((gn_gate_kernel<T, P, N>), grid, dim3(256), 0, stream, static_cast<const raw*>(y), stats,
+                         static_cast<const praw*>(gamma), static_cast<const praw*>(beta), static_cast<const raw*>(z),
+                         z_token_stride, static_cast<const raw*>(x_conv), static_cast<const raw*>(Dp),
+                         static_cast<raw*>(out), int(B * L), int(L), int(C), int(G));
+    };
+    if (vec && param_dtype == 1)
+      go(std::integral_constant<int, NV>{}, BF16{});
+    else if (vec)
+      go(std::integral_constant<int, NV>{}, F32{});
+    else if (param_dtype == 1)
+      go(std::integral_constant<int, 1>{}, BF16{});
+    else
+      go(std::integral_constant<int, 1>{}, F32{});
+    return cdssm_host::check_launch(op);
+  });
+}

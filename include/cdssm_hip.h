@@ -247,10 +247,73 @@ int cdssm_dynamics_fused_bwd(int dtype, const void* grad_A_bar, const void* grad
  * Conv1dSiLU, modules.py:14-35): causal depthwise conv + SiLU,
  *   y[b,t,c] = silu(bias[c] + sum_{j<K} w[c,j] x[b, t-(K-1)+j, c]), x = 0 before t = 0.
  * x, y (B,L,C); weight (C,1,K); bias (C); all `dtype` (the reference: bf16,
- * K = 4 only).  Supported: 1 <= K <= 8.  Forward only.
+ * K = 4 only).  Supported: 1 <= K <= 8, B * ceil(L/16) * C < 2^31.  Forward only.
  */
 int cdssm_conv1d_silu_fwd(int dtype, const void* x, const void* weight, const void* bias, void* y, int64_t B,
                           int64_t L, int64_t C, int64_t K, hipStream_t stream);
+
+/*
+ * cdssm_conv1d_silu_fwd with x read through a token stride (elements between
+ * consecutive tokens, >= C): the block's conv input x_gate is a column slice
+ * of the in_proj output (block.py:162-166, 177), which this reads in place
+ * instead of copying it.  The reference's launcher calls .contiguous() on
+ * the slice (conv1d_silu.cu:223-274).
+ */
+int cdssm_conv1d_silu_fwd_strided(int dtype, const void* x, int64_t x_token_stride, const void* weight,
+                                  const void* bias, void* y, int64_t B, int64_t L, int64_t C, int64_t K,
+                                  hipStream_t stream);
+
+/*
+ * Replaces RMSNorm.forward (modules.py:49-53):
+ *   y = (x * rsqrt(mean(x^2) + eps)).to(dtype) * weight,
+ * statistics in fp32; x, y (rows, C) dense, weight (C), all `dtype`.
+ */
+int cdssm_rms_norm_fwd(int dtype, const void* x, const void* weight, void* y, int64_t rows, int64_t C, float eps,
+                       hipStream_t stream);
+
+/*
+ * Replaces the block's two NormalizeKQFn.forward calls (block.py:191-192 ->
+ * normalize_kq.cu:75-79, x * rsqrt(sum x^2 + 1e-6) per (token, head)) and the
+ * shortcut's q.k (block.py:202, einsum 'blhd,blhd->blh') in one pass.  K and Q
+ * rows (H*D elements per token) are read through token strides (elements;
+ * K may be the in_proj output's column slice); K_out, Q_out (B*L, H, D) dense
+ * in `dtype`; qk (B*L, H) fp32 from the rounded K_out, Q_out.  D = 32, 64,
+ * 128 or 256 (bf16) / 16, 32, 64 or 128 (fp32).
+ */
+int cdssm_normalize_kq_qk_fwd(int dtype, const void* K, int64_t k_token_stride, const void* Q,
+                              int64_t q_token_stride, void* K_out, void* Q_out, float* qk, int64_t BL, int64_t H,
+                              int64_t D, hipStream_t stream);
+
+/*
+ * The current-token shortcut (block.py:202-205) carried through the readout
+ * (block.py:208-211): shortcut_scale (q.k) V_gated k^T read by q and gated
+ * by sel_C adds sel_C * scale * (q.k)^2 * vp * V to the retrieved pair, in
+ * place:  retrieved (n, 2), V (n, 2), vp, sel_c (n) in `dtype`; qk (n) fp32;
+ * scale: one fp32 on the device.  n = B*L*H.
+ */
+int cdssm_shortcut_readout_fwd(int dtype, void* retrieved, const float* qk, const void* V, const void* vp,
+                               const void* sel_c, const float* scale, int64_t n, hipStream_t stream);
+
+/* Bytes of the fp32 workspace cdssm_group_norm_gate_fwd needs (-1 if invalid). */
+int64_t cdssm_group_norm_workspace_bytes(int64_t B, int64_t G, int64_t L);
+
+/*
+ * Replaces the block's epilogue after readout_proj (block.py:215-225):
+ *   a = GroupNorm_G(y)  (statistics per (b, group) over the group's C/G
+ *       channels and all L positions, fp32, biased variance, eps; affine
+ *       gamma, beta in fp32), rounded to `dtype`;
+ *   out = a * silu(z) + D * x_conv, each product and the sum rounded to `dtype`
+ * as the reference's torch ops round them.  y, x_conv, out (B, L, C) dense;
+ * z read through a token stride (the in_proj output's column slice);
+ * gamma, beta (C) of `param_dtype` (0 fp32, 1 bf16; read exactly, as the
+ * reference's .float()); D (C) `dtype`; C divisible by G.  Three launches
+ * (partial sums, per-group statistics, apply); workspace of
+ * cdssm_group_norm_workspace_bytes.
+ */
+int cdssm_group_norm_gate_fwd(int dtype, int param_dtype, const void* y, const void* gamma, const void* beta,
+                              const void* z, int64_t z_token_stride, const void* x_conv, const void* D, void* out,
+                              float* workspace, int64_t B, int64_t L, int64_t C, int64_t G, float eps,
+                              hipStream_t stream);
 
 /*
  * Replaces normalize_kq_fwd_cuda / normalize_kq_bwd_cuda (normalize_kq.cu:168-244;

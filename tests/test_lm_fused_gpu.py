@@ -1,0 +1,123 @@
+"""GPU parity of the block's fused elementwise / normalisation kernels
+(cdssm_rms_norm_fwd, cdssm_normalize_kq_qk_fwd, cdssm_shortcut_readout_fwd,
+cdssm_group_norm_gate_fwd, cdssm_conv1d_silu_fwd_strided) against the CPU
+oracle's restatements in fp64 on the same (dtype-rounded) inputs.
+
+Tolerances (normwise max|x-ref|/max|ref|): fp32 1e-5 (fp32 statistics and
+hardware rsqrt / exp); bf16 1e-2 (the outputs are rounded to bf16 at the
+reference's rounding points, each a relative 2^-9, a few in a row for the
+gated GroupNorm output).
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from _gpu_util import DEV, log, rel
+from oracle import cdssm_lm_oracle as lo
+from oracle import cdssm_oracle as o
+
+pytestmark = pytest.mark.gpu
+
+
+def _tol(dtype):
+    return 1e-5 if dtype == torch.float32 else 1e-2
+
+
+@pytest.mark.parametrize("dtype,rows,C", [(torch.float32, 33, 128), (torch.bfloat16, 100, 1024),
+                                          (torch.bfloat16, 7, 20), (torch.float32, 5, 3)])
+def test_rms_norm(dtype, rows, C):
+    from cdssm_hip.lm import rms_norm
+    log(f"[rms_norm] {dtype} rows {rows} C {C}")
+    g = torch.Generator().manual_seed(1)
+    x = (torch.randn(rows, C, generator=g) * 3 + 0.5).to(dtype)
+    w = (1 + 0.1 * torch.randn(C, generator=g)).to(dtype)
+    eps = 6.103515625e-05
+    y = rms_norm(x.to(DEV), w.to(DEV), eps).cpu()
+    yr = lo.rms_norm(x.double(), w.double(), eps)
+    e = rel(y, yr)
+    log(f"   rel err {e:.2e}")
+    assert y.dtype == dtype and e <= _tol(dtype)
+
+
+@pytest.mark.parametrize("dtype,B,L,H,D,pad", [(torch.bfloat16, 2, 50, 16, 64, 96), (torch.float32, 1, 9, 3, 64, 0),
+                                               (torch.bfloat16, 1, 4, 2, 128, 8), (torch.float32, 2, 5, 2, 128, 4),
+                                               (torch.bfloat16, 1, 1, 1, 32, 0)])
+def test_normalize_kq_qk(dtype, B, L, H, D, pad):
+    """K read as a column slice of a wider (B, L, pad + H*D + 8) tensor, as from the block's in_proj."""
+    from cdssm_hip.lm import normalize_kq_qk
+    log(f"[normalize_kq_qk] {dtype} B{B} L{L} H{H} D{D} K column offset {pad}")
+    g = torch.Generator().manual_seed(2)
+    wide = torch.randn(B, L, pad + H * D + 8, generator=g).to(dtype)
+    q = torch.randn(B, L, H, D, generator=g).to(dtype)
+    wd = wide.to(DEV)
+    Kv = wd[..., pad:pad + H * D].reshape(B, L, H, D)
+    assert not Kv.is_contiguous() or pad == 0
+    Ko, Qo, qk = normalize_kq_qk(Kv, q.to(DEV))
+    Kr, Qr = o.normalize_kq(wide[..., pad:pad + H * D].reshape(B, L, H, D).double(), q.double())
+    ek, eq = rel(Ko.cpu(), Kr), rel(Qo.cpu(), Qr)
+    # qk from the kernel's own (rounded) outputs, in fp64
+    eqk = rel(qk.cpu(), (Ko.cpu().double() * Qo.cpu().double()).sum(-1))
+    log(f"   rel err K {ek:.2e} Q {eq:.2e} qk {eqk:.2e}")
+    assert ek <= _tol(dtype) and eq <= _tol(dtype) and eqk <= 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_shortcut_readout(dtype):
+    from cdssm_hip.lm import shortcut_readout_
+    B, L, H = 2, 33, 4
+    log(f"[shortcut_readout] {dtype} B{B} L{L} H{H}")
+    g = torch.Generator().manual_seed(3)
+    ret = torch.randn(B, L, H, 2, generator=g).to(dtype)
+    qk = torch.rand(B, L, H, generator=g) * 2 - 1
+    V = torch.randn(B, L, H, 2, generator=g).to(dtype)
+    vp = torch.rand(B, L, H, 1, generator=g).to(dtype)
+    sel = torch.rand(B, L, H, generator=g).to(dtype)
+    scale = torch.tensor([0.7])
+    out = shortcut_readout_(ret.to(DEV), qk.to(DEV), V.to(DEV), vp.to(DEV), sel.to(DEV), scale.to(DEV)).cpu()
+    # the reference's form: Y += s (q.k) V_gated k^T, read by q and gated by sel_C (block.py:202-211), with q.k
+    # standing for both the shortcut's factor and the readout's k.q
+    ref = ret.double() + (0.7 * qk.double() ** 2 * sel.double())[..., None] * V.double() * vp.double()
+    e = rel(out, ref)
+    log(f"   rel err {e:.2e}")
+    assert e <= _tol(dtype)
+
+
+@pytest.mark.parametrize("dtype,B,L,C,G,zpad", [(torch.bfloat16, 2, 300, 1024, 32, 64), (torch.float32, 1, 77, 128, 32, 0),
+                                                 (torch.bfloat16, 1, 40, 128, 32, 8), (torch.bfloat16, 2, 513, 96, 3, 3),
+                                                 (torch.float32, 3, 1, 64, 4, 4)])
+def test_group_norm_gate(dtype, B, L, C, G, zpad):
+    from cdssm_hip.lm import group_norm_gate
+    log(f"[group_norm_gate] {dtype} B{B} L{L} C{C} G{G} z column offset {zpad}")
+    g = torch.Generator().manual_seed(4)
+    y = (torch.randn(B, L, C, generator=g) * 2 + 3).to(dtype)  # a mean far from zero
+    zw = torch.randn(B, L, zpad + C + 5, generator=g).to(dtype)
+    xc = torch.randn(B, L, C, generator=g).to(dtype)
+    gamma = 1 + 0.2 * torch.randn(C, generator=g)
+    beta = 0.1 * torch.randn(C, generator=g)
+    Dp = (0.3 * torch.randn(C, generator=g)).to(dtype)
+    eps = 1e-5
+    zd = zw.to(DEV)[..., zpad:zpad + C]
+    out = group_norm_gate(y.to(DEV), G, gamma.to(DEV), beta.to(DEV), eps, zd, xc.to(DEV), Dp.to(DEV)).cpu()
+    z = zw[..., zpad:zpad + C].double()
+    gn = F.group_norm(y.double().transpose(1, 2), G, gamma.double(), beta.double(), eps).transpose(1, 2)
+    ref = gn * (z * torch.sigmoid(z)) + Dp.double() * xc.double()  # block.py:216-225
+    e = rel(out, ref)
+    log(f"   rel err {e:.2e}")
+    assert out.dtype == dtype and e <= (1e-5 if dtype == torch.float32 else 2e-2)
+
+
+@pytest.mark.parametrize("dtype,B,L,C,K,pad", [(torch.bfloat16, 2, 130, 1024, 4, 1024), (torch.float32, 1, 20, 12, 3, 5)])
+def test_conv1d_silu_strided(dtype, B, L, C, K, pad):
+    """conv input read in place as a column slice (the block's x_gate)."""
+    from cdssm_hip.lm import conv1d_silu
+    log(f"[conv1d_silu strided] {dtype} B{B} L{L} C{C} K{K} column offset {pad}")
+    g = torch.Generator().manual_seed(5)
+    wide = torch.randn(B, L, pad + C + 16, generator=g).to(dtype)
+    w = (torch.randn(C, 1, K, generator=g) / K ** 0.5).to(dtype)
+    b = torch.randn(C, generator=g).to(dtype)
+    y = conv1d_silu(wide.to(DEV)[..., pad:pad + C], w.to(DEV), b.to(DEV)).cpu()
+    yr = lo.conv1d_silu(wide[..., pad:pad + C].double(), w.double(), b.double())
+    e = rel(y, yr)
+    log(f"   rel err {e:.2e}")
+    assert e <= (1e-6 if dtype == torch.float32 else 1e-2)
