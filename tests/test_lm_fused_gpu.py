@@ -80,6 +80,10 @@ def test_shortcut_readout(dtype):
     ref = ret.double() + (0.7 * qk.double() ** 2 * sel.double())[..., None] * V.double() * vp.double()
     e = rel(out, ref)
     log(f"   rel err {e:.2e}")
+    if not e <= _tol(dtype):
+        bad = (out.double() - ref).abs() > 1e-3
+        log(f"   bad {int(bad.sum())} of {bad.numel()}; first {bad.nonzero()[:4].tolist()}; "
+            f"out {out[bad][:4].tolist()} ref {ref[bad][:4].tolist()}")
     assert e <= _tol(dtype)
 
 
