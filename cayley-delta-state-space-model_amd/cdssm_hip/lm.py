@@ -220,6 +220,9 @@ def shortcut_readout_(retrieved: Tensor, qk: Tensor, V: Tensor, vp: Tensor, sel_
     """In place: retrieved += sel_C * scale * qk^2 * vp * V (the shortcut of block.py:202-205 through the
     readout of block.py:208-211).  retrieved, V (B, L, H, 2); vp (B, L, H, 1); sel_C (B, L, H); qk fp32."""
     dt = _check_gpu("shortcut_readout", retrieved, V, vp, sel_C)
+    if qk.device != retrieved.device or not qk.is_floating_point():
+        raise TypeError(f"qk must be a floating tensor on {retrieved.device}, got {qk.dtype} on {qk.device}")
+    qk = qk.to(torch.float32)  # the kernel reads fp32 q.k
     for n, t in dict(retrieved=retrieved, V=V, vp=vp, sel_C=sel_C, qk=qk).items():
         if not t.is_contiguous():
             raise ValueError(f"{n} must be contiguous")

@@ -62,18 +62,20 @@ def test_normalize_kq_qk(dtype, B, L, H, D, pad):
     assert ek <= _tol(dtype) and eq <= _tol(dtype) and eqk <= 1e-5
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_shortcut_readout(dtype):
+@pytest.mark.parametrize("dtype,qk_dtype", [(torch.float32, torch.float32), (torch.bfloat16, torch.float32),
+                                            (torch.float32, torch.float64)])
+def test_shortcut_readout(dtype, qk_dtype):
+    """qk in fp64 too: the wrapper hands the kernel fp32 whatever floating dtype it gets."""
     from cdssm_hip.lm import shortcut_readout_
     B, L, H = 2, 33, 4
-    log(f"[shortcut_readout] {dtype} B{B} L{L} H{H}")
+    log(f"[shortcut_readout] {dtype} qk {qk_dtype} B{B} L{L} H{H}")
     g = torch.Generator().manual_seed(3)
-    ret = torch.randn(B, L, H, 2, generator=g).to(dtype)
-    qk = torch.rand(B, L, H, generator=g) * 2 - 1
-    V = torch.randn(B, L, H, 2, generator=g).to(dtype)
-    vp = torch.rand(B, L, H, 1, generator=g).to(dtype)
-    sel = torch.rand(B, L, H, generator=g).to(dtype)
-    scale = torch.tensor([0.7])
+    ret = torch.randn(B, L, H, 2, generator=g, dtype=torch.float32).to(dtype)
+    qk = torch.rand(B, L, H, generator=g, dtype=torch.float32).to(qk_dtype) * 2 - 1
+    V = torch.randn(B, L, H, 2, generator=g, dtype=torch.float32).to(dtype)
+    vp = torch.rand(B, L, H, 1, generator=g, dtype=torch.float32).to(dtype)
+    sel = torch.rand(B, L, H, generator=g, dtype=torch.float32).to(dtype)
+    scale = torch.tensor([0.7], dtype=torch.float32)
     out = shortcut_readout_(ret.to(DEV), qk.to(DEV), V.to(DEV), vp.to(DEV), sel.to(DEV), scale.to(DEV)).cpu()
     # the reference's form: Y += s (q.k) V_gated k^T, read by q and gated by sel_C (block.py:202-211), with q.k
     # standing for both the shortcut's factor and the readout's k.q

@@ -17,8 +17,17 @@ import torch
 
 from oracle import cdssm_oracle as o
 
-torch.set_default_dtype(torch.float64)
 DT = torch.float64
+
+
+@pytest.fixture(autouse=True)
+def _fp64_default():
+    """fp64 as torch's default dtype for this module's tests only, restored after each (a module-level
+    setting would leak into every other test module of the session)."""
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(prev)
 
 
 def rng(seed=0):
