@@ -197,6 +197,59 @@ def time_decode(steps, warmup, B=64, H=16, D=64, prompt=2048):
             "note": "steps launched back to back from Python through ctypes; per-step time includes the launch"}
 
 
+def time_lm_decode(steps=20, warmup=3, B=64, prompt=2048):
+    """Config-4 model decode: the 24-layer LM (as time_lm_forward) prefilled with a 2048-token prompt at
+    batch 64, then one new token per row per step (no re-forward): CDSSMLMHeadModel.decode_step eagerly,
+    then the same step captured in a HIP graph (DecodeGraph).  Time per step (HIP events around `steps`
+    back-to-back steps); ms_per_step is the graph's."""
+    import torch
+    from cdssm_hip.lm import CDSSMConfig, CDSSMLMHeadModel
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    cfg = CDSSMConfig(d_model=1024, n_layers=24, context_length=2048, vocab_size=32000, state_dim=2, d_inner=1024)
+    m = CDSSMLMHeadModel(cfg).to(torch.bfloat16).to(dev).eval()
+    g = torch.Generator().manual_seed(2)
+    ids = torch.randint(0, cfg.vocab_size, (B, prompt), generator=g).to(dev)
+    new = torch.randint(0, cfg.vocab_size, (warmup + steps, B), generator=g).to(dev)
+    stream = torch.cuda.current_stream(dev)
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        p0.record(stream)
+        _, caches = m.prefill(ids)
+        p1.record(stream)
+        for i in range(warmup):
+            m.decode_step(new[i], caches)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            m.decode_step(new[warmup + i], caches)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        # the same step captured in one HIP graph (continues from the eager steps' state)
+        dg = m.decode_graph(caches)
+        for i in range(warmup):
+            dg(new[i])
+        torch.cuda.synchronize()
+        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        g0.record(stream)
+        for i in range(steps):
+            dg(new[warmup + i])
+        g1.record(stream)
+        torch.cuda.synchronize()
+    ms_eager = e0.elapsed_time(e1) / steps
+    ms = g0.elapsed_time(g1) / steps
+    wbytes = sum(p.numel() * p.element_size() for p in m.parameters())
+    return {"workload": f"config 4: LM decode step B{B} from a {prompt}-token prefill, 24 layers, bf16",
+            "ms_per_step": ms, "tokens_per_s": B / (ms * 1e-3), "eager_ms_per_step": ms_eager,
+            "prefill_ms": p0.elapsed_time(p1), "weight_bytes": wbytes, "weight_read_GBs": wbytes / (ms * 1e-3) / 1e9,
+            "note": "one HIP graph per step (DecodeGraph; eager: about 15 launches per layer); per layer: RMSNorm, "
+                    "conv step, dynamics at the position, K/Q norm, scan decode step, shortcut, GroupNorm step on "
+                    "the HIP kernels, GEMMs on torch"}
+
+
 def time_lm_forward(steps=5, warmup=2):
     """Config-4 LM forward: B8 L2048, d_model 1024, 24 layers, 16 heads x 64 (d_inner = 1024,
     as the config states), state_dim 2, vocab 32000, bf16, random init (the reference's
@@ -382,6 +435,7 @@ def main():
         if not args.no_extras:
             out["decode"] = time_decode(200, 20)
             out["lm_forward"] = time_lm_forward()
+            out["lm_decode"] = time_lm_decode()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg, x, args.cpu_sample_batches)
     print(json.dumps(out), flush=True)

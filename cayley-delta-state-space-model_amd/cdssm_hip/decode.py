@@ -17,7 +17,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib
-from .scan import chunkwise_delta_scan
+from .scan import chunkwise_delta_scan, chunkwise_delta_scan_abar
 
 Tensor = torch.Tensor
 
@@ -118,5 +118,56 @@ def prefill(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_C: Tensor, dt: Te
     for t in range(L0, L):
         tok = [x[:, t] for x in (q, k, v, beta, sel_C, dt, r)]
         ys.append(decode_step(st, *tok, alpha, omega, c).unsqueeze(1))
+    y = torch.cat(ys, dim=1) if len(ys) > 1 else ys[0]
+    return y, st
+
+
+def decode_step_abar(st: DecodeState, q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_C: Tensor, A_bar: Tensor,
+                     vp: Tensor, return_carry: bool = False):
+    """``decode_step`` on the gate-level inputs: A_bar (B, H, 2) and vp (B, H) (or (B, H, 1), or the
+    (B, 1, H, ...) slices) of the token in place of (dt, r, alpha, omega, c); the form the model's scan
+    takes (``chunkwise_delta_scan_abar``)."""
+    B, H, D = st.shape
+    dev = st.state.device
+    if q.device != dev:
+        raise RuntimeError(f"inputs are on {q.device}, the state on {dev}")
+    dtype = q.dtype
+    if dtype not in _lib.DTYPE_CODE:
+        raise TypeError(f"inputs must be float32 or bfloat16, got {dtype}")
+    vp = vp.reshape(B, H) if vp.numel() == B * H else vp
+    toks = dict(q=_token(q, B, H, (D,), "q"), k=_token(k, B, H, (D,), "k"), v=_token(v, B, H, (2,), "v"),
+                beta=_token(beta, B, H, (), "beta"), sel_C=_token(sel_C, B, H, (), "sel_C"),
+                A_bar=_token(A_bar, B, H, (2,), "A_bar"), vp=_token(vp, B, H, (), "vp"))
+    for n, t in toks.items():
+        if t.dtype != dtype or t.device != dev:
+            raise TypeError(f"{n} is {t.dtype} on {t.device}, expected {dtype} on {dev}")
+    y = torch.empty(B, H, 2, dtype=dtype, device=dev)
+    h = torch.empty(B, H, 2, D, dtype=torch.float32, device=dev) if return_carry else None
+    status = _lib.load().cdssm_decode_step_abar(
+        _lib.DTYPE_CODE[dtype], *[_lib.ptr(toks[n]) for n in ("q", "k", "v", "beta", "sel_C", "A_bar", "vp")],
+        _lib.ptr(st.state), _lib.ptr(st.gam), _lib.ptr(st.pos), _lib.ptr(y), _lib.ptr(h), B, H, D, 2,
+        st.chunk_size, _lib.stream_of(dev))
+    _lib.check(status, "cdssm_decode_step_abar")
+    return (y, h) if return_carry else y
+
+
+def prefill_abar(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_C: Tensor, A_bar: Tensor, vp: Tensor,
+                 chunk_size: Optional[int] = None) -> Tuple[Tensor, DecodeState]:
+    """``prefill`` on the gate-level inputs: y (B, L, H, 2) of the prompt and the decode state after it
+    (the chunk-aligned prefix through ``chunkwise_delta_scan_abar``, the rest through decode steps)."""
+    B, L, H, D = q.shape
+    Q = D if chunk_size is None else int(chunk_size)
+    L0 = (L // Q) * Q
+    ys = []
+    if L0 > 0:
+        pre = [x[:, :L0] for x in (q, k, v, beta, sel_C, A_bar, vp)]
+        y0, h = chunkwise_delta_scan_abar(*pre, chunk_size=Q)
+        ys.append(y0)
+        st = DecodeState.at_boundary(h, B, H, D, Q, q.device)
+    else:
+        st = DecodeState.at_boundary(None, B, H, D, Q, q.device)
+    for t in range(L0, L):
+        tok = [x[:, t] for x in (q, k, v, beta, sel_C, A_bar, vp)]
+        ys.append(decode_step_abar(st, *tok).unsqueeze(1))
     y = torch.cat(ys, dim=1) if len(ys) > 1 else ys[0]
     return y, st

@@ -10,19 +10,25 @@ vp (HIP, ``cdssm_fused_scan_fwd_abar``) -> current-token shortcut (HIP) ->
 readout_proj -> fp32 GroupNorm, * silu(z), + D x (HIP) -> out_proj with the
 residual in the GEMM epilogue.  Dense projections and the embedding are
 PyTorch (hipBLASLt GEMMs).  Forward only: these kernels have no backward here.
+
+Generation: ``CDSSMLMHeadModel.prefill`` runs the forward over a prompt and keeps
+per-layer decode state (conv window, the scan's R-mode state, GroupNorm running
+sums, position); ``decode_step`` then advances one token per row without
+re-forwarding (the reference re-forwards, predict.py:53-67).
 """
 
 from __future__ import annotations
 
 import math
 from dataclasses import dataclass, field
-from typing import Optional
+from typing import List, Optional
 
 import torch
 import torch.nn as nn
 
 from . import _lib
 from .ops import DynamicsFusedFn
+from .decode import DecodeState, decode_step_abar, prefill_abar
 from .scan import chunkwise_delta_scan_abar
 
 Tensor = torch.Tensor
@@ -143,12 +149,23 @@ def _check_gpu(op: str, *ts: Tensor) -> torch.dtype:
     return dt
 
 
+def _token_stride(x: Tensor, dense: int) -> Optional[int]:
+    """Stride (elements) between consecutive tokens b * L + l of a (B, L, ...) view, or None when the B*L
+    tokens are not uniformly strided; ``dense`` (the elements of one token) when there is one token."""
+    B, L = x.shape[0], x.shape[1]
+    if L > 1 and B > 1:
+        return x.stride(1) if x.stride(0) == L * x.stride(1) else None
+    if L > 1:
+        return x.stride(1)
+    return x.stride(0) if B > 1 else dense
+
+
 def _token_view(x: Tensor, width: int) -> int:
     """Token stride (elements) of a (B, L, width) view whose rows are dense; raises otherwise."""
-    B, L = x.shape[0], x.shape[1]
-    if x.stride(-1) != 1 or (L > 1 and B > 1 and x.stride(0) != L * x.stride(1)):
+    ts = _token_stride(x, width)
+    if x.stride(-1) != 1 or ts is None:
         raise ValueError("expected a (B, L, C) view with dense channels and a uniform token stride")
-    return x.stride(1) if L > 1 else (x.stride(0) if B > 1 else width)
+    return ts
 
 
 def conv1d_silu(x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
@@ -198,10 +215,10 @@ def normalize_kq_qk(K: Tensor, Q: Tensor) -> tuple:
         raise ValueError(f"K and Q shapes differ: {tuple(K.shape)} vs {tuple(Q.shape)}")
     strides, dense = [], []
     for t in (K, Q):
-        ts = t.stride(1) if L > 1 else H * D
+        ts = _token_stride(t, H * D)
         # read in place when the rows are dense and 16-byte aligned, else from a dense copy
-        if (t.stride(3) != 1 or t.stride(2) != D or (L > 1 and t.stride(0) != L * t.stride(1))
-                or t.data_ptr() % 16 or (ts * t.element_size()) % 16):
+        if (t.stride(3) != 1 or t.stride(2) != D or ts is None or t.data_ptr() % 16
+                or (ts * t.element_size()) % 16):
             t, ts = t.contiguous(), H * D
         strides.append(ts)
         dense.append(t)
@@ -238,16 +255,22 @@ def shortcut_readout_(retrieved: Tensor, qk: Tensor, V: Tensor, vp: Tensor, sel_
 
 
 def group_norm_gate(y: Tensor, num_groups: int, gamma: Tensor, beta: Tensor, eps: float, z: Tensor,
-                    x_conv: Tensor, D: Tensor) -> Tensor:
+                    x_conv: Tensor, D: Tensor, return_sums: bool = False):
     """GroupNorm over (channels of a group, all L) in fp32, cast to y's dtype, * silu(z) + D * x_conv
-    (block.py:215-225).  y, x_conv (B, L, C) dense; z (B, L, C) with any token stride."""
+    (block.py:215-225).  y, x_conv (B, L, C) dense; z (B, L, C) with any token stride.  With
+    ``return_sums`` also the running statistics a decode step continues from (``group_norm_sums``'s
+    layout), taken from the kernel's own partial sums."""
     Dp = D.to(y.dtype).contiguous()
     dt = _check_gpu("group_norm_gate", y, z, x_conv, Dp)
     B, L, C = y.shape
     if tuple(z.shape) != (B, L, C) or tuple(x_conv.shape) != (B, L, C):
         raise ValueError("y, z and x_conv must all be (B, L, C)")
     yc, xc = y.contiguous(), x_conv.contiguous()
-    zs = _token_view(z, C)
+    try:
+        zs = _token_view(z, C)
+    except ValueError:  # not one uniform token stride (e.g. a slice along L of a column slice): a dense copy
+        z = z.contiguous()
+        zs = C
     # the affine parameters are read in their own dtype (bf16 or fp32) and widened exactly in the kernel
     pdt = gamma.dtype if gamma.dtype in _lib.DTYPE_CODE else torch.float32
     g = gamma.detach().to(device=y.device, dtype=pdt).contiguous()
@@ -263,7 +286,15 @@ def group_norm_gate(y: Tensor, num_groups: int, gamma: Tensor, beta: Tensor, eps
                                        _lib.ptr(xc), _lib.ptr(Dp), _lib.ptr(out), _lib.ptr(ws), B, L, C, num_groups,
                                        float(eps), _lib.stream_of(y.device))
     _lib.check(st, "cdssm_group_norm_gate_fwd")
-    return out
+    if not return_sums:
+        return out
+    # the partial sums (B, G, S) of (x - shift, (x - shift)^2), shift = the group's first element
+    G = int(num_groups)
+    S = (nb // 8 - B * G) // (B * G)
+    part = ws[:B * G * S * 2].view(B, G, S, 2).sum(2)
+    k0 = yc[:, 0].reshape(B, G, C // G)[..., 0].float()
+    n = torch.full_like(k0, float(L * (C // G)))
+    return out, torch.stack([k0, part[..., 0], part[..., 1], n], dim=-1).contiguous()
 
 
 class Conv1dSiLU(nn.Module):
@@ -280,6 +311,91 @@ class Conv1dSiLU(nn.Module):
 
     def forward(self, x: Tensor) -> Tensor:
         return _Conv1dSiLUFn.apply(x, self.weight, self.bias)
+
+
+def dynamics_at(gate_raw: Tensor, log_dt_scale: Tensor, rope_freqs: Tensor, gating_c: float, omega_thresh: float,
+                adt_delta: float, adt_smoothness: float, adt_eps: float, n_heads: int, state_dim: int,
+                l0: int = 0, l0_dev: Optional[Tensor] = None) -> tuple:
+    """DynamicsFusedFn's forward (dynamics_fused.cu:35-140) for gate rows at sequence positions l0 .. l0+L-1:
+    the RoPE term omega + l * rope_freqs (block.py:59-62) takes the absolute position.  ``l0_dev`` (one
+    int64 on the device) adds a position the kernel reads at run time (a graph-captured decode step).
+    Forward only."""
+    g = gate_raw.contiguous()
+    _check_gpu("dynamics_at", g)
+    H, N = int(n_heads), int(state_dim)
+    B, L, GH = g.shape
+    if GH != (N + 5) * H:
+        raise ValueError(f"gate_raw last dim must be (state_dim + 5) * n_heads = {(N + 5) * H}, got {GH}")
+    lds = log_dt_scale.detach().float().contiguous()
+    rf = rope_freqs.detach().float().contiguous()
+    A = torch.empty(B, L, H, N, dtype=g.dtype, device=g.device)
+    vp = torch.empty(B, L, H, N // 2, dtype=g.dtype, device=g.device)
+    beta = torch.empty(B, L, H, dtype=g.dtype, device=g.device)
+    selc = torch.empty(B, L, H, dtype=g.dtype, device=g.device)
+    st = _lib.load().cdssm_dynamics_fused_fwd_at(
+        _lib.DTYPE_CODE[g.dtype], _lib.ptr(g), _lib.ptr(lds), _lib.ptr(rf), float(gating_c), float(omega_thresh),
+        float(adt_delta), float(adt_smoothness), float(adt_eps), _lib.ptr(A), _lib.ptr(vp), _lib.ptr(beta),
+        _lib.ptr(selc), B, L, H, N, int(l0), _lib.ptr(l0_dev), _lib.stream_of(g.device))
+    _lib.check(st, "cdssm_dynamics_fused_fwd_at")
+    return A, vp, beta, selc
+
+
+def conv1d_silu_step(x: Tensor, window: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
+    """One decode token of conv1d+SiLU: x (B, C) (dense channels, any row stride); window (B, K-1, C), the
+    last K-1 inputs of each row (oldest first), updated in place.  Returns y (B, C), the full
+    convolution's output at the new position."""
+    _check_gpu("conv1d_silu_step", x)
+    B, C = x.shape
+    K = weight.shape[-1]
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    if tuple(window.shape) != (B, K - 1, C) or window.dtype != x.dtype or not window.is_contiguous():
+        raise ValueError(f"window must be a contiguous ({B}, {K - 1}, {C}) {x.dtype} tensor")
+    wc = weight.to(x.dtype).contiguous()
+    bc = bias.to(x.dtype).contiguous()
+    y = torch.empty((B, C), dtype=x.dtype, device=x.device)
+    st = _lib.load().cdssm_conv1d_silu_step(_lib.DTYPE_CODE[x.dtype], _lib.ptr(x), x.stride(0) if B > 1 else C,
+                                           _lib.ptr(window), _lib.ptr(wc), _lib.ptr(bc), _lib.ptr(y), B, C, K,
+                                           _lib.stream_of(x.device))
+    _lib.check(st, "cdssm_conv1d_silu_step")
+    return y
+
+
+def group_norm_sums(y: Tensor, num_groups: int) -> Tensor:
+    """Running GroupNorm statistics of y (B, L, C) per (b, group): (shift, sum (x - shift), sum (x - shift)^2,
+    count) fp32 (B, G, 4), shift = the group's first element; the decode step's state for the epilogue."""
+    B, L, C = y.shape
+    G = int(num_groups)
+    yg = y.reshape(B, L, G, C // G).double()
+    k0 = yg[:, 0, :, 0]
+    d = yg - k0[:, None, :, None]
+    n = torch.full_like(k0, float(L * (C // G)))
+    return torch.stack([k0, d.sum((1, 3)), (d * d).sum((1, 3)), n], dim=-1).float().contiguous()
+
+
+def group_norm_gate_step(y: Tensor, gsum: Tensor, gamma: Tensor, beta: Tensor, eps: float, z: Tensor,
+                         x_conv: Tensor, D: Tensor) -> Tensor:
+    """One decode token of the GroupNorm epilogue (block.py:215-225) with running statistics ``gsum``
+    (B, G, 4), updated in place; y, x_conv (B, C); z (B, C) with any row stride."""
+    Dp = D.to(y.dtype).contiguous()
+    yc, xc = y.contiguous(), x_conv.contiguous()
+    dt = _check_gpu("group_norm_gate_step", yc, z, xc, Dp)
+    B, C = yc.shape
+    G = gsum.shape[1]
+    if tuple(gsum.shape) != (B, G, 4) or gsum.dtype != torch.float32 or not gsum.is_contiguous():
+        raise ValueError(f"gsum must be a contiguous float32 ({B}, G, 4) tensor")
+    if z.stride(1) != 1:
+        z = z.contiguous()
+    pdt = gamma.dtype if gamma.dtype in _lib.DTYPE_CODE else torch.float32
+    g = gamma.detach().to(device=y.device, dtype=pdt).contiguous()
+    b = beta.detach().to(device=y.device, dtype=pdt).contiguous()
+    out = torch.empty_like(yc)
+    st = _lib.load().cdssm_group_norm_gate_step(_lib.DTYPE_CODE[dt], _lib.DTYPE_CODE[pdt], _lib.ptr(yc),
+                                               _lib.ptr(gsum), _lib.ptr(g), _lib.ptr(b), _lib.ptr(z),
+                                               z.stride(0) if B > 1 else C, _lib.ptr(xc), _lib.ptr(Dp),
+                                               _lib.ptr(out), B, C, G, float(eps), _lib.stream_of(y.device))
+    _lib.check(st, "cdssm_group_norm_gate_step")
+    return out
 
 
 class RMSNorm(nn.Module):
@@ -345,7 +461,10 @@ class CDSSMBlock(nn.Module):
         nn.init.normal_(self.out_proj.weight, std=std["out_proj"])
         nn.init.zeros_(self.D)
 
-    def forward(self, x: Tensor, v_first: Optional[Tensor] = None):
+    def forward(self, x: Tensor, v_first: Optional[Tensor] = None, cache: Optional[dict] = None):
+        """x (B, L, d_model) -> (x + block(x), v_first).  With ``cache`` (a dict), also fills it with the
+        state a decode step continues from: the conv window, the scan's decode state, the GroupNorm's
+        running sums and the position."""
         cfg = self.config
         N, H, D, Di = cfg.state_dim, cfg.n_heads, cfg.head_dim, cfg.d_inner
         if N != 2:
@@ -361,6 +480,14 @@ class CDSSMBlock(nn.Module):
         else:
             V = torch.lerp(v_first, V, torch.sigmoid(self.v_residual_gate)[None, None, :, None].to(V.dtype))
         x_conv = self.conv(x_gate)
+        if cache is not None:
+            Kc = self.conv.kernel_size - 1
+            win = x_gate.new_zeros(B, Kc, Di)
+            nk = min(Kc, L)
+            if nk > 0:
+                win[:, Kc - nk:] = x_gate[:, L - nk:]
+            cache["conv"] = win
+            cache["l"] = torch.full((1,), L, dtype=torch.int64, device=x.device)  # position of the next token
         gates = self.gate_proj(x_conv)
         A_bar, vp, beta, sel_C = DynamicsFusedFn.apply(
             gates.contiguous(), self.log_dt_scale.float(), self.rope_freqs, cfg.gating_c, cfg.bf16_omega_thresh,
@@ -368,15 +495,55 @@ class CDSSMBlock(nn.Module):
         Q = self.Q_proj(x_conv).reshape(B, L, H, D)
         K, Q, qk = normalize_kq_qk(K, Q)
         V = V.contiguous()
-        retrieved, _ = chunkwise_delta_scan_abar(Q, K, V, beta, sel_C, A_bar, vp, chunk_size=cfg.chunk_size)
+        if cache is None:
+            retrieved, _ = chunkwise_delta_scan_abar(Q, K, V, beta, sel_C, A_bar, vp, chunk_size=cfg.chunk_size)
+        else:
+            retrieved, cache["scan"] = prefill_abar(Q, K, V, beta, sel_C, A_bar, vp, chunk_size=cfg.chunk_size)
         # current-token shortcut (block.py:202-205) through the readout: sel_C s (q.k)^2 V vp
         shortcut_readout_(retrieved, qk, V, vp, sel_C, self.shortcut_scale)
         y = self.readout_proj(retrieved.reshape(B, L, H * N))
         y = group_norm_gate(y, self.ssm_norm.num_groups, self.ssm_norm.weight, self.ssm_norm.bias,
-                            self.ssm_norm.eps, z, x_conv, self.D)
+                            self.ssm_norm.eps, z, x_conv, self.D, return_sums=cache is not None)
+        if cache is not None:
+            y, cache["gsum"] = y
         # out_proj with the residual added in the GEMM epilogue
         out = torch.addmm(residual.reshape(B * L, -1), y.reshape(B * L, Di), self.out_proj.weight.t())
         return out.reshape(residual.shape), v_first
+
+    def step(self, x: Tensor, v_first: Optional[Tensor], cache: dict):
+        """One decode token: x (B, d_model) at position cache["l"] -> (x + block(x), v_first (B, H, N)),
+        advancing ``cache`` (filled by ``forward(..., cache=...)`` over the prompt).  Every piece of state,
+        the position included, lives on the device, so the step can be captured in a HIP graph.  The scan, conv and
+        dynamics reproduce the forward over prompt + token at that token; the GroupNorm takes running
+        statistics over every position so far, which is the forward's for a one-layer model (the
+        reference's GroupNorm spans all L positions, so in deeper models appending a token also changes
+        earlier positions' activations, which a recurrent step does not revisit)."""
+        cfg = self.config
+        N, H, D, Di = cfg.state_dim, cfg.n_heads, cfg.head_dim, cfg.d_inner
+        B = x.shape[0]
+        proj = self.in_proj(rms_norm(x, self.norm.weight, self.norm.eps))  # (B, 3 Di + H N)
+        z, x_gate, K, V = proj.split([Di, Di, Di, H * N], dim=-1)
+        K = K.reshape(B, 1, H, D)
+        V = V.reshape(B, H, N)
+        if v_first is None:
+            v_first = V.detach()
+        else:
+            V = torch.lerp(v_first, V, torch.sigmoid(self.v_residual_gate)[None, :, None].to(V.dtype))
+        x_conv = conv1d_silu_step(x_gate, cache["conv"], self.conv.weight, self.conv.bias)
+        gates = self.gate_proj(x_conv).reshape(B, 1, -1)
+        A_bar, vp, beta, sel_C = dynamics_at(gates, self.log_dt_scale, self.rope_freqs, cfg.gating_c,
+                                             cfg.bf16_omega_thresh, cfg.bf16_delta, cfg.bf16_smoothness,
+                                             cfg.eps_adaptive_dt, H, N, 0, cache["l"])
+        Q = self.Q_proj(x_conv).reshape(B, 1, H, D)
+        K, Q, qk = normalize_kq_qk(K, Q)
+        V = V.contiguous()
+        retrieved = decode_step_abar(cache["scan"], Q, K, V, beta, sel_C, A_bar, vp)  # (B, H, 2)
+        shortcut_readout_(retrieved, qk, V, vp, sel_C, self.shortcut_scale)
+        y = self.readout_proj(retrieved.reshape(B, H * N))
+        y = group_norm_gate_step(y, cache["gsum"], self.ssm_norm.weight, self.ssm_norm.bias, self.ssm_norm.eps, z,
+                                 x_conv, self.D)
+        cache["l"].add_(1)
+        return torch.addmm(x, y, self.out_proj.weight.t()), v_first
 
 
 class CDSSMLMHeadModel(nn.Module):
@@ -400,3 +567,70 @@ class CDSSMLMHeadModel(nn.Module):
         for blk in self.blocks:
             x, v_first = blk(x, v_first=v_first)
         return self.lm_head(self.final_norm(x))
+
+    def prefill(self, input_ids: Tensor) -> tuple:
+        """Forward over the prompt (B, L): the last position's logits (B, vocab) and the per-layer decode
+        caches that ``decode_step`` continues from (generation without re-forwarding; the reference
+        re-forwards, predict.py:53-67)."""
+        x = self.embedding(input_ids)
+        v_first = None
+        caches: List[dict] = []
+        for blk in self.blocks:
+            c: dict = {}
+            x, v_first = blk(x, v_first=v_first, cache=c)
+            caches.append(c)
+        return self.lm_head(self.final_norm(x[:, -1])), caches
+
+    def decode_step(self, token_ids: Tensor, caches: List[dict]) -> Tensor:
+        """One new token per row, token_ids (B,): logits (B, vocab); advances ``caches`` (see
+        ``CDSSMBlock.step`` for what the step reproduces exactly)."""
+        x = self.embedding(token_ids)
+        v_first = None
+        for blk, c in zip(self.blocks, caches):
+            x, v_first = blk.step(x, v_first, c)
+        return self.lm_head(self.final_norm(x))
+
+    def decode_graph(self, caches: List[dict], warmup: int = 2) -> "DecodeGraph":
+        """``decode_step`` captured once in a HIP graph over ``caches`` (see ``DecodeGraph``)."""
+        return DecodeGraph(self, caches, warmup)
+
+
+def _clone_cache(c: dict) -> dict:
+    out = {}
+    for k, v in c.items():
+        if torch.is_tensor(v):
+            out[k] = v.clone()
+        elif isinstance(v, DecodeState):
+            out[k] = DecodeState(v.state.clone(), v.gam.clone(), v.pos.clone(), v.chunk_size)
+        else:
+            out[k] = v
+    return out
+
+
+class DecodeGraph:
+    """A model's decode step captured in one HIP graph: each call copies the B new token ids into the
+    graph's input, replays every layer's launches at once (no per-kernel host launch cost) and returns
+    the graph's logits buffer (B, vocab), overwritten by the next call.  The graph advances the same
+    ``caches`` as ``decode_step`` would; the warm-up steps before the capture run on copies of them."""
+
+    def __init__(self, model: "CDSSMLMHeadModel", caches: List[dict], warmup: int = 2):
+        dev = caches[0]["conv"].device
+        B = caches[0]["conv"].shape[0]
+        self.ids = torch.zeros(B, dtype=torch.long, device=dev)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side), torch.no_grad():
+            scratch = [_clone_cache(c) for c in caches]
+            for _ in range(warmup):
+                model.decode_step(self.ids, scratch)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        del scratch
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph), torch.no_grad():
+            self.logits = model.decode_step(self.ids, caches)
+
+    def __call__(self, token_ids: Tensor) -> Tensor:
+        self.ids.copy_(token_ids)
+        self.graph.replay()
+        return self.logits

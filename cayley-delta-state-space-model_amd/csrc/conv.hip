@@ -124,6 +124,29 @@ __global__ __launch_bounds__(256) void conv1d_silu_fwd_kernel(const typename T::
   }
 }
 
+// One decode step of the conv: window (B, K-1, C) holds the last K-1 inputs
+// of each row (oldest first, zeros before the sequence start); the new input x
+// (B, C) completes the K taps in the order of the full convolution (so the
+// output equals the full conv's at that position), then the window shifts.
+template <typename T>
+__global__ __launch_bounds__(256) void conv1d_silu_step_kernel(const typename T::raw* __restrict__ x, int64_t x_bs,
+                                                               typename T::raw* __restrict__ win,
+                                                               const typename T::raw* __restrict__ w,
+                                                               const typename T::raw* __restrict__ bias,
+                                                               typename T::raw* __restrict__ y, int B, int C, int K) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= int64_t(B) * C) return;
+  const int b = int(i / C), ch = int(i - int64_t(b) * C);
+  typename T::raw* wr = win + int64_t(b) * (K - 1) * C + ch;
+  const float xn = T::load(x + int64_t(b) * x_bs + ch);
+  float u = T::load(bias + ch);
+  for (int j = 0; j < K - 1; ++j) u = fmaf(T::load(w + int64_t(ch) * K + j), T::load(wr + int64_t(j) * C), u);
+  u = fmaf(T::load(w + int64_t(ch) * K + K - 1), xn, u);
+  T::store(y + i, silu_f(u));
+  for (int j = 0; j + 1 < K - 1; ++j) wr[int64_t(j) * C] = wr[int64_t(j + 1) * C];
+  if (K > 1) T::store(wr + int64_t(K - 2) * C, xn);
+}
+
 template <typename T, int VEC, int K>
 int launch_conv(const void* x, int64_t x_ts, const void* w, const void* bias, void* y, int64_t B, int64_t L,
                 int64_t C, hipStream_t stream) {
@@ -192,4 +215,34 @@ extern "C" int cdssm_conv1d_silu_fwd_strided(int dtype, const void* x, int64_t x
 extern "C" int cdssm_conv1d_silu_fwd(int dtype, const void* x, const void* weight, const void* bias, void* y,
                                      int64_t B, int64_t L, int64_t C, int64_t K, hipStream_t stream) {
   return cdssm_conv1d_silu_fwd_strided(dtype, x, C, weight, bias, y, B, L, C, K, stream);
+}
+
+extern "C" int cdssm_conv1d_silu_step(int dtype, const void* x, int64_t x_batch_stride, void* window,
+                                      const void* weight, const void* bias, void* y, int64_t B, int64_t C, int64_t K,
+                                      hipStream_t stream) {
+  const char* op = "cdssm_conv1d_silu_step";
+  if (dtype != 0 && dtype != 1) {
+    cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
+    return CDSSM_EINVAL;
+  }
+  if (B <= 0 || C <= 0 || K < 1 || K > 8 || B * C >= (int64_t(1) << 31) || x_batch_stride < C) {
+    cdssm_host::set_error("%s: need B, C > 0, B*C < 2^31, 1 <= kernel_size <= 8, x row stride >= C "
+                          "(B=%lld C=%lld K=%lld)", op, (long long)B, (long long)C, (long long)K);
+    return CDSSM_EINVAL;
+  }
+  if (!x || (K > 1 && !window) || !weight || !bias || !y) {
+    cdssm_host::set_error("%s: null pointer argument", op);
+    return CDSSM_EINVAL;
+  }
+  const unsigned grid = unsigned((B * C + 255) / 256);
+  if (dtype == 1)
+    hipLaunchKernelGGL(conv1d_silu_step_kernel<BF16>, dim3(grid), dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(x), x_batch_stride, static_cast<uint16_t*>(window),
+                       static_cast<const uint16_t*>(weight), static_cast<const uint16_t*>(bias),
+                       static_cast<uint16_t*>(y), int(B), int(C), int(K));
+  else
+    hipLaunchKernelGGL(conv1d_silu_step_kernel<F32>, dim3(grid), dim3(256), 0, stream, static_cast<const float*>(x),
+                       x_batch_stride, static_cast<float*>(window), static_cast<const float*>(weight),
+                       static_cast<const float*>(bias), static_cast<float*>(y), int(B), int(C), int(K));
+  return cdssm_host::check_launch(op);
 }

@@ -20,6 +20,11 @@
 // g' s + z' is also the R-mode carry after the token (the fused scan's
 // h_final for a sequence ending there).
 //
+// Input forms: T = BF16 / F32 takes the scan-level (dt, r, alpha, omega, c);
+// ABar<T> takes the gate-level transition a_t (B, H, 2) in dt's place and the
+// VP scale vp_t (B, H) in r's (alpha, omega unused), as the fused scan's
+// ABar form (the model's DynamicsFusedFn outputs).
+//
 // State layout (fp32, caller-owned): state (B, H, 3, 2, D) = rows z_re, z_im,
 // c^_re, c^_im, s_re, s_im; gam (B, H, 2) = g; pos (B, H) int32 = j.
 // Work layout: one wave per (b, group of HPW heads), LPH lanes per head, each
@@ -49,7 +54,11 @@ __global__ __launch_bounds__(kWave) void decode_step_kernel(
 
   // per-token scalars and dynamics (every lane of the head computes them)
   const float bb = T::load(beta + bh), sc = T::load(sel_c + bh);
-  const Transition tr = cayley_gated(T::load(dt + bh), T::load(r + bh), alpha[hl], omega[hl], c);
+  Transition tr;
+  if constexpr (IsABar<T>::value)
+    tr = Transition{T::load(dt + 2 * bh), T::load(dt + 2 * bh + 1), T::load(r + bh)};
+  else
+    tr = cayley_gated(T::load(dt + bh), T::load(r + bh), alpha[hl], omega[hl], c);
   const float wr = bb * tr.vp * T::load(v + 2 * bh), wi = bb * tr.vp * T::load(v + 2 * bh + 1);
 
   float kk[DPL], qq[DPL];
@@ -228,12 +237,13 @@ extern "C" int cdssm_decode_init(const float* h, float* state, float* gam, int* 
   return cdssm_host::check_launch(op);
 }
 
-extern "C" int cdssm_decode_step(int dtype, const void* q, const void* k, const void* v, const void* beta,
-                                 const void* sel_c, const void* dt, const void* r, const float* alpha,
-                                 const float* omega, float c, float* state, float* gam, int* pos, void* y,
-                                 float* h_out, int64_t B, int64_t H, int64_t D, int64_t N, int64_t chunk,
-                                 hipStream_t stream) {
-  const char* op = "cdssm_decode_step";
+namespace {
+
+template <bool ABAR>
+int decode_entry(const char* op, int dtype, const void* q, const void* k, const void* v, const void* beta,
+                 const void* sel_c, const void* dt, const void* r, const float* alpha, const float* omega, float c,
+                 float* state, float* gam, int* pos, void* y, float* h_out, int64_t B, int64_t H, int64_t D,
+                 int64_t N, int64_t chunk, hipStream_t stream) {
   if (dtype != 0 && dtype != 1) {
     cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
     return CDSSM_EINVAL;
@@ -245,21 +255,43 @@ extern "C" int cdssm_decode_step(int dtype, const void* q, const void* k, const 
                           op, (long long)B, (long long)H, (long long)D, (long long)N, (long long)chunk);
     return CDSSM_EINVAL;
   }
-  if (!q || !k || !v || !beta || !sel_c || !dt || !r || !alpha || !omega || !state || !gam || !pos || !y) {
+  if (!q || !k || !v || !beta || !sel_c || !dt || !r || (!ABAR && (!alpha || !omega)) || !state || !gam || !pos ||
+      !y) {
     cdssm_host::set_error("%s: null pointer argument", op);
     return CDSSM_EINVAL;
   }
   const int b = int(B), hh = int(H), qc = int(chunk);
+  using TB = std::conditional_t<ABAR, ABar<BF16>, BF16>;
+  using TF = std::conditional_t<ABAR, ABar<F32>, F32>;
   if (dtype == 1) {
     if (D == 64)
-      return launch_decode<BF16, 64, 8>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, state, gam, pos, y, h_out, b,
-                                        hh, qc, stream);
-    return launch_decode<BF16, 128, 16>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, state, gam, pos, y, h_out, b,
-                                        hh, qc, stream);
+      return launch_decode<TB, 64, 8>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, state, gam, pos, y, h_out, b, hh,
+                                      qc, stream);
+    return launch_decode<TB, 128, 16>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, state, gam, pos, y, h_out, b, hh,
+                                      qc, stream);
   }
   if (D == 64)
-    return launch_decode<F32, 64, 16>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, state, gam, pos, y, h_out, b,
-                                      hh, qc, stream);
-  return launch_decode<F32, 128, 32>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, state, gam, pos, y, h_out, b,
-                                     hh, qc, stream);
+    return launch_decode<TF, 64, 16>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, state, gam, pos, y, h_out, b, hh,
+                                     qc, stream);
+  return launch_decode<TF, 128, 32>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, state, gam, pos, y, h_out, b, hh,
+                                    qc, stream);
+}
+
+}  // namespace
+
+extern "C" int cdssm_decode_step(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                                 const void* sel_c, const void* dt, const void* r, const float* alpha,
+                                 const float* omega, float c, float* state, float* gam, int* pos, void* y,
+                                 float* h_out, int64_t B, int64_t H, int64_t D, int64_t N, int64_t chunk,
+                                 hipStream_t stream) {
+  return decode_entry<false>("cdssm_decode_step", dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, state, gam,
+                             pos, y, h_out, B, H, D, N, chunk, stream);
+}
+
+extern "C" int cdssm_decode_step_abar(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                                      const void* sel_c, const void* a_bar, const void* vp, float* state, float* gam,
+                                      int* pos, void* y, float* h_out, int64_t B, int64_t H, int64_t D, int64_t N,
+                                      int64_t chunk, hipStream_t stream) {
+  return decode_entry<true>("cdssm_decode_step_abar", dtype, q, k, v, beta, sel_c, a_bar, vp, nullptr, nullptr,
+                            0.0f, state, gam, pos, y, h_out, B, H, D, N, chunk, stream);
 }

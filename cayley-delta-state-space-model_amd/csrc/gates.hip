@@ -48,13 +48,13 @@ __global__ __launch_bounds__(256) void dynamics_fwd_kernel(
     const float* __restrict__ rope, typename T::raw* __restrict__ A_out, typename T::raw* __restrict__ vp_out,
     typename T::raw* __restrict__ beta_out, typename T::raw* __restrict__ selc_out, float gating_c,
     float omega_thresh, float adt_delta, float adt_smooth, float adt_eps, int L, int H, int N,
-    int64_t total) {
+    int64_t total, int64_t l0, const int64_t* __restrict__ l0_dev) {
   GateIdx g;
   if (!gate_idx(int64_t(blockIdx.x) * blockDim.x + threadIdx.x, L, H, total, g)) return;
   const int Nh = N / 2, G = N + 5;
   const typename T::raw* row = gate + g.bl * int64_t(G) * H + g.h;
   const float freq = rope[g.h];
-  const float pos = float(g.l) * freq;
+  const float pos = float(g.l + l0 + (l0_dev ? *l0_dev : 0)) * freq;  // sequence position
   const float selB = T::load(row + int64_t(N) * H), selC = T::load(row + int64_t(N + 1) * H);
   const float seldt = T::load(row + int64_t(N + 2) * H), braw = T::load(row + int64_t(N + 3) * H);
   const float rraw = T::load(row + int64_t(N + 4) * H);
@@ -302,12 +302,16 @@ int check_gate_shape(const char* op, int64_t B, int64_t L, int64_t H, int64_t N)
 
 }  // namespace
 
-extern "C" int cdssm_dynamics_fused_fwd(int dtype, const void* gate_raw, const float* log_dt_scale,
-                                        const float* rope_freqs, float gating_c, float omega_thresh,
-                                        float adt_delta, float adt_smoothness, float adt_eps,
-                                        void* A_bar, void* vp_scale, void* beta, void* sel_c, int64_t B,
-                                        int64_t L, int64_t H, int64_t N, hipStream_t stream) {
+extern "C" int cdssm_dynamics_fused_fwd_at(int dtype, const void* gate_raw, const float* log_dt_scale,
+                                           const float* rope_freqs, float gating_c, float omega_thresh,
+                                           float adt_delta, float adt_smoothness, float adt_eps, void* A_bar,
+                                           void* vp_scale, void* beta, void* sel_c, int64_t B, int64_t L, int64_t H,
+                                           int64_t N, int64_t l0, const int64_t* l0_dev, hipStream_t stream) {
   const char* op = "cdssm_dynamics_fused_fwd";
+  if (l0 < 0 || l0 > (int64_t(1) << 40)) {
+    cdssm_host::set_error("%s: position offset %lld out of range", op, (long long)l0);
+    return CDSSM_EINVAL;
+  }
   int st = check_dtype(op, dtype);
   if (!st) st = check_gate_shape(op, B, L, H, N);
   if (st) return st;
@@ -325,13 +329,23 @@ extern "C" int cdssm_dynamics_fused_fwd(int dtype, const void* gate_raw, const f
     hipLaunchKernelGGL(dynamics_fwd_kernel<BF16>, dim3(blocks), dim3(256), 0, stream, (const uint16_t*)gate_raw,
                        log_dt_scale, rope_freqs, (uint16_t*)A_bar, (uint16_t*)vp_scale, (uint16_t*)beta,
                        (uint16_t*)sel_c, gating_c, omega_thresh, adt_delta, adt_smoothness, adt_eps, int(L),
-                       int(H), int(N), total);
+                       int(H), int(N), total, l0, l0_dev);
   else
     hipLaunchKernelGGL(dynamics_fwd_kernel<F32>, dim3(blocks), dim3(256), 0, stream, (const float*)gate_raw,
                        log_dt_scale, rope_freqs, (float*)A_bar, (float*)vp_scale, (float*)beta, (float*)sel_c,
                        gating_c, omega_thresh, adt_delta, adt_smoothness, adt_eps, int(L), int(H), int(N),
-                       total);
+                       total, l0, l0_dev);
   return cdssm_host::check_launch(op);
+}
+
+extern "C" int cdssm_dynamics_fused_fwd(int dtype, const void* gate_raw, const float* log_dt_scale,
+                                        const float* rope_freqs, float gating_c, float omega_thresh,
+                                        float adt_delta, float adt_smoothness, float adt_eps,
+                                        void* A_bar, void* vp_scale, void* beta, void* sel_c, int64_t B,
+                                        int64_t L, int64_t H, int64_t N, hipStream_t stream) {
+  return cdssm_dynamics_fused_fwd_at(dtype, gate_raw, log_dt_scale, rope_freqs, gating_c, omega_thresh, adt_delta,
+                                     adt_smoothness, adt_eps, A_bar, vp_scale, beta, sel_c, B, L, H, N, 0, nullptr,
+                                     stream);
 }
 
 extern "C" int64_t cdssm_dynamics_fused_bwd_workspace_bytes(int64_t B, int64_t L, int64_t H) {

@@ -319,6 +319,55 @@ __global__ __launch_bounds__(256) void gn_gate_kernel(const typename T::raw* __r
   a.store(out + int64_t(tok) * C + c);  // the store rounds the sum
 }
 
+// ---------------------------------------------------------------------------
+// GroupNorm + gate for one decode token per batch row, with running
+// statistics: gsum (B, G, 4) fp32 = (shift K, sum (x - K), sum (x - K)^2,
+// count) over every position so far.  The new token's group sums are added in
+// a fixed order (one thread per group), the statistics formed from the
+// totals, and the token normalised, gated and skipped as gn_gate_kernel does.
+// With the prefix's sums this equals the GroupNorm of a forward over the
+// prefix plus the token, for that token.
+// ---------------------------------------------------------------------------
+template <typename T, typename P>
+__global__ __launch_bounds__(256) void gn_gate_step_kernel(const typename T::raw* __restrict__ y,
+                                                           float4* __restrict__ gsum,
+                                                           const typename P::raw* __restrict__ gamma,
+                                                           const typename P::raw* __restrict__ beta,
+                                                           const typename T::raw* __restrict__ z, int64_t z_bs,
+                                                           const typename T::raw* __restrict__ xc,
+                                                           const typename T::raw* __restrict__ Dp,
+                                                           typename T::raw* __restrict__ out, int C, int G,
+                                                           float eps) {
+  extern __shared__ float2 gst[];  // (mean, rstd) per group
+  const int b = blockIdx.x;
+  const int Cg = C / G;
+  const typename T::raw* yr = y + int64_t(b) * C;
+  for (int g = threadIdx.x; g < G; g += blockDim.x) {
+    float4 a = gsum[int64_t(b) * G + g];
+    float s1 = 0.0f, s2 = 0.0f;
+    for (int c = 0; c < Cg; ++c) {
+      const float d = T::load(yr + g * Cg + c) - a.x;
+      s1 += d;
+      s2 = fmaf(d, d, s2);
+    }
+    a.y += s1;
+    a.z += s2;
+    a.w += float(Cg);
+    gsum[int64_t(b) * G + g] = a;
+    const float m = a.y / a.w;
+    gst[g] = make_float2(a.x + m, rsqrtf(fmaxf(a.z / a.w - m * m, 0.0f) + eps));
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < C; c += blockDim.x) {
+    const float2 st = gst[c / Cg];
+    const float gn = rnd<T>(fmaf((T::load(yr + c) - st.x) * st.y, P::load(gamma + c), P::load(beta + c)));
+    const float s = rnd<T>(silu_fast(T::load(z + int64_t(b) * z_bs + c)));
+    const float p = rnd<T>(gn * s);
+    const float d = rnd<T>(T::load(Dp + c) * T::load(xc + int64_t(b) * C + c));
+    T::store(out + int64_t(b) * C + c, p + d);
+  }
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 template <typename F>
@@ -483,6 +532,45 @@ extern "C" int cdssm_group_norm_gate_fwd(int dtype, int param_dtype, const void*
       go(std::integral_constant<int, 1>{}, BF16{});
     else
       go(std::integral_constant<int, 1>{}, F32{});
+    return cdssm_host::check_launch(op);
+  });
+}
+
+extern "C" int cdssm_group_norm_gate_step(int dtype, int param_dtype, const void* y, float* gsum, const void* gamma,
+                                          const void* beta, const void* z, int64_t z_batch_stride, const void* x_conv,
+                                          const void* Dp, void* out, int64_t B, int64_t C, int64_t G, float eps,
+                                          hipStream_t stream) {
+  const char* op = "cdssm_group_norm_gate_step";
+  return by_dtype(dtype, op, [&](auto t) -> int {
+    using T = decltype(t);
+    using raw = typename T::raw;
+    if (param_dtype != 0 && param_dtype != 1) {
+      cdssm_host::set_error("%s: param_dtype must be 0 (fp32) or 1 (bf16), got %d", op, param_dtype);
+      return CDSSM_EINVAL;
+    }
+    if (B <= 0 || C <= 0 || G <= 0 || C % G != 0 || G > 8192 || B > 0x7fffffffLL || C >= (int64_t(1) << 24) ||
+        z_batch_stride < C) {
+      cdssm_host::set_error("%s: need C divisible by G <= 8192 and a z row stride >= C (B=%lld C=%lld G=%lld)", op,
+                            (long long)B, (long long)C, (long long)G);
+      return CDSSM_EINVAL;
+    }
+    if (!y || !gsum || !gamma || !beta || !z || !x_conv || !Dp || !out) {
+      cdssm_host::set_error("%s: null pointer argument", op);
+      return CDSSM_EINVAL;
+    }
+    auto go = [&](auto pt) {
+      using P = decltype(pt);
+      using praw = typename P::raw;
+      hipLaunchKernelGGL((gn_gate_step_kernel<T, P>), dim3(unsigned(B)), dim3(256), size_t(G) * sizeof(float2),
+                         stream, static_cast<const raw*>(y), reinterpret_cast<float4*>(gsum),
+                         static_cast<const praw*>(gamma), static_cast<const praw*>(beta), static_cast<const raw*>(z),
+                         z_batch_stride, static_cast<const raw*>(x_conv), static_cast<const raw*>(Dp),
+                         static_cast<raw*>(out), int(C), int(G), eps);
+    };
+    if (param_dtype == 1)
+      go(BF16{});
+    else
+      go(F32{});
     return cdssm_host::check_launch(op);
   });
 }

@@ -326,6 +326,56 @@ int cdssm_normalize_kq_bwd(int dtype, const void* grad_K_out, const void* grad_Q
                            const void* Q, void* grad_K, void* grad_Q, int64_t rows, int64_t D,
                            hipStream_t stream);
 
+/*
+ * cdssm_decode_step on the gate-level inputs (the model's DynamicsFusedFn
+ * outputs, block.py:184-198): a_bar (B, H, 2) = A_bar and vp (B, H) = vp_scale
+ * of the token in place of (dt, r, alpha, omega, c); otherwise as
+ * cdssm_decode_step.  No reference counterpart (predict.py:53-67 re-forwards);
+ * the scan it continues is cdssm_fused_scan_fwd_abar's.
+ */
+int cdssm_decode_step_abar(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                           const void* sel_c, const void* a_bar, const void* vp, float* state, float* gam, int* pos,
+                           void* y, float* h_out, int64_t B, int64_t H, int64_t D, int64_t N, int64_t chunk,
+                           hipStream_t stream);
+
+/*
+ * cdssm_dynamics_fused_fwd for gate rows at sequence positions l0 .. l0+L-1
+ * (the RoPE term omega + l * rope_freqs[h] of block.py:59-62, 184-188, uses
+ * the absolute position): one decode token is L = 1 at l0 = its position.
+ * The offset is l0 plus, when l0_dev is non-null, the int64 it points to on
+ * the device (read by the kernel: a decode step captured in a HIP graph keeps
+ * its position there).
+ */
+int cdssm_dynamics_fused_fwd_at(int dtype, const void* gate_raw, const float* log_dt_scale, const float* rope_freqs,
+                                float gating_c, float omega_thresh, float adt_delta, float adt_smoothness,
+                                float adt_eps, void* A_bar, void* vp_scale, void* beta, void* sel_c, int64_t B,
+                                int64_t L, int64_t H, int64_t N, int64_t l0, const int64_t* l0_dev,
+                                hipStream_t stream);
+
+/*
+ * One decode token of the conv1d+SiLU (conv1d_silu.cu:25-90 at the newest
+ * position): x (B, C) with a row stride (elements), window (B, K-1, C) the
+ * last K-1 inputs of each row, oldest first (zeros before the sequence
+ * start), updated in place; y (B, C).  Equals the full convolution's output at
+ * that position.  No reference counterpart (the reference re-forwards).
+ */
+int cdssm_conv1d_silu_step(int dtype, const void* x, int64_t x_batch_stride, void* window, const void* weight,
+                           const void* bias, void* y, int64_t B, int64_t C, int64_t K, hipStream_t stream);
+
+/*
+ * One decode token of the block's GroupNorm epilogue (block.py:215-225) with
+ * running statistics: gsum (B, G, 4) fp32 = (shift, sum (x - shift),
+ * sum (x - shift)^2, count) over every position so far, updated in place with
+ * the token's y (B, C); then out = rnd(rnd(GN(y)) * rnd(silu(z))) + rnd(D x_conv)
+ * as cdssm_group_norm_gate_fwd.  For the token this equals the GroupNorm of a
+ * forward over the prefix plus the token (the reference's statistics span all
+ * positions).  z with a row stride.  No reference counterpart.
+ */
+int cdssm_group_norm_gate_step(int dtype, int param_dtype, const void* y, float* gsum, const void* gamma,
+                               const void* beta, const void* z, int64_t z_batch_stride, const void* x_conv,
+                               const void* D, void* out, int64_t B, int64_t C, int64_t G, float eps,
+                               hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

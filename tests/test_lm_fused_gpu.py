@@ -42,7 +42,7 @@ def test_rms_norm(dtype, rows, C):
 
 @pytest.mark.parametrize("dtype,B,L,H,D,pad", [(torch.bfloat16, 2, 50, 16, 64, 96), (torch.float32, 1, 9, 3, 64, 0),
                                                (torch.bfloat16, 1, 4, 2, 128, 8), (torch.float32, 2, 5, 2, 128, 4),
-                                               (torch.bfloat16, 1, 1, 1, 32, 0)])
+                                               (torch.bfloat16, 1, 1, 1, 32, 0), (torch.bfloat16, 5, 1, 4, 64, 32)])
 def test_normalize_kq_qk(dtype, B, L, H, D, pad):
     """K read as a column slice of a wider (B, L, pad + H*D + 8) tensor, as from the block's in_proj."""
     from cdssm_hip.lm import normalize_kq_qk
