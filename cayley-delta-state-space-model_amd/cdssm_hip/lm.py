@@ -488,6 +488,11 @@ class CDSSMBlock(nn.Module):
                 win[:, Kc - nk:] = x_gate[:, L - nk:]
             cache["conv"] = win
             cache["l"] = torch.full((1,), L, dtype=torch.int64, device=x.device)  # position of the next token
+            # the step's parameter-derived constants, formed once (the weights are fixed while decoding)
+            cache["lds"] = self.log_dt_scale.detach().float().contiguous()
+            cache["rope"] = self.rope_freqs.detach().float().contiguous()
+            cache["scale"] = self.shortcut_scale.detach().float().reshape(1).contiguous()
+            cache["vgate"] = torch.sigmoid(self.v_residual_gate.detach().float())[None, :, None].to(x.dtype)
         gates = self.gate_proj(x_conv)
         A_bar, vp, beta, sel_C = DynamicsFusedFn.apply(
             gates.contiguous(), self.log_dt_scale.float(), self.rope_freqs, cfg.gating_c, cfg.bf16_omega_thresh,
@@ -528,17 +533,17 @@ class CDSSMBlock(nn.Module):
         if v_first is None:
             v_first = V.detach()
         else:
-            V = torch.lerp(v_first, V, torch.sigmoid(self.v_residual_gate)[None, :, None].to(V.dtype))
+            V = torch.lerp(v_first, V, cache["vgate"])
         x_conv = conv1d_silu_step(x_gate, cache["conv"], self.conv.weight, self.conv.bias)
         gates = self.gate_proj(x_conv).reshape(B, 1, -1)
-        A_bar, vp, beta, sel_C = dynamics_at(gates, self.log_dt_scale, self.rope_freqs, cfg.gating_c,
+        A_bar, vp, beta, sel_C = dynamics_at(gates, cache["lds"], cache["rope"], cfg.gating_c,
                                              cfg.bf16_omega_thresh, cfg.bf16_delta, cfg.bf16_smoothness,
                                              cfg.eps_adaptive_dt, H, N, 0, cache["l"])
         Q = self.Q_proj(x_conv).reshape(B, 1, H, D)
         K, Q, qk = normalize_kq_qk(K, Q)
         V = V.contiguous()
         retrieved = decode_step_abar(cache["scan"], Q, K, V, beta, sel_C, A_bar, vp)  # (B, H, 2)
-        shortcut_readout_(retrieved, qk, V, vp, sel_C, self.shortcut_scale)
+        shortcut_readout_(retrieved, qk, V, vp, sel_C, cache["scale"])
         y = self.readout_proj(retrieved.reshape(B, H * N))
         y = group_norm_gate_step(y, cache["gsum"], self.ssm_norm.weight, self.ssm_norm.bias, self.ssm_norm.eps, z,
                                  x_conv, self.D)
