@@ -66,6 +66,15 @@ struct F32 {
   __device__ __forceinline__ static void store(raw* p, float v) { *p = v; }
 };
 
+// An (re, im) pair in one store (the pair's address aligned to its size).
+template <typename T>
+__device__ __forceinline__ void store_pair(typename T::raw* p, float re, float im) {
+  if constexpr (T::bytes == 2)
+    *reinterpret_cast<uint32_t*>(p) = pack_bf16x2(re, im);
+  else
+    *reinterpret_cast<float2*>(p) = make_float2(re, im);
+}
+
 // Input form of the fused forward: ABar<T> (elements of type T) takes the
 // per-token transition a_t (B,L,H,2) and VP scale (B,L,H,1) as computed by the
 // gate-level dynamics (in place of dt and r), instead of the scan-level

@@ -724,8 +724,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
     if (hj < H) {
       const int64_t e = ((tc.row0 + t) * H + hj) * 2;
       const float2 yv = s_y[p];
-      T::store(y + e, yv.x);
-      T::store(y + e + 1, yv.y);
+      store_pair<T>(y + e, yv.x, yv.y);
     }
   }
 }
@@ -1203,8 +1202,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
       if (hj < H) {
         const int64_t e = ((tc.row0 + t) * H + hj) * 2;
         const float2 yv = s_y[p];
-        T::store(y + e, yv.x);
-        T::store(y + e + 1, yv.y);
+        store_pair<T>(y + e, yv.x, yv.y);
       }
     }
   }
@@ -1451,6 +1449,10 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
   }
   if (!aligned16(q) || !aligned16(k)) {
     cdssm_host::set_error("%s: q and k must be 16-byte aligned", op);
+    return CDSSM_EINVAL;
+  }
+  if (reinterpret_cast<uintptr_t>(y) % (dtype == 1 ? 4 : 8) != 0) {
+    cdssm_host::set_error("%s: y must be aligned to its (re, im) pair (%d bytes)", op, dtype == 1 ? 4 : 8);
     return CDSSM_EINVAL;
   }
   const int b = int(B), l = int(L), hh = int(H), qc = int(chunk);

@@ -45,7 +45,8 @@ const char* cdssm_last_error(void);
  * workspace: cdssm_fused_scan_workspace_bytes() bytes of device memory, any
  * contents (scratch for this call; the backward takes the workspace of
  * cdssm_fused_scan_fwd_train instead).  Supported: N = 2, D in {64, 128},
- * 1 <= chunk <= 128.  Where every segment of 4 chunks fits in one round of
+ * 1 <= chunk <= 128; q, k 16-byte aligned, y aligned to one (re, im) pair
+ * (4 bytes bf16, 8 fp32).  Where every segment of 4 chunks fits in one round of
  * resident workgroups (or, for this inference forward, the segments fill
  * whole rounds of a persistent grid), the scan runs as one launch (chunk maps
  * composed by a look-back between workgroups); otherwise as four (chunk

@@ -57,6 +57,8 @@ def _fused_call(lib, **over):
     (dict(B=0), "positive"),
     (dict(q=None), "null"),
     (dict(k=8), "aligned"),
+    (dict(y=18), "(re, im) pair"),
+    (dict(dtype=0, y=20), "(re, im) pair"),
     (dict(H=1 << 19, D=128), "32-bit row offsets"),
 ])
 def test_fused_fwd_rejects_invalid_arguments_without_launching(bad, msg):
