@@ -50,6 +50,8 @@ SIGNATURES = {
     "cdssm_fused_scan_fwd_abar": (_I32, [_I32] + [_P] * 11 + [_I64] * 6 + [_P]),
     "cdssm_conv1d_silu_fwd": (_I32, [_I32] + [_P] * 4 + [_I64] * 4 + [_P]),
     "cdssm_conv1d_silu_fwd_strided": (_I32, [_I32, _P, _I64] + [_P] * 3 + [_I64] * 4 + [_P]),
+    "cdssm_conv1d_silu_bwd_workspace_bytes": (_I64, [_I64] * 4),
+    "cdssm_conv1d_silu_bwd": (_I32, [_I32, _P, _I64] + [_P] * 7 + [_I64] * 4 + [_P]),
     "cdssm_rms_norm_fwd": (_I32, [_I32, _P, _P, _P, _I64, _I64, _F32, _P]),
     "cdssm_normalize_kq_qk_fwd": (_I32, [_I32, _P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _P]),
     "cdssm_shortcut_readout_fwd": (_I32, [_I32] + [_P] * 6 + [_I64, _P]),

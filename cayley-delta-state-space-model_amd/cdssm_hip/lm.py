@@ -9,7 +9,8 @@ with q.k (HIP) -> fused scan with the sel_C readout on the gate-level A_bar /
 vp (HIP, ``cdssm_fused_scan_fwd_abar``) -> current-token shortcut (HIP) ->
 readout_proj -> fp32 GroupNorm, * silu(z), + D x (HIP) -> out_proj with the
 residual in the GEMM epilogue.  Dense projections and the embedding are
-PyTorch (hipBLASLt GEMMs).  Forward only: these kernels have no backward here.
+PyTorch (hipBLASLt GEMMs).  The block is forward-only (the fused kernels carry no
+autograd graph; it raises under autograd); Conv1dSiLU alone has its backward.
 
 Generation: ``CDSSMLMHeadModel.prefill`` runs the forward over a prompt and keeps
 per-layer decode state (conv window, the scan's R-mode state, GroupNorm running
@@ -126,15 +127,20 @@ def spectral_biases(cfg: CDSSMConfig, layer_idx: int):
 
 
 class _Conv1dSiLUFn(torch.autograd.Function):
-    """CUDAConv1dSiLUOp (ops.py:13-28) forward through cdssm_conv1d_silu_fwd."""
+    """CUDAConv1dSiLUOp (ops.py:13-28): forward cdssm_conv1d_silu_fwd_strided, backward cdssm_conv1d_silu_bwd
+    (grad_x in x's dtype; grad_weight / grad_bias summed in fp32 and cast to the parameters' dtype, as the
+    reference's launcher does)."""
 
     @staticmethod
     def forward(ctx, x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
+        ctx.save_for_backward(x, weight, bias)
         return conv1d_silu(x, weight, bias)
 
     @staticmethod
     def backward(ctx, grad_out):
-        raise NotImplementedError("conv1d+SiLU backward is not part of this build (forward-only model path)")
+        x, weight, bias = ctx.saved_tensors
+        gx, gw, gb = conv1d_silu_bwd(x, weight, bias, grad_out)
+        return gx, gw.to(weight.dtype).view_as(weight), gb.to(bias.dtype)
 
 
 def _check_gpu(op: str, *ts: Tensor) -> torch.dtype:
@@ -188,6 +194,35 @@ def conv1d_silu(x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
                                                   _lib.ptr(bc), _lib.ptr(y), B, L, C, K, _lib.stream_of(x.device))
     _lib.check(st, "cdssm_conv1d_silu_fwd_strided")
     return y
+
+
+def conv1d_silu_bwd(x: Tensor, weight: Tensor, bias: Tensor, grad_out: Tensor) -> tuple:
+    """Gradients of conv1d_silu: grad_x (B, L, C) in x's dtype, grad_weight (C, K) and grad_bias (C) fp32
+    (conv1d_silu.cu:95-276; deterministic sums)."""
+    _check_gpu("conv1d_silu_bwd", x)
+    B, L, C = x.shape
+    K = weight.shape[-1]
+    try:
+        xs = _token_view(x, C)
+    except ValueError:
+        x = x.contiguous()
+        xs = C
+    go = grad_out.to(x.dtype).contiguous()
+    wc = weight.detach().to(x.dtype).contiguous()
+    bc = bias.detach().to(x.dtype).contiguous()
+    gx = torch.empty((B, L, C), dtype=x.dtype, device=x.device)
+    gw = torch.empty((C, K), dtype=torch.float32, device=x.device)
+    gb = torch.empty((C,), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    nb = lib.cdssm_conv1d_silu_bwd_workspace_bytes(B, L, C, K)
+    if nb < 0:
+        raise ValueError(f"conv1d_silu_bwd: invalid shape B={B} L={L} C={C} K={K}")
+    ws = torch.empty(max(1, nb // 4), dtype=torch.float32, device=x.device)
+    st = lib.cdssm_conv1d_silu_bwd(_lib.DTYPE_CODE[x.dtype], _lib.ptr(x), xs, _lib.ptr(wc), _lib.ptr(bc),
+                                   _lib.ptr(go), _lib.ptr(gx), _lib.ptr(gw), _lib.ptr(gb), _lib.ptr(ws), B, L, C, K,
+                                   _lib.stream_of(x.device))
+    _lib.check(st, "cdssm_conv1d_silu_bwd")
+    return gx, gw, gb
 
 
 def rms_norm(x: Tensor, weight: Tensor, eps: float) -> Tensor:
@@ -469,6 +504,10 @@ class CDSSMBlock(nn.Module):
         N, H, D, Di = cfg.state_dim, cfg.n_heads, cfg.head_dim, cfg.d_inner
         if N != 2:
             raise ValueError("the fused scan of this build supports state_dim = 2")
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            # the fused block kernels carry no autograd graph: a backward would silently miss them
+            raise RuntimeError("CDSSMBlock is forward-only here: call it under torch.no_grad() or "
+                               "torch.inference_mode(), or freeze its parameters")
         B, L, _ = x.shape
         residual = x
         proj = self.in_proj(self.norm(x))  # (B, L, 3 Di + H N); z, x_gate and K are read in place

@@ -147,6 +147,127 @@ __global__ __launch_bounds__(256) void conv1d_silu_step_kernel(const typename T:
   if (K > 1) T::store(wr + int64_t(K - 2) * C, xn);
 }
 
+// ---------------------------------------------------------------------------
+// Backward (conv1d_silu.cu:95-276, CUDAConv1dSiLUOp.backward ops.py:22-28):
+//   u[t] = bias + sum_j w[j] x[t-(K-1)+j],  gu[t] = gy[t] silu'(u[t]),
+//   silu'(u) = s (1 + u (1 - s)), s = sigmoid(u)
+//   gx[t] = sum_j w[j] gu[t+(K-1)-j]       (gu = 0 past the end)
+//   gw[j] = sum_{b,t} gu[t] x[t-(K-1)+j],  gb = sum_{b,t} gu[t]
+// A thread owns one channel over kConvBwdTB tokens: it recomputes u over its
+// tokens plus the K-1 after them (x from K-1 before to K-1 after), writes gx,
+// and its partial weight / bias sums go to a workspace row per (b, token
+// block); a second kernel adds the rows in order per (channel, tap).  No
+// atomics: the gradients do not depend on timing.
+// ---------------------------------------------------------------------------
+constexpr int kConvBwdTB = 16;
+
+template <typename T, int K>
+__global__ __launch_bounds__(256) void conv1d_silu_bwd_kernel(const typename T::raw* __restrict__ x, int64_t x_ts,
+                                                              const typename T::raw* __restrict__ w,
+                                                              const typename T::raw* __restrict__ bias,
+                                                              const typename T::raw* __restrict__ gy,
+                                                              typename T::raw* __restrict__ gx,
+                                                              float* __restrict__ part, int L, int C, int ntb,
+                                                              int n_threads) {
+  constexpr int TB = kConvBwdTB, NX = TB + 2 * (K - 1), NU = TB + K - 1;
+  const int gid = int(blockIdx.x) * int(blockDim.x) + int(threadIdx.x);  // n_threads < 2^31 (host check)
+  if (gid >= n_threads) return;
+  const int rest = gid / C;
+  const int c = gid - rest * C;
+  const int b = rest / ntb;
+  const int tb = rest - b * ntb;
+  const int t0 = tb * TB;
+  float wt[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) wt[j] = T::load(w + int64_t(c) * K + j);
+  const float bs = T::load(bias + c);
+  const typename T::raw* xb = x + int64_t(b) * L * x_ts + c;
+  const typename T::raw* gyb = gy + int64_t(b) * L * C + c;
+  // xs[i] = x[t0 - (K-1) + i], zero outside [0, L)
+  float xs[NX];
+#pragma unroll
+  for (int i = 0; i < NX; ++i) {
+    const int s = t0 - (K - 1) + i;
+    xs[i] = (s >= 0 && s < L) ? T::load(xb + int64_t(s) * x_ts) : 0.0f;
+  }
+  // gu[i] at token t0 + i (zero at and past L)
+  float gu[NU];
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    const int t = t0 + i;
+    float u = bs;
+#pragma unroll
+    for (int j = 0; j < K; ++j) u = fmaf(wt[j], xs[i + j], u);
+    const float sg = 1.0f / (1.0f + __expf(-u));
+    gu[i] = t < L ? T::load(gyb + int64_t(t) * C) * (sg * (1.0f + u * (1.0f - sg))) : 0.0f;
+  }
+  float gw[K], gb = 0.0f;
+#pragma unroll
+  for (int j = 0; j < K; ++j) gw[j] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < TB; ++i) {
+    const int t = t0 + i;
+    if (t < L) {
+      float a = 0.0f;
+#pragma unroll
+      for (int j = 0; j < K; ++j) a = fmaf(wt[j], gu[i + K - 1 - j], a);
+      T::store(gx + (int64_t(b) * L + t) * C + c, a);
+#pragma unroll
+      for (int j = 0; j < K; ++j) gw[j] = fmaf(gu[i], xs[i + j], gw[j]);
+      gb += gu[i];
+    }
+  }
+  float* pr = part + int64_t(b * ntb + tb) * (K + 1) * C + c;
+#pragma unroll
+  for (int j = 0; j < K; ++j) pr[int64_t(j) * C] = gw[j];
+  pr[int64_t(K) * C] = gb;
+}
+
+// grad_weight (C, K) and grad_bias (C), fp32: the partial rows added in order.
+__global__ __launch_bounds__(256) void conv1d_silu_bwd_reduce_kernel(const float* __restrict__ part,
+                                                                     float* __restrict__ gw, float* __restrict__ gb,
+                                                                     int rows, int C, int K) {
+  const int i = int(blockIdx.x) * int(blockDim.x) + int(threadIdx.x);  // (tap j, channel c), j = K: bias
+  if (i >= (K + 1) * C) return;
+  const int j = i / C, c = i - j * C;
+  float a = 0.0f;
+  for (int r = 0; r < rows; ++r) a += part[(int64_t(r) * (K + 1) + j) * C + c];
+  if (j < K)
+    gw[int64_t(c) * K + j] = a;
+  else
+    gb[c] = a;
+}
+
+template <typename T, int K>
+int launch_conv_bwd(const void* x, int64_t x_ts, const void* w, const void* bias, const void* gy, void* gx,
+                    float* gw, float* gb, float* ws, int64_t B, int64_t L, int64_t C, hipStream_t stream) {
+  using raw = typename T::raw;
+  const int ntb = int((L + kConvBwdTB - 1) / kConvBwdTB);
+  const int n = int(B * ntb * C);
+  hipLaunchKernelGGL((conv1d_silu_bwd_kernel<T, K>), dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const raw*>(x), x_ts, static_cast<const raw*>(w), static_cast<const raw*>(bias),
+                     static_cast<const raw*>(gy), static_cast<raw*>(gx), ws, int(L), int(C), ntb, n);
+  const int nr = int((K + 1) * C);
+  hipLaunchKernelGGL(conv1d_silu_bwd_reduce_kernel, dim3(unsigned((nr + 255) / 256)), dim3(256), 0, stream, ws, gw,
+                     gb, int(B * ntb), int(C), K);
+  return cdssm_host::check_launch("cdssm_conv1d_silu_bwd");
+}
+
+template <typename T>
+int dispatch_bwd(int64_t K, const void* x, int64_t x_ts, const void* w, const void* bias, const void* gy, void* gx,
+                 float* gw, float* gb, float* ws, int64_t B, int64_t L, int64_t C, hipStream_t stream) {
+  switch (K) {
+    case 1: return launch_conv_bwd<T, 1>(x, x_ts, w, bias, gy, gx, gw, gb, ws, B, L, C, stream);
+    case 2: return launch_conv_bwd<T, 2>(x, x_ts, w, bias, gy, gx, gw, gb, ws, B, L, C, stream);
+    case 3: return launch_conv_bwd<T, 3>(x, x_ts, w, bias, gy, gx, gw, gb, ws, B, L, C, stream);
+    case 4: return launch_conv_bwd<T, 4>(x, x_ts, w, bias, gy, gx, gw, gb, ws, B, L, C, stream);
+    case 5: return launch_conv_bwd<T, 5>(x, x_ts, w, bias, gy, gx, gw, gb, ws, B, L, C, stream);
+    case 6: return launch_conv_bwd<T, 6>(x, x_ts, w, bias, gy, gx, gw, gb, ws, B, L, C, stream);
+    case 7: return launch_conv_bwd<T, 7>(x, x_ts, w, bias, gy, gx, gw, gb, ws, B, L, C, stream);
+    default: return launch_conv_bwd<T, 8>(x, x_ts, w, bias, gy, gx, gw, gb, ws, B, L, C, stream);
+  }
+}
+
 template <typename T, int VEC, int K>
 int launch_conv(const void* x, int64_t x_ts, const void* w, const void* bias, void* y, int64_t B, int64_t L,
                 int64_t C, hipStream_t stream) {
@@ -245,4 +366,36 @@ extern "C" int cdssm_conv1d_silu_step(int dtype, const void* x, int64_t x_batch_
                        x_batch_stride, static_cast<float*>(window), static_cast<const float*>(weight),
                        static_cast<const float*>(bias), static_cast<float*>(y), int(B), int(C), int(K));
   return cdssm_host::check_launch(op);
+}
+
+extern "C" int64_t cdssm_conv1d_silu_bwd_workspace_bytes(int64_t B, int64_t L, int64_t C, int64_t K) {
+  if (B <= 0 || L <= 0 || C <= 0 || K < 1 || K > 8) return -1;
+  return B * ((L + kConvBwdTB - 1) / kConvBwdTB) * (K + 1) * C * int64_t(sizeof(float));
+}
+
+extern "C" int cdssm_conv1d_silu_bwd(int dtype, const void* x, int64_t x_token_stride, const void* weight,
+                                     const void* bias, const void* grad_out, void* grad_x, float* grad_weight,
+                                     float* grad_bias, float* workspace, int64_t B, int64_t L, int64_t C, int64_t K,
+                                     hipStream_t stream) {
+  const char* op = "cdssm_conv1d_silu_bwd";
+  if (dtype != 0 && dtype != 1) {
+    cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
+    return CDSSM_EINVAL;
+  }
+  if (B <= 0 || L <= 0 || C <= 0 || K < 1 || K > 8 || x_token_stride < C ||
+      B * ((L + kConvBwdTB - 1) / kConvBwdTB) * C >= (int64_t(1) << 31) || B * L >= (int64_t(1) << 31)) {
+    cdssm_host::set_error("%s: need B, L, C > 0, B * ceil(L/16) * C < 2^31, 1 <= kernel_size <= 8, "
+                          "x token stride >= C (B=%lld L=%lld C=%lld K=%lld)",
+                          op, (long long)B, (long long)L, (long long)C, (long long)K);
+    return CDSSM_EINVAL;
+  }
+  if (!x || !weight || !bias || !grad_out || !grad_x || !grad_weight || !grad_bias || !workspace) {
+    cdssm_host::set_error("%s: null pointer argument", op);
+    return CDSSM_EINVAL;
+  }
+  if (dtype == 1)
+    return dispatch_bwd<BF16>(K, x, x_token_stride, weight, bias, grad_out, grad_x, grad_weight, grad_bias, workspace,
+                              B, L, C, stream);
+  return dispatch_bwd<F32>(K, x, x_token_stride, weight, bias, grad_out, grad_x, grad_weight, grad_bias, workspace,
+                           B, L, C, stream);
 }

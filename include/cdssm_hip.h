@@ -248,10 +248,31 @@ int cdssm_dynamics_fused_bwd(int dtype, const void* grad_A_bar, const void* grad
  * Conv1dSiLU, modules.py:14-35): causal depthwise conv + SiLU,
  *   y[b,t,c] = silu(bias[c] + sum_{j<K} w[c,j] x[b, t-(K-1)+j, c]), x = 0 before t = 0.
  * x, y (B,L,C); weight (C,1,K); bias (C); all `dtype` (the reference: bf16,
- * K = 4 only).  Supported: 1 <= K <= 8, B * ceil(L/16) * C < 2^31.  Forward only.
+ * K = 4 only).  Supported: 1 <= K <= 8, B * ceil(L/16) * C < 2^31.  Backward:
+ * cdssm_conv1d_silu_bwd.
  */
 int cdssm_conv1d_silu_fwd(int dtype, const void* x, const void* weight, const void* bias, void* y, int64_t B,
                           int64_t L, int64_t C, int64_t K, hipStream_t stream);
+
+/* Bytes of the fp32 workspace cdssm_conv1d_silu_bwd needs (-1 if invalid). */
+int64_t cdssm_conv1d_silu_bwd_workspace_bytes(int64_t B, int64_t L, int64_t C, int64_t K);
+
+/*
+ * Replaces conv1d_silu_bwd_cuda (conv1d_silu.cu:95-276, bound at
+ * binding.cpp, called by CUDAConv1dSiLUOp.backward, ops.py:22-28):
+ *   gu = grad_out * silu'(u) with u the recomputed conv output,
+ *   grad_x[t] = sum_j w[c,j] gu[t+(K-1)-j]        (`dtype`, (B,L,C) dense),
+ *   grad_weight[c,j] = sum_{b,t} gu x[t-(K-1)+j]   (fp32 (C,K)),
+ *   grad_bias[c] = sum_{b,t} gu                   (fp32 (C)),
+ * as the reference (which returns the fp32 sums cast to the parameters'
+ * dtype).  x read through a token stride (elements); grad_out (B,L,C) dense.
+ * The weight and bias sums are formed from per-(b, 16-token block) partials
+ * added in a fixed order (the reference uses float atomics): deterministic.
+ * workspace: cdssm_conv1d_silu_bwd_workspace_bytes.  1 <= K <= 8.
+ */
+int cdssm_conv1d_silu_bwd(int dtype, const void* x, int64_t x_token_stride, const void* weight, const void* bias,
+                          const void* grad_out, void* grad_x, float* grad_weight, float* grad_bias, float* workspace,
+                          int64_t B, int64_t L, int64_t C, int64_t K, hipStream_t stream);
 
 /*
  * cdssm_conv1d_silu_fwd with x read through a token stride (elements between

@@ -127,3 +127,41 @@ def test_conv1d_silu_strided(dtype, B, L, C, K, pad):
     e = rel(y, yr)
     log(f"   rel err {e:.2e}")
     assert e <= (1e-6 if dtype == torch.float32 else 1e-2)
+
+
+@pytest.mark.parametrize("dtype,B,L,C,K,pad", [(torch.float32, 2, 37, 24, 4, 0), (torch.float32, 1, 50, 16, 3, 5),
+                                               (torch.bfloat16, 2, 300, 256, 4, 64), (torch.float32, 1, 3, 8, 8, 0)])
+def test_conv1d_silu_backward(dtype, B, L, C, K, pad):
+    """Conv1dSiLU backward (cdssm_conv1d_silu_bwd) against autograd through the oracle's fp64 conv on the same
+    rounded inputs; x read as a column slice when pad > 0."""
+    from cdssm_hip.lm import Conv1dSiLU
+    log(f"[conv1d_silu bwd] {dtype} B{B} L{L} C{C} K{K} column offset {pad}")
+    g = torch.Generator().manual_seed(6)
+    f32 = dict(generator=g, dtype=torch.float32)
+    wide = torch.randn(B, L, pad + C + 8, **f32).to(dtype)
+    w = (torch.randn(C, 1, K, **f32) / K ** 0.5).to(dtype)
+    b = torch.randn(C, **f32).to(dtype)
+    gy = torch.randn(B, L, C, **f32).to(dtype)
+    conv = Conv1dSiLU(C, kernel_size=K).to(dtype).to(DEV)
+    with torch.no_grad():
+        conv.weight.copy_(w)
+        conv.bias.copy_(b)
+    xd = wide.to(DEV)[..., pad:pad + C].detach().requires_grad_(True)
+    conv(xd).backward(gy.to(DEV))
+    xr = wide[..., pad:pad + C].double().requires_grad_(True)
+    wr, br = w.double().requires_grad_(True), b.double().requires_grad_(True)
+    lo.conv1d_silu(xr, wr, br).backward(gy.double())
+    ex, ew, eb = rel(xd.grad, xr.grad), rel(conv.weight.grad, wr.grad), rel(conv.bias.grad, br.grad)
+    log(f"   rel err grad_x {ex:.2e} grad_w {ew:.2e} grad_b {eb:.2e}")
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert ex <= tol and ew <= tol and eb <= tol
+    assert conv.weight.grad.dtype == dtype and xd.grad.dtype == dtype
+
+
+def test_block_refuses_grad_mode():
+    """The fused block kernels carry no autograd graph, so a block run with gradients enabled raises."""
+    from cdssm_hip.lm import CDSSMConfig, CDSSMBlock
+    cfg = CDSSMConfig(d_model=64, n_layers=1, context_length=64, vocab_size=16, state_dim=2, d_inner=64)
+    blk = CDSSMBlock(cfg).to(DEV)
+    with pytest.raises(RuntimeError, match="forward-only"):
+        blk(torch.randn(1, 8, 64, device=DEV))
