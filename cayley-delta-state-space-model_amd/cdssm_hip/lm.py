@@ -293,8 +293,9 @@ def group_norm_gate(y: Tensor, num_groups: int, gamma: Tensor, beta: Tensor, eps
                     x_conv: Tensor, D: Tensor, return_sums: bool = False):
     """GroupNorm over (channels of a group, all L) in fp32, cast to y's dtype, * silu(z) + D * x_conv
     (block.py:215-225).  y, x_conv (B, L, C) dense; z (B, L, C) with any token stride.  With
-    ``return_sums`` also the running statistics a decode step continues from (``group_norm_sums``'s
-    layout), taken from the kernel's own partial sums."""
+    ``return_sums`` also the running statistics a decode step continues from, (B, G, 4) fp32 = (shift,
+    sum (x - shift), sum (x - shift)^2, count) with the shift the group's first element, taken from the
+    kernel's own partial sums."""
     Dp = D.to(y.dtype).contiguous()
     dt = _check_gpu("group_norm_gate", y, z, x_conv, Dp)
     B, L, C = y.shape
@@ -396,22 +397,12 @@ def conv1d_silu_step(x: Tensor, window: Tensor, weight: Tensor, bias: Tensor) ->
     return y
 
 
-def group_norm_sums(y: Tensor, num_groups: int) -> Tensor:
-    """Running GroupNorm statistics of y (B, L, C) per (b, group): (shift, sum (x - shift), sum (x - shift)^2,
-    count) fp32 (B, G, 4), shift = the group's first element; the decode step's state for the epilogue."""
-    B, L, C = y.shape
-    G = int(num_groups)
-    yg = y.reshape(B, L, G, C // G).double()
-    k0 = yg[:, 0, :, 0]
-    d = yg - k0[:, None, :, None]
-    n = torch.full_like(k0, float(L * (C // G)))
-    return torch.stack([k0, d.sum((1, 3)), (d * d).sum((1, 3)), n], dim=-1).float().contiguous()
-
-
 def group_norm_gate_step(y: Tensor, gsum: Tensor, gamma: Tensor, beta: Tensor, eps: float, z: Tensor,
                          x_conv: Tensor, D: Tensor) -> Tensor:
     """One decode token of the GroupNorm epilogue (block.py:215-225) with running statistics ``gsum``
-    (B, G, 4), updated in place; y, x_conv (B, C); z (B, C) with any row stride."""
+    (B, G, 4) fp32 = (shift, sum (x - shift), sum (x - shift)^2, count) per (b, group) over every position
+    so far (as ``group_norm_gate(..., return_sums=True)`` returns them), updated in place; y, x_conv (B, C);
+    z (B, C) with any row stride."""
     Dp = D.to(y.dtype).contiguous()
     yc, xc = y.contiguous(), x_conv.contiguous()
     dt = _check_gpu("group_norm_gate_step", yc, z, xc, Dp)

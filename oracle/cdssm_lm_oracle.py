@@ -10,6 +10,8 @@ Restates, in PyTorch on the CPU (run in float64 by the tests):
                      of cdssm_oracle (dynamics_fused_fwd, normalize_kq,
                      ssd_chunkwise_scan, readout)
   * lm_forward       model.py:38-51 (embedding, blocks, final RMSNorm, tied head)
+  * group_norm_running_sums  the decode step's GroupNorm state (statistics of
+                     block.py:216-223 over the positions so far)
 Parameters come as a ``state_dict`` with the reference's names.
 
 Pins (tests/test_oracle_lm.py): conv1d_silu against torch.nn.functional.conv1d
@@ -18,7 +20,8 @@ the tap order fixed by the reference's comment (conv1d_silu.cu:74-80);
 rms_norm against its closed form; block_forward by invariants (a zero
 out_proj makes the block the identity; batch rows are independent) -- the
 wiring itself, between pinned pieces, follows block.py line by line and is
-otherwise pinned only by those invariants.  Note: the model is not causal in
+otherwise pinned only by those invariants; group_norm_running_sums against
+the groups' mean and variance (torch) and by appending a token.  Note: the model is not causal in
 the reference: its GroupNorm (block.py:216-223) takes statistics over the
 group's channels and all L positions, which this restatement reproduces.
 """
@@ -89,6 +92,20 @@ def block_forward(p: dict, pre: str, x: Tensor, v_first: Optional[Tensor], cfg) 
                      1e-5).transpose(1, 2)                              # block.py:216-223 (nn.GroupNorm eps)
     y = y * F.silu(z) + g("D") * x_conv
     return residual + _linear(y, g("out_proj.weight")), v_first
+
+
+def group_norm_running_sums(y: Tensor, num_groups: int) -> Tensor:
+    """The GroupNorm decode state after positions 0 .. L-1 of y (B, L, C): per (b, group) the shift (the
+    group's first element), sum (x - shift), sum (x - shift)^2 and the count, (B, G, 4) -- the statistics
+    of block.py:216-223 over every position so far, in the layout the decode step keeps.  Computed in
+    float64 (the caller casts)."""
+    B, L, C = y.shape
+    G = int(num_groups)
+    yg = y.reshape(B, L, G, C // G).double()
+    k0 = yg[:, 0, :, 0]
+    d = yg - k0[:, None, :, None]
+    n = torch.full_like(k0, float(L * (C // G)))
+    return torch.stack([k0, d.sum((1, 3)), (d * d).sum((1, 3)), n], dim=-1)
 
 
 def lm_forward(p: dict, input_ids: Tensor, cfg) -> Tensor:

@@ -62,3 +62,21 @@ def test_lm_forward_rows_are_independent_and_groupnorm_spans_the_sequence():
     b = lo.lm_forward(p, ids2, cfg)
     assert torch.equal(a[0], b[0])
     assert not torch.allclose(a[1, :50], b[1, :50])
+
+
+def test_group_norm_running_sums_give_the_group_statistics():
+    """The decode state's (shift, S1, S2, n) reproduce each group's mean and biased variance over all
+    positions (torch's var on the (L, C/G) block), and appending a token's sums equals the sums of the
+    longer sequence."""
+    g = torch.Generator().manual_seed(9)
+    y = torch.randn(2, 37, 24, generator=g, dtype=torch.float64) * 3 + 5
+    s = lo.group_norm_running_sums(y, 4)
+    blk = y.reshape(2, 37, 4, 6)
+    mean = s[..., 0] + s[..., 1] / s[..., 3]
+    var = s[..., 2] / s[..., 3] - (s[..., 1] / s[..., 3]) ** 2
+    assert torch.allclose(mean, blk.mean((1, 3)), rtol=0, atol=1e-12)
+    assert torch.allclose(var, blk.var((1, 3), unbiased=False), rtol=0, atol=1e-10)
+    s36 = lo.group_norm_running_sums(y[:, :36], 4)
+    d = y[:, 36].reshape(2, 4, 6) - s36[..., 0:1]
+    step = torch.stack([s36[..., 0], s36[..., 1] + d.sum(-1), s36[..., 2] + (d * d).sum(-1), s36[..., 3] + 6], -1)
+    assert torch.allclose(step, s, rtol=1e-12, atol=1e-10)
