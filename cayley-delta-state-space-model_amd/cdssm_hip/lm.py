@@ -458,7 +458,19 @@ class CDSSMBlock(nn.Module):
         self.D = nn.Parameter(torch.zeros(Di))
         self.v_residual_gate = nn.Parameter(torch.zeros(H))
         self.shortcut_scale = nn.Parameter(torch.zeros(1))
+        self._f32_cache: dict = {}
         self._init_weights(layer_idx)
+
+    def _fp32(self, name: str) -> Tensor:
+        """A contiguous fp32 copy of parameter / buffer ``name`` (the reference's ``.float()`` casts), kept
+        while the tensor's storage and version are unchanged, so a forward launches no cast kernels."""
+        t = getattr(self, name)
+        key = (t.data_ptr(), t._version, t.dtype, t.device)
+        hit = self._f32_cache.get(name)
+        if hit is None or hit[0] != key:
+            hit = (key, t.detach().float().contiguous())
+            self._f32_cache[name] = hit
+        return hit[1]
 
     @torch.no_grad()
     def _init_weights(self, layer_idx: int) -> None:
@@ -525,8 +537,8 @@ class CDSSMBlock(nn.Module):
             cache["vgate"] = torch.sigmoid(self.v_residual_gate.detach().float())[None, :, None].to(x.dtype)
         gates = self.gate_proj(x_conv)
         A_bar, vp, beta, sel_C = DynamicsFusedFn.apply(
-            gates.contiguous(), self.log_dt_scale.float(), self.rope_freqs, cfg.gating_c, cfg.bf16_omega_thresh,
-            cfg.bf16_delta, cfg.bf16_smoothness, cfg.eps_adaptive_dt, H, N)
+            gates.contiguous(), self._fp32("log_dt_scale"), self._fp32("rope_freqs"), cfg.gating_c,
+            cfg.bf16_omega_thresh, cfg.bf16_delta, cfg.bf16_smoothness, cfg.eps_adaptive_dt, H, N)
         Q = self.Q_proj(x_conv).reshape(B, L, H, D)
         K, Q, qk = normalize_kq_qk(K, Q)
         V = V.contiguous()
@@ -535,7 +547,7 @@ class CDSSMBlock(nn.Module):
         else:
             retrieved, cache["scan"] = prefill_abar(Q, K, V, beta, sel_C, A_bar, vp, chunk_size=cfg.chunk_size)
         # current-token shortcut (block.py:202-205) through the readout: sel_C s (q.k)^2 V vp
-        shortcut_readout_(retrieved, qk, V, vp, sel_C, self.shortcut_scale)
+        shortcut_readout_(retrieved, qk, V, vp, sel_C, self._fp32("shortcut_scale"))
         y = self.readout_proj(retrieved.reshape(B, L, H * N))
         y = group_norm_gate(y, self.ssm_norm.num_groups, self.ssm_norm.weight, self.ssm_norm.bias,
                             self.ssm_norm.eps, z, x_conv, self.D, return_sums=cache is not None)
