@@ -472,6 +472,20 @@ class CDSSMBlock(nn.Module):
             self._f32_cache[name] = hit
         return hit[1]
 
+    def _stacked_gate_q(self) -> tuple:
+        """[gate_proj.weight; Q_proj.weight] and [gate_proj.bias; 0]: the decode step's two projections of
+        x_conv (block.py:180, 190) as one GEMM (one launch fewer per layer; at the forward's B*L rows the
+        two GEMMs are faster apart), kept while the parameters' storage and versions are unchanged."""
+        gw, gb, qw = self.gate_proj.weight, self.gate_proj.bias, self.Q_proj.weight
+        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in (gw, gb, qw))
+        hit = self._f32_cache.get("gate_q")
+        if hit is None or hit[0] != key:
+            w = torch.cat([gw.detach(), qw.detach().to(gw.dtype)], dim=0).contiguous()
+            b = torch.cat([gb.detach(), torch.zeros(qw.shape[0], dtype=gb.dtype, device=gb.device)]).contiguous()
+            hit = (key, (w, b))
+            self._f32_cache["gate_q"] = hit
+        return hit[1]
+
     @torch.no_grad()
     def _init_weights(self, layer_idx: int) -> None:
         """Variance-preserving init (block.py:90-138) and spectral init (init.py:44-126)."""
@@ -535,6 +549,8 @@ class CDSSMBlock(nn.Module):
             cache["rope"] = self.rope_freqs.detach().float().contiguous()
             cache["scale"] = self.shortcut_scale.detach().float().reshape(1).contiguous()
             cache["vgate"] = torch.sigmoid(self.v_residual_gate.detach().float())[None, :, None].to(x.dtype)
+            # gate_proj and Q_proj share their input: one GEMM per step over the stacked weights
+            cache["w_gq"], cache["b_gq"] = self._stacked_gate_q()
         gates = self.gate_proj(x_conv)
         A_bar, vp, beta, sel_C = DynamicsFusedFn.apply(
             gates.contiguous(), self._fp32("log_dt_scale"), self._fp32("rope_freqs"), cfg.gating_c,
@@ -577,11 +593,12 @@ class CDSSMBlock(nn.Module):
         else:
             V = torch.lerp(v_first, V, cache["vgate"])
         x_conv = conv1d_silu_step(x_gate, cache["conv"], self.conv.weight, self.conv.bias)
-        gates = self.gate_proj(x_conv).reshape(B, 1, -1)
-        A_bar, vp, beta, sel_C = dynamics_at(gates, cache["lds"], cache["rope"], cfg.gating_c,
+        GH = (N + 5) * H
+        gq = torch.addmm(cache["b_gq"], x_conv, cache["w_gq"].t())  # (B, GH + Di): gates | Q
+        A_bar, vp, beta, sel_C = dynamics_at(gq[:, :GH].reshape(B, 1, GH), cache["lds"], cache["rope"], cfg.gating_c,
                                              cfg.bf16_omega_thresh, cfg.bf16_delta, cfg.bf16_smoothness,
                                              cfg.eps_adaptive_dt, H, N, 0, cache["l"])
-        Q = self.Q_proj(x_conv).reshape(B, 1, H, D)
+        Q = gq[:, GH:].reshape(B, 1, H, D)  # read in place (a column slice)
         K, Q, qk = normalize_kq_qk(K, Q)
         V = V.contiguous()
         retrieved = decode_step_abar(cache["scan"], Q, K, V, beta, sel_C, A_bar, vp)  # (B, H, 2)
