@@ -136,3 +136,54 @@ def test_product_path_has_no_cpu_fallback():
     s = torch.zeros(1, 64, 2)
     with pytest.raises(RuntimeError, match="GPU only"):
         chunkwise_delta_scan(x, x, torch.zeros(1, 64, 2, 2), s, s, s, s, torch.zeros(2), torch.zeros(2), 1.0)
+
+
+# The block / decode entry points: invalid arguments return -1 with a message and launch nothing
+# (fake, 16-byte-aligned addresses: validation happens before any device access).
+_BLOCK_CALLS = {
+    "cdssm_rms_norm_fwd": dict(dtype=1, x=16, w=16, y=16, rows=4, C=64, eps=1e-5, stream=None),
+    "cdssm_normalize_kq_qk_fwd": dict(dtype=1, K=16, ks=1024, Q=16, qs=1024, Ko=16, Qo=16, qk=16, BL=4, H=16,
+                                      D=64, stream=None),
+    "cdssm_shortcut_readout_fwd": dict(dtype=1, ret=16, qk=16, V=16, vp=16, sel=16, scale=16, n=8, stream=None),
+    "cdssm_group_norm_gate_fwd": dict(dtype=1, pdt=1, y=16, g=16, b=16, z=16, zs=64, xc=16, D=16, out=16, ws=16,
+                                      B=1, L=8, C=64, G=4, eps=1e-5, stream=None),
+    "cdssm_group_norm_gate_step": dict(dtype=1, pdt=1, y=16, gsum=16, g=16, b=16, z=16, zs=64, xc=16, D=16,
+                                       out=16, B=2, C=64, G=4, eps=1e-5, stream=None),
+    "cdssm_conv1d_silu_step": dict(dtype=1, x=16, xs=64, win=16, w=16, b=16, y=16, B=2, C=64, K=4, stream=None),
+    "cdssm_conv1d_silu_bwd": dict(dtype=1, x=16, xs=64, w=16, b=16, go=16, gx=16, gw=16, gb=16, ws=16, B=1, L=8,
+                                  C=64, K=4, stream=None),
+    "cdssm_decode_step_abar": dict(dtype=1, q=16, k=16, v=16, beta=16, sel=16, a=16, vp=16, state=16, gam=16,
+                                   pos=16, y=16, h=None, B=2, H=3, D=64, N=2, chunk=64, stream=None),
+    "cdssm_dynamics_fused_fwd_at": dict(dtype=1, gate=16, lds=16, rope=16, c=1.0, thr=1.0, delta=0.1, smooth=1.0,
+                                        eps=1.0, A=16, vp=16, beta=16, sel=16, B=1, L=1, H=4, N=2, l0=5,
+                                        l0_dev=None, stream=None),
+}
+
+
+@pytest.mark.parametrize("fn,bad,msg", [
+    ("cdssm_rms_norm_fwd", dict(dtype=5), "dtype"),
+    ("cdssm_rms_norm_fwd", dict(rows=0), "rows > 0"),
+    ("cdssm_rms_norm_fwd", dict(w=None), "null"),
+    ("cdssm_normalize_kq_qk_fwd", dict(D=48), "need D in"),
+    ("cdssm_normalize_kq_qk_fwd", dict(ks=512), "token strides"),
+    ("cdssm_normalize_kq_qk_fwd", dict(K=8), "aligned"),
+    ("cdssm_shortcut_readout_fwd", dict(n=0), "n > 0"),
+    ("cdssm_shortcut_readout_fwd", dict(scale=None), "null"),
+    ("cdssm_group_norm_gate_fwd", dict(G=5), "divisible by G"),
+    ("cdssm_group_norm_gate_fwd", dict(pdt=3), "param_dtype"),
+    ("cdssm_group_norm_gate_fwd", dict(ws=None), "null"),
+    ("cdssm_group_norm_gate_step", dict(zs=32), "row stride"),
+    ("cdssm_conv1d_silu_step", dict(K=9), "kernel_size"),
+    ("cdssm_conv1d_silu_step", dict(win=None), "null"),
+    ("cdssm_conv1d_silu_bwd", dict(xs=32), "token stride"),
+    ("cdssm_conv1d_silu_bwd", dict(ws=None), "null"),
+    ("cdssm_decode_step_abar", dict(D=32), "D in"),
+    ("cdssm_decode_step_abar", dict(a=None), "null"),
+    ("cdssm_dynamics_fused_fwd_at", dict(l0=-1), "position offset"),
+])
+def test_block_entry_points_reject_invalid_arguments_without_launching(fn, bad, msg):
+    lib = _lib.load()
+    args = dict(_BLOCK_CALLS[fn])
+    args.update(bad)
+    assert getattr(lib, fn)(*args.values()) == -1
+    assert msg in _lib.last_error()
