@@ -439,6 +439,10 @@ class RMSNorm(nn.Module):
 class CDSSMBlock(nn.Module):
     """One CD-SSM block (block.py:14-229), forward on the HIP kernels."""
 
+    # decode steps take the one-launch token kernel (cdssm_decode_block_token) where its alignment holds;
+    # False: the separate per-token kernels (the same values)
+    fused_step: bool = True
+
     def __init__(self, config: CDSSMConfig, layer_idx: int = 0):
         super().__init__()
         self.config = config
@@ -549,6 +553,7 @@ class CDSSMBlock(nn.Module):
             cache["rope"] = self.rope_freqs.detach().float().contiguous()
             cache["scale"] = self.shortcut_scale.detach().float().reshape(1).contiguous()
             cache["vgate"] = torch.sigmoid(self.v_residual_gate.detach().float())[None, :, None].to(x.dtype)
+            cache["vgate_h"] = cache["vgate"].reshape(-1).contiguous()
             # gate_proj and Q_proj share their input: one GEMM per step over the stacked weights
             cache["w_gq"], cache["b_gq"] = self._stacked_gate_q()
         gates = self.gate_proj(x_conv)
@@ -588,13 +593,33 @@ class CDSSMBlock(nn.Module):
         z, x_gate, K, V = proj.split([Di, Di, Di, H * N], dim=-1)
         K = K.reshape(B, 1, H, D)
         V = V.reshape(B, H, N)
+        x_conv = conv1d_silu_step(x_gate, cache["conv"], self.conv.weight, self.conv.bias)
+        GH = (N + 5) * H
+        gq = torch.addmm(cache["b_gq"], x_conv, cache["w_gq"].t())  # (B, GH + Di): gates | Q
+        es = x.element_size()
+        if (self.fused_step and D in (64, 128) and (gq.data_ptr() + GH * es) % 16 == 0 and (gq.stride(0) * es) % 16 == 0
+                and (proj.data_ptr() + 2 * Di * es) % 16 == 0 and (proj.stride(0) * es) % 16 == 0
+                and proj.stride(1) == 1 and gq.stride(1) == 1):
+            # the token's dynamics, K/Q norm, value residual, scan step and shortcut in one launch
+            st = cache["scan"]
+            retrieved = torch.empty(B, H, N, dtype=x.dtype, device=x.device)
+            v_used = torch.empty(B, H, N, dtype=x.dtype, device=x.device)
+            vf = None if v_first is None else v_first.contiguous()
+            status = _lib.load().cdssm_decode_block_token(
+                _lib.DTYPE_CODE[x.dtype], _lib.ptr(gq), gq.stride(0), _lib.ptr(proj), proj.stride(0), 2 * Di,
+                3 * Di, _lib.ptr(vf), _lib.ptr(cache["vgate_h"]) if vf is not None else None, _lib.ptr(cache["lds"]),
+                _lib.ptr(cache["rope"]), float(cfg.gating_c), float(cfg.bf16_omega_thresh), float(cfg.bf16_delta),
+                float(cfg.bf16_smoothness), float(cfg.eps_adaptive_dt), _lib.ptr(cache["l"]), _lib.ptr(cache["scale"]),
+                _lib.ptr(st.state), _lib.ptr(st.gam), _lib.ptr(st.pos), _lib.ptr(retrieved), _lib.ptr(v_used), B, H,
+                D, N, st.chunk_size, _lib.stream_of(x.device))
+            _lib.check(status, "cdssm_decode_block_token")
+            if v_first is None:
+                v_first = v_used
+            return self._step_tail(x, retrieved, z, x_conv, cache), v_first
         if v_first is None:
             v_first = V.detach()
         else:
             V = torch.lerp(v_first, V, cache["vgate"])
-        x_conv = conv1d_silu_step(x_gate, cache["conv"], self.conv.weight, self.conv.bias)
-        GH = (N + 5) * H
-        gq = torch.addmm(cache["b_gq"], x_conv, cache["w_gq"].t())  # (B, GH + Di): gates | Q
         A_bar, vp, beta, sel_C = dynamics_at(gq[:, :GH].reshape(B, 1, GH), cache["lds"], cache["rope"], cfg.gating_c,
                                              cfg.bf16_omega_thresh, cfg.bf16_delta, cfg.bf16_smoothness,
                                              cfg.eps_adaptive_dt, H, N, 0, cache["l"])
@@ -603,11 +628,16 @@ class CDSSMBlock(nn.Module):
         V = V.contiguous()
         retrieved = decode_step_abar(cache["scan"], Q, K, V, beta, sel_C, A_bar, vp)  # (B, H, 2)
         shortcut_readout_(retrieved, qk, V, vp, sel_C, cache["scale"])
-        y = self.readout_proj(retrieved.reshape(B, H * N))
+        return self._step_tail(x, retrieved, z, x_conv, cache), v_first
+
+    def _step_tail(self, x: Tensor, retrieved: Tensor, z: Tensor, x_conv: Tensor, cache: dict) -> Tensor:
+        """readout_proj, the GroupNorm step, out_proj + residual; advances the position."""
+        B = x.shape[0]
+        y = self.readout_proj(retrieved.reshape(B, -1))
         y = group_norm_gate_step(y, cache["gsum"], self.ssm_norm.weight, self.ssm_norm.bias, self.ssm_norm.eps, z,
                                  x_conv, self.D)
         cache["l"].add_(1)
-        return torch.addmm(x, y, self.out_proj.weight.t()), v_first
+        return torch.addmm(x, y, self.out_proj.weight.t())
 
 
 class CDSSMLMHeadModel(nn.Module):

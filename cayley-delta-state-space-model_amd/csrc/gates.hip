@@ -21,13 +21,10 @@
 // normalize fwd/bwd (NormalizeKQFn, ops.py:84-97; normalize_kq.cu:75-79,
 //   :143-163): x_hat = x rsqrt(sum x^2 + 1e-6); g_in = (g - x_hat <g, x_hat>) rsqrt(...).
 //   Any head_dim D <= 256 (the reference kernel is correct only for D = 64).
-#include "common.hpp"
+#include "gate_math.hpp"
 
 namespace cdssm {
 namespace gates {
-
-__device__ __forceinline__ float softplus(float x) { return x > 20.0f ? x : log1pf(__expf(x)); }
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
 struct GateIdx {
   int64_t bl;   // b*L + l
@@ -55,30 +52,17 @@ __global__ __launch_bounds__(256) void dynamics_fwd_kernel(
   const typename T::raw* row = gate + g.bl * int64_t(G) * H + g.h;
   const float freq = rope[g.h];
   const float pos = float(g.l + l0 + (l0_dev ? *l0_dev : 0)) * freq;  // sequence position
-  const float selB = T::load(row + int64_t(N) * H), selC = T::load(row + int64_t(N + 1) * H);
-  const float seldt = T::load(row + int64_t(N + 2) * H), braw = T::load(row + int64_t(N + 3) * H);
-  const float rraw = T::load(row + int64_t(N + 4) * H);
-  const float rg = sigmoid(rraw);
-  const float a0 = softplus(T::load(row));
-  const float w0 = T::load(row + int64_t(Nh) * H) + pos;
-  const float dts = softplus(log_dt_scale[g.h]);
-  const float wabs = fabsf(w0);
-  const float dt_raw = dts / (a0 + wabs + adt_eps);
-  const float dt_max = (2.0f - adt_delta) / (a0 + adt_eps);
-  const float blend = sigmoid((omega_thresh - wabs) / adt_smooth);
-  const float dt = blend * fminf(dt_raw, dt_max) + (1.0f - blend) * dt_raw + softplus(seldt);
+  const GateConsts kc{gating_c, omega_thresh, adt_delta, adt_smooth, adt_eps};
+  const GateToken gt = gate_token<T>(row, H, N, log_dt_scale[g.h], pos, kc);
   const int64_t o = g.bl * H + g.h;
   for (int j = 0; j < Nh; ++j) {
-    const float aj = softplus(T::load(row + int64_t(j) * H));
-    const float wj = T::load(row + int64_t(Nh + j) * H) + pos;
-    // r enters only through c*r: cayley_gated(dt, r, alpha, omega, c)
-    const Transition tr = cayley_gated(dt, rg, aj, wj, gating_c);
+    const Transition tr = gate_pair<T>(row, H, N, j, pos, gt, kc);
     T::store(A_out + o * N + 2 * j, tr.ar);
     T::store(A_out + o * N + 2 * j + 1, tr.ai);
     T::store(vp_out + o * Nh + j, tr.vp);
   }
-  T::store(beta_out + o, sigmoid(braw) * sigmoid(selB));
-  T::store(selc_out + o, sigmoid(selC));
+  T::store(beta_out + o, gt.beta);
+  T::store(selc_out + o, gt.selc);
 }
 
 template <typename T>

@@ -398,6 +398,31 @@ int cdssm_group_norm_gate_step(int dtype, int param_dtype, const void* y, float*
                                const void* D, void* out, int64_t B, int64_t C, int64_t G, float eps,
                                hipStream_t stream);
 
+/*
+ * One decode token of the model block's scan path in one launch, per (b, h):
+ * the gate-level dynamics at the device-held position (as
+ * cdssm_dynamics_fused_fwd_at), K/Q normalisation and q.k (as
+ * cdssm_normalize_kq_qk_fwd), the value residual V = lerp(v_first, V, vgate)
+ * (block.py:169-174; v_first null for layer 0), the gate-level scan decode
+ * step (as cdssm_decode_step_abar) and the current-token shortcut (as
+ * cdssm_shortcut_readout_fwd), each intermediate rounded where those kernels
+ * store it.  gq (B, 7H + H*D) rows: [gate row | Q] (the stacked gate_proj /
+ * Q_proj GEMM output), row stride gq_stride; proj (B, P) the in_proj output
+ * with K at column k_off and V at v_off, row stride proj_stride; Q and K rows
+ * 16-byte aligned.  vgate (H) = sigmoid(v_residual_gate) in `dtype`;
+ * log_dt_scale, rope_freqs (H) fp32; position: int64 on the device;
+ * shortcut_scale: one fp32 on the device.  Outputs retrieved (B, H, 2) and
+ * v_out (B, H, 2) (the V used; layer 0's is v_first of the later layers).
+ * N = 2, D in {64, 128}.  No reference counterpart (the reference re-forwards).
+ */
+int cdssm_decode_block_token(int dtype, const void* gq, int64_t gq_stride, const void* proj, int64_t proj_stride,
+                             int64_t k_off, int64_t v_off, const void* v_first, const void* vgate,
+                             const float* log_dt_scale, const float* rope_freqs, float gating_c, float omega_thresh,
+                             float adt_delta, float adt_smoothness, float adt_eps, const int64_t* position,
+                             const float* shortcut_scale, float* state, float* gam, int* pos, void* retrieved,
+                             void* v_out, int64_t B, int64_t H, int64_t D, int64_t N, int64_t chunk,
+                             hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -136,10 +136,14 @@ def test_group_norm_step_matches_forward(dtype):
         assert e <= (1e-5 if dtype == torch.float32 else 2e-2)
 
 
-@pytest.mark.parametrize("dtype,n_layers,L0,T", [(torch.float32, 1, 64, 3), (torch.float32, 1, 45, 2),
-                                                  (torch.bfloat16, 1, 128, 2), (torch.float32, 3, 64, 2)])
-def test_model_decode_matches_reforward(dtype, n_layers, L0, T):
-    cfg, m = _cfg(dtype, n_layers=n_layers)
+@pytest.mark.parametrize("dtype,n_layers,L0,T,d_inner", [
+    (torch.float32, 1, 64, 3, 128), (torch.float32, 1, 45, 2, 128), (torch.bfloat16, 1, 128, 2, 128),
+    (torch.float32, 3, 64, 2, 128), (torch.float32, 1, 70, 3, 512), (torch.bfloat16, 1, 64, 2, 512),
+    (torch.bfloat16, 2, 40, 3, 512)])
+def test_model_decode_matches_reforward(dtype, n_layers, L0, T, d_inner):
+    """d_inner 128 (2 heads) takes the separate per-token kernels (the stacked gate / Q columns are not 16-byte
+    aligned); d_inner 512 (8 heads) the one-launch token kernel."""
+    cfg, m = _cfg(dtype, n_layers=n_layers, d_inner=d_inner)
     B = 2
     log(f"[model decode] {dtype} layers {n_layers} prompt {L0} steps {T}")
     g = torch.Generator().manual_seed(15)
@@ -183,3 +187,31 @@ def test_decode_graph_matches_eager(dtype, n_layers):
         # the graph advanced the same state as the eager steps
         assert torch.equal(c_graph[0]["l"], c_eager[0]["l"])
         assert rel(c_graph[-1]["scan"].state, c_eager[-1]["scan"].state) <= 1e-6
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fused_token_kernel_matches_separate_kernels(dtype):
+    """cdssm_decode_block_token against the separate per-token kernels on the same caches: equal logits and
+    scan state up to fp32 rounding (the fused kernel rounds where the separate kernels store; the compiler may
+    contract a multiply-add differently), 1e-5 fp32 / 2e-2 bf16 normwise."""
+    from cdssm_hip.lm import CDSSMBlock, _clone_cache
+    cfg, m = _cfg(dtype, n_layers=2, d_inner=512)
+    B, L0, T = 3, 66, 3
+    log(f"[fused token kernel] {dtype} prompt {L0} steps {T}")
+    g = torch.Generator().manual_seed(17)
+    ids = torch.randint(0, cfg.vocab_size, (B, L0 + T), generator=g).to(DEV)
+    with torch.no_grad():
+        _, ca = m.prefill(ids[:, :L0])
+        cb = [_clone_cache(c) for c in ca]
+        try:
+            for t in range(L0, L0 + T):
+                CDSSMBlock.fused_step = True
+                la = m.decode_step(ids[:, t], ca)
+                CDSSMBlock.fused_step = False
+                lb = m.decode_step(ids[:, t], cb)
+                e = rel(la, lb)
+                log(f"   token {t}: fused vs separate {e:.2e}")
+                assert e <= (1e-5 if dtype == torch.float32 else 2e-2)
+        finally:
+            CDSSMBlock.fused_step = True
+        assert rel(ca[-1]["scan"].state, cb[-1]["scan"].state) <= (1e-5 if dtype == torch.float32 else 2e-2)
