@@ -398,11 +398,11 @@ def conv1d_silu_step(x: Tensor, window: Tensor, weight: Tensor, bias: Tensor) ->
 
 
 def group_norm_gate_step(y: Tensor, gsum: Tensor, gamma: Tensor, beta: Tensor, eps: float, z: Tensor,
-                         x_conv: Tensor, D: Tensor) -> Tensor:
+                         x_conv: Tensor, D: Tensor, position: Optional[Tensor] = None) -> Tensor:
     """One decode token of the GroupNorm epilogue (block.py:215-225) with running statistics ``gsum``
     (B, G, 4) fp32 = (shift, sum (x - shift), sum (x - shift)^2, count) per (b, group) over every position
     so far (as ``group_norm_gate(..., return_sums=True)`` returns them), updated in place; y, x_conv (B, C);
-    z (B, C) with any row stride."""
+    z (B, C) with any row stride.  ``position`` (one int64 on the device) is incremented by the call."""
     Dp = D.to(y.dtype).contiguous()
     yc, xc = y.contiguous(), x_conv.contiguous()
     dt = _check_gpu("group_norm_gate_step", yc, z, xc, Dp)
@@ -419,7 +419,8 @@ def group_norm_gate_step(y: Tensor, gsum: Tensor, gamma: Tensor, beta: Tensor, e
     st = _lib.load().cdssm_group_norm_gate_step(_lib.DTYPE_CODE[dt], _lib.DTYPE_CODE[pdt], _lib.ptr(yc),
                                                _lib.ptr(gsum), _lib.ptr(g), _lib.ptr(b), _lib.ptr(z),
                                                z.stride(0) if B > 1 else C, _lib.ptr(xc), _lib.ptr(Dp),
-                                               _lib.ptr(out), B, C, G, float(eps), _lib.stream_of(y.device))
+                                               _lib.ptr(out), B, C, G, float(eps), _lib.ptr(position),
+                                               _lib.stream_of(y.device))
     _lib.check(st, "cdssm_group_norm_gate_step")
     return out
 
@@ -635,8 +636,7 @@ class CDSSMBlock(nn.Module):
         B = x.shape[0]
         y = self.readout_proj(retrieved.reshape(B, -1))
         y = group_norm_gate_step(y, cache["gsum"], self.ssm_norm.weight, self.ssm_norm.bias, self.ssm_norm.eps, z,
-                                 x_conv, self.D)
-        cache["l"].add_(1)
+                                 x_conv, self.D, position=cache["l"])  # also advances the position
         return torch.addmm(x, y, self.out_proj.weight.t())
 
 

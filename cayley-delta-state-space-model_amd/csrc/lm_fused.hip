@@ -337,8 +337,10 @@ __global__ __launch_bounds__(256) void gn_gate_step_kernel(const typename T::raw
                                                            const typename T::raw* __restrict__ xc,
                                                            const typename T::raw* __restrict__ Dp,
                                                            typename T::raw* __restrict__ out, int C, int G,
-                                                           float eps) {
+                                                           float eps, int64_t* __restrict__ position) {
   extern __shared__ float2 gst[];  // (mean, rstd) per group
+  // the layer's decode position advances with its last per-token kernel
+  if (position && blockIdx.x == 0 && threadIdx.x == 0) position[0] += 1;
   const int b = blockIdx.x;
   const int Cg = C / G;
   const typename T::raw* yr = y + int64_t(b) * C;
@@ -539,7 +541,7 @@ extern "C" int cdssm_group_norm_gate_fwd(int dtype, int param_dtype, const void*
 extern "C" int cdssm_group_norm_gate_step(int dtype, int param_dtype, const void* y, float* gsum, const void* gamma,
                                           const void* beta, const void* z, int64_t z_batch_stride, const void* x_conv,
                                           const void* Dp, void* out, int64_t B, int64_t C, int64_t G, float eps,
-                                          hipStream_t stream) {
+                                          int64_t* position, hipStream_t stream) {
   const char* op = "cdssm_group_norm_gate_step";
   return by_dtype(dtype, op, [&](auto t) -> int {
     using T = decltype(t);
@@ -565,7 +567,7 @@ extern "C" int cdssm_group_norm_gate_step(int dtype, int param_dtype, const void
                          stream, static_cast<const raw*>(y), reinterpret_cast<float4*>(gsum),
                          static_cast<const praw*>(gamma), static_cast<const praw*>(beta), static_cast<const raw*>(z),
                          z_batch_stride, static_cast<const raw*>(x_conv), static_cast<const raw*>(Dp),
-                         static_cast<raw*>(out), int(C), int(G), eps);
+                         static_cast<raw*>(out), int(C), int(G), eps, position);
     };
     if (param_dtype == 1)
       go(BF16{});

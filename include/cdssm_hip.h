@@ -391,12 +391,14 @@ int cdssm_conv1d_silu_step(int dtype, const void* x, int64_t x_batch_stride, voi
  * the token's y (B, C); then out = rnd(rnd(GN(y)) * rnd(silu(z))) + rnd(D x_conv)
  * as cdssm_group_norm_gate_fwd.  For the token this equals the GroupNorm of a
  * forward over the prefix plus the token (the reference's statistics span all
- * positions).  z with a row stride.  No reference counterpart.
+ * positions).  z with a row stride.  position (nullable): an int64 on the
+ * device incremented once by the call (the layer's decode position, read by
+ * the step's earlier kernels).  No reference counterpart.
  */
 int cdssm_group_norm_gate_step(int dtype, int param_dtype, const void* y, float* gsum, const void* gamma,
                                const void* beta, const void* z, int64_t z_batch_stride, const void* x_conv,
                                const void* D, void* out, int64_t B, int64_t C, int64_t G, float eps,
-                               hipStream_t stream);
+                               int64_t* position, hipStream_t stream);
 
 /*
  * One decode token of the model block's scan path in one launch, per (b, h):

@@ -148,7 +148,7 @@ _BLOCK_CALLS = {
     "cdssm_group_norm_gate_fwd": dict(dtype=1, pdt=1, y=16, g=16, b=16, z=16, zs=64, xc=16, D=16, out=16, ws=16,
                                       B=1, L=8, C=64, G=4, eps=1e-5, stream=None),
     "cdssm_group_norm_gate_step": dict(dtype=1, pdt=1, y=16, gsum=16, g=16, b=16, z=16, zs=64, xc=16, D=16,
-                                       out=16, B=2, C=64, G=4, eps=1e-5, stream=None),
+                                       out=16, B=2, C=64, G=4, eps=1e-5, position=None, stream=None),
     "cdssm_conv1d_silu_step": dict(dtype=1, x=16, xs=64, win=16, w=16, b=16, y=16, B=2, C=64, K=4, stream=None),
     "cdssm_conv1d_silu_bwd": dict(dtype=1, x=16, xs=64, w=16, b=16, go=16, gx=16, gw=16, gb=16, ws=16, B=1, L=8,
                                   C=64, K=4, stream=None),
