@@ -15,7 +15,10 @@
 
 namespace cdssm {
 
-constexpr int kConvTB = 16;  // tokens per thread
+#ifndef CDSSM_CONV_TB
+#define CDSSM_CONV_TB 8
+#endif
+constexpr int kConvTB = CDSSM_CONV_TB;  // tokens per thread
 
 // silu(u) = u sigmoid(u), with the hardware reciprocal (about 1 ulp)
 __device__ __forceinline__ float silu_f(float u) { return u * __builtin_amdgcn_rcpf(1.0f + __expf(-u)); }
@@ -309,7 +312,7 @@ extern "C" int cdssm_conv1d_silu_fwd_strided(int dtype, const void* x, int64_t x
   }
   if (B <= 0 || L <= 0 || C <= 0 || K < 1 || K > 8 || L > 0x7fffffffLL || C > 0x7fffffffLL ||
       B * ((L + kConvTB - 1) / kConvTB) * C >= (int64_t(1) << 31)) {
-    cdssm_host::set_error("%s: need B, L, C > 0, B * ceil(L/16) * C < 2^31 and 1 <= kernel_size <= 8 "
+    cdssm_host::set_error("%s: need B, L, C > 0, B * ceil(L/8) * C < 2^31 and 1 <= kernel_size <= 8 "
                           "(B=%lld L=%lld C=%lld K=%lld)", op,
                           (long long)B, (long long)L, (long long)C, (long long)K);
     return CDSSM_EINVAL;

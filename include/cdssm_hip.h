@@ -248,7 +248,7 @@ int cdssm_dynamics_fused_bwd(int dtype, const void* grad_A_bar, const void* grad
  * Conv1dSiLU, modules.py:14-35): causal depthwise conv + SiLU,
  *   y[b,t,c] = silu(bias[c] + sum_{j<K} w[c,j] x[b, t-(K-1)+j, c]), x = 0 before t = 0.
  * x, y (B,L,C); weight (C,1,K); bias (C); all `dtype` (the reference: bf16,
- * K = 4 only).  Supported: 1 <= K <= 8, B * ceil(L/16) * C < 2^31.  Backward:
+ * K = 4 only).  Supported: 1 <= K <= 8, B * ceil(L/8) * C < 2^31.  Backward:
  * cdssm_conv1d_silu_bwd.
  */
 int cdssm_conv1d_silu_fwd(int dtype, const void* x, const void* weight, const void* bias, void* y, int64_t B,
