@@ -254,7 +254,9 @@ int cdssm_dynamics_fused_bwd(int dtype, const void* grad_A_bar, const void* grad
 int cdssm_conv1d_silu_fwd(int dtype, const void* x, const void* weight, const void* bias, void* y, int64_t B,
                           int64_t L, int64_t C, int64_t K, hipStream_t stream);
 
-/* Bytes of the fp32 workspace cdssm_conv1d_silu_bwd needs (-1 if invalid). */
+/* Bytes of the fp32 workspace cdssm_conv1d_silu_bwd needs (-1 if invalid).  No reference counterpart: the
+ * reference's launcher allocates its gradient buffers itself (conv1d_silu.cu:296-305); this library never
+ * allocates. */
 int64_t cdssm_conv1d_silu_bwd_workspace_bytes(int64_t B, int64_t L, int64_t C, int64_t K);
 
 /*
@@ -316,7 +318,8 @@ int cdssm_normalize_kq_qk_fwd(int dtype, const void* K, int64_t k_token_stride, 
 int cdssm_shortcut_readout_fwd(int dtype, void* retrieved, const float* qk, const void* V, const void* vp,
                                const void* sel_c, const float* scale, int64_t n, hipStream_t stream);
 
-/* Bytes of the fp32 workspace cdssm_group_norm_gate_fwd needs (-1 if invalid). */
+/* Bytes of the fp32 workspace cdssm_group_norm_gate_fwd needs (-1 if invalid).  No reference counterpart:
+ * torch's group_norm allocates its statistics (block.py:216-223); this library never allocates. */
 int64_t cdssm_group_norm_workspace_bytes(int64_t B, int64_t G, int64_t L);
 
 /*
