@@ -255,7 +255,7 @@ int cdssm_conv1d_silu_fwd(int dtype, const void* x, const void* weight, const vo
                           int64_t L, int64_t C, int64_t K, hipStream_t stream);
 
 /* Bytes of the fp32 workspace cdssm_conv1d_silu_bwd needs (-1 if invalid).  No reference counterpart: the
- * reference's launcher allocates its gradient buffers itself (conv1d_silu.cu:296-305); this library never
+ * reference's launcher allocates its gradient buffers itself (conv1d_silu.cu:301-312); this library never
  * allocates. */
 int64_t cdssm_conv1d_silu_bwd_workspace_bytes(int64_t B, int64_t L, int64_t C, int64_t K);
 
