@@ -67,6 +67,8 @@ SIGNATURES = {
     "cdssm_conv1d_silu_step": (_I32, [_I32, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "cdssm_group_norm_gate_step": (_I32, [_I32, _I32, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _F32,
                                           _P, _P]),
+    "cdssm_readout_group_norm_gate_step": (_I32, [_I32, _I32, _P, _P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _I64,
+                                                  _I64, _I64, _F32, _P, _P]),
     "cdssm_intra_chunk_scan_fwd": (_I32, [_I32] + [_P] * 6 + [_I64] * 5 + [_P]),
     "cdssm_intra_chunk_scan_bwd": (_I32, [_I32] + [_P] * 12 + [_I64] * 5 + [_P]),
     "cdssm_inter_chunk_scan_fwd": (_I32, [_I32] + [_P] * 3 + [_I64] * 5 + [_P]),

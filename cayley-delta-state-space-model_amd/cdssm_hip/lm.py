@@ -398,15 +398,18 @@ def conv1d_silu_step(x: Tensor, window: Tensor, weight: Tensor, bias: Tensor) ->
 
 
 def group_norm_gate_step(y: Tensor, gsum: Tensor, gamma: Tensor, beta: Tensor, eps: float, z: Tensor,
-                         x_conv: Tensor, D: Tensor, position: Optional[Tensor] = None) -> Tensor:
+                         x_conv: Tensor, D: Tensor, position: Optional[Tensor] = None,
+                         readout_weight: Optional[Tensor] = None) -> Tensor:
     """One decode token of the GroupNorm epilogue (block.py:215-225) with running statistics ``gsum``
     (B, G, 4) fp32 = (shift, sum (x - shift), sum (x - shift)^2, count) per (b, group) over every position
     so far (as ``group_norm_gate(..., return_sums=True)`` returns them), updated in place; y, x_conv (B, C);
-    z (B, C) with any row stride.  ``position`` (one int64 on the device) is incremented by the call."""
+    z (B, C) with any row stride.  ``position`` (one int64 on the device) is incremented by the call.
+    With ``readout_weight`` (C, K), ``y`` is the retrieved readout (B, K) and the readout projection
+    y @ readout_weight^T (block.py:213) runs inside the kernel (cdssm_readout_group_norm_gate_step)."""
     Dp = D.to(y.dtype).contiguous()
     yc, xc = y.contiguous(), x_conv.contiguous()
     dt = _check_gpu("group_norm_gate_step", yc, z, xc, Dp)
-    B, C = yc.shape
+    B, C = xc.shape
     G = gsum.shape[1]
     if tuple(gsum.shape) != (B, G, 4) or gsum.dtype != torch.float32 or not gsum.is_contiguous():
         raise ValueError(f"gsum must be a contiguous float32 ({B}, G, 4) tensor")
@@ -415,7 +418,18 @@ def group_norm_gate_step(y: Tensor, gsum: Tensor, gamma: Tensor, beta: Tensor, e
     pdt = gamma.dtype if gamma.dtype in _lib.DTYPE_CODE else torch.float32
     g = gamma.detach().to(device=y.device, dtype=pdt).contiguous()
     b = beta.detach().to(device=y.device, dtype=pdt).contiguous()
-    out = torch.empty_like(yc)
+    out = torch.empty_like(xc)
+    if readout_weight is not None:
+        wr = readout_weight.detach().to(dt).contiguous()
+        if tuple(wr.shape) != (C, yc.shape[1]) or yc.shape[0] != B:
+            raise ValueError(f"readout_weight must be ({C}, {yc.shape[1]}) and y ({B}, {yc.shape[1]}), got "
+                             f"{tuple(wr.shape)} and {tuple(yc.shape)}")
+        st = _lib.load().cdssm_readout_group_norm_gate_step(
+            _lib.DTYPE_CODE[dt], _lib.DTYPE_CODE[pdt], _lib.ptr(yc), _lib.ptr(wr), yc.shape[1], _lib.ptr(gsum),
+            _lib.ptr(g), _lib.ptr(b), _lib.ptr(z), z.stride(0) if B > 1 else C, _lib.ptr(xc), _lib.ptr(Dp),
+            _lib.ptr(out), B, C, G, float(eps), _lib.ptr(position), _lib.stream_of(y.device))
+        _lib.check(st, "cdssm_readout_group_norm_gate_step")
+        return out
     st = _lib.load().cdssm_group_norm_gate_step(_lib.DTYPE_CODE[dt], _lib.DTYPE_CODE[pdt], _lib.ptr(yc),
                                                _lib.ptr(gsum), _lib.ptr(g), _lib.ptr(b), _lib.ptr(z),
                                                z.stride(0) if B > 1 else C, _lib.ptr(xc), _lib.ptr(Dp),
@@ -632,11 +646,12 @@ class CDSSMBlock(nn.Module):
         return self._step_tail(x, retrieved, z, x_conv, cache), v_first
 
     def _step_tail(self, x: Tensor, retrieved: Tensor, z: Tensor, x_conv: Tensor, cache: dict) -> Tensor:
-        """readout_proj, the GroupNorm step, out_proj + residual; advances the position."""
+        """readout_proj + the GroupNorm step (one kernel), out_proj + residual; advances the position."""
         B = x.shape[0]
-        y = self.readout_proj(retrieved.reshape(B, -1))
-        y = group_norm_gate_step(y, cache["gsum"], self.ssm_norm.weight, self.ssm_norm.bias, self.ssm_norm.eps, z,
-                                 x_conv, self.D, position=cache["l"])  # also advances the position
+        # readout_proj inside the GroupNorm step kernel; the kernel also advances the position
+        y = group_norm_gate_step(retrieved.reshape(B, -1), cache["gsum"], self.ssm_norm.weight, self.ssm_norm.bias,
+                                 self.ssm_norm.eps, z, x_conv, self.D, position=cache["l"],
+                                 readout_weight=self.readout_proj.weight)
         return torch.addmm(x, y, self.out_proj.weight.t())
 
 

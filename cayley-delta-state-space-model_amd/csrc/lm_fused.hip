@@ -330,6 +330,8 @@ __global__ __launch_bounds__(256) void gn_gate_kernel(const typename T::raw* __r
 // ---------------------------------------------------------------------------
 template <typename T, typename P>
 __global__ __launch_bounds__(256) void gn_gate_step_kernel(const typename T::raw* __restrict__ y,
+                                                           const typename T::raw* __restrict__ ret,
+                                                           const typename T::raw* __restrict__ wr, int kr,
                                                            float4* __restrict__ gsum,
                                                            const typename P::raw* __restrict__ gamma,
                                                            const typename P::raw* __restrict__ beta,
@@ -338,17 +340,47 @@ __global__ __launch_bounds__(256) void gn_gate_step_kernel(const typename T::raw
                                                            const typename T::raw* __restrict__ Dp,
                                                            typename T::raw* __restrict__ out, int C, int G,
                                                            float eps, int64_t* __restrict__ position) {
-  extern __shared__ float2 gst[];  // (mean, rstd) per group
+  // (mean, rstd) per group; with ret, the row's y (C values) and retrieved row (kr values) after them
+  extern __shared__ float2 gst[];
+  float* ys = reinterpret_cast<float*>(gst + G);
+  float* rs = ys + C;
   // the layer's decode position advances with its last per-token kernel
   if (position && blockIdx.x == 0 && threadIdx.x == 0) position[0] += 1;
   const int b = blockIdx.x;
   const int Cg = C / G;
   const typename T::raw* yr = y + int64_t(b) * C;
+  if (ret) {
+    // the readout projection of the row, rounded as the GEMM's output: y_c = rnd(sum_j ret_j W[c][j])
+    using raw = typename T::raw;
+    constexpr int E = 16 / int(sizeof(raw));  // elements per 16-byte load
+    const raw* rr = ret + int64_t(b) * kr;
+    for (int j = threadIdx.x; j < kr; j += blockDim.x) rs[j] = T::load(rr + j);
+    __syncthreads();
+    // W rows as 16-byte loads when every row starts on a 16-byte boundary
+    const bool vec = kr % E == 0 && (reinterpret_cast<uintptr_t>(wr) & 15u) == 0;
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+      const raw* wc = wr + int64_t(c) * kr;
+      float a = 0.0f;
+      if (vec) {
+        for (int j = 0; j < kr; j += E) {
+          const uint4 v = *reinterpret_cast<const uint4*>(wc + j);
+          const raw* e = reinterpret_cast<const raw*>(&v);
+#pragma unroll
+          for (int u = 0; u < E; ++u) a = fmaf(rs[j + u], T::load(e + u), a);
+        }
+      } else {
+        for (int j = 0; j < kr; ++j) a = fmaf(rs[j], T::load(wc + j), a);
+      }
+      ys[c] = rnd<T>(a);
+    }
+    __syncthreads();
+  }
+  auto yv = [&](int c) -> float { return ret ? ys[c] : T::load(yr + c); };
   for (int g = threadIdx.x; g < G; g += blockDim.x) {
     float4 a = gsum[int64_t(b) * G + g];
     float s1 = 0.0f, s2 = 0.0f;
     for (int c = 0; c < Cg; ++c) {
-      const float d = T::load(yr + g * Cg + c) - a.x;
+      const float d = yv(g * Cg + c) - a.x;
       s1 += d;
       s2 = fmaf(d, d, s2);
     }
@@ -362,7 +394,7 @@ __global__ __launch_bounds__(256) void gn_gate_step_kernel(const typename T::raw
   __syncthreads();
   for (int c = threadIdx.x; c < C; c += blockDim.x) {
     const float2 st = gst[c / Cg];
-    const float gn = rnd<T>(fmaf((T::load(yr + c) - st.x) * st.y, P::load(gamma + c), P::load(beta + c)));
+    const float gn = rnd<T>(fmaf((yv(c) - st.x) * st.y, P::load(gamma + c), P::load(beta + c)));
     const float s = rnd<T>(silu_fast(T::load(z + int64_t(b) * z_bs + c)));
     const float p = rnd<T>(gn * s);
     const float d = rnd<T>(T::load(Dp + c) * T::load(xc + int64_t(b) * C + c));
@@ -538,11 +570,10 @@ extern "C" int cdssm_group_norm_gate_fwd(int dtype, int param_dtype, const void*
   });
 }
 
-extern "C" int cdssm_group_norm_gate_step(int dtype, int param_dtype, const void* y, float* gsum, const void* gamma,
-                                          const void* beta, const void* z, int64_t z_batch_stride, const void* x_conv,
-                                          const void* Dp, void* out, int64_t B, int64_t C, int64_t G, float eps,
-                                          int64_t* position, hipStream_t stream) {
-  const char* op = "cdssm_group_norm_gate_step";
+static int gn_step(const char* op, int dtype, int param_dtype, const void* y, const void* ret, const void* wr,
+                   int64_t kr, float* gsum, const void* gamma, const void* beta, const void* z, int64_t z_batch_stride,
+                   const void* x_conv, const void* Dp, void* out, int64_t B, int64_t C, int64_t G, float eps,
+                   int64_t* position, hipStream_t stream) {
   return by_dtype(dtype, op, [&](auto t) -> int {
     using T = decltype(t);
     using raw = typename T::raw;
@@ -556,15 +587,22 @@ extern "C" int cdssm_group_norm_gate_step(int dtype, int param_dtype, const void
                             (long long)B, (long long)C, (long long)G);
       return CDSSM_EINVAL;
     }
-    if (!y || !gsum || !gamma || !beta || !z || !x_conv || !Dp || !out) {
+    if (ret && (kr <= 0 || kr > 4096 || (2 * G + C + kr) * int64_t(sizeof(float)) > 65536)) {
+      cdssm_host::set_error("%s: need 0 < readout width K <= 4096 and C + 2 G + K <= 16384 (K=%lld C=%lld G=%lld)", op,
+                            (long long)kr, (long long)C, (long long)G);
+      return CDSSM_EINVAL;
+    }
+    if (!(y || (ret && wr)) || !gsum || !gamma || !beta || !z || !x_conv || !Dp || !out) {
       cdssm_host::set_error("%s: null pointer argument", op);
       return CDSSM_EINVAL;
     }
     auto go = [&](auto pt) {
       using P = decltype(pt);
       using praw = typename P::raw;
-      hipLaunchKernelGGL((gn_gate_step_kernel<T, P>), dim3(unsigned(B)), dim3(256), size_t(G) * sizeof(float2),
-                         stream, static_cast<const raw*>(y), reinterpret_cast<float4*>(gsum),
+      const size_t lds = size_t(G) * sizeof(float2) + (ret ? size_t(C + kr) * sizeof(float) : 0);
+      hipLaunchKernelGGL((gn_gate_step_kernel<T, P>), dim3(unsigned(B)), dim3(256), lds, stream,
+                         static_cast<const raw*>(y), static_cast<const raw*>(ret), static_cast<const raw*>(wr),
+                         int(kr), reinterpret_cast<float4*>(gsum),
                          static_cast<const praw*>(gamma), static_cast<const praw*>(beta), static_cast<const raw*>(z),
                          z_batch_stride, static_cast<const raw*>(x_conv), static_cast<const raw*>(Dp),
                          static_cast<raw*>(out), int(C), int(G), eps, position);
@@ -575,4 +613,27 @@ extern "C" int cdssm_group_norm_gate_step(int dtype, int param_dtype, const void
       go(F32{});
     return cdssm_host::check_launch(op);
   });
+}
+
+extern "C" int cdssm_group_norm_gate_step(int dtype, int param_dtype, const void* y, float* gsum, const void* gamma,
+                                          const void* beta, const void* z, int64_t z_batch_stride, const void* x_conv,
+                                          const void* Dp, void* out, int64_t B, int64_t C, int64_t G, float eps,
+                                          int64_t* position, hipStream_t stream) {
+  return gn_step("cdssm_group_norm_gate_step", dtype, param_dtype, y, nullptr, nullptr, 0, gsum, gamma, beta, z,
+                 z_batch_stride, x_conv, Dp, out, B, C, G, eps, position, stream);
+}
+
+extern "C" int cdssm_readout_group_norm_gate_step(int dtype, int param_dtype, const void* retrieved,
+                                                  const void* readout_weight, int64_t K, float* gsum,
+                                                  const void* gamma, const void* beta, const void* z,
+                                                  int64_t z_batch_stride, const void* x_conv, const void* Dp,
+                                                  void* out, int64_t B, int64_t C, int64_t G, float eps,
+                                                  int64_t* position, hipStream_t stream) {
+  const char* op = "cdssm_readout_group_norm_gate_step";
+  if (!retrieved || !readout_weight) {
+    cdssm_host::set_error("%s: null pointer argument", op);
+    return CDSSM_EINVAL;
+  }
+  return gn_step(op, dtype, param_dtype, nullptr, retrieved, readout_weight, K, gsum, gamma, beta, z, z_batch_stride,
+                 x_conv, Dp, out, B, C, G, eps, position, stream);
 }

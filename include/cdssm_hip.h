@@ -404,6 +404,20 @@ int cdssm_group_norm_gate_step(int dtype, int param_dtype, const void* y, float*
                                int64_t* position, hipStream_t stream);
 
 /*
+ * cdssm_group_norm_gate_step with the block's readout projection
+ * (block.py:213, readout_proj: nn.Linear(H N, C, bias=False)) folded in: y of
+ * each row is computed in the kernel as rnd(retrieved (B, K) . W (C, K)^T),
+ * rounded to the dtype as the projection's output is, and never written.
+ * retrieved and readout_weight dense, in the activation dtype; K <= 4096,
+ * C + 2 G + K <= 16384.  No reference counterpart (one decode launch fewer).
+ */
+int cdssm_readout_group_norm_gate_step(int dtype, int param_dtype, const void* retrieved, const void* readout_weight,
+                                       int64_t K, float* gsum, const void* gamma, const void* beta, const void* z,
+                                       int64_t z_batch_stride, const void* x_conv, const void* Dp, void* out,
+                                       int64_t B, int64_t C, int64_t G, float eps, int64_t* position,
+                                       hipStream_t stream);
+
+/*
  * One decode token of the model block's scan path in one launch, per (b, h):
  * the gate-level dynamics at the device-held position (as
  * cdssm_dynamics_fused_fwd_at), K/Q normalisation and q.k (as

@@ -136,6 +136,35 @@ def test_group_norm_step_matches_forward(dtype):
         assert e <= (1e-5 if dtype == torch.float32 else 2e-2)
 
 
+@pytest.mark.parametrize("dtype,B,K,C,G", [(torch.float32, 3, 32, 128, 32), (torch.bfloat16, 64, 32, 1024, 32),
+                                        (torch.bfloat16, 2, 48, 96, 3)])
+def test_readout_group_norm_step_matches_separate(dtype, B, K, C, G):
+    """cdssm_readout_group_norm_gate_step (the readout projection in the GroupNorm step kernel) against the
+    projection as one fp32-accumulated product rounded to the dtype (as a GEMM's output) followed by
+    cdssm_group_norm_gate_step; both the outputs and the updated running sums."""
+    from cdssm_hip.lm import group_norm_gate_step
+    log(f"[readout + group norm step] {dtype} B{B} K{K} C{C} G{G}")
+    g = torch.Generator().manual_seed(15)
+    f32 = dict(generator=g, dtype=torch.float32)
+    r = torch.randn(B, K, **f32).to(dtype).to(DEV)
+    W = (torch.randn(C, K, **f32) / K ** 0.5).to(dtype).to(DEV)
+    z = torch.randn(B, C + 8, **f32).to(dtype).to(DEV)[:, 8:]
+    xc = torch.randn(B, C, **f32).to(dtype).to(DEV)
+    gamma = (1 + 0.2 * torch.randn(C, **f32)).to(DEV)
+    beta = (0.1 * torch.randn(C, **f32)).to(DEV)
+    Dp = (0.3 * torch.randn(C, **f32)).to(dtype).to(DEV)
+    gs0 = torch.cat([torch.randn(B, G, 1, **f32), torch.randn(B, G, 1, **f32) * 3,
+                     torch.rand(B, G, 1, **f32) * 50 + 20, torch.full((B, G, 1), 40.0)], -1).to(DEV)
+    gs_a, gs_b = gs0.clone(), gs0.clone()
+    y = (r.float() @ W.float().t()).to(dtype)
+    ref = group_norm_gate_step(y, gs_a, gamma, beta, 1e-5, z, xc, Dp)
+    out = group_norm_gate_step(r, gs_b, gamma, beta, 1e-5, z, xc, Dp, readout_weight=W)
+    e, es = rel(out, ref), rel(gs_b, gs_a)
+    log(f"   rel err out {e:.2e} running sums {es:.2e}")
+    assert out.shape == (B, C) and e <= (1e-5 if dtype == torch.float32 else 2e-2)
+    assert es <= (1e-5 if dtype == torch.float32 else 1e-3)
+
+
 @pytest.mark.parametrize("dtype,n_layers,L0,T,d_inner", [
     (torch.float32, 1, 64, 3, 128), (torch.float32, 1, 45, 2, 128), (torch.bfloat16, 1, 128, 2, 128),
     (torch.float32, 3, 64, 2, 128), (torch.float32, 1, 70, 3, 512), (torch.bfloat16, 1, 64, 2, 512),
