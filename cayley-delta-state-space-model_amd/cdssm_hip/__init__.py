@@ -5,8 +5,9 @@ reference-compatible autograd Functions.  Importing this package does not
 touch the GPU; the library is loaded on first use and its absence is an error.
 """
 
-from .scan import (ChunkwiseDeltaScanFn, chunkwise_delta_scan, chunkwise_delta_scan_bwd,  # noqa: F401
-                   chunkwise_delta_scan_fwd, chunkwise_delta_scan_train, set_forward_path)
+from .scan import (ChunkwiseDeltaScanFn, check_lookback, chunkwise_delta_scan,  # noqa: F401
+                   chunkwise_delta_scan_bwd, chunkwise_delta_scan_fwd, chunkwise_delta_scan_train,
+                   lookback_status, set_forward_path)
 
 from .ops import (DynamicsFusedFn, ExactCorrectionFn, InterChunkScanFn,  # noqa: F401
                   IntraChunkScanFn, NormalizeKQFn)
@@ -15,5 +16,6 @@ from .decode import DecodeState, decode_step, prefill  # noqa: F401
 
 __all__ = ["DynamicsFusedFn", "NormalizeKQFn", "IntraChunkScanFn", "InterChunkScanFn", "ExactCorrectionFn",
            "SSDChunkwiseScan", "ChunkwiseDeltaScanFn", "chunkwise_delta_scan", "chunkwise_delta_scan_fwd",
-           "chunkwise_delta_scan_bwd", "chunkwise_delta_scan_train", "set_forward_path", "DecodeState",
+           "chunkwise_delta_scan_bwd", "chunkwise_delta_scan_train", "set_forward_path", "lookback_status",
+           "check_lookback", "DecodeState",
            "decode_step", "prefill"]

@@ -31,6 +31,7 @@ _F32 = ctypes.c_float
 SIGNATURES = {
     "cdssm_abi_version": (_I32, []),
     "cdssm_fused_scan_fwd_set_path": (_I32, [_I32]),
+    "cdssm_lookback_status": (_I32, [_I32, _P]),
     "cdssm_last_error": (ctypes.c_char_p, []),
     "cdssm_fused_scan_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "cdssm_fused_scan_fwd": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _P,

@@ -153,6 +153,32 @@ def set_forward_path(path: str) -> str:
     return {v: n for n, v in FORWARD_PATHS.items()}[prev]
 
 
+LOOKBACK_BITS = {1: "forward one-pass", 2: "backward correction adjoint + carry"}
+
+
+def lookback_status(clear: bool = True) -> int:
+    """Sticky look-back status of the current device (cdssm_lookback_status).
+
+    0 means no look-back wait of a one-launch pass has timed out since the last
+    clear; bit 0 (1) marks the forward, bit 1 (2) the backward.  A timed-out
+    wait writes NaN states, so the affected outputs are NaN as well.
+    Synchronises with the device; do not call it while capturing a graph.
+    """
+    out = ctypes.c_int(0)
+    st = _lib.load().cdssm_lookback_status(1 if clear else 0, ctypes.byref(out))
+    _lib.check(st, "cdssm_lookback_status")
+    return int(out.value)
+
+
+def check_lookback(clear: bool = True) -> None:
+    """Raise RuntimeError if a look-back wait of a one-launch pass has timed out."""
+    bits = lookback_status(clear)
+    if bits:
+        which = ", ".join(n for b, n in LOOKBACK_BITS.items() if bits & b)
+        raise RuntimeError(f"look-back wait timed out in the {which} (status {bits}): the workgroups of a "
+                           f"one-launch pass were not all resident at once; the affected outputs are NaN")
+
+
 def chunkwise_delta_scan(q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0=None, chunk_size=None):
     """y (B,L,H,2) and the final R-mode state (B,H,2,D) of the fused scan."""
     y, h_final, _ = chunkwise_delta_scan_fwd(q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0, chunk_size)

@@ -341,6 +341,7 @@ __device__ __forceinline__ void load_zck(const float2* base, int64_t idx, float2
 
 constexpr int kSegLen = 16;   // chunks per forward carry segment
 constexpr int kOnePassW = 4;  // chunks (waves) per workgroup of the one-pass forward
+constexpr int kCtlWords = 8;  // 8-byte words of a look-back area's control block
 constexpr int kZck = 4;       // token interval of the z checkpoints
 constexpr int kTokRound = 8;  // token loops run to round_up(tokens, kTokRound)
 
@@ -369,7 +370,7 @@ inline FwdLayout fwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t 
   w.n_saved = 4 * B * L * H;
   w.n_gsaved = B * L * H;
   w.NSEG = (w.NC + kOnePassW - 1) / kOnePassW;
-  w.n_op = B * w.NSEG * H * (2 * D + 2);
+  w.n_op = B * w.NSEG * H * (2 * D + 2) + kCtlWords;
   // checkpoints at t = 0, kZck, ... < round_up(chunk, kTokRound)
   w.NCK = int((chunk + kTokRound - 1) / kTokRound * kTokRound / kZck);
   w.n_zck = B * w.NC * H * int64_t(w.NCK) * D;
@@ -424,13 +425,33 @@ constexpr int kAnchor = 63;  // segments folded from one anchor state (<= 63: on
 constexpr uint64_t kSpinTicks = 5000000;  // look-back wait bound: 50 ms of the 100 MHz real-time counter
 
 // Look-back area of a one-launch pass: per (b, segment, head) a map (D
-// complex + one complex scalar), a state (D complex) and an 8-byte flag.
+// complex + one complex scalar), a state (D complex) and an 8-byte flag, then
+// a control block of kCtlWords 8-byte words whose first word is the call's
+// epoch.  The area is never cleared: a flag counts only when its upper bits
+// equal the epoch of the running call, which a one-thread kernel launched
+// just before the pass draws from a device-side counter and writes into the
+// control block.  Drawing it on the device keeps a captured HIP graph correct:
+// every replay runs the epoch kernel again and gets a new epoch.
 struct OnePassBufs {
   float2* seg_f;             // (B, NSEG, H, D) segment map F: state at the segment's end from zero
   float2* seg_s;             // (B, NSEG, H, D) state leaving the segment
   float2* seg_g;             // (B, NSEG, H)    segment rotation product
   unsigned long long* flag;  // (B, NSEG, H); entry hbase serves the head group
+  unsigned long long* ctl;   // kCtlWords words; ctl[0] = epoch of the running call
 };
+
+// Epoch words: the pass's tag in bits 58..59 (so epochs of different passes
+// never match each other's flags, should their areas share memory over time)
+// and the count of calls so far in bits 0..57.  A flag word is epoch << 2 | state.
+__device__ __forceinline__ unsigned long long epoch_word(unsigned tag, unsigned long long n) {
+  return (static_cast<unsigned long long>(tag) << 58) | (n & ((1ull << 58) - 1ull));
+}
+__device__ __forceinline__ unsigned long long load_epoch(const unsigned long long* ctl) {
+  return __hip_atomic_load(const_cast<unsigned long long*>(ctl), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Bits of the sticky look-back status word (cdssm_lookback_status).
+constexpr unsigned kTimeoutFwd = 1u;  // a one-pass forward wait timed out (NaN states were written)
+constexpr unsigned kTimeoutBwd = 2u;  // a one-launch backward carry wait timed out
 
 // Wait until this wave's earlier stores are acknowledged; also a compiler
 // barrier, so no memory access moves across it.
@@ -455,9 +476,11 @@ __device__ __forceinline__ float2 ld_agent(const float2* p) {
 namespace cdssm_host {
 void set_error(const char* fmt, ...);
 int check_launch(const char* op);
-// Look-back epochs: distinct per call and process (62 bits, never 0), started
-// from a clock-mixed value so flag words left in a reused buffer never match.
-unsigned long long next_epoch();
+// Sticky look-back timeout words of the forward and backward units (bits
+// kTimeoutFwd / kTimeoutBwd) on the current device; `clear` resets them.
+// Synchronous (device-to-host copies).
+int fwd_lookback_status(bool clear, unsigned* out);
+int bwd_lookback_status(bool clear, unsigned* out);
 // Workgroups of kernel `fn` (block threads, lds bytes of dynamic LDS) resident
 // on the current device at once; 0 if it cannot run.  Cached.
 int resident_capacity(const void* fn, int block, size_t lds);

@@ -491,8 +491,24 @@ __global__ __launch_bounds__(256) void fused_bwd_rreplay_kernel(
 // since its anchor (kAnchor segments, counted from the right) applied to the
 // anchor state (d h_final, or the published left-end state of the segment
 // right of the anchor); each wave then writes d s_{k+1} of its chunk, and the
-// first segment writes d h0.  Flags and ordering as in the one-pass forward.
+// first segment writes d h0.  Flags and ordering as in the one-pass forward;
+// the epoch comes from bwd_epoch_kernel, launched just before on the same
+// stream, and a wait that gives up sets kTimeoutBwd in g_bwd_status.
 // ---------------------------------------------------------------------------
+
+// Device-side state of this unit's one-launch carry, one copy per GPU: the
+// count of calls (the source of their epochs, tagged apart from the forward's)
+// and the sticky status word.
+__device__ unsigned long long g_bwd_calls;
+__device__ unsigned int g_bwd_status;
+
+__global__ __launch_bounds__(64) void bwd_epoch_kernel(unsigned long long* ctl) {
+  if (threadIdx.x == 0) {
+    const unsigned long long n =
+        __hip_atomic_fetch_add(&g_bwd_calls, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1ull;
+    __hip_atomic_store(ctl, epoch_word(2u, n), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
 template <typename T>
 struct CorrCarryArgs {
   const typename T::raw *q, *k, *beta, *sel_c, *dy;
@@ -501,8 +517,7 @@ struct CorrCarryArgs {
   const float* dh_final;  // (B, H, 2, D) or null
   float2* dsn;            // out: d s_{k+1} per chunk (B, NC, H, D)
   float* dh0;             // out: (B, H, 2, D) or null
-  OnePassBufs ob;         // X in seg_f, A in seg_g, left-end states in seg_s
-  unsigned long long epoch;
+  OnePassBufs ob;         // X in seg_f, A in seg_g, left-end states in seg_s; epoch in ctl[0]
   int L, H, Q, NC, NSEG, n_hg, n_chain;
 };
 
@@ -515,7 +530,7 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
   static_assert(EPT >= 1 && EPT * kWave * W == SEGN && D % EPT == 0, "segment state tiles the workgroup");
   extern __shared__ float4 smem4[];
   const int L = a.L, H = a.H, Q = a.Q, NC = a.NC, NSEG = a.NSEG;
-  const unsigned long long epoch = a.epoch;
+  const unsigned long long epoch = load_epoch(a.ob.ctl);
 
   const int wv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
   const int lane = int(threadIdx.x) % kWave;
@@ -682,7 +697,10 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
         if (__builtin_amdgcn_s_memrealtime() - t_start > kSpinTicks) break;
         __builtin_amdgcn_s_sleep(2);
       }
-      if (lane == 0) ctrl[0] = got;
+      if (lane == 0) {
+        ctrl[0] = got;
+        if (!got) __hip_atomic_fetch_or(&g_bwd_status, kTimeoutBwd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     __syncthreads();
     ok = ctrl[0];
@@ -1162,7 +1180,7 @@ BwdLayout bwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) 
   // one-launch correction adjoint + reverse carry: look-back area per (b,
   // segment of kOnePassW chunks, h): map X (D), left-end state (D), A, flag
   w.NSEG = (w.NC + kOnePassW - 1) / kOnePassW;
-  w.n_cc = B * w.NSEG * H * (2 * D + 2);
+  w.n_cc = B * w.NSEG * H * (2 * D + 2) + kCtlWords;
   return w;
 }
 
@@ -1224,8 +1242,8 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
       a.dh_final = dh_final;
       a.dsn = dsn;
       a.dh0 = dh0;
-      a.ob = OnePassBufs{base, base + nsd, base + 2 * nsd, reinterpret_cast<unsigned long long*>(base + 2 * nsd + nsh)};
-      a.epoch = cdssm_host::next_epoch();
+      unsigned long long* flags = reinterpret_cast<unsigned long long*>(base + 2 * nsd + nsh);
+      a.ob = OnePassBufs{base, base + nsd, base + 2 * nsd, flags, flags + nsh};
       a.L = L;
       a.H = H;
       a.Q = Q;
@@ -1233,6 +1251,9 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
       a.NSEG = w.NSEG;
       a.n_hg = n_hgc;
       a.n_chain = B * n_hgc;
+      hipLaunchKernelGGL(bwd_epoch_kernel, dim3(1), dim3(64), 0, stream, a.ob.ctl);
+      st = cdssm_host::check_launch("cdssm_fused_scan_bwd/epoch");
+      if (st) return st;
       if (ev) (void)hipEventRecord(ev[0], stream);
       hipLaunchKernelGGL((fused_bwd_corrcarry_kernel<T, D>), dim3(unsigned(items)), dim3(kWave * kOnePassW), lds,
                          stream, a);
@@ -1284,6 +1305,26 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
 }
 
 }  // namespace
+
+int cdssm_host::bwd_lookback_status(bool clear, unsigned* out) {
+  unsigned v = 0;
+  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(cdssm::g_bwd_status), sizeof(v), 0, hipMemcpyDeviceToHost) != hipSuccess) {
+    cdssm_host::set_error("cdssm_lookback_status: reading the backward status word failed: %s",
+                          hipGetErrorString(hipGetLastError()));
+    return CDSSM_EHIP;
+  }
+  if (clear && v) {
+    const unsigned zero = 0;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(cdssm::g_bwd_status), &zero, sizeof(zero), 0, hipMemcpyHostToDevice) !=
+        hipSuccess) {
+      cdssm_host::set_error("cdssm_lookback_status: clearing the backward status word failed: %s",
+                            hipGetErrorString(hipGetLastError()));
+      return CDSSM_EHIP;
+    }
+  }
+  *out = v;
+  return CDSSM_OK;
+}
 
 extern "C" int64_t cdssm_fused_scan_bwd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t D,
                                                         int64_t N, int64_t chunk) {

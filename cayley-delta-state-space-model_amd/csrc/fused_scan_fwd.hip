@@ -47,6 +47,21 @@ namespace cdssm {
 
 constexpr int kPrefetch = 8;
 
+// Device-side state of this unit's one-pass forward, one copy per GPU:
+// the count of one-pass calls (the source of their look-back epochs) and the
+// sticky status word (kTimeoutFwd once a look-back wait gave up).
+__device__ unsigned long long g_fwd_calls;
+__device__ unsigned int g_fwd_status;
+
+// One thread: draw the next forward epoch into the control block.
+__global__ __launch_bounds__(64) void fwd_epoch_kernel(unsigned long long* ctl) {
+  if (threadIdx.x == 0) {
+    const unsigned long long n =
+        __hip_atomic_fetch_add(&g_fwd_calls, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1ull;
+    __hip_atomic_store(ctl, epoch_word(1u, n), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // Lanes per head of the bf16 D = 64 forward (8: one 16-byte row slice per
 // lane; 16 or 32: more waves per SIMD at smaller slices).
 #ifndef CDSSM_FWD_LPH_BF16_D64
@@ -751,7 +766,10 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
 // entering every chunk and G_k (the four-launch layout), the per-token records
 // (p_t, pc_t), (c^_{t+1}.q_t, Y_t.q_t) and g_t, as the main pass does.
 // Flags hold epoch << 2 | state (1: map, 2: map and leaving state) with a
-// per-call epoch, so the workspace needs no clearing between calls.  Published
+// per-call epoch read from the look-back area's control block, where
+// fwd_epoch_kernel (launched just before, on the same stream) writes it from a
+// device-side counter; so the workspace needs no clearing between calls and a
+// captured HIP graph draws a new epoch on every replay.  Published
 // data and flags are written and read with agent-scope atomics (stores written
 // through to the device-coherent level, loads served from it), so no cache
 // maintenance is needed: a writer waits until its data stores are acknowledged
@@ -761,7 +779,8 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
 // the correction pass re-reads).  A workgroup waits only on segments of lower
 // index; the launcher sizes the grid to the workgroups resident at once (one
 // per segment, or fewer that take the segments in order), and a bounded wait
-// turns a missing flag into NaN output instead of a hang.
+// turns a missing flag into NaN output instead of a hang, and sets the
+// kTimeoutFwd bit of the sticky status word g_fwd_status.
 // ---------------------------------------------------------------------------
 template <typename T>
 struct OnePassArgs {
@@ -778,7 +797,6 @@ struct OnePassArgs {
   float2* gsaved;  // SAVE: g_t (B, L, H)
   float2* zck;     // SAVE: z_{t-1} at t % kZck == 0 (B, NC, H, NCK, D)
   float2* cend;    // SAVE: c^ after the chunk's last step (B, NC, H, D)
-  unsigned long long epoch;
   int L, H, Q, NC, NSEG, NCK, n_hg, n_chain, n_items;
 };
 
@@ -805,7 +823,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   float2* __restrict__ gsaved = a.gsaved;
   float2* __restrict__ zck = a.zck;
   float2* __restrict__ cend = a.cend;
-  const unsigned long long epoch = a.epoch;
+  const unsigned long long epoch = load_epoch(a.ob.ctl);
   const int L = a.L, H = a.H, Q = a.Q, NC = a.NC, NSEG = a.NSEG, n_hg = a.n_hg;
   using Cfg = FusedCfg<T, D, LPH>;
   constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch, W = kOnePassW;
@@ -1017,7 +1035,10 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
         if (__builtin_amdgcn_s_memrealtime() - t_start > kSpinTicks) break;
         __builtin_amdgcn_s_sleep(2);
       }
-      if (lane == 0) ctrl[0] = got;
+      if (lane == 0) {
+        ctrl[0] = got;
+        if (!got) __hip_atomic_fetch_or(&g_fwd_status, kTimeoutFwd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     __syncthreads();
     ok = ctrl[0];
@@ -1313,15 +1334,14 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
       a.h0 = h0;
       a.y = (raw*)y;
       a.h_final = h_final;
-      a.ob = OnePassBufs{base, base + nsd, base + 2 * nsd,
-                         reinterpret_cast<unsigned long long*>(base + 2 * nsd + nsh)};
+      unsigned long long* flags = reinterpret_cast<unsigned long long*>(base + 2 * nsd + nsh);
+      a.ob = OnePassBufs{base, base + nsd, base + 2 * nsd, flags, flags + nsh};
       a.states = save ? summ : nullptr;
       a.gam = save ? gam : nullptr;
       a.saved = save ? saved : nullptr;
       a.gsaved = save ? gsaved : nullptr;
       a.zck = save ? zck : nullptr;
       a.cend = save ? cend : nullptr;
-      a.epoch = cdssm_host::next_epoch();
       a.L = L;
       a.H = H;
       a.Q = Q;
@@ -1332,6 +1352,9 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
       a.n_chain = B * n_hg;
       a.n_items = int(items);
       if (path) *path = cdssm_host::kPathOne;
+      hipLaunchKernelGGL(fwd_epoch_kernel, dim3(1), dim3(64), 0, stream, a.ob.ctl);
+      const int est = cdssm_host::check_launch("cdssm_fused_scan_fwd/epoch");
+      if (est) return est;
       if (ev)
         for (int i = 0; i < 4; ++i) (void)hipEventRecord(ev[i], stream);
       const dim3 gd = dim3(unsigned(grid)), bd = dim3(kWave * kOnePassW);
@@ -1396,6 +1419,26 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
+
+int cdssm_host::fwd_lookback_status(bool clear, unsigned* out) {
+  unsigned v = 0;
+  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(cdssm::g_fwd_status), sizeof(v), 0, hipMemcpyDeviceToHost) != hipSuccess) {
+    cdssm_host::set_error("cdssm_lookback_status: reading the forward status word failed: %s",
+                          hipGetErrorString(hipGetLastError()));
+    return CDSSM_EHIP;
+  }
+  if (clear && v) {
+    const unsigned zero = 0;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(cdssm::g_fwd_status), &zero, sizeof(zero), 0, hipMemcpyHostToDevice) !=
+        hipSuccess) {
+      cdssm_host::set_error("cdssm_lookback_status: clearing the forward status word failed: %s",
+                            hipGetErrorString(hipGetLastError()));
+      return CDSSM_EHIP;
+    }
+  }
+  *out = v;
+  return CDSSM_OK;
+}
 
 extern "C" int64_t cdssm_fused_scan_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t D,
                                                     int64_t N, int64_t chunk) {

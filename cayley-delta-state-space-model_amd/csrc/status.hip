@@ -4,7 +4,6 @@
 #include <stdio.h>
 
 #include <atomic>
-#include <chrono>
 #include <mutex>
 
 #include "common.hpp"
@@ -29,16 +28,6 @@ int check_launch(const char* op) {
     return CDSSM_EHIP;
   }
   return CDSSM_OK;
-}
-
-unsigned long long next_epoch() {
-  static std::atomic<unsigned long long> ctr{
-      (unsigned long long)(std::chrono::steady_clock::now().time_since_epoch().count()) * 0x9E3779B97F4A7C15ull};
-  unsigned long long e;
-  do {
-    e = ctr.fetch_add(1, std::memory_order_relaxed) & ((1ull << 62) - 1);
-  } while (e == 0);
-  return e;
 }
 
 int resident_capacity(const void* fn, int block, size_t lds) {
@@ -86,6 +75,20 @@ extern "C" int cdssm_fused_scan_fwd_set_path(int mode) {
   return cdssm_host::g_scan_path.exchange(mode);
 }
 
+extern "C" int cdssm_lookback_status(int clear, int* status) {
+  if (!status) {
+    cdssm_host::set_error("cdssm_lookback_status: status must not be NULL");
+    return CDSSM_EINVAL;
+  }
+  unsigned f = 0, b = 0;
+  int st = cdssm_host::fwd_lookback_status(clear != 0, &f);
+  if (st) return st;
+  st = cdssm_host::bwd_lookback_status(clear != 0, &b);
+  if (st) return st;
+  *status = int((f & cdssm::kTimeoutFwd) | (b & cdssm::kTimeoutBwd));
+  return CDSSM_OK;
+}
+
 extern "C" const char* cdssm_last_error(void) { return g_err; }
 
-extern "C" int cdssm_abi_version(void) { return 1; }
+extern "C" int cdssm_abi_version(void) { return 2; }

@@ -153,6 +153,25 @@ int cdssm_fused_scan_bwd_profile(int dtype, const void* q, const void* k, const 
 int cdssm_fused_scan_fwd_set_path(int mode);
 
 /*
+ * Look-back health (no counterpart in the reference, whose inter-chunk pass is
+ * a separate serial launch, inter_chunk_scan.cu:201-234).  The one-launch
+ * forward and the backward's one-launch correction adjoint + carry pass chunk
+ * summaries between workgroups through flags; a wait for a flag is bounded
+ * (50 ms) and, if it gives up, the affected states are written as NaN and a
+ * sticky bit is set on the device: bit 0 (1) for the forward, bit 1 (2) for
+ * the backward.  This call stores the bits of the current device in *status
+ * (0: no wait has timed out) and, if clear != 0, resets them.  It synchronises
+ * with the device (device-to-host copies), so it must not be called while the
+ * stream is being captured into a graph.
+ *
+ * The one-launch passes draw their flag epoch on the device: a one-thread
+ * kernel launched on the same stream just before the pass writes a fresh
+ * epoch from a per-device counter into the workspace, so the workspace needs
+ * no clearing between calls and a captured graph stays correct on every replay.
+ */
+int cdssm_lookback_status(int clear, int* status);
+
+/*
  * Recurrent decode: one new token per (b, h) with the R-mode state carried
  * between calls.  No reference counterpart: the reference generates by
  * re-running the whole forward for every new token (predict.py:53-67, through

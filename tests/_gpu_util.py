@@ -71,3 +71,33 @@ def oracle_fwd(x: dict, chunk_size=None):
     d = {n: (t.double() if isinstance(t, torch.Tensor) else t) for n, t in x.items()}
     return o.fused_scan(d["q"], d["k"], d["v"], d["beta"], d["sel_C"], d["dt"], d["r"], d["alpha"],
                         d["omega"], d["c"], h0=d.get("h0"), chunk_size=chunk_size)
+
+
+GRAD_NAMES = ("q", "k", "v", "beta", "sel_C", "dt", "r", "alpha", "omega")
+
+
+def oracle_grads(x: dict, gy: torch.Tensor, gh: torch.Tensor, chunk_size=None) -> dict:
+    """Reference-mode gradients of sum(y * gy) + sum(h_final * gh) from the fp64 oracle
+    (autograd through the restatement, with the reference's correction-pass backward)."""
+    d = {n: (x[n].double().clone().requires_grad_(True)) for n in GRAD_NAMES}
+    h0 = x.get("h0")
+    h0d = h0.double().clone().requires_grad_(True) if h0 is not None else None
+    y, hf = o.fused_scan(*[d[n] for n in GRAD_NAMES], x["c"], h0=h0d, chunk_size=chunk_size,
+                         grad_mode="reference")
+    loss = (y * gy.double()).sum() + (hf * gh.double()).sum()
+    wrt = [d[n] for n in GRAD_NAMES] + ([h0d] if h0d is not None else [])
+    gs = torch.autograd.grad(loss, wrt)
+    out = dict(zip(GRAD_NAMES, gs[:9]))
+    if h0d is not None:
+        out["h0"] = gs[9]
+    return out
+
+
+def cotangents(cfg, seed: int = 7):
+    """Seeded (dy, dh_final) for a config; dy rounded to bf16 for bf16 configs."""
+    gen = torch.Generator().manual_seed(seed)
+    gy = torch.randn(cfg.B, cfg.L, cfg.H, cfg.N, generator=gen)
+    gh = torch.randn(cfg.B, cfg.H, cfg.N, cfg.D, generator=gen)
+    if cfg.dtype == "bf16":
+        gy = gy.bfloat16().float()
+    return gy, gh

@@ -77,6 +77,28 @@ def test_fused_bwd_rejects_rows_beyond_32_bit_offsets_without_launching():
     assert "32-bit row offsets" in _lib.last_error()
 
 
+def test_lookback_status_rejects_a_null_status_pointer_without_touching_the_gpu():
+    lib = _lib.load()
+    assert lib.cdssm_lookback_status(1, None) == -1
+    assert "status must not be NULL" in _lib.last_error()
+
+
+def test_one_launch_areas_have_a_control_block_for_the_device_epoch():
+    """The workspaces end their look-back areas with the 64-byte control block the
+    epoch kernel writes (8 float2 words more than the flags and maps need)."""
+    lib = _lib.load()
+    B, L, H, D, Q = 2, 1000, 3, 64, 64
+    NC = -(-L // Q)
+    S = -(-NC // 16)
+    NSEG = -(-NC // 4)
+    NCK = -(-Q // 8) * 8 // 4
+    carry = B * NC * H * D + B * NC * H + B * H * S * (D + 1)
+    fwd = carry + (carry & 1) + 5 * B * L * H + B * NSEG * H * (2 * D + 2) + 8 + B * NC * H * NCK * D + B * NC * H * D
+    assert lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, 2, Q) == 8 * fwd
+    bwd = 2 * B * NC * H * D + B * H * S + B * H * S * D + B * NC * H + B * NSEG * H * (2 * D + 2) + 8
+    assert lib.cdssm_fused_scan_bwd_workspace_bytes(B, L, H, D, 2, Q) == 8 * bwd
+
+
 def _decode_call(lib, **over):
     args = dict(dtype=1, q=16, k=16, v=16, beta=16, sel_c=16, dt=16, r=16, alpha=16, omega=16, c=1.0,
                 state=16, gam=16, pos=16, y=16, h_out=None, B=2, H=3, D=64, N=2, chunk=64, stream=None)
@@ -118,7 +140,7 @@ def test_workspace_size_formula():
         saved = 4 * B * L * H         # (p, pc), (c.q, Y.q) per token-head: 2 float4
         gsaved = B * L * H            # g_t per token-head: float2
         NSEG = -(-NC // 4)            # one-pass look-back segments of 4 chunks
-        onepass = B * NSEG * H * (2 * D + 2)   # maps, leaving states, rotations, flags
+        onepass = B * NSEG * H * (2 * D + 2) + 8   # maps, leaving states, rotations, flags, control block
         NCK = -(-Q // 8) * 8 // 4     # z checkpoints per chunk (every 4 tokens of the 8-rounded loop)
         zck = B * NC * H * NCK * D
         cend = B * NC * H * D         # correction state after each chunk

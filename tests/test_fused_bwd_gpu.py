@@ -13,27 +13,9 @@ import math
 import pytest
 import torch
 
-from _gpu_util import DEV, ScanConfig, draw_inputs, log, rel, select, to_dev
-from oracle import cdssm_oracle as o
+from _gpu_util import DEV, GRAD_NAMES as NAMES, ScanConfig, cotangents, draw_inputs, log, oracle_grads, rel, select, to_dev
 
 pytestmark = pytest.mark.gpu
-
-NAMES = ("q", "k", "v", "beta", "sel_C", "dt", "r", "alpha", "omega")
-
-
-def oracle_grads(x, gy, gh, chunk_size=None):
-    d = {n: (x[n].double().clone().requires_grad_(True)) for n in NAMES}
-    h0 = x.get("h0")
-    h0d = h0.double().clone().requires_grad_(True) if h0 is not None else None
-    y, hf = o.fused_scan(*[d[n] for n in NAMES], x["c"], h0=h0d, chunk_size=chunk_size,
-                         grad_mode="reference")
-    loss = (y * gy.double()).sum() + (hf * gh.double()).sum()
-    wrt = [d[n] for n in NAMES] + ([h0d] if h0d is not None else [])
-    gs = torch.autograd.grad(loss, wrt)
-    out = dict(zip(NAMES, gs[:9]))
-    if h0d is not None:
-        out["h0"] = gs[9]
-    return out
 
 
 def hip_grads(x, gy, gh, chunk_size=None):
@@ -50,15 +32,6 @@ def hip_grads(x, gy, gh, chunk_size=None):
     if h0 is not None:
         out["h0"] = h0.grad.cpu()
     return out
-
-
-def cotangents(cfg, seed=7):
-    gen = torch.Generator().manual_seed(seed)
-    gy = torch.randn(cfg.B, cfg.L, cfg.H, cfg.N, generator=gen)
-    gh = torch.randn(cfg.B, cfg.H, cfg.N, cfg.D, generator=gen)
-    if cfg.dtype == "bf16":
-        gy = gy.bfloat16().float()
-    return gy, gh
 
 
 CASES = [
@@ -105,9 +78,10 @@ def test_fused_bwd_matches_oracle(name, cfg, chunk, path):
 def test_fused_bwd_full_c2_sequences_match_oracle():
     """C2 shape (B4 H24 L8192 D128, bf16) on the GPU; selected sequences re-derived by the oracle.
 
-    Per-(b, h) gradients of per-token inputs depend only on that sequence; the
-    per-head alpha/omega gradients sum over batch rows, so the oracle runs on
-    one batch row and is compared with the HIP gradient of a run on that row.
+    Per-(b, h) gradients of per-token inputs depend only on that sequence and are
+    compared on the full-shape run.  The per-head alpha/omega gradients sum over
+    batch rows, so they are compared on a second HIP run over the one selected
+    batch row (all 24 heads), whose sums then cover exactly the oracle's row.
     """
     cfg = ScanConfig("C2", B=4, H=24, L=8192, D=128)
     log("[fused bwd full] C2 B4 H24 L8192 D128 bf16")
@@ -117,14 +91,68 @@ def test_fused_bwd_full_c2_sequences_match_oracle():
     for n in NAMES:
         assert torch.isfinite(got[n].float()).all(), n
     b, heads = [2], [0, 23]
+    bt, ht = torch.tensor(b), torch.tensor(heads)
     xs = select(x, b, heads)
-    gys = gy.index_select(0, torch.tensor(b)).index_select(2, torch.tensor(heads))
-    ghs = gh.index_select(0, torch.tensor(b)).index_select(1, torch.tensor(heads))
+    gys = gy.index_select(0, bt).index_select(2, ht)
+    ghs = gh.index_select(0, bt).index_select(1, ht)
     ref = oracle_grads(xs, gys, ghs)
     errs = {}
     for n in ("q", "k", "v", "beta", "sel_C", "dt", "r"):
-        gsel = got[n].index_select(0, torch.tensor(b)).index_select(2, torch.tensor(heads))
+        gsel = got[n].index_select(0, bt).index_select(2, ht)
         errs[n] = rel(gsel, ref[n])
+    log("   one-row run for the per-head sums (B1 H24 L8192)")
+    row = hip_grads(select(x, b), gy.index_select(0, bt), gh.index_select(0, bt))
+    for n in ("alpha", "omega"):
+        errs[n] = rel(row[n].index_select(0, ht), ref[n])
+    log("   " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
+    assert all(e <= 2e-2 for e in errs.values()), errs
+
+
+def test_one_launch_bwd_carry_past_the_anchor_matches_oracle():
+    """B1 H8 L38400 D64 bf16 with h0: 600 chunks, 150 look-back segments, so the
+    one-launch correction adjoint + reverse carry folds from published anchor
+    states (one every 63 segments, counted from the right).  Both kernels are
+    forced onto their one-launch paths (the call raises if it cannot take them);
+    the oracle re-derives two heads, every gradient including alpha/omega (B = 1)."""
+    cfg = ScanConfig("t", B=1, H=8, L=38400, D=64, h0_std=0.1)
+    log("[fused bwd anchor] B1 H8 L38400 D64 bf16 h0, one-launch forward and carry")
+    x = draw_inputs(cfg, seed=3)
+    gy, gh = cotangents(cfg, seed=11)
+    with forward_path("one_pass"):
+        got = hip_grads(x, gy, gh)
+    from cdssm_hip import lookback_status
+    assert lookback_status() == 0, "a look-back wait timed out"
+    heads = [1, 6]
+    ht = torch.tensor(heads)
+    ref = oracle_grads(select(x, None, heads), gy.index_select(2, ht), gh.index_select(1, ht))
+    errs = {}
+    for n in NAMES:
+        g = got[n].index_select(0, ht) if n in ("alpha", "omega") else got[n].index_select(2, ht)
+        errs[n] = rel(g, ref[n])
+    errs["h0"] = rel(got["h0"].index_select(1, ht), ref["h0"])
+    log("   " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
+    assert all(e <= 2e-2 for e in errs.values()), errs
+
+
+def test_fused_bwd_c3_shape_sequences_match_oracle():
+    """C3 shape (B1 H32 L65536 D64 bf16, fast-rotating heads, h0 ~ N(0, 0.1)) forward +
+    backward on the GPU; the oracle re-derives one head's gradients (B = 1, so the
+    head's alpha/omega gradients too)."""
+    cfg = ScanConfig("C3", B=1, H=32, L=65536, D=64, omega_std=3.0, h0_std=0.1)
+    log("[fused bwd C3] B1 H32 L65536 D64 bf16 h0")
+    x = draw_inputs(cfg, seed=0)
+    gy, gh = cotangents(cfg)
+    got = hip_grads(x, gy, gh)
+    for n in NAMES:
+        assert torch.isfinite(got[n].float()).all(), n
+    heads = [9]
+    ht = torch.tensor(heads)
+    ref = oracle_grads(select(x, None, heads), gy.index_select(2, ht), gh.index_select(1, ht))
+    errs = {}
+    for n in NAMES:
+        g = got[n].index_select(0, ht) if n in ("alpha", "omega") else got[n].index_select(2, ht)
+        errs[n] = rel(g, ref[n])
+    errs["h0"] = rel(got["h0"].index_select(1, ht), ref["h0"])
     log("   " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
     assert all(e <= 2e-2 for e in errs.values()), errs
 
@@ -153,7 +181,7 @@ def test_one_pass_training_forward_writes_the_four_launch_records():
     carry = n_states + n_gam + B * H * S * (D + 1)
     off_saved = carry + (carry & 1)
     NSEG, NCK = -(-NC // 4), -(-Q // 8) * 8 // 4
-    off_zck = off_saved + 5 * B * L * H + B * NSEG * H * (2 * D + 2)
+    off_zck = off_saved + 5 * B * L * H + B * NSEG * H * (2 * D + 2) + 8  # look-back area + control block
     n_zck = B * NC * H * NCK * D
     regions = {"states": (0, n_states), "gam": (n_states, n_states + n_gam),
                "saved": (off_saved, off_saved + 4 * B * L * H),
