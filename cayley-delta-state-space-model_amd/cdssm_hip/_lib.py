@@ -36,6 +36,7 @@ SIGNATURES = {
     "cdssm_fused_scan_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "cdssm_fused_scan_fwd": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _P,
                                     _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "cdssm_fused_scan_fwd_noalloc": (_I32, [_I32] + [_P] * 9 + [_F32] + [_P] * 3 + [_I64] * 6 + [_P]),
     "cdssm_fused_scan_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "cdssm_fused_scan_bwd": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _P, _P, _P,
                                     _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,

@@ -40,6 +40,7 @@
 // count only the oldest load.  Tokens past the end of a ragged last chunk are
 // inert steps (a = 1, w = 0, beta = 0).
 #include <atomic>
+#include <mutex>
 
 #include "common.hpp"
 
@@ -1271,11 +1272,50 @@ int onepass_capacity(size_t lds) {
       reinterpret_cast<const void*>(&fused_fwd_onepass_kernel<T, D, LPH, SAVE, PERSIST>), kWave * kOnePassW, lds);
 }
 
+// Where a forward call keeps its scratch: the carry arrays of the four-launch
+// scan, the one-pass look-back area and, for the training forward, what the
+// backward reads.  The caller's workspace holds all of them (full layout); the
+// inference-only layout (no training records) packs the look-back area and
+// the carry arrays alone.
+struct FwdRegions {
+  float2 *summ, *gam, *segA, *segX;
+  float4* saved;
+  float2 *gsaved, *zck, *cend, *onepass;
+};
+
+FwdRegions full_regions(float* ws, const FwdLayout& w) {
+  FwdRegions g;
+  g.summ = reinterpret_cast<float2*>(ws);
+  g.gam = g.summ + w.n_summ;
+  g.segA = g.gam + w.n_gam;
+  g.segX = g.segA + w.n_segA;
+  g.saved = reinterpret_cast<float4*>(g.segX + w.n_segX + w.n_pad);
+  g.gsaved = reinterpret_cast<float2*>(ws) + w.gsaved_offset();
+  g.onepass = reinterpret_cast<float2*>(ws) + w.onepass_offset();
+  g.zck = reinterpret_cast<float2*>(ws) + w.zck_offset();
+  g.cend = reinterpret_cast<float2*>(ws) + w.cend_offset();
+  return g;
+}
+
+int64_t infer_float2s(const FwdLayout& w) { return w.n_op + w.n_summ + w.n_gam + w.n_segA + w.n_segX; }
+
+FwdRegions infer_regions(float2* base, const FwdLayout& w) {
+  FwdRegions g;
+  g.onepass = base;
+  g.summ = base + w.n_op;
+  g.gam = g.summ + w.n_summ;
+  g.segA = g.gam + w.n_gam;
+  g.segX = g.segA + w.n_segA;
+  g.saved = nullptr;
+  g.gsaved = g.zck = g.cend = nullptr;
+  return g;
+}
+
 template <typename T, int D, int LPH, int LPHS>
 int launch_fused_fwd(const void* q, const void* k, const void* v, const void* beta, const void* sel_c,
                      const void* dt, const void* r, const float* alpha, const float* omega, float c,
-                     const float* h0, void* y, float* h_final, float* ws, int B, int L, int H, int Q,
-                     hipStream_t stream, hipEvent_t* ev, bool save, int* path) {
+                     const float* h0, void* y, float* h_final, const FwdRegions& reg, int B, int L, int H,
+                     int Q, hipStream_t stream, hipEvent_t* ev, bool save, int* path) {
   using raw = typename T::raw;
   constexpr int HPW = kWave / LPH, HPWS = kWave / LPHS;
   // the a_t input form is inference-only: its training branches name the
@@ -1290,14 +1330,14 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
     cdssm_host::set_error("cdssm_fused_scan_fwd: grid too large (%lld tiles)", (long long)tiles);
     return CDSSM_EINVAL;
   }
-  float2* summ = reinterpret_cast<float2*>(ws);
-  float2* gam = summ + w.n_summ;
-  float2* segA = gam + w.n_gam;
-  float2* segX = segA + w.n_segA;
-  float4* saved = reinterpret_cast<float4*>(segX + w.n_segX + w.n_pad);
-  float2* gsaved = reinterpret_cast<float2*>(ws) + w.gsaved_offset();
-  float2* zck = reinterpret_cast<float2*>(ws) + w.zck_offset();
-  float2* cend = reinterpret_cast<float2*>(ws) + w.cend_offset();
+  float2* summ = reg.summ;
+  float2* gam = reg.gam;
+  float2* segA = reg.segA;
+  float2* segX = reg.segX;
+  float4* saved = reg.saved;
+  float2* gsaved = reg.gsaved;
+  float2* zck = reg.zck;
+  float2* cend = reg.cend;
   const int slots = round_up(Q, kWave) * HPW, slots_s = round_up(Q, kWave) * HPWS;
 
   if (cdssm_host::scan_path() != cdssm_host::kPathFour) {
@@ -1318,7 +1358,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
                          (forced || (!save && items * 10 >= rounds * capp * 9));
     if (single || persist) {
       const int grid = single ? int(items) : capp;
-      float2* base = reinterpret_cast<float2*>(ws) + w.onepass_offset();
+      float2* base = reg.onepass;
       const int64_t nsd = int64_t(B) * w.NSEG * H * D, nsh = int64_t(B) * w.NSEG * H;
       OnePassArgs<T> a;
       a.q = (const raw*)q;
@@ -1420,6 +1460,56 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Static scratch of cdssm_fused_scan_fwd_noalloc: the inference forward's
+// look-back area and carry arrays, for callers that cannot allocate device
+// memory.  One copy per GPU, held until the process ends; every no-alloc call
+// on a GPU uses that GPU's copy, so such calls must not overlap on one GPU.
+// Nothing in it needs clearing between calls: the carry arrays are written
+// before they are read in each call, and the look-back flags only count when
+// they carry the running call's epoch (fresh per call, written by the epoch
+// kernel into the area's control block).
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = size_t(32) << 20;  // 32 MiB
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float2* g_scratch_ptr[kMaxDevices];  // device address of `scratch` on each GPU, 0 until looked up
+
+int scratch_regions(const FwdLayout& w, FwdRegions* reg) {
+  const int64_t need = infer_float2s(w) * int64_t(sizeof(float2));
+  if (need > int64_t(kScratchBytes)) {
+    cdssm_host::set_error("cdssm_fused_scan_fwd_noalloc: this shape needs %lld bytes of scratch, more than the "
+                          "%zu bytes of the library's static scratch; use cdssm_fused_scan_fwd with a workspace",
+                          (long long)need, kScratchBytes);
+    return CDSSM_EINVAL;
+  }
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    cdssm_host::set_error("cdssm_fused_scan_fwd_noalloc: no usable current device (%d)", dev);
+    return CDSSM_EHIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    // the array's address on this device (the host-side name is only a stand-in)
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      cdssm_host::set_error("cdssm_fused_scan_fwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                            dev, hipGetErrorString(e));
+      return CDSSM_EHIP;
+    }
+    g_scratch_ptr[dev] = static_cast<float2*>(ptr);
+  }
+  *reg = infer_regions(g_scratch_ptr[dev], w);
+  return CDSSM_OK;
+}
+}  // namespace
+
 int cdssm_host::fwd_lookback_status(bool clear, unsigned* out) {
   unsigned v = 0;
   if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(cdssm::g_fwd_status), sizeof(v), 0, hipMemcpyDeviceToHost) != hipSuccess) {
@@ -1447,13 +1537,18 @@ extern "C" int64_t cdssm_fused_scan_workspace_bytes(int64_t B, int64_t L, int64_
 }
 
 namespace {
+// Scratch of a forward call: the caller's workspace (full layout), or, with
+// workspace NULL, the library's static per-device scratch (inference only).
+int scratch_regions(const FwdLayout& w, FwdRegions* reg);
+
 int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, const void* beta,
                     const void* sel_c, const void* dt, const void* r, const float* alpha,
                     const float* omega, float c, const float* h0, void* y, float* h_final,
                     float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
                     int64_t chunk, hipStream_t stream, hipEvent_t* ev, bool save, int* path = nullptr,
-                    bool abar = false) {
-  const char* op = abar ? "cdssm_fused_scan_fwd_abar" : "cdssm_fused_scan_fwd";
+                    bool abar = false, bool no_alloc = false) {
+  const char* op = no_alloc ? "cdssm_fused_scan_fwd_noalloc"
+                            : (abar ? "cdssm_fused_scan_fwd_abar" : "cdssm_fused_scan_fwd");
   if (dtype != 0 && dtype != 1) {
     cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
     return CDSSM_EINVAL;
@@ -1486,7 +1581,7 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
     return CDSSM_EINVAL;
   }
   if (!q || !k || !v || !beta || !sel_c || !dt || !r || (!abar && (!alpha || !omega)) || !y || !h_final ||
-      !workspace) {
+      (!workspace && !no_alloc)) {
     cdssm_host::set_error("%s: null pointer argument", op);
     return CDSSM_EINVAL;
   }
@@ -1498,8 +1593,16 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
     cdssm_host::set_error("%s: y must be aligned to its (re, im) pair (%d bytes)", op, dtype == 1 ? 4 : 8);
     return CDSSM_EINVAL;
   }
+  const FwdLayout lay = fwd_layout(B, L, H, D, chunk);
+  FwdRegions reg;
+  if (no_alloc) {
+    const int st = scratch_regions(lay, &reg);
+    if (st) return st;
+  } else {
+    reg = full_regions(workspace, lay);
+  }
   const int b = int(B), l = int(L), hh = int(H), qc = int(chunk);
-#define CDSSM_FWD_ARGS q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace, b, l, hh, qc, stream, \
+#define CDSSM_FWD_ARGS q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, reg, b, l, hh, qc, stream, \
                        ev, save, path
   if (abar) {
     if (save) {
@@ -1533,6 +1636,18 @@ extern "C" int cdssm_fused_scan_fwd(int dtype, const void* q, const void* k, con
                                     int64_t chunk, hipStream_t stream) {
   return fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace,
                          B, L, H, D, N, chunk, stream, nullptr, false);
+}
+
+// The inference forward with the library's static scratch in place of a
+// workspace: no allocation, no workspace argument (see `scratch` above).
+extern "C" int cdssm_fused_scan_fwd_noalloc(int dtype, const void* q, const void* k, const void* v,
+                                            const void* beta, const void* sel_c, const void* dt,
+                                            const void* r, const float* alpha, const float* omega, float c,
+                                            const float* h0, void* y, float* h_final, int64_t B, int64_t L,
+                                            int64_t H, int64_t D, int64_t N, int64_t chunk,
+                                            hipStream_t stream) {
+  return fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, nullptr, B, L, H,
+                         D, N, chunk, stream, nullptr, false, nullptr, false, true);
 }
 
 // The fused forward on gate-level inputs: a_t (B,L,H,2) and vp_t (B,L,H,1) of

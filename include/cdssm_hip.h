@@ -61,6 +61,25 @@ int cdssm_fused_scan_fwd(int dtype, const void* q, const void* k, const void* v,
                          int64_t chunk, hipStream_t stream);
 
 /*
+ * The inference forward above with no workspace argument and no allocation.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Its scratch (the look-back area and carry arrays) is a
+ * static 32 MiB device array inside the library, one per GPU, held until the
+ * process ends; shapes needing more return -1 with a message naming the size
+ * (C1 needs 6.7 MB, C3 26.6 MB).  Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU (concurrent streams) race and must not be
+ * issued.  Nothing in the array needs clearing between calls.  Results are
+ * bit-identical to cdssm_fused_scan_fwd on the same inputs.  Arguments and
+ * limits otherwise as cdssm_fused_scan_fwd.
+ */
+int cdssm_fused_scan_fwd_noalloc(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                                 const void* sel_c, const void* dt, const void* r, const float* alpha,
+                                 const float* omega, float c, const float* h0, void* y, float* h_final,
+                                 int64_t B, int64_t L, int64_t H, int64_t D, int64_t N, int64_t chunk,
+                                 hipStream_t stream);
+
+/*
  * The fused forward on gate-level inputs, for the model's block
  * (block.py:177-211): instead of the scan-level dt, r, alpha, omega, c it takes
  * the transition a_bar (B,L,H,N) and VP scale vp (B,L,H,N/2), both of `dtype`,
