@@ -31,6 +31,7 @@ from . import _lib
 from .ops import DynamicsFusedFn
 from .decode import DecodeState, decode_step_abar, prefill_abar
 from .scan import chunkwise_delta_scan_abar
+from .ssd import SSDChunkwiseScan
 
 Tensor = torch.Tensor
 
@@ -538,8 +539,8 @@ class CDSSMBlock(nn.Module):
         running sums and the position."""
         cfg = self.config
         N, H, D, Di = cfg.state_dim, cfg.n_heads, cfg.head_dim, cfg.d_inner
-        if N != 2:
-            raise ValueError("the fused scan of this build supports state_dim = 2")
+        if N != 2 and cache is not None:
+            raise NotImplementedError("decode caches need state_dim = 2 (the decode kernels' state layout)")
         if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
             # the fused block kernels carry no autograd graph: a backward would silently miss them
             raise RuntimeError("CDSSMBlock is forward-only here: call it under torch.no_grad() or "
@@ -578,12 +579,22 @@ class CDSSMBlock(nn.Module):
         Q = self.Q_proj(x_conv).reshape(B, L, H, D)
         K, Q, qk = normalize_kq_qk(K, Q)
         V = V.contiguous()
-        if cache is None:
+        if N != 2:
+            # N/2 complex pairs per head (the reference default is 16): the reference's own pass
+            # structure over the per-pass ops (block.py:194-211 with ssd.py:39-111); the readout and
+            # the shortcut in fp32, then rounded to the model dtype
+            V_gated = V * vp.repeat_interleave(2, dim=-1)                                 # block.py:194-195
+            Y = SSDChunkwiseScan(cfg.chunk_size, N)(A_bar, K, V_gated, beta)              # block.py:198
+            ret = (Y.float() * Q.float().unsqueeze(-2)).sum(-1)                           # block.py:208
+            ret = ret + self._fp32("shortcut_scale") * (qk * qk).unsqueeze(-1) * V_gated.float()  # :202-205
+            retrieved = (ret * sel_C.float().unsqueeze(-1)).to(x.dtype)                   # block.py:211
+        elif cache is None:
             retrieved, _ = chunkwise_delta_scan_abar(Q, K, V, beta, sel_C, A_bar, vp, chunk_size=cfg.chunk_size)
         else:
             retrieved, cache["scan"] = prefill_abar(Q, K, V, beta, sel_C, A_bar, vp, chunk_size=cfg.chunk_size)
-        # current-token shortcut (block.py:202-205) through the readout: sel_C s (q.k)^2 V vp
-        shortcut_readout_(retrieved, qk, V, vp, sel_C, self._fp32("shortcut_scale"))
+        if N == 2:
+            # current-token shortcut (block.py:202-205) through the readout: sel_C s (q.k)^2 V vp
+            shortcut_readout_(retrieved, qk, V, vp, sel_C, self._fp32("shortcut_scale"))
         y = self.readout_proj(retrieved.reshape(B, L, H * N))
         y = group_norm_gate(y, self.ssm_norm.num_groups, self.ssm_norm.weight, self.ssm_norm.bias,
                             self.ssm_norm.eps, z, x_conv, self.D, return_sums=cache is not None)

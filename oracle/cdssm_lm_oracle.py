@@ -18,9 +18,12 @@ Pins (tests/test_oracle_lm.py): conv1d_silu against torch.nn.functional.conv1d
 (causal padding, groups = C) followed by F.silu, i.e. a library routine with
 the tap order fixed by the reference's comment (conv1d_silu.cu:74-80);
 rms_norm against its closed form; block_forward by invariants (a zero
-out_proj makes the block the identity; batch rows are independent) -- the
-wiring itself, between pinned pieces, follows block.py line by line and is
-otherwise pinned only by those invariants; group_norm_running_sums against
+out_proj makes the block the identity; batch rows are independent) and by
+closed-form special cases of its wiring: a zero readout_proj leaves
+residual + out_proj(GroupNorm bias * silu(z) + D * x_conv) built from library
+routines (pins the in_proj split order, the gate and the D-skip), the
+value-residual lerp's direction at sigmoid(gate) = 0 and 1, and the shortcut
+read out as sel_C s (q.k)^2 V_gated; group_norm_running_sums against
 the groups' mean and variance (torch) and by appending a token.  Note: the model is not causal in
 the reference: its GroupNorm (block.py:216-223) takes statistics over the
 group's channels and all L positions, which this restatement reproduces.

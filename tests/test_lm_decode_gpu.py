@@ -190,6 +190,10 @@ def test_model_decode_matches_reforward(dtype, n_layers, L0, T, d_inner):
             assert torch.isfinite(step).all()
             if n_layers == 1:
                 assert e <= (1e-4 if dtype == torch.float32 else 2e-2)
+            else:
+                # deeper: the re-forward also revises earlier positions above layer 1 (the reference's
+                # GroupNorm spans all positions); the step keeps running statistics -- bounded, not equal
+                assert e <= (2e-3 if dtype == torch.float32 else 3e-2)
 
 
 @pytest.mark.parametrize("dtype,n_layers", [(torch.float32, 2), (torch.bfloat16, 2)])
@@ -244,3 +248,43 @@ def test_fused_token_kernel_matches_separate_kernels(dtype):
         finally:
             CDSSMBlock.fused_step = True
         assert rel(ca[-1]["scan"].state, cb[-1]["scan"].state) <= (1e-5 if dtype == torch.float32 else 2e-2)
+
+
+def test_config4_decode_24_layers_batch_64():
+    """Config 4's decode: 24 layers, d_model 1024, 16 heads x 64, vocab 32000, bf16, B = 64 from a
+    2048-token prefill.  Each step is finite; the graph-captured step equals the eager step on every
+    replay (with eager work and synchronisation between replays); and layer 0's step output equals the
+    re-forward of layer 0 over prompt + tokens at the new token (its input, the embedding, is not
+    revised by a re-forward), 2e-2 bf16."""
+    from cdssm_hip.lm import CDSSMConfig, CDSSMLMHeadModel, _clone_cache
+    torch.manual_seed(0)
+    cfg = CDSSMConfig(d_model=1024, n_layers=24, context_length=2048, vocab_size=32000, state_dim=2, d_inner=1024)
+    m = CDSSMLMHeadModel(cfg)
+    with torch.no_grad():
+        for blk in m.blocks:
+            blk.v_residual_gate.normal_(std=1.0)
+            blk.shortcut_scale.fill_(0.3)
+            blk.D.normal_(std=0.1)
+    m = m.to(torch.bfloat16).to(DEV).eval()
+    B, L0, T = 64, 2048, 3
+    log(f"[config-4 decode] 24 layers B{B} prefill {L0} steps {T} bf16")
+    g = torch.Generator().manual_seed(18)
+    ids = torch.randint(0, cfg.vocab_size, (B, L0 + T), generator=g).to(DEV)
+    with torch.no_grad():
+        _, caches = m.prefill(ids[:, :L0])
+        c_eager = [_clone_cache(c) for c in caches]
+        c_layer0 = _clone_cache(caches[0])
+        dg = m.decode_graph(caches)
+        for t in range(L0, L0 + T):
+            want = m.decode_step(ids[:, t], c_eager).clone()
+            torch.cuda.synchronize()
+            got = dg(ids[:, t]).clone()
+            torch.cuda.synchronize()
+            assert torch.isfinite(want).all() and torch.isfinite(got).all()
+            eg = rel(got, want)
+            x0, _ = m.blocks[0].step(m.embedding(ids[:, t]), None, c_layer0)
+            ref0, _ = m.blocks[0](m.embedding(ids[:, :t + 1]))
+            e0 = rel(x0, ref0[:, -1])
+            log(f"   token {t}: graph vs eager {eg:.2e}  layer-0 step vs re-forward {e0:.2e}")
+            assert eg <= 1e-6
+            assert e0 <= 2e-2

@@ -34,11 +34,11 @@ def test_conv1d_silu_matches_oracle(dtype, B, L, C, K):
     assert e <= (1e-6 if dtype == torch.float32 else 1e-2)
 
 
-def _model(d_model, n_layers, vocab, d_inner, L_ctx, dtype, seed=0):
+def _model(d_model, n_layers, vocab, d_inner, L_ctx, dtype, seed=0, state_dim=2):
     from cdssm_hip.lm import CDSSMConfig, CDSSMLMHeadModel
     torch.manual_seed(seed)
-    cfg = CDSSMConfig(d_model=d_model, n_layers=n_layers, context_length=L_ctx, vocab_size=vocab, state_dim=2,
-                      d_inner=d_inner)
+    cfg = CDSSMConfig(d_model=d_model, n_layers=n_layers, context_length=L_ctx, vocab_size=vocab,
+                      state_dim=state_dim, d_inner=d_inner)
     m = CDSSMLMHeadModel(cfg)
     with torch.no_grad():  # exercise the value-residual and shortcut paths (zero at init)
         for blk in m.blocks:
@@ -50,15 +50,18 @@ def _model(d_model, n_layers, vocab, d_inner, L_ctx, dtype, seed=0):
     return cfg, m, p
 
 
-@pytest.mark.parametrize("name,dtype,d_model,n_layers,d_inner,B,L,tol", [
-    ("fp32_small", torch.float32, 128, 2, 128, 2, 200, 1e-3),
-    ("fp32_D128_heads", torch.float32, 64, 2, 256, 1, 150, 1e-3),
-    ("bf16_small", torch.bfloat16, 128, 2, 128, 2, 200, 2e-2),
-    ("bf16_c4_width_2_layers", torch.bfloat16, 1024, 2, 1024, 1, 256, 2e-2),
+@pytest.mark.parametrize("name,dtype,d_model,n_layers,d_inner,B,L,tol,N", [
+    ("fp32_small", torch.float32, 128, 2, 128, 2, 200, 1e-3, 2),
+    ("fp32_D128_heads", torch.float32, 64, 2, 256, 1, 150, 1e-3, 2),
+    ("bf16_small", torch.bfloat16, 128, 2, 128, 2, 200, 2e-2, 2),
+    ("bf16_c4_width_2_layers", torch.bfloat16, 1024, 2, 1024, 1, 256, 2e-2, 2),
+    # the reference's default state_dim 16 (config/model.py:128): the block runs the per-pass ops
+    ("fp32_state16", torch.float32, 128, 2, 256, 2, 150, 1e-3, 16),
+    ("bf16_state16", torch.bfloat16, 128, 2, 256, 1, 200, 2e-2, 16),
 ])
-def test_lm_forward_matches_oracle(name, dtype, d_model, n_layers, d_inner, B, L, tol):
-    log(f"[lm fwd] {name}: d_model {d_model} layers {n_layers} d_inner {d_inner} B{B} L{L} {dtype}")
-    cfg, m, p = _model(d_model, n_layers, 512, d_inner, 2048, dtype)
+def test_lm_forward_matches_oracle(name, dtype, d_model, n_layers, d_inner, B, L, tol, N):
+    log(f"[lm fwd] {name}: d_model {d_model} layers {n_layers} d_inner {d_inner} B{B} L{L} N{N} {dtype}")
+    cfg, m, p = _model(d_model, n_layers, 512, d_inner, 2048, dtype, state_dim=N)
     ids = torch.randint(0, cfg.vocab_size, (B, L), generator=torch.Generator().manual_seed(1))
     with torch.no_grad():
         logits = m(ids.to(DEV)).float().cpu()
@@ -85,3 +88,21 @@ def test_lm_forward_runs_at_the_config4_shape():
     e = rel(y0.float().cpu(), ref)
     log(f"   config-4 block 0 rel err {e:.2e}")
     assert e <= 2e-2
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-3), (torch.bfloat16, 2e-2)])
+def test_lm_24_layer_config4_logits_match_oracle(dtype, tol):
+    """All 24 layers of the config-4 model (d_model 1024, 16 heads x 64, vocab 32000) on a short
+    sequence (B1 L96) against the fp64 oracle LM with the same weights.  fp32 weights: 1e-3 (the
+    hardware log/exp of the dynamics through 24 layers); bf16 weights and activations: 2e-2 (24 layers
+    of bf16 rounding points, against fp64 on the rounded weights; measured 2e-3)."""
+    cfg, m, p = _model(1024, 24, 32000, 1024, 2048, dtype)
+    log(f"[lm fwd 24 layers] config 4, B1 L96 {dtype}")
+    ids = torch.randint(0, cfg.vocab_size, (1, 96), generator=torch.Generator().manual_seed(5))
+    with torch.no_grad():
+        logits = m(ids.to(DEV)).float().cpu()
+    ref = lo.lm_forward(p, ids, cfg)
+    e = rel(logits, ref)
+    log(f"   rel err logits {e:.2e}")
+    assert torch.isfinite(logits).all()
+    assert e <= tol

@@ -356,6 +356,125 @@ def test_correction_known_answers_and_linearity():
         np.testing.assert_allclose((got[..., 0::2, :] + 1j * got[..., 1::2, :]).numpy(), want, atol=1e-12)
 
 
+def _brute_correction(A, K, beta, S0):
+    """Explicit real matrices: corrections[t] = state before step t, each step
+    S <- R_t (S (I - beta_t k_t k_t^T)) with R_t the block-diagonal rotation of the
+    interleaved pairs (exact_correction.cu:83-150).  A (B,NC,C,H,N), S0 (B,NC,H,N,D)."""
+    A, K, beta, S0 = (x.numpy() for x in (A, K, beta, S0))
+    B, NC, C, H, D = K.shape
+    N = A.shape[-1]
+    out = np.zeros((B, NC, C, H, N, D))
+    for b in range(B):
+        for n in range(NC):
+            for h in range(H):
+                S = S0[b, n, h].copy()
+                for t in range(C):
+                    out[b, n, t, h] = S
+                    k = K[b, n, t, h]
+                    S = _blockdiag_rot(A[b, n, t, h]) @ (S @ (np.eye(D) - beta[b, n, t, h] * np.outer(k, k)))
+    return out
+
+
+def test_correction_matches_brute_force_matrices_with_erasures():
+    """beta != 0, N = 4 (two pairs), several chunks: every stored correction state
+    against products of explicit (N x N) rotation and (D x D) projection matrices --
+    a k / beta index slip or a store-after would fail."""
+    g = rng(21)
+    B, NC, C, H, D, N = 2, 3, 6, 2, 5, 4
+    A, K, _, beta = _rand_scan_inputs(g, B * NC, C, H, D, N)
+    A, K, beta = A.reshape(B, NC, C, H, N), K.reshape(B, NC, C, H, D), beta.reshape(B, NC, C, H)
+    S0 = randn(g, B, NC, H, N, D)
+    got = o.exact_correction(A, K, beta, S0, N)
+    np.testing.assert_allclose(got.numpy(), _brute_correction(A, K, beta, S0), atol=1e-12)
+
+
+def test_single_chunk_R_runs_one_step_behind_E_with_state_and_writes():
+    """One chunk, h0 != 0, beta != 0: by linearity E's state is z_t (the local scan from
+    zero) plus h0 pushed through steps 0..t, while R's correction pushes h0 through steps
+    0..t-1 only (F2), so  Y^R_{t+1} - z_{t+1} = Y^E_t - z_t  for every t."""
+    g = rng(22)
+    B, L, H, D, N = 2, 10, 3, 6, 4
+    A, K, V, beta = _full_inputs(g, B, L, H, D, N)
+    h0 = randn(g, B, H, N, D)
+    YR = o.ssd_chunkwise_scan(A, K, V, beta, L, N, h0=h0)
+    YE, _ = o.exact_recurrence(A, K, V, beta, N, h0)
+    z, _ = o.exact_recurrence(A, K, V, beta, N)           # the local scan from zero (one chunk)
+    assert torch.allclose(YR[:, 0] - z[:, 0], h0, atol=1e-12)
+    for t in range(L - 1):
+        assert torch.allclose(YR[:, t + 1] - z[:, t + 1], YE[:, t] - z[:, t], atol=1e-12), t
+
+
+def _eig_sq_np(alpha, omega, dt):
+    """((1-ta)^2 + tw^2) / ((1+ta)^2 + tw^2 + 1e-6), ta = dt/2 max(alpha,0), tw = dt/2 omega (plain numpy)."""
+    ta, tw = 0.5 * dt * max(alpha, 0.0), 0.5 * dt * omega
+    return ((1 - ta) ** 2 + tw ** 2) / ((1 + ta) ** 2 + tw ** 2 + 1e-6)
+
+
+def test_dynamics_bwd_vp_clamp_gradient_by_value():
+    """Inside the VP clamp (1 - E^(c r) < 1e-6, so vp = sqrt(1e-6)) the forward is flat, but the
+    reference passes g_vp * (-0.5 / vp) into d|eig_eff| anyway (dynamics_fused.cu:247-259).  That is
+    the derivative of the smooth surrogate sqrt(1 - E^(c r) + delta) with the constant delta that puts
+    it at 1e-6 here.  The surrogate is built in plain numpy from the closed forms (softplus, sigmoid,
+    Cayley |eig|^2, the adaptive dt with its cap) and differentiated by central differences in every
+    gate it depends on; the restated reference backward must give the same values."""
+    H, N, c = 1, 2, math.log(2048.0)
+    # alpha ~ 1e-13 (E ~ 1 - 1e-6 / D), r ~ 0.0067 (c r ~ 0.05): 1 - E^(c r) ~ 4e-8 < 1e-6
+    raw = {"alpha": -30.0, "omega": 0.7, "sel_B": 0.1, "sel_C": 0.2, "sel_dt": -0.5, "beta": 0.3, "r": -5.0}
+    log_dt_scale, rope, omega_thresh, delta, smooth, eps_adt = 0.4, 0.0, 0.0883883, 0.125, 0.0176777, 1.0
+
+    def sp(x):
+        return x if x > 20 else math.log1p(math.exp(x))
+
+    def sg(x):
+        return 1.0 / (1.0 + math.exp(-x))
+
+    def dt_of(rw, lds):
+        a0, w0 = sp(rw["alpha"]), rw["omega"]
+        dt_raw = sp(lds) / (a0 + abs(w0) + eps_adt)
+        dt_max = (2.0 - delta) / (a0 + eps_adt)
+        bl = sg((omega_thresh - abs(w0)) / smooth)
+        return bl * min(dt_raw, dt_max) + (1 - bl) * dt_raw + sp(rw["sel_dt"])
+
+    def parts(rw, lds):
+        E = max(_eig_sq_np(sp(rw["alpha"]), rw["omega"], dt_of(rw, lds)), 1e-8)
+        return 1.0 - E ** (c * sg(rw["r"]))
+
+    base = parts(raw, log_dt_scale)
+    assert 0 < base < 1e-6                                   # inside the clamp
+    shift = 1e-6 - base
+
+    def surrogate(rw, lds):
+        return math.sqrt(parts(rw, lds) + shift)
+
+    gate_raw = torch.tensor([[[raw["alpha"], raw["omega"], raw["sel_B"], raw["sel_C"], raw["sel_dt"],
+                               raw["beta"], raw["r"]]]], dtype=DT)
+    A, vp, _, _ = o.dynamics_fused_fwd(gate_raw, torch.tensor([log_dt_scale]), torch.tensor([rope]), c,
+                                       omega_thresh, delta, smooth, eps_adt, H, N)
+    assert abs(float(vp) - 1e-3) < 1e-15                     # the clamp value sqrt(1e-6)
+    g_raw, g_lds = o.dynamics_fused_bwd_ref(torch.zeros_like(A), torch.ones_like(vp), torch.zeros(1, 1, 1),
+                                            torch.zeros(1, 1, 1), gate_raw, torch.tensor([log_dt_scale]),
+                                            torch.tensor([rope]), c, omega_thresh, delta, smooth, eps_adt, H, N)
+    order = ["alpha", "omega", "sel_B", "sel_C", "sel_dt", "beta", "r"]
+    h = 1e-6
+    for i, name in enumerate(order):
+        up, dn = dict(raw), dict(raw)
+        up[name] += h
+        dn[name] -= h
+        fd = (surrogate(up, log_dt_scale) - surrogate(dn, log_dt_scale)) / (2 * h)
+        got = float(g_raw[0, 0, i])
+        assert abs(got - fd) <= 1e-6 * max(1.0, abs(fd)), (name, got, fd)
+    fd = (surrogate(raw, log_dt_scale + h) - surrogate(raw, log_dt_scale - h)) / (2 * h)
+    assert abs(float(g_lds[0]) - fd) <= 1e-6 * max(1.0, abs(fd)), (float(g_lds[0]), fd)
+    # the clamped forward itself is flat here: its differences are exactly 0, the rule's gradient is not
+    def clamped(rw):
+        return math.sqrt(max(parts(rw, log_dt_scale), 1e-6))
+    up, dn = dict(raw), dict(raw)
+    up["omega"] += h
+    dn["omega"] -= h
+    assert clamped(up) == clamped(dn)
+    assert float(g_raw.abs().max()) > 1e-5
+
+
 # --------------------------------------------------------------------------
 # Full R-mode scan: relation to the exact recurrence, causality, linearity
 # --------------------------------------------------------------------------
