@@ -60,13 +60,14 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="C1", choices=["C1", "C3"])
+    ap.add_argument("--config", default="C1", choices=["C1", "C2", "C3"],
+                    help="forward workload (C1 is the metric's; C2 and C3 for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-batches", type=int, default=1)
     ap.add_argument("--no-fwd-bwd", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the decode and config-4 LM timings (profiling runs)")
-    ap.add_argument("--forward-path", default="auto", choices=["auto", "four_launch", "one_pass"],
+    ap.add_argument("--forward-path", default="auto", choices=["auto", "four_launch", "one_pass", "four_launch_mfma"],
                     help="how the forward is launched (default: the library's own choice)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a device copy of this many MiB (read + write), 10 times, and exit: "
@@ -131,6 +132,7 @@ def time_fwd_bwd(cfg_name, steps, warmup):
     tb = timed(bwd)
     by = scan_bytes(cfg, backward=True)
     alg = by["fwd"] + by["bwd"]
+    stored = training_record_bytes(cfg)
     fwd()
     phases = {"fwd_" + k: v for k, v in fwd.profile(steps).items()}
     phases.update({"bwd_" + k: v for k, v in bwd.profile(steps).items()})
@@ -138,7 +140,90 @@ def time_fwd_bwd(cfg_name, steps, warmup):
             "tokens_per_s": cfg.B * cfg.L / (ms * 1e-3), "ms_per_step": ms,
             "fwd_ms": tf / steps, "bwd_ms": tb / steps,
             "hbm_frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-            "alg_bytes": alg, "phase_ms": phases}
+            "alg_bytes": alg,
+            "stored_record_bytes": stored,
+            "hbm_frac_with_records": (alg + 2 * stored) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "bytes_note": ("alg_bytes: the inputs read and outputs written by forward and backward (272 B / 812 B "
+                           "per token-head at D 64 bf16); stored_record_bytes: what the training forward writes "
+                           "for the backward (per-token records, z every 4 tokens, chunk entering states, c^ at "
+                           "chunk ends), counted twice (written, read back) in hbm_frac_with_records"),
+            "phase_ms": phases}
+
+
+def training_record_bytes(cfg):
+    """Bytes the training forward stores for the backward (and the backward reads back): per token-head
+    two float4 records and the float2 g_t (40 B); per chunk-head the state every 4 tokens (bf16 complex
+    pairs for bf16 inputs: 4 B per element), the entering state and c^ at the chunk end (fp32 complex),
+    and G_k."""
+    NC = -(-cfg.L // cfg.D)
+    NCK = -(-cfg.D // 8) * 8 // 4
+    pair = 4 if cfg.dtype == "bf16" else 8
+    per_chunk_head = NCK * cfg.D * pair + 2 * cfg.D * 8 + 8
+    return cfg.B * cfg.H * (cfg.L * 40 + NC * per_chunk_head)
+
+
+def time_dropin(cfg_name, steps=10, warmup=2):
+    """The drop-in path unchanged reference callers get (ssd.py:83-100 through the reference's own op
+    classes): SSDChunkwiseScan(chunk, 2) over the per-pass HIP ops (intra-chunk scan, inter-chunk
+    carry, exact correction, Y = local_h + correction), materialising Y (B,L,H,N,D) bf16 as the
+    reference does.  Forward alone and forward + backward (autograd with dY ~ N(0,1)).  Algorithmic
+    bytes of this interface: read A_bar, K, V, beta, write Y = B*H*L*((D + 2N + 1) + N*D)*2 forward;
+    the backward reads dY and the inputs and writes their gradients (the same count again)."""
+    import torch
+    from cdssm_hip.ssd import SSDChunkwiseScan
+    from cdssm_hip.workloads import CONFIGS, draw_inputs
+
+    cfg = CONFIGS[cfg_name]
+    dev = torch.device("cuda:0")
+    x = draw_inputs(cfg, seed=0)
+    # the workload's A_bar and VP scale from (dt, r, alpha, omega, c): conj(mu) E^((c r - 1)/2) and
+    # sqrt(max(1 - E^(c r), 1e-6)) of the Cayley map (dynamics_fused.cu:109-131), in torch on the GPU
+    dt, r = x["dt"].to(dev).float(), x["r"].to(dev).float()
+    ta = 0.5 * dt * x["alpha"].to(dev).clamp_min(0.0)
+    tw = 0.5 * dt * x["omega"].to(dev)
+    den = (1 + ta) ** 2 + tw ** 2 + 1e-6
+    E = (((1 - ta) ** 2 + tw ** 2) / den).clamp_min(1e-8)
+    cr = x["c"] * r
+    scale = E ** ((cr - 1) * 0.5)
+    A = torch.stack([(1 - ta ** 2 - tw ** 2) / den * scale, -(2 * tw) / den * scale], -1).to(torch.bfloat16)
+    vp = (1 - E ** cr).clamp_min(1e-6).sqrt().clamp_max(1.0)
+    V = (x["v"].to(dev).float() * vp[..., None]).to(torch.bfloat16)
+    K = x["k"].to(dev)
+    beta = x["beta"].to(dev)
+    scan = SSDChunkwiseScan(cfg.D, 2)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    with torch.no_grad():
+        ms_f = timed(lambda: scan(A, K, V, beta))
+    leaves = [t.detach().clone().requires_grad_(True) for t in (A, K, V, beta)]
+    gY = torch.randn(cfg.B, cfg.L, cfg.H, 2, cfg.D, generator=torch.Generator().manual_seed(3)).to(
+        torch.bfloat16).to(dev)
+
+    def fb():
+        Y = scan(*leaves)
+        Y.backward(gY)
+
+    ms_fb = timed(fb)
+    BHL, D, N = cfg.B * cfg.H * cfg.L, cfg.D, 2
+    by_f = BHL * ((D + 2 * N + 1) + N * D) * 2
+    return {"workload": f"drop-in SSDChunkwiseScan (per-pass ops), {cfg.name} B{cfg.B} H{cfg.H} L{cfg.L} D{D} bf16",
+            "fwd_ms": ms_f, "fwd_tokens_per_s": cfg.B * cfg.L / (ms_f * 1e-3),
+            "fwd_hbm_frac": by_f / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "fwd_bwd_ms": ms_fb, "fwd_bwd_tokens_per_s": cfg.B * cfg.L / (ms_fb * 1e-3),
+            "fwd_bwd_hbm_frac": 2 * by_f / (ms_fb * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "alg_bytes_fwd": by_f}
 
 
 def time_decode(steps, warmup, B=64, H=16, D=64, prompt=2048):
@@ -284,25 +369,42 @@ def time_lm_forward(steps=5, warmup=2):
                     "GroupNorm + gate on the HIP kernels"}
 
 
-def cpu_baseline(cfg, x, batches, min_seconds=10.0):
-    """Time the fp32 oracle (CPU restatement of ops.py's R-mode scan) on
-    `batches` batch rows of the workload, all heads, full length, repeated
-    until about `min_seconds` of CPU work (at least 3 timed repetitions)."""
+def host_cores():
+    """Cores this process may run on (the GPU box gives a job a share of the host)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+def cpu_baseline(cfg, x, batches, min_seconds=10.0, threads=None, heads=None, backward=False):
+    """Time the fp32 oracle (CPU restatement of ops.py's R-mode scan) on `batches` batch rows and
+    `heads` heads (all if None) of the workload at full length, repeated until about `min_seconds` of
+    CPU work (at least 3 timed repetitions).  `backward`: forward + backward by autograd through the
+    restatement (loss sum(y * g), g ~ N(0,1)).  Tokens/s are scaled to the whole workload's tokens per
+    sample second: (sampled token-heads / all token-heads) of the workload's B*L tokens."""
     import torch
     from oracle import cdssm_oracle as o
 
-    n = os.cpu_count() or 1
+    n = threads or host_cores()
     torch.set_num_threads(n)
-    sl = {k: (t[:batches].float() if isinstance(t, torch.Tensor) and t.dim() >= 3 else t)
-          for k, t in x.items()}
-    sl["alpha"], sl["omega"] = x["alpha"].float(), x["omega"].float()
-    h0 = None if x["h0"] is None else x["h0"][:batches].float()
+    hs = list(range(cfg.H)) if heads is None else list(heads)
+    hi = torch.tensor(hs)
+    sl = {k: x[k][:batches].index_select(2, hi).float() for k in ("q", "k", "v", "beta", "sel_C", "dt", "r")}
+    sl["alpha"], sl["omega"] = x["alpha"].index_select(0, hi).float(), x["omega"].index_select(0, hi).float()
+    h0 = None if x["h0"] is None else x["h0"][:batches].index_select(1, hi).float()
+    names = ("q", "k", "v", "beta", "sel_C", "dt", "r", "alpha", "omega")
+    gy = torch.randn(batches, cfg.L, len(hs), cfg.N, generator=torch.Generator().manual_seed(4))
 
     def once():
         t0 = time.perf_counter()
-        with torch.no_grad():
-            o.fused_scan(sl["q"], sl["k"], sl["v"], sl["beta"], sl["sel_C"], sl["dt"], sl["r"],
-                         sl["alpha"], sl["omega"], x["c"], h0=h0)
+        if backward:
+            leaves = [sl[m].clone().requires_grad_(True) for m in names]
+            y, _ = o.fused_scan(*leaves, x["c"], h0=h0, grad_mode="reference")
+            (y * gy).sum().backward()
+        else:
+            with torch.no_grad():
+                o.fused_scan(*[sl[m] for m in names], x["c"], h0=h0)
         return time.perf_counter() - t0
 
     once()  # warm-up
@@ -310,11 +412,15 @@ def cpu_baseline(cfg, x, batches, min_seconds=10.0):
     while len(times) < 3 or sum(times) < min_seconds:
         times.append(once())
     med = statistics.median(times)
-    tokens = batches * cfg.L
+    frac = batches * len(hs) / (cfg.B * cfg.H)
+    tokens = cfg.B * cfg.L * frac
+    what = "forward + backward (autograd)" if backward else "forward"
     return {"value": tokens / med, "unit": "tokens/s", "cores": n, "kind": "port",
-            "sample": (f"oracle fp32 R-mode fused scan (torch CPU, {n} threads) on {batches} of "
-                       f"{cfg.B} batch rows x all {cfg.H} heads x L={cfg.L}; median of {len(times)} "
-                       f"repetitions after 1 warm-up ({sum(times):.1f} s timed); {med:.3f} s per sample")}
+            "workload": f"{cfg.name} {what}",
+            "sample": (f"oracle fp32 R-mode fused scan {what} (torch CPU, {n} threads) on {batches} of "
+                       f"{cfg.B} batch rows x {len(hs)} of {cfg.H} heads x L={cfg.L}; median of {len(times)} "
+                       f"repetitions after 1 warm-up ({sum(times):.1f} s timed); {med:.3f} s per sample; "
+                       f"tokens/s = the sample's share ({frac:.4f}) of B*L tokens per second")}
 
 
 def main():
@@ -395,11 +501,12 @@ def main():
 
     tokens = cfg.B * cfg.L
     alg = scan_bytes(cfg)["fwd"]
-    achieved = alg / (main_ms * 1e-3) / 1e9
+    # the kernel's time: its event-timed mean launch, never more than the back-to-back step time
+    kern_ms = min(main_ms, ms_per_step)
+    achieved = alg / (kern_ms * 1e-3) / 1e9
     traffic = recorded_traffic(traffic_file) if args.config == "C1" else None
     out = {
-        "metric": "scan tokens/sec (fwd), B8 H16 L4096 D64 bf16" if args.config == "C1"
-                  else "scan tokens/sec (fwd), B1 H32 L65536 D64 bf16",
+        "metric": f"scan tokens/sec (fwd), B{cfg.B} H{cfg.H} L{cfg.L} D{cfg.D} bf16",
         "value": tokens / (ms_per_step * 1e-3),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -417,9 +524,14 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "kernel": kernel,
+                     "headline": "warm: back-to-back calls, inputs resident in HBM (142.7 MB of them also fit "
+                                 "the 256 MB last-level cache between calls)",
+                     "cold_frac": alg / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                     "cold_basis": "one call after a 1 GiB write flushed the last-level cache, median of 10",
                      "basis": (f"algorithmic {alg / 1e6:.2f} MB per launch (272 B per token-head: q, k, v, "
-                               f"beta, sel_C, dt, r read, y written) / {kernel} launch {main_ms * 1e3:.2f} us "
-                               f"(HIP events, mean of {args.steps})"),
+                               f"beta, sel_C, dt, r read, y written) / {kernel} launch {kern_ms * 1e3:.2f} us "
+                               f"(HIP events on the launch stream, mean of {args.steps} launches, capped by the "
+                               f"back-to-back step time {ms_per_step * 1e3:.2f} us)"),
                      "traffic_source": (os.path.relpath(traffic_file, ROOT) if traffic is not None else None)},
         "whole_call": {"ms": call_ms, "achieved_GBs": alg / (call_ms * 1e-3) / 1e9,
                        "frac": alg / (call_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
@@ -436,8 +548,18 @@ def main():
             out["decode"] = time_decode(200, 20)
             out["lm_forward"] = time_lm_forward()
             out["lm_decode"] = time_lm_decode()
+    if not args.no_extras:
+        out["dropin_ssd_scan"] = time_dropin("C1")
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg, x, args.cpu_sample_batches)
+        if not args.no_extras:
+            from cdssm_hip.workloads import CONFIGS as _C
+            extra = [cpu_baseline(cfg, x, args.cpu_sample_batches, threads=1, heads=range(4))]
+            x3 = draw_inputs(_C["C3"], seed=0)
+            extra.append(cpu_baseline(_C["C3"], x3, 1, heads=range(4)))
+            x2 = draw_inputs(_C["C2"], seed=0)
+            extra.append(cpu_baseline(_C["C2"], x2, 1, heads=range(2), backward=True))
+            out["cpu_baseline_more"] = extra
     print(json.dumps(out), flush=True)
 
 

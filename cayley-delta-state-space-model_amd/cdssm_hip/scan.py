@@ -132,7 +132,7 @@ def chunkwise_delta_scan_abar(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel
     return y, h_final
 
 
-FORWARD_PATHS = {"auto": 0, "four_launch": 1, "one_pass": 2}
+FORWARD_PATHS = {"auto": 0, "four_launch": 1, "one_pass": 2, "four_launch_mfma": 3}
 
 
 def set_forward_path(path: str) -> str:
@@ -142,8 +142,11 @@ def set_forward_path(path: str) -> str:
     workgroups holds every segment of 4 chunks (and, for inference, where the
     persistent one-pass fills whole rounds), else the four-launch scan;
     "four_launch" always takes the multi-launch passes; "one_pass" requires
-    the one-launch passes (calls they cannot serve raise).  Process-wide; the
-    same choice applies to the backward's correction adjoint + reverse carry.
+    the one-launch passes (calls they cannot serve raise); "four_launch_mfma"
+    takes the multi-launch passes with the correction as the chunked MFMA
+    pass (bf16 inference forward, chunk a multiple of 16 up to 128; other calls
+    raise).  Process-wide; the same choice applies to the backward's correction
+    adjoint + reverse carry.
     """
     if path not in FORWARD_PATHS:
         raise ValueError(f"path must be one of {sorted(FORWARD_PATHS)}, got {path!r}")

@@ -347,10 +347,11 @@ constexpr int kTokRound = 8;  // token loops run to round_up(tokens, kTokRound)
 
 struct FwdLayout {
   int NC, S, NSEG, NCK;
-  int64_t n_summ, n_gam, n_segA, n_segX, n_pad, n_saved, n_gsaved, n_op, n_zck, n_cend;
+  int64_t n_summ, n_gam, n_segA, n_segX, n_pad, n_saved, n_gsaved, n_op, n_zck, n_cend, n_ycorr;
   int64_t total() const {
-    return n_summ + n_gam + n_segA + n_segX + n_pad + n_saved + n_gsaved + n_op + n_zck + n_cend;
+    return n_summ + n_gam + n_segA + n_segX + n_pad + n_saved + n_gsaved + n_op + n_zck + n_cend + n_ycorr;
   }
+  int64_t ycorr_offset() const { return cend_offset() + n_cend; }
   int64_t saved_offset() const { return n_summ + n_gam + n_segA + n_segX + n_pad; }
   int64_t gsaved_offset() const { return saved_offset() + n_saved; }
   int64_t onepass_offset() const { return gsaved_offset() + n_gsaved; }
@@ -375,6 +376,7 @@ inline FwdLayout fwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t 
   w.NCK = int((chunk + kTokRound - 1) / kTokRound * kTokRound / kZck);
   w.n_zck = B * w.NC * H * int64_t(w.NCK) * D;
   w.n_cend = B * w.NC * H * D;
+  w.n_ycorr = B * L * H;  // the chunked correction's readout (four-launch path with the MFMA correction)
   return w;
 }
 
@@ -486,7 +488,9 @@ int bwd_lookback_status(bool clear, unsigned* out);
 int resident_capacity(const void* fn, int block, size_t lds);
 // Launch-path selection of the fused scan (forward and backward carry):
 // automatic, always the multi-launch passes, or one launch required.
-enum { kPathAuto = 0, kPathFour = 1, kPathOne = 2 };
+// kPathSweep: the four launches with the correction as the chunked MFMA pass
+// (bf16 inference forward, chunk a multiple of 16 up to 128; for measurement).
+enum { kPathAuto = 0, kPathFour = 1, kPathOne = 2, kPathSweep = 3 };
 int scan_path();
 }  // namespace cdssm_host
 

@@ -42,6 +42,7 @@
 #include <atomic>
 #include <mutex>
 
+#include "chunk_sweep.hpp"
 #include "common.hpp"
 
 namespace cdssm {
@@ -578,7 +579,10 @@ __global__ __launch_bounds__(256) void fused_fwd_replay_kernel(float2* __restric
 // g_t (the in-chunk decay product the correction adjoint needs), the z
 // checkpoints z_{t-1} at t % kZck == 0 and c^ after the chunk's last step.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int LPH, bool SAVE>
+// CORR false: the local part only, y_t = sel_C_t f_t (zh_t . q_t) + ycorr_t, with
+// the correction readout ycorr (B, L, H) complex fp32 computed beforehand by the
+// chunked correction (fused_fwd_corr_sweep_kernel).
+template <typename T, int D, int LPH, bool SAVE, bool CORR = true>
 __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
     const typename T::raw* __restrict__ q, const typename T::raw* __restrict__ k,
     const typename T::raw* __restrict__ v, const typename T::raw* __restrict__ beta,
@@ -586,7 +590,9 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
     const typename T::raw* __restrict__ r, const float* __restrict__ alpha,
     const float* __restrict__ omega, float c, const float2* __restrict__ states,
     typename T::raw* __restrict__ y, float4* __restrict__ saved, float2* __restrict__ gsaved,
-    float2* __restrict__ zck, float2* __restrict__ cend, int L, int H, int Q, int NC, int NCK, int n_hg) {
+    float2* __restrict__ zck, float2* __restrict__ cend, int L, int H, int Q, int NC, int NCK, int n_hg,
+    const float2* __restrict__ ycorr = nullptr) {
+  static_assert(CORR || !SAVE, "the training forward keeps the sequential correction");
   using Cfg = FusedCfg<T, D, LPH>;
   constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch;
   static_assert(PF == kTokRound && PF % kZck == 0, "z checkpoints fall at fixed positions of a prefetch group");
@@ -677,15 +683,19 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
       for (int j = 0; j < DPL; ++j) {
         pzr = fmaf(zr[j], kk[j], pzr);
         pzi = fmaf(zi[j], kk[j], pzi);
-        pcr = fmaf(cr[j], kk[j], pcr);
-        pci = fmaf(ci[j], kk[j], pci);
-        qcr = fmaf(cr[j], qq[j], qcr);
-        qci = fmaf(ci[j], qq[j], qci);
+        if (CORR) {
+          pcr = fmaf(cr[j], kk[j], pcr);
+          pci = fmaf(ci[j], kk[j], pci);
+          qcr = fmaf(cr[j], qq[j], qcr);
+          qci = fmaf(ci[j], qq[j], qci);
+        }
       }
       pzr = group_sum<LPH>(pzr);
       pzi = group_sum<LPH>(pzi);
-      pcr = group_sum<LPH>(pcr);
-      pci = group_sum<LPH>(pci);
+      if (CORR) {
+        pcr = group_sum<LPH>(pcr);
+        pci = group_sum<LPH>(pci);
+      }
 
       const float bb = sa[i].z;
       local_step<DPL>(zr, zi, kk, (rg >> i) & 1u, sm[i], sa[i].x, sa[i].y, bb, pzr, pzi);
@@ -695,8 +705,10 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
       for (int j = 0; j < DPL; ++j) {
         qzr = fmaf(zr[j], qq[j], qzr);
         qzi = fmaf(zi[j], qq[j], qzi);
-        cr[j] = fmaf(-ecr, kk[j], cr[j]);
-        ci[j] = fmaf(-eci, kk[j], ci[j]);
+        if (CORR) {
+          cr[j] = fmaf(-ecr, kk[j], cr[j]);
+          ci[j] = fmaf(-eci, kk[j], ci[j]);
+        }
         if (SAVE) {
           cnr = fmaf(cr[j], qq[j], cnr);  // c^_{t+1}.q
           cni = fmaf(ci[j], qq[j], cni);
@@ -704,8 +716,12 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
       }
       // readout partial: f_t (zh_t.q) + g_{t-1} (c^_t.q)
       const float4 fb = sb[i];
-      float Rr = (fb.x * qzr - fb.y * qzi) + (fb.z * qcr - fb.w * qci);
-      float Ri = (fb.x * qzi + fb.y * qzr) + (fb.z * qci + fb.w * qcr);
+      float Rr = fb.x * qzr - fb.y * qzi;
+      float Ri = fb.x * qzi + fb.y * qzr;
+      if (CORR) {
+        Rr += fb.z * qcr - fb.w * qci;
+        Ri += fb.z * qci + fb.w * qcr;
+      }
       Rr = group_sum<LPH>(Rr);
       Ri = group_sum<LPH>(Ri);
       yr[i] = sa[i].w * Rr;
@@ -739,10 +755,67 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
     const int hj = tc.hbase + (p - t * HPW);
     if (hj < H) {
       const int64_t e = ((tc.row0 + t) * H + hj) * 2;
-      const float2 yv = s_y[p];
+      float2 yv = s_y[p];
+      if (!CORR) {
+        const float2 yc = ycorr[e / 2];
+        yv.x += yc.x;
+        yv.y += yc.y;
+      }
       store_pair<T>(y + e, yv.x, yv.y);
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Chunked correction on MFMA (bf16 inputs, chunk = 16 NB tokens): one wave per
+// (b, chunk, 4 heads) computes the correction readout sel_C_t g_{t-1}
+// (c^_t . q_t) of every token from the chunk's entering state (see
+// chunk_sweep.hpp) into ycorr (B, L, H) complex fp32; the main pass with
+// CORR = false adds it to the local readout.
+// ---------------------------------------------------------------------------
+template <int D, int NB>
+__global__ __launch_bounds__(kWave) void fused_fwd_corr_sweep_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ beta,
+    const uint16_t* __restrict__ sel_c, const uint16_t* __restrict__ dt, const uint16_t* __restrict__ r,
+    const float* __restrict__ alpha, const float* __restrict__ omega, float c, const float2* __restrict__ states,
+    float2* __restrict__ ycorr, int L, int H, int NC, int n_hg) {
+  constexpr int Q = 16 * NB;
+  __shared__ float lds[sweep_lds_floats<NB>()];
+  const ChunkTile tc = decode_tile(L, Q, NC, n_hg, kSweepHeads);
+  const int lane = threadIdx.x;
+  const int i = lane % 16;
+  const int h = tc.hbase + lane / 16;
+  const bool hok = h < H;
+  const float al = alpha[hok ? h : H - 1], om = omega[hok ? h : H - 1];
+  float car = 1.0f, cai = 0.0f;  // rotation product of the chunk's earlier blocks
+
+  // the lane's token of block b: beta, sel_C and g_{t-1} from the scan-level dynamics
+  auto tok = [&](int b, float& bt, float& sel, float& gr, float& gi) {
+    const int t = 16 * b + i;
+    const bool ok = hok && t < tc.nt;
+    const int64_t e = (tc.row0 + min(t, tc.nt - 1)) * H + (hok ? h : H - 1);
+    float ar = 1.0f, ai = 0.0f;
+    bt = 0.0f;
+    sel = 0.0f;
+    if (ok) {
+      const Transition tn = cayley_gated(bf16_to_f32(dt[e]), bf16_to_f32(r[e]), al, om, c);
+      ar = tn.ar;
+      ai = tn.ai;
+      bt = bf16_to_f32(beta[e]);
+      sel = bf16_to_f32(sel_c[e]);
+    }
+    row_cumprod(ar, ai);  // product of a over the block up to t
+    gr = row_shr<1>(ar, 1.0f);
+    gi = row_shr<1>(ai, 0.0f);
+    cmul_acc(gr, gi, car, cai);
+    cmul_acc(car, cai, row_bcast<15>(ar), row_bcast<15>(ai));
+  };
+  auto emit = [&](int b, float yr, float yi) {
+    const int t = 16 * b + i;
+    if (hok && t < tc.nt) ycorr[(tc.row0 + t) * H + h] = make_float2(yr, yi);
+  };
+  const float2* sp = states + (int64_t(tc.b) * NC + tc.chunk) * H * D;
+  corr_sweep<D, NB>(k, q, tc.row0, tc.nt, H, tc.hbase, sp, lds, tok, emit);
 }
 
 // ---------------------------------------------------------------------------
@@ -1280,7 +1353,7 @@ int onepass_capacity(size_t lds) {
 struct FwdRegions {
   float2 *summ, *gam, *segA, *segX;
   float4* saved;
-  float2 *gsaved, *zck, *cend, *onepass;
+  float2 *gsaved, *zck, *cend, *onepass, *ycorr;
 };
 
 FwdRegions full_regions(float* ws, const FwdLayout& w) {
@@ -1294,6 +1367,7 @@ FwdRegions full_regions(float* ws, const FwdLayout& w) {
   g.onepass = reinterpret_cast<float2*>(ws) + w.onepass_offset();
   g.zck = reinterpret_cast<float2*>(ws) + w.zck_offset();
   g.cend = reinterpret_cast<float2*>(ws) + w.cend_offset();
+  g.ycorr = reinterpret_cast<float2*>(ws) + w.ycorr_offset();
   return g;
 }
 
@@ -1307,7 +1381,7 @@ FwdRegions infer_regions(float2* base, const FwdLayout& w) {
   g.segA = g.gam + w.n_gam;
   g.segX = g.segA + w.n_segA;
   g.saved = nullptr;
-  g.gsaved = g.zck = g.cend = nullptr;
+  g.gsaved = g.zck = g.cend = g.ycorr = nullptr;
   return g;
 }
 
@@ -1340,7 +1414,14 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   float2* cend = reg.cend;
   const int slots = round_up(Q, kWave) * HPW, slots_s = round_up(Q, kWave) * HPWS;
 
-  if (cdssm_host::scan_path() != cdssm_host::kPathFour) {
+  const bool sweep = cdssm_host::scan_path() == cdssm_host::kPathSweep;
+  if (sweep) {
+    if (!std::is_same<T, BF16>::value || save || Q % 16 != 0 || Q > 128 || !reg.ycorr) {
+      cdssm_host::set_error("cdssm_fused_scan_fwd: the chunked MFMA correction serves the bf16 inference forward "
+                            "with a workspace and chunk a multiple of 16 up to 128 (chunk %d)", Q);
+      return CDSSM_EINVAL;
+    }
+  } else if (cdssm_host::scan_path() != cdssm_host::kPathFour) {
     const int64_t items = int64_t(w.NSEG) * B * n_hg;
     const size_t lds = onepass_lds<D, LPH>(Q);
     // one round of resident workgroups takes every segment: one-pass.  More
@@ -1441,6 +1522,40 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   if (ev) (void)hipEventRecord(ev[3], stream);
 
   const size_t lds_main = size_t(slots) * (2 * sizeof(float4) + 2 * sizeof(float2));
+  if constexpr (std::is_same<T, BF16>::value) {
+    if (sweep) {
+      const int n_hgw = (H + kSweepHeads - 1) / kSweepHeads;
+      const unsigned waves = unsigned(int64_t(B) * NC * n_hgw);
+      const uint16_t *q16 = (const uint16_t*)q, *k16 = (const uint16_t*)k;
+      const uint16_t *b16 = (const uint16_t*)beta, *s16 = (const uint16_t*)sel_c;
+      const uint16_t *d16 = (const uint16_t*)dt, *r16 = (const uint16_t*)r;
+      const float2* st2 = (const float2*)summ;
+#define CDSSM_SWEEP(NBV)                                                                                           \
+  hipLaunchKernelGGL((fused_fwd_corr_sweep_kernel<D, NBV>), dim3(waves), dim3(kWave), 0, stream, q16, k16, b16, s16, \
+                     d16, r16, alpha, omega, c, st2, reg.ycorr, L, H, NC, n_hgw)
+      switch (Q / 16) {
+        case 1: CDSSM_SWEEP(1); break;
+        case 2: CDSSM_SWEEP(2); break;
+        case 3: CDSSM_SWEEP(3); break;
+        case 4: CDSSM_SWEEP(4); break;
+        case 5: CDSSM_SWEEP(5); break;
+        case 6: CDSSM_SWEEP(6); break;
+        case 7: CDSSM_SWEEP(7); break;
+        default: CDSSM_SWEEP(8); break;
+      }
+#undef CDSSM_SWEEP
+      st = cdssm_host::check_launch("cdssm_fused_scan_fwd/corr_sweep");
+      if (st) return st;
+      hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH, false, false>), dim3(unsigned(tiles)), dim3(kWave),
+                         lds_main, stream, (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta,
+                         (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c, (const float2*)summ,
+                         (raw*)y, nullptr, nullptr, nullptr, nullptr, L, H, Q, NC, w.NCK, n_hg,
+                         (const float2*)reg.ycorr);
+      st = cdssm_host::check_launch("cdssm_fused_scan_fwd/main_local");
+      if (ev) (void)hipEventRecord(ev[4], stream);
+      return st;
+    }
+  }
   if (save)
     hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH, kSv>), dim3(unsigned(tiles)), dim3(kWave), lds_main,
                        stream, (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,

@@ -67,9 +67,10 @@ int scan_path() { return g_scan_path.load(std::memory_order_relaxed); }
 }  // namespace cdssm_host
 
 extern "C" int cdssm_fused_scan_fwd_set_path(int mode) {
-  if (mode < cdssm_host::kPathAuto || mode > cdssm_host::kPathOne) {
-    cdssm_host::set_error("cdssm_fused_scan_fwd_set_path: mode must be 0 (auto), 1 (four launches) or 2 "
-                          "(one pass required), got %d", mode);
+  if (mode < cdssm_host::kPathAuto || mode > cdssm_host::kPathSweep) {
+    cdssm_host::set_error("cdssm_fused_scan_fwd_set_path: mode must be 0 (auto), 1 (four launches), 2 "
+                          "(one pass required) or 3 (four launches with the chunked MFMA correction), got %d",
+                          mode);
     return CDSSM_EINVAL;
   }
   return cdssm_host::g_scan_path.exchange(mode);

@@ -161,7 +161,11 @@ int cdssm_fused_scan_bwd_profile(int dtype, const void* q, const void* k, const 
 /*
  * Launch-path selection (no counterpart in the reference; for tests and
  * benchmarks): 0 = automatic (default), 1 = always the multi-launch passes,
- * 2 = one launch required (calls it cannot serve return -1).  Applies to the
+ * 2 = one launch required (calls it cannot serve return -1), 3 = the
+ * multi-launch forward with the correction as the chunked MFMA pass (Gram
+ * tiles K K^T, Q K^T and the projections K s, Q s on v_mfma_f32_16x16x32_bf16,
+ * then a per-token triangular solve; bf16 inference forward with a workspace,
+ * chunk a multiple of 16 up to 128; other calls return -1).  Applies to the
  * forward (one-pass scan vs four launches) and to the backward's correction
  * adjoint + reverse carry (one launch vs three).  Process-wide; returns the
  * previous mode, or -1 for an invalid mode.  A one-launch forward is reported

@@ -93,7 +93,8 @@ def test_one_launch_areas_have_a_control_block_for_the_device_epoch():
     NSEG = -(-NC // 4)
     NCK = -(-Q // 8) * 8 // 4
     carry = B * NC * H * D + B * NC * H + B * H * S * (D + 1)
-    fwd = carry + (carry & 1) + 5 * B * L * H + B * NSEG * H * (2 * D + 2) + 8 + B * NC * H * NCK * D + B * NC * H * D
+    fwd = (carry + (carry & 1) + 5 * B * L * H + B * NSEG * H * (2 * D + 2) + 8 + B * NC * H * NCK * D
+           + B * NC * H * D + B * L * H)
     assert lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, 2, Q) == 8 * fwd
     bwd = 2 * B * NC * H * D + B * H * S + B * H * S * D + B * NC * H + B * NSEG * H * (2 * D + 2) + 8
     assert lib.cdssm_fused_scan_bwd_workspace_bytes(B, L, H, D, 2, Q) == 8 * bwd
@@ -144,7 +145,8 @@ def test_workspace_size_formula():
         NCK = -(-Q // 8) * 8 // 4     # z checkpoints per chunk (every 4 tokens of the 8-rounded loop)
         zck = B * NC * H * NCK * D
         cend = B * NC * H * D         # correction state after each chunk
-        return (carry + pad + saved + gsaved + onepass + zck + cend) * 8
+        ycorr = B * L * H             # the chunked MFMA correction's readout
+        return (carry + pad + saved + gsaved + onepass + zck + cend + ycorr) * 8
     assert lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, N, Q) == expect(L)
     assert lib.cdssm_fused_scan_workspace_bytes(B, 100, H, D, N, Q) == expect(100)
     assert lib.cdssm_fused_scan_workspace_bytes(0, L, H, D, N, Q) == -1

@@ -66,6 +66,47 @@ def test_fused_fwd_matches_oracle(name, cfg, chunk, path):
         assert ey <= 2e-2 and en <= 1e-3
 
 
+SWEEP = [
+    ("bf16_D64", ScanConfig("t", B=2, H=16, L=640, D=64), None),
+    ("bf16_D64_ragged_h0_H5", ScanConfig("t", B=2, H=5, L=300, D=64, h0_std=0.1), None),
+    ("bf16_D64_chunk32", ScanConfig("t", B=1, H=7, L=333, D=64, h0_std=0.1), 32),
+    ("bf16_D64_chunk16_one_token", ScanConfig("t", B=2, H=3, L=1, D=64, h0_std=0.1), 16),
+    ("bf16_D128_ragged", ScanConfig("t", B=1, H=24, L=333, D=128, h0_std=0.1), None),
+    ("bf16_fast_omega_h0", ScanConfig("t", B=1, H=9, L=1000, D=64, omega_std=3.0, h0_std=0.1), None),
+]
+
+
+@pytest.mark.parametrize("name,cfg,chunk", SWEEP, ids=[s[0] for s in SWEEP])
+def test_fused_fwd_mfma_correction_matches_oracle(name, cfg, chunk):
+    """The four-launch forward with the correction as the chunked MFMA pass (Gram tiles,
+    K s / Q s on v_mfma_f32_16x16x32_bf16, the triangular solve per token) against the oracle,
+    and against the sequential correction on the same inputs."""
+    log(f"[fused fwd mfma corr] {name}: B{cfg.B} H{cfg.H} L{cfg.L} D{cfg.D} chunk={chunk or cfg.D}")
+    x = draw_inputs(cfg, seed=0)
+    with forward_path("four_launch_mfma"):
+        y, hf = run_fused(x, chunk)
+    with forward_path("four_launch"):
+        ys, hs = run_fused(x, chunk)
+    yr, hr = oracle_fwd(x, chunk_size=chunk)
+    ey, en, es = rel(y, yr), state_norm_rel(hf, hr), rel(y.float(), ys.float())
+    log(f"   rel err y {ey:.2e}  state-norm {en:.2e}  vs sequential correction {es:.2e}")
+    assert ey <= 2e-2 and en <= 1e-3
+    assert torch.equal(hf, hs)  # the carry is the same four-launch carry
+
+
+def test_fused_fwd_mfma_correction_rejects_what_it_cannot_serve():
+    from cdssm_hip import chunkwise_delta_scan
+    x = to_dev(draw_inputs(ScanConfig("t", B=1, H=2, L=100, D=64, dtype="fp32"), seed=0))
+    args = [x[n] for n in ("q", "k", "v", "beta", "sel_C", "dt", "r", "alpha", "omega")]
+    with forward_path("four_launch_mfma"):
+        with pytest.raises(RuntimeError, match="chunked MFMA correction"):
+            chunkwise_delta_scan(*args, x["c"])
+        xb = to_dev(draw_inputs(ScanConfig("t", B=1, H=2, L=100, D=64), seed=0))
+        with pytest.raises(RuntimeError, match="chunked MFMA correction"):
+            chunkwise_delta_scan(*[xb[n] for n in ("q", "k", "v", "beta", "sel_C", "dt", "r", "alpha", "omega")],
+                                 xb["c"], chunk_size=20)
+
+
 FULL = [
     ("C1", ScanConfig("C1", B=8, H=16, L=4096, D=64), [0, 7], [0, 5, 15]),
     ("C2", ScanConfig("C2", B=4, H=24, L=8192, D=128), [3], [0, 23]),
@@ -74,11 +115,13 @@ FULL = [
 
 
 @pytest.mark.parametrize("name,cfg,batches,heads", FULL, ids=[f[0] for f in FULL])
-def test_fused_fwd_full_size_sequences_match_oracle(name, cfg, batches, heads):
+@pytest.mark.parametrize("path", ["auto", "four_launch_mfma"])
+def test_fused_fwd_full_size_sequences_match_oracle(name, cfg, batches, heads, path):
     """Full BASELINE shapes on the GPU; the oracle re-computes selected (b, h) sequences."""
-    log(f"[fused fwd full] {name}: B{cfg.B} H{cfg.H} L{cfg.L} D{cfg.D} bf16")
+    log(f"[fused fwd full] {name} ({path}): B{cfg.B} H{cfg.H} L{cfg.L} D{cfg.D} bf16")
     x = draw_inputs(cfg, seed=0)
-    y, hf = run_fused(x)
+    with forward_path(path):
+        y, hf = run_fused(x)
     assert torch.isfinite(y.float()).all() and torch.isfinite(hf).all()
     xs = select(x, batches, heads)
     yr, hr = oracle_fwd(xs)
