@@ -9,8 +9,10 @@ with q.k (HIP) -> fused scan with the sel_C readout on the gate-level A_bar /
 vp (HIP, ``cdssm_fused_scan_fwd_abar``) -> current-token shortcut (HIP) ->
 readout_proj -> fp32 GroupNorm, * silu(z), + D x (HIP) -> out_proj with the
 residual in the GEMM epilogue.  Dense projections and the embedding are
-PyTorch (hipBLASLt GEMMs).  The block is forward-only (the fused kernels carry no
-autograd graph; it raises under autograd); Conv1dSiLU alone has its backward.
+PyTorch (hipBLASLt GEMMs).  With gradients enabled (training) the block takes a
+differentiable path instead: conv1d+SiLU, DynamicsFusedFn, NormalizeKQFn and
+SSDChunkwiseScan over the per-pass scan ops (HIP, with the reference's
+backward rules) and torch for the rest.
 
 Generation: ``CDSSMLMHeadModel.prefill`` runs the forward over a prompt and keeps
 per-layer decode state (conv window, the scan's R-mode state, GroupNorm running
@@ -28,7 +30,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib
-from .ops import DynamicsFusedFn
+from .ops import DynamicsFusedFn, NormalizeKQFn
 from .decode import DecodeState, decode_step_abar, prefill_abar
 from .scan import chunkwise_delta_scan_abar
 from .ssd import SSDChunkwiseScan
@@ -449,6 +451,10 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(d_model))
 
     def forward(self, x: Tensor) -> Tensor:
+        if torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad):
+            # training: the reference's expression (modules.py:49-53), differentiable through torch
+            x32 = x.float()
+            return (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + self.eps)).to(x.dtype) * self.weight
         return rms_norm(x, self.weight, self.eps)
 
 
@@ -542,9 +548,10 @@ class CDSSMBlock(nn.Module):
         if N != 2 and cache is not None:
             raise NotImplementedError("decode caches need state_dim = 2 (the decode kernels' state layout)")
         if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
-            # the fused block kernels carry no autograd graph: a backward would silently miss them
-            raise RuntimeError("CDSSMBlock is forward-only here: call it under torch.no_grad() or "
-                               "torch.inference_mode(), or freeze its parameters")
+            # training: the fused block kernels carry no autograd graph, so take the differentiable path
+            if cache is not None:
+                raise RuntimeError("decode caches are filled under torch.no_grad() / torch.inference_mode()")
+            return self._forward_autograd(x, v_first)
         B, L, _ = x.shape
         residual = x
         proj = self.in_proj(self.norm(x))  # (B, L, 3 Di + H N); z, x_gate and K are read in place
@@ -603,6 +610,45 @@ class CDSSMBlock(nn.Module):
         # out_proj with the residual added in the GEMM epilogue
         out = torch.addmm(residual.reshape(B * L, -1), y.reshape(B * L, Di), self.out_proj.weight.t())
         return out.reshape(residual.shape), v_first
+
+    def _forward_autograd(self, x: Tensor, v_first: Optional[Tensor]):
+        """The block with gradients (block.py:140-229, for training): the HIP ops that have a backward --
+        conv1d+SiLU (CUDAConv1dSiLUOp), DynamicsFusedFn, NormalizeKQFn and SSDChunkwiseScan over the
+        per-pass scan ops, whose backwards are the reference's -- and torch for the projections, the
+        RMSNorm, the shortcut, the readout and the fp32 GroupNorm.  The readout and shortcut are formed as
+        sum_d Y q + s (q.k)^2 V_gated (the reference adds s (q.k) V_gated k^T to Y and reads it with q:
+        the same value) with elementwise products in the compute dtype."""
+        cfg = self.config
+        N, H, D, Di = cfg.state_dim, cfg.n_heads, cfg.head_dim, cfg.d_inner
+        B, L, _ = x.shape
+        residual = x
+        proj = self.in_proj(self.norm(x))
+        z, x_gate, K, V = proj.split([Di, Di, Di, H * N], dim=-1)                     # block.py:162-166
+        K = K.reshape(B, L, H, D)
+        V = V.reshape(B, L, H, N)
+        if v_first is None:                                                           # block.py:169-174
+            v_first = V.detach()
+        else:
+            V = torch.lerp(v_first, V, torch.sigmoid(self.v_residual_gate)[None, None, :, None].to(V.dtype))
+        x_conv = self.conv(x_gate)                                                    # block.py:177
+        gates = self.gate_proj(x_conv)
+        A_bar, vp, beta, sel_C = DynamicsFusedFn.apply(
+            gates, self.log_dt_scale.float(), self.rope_freqs, cfg.gating_c, cfg.bf16_omega_thresh,
+            cfg.bf16_delta, cfg.bf16_smoothness, cfg.eps_adaptive_dt, H, N)           # block.py:184-188
+        Q = self.Q_proj(x_conv).reshape(B, L, H, D)
+        K, Q = NormalizeKQFn.apply(K, Q)                                              # block.py:191-192
+        V_gated = V * vp.repeat_interleave(2, dim=-1)                                 # block.py:194-195
+        Y = SSDChunkwiseScan(cfg.chunk_size, N)(A_bar, K, V_gated, beta)              # block.py:198
+        qk = (Q * K).sum(-1)                                                          # block.py:202
+        retrieved = (Y * Q.unsqueeze(-2)).sum(-1) \
+            + self.shortcut_scale * (qk * qk).unsqueeze(-1) * V_gated                 # block.py:204-208
+        retrieved = retrieved * sel_C.unsqueeze(-1)                                   # block.py:211
+        y = self.readout_proj(retrieved.reshape(B, L, H * N))
+        y = torch.nn.functional.group_norm(y.float().transpose(1, 2), self.ssm_norm.num_groups,
+                                           self.ssm_norm.weight.float(), self.ssm_norm.bias.float(),
+                                           self.ssm_norm.eps).to(y.dtype).transpose(1, 2)  # block.py:216-223
+        y = y * torch.nn.functional.silu(z) + self.D * x_conv
+        return residual + self.out_proj(y.to(self.out_proj.weight.dtype)), v_first
 
     def step(self, x: Tensor, v_first: Optional[Tensor], cache: dict):
         """One decode token: x (B, d_model) at position cache["l"] -> (x + block(x), v_first (B, H, N)),

@@ -64,8 +64,12 @@ def _linear(x: Tensor, w: Tensor, b: Optional[Tensor] = None) -> Tensor:
     return y if b is None else y + b
 
 
-def block_forward(p: dict, pre: str, x: Tensor, v_first: Optional[Tensor], cfg) -> tuple:
-    """One CDSSMBlock.forward (block.py:140-229) with the block's parameters p[pre + name]."""
+def block_forward(p: dict, pre: str, x: Tensor, v_first: Optional[Tensor], cfg, grad_mode: str = "exact") -> tuple:
+    """One CDSSMBlock.forward (block.py:140-229) with the block's parameters p[pre + name].
+
+    grad_mode "reference" attaches the reference's own backward rules where they are not the exact
+    derivative of the forward: DynamicsFusedFn.backward (dynamics_fused.cu:145-387) and
+    ExactCorrectionFn.backward (exact_correction.cu:169-383); "exact" differentiates the forward."""
     N, H, D, Di = cfg.state_dim, cfg.n_heads, cfg.head_dim, cfg.d_inner
     B, L, _ = x.shape
     g = lambda n: p[pre + n]  # noqa: E731
@@ -75,21 +79,22 @@ def block_forward(p: dict, pre: str, x: Tensor, v_first: Optional[Tensor], cfg) 
     K = K.reshape(B, L, H, D)
     V = V.reshape(B, L, H, N)
     if v_first is None:                                                 # block.py:169-174
-        v_first = V
+        v_first = V.detach()                                            # layer 0's values, no gradient path
     else:
         V = torch.lerp(v_first, V, torch.sigmoid(g("v_residual_gate"))[None, None, :, None])
     x_conv = conv1d_silu(x_gate, g("conv.weight"), g("conv.bias"))      # block.py:177
     gates = _linear(x_conv, g("gate_proj.weight"), g("gate_proj.bias"))
     rope = 1.0 / (cfg.rope_base ** (torch.arange(0, H, dtype=x.dtype) / H))   # block.py:59-62
-    A_bar, vp, beta, sel_C = o.dynamics_fused_fwd(gates, g("log_dt_scale"), rope, cfg.gating_c,
-                                                  cfg.bf16_omega_thresh, cfg.bf16_delta, cfg.bf16_smoothness,
-                                                  cfg.eps_adaptive_dt, H, N)   # block.py:184-188
+    dyn = o.dynamics_with_reference_grad if grad_mode == "reference" else o.dynamics_fused_fwd
+    A_bar, vp, beta, sel_C = dyn(gates, g("log_dt_scale"), rope, cfg.gating_c, cfg.bf16_omega_thresh,
+                                 cfg.bf16_delta, cfg.bf16_smoothness, cfg.eps_adaptive_dt, H, N)   # block.py:184-188
     Q = _linear(x_conv, g("Q_proj.weight")).reshape(B, L, H, D)
     K, Q = o.normalize_kq(K, Q)                                         # block.py:191-192
     V_gated = V * vp.repeat_interleave(2, dim=-1)                       # block.py:194-195
-    Y = o.ssd_chunkwise_scan(A_bar, K, V_gated, beta, cfg.chunk_size, N)   # block.py:198
+    corr = o.correction_with_reference_grad if grad_mode == "reference" else None
+    Y = o.ssd_chunkwise_scan(A_bar, K, V_gated, beta, cfg.chunk_size, N, correction_fn=corr)   # block.py:198
     retrieved = o.readout(Y, Q, sel_C, K=K, V_gated=V_gated,
-                          shortcut_scale=float(g("shortcut_scale").reshape(-1)[0]))  # block.py:202-211
+                          shortcut_scale=g("shortcut_scale").reshape(()))  # block.py:202-211
     y = _linear(retrieved.reshape(B, L, H * N), g("readout_proj.weight"))
     y = F.group_norm(y.transpose(1, 2), cfg.ssm_norm_groups, g("ssm_norm.weight"), g("ssm_norm.bias"),
                      1e-5).transpose(1, 2)                              # block.py:216-223 (nn.GroupNorm eps)
@@ -111,11 +116,11 @@ def group_norm_running_sums(y: Tensor, num_groups: int) -> Tensor:
     return torch.stack([k0, d.sum((1, 3)), (d * d).sum((1, 3)), n], dim=-1)
 
 
-def lm_forward(p: dict, input_ids: Tensor, cfg) -> Tensor:
-    """CDSSMLMHeadModel.forward (model.py:38-51): logits (B, L, vocab)."""
+def lm_forward(p: dict, input_ids: Tensor, cfg, grad_mode: str = "exact") -> Tensor:
+    """CDSSMLMHeadModel.forward (model.py:38-51): logits (B, L, vocab); grad_mode as block_forward."""
     x = p["embedding.weight"][input_ids]
     v_first = None
     for i in range(cfg.n_layers):
-        x, v_first = block_forward(p, f"blocks.{i}.", x, v_first, cfg)
+        x, v_first = block_forward(p, f"blocks.{i}.", x, v_first, cfg, grad_mode)
     x = rms_norm(x, p["final_norm.weight"], 2.0 ** -14)   # RMSNorm default eps (modules.py:46)
     return x @ p["embedding.weight"].transpose(0, 1)       # tied head (model.py:29-30)

@@ -488,8 +488,9 @@ def exact_recurrence(A_bar: Tensor, K: Tensor, V: Tensor, beta: Tensor, state_di
 
 def readout(Y: Tensor, Qn: Tensor, sel_C: Tensor, K: Optional[Tensor] = None,
             V_gated: Optional[Tensor] = None, shortcut_scale: float = 0.0) -> Tensor:
-    """Shortcut + readout + sel_C gate (block.py:202-211): y = sel_C * (Y q)."""
-    if shortcut_scale != 0.0:
+    """Shortcut + readout + sel_C gate (block.py:202-211): y = sel_C * (Y q).  shortcut_scale may be a
+    tensor (the block's parameter, so that it receives a gradient)."""
+    if isinstance(shortcut_scale, torch.Tensor) or shortcut_scale != 0.0:
         qk = (Qn * K).sum(-1)
         Y = Y + shortcut_scale * qk[..., None, None] * V_gated.unsqueeze(-1) * K.unsqueeze(-2)
     return torch.einsum('blhsd,blhd->blhs', Y, Qn) * sel_C.unsqueeze(-1)
@@ -626,6 +627,32 @@ class _CorrectionRefGrad(torch.autograd.Function):
 
 def correction_with_reference_grad(A_chunk, K_chunk, beta_chunk, chunk_states, state_dim):
     return _CorrectionRefGrad.apply(A_chunk, K_chunk, beta_chunk, chunk_states, state_dim)
+
+
+class _DynamicsRefGrad(torch.autograd.Function):
+    """dynamics_fused_fwd whose backward is the reference's analytic rule (dynamics_fused_bwd_ref);
+    gradients for gate_raw and log_dt_scale, None for the rest (ops.py:68-81)."""
+
+    @staticmethod
+    def forward(ctx, gate_raw, log_dt_scale, rope_freqs, gating_c, omega_thresh, adt_delta, adt_smoothness,
+                adt_eps, n_heads, state_dim):
+        ctx.save_for_backward(gate_raw, log_dt_scale, rope_freqs)
+        ctx.args = (gating_c, omega_thresh, adt_delta, adt_smoothness, adt_eps, n_heads, state_dim)
+        return dynamics_fused_fwd(gate_raw, log_dt_scale, rope_freqs, *ctx.args)
+
+    @staticmethod
+    def backward(ctx, gA, gvp, gbeta, gsel):
+        gate_raw, log_dt_scale, rope_freqs = ctx.saved_tensors
+        with torch.no_grad():
+            g_raw, g_lds = dynamics_fused_bwd_ref(gA, gvp, gbeta, gsel, gate_raw, log_dt_scale, rope_freqs,
+                                                  *ctx.args)
+        return g_raw, g_lds.to(log_dt_scale.dtype), None, None, None, None, None, None, None, None
+
+
+def dynamics_with_reference_grad(gate_raw, log_dt_scale, rope_freqs, gating_c, omega_thresh, adt_delta,
+                                 adt_smoothness, adt_eps, n_heads, state_dim):
+    return _DynamicsRefGrad.apply(gate_raw, log_dt_scale, rope_freqs, gating_c, omega_thresh, adt_delta,
+                                  adt_smoothness, adt_eps, n_heads, state_dim)
 
 
 # --------------------------------------------------------------------------
