@@ -69,6 +69,8 @@ def parse():
                     help="skip the decode and config-4 LM timings (profiling runs)")
     ap.add_argument("--forward-path", default="auto", choices=["auto", "four_launch", "one_pass", "four_launch_mfma"],
                     help="how the forward is launched (default: the library's own choice)")
+    ap.add_argument("--only-dropin", action="store_true",
+                    help="only time the drop-in SSDChunkwiseScan at C1 (fused and per-pass) and print its JSON")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a device copy of this many MiB (read + write), 10 times, and exit: "
                          "the reference kernel for scaling HBM byte counters")
@@ -164,11 +166,12 @@ def training_record_bytes(cfg):
 
 def time_dropin(cfg_name, steps=10, warmup=2):
     """The drop-in path unchanged reference callers get (ssd.py:83-100 through the reference's own op
-    classes): SSDChunkwiseScan(chunk, 2) over the per-pass HIP ops (intra-chunk scan, inter-chunk
-    carry, exact correction, Y = local_h + correction), materialising Y (B,L,H,N,D) bf16 as the
-    reference does.  Forward alone and forward + backward (autograd with dY ~ N(0,1)).  Algorithmic
-    bytes of this interface: read A_bar, K, V, beta, write Y = B*H*L*((D + 2N + 1) + N*D)*2 forward;
-    the backward reads dY and the inputs and writes their gradients (the same count again)."""
+    classes): SSDChunkwiseScan(chunk, 2) materialising Y (B,L,H,N,D) bf16 as the reference does, in its
+    two executions -- the fused kernels (the module's choice for N = 2: cdssm_ssd_scan_fwd / _bwd) and
+    the per-pass ops (intra-chunk scan, inter-chunk carry, exact correction, Y = local_h + correction,
+    fused=False).  Forward alone and forward + backward (autograd with dY ~ N(0,1)).  Algorithmic bytes
+    of this interface: the forward reads A_bar, K, V, beta and writes Y, B*H*L*((D + 2N + 1) + N*D)*2;
+    the backward reads dY and the inputs and writes their gradients, B*H*L*(N*D + 2*(D + 2N + 1))*2."""
     import torch
     from cdssm_hip.ssd import SSDChunkwiseScan
     from cdssm_hip.workloads import CONFIGS, draw_inputs
@@ -190,8 +193,12 @@ def time_dropin(cfg_name, steps=10, warmup=2):
     V = (x["v"].to(dev).float() * vp[..., None]).to(torch.bfloat16)
     K = x["k"].to(dev)
     beta = x["beta"].to(dev)
-    scan = SSDChunkwiseScan(cfg.D, 2)
     stream = torch.cuda.current_stream(dev)
+    gY = torch.randn(cfg.B, cfg.L, cfg.H, 2, cfg.D, generator=torch.Generator().manual_seed(3)).to(
+        torch.bfloat16).to(dev)
+    BHL, D, N = cfg.B * cfg.H * cfg.L, cfg.D, 2
+    by_f = BHL * ((D + 2 * N + 1) + N * D) * 2
+    by_b = BHL * (N * D + 2 * (D + 2 * N + 1)) * 2
 
     def timed(fn):
         for _ in range(warmup):
@@ -205,25 +212,52 @@ def time_dropin(cfg_name, steps=10, warmup=2):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps
 
-    with torch.no_grad():
-        ms_f = timed(lambda: scan(A, K, V, beta))
-    leaves = [t.detach().clone().requires_grad_(True) for t in (A, K, V, beta)]
-    gY = torch.randn(cfg.B, cfg.L, cfg.H, 2, cfg.D, generator=torch.Generator().manual_seed(3)).to(
-        torch.bfloat16).to(dev)
+    def leg(fused):
+        scan = SSDChunkwiseScan(cfg.D, 2, fused=fused)
+        with torch.no_grad():
+            ms_f = timed(lambda: scan(A, K, V, beta))
+        leaves = [t.detach().clone().requires_grad_(True) for t in (A, K, V, beta)]
 
-    def fb():
-        Y = scan(*leaves)
-        Y.backward(gY)
+        def fb():
+            Y = scan(*leaves)
+            Y.backward(gY)
 
-    ms_fb = timed(fb)
-    BHL, D, N = cfg.B * cfg.H * cfg.L, cfg.D, 2
-    by_f = BHL * ((D + 2 * N + 1) + N * D) * 2
-    return {"workload": f"drop-in SSDChunkwiseScan (per-pass ops), {cfg.name} B{cfg.B} H{cfg.H} L{cfg.L} D{D} bf16",
-            "fwd_ms": ms_f, "fwd_tokens_per_s": cfg.B * cfg.L / (ms_f * 1e-3),
-            "fwd_hbm_frac": by_f / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS,
-            "fwd_bwd_ms": ms_fb, "fwd_bwd_tokens_per_s": cfg.B * cfg.L / (ms_fb * 1e-3),
-            "fwd_bwd_hbm_frac": 2 * by_f / (ms_fb * 1e-3) / 1e9 / HBM_PEAK_GBS,
-            "alg_bytes_fwd": by_f}
+        ms_fb = timed(fb)
+        return {"fwd_ms": ms_f, "fwd_tokens_per_s": cfg.B * cfg.L / (ms_f * 1e-3),
+                "fwd_hbm_frac": by_f / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                "fwd_bwd_ms": ms_fb, "fwd_bwd_tokens_per_s": cfg.B * cfg.L / (ms_fb * 1e-3),
+                "fwd_bwd_hbm_frac": (by_f + by_b) / (ms_fb * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+    def graphed(fn):
+        """GPU time per call without the host's per-call work: the call captured once in a HIP graph
+        (torch.cuda.graph) and replayed back to back."""
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                fn()
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        return timed(graph.replay)
+
+    from cdssm_hip.scan import ssd_scan_bwd, ssd_scan_fwd
+    out = {"workload": f"drop-in SSDChunkwiseScan, {cfg.name} B{cfg.B} H{cfg.H} L{cfg.L} D{D} bf16",
+           "alg_bytes_fwd": by_f, "alg_bytes_bwd": by_b}
+    out["fused"] = leg(None)
+    g_f = graphed(lambda: ssd_scan_fwd(A, K, V, beta, cfg.D))
+    g_fb = graphed(lambda: ssd_scan_bwd(gY, A, K, V, beta, ssd_scan_fwd(A, K, V, beta, cfg.D, train=True)[2], cfg.D))
+    out["fused"].update({"graph_fwd_ms": g_f, "graph_fwd_hbm_frac": by_f / (g_f * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                         "graph_fwd_bwd_ms": g_fb,
+                         "graph_fwd_bwd_hbm_frac": (by_f + by_b) / (g_fb * 1e-3) / 1e9 / HBM_PEAK_GBS})
+    out["per_pass"] = leg(False)
+    out["note"] = ("fused: cdssm_ssd_scan_fwd / cdssm_ssd_scan_bwd (its training forward also writes the backward's "
+                   "records into the workspace); per_pass: the reference's op sequence over the per-pass kernels; "
+                   "*_ms: back-to-back module calls (host work per call included); graph_*: the same kernels "
+                   "replayed from a captured graph (GPU time)")
+    return out
 
 
 def time_decode(steps, warmup, B=64, H=16, D=64, prompt=2048):
@@ -433,6 +467,9 @@ def main():
 
     if args.copy_probe_mib:
         copy_probe(args.copy_probe_mib)
+        return
+    if args.only_dropin:
+        print(json.dumps({"dropin_ssd_scan": time_dropin("C1", steps=args.steps, warmup=args.warmup)}), flush=True)
         return
 
     import torch

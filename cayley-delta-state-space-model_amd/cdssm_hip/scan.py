@@ -307,6 +307,115 @@ def chunkwise_delta_scan_train(q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0=
     return ChunkwiseDeltaScanFn.apply(q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0, chunk_size)
 
 
+def _validate_ssd(A_bar, K, V, beta, chunk_size):
+    named = dict(A_bar=A_bar, K=K, V=V, beta=beta)
+    for n, t in named.items():
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{n} must be a tensor")
+    dev = K.device
+    if dev.type != "cuda":
+        raise RuntimeError("the fused SSD scan runs on the GPU only: inputs must be on a cuda device")
+    if K.dim() != 4:
+        raise ValueError(f"K must be (B, L, H, D), got {tuple(K.shape)}")
+    B, L, H, D = K.shape
+    N = V.shape[-1] if V.dim() == 4 else -1
+    shapes = dict(A_bar=(B, L, H, N), V=(B, L, H, N), beta=(B, L, H))
+    for n, shp in shapes.items():
+        if tuple(named[n].shape) != shp:
+            raise ValueError(f"{n} has shape {tuple(named[n].shape)}, expected {shp}")
+    dtype = K.dtype
+    if dtype not in _lib.DTYPE_CODE:
+        raise TypeError(f"inputs must be float32 or bfloat16, got {dtype}")
+    for n, t in named.items():
+        if t.dtype != dtype or t.device != dev:
+            raise TypeError(f"{n} is {t.dtype} on {t.device}, expected {dtype} on {dev} (as K)")
+    if N != 2:
+        raise ValueError(f"the fused SSD scan supports N = 2 (one complex pair per head), got N = {N}")
+    if D not in (64, 128):
+        raise ValueError(f"head_dim D must be 64 or 128, got {D}")
+    Q = int(chunk_size)
+    if not 1 <= Q <= 128:
+        raise ValueError(f"chunk_size must be in [1, 128], got {Q}")
+    return B, L, H, D, N, Q, dtype
+
+
+def ssd_scan_fwd(A_bar: Tensor, K: Tensor, V: Tensor, beta: Tensor, chunk_size: int,
+                 train: bool = False) -> Tuple[Tensor, Tensor, Tensor]:
+    """The SSDChunkwiseScan interface on the fused kernels (cdssm_ssd_scan_fwd).
+
+    A_bar (B,L,H,2), K (B,L,H,D), V (B,L,H,2) (already VP-scaled), beta (B,L,H), one dtype.
+    Returns (Y (B,L,H,2,D) of that dtype = local state + correction per token (ssd.py:39-111),
+    h_final (B,H,2,D) fp32, the workspace); ``train=True`` keeps in the workspace what
+    ``ssd_scan_bwd`` reads.
+    """
+    B, L, H, D, N, Q, dtype = _validate_ssd(A_bar, K, V, beta, chunk_size)
+    lib = _lib.load()
+    ins = [t.contiguous() for t in (A_bar, K, V, beta)]
+    dev = K.device
+    Y = torch.empty(B, L, H, N, D, dtype=dtype, device=dev)
+    h_final = torch.empty(B, H, N, D, dtype=torch.float32, device=dev)
+    nbytes = lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, N, Q)
+    if nbytes <= 0:
+        raise RuntimeError(f"cdssm_fused_scan_workspace_bytes rejected the shape ({nbytes})")
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    st = lib.cdssm_ssd_scan_fwd(_lib.DTYPE_CODE[dtype], *[_lib.ptr(t) for t in ins], _lib.ptr(Y), _lib.ptr(h_final),
+                                _lib.ptr(ws), B, L, H, D, N, Q, 1 if train else 0, _lib.stream_of(dev))
+    _lib.check(st, "cdssm_ssd_scan_fwd")
+    return Y, h_final, ws
+
+
+def ssd_scan_bwd(dY: Tensor, A_bar: Tensor, K: Tensor, V: Tensor, beta: Tensor, fwd_ws: Tensor,
+                 chunk_size: int) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Backward of ``ssd_scan_fwd(..., train=True)`` (cdssm_ssd_scan_bwd): (dA_bar, dK, dV, dbeta)
+    with the reference's rules (exact local and carry branches, the correction branch's shifted
+    gradient, exact_correction.cu:213-382)."""
+    B, L, H, D = K.shape
+    N = V.shape[-1]
+    Q = int(chunk_size)
+    lib = _lib.load()
+    dev = K.device
+    dY = dY.to(K.dtype).contiguous()
+    if tuple(dY.shape) != (B, L, H, N, D):
+        raise ValueError(f"dY must be ({B}, {L}, {H}, {N}, {D}), got {tuple(dY.shape)}")
+    outs = [torch.empty_like(t) for t in (A_bar, K, V, beta)]
+    nbytes = lib.cdssm_fused_scan_bwd_workspace_bytes(B, L, H, D, N, Q)
+    if nbytes <= 0:
+        raise RuntimeError(f"cdssm_fused_scan_bwd_workspace_bytes rejected the shape ({nbytes})")
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    st = lib.cdssm_ssd_scan_bwd(_lib.DTYPE_CODE[K.dtype], *[_lib.ptr(t) for t in (A_bar, K, V, beta)], _lib.ptr(dY),
+                                _lib.ptr(fwd_ws), *[_lib.ptr(t) for t in outs], _lib.ptr(ws), B, L, H, D, N, Q,
+                                _lib.stream_of(dev))
+    _lib.check(st, "cdssm_ssd_scan_bwd")
+    return tuple(outs)
+
+
+class SSDScanFn(torch.autograd.Function):
+    """Autograd Function of the fused SSD scan: (A_bar, K, V, beta, chunk_size) -> Y (B,L,H,2,D).
+
+    The same result and gradients as SSDChunkwiseScan over IntraChunkScanFn, InterChunkScanFn and
+    ExactCorrectionFn (ssd.py:39-111, ops.py:100-195), from one forward and one backward call.
+    Saves the inputs and the training forward's workspace (per-token records, the local state every
+    4 tokens, the state entering and the correction leaving every chunk), no per-token states.
+    """
+
+    @staticmethod
+    def forward(ctx, A_bar, K, V, beta, chunk_size):
+        _validate_ssd(A_bar, K, V, beta, chunk_size)
+        ins = [t.contiguous() for t in (A_bar, K, V, beta)]
+        train = any(t.requires_grad for t in (A_bar, K, V, beta))
+        Y, _, ws = ssd_scan_fwd(*ins, chunk_size, train=train)
+        if train:
+            ctx.save_for_backward(*ins, ws)
+        ctx.Q = int(chunk_size)
+        return Y
+
+    @staticmethod
+    def backward(ctx, dY):
+        A_bar, K, V, beta, ws = ctx.saved_tensors
+        dA, dK, dV, dbeta = ssd_scan_bwd(dY, A_bar, K, V, beta, ws, ctx.Q)
+        return dA, dK, dV, dbeta, None
+
+
 class PreparedBackward:
     """The fused backward bound to a PreparedForward's inputs and workspace.
 

@@ -90,6 +90,27 @@ struct IsABar<ABar<Base>> {
   static constexpr bool value = true;
 };
 
+// Form SsdY<T>: the SSDChunkwiseScan interface (ssd.py:39-111).  The transition
+// a_t comes as A_bar (B,L,H,2) in dt's place, the values are already VP-scaled
+// (vp = 1, r unused), there is no q or sel_C, and the scan's
+// Y_t = local state + correction, (B,L,H,2,D) with the (re, im) rows of each
+// head D apart, is written in place of the readout.
+template <typename Base>
+struct SsdY : Base {};
+template <typename T>
+struct IsSsdY {
+  static constexpr bool value = false;
+};
+template <typename Base>
+struct IsSsdY<SsdY<Base>> {
+  static constexpr bool value = true;
+};
+// a_t read from the input (A_bar) rather than computed from (dt, r, alpha, omega, c)
+template <typename T>
+struct GivenA {
+  static constexpr bool value = IsABar<T>::value || IsSsdY<T>::value;
+};
+
 // A wave's (chunk, head group) tile of a (B, L, H, D) tensor as a buffer
 // resource: the base (wave-uniform, scalar registers) is the tile's first row
 // at its first head, each lane adds its constant byte offset (head, slice),
@@ -265,6 +286,61 @@ __device__ __forceinline__ RowStream tile_stream(const typename T::raw* x, const
   const int hl = tc.hbase + hh < H ? hh : H - 1 - tc.hbase;
   return make_row_stream(x + base, (int64_t(L - tc.t0) * H - tc.hbase) * D * T::bytes,
                          (hl * D + sub_off) * T::bytes);
+}
+
+// Store a lane's DPL consecutive elements (bf16 pairs packed into dwords).
+template <typename T, int DPL>
+__device__ __forceinline__ void store_row(typename T::raw* p, const float (&x)[DPL]) {
+  if constexpr (T::bytes == 2) {
+    uint32_t u[DPL / 2];
+#pragma unroll
+    for (int i = 0; i < DPL / 2; ++i) u[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+    if constexpr (DPL == 8) {
+      *reinterpret_cast<uint4*>(p) = make_uint4(u[0], u[1], u[2], u[3]);
+    } else if constexpr (DPL == 4) {
+      *reinterpret_cast<uint2*>(p) = make_uint2(u[0], u[1]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < DPL / 2; ++i) reinterpret_cast<uint32_t*>(p)[i] = u[i];
+    }
+  } else {
+    if constexpr (DPL % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < DPL / 4; ++i)
+        reinterpret_cast<float4*>(p)[i] = make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) p[i] = x[i];
+    }
+  }
+}
+
+// The same slice stored through a row stream at scalar byte offset soff.
+template <typename T, int DPL>
+__device__ __forceinline__ void store_row(const RowStream& s, int soff, const float (&x)[DPL]) {
+  using u32x4 = __attribute__((ext_vector_type(4))) unsigned int;
+  using u32x2 = __attribute__((ext_vector_type(2))) unsigned int;
+  if constexpr (T::bytes == 2) {
+    uint32_t u[DPL / 2];
+#pragma unroll
+    for (int i = 0; i < DPL / 2; ++i) u[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+    if constexpr (DPL == 8) {
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{u[0], u[1], u[2], u[3]}, s.rs, s.voff, soff, 0);
+    } else if constexpr (DPL == 4) {
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2{u[0], u[1]}, s.rs, s.voff, soff, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < DPL / 2; ++i) __builtin_amdgcn_raw_buffer_store_b32(u[i], s.rs, s.voff + 4 * i, soff, 0);
+    }
+  } else {
+    static_assert(DPL % 4 == 0, "fp32 slices are whole 16-byte vectors");
+#pragma unroll
+    for (int i = 0; i < DPL / 4; ++i)
+      __builtin_amdgcn_raw_buffer_store_b128(
+          u32x4{__float_as_uint(x[4 * i]), __float_as_uint(x[4 * i + 1]), __float_as_uint(x[4 * i + 2]),
+                __float_as_uint(x[4 * i + 3])},
+          s.rs, s.voff + 16 * i, soff, 0);
+  }
 }
 
 __device__ __forceinline__ ChunkTile decode_tile(int L, int Q, int NC, int n_hg, int HPW) {

@@ -78,6 +78,8 @@ constexpr int kBwdCorrPF = CDSSM_BWD_CORR_PF;  // row prefetch depth (correction
 //   S0 = (a_re, a_im, w_re, w_im)       transition and write (w = beta vp v)
 //   S1 = (beta, f_re, f_im, 0)          f = sel_C dy
 //   S2 = (h_re, h_im, gp_re, gp_im)     h = conj(g_t) f, gp = g_{t-1}
+// SSD form (a_t read from A_bar, vp = 1, the adjoint input a whole row dY_t):
+// f = 0 and S2 = (g_t, g_{t-1}).
 struct BwdScalars {
   float4 *S0, *S1, *S2;
 };
@@ -105,6 +107,7 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
   const int hj = tc.hbase + j;
   const bool hok = hj < H;
   const int hl = hok ? hj : H - 1;
+  constexpr bool YM = IsSsdY<T>::value;
   float cgr = 1.0f, cgi = 0.0f;  // g carried in from earlier slabs
   for (int tl = 0; tl < ntr; tl += kWave) {
     const int t0 = tl + blk * TPB;
@@ -114,13 +117,13 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
       const int t = min(t0 + i, tc.nt - 1);
       const int64_t e = (tc.row0 + t) * H + hl;
       bb[i] = T::load(beta + e);
-      dd[i] = T::load(dt + e);
-      rr[i] = T::load(r + e);
+      dd[i] = T::load(dt + (YM ? 2 * e : e));  // SSD form: a_t (re, im) from A_bar
+      rr[i] = T::load(YM ? dt + 2 * e + 1 : r + e);
       v0[i] = WITH_W ? T::load(v + 2 * e) : 0.0f;
       v1[i] = WITH_W ? T::load(v + 2 * e + 1) : 0.0f;
-      sc[i] = T::load(sel_c + e);
-      g0[i] = T::load(dy + 2 * e);
-      g1[i] = T::load(dy + 2 * e + 1);
+      sc[i] = YM ? 0.0f : T::load(sel_c + e);
+      g0[i] = YM ? 0.0f : T::load(dy + 2 * e);
+      g1[i] = YM ? 0.0f : T::load(dy + 2 * e + 1);
     }
     // the training forward's records: (p, pc), (c^_{t+1}.q, Y.q)
     float4 rp[TPB], rq[TPB];
@@ -130,7 +133,7 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
         const int t = min(t0 + i, tc.nt - 1);
         const int64_t e = (tc.row0 + t) * H + hl;
         rp[i] = saved[2 * e];
-        rq[i] = saved[2 * e + 1];
+        rq[i] = YM ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : saved[2 * e + 1];
       }
     }
     float ar[TPB], ai[TPB], Gr[TPB], Gi[TPB];
@@ -138,7 +141,7 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
 #pragma unroll
     for (int i = 0; i < TPB; ++i) {
       const bool real = hok && t0 + i < tc.nt;
-      const Transition tr = cayley_gated(dd[i], rr[i], al, om, c);
+      const Transition tr = YM ? Transition{dd[i], rr[i], 1.0f} : cayley_gated(dd[i], rr[i], al, om, c);
       ar[i] = real ? tr.ar : 1.0f;
       ai[i] = real ? tr.ai : 0.0f;
       const float f = bb[i] * tr.vp;
@@ -172,7 +175,10 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
       float pr = egr, pi = egi;  // g_{t-1}
       if (i > 0) cmul_acc(pr, pi, Gr[i - 1], Gi[i - 1]);
       s.S1[p] = make_float4(bb[i], g0[i], g1[i], 0.0f);
-      s.S2[p] = make_float4(gr * g0[i] + gi * g1[i], gr * g1[i] - gi * g0[i], pr, pi);
+      if constexpr (YM)  // g_t weights the row dY_t: zero past the last token (the rows are clamped there)
+        s.S2[p] = hok && t0 + i < tc.nt ? make_float4(gr, gi, pr, pi) : make_float4(0.0f, 0.0f, pr, pi);
+      else
+        s.S2[p] = make_float4(gr * g0[i] + gi * g1[i], gr * g1[i] - gi * g0[i], pr, pi);
       if constexpr (WITH_W) {
         s.S0[p] = make_float4(ar[i], ai[i], v0[i], v1[i]);
         // past the last token: p = pc = 0 (inert), delta g = 0, Y.q = 0
@@ -193,7 +199,8 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
 
 // Per-token scalars of the correction-adjoint pass: S1 = (beta, 0, 0, 0),
 // S2 = (h, 0, 0) with h = conj(g_t) sel_C dy, g_t read from the training
-// forward's records.  Slots past the last token and heads >= H are inert.
+// forward's records (SSD form: S2 = (g_t, 0, 0), the adjoint's input being a
+// whole row dY_t).  Slots past the last token and heads >= H are inert.
 template <typename T, int HPW>
 __device__ __forceinline__ void stage_corr(const ChunkTile& tc, int H, int ntr,
                                            const typename T::raw* __restrict__ beta,
@@ -207,6 +214,7 @@ __device__ __forceinline__ void stage_corr(const ChunkTile& tc, int H, int ntr,
   const int hj = tc.hbase + j;
   const bool hok = hj < H;
   const int hl = hok ? hj : H - 1;
+  constexpr bool YM = IsSsdY<T>::value;
   for (int tl = 0; tl < ntr; tl += kWave) {
     const int t0 = tl + blk * TPB;
     float bb[TPB], sc[TPB], g0[TPB], g1[TPB];
@@ -216,9 +224,9 @@ __device__ __forceinline__ void stage_corr(const ChunkTile& tc, int H, int ntr,
       const int t = min(t0 + i, tc.nt - 1);
       const int64_t e = (tc.row0 + t) * H + hl;
       bb[i] = T::load(beta + e);
-      sc[i] = T::load(sel_c + e);
-      g0[i] = T::load(dy + 2 * e);
-      g1[i] = T::load(dy + 2 * e + 1);
+      sc[i] = YM ? 1.0f : T::load(sel_c + e);
+      g0[i] = YM ? 0.0f : T::load(dy + 2 * e);
+      g1[i] = YM ? 0.0f : T::load(dy + 2 * e + 1);
       gg[i] = gsaved[e];
     }
 #pragma unroll
@@ -227,63 +235,11 @@ __device__ __forceinline__ void stage_corr(const ChunkTile& tc, int H, int ntr,
       const float fr = real ? sc[i] * g0[i] : 0.0f, fi = real ? sc[i] * g1[i] : 0.0f;
       const int p = (t0 + i) * HPW + j;
       s.S1[p] = make_float4(real ? bb[i] : 0.0f, 0.0f, 0.0f, 0.0f);
-      s.S2[p] = make_float4(gg[i].x * fr + gg[i].y * fi, gg[i].x * fi - gg[i].y * fr, 0.0f, 0.0f);
+      if constexpr (YM)
+        s.S2[p] = real ? make_float4(gg[i].x, gg[i].y, 0.0f, 0.0f) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      else
+        s.S2[p] = make_float4(gg[i].x * fr + gg[i].y * fi, gg[i].x * fi - gg[i].y * fr, 0.0f, 0.0f);
     }
-  }
-}
-
-// Store a lane's DPL consecutive elements (bf16 pairs packed into dwords).
-template <typename T, int DPL>
-__device__ __forceinline__ void store_row(typename T::raw* p, const float (&x)[DPL]) {
-  if constexpr (T::bytes == 2) {
-    uint32_t u[DPL / 2];
-#pragma unroll
-    for (int i = 0; i < DPL / 2; ++i) u[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
-    if constexpr (DPL == 8) {
-      *reinterpret_cast<uint4*>(p) = make_uint4(u[0], u[1], u[2], u[3]);
-    } else if constexpr (DPL == 4) {
-      *reinterpret_cast<uint2*>(p) = make_uint2(u[0], u[1]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < DPL / 2; ++i) reinterpret_cast<uint32_t*>(p)[i] = u[i];
-    }
-  } else {
-    if constexpr (DPL % 4 == 0) {
-#pragma unroll
-      for (int i = 0; i < DPL / 4; ++i)
-        reinterpret_cast<float4*>(p)[i] = make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < DPL; ++i) p[i] = x[i];
-    }
-  }
-}
-
-// The same slice stored through a row stream at scalar byte offset soff.
-template <typename T, int DPL>
-__device__ __forceinline__ void store_row(const RowStream& s, int soff, const float (&x)[DPL]) {
-  using u32x4 = __attribute__((ext_vector_type(4))) unsigned int;
-  using u32x2 = __attribute__((ext_vector_type(2))) unsigned int;
-  if constexpr (T::bytes == 2) {
-    uint32_t u[DPL / 2];
-#pragma unroll
-    for (int i = 0; i < DPL / 2; ++i) u[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
-    if constexpr (DPL == 8) {
-      __builtin_amdgcn_raw_buffer_store_b128(u32x4{u[0], u[1], u[2], u[3]}, s.rs, s.voff, soff, 0);
-    } else if constexpr (DPL == 4) {
-      __builtin_amdgcn_raw_buffer_store_b64(u32x2{u[0], u[1]}, s.rs, s.voff, soff, 0);
-    } else {
-#pragma unroll
-      for (int i = 0; i < DPL / 2; ++i) __builtin_amdgcn_raw_buffer_store_b32(u[i], s.rs, s.voff + 4 * i, soff, 0);
-    }
-  } else {
-    static_assert(DPL % 4 == 0, "fp32 slices are whole 16-byte vectors");
-#pragma unroll
-    for (int i = 0; i < DPL / 4; ++i)
-      __builtin_amdgcn_raw_buffer_store_b128(
-          u32x4{__float_as_uint(x[4 * i]), __float_as_uint(x[4 * i + 1]), __float_as_uint(x[4 * i + 2]),
-                __float_as_uint(x[4 * i + 3])},
-          s.rs, s.voff + 16 * i, soff, 0);
   }
 }
 
@@ -299,6 +255,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
     const typename T::raw* __restrict__ dy, const float2* __restrict__ gsaved, float2* __restrict__ lam0,
     int L, int H, int Q, int NC, int n_hg) {
   constexpr int LPH = BwdCorrCfg<D>::LPH, HPW = BwdCorrCfg<D>::HPW, DPL = BwdCorrCfg<D>::DPL, PF = kBwdCorrPF;
+  constexpr bool YM = IsSsdY<T>::value;  // SSD form: q points at dY (B,L,H,2,D)
   extern __shared__ float4 smem4[];
   const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
@@ -310,16 +267,20 @@ __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
   const int ntr = round_up(tc.nt, PF);
 
   const RowStream ks = tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
-  const RowStream qs = tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
+  // readout form: q rows; SSD form: this lane's slices of the dY re (qs) and im (gs) rows
+  const RowStream qs = tile_stream<T>(q, tc, L, H, YM ? 2 * D : D, hh, sub * DPL);
+  const RowStream gs = YM ? tile_stream<T>(q, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
   const int rowb = H * D * T::bytes;  // token stride in bytes
+  const int rowq = YM ? 2 * rowb : rowb;
   const int tlast = tc.nt - 1;
-  const int slim = tlast * rowb;
+  const int slim = tlast * rowb, slimq = tlast * rowq;
   // reverse ring: slot i holds token ntr-1-(tb+i)
-  RowVec<T, DPL> kb[PF], qb[PF];
+  RowVec<T, DPL> kb[PF], qb[PF], gb[YM ? PF : 1];
 #pragma unroll
   for (int i = 0; i < PF; ++i) {
     kb[i].load(ks, min((ntr - 1 - i) * rowb, slim));
-    qb[i].load(qs, min((ntr - 1 - i) * rowb, slim));
+    qb[i].load(qs, min((ntr - 1 - i) * rowq, slimq));
+    if constexpr (YM) gb[i].load(gs, min((ntr - 1 - i) * rowq, slimq));
   }
   BwdScalars s{nullptr, smem4, smem4 + slots};
   stage_corr<T, HPW>(tc, H, ntr, beta, sel_c, dy, gsaved, s);
@@ -327,6 +288,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
   for (int i = 0; i < PF; ++i) {
     kb[i].pin();
     qb[i].pin();
+    if constexpr (YM) gb[i].pin();
   }
   __syncthreads();
 
@@ -342,20 +304,29 @@ __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
       s2[i] = s.S2[p];
     }
     const int nb = (ntr - 1 - tb - PF) * rowb;  // row offset of the reload for slot 0
+    const int nbq = (ntr - 1 - tb - PF) * rowq;
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      float kk[DPL], qq[DPL];
+      float kk[DPL], qq[DPL], gi[DPL];
       kb[i].unpack_then_reload(kk);
       qb[i].unpack_then_reload(qq);
+      if constexpr (YM) gb[i].unpack_then_reload(gi);
       kb[i].load(ks, max(min(nb - i * rowb, slim), 0));
-      qb[i].load(qs, max(min(nb - i * rowb, slim), 0));
+      qb[i].load(qs, max(min(nbq - i * rowq, slimq), 0));
+      if constexpr (YM) gb[i].load(gs, max(min(nbq - i * rowq, slimq), 0));
       __builtin_amdgcn_sched_barrier(0);  // issue the reloads here, not sunk below later tokens
       // padded steps have h = 0 and beta = 0
       float sr = 0.0f, si = 0.0f;
 #pragma unroll
       for (int jj = 0; jj < DPL; ++jj) {
-        lr[jj] = fmaf(s2[i].x, qq[jj], lr[jj]);
-        li[jj] = fmaf(s2[i].y, qq[jj], li[jj]);
+        if constexpr (YM) {
+          // lambda += conj(g_t) dY_t
+          lr[jj] = fmaf(s2[i].x, qq[jj], fmaf(s2[i].y, gi[jj], lr[jj]));
+          li[jj] = fmaf(s2[i].x, gi[jj], fmaf(-s2[i].y, qq[jj], li[jj]));
+        } else {
+          lr[jj] = fmaf(s2[i].x, qq[jj], lr[jj]);
+          li[jj] = fmaf(s2[i].y, qq[jj], li[jj]);
+        }
         sr = fmaf(lr[jj], kk[jj], sr);
         si = fmaf(li[jj], kk[jj], si);
       }
@@ -569,23 +540,29 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
   float lr[DPL], li[DPL];
 #pragma unroll
   for (int jj = 0; jj < DPL; ++jj) lr[jj] = li[jj] = 0.0f;
+  constexpr bool YM = IsSsdY<T>::value;  // SSD form: q points at dY (B,L,H,2,D)
   const RowStream ks = tile_stream<T>(a.k, tc, L, H, D, hh, sub * DPL);
-  const RowStream qs = tile_stream<T>(a.q, tc, L, H, D, hh, sub * DPL);
+  // readout form: q rows; SSD form: this lane's slices of the dY re (qs) and im (gs) rows
+  const RowStream qs = tile_stream<T>(a.q, tc, L, H, YM ? 2 * D : D, hh, sub * DPL);
+  const RowStream gs = YM ? tile_stream<T>(a.q, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
   const int rowb = H * D * T::bytes;  // token stride in bytes
+  const int rowq = YM ? 2 * rowb : rowb;
   const int tlast = tc.nt - 1;
-  const int slim = tlast * rowb;
-  RowVec<T, DPL> kb[PF], qb[PF];
+  const int slim = tlast * rowb, slimq = tlast * rowq;
+  RowVec<T, DPL> kb[PF], qb[PF], gb[YM ? PF : 1];
   if (live) {
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       kb[i].load(ks, min((ntr - 1 - i) * rowb, slim));
-      qb[i].load(qs, min((ntr - 1 - i) * rowb, slim));
+      qb[i].load(qs, min((ntr - 1 - i) * rowq, slimq));
+      if constexpr (YM) gb[i].load(gs, min((ntr - 1 - i) * rowq, slimq));
     }
     stage_corr<T, HPW>(tc, H, ntr, a.beta, a.sel_c, a.dy, a.gsaved, s);
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       kb[i].pin();
       qb[i].pin();
+      if constexpr (YM) gb[i].pin();
     }
   }
   __syncthreads();  // every wave reaches every barrier of this kernel
@@ -599,19 +576,28 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
         s2[i] = s.S2[p];
       }
       const int nb = (ntr - 1 - tb - PF) * rowb;  // row offset of the reload for slot 0
+      const int nbq = (ntr - 1 - tb - PF) * rowq;
 #pragma unroll
       for (int i = 0; i < PF; ++i) {
-        float kk[DPL], qq[DPL];
+        float kk[DPL], qq[DPL], gi[DPL];
         kb[i].unpack_then_reload(kk);
         qb[i].unpack_then_reload(qq);
+        if constexpr (YM) gb[i].unpack_then_reload(gi);
         kb[i].load(ks, max(min(nb - i * rowb, slim), 0));
-        qb[i].load(qs, max(min(nb - i * rowb, slim), 0));
+        qb[i].load(qs, max(min(nbq - i * rowq, slimq), 0));
+        if constexpr (YM) gb[i].load(gs, max(min(nbq - i * rowq, slimq), 0));
         __builtin_amdgcn_sched_barrier(0);
         float sr = 0.0f, si = 0.0f;
 #pragma unroll
         for (int jj = 0; jj < DPL; ++jj) {
-          lr[jj] = fmaf(s2[i].x, qq[jj], lr[jj]);
-          li[jj] = fmaf(s2[i].y, qq[jj], li[jj]);
+          if constexpr (YM) {
+            // lambda += conj(g_t) dY_t
+            lr[jj] = fmaf(s2[i].x, qq[jj], fmaf(s2[i].y, gi[jj], lr[jj]));
+            li[jj] = fmaf(s2[i].x, gi[jj], fmaf(-s2[i].y, qq[jj], li[jj]));
+          } else {
+            lr[jj] = fmaf(s2[i].x, qq[jj], lr[jj]);
+            li[jj] = fmaf(s2[i].y, qq[jj], li[jj]);
+          }
           sr = fmaf(lr[jj], kk[jj], sr);
           si = fmaf(li[jj], kk[jj], si);
         }
@@ -629,6 +615,7 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
     for (int i = 0; i < PF; ++i) {
       kb[i].pin();
       qb[i].pin();
+      if constexpr (YM) gb[i].pin();
     }
     // lambda_0 and G_k of the chunk (heads >= H: zero map)
 #pragma unroll
@@ -886,15 +873,19 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   const int hl = hok ? h : H - 1;
   const int slots = round_up(Q, kWave) * HPW;
   const int ntr = round_up(tc.nt, PF);
-  const float al = alpha[hl], om = omega[hl];
+  constexpr bool YM = IsSsdY<T>::value;  // SSD form: q points at dY (B,L,H,2,D); dq not formed
+  const float al = YM ? 0.0f : alpha[hl], om = YM ? 0.0f : omega[hl];
 
   const RowStream ks = tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
-  const RowStream qs = tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
+  // readout form: q rows; SSD form: this lane's slices of the dY re (qs) and im (gs) rows
+  const RowStream qs = tile_stream<T>(q, tc, L, H, YM ? 2 * D : D, hh, sub * DPL);
+  const RowStream gs = YM ? tile_stream<T>(q, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
   const RowStream dks = tile_stream<T>(dk, tc, L, H, D, hh, sub * DPL);
-  const RowStream dqs = tile_stream<T>(dq, tc, L, H, D, hh, sub * DPL);
+  const RowStream dqs = YM ? RowStream{} : tile_stream<T>(dq, tc, L, H, D, hh, sub * DPL);
   const int rowb = H * D * T::bytes;  // token stride in bytes
+  const int rowq = YM ? 2 * rowb : rowb;
   const int tlast = tc.nt - 1;
-  const int slim = tlast * rowb;
+  const int slim = tlast * rowb, slimq = tlast * rowq;
   const int64_t chh = (int64_t(tc.b) * NC + tc.chunk) * H + hl;  // (b, chunk, head) index
   // the training forward's z checkpoints of this (chunk, head): z_{t-1} at t = CK * seg
   const int64_t ck0 = chh * NCK * D + sub * DPL;
@@ -940,7 +931,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   // Segments run last to first; the next segment's k / q rows and z checkpoint
   // are loaded while the current one is processed (two buffers, alternating).
   struct SegBuf {
-    RowVec<T, DPL> k[CK], q[CK];
+    RowVec<T, DPL> k[CK], q[CK], g[YM ? CK : 1];
     float2 z0[DPL];
   };
   auto load_seg = [&](SegBuf& R, int seg) {
@@ -948,7 +939,8 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
 #pragma unroll
     for (int i = 0; i < CK; ++i) {
       R.k[i].load(ks, min((tb + i) * rowb, slim));
-      R.q[i].load(qs, min((tb + i) * rowb, slim));
+      R.q[i].load(qs, min((tb + i) * rowq, slimq));
+      if constexpr (YM) R.g[i].load(gs, min((tb + i) * rowq, slimq));
     }
     load_zck<T, DPL>(zck, ck0 + int64_t(seg) * D, R.z0);
   };
@@ -987,24 +979,41 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
         const float4 s0 = s.S0[p], s1 = s.S1[p], s2 = s.S2[p], pv = sP[p], gv = sG[p];
         const float ar = s0.x, ai = s0.y, bb = s1.x;
         const float pr = pv.x, pi = pv.y, pcr = pv.z, pci = pv.w;
-        float kk[DPL], qq[DPL];
+        float kk[DPL], qq[DPL], gq[DPL];
         R.k[i].unpack(kk);
         R.q[i].unpack(qq);
-        float red[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (YM) R.g[i].unpack(gq);
+        constexpr int NRED = YM ? 8 : 6;
+        float red[NRED];
+#pragma unroll
+        for (int x = 0; x < NRED; ++x) red[x] = 0.0f;
         float dqv[DPL];
         // dq = Re(conj(f) Y_t), Y_t = z_t + g_{t-1} c^_t, f = (s1.y, -s1.z), g_{t-1} = (s2.z, s2.w):
         // the c^ part's weight conj(f) g_{t-1} is formed once per token
         const float wcr = s2.z * s1.y + s2.w * s1.z, wci = s2.z * s1.z - s2.w * s1.y;
 #pragma unroll
         for (int jj = 0; jj < DPL; ++jj) {
+          if constexpr (YM) {
+            // delta g_t = sum_d dY_t[d] conj(c^_{t+1}[d]), c^_{t+1} before the rebuild below
+            red[6] = fmaf(qq[jj], cr[jj], fmaf(gq[jj], ci[jj], red[6]));
+            red[7] = fmaf(gq[jj], cr[jj], fmaf(-qq[jj], ci[jj], red[7]));
+          }
           // c^_t = c^_{t+1} + beta pc k
           cr[jj] = fmaf(bb * pcr, kk[jj], cr[jj]);
           ci[jj] = fmaf(bb * pci, kk[jj], ci[jj]);
-          dqv[jj] = fmaf(zbr[i + 1][jj], s1.y, fmaf(zbi[i + 1][jj], s1.z, fmaf(cr[jj], wcr, ci[jj] * wci)));
-          mr[jj] = fmaf(s1.y, qq[jj], mr[jj]);
-          mi[jj] = fmaf(s1.z, qq[jj], mi[jj]);
-          lr[jj] = fmaf(s2.x, qq[jj], lr[jj]);
-          li[jj] = fmaf(s2.y, qq[jj], li[jj]);
+          if constexpr (YM) {
+            // mu += dY_t; lambda += conj(g_t) dY_t
+            mr[jj] += qq[jj];
+            mi[jj] += gq[jj];
+            lr[jj] = fmaf(s2.x, qq[jj], fmaf(s2.y, gq[jj], lr[jj]));
+            li[jj] = fmaf(s2.x, gq[jj], fmaf(-s2.y, qq[jj], li[jj]));
+          } else {
+            dqv[jj] = fmaf(zbr[i + 1][jj], s1.y, fmaf(zbi[i + 1][jj], s1.z, fmaf(cr[jj], wcr, ci[jj] * wci)));
+            mr[jj] = fmaf(s1.y, qq[jj], mr[jj]);
+            mi[jj] = fmaf(s1.z, qq[jj], mi[jj]);
+            lr[jj] = fmaf(s2.x, qq[jj], lr[jj]);
+            li[jj] = fmaf(s2.y, qq[jj], li[jj]);
+          }
           red[0] = fmaf(mr[jj], kk[jj], red[0]);
           red[1] = fmaf(mi[jj], kk[jj], red[1]);
           red[2] = fmaf(mr[jj], zbr[i][jj], fmaf(mi[jj], zbi[i][jj], red[2]));
@@ -1013,13 +1022,13 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
           red[5] = fmaf(li[jj], kk[jj], red[5]);
         }
 #pragma unroll
-        for (int x = 0; x < 6; ++x) red[x] = group_sum<LPH>(red[x]);
+        for (int x = 0; x < NRED; ++x) red[x] = group_sum<LPH>(red[x]);
         const float dwr = red[0], dwi = red[1], slr = red[4], sli = red[5];
         const float mkr = ar * dwr + ai * dwi, mki = ar * dwi - ai * dwr;
         float dar = red[2] - bb * (pr * dwr + pi * dwi);
         float dai = red[3] - bb * (pr * dwi - pi * dwr);
         const float dbe = -(pr * mkr + pi * mki) - (pcr * slr + pci * sli);
-        float dgr = gv.x, dgi = gv.y;
+        float dgr = YM ? red[NRED - 2] : gv.x, dgi = YM ? red[NRED - 1] : gv.y;
         if (t == tc.nt - 1) {
           dgr += dGr;
           dgi += dGi;
@@ -1058,7 +1067,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
         }
         if (hok) {
           store_row<T, DPL>(dks, t * rowb, dkv);
-          store_row<T, DPL>(dqs, t * rowb, dqv);
+          if constexpr (!YM) store_row<T, DPL>(dqs, t * rowb, dqv);
         }
         if (sub == 0) {
           sP[p] = make_float4(dar, dai, dwr, dwi);
@@ -1091,7 +1100,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
     const int hj = tc.hbase + j;
     const bool jok = hj < H;
     const int hjl = jok ? hj : H - 1;
-    const float alj = alpha[hjl], omj = omega[hjl];
+    const float alj = YM ? 0.0f : alpha[hjl], omj = YM ? 0.0f : omega[hjl];
     float dal = 0.0f, dom = 0.0f;
     for (int tl = 0; tl < ntr; tl += kWave) {
 #pragma unroll
@@ -1102,6 +1111,15 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
           const int p = t * HPW + j;
           const float4 rv = sP[p], gv = sG[p];
           const float bb = T::load(beta + e), v0 = T::load(v + 2 * e), v1 = T::load(v + 2 * e + 1);
+          if constexpr (YM) {
+            // SSD form: d A_bar_t = d a_t (into ddt's place, (re, im) pairs), dV = beta dw,
+            // dbeta = erase part + dw . V (w = beta V)
+            store_pair<T>(ddt + 2 * e, rv.x, rv.y);
+            T::store(dv + 2 * e, bb * rv.z);
+            T::store(dv + 2 * e + 1, bb * rv.w);
+            T::store(dbeta + e, gv.x + (rv.z * v0 + rv.w * v1));
+            continue;
+          }
           const float dtv = T::load(dt + e), rrv = T::load(r + e);
           const float g0 = T::load(dy + 2 * e), g1 = T::load(dy + 2 * e + 1);
           const Transition tr = cayley_gated(dtv, rrv, alj, omj, c);
@@ -1118,9 +1136,11 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
         }
       }
     }
-    dal = group_sum<NB>(dal);
-    dom = group_sum<NB>(dom);
-    if (blk == 0 && jok) dhead_parts[(int64_t(tc.b) * NC + tc.chunk) * H + hj] = make_float2(dal, dom);
+    if constexpr (!YM) {
+      dal = group_sum<NB>(dal);
+      dom = group_sum<NB>(dom);
+      if (blk == 0 && jok) dhead_parts[(int64_t(tc.b) * NC + tc.chunk) * H + hj] = make_float2(dal, dom);
+    }
   }
 }
 
@@ -1297,6 +1317,10 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
   st = cdssm_host::check_launch("cdssm_fused_scan_bwd/main");
   if (st) return st;
   if (ev) (void)hipEventRecord(ev[4], stream);
+  if constexpr (IsSsdY<T>::value) {  // no per-head dynamics parameters
+    if (ev) (void)hipEventRecord(ev[5], stream);
+    return st;
+  }
   hipLaunchKernelGGL(fused_bwd_heads_kernel, dim3(unsigned(H)), dim3(256), 0, stream,
                      (const float2*)parts, dalpha, domega, B * NC, H);
   st = cdssm_host::check_launch("cdssm_fused_scan_bwd/heads");
@@ -1339,8 +1363,8 @@ int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, cons
                     const float* fwd_workspace, void* dq, void* dk, void* dv, void* dbeta, void* dsel,
                     void* ddt, void* dr, float* dalpha, float* domega, float* dh0, float* workspace,
                     int64_t B, int64_t L, int64_t H, int64_t D, int64_t N, int64_t chunk,
-                    hipStream_t stream, hipEvent_t* ev, int* carry_fused = nullptr) {
-  const char* op = "cdssm_fused_scan_bwd";
+                    hipStream_t stream, hipEvent_t* ev, int* carry_fused = nullptr, bool ssd = false) {
+  const char* op = ssd ? "cdssm_ssd_scan_bwd" : "cdssm_fused_scan_bwd";
   if (dtype != 0 && dtype != 1) {
     cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
     return CDSSM_EINVAL;
@@ -1365,18 +1389,33 @@ int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, cons
     cdssm_host::set_error("%s: problem too large", op);
     return CDSSM_EINVAL;
   }
-  // q/k/dq/dk rows of a chunk tile are addressed by 32-bit byte offsets
-  if ((chunk + 16) * H * D * 4 > 0x7fffffffLL) {
+  // q/k/dq/dk rows (dY rows: 2 D per head) of a chunk tile are addressed by 32-bit byte offsets
+  if ((chunk + 16) * H * D * 4 * (ssd ? 2 : 1) > 0x7fffffffLL) {
     cdssm_host::set_error("%s: H * D too large for 32-bit row offsets (H=%lld D=%lld)", op, (long long)H,
                           (long long)D);
     return CDSSM_EINVAL;
   }
-  if (!q || !k || !v || !beta || !sel_c || !dt || !r || !alpha || !omega || !dy || !fwd_workspace ||
-      !dq || !dk || !dv || !dbeta || !dsel || !ddt || !dr || !dalpha || !domega || !workspace) {
+  if (ssd ? (!q || !k || !v || !beta || !dt || !fwd_workspace || !dk || !dv || !dbeta || !ddt || !workspace)
+          : (!q || !k || !v || !beta || !sel_c || !dt || !r || !alpha || !omega || !dy || !fwd_workspace || !dq ||
+             !dk || !dv || !dbeta || !dsel || !ddt || !dr || !dalpha || !domega || !workspace)) {
     cdssm_host::set_error("%s: null pointer argument", op);
     return CDSSM_EINVAL;
   }
   const int b = int(B), l = int(L), hh = int(H), qc = int(chunk);
+  if (ssd) {
+    const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (!a16(q) || !a16(k) || !a16(dk) || reinterpret_cast<uintptr_t>(ddt) % (dtype == 1 ? 4 : 8) != 0) {
+      cdssm_host::set_error("%s: K, dY and dK must be 16-byte aligned, dA_bar aligned to its (re, im) pair", op);
+      return CDSSM_EINVAL;
+    }
+#define CDSSM_SSD_BWD(TT, DD)                                                                                     \
+  launch_fused_bwd<TT, DD>(q, k, v, beta, nullptr, dt, nullptr, nullptr, nullptr, 0.0f, nullptr, nullptr,        \
+                           fwd_workspace, nullptr, dk, dv, dbeta, nullptr, ddt, nullptr, nullptr, nullptr, nullptr, \
+                           workspace, b, l, hh, qc, stream, ev, carry_fused)
+    if (dtype == 1) return D == 64 ? CDSSM_SSD_BWD(SsdY<BF16>, 64) : CDSSM_SSD_BWD(SsdY<BF16>, 128);
+    return D == 64 ? CDSSM_SSD_BWD(SsdY<F32>, 64) : CDSSM_SSD_BWD(SsdY<F32>, 128);
+#undef CDSSM_SSD_BWD
+  }
   if (dtype == 1) {
     if (D == 64)
       return launch_fused_bwd<BF16, 64>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final,
@@ -1407,6 +1446,21 @@ extern "C" int cdssm_fused_scan_bwd(int dtype, const void* q, const void* k, con
   return fused_bwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final, fwd_workspace,
                          dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0, workspace, B, L, H, D, N,
                          chunk, stream, nullptr);
+}
+
+// Backward of cdssm_ssd_scan_fwd (the SSDChunkwiseScan interface), with the
+// reference's gradient rules (exact for the local and carry branches, the
+// correction branch's shifted rule): given dY (B,L,H,2,D) of `dtype` and the
+// workspace of a cdssm_ssd_scan_fwd call with train != 0 on the same inputs,
+// writes dA_bar (B,L,H,2), dK (B,L,H,D), dV (B,L,H,2) and dbeta (B,L,H), all of
+// `dtype`.  workspace: cdssm_fused_scan_bwd_workspace_bytes().
+extern "C" int cdssm_ssd_scan_bwd(int dtype, const void* a_bar, const void* k, const void* v, const void* beta,
+                                  const void* dY, const float* fwd_workspace, void* dA, void* dK, void* dV,
+                                  void* dbeta, float* workspace, int64_t B, int64_t L, int64_t H, int64_t D,
+                                  int64_t N, int64_t chunk, hipStream_t stream) {
+  return fused_bwd_entry(dtype, dY, k, v, beta, nullptr, a_bar, nullptr, nullptr, nullptr, 0.0f, nullptr, nullptr,
+                         fwd_workspace, nullptr, dK, dV, dbeta, nullptr, dA, nullptr, nullptr, nullptr, nullptr,
+                         workspace, B, L, H, D, N, chunk, stream, nullptr, nullptr, true);
 }
 
 extern "C" int cdssm_fused_scan_bwd_profile(int dtype, const void* q, const void* k, const void* v,

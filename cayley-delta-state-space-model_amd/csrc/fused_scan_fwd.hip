@@ -164,7 +164,8 @@ __device__ __forceinline__ ResetMask<HPW> stage_scalars(const ChunkTile& tc, int
   const int hj = tc.hbase + j;
   const bool hok = hj < H;
   const int hl = hok ? hj : H - 1;
-  constexpr bool kAbar = IsABar<T>::value;  // a_t and vp_t given (dt -> a (B,L,H,2), r -> vp)
+  constexpr bool kAbar = GivenA<T>::value;  // a_t and vp_t given (dt -> a (B,L,H,2), r -> vp)
+  constexpr bool kSsd = IsSsdY<T>::value;   // SSD form: vp = 1 (values already scaled), no sel_C
   const float al = kAbar ? 0.0f : alpha[hl], om = kAbar ? 0.0f : omega[hl];
   const int glast = j * NB + NB - 1;  // the head's last lane
 
@@ -181,7 +182,7 @@ __device__ __forceinline__ ResetMask<HPW> stage_scalars(const ChunkTile& tc, int
       if constexpr (kAbar) {
         dd[i] = T::load(dt + 2 * e);  // a_t re, im
         rr[i] = T::load(dt + 2 * e + 1);
-        vq[i] = T::load(r + e);  // vp_t
+        vq[i] = kSsd ? 1.0f : T::load(r + e);  // vp_t
       } else {
         dd[i] = T::load(dt + e);
         rr[i] = T::load(r + e);
@@ -189,7 +190,7 @@ __device__ __forceinline__ ResetMask<HPW> stage_scalars(const ChunkTile& tc, int
       }
       v0[i] = T::load(v + 2 * e);
       v1[i] = T::load(v + 2 * e + 1);
-      sc[i] = MAIN ? T::load(sel_c + e) : 0.0f;
+      sc[i] = MAIN && !kSsd ? T::load(sel_c + e) : 0.0f;
     }
     // the caller's row prefetch goes after these small loads, so waiting for
     // them does not wait for the rows
@@ -593,6 +594,8 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
     float2* __restrict__ zck, float2* __restrict__ cend, int L, int H, int Q, int NC, int NCK, int n_hg,
     const float2* __restrict__ ycorr = nullptr) {
   static_assert(CORR || !SAVE, "the training forward keeps the sequential correction");
+  constexpr bool YM = IsSsdY<T>::value;  // SSD form: write Y (B,L,H,2,D), no q, no readout
+  static_assert(CORR || !YM, "the SSD form keeps the sequential correction");
   using Cfg = FusedCfg<T, D, LPH>;
   constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch;
   static_assert(PF == kTokRound && PF % kZck == 0, "z checkpoints fall at fixed positions of a prefetch group");
@@ -607,7 +610,11 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
   const int slots = round_up(Q, kWave) * HPW;
 
   const RowStream ks = tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
-  const RowStream qs = tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
+  const RowStream qs = YM ? RowStream{} : tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
+  // SSD form: this lane's slices of its head's Y re and im rows (D apart)
+  const RowStream yre = YM ? tile_stream<T>(y, tc, L, H, 2 * D, hh, sub * DPL) : RowStream{};
+  const RowStream yim = YM ? tile_stream<T>(y, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
+  const int rowy = 2 * H * D * T::bytes;  // token stride of Y in bytes
   const int rowb = H * D * T::bytes;  // token stride in bytes
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb;
@@ -632,13 +639,13 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
 #pragma unroll
                                                      for (int i = 0; i < PF; ++i) {
                                                        kb[i].load(ks, min(i * rowb, slim));
-                                                       qb[i].load(qs, min(i * rowb, slim));
+                                                       if constexpr (!YM) qb[i].load(qs, min(i * rowb, slim));
                                                      }
                                                    });
 #pragma unroll
   for (int i = 0; i < PF; ++i) {
     kb[i].pin();
-    qb[i].pin();
+    if constexpr (!YM) qb[i].pin();
   }
   __syncthreads();
 
@@ -674,9 +681,9 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
       }
       float kk[DPL], qq[DPL];
       kb[i].unpack_then_reload(kk);
-      qb[i].unpack_then_reload(qq);
+      if constexpr (!YM) qb[i].unpack_then_reload(qq);
       kb[i].load(ks, min(nb + i * rowb, slim));
-      qb[i].load(qs, min(nb + i * rowb, slim));
+      if constexpr (!YM) qb[i].load(qs, min(nb + i * rowb, slim));
 
       float pzr = 0.0f, pzi = 0.0f, pcr = 0.0f, pci = 0.0f, qcr = 0.0f, qci = 0.0f;
 #pragma unroll
@@ -686,8 +693,10 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
         if (CORR) {
           pcr = fmaf(cr[j], kk[j], pcr);
           pci = fmaf(ci[j], kk[j], pci);
-          qcr = fmaf(cr[j], qq[j], qcr);
-          qci = fmaf(ci[j], qq[j], qci);
+          if constexpr (!YM) {
+            qcr = fmaf(cr[j], qq[j], qcr);
+            qci = fmaf(ci[j], qq[j], qci);
+          }
         }
       }
       pzr = group_sum<LPH>(pzr);
@@ -700,6 +709,29 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
       const float bb = sa[i].z;
       local_step<DPL>(zr, zi, kk, (rg >> i) & 1u, sm[i], sa[i].x, sa[i].y, bb, pzr, pzi);
       const float ecr = bb * pcr, eci = bb * pci;
+      if constexpr (YM) {
+        // Y_t = f_t zh_t + g_{t-1} c^_t (the correction before this token's step)
+        const float4 fb = sb[i];
+        float ya[DPL], yb[DPL];
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          ya[j] = fmaf(fb.x, zr[j], fmaf(-fb.y, zi[j], fmaf(fb.z, cr[j], -fb.w * ci[j])));
+          yb[j] = fmaf(fb.x, zi[j], fmaf(fb.y, zr[j], fmaf(fb.z, ci[j], fb.w * cr[j])));
+          cr[j] = fmaf(-ecr, kk[j], cr[j]);
+          ci[j] = fmaf(-eci, kk[j], ci[j]);
+        }
+        if (hok && t < tc.nt) {
+          store_row<T, DPL>(yre, t * rowy, ya);
+          store_row<T, DPL>(yim, t * rowy, yb);
+        }
+        if (SAVE) {
+          if (sub == 0 && hok && t < tc.nt)
+            svp[2 * int64_t(t) * H] = make_float4(fpr * pzr - fpi * pzi, fpr * pzi + fpi * pzr, pcr, pci);
+          fpr = fb.x;
+          fpi = fb.y;
+        }
+        continue;
+      }
       float qzr = 0.0f, qzi = 0.0f, cnr = 0.0f, cni = 0.0f;
 #pragma unroll
       for (int j = 0; j < DPL; ++j) {
@@ -737,7 +769,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
         fpi = fb.y;
       }
     }
-    if (sub == 0) {
+    if (!YM && sub == 0) {
 #pragma unroll
       for (int i = 0; i < PF; ++i) s_y[(tb + i) * HPW + hh] = make_float2(yr[i], yi[i]);
     }
@@ -746,6 +778,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
 #pragma unroll
     for (int j = 0; j < DPL; ++j) cend[tile_h * D + sub * DPL + j] = make_float2(cr[j], ci[j]);
   }
+  if constexpr (YM) return;  // Y went out token by token
   __syncthreads();
 
   // coalesced write of y (B, L, H, 2) for the tile
@@ -900,6 +933,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   const unsigned long long epoch = load_epoch(a.ob.ctl);
   const int L = a.L, H = a.H, Q = a.Q, NC = a.NC, NSEG = a.NSEG, n_hg = a.n_hg;
   using Cfg = FusedCfg<T, D, LPH>;
+  constexpr bool YM = IsSsdY<T>::value;  // SSD form: write Y (B,L,H,2,D), no q, no readout
   constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch, W = kOnePassW;
   constexpr int SEGN = HPW * D;  // complex elements of a head group's state
   constexpr int EPT = DPL / W;   // of which each thread of the workgroup composes EPT
@@ -944,7 +978,11 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   int* ctrl = reinterpret_cast<int*>(Sx + SEGN);
 
   const RowStream ks = tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
-  const RowStream qs = tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
+  const RowStream qs = YM ? RowStream{} : tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
+  // SSD form: this lane's slices of its head's Y re and im rows (D apart)
+  const RowStream yre = YM ? tile_stream<T>(y, tc, L, H, 2 * D, hh, sub * DPL) : RowStream{};
+  const RowStream yim = YM ? tile_stream<T>(y, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
+  const int rowy = 2 * H * D * T::bytes;  // token stride of Y in bytes
   const int rowb = H * D * T::bytes;  // token stride in bytes
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb;
@@ -1032,8 +1070,10 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
         for (int i = 0; i < PF; ++i) s_y[(tb + i) * HPW + hh] = ec[i];
       }
     }
+    if constexpr (!YM) {
 #pragma unroll
-    for (int i = 0; i < PF; ++i) qb[i].load(qs, min(i * rowb, slim));
+      for (int i = 0; i < PF; ++i) qb[i].load(qs, min(i * rowb, slim));
+    }
 #pragma unroll
     for (int i = 0; i < PF; ++i) kb[i].pin();
     // chunk map F = f_end zh (zero for heads >= H: their steps are inert)
@@ -1210,8 +1250,10 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
     // the local state is replayed from its update coefficients
 #pragma unroll
     for (int j = 0; j < DPL; ++j) zr[j] = zi[j] = 0.0f;
+    if constexpr (!YM) {
 #pragma unroll
-    for (int i = 0; i < PF; ++i) qb[i].pin();  // loaded after the local pass
+      for (int i = 0; i < PF; ++i) qb[i].pin();  // loaded after the local pass
+    }
     for (int tb = 0; tb < ntr; tb += PF) {
       float4 sa[PF], sb[PF];
       float2 se[PF], sm[PF];
@@ -1230,11 +1272,41 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
         const int t = tb + i;
         float kk[DPL], qq[DPL];
         kb[i].unpack_then_reload(kk);
-        qb[i].unpack_then_reload(qq);
+        if constexpr (!YM) qb[i].unpack_then_reload(qq);
         kb[i].load(ks, min(nb + i * rowb, slim));
-        qb[i].load(qs, min(nb + i * rowb, slim));
+        if constexpr (!YM) qb[i].load(qs, min(nb + i * rowb, slim));
         // zh_t = (m_t zh_{t-1} at a frame reset) + e_t k_t
         if ((rg >> i) & 1u) zscale<DPL>(zr, zi, sm[i]);
+        if constexpr (YM) {
+          float pcr = 0.0f, pci = 0.0f;
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) {
+            zr[j] = fmaf(se[i].x, kk[j], zr[j]);
+            zi[j] = fmaf(se[i].y, kk[j], zi[j]);
+            pcr = fmaf(cr[j], kk[j], pcr);
+            pci = fmaf(ci[j], kk[j], pci);
+          }
+          pcr = group_sum<LPH>(pcr);
+          pci = group_sum<LPH>(pci);
+          const float bb = sa[i].z;
+          const float ecr = bb * pcr, eci = bb * pci;
+          // Y_t = f_t zh_t + g_{t-1} c^_t (the correction before this token's step)
+          const float4 fb = sb[i];
+          float ya[DPL], yb[DPL];
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) {
+            ya[j] = fmaf(fb.x, zr[j], fmaf(-fb.y, zi[j], fmaf(fb.z, cr[j], -fb.w * ci[j])));
+            yb[j] = fmaf(fb.x, zi[j], fmaf(fb.y, zr[j], fmaf(fb.z, ci[j], fb.w * cr[j])));
+            cr[j] = fmaf(-ecr, kk[j], cr[j]);
+            ci[j] = fmaf(-eci, kk[j], ci[j]);
+          }
+          if (hok && t < tc.nt) {
+            store_row<T, DPL>(yre, t * rowy, ya);
+            store_row<T, DPL>(yim, t * rowy, yb);
+            if (SAVE && sub == 0) reinterpret_cast<float2*>(svp + 2 * int64_t(t) * H)[1] = make_float2(pcr, pci);
+          }
+          continue;
+        }
         float pcr = 0.0f, pci = 0.0f, zqr = 0.0f, zqi = 0.0f, qcr = 0.0f, qci = 0.0f;
 #pragma unroll
         for (int j = 0; j < DPL; ++j) {
@@ -1276,7 +1348,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
           }
         }
       }
-      if (sub == 0) {
+      if (!YM && sub == 0) {
 #pragma unroll
         for (int i = 0; i < PF; ++i) s_y[(tb + i) * HPW + hh] = make_float2(yr[i], yi[i]);
       }
@@ -1289,7 +1361,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   __syncthreads();
 
   // coalesced write of y (B, L, H, 2) for the wave's tile
-  if (live) {
+  if (!YM && live) {
     const int n = tc.nt * HPW;
     for (int p = lane; p < n; p += kWave) {
       const int t = p / HPW;
@@ -1414,14 +1486,17 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   float2* cend = reg.cend;
   const int slots = round_up(Q, kWave) * HPW, slots_s = round_up(Q, kWave) * HPWS;
 
-  const bool sweep = cdssm_host::scan_path() == cdssm_host::kPathSweep;
+  // the SSD form has no chunked-correction variant: it takes the automatic choice there
+  const int mode = IsSsdY<T>::value && cdssm_host::scan_path() == cdssm_host::kPathSweep ? cdssm_host::kPathAuto
+                                                                                          : cdssm_host::scan_path();
+  const bool sweep = mode == cdssm_host::kPathSweep;
   if (sweep) {
     if (!std::is_same<T, BF16>::value || save || Q % 16 != 0 || Q > 128 || !reg.ycorr) {
       cdssm_host::set_error("cdssm_fused_scan_fwd: the chunked MFMA correction serves the bf16 inference forward "
                             "with a workspace and chunk a multiple of 16 up to 128 (chunk %d)", Q);
       return CDSSM_EINVAL;
     }
-  } else if (cdssm_host::scan_path() != cdssm_host::kPathFour) {
+  } else if (mode != cdssm_host::kPathFour) {
     const int64_t items = int64_t(w.NSEG) * B * n_hg;
     const size_t lds = onepass_lds<D, LPH>(Q);
     // one round of resident workgroups takes every segment: one-pass.  More
@@ -1433,7 +1508,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
     const int capp = save ? onepass_capacity<T, D, LPH, kSv, true>(lds)
                           : onepass_capacity<T, D, LPH, false, true>(lds);
     const bool single = cap1 > 0 && items <= cap1;
-    const bool forced = cdssm_host::scan_path() == cdssm_host::kPathOne;
+    const bool forced = mode == cdssm_host::kPathOne;
     const int64_t rounds = capp > 0 ? (items + capp - 1) / capp : 0;
     const bool persist = !single && capp > 0 && items <= 0x7fffffff &&
                          (forced || (!save && items * 10 >= rounds * capp * 9));
@@ -1661,9 +1736,10 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
                     const float* omega, float c, const float* h0, void* y, float* h_final,
                     float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
                     int64_t chunk, hipStream_t stream, hipEvent_t* ev, bool save, int* path = nullptr,
-                    bool abar = false, bool no_alloc = false) {
-  const char* op = no_alloc ? "cdssm_fused_scan_fwd_noalloc"
-                            : (abar ? "cdssm_fused_scan_fwd_abar" : "cdssm_fused_scan_fwd");
+                    bool abar = false, bool no_alloc = false, bool ssd = false) {
+  const char* op = ssd ? "cdssm_ssd_scan_fwd"
+                       : (no_alloc ? "cdssm_fused_scan_fwd_noalloc"
+                                   : (abar ? "cdssm_fused_scan_fwd_abar" : "cdssm_fused_scan_fwd"));
   if (dtype != 0 && dtype != 1) {
     cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
     return CDSSM_EINVAL;
@@ -1689,19 +1765,23 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
     cdssm_host::set_error("%s: problem too large", op);
     return CDSSM_EINVAL;
   }
-  // q/k rows of a chunk tile are addressed by 32-bit byte offsets
-  if ((chunk + 16) * H * D * 4 > 0x7fffffffLL) {
+  // q/k rows (Y rows: 2 D per head) of a chunk tile are addressed by 32-bit byte offsets
+  if ((chunk + 16) * H * D * 4 * (ssd ? 2 : 1) > 0x7fffffffLL) {
     cdssm_host::set_error("%s: H * D too large for 32-bit row offsets (H=%lld D=%lld)", op, (long long)H,
                           (long long)D);
     return CDSSM_EINVAL;
   }
-  if (!q || !k || !v || !beta || !sel_c || !dt || !r || (!abar && (!alpha || !omega)) || !y || !h_final ||
-      (!workspace && !no_alloc)) {
+  if ((!ssd && (!q || !sel_c || !r || (!abar && (!alpha || !omega)))) || !k || !v || !beta || !dt || !y ||
+      !h_final || (!workspace && !no_alloc)) {
     cdssm_host::set_error("%s: null pointer argument", op);
     return CDSSM_EINVAL;
   }
-  if (!aligned16(q) || !aligned16(k)) {
+  if ((!ssd && !aligned16(q)) || !aligned16(k)) {
     cdssm_host::set_error("%s: q and k must be 16-byte aligned", op);
+    return CDSSM_EINVAL;
+  }
+  if (ssd && !aligned16(y)) {
+    cdssm_host::set_error("%s: Y must be 16-byte aligned", op);
     return CDSSM_EINVAL;
   }
   if (reinterpret_cast<uintptr_t>(y) % (dtype == 1 ? 4 : 8) != 0) {
@@ -1719,6 +1799,15 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
   const int b = int(B), l = int(L), hh = int(H), qc = int(chunk);
 #define CDSSM_FWD_ARGS q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, reg, b, l, hh, qc, stream, \
                        ev, save, path
+  if (ssd) {
+    if (dtype == 1) {
+      if (D == 64)
+        return launch_fused_fwd<SsdY<BF16>, 64, CDSSM_FWD_LPH_BF16_D64, CDSSM_FWD_LPHS_BF16_D64>(CDSSM_FWD_ARGS);
+      return launch_fused_fwd<SsdY<BF16>, 128, 16, CDSSM_FWD_LPHS_BF16_D128>(CDSSM_FWD_ARGS);
+    }
+    if (D == 64) return launch_fused_fwd<SsdY<F32>, 64, 16, 16>(CDSSM_FWD_ARGS);
+    return launch_fused_fwd<SsdY<F32>, 128, 32, 32>(CDSSM_FWD_ARGS);
+  }
   if (abar) {
     if (save) {
       cdssm_host::set_error("%s: the a_t input form has no training forward", op);
@@ -1775,6 +1864,20 @@ extern "C" int cdssm_fused_scan_fwd_abar(int dtype, const void* q, const void* k
                                          int64_t N, int64_t chunk, hipStream_t stream) {
   return fused_fwd_entry(dtype, q, k, v, beta, sel_c, a_bar, vp, nullptr, nullptr, 0.0f, h0, y, h_final, workspace,
                          B, L, H, D, N, chunk, stream, nullptr, false, nullptr, true);
+}
+
+// The SSDChunkwiseScan interface (ssd.py:39-111) on the fused kernels: A_bar
+// (B,L,H,2), K (B,L,H,D), V (B,L,H,2), already VP-scaled, and beta (B,L,H) of
+// `dtype` -> Y (B,L,H,2,D) of `dtype`, the R-mode local state + correction of
+// every token; h_final (B,H,2,D) fp32 receives the carry after the last token
+// (the sequence starts from a zero state).  train != 0 also writes, into the
+// workspace, what cdssm_ssd_scan_bwd reads.
+extern "C" int cdssm_ssd_scan_fwd(int dtype, const void* a_bar, const void* k, const void* v, const void* beta,
+                                  void* Y, float* h_final, float* workspace, int64_t B, int64_t L, int64_t H,
+                                  int64_t D, int64_t N, int64_t chunk, int train, hipStream_t stream) {
+  return fused_fwd_entry(dtype, nullptr, k, v, beta, nullptr, a_bar, nullptr, nullptr, nullptr, 0.0f, nullptr, Y,
+                         h_final, workspace, B, L, H, D, N, chunk, stream, nullptr, train != 0, nullptr, false, false,
+                         true);
 }
 
 extern "C" int cdssm_fused_scan_fwd_train(int dtype, const void* q, const void* k, const void* v,

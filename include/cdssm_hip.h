@@ -135,6 +135,36 @@ int cdssm_fused_scan_bwd(int dtype, const void* q, const void* k, const void* v,
                          int64_t chunk, hipStream_t stream);
 
 /*
+ * SSDChunkwiseScan on the fused kernels, forward: replaces SSDChunkwiseScan.forward
+ * (ssd.py:39-111), i.e. IntraChunkScanFn (ops.py:108-121, intra_chunk_scan.cu:560-609),
+ * InterChunkScanFn (ops.py:146-155, inter_chunk_scan.cu:201-234), ExactCorrectionFn
+ * (ops.py:173-186, exact_correction.cu:390-438) and Y = local_h + corrections, for
+ * state_dim N = 2.  Inputs of `dtype`: a_bar (B,L,H,2), k (B,L,H,D), v (B,L,H,2) (already
+ * VP-scaled, as block.py:194-195 passes it), beta (B,L,H).  Output Y (B,L,H,2,D) of `dtype`
+ * (16-byte aligned) and h_final (B,H,2,D) fp32, the carry after the last token (the scan
+ * starts from zero, as the reference's).  Intermediate states stay fp32.  train != 0 also
+ * writes what cdssm_ssd_scan_bwd reads into the workspace
+ * (cdssm_fused_scan_workspace_bytes() bytes).  Limits as cdssm_fused_scan_fwd.
+ */
+int cdssm_ssd_scan_fwd(int dtype, const void* a_bar, const void* k, const void* v, const void* beta, void* Y,
+                       float* h_final, float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                       int64_t chunk, int train, hipStream_t stream);
+
+/*
+ * SSDChunkwiseScan on the fused kernels, backward: replaces the autograd backward of
+ * SSDChunkwiseScan through IntraChunkScanFn.backward (ops.py:123-135), InterChunkScanFn.backward
+ * (ops.py:157-163) and ExactCorrectionFn.backward (ops.py:188-195, the reference's shifted rule),
+ * as cdssm_fused_scan_bwd does for the readout form.  Inputs: the forward's inputs, dY
+ * (B,L,H,2,D) of `dtype` and fwd_workspace as filled by cdssm_ssd_scan_fwd with train != 0.
+ * Outputs of `dtype`: dA (B,L,H,2), dK (B,L,H,D), dV (B,L,H,2), dbeta (B,L,H).  k, dY and dK
+ * 16-byte aligned.  workspace: cdssm_fused_scan_bwd_workspace_bytes() bytes.
+ */
+int cdssm_ssd_scan_bwd(int dtype, const void* a_bar, const void* k, const void* v, const void* beta,
+                       const void* dY, const float* fwd_workspace, void* dA, void* dK, void* dV, void* dbeta,
+                       float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N, int64_t chunk,
+                       hipStream_t stream);
+
+/*
  * Instrumentation (no counterpart in the reference; for benchmarks and
  * profilers): run the fused forward / backward `iters` times on `stream` with
  * HIP events recorded between its kernel launches, synchronise, and return in

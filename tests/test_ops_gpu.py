@@ -106,13 +106,16 @@ def test_exact_correction_fwd_bwd(dtype, N, D, C):
     assert max(errs) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("fused", [False, None], ids=["per_pass", "auto"])
 @pytest.mark.parametrize("dtype,L,N,D,Q", [(torch.float32, 200, 2, 64, 64), (torch.float32, 130, 16, 64, 32),
                                            (torch.bfloat16, 256, 2, 128, 128)])
-def test_ssd_chunkwise_scan_module_matches_reference_algorithm(dtype, L, N, D, Q):
+def test_ssd_chunkwise_scan_module_matches_reference_algorithm(dtype, L, N, D, Q, fused):
     """SSDChunkwiseScan forward (Y) and its autograd gradients vs the oracle's
-    ssd.py restatement with the reference's correction backward attached."""
+    ssd.py restatement with the reference's correction backward attached; the
+    per-pass ops (fused=False) and the module's own choice (the fused kernels
+    for N = 2)."""
     from cdssm_hip.ssd import SSDChunkwiseScan
-    log(f"[SSDChunkwiseScan] {dtype} L{L} N{N} D{D} Q{Q}")
+    log(f"[SSDChunkwiseScan] {dtype} L{L} N{N} D{D} Q{Q} fused={fused}")
     gen = torch.Generator().manual_seed(4)
     B, H = 2, 3
     A, K, V, beta = rounded(dtype, *rand_scan(gen, (B,), L, H, D, N, amax=0.99))
@@ -121,7 +124,7 @@ def test_ssd_chunkwise_scan_module_matches_reference_algorithm(dtype, L, N, D, Q
     Y_ref = o.ssd_chunkwise_scan(*leaves, Q, N, correction_fn=o.correction_with_reference_grad)
     g_ref = torch.autograd.grad((Y_ref * gY.double()).sum(), leaves)
     a, k, v, b = dev(A, K, V, beta, req=True)
-    Y = SSDChunkwiseScan(Q, N)(a, k, v, b)
+    Y = SSDChunkwiseScan(Q, N, fused=fused)(a, k, v, b)
     Y.backward(gY.to(DEV))
     torch.cuda.synchronize()
     errs = [rel(Y, Y_ref)] + [rel(x.grad, y) for x, y in zip((a, k, v, b), g_ref)]

@@ -1,0 +1,165 @@
+"""GPU parity of the fused SSDChunkwiseScan (cdssm_ssd_scan_fwd / cdssm_ssd_scan_bwd).
+
+The reference is the oracle's fp64 restatement of ssd.py:39-111 with the
+reference's correction backward attached (exact_correction.cu:213-382), on the
+same inputs rounded to the tested dtype and the same cotangent dY.  Tolerances,
+normwise max|x-ref|/max|ref| per tensor: fp32 1e-4, bf16 2e-2.
+"""
+
+import contextlib
+import math
+
+import pytest
+import torch
+
+from _gpu_util import DEV, log, rel
+from oracle import cdssm_oracle as o
+
+pytestmark = pytest.mark.gpu
+TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2}
+
+
+def rand_ssd(gen, B, L, H, D, amax=1.0, amin=0.0):
+    """A_bar of magnitude in [amin, amax) and uniform phase, unit-norm keys, N(0,1) values, beta in [0, 1)."""
+    ang = torch.rand(B, L, H, generator=gen) * 2 * math.pi
+    mag = amin + torch.rand(B, L, H, generator=gen) * (amax - amin)
+    A = torch.stack([mag * torch.cos(ang), mag * torch.sin(ang)], -1)
+    K = torch.randn(B, L, H, D, generator=gen)
+    K = K / K.norm(dim=-1, keepdim=True)
+    V = torch.randn(B, L, H, 2, generator=gen)
+    beta = torch.rand(B, L, H, generator=gen)
+    return A, K, V, beta
+
+
+@contextlib.contextmanager
+def forward_path(path):
+    from cdssm_hip import set_forward_path
+    prev = set_forward_path(path)
+    try:
+        yield
+    finally:
+        set_forward_path(prev)
+
+
+def fused_grads(A, K, V, beta, gY, Q):
+    from cdssm_hip import SSDScanFn
+    leaves = [t.to(DEV).requires_grad_(True) for t in (A, K, V, beta)]
+    Y = SSDScanFn.apply(*leaves, Q)
+    Y.backward(gY.to(DEV, Y.dtype))
+    torch.cuda.synchronize()
+    return Y.detach().cpu(), [x.grad.cpu() for x in leaves]
+
+
+def oracle_grads(A, K, V, beta, gY, Q):
+    leaves = [t.double().requires_grad_(True) for t in (A, K, V, beta)]
+    Y = o.ssd_chunkwise_scan(*leaves, Q, 2, correction_fn=o.correction_with_reference_grad)
+    g = torch.autograd.grad((Y * gY.double()).sum(), leaves)
+    return Y.detach(), list(g)
+
+
+CASES = [
+    # name, dtype, B, L, H, D, Q, amax
+    ("fp32_D64", torch.float32, 2, 256, 4, 64, 64, 0.99),
+    ("fp32_ragged_H5", torch.float32, 2, 300, 5, 64, 64, 0.99),
+    ("fp32_D128_chunk48", torch.float32, 1, 333, 3, 128, 48, 0.99),
+    ("fp32_small_a", torch.float32, 1, 256, 4, 64, 64, 0.05),
+    ("bf16_D64", torch.bfloat16, 2, 512, 16, 64, 64, 0.99),
+    ("bf16_D128_ragged", torch.bfloat16, 1, 700, 6, 128, 128, 0.99),
+    ("bf16_chunk20", torch.bfloat16, 1, 200, 3, 64, 20, 0.99),
+]
+
+
+@pytest.mark.parametrize("path", ["four_launch", "one_pass"])
+@pytest.mark.parametrize("name,dtype,B,L,H,D,Q,amax", CASES, ids=[c[0] for c in CASES])
+def test_fused_ssd_matches_oracle(name, dtype, B, L, H, D, Q, amax, path):
+    """Y and dA_bar, dK, dV, dbeta on both forward paths (the backward's carry takes its three-launch
+    form with four_launch, its one-launch form with one_pass)."""
+    log(f"[fused SSD] {name} B{B} L{L} H{H} D{D} Q{Q} path {path}")
+    gen = torch.Generator().manual_seed(11)
+    A, K, V, beta = [t.to(dtype) for t in rand_ssd(gen, B, L, H, D, amax=amax)]
+    gY = torch.randn(B, L, H, 2, D, generator=gen).to(dtype)
+    Y_ref, g_ref = oracle_grads(A, K, V, beta, gY, Q)
+    with forward_path(path):
+        Y, g = fused_grads(A, K, V, beta, gY, Q)
+    from cdssm_hip import lookback_status
+    assert lookback_status() == 0, "a look-back wait timed out"
+    errs = {"Y": rel(Y, Y_ref)}
+    errs.update({n: rel(x, y) for n, x, y in zip(("dA", "dK", "dV", "dbeta"), g, g_ref)})
+    log("   " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
+    assert Y.shape == (B, L, H, 2, D) and Y.dtype == dtype
+    assert all(e <= TOL[dtype] for e in errs.values()), errs
+
+
+def test_fused_ssd_c1_shape_matches_oracle_and_per_pass():
+    """The C1 shape (B8 H16 L4096 D64 bf16): the fused module against the oracle on one batch row and
+    two heads, and against the per-pass ops on everything (the per-pass ops round local_h,
+    chunk_states and corrections to bf16 between passes, as the reference does, so the two agree to
+    bf16 accuracy)."""
+    from cdssm_hip.ssd import SSDChunkwiseScan
+    log("[fused SSD C1] B8 H16 L4096 D64 bf16")
+    gen = torch.Generator().manual_seed(2)
+    B, L, H, D, Q = 8, 4096, 16, 64, 64
+    A, K, V, beta = [t.to(torch.bfloat16) for t in rand_ssd(gen, B, L, H, D, amax=0.99, amin=0.5)]
+    gY = torch.randn(B, L, H, 2, D, generator=gen).to(torch.bfloat16)
+    Y, g = fused_grads(A, K, V, beta, gY, Q)
+    b, heads = 5, torch.tensor([3, 12])
+    sel = lambda t: t[b:b + 1].index_select(2, heads)  # noqa: E731
+    Y_ref, g_ref = oracle_grads(*[sel(t) for t in (A, K, V, beta)], sel(gY), Q)
+    errs = {"Y": rel(sel(Y), Y_ref)}
+    errs.update({n: rel(sel(x), y) for n, x, y in zip(("dA", "dK", "dV", "dbeta"), g, g_ref)})
+    log("   oracle: " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
+    assert all(e <= 2e-2 for e in errs.values()), errs
+    leaves = [t.to(DEV).requires_grad_(True) for t in (A, K, V, beta)]
+    Yp = SSDChunkwiseScan(Q, 2, fused=False)(*leaves)
+    Yp.backward(gY.to(DEV))
+    torch.cuda.synchronize()
+    perr = {"Y": rel(Y, Yp)}
+    perr.update({n: rel(x, y.grad) for n, x, y in zip(("dA", "dK", "dV", "dbeta"), g, leaves)})
+    log("   per-pass: " + "  ".join(f"{n} {e:.1e}" for n, e in perr.items()))
+    assert all(e <= 2e-2 for e in perr.values()), perr
+
+
+def test_fused_ssd_one_launch_past_the_anchor_matches_oracle():
+    """B1 H4 L19200 D64 bf16 forced onto the one-launch paths: 300 chunks = 75 segments, so the
+    forward and the backward carry both fold from published anchor states (every 63 segments)."""
+    log("[fused SSD anchor] B1 H4 L19200 D64 bf16 one_pass")
+    gen = torch.Generator().manual_seed(5)
+    B, L, H, D, Q = 1, 19200, 4, 64, 64
+    A, K, V, beta = [t.to(torch.bfloat16) for t in rand_ssd(gen, B, L, H, D, amax=0.999, amin=0.9)]
+    gY = torch.randn(B, L, H, 2, D, generator=gen).to(torch.bfloat16)
+    with forward_path("one_pass"):
+        Y, g = fused_grads(A, K, V, beta, gY, Q)
+    from cdssm_hip import lookback_status
+    assert lookback_status() == 0, "a look-back wait timed out"
+    heads = torch.tensor([0, 3])
+    sel = lambda t: t.index_select(2, heads)  # noqa: E731
+    Y_ref, g_ref = oracle_grads(*[sel(t) for t in (A, K, V, beta)], sel(gY), Q)
+    errs = {"Y": rel(sel(Y), Y_ref)}
+    errs.update({n: rel(sel(x), y) for n, x, y in zip(("dA", "dK", "dV", "dbeta"), g, g_ref)})
+    log("   " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
+    assert all(e <= 2e-2 for e in errs.values()), errs
+
+
+def test_fused_ssd_inference_call_keeps_no_records_and_matches_training_forward():
+    """Without gradients the forward runs without the training records; Y is the same (bit-identical)
+    as the training forward's."""
+    from cdssm_hip import SSDScanFn
+    gen = torch.Generator().manual_seed(9)
+    A, K, V, beta = [t.to(torch.bfloat16).to(DEV) for t in rand_ssd(gen, 2, 640, 8, 64, amax=0.99)]
+    with torch.no_grad():
+        Y0 = SSDScanFn.apply(A, K, V, beta, 64)
+    leaves = [t.clone().requires_grad_(True) for t in (A, K, V, beta)]
+    Y1 = SSDScanFn.apply(*leaves, 64)
+    torch.cuda.synchronize()
+    assert torch.equal(Y0, Y1.detach())
+
+
+def test_fused_ssd_rejects_what_it_cannot_serve():
+    from cdssm_hip.ssd import SSDChunkwiseScan
+    gen = torch.Generator().manual_seed(1)
+    A, K, V, beta = [t.to(DEV) for t in rand_ssd(gen, 1, 64, 2, 48)]
+    with pytest.raises(ValueError, match="head_dim"):
+        SSDChunkwiseScan(64, 2, fused=True)(A, K, V, beta)
+    # the module's own choice falls back to the per-pass ops for such a shape
+    Y = SSDChunkwiseScan(64, 2)(A, K, V, beta)
+    assert Y.shape == (1, 64, 2, 2, 48)
