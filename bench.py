@@ -514,11 +514,14 @@ def main():
     per_call = sorted(evs[2 * i].elapsed_time(evs[2 * i + 1]) for i in range(50))
     call_ms = statistics.median(per_call)
 
-    # cold: last-level cache (256 MB MALL) flushed before each call
-    flush = torch.empty(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+    # cold: the last-level cache (256 MB MALL) and the L2s refilled with other data before each call.  The
+    # refill reads 1 GiB (a max over it): a write would leave dirty lines whose write-back then competes
+    # with the timed call's reads, which would understate the cold rate.
+    flush = torch.zeros(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB, written once here
+    torch.cuda.synchronize()
     cold = []
     for i in range(10):
-        flush.fill_(float(i))
+        flush.max()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
@@ -564,7 +567,7 @@ def main():
                      "headline": "warm: back-to-back calls, inputs resident in HBM (142.7 MB of them also fit "
                                  "the 256 MB last-level cache between calls)",
                      "cold_frac": alg / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                     "cold_basis": "one call after a 1 GiB write flushed the last-level cache, median of 10",
+                     "cold_basis": "one call after a 1 GiB read refilled the last-level cache, median of 10",
                      "basis": (f"algorithmic {alg / 1e6:.2f} MB per launch (272 B per token-head: q, k, v, "
                                f"beta, sel_C, dt, r read, y written) / {kernel} launch {kern_ms * 1e3:.2f} us "
                                f"(HIP events on the launch stream, mean of {args.steps} launches, capped by the "
