@@ -329,8 +329,8 @@ def _validate_ssd(A_bar, K, V, beta, chunk_size):
     for n, t in named.items():
         if t.dtype != dtype or t.device != dev:
             raise TypeError(f"{n} is {t.dtype} on {t.device}, expected {dtype} on {dev} (as K)")
-    if N != 2:
-        raise ValueError(f"the fused SSD scan supports N = 2 (one complex pair per head), got N = {N}")
+    if N < 2 or N > 32 or N % 2:
+        raise ValueError(f"the fused SSD scan supports even state_dim 2 <= N <= 32, got N = {N}")
     if D not in (64, 128):
         raise ValueError(f"head_dim D must be 64 or 128, got {D}")
     Q = int(chunk_size)
@@ -343,10 +343,11 @@ def ssd_scan_fwd(A_bar: Tensor, K: Tensor, V: Tensor, beta: Tensor, chunk_size: 
                  train: bool = False) -> Tuple[Tensor, Tensor, Tensor]:
     """The SSDChunkwiseScan interface on the fused kernels (cdssm_ssd_scan_fwd).
 
-    A_bar (B,L,H,2), K (B,L,H,D), V (B,L,H,2) (already VP-scaled), beta (B,L,H), one dtype.
-    Returns (Y (B,L,H,2,D) of that dtype = local state + correction per token (ssd.py:39-111),
-    h_final (B,H,2,D) fp32, the workspace); ``train=True`` keeps in the workspace what
-    ``ssd_scan_bwd`` reads.
+    A_bar (B,L,H,N), K (B,L,H,D), V (B,L,H,N) (already VP-scaled), beta (B,L,H), one dtype, N even
+    (N / 2 complex state rows per head, each scanned as a virtual head that shares the head's k and
+    beta).  Returns (Y (B,L,H,N,D) of that dtype = local state + correction per token
+    (ssd.py:39-111), h_final (B,H,N,D) fp32, the workspace); ``train=True`` keeps in the workspace
+    what ``ssd_scan_bwd`` reads.
     """
     B, L, H, D, N, Q, dtype = _validate_ssd(A_bar, K, V, beta, chunk_size)
     lib = _lib.load()
@@ -354,9 +355,9 @@ def ssd_scan_fwd(A_bar: Tensor, K: Tensor, V: Tensor, beta: Tensor, chunk_size: 
     dev = K.device
     Y = torch.empty(B, L, H, N, D, dtype=dtype, device=dev)
     h_final = torch.empty(B, H, N, D, dtype=torch.float32, device=dev)
-    nbytes = lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, N, Q)
+    nbytes = lib.cdssm_ssd_scan_workspace_bytes(B, L, H, D, N, Q)
     if nbytes <= 0:
-        raise RuntimeError(f"cdssm_fused_scan_workspace_bytes rejected the shape ({nbytes})")
+        raise RuntimeError(f"cdssm_ssd_scan_workspace_bytes rejected the shape ({nbytes})")
     ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
     st = lib.cdssm_ssd_scan_fwd(_lib.DTYPE_CODE[dtype], *[_lib.ptr(t) for t in ins], _lib.ptr(Y), _lib.ptr(h_final),
                                 _lib.ptr(ws), B, L, H, D, N, Q, 1 if train else 0, _lib.stream_of(dev))
@@ -378,9 +379,9 @@ def ssd_scan_bwd(dY: Tensor, A_bar: Tensor, K: Tensor, V: Tensor, beta: Tensor, 
     if tuple(dY.shape) != (B, L, H, N, D):
         raise ValueError(f"dY must be ({B}, {L}, {H}, {N}, {D}), got {tuple(dY.shape)}")
     outs = [torch.empty_like(t) for t in (A_bar, K, V, beta)]
-    nbytes = lib.cdssm_fused_scan_bwd_workspace_bytes(B, L, H, D, N, Q)
+    nbytes = lib.cdssm_ssd_scan_bwd_workspace_bytes(B, L, H, D, N, Q)
     if nbytes <= 0:
-        raise RuntimeError(f"cdssm_fused_scan_bwd_workspace_bytes rejected the shape ({nbytes})")
+        raise RuntimeError(f"cdssm_ssd_scan_bwd_workspace_bytes rejected the shape ({nbytes})")
     ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
     st = lib.cdssm_ssd_scan_bwd(_lib.DTYPE_CODE[K.dtype], *[_lib.ptr(t) for t in (A_bar, K, V, beta)], _lib.ptr(dY),
                                 _lib.ptr(fwd_ws), *[_lib.ptr(t) for t in outs], _lib.ptr(ws), B, L, H, D, N, Q,
@@ -390,7 +391,7 @@ def ssd_scan_bwd(dY: Tensor, A_bar: Tensor, K: Tensor, V: Tensor, beta: Tensor, 
 
 
 class SSDScanFn(torch.autograd.Function):
-    """Autograd Function of the fused SSD scan: (A_bar, K, V, beta, chunk_size) -> Y (B,L,H,2,D).
+    """Autograd Function of the fused SSD scan: (A_bar, K, V, beta, chunk_size) -> Y (B,L,H,N,D).
 
     The same result and gradients as SSDChunkwiseScan over IntraChunkScanFn, InterChunkScanFn and
     ExactCorrectionFn (ssd.py:39-111, ops.py:100-195), from one forward and one backward call.

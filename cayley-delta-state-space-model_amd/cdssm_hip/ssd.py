@@ -3,11 +3,13 @@
 Same constructor, forward signature and result as the reference.  Two
 executions of the same algorithm:
 
-* fused (state_dim 2, head_dim 64 or 128, chunk <= 128, one float dtype on the
-  GPU): ``scan.SSDScanFn``, one forward call (cdssm_ssd_scan_fwd) that writes
-  Y once, and one backward call (cdssm_ssd_scan_bwd) with the reference's
-  gradient rules; intermediate states stay fp32 (the reference rounds
-  local_h, chunk_states and corrections to the input dtype between passes);
+* fused (even state_dim up to 32, head_dim 64 or 128, chunk <= 128, one float
+  dtype on the GPU): ``scan.SSDScanFn``, one forward call (cdssm_ssd_scan_fwd)
+  that writes Y once, and one backward call (cdssm_ssd_scan_bwd) with the
+  reference's gradient rules; each of a head's N / 2 complex state rows is
+  scanned as a virtual head sharing the head's k and beta; intermediate states
+  stay fp32 (the reference rounds local_h, chunk_states and corrections to the
+  input dtype between passes);
 * per-pass (any other shape): pad the sequence to whole chunks with zeros
   (A_bar = 0 on padded steps), run the intra-chunk scan, take the chunk
   summaries (total_A = cum_A[:, :, -1], final_local_h = local_h[:, :, -1]), run
@@ -42,7 +44,8 @@ class SSDChunkwiseScan(nn.Module):
 
     def fused_applies(self, A_bar: Tensor, K: Tensor, V: Tensor, beta: Tensor) -> bool:
         """Whether the fused kernels serve these inputs."""
-        return (self.state_dim == 2 and K.dim() == 4 and K.is_cuda and K.shape[-1] in (64, 128)
+        return (2 <= self.state_dim <= 32 and self.state_dim % 2 == 0 and K.dim() == 4 and K.is_cuda
+                and V.shape[-1] == self.state_dim and K.shape[-1] in (64, 128)
                 and 1 <= self.chunk_size <= 128 and K.dtype in (torch.float32, torch.bfloat16)
                 and all(t.dtype == K.dtype and t.device == K.device for t in (A_bar, V, beta)))
 
@@ -52,8 +55,8 @@ class SSDChunkwiseScan(nn.Module):
             if self.fused_applies(A_bar, K, V, beta):
                 return SSDScanFn.apply(A_bar, K, V, beta, self.chunk_size)
             if self.fused:
-                raise ValueError("the fused SSD scan needs state_dim 2, head_dim 64 or 128, chunk_size <= 128 "
-                                 "and float32 or bfloat16 inputs of one dtype on the GPU")
+                raise ValueError("the fused SSD scan needs an even state_dim <= 32, head_dim 64 or 128, "
+                                 "chunk_size <= 128 and float32 or bfloat16 inputs of one dtype on the GPU")
         B, L, H, D = K.shape
         N = self.state_dim
         C = self.chunk_size

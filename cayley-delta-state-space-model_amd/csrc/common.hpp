@@ -343,6 +343,18 @@ __device__ __forceinline__ void store_row(const RowStream& s, int soff, const fl
   }
 }
 
+// The tile stream of a per-head tensor (B, L, H / R, D) read by virtual heads:
+// with state_dim N = 2 R each head's R complex state rows are scanned as R
+// consecutive virtual heads (H counts them) that share the head's k rows.
+template <typename T>
+__device__ __forceinline__ RowStream tile_stream_rows(const typename T::raw* x, const ChunkTile& tc, int L, int H, int R,
+                                                      int D, int hh, int sub_off) {
+  const int Hk = H / R;
+  const int hv = min(tc.hbase + hh, H - 1);  // this lane's virtual head, clamped into the tensor
+  return make_row_stream(x + tc.row0 * Hk * D, int64_t(L - tc.t0) * Hk * D * T::bytes,
+                         ((hv / R) * D + sub_off) * T::bytes);
+}
+
 __device__ __forceinline__ ChunkTile decode_tile(int L, int Q, int NC, int n_hg, int HPW) {
   ChunkTile c;
   int g = blockIdx.x;

@@ -99,7 +99,8 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
                                           const typename T::raw* __restrict__ dy, float al, float om,
                                           float c, const BwdScalars& s,
                                           const float4* __restrict__ saved = nullptr,
-                                          float4* __restrict__ sP = nullptr, float4* __restrict__ sG = nullptr) {
+                                          float4* __restrict__ sP = nullptr, float4* __restrict__ sG = nullptr,
+                                          int R = 1) {
   constexpr int NB = kWave / HPW, TPB = HPW;
   const int lane = int(threadIdx.x) % kWave;  // lane in the wave (one-launch workgroups have several)
   const int j = lane / NB;
@@ -116,7 +117,7 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
     for (int i = 0; i < TPB; ++i) {
       const int t = min(t0 + i, tc.nt - 1);
       const int64_t e = (tc.row0 + t) * H + hl;
-      bb[i] = T::load(beta + e);
+      bb[i] = T::load(beta + (YM ? (tc.row0 + t) * (H / R) + hl / R : e));  // SSD form: beta per real head
       dd[i] = T::load(dt + (YM ? 2 * e : e));  // SSD form: a_t (re, im) from A_bar
       rr[i] = T::load(YM ? dt + 2 * e + 1 : r + e);
       v0[i] = WITH_W ? T::load(v + 2 * e) : 0.0f;
@@ -206,7 +207,7 @@ __device__ __forceinline__ void stage_corr(const ChunkTile& tc, int H, int ntr,
                                            const typename T::raw* __restrict__ beta,
                                            const typename T::raw* __restrict__ sel_c,
                                            const typename T::raw* __restrict__ dy,
-                                           const float2* __restrict__ gsaved, const BwdScalars& s) {
+                                           const float2* __restrict__ gsaved, const BwdScalars& s, int R = 1) {
   constexpr int NB = kWave / HPW, TPB = HPW;
   const int lane = int(threadIdx.x) % kWave;  // lane in the wave (one-launch workgroups have several)
   const int j = lane / NB;
@@ -223,7 +224,7 @@ __device__ __forceinline__ void stage_corr(const ChunkTile& tc, int H, int ntr,
     for (int i = 0; i < TPB; ++i) {
       const int t = min(t0 + i, tc.nt - 1);
       const int64_t e = (tc.row0 + t) * H + hl;
-      bb[i] = T::load(beta + e);
+      bb[i] = T::load(beta + (YM ? (tc.row0 + t) * (H / R) + hl / R : e));  // SSD form: per real head
       sc[i] = YM ? 1.0f : T::load(sel_c + e);
       g0[i] = YM ? 0.0f : T::load(dy + 2 * e);
       g1[i] = YM ? 0.0f : T::load(dy + 2 * e + 1);
@@ -253,7 +254,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
     const typename T::raw* __restrict__ q, const typename T::raw* __restrict__ k,
     const typename T::raw* __restrict__ beta, const typename T::raw* __restrict__ sel_c,
     const typename T::raw* __restrict__ dy, const float2* __restrict__ gsaved, float2* __restrict__ lam0,
-    int L, int H, int Q, int NC, int n_hg) {
+    int L, int H, int Q, int NC, int n_hg, int R = 1) {
   constexpr int LPH = BwdCorrCfg<D>::LPH, HPW = BwdCorrCfg<D>::HPW, DPL = BwdCorrCfg<D>::DPL, PF = kBwdCorrPF;
   constexpr bool YM = IsSsdY<T>::value;  // SSD form: q points at dY (B,L,H,2,D)
   extern __shared__ float4 smem4[];
@@ -266,12 +267,14 @@ __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
   const int slots = round_up(Q, kWave) * HPW;
   const int ntr = round_up(tc.nt, PF);
 
-  const RowStream ks = tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
+  // SSD form: R virtual heads (state rows) share each k row
+  const RowStream ks = YM ? tile_stream_rows<T>(k, tc, L, H, R, D, hh, sub * DPL)
+                          : tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
   // readout form: q rows; SSD form: this lane's slices of the dY re (qs) and im (gs) rows
   const RowStream qs = tile_stream<T>(q, tc, L, H, YM ? 2 * D : D, hh, sub * DPL);
   const RowStream gs = YM ? tile_stream<T>(q, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
-  const int rowb = H * D * T::bytes;  // token stride in bytes
-  const int rowq = YM ? 2 * rowb : rowb;
+  const int rowb = (YM ? H / R : H) * D * T::bytes;  // token stride of k in bytes
+  const int rowq = YM ? 2 * H * D * T::bytes : rowb;  // of q, or of dY
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb, slimq = tlast * rowq;
   // reverse ring: slot i holds token ntr-1-(tb+i)
@@ -283,7 +286,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
     if constexpr (YM) gb[i].load(gs, min((ntr - 1 - i) * rowq, slimq));
   }
   BwdScalars s{nullptr, smem4, smem4 + slots};
-  stage_corr<T, HPW>(tc, H, ntr, beta, sel_c, dy, gsaved, s);
+  stage_corr<T, HPW>(tc, H, ntr, beta, sel_c, dy, gsaved, s, R);
 #pragma unroll
   for (int i = 0; i < PF; ++i) {
     kb[i].pin();
@@ -490,6 +493,7 @@ struct CorrCarryArgs {
   float* dh0;             // out: (B, H, 2, D) or null
   OnePassBufs ob;         // X in seg_f, A in seg_g, left-end states in seg_s; epoch in ctl[0]
   int L, H, Q, NC, NSEG, n_hg, n_chain;
+  int R;                  // SSD form: state rows per head (virtual heads sharing a k row); 1 otherwise
 };
 
 template <typename T, int D>
@@ -541,12 +545,14 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
 #pragma unroll
   for (int jj = 0; jj < DPL; ++jj) lr[jj] = li[jj] = 0.0f;
   constexpr bool YM = IsSsdY<T>::value;  // SSD form: q points at dY (B,L,H,2,D)
-  const RowStream ks = tile_stream<T>(a.k, tc, L, H, D, hh, sub * DPL);
+  // SSD form: R virtual heads (state rows) share each k row
+  const RowStream ks = YM ? tile_stream_rows<T>(a.k, tc, L, H, a.R, D, hh, sub * DPL)
+                          : tile_stream<T>(a.k, tc, L, H, D, hh, sub * DPL);
   // readout form: q rows; SSD form: this lane's slices of the dY re (qs) and im (gs) rows
   const RowStream qs = tile_stream<T>(a.q, tc, L, H, YM ? 2 * D : D, hh, sub * DPL);
   const RowStream gs = YM ? tile_stream<T>(a.q, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
-  const int rowb = H * D * T::bytes;  // token stride in bytes
-  const int rowq = YM ? 2 * rowb : rowb;
+  const int rowb = (YM ? H / a.R : H) * D * T::bytes;  // token stride of k in bytes
+  const int rowq = YM ? 2 * H * D * T::bytes : rowb;   // of q, or of dY
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb, slimq = tlast * rowq;
   RowVec<T, DPL> kb[PF], qb[PF], gb[YM ? PF : 1];
@@ -557,7 +563,7 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
       qb[i].load(qs, min((ntr - 1 - i) * rowq, slimq));
       if constexpr (YM) gb[i].load(gs, min((ntr - 1 - i) * rowq, slimq));
     }
-    stage_corr<T, HPW>(tc, H, ntr, a.beta, a.sel_c, a.dy, a.gsaved, s);
+    stage_corr<T, HPW>(tc, H, ntr, a.beta, a.sel_c, a.dy, a.gsaved, s, a.R);
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       kb[i].pin();
@@ -861,7 +867,8 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
     typename T::raw* __restrict__ dv,
     typename T::raw* __restrict__ dbeta, typename T::raw* __restrict__ dsel,
     typename T::raw* __restrict__ ddt, typename T::raw* __restrict__ dr, float2* __restrict__ dhead_parts,
-    int L, int H, int Q, int NC, int NCK, int n_hg) {
+    int L, int H, int Q, int NC, int NCK, int n_hg, int R = 1, float* __restrict__ dkp = nullptr,
+    float* __restrict__ dbp = nullptr) {
   constexpr int LPH = BwdCfg<D>::LPH, HPW = BwdCfg<D>::HPW, DPL = BwdCfg<D>::DPL, PF = kBwdPF, CK = kBwdCK;
   static_assert(CK == kZck && PF == kTokRound, "the training forward's z checkpoints: every CK tokens");
   extern __shared__ float4 smem4[];
@@ -876,14 +883,20 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   constexpr bool YM = IsSsdY<T>::value;  // SSD form: q points at dY (B,L,H,2,D); dq not formed
   const float al = YM ? 0.0f : alpha[hl], om = YM ? 0.0f : omega[hl];
 
-  const RowStream ks = tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
+  // SSD form: R virtual heads (state rows) share each k row; with R > 1 each writes its own fp32 dk row
+  // into dkp (B, L, H, D) and a row-sum kernel forms dk
+  const bool rows = YM && R > 1;
+  const RowStream ks = YM ? tile_stream_rows<T>(k, tc, L, H, R, D, hh, sub * DPL)
+                          : tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
   // readout form: q rows; SSD form: this lane's slices of the dY re (qs) and im (gs) rows
   const RowStream qs = tile_stream<T>(q, tc, L, H, YM ? 2 * D : D, hh, sub * DPL);
   const RowStream gs = YM ? tile_stream<T>(q, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
-  const RowStream dks = tile_stream<T>(dk, tc, L, H, D, hh, sub * DPL);
+  const RowStream dks = rows ? RowStream{} : tile_stream<T>(dk, tc, L, H, D, hh, sub * DPL);
+  const RowStream dkps = rows ? tile_stream<F32>(dkp, tc, L, H, D, hh, sub * DPL) : RowStream{};
   const RowStream dqs = YM ? RowStream{} : tile_stream<T>(dq, tc, L, H, D, hh, sub * DPL);
-  const int rowb = H * D * T::bytes;  // token stride in bytes
-  const int rowq = YM ? 2 * rowb : rowb;
+  const int rowb = (YM ? H / R : H) * D * T::bytes;  // token stride of k (and q, dq, dk) in bytes
+  const int rowq = YM ? 2 * H * D * T::bytes : rowb;  // of q, or of dY
+  const int rowp = H * D * 4;                          // of dkp
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb, slimq = tlast * rowq;
   const int64_t chh = (int64_t(tc.b) * NC + tc.chunk) * H + hl;  // (b, chunk, head) index
@@ -905,7 +918,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   BwdScalars s{smem4, smem4 + slots, smem4 + 2 * slots};
   float4* sP = smem4 + 3 * slots;
   float4* sG = smem4 + 4 * slots;
-  stage_bwd<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, dy, al, om, c, s, saved, sP, sG);
+  stage_bwd<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, dy, al, om, c, s, saved, sP, sG, R);
   __syncthreads();
 
   // ---- reverse pass ----
@@ -1066,7 +1079,10 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
           li[jj] = fmaf(-bsli, kk[jj], li[jj]);
         }
         if (hok) {
-          store_row<T, DPL>(dks, t * rowb, dkv);
+          if (rows)
+            store_row<F32, DPL>(dkps, t * rowp, dkv);
+          else
+            store_row<T, DPL>(dks, t * rowb, dkv);
           if constexpr (!YM) store_row<T, DPL>(dqs, t * rowb, dqv);
         }
         if (sub == 0) {
@@ -1110,14 +1126,20 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
           const int64_t e = (tc.row0 + t) * H + hj;
           const int p = t * HPW + j;
           const float4 rv = sP[p], gv = sG[p];
-          const float bb = T::load(beta + e), v0 = T::load(v + 2 * e), v1 = T::load(v + 2 * e + 1);
+          // SSD form: beta per real head (the R virtual heads of its state rows share it)
+          const float bb = T::load(beta + (YM ? (tc.row0 + t) * (H / R) + hj / R : e));
+          const float v0 = T::load(v + 2 * e), v1 = T::load(v + 2 * e + 1);
           if constexpr (YM) {
             // SSD form: d A_bar_t = d a_t (into ddt's place, (re, im) pairs), dV = beta dw,
             // dbeta = erase part + dw . V (w = beta V)
             store_pair<T>(ddt + 2 * e, rv.x, rv.y);
             T::store(dv + 2 * e, bb * rv.z);
             T::store(dv + 2 * e + 1, bb * rv.w);
-            T::store(dbeta + e, gv.x + (rv.z * v0 + rv.w * v1));
+            const float db = gv.x + (rv.z * v0 + rv.w * v1);
+            if (R > 1)
+              dbp[e] = db;  // summed over the head's rows by the row-sum kernel
+            else
+              T::store(dbeta + e, db);
             continue;
           }
           const float dtv = T::load(dt + e), rrv = T::load(r + e);
@@ -1174,6 +1196,44 @@ __global__ __launch_bounds__(256) void fused_bwd_heads_kernel(const float2* __re
   }
 }
 
+// ---------------------------------------------------------------------------
+// SSD form with R > 1 state rows per head: dk and dbeta of each head are the
+// sums over its R virtual heads of the fp32 partials the main pass wrote,
+// dk[n, h, :] = sum_j dkp[n, h R + j, :], dbeta[n, h] = sum_j dbp[n, h R + j]
+// (n = token), in a fixed order.  One thread per 4 consecutive elements of
+// dk (D % 4 == 0); the first of a row's threads also sums dbeta.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void ssd_rows_sum_kernel(const float* __restrict__ dkp,
+                                                           const float* __restrict__ dbp,
+                                                           typename T::raw* __restrict__ dk,
+                                                           typename T::raw* __restrict__ dbeta, int64_t n_rows,
+                                                           int R, int D) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;  // (token, head, 4 elements)
+  const int qd = D / 4;
+  if (i >= n_rows * qd) return;
+  const int64_t row = i / qd;  // token * Hk + head
+  const int d0 = int(i - row * qd) * 4;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int j = 0; j < R; ++j) {
+    const float4 x = *reinterpret_cast<const float4*>(dkp + (row * R + j) * D + d0);
+    acc.x += x.x;
+    acc.y += x.y;
+    acc.z += x.z;
+    acc.w += x.w;
+  }
+  typename T::raw* o = dk + row * D + d0;
+  T::store(o, acc.x);
+  T::store(o + 1, acc.y);
+  T::store(o + 2, acc.z);
+  T::store(o + 3, acc.w);
+  if (d0 == 0) {
+    float b = 0.0f;
+    for (int j = 0; j < R; ++j) b += dbp[row * R + j];
+    T::store(dbeta + row, b);
+  }
+}
+
 }  // namespace cdssm
 
 // ---------------------------------------------------------------------------
@@ -1204,13 +1264,19 @@ BwdLayout bwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) 
   return w;
 }
 
+// SSD form with R > 1 state rows per head (H counting the virtual heads): the
+// fp32 partials dkp (B, L, H, D) and dbp (B, L, H) after the layout above,
+// 16-byte aligned.
+int64_t rows_partials_offset_floats(const BwdLayout& w) { return 2 * ((w.total() + 1) / 2) * 2; }
+int64_t rows_partials_floats(int64_t B, int64_t L, int64_t H, int64_t D) { return B * L * H * (D + 1); }
+
 template <typename T, int D>
 int launch_fused_bwd(const void* q, const void* k, const void* v, const void* beta, const void* sel_c,
                      const void* dt, const void* r, const float* alpha, const float* omega, float c,
                      const void* dy, const float* dh_final, const float* fwd_ws, void* dq, void* dk,
                      void* dv, void* dbeta, void* dsel, void* ddt, void* dr, float* dalpha,
                      float* domega, float* dh0, float* ws, int B, int L, int H, int Q,
-                     hipStream_t stream, hipEvent_t* ev, int* carry_fused) {
+                     hipStream_t stream, hipEvent_t* ev, int* carry_fused, int R = 1) {
   using raw = typename T::raw;
   const BwdLayout w = bwd_layout(B, L, H, D, Q);
   const int NC = w.NC, S = w.S;
@@ -1271,6 +1337,7 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
       a.NSEG = w.NSEG;
       a.n_hg = n_hgc;
       a.n_chain = B * n_hgc;
+      a.R = R;
       hipLaunchKernelGGL(bwd_epoch_kernel, dim3(1), dim3(64), 0, stream, a.ob.ctl);
       st = cdssm_host::check_launch("cdssm_fused_scan_bwd/epoch");
       if (st) return st;
@@ -1293,7 +1360,7 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
     if (ev) (void)hipEventRecord(ev[0], stream);
     hipLaunchKernelGGL((fused_bwd_corr_kernel<T, D>), dim3(unsigned(tiles_c)), dim3(kWave),
                        size_t(slots_c) * 2 * sizeof(float4), stream, (const raw*)q, (const raw*)k,
-                       (const raw*)beta, (const raw*)sel_c, (const raw*)dy, gsaved, lam0, L, H, Q, NC, n_hgc);
+                       (const raw*)beta, (const raw*)sel_c, (const raw*)dy, gsaved, lam0, L, H, Q, NC, n_hgc, R);
     st = cdssm_host::check_launch("cdssm_fused_scan_bwd/corr");
     if (st) return st;
     if (ev) (void)hipEventRecord(ev[1], stream);
@@ -1309,15 +1376,24 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
     if (st) return st;
     if (ev) (void)hipEventRecord(ev[3], stream);
   }
+  float* dkp = R > 1 ? ws + rows_partials_offset_floats(w) : nullptr;
+  float* dbp = R > 1 ? dkp + int64_t(B) * L * H * D : nullptr;
   hipLaunchKernelGGL((fused_bwd_main_kernel<T, D>), dim3(unsigned(tiles)), dim3(kWave),
                      size_t(slots) * 5 * sizeof(float4), stream, (const raw*)q, (const raw*)k, (const raw*)v,
                      (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c,
                      (const raw*)dy, states, saved, (const float2*)dsn, zck, cend, (raw*)dq, (raw*)dk, (raw*)dv,
-                     (raw*)dbeta, (raw*)dsel, (raw*)ddt, (raw*)dr, parts, L, H, Q, NC, fw.NCK, n_hg);
+                     (raw*)dbeta, (raw*)dsel, (raw*)ddt, (raw*)dr, parts, L, H, Q, NC, fw.NCK, n_hg, R, dkp, dbp);
   st = cdssm_host::check_launch("cdssm_fused_scan_bwd/main");
   if (st) return st;
   if (ev) (void)hipEventRecord(ev[4], stream);
   if constexpr (IsSsdY<T>::value) {  // no per-head dynamics parameters
+    if (R > 1) {
+      const int64_t n_rows = int64_t(B) * L * (H / R);
+      const int64_t threads = n_rows * (D / 4);
+      hipLaunchKernelGGL(ssd_rows_sum_kernel<T>, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, stream,
+                         (const float*)dkp, (const float*)dbp, (raw*)dk, (raw*)dbeta, n_rows, R, D);
+      st = cdssm_host::check_launch("cdssm_ssd_scan_bwd/rows_sum");
+    }
     if (ev) (void)hipEventRecord(ev[5], stream);
     return st;
   }
@@ -1356,6 +1432,17 @@ extern "C" int64_t cdssm_fused_scan_bwd_workspace_bytes(int64_t B, int64_t L, in
   return bwd_layout(B, L, H, D, chunk).total() * int64_t(sizeof(float2));
 }
 
+// The SSD form's backward workspace: the fused scan's with H N / 2 (virtual)
+// heads, plus, for N > 2, the fp32 dk and dbeta partials of every state row.
+extern "C" int64_t cdssm_ssd_scan_bwd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                                      int64_t chunk) {
+  if (B <= 0 || L <= 0 || H <= 0 || D <= 0 || chunk <= 0 || N < 2 || N > 32 || N % 2 != 0) return -1;
+  const int64_t Hv = H * (N / 2);
+  const BwdLayout w = bwd_layout(B, L, Hv, D, chunk);
+  if (N == 2) return w.total() * int64_t(sizeof(float2));
+  return (rows_partials_offset_floats(w) + rows_partials_floats(B, L, Hv, D)) * int64_t(sizeof(float));
+}
+
 namespace {
 int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, const void* beta,
                     const void* sel_c, const void* dt, const void* r, const float* alpha,
@@ -1373,8 +1460,16 @@ int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, cons
     cdssm_host::set_error("%s: B, L, H must be positive", op);
     return CDSSM_EINVAL;
   }
+  // SSD form: the N = 2 R state rows of a head run as R virtual heads (sharing the head's k and beta)
+  int64_t R = 1;
+  if (ssd && N > 2 && N % 2 == 0 && N <= 32) {
+    R = N / 2;
+    H *= R;
+    N = 2;
+  }
   if (N != 2) {
-    cdssm_host::set_error("%s: the fused scan supports state_dim N = 2, got %lld", op, (long long)N);
+    cdssm_host::set_error(ssd ? "%s: state_dim N must be even, 2 <= N <= 32, got %lld"
+                              : "%s: the fused scan supports state_dim N = 2, got %lld", op, (long long)N);
     return CDSSM_EINVAL;
   }
   if (D != 64 && D != 128) {
@@ -1408,10 +1503,11 @@ int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, cons
       cdssm_host::set_error("%s: K, dY and dK must be 16-byte aligned, dA_bar aligned to its (re, im) pair", op);
       return CDSSM_EINVAL;
     }
+    const int rr = int(R);
 #define CDSSM_SSD_BWD(TT, DD)                                                                                     \
   launch_fused_bwd<TT, DD>(q, k, v, beta, nullptr, dt, nullptr, nullptr, nullptr, 0.0f, nullptr, nullptr,        \
                            fwd_workspace, nullptr, dk, dv, dbeta, nullptr, ddt, nullptr, nullptr, nullptr, nullptr, \
-                           workspace, b, l, hh, qc, stream, ev, carry_fused)
+                           workspace, b, l, hh, qc, stream, ev, carry_fused, rr)
     if (dtype == 1) return D == 64 ? CDSSM_SSD_BWD(SsdY<BF16>, 64) : CDSSM_SSD_BWD(SsdY<BF16>, 128);
     return D == 64 ? CDSSM_SSD_BWD(SsdY<F32>, 64) : CDSSM_SSD_BWD(SsdY<F32>, 128);
 #undef CDSSM_SSD_BWD

@@ -154,7 +154,7 @@ __device__ __forceinline__ ResetMask<HPW> stage_scalars(const ChunkTile& tc, int
                                                    const float* __restrict__ omega, float c,
                                                    const TileScalars& s, float2* __restrict__ gam,
                                                    int64_t gam_base, float2* __restrict__ gsv = nullptr,
-                                                   float4* __restrict__ cend = nullptr, Pre pre = Pre{}) {
+                                                   float4* __restrict__ cend = nullptr, Pre pre = Pre{}, int R = 1) {
   constexpr int NB = kWave / HPW;
   constexpr int TPB = HPW;
   static_assert(NB * TPB == kWave, "blocks tile the slab");
@@ -178,7 +178,8 @@ __device__ __forceinline__ ResetMask<HPW> stage_scalars(const ChunkTile& tc, int
     for (int i = 0; i < TPB; ++i) {
       const int t = min(t0 + i, tc.nt - 1);
       const int64_t e = (tc.row0 + t) * H + hl;
-      bb[i] = T::load(beta + e);
+      // SSD form with R state rows per head: beta per real head (R virtual heads share it)
+      bb[i] = T::load(beta + (kSsd ? (tc.row0 + t) * (H / R) + hl / R : e));
       if constexpr (kAbar) {
         dd[i] = T::load(dt + 2 * e);  // a_t re, im
         rr[i] = T::load(dt + 2 * e + 1);
@@ -386,9 +387,10 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
     const typename T::raw* __restrict__ beta, const typename T::raw* __restrict__ dt,
     const typename T::raw* __restrict__ r, const float* __restrict__ alpha,
     const float* __restrict__ omega, float c, float2* __restrict__ summ, float2* __restrict__ gam,
-    int L, int H, int Q, int NC, int n_hg) {
+    int L, int H, int Q, int NC, int n_hg, int R = 1) {
   using Cfg = FusedCfg<T, D, LPH>;
   constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch;
+  constexpr bool YM = IsSsdY<T>::value;  // SSD form: R virtual heads (state rows) share each k row
   extern __shared__ float4 smem4[];
   const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
@@ -400,8 +402,9 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
   const int slots = round_up(Q, kWave) * HPW;
   const int64_t ch0 = (int64_t(tc.b) * NC + tc.chunk) * H + tc.hbase;
 
-  const RowStream ks = tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
-  const int rowb = H * D * T::bytes;  // token stride in bytes
+  const RowStream ks = YM ? tile_stream_rows<T>(k, tc, L, H, R, D, hh, sub * DPL)
+                          : tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
+  const int rowb = (YM ? H / R : H) * D * T::bytes;  // token stride of k in bytes
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb;
   RowVec<T, DPL> kb[PF];
@@ -411,7 +414,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
 #pragma unroll
                                                       for (int i = 0; i < PF; ++i)
                                                         kb[i].load(ks, min(i * rowb, slim));
-                                                    });
+                                                    }, R);
 #pragma unroll
   for (int i = 0; i < PF; ++i) kb[i].pin();
   __syncthreads();
@@ -592,7 +595,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
     const float* __restrict__ omega, float c, const float2* __restrict__ states,
     typename T::raw* __restrict__ y, float4* __restrict__ saved, float2* __restrict__ gsaved,
     float2* __restrict__ zck, float2* __restrict__ cend, int L, int H, int Q, int NC, int NCK, int n_hg,
-    const float2* __restrict__ ycorr = nullptr) {
+    const float2* __restrict__ ycorr = nullptr, int R = 1) {
   static_assert(CORR || !SAVE, "the training forward keeps the sequential correction");
   constexpr bool YM = IsSsdY<T>::value;  // SSD form: write Y (B,L,H,2,D), no q, no readout
   static_assert(CORR || !YM, "the SSD form keeps the sequential correction");
@@ -609,13 +612,15 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
   const int ntr = round_up(tc.nt, PF);
   const int slots = round_up(Q, kWave) * HPW;
 
-  const RowStream ks = tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
+  // SSD form: R virtual heads (state rows) share each k row
+  const RowStream ks = YM ? tile_stream_rows<T>(k, tc, L, H, R, D, hh, sub * DPL)
+                          : tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
   const RowStream qs = YM ? RowStream{} : tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
   // SSD form: this lane's slices of its head's Y re and im rows (D apart)
   const RowStream yre = YM ? tile_stream<T>(y, tc, L, H, 2 * D, hh, sub * DPL) : RowStream{};
   const RowStream yim = YM ? tile_stream<T>(y, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
   const int rowy = 2 * H * D * T::bytes;  // token stride of Y in bytes
-  const int rowb = H * D * T::bytes;  // token stride in bytes
+  const int rowb = (YM ? H / R : H) * D * T::bytes;  // token stride of k (and q) in bytes
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb;
   RowVec<T, DPL> kb[PF], qb[PF];
@@ -641,7 +646,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
                                                        kb[i].load(ks, min(i * rowb, slim));
                                                        if constexpr (!YM) qb[i].load(qs, min(i * rowb, slim));
                                                      }
-                                                   });
+                                                   }, R);
 #pragma unroll
   for (int i = 0; i < PF; ++i) {
     kb[i].pin();
@@ -905,6 +910,7 @@ struct OnePassArgs {
   float2* zck;     // SAVE: z_{t-1} at t % kZck == 0 (B, NC, H, NCK, D)
   float2* cend;    // SAVE: c^ after the chunk's last step (B, NC, H, D)
   int L, H, Q, NC, NSEG, NCK, n_hg, n_chain, n_items;
+  int R;           // SSD form: state rows per head (virtual heads sharing a k row); 1 otherwise
 };
 
 // One segment (work item): item = seg * n_chain + chain.
@@ -977,13 +983,15 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   float2* Sx = reinterpret_cast<float2*>(GF + W * HPW);
   int* ctrl = reinterpret_cast<int*>(Sx + SEGN);
 
-  const RowStream ks = tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
+  // SSD form: R virtual heads (state rows) share each k row
+  const RowStream ks = YM ? tile_stream_rows<T>(k, tc, L, H, a.R, D, hh, sub * DPL)
+                          : tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
   const RowStream qs = YM ? RowStream{} : tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
   // SSD form: this lane's slices of its head's Y re and im rows (D apart)
   const RowStream yre = YM ? tile_stream<T>(y, tc, L, H, 2 * D, hh, sub * DPL) : RowStream{};
   const RowStream yim = YM ? tile_stream<T>(y, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
   const int rowy = 2 * H * D * T::bytes;  // token stride of Y in bytes
-  const int rowb = H * D * T::bytes;  // token stride in bytes
+  const int rowb = (YM ? H / a.R : H) * D * T::bytes;  // token stride of k (and q) in bytes
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb;
   RowVec<T, DPL> kb[PF], qb[PF];
@@ -997,7 +1005,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
                                      SAVE ? gsaved : nullptr, GF + wv * HPW, [&] {
 #pragma unroll
                                        for (int i = 0; i < PF; ++i) kb[i].load(ks, min(i * rowb, slim));
-                                     });
+                                     }, a.R);
 #pragma unroll
     for (int i = 0; i < PF; ++i) kb[i].pin();
   }
@@ -1461,7 +1469,7 @@ template <typename T, int D, int LPH, int LPHS>
 int launch_fused_fwd(const void* q, const void* k, const void* v, const void* beta, const void* sel_c,
                      const void* dt, const void* r, const float* alpha, const float* omega, float c,
                      const float* h0, void* y, float* h_final, const FwdRegions& reg, int B, int L, int H,
-                     int Q, hipStream_t stream, hipEvent_t* ev, bool save, int* path) {
+                     int Q, hipStream_t stream, hipEvent_t* ev, bool save, int* path, int R = 1) {
   using raw = typename T::raw;
   constexpr int HPW = kWave / LPH, HPWS = kWave / LPHS;
   // the a_t input form is inference-only: its training branches name the
@@ -1547,6 +1555,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
       a.n_hg = n_hg;
       a.n_chain = B * n_hg;
       a.n_items = int(items);
+      a.R = R;
       if (path) *path = cdssm_host::kPathOne;
       hipLaunchKernelGGL(fwd_epoch_kernel, dim3(1), dim3(64), 0, stream, a.ob.ctl);
       const int est = cdssm_host::check_launch("cdssm_fused_scan_fwd/epoch");
@@ -1578,7 +1587,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   hipLaunchKernelGGL((fused_fwd_summary_kernel<T, D, LPHS>), dim3(unsigned(tiles_s)), dim3(kWave),
                      size_t(slots_s) * (sizeof(float4) + sizeof(float2)) + HPWS * sizeof(float4), stream,
                      (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)dt, (const raw*)r, alpha,
-                     omega, c, summ, gam, L, H, Q, NC, n_hgs);
+                     omega, c, summ, gam, L, H, Q, NC, n_hgs, R);
   int st = cdssm_host::check_launch("cdssm_fused_scan_fwd/summary");
   if (st) return st;
 
@@ -1635,12 +1644,12 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
     hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH, kSv>), dim3(unsigned(tiles)), dim3(kWave), lds_main,
                        stream, (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,
                        (const raw*)dt, (const raw*)r, alpha, omega, c, (const float2*)summ, (raw*)y, saved,
-                       gsaved, zck, cend, L, H, Q, NC, w.NCK, n_hg);
+                       gsaved, zck, cend, L, H, Q, NC, w.NCK, n_hg, nullptr, R);
   else
     hipLaunchKernelGGL((fused_fwd_main_kernel<T, D, LPH, false>), dim3(unsigned(tiles)), dim3(kWave), lds_main,
                        stream, (const raw*)q, (const raw*)k, (const raw*)v, (const raw*)beta, (const raw*)sel_c,
                        (const raw*)dt, (const raw*)r, alpha, omega, c, (const float2*)summ, (raw*)y, nullptr,
-                       nullptr, nullptr, nullptr, L, H, Q, NC, w.NCK, n_hg);
+                       nullptr, nullptr, nullptr, L, H, Q, NC, w.NCK, n_hg, nullptr, R);
   st = cdssm_host::check_launch("cdssm_fused_scan_fwd/main");
   if (ev) (void)hipEventRecord(ev[4], stream);
   return st;
@@ -1726,6 +1735,14 @@ extern "C" int64_t cdssm_fused_scan_workspace_bytes(int64_t B, int64_t L, int64_
   return fwd_layout(B, L, H, D, chunk).total() * int64_t(sizeof(float2));
 }
 
+// The SSD form's forward workspace: its N / 2 state rows per head are scanned as
+// virtual heads, so the layout is the fused scan's with H N / 2 heads.
+extern "C" int64_t cdssm_ssd_scan_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                                  int64_t chunk) {
+  if (N < 2 || N > 32 || N % 2 != 0) return -1;
+  return cdssm_fused_scan_workspace_bytes(B, L, H * (N / 2), D, 2, chunk);
+}
+
 namespace {
 // Scratch of a forward call: the caller's workspace (full layout), or, with
 // workspace NULL, the library's static per-device scratch (inference only).
@@ -1749,8 +1766,16 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
                           (long long)L, (long long)H);
     return CDSSM_EINVAL;
   }
+  // SSD form: the N = 2 R state rows of a head run as R virtual heads (sharing the head's k and beta)
+  int64_t R = 1;
+  if (ssd && N > 2 && N % 2 == 0 && N <= 32) {
+    R = N / 2;
+    H *= R;
+    N = 2;
+  }
   if (N != 2) {
-    cdssm_host::set_error("%s: the fused scan supports state_dim N = 2, got %lld", op, (long long)N);
+    cdssm_host::set_error(ssd ? "%s: state_dim N must be even, 2 <= N <= 32, got %lld"
+                              : "%s: the fused scan supports state_dim N = 2, got %lld", op, (long long)N);
     return CDSSM_EINVAL;
   }
   if (D != 64 && D != 128) {
@@ -1800,13 +1825,14 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
 #define CDSSM_FWD_ARGS q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, reg, b, l, hh, qc, stream, \
                        ev, save, path
   if (ssd) {
+    const int rr = int(R);
     if (dtype == 1) {
       if (D == 64)
-        return launch_fused_fwd<SsdY<BF16>, 64, CDSSM_FWD_LPH_BF16_D64, CDSSM_FWD_LPHS_BF16_D64>(CDSSM_FWD_ARGS);
-      return launch_fused_fwd<SsdY<BF16>, 128, 16, CDSSM_FWD_LPHS_BF16_D128>(CDSSM_FWD_ARGS);
+        return launch_fused_fwd<SsdY<BF16>, 64, CDSSM_FWD_LPH_BF16_D64, CDSSM_FWD_LPHS_BF16_D64>(CDSSM_FWD_ARGS, rr);
+      return launch_fused_fwd<SsdY<BF16>, 128, 16, CDSSM_FWD_LPHS_BF16_D128>(CDSSM_FWD_ARGS, rr);
     }
-    if (D == 64) return launch_fused_fwd<SsdY<F32>, 64, 16, 16>(CDSSM_FWD_ARGS);
-    return launch_fused_fwd<SsdY<F32>, 128, 32, 32>(CDSSM_FWD_ARGS);
+    if (D == 64) return launch_fused_fwd<SsdY<F32>, 64, 16, 16>(CDSSM_FWD_ARGS, rr);
+    return launch_fused_fwd<SsdY<F32>, 128, 32, 32>(CDSSM_FWD_ARGS, rr);
   }
   if (abar) {
     if (save) {

@@ -138,14 +138,17 @@ int cdssm_fused_scan_bwd(int dtype, const void* q, const void* k, const void* v,
  * SSDChunkwiseScan on the fused kernels, forward: replaces SSDChunkwiseScan.forward
  * (ssd.py:39-111), i.e. IntraChunkScanFn (ops.py:108-121, intra_chunk_scan.cu:560-609),
  * InterChunkScanFn (ops.py:146-155, inter_chunk_scan.cu:201-234), ExactCorrectionFn
- * (ops.py:173-186, exact_correction.cu:390-438) and Y = local_h + corrections, for
- * state_dim N = 2.  Inputs of `dtype`: a_bar (B,L,H,2), k (B,L,H,D), v (B,L,H,2) (already
- * VP-scaled, as block.py:194-195 passes it), beta (B,L,H).  Output Y (B,L,H,2,D) of `dtype`
- * (16-byte aligned) and h_final (B,H,2,D) fp32, the carry after the last token (the scan
- * starts from zero, as the reference's).  Intermediate states stay fp32.  train != 0 also
- * writes what cdssm_ssd_scan_bwd reads into the workspace
- * (cdssm_fused_scan_workspace_bytes() bytes).  Limits as cdssm_fused_scan_fwd.
+ * (ops.py:173-186, exact_correction.cu:390-438) and Y = local_h + corrections, for even
+ * state_dim 2 <= N <= 32.  Inputs of `dtype`: a_bar (B,L,H,N), k (B,L,H,D), v (B,L,H,N)
+ * (already VP-scaled, as block.py:194-195 passes it), beta (B,L,H).  Output Y (B,L,H,N,D) of
+ * `dtype` (16-byte aligned) and h_final (B,H,N,D) fp32, the carry after the last token (the
+ * scan starts from zero, as the reference's).  Each head's N / 2 complex state rows are scanned
+ * as virtual heads sharing the head's k rows and beta (the rows' recurrences are independent);
+ * intermediate states stay fp32.  train != 0 also writes what cdssm_ssd_scan_bwd reads into the
+ * workspace (cdssm_ssd_scan_workspace_bytes() bytes).  Limits otherwise as cdssm_fused_scan_fwd,
+ * with H N / 2 heads.
  */
+int64_t cdssm_ssd_scan_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t D, int64_t N, int64_t chunk);
 int cdssm_ssd_scan_fwd(int dtype, const void* a_bar, const void* k, const void* v, const void* beta, void* Y,
                        float* h_final, float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
                        int64_t chunk, int train, hipStream_t stream);
@@ -155,10 +158,13 @@ int cdssm_ssd_scan_fwd(int dtype, const void* a_bar, const void* k, const void* 
  * SSDChunkwiseScan through IntraChunkScanFn.backward (ops.py:123-135), InterChunkScanFn.backward
  * (ops.py:157-163) and ExactCorrectionFn.backward (ops.py:188-195, the reference's shifted rule),
  * as cdssm_fused_scan_bwd does for the readout form.  Inputs: the forward's inputs, dY
- * (B,L,H,2,D) of `dtype` and fwd_workspace as filled by cdssm_ssd_scan_fwd with train != 0.
- * Outputs of `dtype`: dA (B,L,H,2), dK (B,L,H,D), dV (B,L,H,2), dbeta (B,L,H).  k, dY and dK
- * 16-byte aligned.  workspace: cdssm_fused_scan_bwd_workspace_bytes() bytes.
+ * (B,L,H,N,D) of `dtype` and fwd_workspace as filled by cdssm_ssd_scan_fwd with train != 0.
+ * Outputs of `dtype`: dA (B,L,H,N), dK (B,L,H,D), dV (B,L,H,N), dbeta (B,L,H); for N > 2, dK
+ * and dbeta sum the state rows' fp32 contributions in a fixed order.  k, dY and dK 16-byte
+ * aligned.  workspace: cdssm_ssd_scan_bwd_workspace_bytes() bytes.
  */
+int64_t cdssm_ssd_scan_bwd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                           int64_t chunk);
 int cdssm_ssd_scan_bwd(int dtype, const void* a_bar, const void* k, const void* v, const void* beta,
                        const void* dY, const float* fwd_workspace, void* dA, void* dK, void* dV, void* dbeta,
                        float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N, int64_t chunk,

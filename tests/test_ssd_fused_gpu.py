@@ -19,14 +19,15 @@ pytestmark = pytest.mark.gpu
 TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2}
 
 
-def rand_ssd(gen, B, L, H, D, amax=1.0, amin=0.0):
-    """A_bar of magnitude in [amin, amax) and uniform phase, unit-norm keys, N(0,1) values, beta in [0, 1)."""
-    ang = torch.rand(B, L, H, generator=gen) * 2 * math.pi
-    mag = amin + torch.rand(B, L, H, generator=gen) * (amax - amin)
-    A = torch.stack([mag * torch.cos(ang), mag * torch.sin(ang)], -1)
+def rand_ssd(gen, B, L, H, D, amax=1.0, amin=0.0, N=2):
+    """A_bar (N / 2 complex pairs per head) of magnitude in [amin, amax) and uniform phase, unit-norm
+    keys, N(0,1) values, beta in [0, 1)."""
+    ang = torch.rand(B, L, H, N // 2, generator=gen) * 2 * math.pi
+    mag = amin + torch.rand(B, L, H, N // 2, generator=gen) * (amax - amin)
+    A = torch.stack([mag * torch.cos(ang), mag * torch.sin(ang)], -1).flatten(-2)
     K = torch.randn(B, L, H, D, generator=gen)
     K = K / K.norm(dim=-1, keepdim=True)
-    V = torch.randn(B, L, H, 2, generator=gen)
+    V = torch.randn(B, L, H, N, generator=gen)
     beta = torch.rand(B, L, H, generator=gen)
     return A, K, V, beta
 
@@ -52,7 +53,7 @@ def fused_grads(A, K, V, beta, gY, Q):
 
 def oracle_grads(A, K, V, beta, gY, Q):
     leaves = [t.double().requires_grad_(True) for t in (A, K, V, beta)]
-    Y = o.ssd_chunkwise_scan(*leaves, Q, 2, correction_fn=o.correction_with_reference_grad)
+    Y = o.ssd_chunkwise_scan(*leaves, Q, V.shape[-1], correction_fn=o.correction_with_reference_grad)
     g = torch.autograd.grad((Y * gY.double()).sum(), leaves)
     return Y.detach(), list(g)
 
@@ -138,6 +139,39 @@ def test_fused_ssd_one_launch_past_the_anchor_matches_oracle():
     errs.update({n: rel(sel(x), y) for n, x, y in zip(("dA", "dK", "dV", "dbeta"), g, g_ref)})
     log("   " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
     assert all(e <= 2e-2 for e in errs.values()), errs
+
+
+ROW_CASES = [
+    # name, dtype, N, B, L, H, D, Q
+    ("fp32_N4_D64", torch.float32, 4, 2, 300, 3, 64, 64),
+    ("fp32_N16_D64", torch.float32, 16, 1, 256, 2, 64, 64),
+    ("fp32_N16_D128_chunk48", torch.float32, 16, 1, 200, 3, 128, 48),
+    ("bf16_N16_D64", torch.bfloat16, 16, 2, 512, 4, 64, 64),
+    ("bf16_N8_D128_ragged", torch.bfloat16, 8, 1, 333, 5, 128, 128),
+    ("bf16_N32_D64", torch.bfloat16, 32, 1, 256, 2, 64, 64),
+]
+
+
+@pytest.mark.parametrize("path", ["four_launch", "one_pass"])
+@pytest.mark.parametrize("name,dtype,N,B,L,H,D,Q", ROW_CASES, ids=[c[0] for c in ROW_CASES])
+def test_fused_ssd_state_rows_match_oracle(name, dtype, N, B, L, H, D, Q, path):
+    """state_dim N > 2 (the reference default is 16): the N / 2 complex rows of each head run as
+    virtual heads sharing the head's k and beta; Y and every gradient against the oracle's
+    ssd_chunkwise_scan at that N (dK and dbeta sum the rows' contributions)."""
+    log(f"[fused SSD rows] {name} N{N} B{B} L{L} H{H} D{D} Q{Q} path {path}")
+    gen = torch.Generator().manual_seed(21)
+    A, K, V, beta = [t.to(dtype) for t in rand_ssd(gen, B, L, H, D, amax=0.99, N=N)]
+    gY = torch.randn(B, L, H, N, D, generator=gen).to(dtype)
+    Y_ref, g_ref = oracle_grads(A, K, V, beta, gY, Q)
+    with forward_path(path):
+        Y, g = fused_grads(A, K, V, beta, gY, Q)
+    from cdssm_hip import lookback_status
+    assert lookback_status() == 0, "a look-back wait timed out"
+    errs = {"Y": rel(Y, Y_ref)}
+    errs.update({n: rel(x, y) for n, x, y in zip(("dA", "dK", "dV", "dbeta"), g, g_ref)})
+    log("   " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
+    assert Y.shape == (B, L, H, N, D)
+    assert all(e <= TOL[dtype] for e in errs.values()), errs
 
 
 def test_fused_ssd_inference_call_keeps_no_records_and_matches_training_forward():
