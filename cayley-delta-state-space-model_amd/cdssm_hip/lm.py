@@ -11,8 +11,9 @@ readout_proj -> fp32 GroupNorm, * silu(z), + D x (HIP) -> out_proj with the
 residual in the GEMM epilogue.  Dense projections and the embedding are
 PyTorch (hipBLASLt GEMMs).  With gradients enabled (training) the block takes a
 differentiable path instead: conv1d+SiLU, DynamicsFusedFn, NormalizeKQFn and
-SSDChunkwiseScan over the per-pass scan ops (HIP, with the reference's
-backward rules) and torch for the rest.
+SSDChunkwiseScan (the fused scan kernels in their Y-materialising form, HIP,
+with the reference's backward rules) and torch for the rest.  With state_dim
+N != 2 the inference forward also materialises Y through SSDChunkwiseScan.
 
 Generation: ``CDSSMLMHeadModel.prefill`` runs the forward over a prompt and keeps
 per-layer decode state (conv window, the scan's R-mode state, GroupNorm running
@@ -587,9 +588,9 @@ class CDSSMBlock(nn.Module):
         K, Q, qk = normalize_kq_qk(K, Q)
         V = V.contiguous()
         if N != 2:
-            # N/2 complex pairs per head (the reference default is 16): the reference's own pass
-            # structure over the per-pass ops (block.py:194-211 with ssd.py:39-111); the readout and
-            # the shortcut in fp32, then rounded to the model dtype
+            # N/2 complex pairs per head (the reference default is 16): Y from SSDChunkwiseScan (its
+            # fused kernels, each pair a virtual head sharing k; block.py:194-211 with ssd.py:39-111);
+            # the readout and the shortcut in fp32, then rounded to the model dtype
             V_gated = V * vp.repeat_interleave(2, dim=-1)                                 # block.py:194-195
             Y = SSDChunkwiseScan(cfg.chunk_size, N)(A_bar, K, V_gated, beta)              # block.py:198
             ret = (Y.float() * Q.float().unsqueeze(-2)).sum(-1)                           # block.py:208
@@ -613,8 +614,8 @@ class CDSSMBlock(nn.Module):
 
     def _forward_autograd(self, x: Tensor, v_first: Optional[Tensor]):
         """The block with gradients (block.py:140-229, for training): the HIP ops that have a backward --
-        conv1d+SiLU (CUDAConv1dSiLUOp), DynamicsFusedFn, NormalizeKQFn and SSDChunkwiseScan over the
-        per-pass scan ops, whose backwards are the reference's -- and torch for the projections, the
+        conv1d+SiLU (CUDAConv1dSiLUOp), DynamicsFusedFn, NormalizeKQFn and SSDChunkwiseScan (the fused
+        scan kernels), whose backwards are the reference's -- and torch for the projections, the
         RMSNorm, the shortcut, the readout and the fp32 GroupNorm.  The readout and shortcut are formed as
         sum_d Y q + s (q.k)^2 V_gated (the reference adds s (q.k) V_gated k^T to Y and reads it with q:
         the same value) with elementwise products in the compute dtype."""
