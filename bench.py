@@ -260,6 +260,60 @@ def time_dropin(cfg_name, steps=10, warmup=2):
     return out
 
 
+def time_dropin_rows(B=4, L=2048, H=16, D=64, N=16, steps=5, warmup=2):
+    """The drop-in SSDChunkwiseScan at the reference's default state_dim (N = 16: 8 complex state rows per
+    head), fused kernels (each row a virtual head sharing k) against the per-pass ops, bf16, synthetic
+    inputs (|A_bar| in [0.5, 0.99), unit-norm keys).  Bytes of the interface: forward reads A_bar, K, V,
+    beta and writes Y (N D per token-head); backward reads dY and the inputs and writes their gradients."""
+    import torch
+    from cdssm_hip.ssd import SSDChunkwiseScan
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(0)
+    ang = torch.rand(B, L, H, N // 2, generator=g) * 2 * math.pi
+    mag = 0.5 + 0.49 * torch.rand(B, L, H, N // 2, generator=g)
+    A = torch.stack([mag * torch.cos(ang), mag * torch.sin(ang)], -1).flatten(-2).to(torch.bfloat16).to(dev)
+    K = torch.randn(B, L, H, D, generator=g)
+    K = (K / K.norm(dim=-1, keepdim=True)).to(torch.bfloat16).to(dev)
+    V = torch.randn(B, L, H, N, generator=g).to(torch.bfloat16).to(dev)
+    beta = torch.rand(B, L, H, generator=g).to(torch.bfloat16).to(dev)
+    gY = torch.randn(B, L, H, N, D, generator=g).to(torch.bfloat16).to(dev)
+    stream = torch.cuda.current_stream(dev)
+    BHL = B * H * L
+    by_f = BHL * ((D + 2 * N + 1) + N * D) * 2
+    by_b = BHL * (N * D + 2 * (D + 2 * N + 1)) * 2
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    out = {"workload": f"drop-in SSDChunkwiseScan B{B} L{L} H{H} D{D} N{N} bf16", "alg_bytes_fwd": by_f,
+           "alg_bytes_bwd": by_b}
+    for name, fused in (("fused", None), ("per_pass", False)):
+        m = SSDChunkwiseScan(D, N, fused=fused)
+        with torch.no_grad():
+            ms_f = timed(lambda: m(A, K, V, beta))
+        leaves = [t.detach().clone().requires_grad_(True) for t in (A, K, V, beta)]
+
+        def fb():
+            Y = m(*leaves)
+            Y.backward(gY)
+
+        ms_fb = timed(fb)
+        out[name] = {"fwd_ms": ms_f, "fwd_hbm_frac": by_f / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                     "fwd_bwd_ms": ms_fb,
+                     "fwd_bwd_hbm_frac": (by_f + by_b) / (ms_fb * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    return out
+
+
 def time_decode(steps, warmup, B=64, H=16, D=64, prompt=2048):
     """Recurrent decode at the config-4 decode shape, one layer: B64 H16 D64 bf16
     from a 2048-token prompt (fused scan over the prompt, then decode steps).
@@ -469,7 +523,8 @@ def main():
         copy_probe(args.copy_probe_mib)
         return
     if args.only_dropin:
-        print(json.dumps({"dropin_ssd_scan": time_dropin("C1", steps=args.steps, warmup=args.warmup)}), flush=True)
+        print(json.dumps({"dropin_ssd_scan": time_dropin("C1", steps=args.steps, warmup=args.warmup),
+                          "dropin_ssd_scan_n16": time_dropin_rows()}), flush=True)
         return
 
     import torch
@@ -590,6 +645,7 @@ def main():
             out["lm_decode"] = time_lm_decode()
     if not args.no_extras:
         out["dropin_ssd_scan"] = time_dropin("C1")
+        out["dropin_ssd_scan_n16"] = time_dropin_rows()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg, x, args.cpu_sample_batches)
         if not args.no_extras:

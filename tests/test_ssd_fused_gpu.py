@@ -174,6 +174,23 @@ def test_fused_ssd_state_rows_match_oracle(name, dtype, N, B, L, H, D, Q, path):
     assert all(e <= TOL[dtype] for e in errs.values()), errs
 
 
+@pytest.mark.parametrize("N,L", [(2, 256), (2, 300), (16, 200)])
+def test_fused_ssd_final_state_matches_oracle(N, L):
+    """h_final (B,H,N,D) fp32 of cdssm_ssd_scan_fwd: the R-mode carry after the last token, against the
+    oracle's return_final (equal to the state after the last chunk when L is a multiple of the chunk)."""
+    from cdssm_hip.scan import ssd_scan_fwd
+    gen = torch.Generator().manual_seed(31)
+    B, H, D, Q = 2, 3, 64, 64
+    A, K, V, beta = rand_ssd(gen, B, L, H, D, amax=0.99, N=N)
+    with torch.no_grad():
+        _, hf, _ = ssd_scan_fwd(*[t.to(DEV) for t in (A, K, V, beta)], Q)
+    torch.cuda.synchronize()
+    _, h_ref = o.ssd_chunkwise_scan(*[t.double() for t in (A, K, V, beta)], Q, N, return_final=True)
+    e = rel(hf, h_ref)
+    log(f"[fused SSD h_final] N{N} L{L}: rel err {e:.1e}")
+    assert hf.shape == (B, H, N, D) and e <= 1e-4
+
+
 def test_fused_ssd_inference_call_keeps_no_records_and_matches_training_forward():
     """Without gradients the forward runs without the training records; Y is the same (bit-identical)
     as the training forward's."""
