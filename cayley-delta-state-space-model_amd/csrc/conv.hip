@@ -227,18 +227,44 @@ __global__ __launch_bounds__(256) void conv1d_silu_bwd_kernel(const typename T::
 }
 
 // grad_weight (C, K) and grad_bias (C), fp32: the partial rows added in order.
-__global__ __launch_bounds__(256) void conv1d_silu_bwd_reduce_kernel(const float* __restrict__ part,
-                                                                     float* __restrict__ gw, float* __restrict__ gb,
-                                                                     int rows, int C, int K) {
-  const int i = int(blockIdx.x) * int(blockDim.x) + int(threadIdx.x);  // (tap j, channel c), j = K: bias
-  if (i >= (K + 1) * C) return;
-  const int j = i / C, c = i - j * C;
-  float a = 0.0f;
-  for (int r = 0; r < rows; ++r) a += part[(int64_t(r) * (K + 1) + j) * C + c];
-  if (j < K)
-    gw[int64_t(c) * K + j] = a;
-  else
-    gb[c] = a;
+// Sum of the partial rows: a workgroup of kRedWaves waves owns 64 adjacent
+// columns (j, c) of the (rows, K + 1, C) partials (one column per lane, so each
+// row's 64 values are one 256-byte load); wave w adds rows w, w + kRedWaves, ...
+// with four independent accumulators, and the waves' sums are added through LDS
+// in wave order, so the result does not depend on timing.
+constexpr int kRedWaves = 16;
+
+__global__ __launch_bounds__(64 * kRedWaves) void conv1d_silu_bwd_reduce_kernel(const float* __restrict__ part,
+                                                                                float* __restrict__ gw,
+                                                                                float* __restrict__ gb, int rows,
+                                                                                int C, int K) {
+  __shared__ float acc_s[kRedWaves][64];
+  const int lane = int(threadIdx.x) % 64, wv = int(threadIdx.x) / 64;
+  const int ncol = (K + 1) * C;
+  const int col = int(blockIdx.x) * 64 + lane;  // (tap j, channel c) = j * C + c; j = K: bias
+  const bool ok = col < ncol;
+  const int cc = ok ? col : ncol - 1;
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  int r = wv;
+  for (; r + 3 * kRedWaves < rows; r += 4 * kRedWaves) {
+    a0 += part[int64_t(r) * ncol + cc];
+    a1 += part[int64_t(r + kRedWaves) * ncol + cc];
+    a2 += part[int64_t(r + 2 * kRedWaves) * ncol + cc];
+    a3 += part[int64_t(r + 3 * kRedWaves) * ncol + cc];
+  }
+  for (; r < rows; r += kRedWaves) a0 += part[int64_t(r) * ncol + cc];
+  acc_s[wv][lane] = (a0 + a1) + (a2 + a3);
+  __syncthreads();
+  if (wv == 0 && ok) {
+    float a = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kRedWaves; ++w) a += acc_s[w][lane];
+    const int j = col / C, c = col - j * C;
+    if (j < K)
+      gw[int64_t(c) * K + j] = a;
+    else
+      gb[c] = a;
+  }
 }
 
 template <typename T, int K>
@@ -251,8 +277,8 @@ int launch_conv_bwd(const void* x, int64_t x_ts, const void* w, const void* bias
                      static_cast<const raw*>(x), x_ts, static_cast<const raw*>(w), static_cast<const raw*>(bias),
                      static_cast<const raw*>(gy), static_cast<raw*>(gx), ws, int(L), int(C), ntb, n);
   const int nr = int((K + 1) * C);
-  hipLaunchKernelGGL(conv1d_silu_bwd_reduce_kernel, dim3(unsigned((nr + 255) / 256)), dim3(256), 0, stream, ws, gw,
-                     gb, int(B * ntb), int(C), K);
+  hipLaunchKernelGGL(conv1d_silu_bwd_reduce_kernel, dim3(unsigned((nr + 63) / 64)), dim3(64 * kRedWaves), 0, stream,
+                     ws, gw, gb, int(B * ntb), int(C), K);
   return cdssm_host::check_launch("cdssm_conv1d_silu_bwd");
 }
 
