@@ -77,6 +77,70 @@ def test_fused_bwd_rejects_rows_beyond_32_bit_offsets_without_launching():
     assert "32-bit row offsets" in _lib.last_error()
 
 
+def _ssd_fwd_call(lib, **over):
+    args = dict(dtype=1, a_bar=16, k=16, v=16, beta=16, Y=16, h_final=16, ws=16, B=1, L=64, H=2, D=64, N=2,
+                chunk=64, train=0, stream=None)
+    args.update(over)
+    return lib.cdssm_ssd_scan_fwd(*args.values())
+
+
+def _ssd_bwd_call(lib, **over):
+    args = dict(dtype=1, a_bar=16, k=16, v=16, beta=16, dY=16, fwd_ws=16, dA=16, dK=16, dV=16, dbeta=16, ws=16,
+                B=1, L=64, H=2, D=64, N=2, chunk=64, stream=None)
+    args.update(over)
+    return lib.cdssm_ssd_scan_bwd(*args.values())
+
+
+@pytest.mark.parametrize("bad,msg", [
+    (dict(dtype=5), "dtype"),
+    (dict(N=3), "state_dim N must be even"),
+    (dict(N=34), "state_dim N must be even"),
+    (dict(D=48), "head_dim"),
+    (dict(chunk=129), "chunk"),
+    (dict(k=None), "null"),
+    (dict(Y=None), "null"),
+    (dict(k=8), "aligned"),
+    (dict(Y=24), "Y must be 16-byte aligned"),
+    (dict(H=1 << 18, D=128), "32-bit row offsets"),
+])
+def test_ssd_fwd_rejects_invalid_arguments_without_launching(bad, msg):
+    lib = _lib.load()
+    assert _ssd_fwd_call(lib, **bad) == -1
+    assert msg in _lib.last_error()
+
+
+@pytest.mark.parametrize("bad,msg", [
+    (dict(N=5), "state_dim N must be even"),
+    (dict(D=96), "head_dim"),
+    (dict(dY=None), "null"),
+    (dict(fwd_ws=None), "null"),
+    (dict(dY=8), "16-byte aligned"),
+    (dict(dK=40), "16-byte aligned"),
+    (dict(dA=2), "(re, im) pair"),
+])
+def test_ssd_bwd_rejects_invalid_arguments_without_launching(bad, msg):
+    lib = _lib.load()
+    assert _ssd_bwd_call(lib, **bad) == -1
+    assert msg in _lib.last_error()
+
+
+def test_ssd_workspaces_are_the_fused_scans_with_virtual_heads():
+    """N / 2 state rows per head scan as that many virtual heads: the forward workspace is the fused
+    scan's with H N / 2 heads; the backward's adds, for N > 2, fp32 dk and dbeta partials per row after
+    a 16-byte aligned layout."""
+    lib = _lib.load()
+    B, L, H, D, Q = 2, 1000, 3, 64, 64
+    for N in (2, 4, 16):
+        Hv = H * N // 2
+        assert lib.cdssm_ssd_scan_workspace_bytes(B, L, H, D, N, Q) == \
+            lib.cdssm_fused_scan_workspace_bytes(B, L, Hv, D, 2, Q)
+        base = lib.cdssm_fused_scan_bwd_workspace_bytes(B, L, Hv, D, 2, Q)
+        want = base if N == 2 else (-(-base // 16) * 16 + B * L * Hv * (D + 1) * 4)
+        assert lib.cdssm_ssd_scan_bwd_workspace_bytes(B, L, H, D, N, Q) == want
+    assert lib.cdssm_ssd_scan_workspace_bytes(B, L, H, D, 3, Q) == -1
+    assert lib.cdssm_ssd_scan_bwd_workspace_bytes(B, L, H, D, 34, Q) == -1
+
+
 def test_lookback_status_rejects_a_null_status_pointer_without_touching_the_gpu():
     lib = _lib.load()
     assert lib.cdssm_lookback_status(1, None) == -1
