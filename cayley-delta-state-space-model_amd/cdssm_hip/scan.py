@@ -194,7 +194,10 @@ class PreparedForward:
     Calling it re-launches the scan's kernels on torch's current stream with no
     validation, allocation or tensor creation on the host: the launch path for
     serving loops, graph capture and timing.  The bound tensors must stay alive
-    and keep their shapes.
+    and keep their shapes.  The first call draws the one-launch pass's look-back
+    epoch with a kernel of its own (cdssm_fused_scan_fwd); later calls reuse
+    the epoch the previous call left in the workspace it owns
+    (cdssm_fused_scan_fwd_continue): one launch per call.
     """
 
     def __init__(self, q, k, v, beta, sel_C, dt, r, alpha, omega, c, h0=None, chunk_size=None,
@@ -218,12 +221,19 @@ class PreparedForward:
         self._args = (_lib.DTYPE_CODE[dtype], *[_lib.ptr(t) for t in self.inputs[:9]], float(c),
                       _lib.ptr(h0), _lib.ptr(self.y), _lib.ptr(self.h_final), _lib.ptr(self.workspace),
                       B, L, H, D, N, Q)
+        self._continue = False  # the workspace holds a previous forward call's look-back area
 
     def __call__(self):
-        fn = self._lib.cdssm_fused_scan_fwd_train if self.train else self._lib.cdssm_fused_scan_fwd
+        lib = self._lib
+        if self._continue:
+            fn = lib.cdssm_fused_scan_fwd_train_continue if self.train else lib.cdssm_fused_scan_fwd_continue
+        else:
+            fn = lib.cdssm_fused_scan_fwd_train if self.train else lib.cdssm_fused_scan_fwd
         st = fn(*self._args, _lib.stream_of(self.device))
         if st != 0:
             _lib.check(st, "cdssm_fused_scan_fwd")
+        # a captured call does not run now: the workspace holds no call until one executes
+        self._continue = self._continue or not torch.cuda.is_current_stream_capturing()
         return self.y, self.h_final
 
     PHASES = ("summary", "carry_fold", "carry_replay", "main")
@@ -423,7 +433,9 @@ class PreparedBackward:
     Gradient buffers and the backward workspace are allocated once; each call
     re-launches the backward kernels for the bound cotangents on torch's
     current stream.  Call the forward first: the backward reads the entering
-    states the forward left in its workspace.
+    states the forward left in its workspace.  As PreparedForward, calls after
+    the first reuse the look-back epoch the previous call left in the backward
+    workspace (cdssm_fused_scan_bwd_continue).
     """
 
     def __init__(self, fwd: PreparedForward, dy: Tensor, dh_final: Optional[Tensor] = None, c: float = None):
@@ -448,11 +460,14 @@ class PreparedBackward:
                       _lib.ptr(alpha), _lib.ptr(omega), cval, _lib.ptr(self.dy), _lib.ptr(self.dh_final),
                       _lib.ptr(fwd.workspace), *[_lib.ptr(t) for t in self.grads], _lib.ptr(self.dalpha),
                       _lib.ptr(self.domega), _lib.ptr(self.dh0), _lib.ptr(self.workspace), B, L, H, D, N, Q)
+        self._continue = False
 
     def __call__(self):
-        st = self._lib.cdssm_fused_scan_bwd(*self._args, _lib.stream_of(self.device))
+        fn = self._lib.cdssm_fused_scan_bwd_continue if self._continue else self._lib.cdssm_fused_scan_bwd
+        st = fn(*self._args, _lib.stream_of(self.device))
         if st != 0:
             _lib.check(st, "cdssm_fused_scan_bwd")
+        self._continue = self._continue or not torch.cuda.is_current_stream_capturing()
         return self.grads
 
     PHASES = ("corr_adjoint", "rcarry_fold", "rcarry_replay", "main", "heads")

@@ -480,6 +480,7 @@ __global__ __launch_bounds__(64) void bwd_epoch_kernel(unsigned long long* ctl) 
   if (threadIdx.x == 0) {
     const unsigned long long n =
         __hip_atomic_fetch_add(&g_bwd_calls, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1ull;
+    __hip_atomic_store(ctl + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(ctl, epoch_word(2u, n), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
@@ -779,6 +780,7 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
 #pragma unroll
     for (int jj = 0; jj < DPL; ++jj) dp[jj] = acc[jj];
   }
+  advance_epoch_at_exit(a.ob.ctl, &g_bwd_calls, 2u);
 }
 
 // ---------------------------------------------------------------------------
@@ -1276,7 +1278,7 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
                      const void* dy, const float* dh_final, const float* fwd_ws, void* dq, void* dk,
                      void* dv, void* dbeta, void* dsel, void* ddt, void* dr, float* dalpha,
                      float* domega, float* dh0, float* ws, int B, int L, int H, int Q,
-                     hipStream_t stream, hipEvent_t* ev, int* carry_fused, int R = 1) {
+                     hipStream_t stream, hipEvent_t* ev, int* carry_fused, bool cont, int R = 1) {
   using raw = typename T::raw;
   const BwdLayout w = bwd_layout(B, L, H, D, Q);
   const int NC = w.NC, S = w.S;
@@ -1338,9 +1340,12 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
       a.n_hg = n_hgc;
       a.n_chain = B * n_hgc;
       a.R = R;
-      hipLaunchKernelGGL(bwd_epoch_kernel, dim3(1), dim3(64), 0, stream, a.ob.ctl);
-      st = cdssm_host::check_launch("cdssm_fused_scan_bwd/epoch");
-      if (st) return st;
+      // a continuing call runs on the epoch the previous call's last workgroup left
+      if (!cont) {
+        hipLaunchKernelGGL(bwd_epoch_kernel, dim3(1), dim3(64), 0, stream, a.ob.ctl);
+        st = cdssm_host::check_launch("cdssm_fused_scan_bwd/epoch");
+        if (st) return st;
+      }
       if (ev) (void)hipEventRecord(ev[0], stream);
       hipLaunchKernelGGL((fused_bwd_corrcarry_kernel<T, D>), dim3(unsigned(items)), dim3(kWave * kOnePassW), lds,
                          stream, a);
@@ -1450,7 +1455,8 @@ int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, cons
                     const float* fwd_workspace, void* dq, void* dk, void* dv, void* dbeta, void* dsel,
                     void* ddt, void* dr, float* dalpha, float* domega, float* dh0, float* workspace,
                     int64_t B, int64_t L, int64_t H, int64_t D, int64_t N, int64_t chunk,
-                    hipStream_t stream, hipEvent_t* ev, int* carry_fused = nullptr, bool ssd = false) {
+                    hipStream_t stream, hipEvent_t* ev, int* carry_fused = nullptr, bool ssd = false,
+                    bool cont = false) {
   const char* op = ssd ? "cdssm_ssd_scan_bwd" : "cdssm_fused_scan_bwd";
   if (dtype != 0 && dtype != 1) {
     cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
@@ -1507,7 +1513,7 @@ int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, cons
 #define CDSSM_SSD_BWD(TT, DD)                                                                                     \
   launch_fused_bwd<TT, DD>(q, k, v, beta, nullptr, dt, nullptr, nullptr, nullptr, 0.0f, nullptr, nullptr,        \
                            fwd_workspace, nullptr, dk, dv, dbeta, nullptr, ddt, nullptr, nullptr, nullptr, nullptr, \
-                           workspace, b, l, hh, qc, stream, ev, carry_fused, rr)
+                           workspace, b, l, hh, qc, stream, ev, carry_fused, cont, rr)
     if (dtype == 1) return D == 64 ? CDSSM_SSD_BWD(SsdY<BF16>, 64) : CDSSM_SSD_BWD(SsdY<BF16>, 128);
     return D == 64 ? CDSSM_SSD_BWD(SsdY<F32>, 64) : CDSSM_SSD_BWD(SsdY<F32>, 128);
 #undef CDSSM_SSD_BWD
@@ -1516,18 +1522,18 @@ int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, cons
     if (D == 64)
       return launch_fused_bwd<BF16, 64>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final,
                                         fwd_workspace, dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega,
-                                        dh0, workspace, b, l, hh, qc, stream, ev, carry_fused);
+                                        dh0, workspace, b, l, hh, qc, stream, ev, carry_fused, cont);
     return launch_fused_bwd<BF16, 128>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final,
                                        fwd_workspace, dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega,
-                                       dh0, workspace, b, l, hh, qc, stream, ev, carry_fused);
+                                       dh0, workspace, b, l, hh, qc, stream, ev, carry_fused, cont);
   }
   if (D == 64)
     return launch_fused_bwd<F32, 64>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final,
                                      fwd_workspace, dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0,
-                                     workspace, b, l, hh, qc, stream, ev, carry_fused);
+                                     workspace, b, l, hh, qc, stream, ev, carry_fused, cont);
   return launch_fused_bwd<F32, 128>(q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final,
                                     fwd_workspace, dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0,
-                                    workspace, b, l, hh, qc, stream, ev, carry_fused);
+                                    workspace, b, l, hh, qc, stream, ev, carry_fused, cont);
 }
 }  // namespace
 
@@ -1542,6 +1548,25 @@ extern "C" int cdssm_fused_scan_bwd(int dtype, const void* q, const void* k, con
   return fused_bwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final, fwd_workspace,
                          dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0, workspace, B, L, H, D, N,
                          chunk, stream, nullptr);
+}
+
+// cdssm_fused_scan_bwd for a workspace whose previous use was a backward call
+// (this entry or cdssm_fused_scan_bwd) of the same shape, completed or
+// ordered before this one on the stream, with the workspace untouched since:
+// the one-launch correction adjoint + carry reuses the look-back epoch that
+// call's last workgroup left in the workspace instead of a separate launch
+// drawing one.
+extern "C" int cdssm_fused_scan_bwd_continue(int dtype, const void* q, const void* k, const void* v,
+                                             const void* beta, const void* sel_c, const void* dt,
+                                             const void* r, const float* alpha, const float* omega, float c,
+                                             const void* dy, const float* dh_final, const float* fwd_workspace,
+                                             void* dq, void* dk, void* dv, void* dbeta, void* dsel, void* ddt,
+                                             void* dr, float* dalpha, float* domega, float* dh0, float* workspace,
+                                             int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                             int64_t chunk, hipStream_t stream) {
+  return fused_bwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final, fwd_workspace,
+                         dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0, workspace, B, L, H, D, N,
+                         chunk, stream, nullptr, nullptr, false, true);
 }
 
 // Backward of cdssm_ssd_scan_fwd (the SSDChunkwiseScan interface), with the

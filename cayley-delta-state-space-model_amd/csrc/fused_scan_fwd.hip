@@ -55,11 +55,13 @@ constexpr int kPrefetch = 8;
 __device__ unsigned long long g_fwd_calls;
 __device__ unsigned int g_fwd_status;
 
-// One thread: draw the next forward epoch into the control block.
+// One thread: draw the next forward epoch into the control block and clear
+// the count of finished workgroups.
 __global__ __launch_bounds__(64) void fwd_epoch_kernel(unsigned long long* ctl) {
   if (threadIdx.x == 0) {
     const unsigned long long n =
         __hip_atomic_fetch_add(&g_fwd_calls, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1ull;
+    __hip_atomic_store(ctl + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(ctl, epoch_word(1u, n), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
@@ -1391,12 +1393,13 @@ template <typename T, int D, int LPH, bool SAVE, bool PERSIST>
 __global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(OnePassArgs<T> a) {
   if (!PERSIST) {
     onepass_segment<T, D, LPH, SAVE>(a, int(blockIdx.x));
-    return;
+  } else {
+    for (int item = int(blockIdx.x); item < a.n_items; item += int(gridDim.x)) {
+      onepass_segment<T, D, LPH, SAVE>(a, item);
+      __syncthreads();  // LDS is reused by the next segment
+    }
   }
-  for (int item = int(blockIdx.x); item < a.n_items; item += int(gridDim.x)) {
-    onepass_segment<T, D, LPH, SAVE>(a, item);
-    __syncthreads();  // LDS is reused by the next segment
-  }
+  advance_epoch_at_exit(a.ob.ctl, &g_fwd_calls, 1u);
 }
 
 }  // namespace cdssm
@@ -1469,7 +1472,7 @@ template <typename T, int D, int LPH, int LPHS>
 int launch_fused_fwd(const void* q, const void* k, const void* v, const void* beta, const void* sel_c,
                      const void* dt, const void* r, const float* alpha, const float* omega, float c,
                      const float* h0, void* y, float* h_final, const FwdRegions& reg, int B, int L, int H,
-                     int Q, hipStream_t stream, hipEvent_t* ev, bool save, int* path, int R = 1) {
+                     int Q, hipStream_t stream, hipEvent_t* ev, bool save, int* path, bool cont, int R = 1) {
   using raw = typename T::raw;
   constexpr int HPW = kWave / LPH, HPWS = kWave / LPHS;
   // the a_t input form is inference-only: its training branches name the
@@ -1557,9 +1560,12 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
       a.n_items = int(items);
       a.R = R;
       if (path) *path = cdssm_host::kPathOne;
-      hipLaunchKernelGGL(fwd_epoch_kernel, dim3(1), dim3(64), 0, stream, a.ob.ctl);
-      const int est = cdssm_host::check_launch("cdssm_fused_scan_fwd/epoch");
-      if (est) return est;
+      // a continuing call runs on the epoch the previous call's last workgroup left
+      if (!cont) {
+        hipLaunchKernelGGL(fwd_epoch_kernel, dim3(1), dim3(64), 0, stream, a.ob.ctl);
+        const int est = cdssm_host::check_launch("cdssm_fused_scan_fwd/epoch");
+        if (est) return est;
+      }
       if (ev)
         for (int i = 0; i < 4; ++i) (void)hipEventRecord(ev[i], stream);
       const dim3 gd = dim3(unsigned(grid)), bd = dim3(kWave * kOnePassW);
@@ -1753,7 +1759,7 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
                     const float* omega, float c, const float* h0, void* y, float* h_final,
                     float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
                     int64_t chunk, hipStream_t stream, hipEvent_t* ev, bool save, int* path = nullptr,
-                    bool abar = false, bool no_alloc = false, bool ssd = false) {
+                    bool abar = false, bool no_alloc = false, bool ssd = false, bool cont = false) {
   const char* op = ssd ? "cdssm_ssd_scan_fwd"
                        : (no_alloc ? "cdssm_fused_scan_fwd_noalloc"
                                    : (abar ? "cdssm_fused_scan_fwd_abar" : "cdssm_fused_scan_fwd"));
@@ -1823,7 +1829,7 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
   }
   const int b = int(B), l = int(L), hh = int(H), qc = int(chunk);
 #define CDSSM_FWD_ARGS q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, reg, b, l, hh, qc, stream, \
-                       ev, save, path
+                       ev, save, path, cont
   if (ssd) {
     const int rr = int(R);
     if (dtype == 1) {
@@ -1866,6 +1872,22 @@ extern "C" int cdssm_fused_scan_fwd(int dtype, const void* q, const void* k, con
                                     int64_t chunk, hipStream_t stream) {
   return fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace,
                          B, L, H, D, N, chunk, stream, nullptr, false);
+}
+
+// cdssm_fused_scan_fwd for a workspace whose previous use was a forward call
+// (this entry, cdssm_fused_scan_fwd, or their training forms) of the same
+// shape, completed or ordered before this one on the stream, with the
+// workspace untouched since: the one-pass kernel reuses the look-back epoch
+// that call's last workgroup left in the workspace instead of a separate
+// launch drawing one.
+extern "C" int cdssm_fused_scan_fwd_continue(int dtype, const void* q, const void* k, const void* v,
+                                             const void* beta, const void* sel_c, const void* dt,
+                                             const void* r, const float* alpha, const float* omega, float c,
+                                             const float* h0, void* y, float* h_final, float* workspace,
+                                             int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                             int64_t chunk, hipStream_t stream) {
+  return fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace,
+                         B, L, H, D, N, chunk, stream, nullptr, false, nullptr, false, false, false, true);
 }
 
 // The inference forward with the library's static scratch in place of a
@@ -1914,6 +1936,17 @@ extern "C" int cdssm_fused_scan_fwd_train(int dtype, const void* q, const void* 
                                           int64_t chunk, hipStream_t stream) {
   return fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace,
                          B, L, H, D, N, chunk, stream, nullptr, true);
+}
+
+// cdssm_fused_scan_fwd_train on the same terms as cdssm_fused_scan_fwd_continue.
+extern "C" int cdssm_fused_scan_fwd_train_continue(int dtype, const void* q, const void* k, const void* v,
+                                                   const void* beta, const void* sel_c, const void* dt,
+                                                   const void* r, const float* alpha, const float* omega,
+                                                   float c, const float* h0, void* y, float* h_final,
+                                                   float* workspace, int64_t B, int64_t L, int64_t H, int64_t D,
+                                                   int64_t N, int64_t chunk, hipStream_t stream) {
+  return fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace,
+                         B, L, H, D, N, chunk, stream, nullptr, true, nullptr, false, false, false, true);
 }
 
 extern "C" int cdssm_fused_scan_fwd_profile(int dtype, const void* q, const void* k, const void* v,

@@ -110,6 +110,31 @@ int cdssm_fused_scan_fwd_train(int dtype, const void* q, const void* k, const vo
                                int64_t chunk, hipStream_t stream);
 
 /*
+ * cdssm_fused_scan_fwd and cdssm_fused_scan_fwd_train for a workspace whose
+ * previous use was a call of one of these four forward entries with the same
+ * shape, completed or ordered earlier on the same stream, with the workspace
+ * untouched since.  No counterpart in the reference: for callers that keep a
+ * workspace across calls (serving loops, training steps, captured graphs).
+ * Every one-launch pass draws a look-back epoch, a tag that tells this call's
+ * flags from earlier calls' in the never-cleared workspace; the entries above
+ * launch a one-thread kernel for it, while these reuse the one that the
+ * previous call's last workgroup left in the workspace (one launch per call
+ * instead of two).  Results are bit-identical to the entries above.  Calling
+ * them on a workspace that has not held such a call, or whose contents were
+ * changed since, may read stale look-back flags as ready.
+ */
+int cdssm_fused_scan_fwd_continue(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                                  const void* sel_c, const void* dt, const void* r, const float* alpha,
+                                  const float* omega, float c, const float* h0, void* y, float* h_final,
+                                  float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                  int64_t chunk, hipStream_t stream);
+int cdssm_fused_scan_fwd_train_continue(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                                        const void* sel_c, const void* dt, const void* r, const float* alpha,
+                                        const float* omega, float c, const float* h0, void* y, float* h_final,
+                                        float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                        int64_t chunk, hipStream_t stream);
+
+/*
  * Fused scan, backward.  Gradients are those the reference ops.py autograd
  * path produces for the same forward: exact for the readout (block.py:208-211),
  * for IntraChunkScanFn.backward (ops.py:123-135, intra_chunk_scan.cu:611-674)
@@ -133,6 +158,22 @@ int cdssm_fused_scan_bwd(int dtype, const void* q, const void* k, const void* v,
                          void* dsel_c, void* ddt, void* dr, float* dalpha, float* domega, float* dh0,
                          float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
                          int64_t chunk, hipStream_t stream);
+
+/*
+ * cdssm_fused_scan_bwd for a workspace whose previous use was a call of this
+ * entry or cdssm_fused_scan_bwd with the same shape, completed or ordered
+ * earlier on the same stream, with the workspace untouched since: the
+ * one-launch correction adjoint + carry reuses the look-back epoch the
+ * previous call left (as cdssm_fused_scan_fwd_continue; no counterpart in the
+ * reference).  Results are bit-identical to cdssm_fused_scan_bwd.
+ */
+int cdssm_fused_scan_bwd_continue(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                                  const void* sel_c, const void* dt, const void* r, const float* alpha,
+                                  const float* omega, float c, const void* dy, const float* dh_final,
+                                  const float* fwd_workspace, void* dq, void* dk, void* dv, void* dbeta,
+                                  void* dsel_c, void* ddt, void* dr, float* dalpha, float* domega, float* dh0,
+                                  float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                  int64_t chunk, hipStream_t stream);
 
 /*
  * SSDChunkwiseScan on the fused kernels, forward: replaces SSDChunkwiseScan.forward

@@ -2,9 +2,11 @@
 
 The one-pass forward and the backward's one-launch correction adjoint + carry
 exchange chunk summaries between workgroups through flags tagged with a
-per-call epoch.  The epoch is drawn on the device by a one-thread kernel
-launched before each pass, so a captured graph gets a fresh epoch on every
-replay.  These tests capture the passes once, then rewrite the bound inputs in
+per-call epoch.  The epoch is drawn on the device: by a one-thread kernel
+launched before the pass, or, for the calls PreparedForward / PreparedBackward
+make after their first (captured here), by the previous call's last workgroup,
+so a captured graph gets a fresh epoch on every replay either way.  These
+tests capture the passes once, then rewrite the bound inputs in
 place with new seeds between replays and check every replay against the fp64
 oracle (and against an eager call on the same inputs).  Tolerances as the
 other parity tests: fp32 <= 1e-4; bf16 y <= 2e-2, state norms <= 1e-3.
