@@ -517,13 +517,13 @@ constexpr uint64_t kSpinTicks = 5000000;  // look-back wait bound: 50 ms of the 
 // Look-back area of a one-launch pass: per (b, segment, head) a map (D
 // complex + one complex scalar), a state (D complex) and an 8-byte flag, then
 // a control block of kCtlWords 8-byte words whose first word is the call's
-// epoch and second the count of finished workgroups.  The area is never
-// cleared: a flag counts only when its upper bits equal the epoch of the
-// running call, which a one-thread kernel launched just before the pass draws
-// from a device-side counter and writes into the control block, or, for the
-// *_continue calls, the previous call's last workgroup left there
-// (advance_epoch_at_exit).  Drawing it on the device keeps a captured HIP
-// graph correct: every replay gets a new epoch.
+// epoch and second a count of workgroups.  The area is never cleared: a flag
+// counts only when its upper bits equal the epoch of the running call, which
+// a one-thread kernel launched just before the pass draws from a device-side
+// counter and writes into the control block, or, for the *_continue calls,
+// the previous call left there (arrive_and_draw_next_epoch).  Drawing it on
+// the device keeps a captured HIP graph correct: every replay gets a new
+// epoch.
 struct OnePassBufs {
   float2* seg_f;             // (B, NSEG, H, D) segment map F: state at the segment's end from zero
   float2* seg_s;             // (B, NSEG, H, D) state leaving the segment
@@ -541,28 +541,26 @@ __device__ __forceinline__ unsigned long long epoch_word(unsigned tag, unsigned 
 __device__ __forceinline__ unsigned long long load_epoch(const unsigned long long* ctl) {
   return __hip_atomic_load(const_cast<unsigned long long*>(ctl), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// The last workgroup of a one-launch pass to finish draws the epoch of the
-// next call on the same look-back area.  Each workgroup, after its last use
-// of the area (and so after it read ctl[0] at entry), counts itself in ctl[1];
-// the one whose count completes a multiple of the grid size resets the count
-// and stores a new epoch, drawn from the pass's call counter, into ctl[0].
-// Counting modulo the grid size elects exactly one workgroup whatever ctl[1]
-// held before.  A caller whose previous use of the workspace was a call of the
-// same pass and shape can then skip the epoch kernel (the *_continue entry
-// points); a captured graph of such calls leaves a new epoch after every replay.
-__device__ __forceinline__ void advance_epoch_at_exit(unsigned long long* ctl, unsigned long long* calls,
-                                                      unsigned tag) {
-  __syncthreads();  // every wave of the workgroup is done with the area
-  if (threadIdx.x == 0) {
-    const unsigned long long g = gridDim.x;
-    const unsigned long long old =
-        __hip_atomic_fetch_add(ctl + 1, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((old + 1ull) % g == 0ull) {
-      const unsigned long long n =
-          __hip_atomic_fetch_add(calls, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1ull;
-      __hip_atomic_store(ctl + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(ctl, epoch_word(tag, n), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+// The epoch of the next call on the same look-back area is drawn by the last
+// workgroup of a one-launch pass to have read this call's.  Each workgroup
+// reads ctl[0] once, at entry, and after it has published its first flag
+// (which used that epoch) one thread counts the workgroup in ctl[1]; the one
+// whose count completes a multiple of the grid size resets the count and
+// stores a new epoch, drawn from the pass's call counter, into ctl[0].  Every
+// workgroup of the call holds its epoch by then, so the store can come
+// mid-pass, off the kernel's tail.  Counting modulo the grid size elects
+// exactly one workgroup whatever ctl[1] held before.  A caller whose previous
+// use of the workspace was a call of the same pass and shape can then skip the
+// epoch kernel (the *_continue entry points); a captured graph of such calls
+// leaves a new epoch after every replay.
+__device__ __forceinline__ void arrive_and_draw_next_epoch(unsigned long long* ctl, unsigned long long* calls,
+                                                           unsigned tag) {
+  const unsigned long long g = gridDim.x;
+  const unsigned long long old = __hip_atomic_fetch_add(ctl + 1, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if ((old + 1ull) % g == 0ull) {
+    const unsigned long long n = __hip_atomic_fetch_add(calls, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1ull;
+    __hip_atomic_store(ctl + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ctl, epoch_word(tag, n), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 // Bits of the sticky look-back status word (cdssm_lookback_status).

@@ -661,8 +661,11 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
   }
   wait_stores_acked();
   __syncthreads();
-  if (threadIdx.x == 0)
+  if (threadIdx.x == 0) {
     __hip_atomic_store(flag, (epoch << 2) | 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // every workgroup of the grid holds this call's epoch once all have published
+    arrive_and_draw_next_epoch(ob.ctl, &g_bwd_calls, 2u);
+  }
 
   // ---- carry adjoint at the segment's right end, from its anchor ----
   const int anc = rs == 0 ? 0 : kAnchor * ((rs - 1) / kAnchor);  // counted from the right
@@ -780,7 +783,6 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
 #pragma unroll
     for (int jj = 0; jj < DPL; ++jj) dp[jj] = acc[jj];
   }
-  advance_epoch_at_exit(a.ob.ctl, &g_bwd_calls, 2u);
 }
 
 // ---------------------------------------------------------------------------

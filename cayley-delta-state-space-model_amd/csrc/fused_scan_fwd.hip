@@ -916,8 +916,12 @@ struct OnePassArgs {
 };
 
 // One segment (work item): item = seg * n_chain + chain.
+// epoch: this call's, read once by the workgroup at entry; arrive: this is the
+// workgroup's first segment, after whose first flag it counts itself for the
+// next call's epoch (arrive_and_draw_next_epoch).
 template <typename T, int D, int LPH, bool SAVE>
-__device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int item) {
+__device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int item, unsigned long long epoch,
+                                                bool arrive) {
   const typename T::raw* __restrict__ q = a.q;
   const typename T::raw* __restrict__ k = a.k;
   const typename T::raw* __restrict__ v = a.v;
@@ -938,7 +942,6 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   float2* __restrict__ gsaved = a.gsaved;
   float2* __restrict__ zck = a.zck;
   float2* __restrict__ cend = a.cend;
-  const unsigned long long epoch = load_epoch(a.ob.ctl);
   const int L = a.L, H = a.H, Q = a.Q, NC = a.NC, NSEG = a.NSEG, n_hg = a.n_hg;
   using Cfg = FusedCfg<T, D, LPH>;
   constexpr bool YM = IsSsdY<T>::value;  // SSD form: write Y (B,L,H,2,D), no q, no readout
@@ -1127,8 +1130,10 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   }
   wait_stores_acked();
   __syncthreads();
-  if (threadIdx.x == 0)
+  if (threadIdx.x == 0) {
     __hip_atomic_store(flag, (epoch << 2) | 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (arrive) arrive_and_draw_next_epoch(ob.ctl, &g_fwd_calls, 1u);
+  }
 
   // state entering the segment, in a fixed order (so results do not depend on
   // timing): from the anchor a = kAnchor * floor((seg - 1) / kAnchor) -- h0
@@ -1391,15 +1396,16 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
 // finished ones.
 template <typename T, int D, int LPH, bool SAVE, bool PERSIST>
 __global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(OnePassArgs<T> a) {
+  // read once: the call's last workgroup to have read it stores the next call's
+  const unsigned long long epoch = load_epoch(a.ob.ctl);
   if (!PERSIST) {
-    onepass_segment<T, D, LPH, SAVE>(a, int(blockIdx.x));
-  } else {
-    for (int item = int(blockIdx.x); item < a.n_items; item += int(gridDim.x)) {
-      onepass_segment<T, D, LPH, SAVE>(a, item);
-      __syncthreads();  // LDS is reused by the next segment
-    }
+    onepass_segment<T, D, LPH, SAVE>(a, int(blockIdx.x), epoch, true);
+    return;
   }
-  advance_epoch_at_exit(a.ob.ctl, &g_fwd_calls, 1u);
+  for (int item = int(blockIdx.x); item < a.n_items; item += int(gridDim.x)) {
+    onepass_segment<T, D, LPH, SAVE>(a, item, epoch, item == int(blockIdx.x));
+    __syncthreads();  // LDS is reused by the next segment
+  }
 }
 
 }  // namespace cdssm
