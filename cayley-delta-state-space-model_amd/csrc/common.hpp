@@ -604,6 +604,8 @@ int resident_capacity(const void* fn, int block, size_t lds);
 // (bf16 inference forward, chunk a multiple of 16 up to 128; for measurement).
 enum { kPathAuto = 0, kPathFour = 1, kPathOne = 2, kPathSweep = 3 };
 int scan_path();
+// Wide staging loads in the one-pass inference forward (off with CDSSM_NARROW_STAGING set; for measurement).
+bool wide_staging();
 }  // namespace cdssm_host
 
 // Status codes returned by every entry point.

@@ -145,7 +145,17 @@ struct NoPrefetch {
   __device__ void operator()() const {}
 };
 
-template <typename T, int HPW, bool MAIN, typename Pre = NoPrefetch>
+// Wide staging loads (WIDE: the scan-level bf16 form, 8 heads per wave, H a
+// multiple of 8 and chunks of at most 64 tokens): lane t loads token t's
+// 16-byte rows of the wave's 8 heads (beta, sel_C, dt, r; v as two rows of 4
+// (re, im) pairs) -- six loads instead of 7 * 8 two-byte ones -- and writes
+// them to LDS, from where the staging lanes read their (head, token block)
+// values.  Token t's rows sit at 16-byte unit t + t / 8 of each array (a
+// 16-byte pad after every 8 tokens), so the reads of one instruction fall in
+// 32 distinct banks.
+constexpr int kWideUnits = kWave + kWave / 8;  // 16-byte units of one array
+
+template <typename T, int HPW, bool MAIN, typename Pre = NoPrefetch, bool WIDE = false>
 __device__ __forceinline__ ResetMask<HPW> stage_scalars(const ChunkTile& tc, int H, int ntr,
                                                    const typename T::raw* __restrict__ v,
                                                    const typename T::raw* __restrict__ beta,
@@ -176,6 +186,43 @@ __device__ __forceinline__ ResetMask<HPW> stage_scalars(const ChunkTile& tc, int
   for (int tl = 0; tl < ntr; tl += kWave) {
     const int t0 = tl + blk * TPB;
     float bb[TPB], dd[TPB], rr[TPB], v0[TPB], v1[TPB], sc[TPB], vq[TPB];
+    if constexpr (WIDE) {
+      static_assert(MAIN && HPW == 8 && T::bytes == 2 && !kAbar, "wide staging: scan-level bf16, 8 heads");
+      // lane = token (clamped into the chunk): 16-byte rows of the wave's 8 heads
+      const int64_t e0 = (tc.row0 + min(lane, tc.nt - 1)) * H + tc.hbase;
+      const uint4 lb = *reinterpret_cast<const uint4*>(beta + e0);
+      const uint4 ls = *reinterpret_cast<const uint4*>(sel_c + e0);
+      const uint4 ld = *reinterpret_cast<const uint4*>(dt + e0);
+      const uint4 lr = *reinterpret_cast<const uint4*>(r + e0);
+      const uint4 lv0 = *reinterpret_cast<const uint4*>(v + 2 * e0);
+      const uint4 lv1 = *reinterpret_cast<const uint4*>(v + 2 * e0 + 8);
+      // the caller's row loads go out before these rows are waited for
+      pre();
+      __builtin_amdgcn_sched_barrier(0);
+      // exchange through LDS: the wave's B slots, which are written only after these reads
+      uint4* xw = reinterpret_cast<uint4*>(s.B);
+      const int u = lane + lane / 8;
+      xw[0 * kWideUnits + u] = lb;
+      xw[1 * kWideUnits + u] = ls;
+      xw[2 * kWideUnits + u] = ld;
+      xw[3 * kWideUnits + u] = lr;
+      xw[4 * kWideUnits + u] = lv0;
+      xw[5 * kWideUnits + u] = lv1;
+      const uint16_t* xh = reinterpret_cast<const uint16_t*>(s.B);
+      const uint32_t* xv = reinterpret_cast<const uint32_t*>(s.B);
+#pragma unroll
+      for (int i = 0; i < TPB; ++i) {
+        const int ut = t0 + i + blk;  // 16-byte unit of token t0 + i (t0 = 8 blk)
+        bb[i] = bf16_to_f32(xh[(0 * kWideUnits + ut) * 8 + j]);
+        sc[i] = bf16_to_f32(xh[(1 * kWideUnits + ut) * 8 + j]);
+        dd[i] = bf16_to_f32(xh[(2 * kWideUnits + ut) * 8 + j]);
+        rr[i] = bf16_to_f32(xh[(3 * kWideUnits + ut) * 8 + j]);
+        const uint32_t pv = xv[((4 + j / 4) * kWideUnits + ut) * 4 + j % 4];
+        v0[i] = bf16_lo(pv);
+        v1[i] = bf16_hi(pv);
+        vq[i] = 0.0f;
+      }
+    } else {
 #pragma unroll
     for (int i = 0; i < TPB; ++i) {
       const int t = min(t0 + i, tc.nt - 1);
@@ -198,6 +245,7 @@ __device__ __forceinline__ ResetMask<HPW> stage_scalars(const ChunkTile& tc, int
     // the caller's row prefetch goes after these small loads, so waiting for
     // them does not wait for the rows
     if (tl == 0) pre();
+    }
     // dynamics and local (in-block) prefixes; computed for every slot (the
     // clamped loads hold valid numbers) and replaced by an inert step where
     // the slot is not a real token, so the tokens interleave without branches
@@ -919,7 +967,7 @@ struct OnePassArgs {
 // epoch: this call's, read once by the workgroup at entry; arrive: this is the
 // workgroup's first segment, after whose first flag it counts itself for the
 // next call's epoch (arrive_and_draw_next_epoch).
-template <typename T, int D, int LPH, bool SAVE>
+template <typename T, int D, int LPH, bool SAVE, bool WIDE>
 __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int item, unsigned long long epoch,
                                                 bool arrive) {
   const typename T::raw* __restrict__ q = a.q;
@@ -1006,11 +1054,13 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   ResetMask<HPW> rm{0u, 0u};
 
   if (live) {
-    rm = stage_scalars<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, alpha, omega, c, s, nullptr, 0,
-                                     SAVE ? gsaved : nullptr, GF + wv * HPW, [&] {
+    const auto pre = [&] {
 #pragma unroll
-                                       for (int i = 0; i < PF; ++i) kb[i].load(ks, min(i * rowb, slim));
-                                     }, a.R);
+      for (int i = 0; i < PF; ++i) kb[i].load(ks, min(i * rowb, slim));
+    };
+    rm = stage_scalars<T, HPW, true, decltype(pre), WIDE>(tc, H, ntr, v, beta, sel_c, dt, r, alpha, omega, c, s,
+                                                          nullptr, 0, SAVE ? gsaved : nullptr, GF + wv * HPW, pre,
+                                                          a.R);
 #pragma unroll
     for (int i = 0; i < PF; ++i) kb[i].pin();
   }
@@ -1394,16 +1444,17 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
 // PERSIST true: the grid is resident at once and takes the segments in order,
 // so the lowest unfinished segment is always running and waits only on
 // finished ones.
-template <typename T, int D, int LPH, bool SAVE, bool PERSIST>
+// WIDE: the wide staging loads (the caller checks H % 8 == 0 and chunk <= 64).
+template <typename T, int D, int LPH, bool SAVE, bool PERSIST, bool WIDE = false>
 __global__ __launch_bounds__(kWave * kOnePassW) void fused_fwd_onepass_kernel(OnePassArgs<T> a) {
   // read once: the call's last workgroup to have read it stores the next call's
   const unsigned long long epoch = load_epoch(a.ob.ctl);
   if (!PERSIST) {
-    onepass_segment<T, D, LPH, SAVE>(a, int(blockIdx.x), epoch, true);
+    onepass_segment<T, D, LPH, SAVE, WIDE>(a, int(blockIdx.x), epoch, true);
     return;
   }
   for (int item = int(blockIdx.x); item < a.n_items; item += int(gridDim.x)) {
-    onepass_segment<T, D, LPH, SAVE>(a, item, epoch, item == int(blockIdx.x));
+    onepass_segment<T, D, LPH, SAVE, WIDE>(a, item, epoch, item == int(blockIdx.x));
     __syncthreads();  // LDS is reused by the next segment
   }
 }
@@ -1428,10 +1479,11 @@ size_t onepass_lds(int Q) {
 
 // Workgroups of the one-pass kernel resident at once (its grid: a workgroup
 // may wait on any earlier segment); 0 if it cannot run.
-template <typename T, int D, int LPH, bool SAVE, bool PERSIST>
+template <typename T, int D, int LPH, bool SAVE, bool PERSIST, bool WIDE = false>
 int onepass_capacity(size_t lds) {
   return cdssm_host::resident_capacity(
-      reinterpret_cast<const void*>(&fused_fwd_onepass_kernel<T, D, LPH, SAVE, PERSIST>), kWave * kOnePassW, lds);
+      reinterpret_cast<const void*>(&fused_fwd_onepass_kernel<T, D, LPH, SAVE, PERSIST, WIDE>), kWave * kOnePassW,
+      lds);
 }
 
 // Where a forward call keeps its scratch: the carry arrays of the four-launch
@@ -1520,10 +1572,15 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
     // segments than that: the persistent one-pass only for inference with
     // full rounds (measured on MI355X: faster than four launches at C3,
     // slower at C2's 1.5 rounds and for the training forward's records)
-    const int cap1 = save ? onepass_capacity<T, D, LPH, kSv, false>(lds)
-                          : onepass_capacity<T, D, LPH, false, false>(lds);
-    const int capp = save ? onepass_capacity<T, D, LPH, kSv, true>(lds)
-                          : onepass_capacity<T, D, LPH, false, true>(lds);
+    // the inference forward's wide staging loads: bf16 scan-level form, 8 heads per wave
+    constexpr bool kWideOk = std::is_same<T, BF16>::value && kWave / LPH == 8;
+    const bool wide = kWideOk && !save && H % 8 == 0 && Q <= kWave && cdssm_host::wide_staging();
+    const int cap1 = save   ? onepass_capacity<T, D, LPH, kSv, false>(lds)
+                     : wide ? onepass_capacity<T, D, LPH, false, false, kWideOk>(lds)
+                            : onepass_capacity<T, D, LPH, false, false>(lds);
+    const int capp = save   ? onepass_capacity<T, D, LPH, kSv, true>(lds)
+                     : wide ? onepass_capacity<T, D, LPH, false, true, kWideOk>(lds)
+                            : onepass_capacity<T, D, LPH, false, true>(lds);
     const bool single = cap1 > 0 && items <= cap1;
     const bool forced = mode == cdssm_host::kPathOne;
     const int64_t rounds = capp > 0 ? (items + capp - 1) / capp : 0;
@@ -1579,6 +1636,10 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
         hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, kSv, false>), gd, bd, lds, stream, a);
       else if (save)
         hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, kSv, true>), gd, bd, lds, stream, a);
+      else if (single && wide)
+        hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, false, false, kWideOk>), gd, bd, lds, stream, a);
+      else if (wide)
+        hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, false, true, kWideOk>), gd, bd, lds, stream, a);
       else if (single)
         hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, false, false>), gd, bd, lds, stream, a);
       else

@@ -1,5 +1,6 @@
 // Error reporting for the C-ABI: every entry point returns an int status and
 // leaves a human-readable message retrievable with cdssm_last_error().
+#include <cstdlib>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -63,6 +64,10 @@ std::atomic<int> g_scan_path{kPathAuto};
 }
 
 int scan_path() { return g_scan_path.load(std::memory_order_relaxed); }
+bool wide_staging() {
+  static const bool on = std::getenv("CDSSM_NARROW_STAGING") == nullptr;
+  return on;
+}
 
 }  // namespace cdssm_host
 
