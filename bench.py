@@ -71,6 +71,9 @@ def parse():
                     help="how the forward is launched (default: the library's own choice)")
     ap.add_argument("--only-dropin", action="store_true",
                     help="only time the drop-in SSDChunkwiseScan at C1 (fused and per-pass) and print its JSON")
+    ap.add_argument("--phase-stamps", type=int, default=0,
+                    help="only run this many stamped one-pass forwards of --config (after --warmup plain "
+                         "calls) and print the per-wave phase durations of the one-pass kernel as JSON")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a device copy of this many MiB (read + write), 10 times, and exit: "
                          "the reference kernel for scaling HBM byte counters")
@@ -86,6 +89,47 @@ def copy_probe(mib):
         b.copy_(a)
     torch.cuda.synchronize()
     print(json.dumps({"copy_probe_bytes_read_per_call": n * 4, "bytes_written_per_call": n * 4, "calls": 10}))
+
+
+def phase_stamps(cfg_name, calls, warmup):
+    """Per-wave phase durations of the one-pass forward kernel, from the real-time
+    counter (100 MHz) that the stamped entry records at eight points of each wave's
+    segment.  Percentiles over every wave of `calls` stamped calls, in microseconds."""
+    import torch
+    from cdssm_hip.scan import PreparedForward
+    from cdssm_hip.workloads import CONFIGS, draw_inputs
+
+    cfg = CONFIGS[cfg_name]
+    dev = torch.device("cuda:0")
+    x = draw_inputs(cfg, seed=0)
+    g = {n: (t.to(dev) if isinstance(t, torch.Tensor) else t) for n, t in x.items()}
+    run = PreparedForward(g["q"], g["k"], g["v"], g["beta"], g["sel_C"], g["dt"], g["r"], g["alpha"],
+                          g["omega"], g["c"], h0=g["h0"])
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    us = 0.01  # microseconds per tick
+    pts = PreparedForward.STAMP_POINTS
+    rows, spans, starts = [], [], []
+    for _ in range(calls):
+        st = run.phase_stamps().double()
+        t0 = st[:, 0].min()
+        spans.append(float(st[:, 7].max() - t0) * us)
+        starts.append((st[:, 0] - t0) * us)
+        rows.append((st[:, 1:] - st[:, :-1]) * us)
+    d = torch.cat(rows)
+    start = torch.cat(starts)
+    qs = torch.tensor([0.1, 0.5, 0.9], dtype=torch.float64)
+
+    def pct(t):
+        return [round(float(v), 2) for v in torch.quantile(t, qs)]
+
+    phases = {f"{pts[i]}->{pts[i + 1]}": pct(d[:, i]) for i in range(len(pts) - 1)}
+    phases["entry offset"] = pct(start)
+    phases["wave total"] = pct(d.sum(dim=1))
+    return {"phase_stamps": {"config": cfg_name, "calls": calls, "waves_per_call": int(d.shape[0] // calls),
+                             "unit": "us (p10, p50, p90 over waves)", "phases": phases,
+                             "kernel_span_us_median": round(statistics.median(spans), 2)}}
 
 
 def time_fwd_bwd(cfg_name, steps, warmup):
@@ -521,6 +565,9 @@ def main():
 
     if args.copy_probe_mib:
         copy_probe(args.copy_probe_mib)
+        return
+    if args.phase_stamps:
+        print(json.dumps(phase_stamps(args.config, args.phase_stamps, args.warmup)), flush=True)
         return
     if args.only_dropin:
         print(json.dumps({"dropin_ssd_scan": time_dropin("C1", steps=args.steps, warmup=args.warmup),

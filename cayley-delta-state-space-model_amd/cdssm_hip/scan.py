@@ -237,6 +237,24 @@ class PreparedForward:
         return self.y, self.h_final
 
     PHASES = ("summary", "carry_fold", "carry_replay", "main")
+    STAMP_POINTS = ("entry", "staged", "local", "published", "waited", "folded", "corrected", "end")
+
+    def phase_stamps(self) -> Tensor:
+        """One inference forward (cdssm_fused_scan_fwd_stamped, instrumentation) recording,
+        per wave of the one-pass kernel, the 100 MHz real-time counter at the points
+        STAMP_POINTS of its segment.  Returns an int64 (waves, 8) CPU tensor in ticks
+        (rows of unwritten records dropped); raises if the shape takes the four-launch
+        forward."""
+        B, L, H, D, N, Q = self.shape
+        nseg = -(-(-(-L // Q)) // 4)
+        n_items = nseg * B * H  # an upper bound on segment items (head groups <= H)
+        buf = torch.zeros(n_items * 4 * 8, dtype=torch.int64, device=self.device)
+        st = self._lib.cdssm_fused_scan_fwd_stamped(*self._args, _lib.ptr(buf), buf.numel(),
+                                                    _lib.stream_of(self.device))
+        if st != 0:
+            _lib.check(st, "cdssm_fused_scan_fwd_stamped")
+        out = buf.view(-1, 8).cpu()
+        return out[out[:, 0] != 0]
 
     def profile(self, iters: int) -> dict:
         """Average milliseconds of each kernel launch over `iters` calls, from HIP

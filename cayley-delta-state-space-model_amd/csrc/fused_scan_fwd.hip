@@ -961,15 +961,30 @@ struct OnePassArgs {
   float2* cend;    // SAVE: c^ after the chunk's last step (B, NC, H, D)
   int L, H, Q, NC, NSEG, NCK, n_hg, n_chain, n_items;
   int R;           // SSD form: state rows per head (virtual heads sharing a k row); 1 otherwise
+  // instrumentation (cdssm_fused_scan_fwd_stamped), else null: per (item, wave) the
+  // 100 MHz real-time counter at kStampPoints points of the segment
+  unsigned long long* stamps;
 };
 
 // One segment (work item): item = seg * n_chain + chain.
+// Phase stamps of cdssm_fused_scan_fwd_stamped: segment entry, staging done,
+// local pass done, segment map published, look-back wait done, carry folded,
+// correction pass done, segment end.
+constexpr int kStampPoints = 8;
+
 // epoch: this call's, read once by the workgroup at entry; arrive: this is the
 // workgroup's first segment, after whose first flag it counts itself for the
 // next call's epoch (arrive_and_draw_next_epoch).
 template <typename T, int D, int LPH, bool SAVE, bool WIDE>
 __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int item, unsigned long long epoch,
                                                 bool arrive) {
+  // phase stamps, read and stored only when a.stamps is set (a uniform branch)
+  unsigned long long ts[kStampPoints] = {};
+  const bool stamping = a.stamps != nullptr;
+  auto stamp = [&](int i) {
+    if (stamping) ts[i] = __builtin_amdgcn_s_memrealtime();
+  };
+  stamp(0);
   const typename T::raw* __restrict__ q = a.q;
   const typename T::raw* __restrict__ k = a.k;
   const typename T::raw* __restrict__ v = a.v;
@@ -1064,6 +1079,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
 #pragma unroll
     for (int i = 0; i < PF; ++i) kb[i].pin();
   }
+  stamp(1);
   __syncthreads();
 
   const int64_t tile_h = (int64_t(bi) * NC + tc.chunk) * H + (hok ? h : H - 1);  // (b, chunk, h)
@@ -1148,6 +1164,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   }
   __syncthreads();
 
+  stamp(2);
   // 2. segment map over the live chunks; thread x composes elements
   // e = x * EPT + i of the head group's state (head e / D, element e % D)
   const int e0 = int(threadIdx.x) * EPT;
@@ -1185,6 +1202,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
     if (arrive) arrive_and_draw_next_epoch(ob.ctl, &g_fwd_calls, 1u);
   }
 
+  stamp(3);
   // state entering the segment, in a fixed order (so results do not depend on
   // timing): from the anchor a = kAnchor * floor((seg - 1) / kAnchor) -- h0
   // for a = 0, else the published state leaving segment a - 1 -- fold the
@@ -1222,6 +1240,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
     __syncthreads();
     ok = ctrl[0];
   }
+  stamp(4);
   float2 Sin[EPT];
 #pragma unroll
   for (int i = 0; i < EPT; ++i) Sin[i] = make_float2(0.0f, 0.0f);
@@ -1285,6 +1304,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   if (anchor_end && threadIdx.x == 0)
     __hip_atomic_store(flag, (epoch << 2) | 2ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
+  stamp(5);
   // 3. state entering this wave's chunk, then the correction with the readout
   if (live) {
     float cr[DPL], ci[DPL];
@@ -1425,6 +1445,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   }
   __syncthreads();
 
+  stamp(6);
   // coalesced write of y (B, L, H, 2) for the wave's tile
   if (!YM && live) {
     const int n = tc.nt * HPW;
@@ -1437,6 +1458,12 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
         store_pair<T>(y + e, yv.x, yv.y);
       }
     }
+  }
+  if (stamping && lane == 0) {
+    ts[7] = __builtin_amdgcn_s_memrealtime();
+    unsigned long long* o = a.stamps + (int64_t(item) * kOnePassW + wv) * kStampPoints;
+#pragma unroll
+    for (int i = 0; i < kStampPoints; ++i) o[i] = ts[i];
   }
 }
 
@@ -1525,6 +1552,14 @@ FwdRegions infer_regions(float2* base, const FwdLayout& w) {
   g.gsaved = g.zck = g.cend = g.ycorr = nullptr;
   return g;
 }
+
+// Phase-stamp buffer of the running cdssm_fused_scan_fwd_stamped call on this
+// host thread (instrumentation only): device memory of `len` 8-byte words.
+struct StampRequest {
+  unsigned long long* buf = nullptr;
+  int64_t len = 0;
+};
+thread_local StampRequest t_stamps;
 
 template <typename T, int D, int LPH, int LPHS>
 int launch_fused_fwd(const void* q, const void* k, const void* v, const void* beta, const void* sel_c,
@@ -1622,6 +1657,15 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
       a.n_chain = B * n_hg;
       a.n_items = int(items);
       a.R = R;
+      a.stamps = nullptr;
+      if (t_stamps.buf) {
+        if (t_stamps.len < items * kOnePassW * kStampPoints) {
+          cdssm_host::set_error("cdssm_fused_scan_fwd_stamped: %lld stamp words needed (%lld given)",
+                                (long long)(items * kOnePassW * kStampPoints), (long long)t_stamps.len);
+          return CDSSM_EINVAL;
+        }
+        a.stamps = t_stamps.buf;
+      }
       if (path) *path = cdssm_host::kPathOne;
       // a continuing call runs on the epoch the previous call's last workgroup left
       if (!cont) {
@@ -1655,6 +1699,10 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
     }
   }
 
+  if (t_stamps.buf) {
+    cdssm_host::set_error("cdssm_fused_scan_fwd_stamped: the shape runs the four-launch forward, which has no phase stamps");
+    return CDSSM_EINVAL;
+  }
   if (path) *path = cdssm_host::kPathFour;
   if (ev) (void)hipEventRecord(ev[0], stream);
   hipLaunchKernelGGL((fused_fwd_summary_kernel<T, D, LPHS>), dim3(unsigned(tiles_s)), dim3(kWave),
@@ -2014,6 +2062,28 @@ extern "C" int cdssm_fused_scan_fwd_train_continue(int dtype, const void* q, con
                                                    int64_t N, int64_t chunk, hipStream_t stream) {
   return fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace,
                          B, L, H, D, N, chunk, stream, nullptr, true, nullptr, false, false, false, true);
+}
+
+// Instrumentation (no reference counterpart): cdssm_fused_scan_fwd, recording
+// for every wave of the one-pass kernel the 100 MHz real-time counter at
+// kStampPoints points of its segment into `stamps` (device memory, stamps_len
+// 8-byte words, word ((segment item * 4 + wave) * 8 + point)); -1 if the
+// buffer is too small or the shape takes the four-launch forward.
+extern "C" int cdssm_fused_scan_fwd_stamped(int dtype, const void* q, const void* k, const void* v,
+                                            const void* beta, const void* sel_c, const void* dt, const void* r,
+                                            const float* alpha, const float* omega, float c, const float* h0,
+                                            void* y, float* h_final, float* workspace, int64_t B, int64_t L,
+                                            int64_t H, int64_t D, int64_t N, int64_t chunk,
+                                            unsigned long long* stamps, int64_t stamps_len, hipStream_t stream) {
+  if (!stamps || stamps_len <= 0) {
+    cdssm_host::set_error("cdssm_fused_scan_fwd_stamped: a stamp buffer is required");
+    return CDSSM_EINVAL;
+  }
+  t_stamps = StampRequest{stamps, stamps_len};
+  const int st = fused_fwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, h0, y, h_final, workspace,
+                                 B, L, H, D, N, chunk, stream, nullptr, false);
+  t_stamps = StampRequest{};
+  return st;
 }
 
 extern "C" int cdssm_fused_scan_fwd_profile(int dtype, const void* q, const void* k, const void* v,

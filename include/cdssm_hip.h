@@ -236,6 +236,28 @@ int cdssm_fused_scan_bwd_profile(int dtype, const void* q, const void* k, const 
                                  int64_t N, int64_t chunk, hipStream_t stream, int iters, float* phase_ms);
 
 /*
+ * Instrumentation (no counterpart in the reference): cdssm_fused_scan_fwd
+ * (with its epoch kernel), recording for every wave of the one-pass kernel the
+ * 100 MHz real-time counter (s_memrealtime) at 8 points of its segment: entry,
+ * staging done, local pass done, segment map published, look-back wait done,
+ * carry folded, correction pass done, segment end.  stamps: device memory of
+ * stamps_len 8-byte words; word ((item * 4 + wave) * 8 + point) for wave
+ * 0..3 of the workgroup of item = segment * B * n_hg + b * n_hg + head group
+ * (n_hg = ceil(H / 8) head groups for bf16 D = 64, the same layout for the
+ * other instances with their heads per wave); the caller clears the buffer to
+ * tell unwritten records.
+ * Returns -1 (nothing launched) if the buffer holds fewer than
+ * items * 32 words or the shape takes the four-launch forward.  Results are
+ * bit-identical to cdssm_fused_scan_fwd.
+ */
+int cdssm_fused_scan_fwd_stamped(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                                 const void* sel_c, const void* dt, const void* r, const float* alpha,
+                                 const float* omega, float c, const float* h0, void* y, float* h_final,
+                                 float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                 int64_t chunk, unsigned long long* stamps, int64_t stamps_len,
+                                 hipStream_t stream);
+
+/*
  * Launch-path selection (no counterpart in the reference; for tests and
  * benchmarks): 0 = automatic (default), 1 = always the multi-launch passes,
  * 2 = one launch required (calls it cannot serve return -1), 3 = the

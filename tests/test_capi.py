@@ -68,6 +68,20 @@ def test_fused_fwd_rejects_invalid_arguments_without_launching(bad, msg):
     assert msg in _lib.last_error()
 
 
+@pytest.mark.parametrize("stamps,n", [(None, 64), (16, 0), (16, -1)])
+def test_stamped_fwd_rejects_a_missing_stamp_buffer_without_launching(stamps, n):
+    """The instrumentation entry refuses a null or empty stamp buffer before its
+    other checks (a short buffer is refused by the launcher, which first queries
+    the device: covered by the gpu test)."""
+    lib = _lib.load()
+    args = dict(dtype=1, q=16, k=16, v=16, beta=16, sel_c=16, dt=16, r=16, alpha=16, omega=16, c=1.0,
+                h0=None, y=16, h_final=16, ws=16, B=1, L=64, H=2, D=64, N=2, chunk=64)
+    st = lib.cdssm_fused_scan_fwd_stamped(*args.values(), stamps, n, None)
+    msg = "stamp buffer"
+    assert st == -1
+    assert msg in _lib.last_error()
+
+
 def test_fused_bwd_rejects_rows_beyond_32_bit_offsets_without_launching():
     lib = _lib.load()
     ptrs = [16] * 9
