@@ -232,6 +232,20 @@ __device__ __forceinline__ V seg_shift_up(V x) {
   }
 }
 
+// x from lane (lane + OFF) of the same NB-lane segment (the mirror of
+// seg_shift_up); lanes whose offset in the segment is NB - OFF or more get an
+// unspecified value; callers mask them.
+template <int NB, int OFF, typename V>
+__device__ __forceinline__ V seg_shift_down(V x) {
+  static_assert(sizeof(V) == 4 && OFF >= 1 && OFF < NB, "32-bit values, shift inside the segment");
+  if constexpr (NB <= 16) {
+    const int u = __builtin_bit_cast(int, x);
+    return __builtin_bit_cast(V, __builtin_amdgcn_update_dpp(u, u, 0x100 + OFF, 0xF, 0xF, false));
+  } else {
+    return __shfl_down(x, OFF, NB);
+  }
+}
+
 // f(std::integral_constant<int, s>) for s = 1, 2, 4, ... < NB (the steps of a
 // segmented Hillis-Steele scan over NB lanes)
 template <int NB, typename F>

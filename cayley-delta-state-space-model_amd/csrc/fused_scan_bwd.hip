@@ -75,7 +75,9 @@ constexpr int kBwdPF = 8;     // row prefetch depth (main pass)
 constexpr int kBwdCorrPF = CDSSM_BWD_CORR_PF;  // row prefetch depth (correction-adjoint pass)
 
 // Per-token scalars of a backward tile in LDS, slot p = t*HPW + j:
-//   S0 = (a_re, a_im, w_re, w_im)       transition and write (w = beta vp v)
+//   S0 = (a_re, a_im, e_re, e_im)       transition and the coefficient of k_t in
+//                                       z_t = a_t z_{t-1} + e_t k_t: e = w - beta a p,
+//                                       w = beta vp v, p = z_{t-1}.k_t (recorded)
 //   S1 = (beta, f_re, f_im, 0)          f = sel_C dy
 //   S2 = (h_re, h_im, gp_re, gp_im)     h = conj(g_t) f, gp = g_{t-1}
 // SSD form (a_t read from A_bar, vp = 1, the adjoint input a whole row dY_t):
@@ -181,11 +183,13 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
       else
         s.S2[p] = make_float4(gr * g0[i] + gi * g1[i], gr * g1[i] - gi * g0[i], pr, pi);
       if constexpr (WITH_W) {
-        s.S0[p] = make_float4(ar[i], ai[i], v0[i], v1[i]);
         // past the last token: p = pc = 0 (inert), delta g = 0, Y.q = 0
         const bool real = hok && t0 + i < tc.nt;
         const float4 pp = real ? rp[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         const float4 qq = real ? rq[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        // e = w - beta a p, the coefficient of k_t in z_t = a z_{t-1} + e k_t
+        const float bpr = bb[i] * pp.x, bpi = bb[i] * pp.y;
+        s.S0[p] = make_float4(ar[i], ai[i], v0[i] - (ar[i] * bpr - ai[i] * bpi), v1[i] - (ar[i] * bpi + ai[i] * bpr));
         sP[p] = pp;
         // delta g_t = f conj(c^_{t+1}.q), f = sel dy
         sG[p] = make_float4(g0[i] * qq.x + g1[i] * qq.y, g1[i] * qq.x - g0[i] * qq.y, qq.z, qq.w);
@@ -849,14 +853,17 @@ __device__ __forceinline__ DynGrad cayley_gated_bwd(float dt, float r, float alp
 //   and per token p_t = z_{t-1}.k_t, pc_t = c^_t.k_t, c^_{t+1}.q_t, Y_t.q_t
 //   (staged in LDS with the correction's delta g_t);
 //   reverse pass, kBwdCK tokens at a time: z of the segment is recomputed
-//     from its checkpoint with the stored p_t (no reductions); c^_t is rebuilt
+//     from its checkpoint with the staged e_t (no reductions); c^_t is rebuilt
 //     backward, exactly, as c^_t = c^_{t+1} + beta_t pc_t k_t; the local adjoint
-//     mu and the correction adjoint lambda step back and dk is emitted;
-//   epilogue, lanes owning blocks of tokens: dynamics chain rule, dv, dbeta,
-//     dsel, ddt, dr, and the chunk's d alpha / d omega per head.
+//     mu and the correction adjoint lambda step back and dk, dq are emitted;
+//   epilogue, lanes owning blocks of tokens: the token's scalar gradients
+//     (d a_t with the backward recurrence psi of the rotation products, the
+//     erase part of d beta), the dynamics chain rule, dv, dbeta, dsel, ddt, dr,
+//     and the chunk's d alpha / d omega per head.
 // LDS (float4 per (token, head) slot): S0, S1, S2 (staged scalars), P = (p,
-// pc), then (da, dw) after the reverse pass, G = (delta g, Y.q), then
-// (dbeta_erase, 0, Y.q).
+// pc), G = (delta g, Y.q); the reverse step of token t leaves S0 = (a,
+// mu.z_{t-1}) and S1 = (mu.k, lambda.k) for the epilogue (SSD form: G =
+// (delta g, 0, 0), delta g formed in the step).
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
@@ -876,6 +883,13 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   constexpr int LPH = BwdCfg<D>::LPH, HPW = BwdCfg<D>::HPW, DPL = BwdCfg<D>::DPL, PF = kBwdPF, CK = kBwdCK;
   static_assert(CK == kZck && PF == kTokRound, "the training forward's z checkpoints: every CK tokens");
   extern __shared__ float4 smem4[];
+  // Reserve the whole 256-register budget: at most two waves share a SIMD.
+  // The kernel needs ~155 registers, which would let three waves onto some
+  // SIMDs while others hold one (one-wave workgroups are placed per SIMD as
+  // slots free up); those SIMDs then set the kernel's tail.  Measured on
+  // MI355X at C2 (D = 128, 1.5 rounds of waves): 287 us with three allowed,
+  // 248 us with two.
+  asm volatile("" ::: "v255");
   const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
   const int hh = lane / LPH, sub = lane % LPH;
@@ -943,8 +957,6 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
     dGr = group_sum<LPH>(dGr);
     dGi = group_sum<LPH>(dGi);
   }
-  float psr = 0.0f, psi = 0.0f;  // psi_{t+1}
-  float anr = 1.0f, ani = 0.0f;  // a_{t+1}
   // Segments run last to first; the next segment's k / q rows and z checkpoint
   // are loaded while the current one is processed (two buffers, alternating).
   struct SegBuf {
@@ -963,8 +975,9 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   };
   auto run_seg = [&](const SegBuf& R, int seg) {
     const int tb = seg * CK;
-    // z_{tb-1+i} for i = 0..CK, recomputed with the stored p_t
-    float zbr[CK + 1][DPL], zbi[CK + 1][DPL];
+    // z_{tb-1+i} for i = 0..CK, recomputed with the staged e_t (no reductions);
+    // the unpacked k rows are kept for the reverse steps
+    float zbr[CK + 1][DPL], zbi[CK + 1][DPL], kr[CK][DPL];
 #pragma unroll
     for (int jj = 0; jj < DPL; ++jj) {
       zbr[0][jj] = R.z0[jj].x;
@@ -972,20 +985,13 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
     }
 #pragma unroll
     for (int i = 0; i < CK; ++i) {
-      const int p = (tb + i) * HPW + hh;
-      const float4 s0 = s.S0[p];
-      const float bb = s.S1[p].x;
-      const float4 pv = sP[p];
-      // slots past the last token are inert: a = 1, w = 0, beta = 0 (p may be stale)
-      const float bpr = bb * pv.x, bpi = bb * pv.y;
-      const float er = s0.z - (s0.x * bpr - s0.y * bpi);
-      const float ei = s0.w - (s0.x * bpi + s0.y * bpr);
-      float kk[DPL];
-      R.k[i].unpack(kk);
+      // slots past the last token are inert: a = 1, e = 0
+      const float4 s0 = s.S0[(tb + i) * HPW + hh];
+      R.k[i].unpack(kr[i]);
 #pragma unroll
       for (int jj = 0; jj < DPL; ++jj) {
-        zbr[i + 1][jj] = fmaf(s0.x, zbr[i][jj], fmaf(-s0.y, zbi[i][jj], er * kk[jj]));
-        zbi[i + 1][jj] = fmaf(s0.x, zbi[i][jj], fmaf(s0.y, zbr[i][jj], ei * kk[jj]));
+        zbr[i + 1][jj] = fmaf(s0.x, zbr[i][jj], fmaf(-s0.y, zbi[i][jj], s0.z * kr[i][jj]));
+        zbi[i + 1][jj] = fmaf(s0.x, zbi[i][jj], fmaf(s0.y, zbr[i][jj], s0.w * kr[i][jj]));
       }
     }
 #pragma unroll
@@ -993,11 +999,11 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
       const int t = tb + i;
       if (t < tc.nt) {
         const int p = t * HPW + hh;
-        const float4 s0 = s.S0[p], s1 = s.S1[p], s2 = s.S2[p], pv = sP[p], gv = sG[p];
-        const float ar = s0.x, ai = s0.y, bb = s1.x;
-        const float pr = pv.x, pi = pv.y, pcr = pv.z, pci = pv.w;
-        float kk[DPL], qq[DPL], gq[DPL];
-        R.k[i].unpack(kk);
+        const float4 s0 = s.S0[p], s1 = s.S1[p], s2 = s.S2[p], pv = sP[p];
+        const float ar = s0.x, ai = s0.y, er = s0.z, ei = s0.w, bb = s1.x;
+        const float pcr = pv.z, pci = pv.w;
+        const float* kk = kr[i];
+        float qq[DPL], gq[DPL];
         R.q[i].unpack(qq);
         if constexpr (YM) R.g[i].unpack(gq);
         constexpr int NRED = YM ? 8 : 6;
@@ -1008,6 +1014,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
         // dq = Re(conj(f) Y_t), Y_t = z_t + g_{t-1} c^_t, f = (s1.y, -s1.z), g_{t-1} = (s2.z, s2.w):
         // the c^ part's weight conj(f) g_{t-1} is formed once per token
         const float wcr = s2.z * s1.y + s2.w * s1.z, wci = s2.z * s1.z - s2.w * s1.y;
+        const float bpcr = bb * pcr, bpci = bb * pci;
 #pragma unroll
         for (int jj = 0; jj < DPL; ++jj) {
           if constexpr (YM) {
@@ -1016,8 +1023,8 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
             red[7] = fmaf(gq[jj], cr[jj], fmaf(-qq[jj], ci[jj], red[7]));
           }
           // c^_t = c^_{t+1} + beta pc k
-          cr[jj] = fmaf(bb * pcr, kk[jj], cr[jj]);
-          ci[jj] = fmaf(bb * pci, kk[jj], ci[jj]);
+          cr[jj] = fmaf(bpcr, kk[jj], cr[jj]);
+          ci[jj] = fmaf(bpci, kk[jj], ci[jj]);
           if constexpr (YM) {
             // mu += dY_t; lambda += conj(g_t) dY_t
             mr[jj] += qq[jj];
@@ -1040,31 +1047,12 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
         }
 #pragma unroll
         for (int x = 0; x < NRED; ++x) red[x] = group_sum<LPH>(red[x]);
+        // dw = mu.k, mk = conj(a) dw, sl = lambda.k
         const float dwr = red[0], dwi = red[1], slr = red[4], sli = red[5];
         const float mkr = ar * dwr + ai * dwi, mki = ar * dwi - ai * dwr;
-        float dar = red[2] - bb * (pr * dwr + pi * dwi);
-        float dai = red[3] - bb * (pr * dwi - pi * dwr);
-        const float dbe = -(pr * mkr + pi * mki) - (pcr * slr + pci * sli);
-        float dgr = YM ? red[NRED - 2] : gv.x, dgi = YM ? red[NRED - 1] : gv.y;
-        if (t == tc.nt - 1) {
-          dgr += dGr;
-          dgi += dGi;
-        }
-        const float npr = dgr + anr * psr + ani * psi;
-        const float npi = dgi + anr * psi - ani * psr;
-        psr = npr;
-        psi = npi;
-        anr = ar;
-        ani = ai;
-        dar += s2.z * psr + s2.w * psi;
-        dai += s2.z * psi - s2.w * psr;
         // dk = mu.e - beta (z_{t-1}.mk + c^_t.(lambda.k) + lambda.pc), e = w - beta a p:
         // the mu.w and conj(a) mu . p terms combine into mu.e
-        const float bpr = bb * pr, bpi = bb * pi;
-        const float er = s0.z - (ar * bpr - ai * bpi);
-        const float ei = s0.w - (ar * bpi + ai * bpr);
         const float bmkr = bb * mkr, bmki = bb * mki, bslr = bb * slr, bsli = bb * sli;
-        const float bpcr = bb * pcr, bpci = bb * pci;
         float dkv[DPL];
 #pragma unroll
         for (int jj = 0; jj < DPL; ++jj) {
@@ -1089,9 +1077,13 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
             store_row<T, DPL>(dks, t * rowb, dkv);
           if constexpr (!YM) store_row<T, DPL>(dqs, t * rowb, dqv);
         }
+        // the token's scalar gradients are formed in the epilogue (one lane per
+        // token, not LPH): keep mu.z_{t-1}, dw and sl in the slots this step
+        // has read (a stays for the epilogue's psi recurrence)
         if (sub == 0) {
-          sP[p] = make_float4(dar, dai, dwr, dwi);
-          sG[p] = make_float4(dbe, 0.0f, gv.z, gv.w);
+          s.S0[p] = make_float4(ar, ai, red[2], red[3]);
+          s.S1[p] = make_float4(dwr, dwi, slr, sli);
+          if constexpr (YM) sG[p] = make_float4(red[6], red[7], 0.0f, 0.0f);  // delta g_t
         }
       }
     }
@@ -1113,33 +1105,112 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   }
   __syncthreads();
 
-  // ---- per-token dynamics backward: lane = (head j, block of TPB tokens) ----
+  // ---- per-token scalar gradients and dynamics backward: lane = (head j, block of TPB tokens) ----
+  // Slots now hold S0 = (a, mu.z_{t-1}), S1 = (dw, sl), S2 = (h, g_{t-1}), P = (p, pc),
+  // G = (delta g, Y.q).  psi_t, the adjoint of the rotation product g_t, runs
+  // backward: psi_t = delta g_t + conj(a_{t+1}) psi_{t+1} (+ dG at the chunk's last
+  // token), psi_nt = 0; each lane composes its block, a segmented suffix scan over
+  // the head's NB blocks joins them, and slabs of kWave tokens run last to first.
   {
     constexpr int NB = kWave / HPW, TPB = HPW;
+    static_assert(NB == LPH, "the epilogue's head of a lane is its reverse-pass head");
     const int j = lane / NB, blk = lane % NB;
     const int hj = tc.hbase + j;
     const bool jok = hj < H;
     const int hjl = jok ? hj : H - 1;
     const float alj = YM ? 0.0f : alpha[hjl], omj = YM ? 0.0f : omega[hjl];
+    const int tend = round_up(ntr, kWave);  // staged slots: [0, tend)
     float dal = 0.0f, dom = 0.0f;
-    for (int tl = 0; tl < ntr; tl += kWave) {
+    float pinr = 0.0f, pini = 0.0f;  // psi at the first token right of the slab
+    for (int tl = tend - kWave; tl >= 0; tl -= kWave) {
+      const int t0 = tl + blk * TPB;
+      // the block with zero input: psi_t = X_t + A_t psi_{t0+TPB}
+      float xr[TPB], xi[TPB], Ar[TPB], Ai[TPB];
+      {
+        float2 an = t0 + TPB < tend ? make_float2(s.S0[(t0 + TPB) * HPW + j].x, s.S0[(t0 + TPB) * HPW + j].y)
+                                    : make_float2(1.0f, 0.0f);
+        float cxr = 0.0f, cxi = 0.0f, car = 1.0f, cai = 0.0f;
+#pragma unroll
+        for (int i = TPB - 1; i >= 0; --i) {
+          const int t = t0 + i;
+          const int p = t * HPW + j;
+          const float4 gv = sG[p];
+          float dgr = gv.x, dgi = gv.y;
+          if (t == tc.nt - 1) {
+            dgr += dGr;
+            dgi += dGi;
+          }
+          // (X, A) <- (dg + conj(an) X, conj(an) A)
+          const float nxr = dgr + an.x * cxr + an.y * cxi, nxi = dgi + an.x * cxi - an.y * cxr;
+          const float nar = an.x * car + an.y * cai, nai = an.x * cai - an.y * car;
+          cxr = nxr;
+          cxi = nxi;
+          car = nar;
+          cai = nai;
+          xr[i] = cxr;
+          xi[i] = cxi;
+          Ar[i] = car;
+          Ai[i] = cai;
+          const float4 s0 = s.S0[p];
+          an = make_float2(s0.x, s0.y);
+        }
+      }
+      // suffix scan over the head's blocks: (SX, SA) maps psi right of block
+      // blk + span - 1 to psi at the block's first token
+      float sxr = xr[0], sxi = xi[0], sar = Ar[0], sai = Ai[0];
+      for_shifts<NB>([&](auto offc) {
+        constexpr int off = decltype(offc)::value;
+        const float yxr = seg_shift_down<NB, off>(sxr), yxi = seg_shift_down<NB, off>(sxi);
+        const float yar = seg_shift_down<NB, off>(sar), yai = seg_shift_down<NB, off>(sai);
+        if (blk + off < NB) {
+          // (SX, SA) o (YX, YA): SX + SA YX, SA YA
+          const float nxr = sxr + (sar * yxr - sai * yxi), nxi = sxi + (sar * yxi + sai * yxr);
+          const float nar = sar * yar - sai * yai, nai = sar * yai + sai * yar;
+          sxr = nxr;
+          sxi = nxi;
+          sar = nar;
+          sai = nai;
+        }
+      });
+      // psi right of this block: the next block's inclusive map applied to the slab's input
+      float rxr = seg_shift_down<NB, 1>(sxr), rxi = seg_shift_down<NB, 1>(sxi);
+      float rar = seg_shift_down<NB, 1>(sar), rai = seg_shift_down<NB, 1>(sai);
+      if (blk == NB - 1) {
+        rxr = rxi = 0.0f;
+        rar = 1.0f;
+        rai = 0.0f;
+      }
+      const float per = rxr + (rar * pinr - rai * pini), pei = rxi + (rar * pini + rai * pinr);
+      // psi at the slab's first token, for the slab to the left (block 0 of the head)
+      const float hxr = sxr + (sar * pinr - sai * pini), hxi = sxi + (sar * pini + sai * pinr);
+      pinr = __shfl(hxr, j * NB, kWave);
+      pini = __shfl(hxi, j * NB, kWave);
 #pragma unroll
       for (int i = 0; i < TPB; ++i) {
-        const int t = tl + blk * TPB + i;
+        const int t = t0 + i;
         if (t < tc.nt && jok) {
           const int64_t e = (tc.row0 + t) * H + hj;
           const int p = t * HPW + j;
-          const float4 rv = sP[p], gv = sG[p];
+          const float4 s0 = s.S0[p], s1 = s.S1[p], s2 = s.S2[p], pv = sP[p], gv = sG[p];
+          const float psr = xr[i] + (Ar[i] * per - Ai[i] * pei), psi = xi[i] + (Ar[i] * pei + Ai[i] * per);
+          const float ar = s0.x, ai = s0.y, dwr = s1.x, dwi = s1.y, slr = s1.z, sli = s1.w;
+          const float pr = pv.x, pi = pv.y, pcr = pv.z, pci = pv.w;
           // SSD form: beta per real head (the R virtual heads of its state rows share it)
           const float bb = T::load(beta + (YM ? (tc.row0 + t) * (H / R) + hj / R : e));
+          // d a_t = mu.z_{t-1} - beta (mu.k) conj(p) + psi_t conj(g_{t-1})
+          const float dar = s0.z - bb * (pr * dwr + pi * dwi) + (s2.z * psr + s2.w * psi);
+          const float dai = s0.w - bb * (pr * dwi - pi * dwr) + (s2.z * psi - s2.w * psr);
+          // d beta (erase part) = -(p . conj(a) dw) - (pc . sl)
+          const float mkr = ar * dwr + ai * dwi, mki = ar * dwi - ai * dwr;
+          const float dbe = -(pr * mkr + pi * mki) - (pcr * slr + pci * sli);
           const float v0 = T::load(v + 2 * e), v1 = T::load(v + 2 * e + 1);
           if constexpr (YM) {
             // SSD form: d A_bar_t = d a_t (into ddt's place, (re, im) pairs), dV = beta dw,
             // dbeta = erase part + dw . V (w = beta V)
-            store_pair<T>(ddt + 2 * e, rv.x, rv.y);
-            T::store(dv + 2 * e, bb * rv.z);
-            T::store(dv + 2 * e + 1, bb * rv.w);
-            const float db = gv.x + (rv.z * v0 + rv.w * v1);
+            store_pair<T>(ddt + 2 * e, dar, dai);
+            T::store(dv + 2 * e, bb * dwr);
+            T::store(dv + 2 * e + 1, bb * dwi);
+            const float db = dbe + (dwr * v0 + dwi * v1);
             if (R > 1)
               dbp[e] = db;  // summed over the head's rows by the row-sum kernel
             else
@@ -1149,11 +1220,11 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
           const float dtv = T::load(dt + e), rrv = T::load(r + e);
           const float g0 = T::load(dy + 2 * e), g1 = T::load(dy + 2 * e + 1);
           const Transition tr = cayley_gated(dtv, rrv, alj, omj, c);
-          const float dwv = rv.z * v0 + rv.w * v1;
-          const DynGrad g = cayley_gated_bwd(dtv, rrv, alj, omj, c, rv.x, rv.y, bb * dwv);
-          T::store(dv + 2 * e, bb * tr.vp * rv.z);
-          T::store(dv + 2 * e + 1, bb * tr.vp * rv.w);
-          T::store(dbeta + e, gv.x + tr.vp * dwv);
+          const float dwv = dwr * v0 + dwi * v1;
+          const DynGrad g = cayley_gated_bwd(dtv, rrv, alj, omj, c, dar, dai, bb * dwv);
+          T::store(dv + 2 * e, bb * tr.vp * dwr);
+          T::store(dv + 2 * e + 1, bb * tr.vp * dwi);
+          T::store(dbeta + e, dbe + tr.vp * dwv);
           T::store(dsel + e, g0 * gv.z + g1 * gv.w);
           T::store(ddt + e, g.ddt);
           T::store(dr + e, g.dr);
