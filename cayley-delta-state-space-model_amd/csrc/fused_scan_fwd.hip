@@ -1607,10 +1607,12 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
     // segments than that: the persistent one-pass only for inference with
     // full rounds (measured on MI355X: faster than four launches at C3,
     // slower at C2's 1.5 rounds and for the training forward's records)
-    // the inference forward's wide staging loads: bf16 scan-level form, 8 heads per wave
+    // wide staging loads (bf16 scan-level form, 8 heads per wave); the persistent
+    // training forward (taken only when the one-pass path is forced) keeps the narrow ones
     constexpr bool kWideOk = std::is_same<T, BF16>::value && kWave / LPH == 8;
-    const bool wide = kWideOk && !save && H % 8 == 0 && Q <= kWave && cdssm_host::wide_staging();
-    const int cap1 = save   ? onepass_capacity<T, D, LPH, kSv, false>(lds)
+    const bool wide = kWideOk && H % 8 == 0 && Q <= kWave && cdssm_host::wide_staging();
+    const int cap1 = save   ? (wide ? onepass_capacity<T, D, LPH, kSv, false, kWideOk>(lds)
+                                    : onepass_capacity<T, D, LPH, kSv, false>(lds))
                      : wide ? onepass_capacity<T, D, LPH, false, false, kWideOk>(lds)
                             : onepass_capacity<T, D, LPH, false, false>(lds);
     const int capp = save   ? onepass_capacity<T, D, LPH, kSv, true>(lds)
@@ -1676,7 +1678,9 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
       if (ev)
         for (int i = 0; i < 4; ++i) (void)hipEventRecord(ev[i], stream);
       const dim3 gd = dim3(unsigned(grid)), bd = dim3(kWave * kOnePassW);
-      if (save && single)
+      if (save && single && wide)
+        hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, kSv, false, kWideOk>), gd, bd, lds, stream, a);
+      else if (save && single)
         hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, kSv, false>), gd, bd, lds, stream, a);
       else if (save)
         hipLaunchKernelGGL((fused_fwd_onepass_kernel<T, D, LPH, kSv, true>), gd, bd, lds, stream, a);
