@@ -191,18 +191,18 @@ def time_fwd_bwd(cfg_name, steps, warmup):
             "hbm_frac_with_records": (alg + 2 * stored) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "bytes_note": ("alg_bytes: the inputs read and outputs written by forward and backward (272 B / 812 B "
                            "per token-head at D 64 bf16); stored_record_bytes: what the training forward writes "
-                           "for the backward (per-token records, z every 4 tokens, chunk entering states, c^ at "
+                           "for the backward (per-token records, z every 8 tokens, chunk entering states, c^ at "
                            "chunk ends), counted twice (written, read back) in hbm_frac_with_records"),
             "phase_ms": phases}
 
 
 def training_record_bytes(cfg):
     """Bytes the training forward stores for the backward (and the backward reads back): per token-head
-    two float4 records and the float2 g_t (40 B); per chunk-head the state every 4 tokens (bf16 complex
+    two float4 records and the float2 g_t (40 B); per chunk-head the state every 8 tokens (bf16 complex
     pairs for bf16 inputs: 4 B per element), the entering state and c^ at the chunk end (fp32 complex),
     and G_k."""
     NC = -(-cfg.L // cfg.D)
-    NCK = -(-cfg.D // 8) * 8 // 4
+    NCK = -(-cfg.D // 8) * 8 // 8
     pair = 4 if cfg.dtype == "bf16" else 8
     per_chunk_head = NCK * cfg.D * pair + 2 * cfg.D * 8 + 8
     return cfg.B * cfg.H * (cfg.L * 40 + NC * per_chunk_head)

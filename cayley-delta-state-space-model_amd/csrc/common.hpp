@@ -444,7 +444,7 @@ __device__ __forceinline__ void load_zck(const float2* base, int64_t idx, float2
 constexpr int kSegLen = 16;   // chunks per forward carry segment
 constexpr int kOnePassW = 4;  // chunks (waves) per workgroup of the one-pass forward
 constexpr int kCtlWords = 8;  // 8-byte words of a look-back area's control block
-constexpr int kZck = 4;       // token interval of the z checkpoints
+constexpr int kZck = 8;       // token interval of the z checkpoints
 constexpr int kTokRound = 8;  // token loops run to round_up(tokens, kTokRound)
 
 struct FwdLayout {

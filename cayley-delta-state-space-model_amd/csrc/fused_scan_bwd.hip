@@ -67,7 +67,7 @@ struct BwdCorrCfg {
   static constexpr int HPW = kWave / LPH;
   static constexpr int DPL = D / LPH;
 };
-constexpr int kBwdCK = 4;     // z checkpoint interval (the training forward writes them)
+constexpr int kBwdCK = 8;     // z checkpoint interval (the training forward writes them)
 constexpr int kBwdPF = 8;     // row prefetch depth (main pass)
 #ifndef CDSSM_BWD_CORR_PF
 #define CDSSM_BWD_CORR_PF 8

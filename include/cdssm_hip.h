@@ -98,7 +98,7 @@ int cdssm_fused_scan_fwd_abar(int dtype, const void* q, const void* k, const voi
  * passes' full outputs for backward instead): the forward above, which also
  * stores in the workspace what the backward reads: per (token, head) the dot
  * products of the chunk recurrences (p_t = z_{t-1}.k_t, c^_t.k_t,
- * c^_{t+1}.q_t, Y_t.q_t; 32 bytes) and g_t, the local state every 4 tokens and
+ * c^_{t+1}.q_t, Y_t.q_t; 32 bytes) and g_t, the local state every 8 tokens and
  * the correction state after every chunk, so that the backward rebuilds the
  * chunk states without reductions or a forward recompute.  Same arguments and
  * workspace size as cdssm_fused_scan_fwd.

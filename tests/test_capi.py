@@ -169,7 +169,7 @@ def test_one_launch_areas_have_a_control_block_for_the_device_epoch():
     NC = -(-L // Q)
     S = -(-NC // 16)
     NSEG = -(-NC // 4)
-    NCK = -(-Q // 8) * 8 // 4
+    NCK = -(-Q // 8) * 8 // 8
     carry = B * NC * H * D + B * NC * H + B * H * S * (D + 1)
     fwd = (carry + (carry & 1) + 5 * B * L * H + B * NSEG * H * (2 * D + 2) + 8 + B * NC * H * NCK * D
            + B * NC * H * D + B * L * H)
@@ -220,7 +220,7 @@ def test_workspace_size_formula():
         gsaved = B * L * H            # g_t per token-head: float2
         NSEG = -(-NC // 4)            # one-pass look-back segments of 4 chunks
         onepass = B * NSEG * H * (2 * D + 2) + 8   # maps, leaving states, rotations, flags, control block
-        NCK = -(-Q // 8) * 8 // 4     # z checkpoints per chunk (every 4 tokens of the 8-rounded loop)
+        NCK = -(-Q // 8) * 8 // 8     # z checkpoints per chunk (every 8 tokens of the 8-rounded loop)
         zck = B * NC * H * NCK * D
         cend = B * NC * H * D         # correction state after each chunk
         ycorr = B * L * H             # the chunked MFMA correction's readout

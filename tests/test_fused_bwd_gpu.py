@@ -180,7 +180,7 @@ def test_one_pass_training_forward_writes_the_four_launch_records():
     n_states, n_gam = B * NC * H * D, B * NC * H
     carry = n_states + n_gam + B * H * S * (D + 1)
     off_saved = carry + (carry & 1)
-    NSEG, NCK = -(-NC // 4), -(-Q // 8) * 8 // 4
+    NSEG, NCK = -(-NC // 4), -(-Q // 8) * 8 // 8
     off_zck = off_saved + 5 * B * L * H + B * NSEG * H * (2 * D + 2) + 8  # look-back area + control block
     n_zck = B * NC * H * NCK * D
     regions = {"states": (0, n_states), "gam": (n_states, n_states + n_gam),
@@ -193,7 +193,7 @@ def test_one_pass_training_forward_writes_the_four_launch_records():
     # checkpoint slots past a ragged last chunk's token loop are not written
     nt_last = L - (NC - 1) * Q
     ck_used = torch.ones(B, NC, H, NCK, D, 2, dtype=torch.bool)
-    ck_used[:, NC - 1, :, -(-nt_last // 8) * 8 // 4:] = False
+    ck_used[:, NC - 1, :, -(-nt_last // 8) * 8 // 8:] = False
     for name, (lo, hi) in regions.items():
         a1, a4 = w1[lo:hi], w4[lo:hi]
         if name == "z checkpoints":
