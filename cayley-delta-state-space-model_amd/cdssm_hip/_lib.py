@@ -43,6 +43,7 @@ SIGNATURES = {
                                     _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "cdssm_fused_scan_fwd_train": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _P,
                                           _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "cdssm_skinny_gemm": (_I32, [_I32, _P, _I64, _P, _I64, _P, _P, _I64, _P, _F32, _P, _I64, _I64, _I64, _I64, _P]),
     "cdssm_fused_scan_fwd_stamped": (_I32, [_I32] + [_P] * 9 + [_F32] + [_P] * 4 + [_I64] * 6 + [_P, _I64, _P]),
     "cdssm_fused_scan_fwd_continue": (_I32, [_I32] + [_P] * 9 + [_F32] + [_P] * 4 + [_I64] * 6 + [_P]),
     "cdssm_fused_scan_fwd_train_continue": (_I32, [_I32] + [_P] * 9 + [_F32] + [_P] * 4 + [_I64] * 6 + [_P]),

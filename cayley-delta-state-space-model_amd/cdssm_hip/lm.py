@@ -242,6 +242,39 @@ def rms_norm(x: Tensor, weight: Tensor, eps: float) -> Tensor:
     return y
 
 
+def _skinny_ok(x: Tensor, weight: Tensor) -> bool:
+    """Whether cdssm_skinny_gemm serves x (M, K) @ weight (N, K)^T: bf16, M <= 64, K % 128 == 0,
+    16-byte aligned rows."""
+    return (x.dim() == 2 and x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and x.is_cuda
+            and 1 <= x.shape[0] <= 64 and x.shape[1] % 128 == 0 and weight.shape[1] == x.shape[1]
+            and x.stride(1) == 1 and weight.stride(1) == 1 and x.stride(0) % 8 == 0 and weight.stride(0) % 8 == 0
+            and x.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0)
+
+
+def skinny_linear(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None, residual: Optional[Tensor] = None,
+                  norm_weight: Optional[Tensor] = None, eps: float = 0.0) -> Tensor:
+    """Decode-size linear layer on the skinny GEMM kernel (cdssm_skinny_gemm): x (M, K) bf16, M <= 64,
+    -> (M, N) = x' @ weight^T (+ bias) (+ residual), where x' = rms_norm(x, norm_weight, eps) when a
+    norm weight is given (the RMSNorm folded into the product: x * norm_weight rounded to bf16 enters
+    the matrix cores, the row scale rsqrt(mean(x^2) + eps) is applied to the fp32 result).  Shapes the
+    kernel does not serve raise (callers check ``_skinny_ok``)."""
+    if not _skinny_ok(x, weight):
+        raise ValueError("skinny_linear: needs bf16 x (M <= 64, K % 128 == 0) and weight with aligned rows")
+    M, K = x.shape
+    N = weight.shape[0]
+    b = None if bias is None else bias.to(torch.bfloat16).contiguous()
+    r = None if residual is None else residual.to(torch.bfloat16)
+    if r is not None and (r.shape != (M, N) or r.stride(1) != 1):
+        raise ValueError("skinny_linear: residual must be (M, N) with unit column stride")
+    g = None if norm_weight is None else norm_weight.to(torch.bfloat16).contiguous()
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
+    st = _lib.load().cdssm_skinny_gemm(1, _lib.ptr(x), x.stride(0), _lib.ptr(weight), weight.stride(0), _lib.ptr(b),
+                                       _lib.ptr(r), r.stride(0) if r is not None else 0, _lib.ptr(g), float(eps),
+                                       _lib.ptr(y), N, M, N, K, _lib.stream_of(x.device))
+    _lib.check(st, "cdssm_skinny_gemm")
+    return y
+
+
 def normalize_kq_qk(K: Tensor, Q: Tensor) -> tuple:
     """K^, Q^ = x * rsqrt(sum_d x^2 + 1e-6) per (token, head) and qk = K^.Q^ (fp32), in one pass.
 
@@ -662,13 +695,20 @@ class CDSSMBlock(nn.Module):
         cfg = self.config
         N, H, D, Di = cfg.state_dim, cfg.n_heads, cfg.head_dim, cfg.d_inner
         B = x.shape[0]
-        proj = self.in_proj(rms_norm(x, self.norm.weight, self.norm.eps))  # (B, 3 Di + H N)
+        if _skinny_ok(x, self.in_proj.weight):  # RMSNorm + in_proj in one skinny product
+            proj = skinny_linear(x, self.in_proj.weight, self.in_proj.bias, norm_weight=self.norm.weight,
+                                 eps=self.norm.eps)
+        else:
+            proj = self.in_proj(rms_norm(x, self.norm.weight, self.norm.eps))  # (B, 3 Di + H N)
         z, x_gate, K, V = proj.split([Di, Di, Di, H * N], dim=-1)
         K = K.reshape(B, 1, H, D)
         V = V.reshape(B, H, N)
         x_conv = conv1d_silu_step(x_gate, cache["conv"], self.conv.weight, self.conv.bias)
         GH = (N + 5) * H
-        gq = torch.addmm(cache["b_gq"], x_conv, cache["w_gq"].t())  # (B, GH + Di): gates | Q
+        if _skinny_ok(x_conv, cache["w_gq"]):
+            gq = skinny_linear(x_conv, cache["w_gq"], cache["b_gq"])  # (B, GH + Di): gates | Q
+        else:
+            gq = torch.addmm(cache["b_gq"], x_conv, cache["w_gq"].t())
         es = x.element_size()
         if (self.fused_step and D in (64, 128) and (gq.data_ptr() + GH * es) % 16 == 0 and (gq.stride(0) * es) % 16 == 0
                 and (proj.data_ptr() + 2 * Di * es) % 16 == 0 and (proj.stride(0) * es) % 16 == 0
@@ -710,6 +750,8 @@ class CDSSMBlock(nn.Module):
         y = group_norm_gate_step(retrieved.reshape(B, -1), cache["gsum"], self.ssm_norm.weight, self.ssm_norm.bias,
                                  self.ssm_norm.eps, z, x_conv, self.D, position=cache["l"],
                                  readout_weight=self.readout_proj.weight)
+        if _skinny_ok(y, self.out_proj.weight) and x.dtype == torch.bfloat16:
+            return skinny_linear(y, self.out_proj.weight, residual=x)
         return torch.addmm(x, y, self.out_proj.weight.t())
 
 
@@ -755,6 +797,8 @@ class CDSSMLMHeadModel(nn.Module):
         v_first = None
         for blk, c in zip(self.blocks, caches):
             x, v_first = blk.step(x, v_first, c)
+        if _skinny_ok(x, self.lm_head.weight):  # final RMSNorm + tied head in one skinny product
+            return skinny_linear(x, self.lm_head.weight, norm_weight=self.final_norm.weight, eps=self.final_norm.eps)
         return self.lm_head(self.final_norm(x))
 
     def decode_graph(self, caches: List[dict], warmup: int = 2) -> "DecodeGraph":

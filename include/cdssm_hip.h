@@ -559,6 +559,24 @@ int cdssm_readout_group_norm_gate_step(int dtype, int param_dtype, const void* r
                                        hipStream_t stream);
 
 /*
+ * Decode-size linear layer: Y (M x N, row stride ldy) = X (M x K, row stride
+ * ldx) W^T (W: N x K, row stride ldw) + bias (N, or NULL) + R (M x N, row
+ * stride ldr, or NULL).  With wnorm (K, or NULL) the rows of X are
+ * RMS-normalised first as the model's RMSNorm does (modules.py:49-53; eps):
+ * X * wnorm enters the product rounded to bf16 and the row scale
+ * rsqrt(mean(X^2) + eps) is applied to the fp32 result.  bf16 only (dtype 1),
+ * M in 1..64, K a multiple of 128, X / W / wnorm rows 16-byte aligned.
+ * Replaces, in the decode step, torch's GEMMs behind nn.Linear for in_proj
+ * (with the block's RMSNorm; block.py:155-156), the stacked gate/Q projection
+ * (gate_proj, Q_proj), out_proj (with the residual) and the tied LM head (with
+ * the final RMSNorm; model.py:50-51).  No reference counterpart as a function:
+ * the reference decodes by re-forwarding (predict.py:53-67).
+ */
+int cdssm_skinny_gemm(int dtype, const void* X, int64_t ldx, const void* W, int64_t ldw, const void* bias,
+                      const void* R, int64_t ldr, const void* wnorm, float eps, void* Y, int64_t ldy, int64_t M,
+                      int64_t N, int64_t K, hipStream_t stream);
+
+/*
  * One decode token of the model block's scan path in one launch, per (b, h):
  * the gate-level dynamics at the device-held position (as
  * cdssm_dynamics_fused_fwd_at), K/Q normalisation and q.k (as

@@ -82,6 +82,23 @@ def test_stamped_fwd_rejects_a_missing_stamp_buffer_without_launching(stamps, n)
     assert msg in _lib.last_error()
 
 
+@pytest.mark.parametrize("over,msg", [
+    (dict(dtype=0), "bf16 only"),
+    (dict(X=None), "must not be null"),
+    (dict(M=65), "M <= 64"),
+    (dict(K=200, ldx=200, ldw=200), "multiple of 128"),
+    (dict(ldx=1000), "16-byte aligned"),
+    (dict(W=24), "16-byte aligned"),
+])
+def test_skinny_gemm_rejects_invalid_arguments_without_launching(over, msg):
+    lib = _lib.load()
+    args = dict(dtype=1, X=16, ldx=1024, W=16, ldw=1024, bias=None, R=None, ldr=0, wnorm=None, eps=0.0, Y=16,
+                ldy=1024, M=64, N=1024, K=1024, stream=None)
+    args.update(over)
+    assert lib.cdssm_skinny_gemm(*args.values()) == -1
+    assert msg in _lib.last_error()
+
+
 def test_fused_bwd_rejects_rows_beyond_32_bit_offsets_without_launching():
     lib = _lib.load()
     ptrs = [16] * 9
