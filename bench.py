@@ -462,9 +462,10 @@ def time_lm_decode(steps=20, warmup=3, B=64, prompt=2048):
     return {"workload": f"config 4: LM decode step B{B} from a {prompt}-token prefill, 24 layers, bf16",
             "ms_per_step": ms, "tokens_per_s": B / (ms * 1e-3), "eager_ms_per_step": ms_eager,
             "prefill_ms": p0.elapsed_time(p1), "weight_bytes": wbytes, "weight_read_GBs": wbytes / (ms * 1e-3) / 1e9,
-            "note": "one HIP graph per step (DecodeGraph); per layer 7 launches: RMSNorm, in_proj, conv step, "
-                    "stacked gate/Q GEMM, one token kernel (dynamics, K/Q norm, value residual, scan step, "
-                    "shortcut), readout_proj + GroupNorm step (one kernel), out_proj with the residual"}
+            "note": "one HIP graph per step (DecodeGraph); per layer 6 launches: RMSNorm + in_proj (skinny GEMM), "
+                    "conv step, stacked gate/Q projection (skinny GEMM), one token kernel (dynamics, K/Q norm, value "
+                    "residual, scan step, shortcut), readout_proj + GroupNorm step (one kernel), out_proj with the "
+                    "residual (skinny GEMM); the final RMSNorm + tied head as one skinny GEMM"}
 
 
 def time_lm_forward(steps=5, warmup=2):
