@@ -465,7 +465,7 @@ def time_lm_decode(steps=20, warmup=3, B=64, prompt=2048):
             "note": "one HIP graph per step (DecodeGraph); per layer 6 launches: RMSNorm + in_proj (skinny GEMM), "
                     "conv step, stacked gate/Q projection (skinny GEMM), one token kernel (dynamics, K/Q norm, value "
                     "residual, scan step, shortcut), readout_proj + GroupNorm step (one kernel), out_proj with the "
-                    "residual (skinny GEMM); the final RMSNorm + tied head as one skinny GEMM"}
+                    "residual (skinny GEMM); then the final RMSNorm and the tied head (library GEMM)"}
 
 
 def time_lm_forward(steps=5, warmup=2):

@@ -797,8 +797,8 @@ class CDSSMLMHeadModel(nn.Module):
         v_first = None
         for blk, c in zip(self.blocks, caches):
             x, v_first = blk.step(x, v_first, c)
-        if _skinny_ok(x, self.lm_head.weight):  # final RMSNorm + tied head in one skinny product
-            return skinny_linear(x, self.lm_head.weight, norm_weight=self.final_norm.weight, eps=self.final_norm.eps)
+        # the tied head (N = vocab) stays on the library GEMM: the skinny kernel re-reads the 64-row
+        # activation for every 16 of the 32000 columns (46 us against 18 us, measured on MI355X)
         return self.lm_head(self.final_norm(x))
 
     def decode_graph(self, caches: List[dict], warmup: int = 2) -> "DecodeGraph":

@@ -568,9 +568,9 @@ int cdssm_readout_group_norm_gate_step(int dtype, int param_dtype, const void* r
  * M in 1..64, K a multiple of 128, X / W / wnorm rows 16-byte aligned.
  * Replaces, in the decode step, torch's GEMMs behind nn.Linear for in_proj
  * (with the block's RMSNorm; block.py:155-156), the stacked gate/Q projection
- * (gate_proj, Q_proj), out_proj (with the residual) and the tied LM head (with
- * the final RMSNorm; model.py:50-51).  No reference counterpart as a function:
- * the reference decodes by re-forwarding (predict.py:53-67).
+ * (gate_proj, Q_proj) and out_proj (with the residual).  No reference
+ * counterpart as a function: the reference decodes by re-forwarding
+ * (predict.py:53-67).
  */
 int cdssm_skinny_gemm(int dtype, const void* X, int64_t ldx, const void* W, int64_t ldw, const void* bias,
                       const void* R, int64_t ldr, const void* wnorm, float eps, void* Y, int64_t ldy, int64_t M,
