@@ -424,7 +424,7 @@ class SSDScanFn(torch.autograd.Function):
     The same result and gradients as SSDChunkwiseScan over IntraChunkScanFn, InterChunkScanFn and
     ExactCorrectionFn (ssd.py:39-111, ops.py:100-195), from one forward and one backward call.
     Saves the inputs and the training forward's workspace (per-token records, the local state every
-    4 tokens, the state entering and the correction leaving every chunk), no per-token states.
+    8 tokens, the state entering and the correction leaving every chunk), no per-token states.
     """
 
     @staticmethod
