@@ -86,13 +86,41 @@ struct BwdScalars {
   float4 *S0, *S1, *S2;
 };
 
+// Rescaled frames of the main pass (readout form).  In a segment of CK tokens
+// from tb, with the segment's own rotation products G_i = prod_{u=tb}^{tb+i-1}
+// a_u (G_0 = 1), token t = tb + i:
+//   z~_i  = z_{t-1} / G_i:         z~_{i+1} = z~_i + (e_t / G_{i+1}) k_t
+//   mu^_t = conj(G_{i+1}) mu_t:    mu^ += (conj(G_{i+1}) f_t) q_t, then
+//                                  mu^ -= beta (mu^.k) k_t
+// (mu_t the adjoint of z_t), so neither recurrence multiplies by a_t per state
+// element.  The products the step needs keep their form with per-token
+// coefficients: Re(mu conj(e)) = Re(mu^ conj(e / G_{i+1})), the z_{t-1} term of
+// dk is Re(z~_i conj(beta mu^.k)), Re(z_t conj(f)) = Re(z~_{i+1} conj(conj(G_{i+1})
+// f)); what leaves the step is mu^.k = conj(G_{i+1}) (mu.k) and
+// mu^ conj(z~_i) = conj(a_t) mu conj(z_{t-1}), converted back per token after
+// the pass.  mu^ enters a segment as conj(G_CK) mu and leaves it as mu_{tb-1}
+// (G_0 = 1).  The frames stay within 2^-60 .. 2^60 of the true scale when every
+// |G_i|^2 lies in [2^-120, 2^120]; a wave with any segment outside that runs
+// the unscaled step instead.
+// Slots (RS staging): S0 = (e / G_{i+1}, conj(G_{i+1}) f), S1 = (beta, pc, Re
+// G_CK for even t or Im G_CK for odd t), S2 = (h, conj(g_{t-1}) f), P = (p, a),
+// G = (delta g, g_{t-1}); d sel_C is stored by the staging itself.
+constexpr float kRsLo = 0x1p-120f, kRsHi = 0x1p120f;
+
 // Stage the per-token scalars of a tile, every slot of the slabs covering
 // [0, ntr).  Lane = (head j, block of TPB tokens); each lane loads and computes
 // its own tokens, runs g = prod a sequentially over them and joins the blocks
 // of its head with log2(NB) shuffle steps.  Slots past the last token and
-// heads >= H hold inert steps (a = 1, w = 0, beta = 0, f = 0).
-template <typename T, int HPW, bool WITH_W>
-__device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
+// heads >= H hold inert steps (a = 1, w = 0, beta = 0, f = 0).  With RS each
+// slab takes the rescaled-frame layout described above while every segment of
+// the wave's heads so far is in range (a wave vote per slab, before its slots
+// are written), else the unscaled layout; the return value is kStageRs when
+// every slab is rescaled, kStagePlain when none is, and kStageMixed when a
+// later slab fell back after an earlier one was written rescaled (the caller
+// then stages again without RS).  Without RS it is kStagePlain.
+constexpr int kStagePlain = 0, kStageMixed = 1, kStageRs = 2;
+template <typename T, int HPW, bool WITH_W, bool RS = false>
+__device__ __forceinline__ int stage_bwd(const ChunkTile& tc, int H, int ntr,
                                           const typename T::raw* __restrict__ v,
                                           const typename T::raw* __restrict__ beta,
                                           const typename T::raw* __restrict__ sel_c,
@@ -102,7 +130,7 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
                                           float c, const BwdScalars& s,
                                           const float4* __restrict__ saved = nullptr,
                                           float4* __restrict__ sP = nullptr, float4* __restrict__ sG = nullptr,
-                                          int R = 1) {
+                                          int R = 1, typename T::raw* __restrict__ dsel = nullptr) {
   constexpr int NB = kWave / HPW, TPB = HPW;
   const int lane = int(threadIdx.x) % kWave;  // lane in the wave (one-launch workgroups have several)
   const int j = lane / NB;
@@ -111,6 +139,10 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
   const bool hok = hj < H;
   const int hl = hok ? hj : H - 1;
   constexpr bool YM = IsSsdY<T>::value;
+  static_assert(!RS || (WITH_W && !YM), "rescaled frames: the readout form's main pass");
+  static_assert(kBwdCK % TPB == 0, "a segment is a whole number of blocks");
+  constexpr int SB = kBwdCK / TPB;  // blocks per segment
+  bool rsok = RS, wrote_rs = false;
   float cgr = 1.0f, cgi = 0.0f;  // g carried in from earlier slabs
   for (int tl = 0; tl < ntr; tl += kWave) {
     const int t0 = tl + blk * TPB;
@@ -144,6 +176,10 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
 #pragma unroll
     for (int i = 0; i < TPB; ++i) {
       const bool real = hok && t0 + i < tc.nt;
+      if constexpr (RS) {
+        // d sel_C = dy . (Y.q) needs nothing from the reverse pass: stored here
+        if (real) T::store(dsel + (tc.row0 + t0 + i) * H + hl, g0[i] * rq[i].z + g1[i] * rq[i].w);
+      }
       const Transition tr = YM ? Transition{dd[i], rr[i], 1.0f} : cayley_gated(dd[i], rr[i], al, om, c);
       ar[i] = real ? tr.ar : 1.0f;
       ai[i] = real ? tr.ai : 0.0f;
@@ -170,6 +206,39 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
       egi = 0.0f;
     }
     cmul_acc(egr, egi, cgr, cgi);
+    // RS: the segment's product entering this block (sgr, sgi) and over the
+    // whole segment (Sr, Si), by a scan over the SB blocks of the segment
+    float sgr = 1.0f, sgi = 0.0f, Sr = 1.0f, Si = 0.0f;
+    if constexpr (RS) {
+      float ir = gpr, ii = gpi;
+      for_shifts<SB>([&](auto offc) {
+        constexpr int off = decltype(offc)::value;
+        const float yr = seg_shift_up<SB, off>(ir), yi = seg_shift_up<SB, off>(ii);
+        if (blk % SB >= off) cmul_acc(ir, ii, yr, yi);
+      });
+      if constexpr (SB > 1) {
+        sgr = seg_shift_up<SB, 1>(ir);
+        sgi = seg_shift_up<SB, 1>(ii);
+        if (blk % SB == 0) {
+          sgr = 1.0f;
+          sgi = 0.0f;
+        }
+      }
+      const int last = lane - blk % SB + SB - 1;
+      Sr = __shfl(ir, last, kWave);
+      Si = __shfl(ii, last, kWave);
+      // every |G_{i+1}|^2 of the slab within the frames' range, on every lane
+      bool ok = true;
+#pragma unroll
+      for (int i = 0; i < TPB; ++i) {
+        float zr = sgr, zi = sgi;
+        cmul_acc(zr, zi, Gr[i], Gi[i]);
+        const float n2 = zr * zr + zi * zi;
+        ok = ok && n2 >= kRsLo && n2 <= kRsHi;
+      }
+      rsok = rsok && __all(ok);
+      wrote_rs = wrote_rs || rsok;
+    }
 #pragma unroll
     for (int i = 0; i < TPB; ++i) {
       const int p = (t0 + i) * HPW + j;
@@ -177,6 +246,26 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
       cmul_acc(gr, gi, Gr[i], Gi[i]);
       float pr = egr, pi = egi;  // g_{t-1}
       if (i > 0) cmul_acc(pr, pi, Gr[i - 1], Gi[i - 1]);
+      if (RS && rsok) {
+        // G_{i+1} of the token's segment, e = w - beta a p, and the rescaled coefficients
+        float zr = sgr, zi = sgi;
+        cmul_acc(zr, zi, Gr[i], Gi[i]);
+        const float inv = __builtin_amdgcn_rcpf(zr * zr + zi * zi);
+        const bool real = hok && t0 + i < tc.nt;
+        const float4 pp = real ? rp[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float4 qq = real ? rq[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float bpr = bb[i] * pp.x, bpi = bb[i] * pp.y;
+        const float er = v0[i] - (ar[i] * bpr - ai[i] * bpi), ei = v1[i] - (ar[i] * bpi + ai[i] * bpr);
+        const float ezr = (er * zr + ei * zi) * inv, ezi = (ei * zr - er * zi) * inv;  // e / G
+        const float fmr = zr * g0[i] + zi * g1[i], fmi = zr * g1[i] - zi * g0[i];      // conj(G) f
+        s.S0[p] = make_float4(ezr, ezi, fmr, fmi);
+        s.S1[p] = make_float4(bb[i], pp.z, pp.w, ((t0 + i) & 1) ? Si : Sr);
+        s.S2[p] = make_float4(gr * g0[i] + gi * g1[i], gr * g1[i] - gi * g0[i], pr * g0[i] + pi * g1[i],
+                              pr * g1[i] - pi * g0[i]);
+        sP[p] = make_float4(pp.x, pp.y, ar[i], ai[i]);
+        sG[p] = make_float4(g0[i] * qq.x + g1[i] * qq.y, g1[i] * qq.x - g0[i] * qq.y, pr, pi);
+        continue;
+      }
       s.S1[p] = make_float4(bb[i], g0[i], g1[i], 0.0f);
       if constexpr (YM)  // g_t weights the row dY_t: zero past the last token (the rows are clamped there)
         s.S2[p] = hok && t0 + i < tc.nt ? make_float4(gr, gi, pr, pi) : make_float4(0.0f, 0.0f, pr, pi);
@@ -200,6 +289,7 @@ __device__ __forceinline__ void stage_bwd(const ChunkTile& tc, int H, int ntr,
     cgr = __shfl(gtr, j * NB + NB - 1, kWave);
     cgi = __shfl(gti, j * NB + NB - 1, kWave);
   }
+  return rsok ? kStageRs : wrote_rs ? kStageMixed : kStagePlain;
 }
 
 // Per-token scalars of the correction-adjoint pass: S1 = (beta, 0, 0, 0),
@@ -855,7 +945,10 @@ __device__ __forceinline__ DynGrad cayley_gated_bwd(float dt, float r, float alp
 //   reverse pass, kBwdCK tokens at a time: z of the segment is recomputed
 //     from its checkpoint with the staged e_t (no reductions); c^_t is rebuilt
 //     backward, exactly, as c^_t = c^_{t+1} + beta_t pc_t k_t; the local adjoint
-//     mu and the correction adjoint lambda step back and dk, dq are emitted;
+//     mu and the correction adjoint lambda step back and dk, dq are emitted.
+//     Readout form: z and mu run in the segment's rescaled frames (no
+//     multiply by a_t per state element), unless a segment's rotation
+//     products leave the frames' range (then the wave takes the unscaled step);
 //   epilogue, lanes owning blocks of tokens: the token's scalar gradients
 //     (d a_t with the backward recurrence psi of the rotation products, the
 //     erase part of d beta), the dynamics chain rule, dv, dbeta, dsel, ddt, dr,
@@ -866,7 +959,7 @@ __device__ __forceinline__ DynGrad cayley_gated_bwd(float dt, float r, float alp
 // (delta g, 0, 0), delta g formed in the step).
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes == 2 ? 2 : 1, 2))) void fused_bwd_main_kernel(
     const typename T::raw* __restrict__ q, const typename T::raw* __restrict__ k,
     const typename T::raw* __restrict__ v, const typename T::raw* __restrict__ beta,
     const typename T::raw* __restrict__ sel_c, const typename T::raw* __restrict__ dt,
@@ -883,12 +976,13 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   constexpr int LPH = BwdCfg<D>::LPH, HPW = BwdCfg<D>::HPW, DPL = BwdCfg<D>::DPL, PF = kBwdPF, CK = kBwdCK;
   static_assert(CK == kZck && PF == kTokRound, "the training forward's z checkpoints: every CK tokens");
   extern __shared__ float4 smem4[];
-  // Reserve the whole 256-register budget: at most two waves share a SIMD.
-  // The kernel needs ~155 registers, which would let three waves onto some
-  // SIMDs while others hold one (one-wave workgroups are placed per SIMD as
-  // slots free up); those SIMDs then set the kernel's tail.  Measured on
-  // MI355X at C2 (D = 128, 1.5 rounds of waves): 287 us with three allowed,
-  // 248 us with two.
+  // Two waves per SIMD, never three: the attribute above holds the 2-byte
+  // kernels (rescaled and unscaled step in one kernel) to the 256-register
+  // budget of two waves, spilling a few values that live across the reverse
+  // pass; the reservation below keeps a lighter build from letting three waves
+  // onto some SIMDs while others hold one (one-wave workgroups are placed per
+  // SIMD as slots free up), which measured 287 against 248 us at C2 (D = 128,
+  // 1.5 rounds of waves) on MI355X.
   asm volatile("" ::: "v255");
   const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
@@ -936,7 +1030,14 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
   BwdScalars s{smem4, smem4 + slots, smem4 + 2 * slots};
   float4* sP = smem4 + 3 * slots;
   float4* sG = smem4 + 4 * slots;
-  stage_bwd<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, dy, al, om, c, s, saved, sP, sG, R);
+  // readout form: rescaled frames unless a segment's rotation product leaves their range
+  int staged = kStagePlain;
+  if constexpr (!YM)
+    staged = stage_bwd<T, HPW, true, true>(tc, H, ntr, v, beta, sel_c, dt, r, dy, al, om, c, s, saved, sP, sG, 1, dsel);
+  else
+    stage_bwd<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, dy, al, om, c, s, saved, sP, sG, R);
+  if (staged == kStageMixed) stage_bwd<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, dy, al, om, c, s, saved, sP, sG, R);
+  const bool rs = staged == kStageRs;
   __syncthreads();
 
   // ---- reverse pass ----
@@ -1088,26 +1189,135 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
       }
     }
   };
-  {
+  // The same step in the rescaled frames (readout form; slots in the RS layout).
+  // It leaves S0 = (mu^ conj(z~_i), mu^.k) and S1 = (lambda.k, pc); the
+  // epilogue converts them back to the true scale.
+  auto run_seg_rs = [&](const SegBuf& R, int seg) {
+    const int tb = seg * CK;
+    // z~_i for i = 0..CK: z~_{i+1} = z~_i + (e/G_{i+1}) k (no reductions); the k rows stay unpacked
+    float zbr[CK + 1][DPL], zbi[CK + 1][DPL], kr[CK][DPL];
+#pragma unroll
+    for (int jj = 0; jj < DPL; ++jj) {
+      zbr[0][jj] = R.z0[jj].x;
+      zbi[0][jj] = R.z0[jj].y;
+    }
+#pragma unroll
+    for (int i = 0; i < CK; ++i) {
+      const float4 s0 = s.S0[(tb + i) * HPW + hh];
+      R.k[i].unpack(kr[i]);
+#pragma unroll
+      for (int jj = 0; jj < DPL; ++jj) {
+        zbr[i + 1][jj] = fmaf(s0.x, kr[i][jj], zbr[i][jj]);
+        zbi[i + 1][jj] = fmaf(s0.y, kr[i][jj], zbi[i][jj]);
+      }
+    }
+    // mu into this segment's frame: mu^ = conj(G_CK) mu (G_CK: Re in the slot of
+    // an even token, Im in the slot of an odd one)
+    {
+      const float Gr = s.S1[(tb + CK - 2) * HPW + hh].w, Gi = s.S1[(tb + CK - 1) * HPW + hh].w;
+#pragma unroll
+      for (int jj = 0; jj < DPL; ++jj) {
+        const float nr = fmaf(Gr, mr[jj], Gi * mi[jj]);
+        mi[jj] = fmaf(Gr, mi[jj], -Gi * mr[jj]);
+        mr[jj] = nr;
+      }
+    }
+#pragma unroll
+    for (int i = CK - 1; i >= 0; --i) {
+      const int t = tb + i;
+      if (t < tc.nt) {
+        const int p = t * HPW + hh;
+        const float4 s0 = s.S0[p], s1 = s.S1[p], s2 = s.S2[p];
+        const float ezr = s0.x, ezi = s0.y, fmr = s0.z, fmi = s0.w, bb = s1.x;
+        const float pcr = s1.y, pci = s1.z;
+        const float* kk = kr[i];
+        float qq[DPL];
+        R.q[i].unpack(qq);
+        float red[6];
+#pragma unroll
+        for (int x = 0; x < 6; ++x) red[x] = 0.0f;
+        float dqv[DPL];
+        const float bpcr = bb * pcr, bpci = bb * pci;
+#pragma unroll
+        for (int jj = 0; jj < DPL; ++jj) {
+          // c^_t = c^_{t+1} + beta pc k
+          cr[jj] = fmaf(bpcr, kk[jj], cr[jj]);
+          ci[jj] = fmaf(bpci, kk[jj], ci[jj]);
+          // dq = Re(z_t conj(f)) + Re(c^_t conj(conj(g_{t-1}) f))
+          dqv[jj] = fmaf(zbr[i + 1][jj], fmr, fmaf(zbi[i + 1][jj], fmi, fmaf(cr[jj], s2.z, ci[jj] * s2.w)));
+          mr[jj] = fmaf(fmr, qq[jj], mr[jj]);
+          mi[jj] = fmaf(fmi, qq[jj], mi[jj]);
+          lr[jj] = fmaf(s2.x, qq[jj], lr[jj]);
+          li[jj] = fmaf(s2.y, qq[jj], li[jj]);
+          red[0] = fmaf(mr[jj], kk[jj], red[0]);
+          red[1] = fmaf(mi[jj], kk[jj], red[1]);
+          red[2] = fmaf(mr[jj], zbr[i][jj], fmaf(mi[jj], zbi[i][jj], red[2]));
+          red[3] = fmaf(mi[jj], zbr[i][jj], fmaf(-mr[jj], zbi[i][jj], red[3]));
+          red[4] = fmaf(lr[jj], kk[jj], red[4]);
+          red[5] = fmaf(li[jj], kk[jj], red[5]);
+        }
+#pragma unroll
+        for (int x = 0; x < 6; ++x) red[x] = group_sum<LPH>(red[x]);
+        // mu^.k, lambda.k
+        const float bdwr = bb * red[0], bdwi = bb * red[1], bslr = bb * red[4], bsli = bb * red[5];
+        float dkv[DPL];
+#pragma unroll
+        for (int jj = 0; jj < DPL; ++jj) {
+          float acc = mr[jj] * ezr;
+          acc = fmaf(mi[jj], ezi, acc);
+          acc = fmaf(-zbr[i][jj], bdwr, acc);
+          acc = fmaf(-zbi[i][jj], bdwi, acc);
+          acc = fmaf(-cr[jj], bslr, acc);
+          acc = fmaf(-ci[jj], bsli, acc);
+          acc = fmaf(-lr[jj], bpcr, acc);
+          dkv[jj] = fmaf(-li[jj], bpci, acc);
+          mr[jj] = fmaf(-bdwr, kk[jj], mr[jj]);
+          mi[jj] = fmaf(-bdwi, kk[jj], mi[jj]);
+          lr[jj] = fmaf(-bslr, kk[jj], lr[jj]);
+          li[jj] = fmaf(-bsli, kk[jj], li[jj]);
+        }
+        if (hok) {
+          store_row<T, DPL>(dks, t * rowb, dkv);
+          store_row<T, DPL>(dqs, t * rowb, dqv);
+        }
+        if (sub == 0) {
+          s.S0[p] = make_float4(red[2], red[3], red[0], red[1]);
+          s.S1[p] = make_float4(red[4], red[5], pcr, pci);
+        }
+      }
+    }
+  };
+  auto drive = [&](auto run) {
     SegBuf bufA, bufB;
     int seg = ntr / CK - 1;
     load_seg(bufA, seg);
     while (true) {
       load_seg(bufB, max(seg - 1, 0));  // unconditional: a clamped reload past segment 0 is harmless
       __builtin_amdgcn_sched_barrier(0);
-      run_seg(bufA, seg);
+      run(bufA, seg);
       if (--seg < 0) break;
       load_seg(bufA, max(seg - 1, 0));
       __builtin_amdgcn_sched_barrier(0);
-      run_seg(bufB, seg);
+      run(bufB, seg);
       if (--seg < 0) break;
     }
-  }
+  };
+  if constexpr (!YM)
+    drive([&](const SegBuf& R, int seg) {
+      if (rs)
+        run_seg_rs(R, seg);
+      else
+        run_seg(R, seg);
+    });
+  else
+    drive(run_seg);
   __syncthreads();
-
   // ---- per-token scalar gradients and dynamics backward: lane = (head j, block of TPB tokens) ----
   // Slots now hold S0 = (a, mu.z_{t-1}), S1 = (dw, sl), S2 = (h, g_{t-1}), P = (p, pc),
-  // G = (delta g, Y.q).  psi_t, the adjoint of the rotation product g_t, runs
+  // G = (delta g, Y.q); after the rescaled step S0 = (mu^ conj(z~_i), mu^.k),
+  // S1 = (sl, pc), P = (p, a), G = (delta g, g_{t-1}), and per token, with G_i and
+  // G_{i+1} of its segment, mu.k = (mu^.k) / conj(G_{i+1}) and mu conj(z_{t-1}) =
+  // (mu^ conj(z~_i)) conj(G_i) / conj(G_{i+1}).  psi_t, the adjoint of the rotation product g_t, runs
   // backward: psi_t = delta g_t + conj(a_{t+1}) psi_{t+1} (+ dG at the chunk's last
   // token), psi_nt = 0; each lane composes its block, a segmented suffix scan over
   // the head's NB blocks joins them, and slabs of kWave tokens run last to first.
@@ -1118,17 +1328,27 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
     const int hj = tc.hbase + j;
     const bool jok = hj < H;
     const int hjl = jok ? hj : H - 1;
-    const float alj = YM ? 0.0f : alpha[hjl], omj = YM ? 0.0f : omega[hjl];
+    const float alj = al, omj = om;  // head j is the reverse pass's head hh
     const int tend = round_up(ntr, kWave);  // staged slots: [0, tend)
+    constexpr int SB = CK / TPB;            // blocks per segment
+    // a_t of a slot in either layout
+    const auto a_of = [&](int p) {
+      if (rs) {
+        const float4 v4 = sP[p];
+        return make_float2(v4.z, v4.w);
+      }
+      const float4 v4 = s.S0[p];
+      return make_float2(v4.x, v4.y);
+    };
     float dal = 0.0f, dom = 0.0f;
     float pinr = 0.0f, pini = 0.0f;  // psi at the first token right of the slab
     for (int tl = tend - kWave; tl >= 0; tl -= kWave) {
       const int t0 = tl + blk * TPB;
       // the block with zero input: psi_t = X_t + A_t psi_{t0+TPB}
       float xr[TPB], xi[TPB], Ar[TPB], Ai[TPB];
+      float2 aa[TPB];  // a_t of the block's tokens
       {
-        float2 an = t0 + TPB < tend ? make_float2(s.S0[(t0 + TPB) * HPW + j].x, s.S0[(t0 + TPB) * HPW + j].y)
-                                    : make_float2(1.0f, 0.0f);
+        float2 an = t0 + TPB < tend ? a_of((t0 + TPB) * HPW + j) : make_float2(1.0f, 0.0f);
         float cxr = 0.0f, cxi = 0.0f, car = 1.0f, cai = 0.0f;
 #pragma unroll
         for (int i = TPB - 1; i >= 0; --i) {
@@ -1151,8 +1371,47 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
           xi[i] = cxi;
           Ar[i] = car;
           Ai[i] = cai;
-          const float4 s0 = s.S0[p];
-          an = make_float2(s0.x, s0.y);
+          an = a_of(p);
+          aa[i] = an;
+        }
+      }
+      // rescaled step: the factors back to the true scale, 1 / conj(G_{i+1}) and
+      // conj(G_i) / conj(G_{i+1}), from the segment's products over the block's
+      // tokens and a scan over the SB blocks of the segment
+      float cfr[TPB], cfi[TPB], gar[TPB], gai[TPB];
+      if (rs) {
+        float Pr[TPB], Pi[TPB], br = 1.0f, bi = 0.0f;
+#pragma unroll
+        for (int i = 0; i < TPB; ++i) {
+          cmul_acc(br, bi, aa[i].x, aa[i].y);
+          Pr[i] = br;
+          Pi[i] = bi;
+        }
+        float ir = br, ii = bi;
+        for_shifts<SB>([&](auto offc) {
+          constexpr int off = decltype(offc)::value;
+          const float yr = seg_shift_up<SB, off>(ir), yi = seg_shift_up<SB, off>(ii);
+          if (blk % SB >= off) cmul_acc(ir, ii, yr, yi);
+        });
+        float sgr = 1.0f, sgi = 0.0f;
+        if constexpr (SB > 1) {
+          sgr = seg_shift_up<SB, 1>(ir);
+          sgi = seg_shift_up<SB, 1>(ii);
+          if (blk % SB == 0) {
+            sgr = 1.0f;
+            sgi = 0.0f;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < TPB; ++i) {
+          float g0r = sgr, g0i = sgi, g1r = sgr, g1i = sgi;  // G_i, G_{i+1}
+          if (i > 0) cmul_acc(g0r, g0i, Pr[i - 1], Pi[i - 1]);
+          cmul_acc(g1r, g1i, Pr[i], Pi[i]);
+          const float inv = __builtin_amdgcn_rcpf(g1r * g1r + g1i * g1i);
+          cfr[i] = g1r * inv;
+          cfi[i] = g1i * inv;
+          gar[i] = g0r * cfr[i] + g0i * cfi[i];
+          gai[i] = g0r * cfi[i] - g0i * cfr[i];
         }
       }
       // suffix scan over the head's blocks: (SX, SA) maps psi right of block
@@ -1193,13 +1452,28 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
           const int p = t * HPW + j;
           const float4 s0 = s.S0[p], s1 = s.S1[p], s2 = s.S2[p], pv = sP[p], gv = sG[p];
           const float psr = xr[i] + (Ar[i] * per - Ai[i] * pei), psi = xi[i] + (Ar[i] * pei + Ai[i] * per);
-          const float ar = s0.x, ai = s0.y, dwr = s1.x, dwi = s1.y, slr = s1.z, sli = s1.w;
-          const float pr = pv.x, pi = pv.y, pcr = pv.z, pci = pv.w;
+          float ar = s0.x, ai = s0.y, mzr = s0.z, mzi = s0.w, dwr = s1.x, dwi = s1.y, slr = s1.z, sli = s1.w;
+          float pcr = pv.z, pci = pv.w, gpr = s2.z, gpi = s2.w;
+          if (rs) {
+            ar = aa[i].x;
+            ai = aa[i].y;
+            mzr = s0.x * gar[i] - s0.y * gai[i];
+            mzi = s0.x * gai[i] + s0.y * gar[i];
+            dwr = s0.z * cfr[i] - s0.w * cfi[i];
+            dwi = s0.z * cfi[i] + s0.w * cfr[i];
+            slr = s1.x;
+            sli = s1.y;
+            pcr = s1.z;
+            pci = s1.w;
+            gpr = gv.z;
+            gpi = gv.w;
+          }
+          const float pr = pv.x, pi = pv.y;
           // SSD form: beta per real head (the R virtual heads of its state rows share it)
           const float bb = T::load(beta + (YM ? (tc.row0 + t) * (H / R) + hj / R : e));
           // d a_t = mu.z_{t-1} - beta (mu.k) conj(p) + psi_t conj(g_{t-1})
-          const float dar = s0.z - bb * (pr * dwr + pi * dwi) + (s2.z * psr + s2.w * psi);
-          const float dai = s0.w - bb * (pr * dwi - pi * dwr) + (s2.z * psi - s2.w * psr);
+          const float dar = mzr - bb * (pr * dwr + pi * dwi) + (gpr * psr + gpi * psi);
+          const float dai = mzi - bb * (pr * dwi - pi * dwr) + (gpr * psi - gpi * psr);
           // d beta (erase part) = -(p . conj(a) dw) - (pc . sl)
           const float mkr = ar * dwr + ai * dwi, mki = ar * dwi - ai * dwr;
           const float dbe = -(pr * mkr + pi * mki) - (pcr * slr + pci * sli);
@@ -1225,7 +1499,7 @@ __global__ __launch_bounds__(kWave) void fused_bwd_main_kernel(
           T::store(dv + 2 * e, bb * tr.vp * dwr);
           T::store(dv + 2 * e + 1, bb * tr.vp * dwi);
           T::store(dbeta + e, dbe + tr.vp * dwv);
-          T::store(dsel + e, g0 * gv.z + g1 * gv.w);
+          if (!rs) T::store(dsel + e, g0 * gv.z + g1 * gv.w);  // (rescaled: stored by the staging)
           T::store(ddt + e, g.ddt);
           T::store(dr + e, g.dr);
           dal += g.dalpha;

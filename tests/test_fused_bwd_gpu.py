@@ -75,6 +75,34 @@ def test_fused_bwd_matches_oracle(name, cfg, chunk, path):
     assert not bad, f"gradients beyond {tol}: {bad}"
 
 
+@pytest.mark.parametrize("dtype,D", [("bf16", 64), ("fp32", 128)])
+def test_fused_bwd_vanishing_transitions_match_oracle(dtype, D):
+    """A few tokens of head 1 with a vanishing transition: alpha = 2, omega = 0,
+    dt = 1 and r = 1 give tau * alpha = 1, so E sits at its 1e-8 floor and
+    |a_t|^2 = 1e-8^(c r) is below the fp32 range.  The main pass's rescaled
+    frames need every segment's rotation products within 2^-120 .. 2^120, so
+    the waves holding those tokens take the unscaled step and the rest the
+    rescaled one, in the same call; both must match the oracle."""
+    cfg = ScanConfig("t", B=2, H=4, L=640, D=D, dtype=dtype)
+    log(f"[fused bwd vanishing a] B2 H4 L640 D{D} {dtype}")
+    x = draw_inputs(cfg, seed=5)
+    x["alpha"][1] = 2.0
+    x["omega"][1] = 0.0
+    dt, r = x["dt"].clone(), x["r"].clone()
+    for b, t in ((0, 70), (0, 71), (0, 400), (1, 200)):
+        dt[b, t, 1] = 1.0
+        r[b, t, 1] = 1.0
+    x["dt"], x["r"] = dt, r
+    gy, gh = cotangents(cfg)
+    ref = oracle_grads(x, gy, gh)
+    got = hip_grads(x, gy, gh)
+    tol = 1e-4 if dtype == "fp32" else 2e-2
+    errs = {n: rel(got[n], ref[n]) for n in ref}
+    log("   " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
+    bad = {n: e for n, e in errs.items() if not e <= tol}
+    assert not bad, f"gradients beyond {tol}: {bad}"
+
+
 def test_fused_bwd_full_c2_sequences_match_oracle():
     """C2 shape (B4 H24 L8192 D128, bf16) on the GPU; selected sequences re-derived by the oracle.
 
