@@ -1344,6 +1344,27 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
     float pinr = 0.0f, pini = 0.0f;  // psi at the first token right of the slab
     for (int tl = tend - kWave; tl >= 0; tl -= kWave) {
       const int t0 = tl + blk * TPB;
+      // the slab's per-token inputs, requested before the psi pass so that its
+      // latency covers theirs (rows past the last token clamped, unused)
+      float lbb[TPB], lv0[TPB], lv1[TPB], ldt[TPB], lrr[TPB], lg0[TPB], lg1[TPB];
+#pragma unroll
+      for (int i = 0; i < TPB; ++i) {
+        const int tt = min(t0 + i, tc.nt - 1);
+        const int64_t ee = (tc.row0 + tt) * H + hjl;
+        // SSD form: beta per real head (the R virtual heads of its state rows share it)
+        lbb[i] = T::load(beta + (YM ? (tc.row0 + tt) * (H / R) + hjl / R : ee));
+        lv0[i] = T::load(v + 2 * ee);
+        lv1[i] = T::load(v + 2 * ee + 1);
+        ldt[i] = lrr[i] = lg0[i] = lg1[i] = 0.0f;
+        if constexpr (!YM) {
+          ldt[i] = T::load(dt + ee);
+          lrr[i] = T::load(r + ee);
+          if (!rs) {
+            lg0[i] = T::load(dy + 2 * ee);
+            lg1[i] = T::load(dy + 2 * ee + 1);
+          }
+        }
+      }
       // the block with zero input: psi_t = X_t + A_t psi_{t0+TPB}
       float xr[TPB], xi[TPB], Ar[TPB], Ai[TPB];
       float2 aa[TPB];  // a_t of the block's tokens
@@ -1469,15 +1490,14 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
             gpi = gv.w;
           }
           const float pr = pv.x, pi = pv.y;
-          // SSD form: beta per real head (the R virtual heads of its state rows share it)
-          const float bb = T::load(beta + (YM ? (tc.row0 + t) * (H / R) + hj / R : e));
+          const float bb = lbb[i];
           // d a_t = mu.z_{t-1} - beta (mu.k) conj(p) + psi_t conj(g_{t-1})
           const float dar = mzr - bb * (pr * dwr + pi * dwi) + (gpr * psr + gpi * psi);
           const float dai = mzi - bb * (pr * dwi - pi * dwr) + (gpr * psi - gpi * psr);
           // d beta (erase part) = -(p . conj(a) dw) - (pc . sl)
           const float mkr = ar * dwr + ai * dwi, mki = ar * dwi - ai * dwr;
           const float dbe = -(pr * mkr + pi * mki) - (pcr * slr + pci * sli);
-          const float v0 = T::load(v + 2 * e), v1 = T::load(v + 2 * e + 1);
+          const float v0 = lv0[i], v1 = lv1[i];
           if constexpr (YM) {
             // SSD form: d A_bar_t = d a_t (into ddt's place, (re, im) pairs), dV = beta dw,
             // dbeta = erase part + dw . V (w = beta V)
@@ -1491,8 +1511,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
               T::store(dbeta + e, db);
             continue;
           }
-          const float dtv = T::load(dt + e), rrv = T::load(r + e);
-          const float g0 = T::load(dy + 2 * e), g1 = T::load(dy + 2 * e + 1);
+          const float dtv = ldt[i], rrv = lrr[i];
+          const float g0 = lg0[i], g1 = lg1[i];
           const Transition tr = cayley_gated(dtv, rrv, alj, omj, c);
           const float dwv = dwr * v0 + dwi * v1;
           const DynGrad g = cayley_gated_bwd(dtv, rrv, alj, omj, c, dar, dai, bb * dwv);
