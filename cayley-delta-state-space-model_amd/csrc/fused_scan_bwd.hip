@@ -144,32 +144,51 @@ __device__ __forceinline__ int stage_bwd(const ChunkTile& tc, int H, int ntr,
   constexpr int SB = kBwdCK / TPB;  // blocks per segment
   bool rsok = RS, wrote_rs = false;
   float cgr = 1.0f, cgi = 0.0f;  // g carried in from earlier slabs
-  for (int tl = 0; tl < ntr; tl += kWave) {
-    const int t0 = tl + blk * TPB;
+  // a slab's inputs and the training forward's records (p, pc), (c^_{t+1}.q, Y.q);
+  // the next slab's are requested before this one is worked on
+  struct SlabIn {
     float bb[TPB], dd[TPB], rr[TPB], v0[TPB], v1[TPB], sc[TPB], g0[TPB], g1[TPB];
+    float4 rp[TPB], rq[TPB];
+  };
+  const auto load_slab = [&](SlabIn& in, int tl) {
 #pragma unroll
     for (int i = 0; i < TPB; ++i) {
-      const int t = min(t0 + i, tc.nt - 1);
+      const int t = min(tl + blk * TPB + i, tc.nt - 1);
       const int64_t e = (tc.row0 + t) * H + hl;
-      bb[i] = T::load(beta + (YM ? (tc.row0 + t) * (H / R) + hl / R : e));  // SSD form: beta per real head
-      dd[i] = T::load(dt + (YM ? 2 * e : e));  // SSD form: a_t (re, im) from A_bar
-      rr[i] = T::load(YM ? dt + 2 * e + 1 : r + e);
-      v0[i] = WITH_W ? T::load(v + 2 * e) : 0.0f;
-      v1[i] = WITH_W ? T::load(v + 2 * e + 1) : 0.0f;
-      sc[i] = YM ? 0.0f : T::load(sel_c + e);
-      g0[i] = YM ? 0.0f : T::load(dy + 2 * e);
-      g1[i] = YM ? 0.0f : T::load(dy + 2 * e + 1);
-    }
-    // the training forward's records: (p, pc), (c^_{t+1}.q, Y.q)
-    float4 rp[TPB], rq[TPB];
-    if constexpr (WITH_W) {
-#pragma unroll
-      for (int i = 0; i < TPB; ++i) {
-        const int t = min(t0 + i, tc.nt - 1);
-        const int64_t e = (tc.row0 + t) * H + hl;
-        rp[i] = saved[2 * e];
-        rq[i] = YM ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : saved[2 * e + 1];
+      in.bb[i] = T::load(beta + (YM ? (tc.row0 + t) * (H / R) + hl / R : e));  // SSD form: beta per real head
+      in.dd[i] = T::load(dt + (YM ? 2 * e : e));  // SSD form: a_t (re, im) from A_bar
+      in.rr[i] = T::load(YM ? dt + 2 * e + 1 : r + e);
+      in.v0[i] = WITH_W ? T::load(v + 2 * e) : 0.0f;
+      in.v1[i] = WITH_W ? T::load(v + 2 * e + 1) : 0.0f;
+      in.sc[i] = YM ? 0.0f : T::load(sel_c + e);
+      in.g0[i] = YM ? 0.0f : T::load(dy + 2 * e);
+      in.g1[i] = YM ? 0.0f : T::load(dy + 2 * e + 1);
+      if constexpr (WITH_W) {
+        in.rp[i] = saved[2 * e];
+        in.rq[i] = YM ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : saved[2 * e + 1];
       }
+    }
+  };
+  SlabIn nx;
+  load_slab(nx, 0);
+  for (int tl = 0; tl < ntr; tl += kWave) {
+    const int t0 = tl + blk * TPB;
+    const SlabIn in = nx;
+    if (tl + kWave < ntr) load_slab(nx, tl + kWave);
+    float bb[TPB], dd[TPB], rr[TPB], v0[TPB], v1[TPB], sc[TPB], g0[TPB], g1[TPB];
+    float4 rp[TPB], rq[TPB];
+#pragma unroll
+    for (int i = 0; i < TPB; ++i) {
+      bb[i] = in.bb[i];
+      dd[i] = in.dd[i];
+      rr[i] = in.rr[i];
+      v0[i] = in.v0[i];
+      v1[i] = in.v1[i];
+      sc[i] = in.sc[i];
+      g0[i] = in.g0[i];
+      g1[i] = in.g1[i];
+      rp[i] = in.rp[i];
+      rq[i] = in.rq[i];
     }
     float ar[TPB], ai[TPB], Gr[TPB], Gi[TPB];
     float gpr = 1.0f, gpi = 0.0f;
