@@ -134,6 +134,12 @@ def chunkwise_delta_scan_abar(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel
 
 FORWARD_PATHS = {"auto": 0, "four_launch": 1, "one_pass": 2, "four_launch_mfma": 3}
 
+# Bumped by every set_forward_path call.  A prepared call continues on the
+# look-back epoch its previous call left only while the path setting is the one
+# that call ran under: a call made under another setting may have taken the
+# multi-launch passes, which never write the workspace's control block.
+_path_generation = [0]
+
 
 def set_forward_path(path: str) -> str:
     """Select how the inference forward is launched; returns the previous setting.
@@ -153,6 +159,7 @@ def set_forward_path(path: str) -> str:
     prev = _lib.load().cdssm_fused_scan_fwd_set_path(FORWARD_PATHS[path])
     if prev < 0:
         _lib.check(prev, "cdssm_fused_scan_fwd_set_path")
+    _path_generation[0] += 1
     return {v: n for n, v in FORWARD_PATHS.items()}[prev]
 
 
@@ -222,10 +229,13 @@ class PreparedForward:
                       _lib.ptr(h0), _lib.ptr(self.y), _lib.ptr(self.h_final), _lib.ptr(self.workspace),
                       B, L, H, D, N, Q)
         self._continue = False  # the workspace holds a previous forward call's look-back area
+        self._gen = -1  # the path setting that call ran under
 
     def __call__(self):
         lib = self._lib
-        if self._continue:
+        gen = _path_generation[0]
+        cont = self._continue and self._gen == gen
+        if cont:
             fn = lib.cdssm_fused_scan_fwd_train_continue if self.train else lib.cdssm_fused_scan_fwd_continue
         else:
             fn = lib.cdssm_fused_scan_fwd_train if self.train else lib.cdssm_fused_scan_fwd
@@ -233,7 +243,8 @@ class PreparedForward:
         if st != 0:
             _lib.check(st, "cdssm_fused_scan_fwd")
         # a captured call does not run now: the workspace holds no call until one executes
-        self._continue = self._continue or not torch.cuda.is_current_stream_capturing()
+        self._continue = cont or not torch.cuda.is_current_stream_capturing()
+        self._gen = gen
         return self.y, self.h_final
 
     PHASES = ("summary", "carry_fold", "carry_replay", "main")
@@ -479,13 +490,17 @@ class PreparedBackward:
                       _lib.ptr(fwd.workspace), *[_lib.ptr(t) for t in self.grads], _lib.ptr(self.dalpha),
                       _lib.ptr(self.domega), _lib.ptr(self.dh0), _lib.ptr(self.workspace), B, L, H, D, N, Q)
         self._continue = False
+        self._gen = -1
 
     def __call__(self):
-        fn = self._lib.cdssm_fused_scan_bwd_continue if self._continue else self._lib.cdssm_fused_scan_bwd
+        gen = _path_generation[0]
+        cont = self._continue and self._gen == gen
+        fn = self._lib.cdssm_fused_scan_bwd_continue if cont else self._lib.cdssm_fused_scan_bwd
         st = fn(*self._args, _lib.stream_of(self.device))
         if st != 0:
             _lib.check(st, "cdssm_fused_scan_bwd")
-        self._continue = self._continue or not torch.cuda.is_current_stream_capturing()
+        self._continue = cont or not torch.cuda.is_current_stream_capturing()
+        self._gen = gen
         return self.grads
 
     PHASES = ("corr_adjoint", "rcarry_fold", "rcarry_replay", "main", "heads")

@@ -1553,6 +1553,8 @@ FwdRegions infer_regions(float2* base, const FwdLayout& w) {
   return g;
 }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 // Phase-stamp buffer of the running cdssm_fused_scan_fwd_stamped call on this
 // host thread (instrumentation only): device memory of `len` 8-byte words.
 struct StampRequest {
@@ -1610,7 +1612,10 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
     // wide staging loads (bf16 scan-level form, 8 heads per wave); the persistent
     // training forward (taken only when the one-pass path is forced) keeps the narrow ones
     constexpr bool kWideOk = std::is_same<T, BF16>::value && kWave / LPH == 8;
-    const bool wide = kWideOk && H % 8 == 0 && Q <= kWave && cdssm_host::wide_staging();
+    // the wide loads are 16-byte vector loads of beta, sel_C, dt, r and v rows:
+    // every one of those arrays must start on a 16-byte boundary
+    const bool wide = kWideOk && H % 8 == 0 && Q <= kWave && cdssm_host::wide_staging() && aligned16(beta) &&
+                      aligned16(sel_c) && aligned16(dt) && aligned16(r) && aligned16(v);
     const int cap1 = save   ? (wide ? onepass_capacity<T, D, LPH, kSv, false, kWideOk>(lds)
                                     : onepass_capacity<T, D, LPH, kSv, false>(lds))
                      : wide ? onepass_capacity<T, D, LPH, false, false, kWideOk>(lds)
@@ -1624,7 +1629,9 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
     const bool persist = !single && capp > 0 && items <= 0x7fffffff &&
                          (forced || (!save && items * 10 >= rounds * capp * 9));
     if (single || persist) {
-      const int grid = single ? int(items) : capp;
+      // a persistent workgroup joins the epoch count on its first item, so the
+      // grid never exceeds the items (every workgroup gets at least one)
+      const int grid = single ? int(items) : int(std::min<int64_t>(capp, items));
       float2* base = reg.onepass;
       const int64_t nsd = int64_t(B) * w.NSEG * H * D, nsh = int64_t(B) * w.NSEG * H;
       OnePassArgs<T> a;
@@ -1779,8 +1786,6 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
   if (ev) (void)hipEventRecord(ev[4], stream);
   return st;
 }
-
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
 

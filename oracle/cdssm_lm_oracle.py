@@ -64,6 +64,17 @@ def _linear(x: Tensor, w: Tensor, b: Optional[Tensor] = None) -> Tensor:
     return y if b is None else y + b
 
 
+def block_gate_rows(p: dict, pre: str, x: Tensor, cfg) -> tuple:
+    """The block's in_proj output, conv output and gate rows (block.py:160-181): (proj, x_conv, gate_raw)."""
+    Di = cfg.d_inner
+    g = lambda n: p[pre + n]  # noqa: E731
+    proj = _linear(rms_norm(x, g("norm.weight"), cfg.eps_norm), g("in_proj.weight"), g("in_proj.bias"))
+    x_gate = proj[..., Di:2 * Di]                                       # block.py:162-166 split order
+    x_conv = conv1d_silu(x_gate, g("conv.weight"), g("conv.bias"))      # block.py:177
+    gates = _linear(x_conv, g("gate_proj.weight"), g("gate_proj.bias"))
+    return proj, x_conv, gates
+
+
 def block_forward(p: dict, pre: str, x: Tensor, v_first: Optional[Tensor], cfg, grad_mode: str = "exact") -> tuple:
     """One CDSSMBlock.forward (block.py:140-229) with the block's parameters p[pre + name].
 
@@ -74,16 +85,14 @@ def block_forward(p: dict, pre: str, x: Tensor, v_first: Optional[Tensor], cfg, 
     B, L, _ = x.shape
     g = lambda n: p[pre + n]  # noqa: E731
     residual = x
-    proj = _linear(rms_norm(x, g("norm.weight"), cfg.eps_norm), g("in_proj.weight"), g("in_proj.bias"))
-    z, x_gate, K, V = proj.split([Di, Di, Di, H * N], dim=-1)           # block.py:162-166
+    proj, x_conv, gates = block_gate_rows(p, pre, x, cfg)
+    z, _, K, V = proj.split([Di, Di, Di, H * N], dim=-1)                # block.py:162-166
     K = K.reshape(B, L, H, D)
     V = V.reshape(B, L, H, N)
     if v_first is None:                                                 # block.py:169-174
         v_first = V.detach()                                            # layer 0's values, no gradient path
     else:
         V = torch.lerp(v_first, V, torch.sigmoid(g("v_residual_gate"))[None, None, :, None])
-    x_conv = conv1d_silu(x_gate, g("conv.weight"), g("conv.bias"))      # block.py:177
-    gates = _linear(x_conv, g("gate_proj.weight"), g("gate_proj.bias"))
     rope = 1.0 / (cfg.rope_base ** (torch.arange(0, H, dtype=x.dtype) / H))   # block.py:59-62
     dyn = o.dynamics_with_reference_grad if grad_mode == "reference" else o.dynamics_fused_fwd
     A_bar, vp, beta, sel_C = dyn(gates, g("log_dt_scale"), rope, cfg.gating_c, cfg.bf16_omega_thresh,

@@ -166,9 +166,10 @@ def _split_gates(gate_raw: Tensor, n_heads: int, state_dim: int):
     )
 
 
-def adaptive_dt(alpha0: Tensor, omega0: Tensor, log_dt_scale: Tensor, sel_dt_raw: Tensor,
-                omega_thresh: float, adt_delta: float, adt_smoothness: float, adt_eps: float) -> Tensor:
-    """dt = blend*min(dt_raw, dt_max) + (1-blend)*dt_raw + softplus(sel_dt) (dynamics_fused.cu:85-94)."""
+def adaptive_dt_parts(alpha0: Tensor, omega0: Tensor, log_dt_scale: Tensor, sel_dt_raw: Tensor,
+                      omega_thresh: float, adt_delta: float, adt_smoothness: float, adt_eps: float) -> dict:
+    """The adaptive timestep's pieces (dynamics_fused.cu:85-94): dt_raw, dt_max, blend, capped
+    (dt_raw > dt_max, the branch :350-352 differentiates) and dt."""
     dt_scale = softplus(log_dt_scale)
     om_abs = omega0.abs()
     char_freq = alpha0 + om_abs + adt_eps
@@ -176,7 +177,37 @@ def adaptive_dt(alpha0: Tensor, omega0: Tensor, log_dt_scale: Tensor, sel_dt_raw
     dt_max = (2.0 - adt_delta) / (alpha0 + adt_eps)
     blend = sigmoid((omega_thresh - om_abs) / adt_smoothness)
     dt_capped = torch.minimum(dt_raw, dt_max)
-    return blend * dt_capped + (1.0 - blend) * dt_raw + softplus(sel_dt_raw)
+    dt = blend * dt_capped + (1.0 - blend) * dt_raw + softplus(sel_dt_raw)
+    return dict(dt_raw=dt_raw, dt_max=dt_max, blend=blend, capped=dt_raw > dt_max, dt=dt)
+
+
+def adaptive_dt(alpha0: Tensor, omega0: Tensor, log_dt_scale: Tensor, sel_dt_raw: Tensor,
+                omega_thresh: float, adt_delta: float, adt_smoothness: float, adt_eps: float) -> Tensor:
+    """dt = blend*min(dt_raw, dt_max) + (1-blend)*dt_raw + softplus(sel_dt) (dynamics_fused.cu:85-94)."""
+    return adaptive_dt_parts(alpha0, omega0, log_dt_scale, sel_dt_raw, omega_thresh, adt_delta,
+                             adt_smoothness, adt_eps)["dt"]
+
+
+def dynamics_regimes(gate_raw: Tensor, log_dt_scale: Tensor, rope_freqs: Tensor, gating_c: float,
+                     omega_thresh: float, adt_delta: float, adt_smoothness: float, adt_eps: float,
+                     n_heads: int, state_dim: int) -> dict:
+    """Which branches of DynamicsFusedFn each (b, l, h) takes, from this module's own forward: boolean
+    (B, L, H) masks ``capped`` (the adaptive-dt cap, dt_raw > dt_max), ``blend_mid`` (capped with the
+    blend in (0.05, 0.95), where the blend's derivative :355-359 is material) and, per pair (B, L, H, N/2),
+    ``vp_clamped`` (vp at its floor sqrt(1e-6), the clamp :113-118 / :247-259) and ``vp_one`` (vp within
+    2^-25 of 1, i.e. 1 in fp32, where the reference's backward drops the vp cotangent, :247)."""
+    B, L, _ = gate_raw.shape
+    g = _split_gates(gate_raw, n_heads, state_dim)
+    pos = torch.arange(L, dtype=gate_raw.dtype)[None, :, None]
+    alpha0 = softplus(g["alpha_raw"][:, :, 0])
+    omega0 = g["omega_raw"][:, :, 0] + pos * rope_freqs.to(gate_raw.dtype)[None, None, :]
+    parts = adaptive_dt_parts(alpha0, omega0, log_dt_scale.to(gate_raw.dtype)[None, None, :], g["sel_dt"],
+                              omega_thresh, adt_delta, adt_smoothness, adt_eps)
+    _, vp, _, _ = dynamics_fused_fwd(gate_raw, log_dt_scale, rope_freqs, gating_c, omega_thresh, adt_delta,
+                                     adt_smoothness, adt_eps, n_heads, state_dim)
+    mid = (parts["blend"] > 0.05) & (parts["blend"] < 0.95)
+    return dict(capped=parts["capped"], blend_mid=parts["capped"] & mid,
+                vp_clamped=(vp - math.sqrt(EPS_DEFAULT)).abs() < 1e-12, vp_one=vp >= 1.0 - 2.0 ** -25)
 
 
 def dynamics_fused_fwd(gate_raw: Tensor, log_dt_scale: Tensor, rope_freqs: Tensor,

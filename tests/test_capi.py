@@ -306,3 +306,10 @@ def test_block_entry_points_reject_invalid_arguments_without_launching(fn, bad, 
     args.update(bad)
     assert getattr(lib, fn)(*args.values()) == -1
     assert msg in _lib.last_error()
+
+
+def test_noalloc_rejects_shapes_beyond_its_scratch_without_launching():
+    # the size check comes before any device query, so fake pointers never reach a kernel
+    lib = _lib.load()
+    st = lib.cdssm_fused_scan_fwd_noalloc(1, *([16] * 9), 1.0, None, 16, 16, 64, 65536, 32, 64, 2, 64, None)
+    assert st == -1 and "static scratch" in _lib.last_error()

@@ -1,4 +1,4 @@
-"""Reference checkpoints load into cdssm_hip.lm (CPU only).
+"""Reference checkpoints load into cdssm_hip.lm, and run on the GPU as predict.py does.
 
 The key list below is written out from the reference's modules -- block.py:41-82
 (in_proj, conv, gate_proj, log_dt_scale, Q_proj, readout_proj, out_proj, norm,
@@ -9,6 +9,11 @@ with the shapes their constructors give for the reference config, so a renamed
 or reshaped parameter in this build fails the strict load.  The checkpoint is
 written the way trainer.py:201-215 writes it, with torch.compile's `_orig_mod.`
 prefix (predict.py:23) and asdict(config) including the derived fields.
+
+The one GPU test (marked gpu) follows predict.py:10-30 to the end: a checkpoint of
+the reference config (d_inner = 2 d_model, the default state_dim 16) loaded onto the
+GPU in bf16 (predict.py:27) and run, its logits against the fp64 oracle LM on the
+loaded (bf16-rounded) weights, 2e-2 normwise.
 """
 
 import math
@@ -113,3 +118,36 @@ def test_a_strict_load_rejects_a_missing_or_renamed_key(tmp_path):
     _write_checkpoint(path, cfg_dict, shapes)
     with pytest.raises(RuntimeError, match="Q_proj"):
         load_reference_checkpoint(str(path))
+
+
+@pytest.mark.gpu
+def test_reference_checkpoint_runs_on_the_gpu_in_bf16_like_predict(tmp_path):
+    from _gpu_util import DEV, log, rel
+    from cdssm_hip.lm import CDSSMConfig, CDSSMLMHeadModel
+    from oracle import cdssm_lm_oracle as lo
+    torch.manual_seed(0)
+    cfg = CDSSMConfig(d_model=128, n_layers=2, context_length=512, vocab_size=97, state_dim=16)
+    assert cfg.d_inner == 256 and cfg.n_heads == 4  # the reference's derivation (config/model.py:57)
+    m = CDSSMLMHeadModel(cfg)
+    with torch.no_grad():  # trained-looking weights: the value residual, shortcut and skip are live
+        for blk in m.blocks:
+            blk.v_residual_gate.normal_(std=1.0)
+            blk.shortcut_scale.fill_(0.3)
+            blk.D.normal_(std=0.1)
+            blk.log_dt_scale.normal_(std=0.5)
+    sd = {"_orig_mod." + k: v for k, v in m.state_dict().items()}
+    path = tmp_path / "ref_best.pt"
+    torch.save({"model_state_dict": sd, "config": reference_config_dict(128, 2, 512, 97, 16), "step": 3,
+                "tokens_seen": 99, "seed": 0, "timestamp": "2026-01-01T00:00:00",
+                "optimizer_state_dict": {"state": {}, "param_groups": []}, "metrics": {}}, path)
+    log("[checkpoint on the GPU] reference config d_model 128 d_inner 256 N16, bf16 like predict.py:27")
+    model, _ = load_reference_checkpoint(str(path), device=DEV, dtype=torch.bfloat16)
+    assert model.config.d_inner == 256 and model.config.state_dim == 16
+    assert next(model.parameters()).dtype == torch.bfloat16 and next(model.parameters()).is_cuda
+    p = {k: v.detach().double().cpu() for k, v in model.state_dict().items()}
+    ids = torch.randint(0, cfg.vocab_size, (2, 150), generator=torch.Generator().manual_seed(4))
+    with torch.no_grad():
+        logits = model(ids.to(DEV)).float().cpu()
+    e = rel(logits, lo.lm_forward(p, ids, model.config))
+    log(f"   rel err logits {e:.2e}")
+    assert torch.isfinite(logits).all() and e <= 2e-2

@@ -182,6 +182,50 @@ def test_dynamics_bwd_restatement_matches_autograd_off_clamps():
     assert float(ga.abs().max()) > 0.1
 
 
+def _capped_gate_inputs(g, B, L, H, N):
+    """Gate rows in the adaptive-dt cap with a material blend: alpha_0 ~ softplus(-3) ~ 0.05,
+    |omega_0| within 0.035 of omega_thresh (0.088; either sign), log_dt_scale ~ 3, so
+    dt_raw = softplus(3)/(alpha_0 + |omega_0| + 1) ~ 2.7 > dt_max = 1.875/(alpha_0 + 1) ~ 1.8 and
+    blend = sigmoid((thr - |omega_0|)/smooth) spans (0.1, 0.9).  Other gates: N(0, 0.5)."""
+    freqs = 1.0 / (float(L) ** (torch.arange(H, dtype=DT) / H))
+    gate = randn(g, B, L, N + 5, H) * 0.5
+    pos = torch.arange(L, dtype=DT)[None, :, None]
+    gate[:, :, 0] = -3.0 + 0.3 * randn(g, B, L, H)
+    sign = torch.where(torch.rand(B, L, H, generator=g, dtype=DT) < 0.5, -1.0, 1.0)
+    target = CONSTS["omega_thresh"] + (torch.rand(B, L, H, generator=g, dtype=DT) * 2 - 1) * 0.035
+    gate[:, :, N // 2] = sign * target - pos * freqs
+    lds = 3.0 + 0.2 * randn(g, H)
+    return gate.reshape(B, L, (N + 5) * H), lds, freqs
+
+
+@pytest.mark.parametrize("N", [2, 4])
+def test_dynamics_bwd_restatement_matches_autograd_with_the_cap_active(N):
+    """The cap branch of the restated backward (dynamics_fused.cu:345-374: the capped/uncapped split of
+    g_dt, d blend / d|omega_0|, the dt_max term of alpha_0) against autograd of the forward, on rows where
+    every token-head is capped with the blend in (0.05, 0.95) and no VP clamp is near.  The reference's
+    cap terms are the exact derivative, so the only departure is the eps-free |D|^2 term (O(1e-6)).  A
+    swapped sign of the blend's derivative changes the omega_0 gradients by O(1) here."""
+    g = rng(21)
+    B, L, H = 2, 24, 3
+    gate, lds, freqs = _capped_gate_inputs(g, B, L, H, N)
+    reg = o.dynamics_regimes(gate, lds, freqs, n_heads=H, state_dim=N, **CONSTS)
+    assert bool(reg["blend_mid"].all()), "every token-head must be capped with a material blend"
+    assert not bool(reg["vp_clamped"].any()) and not bool(reg["vp_one"].any())
+    gate.requires_grad_(True)
+    lds.requires_grad_(True)
+    outs = o.dynamics_fused_fwd(gate, lds, freqs, n_heads=H, state_dim=N, **CONSTS)
+    grads = [randn(g, *t.shape) for t in outs]
+    loss = sum((t * w).sum() for t, w in zip(outs, grads))
+    ga, gl = torch.autograd.grad(loss, [gate, lds])
+    gh, glh = o.dynamics_fused_bwd_ref(*grads, gate.detach(), lds.detach(), freqs,
+                                       n_heads=H, state_dim=N, **CONSTS)
+    assert float((gh - ga).abs().max()) <= 1e-5 * float(ga.abs().max())
+    assert float((glh - gl).abs().max()) <= 1e-5 * float(gl.abs().max())
+    # the omega_0 column carries the blend's derivative: it is large here
+    w0 = ga.reshape(B, L, N + 5, H)[:, :, N // 2]
+    assert float(w0.abs().max()) > 1.0
+
+
 def test_dynamics_bwd_restatement_keeps_vp_clamp_gradient():
     """Inside the VP clamp the reference still passes -0.5/vp * g_vp (dynamics_fused.cu:256-259)."""
     H, N, L = 1, 2, 1

@@ -66,10 +66,3 @@ def test_noalloc_forward_matches_workspace_forward_on_two_calls(path):
     finally:
         set_forward_path(prev)
     assert lookback_status() == 0, "a look-back wait timed out"
-
-
-def test_noalloc_rejects_shapes_beyond_its_scratch():
-    from cdssm_hip import _lib
-    lib = _lib.load()
-    st = lib.cdssm_fused_scan_fwd_noalloc(1, *([16] * 9), 1.0, None, 16, 16, 64, 65536, 32, 64, 2, 64, None)
-    assert st == -1 and "static scratch" in _lib.last_error()
