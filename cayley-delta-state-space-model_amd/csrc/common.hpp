@@ -461,6 +461,28 @@ struct FwdLayout {
   int64_t cend_offset() const { return zck_offset() + n_zck; }
 };
 
+// The one-pass forward's look-back folds two levels: every kFwdGroup-th
+// segment publishes the composed map of its group of kFwdGroup segments, and
+// the state entering a segment is folded from its anchor (every kFwdAnchor
+// segments, a multiple of kFwdGroup) over the maps of the whole groups since
+// the anchor, then over the maps of its own group's earlier segments.
+// A segment at most kFwdDirect segments past its anchor folds the segment
+// maps directly (no wait on a group map); group ends compose their group's
+// map only where a later segment reads it.
+constexpr int kFwdGroup = 8;
+constexpr int kFwdAnchor = 64;
+constexpr int kFwdDirect = 2 * kFwdGroup - 1;
+static_assert(kFwdAnchor % kFwdGroup == 0, "anchors start groups");
+__host__ __device__ constexpr int fwd_groups(int nseg) { return (nseg + kFwdGroup - 1) / kFwdGroup; }
+// Whether some segment folds the map of group g (segments kFwdGroup g ..
+// kFwdGroup g + kFwdGroup - 1): one past the group, more than kFwdDirect
+// past its anchor, in the same anchor window, before NSEG.
+__host__ __device__ constexpr bool fwd_group_read(int g, int nseg) {
+  return (g * kFwdGroup + kFwdGroup > (g * kFwdGroup / kFwdAnchor) * kFwdAnchor + kFwdDirect + 1
+              ? g * kFwdGroup + kFwdGroup
+              : (g * kFwdGroup / kFwdAnchor) * kFwdAnchor + kFwdDirect + 1) <= nseg - 1;
+}
+
 inline FwdLayout fwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) {
   FwdLayout w;
   w.NC = int((L + chunk - 1) / chunk);
@@ -473,7 +495,8 @@ inline FwdLayout fwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t 
   w.n_saved = 4 * B * L * H;
   w.n_gsaved = B * L * H;
   w.NSEG = (w.NC + kOnePassW - 1) / kOnePassW;
-  w.n_op = B * w.NSEG * H * (2 * D + 2) + kCtlWords;
+  // maps, leaving states, rotations, flags, the control block, then the group maps of the two-level fold
+  w.n_op = B * w.NSEG * H * (2 * D + 2) + kCtlWords + B * int64_t(fwd_groups(w.NSEG)) * H * (D + 1);
   // checkpoints at t = 0, kZck, ... < round_up(chunk, kTokRound)
   w.NCK = int((chunk + kTokRound - 1) / kTokRound * kTokRound / kZck);
   w.n_zck = B * w.NC * H * int64_t(w.NCK) * D;
@@ -544,6 +567,9 @@ struct OnePassBufs {
   float2* seg_g;             // (B, NSEG, H)    segment rotation product
   unsigned long long* flag;  // (B, NSEG, H); entry hbase serves the head group
   unsigned long long* ctl;   // kCtlWords words; ctl[0] = epoch of the running call
+  // forward only (two-level fold): (B, NGRP, H, D) group map F and (B, NGRP, H) its rotation product
+  float2* grp_f = nullptr;
+  float2* grp_g = nullptr;
 };
 
 // Epoch words: the pass's tag in bits 58..59 (so epochs of different passes

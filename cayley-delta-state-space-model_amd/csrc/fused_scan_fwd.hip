@@ -914,12 +914,18 @@ __global__ __launch_bounds__(kWave) void fused_fwd_corr_sweep_kernel(
 //      (rescaled frame) over the k rows, keeping each step's update
 //      coefficient in LDS; its chunk map is (G_k, F_k = z_{Q-1});
 //   2. the segment's chunk maps are composed through LDS into the segment
-//      map, which is published.  The state entering the segment is the
-//      composition, oldest first, of the maps of the segments since its
-//      anchor (segment kAnchor * floor((seg - 1) / kAnchor)) applied to the
-//      anchor state (h0, or the published state leaving the segment before the
-//      anchor): a fixed order, so the results do not depend on timing.  Anchor
-//      ends publish their leaving state for the next kAnchor segments;
+//      map, which is published.  Every kFwdGroup-th segment (a group end)
+//      then composes and publishes its group's map from the maps of the
+//      group's segments.  The state entering a segment is the composition,
+//      oldest first, of the maps of the whole groups since its anchor
+//      (segment kFwdAnchor * floor((seg - 1) / kFwdAnchor)) and then of its
+//      own group's earlier segments, applied to the anchor state (h0, or the
+//      published state leaving the segment before the anchor): a fixed order,
+//      so the results do not depend on timing, and at most
+//      kFwdAnchor / kFwdGroup + kFwdGroup - 1 maps read per segment (the fold
+//      reads published maps from the device-coherent level; one level over
+//      62 maps made that read the bound at 1024 chunks).  Anchor ends publish
+//      their leaving state for the next kFwdAnchor segments;
 //   3. each wave derives the state entering its chunk and runs the decay-free
 //      correction, replaying the local state from the stored coefficients,
 //      with the full readout f_t (zh_t.q_t) + g_{t-1} (c^_t.q_t) reduced once;
@@ -927,7 +933,7 @@ __global__ __launch_bounds__(kWave) void fused_fwd_corr_sweep_kernel(
 // SAVE (training forward) also writes what the backward reads: the state
 // entering every chunk and G_k (the four-launch layout), the per-token records
 // (p_t, pc_t), (c^_{t+1}.q_t, Y_t.q_t) and g_t, as the main pass does.
-// Flags hold epoch << 2 | state (1: map, 2: map and leaving state) with a
+// Flags hold epoch << 3 | bits (kFlagMap, kFlagLeave, kFlagGroup) with a
 // per-call epoch read from the look-back area's control block, where
 // fwd_epoch_kernel (launched just before, on the same stream) writes it from a
 // device-side counter; so the workspace needs no clearing between calls and a
@@ -944,6 +950,31 @@ __global__ __launch_bounds__(kWave) void fused_fwd_corr_sweep_kernel(
 // turns a missing flag into NaN output instead of a hang, and sets the
 // kTimeoutFwd bit of the sticky status word g_fwd_status.
 // ---------------------------------------------------------------------------
+// Look-back flag bits of the one-pass forward (below the epoch, flag = epoch << 3 | bits).
+constexpr unsigned long long kFlagMap = 1ull;    // segment map published
+constexpr unsigned long long kFlagLeave = 2ull;  // state leaving the segment published (anchor ends)
+constexpr unsigned long long kFlagGroup = 4ull;  // group map published (group ends)
+
+// Wave-wide wait: lane i watches the flag of segment js (>= 0; -1: nothing)
+// of the head group's flags f0 (stride H per segment) until it carries this
+// call's epoch and the bits `need`.  True once every lane's flag does; false
+// when the wait bound passes first.  Wave-uniform.
+__device__ __forceinline__ bool watch_flags(const unsigned long long* f0, int H, unsigned long long epoch, int js,
+                                            unsigned long long need) {
+  const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
+  for (;;) {
+    bool ready = true;
+    if (js >= 0) {
+      const unsigned long long fv = __hip_atomic_load(const_cast<unsigned long long*>(f0 + int64_t(js) * H),
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ready = (fv >> 3) == epoch && (fv & need) == need;
+    }
+    if (__builtin_amdgcn_ballot_w64(!ready) == 0ull) return true;
+    if (__builtin_amdgcn_s_memrealtime() - t_start > kSpinTicks) return false;
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
 template <typename T>
 struct OnePassArgs {
   const typename T::raw *q, *k, *v, *beta, *sel_c, *dt, *r;
@@ -1189,49 +1220,116 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   const int64_t sb0 = (int64_t(bi) * NSEG + seg) * H;  // (b, seg, head 0)
   unsigned long long* flag = ob.flag + sb0 + hbase;
 
-  // publish the segment map (every segment: later ones fold it in)
+  // publish the segment map (every segment: later ones fold it in).  Flag
+  // words are epoch << 3 | bits: kFlagMap the segment map, kFlagLeave the
+  // state leaving the segment (anchor ends), kFlagGroup its group's map
+  // (group ends); thread 0 stores the word with every bit published so far.
+  // A group end whose group map some later segment reads flags its own map
+  // together with the group map (one store acknowledgement, one flag): it
+  // waits only on lower segments' maps, which never wait on it.
   if (ehok) {
 #pragma unroll
     for (int i = 0; i < EPT; ++i) st_agent(ob.seg_f + (sb0 + eh) * D + ed + i, segF[i]);
     if (ed == 0) st_agent(ob.seg_g + sb0 + eh, segG);
   }
-  wait_stores_acked();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __hip_atomic_store(flag, (epoch << 2) | 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (arrive) arrive_and_draw_next_epoch(ob.ctl, &g_fwd_calls, 1u);
+  const bool gend = seg % kFwdGroup == kFwdGroup - 1 && fwd_group_read(seg / kFwdGroup, NSEG);
+  unsigned long long bits = kFlagMap;
+  if (!gend) {
+    wait_stores_acked();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      __hip_atomic_store(flag, (epoch << 3) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (arrive) arrive_and_draw_next_epoch(ob.ctl, &g_fwd_calls, 1u);
+    }
   }
 
   stamp(3);
+  const unsigned long long* f0 = ob.flag + (int64_t(bi) * NSEG) * H + hbase;  // (b, segment 0, head group)
+  const int64_t lb = int64_t(bi) * NSEG * H + eh;                            // (b, segment 0, head eh)
+  const int ngrp_all = fwd_groups(NSEG);
+  // a group end (the last segment of a group some later segment folds)
+  // composes its group's map, oldest first: the maps its group's other
+  // segments published, then its own
+  if (gend) {
+    const int s0 = seg - (kFwdGroup - 1);
+    if (wv == 0) {
+      const bool got = watch_flags(f0, H, epoch, lane < kFwdGroup - 1 ? s0 + lane : -1, kFlagMap);
+      if (lane == 0) {
+        ctrl[0] = got;
+        if (!got) __hip_atomic_fetch_or(&g_fwd_status, kTimeoutFwd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __syncthreads();
+    const int okg = ctrl[0];
+    if (ehok) {
+      float2 G[kFwdGroup - 1], F[kFwdGroup - 1][EPT];
+#pragma unroll
+      for (int u = 0; u < kFwdGroup - 1; ++u) {
+        G[u] = ld_agent(ob.seg_g + lb + int64_t(s0 + u) * H);
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) F[u][i] = ld_agent(ob.seg_f + (lb + int64_t(s0 + u) * H) * D + ed + i);
+      }
+      float2 Gg = make_float2(1.0f, 0.0f), Fg[EPT];
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) Fg[i] = make_float2(0.0f, 0.0f);
+#pragma unroll
+      for (int u = 0; u < kFwdGroup; ++u) {
+        const float2 gu = u < kFwdGroup - 1 ? G[u] : segG;
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+          const float2 f = u < kFwdGroup - 1 ? F[u][i] : segF[i];
+          Fg[i] = make_float2(gu.x * Fg[i].x - gu.y * Fg[i].y + f.x, gu.x * Fg[i].y + gu.y * Fg[i].x + f.y);
+        }
+        Gg = make_float2(gu.x * Gg.x - gu.y * Gg.y, gu.x * Gg.y + gu.y * Gg.x);
+      }
+      if (!okg) {
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) Fg[i] = make_float2(__builtin_nanf(""), __builtin_nanf(""));
+      }
+      const int64_t gb = (int64_t(bi) * ngrp_all + seg / kFwdGroup) * H + eh;
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) st_agent(ob.grp_f + gb * D + ed + i, Fg[i]);
+      if (ed == 0) st_agent(ob.grp_g + gb, Gg);
+    }
+    wait_stores_acked();  // the segment map and the group map
+    __syncthreads();
+    bits |= kFlagGroup;
+    if (threadIdx.x == 0) {
+      __hip_atomic_store(flag, (epoch << 3) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (arrive) arrive_and_draw_next_epoch(ob.ctl, &g_fwd_calls, 1u);
+    }
+  }
+
   // state entering the segment, in a fixed order (so results do not depend on
-  // timing): from the anchor a = kAnchor * floor((seg - 1) / kAnchor) -- h0
-  // for a = 0, else the published state leaving segment a - 1 -- fold the
-  // maps of segments a .. seg - 1, oldest first.  Wave 0 waits until they are
-  // published (lane i: map of segment a + i; lane 63: the anchor state).
-  const int anc = seg == 0 ? 0 : kAnchor * ((seg - 1) / kAnchor);
-  const int nmap = seg - anc;
+  // timing): from the anchor a = kFwdAnchor * floor((seg - 1) / kFwdAnchor)
+  // -- h0 for a = 0, else the published state leaving segment a - 1 -- fold
+  // the maps of the segments a .. seg - 1 where there are at most kFwdDirect
+  // of them, else the maps of the whole groups in [a, seg) and then those of
+  // the segments of seg's own group before it; oldest first.  Wave 0 waits
+  // until they are published (lanes 0 .. ngrp-1: group maps; then the segment
+  // maps; lane 63: the anchor state).
+  const int anc = seg == 0 ? 0 : kFwdAnchor * ((seg - 1) / kFwdAnchor);
+  const bool direct = seg - anc <= kFwdDirect;
+  const int g0 = anc / kFwdGroup, g1 = direct ? g0 : seg / kFwdGroup;
+  const int ngrp = g1 - g0;                  // <= kFwdAnchor / kFwdGroup
+  const int sg0 = g1 * kFwdGroup;            // first segment folded one by one
+  const int nmap = seg - sg0;                // <= kFwdDirect
   int ok = 1;
   if (seg > 0) {
     if (wv == 0) {
-      const unsigned long long* f0 = ob.flag + (int64_t(bi) * NSEG) * H + hbase;
-      int got = 0;
-      const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
-      for (;;) {
-        int st = 3;  // lanes with nothing to watch count as ready
-        const int js = lane < nmap ? anc + lane : (lane == kWave - 1 && anc > 0 ? anc - 1 : -1);
-        if (js >= 0) {
-          const unsigned long long fv = __hip_atomic_load(const_cast<unsigned long long*>(f0 + int64_t(js) * H),
-                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          st = (fv >> 2) == epoch ? int(fv & 3ull) : 0;
-        }
-        const bool ready = lane < nmap ? st >= 1 : (lane == kWave - 1 && anc > 0 ? st == 2 : true);
-        if (__builtin_amdgcn_ballot_w64(!ready) == 0ull) {
-          got = 1;
-          break;
-        }
-        if (__builtin_amdgcn_s_memrealtime() - t_start > kSpinTicks) break;
-        __builtin_amdgcn_s_sleep(2);
+      int js = -1;
+      unsigned long long need = 0ull;
+      if (lane < ngrp) {
+        js = (g0 + lane) * kFwdGroup + kFwdGroup - 1;
+        need = kFlagGroup;
+      } else if (lane < ngrp + nmap) {
+        js = sg0 + lane - ngrp;
+        need = kFlagMap;
+      } else if (lane == kWave - 1 && anc > 0) {
+        js = anc - 1;
+        need = kFlagLeave;
       }
+      const bool got = watch_flags(f0, H, epoch, js, need);
       if (lane == 0) {
         ctrl[0] = got;
         if (!got) __hip_atomic_fetch_or(&g_fwd_status, kTimeoutFwd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1245,7 +1343,6 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
 #pragma unroll
   for (int i = 0; i < EPT; ++i) Sin[i] = make_float2(0.0f, 0.0f);
   if (ehok) {
-    const int64_t lb = int64_t(bi) * NSEG * H + eh;  // (b, segment 0, head eh)
     if (anc == 0) {
       if (h0) {
         const int64_t hb = (int64_t(bi) * H + eh) * 2 * D;
@@ -1256,23 +1353,31 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
 #pragma unroll
       for (int i = 0; i < EPT; ++i) Sin[i] = ld_agent(ob.seg_s + (lb + int64_t(anc - 1) * H) * D + ed + i);
     }
-    for (int jb = 0; jb < nmap; jb += kLookbackBatch) {
-      float2 G[kLookbackBatch], F[kLookbackBatch][EPT];
+    // at most max(kFwdDirect, kFwdAnchor / kFwdGroup + kFwdGroup - 1) maps, all requested at once
+    constexpr int kMaps = kFwdDirect > kFwdAnchor / kFwdGroup + kFwdGroup - 1 ? kFwdDirect
+                                                                            : kFwdAnchor / kFwdGroup + kFwdGroup - 1;
+    float2 G[kMaps], F[kMaps][EPT];
 #pragma unroll
-      for (int u = 0; u < kLookbackBatch; ++u) {
-        const int js = anc + min(jb + u, nmap - 1);
-        G[u] = ld_agent(ob.seg_g + lb + int64_t(js) * H);
+    for (int u = 0; u < kMaps; ++u) {
+      if (u < ngrp) {
+        const int64_t gb = (int64_t(bi) * ngrp_all + g0 + u) * H + eh;
+        G[u] = ld_agent(ob.grp_g + gb);
 #pragma unroll
-        for (int i = 0; i < EPT; ++i) F[u][i] = ld_agent(ob.seg_f + (lb + int64_t(js) * H) * D + ed + i);
+        for (int i = 0; i < EPT; ++i) F[u][i] = ld_agent(ob.grp_f + gb * D + ed + i);
+      } else if (u < ngrp + nmap) {
+        const int64_t sb = lb + int64_t(sg0 + u - ngrp) * H;
+        G[u] = ld_agent(ob.seg_g + sb);
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) F[u][i] = ld_agent(ob.seg_f + sb * D + ed + i);
       }
+    }
 #pragma unroll
-      for (int u = 0; u < kLookbackBatch; ++u) {
-        if (jb + u < nmap) {
+    for (int u = 0; u < kMaps; ++u) {
+      if (u < ngrp + nmap) {
 #pragma unroll
-          for (int i = 0; i < EPT; ++i)
-            Sin[i] = make_float2(G[u].x * Sin[i].x - G[u].y * Sin[i].y + F[u][i].x,
-                                 G[u].x * Sin[i].y + G[u].y * Sin[i].x + F[u][i].y);
-        }
+        for (int i = 0; i < EPT; ++i)
+          Sin[i] = make_float2(G[u].x * Sin[i].x - G[u].y * Sin[i].y + F[u][i].x,
+                               G[u].x * Sin[i].y + G[u].y * Sin[i].x + F[u][i].y);
       }
     }
     if (!ok) {
@@ -1281,8 +1386,8 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
     }
   }
   // the state leaving the segment: h_final for the last segment; published
-  // for the segments that start from it (anchor ends, (seg + 1) % kAnchor == 0)
-  const bool anchor_end = seg + 1 < NSEG && (seg + 1) % kAnchor == 0;
+  // for the segments that start from it (anchor ends, (seg + 1) % kFwdAnchor == 0)
+  const bool anchor_end = seg + 1 < NSEG && (seg + 1) % kFwdAnchor == 0;
 #pragma unroll
   for (int i = 0; i < EPT; ++i) Sx[e0 + i] = Sin[i];
   if (ehok && (anchor_end || seg + 1 == NSEG)) {
@@ -1302,7 +1407,7 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   if (anchor_end) wait_stores_acked();
   __syncthreads();
   if (anchor_end && threadIdx.x == 0)
-    __hip_atomic_store(flag, (epoch << 2) | 2ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(flag, (epoch << 3) | bits | kFlagLeave, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   stamp(5);
   // 3. state entering this wave's chunk, then the correction with the readout
@@ -1650,6 +1755,8 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
       a.h_final = h_final;
       unsigned long long* flags = reinterpret_cast<unsigned long long*>(base + 2 * nsd + nsh);
       a.ob = OnePassBufs{base, base + nsd, base + 2 * nsd, flags, flags + nsh};
+      a.ob.grp_f = reinterpret_cast<float2*>(flags + nsh + kCtlWords);
+      a.ob.grp_g = a.ob.grp_f + int64_t(B) * fwd_groups(w.NSEG) * H * D;
       a.states = save ? summ : nullptr;
       a.gam = save ? gam : nullptr;
       a.saved = save ? saved : nullptr;

@@ -188,8 +188,9 @@ def test_one_launch_areas_have_a_control_block_for_the_device_epoch():
     NSEG = -(-NC // 4)
     NCK = -(-Q // 8) * 8 // 8
     carry = B * NC * H * D + B * NC * H + B * H * S * (D + 1)
-    fwd = (carry + (carry & 1) + 5 * B * L * H + B * NSEG * H * (2 * D + 2) + 8 + B * NC * H * NCK * D
-           + B * NC * H * D + B * L * H)
+    NGRP = -(-NSEG // 8)  # groups of 8 segments of the two-level fold
+    fwd = (carry + (carry & 1) + 5 * B * L * H + B * NSEG * H * (2 * D + 2) + 8 + B * NGRP * H * (D + 1)
+           + B * NC * H * NCK * D + B * NC * H * D + B * L * H)
     assert lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, 2, Q) == 8 * fwd
     bwd = 2 * B * NC * H * D + B * H * S + B * H * S * D + B * NC * H + B * NSEG * H * (2 * D + 2) + 8
     assert lib.cdssm_fused_scan_bwd_workspace_bytes(B, L, H, D, 2, Q) == 8 * bwd
@@ -236,7 +237,9 @@ def test_workspace_size_formula():
         saved = 4 * B * L * H         # (p, pc), (c.q, Y.q) per token-head: 2 float4
         gsaved = B * L * H            # g_t per token-head: float2
         NSEG = -(-NC // 4)            # one-pass look-back segments of 4 chunks
-        onepass = B * NSEG * H * (2 * D + 2) + 8   # maps, leaving states, rotations, flags, control block
+        NGRP = -(-NSEG // 8)          # groups of 8 segments (the two-level look-back fold)
+        # maps, leaving states, rotations, flags, control block; group maps and their rotations
+        onepass = B * NSEG * H * (2 * D + 2) + 8 + B * NGRP * H * (D + 1)
         NCK = -(-Q // 8) * 8 // 8     # z checkpoints per chunk (every 8 tokens of the 8-rounded loop)
         zck = B * NC * H * NCK * D
         cend = B * NC * H * D         # correction state after each chunk

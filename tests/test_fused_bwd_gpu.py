@@ -209,7 +209,9 @@ def test_one_pass_training_forward_writes_the_four_launch_records():
     carry = n_states + n_gam + B * H * S * (D + 1)
     off_saved = carry + (carry & 1)
     NSEG, NCK = -(-NC // 4), -(-Q // 8) * 8 // 8
-    off_zck = off_saved + 5 * B * L * H + B * NSEG * H * (2 * D + 2) + 8  # look-back area + control block
+    NGRP = -(-NSEG // 8)  # group maps of the two-level look-back fold
+    # look-back area, control block, group maps
+    off_zck = off_saved + 5 * B * L * H + B * NSEG * H * (2 * D + 2) + 8 + B * NGRP * H * (D + 1)
     n_zck = B * NC * H * NCK * D
     regions = {"states": (0, n_states), "gam": (n_states, n_states + n_gam),
                "saved": (off_saved, off_saved + 4 * B * L * H),
