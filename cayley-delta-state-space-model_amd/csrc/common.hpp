@@ -638,6 +638,8 @@ int bwd_lookback_status(bool clear, unsigned* out);
 // Workgroups of kernel `fn` (block threads, lds bytes of dynamic LDS) resident
 // on the current device at once; 0 if it cannot run.  Cached.
 int resident_capacity(const void* fn, int block, size_t lds);
+// Compute units of the current device (0 if it cannot be read).  Cached.
+int device_cus();
 // Launch-path selection of the fused scan (forward and backward carry):
 // automatic, always the multi-launch passes, or one launch required.
 // kPathSweep: the four launches with the correction as the chunked MFMA pass

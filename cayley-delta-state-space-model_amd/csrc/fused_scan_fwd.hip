@@ -1660,6 +1660,17 @@ FwdRegions infer_regions(float2* base, const FwdLayout& w) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The bf16 D = 64 forward runs 8 heads per wave (8 lanes per head).  Where the
+// one-pass grid that gives (segments x batch x head groups) has fewer
+// workgroups than the device has CUs, CUs sit idle for the whole call; 4 heads
+// per wave (16 lanes per head) doubles the workgroups (measured on MI355X at
+// config 4's B8 L2048 H16: 128 -> 256 workgroups).
+bool fill_with_4_heads_per_wave(int64_t B, int64_t L, int64_t H, int64_t chunk) {
+  const int64_t nc = (L + chunk - 1) / chunk, nseg = (nc + kOnePassW - 1) / kOnePassW;
+  const int64_t items = nseg * B * ((H + 7) / 8);
+  return H > 4 && items < cdssm_host::device_cus();
+}
+
 // Phase-stamp buffer of the running cdssm_fused_scan_fwd_stamped call on this
 // host thread (instrumentation only): device memory of `len` 8-byte words.
 struct StampRequest {
@@ -2077,6 +2088,8 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
       return CDSSM_EINVAL;
     }
     if (dtype == 1) {
+      if (D == 64 && fill_with_4_heads_per_wave(B, L, H, chunk))
+        return launch_fused_fwd<ABar<BF16>, 64, 16, CDSSM_FWD_LPHS_BF16_D64>(CDSSM_FWD_ARGS);
       if (D == 64)
         return launch_fused_fwd<ABar<BF16>, 64, CDSSM_FWD_LPH_BF16_D64, CDSSM_FWD_LPHS_BF16_D64>(CDSSM_FWD_ARGS);
       return launch_fused_fwd<ABar<BF16>, 128, 16, CDSSM_FWD_LPHS_BF16_D128>(CDSSM_FWD_ARGS);
@@ -2085,6 +2098,10 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
     return launch_fused_fwd<ABar<F32>, 128, 32, 32>(CDSSM_FWD_ARGS);
   }
   if (dtype == 1) {
+    // the training forward takes the same layout as the inference forward of the
+    // shape (its workspace does not depend on it), so the two stay bit-identical
+    if (D == 64 && fill_with_4_heads_per_wave(B, L, H, chunk))
+      return launch_fused_fwd<BF16, 64, 16, CDSSM_FWD_LPHS_BF16_D64>(CDSSM_FWD_ARGS);
     if (D == 64)
       return launch_fused_fwd<BF16, 64, CDSSM_FWD_LPH_BF16_D64, CDSSM_FWD_LPHS_BF16_D64>(CDSSM_FWD_ARGS);
     return launch_fused_fwd<BF16, 128, 16, CDSSM_FWD_LPHS_BF16_D128>(CDSSM_FWD_ARGS);

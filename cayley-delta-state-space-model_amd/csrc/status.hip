@@ -59,6 +59,23 @@ int resident_capacity(const void* fn, int block, size_t lds) {
   return capacity;
 }
 
+int device_cus() {
+  int dev = 0, n_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  static std::atomic<int> cache[64];
+  const int c = cache[dev].load(std::memory_order_relaxed);
+  if (c > 0) return c;
+  if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  cache[dev].store(n_cu, std::memory_order_relaxed);
+  return n_cu;
+}
+
 namespace {
 std::atomic<int> g_scan_path{kPathAuto};
 }

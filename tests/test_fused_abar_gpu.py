@@ -24,6 +24,8 @@ CASES = [
     ("bf16_D64", ScanConfig("t", B=2, H=16, L=640, D=64), None),
     ("bf16_D128_fast_omega", ScanConfig("t", B=1, H=9, L=333, D=128, omega_std=3.0, h0_std=0.1), None),
     ("bf16_C1_shape", ScanConfig("C1", B=8, H=16, L=4096, D=64), None),
+    # config 4's gate-level scan: 128 one-pass workgroups at 8 heads per wave, so it runs 4 per wave
+    ("bf16_C4_shape", ScanConfig("C4", B=8, H=16, L=2048, D=64), None),
 ]
 
 
