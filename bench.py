@@ -42,17 +42,35 @@ TRAFFIC_FILES = {
 }
 
 
-def recorded_traffic(path):
-    """Bytes per launch from a committed counter summary
-    (`traffic_bytes_per_launch: N` line), or None."""
+def recorded_traffic(path, key="traffic_bytes_per_launch"):
+    """A number recorded in a committed counter summary (a `key: N` line), or None."""
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith(key + ":"):
                     return float(line.split(":", 1)[1])
     except OSError:
         return None
     return None
+
+
+FWD_BWD_TRAFFIC = os.path.join(ROOT, "profiles", "fused_fwd_bwd_C1_C2_hbm_traffic.txt")
+MFMA_PROFILE = os.path.join(ROOT, "profiles", "fused_fwd_onepass_C1_sq_counters.md")
+MFMA_VARIANT_PROFILE = os.path.join(ROOT, "profiles", "mfma_correction_vs_sequential_C1_C2.md")
+
+
+def mfma_util(kernel):
+    """MFMA utilisation of the forward kernel the bench times, from committed SQ counters (rocprofv3 cannot
+    run inside this process): MFMA FLOPs / kernel time / 2.5 PFLOP/s dense bf16, with the path named.  The
+    chunked MFMA correction (not the default) is quoted beside it."""
+    return {"path": kernel + " (sequential correction: no MFMA instructions)"
+            if kernel == "fused_fwd_onepass_kernel" else kernel,
+            "value": recorded_traffic(MFMA_PROFILE, "mfma_util"),
+            "mfma_insts_per_wave": recorded_traffic(MFMA_PROFILE, "mfma_insts_per_wave"),
+            "source": os.path.relpath(MFMA_PROFILE, ROOT),
+            "chunked_mfma_correction": {"path": "four_launch_mfma (fused_fwd_corr_sweep_kernel, not default)",
+                                        "value": recorded_traffic(MFMA_VARIANT_PROFILE, "mfma_util_C1"),
+                                        "source": os.path.relpath(MFMA_VARIANT_PROFILE, ROOT)}}
 
 
 def parse():
@@ -91,10 +109,11 @@ def copy_probe(mib):
     print(json.dumps({"copy_probe_bytes_read_per_call": n * 4, "bytes_written_per_call": n * 4, "calls": 10}))
 
 
-def phase_stamps(cfg_name, calls, warmup):
-    """Per-wave phase durations of the one-pass forward kernel, from the real-time
-    counter (100 MHz) that the stamped entry records at eight points of each wave's
-    segment.  Percentiles over every wave of `calls` stamped calls, in microseconds."""
+def _stamp_rows(cfg_name, calls, warmup):
+    """Per-wave phase durations (waves x 7, microseconds) of `calls` stamped one-pass
+    forwards of the configuration, the waves' entry offsets from the first, and each
+    call's kernel span.  The stamped entry records the 100 MHz real-time counter at
+    eight points of each wave's segment (PreparedForward.STAMP_POINTS)."""
     import torch
     from cdssm_hip.scan import PreparedForward
     from cdssm_hip.workloads import CONFIGS, draw_inputs
@@ -109,7 +128,6 @@ def phase_stamps(cfg_name, calls, warmup):
         run()
     torch.cuda.synchronize()
     us = 0.01  # microseconds per tick
-    pts = PreparedForward.STAMP_POINTS
     rows, spans, starts = [], [], []
     for _ in range(calls):
         st = run.phase_stamps().double()
@@ -117,19 +135,48 @@ def phase_stamps(cfg_name, calls, warmup):
         spans.append(float(st[:, 7].max() - t0) * us)
         starts.append((st[:, 0] - t0) * us)
         rows.append((st[:, 1:] - st[:, :-1]) * us)
-    d = torch.cat(rows)
-    start = torch.cat(starts)
-    qs = torch.tensor([0.1, 0.5, 0.9], dtype=torch.float64)
+    del run, g
+    torch.cuda.synchronize()
+    return torch.cat(rows), torch.cat(starts), spans
 
-    def pct(t):
-        return [round(float(v), 2) for v in torch.quantile(t, qs)]
 
-    phases = {f"{pts[i]}->{pts[i + 1]}": pct(d[:, i]) for i in range(len(pts) - 1)}
-    phases["entry offset"] = pct(start)
-    phases["wave total"] = pct(d.sum(dim=1))
+def _pct(t):
+    import torch
+    return [round(float(v), 2) for v in torch.quantile(t, torch.tensor([0.1, 0.5, 0.9], dtype=torch.float64))]
+
+
+def phase_stamps(cfg_name, calls, warmup):
+    """Per-wave phase durations of the one-pass forward kernel: percentiles over every
+    wave of `calls` stamped calls, in microseconds."""
+    from cdssm_hip.scan import PreparedForward
+    d, start, spans = _stamp_rows(cfg_name, calls, warmup)
+    pts = PreparedForward.STAMP_POINTS
+    phases = {f"{pts[i]}->{pts[i + 1]}": _pct(d[:, i]) for i in range(len(pts) - 1)}
+    phases["entry offset"] = _pct(start)
+    phases["wave total"] = _pct(d.sum(dim=1))
     return {"phase_stamps": {"config": cfg_name, "calls": calls, "waves_per_call": int(d.shape[0] // calls),
                              "unit": "us (p10, p50, p90 over waves)", "phases": phases,
                              "kernel_span_us_median": round(statistics.median(spans), 2)}}
+
+
+def interchunk_share(cfg_name="C3", calls=3, warmup=3):
+    """The inter-chunk part of the default (one-pass) forward's time, from live phase stamps: per wave,
+    (segment map composed and published + look-back wait + carry fold) / the wave's whole segment.  This
+    is the work the reference does in its serial inter-chunk pass (inter_chunk_scan.cu:52-84)."""
+    d, _, spans = _stamp_rows(cfg_name, calls, warmup)
+    inter = d[:, 2] + d[:, 3] + d[:, 4]   # local->published, published->waited, waited->folded
+    total = d.sum(dim=1)
+    med = [float(d[:, i].median()) for i in (2, 3, 4)]
+    return {"config": cfg_name, "path": "one-pass forward (persistent at C3)", "calls": calls,
+            "waves": int(d.shape[0]),
+            "share": sum(med) / float(total.median()),
+            "share_per_wave_p10_p50_p90": _pct(inter / total),
+            "median_us": {"compose_publish": round(med[0], 2), "lookback_wait": round(med[1], 2),
+                          "fold": round(med[2], 2), "wave_total": round(float(total.median()), 2)},
+            "kernel_span_us_median": round(statistics.median(spans), 2),
+            "target": "< 0.15",
+            "basis": "share = (median compose+publish + median wait + median fold) / median wave total, "
+                     "from the stamped entry (cdssm_fused_scan_fwd_stamped) on this run"}
 
 
 def time_fwd_bwd(cfg_name, steps, warmup):
@@ -193,7 +240,11 @@ def time_fwd_bwd(cfg_name, steps, warmup):
                            "per token-head at D 64 bf16); stored_record_bytes: what the training forward writes "
                            "for the backward (per-token records, z every 8 tokens, chunk entering states, c^ at "
                            "chunk ends), counted twice (written, read back) in hbm_frac_with_records"),
-            "phase_ms": phases}
+            "phase_ms": phases,
+            "traffic_bytes": recorded_traffic(FWD_BWD_TRAFFIC, f"traffic_bytes_per_step_{cfg.name}"),
+            "traffic_over_alg": (lambda t: None if t is None else t / alg)(
+                recorded_traffic(FWD_BWD_TRAFFIC, f"traffic_bytes_per_step_{cfg.name}")),
+            "traffic_source": os.path.relpath(FWD_BWD_TRAFFIC, ROOT)}
 
 
 def training_record_bytes(cfg):
@@ -685,6 +736,9 @@ def main():
         "cold_frac": alg / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "wall_s_timed": wall,
     }
+    out["mfma_util"] = mfma_util(kernel)
+    if not args.no_extras:
+        out["c3_interchunk"] = interchunk_share()
     if not args.no_fwd_bwd:
         out["fwd_bwd"] = [time_fwd_bwd(n, 20, 3) for n in ("C1", "C2")]
         if not args.no_extras:
