@@ -553,6 +553,53 @@ def time_lm_forward(steps=5, warmup=2):
                     "GroupNorm + gate on the HIP kernels"}
 
 
+def time_block_train(steps=5, warmup=2, B=8, L=2048):
+    """One training step through one CDSSMBlock at config 4's shape (d_model 1024, 16 heads x 64,
+    d_inner 1024, state_dim 2, bf16; B8 L2048): forward and backward of sum(out * g), the way the
+    reference trains (block.py:140-229 under autograd, trainer.py:235-247).  Timed with the readout-form
+    scan (no (B,L,H,2,D) Y) and with SSDChunkwiseScan's Y read out in torch, the reference's op sequence."""
+    import torch
+    from cdssm_hip.lm import CDSSMBlock, CDSSMConfig
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    cfg = CDSSMConfig(d_model=1024, n_layers=24, context_length=2048, vocab_size=32000, state_dim=2, d_inner=1024)
+    blk = CDSSMBlock(cfg, 0).to(torch.bfloat16).to(dev).train()
+    gen = torch.Generator().manual_seed(1)
+    x = torch.randn(B, L, cfg.d_model, generator=gen).to(torch.bfloat16).to(dev).requires_grad_(True)
+    g = torch.randn(B, L, cfg.d_model, generator=gen).to(torch.bfloat16).to(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        out, _ = blk(x)
+        out.backward(g)
+
+    res = {}
+    prev = CDSSMBlock.readout_scan
+    try:
+        for name, flag in (("readout_scan", True), ("ssd_y_readout", False)):
+            CDSSMBlock.readout_scan = flag
+            for _ in range(warmup):
+                step()
+            torch.cuda.synchronize()
+            torch.cuda.reset_peak_memory_stats(dev)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(steps):
+                step()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / steps
+            res[name] = {"ms_per_step": ms, "tokens_per_s": B * L / (ms * 1e-3),
+                         "peak_mem_GB": torch.cuda.max_memory_allocated(dev) / 1e9}
+    finally:
+        CDSSMBlock.readout_scan = prev
+    return {"workload": "one CDSSMBlock training step (forward + backward), config 4 shape B8 L2048 d_model 1024 "
+                        "16x64 heads N=2 bf16", **res,
+            "note": "readout_scan: ChunkwiseDeltaScanAbarFn (cdssm_fused_scan_fwd_abar_train / cdssm_fused_scan_bwd_abar); "
+                    "ssd_y_readout: SSDChunkwiseScan's (B,L,H,2,D) Y read out in torch"}
+
+
 def host_cores():
     """Cores this process may run on (the GPU box gives a job a share of the host)."""
     try:
@@ -744,6 +791,7 @@ def main():
         if not args.no_extras:
             out["decode"] = time_decode(200, 20)
             out["lm_forward"] = time_lm_forward()
+            out["block_train"] = time_block_train()
             out["lm_decode"] = time_lm_decode()
     if not args.no_extras:
         out["dropin_ssd_scan"] = time_dropin("C1")

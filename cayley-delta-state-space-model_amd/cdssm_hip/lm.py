@@ -11,9 +11,11 @@ readout_proj -> fp32 GroupNorm, * silu(z), + D x (HIP) -> out_proj with the
 residual in the GEMM epilogue.  Dense projections and the embedding are
 PyTorch (hipBLASLt GEMMs).  With gradients enabled (training) the block takes a
 differentiable path instead: conv1d+SiLU, DynamicsFusedFn, NormalizeKQFn and
-SSDChunkwiseScan (the fused scan kernels in their Y-materialising form, HIP,
-with the reference's backward rules) and torch for the rest.  With state_dim
-N != 2 the inference forward also materialises Y through SSDChunkwiseScan.
+the fused scan (HIP, with the reference's backward rules: for state_dim 2 the
+gate-level readout form ChunkwiseDeltaScanAbarFn, which never forms the
+(B,L,H,2,D) Y; otherwise SSDChunkwiseScan) and torch for the rest.  With
+state_dim N != 2 the inference forward also materialises Y through
+SSDChunkwiseScan.
 
 Generation: ``CDSSMLMHeadModel.prefill`` runs the forward over a prompt and keeps
 per-layer decode state (conv window, the scan's R-mode state, GroupNorm running
@@ -33,7 +35,7 @@ import torch.nn as nn
 from . import _lib
 from .ops import DynamicsFusedFn, NormalizeKQFn
 from .decode import DecodeState, decode_step_abar, prefill_abar
-from .scan import chunkwise_delta_scan_abar
+from .scan import ChunkwiseDeltaScanAbarFn, chunkwise_delta_scan_abar
 from .ssd import SSDChunkwiseScan
 
 Tensor = torch.Tensor
@@ -498,6 +500,9 @@ class CDSSMBlock(nn.Module):
     # decode steps take the one-launch token kernel (cdssm_decode_block_token) where its alignment holds;
     # False: the separate per-token kernels (the same values)
     fused_step: bool = True
+    # training with state_dim 2 takes the readout-form scan (ChunkwiseDeltaScanAbarFn, no Y); False:
+    # SSDChunkwiseScan's Y read out in torch (the reference's op sequence; the same gradients)
+    readout_scan: bool = True
 
     def __init__(self, config: CDSSMConfig, layer_idx: int = 0):
         super().__init__()
@@ -647,11 +652,12 @@ class CDSSMBlock(nn.Module):
 
     def _forward_autograd(self, x: Tensor, v_first: Optional[Tensor]):
         """The block with gradients (block.py:140-229, for training): the HIP ops that have a backward --
-        conv1d+SiLU (CUDAConv1dSiLUOp), DynamicsFusedFn, NormalizeKQFn and SSDChunkwiseScan (the fused
-        scan kernels), whose backwards are the reference's -- and torch for the projections, the
-        RMSNorm, the shortcut, the readout and the fp32 GroupNorm.  The readout and shortcut are formed as
-        sum_d Y q + s (q.k)^2 V_gated (the reference adds s (q.k) V_gated k^T to Y and reads it with q:
-        the same value) with elementwise products in the compute dtype."""
+        conv1d+SiLU (CUDAConv1dSiLUOp), DynamicsFusedFn, NormalizeKQFn and the fused scan, whose backwards
+        are the reference's -- and torch for the projections, the RMSNorm, the shortcut and the fp32
+        GroupNorm.  For state_dim 2 the scan is ChunkwiseDeltaScanAbarFn, which returns the readout
+        sel_C (Y.q) itself and never forms Y; otherwise SSDChunkwiseScan's Y is read out here.  The
+        shortcut enters as s (q.k)^2 V_gated (the reference adds s (q.k) V_gated k^T to Y and reads it with
+        q: the same value), with elementwise products in the compute dtype."""
         cfg = self.config
         N, H, D, Di = cfg.state_dim, cfg.n_heads, cfg.head_dim, cfg.d_inner
         B, L, _ = x.shape
@@ -672,11 +678,16 @@ class CDSSMBlock(nn.Module):
         Q = self.Q_proj(x_conv).reshape(B, L, H, D)
         K, Q = NormalizeKQFn.apply(K, Q)                                              # block.py:191-192
         V_gated = V * vp.repeat_interleave(2, dim=-1)                                 # block.py:194-195
-        Y = SSDChunkwiseScan(cfg.chunk_size, N)(A_bar, K, V_gated, beta)              # block.py:198
         qk = (Q * K).sum(-1)                                                          # block.py:202
-        retrieved = (Y * Q.unsqueeze(-2)).sum(-1) \
-            + self.shortcut_scale * (qk * qk).unsqueeze(-1) * V_gated                 # block.py:204-208
-        retrieved = retrieved * sel_C.unsqueeze(-1)                                   # block.py:211
+        shortcut = self.shortcut_scale * (qk * qk).unsqueeze(-1) * V_gated            # block.py:204-208
+        if self.readout_scan and N == 2 and D in (64, 128):
+            # the fused scan with its readout, sel_C (Y.q) (block.py:198, 208-211), without forming the
+            # (B,L,H,2,D) Y: its backward rebuilds chunk states from the forward's records
+            y_scan, _ = ChunkwiseDeltaScanAbarFn.apply(Q, K, V, beta, sel_C, A_bar, vp, None, cfg.chunk_size)
+            retrieved = y_scan + shortcut * sel_C.unsqueeze(-1)
+        else:
+            Y = SSDChunkwiseScan(cfg.chunk_size, N)(A_bar, K, V_gated, beta)          # block.py:198
+            retrieved = ((Y * Q.unsqueeze(-2)).sum(-1) + shortcut) * sel_C.unsqueeze(-1)  # block.py:208-211
         y = self.readout_proj(retrieved.reshape(B, L, H * N))
         y = torch.nn.functional.group_norm(y.float().transpose(1, 2), self.ssm_norm.num_groups,
                                            self.ssm_norm.weight.float(), self.ssm_norm.bias.float(),

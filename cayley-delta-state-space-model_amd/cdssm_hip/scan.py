@@ -96,15 +96,7 @@ def chunkwise_delta_scan_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_
     return y, h_final, ws
 
 
-def chunkwise_delta_scan_abar(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_C: Tensor, A_bar: Tensor,
-                              vp: Tensor, h0: Optional[Tensor] = None,
-                              chunk_size: Optional[int] = None) -> Tuple[Tensor, Tensor]:
-    """The fused scan on gate-level inputs (cdssm_fused_scan_fwd_abar), inference only.
-
-    ``A_bar`` (B,L,H,2) and ``vp`` (B,L,H,1) are DynamicsFusedFn's outputs; the result is
-    ``sel_C * einsum('blhsd,blhd->blhs', SSDChunkwiseScan(Q, 2)(A_bar, k, v * vp, beta), q)``
-    (block.py:194-211 without the shortcut) and the final R-mode state (B,H,2,D) fp32.
-    """
+def _abar_validate(q, k, v, beta, sel_C, A_bar, vp, h0, chunk_size):
     if not isinstance(A_bar, torch.Tensor) or not isinstance(vp, torch.Tensor):
         raise TypeError("A_bar and vp must be tensors")
     B, L, H, D = q.shape
@@ -115,7 +107,16 @@ def chunkwise_delta_scan_abar(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel
         raise TypeError("A_bar and vp must have q's dtype and device")
     # shape/dtype checks of the other inputs (A_bar and vp stand in for dt and r there)
     ones = torch.empty(H, dtype=torch.float32, device=q.device)
-    _, _, _, _, N, Q, dtype = _validate(q, k, v, beta, sel_C, beta, beta, ones, ones, h0, chunk_size)
+    return _validate(q, k, v, beta, sel_C, beta, beta, ones, ones, h0, chunk_size)
+
+
+def chunkwise_delta_scan_abar_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_C: Tensor, A_bar: Tensor,
+                                  vp: Tensor, h0: Optional[Tensor] = None, chunk_size: Optional[int] = None,
+                                  train: bool = False) -> Tuple[Tensor, Tensor, Tensor]:
+    """The fused scan on gate-level inputs: (y, h_final, workspace).  ``train=True``
+    (cdssm_fused_scan_fwd_abar_train) keeps in the workspace what
+    ``chunkwise_delta_scan_abar_bwd`` reads."""
+    B, L, H, D, N, Q, dtype = _abar_validate(q, k, v, beta, sel_C, A_bar, vp, h0, chunk_size)
     lib = _lib.load()
     ins = [t.contiguous() for t in (q, k, v, beta, sel_C, A_bar, vp)]
     h0c = h0.contiguous() if h0 is not None else None
@@ -125,11 +126,77 @@ def chunkwise_delta_scan_abar(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel
     if nbytes <= 0:
         raise RuntimeError(f"cdssm_fused_scan_workspace_bytes rejected the shape ({nbytes})")
     ws = torch.empty(nbytes // 4, dtype=torch.float32, device=q.device)
-    st = lib.cdssm_fused_scan_fwd_abar(_lib.DTYPE_CODE[dtype], *[_lib.ptr(t) for t in ins], _lib.ptr(h0c),
-                                       _lib.ptr(y), _lib.ptr(h_final), _lib.ptr(ws), B, L, H, D, N, Q,
-                                       _lib.stream_of(q.device))
-    _lib.check(st, "cdssm_fused_scan_fwd_abar")
+    name = "cdssm_fused_scan_fwd_abar_train" if train else "cdssm_fused_scan_fwd_abar"
+    st = getattr(lib, name)(_lib.DTYPE_CODE[dtype], *[_lib.ptr(t) for t in ins], _lib.ptr(h0c), _lib.ptr(y),
+                            _lib.ptr(h_final), _lib.ptr(ws), B, L, H, D, N, Q, _lib.stream_of(q.device))
+    _lib.check(st, name)
+    return y, h_final, ws
+
+
+def chunkwise_delta_scan_abar(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_C: Tensor, A_bar: Tensor,
+                              vp: Tensor, h0: Optional[Tensor] = None,
+                              chunk_size: Optional[int] = None) -> Tuple[Tensor, Tensor]:
+    """The fused scan on gate-level inputs (cdssm_fused_scan_fwd_abar), inference.
+
+    ``A_bar`` (B,L,H,2) and ``vp`` (B,L,H,1) are DynamicsFusedFn's outputs; the result is
+    ``sel_C * einsum('blhsd,blhd->blhs', SSDChunkwiseScan(Q, 2)(A_bar, k, v * vp, beta), q)``
+    (block.py:194-211 without the shortcut) and the final R-mode state (B,H,2,D) fp32.
+    ``ChunkwiseDeltaScanAbarFn`` is the differentiable form.
+    """
+    y, h_final, _ = chunkwise_delta_scan_abar_fwd(q, k, v, beta, sel_C, A_bar, vp, h0, chunk_size)
     return y, h_final
+
+
+def chunkwise_delta_scan_abar_bwd(dy: Tensor, dh_final: Optional[Tensor], q, k, v, beta, sel_C, A_bar, vp,
+                                  fwd_ws: Tensor, has_h0: bool, chunk_size: int):
+    """Backward of ``chunkwise_delta_scan_abar_fwd(..., train=True)`` (cdssm_fused_scan_bwd_abar):
+    (dq, dk, dv, dbeta, dsel_C, dA_bar, dvp, dh0), dh0 None without an initial state."""
+    B, L, H, D = q.shape
+    N = v.shape[-1]
+    Q = int(chunk_size)
+    lib = _lib.load()
+    dev = q.device
+    dy = dy.to(q.dtype).contiguous()
+    dhf = None if dh_final is None else dh_final.float().contiguous()
+    outs = [torch.empty_like(t) for t in (q, k, v, beta, sel_C, A_bar, vp)]
+    dh0 = torch.empty(B, H, N, D, dtype=torch.float32, device=dev) if has_h0 else None
+    nbytes = lib.cdssm_fused_scan_bwd_workspace_bytes(B, L, H, D, N, Q)
+    if nbytes <= 0:
+        raise RuntimeError(f"cdssm_fused_scan_bwd_workspace_bytes rejected the shape ({nbytes})")
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    st = lib.cdssm_fused_scan_bwd_abar(_lib.DTYPE_CODE[q.dtype], *[_lib.ptr(t) for t in (q, k, v, beta, sel_C, A_bar, vp)],
+                                       _lib.ptr(dy), _lib.ptr(dhf), _lib.ptr(fwd_ws), *[_lib.ptr(t) for t in outs],
+                                       _lib.ptr(dh0), _lib.ptr(ws), B, L, H, D, N, Q, _lib.stream_of(dev))
+    _lib.check(st, "cdssm_fused_scan_bwd_abar")
+    return (*outs, dh0)
+
+
+class ChunkwiseDeltaScanAbarFn(torch.autograd.Function):
+    """Autograd Function of the fused scan on gate-level inputs: (q, k, v, beta, sel_C, A_bar, vp, h0,
+    chunk_size) -> (y, h_final), y = sel_C (Y . q) of SSDChunkwiseScan(A_bar, k, v * vp, beta)
+    (block.py:194-211 without the shortcut).  The training step through the block (trainer.py:235-247)
+    without the (B,L,H,2,D) Y: the forward keeps only the training records in its workspace, the
+    backward rebuilds chunk states from them and returns the reference's gradients (exact for the
+    readout, the local and carry branches; the correction branch's shifted rule)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, beta, sel_C, A_bar, vp, h0=None, chunk_size=None):
+        _, _, _, _, _, Q, _ = _abar_validate(q, k, v, beta, sel_C, A_bar, vp, h0, chunk_size)
+        ins = [t.contiguous() for t in (q, k, v, beta, sel_C, A_bar, vp)]
+        y, h_final, ws = chunkwise_delta_scan_abar_fwd(*ins, h0, Q, train=True)
+        ctx.save_for_backward(*ins, ws)
+        ctx.Q = Q
+        ctx.has_h0 = h0 is not None
+        return y, h_final
+
+    @staticmethod
+    def backward(ctx, dy, dh_final):
+        *ins, ws = ctx.saved_tensors
+        if dy is None:
+            dy = torch.zeros_like(ins[2])
+        dq, dk, dv, dbeta, dsel, dA, dvp, dh0 = chunkwise_delta_scan_abar_bwd(dy, dh_final, *ins, ws, ctx.has_h0,
+                                                                              ctx.Q)
+        return dq, dk, dv, dbeta, dsel, dA, dvp, dh0, None
 
 
 FORWARD_PATHS = {"auto": 0, "four_launch": 1, "one_pass": 2, "four_launch_mfma": 3}

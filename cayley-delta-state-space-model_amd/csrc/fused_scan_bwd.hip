@@ -139,6 +139,8 @@ __device__ __forceinline__ int stage_bwd(const ChunkTile& tc, int H, int ntr,
   const bool hok = hj < H;
   const int hl = hok ? hj : H - 1;
   constexpr bool YM = IsSsdY<T>::value;
+  constexpr bool GA = GivenA<T>::value;  // a_t read from A_bar (dt's place); ABar: vp from r's place
+  constexpr bool kAbar = IsABar<T>::value;
   static_assert(!RS || (WITH_W && !YM), "rescaled frames: the readout form's main pass");
   static_assert(kBwdCK % TPB == 0, "a segment is a whole number of blocks");
   constexpr int SB = kBwdCK / TPB;  // blocks per segment
@@ -147,7 +149,7 @@ __device__ __forceinline__ int stage_bwd(const ChunkTile& tc, int H, int ntr,
   // a slab's inputs and the training forward's records (p, pc), (c^_{t+1}.q, Y.q);
   // the next slab's are requested before this one is worked on
   struct SlabIn {
-    float bb[TPB], dd[TPB], rr[TPB], v0[TPB], v1[TPB], sc[TPB], g0[TPB], g1[TPB];
+    float bb[TPB], dd[TPB], rr[TPB], vq[TPB], v0[TPB], v1[TPB], sc[TPB], g0[TPB], g1[TPB];
     float4 rp[TPB], rq[TPB];
   };
   const auto load_slab = [&](SlabIn& in, int tl) {
@@ -156,8 +158,9 @@ __device__ __forceinline__ int stage_bwd(const ChunkTile& tc, int H, int ntr,
       const int t = min(tl + blk * TPB + i, tc.nt - 1);
       const int64_t e = (tc.row0 + t) * H + hl;
       in.bb[i] = T::load(beta + (YM ? (tc.row0 + t) * (H / R) + hl / R : e));  // SSD form: beta per real head
-      in.dd[i] = T::load(dt + (YM ? 2 * e : e));  // SSD form: a_t (re, im) from A_bar
-      in.rr[i] = T::load(YM ? dt + 2 * e + 1 : r + e);
+      in.dd[i] = T::load(dt + (GA ? 2 * e : e));  // SSD and ABar forms: a_t (re, im) from A_bar
+      in.rr[i] = T::load(GA ? dt + 2 * e + 1 : r + e);
+      in.vq[i] = kAbar ? T::load(r + e) : 1.0f;   // ABar form: vp_t
       in.v0[i] = WITH_W ? T::load(v + 2 * e) : 0.0f;
       in.v1[i] = WITH_W ? T::load(v + 2 * e + 1) : 0.0f;
       in.sc[i] = YM ? 0.0f : T::load(sel_c + e);
@@ -175,13 +178,14 @@ __device__ __forceinline__ int stage_bwd(const ChunkTile& tc, int H, int ntr,
     const int t0 = tl + blk * TPB;
     const SlabIn in = nx;
     if (tl + kWave < ntr) load_slab(nx, tl + kWave);
-    float bb[TPB], dd[TPB], rr[TPB], v0[TPB], v1[TPB], sc[TPB], g0[TPB], g1[TPB];
+    float bb[TPB], dd[TPB], rr[TPB], vq[TPB], v0[TPB], v1[TPB], sc[TPB], g0[TPB], g1[TPB];
     float4 rp[TPB], rq[TPB];
 #pragma unroll
     for (int i = 0; i < TPB; ++i) {
       bb[i] = in.bb[i];
       dd[i] = in.dd[i];
       rr[i] = in.rr[i];
+      vq[i] = in.vq[i];
       v0[i] = in.v0[i];
       v1[i] = in.v1[i];
       sc[i] = in.sc[i];
@@ -199,7 +203,7 @@ __device__ __forceinline__ int stage_bwd(const ChunkTile& tc, int H, int ntr,
         // d sel_C = dy . (Y.q) needs nothing from the reverse pass: stored here
         if (real) T::store(dsel + (tc.row0 + t0 + i) * H + hl, g0[i] * rq[i].z + g1[i] * rq[i].w);
       }
-      const Transition tr = YM ? Transition{dd[i], rr[i], 1.0f} : cayley_gated(dd[i], rr[i], al, om, c);
+      const Transition tr = GA ? Transition{dd[i], rr[i], vq[i]} : cayley_gated(dd[i], rr[i], al, om, c);
       ar[i] = real ? tr.ar : 1.0f;
       ai[i] = real ? tr.ai : 0.0f;
       const float f = bb[i] * tr.vp;
@@ -1012,7 +1016,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
   const int slots = round_up(Q, kWave) * HPW;
   const int ntr = round_up(tc.nt, PF);
   constexpr bool YM = IsSsdY<T>::value;  // SSD form: q points at dY (B,L,H,2,D); dq not formed
-  const float al = YM ? 0.0f : alpha[hl], om = YM ? 0.0f : omega[hl];
+  constexpr bool kAbar = IsABar<T>::value;  // gate-level a_t and vp given: no per-head dynamics parameters
+  const float al = YM || kAbar ? 0.0f : alpha[hl], om = YM || kAbar ? 0.0f : omega[hl];
 
   // SSD form: R virtual heads (state rows) share each k row; with R > 1 each writes its own fp32 dk row
   // into dkp (B, L, H, D) and a row-sum kernel forms dk
@@ -1376,8 +1381,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
         lv1[i] = T::load(v + 2 * ee + 1);
         ldt[i] = lrr[i] = lg0[i] = lg1[i] = 0.0f;
         if constexpr (!YM) {
-          ldt[i] = T::load(dt + ee);
-          lrr[i] = T::load(r + ee);
+          if constexpr (!kAbar) ldt[i] = T::load(dt + ee);
+          lrr[i] = T::load(r + ee);  // ABar form: vp_t
           if (!rs) {
             lg0[i] = T::load(dy + 2 * ee);
             lg1[i] = T::load(dy + 2 * ee + 1);
@@ -1530,8 +1535,21 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
               T::store(dbeta + e, db);
             continue;
           }
-          const float dtv = ldt[i], rrv = lrr[i];
           const float g0 = lg0[i], g1 = lg1[i];
+          if constexpr (kAbar) {
+            // gate-level form (w = beta vp v): d A_bar_t = d a_t ((re, im) pairs in ddt's place),
+            // d vp_t = beta (dw . v) in dr's place, dv = beta vp dw, dbeta = erase part + vp (dw . v)
+            const float vpv = lrr[i];
+            const float dwv = dwr * v0 + dwi * v1;
+            store_pair<T>(ddt + 2 * e, dar, dai);
+            T::store(dr + e, bb * dwv);
+            T::store(dv + 2 * e, bb * vpv * dwr);
+            T::store(dv + 2 * e + 1, bb * vpv * dwi);
+            T::store(dbeta + e, dbe + vpv * dwv);
+            if (!rs) T::store(dsel + e, g0 * gv.z + g1 * gv.w);  // (rescaled: stored by the staging)
+            continue;
+          }
+          const float dtv = ldt[i], rrv = lrr[i];
           const Transition tr = cayley_gated(dtv, rrv, alj, omj, c);
           const float dwv = dwr * v0 + dwi * v1;
           const DynGrad g = cayley_gated_bwd(dtv, rrv, alj, omj, c, dar, dai, bb * dwv);
@@ -1546,7 +1564,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
         }
       }
     }
-    if constexpr (!YM) {
+    if constexpr (!YM && !kAbar) {
       dal = group_sum<NB>(dal);
       dom = group_sum<NB>(dom);
       if (blk == 0 && jok) dhead_parts[(int64_t(tc.b) * NC + tc.chunk) * H + hj] = make_float2(dal, dom);
@@ -1788,6 +1806,10 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
     if (ev) (void)hipEventRecord(ev[5], stream);
     return st;
   }
+  if constexpr (IsABar<T>::value) {  // gate-level form: no per-head dynamics parameters either
+    if (ev) (void)hipEventRecord(ev[5], stream);
+    return st;
+  }
   hipLaunchKernelGGL(fused_bwd_heads_kernel, dim3(unsigned(H)), dim3(256), 0, stream,
                      (const float2*)parts, dalpha, domega, B * NC, H);
   st = cdssm_host::check_launch("cdssm_fused_scan_bwd/heads");
@@ -1842,8 +1864,8 @@ int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, cons
                     void* ddt, void* dr, float* dalpha, float* domega, float* dh0, float* workspace,
                     int64_t B, int64_t L, int64_t H, int64_t D, int64_t N, int64_t chunk,
                     hipStream_t stream, hipEvent_t* ev, int* carry_fused = nullptr, bool ssd = false,
-                    bool cont = false) {
-  const char* op = ssd ? "cdssm_ssd_scan_bwd" : "cdssm_fused_scan_bwd";
+                    bool cont = false, bool abar = false) {
+  const char* op = ssd ? "cdssm_ssd_scan_bwd" : (abar ? "cdssm_fused_scan_bwd_abar" : "cdssm_fused_scan_bwd");
   if (dtype != 0 && dtype != 1) {
     cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
     return CDSSM_EINVAL;
@@ -1883,12 +1905,28 @@ int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, cons
     return CDSSM_EINVAL;
   }
   if (ssd ? (!q || !k || !v || !beta || !dt || !fwd_workspace || !dk || !dv || !dbeta || !ddt || !workspace)
-          : (!q || !k || !v || !beta || !sel_c || !dt || !r || !alpha || !omega || !dy || !fwd_workspace || !dq ||
-             !dk || !dv || !dbeta || !dsel || !ddt || !dr || !dalpha || !domega || !workspace)) {
+          : (!q || !k || !v || !beta || !sel_c || !dt || !r || (!abar && (!alpha || !omega)) || !dy ||
+             !fwd_workspace || !dq || !dk || !dv || !dbeta || !dsel || !ddt || !dr ||
+             (!abar && (!dalpha || !domega)) || !workspace)) {
     cdssm_host::set_error("%s: null pointer argument", op);
     return CDSSM_EINVAL;
   }
   const int b = int(B), l = int(L), hh = int(H), qc = int(chunk);
+  if (abar) {
+    // a_bar / dA_bar hold (re, im) pairs
+    if (reinterpret_cast<uintptr_t>(dt) % (dtype == 1 ? 4 : 8) != 0 ||
+        reinterpret_cast<uintptr_t>(ddt) % (dtype == 1 ? 4 : 8) != 0) {
+      cdssm_host::set_error("%s: A_bar and dA_bar must be aligned to their (re, im) pairs", op);
+      return CDSSM_EINVAL;
+    }
+#define CDSSM_ABAR_BWD(TT, DD)                                                                                   \
+  launch_fused_bwd<TT, DD>(q, k, v, beta, sel_c, dt, r, nullptr, nullptr, 0.0f, dy, dh_final, fwd_workspace, dq,  \
+                           dk, dv, dbeta, dsel, ddt, dr, nullptr, nullptr, dh0, workspace, b, l, hh, qc, stream, \
+                           ev, carry_fused, cont)
+    if (dtype == 1) return D == 64 ? CDSSM_ABAR_BWD(ABar<BF16>, 64) : CDSSM_ABAR_BWD(ABar<BF16>, 128);
+    return D == 64 ? CDSSM_ABAR_BWD(ABar<F32>, 64) : CDSSM_ABAR_BWD(ABar<F32>, 128);
+#undef CDSSM_ABAR_BWD
+  }
   if (ssd) {
     const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     if (!a16(q) || !a16(k) || !a16(dk) || reinterpret_cast<uintptr_t>(ddt) % (dtype == 1 ? 4 : 8) != 0) {
@@ -1953,6 +1991,21 @@ extern "C" int cdssm_fused_scan_bwd_continue(int dtype, const void* q, const voi
   return fused_bwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final, fwd_workspace,
                          dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0, workspace, B, L, H, D, N,
                          chunk, stream, nullptr, nullptr, false, true);
+}
+
+// Backward of the gate-level (A_bar, vp) forward, cdssm_fused_scan_fwd_abar_train:
+// the readout form's gradients with dA_bar (B,L,H,2) and dvp (B,L,H) in place
+// of the scan-level dynamics chain (no per-head dalpha / domega).  Same rules
+// as cdssm_fused_scan_bwd (the correction branch's shifted rule).
+extern "C" int cdssm_fused_scan_bwd_abar(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                                         const void* sel_c, const void* a_bar, const void* vp, const void* dy,
+                                         const float* dh_final, const float* fwd_workspace, void* dq, void* dk,
+                                         void* dv, void* dbeta, void* dsel, void* da_bar, void* dvp, float* dh0,
+                                         float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                         int64_t chunk, hipStream_t stream) {
+  return fused_bwd_entry(dtype, q, k, v, beta, sel_c, a_bar, vp, nullptr, nullptr, 0.0f, dy, dh_final,
+                         fwd_workspace, dq, dk, dv, dbeta, dsel, da_bar, dvp, nullptr, nullptr, dh0, workspace, B, L,
+                         H, D, N, chunk, stream, nullptr, nullptr, false, false, true);
 }
 
 // Backward of cdssm_ssd_scan_fwd (the SSDChunkwiseScan interface), with the

@@ -1686,9 +1686,7 @@ int launch_fused_fwd(const void* q, const void* k, const void* v, const void* be
                      int Q, hipStream_t stream, hipEvent_t* ev, bool save, int* path, bool cont, int R = 1) {
   using raw = typename T::raw;
   constexpr int HPW = kWave / LPH, HPWS = kWave / LPHS;
-  // the a_t input form is inference-only: its training branches name the
-  // inference kernels (never taken: save is false for it)
-  constexpr bool kSv = !IsABar<T>::value;
+  constexpr bool kSv = true;  // the training instances (every input form has a training forward)
   const FwdLayout w = fwd_layout(B, L, H, D, Q);
   const int NC = w.NC, S = w.S;
   const int n_hg = (H + HPW - 1) / HPW, n_hgs = (H + HPWS - 1) / HPWS;
@@ -2083,10 +2081,6 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
     return launch_fused_fwd<SsdY<F32>, 128, 32, 32>(CDSSM_FWD_ARGS, rr);
   }
   if (abar) {
-    if (save) {
-      cdssm_host::set_error("%s: the a_t input form has no training forward", op);
-      return CDSSM_EINVAL;
-    }
     if (dtype == 1) {
       if (D == 64 && fill_with_4_heads_per_wave(B, L, H, chunk))
         return launch_fused_fwd<ABar<BF16>, 64, 16, CDSSM_FWD_LPHS_BF16_D64>(CDSSM_FWD_ARGS);
@@ -2160,6 +2154,18 @@ extern "C" int cdssm_fused_scan_fwd_abar(int dtype, const void* q, const void* k
                                          int64_t N, int64_t chunk, hipStream_t stream) {
   return fused_fwd_entry(dtype, q, k, v, beta, sel_c, a_bar, vp, nullptr, nullptr, 0.0f, h0, y, h_final, workspace,
                          B, L, H, D, N, chunk, stream, nullptr, false, nullptr, true);
+}
+
+// Training forward of the gate-level form: cdssm_fused_scan_fwd_abar that also
+// stores in the workspace what cdssm_fused_scan_bwd_abar reads (the records of
+// cdssm_fused_scan_fwd_train).
+extern "C" int cdssm_fused_scan_fwd_abar_train(int dtype, const void* q, const void* k, const void* v,
+                                               const void* beta, const void* sel_c, const void* a_bar,
+                                               const void* vp, const float* h0, void* y, float* h_final,
+                                               float* workspace, int64_t B, int64_t L, int64_t H, int64_t D,
+                                               int64_t N, int64_t chunk, hipStream_t stream) {
+  return fused_fwd_entry(dtype, q, k, v, beta, sel_c, a_bar, vp, nullptr, nullptr, 0.0f, h0, y, h_final, workspace,
+                         B, L, H, D, N, chunk, stream, nullptr, true, nullptr, true);
 }
 
 // The SSDChunkwiseScan interface (ssd.py:39-111) on the fused kernels: A_bar

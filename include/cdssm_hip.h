@@ -94,6 +94,33 @@ int cdssm_fused_scan_fwd_abar(int dtype, const void* q, const void* k, const voi
                               int64_t N, int64_t chunk, hipStream_t stream);
 
 /*
+ * Training path of the gate-level form: the scan the block's training step
+ * runs (block.py:181-211 under autograd, trainer.py:235-247) without writing
+ * the (B,L,H,2,D) Y that SSDChunkwiseScan returns (ssd.py:39-111; the reference
+ * stores it, and its passes' states, for its backward, ops.py:119,153,184).
+ * cdssm_fused_scan_fwd_abar_train: the forward above that also stores in the
+ * workspace what the backward reads (the records of cdssm_fused_scan_fwd_train).
+ * cdssm_fused_scan_bwd_abar: given dy (B,L,H,2), dh_final (B,H,2,D) fp32 or
+ * NULL and that workspace, writes dq, dk (B,L,H,D), dv (B,L,H,2), dbeta,
+ * dsel_c (B,L,H), da_bar (B,L,H,2), dvp (B,L,H) of `dtype` and dh0 (B,H,2,D)
+ * fp32 or NULL: the gradients ops.py's autograd yields through
+ * SSDChunkwiseScan and the readout (exact for the readout, the local and carry
+ * branches; the correction branch's shifted rule, exact_correction.cu:213-382),
+ * with d A_bar and d vp in place of the scan-level dynamics chain of
+ * cdssm_fused_scan_bwd.  workspace: cdssm_fused_scan_bwd_workspace_bytes().
+ */
+int cdssm_fused_scan_fwd_abar_train(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                                    const void* sel_c, const void* a_bar, const void* vp, const float* h0, void* y,
+                                    float* h_final, float* workspace, int64_t B, int64_t L, int64_t H, int64_t D,
+                                    int64_t N, int64_t chunk, hipStream_t stream);
+int cdssm_fused_scan_bwd_abar(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                              const void* sel_c, const void* a_bar, const void* vp, const void* dy,
+                              const float* dh_final, const float* fwd_workspace, void* dq, void* dk, void* dv,
+                              void* dbeta, void* dsel_c, void* da_bar, void* dvp, float* dh0, float* workspace,
+                              int64_t B, int64_t L, int64_t H, int64_t D, int64_t N, int64_t chunk,
+                              hipStream_t stream);
+
+/*
  * Training forward (no counterpart in the reference; the reference keeps its
  * passes' full outputs for backward instead): the forward above, which also
  * stores in the workspace what the backward reads: per (token, head) the dot
