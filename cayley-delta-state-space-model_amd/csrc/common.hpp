@@ -278,6 +278,24 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// Sum over the wave's heads of a value its lanes hold per head, for heads of
+// LPH lanes (lane = head * LPH + slice): every lane gets the sum over the lanes
+// of its slice in all heads.  Row swaps only (heads are whole rows of 16 lanes
+// or more), in a fixed order.
+template <int LPH>
+__device__ __forceinline__ float cross_head_sum(float x) {
+  static_assert(LPH == 16 || LPH == 32 || LPH == 64, "heads of whole 16-lane rows");
+  if constexpr (LPH <= 16) {
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+  if constexpr (LPH <= 32) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+  return x;
+}
+
 // ---------------------------------------------------------------------------
 // Tiles of the fused scan: one wave per (b, chunk, group of HPW heads).
 // ---------------------------------------------------------------------------

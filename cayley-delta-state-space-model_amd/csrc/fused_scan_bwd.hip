@@ -1019,20 +1019,27 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
   constexpr bool kAbar = IsABar<T>::value;  // gate-level a_t and vp given: no per-head dynamics parameters
   const float al = YM || kAbar ? 0.0f : alpha[hl], om = YM || kAbar ? 0.0f : omega[hl];
 
-  // SSD form: R virtual heads (state rows) share each k row; with R > 1 each writes its own fp32 dk row
-  // into dkp (B, L, H, D) and a row-sum kernel forms dk
+  // SSD form: R virtual heads (state rows) share each k row; with R > 1 their fp32 dk rows go to dkp and a
+  // row-sum kernel forms dk.  Where a wave's HPW heads are rows of one real head (R % HPW == 0) the wave
+  // sums them first and writes one row per wave, dkp (B, L, H / HPW, D); otherwise one per virtual head,
+  // dkp (B, L, H, D)
   const bool rows = YM && R > 1;
+  const bool rows_pre = rows && R % HPW == 0;
   const RowStream ks = YM ? tile_stream_rows<T>(k, tc, L, H, R, D, hh, sub * DPL)
                           : tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
   // readout form: q rows; SSD form: this lane's slices of the dY re (qs) and im (gs) rows
   const RowStream qs = tile_stream<T>(q, tc, L, H, YM ? 2 * D : D, hh, sub * DPL);
   const RowStream gs = YM ? tile_stream<T>(q, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
   const RowStream dks = rows ? RowStream{} : tile_stream<T>(dk, tc, L, H, D, hh, sub * DPL);
-  const RowStream dkps = rows ? tile_stream<F32>(dkp, tc, L, H, D, hh, sub * DPL) : RowStream{};
+  ChunkTile tcp = tc;  // the wave's partial row: head hbase / HPW of H / HPW
+  tcp.hbase = tc.hbase / HPW;
+  const RowStream dkps = !rows      ? RowStream{}
+                         : rows_pre ? tile_stream<F32>(dkp, tcp, L, H / HPW, D, 0, sub * DPL)
+                                    : tile_stream<F32>(dkp, tc, L, H, D, hh, sub * DPL);
   const RowStream dqs = YM ? RowStream{} : tile_stream<T>(dq, tc, L, H, D, hh, sub * DPL);
   const int rowb = (YM ? H / R : H) * D * T::bytes;  // token stride of k (and q, dq, dk) in bytes
   const int rowq = YM ? 2 * H * D * T::bytes : rowb;  // of q, or of dY
-  const int rowp = H * D * 4;                          // of dkp
+  const int rowp = (rows_pre ? H / HPW : H) * D * 4;   // of dkp
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb, slimq = tlast * rowq;
   const int64_t chh = (int64_t(tc.b) * NC + tc.chunk) * H + hl;  // (b, chunk, head) index
@@ -1195,7 +1202,12 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
           lr[jj] = fmaf(-bslr, kk[jj], lr[jj]);
           li[jj] = fmaf(-bsli, kk[jj], li[jj]);
         }
-        if (hok) {
+        if (rows_pre) {
+          // the wave's heads are rows of one real head: their sum, stored by head 0's lanes
+#pragma unroll
+          for (int jj = 0; jj < DPL; ++jj) dkv[jj] = cross_head_sum<LPH>(dkv[jj]);
+          if (hh == 0) store_row<F32, DPL>(dkps, t * rowp, dkv);
+        } else if (hok) {
           if (rows)
             store_row<F32, DPL>(dkps, t * rowp, dkv);
           else
@@ -1604,25 +1616,27 @@ __global__ __launch_bounds__(256) void fused_bwd_heads_kernel(const float2* __re
 
 // ---------------------------------------------------------------------------
 // SSD form with R > 1 state rows per head: dk and dbeta of each head are the
-// sums over its R virtual heads of the fp32 partials the main pass wrote,
-// dk[n, h, :] = sum_j dkp[n, h R + j, :], dbeta[n, h] = sum_j dbp[n, h R + j]
-// (n = token), in a fixed order.  One thread per 4 consecutive elements of
-// dk (D % 4 == 0); the first of a row's threads also sums dbeta.
+// sums of the fp32 partials the main pass wrote, dk[n, h, :] = sum_j
+// dkp[n, h P + j, :] over the head's P partial rows (P = R, or R / HPW where
+// the main pass already summed each wave's HPW rows), dbeta[n, h] = sum_j
+// dbp[n, h R + j] (n = token), in a fixed order.  One thread per 4
+// consecutive elements of dk (D % 4 == 0); the first of a row's threads also
+// sums dbeta.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void ssd_rows_sum_kernel(const float* __restrict__ dkp,
                                                            const float* __restrict__ dbp,
                                                            typename T::raw* __restrict__ dk,
                                                            typename T::raw* __restrict__ dbeta, int64_t n_rows,
-                                                           int R, int D) {
+                                                           int R, int P, int D) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;  // (token, head, 4 elements)
   const int qd = D / 4;
   if (i >= n_rows * qd) return;
   const int64_t row = i / qd;  // token * Hk + head
   const int d0 = int(i - row * qd) * 4;
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  for (int j = 0; j < R; ++j) {
-    const float4 x = *reinterpret_cast<const float4*>(dkp + (row * R + j) * D + d0);
+  for (int j = 0; j < P; ++j) {
+    const float4 x = *reinterpret_cast<const float4*>(dkp + (row * P + j) * D + d0);
     acc.x += x.x;
     acc.y += x.y;
     acc.z += x.z;
@@ -1800,7 +1814,8 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
       const int64_t n_rows = int64_t(B) * L * (H / R);
       const int64_t threads = n_rows * (D / 4);
       hipLaunchKernelGGL(ssd_rows_sum_kernel<T>, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, stream,
-                         (const float*)dkp, (const float*)dbp, (raw*)dk, (raw*)dbeta, n_rows, R, D);
+                         (const float*)dkp, (const float*)dbp, (raw*)dk, (raw*)dbeta, n_rows, R,
+                         R % HPW == 0 ? R / HPW : R, D);
       st = cdssm_host::check_launch("cdssm_ssd_scan_bwd/rows_sum");
     }
     if (ev) (void)hipEventRecord(ev[5], stream);
