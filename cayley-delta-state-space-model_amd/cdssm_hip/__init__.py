@@ -6,7 +6,7 @@ touch the GPU; the library is loaded on first use and its absence is an error.
 """
 
 from .scan import (ChunkwiseDeltaScanAbarFn, ChunkwiseDeltaScanFn, SSDScanFn, check_lookback,  # noqa: F401
-                   chunkwise_delta_scan, chunkwise_delta_scan_abar, chunkwise_delta_scan_bwd,
+                   chunked_scan_abar, chunkwise_delta_scan, chunkwise_delta_scan_abar, chunkwise_delta_scan_bwd,
                    chunkwise_delta_scan_fwd, chunkwise_delta_scan_train, lookback_status, set_forward_path,
                    ssd_scan_bwd, ssd_scan_fwd)
 
@@ -17,7 +17,7 @@ from .decode import DecodeState, decode_step, prefill  # noqa: F401
 
 __all__ = ["DynamicsFusedFn", "NormalizeKQFn", "IntraChunkScanFn", "InterChunkScanFn", "ExactCorrectionFn",
            "SSDChunkwiseScan", "SSDScanFn", "ssd_scan_fwd", "ssd_scan_bwd", "ChunkwiseDeltaScanFn", "ChunkwiseDeltaScanAbarFn", "chunkwise_delta_scan",
-           "chunkwise_delta_scan_abar", "chunkwise_delta_scan_fwd",
+           "chunkwise_delta_scan_abar", "chunked_scan_abar", "chunkwise_delta_scan_fwd",
            "chunkwise_delta_scan_bwd", "chunkwise_delta_scan_train", "set_forward_path", "lookback_status",
            "check_lookback", "DecodeState",
            "decode_step", "prefill"]

@@ -147,6 +147,53 @@ def chunkwise_delta_scan_abar(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel
     return y, h_final
 
 
+def chunked_scan_abar(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_C: Tensor, A_bar: Tensor, vp: Tensor,
+                      h0: Optional[Tensor] = None, chunk_size: Optional[int] = None) -> Tuple[Tensor, Tensor]:
+    """The gate-level readout form for state_dim N = 16 in the chunked (UT) form on the matrix cores
+    (cdssm_chunked_scan_fwd_abar), inference, bf16: ``(y, h_final)`` with
+    ``y = sel_C * einsum('blhsd,blhd->blhs', SSDChunkwiseScan(Q, 16)(A_bar, k, v * vp.repeat_interleave(2, -1),
+    beta), q)`` (B,L,H,16) (block.py:194-211 without the shortcut) and the final R-mode state (B,H,16,D) fp32,
+    without forming Y.  ``A_bar`` (B,L,H,16) and ``vp`` (B,L,H,8) are DynamicsFusedFn's outputs; q, k (B,L,H,D)
+    with D in {64, 128}; chunk_size (default D) a multiple of 16 up to 256."""
+    named = dict(q=q, k=k, v=v, beta=beta, sel_C=sel_C, A_bar=A_bar, vp=vp)
+    for n, t in named.items():
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{n} must be a tensor")
+    dev = q.device
+    if dev.type != "cuda":
+        raise RuntimeError("chunked_scan_abar runs on the GPU only: inputs must be on a cuda device")
+    if q.dim() != 4:
+        raise ValueError(f"q must be (B, L, H, D), got {tuple(q.shape)}")
+    B, L, H, D = q.shape
+    N = v.shape[-1] if v.dim() == 4 else -1
+    shapes = dict(q=(B, L, H, D), k=(B, L, H, D), v=(B, L, H, N), beta=(B, L, H), sel_C=(B, L, H),
+                  A_bar=(B, L, H, N), vp=(B, L, H, N // 2))
+    for n, shp in shapes.items():
+        t = named[n]
+        if tuple(t.shape) != shp:
+            raise ValueError(f"{n} has shape {tuple(t.shape)}, expected {shp}")
+        if t.dtype != torch.bfloat16 or t.device != dev:
+            raise TypeError(f"{n} must be bfloat16 on {dev} (the chunked form takes bf16), got {t.dtype} {t.device}")
+    Q = D if chunk_size is None else int(chunk_size)
+    lib = _lib.load()
+    nbytes = lib.cdssm_chunked_scan_workspace_bytes(B, L, H, D, N, Q)
+    if nbytes <= 0:
+        raise ValueError(f"the chunked form needs N = 16, D in (64, 128) and chunk_size a multiple of 16 in "
+                         f"[16, 256] (N={N} D={D} chunk_size={Q})")
+    if h0 is not None and (h0.dtype != torch.float32 or tuple(h0.shape) != (B, H, N, D) or h0.device != dev):
+        raise ValueError(f"h0 must be float32 ({B}, {H}, {N}, {D}) on {dev}")
+    ins = [t.contiguous() for t in (q, k, v, beta, sel_C, A_bar, vp)]
+    h0c = h0.contiguous() if h0 is not None else None
+    y = torch.empty(B, L, H, N, dtype=q.dtype, device=dev)
+    h_final = torch.empty(B, H, N, D, dtype=torch.float32, device=dev)
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    st = lib.cdssm_chunked_scan_fwd_abar(_lib.DTYPE_CODE[q.dtype], *[_lib.ptr(t) for t in ins], _lib.ptr(h0c),
+                                         _lib.ptr(y), _lib.ptr(h_final), _lib.ptr(ws), B, L, H, D, N, Q,
+                                         _lib.stream_of(dev))
+    _lib.check(st, "cdssm_chunked_scan_fwd_abar")
+    return y, h_final
+
+
 def chunkwise_delta_scan_abar_bwd(dy: Tensor, dh_final: Optional[Tensor], q, k, v, beta, sel_C, A_bar, vp,
                                   fwd_ws: Tensor, has_h0: bool, chunk_size: int):
     """Backward of ``chunkwise_delta_scan_abar_fwd(..., train=True)`` (cdssm_fused_scan_bwd_abar):
