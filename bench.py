@@ -89,6 +89,8 @@ def parse():
                     help="how the forward is launched (default: the library's own choice)")
     ap.add_argument("--only-dropin", action="store_true",
                     help="only time the drop-in SSDChunkwiseScan at C1 (fused and per-pass) and print its JSON")
+    ap.add_argument("--only-chunked", action="store_true",
+                    help="only time the chunked state_dim-16 scan (and the Y route beside it) and print its JSON")
     ap.add_argument("--phase-stamps", type=int, default=0,
                     help="only run this many stamped one-pass forwards of --config (after --warmup plain "
                          "calls) and print the per-wave phase durations of the one-pass kernel as JSON")
@@ -314,6 +316,8 @@ def time_dropin(cfg_name, steps=10, warmup=2):
         leaves = [t.detach().clone().requires_grad_(True) for t in (A, K, V, beta)]
 
         def fb():
+            for t in leaves:
+                t.grad = None  # each step's gradients, not a running sum
             Y = scan(*leaves)
             Y.backward(gY)
 
@@ -399,6 +403,8 @@ def time_dropin_rows(B=4, L=2048, H=16, D=64, N=16, steps=5, warmup=2):
         leaves = [t.detach().clone().requires_grad_(True) for t in (A, K, V, beta)]
 
         def fb():
+            for t in leaves:
+                t.grad = None  # each step's gradients, not a running sum
             Y = m(*leaves)
             Y.backward(gY)
 
@@ -407,6 +413,62 @@ def time_dropin_rows(B=4, L=2048, H=16, D=64, N=16, steps=5, warmup=2):
                      "fwd_bwd_ms": ms_fb,
                      "fwd_bwd_hbm_frac": (by_f + by_b) / (ms_fb * 1e-3) / 1e9 / HBM_PEAK_GBS}
     return out
+
+
+def time_chunked_rows(B=8, L=2048, H=16, D=64, N=16, steps=20, warmup=3):
+    """The block's scan at the reference's default state_dim 16 (8 complex rows per head), inference,
+    bf16, config 4's shape: the chunked (UT) form on the matrix cores (cdssm_chunked_scan_fwd_abar: the
+    readout y = sel_C (Y.q) without Y) against this build's other route for N > 2, the fused SSD form
+    writing Y (B,L,H,16,D) and the readout in torch (what block.py:198-211 computes).  Synthetic inputs
+    (|A_bar| in [0.5, 0.99), unit-norm k and q).  Bytes of the interface: q, k, v, A_bar, vp, beta, sel_C
+    read, y written."""
+    import torch
+    from cdssm_hip import chunked_scan_abar
+    from cdssm_hip.ssd import SSDChunkwiseScan
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(0)
+    R = N // 2
+    ang = torch.rand(B, L, H, R, generator=g) * 2 * math.pi
+    mag = 0.5 + 0.49 * torch.rand(B, L, H, R, generator=g)
+    bf = lambda t: t.to(torch.bfloat16).to(dev)  # noqa: E731
+    A = bf(torch.stack([mag * torch.cos(ang), mag * torch.sin(ang)], -1).flatten(-2))
+    k = torch.randn(B, L, H, D, generator=g)
+    q = torch.randn(B, L, H, D, generator=g)
+    k, q = bf(k / k.norm(dim=-1, keepdim=True)), bf(q / q.norm(dim=-1, keepdim=True))
+    v, vp = bf(torch.randn(B, L, H, N, generator=g)), bf(torch.rand(B, L, H, R, generator=g))
+    beta, sel = bf(torch.rand(B, L, H, generator=g)), bf(torch.rand(B, L, H, generator=g))
+    stream = torch.cuda.current_stream(dev)
+    alg = B * L * H * (2 * D + 2 * N + R + 2 + N) * 2
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    m = SSDChunkwiseScan(D, N)
+
+    def via_y():
+        Vg = v * vp.repeat_interleave(2, dim=-1)
+        Y = m(A, k, Vg, beta)
+        return (Y.float() * q.float().unsqueeze(-2)).sum(-1) * sel.float().unsqueeze(-1)
+
+    with torch.no_grad():
+        ms_c = timed(lambda: chunked_scan_abar(q, k, v, beta, sel, A, vp))
+        ms_y = timed(via_y)
+    return {"workload": f"block scan, state_dim {N}, B{B} L{L} H{H} D{D} bf16 inference", "alg_bytes": alg,
+            "chunked_ms": ms_c, "chunked_tokens_per_s": B * L / (ms_c * 1e-3),
+            "chunked_hbm_frac": alg / (ms_c * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "ssd_form_plus_readout_ms": ms_y,
+            "note": "chunked: cdssm_chunked_scan_fwd_abar (local pass, carry, correction pass; MFMA); "
+                    "ssd_form_plus_readout: SSDChunkwiseScan's fused kernels write Y, torch reads it out"}
 
 
 def time_decode(steps, warmup, B=64, H=16, D=64, prompt=2048):
@@ -668,6 +730,9 @@ def main():
     if args.phase_stamps:
         print(json.dumps(phase_stamps(args.config, args.phase_stamps, args.warmup)), flush=True)
         return
+    if args.only_chunked:
+        print(json.dumps({"chunked_scan_n16": time_chunked_rows(steps=args.steps, warmup=args.warmup)}), flush=True)
+        return
     if args.only_dropin:
         print(json.dumps({"dropin_ssd_scan": time_dropin("C1", steps=args.steps, warmup=args.warmup),
                           "dropin_ssd_scan_n16": time_dropin_rows()}), flush=True)
@@ -796,6 +861,7 @@ def main():
     if not args.no_extras:
         out["dropin_ssd_scan"] = time_dropin("C1")
         out["dropin_ssd_scan_n16"] = time_dropin_rows()
+        out["chunked_scan_n16"] = time_chunked_rows()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg, x, args.cpu_sample_batches)
         if not args.no_extras:

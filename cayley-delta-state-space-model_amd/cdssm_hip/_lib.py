@@ -59,7 +59,7 @@ SIGNATURES = {
     "cdssm_fused_scan_bwd_abar": (_I32, [_I32] + [_P] * 19 + [_I64] * 6 + [_P]),
     "cdssm_ssd_scan_workspace_bytes": (_I64, [_I64] * 6),
     "cdssm_chunked_scan_workspace_bytes": (_I64, [_I64] * 6),
-    "cdssm_chunked_scan_fwd_abar": (_I32, [_I32] + [_P] * 11 + [_I64] * 6 + [_P]),
+    "cdssm_chunked_scan_fwd_abar": (_I32, [_I32] + [_P] * 12 + [_I64] * 6 + [_P]),
     "cdssm_ssd_scan_bwd_workspace_bytes": (_I64, [_I64] * 6),
     "cdssm_ssd_scan_fwd": (_I32, [_I32] + [_P] * 7 + [_I64] * 6 + [_I32, _P]),
     "cdssm_ssd_scan_bwd": (_I32, [_I32] + [_P] * 11 + [_I64] * 6 + [_P]),

@@ -14,8 +14,10 @@ differentiable path instead: conv1d+SiLU, DynamicsFusedFn, NormalizeKQFn and
 the fused scan (HIP, with the reference's backward rules: for state_dim 2 the
 gate-level readout form ChunkwiseDeltaScanAbarFn, which never forms the
 (B,L,H,2,D) Y; otherwise SSDChunkwiseScan) and torch for the rest.  With
-state_dim N != 2 the inference forward also materialises Y through
-SSDChunkwiseScan.
+state_dim 16 (the reference's default) in bf16 the inference forward runs the
+scan, readout and shortcut in the chunked (UT) form on the matrix cores
+(``cdssm_chunked_scan_fwd_abar``), which never forms Y; other state_dim
+materialise Y through SSDChunkwiseScan.
 
 Generation: ``CDSSMLMHeadModel.prefill`` runs the forward over a prompt and keeps
 per-layer decode state (conv window, the scan's R-mode state, GroupNorm running
@@ -35,7 +37,7 @@ import torch.nn as nn
 from . import _lib
 from .ops import DynamicsFusedFn, NormalizeKQFn
 from .decode import DecodeState, decode_step_abar, prefill_abar
-from .scan import ChunkwiseDeltaScanAbarFn, chunkwise_delta_scan_abar
+from .scan import ChunkwiseDeltaScanAbarFn, chunked_scan_abar, chunkwise_delta_scan_abar
 from .ssd import SSDChunkwiseScan
 
 Tensor = torch.Tensor
@@ -625,7 +627,13 @@ class CDSSMBlock(nn.Module):
         Q = self.Q_proj(x_conv).reshape(B, L, H, D)
         K, Q, qk = normalize_kq_qk(K, Q)
         V = V.contiguous()
-        if N != 2:
+        if N == 16 and x.dtype == torch.bfloat16 and D in (64, 128) and cfg.chunk_size % 16 == 0 \
+                and 16 <= cfg.chunk_size <= 256:
+            # the reference's default state_dim: the chunked (UT) form on the matrix cores returns the
+            # retrieved vector sel_C (Y.q + shortcut) (block.py:194-211) without forming Y
+            retrieved, _ = chunked_scan_abar(Q, K, V, beta, sel_C, A_bar, vp, chunk_size=cfg.chunk_size,
+                                             shortcut_scale=self._fp32("shortcut_scale"))
+        elif N != 2:
             # N/2 complex pairs per head (the reference default is 16): Y from SSDChunkwiseScan (its
             # fused kernels, each pair a virtual head sharing k; block.py:194-211 with ssd.py:39-111);
             # the readout and the shortcut in fp32, then rounded to the model dtype

@@ -148,13 +148,16 @@ def chunkwise_delta_scan_abar(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel
 
 
 def chunked_scan_abar(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_C: Tensor, A_bar: Tensor, vp: Tensor,
-                      h0: Optional[Tensor] = None, chunk_size: Optional[int] = None) -> Tuple[Tensor, Tensor]:
+                      h0: Optional[Tensor] = None, chunk_size: Optional[int] = None,
+                      shortcut_scale: Optional[Tensor] = None) -> Tuple[Tensor, Tensor]:
     """The gate-level readout form for state_dim N = 16 in the chunked (UT) form on the matrix cores
     (cdssm_chunked_scan_fwd_abar), inference, bf16: ``(y, h_final)`` with
     ``y = sel_C * einsum('blhsd,blhd->blhs', SSDChunkwiseScan(Q, 16)(A_bar, k, v * vp.repeat_interleave(2, -1),
     beta), q)`` (B,L,H,16) (block.py:194-211 without the shortcut) and the final R-mode state (B,H,16,D) fp32,
     without forming Y.  ``A_bar`` (B,L,H,16) and ``vp`` (B,L,H,8) are DynamicsFusedFn's outputs; q, k (B,L,H,D)
-    with D in {64, 128}; chunk_size (default D) a multiple of 16 up to 256."""
+    with D in {64, 128}; chunk_size (default D) a multiple of 16 up to 256.  With ``shortcut_scale`` (a
+    one-element fp32 tensor on the device) y also carries the current-token shortcut
+    ``sel_C * shortcut_scale * (q.k)^2 * v * vp`` (block.py:202-208): the block's retrieved vector."""
     named = dict(q=q, k=k, v=v, beta=beta, sel_C=sel_C, A_bar=A_bar, vp=vp)
     for n, t in named.items():
         if not isinstance(t, torch.Tensor):
@@ -184,11 +187,14 @@ def chunked_scan_abar(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_C: Tens
         raise ValueError(f"h0 must be float32 ({B}, {H}, {N}, {D}) on {dev}")
     ins = [t.contiguous() for t in (q, k, v, beta, sel_C, A_bar, vp)]
     h0c = h0.contiguous() if h0 is not None else None
+    sc = None
+    if shortcut_scale is not None:
+        sc = shortcut_scale.detach().reshape(1).to(device=dev, dtype=torch.float32).contiguous()
     y = torch.empty(B, L, H, N, dtype=q.dtype, device=dev)
     h_final = torch.empty(B, H, N, D, dtype=torch.float32, device=dev)
     ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
     st = lib.cdssm_chunked_scan_fwd_abar(_lib.DTYPE_CODE[q.dtype], *[_lib.ptr(t) for t in ins], _lib.ptr(h0c),
-                                         _lib.ptr(y), _lib.ptr(h_final), _lib.ptr(ws), B, L, H, D, N, Q,
+                                         _lib.ptr(sc), _lib.ptr(y), _lib.ptr(h_final), _lib.ptr(ws), B, L, H, D, N, Q,
                                          _lib.stream_of(dev))
     _lib.check(st, "cdssm_chunked_scan_fwd_abar")
     return y, h_final

@@ -1,8 +1,9 @@
 // Chunked (UT-transform) scan on the gfx950 matrix cores for state_dim N = 16,
 // the reference's default (config/model.py:128), gate-level readout form:
 //   y = sel_C (Y . q),  Y = SSDChunkwiseScan(A_bar, K, V vp, beta)
-// (ssd.py:39-111 with block.py:194-211, the shortcut excepted), without
-// forming Y (B,L,H,N,D).  bf16 inputs, fp32 states.
+// (ssd.py:39-111 with block.py:194-211; the current-token shortcut of
+// block.py:202-205 optionally folded in), without forming Y (B,L,H,N,D).
+// bf16 inputs, fp32 states.
 //
 // A head's N/2 = 8 complex state rows share k, q and beta; only their
 // transitions a_t and values differ.  So a block of 16 tokens of the chunk
@@ -55,6 +56,7 @@ constexpr int cs_lds_floats() {
 
 struct CsArgs {
   const uint16_t *q, *k, *v, *beta, *sel, *a, *vp;
+  const float* scut;  // shortcut scale (one fp32 on the device) or null
   float* yloc;  // (B, L, H, 16) local readout
   float* st;    // (B, NC, H, 16, D): the chunk's z_end, then (carry) its entering state
   float2* ap;   // (B, NC, H, 8): the chunk's product of a
@@ -122,6 +124,7 @@ __global__ __launch_bounds__(kWave* kCsWaves) void chunked_sweep_kernel(CsArgs p
     }
     // the lane's token: a of rows 2g, 2g+1, beta, and w = beta vp v (local) or sel_C (corr)
     float ar[2] = {1.0f, 1.0f}, ai[2] = {0.0f, 0.0f}, wr[2] = {0.0f, 0.0f}, wi[2] = {0.0f, 0.0f};
+    float vr[2] = {0.0f, 0.0f}, vi[2] = {0.0f, 0.0f};  // vp v (the shortcut's value)
     float bt = 0.0f, sel = 0.0f;
     if (ok) {
       const uint2 araw = *reinterpret_cast<const uint2*>(p.a + tk * 16 + 4 * g);
@@ -135,16 +138,22 @@ __global__ __launch_bounds__(kWave* kCsWaves) void chunked_sweep_kernel(CsArgs p
       } else {
         const uint2 vraw = *reinterpret_cast<const uint2*>(p.v + tk * 16 + 4 * g);
         const uint32_t praw = *reinterpret_cast<const uint32_t*>(p.vp + tk * 8 + 2 * g);
-        const float s0 = bt * bf16_lo(praw), s1 = bt * bf16_hi(praw);
-        wr[0] = s0 * bf16_lo(vraw.x);
-        wi[0] = s0 * bf16_hi(vraw.x);
-        wr[1] = s1 * bf16_lo(vraw.y);
-        wi[1] = s1 * bf16_hi(vraw.y);
+        const float p0 = bf16_lo(praw), p1 = bf16_hi(praw);
+        vr[0] = p0 * bf16_lo(vraw.x);
+        vi[0] = p0 * bf16_hi(vraw.x);
+        vr[1] = p1 * bf16_lo(vraw.y);
+        vi[1] = p1 * bf16_hi(vraw.y);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          wr[u] = bt * vr[u];
+          wi[u] = bt * vi[u];
+        }
       }
     }
 
     // Gram rows: lane (g, j) gets row j of G = K K^T and of P = Q K^T (P[t][s] = q_t . k_s)
     float grow[16], prow[16];
+    float qk = 0.0f;  // q_t . k_t
     {
       f32x4_t gt = {0.0f, 0.0f, 0.0f, 0.0f}, pt = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -170,6 +179,7 @@ __global__ __launch_bounds__(kWave* kCsWaves) void chunked_sweep_kernel(CsArgs p
       }
 #pragma unroll
       for (int s = 0; s < 16; ++s) {
+        qk = s == j ? prow[s] : qk;
         grow[s] = s < j ? grow[s] : 0.0f;                        // the solve: s < t
         prow[s] = (CORR ? s < j : s <= j) ? prow[s] : 0.0f;      // readout: after (local) / before (corr) token t
       }
@@ -291,6 +301,15 @@ __global__ __launch_bounds__(kWave* kCsWaves) void chunked_sweep_kernel(CsArgs p
         o.y = pack_bf16x2(sel * (l.z + ro[2]), sel * (l.w + ro[3]));
         *reinterpret_cast<uint2*>(p.y + tk * 16 + 4 * g) = o;
       } else {
+        if (p.scut) {
+          // the current-token shortcut through the readout (block.py:202-208): scale (q.k)^2 vp v
+          const float sq = *p.scut * qk * qk;
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            ro[2 * u] = fmaf(sq, vr[u], ro[2 * u]);
+            ro[2 * u + 1] = fmaf(sq, vi[u], ro[2 * u + 1]);
+          }
+        }
         *reinterpret_cast<float4*>(yl) = make_float4(ro[0], ro[1], ro[2], ro[3]);
       }
     }
@@ -365,7 +384,7 @@ __global__ __launch_bounds__(256) void chunked_carry_kernel(float* __restrict__ 
   const int64_t b = bh / H;
   const int64_t hrow = (bh * kCsCols + 2 * n) * D + d;
   float sr = h0 ? h0[hrow] : 0.0f, si = h0 ? h0[hrow + D] : 0.0f;
-  constexpr int U = 4;
+  constexpr int U = 16;  // chunks whose loads are in flight at once (they do not depend on the carry)
 #pragma unroll 1
   for (int c0 = 0; c0 < NC; c0 += U) {
     float zr[U], zi[U];
@@ -448,7 +467,8 @@ extern "C" int64_t cdssm_chunked_scan_workspace_bytes(int64_t B, int64_t L, int6
 
 extern "C" int cdssm_chunked_scan_fwd_abar(int dtype, const void* q, const void* k, const void* v, const void* beta,
                                            const void* sel_c, const void* a_bar, const void* vp, const float* h0,
-                                           void* y, float* h_final, float* workspace, int64_t B, int64_t L,
+                                           const float* shortcut_scale, void* y, float* h_final, float* workspace,
+                                           int64_t B, int64_t L,
                                            int64_t H, int64_t D, int64_t N, int64_t chunk, hipStream_t stream) {
   const char* op = "cdssm_chunked_scan_fwd_abar";
   if (dtype != 1) {
@@ -487,6 +507,7 @@ extern "C" int cdssm_chunked_scan_fwd_abar(int dtype, const void* q, const void*
   a.sel = static_cast<const uint16_t*>(sel_c);
   a.a = static_cast<const uint16_t*>(a_bar);
   a.vp = static_cast<const uint16_t*>(vp);
+  a.scut = shortcut_scale;
   a.yloc = workspace + w.yloc;
   a.st = workspace + w.st;
   a.ap = reinterpret_cast<float2*>(workspace + w.ap);

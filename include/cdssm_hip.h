@@ -125,21 +125,23 @@ int cdssm_fused_scan_bwd_abar(int dtype, const void* q, const void* k, const voi
  * config/model.py:128) in the chunked (UT) form on the matrix cores, inference:
  * replaces SSDChunkwiseScan.forward (ssd.py:39-111: IntraChunkScanFn,
  * InterChunkScanFn, ExactCorrectionFn, Y = local_h + correction) followed by
- * the block's readout y = sel_C * (Y . q) (block.py:194-211, the shortcut
- * excepted) without forming Y (B,L,H,16,D).  bf16 only (dtype 1): q, k
- * (B,L,H,D) 16-byte aligned, v (B,L,H,16) and a_bar (B,L,H,16) 8-byte aligned,
- * vp (B,L,H,8) 4-byte aligned, beta, sel_c (B,L,H); h0 (B,H,16,D) fp32 or NULL;
- * outputs y (B,L,H,16) bf16 (8-byte aligned) and h_final (B,H,16,D) fp32 or
- * NULL.  D in {64, 128}; chunk a multiple of 16 in [16, 256].  workspace:
+ * the block's readout y = sel_C * (Y . q) (block.py:194-211) without forming
+ * Y (B,L,H,16,D).  bf16 only (dtype 1): q, k (B,L,H,D) 16-byte aligned, v
+ * (B,L,H,16) and a_bar (B,L,H,16) 8-byte aligned, vp (B,L,H,8) 4-byte aligned,
+ * beta, sel_c (B,L,H); h0 (B,H,16,D) fp32 or NULL; shortcut_scale: one fp32 on
+ * the device, or NULL -- when given, y also carries the current-token shortcut
+ * sel_C * scale * (q.k)^2 * vp v (block.py:202-208), as the block's retrieved
+ * vector; outputs y (B,L,H,16) bf16 (8-byte aligned) and h_final (B,H,16,D)
+ * fp32 or NULL.  D in {64, 128}; chunk a multiple of 16 in [16, 256].  workspace:
  * cdssm_chunked_scan_workspace_bytes() bytes, 16-byte aligned (-1: the shape
  * is not supported).  Three launches: the local pass, the carry, the
  * correction pass.
  */
 int64_t cdssm_chunked_scan_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t D, int64_t N, int64_t chunk);
 int cdssm_chunked_scan_fwd_abar(int dtype, const void* q, const void* k, const void* v, const void* beta,
-                                const void* sel_c, const void* a_bar, const void* vp, const float* h0, void* y,
-                                float* h_final, float* workspace, int64_t B, int64_t L, int64_t H, int64_t D,
-                                int64_t N, int64_t chunk, hipStream_t stream);
+                                const void* sel_c, const void* a_bar, const void* vp, const float* h0,
+                                const float* shortcut_scale, void* y, float* h_final, float* workspace, int64_t B,
+                                int64_t L, int64_t H, int64_t D, int64_t N, int64_t chunk, hipStream_t stream);
 
 /*
  * Training forward (no counterpart in the reference; the reference keeps its

@@ -6,7 +6,8 @@ v (B,L,H,16) and vp (B,L,H,8) are drawn directly, rounded once to bf16, and the 
 with the oracle's ssd_chunkwise_scan + readout in fp64 on the same rounded values.  Heads with strong
 decay (|a| <= 0.02, so a 16-token product falls below 2^-48) run the kernel's true-units blocks; the
 others its rescaled blocks; a token with a = 0 exactly is included.  Tolerances (bf16 inputs, fp32
-state): y <= 2e-2 normwise, final-state norms <= 1e-3.
+state): y <= 2e-2 normwise, final-state norms <= 1e-3.  Cases with a shortcut scale also check the
+current-token shortcut folded into y (block.py:202-208).
 """
 
 import math
@@ -41,42 +42,43 @@ def draw(B, L, H, D, N=16, seed=0, strong_heads=(), h0_std=0.0):
     return x
 
 
-def oracle_of(x, chunk, bsel, hsel):
+def oracle_of(x, chunk, bsel, hsel, shortcut=0.0):
     sl = lambda t: t.double()[bsel][:, :, hsel]  # noqa: E731
     N = x["v"].shape[-1]
     Vg = sl(x["v"]) * sl(x["vp"]).repeat_interleave(2, dim=-1)
     h0 = x["h0"].double()[bsel][:, hsel] if x["h0"] is not None else None
     Y, hr = o.ssd_chunkwise_scan(sl(x["A_bar"]), sl(x["k"]), Vg, sl(x["beta"]), chunk, N, h0=h0, return_final=True)
-    return o.readout(Y, sl(x["q"]), sl(x["sel_C"])), hr
+    return o.readout(Y, sl(x["q"]), sl(x["sel_C"]), K=sl(x["k"]), V_gated=Vg, shortcut_scale=shortcut), hr
 
 
 CASES = [
-    # name, B, L, H, D, chunk, strong-decay heads, h0 std
-    ("D64_chunk64_ragged_h0", 2, 300, 4, 64, 64, (), 0.1),
-    ("D64_strong_decay_heads", 1, 256, 4, 64, 64, (1, 3), 0.0),
-    ("D64_chunk16", 1, 100, 2, 64, 16, (1,), 0.1),
-    ("D64_chunk48_items_not_multiple_of_4", 1, 130, 3, 64, 48, (), 0.0),
-    ("D128_chunk64", 1, 200, 3, 128, 64, (2,), 0.1),
-    ("D128_chunk128", 2, 300, 2, 128, 128, (), 0.0),
-    ("D64_chunk256", 1, 600, 2, 64, 256, (0,), 0.0),
-    ("C4_shape_B8_L2048_H16", 8, 2048, 16, 64, 64, (5,), 0.0),
+    # name, B, L, H, D, chunk, strong-decay heads, h0 std, shortcut scale
+    ("D64_chunk64_ragged_h0", 2, 300, 4, 64, 64, (), 0.1, None),
+    ("D64_strong_decay_heads", 1, 256, 4, 64, 64, (1, 3), 0.0, None),
+    ("D64_chunk16_shortcut", 1, 100, 2, 64, 16, (1,), 0.1, 0.7),
+    ("D64_chunk48_items_not_multiple_of_4", 1, 130, 3, 64, 48, (), 0.0, None),
+    ("D128_chunk64_shortcut", 1, 200, 3, 128, 64, (2,), 0.1, -1.3),
+    ("D128_chunk128", 2, 300, 2, 128, 128, (), 0.0, None),
+    ("D64_chunk256", 1, 600, 2, 64, 256, (0,), 0.0, None),
+    ("C4_shape_B8_L2048_H16_shortcut", 8, 2048, 16, 64, 64, (5,), 0.0, 0.5),
 ]
 
 
-@pytest.mark.parametrize("name,B,L,H,D,chunk,strong,h0_std", CASES, ids=[c[0] for c in CASES])
-def test_chunked_scan_matches_oracle(name, B, L, H, D, chunk, strong, h0_std):
+@pytest.mark.parametrize("name,B,L,H,D,chunk,strong,h0_std,scut", CASES, ids=[c[0] for c in CASES])
+def test_chunked_scan_matches_oracle(name, B, L, H, D, chunk, strong, h0_std, scut):
     from cdssm_hip import chunked_scan_abar
-    log(f"[chunked N16] {name}: B{B} L{L} H{H} D{D} chunk={chunk} strong={strong}")
+    log(f"[chunked N16] {name}: B{B} L{L} H{H} D{D} chunk={chunk} strong={strong} shortcut={scut}")
     x = draw(B, L, H, D, seed=3, strong_heads=strong, h0_std=h0_std)
     g = {n: (t.to(DEV) if t is not None else None) for n, t in x.items()}
+    sc = torch.tensor([scut], device=DEV) if scut is not None else None
     y, hf = chunked_scan_abar(g["q"], g["k"], g["v"], g["beta"], g["sel_C"], g["A_bar"], g["vp"], h0=g["h0"],
-                              chunk_size=chunk)
+                              chunk_size=chunk, shortcut_scale=sc)
     torch.cuda.synchronize()
     y, hf = y.cpu(), hf.cpu()
     assert torch.isfinite(y.float()).all() and torch.isfinite(hf).all()
     bsel = [0, B - 1] if B > 2 else list(range(B))
     hsel = sorted({0, H - 1, *strong}) if H > 4 else list(range(H))
-    yr, hr = oracle_of(x, chunk, bsel, hsel)
+    yr, hr = oracle_of(x, chunk, bsel, hsel, shortcut=scut or 0.0)
     ys, hs = y[bsel][:, :, hsel], hf[bsel][:, hsel]
     ey, eh, en = rel(ys, yr), rel(hs, hr), state_norm_rel(hs, hr)
     log(f"   rel err y {ey:.2e}  h_final {eh:.2e}  state-norm {en:.2e}")

@@ -55,9 +55,11 @@ def _model(d_model, n_layers, vocab, d_inner, L_ctx, dtype, seed=0, state_dim=2)
     ("fp32_D128_heads", torch.float32, 64, 2, 256, 1, 150, 1e-3, 2),
     ("bf16_small", torch.bfloat16, 128, 2, 128, 2, 200, 2e-2, 2),
     ("bf16_c4_width_2_layers", torch.bfloat16, 1024, 2, 1024, 1, 256, 2e-2, 2),
-    # the reference's default state_dim 16 (config/model.py:128): the block runs the per-pass ops
+    # the reference's default state_dim 16 (config/model.py:128): fp32 runs the fused SSD form and the
+    # readout in torch; bf16 the chunked MFMA form with the readout and shortcut folded in
     ("fp32_state16", torch.float32, 128, 2, 256, 2, 150, 1e-3, 16),
     ("bf16_state16", torch.bfloat16, 128, 2, 256, 1, 200, 2e-2, 16),
+    ("bf16_state16_c4_width_ragged", torch.bfloat16, 1024, 2, 1024, 2, 333, 2e-2, 16),
 ])
 def test_lm_forward_matches_oracle(name, dtype, d_model, n_layers, d_inner, B, L, tol, N):
     log(f"[lm fwd] {name}: d_model {d_model} layers {n_layers} d_inner {d_inner} B{B} L{L} N{N} {dtype}")
