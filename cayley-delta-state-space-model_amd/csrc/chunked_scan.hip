@@ -73,6 +73,25 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_wave_barrier();
 }
 
+// Two floats as bf16 hi + lo parts, packed in pairs: hi is x truncated to bf16 (its upper 16 bits, taken
+// with one v_perm), lo = bf16(x - hi) rounded to nearest; hi + lo = x within 2^-16 |x|.
+__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+  const uint32_t u0 = __float_as_uint(x0), u1 = __float_as_uint(x1);
+  hi = __builtin_amdgcn_perm(u1, u0, 0x07060302u);
+  lo = pack_bf16x2(x0 - __uint_as_float(u0 & 0xffff0000u), x1 - __uint_as_float(u1 & 0xffff0000u));
+}
+
+// One block's inputs of a lane (token j of the block): the k and q fragments and the token's scalars,
+// loaded a block ahead of their use.
+template <int KS>
+struct CsBlockIn {
+  bf16x8_t kf[KS], qf[KS];
+  uint2 araw, vraw;
+  uint32_t praw;
+  uint16_t braw, sraw;
+  bool ok;
+};
+
 // x from lane i + N of the lane's 16-lane row; lanes past the row get `fill` (DPP row_shl)
 template <int N>
 __device__ __forceinline__ float row_shl(float x, float fill) {
@@ -111,33 +130,52 @@ __global__ __launch_bounds__(kWave* kCsWaves) void chunked_sweep_kernel(CsArgs p
   float par[2] = {1.0f, 1.0f}, pai[2] = {0.0f, 0.0f};  // product of a over the chunk (local)
   const bf16x8_t zero8 = {};
 
-#pragma unroll 1
-  for (int ib = 0; ib * 16 < p.Q; ++ib) {
+  // the inputs of block ib (token j of the block; tokens past the chunk read as inert: a = 1, k = q = 0, beta = 0)
+  auto load_block = [&](int ib, CsBlockIn<KS>& in) {
     const int tl = 16 * ib + j;
-    const bool ok = tl < nt;
+    in.ok = tl < nt;
     const int64_t tk = (row0 + min(tl, nt - 1)) * p.H + h;  // (b, t, h), clamped into the chunk
-    bf16x8_t kf[KS], qf[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      kf[ks] = ok ? load_frag(p.k + tk * D + 32 * ks + 8 * g) : zero8;
-      qf[ks] = ok ? load_frag(p.q + tk * D + 32 * ks + 8 * g) : zero8;
+      in.kf[ks] = in.ok ? load_frag(p.k + tk * D + 32 * ks + 8 * g) : zero8;
+      in.qf[ks] = in.ok ? load_frag(p.q + tk * D + 32 * ks + 8 * g) : zero8;
     }
+    in.araw = in.ok ? *reinterpret_cast<const uint2*>(p.a + tk * 16 + 4 * g) : make_uint2(0x3f80u, 0x3f80u);
+    in.braw = in.ok ? p.beta[tk] : uint16_t(0);
+    if constexpr (CORR) {
+      in.sraw = in.ok ? p.sel[tk] : uint16_t(0);
+    } else {
+      in.vraw = in.ok ? *reinterpret_cast<const uint2*>(p.v + tk * 16 + 4 * g) : make_uint2(0u, 0u);
+      in.praw = in.ok ? *reinterpret_cast<const uint32_t*>(p.vp + tk * 8 + 2 * g) : 0u;
+    }
+  };
+  CsBlockIn<KS> nxt;
+  load_block(0, nxt);
+
+#pragma unroll 1
+  for (int ib = 0; ib * 16 < p.Q; ++ib) {
+    const CsBlockIn<KS> cur = nxt;
+    if ((ib + 1) * 16 < p.Q) load_block(ib + 1, nxt);
+    const int tl = 16 * ib + j;
+    const bool ok = cur.ok;
+    const int64_t tk = (row0 + min(tl, nt - 1)) * p.H + h;
+    const bf16x8_t* kf = cur.kf;
+    const bf16x8_t* qf = cur.qf;
     // the lane's token: a of rows 2g, 2g+1, beta, and w = beta vp v (local) or sel_C (corr)
-    float ar[2] = {1.0f, 1.0f}, ai[2] = {0.0f, 0.0f}, wr[2] = {0.0f, 0.0f}, wi[2] = {0.0f, 0.0f};
+    float ar[2], ai[2], wr[2] = {0.0f, 0.0f}, wi[2] = {0.0f, 0.0f};
     float vr[2] = {0.0f, 0.0f}, vi[2] = {0.0f, 0.0f};  // vp v (the shortcut's value)
-    float bt = 0.0f, sel = 0.0f;
-    if (ok) {
-      const uint2 araw = *reinterpret_cast<const uint2*>(p.a + tk * 16 + 4 * g);
-      ar[0] = bf16_lo(araw.x);
-      ai[0] = bf16_hi(araw.x);
-      ar[1] = bf16_lo(araw.y);
-      ai[1] = bf16_hi(araw.y);
-      bt = bf16_to_f32(p.beta[tk]);
+    ar[0] = bf16_lo(cur.araw.x);
+    ai[0] = bf16_hi(cur.araw.x);
+    ar[1] = bf16_lo(cur.araw.y);
+    ai[1] = bf16_hi(cur.araw.y);
+    const float bt = bf16_to_f32(cur.braw);
+    float sel = 0.0f;
+    {
       if constexpr (CORR) {
-        sel = bf16_to_f32(p.sel[tk]);
+        sel = bf16_to_f32(cur.sraw);
       } else {
-        const uint2 vraw = *reinterpret_cast<const uint2*>(p.v + tk * 16 + 4 * g);
-        const uint32_t praw = *reinterpret_cast<const uint32_t*>(p.vp + tk * 8 + 2 * g);
+        const uint2 vraw = cur.vraw;
+        const uint32_t praw = cur.praw;
         const float p0 = bf16_lo(praw), p1 = bf16_hi(praw);
         vr[0] = p0 * bf16_lo(vraw.x);
         vi[0] = p0 * bf16_hi(vraw.x);
@@ -195,17 +233,14 @@ __global__ __launch_bounds__(kWave* kCsWaves) void chunked_sweep_kernel(CsArgs p
       wave_lds_sync();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        bf16x8_t hhi, hlo;
         const float* src = hs + j * (D + 4) + 32 * ks + 8 * g;
         const float4 x0 = *reinterpret_cast<const float4*>(src), x1 = *reinterpret_cast<const float4*>(src + 4);
-        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float hi, lo;
-          split_bf16(xs[e], hi, lo);
-          hhi[e] = __builtin_bit_cast(__bf16, f32_to_bf16(hi));
-          hlo[e] = __builtin_bit_cast(__bf16, f32_to_bf16(lo));
-        }
+        uint4 uh, ul;
+        split_pair(x0.x, x0.y, uh.x, ul.x);
+        split_pair(x0.z, x0.w, uh.y, ul.y);
+        split_pair(x1.x, x1.y, uh.z, ul.z);
+        split_pair(x1.z, x1.w, uh.w, ul.w);
+        const bf16x8_t hhi = __builtin_bit_cast(bf16x8_t, uh), hlo = __builtin_bit_cast(bf16x8_t, ul);
         ckh = mfma16(hhi, kf[ks], ckh);
         ckh = mfma16(hlo, kf[ks], ckh);
         cqh = mfma16(hhi, qf[ks], cqh);
@@ -241,7 +276,8 @@ __global__ __launch_bounds__(kWave* kCsWaves) void chunked_sweep_kernel(CsArgs p
       if (!exact) {
         // rescaled frame: r_t = w_t / g_t - beta_t (k_t . H), e^_t = r_t - beta_t sum_{s<t} G_ts e^_s
         const float m2 = gr[u] * gr[u] + gi[u] * gi[u];
-        const float ir = gr[u] / m2, ii = -gi[u] / m2;
+        const float rm = __builtin_amdgcn_rcpf(m2);
+        const float ir = gr[u] * rm, ii = -gi[u] * rm;
         const float rr = wr[u] * ir - wi[u] * ii - bt * khr, ri = wr[u] * ii + wi[u] * ir - bt * khi;
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
@@ -323,11 +359,13 @@ __global__ __launch_bounds__(kWave* kCsWaves) void chunked_sweep_kernel(CsArgs p
     };
     if (exact) scale_state();
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float hi, lo;
-      split_bf16(ec[r], hi, lo);
-      et[(4 * g + r) * 32 + j] = f32_to_bf16(hi);
-      et[(4 * g + r) * 32 + 16 + j] = f32_to_bf16(lo);
+    for (int r = 0; r < 4; r += 2) {
+      uint32_t hi, lo;
+      split_pair(ec[r], ec[r + 1], hi, lo);
+      et[(4 * g + r) * 32 + j] = uint16_t(hi & 0xffffu);
+      et[(4 * g + r + 1) * 32 + j] = uint16_t(hi >> 16);
+      et[(4 * g + r) * 32 + 16 + j] = uint16_t(lo & 0xffffu);
+      et[(4 * g + r + 1) * 32 + 16 + j] = uint16_t(lo >> 16);
     }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
