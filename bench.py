@@ -57,6 +57,7 @@ def recorded_traffic(path, key="traffic_bytes_per_launch"):
 FWD_BWD_TRAFFIC = os.path.join(ROOT, "profiles", "fused_fwd_bwd_C1_C2_hbm_traffic.txt")
 MFMA_PROFILE = os.path.join(ROOT, "profiles", "fused_fwd_onepass_C1_sq_counters.md")
 MFMA_VARIANT_PROFILE = os.path.join(ROOT, "profiles", "mfma_correction_vs_sequential_C1_C2.md")
+CHUNKED_PROFILE = os.path.join(ROOT, "profiles", "chunked_scan_n16_C4_counters.md")
 
 
 def mfma_util(kernel):
@@ -70,7 +71,12 @@ def mfma_util(kernel):
             "source": os.path.relpath(MFMA_PROFILE, ROOT),
             "chunked_mfma_correction": {"path": "four_launch_mfma (fused_fwd_corr_sweep_kernel, not default)",
                                         "value": recorded_traffic(MFMA_VARIANT_PROFILE, "mfma_util_C1"),
-                                        "source": os.path.relpath(MFMA_VARIANT_PROFILE, ROOT)}}
+                                        "source": os.path.relpath(MFMA_VARIANT_PROFILE, ROOT)},
+            "state_dim16_block_scan": {"path": "cdssm_chunked_scan_fwd_abar (chunked_sweep_kernel, the block's "
+                                               "default at state_dim 16 bf16)",
+                                       "value_local_pass": recorded_traffic(CHUNKED_PROFILE, "mfma_util_local"),
+                                       "value_correction_pass": recorded_traffic(CHUNKED_PROFILE, "mfma_util_corr"),
+                                       "source": os.path.relpath(CHUNKED_PROFILE, ROOT)}}
 
 
 def parse():
@@ -467,6 +473,9 @@ def time_chunked_rows(B=8, L=2048, H=16, D=64, N=16, steps=20, warmup=3):
             "chunked_ms": ms_c, "chunked_tokens_per_s": B * L / (ms_c * 1e-3),
             "chunked_hbm_frac": alg / (ms_c * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "ssd_form_plus_readout_ms": ms_y,
+            "mfma_util": {"local_pass": recorded_traffic(CHUNKED_PROFILE, "mfma_util_local"),
+                          "correction_pass": recorded_traffic(CHUNKED_PROFILE, "mfma_util_corr"),
+                          "source": os.path.relpath(CHUNKED_PROFILE, ROOT)},
             "note": "chunked: cdssm_chunked_scan_fwd_abar (local pass, carry, correction pass; MFMA); "
                     "ssd_form_plus_readout: SSDChunkwiseScan's fused kernels write Y, torch reads it out"}
 
