@@ -590,16 +590,18 @@ def time_lm_decode(steps=20, warmup=3, B=64, prompt=2048):
                     "residual (skinny GEMM); then the final RMSNorm and the tied head (library GEMM)"}
 
 
-def time_lm_forward(steps=5, warmup=2):
+def time_lm_forward(steps=5, warmup=2, state_dim=2):
     """Config-4 LM forward: B8 L2048, d_model 1024, 24 layers, 16 heads x 64 (d_inner = 1024,
-    as the config states), state_dim 2, vocab 32000, bf16, random init (the reference's
-    init scheme), uniform random tokens.  Tokens/s of the whole forward (logits included)."""
+    as the config states), state_dim 2 (or the reference's default 16), vocab 32000, bf16, random init
+    (the reference's init scheme), uniform random tokens.  Tokens/s of the whole forward (logits
+    included)."""
     import torch
     from cdssm_hip.lm import CDSSMConfig, CDSSMLMHeadModel
 
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
-    cfg = CDSSMConfig(d_model=1024, n_layers=24, context_length=2048, vocab_size=32000, state_dim=2, d_inner=1024)
+    cfg = CDSSMConfig(d_model=1024, n_layers=24, context_length=2048, vocab_size=32000, state_dim=state_dim,
+                      d_inner=1024)
     m = CDSSMLMHeadModel(cfg).to(torch.bfloat16).to(dev).eval()
     B, L = 8, 2048
     ids = torch.randint(0, cfg.vocab_size, (B, L), generator=torch.Generator().manual_seed(1)).to(dev)
@@ -617,11 +619,30 @@ def time_lm_forward(steps=5, warmup=2):
     ms = e0.elapsed_time(e1) / steps
     n_params = sum(p.numel() for p in m.parameters())
     flops = 2.0 * n_params * B * L  # dense GEMM work; the scan adds O(L D) per head
-    return {"workload": "config 4: LM forward B8 L2048 d_model 1024 24 layers 16x64 heads N=2 vocab 32000 bf16",
+    return {"workload": f"config 4: LM forward B8 L2048 d_model 1024 24 layers 16x64 heads N={state_dim} vocab "
+                        "32000 bf16",
             "ms_per_step": ms, "tokens_per_s": B * L / (ms * 1e-3), "params": n_params,
             "gemm_tflops": flops / (ms * 1e-3) / 1e12,
             "note": "GEMMs through torch (hipBLASLt); RMSNorm, conv1d+SiLU, dynamics, K/Q norm + q.k, scan, shortcut, "
                     "GroupNorm + gate on the HIP kernels"}
+
+
+def time_lm_forward_state16(steps=3, warmup=1):
+    """time_lm_forward at the reference's default state_dim 16: the block's scan in the chunked MFMA form
+    (its default there) and, for comparison, through SSDChunkwiseScan's Y read out in torch."""
+    from cdssm_hip.lm import CDSSMBlock
+    prev = CDSSMBlock.chunked_scan
+    try:
+        CDSSMBlock.chunked_scan = True
+        chunked = time_lm_forward(steps, warmup, state_dim=16)
+        CDSSMBlock.chunked_scan = False
+        via_y = time_lm_forward(steps, warmup, state_dim=16)
+    finally:
+        CDSSMBlock.chunked_scan = prev
+    return {"workload": chunked["workload"], "chunked_ms_per_step": chunked["ms_per_step"],
+            "chunked_tokens_per_s": chunked["tokens_per_s"], "via_y_ms_per_step": via_y["ms_per_step"],
+            "note": "chunked: each block's scan, readout and shortcut in one cdssm_chunked_scan_fwd_abar call; "
+                    "via_y: SSDChunkwiseScan's fused kernels write Y and torch reads it out"}
 
 
 def time_block_train(steps=5, warmup=2, B=8, L=2048):
@@ -740,7 +761,8 @@ def main():
         print(json.dumps(phase_stamps(args.config, args.phase_stamps, args.warmup)), flush=True)
         return
     if args.only_chunked:
-        print(json.dumps({"chunked_scan_n16": time_chunked_rows(steps=args.steps, warmup=args.warmup)}), flush=True)
+        print(json.dumps({"chunked_scan_n16": time_chunked_rows(steps=args.steps, warmup=args.warmup),
+                          "lm_forward_state16": time_lm_forward_state16()}), flush=True)
         return
     if args.only_dropin:
         print(json.dumps({"dropin_ssd_scan": time_dropin("C1", steps=args.steps, warmup=args.warmup),
@@ -871,6 +893,8 @@ def main():
         out["dropin_ssd_scan"] = time_dropin("C1")
         out["dropin_ssd_scan_n16"] = time_dropin_rows()
         out["chunked_scan_n16"] = time_chunked_rows()
+        if not args.no_fwd_bwd:
+            out["lm_forward_state16"] = time_lm_forward_state16()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(cfg, x, args.cpu_sample_batches)
         if not args.no_extras:

@@ -505,6 +505,9 @@ class CDSSMBlock(nn.Module):
     # training with state_dim 2 takes the readout-form scan (ChunkwiseDeltaScanAbarFn, no Y); False:
     # SSDChunkwiseScan's Y read out in torch (the reference's op sequence; the same gradients)
     readout_scan: bool = True
+    # inference with state_dim 16 in bf16 takes the chunked MFMA form (cdssm_chunked_scan_fwd_abar, no Y);
+    # False: SSDChunkwiseScan's Y read out in fp32 torch (the reference's op sequence)
+    chunked_scan: bool = True
 
     def __init__(self, config: CDSSMConfig, layer_idx: int = 0):
         super().__init__()
@@ -627,8 +630,8 @@ class CDSSMBlock(nn.Module):
         Q = self.Q_proj(x_conv).reshape(B, L, H, D)
         K, Q, qk = normalize_kq_qk(K, Q)
         V = V.contiguous()
-        if N == 16 and x.dtype == torch.bfloat16 and D in (64, 128) and cfg.chunk_size % 16 == 0 \
-                and 16 <= cfg.chunk_size <= 256:
+        if self.chunked_scan and N == 16 and x.dtype == torch.bfloat16 and D in (64, 128) \
+                and cfg.chunk_size % 16 == 0 and 16 <= cfg.chunk_size <= 256:
             # the reference's default state_dim: the chunked (UT) form on the matrix cores returns the
             # retrieved vector sel_C (Y.q + shortcut) (block.py:194-211) without forming Y
             retrieved, _ = chunked_scan_abar(Q, K, V, beta, sel_C, A_bar, vp, chunk_size=cfg.chunk_size,
