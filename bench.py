@@ -647,49 +647,64 @@ def time_lm_forward_state16(steps=3, warmup=1):
 
 def time_block_train(steps=5, warmup=2, B=8, L=2048):
     """One training step through one CDSSMBlock at config 4's shape (d_model 1024, 16 heads x 64,
-    d_inner 1024, state_dim 2, bf16; B8 L2048): forward and backward of sum(out * g), the way the
-    reference trains (block.py:140-229 under autograd, trainer.py:235-247).  Timed with the readout-form
-    scan (no (B,L,H,2,D) Y) and with SSDChunkwiseScan's Y read out in torch, the reference's op sequence."""
+    d_inner 1024, bf16; B8 L2048): forward and backward of sum(out * g), the way the reference trains
+    (block.py:140-229 under autograd, trainer.py:235-247; gradients cleared each step as
+    zero_grad(set_to_none=True) does).  state_dim 2 with the readout-form scan (no (B,L,H,2,D) Y) and with
+    SSDChunkwiseScan's Y read out (the reference's op sequence); state_dim 16 (the reference's default)
+    through SSDChunkwiseScan's Y and the HIP readout of it."""
     import torch
     from cdssm_hip.lm import CDSSMBlock, CDSSMConfig
 
     dev = torch.device("cuda:0")
-    torch.manual_seed(0)
-    cfg = CDSSMConfig(d_model=1024, n_layers=24, context_length=2048, vocab_size=32000, state_dim=2, d_inner=1024)
-    blk = CDSSMBlock(cfg, 0).to(torch.bfloat16).to(dev).train()
     gen = torch.Generator().manual_seed(1)
-    x = torch.randn(B, L, cfg.d_model, generator=gen).to(torch.bfloat16).to(dev).requires_grad_(True)
-    g = torch.randn(B, L, cfg.d_model, generator=gen).to(torch.bfloat16).to(dev)
+    x = torch.randn(B, L, 1024, generator=gen).to(torch.bfloat16).to(dev).requires_grad_(True)
+    g = torch.randn(B, L, 1024, generator=gen).to(torch.bfloat16).to(dev)
     stream = torch.cuda.current_stream(dev)
 
-    def step():
-        out, _ = blk(x)
-        out.backward(g)
+    def measure(blk):
+        def step():
+            x.grad = None
+            for p in blk.parameters():
+                p.grad = None
+            out, _ = blk(x)
+            out.backward(g)
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        return {"ms_per_step": ms, "tokens_per_s": B * L / (ms * 1e-3),
+                "peak_mem_GB": torch.cuda.max_memory_allocated(dev) / 1e9}
 
     res = {}
     prev = CDSSMBlock.readout_scan
     try:
-        for name, flag in (("readout_scan", True), ("ssd_y_readout", False)):
-            CDSSMBlock.readout_scan = flag
-            for _ in range(warmup):
-                step()
-            torch.cuda.synchronize()
-            torch.cuda.reset_peak_memory_stats(dev)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for _ in range(steps):
-                step()
-            e1.record(stream)
-            torch.cuda.synchronize()
-            ms = e0.elapsed_time(e1) / steps
-            res[name] = {"ms_per_step": ms, "tokens_per_s": B * L / (ms * 1e-3),
-                         "peak_mem_GB": torch.cuda.max_memory_allocated(dev) / 1e9}
+        for N in (2, 16):
+            torch.manual_seed(0)
+            cfg = CDSSMConfig(d_model=1024, n_layers=24, context_length=2048, vocab_size=32000, state_dim=N,
+                              d_inner=1024)
+            blk = CDSSMBlock(cfg, 0).to(torch.bfloat16).to(dev).train()
+            if N == 2:
+                for name, flag in (("readout_scan", True), ("ssd_y_readout", False)):
+                    CDSSMBlock.readout_scan = flag
+                    res[name] = measure(blk)
+            else:
+                res["state16_ssd_y_readout"] = measure(blk)
+            del blk
     finally:
         CDSSMBlock.readout_scan = prev
     return {"workload": "one CDSSMBlock training step (forward + backward), config 4 shape B8 L2048 d_model 1024 "
-                        "16x64 heads N=2 bf16", **res,
-            "note": "readout_scan: ChunkwiseDeltaScanAbarFn (cdssm_fused_scan_fwd_abar_train / cdssm_fused_scan_bwd_abar); "
-                    "ssd_y_readout: SSDChunkwiseScan's (B,L,H,2,D) Y read out in torch"}
+                        "16x64 heads bf16", **res,
+            "note": "readout_scan (N=2): ChunkwiseDeltaScanAbarFn (cdssm_fused_scan_fwd_abar_train / "
+                    "cdssm_fused_scan_bwd_abar); ssd_y_readout (N=2) and state16_ssd_y_readout (N=16): "
+                    "SSDChunkwiseScan's (B,L,H,N,D) Y read out by StateReadoutFn (cdssm_state_readout_fwd/_bwd)"}
 
 
 def host_cores():

@@ -309,6 +309,38 @@ def normalize_kq_qk(K: Tensor, Q: Tensor) -> tuple:
     return Ko, Qo, qk
 
 
+class StateReadoutFn(torch.autograd.Function):
+    """The block's readout of per-token states for state_dim N > 2 (block.py:208): (Y (B,L,H,N,D), Q
+    (B,L,H,D)) -> einsum('blhsd,blhd->blhs', Y, Q) with fp32 accumulation, rounded once to the input dtype
+    (cdssm_state_readout_fwd); backward dY = dr Q, dQ = sum_s dr_s Y_s (cdssm_state_readout_bwd)."""
+
+    @staticmethod
+    def forward(ctx, Y, Q):
+        dt = _check_gpu("state_readout", Y, Q)
+        B, L, H, N, D = Y.shape
+        if tuple(Q.shape) != (B, L, H, D):
+            raise ValueError(f"Q must be {(B, L, H, D)}, got {tuple(Q.shape)}")
+        Yc, Qc = Y.contiguous(), Q.contiguous()
+        r = torch.empty(B, L, H, N, dtype=dt, device=Y.device)
+        st = _lib.load().cdssm_state_readout_fwd(_lib.DTYPE_CODE[dt], _lib.ptr(Yc), _lib.ptr(Qc), _lib.ptr(r),
+                                                 B * L * H, N, D, _lib.stream_of(Y.device))
+        _lib.check(st, "cdssm_state_readout_fwd")
+        ctx.save_for_backward(Yc, Qc)
+        return r
+
+    @staticmethod
+    def backward(ctx, dr):
+        Y, Q = ctx.saved_tensors
+        B, L, H, N, D = Y.shape
+        drc = dr.to(Y.dtype).contiguous()
+        dY, dQ = torch.empty_like(Y), torch.empty_like(Q)
+        st = _lib.load().cdssm_state_readout_bwd(_lib.DTYPE_CODE[Y.dtype], _lib.ptr(Y), _lib.ptr(Q), _lib.ptr(drc),
+                                                 _lib.ptr(dY), _lib.ptr(dQ), B * L * H, N, D,
+                                                 _lib.stream_of(Y.device))
+        _lib.check(st, "cdssm_state_readout_bwd")
+        return dY, dQ
+
+
 def shortcut_readout_(retrieved: Tensor, qk: Tensor, V: Tensor, vp: Tensor, sel_C: Tensor, scale: Tensor) -> Tensor:
     """In place: retrieved += sel_C * scale * qk^2 * vp * V (the shortcut of block.py:202-205 through the
     readout of block.py:208-211).  retrieved, V (B, L, H, 2); vp (B, L, H, 1); sel_C (B, L, H); qk fp32."""
@@ -666,7 +698,8 @@ class CDSSMBlock(nn.Module):
         conv1d+SiLU (CUDAConv1dSiLUOp), DynamicsFusedFn, NormalizeKQFn and the fused scan, whose backwards
         are the reference's -- and torch for the projections, the RMSNorm, the shortcut and the fp32
         GroupNorm.  For state_dim 2 the scan is ChunkwiseDeltaScanAbarFn, which returns the readout
-        sel_C (Y.q) itself and never forms Y; otherwise SSDChunkwiseScan's Y is read out here.  The
+        sel_C (Y.q) itself and never forms Y; otherwise SSDChunkwiseScan's Y is read out here by
+        StateReadoutFn (the HIP readout and its backward).  The
         shortcut enters as s (q.k)^2 V_gated (the reference adds s (q.k) V_gated k^T to Y and reads it with
         q: the same value), with elementwise products in the compute dtype."""
         cfg = self.config
@@ -698,7 +731,7 @@ class CDSSMBlock(nn.Module):
             retrieved = y_scan + shortcut * sel_C.unsqueeze(-1)
         else:
             Y = SSDChunkwiseScan(cfg.chunk_size, N)(A_bar, K, V_gated, beta)          # block.py:198
-            retrieved = ((Y * Q.unsqueeze(-2)).sum(-1) + shortcut) * sel_C.unsqueeze(-1)  # block.py:208-211
+            retrieved = (StateReadoutFn.apply(Y, Q) + shortcut) * sel_C.unsqueeze(-1)     # block.py:208-211
         y = self.readout_proj(retrieved.reshape(B, L, H * N))
         y = torch.nn.functional.group_norm(y.float().transpose(1, 2), self.ssm_norm.num_groups,
                                            self.ssm_norm.weight.float(), self.ssm_norm.bias.float(),

@@ -404,6 +404,64 @@ __global__ __launch_bounds__(256) void gn_gate_step_kernel(const typename T::raw
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The block's readout of the per-token states (block.py:208, torch.einsum('blhsd,blhd->blhs', Y, Q)) for
+// state_dim N > 2, where the scan returns Y (B,L,H,N,D): r[n] = Y[n] . q, fp32 accumulation, rounded
+// once to the element type.  One thread per (token-head, state row), 16-byte loads.
+template <typename T>
+__global__ __launch_bounds__(256) void state_readout_fwd_kernel(const typename T::raw* __restrict__ Y,
+                                                                const typename T::raw* __restrict__ q,
+                                                                typename T::raw* __restrict__ r, int64_t rows, int N,
+                                                                int D) {
+  constexpr int V = Vec16<T>::N;
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= rows) return;
+  const typename T::raw* y = Y + idx * D;
+  const typename T::raw* qq = q + (idx / N) * D;
+  float acc = 0.0f;
+  for (int c = 0; c < D; c += V) {
+    Vec16<T> a, b;
+    a.load(y + c);
+    b.load(qq + c);
+#pragma unroll
+    for (int e = 0; e < V; ++e) acc = fmaf(a.v[e], b.v[e], acc);
+  }
+  T::store(r + idx, acc);
+}
+
+// Its backward: dY[n] = dr[n] q (each product rounded once), dq = sum_n dr[n] Y[n] (fp32 accumulation in row
+// order).  One thread per (token-head, 16-byte slice of D).
+template <typename T>
+__global__ __launch_bounds__(256) void state_readout_bwd_kernel(const typename T::raw* __restrict__ Y,
+                                                                const typename T::raw* __restrict__ q,
+                                                                const typename T::raw* __restrict__ dr,
+                                                                typename T::raw* __restrict__ dY,
+                                                                typename T::raw* __restrict__ dq, int64_t n, int N,
+                                                                int D) {
+  constexpr int V = Vec16<T>::N;
+  const int S = D / V;
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= n * S) return;
+  const int64_t th = idx / S;
+  const int off = int(idx - th * S) * V;
+  Vec16<T> qv, acc;
+  qv.load(q + th * D + off);
+#pragma unroll
+  for (int e = 0; e < V; ++e) acc.v[e] = 0.0f;
+  for (int s = 0; s < N; ++s) {
+    const float g = T::load(dr + th * N + s);
+    const int64_t row = (th * N + s) * D + off;
+    Vec16<T> yv, o;
+    yv.load(Y + row);
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      o.v[e] = g * qv.v[e];
+      acc.v[e] = fmaf(g, yv.v[e], acc.v[e]);
+    }
+    o.store(dY + row);
+  }
+  acc.store(dq + th * D + off);
+}
+
 template <typename F>
 int by_dtype(int dtype, const char* op, F&& f) {
   if (dtype == 1) return f(BF16{});
@@ -503,6 +561,63 @@ extern "C" int cdssm_shortcut_readout_fwd(int dtype, void* retrieved, const floa
     hipLaunchKernelGGL(shortcut_kernel<T>, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream,
                        static_cast<raw*>(retrieved), qk, static_cast<const raw*>(V), static_cast<const raw*>(vp),
                        static_cast<const raw*>(sel_c), scale, n);
+    return cdssm_host::check_launch(op);
+  });
+}
+
+extern "C" int cdssm_state_readout_fwd(int dtype, const void* Y, const void* q, void* r, int64_t n, int64_t N,
+                                       int64_t D, hipStream_t stream) {
+  const char* op = "cdssm_state_readout_fwd";
+  return by_dtype(dtype, op, [&](auto t) -> int {
+    using T = decltype(t);
+    using raw = typename T::raw;
+    constexpr int V = Vec16<T>::N;
+    if (n <= 0 || N <= 0 || D <= 0 || D % V != 0 || n * N > (int64_t(1) << 38)) {
+      cdssm_host::set_error("%s: need n, N > 0 and D a positive multiple of %d (n=%lld N=%lld D=%lld)", op, V,
+                            (long long)n, (long long)N, (long long)D);
+      return CDSSM_EINVAL;
+    }
+    if (!Y || !q || !r) {
+      cdssm_host::set_error("%s: null pointer argument", op);
+      return CDSSM_EINVAL;
+    }
+    if ((reinterpret_cast<uintptr_t>(Y) | reinterpret_cast<uintptr_t>(q)) & 15) {
+      cdssm_host::set_error("%s: Y and q must be 16-byte aligned", op);
+      return CDSSM_EINVAL;
+    }
+    const int64_t rows = n * N;
+    hipLaunchKernelGGL(state_readout_fwd_kernel<T>, dim3(unsigned((rows + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<const raw*>(Y), static_cast<const raw*>(q), static_cast<raw*>(r), rows, int(N),
+                       int(D));
+    return cdssm_host::check_launch(op);
+  });
+}
+
+extern "C" int cdssm_state_readout_bwd(int dtype, const void* Y, const void* q, const void* dr, void* dY, void* dq,
+                                       int64_t n, int64_t N, int64_t D, hipStream_t stream) {
+  const char* op = "cdssm_state_readout_bwd";
+  return by_dtype(dtype, op, [&](auto t) -> int {
+    using T = decltype(t);
+    using raw = typename T::raw;
+    constexpr int V = Vec16<T>::N;
+    if (n <= 0 || N <= 0 || D <= 0 || D % V != 0 || n * N > (int64_t(1) << 38)) {
+      cdssm_host::set_error("%s: need n, N > 0 and D a positive multiple of %d (n=%lld N=%lld D=%lld)", op, V,
+                            (long long)n, (long long)N, (long long)D);
+      return CDSSM_EINVAL;
+    }
+    if (!Y || !q || !dr || !dY || !dq) {
+      cdssm_host::set_error("%s: null pointer argument", op);
+      return CDSSM_EINVAL;
+    }
+    if ((reinterpret_cast<uintptr_t>(Y) | reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(dY) |
+         reinterpret_cast<uintptr_t>(dq)) & 15) {
+      cdssm_host::set_error("%s: Y, q, dY and dq must be 16-byte aligned", op);
+      return CDSSM_EINVAL;
+    }
+    const int64_t threads = n * (D / V);
+    hipLaunchKernelGGL(state_readout_bwd_kernel<T>, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<const raw*>(Y), static_cast<const raw*>(q), static_cast<const raw*>(dr),
+                       static_cast<raw*>(dY), static_cast<raw*>(dq), n, int(N), int(D));
     return cdssm_host::check_launch(op);
   });
 }

@@ -500,6 +500,19 @@ int cdssm_normalize_kq_qk_fwd(int dtype, const void* K, int64_t k_token_stride, 
                               int64_t D, hipStream_t stream);
 
 /*
+ * The block's readout of per-token states for state_dim N > 2, where
+ * SSDChunkwiseScan returns Y (block.py:208: einsum('blhsd,blhd->blhs', Y, Q)):
+ * cdssm_state_readout_fwd writes r (n, N) = Y (n, N, D) . q (n, D) with fp32
+ * accumulation; cdssm_state_readout_bwd, given dr (n, N), writes dY = dr q
+ * (n, N, D) and dq = sum over N of dr Y (n, D).  All of `dtype`; n = B*L*H; D a
+ * multiple of 8 (bf16) or 4 (fp32); Y, q, dY, dq 16-byte aligned.
+ */
+int cdssm_state_readout_fwd(int dtype, const void* Y, const void* q, void* r, int64_t n, int64_t N, int64_t D,
+                            hipStream_t stream);
+int cdssm_state_readout_bwd(int dtype, const void* Y, const void* q, const void* dr, void* dY, void* dq, int64_t n,
+                            int64_t N, int64_t D, hipStream_t stream);
+
+/*
  * The current-token shortcut (block.py:202-205) carried through the readout
  * (block.py:208-211): shortcut_scale (q.k) V_gated k^T read by q and gated
  * by sel_C adds sel_C * scale * (q.k)^2 * vp * V to the retrieved pair, in

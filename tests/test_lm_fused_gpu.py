@@ -89,6 +89,29 @@ def test_shortcut_readout(dtype, qk_dtype):
     assert e <= _tol(dtype)
 
 
+@pytest.mark.parametrize("dtype,B,L,H,N,D", [(torch.bfloat16, 2, 37, 3, 16, 64), (torch.float32, 1, 50, 2, 16, 128),
+                                             (torch.bfloat16, 1, 9, 4, 4, 48), (torch.float32, 2, 5, 1, 32, 12)])
+def test_state_readout(dtype, B, L, H, N, D):
+    """StateReadoutFn (cdssm_state_readout_fwd / _bwd) against fp64 autograd of einsum('blhsd,blhd->blhs', Y, Q)
+    (block.py:208) on the same rounded inputs: fp32 1e-5, bf16 4e-3 (one rounding of each output)."""
+    from cdssm_hip.lm import StateReadoutFn
+    log(f"[state_readout] {dtype} B{B} L{L} H{H} N{N} D{D}")
+    g = torch.Generator().manual_seed(5)
+    Y = torch.randn(B, L, H, N, D, generator=g).to(dtype)
+    Q = torch.randn(B, L, H, D, generator=g).to(dtype)
+    dr = torch.randn(B, L, H, N, generator=g).to(dtype)
+    Yr, Qr = Y.double().requires_grad_(True), Q.double().requires_grad_(True)
+    rr = torch.einsum('blhsd,blhd->blhs', Yr, Qr)
+    rr.backward(dr.double())
+    Yg, Qg = Y.to(DEV).requires_grad_(True), Q.to(DEV).requires_grad_(True)
+    r = StateReadoutFn.apply(Yg, Qg)
+    r.backward(dr.to(DEV))
+    tol = 1e-5 if dtype == torch.float32 else 4e-3
+    errs = dict(r=rel(r.cpu(), rr), dY=rel(Yg.grad.cpu(), Yr.grad), dQ=rel(Qg.grad.cpu(), Qr.grad))
+    log("   " + "  ".join(f"{k} {v:.1e}" for k, v in errs.items()))
+    assert all(v <= tol for v in errs.values()), errs
+
+
 @pytest.mark.parametrize("dtype,B,L,C,G,zpad", [(torch.bfloat16, 2, 300, 1024, 32, 64), (torch.float32, 1, 77, 128, 32, 0),
                                                  (torch.bfloat16, 1, 40, 128, 32, 8), (torch.bfloat16, 2, 513, 96, 3, 3),
                                                  (torch.float32, 3, 1, 64, 4, 4)])
