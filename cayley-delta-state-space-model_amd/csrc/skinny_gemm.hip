@@ -11,10 +11,12 @@
 // once and a 128 KB activation many times; the library GEMMs tile them for
 // large M.  (At N = 32000, the tied head, the activation's re-reads dominate:
 // 46 us here against 18 us for the library GEMM.)  Here a workgroup owns 16
-// output columns and all M <= 64 rows: its 4 waves split K, each running
-// v_mfma_f32_16x16x32_bf16 on operands loaded straight from global memory in
-// the instruction's layout (a 16-byte load per lane per fragment: rows of X,
-// rows of W), and the 4 partial tiles are summed in a fixed order through LDS.
+// output columns and all M <= 64 rows: its waves split K (8 waves when K is a
+// multiple of 256, so that at K = 1024 each wave issues all of its loads in
+// one batch; 4 otherwise), each running v_mfma_f32_16x16x32_bf16 on operands
+// loaded straight from global memory in the instruction's layout (a 16-byte
+// load per lane per fragment: rows of X, rows of W), and the waves' partial
+// tiles are summed in a fixed order through LDS.
 // So W streams from HBM once with 16-byte loads, X is served by the L2, and a
 // call launches ceil(N / 16) workgroups.
 //
@@ -33,7 +35,6 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kCols = 16;   // output columns per workgroup
-constexpr int kWaves = 4;   // waves per workgroup, each a quarter of K
 constexpr int kMaxRows = 64;
 constexpr int kUnroll = 4;  // k-steps (of 32) whose loads are issued together
 
@@ -59,12 +60,12 @@ __device__ __forceinline__ float sumsq_frag(uint4 a, float s) {
   return s;
 }
 
-template <bool NORM>
+template <bool NORM, int kWaves>
 __global__ __launch_bounds__(kWave * kWaves) void skinny_gemm_kernel(
     const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ W, int64_t ldw,
     const uint16_t* __restrict__ bias, const uint16_t* __restrict__ R, int64_t ldr,
     const uint16_t* __restrict__ wnorm, float eps, uint16_t* __restrict__ Y, int64_t ldy, int M, int N, int K) {
-  __shared__ f32x4_t part[kWaves][kMaxRows / 16][kWave];  // 16 KB: each wave's partial tiles
+  __shared__ f32x4_t part[kWaves][kMaxRows / 16][kWave];  // 4 KB per wave: its partial tiles
   __shared__ float ssq[kWaves][kMaxRows];                  // each wave's partial row sums of squares
   const int wave = int(threadIdx.x) / kWave;
   const int lane = int(threadIdx.x) % kWave;
@@ -129,7 +130,8 @@ __global__ __launch_bounds__(kWave * kWaves) void skinny_gemm_kernel(
   }
   __syncthreads();
 
-  // wave w finishes row tile w: the 4 partials in wave order, then the epilogue
+  // wave w < 4 finishes row tile w: the partials in wave order, then the epilogue
+  if (wave >= kMaxRows / 16) return;
   const int mt = wave;
   f32x4_t c = part[0][mt][lane];
 #pragma unroll
@@ -149,7 +151,10 @@ __global__ __launch_bounds__(kWave * kWaves) void skinny_gemm_kernel(
     if (m < M) {
       float y = c[i];
       if constexpr (NORM) {
-        const float s = ((ssq[0][m] + ssq[1][m]) + (ssq[2][m] + ssq[3][m])) / float(K);
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) s += ssq[w][m];
+        s /= float(K);
         y *= __builtin_amdgcn_rsqf(s + eps);
       }
       y += bv;
@@ -193,18 +198,25 @@ extern "C" int cdssm_skinny_gemm(int dtype, const void* X, int64_t ldx, const vo
                           "leading dimensions cover the rows");
     return CDSSM_EINVAL;
   }
-  const dim3 grid(unsigned((N + sg::kCols - 1) / sg::kCols)), block(kWave * sg::kWaves);
+  const bool eight = K % 256 == 0;  // 8 waves of K / 8 (a multiple of 32) each
+  const dim3 grid(unsigned((N + sg::kCols - 1) / sg::kCols)), block(kWave * (eight ? 8 : 4));
   const auto* x = static_cast<const uint16_t*>(X);
   const auto* w = static_cast<const uint16_t*>(W);
   const auto* b = static_cast<const uint16_t*>(bias);
   const auto* r = static_cast<const uint16_t*>(R);
   const auto* g = static_cast<const uint16_t*>(wnorm);
   auto* y = static_cast<uint16_t*>(Y);
-  if (wnorm)
-    hipLaunchKernelGGL(sg::skinny_gemm_kernel<true>, grid, block, 0, stream, x, ldx, w, ldw, b, r, ldr, g, eps, y,
-                       ldy, int(M), int(N), int(K));
+  if (wnorm && eight)
+    hipLaunchKernelGGL((sg::skinny_gemm_kernel<true, 8>), grid, block, 0, stream, x, ldx, w, ldw, b, r, ldr, g, eps,
+                       y, ldy, int(M), int(N), int(K));
+  else if (wnorm)
+    hipLaunchKernelGGL((sg::skinny_gemm_kernel<true, 4>), grid, block, 0, stream, x, ldx, w, ldw, b, r, ldr, g, eps,
+                       y, ldy, int(M), int(N), int(K));
+  else if (eight)
+    hipLaunchKernelGGL((sg::skinny_gemm_kernel<false, 8>), grid, block, 0, stream, x, ldx, w, ldw, b, r, ldr, g,
+                       eps, y, ldy, int(M), int(N), int(K));
   else
-    hipLaunchKernelGGL(sg::skinny_gemm_kernel<false>, grid, block, 0, stream, x, ldx, w, ldw, b, r, ldr, g, eps, y,
-                       ldy, int(M), int(N), int(K));
+    hipLaunchKernelGGL((sg::skinny_gemm_kernel<false, 4>), grid, block, 0, stream, x, ldx, w, ldw, b, r, ldr, g,
+                       eps, y, ldy, int(M), int(N), int(K));
   return cdssm_host::check_launch("cdssm_skinny_gemm");
 }

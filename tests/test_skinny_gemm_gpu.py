@@ -38,6 +38,8 @@ def _reference(x, w, bias=None, residual=None, norm_weight=None, eps=0.0):
     ("out_proj + residual", 64, 1024, 1024, False, True, False),
     ("tied head + RMSNorm", 64, 1024, 32000, False, False, True),
     ("ragged rows and columns", 7, 256, 45, True, True, True),
+    ("K 2048 (d_inner of the reference config)", 64, 2048, 1024, False, True, False),
+    ("K 384: four waves", 33, 384, 100, True, False, True),
     ("one row", 1, 128, 16, False, False, False),
 ])
 def test_skinny_gemm_matches_fp32_reference(name, M, K, N, use_bias, use_res, use_norm):
