@@ -237,7 +237,10 @@ def time_fwd_bwd(cfg_name, steps, warmup):
     fwd()
     phases = {"fwd_" + k: v for k, v in fwd.profile(steps).items()}
     phases.update({"bwd_" + k: v for k, v in bwd.profile(steps).items()})
+    fwd()
+    stamps = bwd_phase_summary(bwd, 3)
     return {"workload": f"{cfg.name} fwd+bwd B{cfg.B} H{cfg.H} L{cfg.L} D{cfg.D} bf16",
+            "bwd_phase_stamps": stamps,
             "tokens_per_s": cfg.B * cfg.L / (ms * 1e-3), "ms_per_step": ms,
             "fwd_ms": tf / steps, "bwd_ms": tb / steps,
             "hbm_frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
@@ -253,6 +256,37 @@ def time_fwd_bwd(cfg_name, steps, warmup):
             "traffic_over_alg": (lambda t: None if t is None else t / alg)(
                 recorded_traffic(FWD_BWD_TRAFFIC, f"traffic_bytes_per_step_{cfg.name}")),
             "traffic_source": os.path.relpath(FWD_BWD_TRAFFIC, ROOT)}
+
+
+def bwd_phase_summary(bwd, calls):
+    """Per-wave phase durations of the backward kernels from `calls` stamped backwards
+    (cdssm_fused_scan_bwd_stamped, PreparedBackward.phase_stamps): 10th/50th/90th
+    percentiles in microseconds, per phase of the one-launch correction adjoint + carry
+    and of the main pass, and each kernel's span (first entry to last end, median over
+    the calls).  None when the shape runs the three-launch correction adjoint."""
+    import torch
+    us = 0.01  # microseconds per tick of the 100 MHz counter
+    corr, main, spans_c, spans_m = [], [], [], []
+    try:
+        for _ in range(calls):
+            c, m = bwd.phase_stamps()
+            c, m = c.double(), m.double()
+            corr.append((c[:, 1:] - c[:, :-1]) * us)
+            main.append((m[:, 1:] - m[:, :-1]) * us)
+            spans_c.append(float(c[:, 7].max() - c[:, 0].min()) * us)
+            spans_m.append(float(m[:, 3].max() - m[:, 0].min()) * us)
+    except RuntimeError:
+        return None
+    corr, main = torch.cat(corr), torch.cat(main)
+    cp = bwd.CORR_STAMP_POINTS
+    mp = bwd.MAIN_STAMP_POINTS
+    return {"corr_adjoint_carry": {f"{cp[i]}->{cp[i + 1]}": _pct(corr[:, i]) for i in range(7)},
+            "corr_adjoint_carry_wave_total": _pct(corr.sum(1)),
+            "corr_adjoint_carry_span_us": sorted(spans_c)[len(spans_c) // 2],
+            "main": {f"{mp[i]}->{mp[i + 1]}": _pct(main[:, i]) for i in range(3)},
+            "main_wave_total": _pct(main.sum(1)),
+            "main_span_us": sorted(spans_m)[len(spans_m) // 2],
+            "basis": "cdssm_fused_scan_bwd_stamped: per wave, percentiles 10/50/90 of each phase in us"}
 
 
 def training_record_bytes(cfg):

@@ -41,6 +41,9 @@ SIGNATURES = {
     "cdssm_fused_scan_bwd": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _P, _P, _P,
                                     _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                     _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "cdssm_fused_scan_bwd_stamped": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _P, _P, _P,
+                                            _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                            _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P]),
     "cdssm_fused_scan_fwd_train": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _P,
                                           _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "cdssm_skinny_gemm": (_I32, [_I32, _P, _I64, _P, _I64, _P, _P, _I64, _P, _F32, _P, _I64, _I64, _I64, _I64, _P]),

@@ -611,6 +611,7 @@ class PreparedBackward:
                       _lib.ptr(self.domega), _lib.ptr(self.dh0), _lib.ptr(self.workspace), B, L, H, D, N, Q)
         self._continue = False
         self._gen = -1
+        self.shape = fwd.shape
 
     def __call__(self):
         gen = _path_generation[0]
@@ -624,6 +625,27 @@ class PreparedBackward:
         return self.grads
 
     PHASES = ("corr_adjoint", "rcarry_fold", "rcarry_replay", "main", "heads")
+    CORR_STAMP_POINTS = ("entry", "staged", "lambda", "published", "waited", "folded", "left_end", "end")
+    MAIN_STAMP_POINTS = ("entry", "staged", "reverse", "end")
+
+    def phase_stamps(self) -> Tuple[Tensor, Tensor]:
+        """One backward (cdssm_fused_scan_bwd_stamped, instrumentation) recording the 100 MHz real-time
+        counter per wave at CORR_STAMP_POINTS of the one-launch correction adjoint + carry and at
+        MAIN_STAMP_POINTS of the main pass.  Returns two int64 CPU tensors in ticks, (waves, 8) and
+        (waves, 4), rows of unwritten records dropped; raises if the shape runs the three-launch
+        correction adjoint."""
+        B, L, H, D, N, Q = self.shape
+        nc = -(-L // Q)
+        nseg = -(-nc // 4)
+        m = nseg * B * H * 32
+        buf = torch.zeros(m + B * nc * H * 4, dtype=torch.int64, device=self.device)
+        st = self._lib.cdssm_fused_scan_bwd_stamped(*self._args, _lib.ptr(buf), buf.numel(),
+                                                    _lib.stream_of(self.device))
+        if st != 0:
+            _lib.check(st, "cdssm_fused_scan_bwd_stamped")
+        out = buf.cpu()
+        corr, main = out[:m].view(-1, 8), out[m:].view(-1, 4)
+        return corr[corr[:, 0] != 0], main[main[:, 0] != 0]
 
     def profile(self, iters: int) -> dict:
         """Average milliseconds of each backward kernel launch over `iters` calls."""

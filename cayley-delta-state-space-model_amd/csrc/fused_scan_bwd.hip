@@ -601,6 +601,11 @@ __global__ __launch_bounds__(64) void bwd_epoch_kernel(unsigned long long* ctl) 
     __hip_atomic_store(ctl, epoch_word(2u, n), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
+// Phase stamps of cdssm_fused_scan_bwd_stamped (instrumentation only): the 100
+// MHz real-time counter per wave at kBwdCorrStamps points of the one-launch
+// correction adjoint + carry and kBwdMainStamps points of the main pass.
+constexpr int kBwdCorrStamps = 8, kBwdMainStamps = 4;
+
 template <typename T>
 struct CorrCarryArgs {
   const typename T::raw *q, *k, *beta, *sel_c, *dy;
@@ -612,6 +617,7 @@ struct CorrCarryArgs {
   OnePassBufs ob;         // X in seg_f, A in seg_g, left-end states in seg_s; epoch in ctl[0]
   int L, H, Q, NC, NSEG, n_hg, n_chain;
   int R;                  // SSD form: state rows per head (virtual heads sharing a k row); 1 otherwise
+  unsigned long long* stamps;  // instrumentation: kBwdCorrStamps words per wave, or null
 };
 
 template <typename T, int D>
@@ -627,6 +633,14 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
 
   const int wv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
   const int lane = int(threadIdx.x) % kWave;
+  // phase stamps, read and stored only when a.stamps is set (a uniform branch): entry, staged, lambda pass
+  // done, segment map published, look-back wait done, carry folded, left-end state published, end
+  const bool stamping = a.stamps != nullptr;
+  unsigned long long ts[kBwdCorrStamps];
+  auto stamp = [&](int i) {
+    if (stamping) ts[i] = __builtin_amdgcn_s_memrealtime();
+  };
+  stamp(0);
   const int chain = int(blockIdx.x) % a.n_chain;
   const int rs = int(blockIdx.x) / a.n_chain;  // segments counted from the right
   const int seg = NSEG - 1 - rs;
@@ -690,6 +704,7 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
     }
   }
   __syncthreads();  // every wave reaches every barrier of this kernel
+  stamp(1);
   if (live) {
     for (int tb = 0; tb < ntr; tb += PF) {
       float4 s1[PF], s2[PF];
@@ -748,6 +763,7 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
     if (sub == 0)
       Gx[wv * HPW + hh] = hok ? a.gam[(int64_t(bi) * NC + tc.chunk) * H + h] : make_float2(1.0f, 0.0f);
   }
+  stamp(2);
   __syncthreads();
 
   // ---- the segment's reverse map over its live chunks ----
@@ -784,6 +800,7 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
     arrive_and_draw_next_epoch(ob.ctl, &g_bwd_calls, 2u);
   }
 
+  stamp(3);
   // ---- carry adjoint at the segment's right end, from its anchor ----
   const int anc = rs == 0 ? 0 : kAnchor * ((rs - 1) / kAnchor);  // counted from the right
   const int nmap = rs - anc;
@@ -819,6 +836,7 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
     __syncthreads();
     ok = ctrl[0];
   }
+  stamp(4);
   float2 Sin[EPT];
 #pragma unroll
   for (int i = 0; i < EPT; ++i) Sin[i] = make_float2(0.0f, 0.0f);
@@ -859,6 +877,7 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
       for (int i = 0; i < EPT; ++i) Sin[i] = make_float2(__builtin_nanf(""), __builtin_nanf(""));
     }
   }
+  stamp(5);
   // the segment's left-end state: published for the segments that start from
   // it, and d h0 for the first segment
   const bool anchor_end = rs + 1 < NSEG && (rs + 1) % kAnchor == 0;
@@ -882,6 +901,7 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
   if (anchor_end && threadIdx.x == 0)
     __hip_atomic_store(flag, (epoch << 2) | 2ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
+  stamp(6);
   // ---- d s_{k+1} of this wave's chunk: the maps of the later chunks of the
   // segment applied to the right-end state ----
   if (live && hok) {
@@ -899,6 +919,12 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
     float2* dp = a.dsn + ((int64_t(bi) * NC + tc.chunk) * H + h) * D + sub * DPL;
 #pragma unroll
     for (int jj = 0; jj < DPL; ++jj) dp[jj] = acc[jj];
+  }
+  stamp(7);
+  if (stamping && lane == 0) {
+    unsigned long long* o = a.stamps + (int64_t(blockIdx.x) * W + wv) * kBwdCorrStamps;
+#pragma unroll
+    for (int i = 0; i < kBwdCorrStamps; ++i) o[i] = ts[i];
   }
 }
 
@@ -995,7 +1021,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
     typename T::raw* __restrict__ dbeta, typename T::raw* __restrict__ dsel,
     typename T::raw* __restrict__ ddt, typename T::raw* __restrict__ dr, float2* __restrict__ dhead_parts,
     int L, int H, int Q, int NC, int NCK, int n_hg, int R = 1, float* __restrict__ dkp = nullptr,
-    float* __restrict__ dbp = nullptr) {
+    float* __restrict__ dbp = nullptr, unsigned long long* __restrict__ stamps = nullptr) {
   constexpr int LPH = BwdCfg<D>::LPH, HPW = BwdCfg<D>::HPW, DPL = BwdCfg<D>::DPL, PF = kBwdPF, CK = kBwdCK;
   static_assert(CK == kZck && PF == kTokRound, "the training forward's z checkpoints: every CK tokens");
   extern __shared__ float4 smem4[];
@@ -1007,6 +1033,13 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
   // SIMD as slots free up), which measured 287 against 248 us at C2 (D = 128,
   // 1.5 rounds of waves) on MI355X.
   asm volatile("" ::: "v255");
+  // phase stamps (instrumentation, when stamps is set): entry, staged, reverse pass done, end
+  const bool stamping = stamps != nullptr;
+  unsigned long long ts[kBwdMainStamps];
+  auto stamp = [&](int i) {
+    if (stamping) ts[i] = __builtin_amdgcn_s_memrealtime();
+  };
+  stamp(0);
   const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
   const int hh = lane / LPH, sub = lane % LPH;
@@ -1070,6 +1103,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
   if (staged == kStageMixed) stage_bwd<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, dy, al, om, c, s, saved, sP, sG, R);
   const bool rs = staged == kStageRs;
   __syncthreads();
+  stamp(1);
 
   // ---- reverse pass ----
   float mr[DPL], mi[DPL], lr[DPL], li[DPL];
@@ -1348,6 +1382,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
   else
     drive(run_seg);
   __syncthreads();
+  stamp(2);
   // ---- per-token scalar gradients and dynamics backward: lane = (head j, block of TPB tokens) ----
   // Slots now hold S0 = (a, mu.z_{t-1}), S1 = (dw, sl), S2 = (h, g_{t-1}), P = (p, pc),
   // G = (delta g, Y.q); after the rescaled step S0 = (mu^ conj(z~_i), mu^.k),
@@ -1582,6 +1617,11 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
       if (blk == 0 && jok) dhead_parts[(int64_t(tc.b) * NC + tc.chunk) * H + hj] = make_float2(dal, dom);
     }
   }
+  stamp(3);
+  if (stamping && threadIdx.x == 0) {
+#pragma unroll
+    for (int i = 0; i < kBwdMainStamps; ++i) stamps[int64_t(blockIdx.x) * kBwdMainStamps + i] = ts[i];
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1690,6 +1730,14 @@ BwdLayout bwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) 
 int64_t rows_partials_offset_floats(const BwdLayout& w) { return 2 * ((w.total() + 1) / 2) * 2; }
 int64_t rows_partials_floats(int64_t B, int64_t L, int64_t H, int64_t D) { return B * L * H * (D + 1); }
 
+// Phase-stamp buffer of the running cdssm_fused_scan_bwd_stamped call on this
+// host thread (instrumentation only): device memory of `len` 8-byte words.
+struct BwdStampRequest {
+  unsigned long long* buf = nullptr;
+  int64_t len = 0;
+};
+thread_local BwdStampRequest t_bstamps;
+
 template <typename T, int D>
 int launch_fused_bwd(const void* q, const void* k, const void* v, const void* beta, const void* sel_c,
                      const void* dt, const void* r, const float* alpha, const float* omega, float c,
@@ -1726,6 +1774,7 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
   // workgroups holds every segment, else three (B1, fold, replay)
   int st = CDSSM_OK;
   bool fused = false;
+  int64_t corr_words = 0;  // stamp words of the one-launch carry (instrumentation)
   if (cdssm_host::scan_path() != cdssm_host::kPathFour) {
     constexpr int SEGN = HPWC * D;
     const int64_t items = int64_t(w.NSEG) * B * n_hgc;
@@ -1758,6 +1807,19 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
       a.n_hg = n_hgc;
       a.n_chain = B * n_hgc;
       a.R = R;
+      a.stamps = nullptr;
+      if (t_bstamps.buf) {
+        // the main pass's words follow a region sized for one workgroup per (segment, batch, head), a bound
+        // the caller can form without the pass's heads per wave
+        corr_words = int64_t(w.NSEG) * B * H * kOnePassW * kBwdCorrStamps;
+        const int64_t need = corr_words + int64_t(tiles) * kBwdMainStamps;
+        if (t_bstamps.len < need) {
+          cdssm_host::set_error("cdssm_fused_scan_bwd_stamped: %lld stamp words needed (%lld given)",
+                                (long long)need, (long long)t_bstamps.len);
+          return CDSSM_EINVAL;
+        }
+        a.stamps = t_bstamps.buf;
+      }
       // a continuing call runs on the epoch the previous call's last workgroup left
       if (!cont) {
         hipLaunchKernelGGL(bwd_epoch_kernel, dim3(1), dim3(64), 0, stream, a.ob.ctl);
@@ -1779,6 +1841,11 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
     }
   }
   if (carry_fused) *carry_fused = fused;
+  if (!fused && t_bstamps.buf) {
+    cdssm_host::set_error("cdssm_fused_scan_bwd_stamped: the shape runs the three-launch correction adjoint, "
+                          "which has no phase stamps");
+    return CDSSM_EINVAL;
+  }
   if (!fused) {
     if (ev) (void)hipEventRecord(ev[0], stream);
     hipLaunchKernelGGL((fused_bwd_corr_kernel<T, D>), dim3(unsigned(tiles_c)), dim3(kWave),
@@ -1805,7 +1872,8 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
                      size_t(slots) * 5 * sizeof(float4), stream, (const raw*)q, (const raw*)k, (const raw*)v,
                      (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c,
                      (const raw*)dy, states, saved, (const float2*)dsn, zck, cend, (raw*)dq, (raw*)dk, (raw*)dv,
-                     (raw*)dbeta, (raw*)dsel, (raw*)ddt, (raw*)dr, parts, L, H, Q, NC, fw.NCK, n_hg, R, dkp, dbp);
+                     (raw*)dbeta, (raw*)dsel, (raw*)ddt, (raw*)dr, parts, L, H, Q, NC, fw.NCK, n_hg, R, dkp, dbp,
+                     t_bstamps.buf ? t_bstamps.buf + corr_words : nullptr);
   st = cdssm_host::check_launch("cdssm_fused_scan_bwd/main");
   if (st) return st;
   if (ev) (void)hipEventRecord(ev[4], stream);
@@ -1987,6 +2055,32 @@ extern "C" int cdssm_fused_scan_bwd(int dtype, const void* q, const void* k, con
   return fused_bwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final, fwd_workspace,
                          dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0, workspace, B, L, H, D, N,
                          chunk, stream, nullptr);
+}
+
+// Instrumentation (no reference counterpart): cdssm_fused_scan_bwd, recording
+// the 100 MHz real-time counter per wave at kBwdCorrStamps points of the
+// one-launch correction adjoint + carry (words ((workgroup * 4 + wave) * 8 +
+// point)) and kBwdMainStamps points of the main pass (words M + workgroup * 4 +
+// point, M = NSEG B H * 32 with NSEG = ceil(ceil(L / chunk) / 4)); -1 if the
+// buffer is too small or the shape runs the three-launch correction adjoint.
+extern "C" int cdssm_fused_scan_bwd_stamped(int dtype, const void* q, const void* k, const void* v,
+                                            const void* beta, const void* sel_c, const void* dt,
+                                            const void* r, const float* alpha, const float* omega, float c,
+                                            const void* dy, const float* dh_final, const float* fwd_workspace,
+                                            void* dq, void* dk, void* dv, void* dbeta, void* dsel, void* ddt,
+                                            void* dr, float* dalpha, float* domega, float* dh0, float* workspace,
+                                            int64_t B, int64_t L, int64_t H, int64_t D, int64_t N, int64_t chunk,
+                                            unsigned long long* stamps, int64_t stamps_len, hipStream_t stream) {
+  if (!stamps || stamps_len <= 0) {
+    cdssm_host::set_error("cdssm_fused_scan_bwd_stamped: a stamp buffer is required");
+    return CDSSM_EINVAL;
+  }
+  t_bstamps = BwdStampRequest{stamps, stamps_len};
+  const int st = fused_bwd_entry(dtype, q, k, v, beta, sel_c, dt, r, alpha, omega, c, dy, dh_final, fwd_workspace,
+                                 dq, dk, dv, dbeta, dsel, ddt, dr, dalpha, domega, dh0, workspace, B, L, H, D, N,
+                                 chunk, stream, nullptr);
+  t_bstamps = BwdStampRequest{};
+  return st;
 }
 
 // cdssm_fused_scan_bwd for a workspace whose previous use was a backward call

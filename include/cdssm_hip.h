@@ -201,6 +201,27 @@ int cdssm_fused_scan_fwd_train_continue(int dtype, const void* q, const void* k,
  */
 int64_t cdssm_fused_scan_bwd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
                                              int64_t chunk);
+
+/*
+ * Instrumentation (no reference counterpart): cdssm_fused_scan_bwd, recording
+ * the 100 MHz real-time counter (s_memrealtime) per wave at 8 points of the
+ * one-launch correction adjoint + carry (entry, staged, lambda pass done,
+ * segment map published, look-back wait done, carry folded, left-end state
+ * published, end; word (workgroup * 4 + wave) * 8 + point) and at 4 points of
+ * the main pass (entry, staged, reverse pass done, end; word M + workgroup * 4
+ * + point, M = NSEG * B * H * 32, NSEG = ceil(ceil(L / chunk) / 4)).  stamps:
+ * device memory of stamps_len 8-byte words, at least M + B * ceil(L / chunk) *
+ * H * 4; the caller clears it to tell unwritten records.  Returns -1 (nothing
+ * launched) if the buffer is too small or the shape runs the three-launch
+ * correction adjoint.  Results are bit-identical to cdssm_fused_scan_bwd.
+ */
+int cdssm_fused_scan_bwd_stamped(int dtype, const void* q, const void* k, const void* v, const void* beta,
+                                 const void* sel_c, const void* dt, const void* r, const float* alpha,
+                                 const float* omega, float c, const void* dy, const float* dh_final,
+                                 const float* fwd_workspace, void* dq, void* dk, void* dv, void* dbeta,
+                                 void* dsel_c, void* ddt, void* dr, float* dalpha, float* domega, float* dh0,
+                                 float* workspace, int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
+                                 int64_t chunk, unsigned long long* stamps, int64_t stamps_len, hipStream_t stream);
 int cdssm_fused_scan_bwd(int dtype, const void* q, const void* k, const void* v, const void* beta,
                          const void* sel_c, const void* dt, const void* r, const float* alpha,
                          const float* omega, float c, const void* dy, const float* dh_final,

@@ -76,3 +76,34 @@ def test_stamped_call_rejects_a_short_buffer_and_the_four_launch_forward():
         pf = _prepared(cfg)
         with pytest.raises(RuntimeError, match="four-launch"):
             pf.phase_stamps()
+
+
+@pytest.mark.parametrize("name,B,H,L,D", [("C1-like D64", 2, 16, 2048, 64), ("D128", 1, 8, 1024, 128)])
+def test_stamped_backward_equals_plain_backward_and_records_every_wave(name, B, H, L, D):
+    """cdssm_fused_scan_bwd_stamped: the gradients of a stamped backward are bit-identical to a plain
+    backward's of the same forward; every wave of the one-launch correction adjoint + carry (segments of
+    4 chunks, 4 waves each) and every main-pass wave (one per chunk and head group) leaves a record
+    whose points never decrease."""
+    from cdssm_hip.scan import PreparedBackward, PreparedForward
+    cfg = ScanConfig("s", B=B, H=H, L=L, D=D, h0_std=0.1)
+    log(f"[bwd phase stamps] {name}: B{B} H{H} L{L} D{D} bf16 h0")
+    x = to_dev(draw_inputs(cfg, seed=2))
+    gen = torch.Generator().manual_seed(3)
+    dy = torch.randn(B, L, H, 2, generator=gen).to(DEV)
+    dhf = torch.randn(B, H, 2, D, generator=gen).to(DEV)
+    with forward_path("one_pass"):
+        fwd = PreparedForward(*[x[n] for n in TOKEN_INPUTS], x["c"], h0=x.get("h0"), train=True)
+        bwd = PreparedBackward(fwd, dy, dhf)
+        fwd()
+        grads = [t.cpu().clone() for t in bwd()] + [bwd.dh0.cpu().clone()]
+        corr, main = bwd.phase_stamps()
+        torch.cuda.synchronize()
+    again = [t.cpu() for t in bwd.grads] + [bwd.dh0.cpu()]
+    assert all(torch.equal(a, b) for a, b in zip(grads, again)), "stamped backward changed the gradients"
+    nc = L // 64 if D == 64 else L // 128
+    assert corr.shape[0] > 0 and corr.shape[0] % 4 == 0 and main.shape[0] > 0
+    assert bool(((corr[:, 1:] - corr[:, :-1]) >= 0).all()), "a correction-pass wave's stamps go backwards"
+    assert bool(((main[:, 1:] - main[:, :-1]) >= 0).all()), "a main-pass wave's stamps go backwards"
+    # one main-pass wave per (b, chunk, head group): head groups divide H
+    assert (B * nc * H) % main.shape[0] == 0, (main.shape, B, nc, H)
+    log(f"   {corr.shape[0]} correction-pass and {main.shape[0]} main-pass wave records, points in order")
