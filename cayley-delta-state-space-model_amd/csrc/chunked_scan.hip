@@ -48,10 +48,10 @@ constexpr int kCsCols = 16;   // real state columns
 constexpr int kCsWaves = 4;   // waves per workgroup, one (b, chunk, h) each
 constexpr float kCsTiny = 0x1p-96f;  // |g|^2 below this: the block runs in true units
 
-// LDS of one wave (floats): Gram transpose, state transpose, K^T of the block (bf16), E (bf16 hi | lo)
+// LDS of one wave (floats): the two Gram tile transposes, state transpose, K^T of the block (bf16), E (bf16 hi | lo)
 template <int D>
 constexpr int cs_lds_floats() {
-  return 16 * kSweepRow + 16 * (D + 4) + D * 8 + 256;
+  return 2 * 16 * kSweepRow + 16 * (D + 4) + D * 8 + 256;
 }
 
 struct CsArgs {
@@ -116,7 +116,8 @@ __global__ __launch_bounds__(kWave* kCsWaves) void chunked_sweep_kernel(CsArgs p
   const int64_t row0 = b * p.L + int64_t(c) * p.Q;
 
   float* tr = cs_lds + wave * cs_lds_floats<D>();
-  float* hs = tr + 16 * kSweepRow;
+  float* tp = tr + 16 * kSweepRow;  // the second Gram tile's transpose
+  float* hs = tp + 16 * kSweepRow;
   uint16_t* kt = reinterpret_cast<uint16_t*>(hs + 16 * (D + 4));
   uint16_t* et = kt + D * 16;
 
@@ -199,28 +200,33 @@ __global__ __launch_bounds__(kWave* kCsWaves) void chunked_sweep_kernel(CsArgs p
         gt = mfma16(kf[ks], kf[ks], gt);
         pt = mfma16(kf[ks], qf[ks], pt);
       }
+      // masked by the writing lane, which holds columns s = 4g + r of row j: G for the solve (s < t),
+      // P for the readout (s <= t after the token, local; s < t before it, correction)
+      float gm[4], pm[4];
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const f32x4_t src = m == 0 ? gt : pt;
-        *reinterpret_cast<float4*>(tr + j * kSweepRow + 4 * g) = make_float4(src[0], src[1], src[2], src[3]);
-        wave_lds_sync();
-        float* dst = m == 0 ? grow : prow;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const float4 x = *reinterpret_cast<const float4*>(tr + j * kSweepRow + 4 * u);
-          dst[4 * u + 0] = x.x;
-          dst[4 * u + 1] = x.y;
-          dst[4 * u + 2] = x.z;
-          dst[4 * u + 3] = x.w;
-        }
-        wave_lds_sync();
+      for (int r = 0; r < 4; ++r) {
+        const int sc = 4 * g + r;
+        gm[r] = sc < j ? gt[r] : 0.0f;
+        pm[r] = (CORR ? sc < j : sc <= j) ? pt[r] : 0.0f;
       }
+      *reinterpret_cast<float4*>(tr + j * kSweepRow + 4 * g) = make_float4(gm[0], gm[1], gm[2], gm[3]);
+      *reinterpret_cast<float4*>(tp + j * kSweepRow + 4 * g) = make_float4(pm[0], pm[1], pm[2], pm[3]);
+      wave_lds_sync();
 #pragma unroll
-      for (int s = 0; s < 16; ++s) {
-        qk = s == j ? prow[s] : qk;
-        grow[s] = s < j ? grow[s] : 0.0f;                        // the solve: s < t
-        prow[s] = (CORR ? s < j : s <= j) ? prow[s] : 0.0f;      // readout: after (local) / before (corr) token t
+      for (int u = 0; u < 4; ++u) {
+        const float4 x = *reinterpret_cast<const float4*>(tr + j * kSweepRow + 4 * u);
+        const float4 y = *reinterpret_cast<const float4*>(tp + j * kSweepRow + 4 * u);
+        grow[4 * u + 0] = x.x;
+        grow[4 * u + 1] = x.y;
+        grow[4 * u + 2] = x.z;
+        grow[4 * u + 3] = x.w;
+        prow[4 * u + 0] = y.x;
+        prow[4 * u + 1] = y.y;
+        prow[4 * u + 2] = y.z;
+        prow[4 * u + 3] = y.w;
       }
+      if constexpr (!CORR) qk = tp[j * kSweepRow + j];  // the local readout keeps the diagonal
+      wave_lds_sync();
     }
 
     // K H and Q H: lane (g, j) gets k_j . H and q_j . H for columns 4g .. 4g+3
