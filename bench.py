@@ -683,9 +683,9 @@ def time_block_train(steps=5, warmup=2, B=8, L=2048):
     """One training step through one CDSSMBlock at config 4's shape (d_model 1024, 16 heads x 64,
     d_inner 1024, bf16; B8 L2048): forward and backward of sum(out * g), the way the reference trains
     (block.py:140-229 under autograd, trainer.py:235-247; gradients cleared each step as
-    zero_grad(set_to_none=True) does).  state_dim 2 with the readout-form scan (no (B,L,H,2,D) Y) and with
-    SSDChunkwiseScan's Y read out (the reference's op sequence); state_dim 16 (the reference's default)
-    through SSDChunkwiseScan's Y and the HIP readout of it."""
+    zero_grad(set_to_none=True) does).  state_dim 2 and 16 (the reference's default), each with the
+    readout-form scan (no (B,L,H,N,D) Y; at N = 16 the 8 complex state rows of a head run as virtual heads)
+    and with SSDChunkwiseScan's Y read out by the HIP readout (the reference's op sequence)."""
     import torch
     from cdssm_hip.lm import CDSSMBlock, CDSSMConfig
 
@@ -725,19 +725,17 @@ def time_block_train(steps=5, warmup=2, B=8, L=2048):
             cfg = CDSSMConfig(d_model=1024, n_layers=24, context_length=2048, vocab_size=32000, state_dim=N,
                               d_inner=1024)
             blk = CDSSMBlock(cfg, 0).to(torch.bfloat16).to(dev).train()
-            if N == 2:
-                for name, flag in (("readout_scan", True), ("ssd_y_readout", False)):
-                    CDSSMBlock.readout_scan = flag
-                    res[name] = measure(blk)
-            else:
-                res["state16_ssd_y_readout"] = measure(blk)
+            pre = "" if N == 2 else "state16_"
+            for name, flag in (("readout_scan", True), ("ssd_y_readout", False)):
+                CDSSMBlock.readout_scan = flag
+                res[pre + name] = measure(blk)
             del blk
     finally:
         CDSSMBlock.readout_scan = prev
     return {"workload": "one CDSSMBlock training step (forward + backward), config 4 shape B8 L2048 d_model 1024 "
                         "16x64 heads bf16", **res,
-            "note": "readout_scan (N=2): ChunkwiseDeltaScanAbarFn (cdssm_fused_scan_fwd_abar_train / "
-                    "cdssm_fused_scan_bwd_abar); ssd_y_readout (N=2) and state16_ssd_y_readout (N=16): "
+            "note": "readout_scan: ChunkwiseDeltaScanAbarFn (cdssm_fused_scan_fwd_abar_train / "
+                    "cdssm_fused_scan_bwd_abar; N=16: 8 state rows per head as virtual heads); ssd_y_readout: "
                     "SSDChunkwiseScan's (B,L,H,N,D) Y read out by StateReadoutFn (cdssm_state_readout_fwd/_bwd)"}
 
 

@@ -11,13 +11,15 @@ readout_proj -> fp32 GroupNorm, * silu(z), + D x (HIP) -> out_proj with the
 residual in the GEMM epilogue.  Dense projections and the embedding are
 PyTorch (hipBLASLt GEMMs).  With gradients enabled (training) the block takes a
 differentiable path instead: conv1d+SiLU, DynamicsFusedFn, NormalizeKQFn and
-the fused scan (HIP, with the reference's backward rules: for state_dim 2 the
-gate-level readout form ChunkwiseDeltaScanAbarFn, which never forms the
-(B,L,H,2,D) Y; otherwise SSDChunkwiseScan) and torch for the rest.  With
-state_dim 16 (the reference's default) in bf16 the inference forward runs the
-scan, readout and shortcut in the chunked (UT) form on the matrix cores
-(``cdssm_chunked_scan_fwd_abar``), which never forms Y; other state_dim
-materialise Y through SSDChunkwiseScan.
+the fused scan (HIP, with the reference's backward rules: the gate-level
+readout form ChunkwiseDeltaScanAbarFn, which never forms the (B,L,H,N,D) Y; for
+state_dim N > 2 the head's N/2 complex state rows run as virtual heads sharing
+k, q, beta and sel_C) and torch for the rest.  With state_dim 16 (the
+reference's default) in bf16 the inference forward runs the scan, readout and
+shortcut in the chunked (UT) form on the matrix cores
+(``cdssm_chunked_scan_fwd_abar``); other state_dim take the readout form too.
+With ``readout_scan`` off the block materialises Y through SSDChunkwiseScan
+(the reference's op sequence).
 
 Generation: ``CDSSMLMHeadModel.prefill`` runs the forward over a prompt and keeps
 per-layer decode state (conv window, the scan's R-mode state, GroupNorm running
@@ -534,8 +536,9 @@ class CDSSMBlock(nn.Module):
     # decode steps take the one-launch token kernel (cdssm_decode_block_token) where its alignment holds;
     # False: the separate per-token kernels (the same values)
     fused_step: bool = True
-    # training with state_dim 2 takes the readout-form scan (ChunkwiseDeltaScanAbarFn, no Y); False:
-    # SSDChunkwiseScan's Y read out in torch (the reference's op sequence; the same gradients)
+    # training (and inference where the chunked form does not apply) takes the readout-form scan
+    # (ChunkwiseDeltaScanAbarFn, no Y); False: SSDChunkwiseScan's Y read out in torch (the reference's op
+    # sequence; the same gradients)
     readout_scan: bool = True
     # inference with state_dim 16 in bf16 takes the chunked MFMA form (cdssm_chunked_scan_fwd_abar, no Y);
     # False: SSDChunkwiseScan's Y read out in fp32 torch (the reference's op sequence)
@@ -668,6 +671,14 @@ class CDSSMBlock(nn.Module):
             # retrieved vector sel_C (Y.q + shortcut) (block.py:194-211) without forming Y
             retrieved, _ = chunked_scan_abar(Q, K, V, beta, sel_C, A_bar, vp, chunk_size=cfg.chunk_size,
                                              shortcut_scale=self._fp32("shortcut_scale"))
+        elif N != 2 and self.readout_scan and D in (64, 128) and 1 <= cfg.chunk_size <= 128:
+            # N/2 complex state rows per head: the fused scan with its readout, each row a virtual head
+            # sharing k, q, beta and sel_C (block.py:194-211 with ssd.py:39-111), without forming Y; the
+            # shortcut s (q.k)^2 V_gated (block.py:202-205) through the readout in fp32
+            ret, _ = chunkwise_delta_scan_abar(Q, K, V, beta, sel_C, A_bar, vp, chunk_size=cfg.chunk_size)
+            V_gated = V.float() * vp.float().repeat_interleave(2, dim=-1)
+            ret = ret.float() + (self._fp32("shortcut_scale") * (qk * qk) * sel_C.float()).unsqueeze(-1) * V_gated
+            retrieved = ret.to(x.dtype)
         elif N != 2:
             # N/2 complex pairs per head (the reference default is 16): Y from SSDChunkwiseScan (its
             # fused kernels, each pair a virtual head sharing k; block.py:194-211 with ssd.py:39-111);
@@ -697,9 +708,10 @@ class CDSSMBlock(nn.Module):
         """The block with gradients (block.py:140-229, for training): the HIP ops that have a backward --
         conv1d+SiLU (CUDAConv1dSiLUOp), DynamicsFusedFn, NormalizeKQFn and the fused scan, whose backwards
         are the reference's -- and torch for the projections, the RMSNorm, the shortcut and the fp32
-        GroupNorm.  For state_dim 2 the scan is ChunkwiseDeltaScanAbarFn, which returns the readout
-        sel_C (Y.q) itself and never forms Y; otherwise SSDChunkwiseScan's Y is read out here by
-        StateReadoutFn (the HIP readout and its backward).  The
+        GroupNorm.  The scan is ChunkwiseDeltaScanAbarFn, which returns the readout sel_C (Y.q) itself
+        and never forms Y (state_dim N > 2: N/2 state rows per head as virtual heads); with
+        ``readout_scan`` off, SSDChunkwiseScan's Y is read out here by StateReadoutFn (the HIP readout
+        and its backward).  The
         shortcut enters as s (q.k)^2 V_gated (the reference adds s (q.k) V_gated k^T to Y and reads it with
         q: the same value), with elementwise products in the compute dtype."""
         cfg = self.config
@@ -724,9 +736,10 @@ class CDSSMBlock(nn.Module):
         V_gated = V * vp.repeat_interleave(2, dim=-1)                                 # block.py:194-195
         qk = (Q * K).sum(-1)                                                          # block.py:202
         shortcut = self.shortcut_scale * (qk * qk).unsqueeze(-1) * V_gated            # block.py:204-208
-        if self.readout_scan and N == 2 and D in (64, 128):
+        if self.readout_scan and D in (64, 128) and 1 <= cfg.chunk_size <= 128:
             # the fused scan with its readout, sel_C (Y.q) (block.py:198, 208-211), without forming the
-            # (B,L,H,2,D) Y: its backward rebuilds chunk states from the forward's records
+            # (B,L,H,N,D) Y: its backward rebuilds chunk states from the forward's records (N > 2: the
+            # head's N/2 complex state rows run as virtual heads sharing k, q, beta and sel_C)
             y_scan, _ = ChunkwiseDeltaScanAbarFn.apply(Q, K, V, beta, sel_C, A_bar, vp, None, cfg.chunk_size)
             retrieved = y_scan + shortcut * sel_C.unsqueeze(-1)
         else:

@@ -23,7 +23,9 @@ Tensor = torch.Tensor
 PER_TOKEN = ("q", "k", "v", "beta", "sel_C", "dt", "r")
 
 
-def _validate(q, k, v, beta, sel_C, dt, r, alpha, omega, h0, chunk_size):
+def _validate(q, k, v, beta, sel_C, dt, r, alpha, omega, h0, chunk_size, rows: bool = False):
+    """Shapes, dtypes and devices of a fused-scan call; ``rows`` admits the gate-level form's even
+    state_dim N up to 32 (N / 2 complex state rows per head), else N = 2."""
     named = dict(q=q, k=k, v=v, beta=beta, sel_C=sel_C, dt=dt, r=r, alpha=alpha, omega=omega)
     for n, t in named.items():
         if not isinstance(t, torch.Tensor):
@@ -53,7 +55,9 @@ def _validate(q, k, v, beta, sel_C, dt, r, alpha, omega, h0, chunk_size):
         t = named[n]
         if t.dtype != torch.float32 or tuple(t.shape) != (H,):
             raise ValueError(f"{n} must be float32 of shape ({H},), got {t.dtype} {tuple(t.shape)}")
-    if N != 2:
+    if rows and not (2 <= N <= 32 and N % 2 == 0):
+        raise ValueError(f"state_dim N must be even, 2 <= N <= 32, got N = {N}")
+    if not rows and N != 2:
         raise ValueError(f"the fused scan supports N = 2 (one complex pair per head), got N = {N}")
     if D not in (64, 128):
         raise ValueError(f"head_dim D must be 64 or 128, got {D}")
@@ -100,14 +104,15 @@ def _abar_validate(q, k, v, beta, sel_C, A_bar, vp, h0, chunk_size):
     if not isinstance(A_bar, torch.Tensor) or not isinstance(vp, torch.Tensor):
         raise TypeError("A_bar and vp must be tensors")
     B, L, H, D = q.shape
-    if tuple(A_bar.shape) != (B, L, H, 2) or tuple(vp.shape) != (B, L, H, 1):
-        raise ValueError(f"A_bar must be ({B}, {L}, {H}, 2) and vp ({B}, {L}, {H}, 1), got "
+    N = v.shape[-1] if v.dim() == 4 else 2
+    if tuple(A_bar.shape) != (B, L, H, N) or tuple(vp.shape) != (B, L, H, max(N // 2, 1)):
+        raise ValueError(f"A_bar must be ({B}, {L}, {H}, {N}) and vp ({B}, {L}, {H}, {max(N // 2, 1)}), got "
                          f"{tuple(A_bar.shape)} and {tuple(vp.shape)}")
     if A_bar.dtype != q.dtype or vp.dtype != q.dtype or A_bar.device != q.device or vp.device != q.device:
         raise TypeError("A_bar and vp must have q's dtype and device")
     # shape/dtype checks of the other inputs (A_bar and vp stand in for dt and r there)
     ones = torch.empty(H, dtype=torch.float32, device=q.device)
-    return _validate(q, k, v, beta, sel_C, beta, beta, ones, ones, h0, chunk_size)
+    return _validate(q, k, v, beta, sel_C, beta, beta, ones, ones, h0, chunk_size, rows=True)
 
 
 def chunkwise_delta_scan_abar_fwd(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel_C: Tensor, A_bar: Tensor,
@@ -138,10 +143,12 @@ def chunkwise_delta_scan_abar(q: Tensor, k: Tensor, v: Tensor, beta: Tensor, sel
                               chunk_size: Optional[int] = None) -> Tuple[Tensor, Tensor]:
     """The fused scan on gate-level inputs (cdssm_fused_scan_fwd_abar), inference.
 
-    ``A_bar`` (B,L,H,2) and ``vp`` (B,L,H,1) are DynamicsFusedFn's outputs; the result is
-    ``sel_C * einsum('blhsd,blhd->blhs', SSDChunkwiseScan(Q, 2)(A_bar, k, v * vp, beta), q)``
-    (block.py:194-211 without the shortcut) and the final R-mode state (B,H,2,D) fp32.
-    ``ChunkwiseDeltaScanAbarFn`` is the differentiable form.
+    ``A_bar`` (B,L,H,N) and ``vp`` (B,L,H,N/2) are DynamicsFusedFn's outputs (N even, 2 to 32); the
+    result is ``sel_C * einsum('blhsd,blhd->blhs', SSDChunkwiseScan(Q, N)(A_bar, k,
+    v * vp.repeat_interleave(2, -1), beta), q)`` (B,L,H,N) (block.py:194-211 without the shortcut) and the
+    final R-mode state (B,H,N,D) fp32.  For N > 2 the head's N / 2 complex state rows, which share k, q,
+    beta and sel_C, run as virtual heads of the sequential scan.  ``ChunkwiseDeltaScanAbarFn`` is the
+    differentiable form.
     """
     y, h_final, _ = chunkwise_delta_scan_abar_fwd(q, k, v, beta, sel_C, A_bar, vp, h0, chunk_size)
     return y, h_final
@@ -227,10 +234,12 @@ def chunkwise_delta_scan_abar_bwd(dy: Tensor, dh_final: Optional[Tensor], q, k, 
 class ChunkwiseDeltaScanAbarFn(torch.autograd.Function):
     """Autograd Function of the fused scan on gate-level inputs: (q, k, v, beta, sel_C, A_bar, vp, h0,
     chunk_size) -> (y, h_final), y = sel_C (Y . q) of SSDChunkwiseScan(A_bar, k, v * vp, beta)
-    (block.py:194-211 without the shortcut).  The training step through the block (trainer.py:235-247)
-    without the (B,L,H,2,D) Y: the forward keeps only the training records in its workspace, the
-    backward rebuilds chunk states from them and returns the reference's gradients (exact for the
-    readout, the local and carry branches; the correction branch's shifted rule)."""
+    (block.py:194-211 without the shortcut), for any even state_dim N up to 32 (vp (B,L,H,N/2) per
+    complex state row).  The training step through the block (trainer.py:235-247) without the
+    (B,L,H,N,D) Y: the forward keeps only the training records in its workspace, the backward rebuilds
+    chunk states from them and returns the reference's gradients (exact for the readout, the local and
+    carry branches; the correction branch's shifted rule); with N > 2 the gradients of the per-head
+    k, q, beta and sel_C are summed over the head's state rows in a fixed order."""
 
     @staticmethod
     def forward(ctx, q, k, v, beta, sel_C, A_bar, vp, h0=None, chunk_size=None):

@@ -130,7 +130,8 @@ __device__ __forceinline__ int stage_bwd(const ChunkTile& tc, int H, int ntr,
                                           float c, const BwdScalars& s,
                                           const float4* __restrict__ saved = nullptr,
                                           float4* __restrict__ sP = nullptr, float4* __restrict__ sG = nullptr,
-                                          int R = 1, typename T::raw* __restrict__ dsel = nullptr) {
+                                          int R = 1, typename T::raw* __restrict__ dsel = nullptr,
+                                          float* __restrict__ dsp = nullptr) {
   constexpr int NB = kWave / HPW, TPB = HPW;
   const int lane = int(threadIdx.x) % kWave;  // lane in the wave (one-launch workgroups have several)
   const int j = lane / NB;
@@ -152,18 +153,22 @@ __device__ __forceinline__ int stage_bwd(const ChunkTile& tc, int H, int ntr,
     float bb[TPB], dd[TPB], rr[TPB], vq[TPB], v0[TPB], v1[TPB], sc[TPB], g0[TPB], g1[TPB];
     float4 rp[TPB], rq[TPB];
   };
+  // R state rows per head (the given-transition forms): beta and sel_C per real
+  // head, which its R virtual heads share
+  const int Hk = H / R, hk = hl / R;
   const auto load_slab = [&](SlabIn& in, int tl) {
 #pragma unroll
     for (int i = 0; i < TPB; ++i) {
       const int t = min(tl + blk * TPB + i, tc.nt - 1);
       const int64_t e = (tc.row0 + t) * H + hl;
-      in.bb[i] = T::load(beta + (YM ? (tc.row0 + t) * (H / R) + hl / R : e));  // SSD form: beta per real head
+      const int64_t ek = (tc.row0 + t) * Hk + hk;
+      in.bb[i] = T::load(beta + ek);
       in.dd[i] = T::load(dt + (GA ? 2 * e : e));  // SSD and ABar forms: a_t (re, im) from A_bar
       in.rr[i] = T::load(GA ? dt + 2 * e + 1 : r + e);
       in.vq[i] = kAbar ? T::load(r + e) : 1.0f;   // ABar form: vp_t
       in.v0[i] = WITH_W ? T::load(v + 2 * e) : 0.0f;
       in.v1[i] = WITH_W ? T::load(v + 2 * e + 1) : 0.0f;
-      in.sc[i] = YM ? 0.0f : T::load(sel_c + e);
+      in.sc[i] = YM ? 0.0f : T::load(sel_c + ek);
       in.g0[i] = YM ? 0.0f : T::load(dy + 2 * e);
       in.g1[i] = YM ? 0.0f : T::load(dy + 2 * e + 1);
       if constexpr (WITH_W) {
@@ -200,8 +205,16 @@ __device__ __forceinline__ int stage_bwd(const ChunkTile& tc, int H, int ntr,
     for (int i = 0; i < TPB; ++i) {
       const bool real = hok && t0 + i < tc.nt;
       if constexpr (RS) {
-        // d sel_C = dy . (Y.q) needs nothing from the reverse pass: stored here
-        if (real) T::store(dsel + (tc.row0 + t0 + i) * H + hl, g0[i] * rq[i].z + g1[i] * rq[i].w);
+        // d sel_C = dy . (Y.q) needs nothing from the reverse pass: stored here (R > 1:
+        // the state row's part, summed over the head's rows by the row-sum kernel)
+        if (real) {
+          const int64_t e = (tc.row0 + t0 + i) * H + hl;
+          const float ds = g0[i] * rq[i].z + g1[i] * rq[i].w;
+          if (R > 1)
+            dsp[e] = ds;
+          else
+            T::store(dsel + e, ds);
+        }
       }
       const Transition tr = GA ? Transition{dd[i], rr[i], vq[i]} : cayley_gated(dd[i], rr[i], al, om, c);
       ar[i] = real ? tr.ar : 1.0f;
@@ -333,6 +346,7 @@ __device__ __forceinline__ void stage_corr(const ChunkTile& tc, int H, int ntr,
   const bool hok = hj < H;
   const int hl = hok ? hj : H - 1;
   constexpr bool YM = IsSsdY<T>::value;
+  const int Hk = H / R, hk = hl / R;  // beta and sel_C per real head (R state rows share them)
   for (int tl = 0; tl < ntr; tl += kWave) {
     const int t0 = tl + blk * TPB;
     float bb[TPB], sc[TPB], g0[TPB], g1[TPB];
@@ -341,8 +355,9 @@ __device__ __forceinline__ void stage_corr(const ChunkTile& tc, int H, int ntr,
     for (int i = 0; i < TPB; ++i) {
       const int t = min(t0 + i, tc.nt - 1);
       const int64_t e = (tc.row0 + t) * H + hl;
-      bb[i] = T::load(beta + (YM ? (tc.row0 + t) * (H / R) + hl / R : e));  // SSD form: per real head
-      sc[i] = YM ? 1.0f : T::load(sel_c + e);
+      const int64_t ek = (tc.row0 + t) * Hk + hk;
+      bb[i] = T::load(beta + ek);
+      sc[i] = YM ? 1.0f : T::load(sel_c + ek);
       g0[i] = YM ? 0.0f : T::load(dy + 2 * e);
       g1[i] = YM ? 0.0f : T::load(dy + 2 * e + 1);
       gg[i] = gsaved[e];
@@ -384,13 +399,16 @@ __global__ __launch_bounds__(kWave) void fused_bwd_corr_kernel(
   const int slots = round_up(Q, kWave) * HPW;
   const int ntr = round_up(tc.nt, PF);
 
-  // SSD form: R virtual heads (state rows) share each k row
-  const RowStream ks = YM ? tile_stream_rows<T>(k, tc, L, H, R, D, hh, sub * DPL)
+  // the given-transition forms: R virtual heads (state rows) share each k (and q) row
+  constexpr bool RW = GivenA<T>::value;
+  const RowStream ks = RW ? tile_stream_rows<T>(k, tc, L, H, R, D, hh, sub * DPL)
                           : tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
   // readout form: q rows; SSD form: this lane's slices of the dY re (qs) and im (gs) rows
-  const RowStream qs = tile_stream<T>(q, tc, L, H, YM ? 2 * D : D, hh, sub * DPL);
+  const RowStream qs = YM   ? tile_stream<T>(q, tc, L, H, 2 * D, hh, sub * DPL)
+                       : RW ? tile_stream_rows<T>(q, tc, L, H, R, D, hh, sub * DPL)
+                            : tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
   const RowStream gs = YM ? tile_stream<T>(q, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
-  const int rowb = (YM ? H / R : H) * D * T::bytes;  // token stride of k in bytes
+  const int rowb = (RW ? H / R : H) * D * T::bytes;  // token stride of k (and q) in bytes
   const int rowq = YM ? 2 * H * D * T::bytes : rowb;  // of q, or of dY
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb, slimq = tlast * rowq;
@@ -677,13 +695,16 @@ __global__ __launch_bounds__(kWave * kOnePassW) void fused_bwd_corrcarry_kernel(
 #pragma unroll
   for (int jj = 0; jj < DPL; ++jj) lr[jj] = li[jj] = 0.0f;
   constexpr bool YM = IsSsdY<T>::value;  // SSD form: q points at dY (B,L,H,2,D)
-  // SSD form: R virtual heads (state rows) share each k row
-  const RowStream ks = YM ? tile_stream_rows<T>(a.k, tc, L, H, a.R, D, hh, sub * DPL)
+  // the given-transition forms: R virtual heads (state rows) share each k (and q) row
+  constexpr bool RW = GivenA<T>::value;
+  const RowStream ks = RW ? tile_stream_rows<T>(a.k, tc, L, H, a.R, D, hh, sub * DPL)
                           : tile_stream<T>(a.k, tc, L, H, D, hh, sub * DPL);
   // readout form: q rows; SSD form: this lane's slices of the dY re (qs) and im (gs) rows
-  const RowStream qs = tile_stream<T>(a.q, tc, L, H, YM ? 2 * D : D, hh, sub * DPL);
+  const RowStream qs = YM   ? tile_stream<T>(a.q, tc, L, H, 2 * D, hh, sub * DPL)
+                       : RW ? tile_stream_rows<T>(a.q, tc, L, H, a.R, D, hh, sub * DPL)
+                            : tile_stream<T>(a.q, tc, L, H, D, hh, sub * DPL);
   const RowStream gs = YM ? tile_stream<T>(a.q, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
-  const int rowb = (YM ? H / a.R : H) * D * T::bytes;  // token stride of k in bytes
+  const int rowb = (RW ? H / a.R : H) * D * T::bytes;  // token stride of k (and q) in bytes
   const int rowq = YM ? 2 * H * D * T::bytes : rowb;   // of q, or of dY
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb, slimq = tlast * rowq;
@@ -1007,6 +1028,36 @@ __device__ __forceinline__ DynGrad cayley_gated_bwd(float dt, float r, float alp
 // mu.z_{t-1}) and S1 = (mu.k, lambda.k) for the epilogue (SSD form: G =
 // (delta g, 0, 0), delta g formed in the step).
 // ---------------------------------------------------------------------------
+// A token's dk (and dq) rows: per virtual head into dk / dq, or, with R > 1
+// state rows per head, as fp32 partials (dkp / dqp) that the row-sum kernel adds
+// up; where the wave's heads are rows of one real head they are summed over the
+// wave first and stored by head 0's lanes.
+template <typename T, int LPH, int DPL, bool WITH_Q>
+__device__ __forceinline__ void store_dk_dq(bool rows, bool rows_pre, bool hok, int hh, float (&dkv)[DPL],
+                                            float (&dqv)[DPL], const RowStream& dks, const RowStream& dkps,
+                                            const RowStream& dqs, const RowStream& dqps, int off, int offp) {
+  if (rows_pre) {
+#pragma unroll
+    for (int jj = 0; jj < DPL; ++jj) dkv[jj] = cross_head_sum<LPH>(dkv[jj]);
+    if constexpr (WITH_Q) {
+#pragma unroll
+      for (int jj = 0; jj < DPL; ++jj) dqv[jj] = cross_head_sum<LPH>(dqv[jj]);
+    }
+    if (hh == 0) {
+      store_row<F32, DPL>(dkps, offp, dkv);
+      if constexpr (WITH_Q) store_row<F32, DPL>(dqps, offp, dqv);
+    }
+  } else if (hok) {
+    if (rows) {
+      store_row<F32, DPL>(dkps, offp, dkv);
+      if constexpr (WITH_Q) store_row<F32, DPL>(dqps, offp, dqv);
+    } else {
+      store_row<T, DPL>(dks, off, dkv);
+      if constexpr (WITH_Q) store_row<T, DPL>(dqs, off, dqv);
+    }
+  }
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes == 2 ? 2 : 1, 2))) void fused_bwd_main_kernel(
     const typename T::raw* __restrict__ q, const typename T::raw* __restrict__ k,
@@ -1021,7 +1072,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
     typename T::raw* __restrict__ dbeta, typename T::raw* __restrict__ dsel,
     typename T::raw* __restrict__ ddt, typename T::raw* __restrict__ dr, float2* __restrict__ dhead_parts,
     int L, int H, int Q, int NC, int NCK, int n_hg, int R = 1, float* __restrict__ dkp = nullptr,
-    float* __restrict__ dbp = nullptr, unsigned long long* __restrict__ stamps = nullptr) {
+    float* __restrict__ dbp = nullptr, float* __restrict__ dqp = nullptr, float* __restrict__ dsp = nullptr,
+    unsigned long long* __restrict__ stamps = nullptr) {
   constexpr int LPH = BwdCfg<D>::LPH, HPW = BwdCfg<D>::HPW, DPL = BwdCfg<D>::DPL, PF = kBwdPF, CK = kBwdCK;
   static_assert(CK == kZck && PF == kTokRound, "the training forward's z checkpoints: every CK tokens");
   extern __shared__ float4 smem4[];
@@ -1052,16 +1104,19 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
   constexpr bool kAbar = IsABar<T>::value;  // gate-level a_t and vp given: no per-head dynamics parameters
   const float al = YM || kAbar ? 0.0f : alpha[hl], om = YM || kAbar ? 0.0f : omega[hl];
 
-  // SSD form: R virtual heads (state rows) share each k row; with R > 1 their fp32 dk rows go to dkp and a
-  // row-sum kernel forms dk.  Where a wave's HPW heads are rows of one real head (R % HPW == 0) the wave
-  // sums them first and writes one row per wave, dkp (B, L, H / HPW, D); otherwise one per virtual head,
-  // dkp (B, L, H, D)
-  const bool rows = YM && R > 1;
+  // The given-transition forms (SSD, gate-level): R virtual heads (state rows) share each k row (and q,
+  // beta, sel_C); with R > 1 their fp32 dk (and dq) rows go to dkp (dqp) and a row-sum kernel forms dk
+  // (dq).  Where a wave's HPW heads are rows of one real head (R % HPW == 0) the wave sums them first and
+  // writes one row per wave, dkp (B, L, H / HPW, D); otherwise one per virtual head, dkp (B, L, H, D)
+  constexpr bool RW = GivenA<T>::value;
+  const bool rows = RW && R > 1;
   const bool rows_pre = rows && R % HPW == 0;
-  const RowStream ks = YM ? tile_stream_rows<T>(k, tc, L, H, R, D, hh, sub * DPL)
+  const RowStream ks = RW ? tile_stream_rows<T>(k, tc, L, H, R, D, hh, sub * DPL)
                           : tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
   // readout form: q rows; SSD form: this lane's slices of the dY re (qs) and im (gs) rows
-  const RowStream qs = tile_stream<T>(q, tc, L, H, YM ? 2 * D : D, hh, sub * DPL);
+  const RowStream qs = YM   ? tile_stream<T>(q, tc, L, H, 2 * D, hh, sub * DPL)
+                       : RW ? tile_stream_rows<T>(q, tc, L, H, R, D, hh, sub * DPL)
+                            : tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
   const RowStream gs = YM ? tile_stream<T>(q, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
   const RowStream dks = rows ? RowStream{} : tile_stream<T>(dk, tc, L, H, D, hh, sub * DPL);
   ChunkTile tcp = tc;  // the wave's partial row: head hbase / HPW of H / HPW
@@ -1069,10 +1124,13 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
   const RowStream dkps = !rows      ? RowStream{}
                          : rows_pre ? tile_stream<F32>(dkp, tcp, L, H / HPW, D, 0, sub * DPL)
                                     : tile_stream<F32>(dkp, tc, L, H, D, hh, sub * DPL);
-  const RowStream dqs = YM ? RowStream{} : tile_stream<T>(dq, tc, L, H, D, hh, sub * DPL);
-  const int rowb = (YM ? H / R : H) * D * T::bytes;  // token stride of k (and q, dq, dk) in bytes
+  const RowStream dqs = YM || rows ? RowStream{} : tile_stream<T>(dq, tc, L, H, D, hh, sub * DPL);
+  const RowStream dqps = YM || !rows ? RowStream{}
+                         : rows_pre  ? tile_stream<F32>(dqp, tcp, L, H / HPW, D, 0, sub * DPL)
+                                     : tile_stream<F32>(dqp, tc, L, H, D, hh, sub * DPL);
+  const int rowb = (RW ? H / R : H) * D * T::bytes;  // token stride of k (and q, dq, dk) in bytes
   const int rowq = YM ? 2 * H * D * T::bytes : rowb;  // of q, or of dY
-  const int rowp = (rows_pre ? H / HPW : H) * D * 4;   // of dkp
+  const int rowp = (rows_pre ? H / HPW : H) * D * 4;   // of dkp (and dqp)
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb, slimq = tlast * rowq;
   const int64_t chh = (int64_t(tc.b) * NC + tc.chunk) * H + hl;  // (b, chunk, head) index
@@ -1097,7 +1155,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
   // readout form: rescaled frames unless a segment's rotation product leaves their range
   int staged = kStagePlain;
   if constexpr (!YM)
-    staged = stage_bwd<T, HPW, true, true>(tc, H, ntr, v, beta, sel_c, dt, r, dy, al, om, c, s, saved, sP, sG, 1, dsel);
+    staged = stage_bwd<T, HPW, true, true>(tc, H, ntr, v, beta, sel_c, dt, r, dy, al, om, c, s, saved, sP, sG, R,
+                                           dsel, dsp);
   else
     stage_bwd<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, dy, al, om, c, s, saved, sP, sG, R);
   if (staged == kStageMixed) stage_bwd<T, HPW, true>(tc, H, ntr, v, beta, sel_c, dt, r, dy, al, om, c, s, saved, sP, sG, R);
@@ -1236,18 +1295,12 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
           lr[jj] = fmaf(-bslr, kk[jj], lr[jj]);
           li[jj] = fmaf(-bsli, kk[jj], li[jj]);
         }
-        if (rows_pre) {
-          // the wave's heads are rows of one real head: their sum, stored by head 0's lanes
-#pragma unroll
-          for (int jj = 0; jj < DPL; ++jj) dkv[jj] = cross_head_sum<LPH>(dkv[jj]);
-          if (hh == 0) store_row<F32, DPL>(dkps, t * rowp, dkv);
-        } else if (hok) {
-          if (rows)
-            store_row<F32, DPL>(dkps, t * rowp, dkv);
-          else
-            store_row<T, DPL>(dks, t * rowb, dkv);
-          if constexpr (!YM) store_row<T, DPL>(dqs, t * rowb, dqv);
-        }
+        if constexpr (YM)
+          store_dk_dq<T, LPH, DPL, false>(rows, rows_pre, hok, hh, dkv, dkv, dks, dkps, dqs, dqps, t * rowb,
+                                          t * rowp);
+        else
+          store_dk_dq<T, LPH, DPL, true>(rows, rows_pre, hok, hh, dkv, dqv, dks, dkps, dqs, dqps, t * rowb,
+                                         t * rowp);
         // the token's scalar gradients are formed in the epilogue (one lane per
         // token, not LPH): keep mu.z_{t-1}, dw and sl in the slots this step
         // has read (a stays for the epilogue's psi recurrence)
@@ -1346,10 +1399,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
           lr[jj] = fmaf(-bslr, kk[jj], lr[jj]);
           li[jj] = fmaf(-bsli, kk[jj], li[jj]);
         }
-        if (hok) {
-          store_row<T, DPL>(dks, t * rowb, dkv);
-          store_row<T, DPL>(dqs, t * rowb, dqv);
-        }
+        store_dk_dq<T, LPH, DPL, true>(rows, rows_pre, hok, hh, dkv, dqv, dks, dkps, dqs, dqps, t * rowb, t * rowp);
         if (sub == 0) {
           s.S0[p] = make_float4(red[2], red[3], red[0], red[1]);
           s.S1[p] = make_float4(red[4], red[5], pcr, pci);
@@ -1422,8 +1472,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
       for (int i = 0; i < TPB; ++i) {
         const int tt = min(t0 + i, tc.nt - 1);
         const int64_t ee = (tc.row0 + tt) * H + hjl;
-        // SSD form: beta per real head (the R virtual heads of its state rows share it)
-        lbb[i] = T::load(beta + (YM ? (tc.row0 + tt) * (H / R) + hjl / R : ee));
+        // beta per real head (the R virtual heads of its state rows share it)
+        lbb[i] = T::load(beta + (tc.row0 + tt) * (H / R) + hjl / R);
         lv0[i] = T::load(v + 2 * ee);
         lv1[i] = T::load(v + 2 * ee + 1);
         ldt[i] = lrr[i] = lg0[i] = lg1[i] = 0.0f;
@@ -1592,8 +1642,14 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(T::bytes 
             T::store(dr + e, bb * dwv);
             T::store(dv + 2 * e, bb * vpv * dwr);
             T::store(dv + 2 * e + 1, bb * vpv * dwi);
-            T::store(dbeta + e, dbe + vpv * dwv);
-            if (!rs) T::store(dsel + e, g0 * gv.z + g1 * gv.w);  // (rescaled: stored by the staging)
+            // R > 1: the state row's parts of dbeta and dsel, summed over the head's rows by the row-sum kernel
+            if (R > 1) {
+              dbp[e] = dbe + vpv * dwv;
+              if (!rs) dsp[e] = g0 * gv.z + g1 * gv.w;
+            } else {
+              T::store(dbeta + e, dbe + vpv * dwv);
+              if (!rs) T::store(dsel + e, g0 * gv.z + g1 * gv.w);  // (rescaled: stored by the staging)
+            }
             continue;
           }
           const float dtv = ldt[i], rrv = lrr[i];
@@ -1655,42 +1711,56 @@ __global__ __launch_bounds__(256) void fused_bwd_heads_kernel(const float2* __re
 }
 
 // ---------------------------------------------------------------------------
-// SSD form with R > 1 state rows per head: dk and dbeta of each head are the
-// sums of the fp32 partials the main pass wrote, dk[n, h, :] = sum_j
-// dkp[n, h P + j, :] over the head's P partial rows (P = R, or R / HPW where
-// the main pass already summed each wave's HPW rows), dbeta[n, h] = sum_j
-// dbp[n, h R + j] (n = token), in a fixed order.  One thread per 4
+// R > 1 state rows per head (the SSD and gate-level forms): dk and dbeta (the
+// gate-level form: also dq and dsel) of each head are the sums of the fp32
+// partials the main pass wrote, dk[n, h, :] = sum_j dkp[n, h P + j, :] over the
+// head's P partial rows (P = R, or R / HPW where the main pass already summed
+// each wave's HPW rows), dbeta[n, h] = sum_j dbp[n, h R + j] (n = token), dq
+// and dsel alike from dqp and dsp, in a fixed order.  One thread per 4
 // consecutive elements of dk (D % 4 == 0); the first of a row's threads also
-// sums dbeta.
+// sums dbeta (and dsel).
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(256) void ssd_rows_sum_kernel(const float* __restrict__ dkp,
-                                                           const float* __restrict__ dbp,
-                                                           typename T::raw* __restrict__ dk,
-                                                           typename T::raw* __restrict__ dbeta, int64_t n_rows,
-                                                           int R, int P, int D) {
+__global__ __launch_bounds__(256) void rows_sum_kernel(const float* __restrict__ dkp,
+                                                       const float* __restrict__ dbp,
+                                                       const float* __restrict__ dqp,
+                                                       const float* __restrict__ dsp,
+                                                       typename T::raw* __restrict__ dk,
+                                                       typename T::raw* __restrict__ dbeta,
+                                                       typename T::raw* __restrict__ dq,
+                                                       typename T::raw* __restrict__ dsel, int64_t n_rows,
+                                                       int R, int P, int D) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;  // (token, head, 4 elements)
   const int qd = D / 4;
   if (i >= n_rows * qd) return;
   const int64_t row = i / qd;  // token * Hk + head
   const int d0 = int(i - row * qd) * 4;
-  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  for (int j = 0; j < P; ++j) {
-    const float4 x = *reinterpret_cast<const float4*>(dkp + (row * P + j) * D + d0);
-    acc.x += x.x;
-    acc.y += x.y;
-    acc.z += x.z;
-    acc.w += x.w;
-  }
-  typename T::raw* o = dk + row * D + d0;
-  T::store(o, acc.x);
-  T::store(o + 1, acc.y);
-  T::store(o + 2, acc.z);
-  T::store(o + 3, acc.w);
+  const auto sum4 = [&](const float* x, typename T::raw* o) {
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int j = 0; j < P; ++j) {
+      const float4 v = *reinterpret_cast<const float4*>(x + (row * P + j) * D + d0);
+      acc.x += v.x;
+      acc.y += v.y;
+      acc.z += v.z;
+      acc.w += v.w;
+    }
+    o += row * D + d0;
+    T::store(o, acc.x);
+    T::store(o + 1, acc.y);
+    T::store(o + 2, acc.z);
+    T::store(o + 3, acc.w);
+  };
+  sum4(dkp, dk);
+  if (dqp) sum4(dqp, dq);
   if (d0 == 0) {
     float b = 0.0f;
     for (int j = 0; j < R; ++j) b += dbp[row * R + j];
     T::store(dbeta + row, b);
+    if (dsp) {
+      float g = 0.0f;
+      for (int j = 0; j < R; ++j) g += dsp[row * R + j];
+      T::store(dsel + row, g);
+    }
   }
 }
 
@@ -1724,11 +1794,20 @@ BwdLayout bwd_layout(int64_t B, int64_t L, int64_t H, int64_t D, int64_t chunk) 
   return w;
 }
 
-// SSD form with R > 1 state rows per head (H counting the virtual heads): the
-// fp32 partials dkp (B, L, H, D) and dbp (B, L, H) after the layout above,
-// 16-byte aligned.
+// R > 1 state rows per head, after the layout above, 16-byte aligned: the fp32
+// partials dkp (B, L, Hk P, D) and dbp (B, L, Hk R) of the SSD form; dkp, dqp
+// (B, L, Hk P, D), dbp and dsp (B, L, Hk R) of the gate-level form (Hk real
+// heads; P partial rows per head: R, or R / HPW where the main pass sums each
+// wave's HPW rows first).
 int64_t rows_partials_offset_floats(const BwdLayout& w) { return 2 * ((w.total() + 1) / 2) * 2; }
-int64_t rows_partials_floats(int64_t B, int64_t L, int64_t H, int64_t D) { return B * L * H * (D + 1); }
+int64_t rows_partials_per_head(int64_t D, int64_t R) {
+  const int64_t hpw = D == 64 ? BwdCfg<64>::HPW : BwdCfg<128>::HPW;
+  return R % hpw == 0 ? R / hpw : R;
+}
+// one form's dk (or dq) and dbeta (or dsel) partials
+int64_t rows_partials_floats(int64_t B, int64_t L, int64_t Hk, int64_t R, int64_t D) {
+  return B * L * Hk * (rows_partials_per_head(D, R) * D + R);
+}
 
 // Phase-stamp buffer of the running cdssm_fused_scan_bwd_stamped call on this
 // host thread (instrumentation only): device memory of `len` 8-byte words.
@@ -1866,30 +1945,31 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
     if (st) return st;
     if (ev) (void)hipEventRecord(ev[3], stream);
   }
+  constexpr bool kAbar = IsABar<T>::value;
+  const int64_t nrow = int64_t(B) * L * H;                                  // (token, virtual head) pairs
+  const int64_t nprow = int64_t(B) * L * (H / R) * rows_partials_per_head(D, R);  // (token, partial row)
   float* dkp = R > 1 ? ws + rows_partials_offset_floats(w) : nullptr;
-  float* dbp = R > 1 ? dkp + int64_t(B) * L * H * D : nullptr;
+  float* dqp = R > 1 && kAbar ? dkp + nprow * D : nullptr;
+  float* dbp = R > 1 ? dkp + nprow * D * (kAbar ? 2 : 1) : nullptr;
+  float* dsp = R > 1 && kAbar ? dbp + nrow : nullptr;
   hipLaunchKernelGGL((fused_bwd_main_kernel<T, D>), dim3(unsigned(tiles)), dim3(kWave),
                      size_t(slots) * 5 * sizeof(float4), stream, (const raw*)q, (const raw*)k, (const raw*)v,
                      (const raw*)beta, (const raw*)sel_c, (const raw*)dt, (const raw*)r, alpha, omega, c,
                      (const raw*)dy, states, saved, (const float2*)dsn, zck, cend, (raw*)dq, (raw*)dk, (raw*)dv,
                      (raw*)dbeta, (raw*)dsel, (raw*)ddt, (raw*)dr, parts, L, H, Q, NC, fw.NCK, n_hg, R, dkp, dbp,
-                     t_bstamps.buf ? t_bstamps.buf + corr_words : nullptr);
+                     dqp, dsp, t_bstamps.buf ? t_bstamps.buf + corr_words : nullptr);
   st = cdssm_host::check_launch("cdssm_fused_scan_bwd/main");
   if (st) return st;
   if (ev) (void)hipEventRecord(ev[4], stream);
-  if constexpr (IsSsdY<T>::value) {  // no per-head dynamics parameters
+  if constexpr (GivenA<T>::value) {  // SSD and gate-level forms: no per-head dynamics parameters
     if (R > 1) {
       const int64_t n_rows = int64_t(B) * L * (H / R);
       const int64_t threads = n_rows * (D / 4);
-      hipLaunchKernelGGL(ssd_rows_sum_kernel<T>, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, stream,
-                         (const float*)dkp, (const float*)dbp, (raw*)dk, (raw*)dbeta, n_rows, R,
-                         R % HPW == 0 ? R / HPW : R, D);
-      st = cdssm_host::check_launch("cdssm_ssd_scan_bwd/rows_sum");
+      hipLaunchKernelGGL(rows_sum_kernel<T>, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, stream,
+                         (const float*)dkp, (const float*)dbp, (const float*)dqp, (const float*)dsp, (raw*)dk,
+                         (raw*)dbeta, (raw*)dq, (raw*)dsel, n_rows, R, int(rows_partials_per_head(D, R)), D);
+      st = cdssm_host::check_launch(kAbar ? "cdssm_fused_scan_bwd_abar/rows_sum" : "cdssm_ssd_scan_bwd/rows_sum");
     }
-    if (ev) (void)hipEventRecord(ev[5], stream);
-    return st;
-  }
-  if constexpr (IsABar<T>::value) {  // gate-level form: no per-head dynamics parameters either
     if (ev) (void)hipEventRecord(ev[5], stream);
     return st;
   }
@@ -1924,19 +2004,24 @@ int cdssm_host::bwd_lookback_status(bool clear, unsigned* out) {
 
 extern "C" int64_t cdssm_fused_scan_bwd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t D,
                                                         int64_t N, int64_t chunk) {
-  if (B <= 0 || L <= 0 || H <= 0 || D <= 0 || N != 2 || chunk <= 0) return -1;
-  return bwd_layout(B, L, H, D, chunk).total() * int64_t(sizeof(float2));
+  if (B <= 0 || L <= 0 || H <= 0 || D <= 0 || chunk <= 0 || N < 2 || N > 32 || N % 2 != 0) return -1;
+  if (N == 2) return bwd_layout(B, L, H, D, chunk).total() * int64_t(sizeof(float2));
+  // the gate-level form's N / 2 state rows per head as virtual heads, plus the
+  // fp32 dk, dq, dbeta and dsel partials of the state rows
+  const int64_t Hv = H * (N / 2);
+  const BwdLayout w = bwd_layout(B, L, Hv, D, chunk);
+  return (rows_partials_offset_floats(w) + 2 * rows_partials_floats(B, L, H, N / 2, D)) * int64_t(sizeof(float));
 }
 
 // The SSD form's backward workspace: the fused scan's with H N / 2 (virtual)
-// heads, plus, for N > 2, the fp32 dk and dbeta partials of every state row.
+// heads, plus, for N > 2, the fp32 dk and dbeta partials of the state rows.
 extern "C" int64_t cdssm_ssd_scan_bwd_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t D, int64_t N,
                                                       int64_t chunk) {
   if (B <= 0 || L <= 0 || H <= 0 || D <= 0 || chunk <= 0 || N < 2 || N > 32 || N % 2 != 0) return -1;
   const int64_t Hv = H * (N / 2);
   const BwdLayout w = bwd_layout(B, L, Hv, D, chunk);
   if (N == 2) return w.total() * int64_t(sizeof(float2));
-  return (rows_partials_offset_floats(w) + rows_partials_floats(B, L, Hv, D)) * int64_t(sizeof(float));
+  return (rows_partials_offset_floats(w) + rows_partials_floats(B, L, H, N / 2, D)) * int64_t(sizeof(float));
 }
 
 namespace {
@@ -1957,16 +2042,17 @@ int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, cons
     cdssm_host::set_error("%s: B, L, H must be positive", op);
     return CDSSM_EINVAL;
   }
-  // SSD form: the N = 2 R state rows of a head run as R virtual heads (sharing the head's k and beta)
+  // SSD and gate-level forms: the N / 2 complex state rows of a head run as R
+  // virtual heads sharing the head's k, beta (and q, sel_C)
   int64_t R = 1;
-  if (ssd && N > 2 && N % 2 == 0 && N <= 32) {
+  if ((ssd || abar) && N > 2 && N % 2 == 0 && N <= 32) {
     R = N / 2;
     H *= R;
     N = 2;
   }
   if (N != 2) {
-    cdssm_host::set_error(ssd ? "%s: state_dim N must be even, 2 <= N <= 32, got %lld"
-                              : "%s: the fused scan supports state_dim N = 2, got %lld", op, (long long)N);
+    cdssm_host::set_error(ssd || abar ? "%s: state_dim N must be even, 2 <= N <= 32, got %lld"
+                                      : "%s: the fused scan supports state_dim N = 2, got %lld", op, (long long)N);
     return CDSSM_EINVAL;
   }
   if (D != 64 && D != 128) {
@@ -2002,10 +2088,11 @@ int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, cons
       cdssm_host::set_error("%s: A_bar and dA_bar must be aligned to their (re, im) pairs", op);
       return CDSSM_EINVAL;
     }
+    const int rr = int(R);
 #define CDSSM_ABAR_BWD(TT, DD)                                                                                   \
   launch_fused_bwd<TT, DD>(q, k, v, beta, sel_c, dt, r, nullptr, nullptr, 0.0f, dy, dh_final, fwd_workspace, dq,  \
                            dk, dv, dbeta, dsel, ddt, dr, nullptr, nullptr, dh0, workspace, b, l, hh, qc, stream, \
-                           ev, carry_fused, cont)
+                           ev, carry_fused, cont, rr)
     if (dtype == 1) return D == 64 ? CDSSM_ABAR_BWD(ABar<BF16>, 64) : CDSSM_ABAR_BWD(ABar<BF16>, 128);
     return D == 64 ? CDSSM_ABAR_BWD(ABar<F32>, 64) : CDSSM_ABAR_BWD(ABar<F32>, 128);
 #undef CDSSM_ABAR_BWD

@@ -223,12 +223,15 @@ __device__ __forceinline__ ResetMask<HPW> stage_scalars(const ChunkTile& tc, int
         vq[i] = 0.0f;
       }
     } else {
+    // R state rows per head (the given-transition forms): beta and sel_C per real
+    // head, which the head's R virtual heads share; R = 1 otherwise
+    const int Hk = H / R, hk = hl / R;
 #pragma unroll
     for (int i = 0; i < TPB; ++i) {
       const int t = min(t0 + i, tc.nt - 1);
       const int64_t e = (tc.row0 + t) * H + hl;
-      // SSD form with R state rows per head: beta per real head (R virtual heads share it)
-      bb[i] = T::load(beta + (kSsd ? (tc.row0 + t) * (H / R) + hl / R : e));
+      const int64_t ek = (tc.row0 + t) * Hk + hk;
+      bb[i] = T::load(beta + ek);
       if constexpr (kAbar) {
         dd[i] = T::load(dt + 2 * e);  // a_t re, im
         rr[i] = T::load(dt + 2 * e + 1);
@@ -240,7 +243,7 @@ __device__ __forceinline__ ResetMask<HPW> stage_scalars(const ChunkTile& tc, int
       }
       v0[i] = T::load(v + 2 * e);
       v1[i] = T::load(v + 2 * e + 1);
-      sc[i] = MAIN && !kSsd ? T::load(sel_c + e) : 0.0f;
+      sc[i] = MAIN && !kSsd ? T::load(sel_c + ek) : 0.0f;
     }
     // the caller's row prefetch goes after these small loads, so waiting for
     // them does not wait for the rows
@@ -440,7 +443,8 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
     int L, int H, int Q, int NC, int n_hg, int R = 1) {
   using Cfg = FusedCfg<T, D, LPH>;
   constexpr int DPL = Cfg::DPL, HPW = Cfg::HPW, PF = kPrefetch;
-  constexpr bool YM = IsSsdY<T>::value;  // SSD form: R virtual heads (state rows) share each k row
+  // the given-transition forms: R virtual heads (state rows) share each k row
+  constexpr bool RW = GivenA<T>::value;
   extern __shared__ float4 smem4[];
   const ChunkTile tc = decode_tile(L, Q, NC, n_hg, HPW);
   const int lane = threadIdx.x;
@@ -452,9 +456,9 @@ __global__ __launch_bounds__(kWave) void fused_fwd_summary_kernel(
   const int slots = round_up(Q, kWave) * HPW;
   const int64_t ch0 = (int64_t(tc.b) * NC + tc.chunk) * H + tc.hbase;
 
-  const RowStream ks = YM ? tile_stream_rows<T>(k, tc, L, H, R, D, hh, sub * DPL)
+  const RowStream ks = RW ? tile_stream_rows<T>(k, tc, L, H, R, D, hh, sub * DPL)
                           : tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
-  const int rowb = (YM ? H / R : H) * D * T::bytes;  // token stride of k in bytes
+  const int rowb = (RW ? H / R : H) * D * T::bytes;  // token stride of k in bytes
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb;
   RowVec<T, DPL> kb[PF];
@@ -662,15 +666,18 @@ __global__ __launch_bounds__(kWave) void fused_fwd_main_kernel(
   const int ntr = round_up(tc.nt, PF);
   const int slots = round_up(Q, kWave) * HPW;
 
-  // SSD form: R virtual heads (state rows) share each k row
-  const RowStream ks = YM ? tile_stream_rows<T>(k, tc, L, H, R, D, hh, sub * DPL)
+  // the given-transition forms: R virtual heads (state rows) share each k (and q) row
+  constexpr bool RW = GivenA<T>::value;
+  const RowStream ks = RW ? tile_stream_rows<T>(k, tc, L, H, R, D, hh, sub * DPL)
                           : tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
-  const RowStream qs = YM ? RowStream{} : tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
+  const RowStream qs = YM   ? RowStream{}
+                       : RW ? tile_stream_rows<T>(q, tc, L, H, R, D, hh, sub * DPL)
+                            : tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
   // SSD form: this lane's slices of its head's Y re and im rows (D apart)
   const RowStream yre = YM ? tile_stream<T>(y, tc, L, H, 2 * D, hh, sub * DPL) : RowStream{};
   const RowStream yim = YM ? tile_stream<T>(y, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
   const int rowy = 2 * H * D * T::bytes;  // token stride of Y in bytes
-  const int rowb = (YM ? H / R : H) * D * T::bytes;  // token stride of k (and q) in bytes
+  const int rowb = (RW ? H / R : H) * D * T::bytes;  // token stride of k (and q) in bytes
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb;
   RowVec<T, DPL> kb[PF], qb[PF];
@@ -1082,15 +1089,18 @@ __device__ __forceinline__ void onepass_segment(const OnePassArgs<T>& a, int ite
   float2* Sx = reinterpret_cast<float2*>(GF + W * HPW);
   int* ctrl = reinterpret_cast<int*>(Sx + SEGN);
 
-  // SSD form: R virtual heads (state rows) share each k row
-  const RowStream ks = YM ? tile_stream_rows<T>(k, tc, L, H, a.R, D, hh, sub * DPL)
+  // the given-transition forms: R virtual heads (state rows) share each k (and q) row
+  constexpr bool RW = GivenA<T>::value;
+  const RowStream ks = RW ? tile_stream_rows<T>(k, tc, L, H, a.R, D, hh, sub * DPL)
                           : tile_stream<T>(k, tc, L, H, D, hh, sub * DPL);
-  const RowStream qs = YM ? RowStream{} : tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
+  const RowStream qs = YM   ? RowStream{}
+                       : RW ? tile_stream_rows<T>(q, tc, L, H, a.R, D, hh, sub * DPL)
+                            : tile_stream<T>(q, tc, L, H, D, hh, sub * DPL);
   // SSD form: this lane's slices of its head's Y re and im rows (D apart)
   const RowStream yre = YM ? tile_stream<T>(y, tc, L, H, 2 * D, hh, sub * DPL) : RowStream{};
   const RowStream yim = YM ? tile_stream<T>(y, tc, L, H, 2 * D, hh, D + sub * DPL) : RowStream{};
   const int rowy = 2 * H * D * T::bytes;  // token stride of Y in bytes
-  const int rowb = (YM ? H / a.R : H) * D * T::bytes;  // token stride of k (and q) in bytes
+  const int rowb = (RW ? H / a.R : H) * D * T::bytes;  // token stride of k (and q) in bytes
   const int tlast = tc.nt - 1;
   const int slim = tlast * rowb;
   RowVec<T, DPL> kb[PF], qb[PF];
@@ -1977,8 +1987,9 @@ int cdssm_host::fwd_lookback_status(bool clear, unsigned* out) {
 
 extern "C" int64_t cdssm_fused_scan_workspace_bytes(int64_t B, int64_t L, int64_t H, int64_t D,
                                                     int64_t N, int64_t chunk) {
-  if (B <= 0 || L <= 0 || H <= 0 || D <= 0 || N != 2 || chunk <= 0) return -1;
-  return fwd_layout(B, L, H, D, chunk).total() * int64_t(sizeof(float2));
+  if (B <= 0 || L <= 0 || H <= 0 || D <= 0 || chunk <= 0 || N < 2 || N > 32 || N % 2 != 0) return -1;
+  // N > 2 (the gate-level form): the N / 2 state rows of a head are scanned as virtual heads
+  return fwd_layout(B, L, H * (N / 2), D, chunk).total() * int64_t(sizeof(float2));
 }
 
 // The SSD form's forward workspace: its N / 2 state rows per head are scanned as
@@ -2012,16 +2023,18 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
                           (long long)L, (long long)H);
     return CDSSM_EINVAL;
   }
-  // SSD form: the N = 2 R state rows of a head run as R virtual heads (sharing the head's k and beta)
+  // SSD and gate-level forms: the N / 2 complex state rows of a head run as R
+  // virtual heads sharing the head's k, beta (and q, sel_C); each has its own
+  // a_t, values (and vp_t, readout pair), in the (B,L,H,N) layouts as given
   int64_t R = 1;
-  if (ssd && N > 2 && N % 2 == 0 && N <= 32) {
+  if ((ssd || abar) && N > 2 && N % 2 == 0 && N <= 32) {
     R = N / 2;
     H *= R;
     N = 2;
   }
   if (N != 2) {
-    cdssm_host::set_error(ssd ? "%s: state_dim N must be even, 2 <= N <= 32, got %lld"
-                              : "%s: the fused scan supports state_dim N = 2, got %lld", op, (long long)N);
+    cdssm_host::set_error(ssd || abar ? "%s: state_dim N must be even, 2 <= N <= 32, got %lld"
+                                      : "%s: the fused scan supports state_dim N = 2, got %lld", op, (long long)N);
     return CDSSM_EINVAL;
   }
   if (D != 64 && D != 128) {
@@ -2081,15 +2094,17 @@ int fused_fwd_entry(int dtype, const void* q, const void* k, const void* v, cons
     return launch_fused_fwd<SsdY<F32>, 128, 32, 32>(CDSSM_FWD_ARGS, rr);
   }
   if (abar) {
+    const int rr = int(R);
     if (dtype == 1) {
       if (D == 64 && fill_with_4_heads_per_wave(B, L, H, chunk))
-        return launch_fused_fwd<ABar<BF16>, 64, 16, CDSSM_FWD_LPHS_BF16_D64>(CDSSM_FWD_ARGS);
+        return launch_fused_fwd<ABar<BF16>, 64, 16, CDSSM_FWD_LPHS_BF16_D64>(CDSSM_FWD_ARGS, rr);
       if (D == 64)
-        return launch_fused_fwd<ABar<BF16>, 64, CDSSM_FWD_LPH_BF16_D64, CDSSM_FWD_LPHS_BF16_D64>(CDSSM_FWD_ARGS);
-      return launch_fused_fwd<ABar<BF16>, 128, 16, CDSSM_FWD_LPHS_BF16_D128>(CDSSM_FWD_ARGS);
+        return launch_fused_fwd<ABar<BF16>, 64, CDSSM_FWD_LPH_BF16_D64, CDSSM_FWD_LPHS_BF16_D64>(CDSSM_FWD_ARGS,
+                                                                                               rr);
+      return launch_fused_fwd<ABar<BF16>, 128, 16, CDSSM_FWD_LPHS_BF16_D128>(CDSSM_FWD_ARGS, rr);
     }
-    if (D == 64) return launch_fused_fwd<ABar<F32>, 64, 16, 16>(CDSSM_FWD_ARGS);
-    return launch_fused_fwd<ABar<F32>, 128, 32, 32>(CDSSM_FWD_ARGS);
+    if (D == 64) return launch_fused_fwd<ABar<F32>, 64, 16, 16>(CDSSM_FWD_ARGS, rr);
+    return launch_fused_fwd<ABar<F32>, 128, 32, 32>(CDSSM_FWD_ARGS, rr);
   }
   if (dtype == 1) {
     // the training forward takes the same layout as the inference forward of the

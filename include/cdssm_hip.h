@@ -44,7 +44,8 @@ const char* cdssm_last_error(void);
  * after the last token; an extension -- the reference has no state output).
  * workspace: cdssm_fused_scan_workspace_bytes() bytes of device memory, any
  * contents (scratch for this call; the backward takes the workspace of
- * cdssm_fused_scan_fwd_train instead).  Supported: N = 2, D in {64, 128},
+ * cdssm_fused_scan_fwd_train instead; the size function also takes the
+ * gate-level form's even N <= 32).  Supported: N = 2, D in {64, 128},
  * 1 <= chunk <= 128; q, k 16-byte aligned, y aligned to one (re, im) pair
  * (4 bytes bf16, 8 fp32).  Where every segment of 4 chunks fits in one round of
  * resident workgroups (or, for this inference forward, the segments fill
@@ -85,8 +86,12 @@ int cdssm_fused_scan_fwd_noalloc(int dtype, const void* q, const void* k, const 
  * the transition a_bar (B,L,H,N) and VP scale vp (B,L,H,N/2), both of `dtype`,
  * as DynamicsFusedFn produces them (ops.py:39-66, dynamics_fused.cu:35-140),
  * and computes SSDChunkwiseScan(A_bar, K, V * vp, beta) (ssd.py:39-111) with the
- * readout y = sel_C (Y . q) (block.py:194-211, shortcut excluded).  Other
- * arguments, workspace and limits as cdssm_fused_scan_fwd.  Inference only.
+ * readout y = sel_C (Y . q) (block.py:194-211, shortcut excluded).  N even,
+ * 2 <= N <= 32: the N / 2 complex state rows of a head share its k, q, beta and
+ * sel_c and are scanned as virtual heads (v, a_bar, y (B,L,H,N), vp (B,L,H,N/2),
+ * h0 / h_final (B,H,N,D) in the reference's layouts).  Other arguments,
+ * workspace (cdssm_fused_scan_workspace_bytes with this N) and limits as
+ * cdssm_fused_scan_fwd.  Inference only.
  */
 int cdssm_fused_scan_fwd_abar(int dtype, const void* q, const void* k, const void* v, const void* beta,
                               const void* sel_c, const void* a_bar, const void* vp, const float* h0, void* y,
@@ -100,14 +105,18 @@ int cdssm_fused_scan_fwd_abar(int dtype, const void* q, const void* k, const voi
  * stores it, and its passes' states, for its backward, ops.py:119,153,184).
  * cdssm_fused_scan_fwd_abar_train: the forward above that also stores in the
  * workspace what the backward reads (the records of cdssm_fused_scan_fwd_train).
- * cdssm_fused_scan_bwd_abar: given dy (B,L,H,2), dh_final (B,H,2,D) fp32 or
- * NULL and that workspace, writes dq, dk (B,L,H,D), dv (B,L,H,2), dbeta,
- * dsel_c (B,L,H), da_bar (B,L,H,2), dvp (B,L,H) of `dtype` and dh0 (B,H,2,D)
- * fp32 or NULL: the gradients ops.py's autograd yields through
+ * cdssm_fused_scan_bwd_abar: given dy (B,L,H,N), dh_final (B,H,N,D) fp32 or
+ * NULL and that workspace, writes dq, dk (B,L,H,D), dv (B,L,H,N), dbeta,
+ * dsel_c (B,L,H), da_bar (B,L,H,N), dvp (B,L,H,N/2) of `dtype` and dh0
+ * (B,H,N,D) fp32 or NULL: the gradients ops.py's autograd yields through
  * SSDChunkwiseScan and the readout (exact for the readout, the local and carry
  * branches; the correction branch's shifted rule, exact_correction.cu:213-382),
  * with d A_bar and d vp in place of the scan-level dynamics chain of
- * cdssm_fused_scan_bwd.  workspace: cdssm_fused_scan_bwd_workspace_bytes().
+ * cdssm_fused_scan_bwd.  N even, 2 <= N <= 32 as in the forward; for N > 2
+ * the gradients of the shared dq, dk, dbeta, dsel_c are summed over the head's
+ * state rows in a fixed order (bit-reproducible).  workspace:
+ * cdssm_fused_scan_bwd_workspace_bytes() with this N (for N > 2 it holds the
+ * fp32 per-row partials of those sums).
  */
 int cdssm_fused_scan_fwd_abar_train(int dtype, const void* q, const void* k, const void* v, const void* beta,
                                     const void* sel_c, const void* a_bar, const void* vp, const float* h0, void* y,

@@ -157,8 +157,9 @@ def test_ssd_bwd_rejects_invalid_arguments_without_launching(bad, msg):
 
 def test_ssd_workspaces_are_the_fused_scans_with_virtual_heads():
     """N / 2 state rows per head scan as that many virtual heads: the forward workspace is the fused
-    scan's with H N / 2 heads; the backward's adds, for N > 2, fp32 dk and dbeta partials per row after
-    a 16-byte aligned layout."""
+    scan's with H N / 2 heads; the backward's adds, for N > 2, fp32 dk partials (P rows per head: R = N / 2,
+    or R / 4 where a D-64 backward wave of 4 virtual heads sums its rows first) and dbeta partials per
+    state row after a 16-byte aligned layout."""
     lib = _lib.load()
     B, L, H, D, Q = 2, 1000, 3, 64, 64
     for N in (2, 4, 16):
@@ -166,10 +167,42 @@ def test_ssd_workspaces_are_the_fused_scans_with_virtual_heads():
         assert lib.cdssm_ssd_scan_workspace_bytes(B, L, H, D, N, Q) == \
             lib.cdssm_fused_scan_workspace_bytes(B, L, Hv, D, 2, Q)
         base = lib.cdssm_fused_scan_bwd_workspace_bytes(B, L, Hv, D, 2, Q)
-        want = base if N == 2 else (-(-base // 16) * 16 + B * L * Hv * (D + 1) * 4)
+        R = N // 2
+        P = R // 4 if R % 4 == 0 else R
+        want = base if N == 2 else (-(-base // 16) * 16 + B * L * H * (P * D + R) * 4)
         assert lib.cdssm_ssd_scan_bwd_workspace_bytes(B, L, H, D, N, Q) == want
     assert lib.cdssm_ssd_scan_workspace_bytes(B, L, H, D, 3, Q) == -1
     assert lib.cdssm_ssd_scan_bwd_workspace_bytes(B, L, H, D, 34, Q) == -1
+
+
+def test_gate_level_workspaces_with_state_rows():
+    """The gate-level form at even N > 2 scans N / 2 state rows per head as virtual heads: the forward
+    workspace is the fused scan's with H N / 2 heads; the backward's adds fp32 dk and dq partials (B, L,
+    H P, D) (P = N / 2, or N / 8 where a D-64 backward wave of 4 virtual heads sums its rows first) and
+    dbeta, dsel (B, L, H N/2) partials after a 16-byte aligned layout."""
+    lib = _lib.load()
+    B, L, H, D, Q = 2, 1000, 3, 64, 64
+    for N in (4, 6, 16, 32):
+        Hv = H * N // 2
+        assert lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, N, Q) == \
+            lib.cdssm_fused_scan_workspace_bytes(B, L, Hv, D, 2, Q)
+        base = lib.cdssm_fused_scan_bwd_workspace_bytes(B, L, Hv, D, 2, Q)
+        R = N // 2
+        P = R // 4 if R % 4 == 0 else R
+        want = -(-base // 16) * 16 + 2 * B * L * H * (P * D + R) * 4
+        assert lib.cdssm_fused_scan_bwd_workspace_bytes(B, L, H, D, N, Q) == want
+    for N in (3, 34, 0):
+        assert lib.cdssm_fused_scan_workspace_bytes(B, L, H, D, N, Q) == -1
+        assert lib.cdssm_fused_scan_bwd_workspace_bytes(B, L, H, D, N, Q) == -1
+
+
+def test_scan_level_entries_still_reject_state_rows():
+    """Only the gate-level and SSD entries take N > 2; the scan-level forward rejects it before any
+    device work (fake pointers are never touched)."""
+    lib = _lib.load()
+    p = 16
+    st = lib.cdssm_fused_scan_fwd(1, *([p] * 7), p, p, 1.0, None, p, p, p, 1, 64, 2, 64, 4, 64, None)
+    assert st != 0 and "state_dim N = 2" in _lib.last_error()
 
 
 def test_lookback_status_rejects_a_null_status_pointer_without_touching_the_gpu():
