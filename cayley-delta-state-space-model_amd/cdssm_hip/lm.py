@@ -408,6 +408,74 @@ def group_norm_gate(y: Tensor, num_groups: int, gamma: Tensor, beta: Tensor, eps
     return out, torch.stack([k0, part[..., 0], part[..., 1], n], dim=-1).contiguous()
 
 
+class GroupNormGateFn(torch.autograd.Function):
+    """The block's epilogue after readout_proj with gradients (block.py:215-225 under autograd):
+    out = GroupNorm_G(y) (fp32, rounded to y's dtype) * silu(z) + D * x_conv on the HIP kernels, forward
+    ``cdssm_group_norm_gate_fwd`` and backward ``cdssm_group_norm_gate_bwd`` (dy, dz, dx_conv for the
+    D x_conv term, dgamma, dbeta, dD with the reference's rounding points and the GroupNorm backward in
+    fp32), in place of torch's cast, group_norm, silu, products and sum and their backwards.  y, x_conv
+    (B, L, C) dense, z (B, L, C) with one token stride, all 16-byte aligned; ``usable`` says whether a call
+    qualifies."""
+
+    @staticmethod
+    def usable(y: Tensor, z: Tensor, x_conv: Tensor, num_groups: int, params) -> bool:
+        if not (y.is_cuda and y.dtype in _lib.DTYPE_CODE and z.dtype == y.dtype and x_conv.dtype == y.dtype):
+            return False
+        B, L, C = y.shape
+        nv = 16 // y.element_size()
+        if C % num_groups or (C // num_groups) % nv or (64 * nv) % (C // num_groups):
+            return False
+        try:
+            zs = _token_view(z, C)
+        except ValueError:
+            return False
+        if not (y.is_contiguous() and x_conv.is_contiguous()) or (zs * y.element_size()) % 16:
+            return False
+        return all(t.data_ptr() % 16 == 0 for t in (y, z, x_conv, *params))
+
+    @staticmethod
+    def forward(ctx, y, z, x_conv, gamma, beta, D, num_groups, eps):
+        B, L, C = y.shape
+        G = int(num_groups)
+        zs = _token_view(z, C)
+        pdt = gamma.dtype if gamma.dtype in _lib.DTYPE_CODE else torch.float32
+        g = gamma.detach().to(dtype=pdt).contiguous()
+        b = beta.detach().to(dtype=pdt).contiguous()
+        Dp = D.detach().to(y.dtype).contiguous()
+        lib = _lib.load()
+        ws = torch.empty(max(1, lib.cdssm_group_norm_workspace_bytes(B, G, L) // 4), dtype=torch.float32,
+                         device=y.device)
+        out = torch.empty_like(y)
+        st = lib.cdssm_group_norm_gate_fwd(_lib.DTYPE_CODE[y.dtype], _lib.DTYPE_CODE[pdt], _lib.ptr(y), _lib.ptr(g),
+                                           _lib.ptr(b), _lib.ptr(z), zs, _lib.ptr(x_conv), _lib.ptr(Dp),
+                                           _lib.ptr(out), _lib.ptr(ws), B, L, C, G, float(eps),
+                                           _lib.stream_of(y.device))
+        _lib.check(st, "cdssm_group_norm_gate_fwd")
+        ctx.save_for_backward(y, z, x_conv, g, b, Dp, ws)
+        ctx.meta = (G, zs, pdt, gamma.dtype, beta.dtype, D.dtype, tuple(D.shape))
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        y, z, x_conv, g, b, Dp, ws = ctx.saved_tensors
+        G, zs, pdt, gdt, bdt, ddt, dshape = ctx.meta
+        B, L, C = y.shape
+        dout = dout.to(y.dtype).contiguous()
+        lib = _lib.load()
+        wsb = torch.empty(max(1, lib.cdssm_group_norm_gate_bwd_workspace_bytes(B, G, L, C) // 4),
+                          dtype=torch.float32, device=y.device)
+        dy, dz, dx = torch.empty_like(y), torch.empty_like(y), torch.empty_like(y)
+        dg, db = torch.empty_like(g), torch.empty_like(b)
+        dD = torch.empty_like(Dp)
+        st = lib.cdssm_group_norm_gate_bwd(_lib.DTYPE_CODE[y.dtype], _lib.DTYPE_CODE[pdt], _lib.ptr(y), _lib.ptr(g),
+                                           _lib.ptr(b), _lib.ptr(z), zs, _lib.ptr(x_conv), _lib.ptr(Dp),
+                                           _lib.ptr(ws), _lib.ptr(dout), _lib.ptr(dy), _lib.ptr(dz), _lib.ptr(dx),
+                                           _lib.ptr(dg), _lib.ptr(db), _lib.ptr(dD), _lib.ptr(wsb), B, L, C, G,
+                                           _lib.stream_of(y.device))
+        _lib.check(st, "cdssm_group_norm_gate_bwd")
+        return (dy, dz, dx, dg.to(gdt), db.to(bdt), dD.to(ddt).reshape(dshape), None, None)
+
+
 class Conv1dSiLU(nn.Module):
     """Depthwise causal conv1d + SiLU (modules.py:14-35); weight (C, 1, K), bias (C)."""
 
@@ -543,6 +611,9 @@ class CDSSMBlock(nn.Module):
     # inference with state_dim 16 in bf16 takes the chunked MFMA form (cdssm_chunked_scan_fwd_abar, no Y);
     # False: SSDChunkwiseScan's Y read out in fp32 torch (the reference's op sequence)
     chunked_scan: bool = True
+    # training runs the GroupNorm + gate epilogue on the HIP kernels with their backward (GroupNormGateFn);
+    # False: torch's group_norm and elementwise ops (the reference's op sequence)
+    fused_epilogue: bool = True
 
     def __init__(self, config: CDSSMConfig, layer_idx: int = 0):
         super().__init__()
@@ -707,8 +778,8 @@ class CDSSMBlock(nn.Module):
     def _forward_autograd(self, x: Tensor, v_first: Optional[Tensor]):
         """The block with gradients (block.py:140-229, for training): the HIP ops that have a backward --
         conv1d+SiLU (CUDAConv1dSiLUOp), DynamicsFusedFn, NormalizeKQFn and the fused scan, whose backwards
-        are the reference's -- and torch for the projections, the RMSNorm, the shortcut and the fp32
-        GroupNorm.  The scan is ChunkwiseDeltaScanAbarFn, which returns the readout sel_C (Y.q) itself
+        are the reference's, and the GroupNorm + gate epilogue (GroupNormGateFn) -- and torch for the
+        projections, the RMSNorm and the shortcut.  The scan is ChunkwiseDeltaScanAbarFn, which returns the readout sel_C (Y.q) itself
         and never forms Y (state_dim N > 2: N/2 state rows per head as virtual heads); with
         ``readout_scan`` off, SSDChunkwiseScan's Y is read out here by StateReadoutFn (the HIP readout
         and its backward).  The
@@ -746,10 +817,14 @@ class CDSSMBlock(nn.Module):
             Y = SSDChunkwiseScan(cfg.chunk_size, N)(A_bar, K, V_gated, beta)          # block.py:198
             retrieved = (StateReadoutFn.apply(Y, Q) + shortcut) * sel_C.unsqueeze(-1)     # block.py:208-211
         y = self.readout_proj(retrieved.reshape(B, L, H * N))
-        y = torch.nn.functional.group_norm(y.float().transpose(1, 2), self.ssm_norm.num_groups,
-                                           self.ssm_norm.weight.float(), self.ssm_norm.bias.float(),
-                                           self.ssm_norm.eps).to(y.dtype).transpose(1, 2)  # block.py:216-223
-        y = y * torch.nn.functional.silu(z) + self.D * x_conv
+        G, gn = self.ssm_norm.num_groups, self.ssm_norm
+        if self.fused_epilogue and GroupNormGateFn.usable(y, z, x_conv, G, (gn.weight, gn.bias, self.D)):
+            # block.py:216-225 on the HIP kernels, forward and backward
+            y = GroupNormGateFn.apply(y, z, x_conv, gn.weight, gn.bias, self.D, G, gn.eps)
+        else:
+            y = torch.nn.functional.group_norm(y.float().transpose(1, 2), G, gn.weight.float(), gn.bias.float(),
+                                               gn.eps).to(y.dtype).transpose(1, 2)  # block.py:216-223
+            y = y * torch.nn.functional.silu(z) + self.D * x_conv
         return residual + self.out_proj(y.to(self.out_proj.weight.dtype)), v_first
 
     def step(self, x: Tensor, v_first: Optional[Tensor], cache: dict):

@@ -462,6 +462,194 @@ __global__ __launch_bounds__(256) void state_readout_bwd_kernel(const typename T
   acc.store(dq + th * D + off);
 }
 
+// ---------------------------------------------------------------------------
+// Backward of the GroupNorm + gate + skip epilogue (block.py:215-225 under
+// autograd) with the forward's rounding points: xh = (y - mean) rstd,
+// gn = rnd(xh gamma + beta), s = rnd(silu(z)), out = rnd(rnd(gn s) + rnd(D x)).
+// Given dout: dgn = rnd(dout s) (from here the GroupNorm backward in fp32),
+//   dgamma = sum over (b, l) of dgn xh, dbeta = sum dgn, dD = sum rnd(dout x),
+//   dy = rnd(rstd (dgn gamma - A - xh Bm)) with A, Bm the means of dgn gamma
+//        and dgn gamma xh over the (b, group) the element normalises with,
+//   dz = rnd(rnd(dout gn) sigmoid(z) (1 + z (1 - sigmoid(z)))),
+//   dx = rnd(dout D).
+// Three launches: per (b, slice of tokens) the partial sums (gnb_reduce), their
+// totals in a fixed order (gnb_finalize), the elementwise gradients
+// (gnb_apply).  One 16-byte vector of channels per thread; a channel vector
+// lies in one group and a block's 64 vectors hold whole groups (the entry
+// checks both).
+// ---------------------------------------------------------------------------
+template <typename P, int N>
+__device__ __forceinline__ void load_affine(const typename P::raw* gamma, const typename P::raw* beta, int c,
+                                            float (&ga)[N], float (&be)[N]) {
+  constexpr int M = 16 / P::bytes <= N ? 16 / P::bytes : 1;
+#pragma unroll
+  for (int h = 0; h < N; h += M) {
+    Vec16<P, M> g, bb;
+    g.load(gamma + c + h);
+    bb.load(beta + c + h);
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+      ga[h + j] = g.v[j];
+      be[h + j] = bb.v[j];
+    }
+  }
+}
+
+template <typename T, typename P>
+__global__ __launch_bounds__(256) void gnb_reduce_kernel(const typename T::raw* __restrict__ y,
+                                                         const float2* __restrict__ stats,
+                                                         const typename P::raw* __restrict__ gamma,
+                                                         const typename P::raw* __restrict__ beta,
+                                                         const typename T::raw* __restrict__ z, int64_t z_ts,
+                                                         const typename T::raw* __restrict__ xc,
+                                                         const typename T::raw* __restrict__ dout,
+                                                         float* __restrict__ chan_part, float2* __restrict__ grp_part,
+                                                         int L, int C, int G, int S) {
+  constexpr int N = 16 / T::bytes;
+  __shared__ float red[4][kWave][3 * N];
+  __shared__ float2 gred[4][kWave];
+  const int tx = int(threadIdx.x) % kWave, ty = int(threadIdx.x) / kWave;
+  const int bs = blockIdx.x, b = bs / S, sp = bs % S;
+  const int ls = (L + S - 1) / S;
+  const int t0 = sp * ls, t1 = min(L, t0 + ls);
+  const int Cg = C / G, vpg = Cg / N;  // channel vectors per group
+  const int c = (int(blockIdx.y) * kWave + tx) * N;
+  const bool act = c < C;
+  const int cc = act ? c : 0;
+  const int g = cc / Cg;
+  const float2 st = stats[b * G + g];
+  float ga[N], be[N];
+  load_affine<P, N>(gamma, beta, cc, ga, be);
+  float ag[N], ab[N], ad[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) ag[j] = ab[j] = ad[j] = 0.0f;
+  float sa = 0.0f, sb = 0.0f;
+  if (act) {
+    for (int t = t0 + ty; t < t1; t += 4) {
+      const int64_t tok = int64_t(b) * L + t;
+      Vec16<T> yv, zv, xv, dv;
+      yv.load(y + tok * C + c);
+      zv.load(z + tok * z_ts + c);
+      xv.load(xc + tok * C + c);
+      dv.load(dout + tok * C + c);
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        const float xh = (yv.v[j] - st.x) * st.y;
+        const float sv = rnd<T>(silu_fast(zv.v[j]));
+        const float dg = rnd<T>(dv.v[j] * sv);
+        ag[j] = fmaf(dg, xh, ag[j]);
+        ab[j] += dg;
+        ad[j] += rnd<T>(dv.v[j] * xv.v[j]);
+        const float dgg = dg * ga[j];
+        sa += dgg;
+        sb = fmaf(dgg, xh, sb);
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    red[ty][tx][j] = ag[j];
+    red[ty][tx][N + j] = ab[j];
+    red[ty][tx][2 * N + j] = ad[j];
+  }
+  gred[ty][tx] = make_float2(sa, sb);
+  __syncthreads();
+  if (ty == 0 && act) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        const float v = ((red[0][tx][k * N + j] + red[1][tx][k * N + j]) + red[2][tx][k * N + j]) +
+                        red[3][tx][k * N + j];
+        chan_part[(int64_t(bs) * 3 + k) * C + c + j] = v;
+      }
+    }
+    if (tx % vpg == 0) {
+      float2 acc = make_float2(0.0f, 0.0f);
+      for (int u = 0; u < vpg; ++u)
+        for (int r = 0; r < 4; ++r) {
+          acc.x += gred[r][tx + u].x;
+          acc.y += gred[r][tx + u].y;
+        }
+      grp_part[(int64_t(b) * G + g) * S + sp] = acc;
+    }
+  }
+}
+
+template <typename T, typename P>
+__global__ __launch_bounds__(256) void gnb_finalize_kernel(const float* __restrict__ chan_part,
+                                                           const float2* __restrict__ grp_part,
+                                                           typename P::raw* __restrict__ dgamma,
+                                                           typename P::raw* __restrict__ dbeta,
+                                                           typename T::raw* __restrict__ dD,
+                                                           float2* __restrict__ gmeans, int BS, int C, int BG,
+                                                           int S, float inv_n) {
+  const int i = int(blockIdx.x) * 256 + int(threadIdx.x);
+  if (i < C) {
+    float a = 0.0f, bb = 0.0f, d = 0.0f;
+    for (int r = 0; r < BS; ++r) {
+      a += chan_part[(int64_t(r) * 3 + 0) * C + i];
+      bb += chan_part[(int64_t(r) * 3 + 1) * C + i];
+      d += chan_part[(int64_t(r) * 3 + 2) * C + i];
+    }
+    P::store(dgamma + i, a);
+    P::store(dbeta + i, bb);
+    T::store(dD + i, d);
+  }
+  if (i < BG) {
+    float2 acc = make_float2(0.0f, 0.0f);
+    for (int s = 0; s < S; ++s) {
+      acc.x += grp_part[int64_t(i) * S + s].x;
+      acc.y += grp_part[int64_t(i) * S + s].y;
+    }
+    gmeans[i] = make_float2(acc.x * inv_n, acc.y * inv_n);
+  }
+}
+
+template <typename T, typename P>
+__global__ __launch_bounds__(256) void gnb_apply_kernel(const typename T::raw* __restrict__ y,
+                                                        const float2* __restrict__ stats,
+                                                        const float2* __restrict__ gmeans,
+                                                        const typename P::raw* __restrict__ gamma,
+                                                        const typename P::raw* __restrict__ beta,
+                                                        const typename T::raw* __restrict__ z, int64_t z_ts,
+                                                        const typename T::raw* __restrict__ Dp,
+                                                        const typename T::raw* __restrict__ dout,
+                                                        typename T::raw* __restrict__ dy,
+                                                        typename T::raw* __restrict__ dz,
+                                                        typename T::raw* __restrict__ dx, int BL, int L, int C,
+                                                        int G) {
+  constexpr int N = 16 / T::bytes;
+  // block: 4 tokens x 64 channel vectors; grid (tokens / 4, vectors per row / 64)
+  const int tok = int(blockIdx.x) * 4 + int(threadIdx.x) / kWave;
+  const int c = (int(blockIdx.y) * kWave + int(threadIdx.x) % kWave) * N;
+  if (tok >= BL || c >= C) return;
+  const int bg = (tok / L) * G + c / (C / G);
+  const float2 st = stats[bg], gm = gmeans[bg];
+  float ga[N], be[N];
+  load_affine<P, N>(gamma, beta, c, ga, be);
+  Vec16<T> yv, zv, dv, Dv, oy, oz, ox;
+  yv.load(y + int64_t(tok) * C + c);
+  zv.load(z + int64_t(tok) * z_ts + c);
+  dv.load(dout + int64_t(tok) * C + c);
+  Dv.load(Dp + c);
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const float xh = (yv.v[j] - st.x) * st.y;
+    const float gn = rnd<T>(fmaf(xh, ga[j], be[j]));
+    const float zj = zv.v[j];
+    const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-zj));
+    const float sv = rnd<T>(zj * sg);
+    const float dg = rnd<T>(dv.v[j] * sv);
+    oy.v[j] = st.y * (dg * ga[j] - gm.x - xh * gm.y);
+    oz.v[j] = rnd<T>(dv.v[j] * gn) * sg * (1.0f + zj * (1.0f - sg));
+    ox.v[j] = dv.v[j] * Dv.v[j];
+  }
+  oy.store(dy + int64_t(tok) * C + c);
+  oz.store(dz + int64_t(tok) * C + c);
+  ox.store(dx + int64_t(tok) * C + c);
+}
+
 template <typename F>
 int by_dtype(int dtype, const char* op, F&& f) {
   if (dtype == 1) return f(BF16{});
@@ -622,9 +810,12 @@ extern "C" int cdssm_state_readout_bwd(int dtype, const void* Y, const void* q, 
   });
 }
 
+// Slices of the token axis per batch row in the GroupNorm passes.
+static int gn_slices(int64_t L) { return int(std::min<int64_t>(16, std::max<int64_t>(1, L / 256))); }
+
 extern "C" int64_t cdssm_group_norm_workspace_bytes(int64_t B, int64_t G, int64_t L) {
   if (B <= 0 || G <= 0 || L <= 0) return -1;
-  const int64_t S = std::min<int64_t>(16, std::max<int64_t>(1, L / 256));
+  const int64_t S = gn_slices(L);
   return (B * G * S + B * G) * int64_t(sizeof(float2));
 }
 
@@ -654,7 +845,7 @@ extern "C" int cdssm_group_norm_gate_fwd(int dtype, int param_dtype, const void*
     constexpr int NV = 16 / T::bytes;
     const bool vec = (C / G) % NV == 0 && aligned16(y) && aligned16(z) && aligned16(x_conv) && aligned16(Dp) &&
                      aligned16(out) && aligned16(gamma) && aligned16(beta) && (z_token_stride * T::bytes) % 16 == 0;
-    const int S = int(std::min<int64_t>(16, std::max<int64_t>(1, L / 256)));
+    const int S = gn_slices(L);
     const int BG = int(B * G);
     float2* part = reinterpret_cast<float2*>(workspace);
     float2* stats = part + int64_t(BG) * S;
@@ -681,6 +872,87 @@ extern "C" int cdssm_group_norm_gate_fwd(int dtype, int param_dtype, const void*
       go(std::integral_constant<int, 1>{}, BF16{});
     else
       go(std::integral_constant<int, 1>{}, F32{});
+    return cdssm_host::check_launch(op);
+  });
+}
+
+extern "C" int64_t cdssm_group_norm_gate_bwd_workspace_bytes(int64_t B, int64_t G, int64_t L, int64_t C) {
+  if (B <= 0 || G <= 0 || L <= 0 || C <= 0) return -1;
+  const int64_t S = gn_slices(L);
+  // per-channel partials (B S, 3, C), per-group partials (B G S) and means (B G)
+  return B * S * 3 * C * int64_t(sizeof(float)) + (B * G * S + B * G) * int64_t(sizeof(float2));
+}
+
+extern "C" int cdssm_group_norm_gate_bwd(int dtype, int param_dtype, const void* y, const void* gamma,
+                                         const void* beta, const void* z, int64_t z_token_stride, const void* x_conv,
+                                         const void* Dp, const float* fwd_workspace, const void* dout, void* dy,
+                                         void* dz, void* dx_conv, void* dgamma, void* dbeta, void* dD,
+                                         float* workspace, int64_t B, int64_t L, int64_t C, int64_t G,
+                                         hipStream_t stream) {
+  const char* op = "cdssm_group_norm_gate_bwd";
+  return by_dtype(dtype, op, [&](auto t) -> int {
+    using T = decltype(t);
+    using raw = typename T::raw;
+    constexpr int NV = 16 / T::bytes;
+    if (param_dtype != 0 && param_dtype != 1) {
+      cdssm_host::set_error("%s: param_dtype must be 0 (fp32) or 1 (bf16), got %d", op, param_dtype);
+      return CDSSM_EINVAL;
+    }
+    if (B <= 0 || L <= 0 || C <= 0 || G <= 0 || C % G != 0 || z_token_stride < C || B * L >= (int64_t(1) << 31) ||
+        C >= (int64_t(1) << 24) || B * G * C > 0x7fffffffLL) {
+      cdssm_host::set_error("%s: need C divisible by G and a z token stride >= C (B=%lld L=%lld C=%lld G=%lld)",
+                            op, (long long)B, (long long)L, (long long)C, (long long)G);
+      return CDSSM_EINVAL;
+    }
+    // a channel vector in one group, whole groups in a block's 64 vectors
+    const int64_t Cg = C / G;
+    if (Cg % NV != 0 || (int64_t(kWave) * NV) % Cg != 0) {
+      cdssm_host::set_error("%s: the group width C / G = %lld must be a multiple of %d dividing %d", op,
+                            (long long)Cg, NV, kWave * NV);
+      return CDSSM_EINVAL;
+    }
+    if (!y || !gamma || !beta || !z || !x_conv || !Dp || !fwd_workspace || !dout || !dy || !dz || !dx_conv ||
+        !dgamma || !dbeta || !dD || !workspace) {
+      cdssm_host::set_error("%s: null pointer argument", op);
+      return CDSSM_EINVAL;
+    }
+    if (!aligned16(y) || !aligned16(z) || !aligned16(x_conv) || !aligned16(Dp) || !aligned16(dout) ||
+        !aligned16(dy) || !aligned16(dz) || !aligned16(dx_conv) || !aligned16(gamma) || !aligned16(beta) ||
+        (z_token_stride * T::bytes) % 16 != 0) {
+      cdssm_host::set_error("%s: tensors must be 16-byte aligned (and z's token stride a multiple of 16 bytes)", op);
+      return CDSSM_EINVAL;
+    }
+    const int S = gn_slices(L);
+    const int BG = int(B * G), BS = int(B) * S;
+    // the forward's statistics (mean, rstd) follow its partial sums
+    const float2* stats = reinterpret_cast<const float2*>(fwd_workspace) + int64_t(BG) * S;
+    float* chan = workspace;
+    float2* gpart = reinterpret_cast<float2*>(chan + int64_t(BS) * 3 * C);
+    float2* gm = gpart + int64_t(BG) * S;
+    auto go = [&](auto pt) {
+      using P = decltype(pt);
+      using praw = typename P::raw;
+      const int vpr = int(C) / NV;
+      hipLaunchKernelGGL((gnb_reduce_kernel<T, P>), dim3(unsigned(BS), unsigned((vpr + kWave - 1) / kWave)),
+                         dim3(256), 0, stream, static_cast<const raw*>(y), stats, static_cast<const praw*>(gamma),
+                         static_cast<const praw*>(beta), static_cast<const raw*>(z), z_token_stride,
+                         static_cast<const raw*>(x_conv), static_cast<const raw*>(dout), chan, gpart, int(L), int(C),
+                         int(G), S);
+      const int n = int(std::max<int64_t>(C, BG));
+      hipLaunchKernelGGL((gnb_finalize_kernel<T, P>), dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, chan,
+                         gpart, static_cast<praw*>(dgamma), static_cast<praw*>(dbeta), static_cast<raw*>(dD), gm, BS,
+                         int(C), BG, S, 1.0f / (float(L) * float(Cg)));
+      const dim3 grid(unsigned((B * L + 3) / 4), unsigned((vpr + kWave - 1) / kWave));
+      hipLaunchKernelGGL((gnb_apply_kernel<T, P>), grid, dim3(256), 0, stream, static_cast<const raw*>(y), stats, gm,
+                         static_cast<const praw*>(gamma), static_cast<const praw*>(beta), static_cast<const raw*>(z),
+                         z_token_stride, static_cast<const raw*>(Dp), static_cast<const raw*>(dout),
+                         static_cast<raw*>(dy), static_cast<raw*>(dz), static_cast<raw*>(dx_conv), int(B * L), int(L),
+                         int(C), int(G));
+    };
+    if (param_dtype == 1)
+      go(BF16{});
+    else
+      go(F32{});
     return cdssm_host::check_launch(op);
   });
 }

@@ -575,6 +575,28 @@ int cdssm_group_norm_gate_fwd(int dtype, int param_dtype, const void* y, const v
                               hipStream_t stream);
 
 /*
+ * Backward of cdssm_group_norm_gate_fwd, for training through the block
+ * (block.py:215-225 under autograd; replaces the backward of torch's
+ * group_norm, silu, the products and the sum): given dout (B, L, C) and the
+ * forward's workspace (its per-group statistics), writes dy, dz, dx_conv
+ * (B, L, C) dense of `dtype` (dx_conv: the D x_conv term's part only),
+ * dgamma, dbeta (C) of `param_dtype` and dD (C) of `dtype`, with the rounding
+ * points of the reference's ops (each torch op's bf16 output) and the
+ * GroupNorm backward in fp32; every sum in a fixed order (bit-reproducible).
+ * The group width C / G must be a multiple of 16 / element bytes dividing
+ * 64 times that; every tensor 16-byte aligned.  Three launches (partial sums
+ * per batch row and token slice, totals, elementwise); workspace of
+ * cdssm_group_norm_gate_bwd_workspace_bytes.  No reference counterpart beyond
+ * the torch ops it replaces.
+ */
+int64_t cdssm_group_norm_gate_bwd_workspace_bytes(int64_t B, int64_t G, int64_t L, int64_t C);
+int cdssm_group_norm_gate_bwd(int dtype, int param_dtype, const void* y, const void* gamma, const void* beta,
+                              const void* z, int64_t z_token_stride, const void* x_conv, const void* D,
+                              const float* fwd_workspace, const void* dout, void* dy, void* dz, void* dx_conv,
+                              void* dgamma, void* dbeta, void* dD, float* workspace, int64_t B, int64_t L, int64_t C,
+                              int64_t G, hipStream_t stream);
+
+/*
  * Replaces normalize_kq_fwd_cuda / normalize_kq_bwd_cuda (normalize_kq.cu:168-244;
  * NormalizeKQFn, ops.py:84-97): rows of length D (any D <= 256; the reference kernel is
  * correct only for D = 64), x_hat = x rsqrt(sum x^2 + 1e-6).
