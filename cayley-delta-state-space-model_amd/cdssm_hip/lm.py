@@ -281,6 +281,23 @@ def skinny_linear(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None, resi
     return y
 
 
+def _kq_rows(K: Tensor, Q: Tensor) -> tuple:
+    """K, Q (B, L, H, D) as the fused normalisation reads them: in place where each token's (H, D) block is
+    dense and 16-byte aligned with a uniform token stride, else dense copies; (K, Q, token strides)."""
+    B, L, H, D = K.shape
+    if tuple(Q.shape) != (B, L, H, D):
+        raise ValueError(f"K and Q shapes differ: {tuple(K.shape)} vs {tuple(Q.shape)}")
+    strides, dense = [], []
+    for t in (K, Q):
+        ts = _token_stride(t, H * D)
+        if (t.stride(3) != 1 or t.stride(2) != D or ts is None or t.data_ptr() % 16
+                or (ts * t.element_size()) % 16):
+            t, ts = t.contiguous(), H * D
+        strides.append(ts)
+        dense.append(t)
+    return dense[0], dense[1], strides
+
+
 def normalize_kq_qk(K: Tensor, Q: Tensor) -> tuple:
     """K^, Q^ = x * rsqrt(sum_d x^2 + 1e-6) per (token, head) and qk = K^.Q^ (fp32), in one pass.
 
@@ -289,18 +306,7 @@ def normalize_kq_qk(K: Tensor, Q: Tensor) -> tuple:
     block.py:191-192, 202)."""
     dt = _check_gpu("normalize_kq_qk", K, Q)
     B, L, H, D = K.shape
-    if tuple(Q.shape) != (B, L, H, D):
-        raise ValueError(f"K and Q shapes differ: {tuple(K.shape)} vs {tuple(Q.shape)}")
-    strides, dense = [], []
-    for t in (K, Q):
-        ts = _token_stride(t, H * D)
-        # read in place when the rows are dense and 16-byte aligned, else from a dense copy
-        if (t.stride(3) != 1 or t.stride(2) != D or ts is None or t.data_ptr() % 16
-                or (ts * t.element_size()) % 16):
-            t, ts = t.contiguous(), H * D
-        strides.append(ts)
-        dense.append(t)
-    K, Q = dense
+    K, Q, strides = _kq_rows(K, Q)
     Ko = torch.empty((B, L, H, D), dtype=dt, device=K.device)
     Qo = torch.empty_like(Ko)
     qk = torch.empty((B, L, H), dtype=torch.float32, device=K.device)
@@ -309,6 +315,39 @@ def normalize_kq_qk(K: Tensor, Q: Tensor) -> tuple:
                                               _lib.stream_of(K.device))
     _lib.check(st, "cdssm_normalize_kq_qk_fwd")
     return Ko, Qo, qk
+
+
+class NormalizeKQQkFn(torch.autograd.Function):
+    """NormalizeKQFn (ops.py:84-97, normalize_kq.cu's rule) with the current-token q.k (block.py:191-192,
+    202) in one kernel each way: (K, Q) -> (K^, Q^, qk) with qk = K^.Q^ fp32 (B, L, H), forward
+    ``cdssm_normalize_kq_qk_fwd`` and backward ``cdssm_normalize_kq_qk_bwd``, which folds qk's gradient
+    (dK^ += dqk Q^, dQ^ += dqk K^) into the normalisation's backward.  For training through the block, in
+    place of NormalizeKQFn followed by torch's product and sum."""
+
+    @staticmethod
+    def forward(ctx, K, Q):
+        B, L, H, D = K.shape
+        Kr, Qr, strides = _kq_rows(K, Q)
+        Ko, Qo, qk = normalize_kq_qk(Kr, Qr)
+        ctx.save_for_backward(Kr, Qr)
+        ctx.strides = strides
+        return Ko, Qo, qk
+
+    @staticmethod
+    def backward(ctx, dKo, dQo, dqk):
+        Kr, Qr = ctx.saved_tensors
+        B, L, H, D = Kr.shape
+        dt = Kr.dtype
+        dKo = torch.zeros((B, L, H, D), dtype=dt, device=Kr.device) if dKo is None else dKo.to(dt).contiguous()
+        dQo = torch.zeros((B, L, H, D), dtype=dt, device=Kr.device) if dQo is None else dQo.to(dt).contiguous()
+        dqk = (torch.zeros((B, L, H), dtype=torch.float32, device=Kr.device) if dqk is None
+               else dqk.to(torch.float32).contiguous())
+        dK, dQ = torch.empty_like(dKo), torch.empty_like(dQo)
+        st = _lib.load().cdssm_normalize_kq_qk_bwd(_lib.DTYPE_CODE[dt], _lib.ptr(Kr), ctx.strides[0], _lib.ptr(Qr),
+                                                  ctx.strides[1], _lib.ptr(dKo), _lib.ptr(dQo), _lib.ptr(dqk),
+                                                  _lib.ptr(dK), _lib.ptr(dQ), B * L, H, D, _lib.stream_of(Kr.device))
+        _lib.check(st, "cdssm_normalize_kq_qk_bwd")
+        return dK, dQ
 
 
 class StateReadoutFn(torch.autograd.Function):
@@ -803,9 +842,14 @@ class CDSSMBlock(nn.Module):
             gates, self.log_dt_scale.float(), self.rope_freqs, cfg.gating_c, cfg.bf16_omega_thresh,
             cfg.bf16_delta, cfg.bf16_smoothness, cfg.eps_adaptive_dt, H, N)           # block.py:184-188
         Q = self.Q_proj(x_conv).reshape(B, L, H, D)
-        K, Q = NormalizeKQFn.apply(K, Q)                                              # block.py:191-192
+        if self.fused_epilogue and D // (16 // K.element_size()) in (4, 8, 16, 32) and D % (16 // K.element_size()) == 0:
+            # block.py:191-192 and the q.k of :202 in one kernel each way
+            K, Q, qk = NormalizeKQQkFn.apply(K, Q)
+            qk = qk.to(V.dtype)
+        else:
+            K, Q = NormalizeKQFn.apply(K, Q)                                          # block.py:191-192
+            qk = (Q * K).sum(-1)                                                      # block.py:202
         V_gated = V * vp.repeat_interleave(2, dim=-1)                                 # block.py:194-195
-        qk = (Q * K).sum(-1)                                                          # block.py:202
         shortcut = self.shortcut_scale * (qk * qk).unsqueeze(-1) * V_gated            # block.py:204-208
         if self.readout_scan and D in (64, 128) and 1 <= cfg.chunk_size <= 128:
             # the fused scan with its readout, sel_C (Y.q) (block.py:198, 208-211), without forming the

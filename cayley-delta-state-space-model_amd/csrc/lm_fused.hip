@@ -158,6 +158,65 @@ __global__ __launch_bounds__(256) void normalize_qk_kernel(const typename T::raw
   if (sub == 0) qk[r] = d;
 }
 
+// Backward of normalize_qk_kernel (training): given the gradients of K^, Q^
+// (dense) and of qk (fp32), per row gk = dK^ + dqk Q^, gq = dQ^ + dqk K^ in
+// fp32 and the normalisation's backward dK = (gk - K^ <gk, K^>) rsqrt(sum k^2
+// + 1e-6) (normalize_kq.cu's rule, as NormalizeKQFn), likewise dQ; K^, Q^ are
+// rebuilt from K, Q as the forward rounds them.  dK, dQ dense.
+template <typename T, int LPR>
+__global__ __launch_bounds__(256) void normalize_qk_bwd_kernel(const typename T::raw* __restrict__ k, int64_t k_ts,
+                                                               const typename T::raw* __restrict__ q, int64_t q_ts,
+                                                               const typename T::raw* __restrict__ dko,
+                                                               const typename T::raw* __restrict__ dqo,
+                                                               const float* __restrict__ dqk,
+                                                               typename T::raw* __restrict__ dk,
+                                                               typename T::raw* __restrict__ dq, int64_t rows,
+                                                               int H) {
+  constexpr int N = Vec16<T>::N, D = LPR * N;
+  const int r = int((int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / LPR);  // rows < 2^31 (host check)
+  const int sub = threadIdx.x % LPR;
+  const bool ok = r < rows;
+  const int rr = ok ? r : int(rows) - 1;  // clamped row: every lane takes part in the reductions
+  const int tok = rr / H;
+  const int h = rr - tok * H;
+  Vec16<T> a, b, ga, gb;
+  a.load(k + int64_t(tok) * k_ts + h * D + sub * N);
+  b.load(q + int64_t(tok) * q_ts + h * D + sub * N);
+  ga.load(dko + int64_t(rr) * D + sub * N);
+  gb.load(dqo + int64_t(rr) * D + sub * N);
+  const float g = dqk[rr];
+  float sk = 0.0f, sq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    sk = fmaf(a.v[i], a.v[i], sk);
+    sq = fmaf(b.v[i], b.v[i], sq);
+  }
+  sk = group_sum<LPR>(sk);
+  sq = group_sum<LPR>(sq);
+  const float ik = rsqrtf(sk + 1e-6f), iq = rsqrtf(sq + 1e-6f);
+  float kh[N], qh[N], pk = 0.0f, pq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    kh[i] = rnd<T>(a.v[i] * ik);
+    qh[i] = rnd<T>(b.v[i] * iq);
+    ga.v[i] = fmaf(g, qh[i], ga.v[i]);
+    gb.v[i] = fmaf(g, kh[i], gb.v[i]);
+    // the projections onto the unrounded directions x * inv, as the normalisation's backward takes them
+    pk = fmaf(ga.v[i], a.v[i] * ik, pk);
+    pq = fmaf(gb.v[i], b.v[i] * iq, pq);
+  }
+  pk = group_sum<LPR>(pk);
+  pq = group_sum<LPR>(pq);
+  if (!ok) return;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    ga.v[i] = (ga.v[i] - a.v[i] * ik * pk) * ik;
+    gb.v[i] = (gb.v[i] - b.v[i] * iq * pq) * iq;
+  }
+  ga.store(dk + int64_t(r) * D + sub * N);
+  gb.store(dq + int64_t(r) * D + sub * N);
+}
+
 // ---------------------------------------------------------------------------
 // Current-token shortcut through the readout, per (token, head):
 //   retrieved[j] += scale * (q.k)^2 * sel_C * vp * V[j],  j = re, im.
@@ -576,6 +635,9 @@ __global__ __launch_bounds__(256) void gnb_reduce_kernel(const typename T::raw* 
   }
 }
 
+// Blocks [0, ceil(C / 64)): 64 channels each, the partial rows split over 4
+// thread rows and joined in a fixed order; the blocks after: one (b, group)
+// per thread.
 template <typename T, typename P>
 __global__ __launch_bounds__(256) void gnb_finalize_kernel(const float* __restrict__ chan_part,
                                                            const float2* __restrict__ grp_part,
@@ -584,18 +646,34 @@ __global__ __launch_bounds__(256) void gnb_finalize_kernel(const float* __restri
                                                            typename T::raw* __restrict__ dD,
                                                            float2* __restrict__ gmeans, int BS, int C, int BG,
                                                            int S, float inv_n) {
-  const int i = int(blockIdx.x) * 256 + int(threadIdx.x);
-  if (i < C) {
+  __shared__ float red[4][kWave][3];
+  const int ncb = (C + kWave - 1) / kWave;
+  if (int(blockIdx.x) < ncb) {
+    const int tx = int(threadIdx.x) % kWave, ty = int(threadIdx.x) / kWave;
+    const int c = int(blockIdx.x) * kWave + tx;
     float a = 0.0f, bb = 0.0f, d = 0.0f;
-    for (int r = 0; r < BS; ++r) {
-      a += chan_part[(int64_t(r) * 3 + 0) * C + i];
-      bb += chan_part[(int64_t(r) * 3 + 1) * C + i];
-      d += chan_part[(int64_t(r) * 3 + 2) * C + i];
+    if (c < C) {
+      for (int r = ty; r < BS; r += 4) {
+        a += chan_part[(int64_t(r) * 3 + 0) * C + c];
+        bb += chan_part[(int64_t(r) * 3 + 1) * C + c];
+        d += chan_part[(int64_t(r) * 3 + 2) * C + c];
+      }
     }
-    P::store(dgamma + i, a);
-    P::store(dbeta + i, bb);
-    T::store(dD + i, d);
+    red[ty][tx][0] = a;
+    red[ty][tx][1] = bb;
+    red[ty][tx][2] = d;
+    __syncthreads();
+    if (ty == 0 && c < C) {
+      float v[3];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) v[k] = ((red[0][tx][k] + red[1][tx][k]) + red[2][tx][k]) + red[3][tx][k];
+      P::store(dgamma + c, v[0]);
+      P::store(dbeta + c, v[1]);
+      T::store(dD + c, v[2]);
+    }
+    return;
   }
+  const int i = (int(blockIdx.x) - ncb) * 256 + int(threadIdx.x);
   if (i < BG) {
     float2 acc = make_float2(0.0f, 0.0f);
     for (int s = 0; s < S; ++s) {
@@ -722,6 +800,45 @@ extern "C" int cdssm_normalize_kq_qk_fwd(int dtype, const void* K, int64_t k_tok
       hipLaunchKernelGGL((normalize_qk_kernel<T, LPR>), dim3(grid), dim3(256), 0, stream,
                          static_cast<const raw*>(K), k_token_stride, static_cast<const raw*>(Q), q_token_stride,
                          static_cast<raw*>(K_out), static_cast<raw*>(Q_out), qk, rows, int(H));
+    };
+    if (lpr == 4) go(std::integral_constant<int, 4>{});
+    else if (lpr == 8) go(std::integral_constant<int, 8>{});
+    else if (lpr == 16) go(std::integral_constant<int, 16>{});
+    else go(std::integral_constant<int, 32>{});
+    return cdssm_host::check_launch(op);
+  });
+}
+
+extern "C" int cdssm_normalize_kq_qk_bwd(int dtype, const void* K, int64_t k_token_stride, const void* Q,
+                                         int64_t q_token_stride, const void* dK_out, const void* dQ_out,
+                                         const float* dqk, void* dK, void* dQ, int64_t BL, int64_t H, int64_t D,
+                                         hipStream_t stream) {
+  const char* op = "cdssm_normalize_kq_qk_bwd";
+  return by_dtype(dtype, op, [&](auto t) -> int {
+    using T = decltype(t);
+    using raw = typename T::raw;
+    constexpr int N = Vec16<T>::N;
+    const int64_t lpr = D / N;
+    if (BL <= 0 || H <= 0 || D % N != 0 || !(lpr == 4 || lpr == 8 || lpr == 16 || lpr == 32) ||
+        k_token_stride < H * D || q_token_stride < H * D || BL * H >= (int64_t(1) << 31)) {
+      cdssm_host::set_error("%s: need D in {%d, %d, %d, %d} and token strides >= H*D (BL=%lld H=%lld D=%lld)", op,
+                            4 * N, 8 * N, 16 * N, 32 * N, (long long)BL, (long long)H, (long long)D);
+      return CDSSM_EINVAL;
+    }
+    if (!K || !Q || !dK_out || !dQ_out || !dqk || !dK || !dQ || !aligned16(K) || !aligned16(Q) ||
+        !aligned16(dK_out) || !aligned16(dQ_out) || !aligned16(dK) || !aligned16(dQ) ||
+        (k_token_stride * T::bytes) % 16 != 0 || (q_token_stride * T::bytes) % 16 != 0) {
+      cdssm_host::set_error("%s: pointers must be non-null and 16-byte aligned, token strides whole 16 bytes", op);
+      return CDSSM_EINVAL;
+    }
+    const int64_t rows = BL * H;
+    const unsigned grid = unsigned((rows * lpr + 255) / 256);
+    auto go = [&](auto lc) {
+      constexpr int LPR = decltype(lc)::value;
+      hipLaunchKernelGGL((normalize_qk_bwd_kernel<T, LPR>), dim3(grid), dim3(256), 0, stream,
+                         static_cast<const raw*>(K), k_token_stride, static_cast<const raw*>(Q), q_token_stride,
+                         static_cast<const raw*>(dK_out), static_cast<const raw*>(dQ_out), dqk, static_cast<raw*>(dK),
+                         static_cast<raw*>(dQ), rows, int(H));
     };
     if (lpr == 4) go(std::integral_constant<int, 4>{});
     else if (lpr == 8) go(std::integral_constant<int, 8>{});
@@ -876,9 +993,13 @@ extern "C" int cdssm_group_norm_gate_fwd(int dtype, int param_dtype, const void*
   });
 }
 
+// Token slices per batch row of the backward's partial sums: 32 tokens each
+// (8 per thread), so that a config-4 call (B8 L2048, C 1024) has 1024 blocks.
+static int gnb_slices(int64_t L) { return int(std::min<int64_t>(512, std::max<int64_t>(1, (L + 31) / 32))); }
+
 extern "C" int64_t cdssm_group_norm_gate_bwd_workspace_bytes(int64_t B, int64_t G, int64_t L, int64_t C) {
   if (B <= 0 || G <= 0 || L <= 0 || C <= 0) return -1;
-  const int64_t S = gn_slices(L);
+  const int64_t S = gnb_slices(L);
   // per-channel partials (B S, 3, C), per-group partials (B G S) and means (B G)
   return B * S * 3 * C * int64_t(sizeof(float)) + (B * G * S + B * G) * int64_t(sizeof(float2));
 }
@@ -922,10 +1043,10 @@ extern "C" int cdssm_group_norm_gate_bwd(int dtype, int param_dtype, const void*
       cdssm_host::set_error("%s: tensors must be 16-byte aligned (and z's token stride a multiple of 16 bytes)", op);
       return CDSSM_EINVAL;
     }
-    const int S = gn_slices(L);
+    const int S = gnb_slices(L);
     const int BG = int(B * G), BS = int(B) * S;
     // the forward's statistics (mean, rstd) follow its partial sums
-    const float2* stats = reinterpret_cast<const float2*>(fwd_workspace) + int64_t(BG) * S;
+    const float2* stats = reinterpret_cast<const float2*>(fwd_workspace) + int64_t(BG) * gn_slices(L);
     float* chan = workspace;
     float2* gpart = reinterpret_cast<float2*>(chan + int64_t(BS) * 3 * C);
     float2* gm = gpart + int64_t(BG) * S;
@@ -938,8 +1059,8 @@ extern "C" int cdssm_group_norm_gate_bwd(int dtype, int param_dtype, const void*
                          static_cast<const praw*>(beta), static_cast<const raw*>(z), z_token_stride,
                          static_cast<const raw*>(x_conv), static_cast<const raw*>(dout), chan, gpart, int(L), int(C),
                          int(G), S);
-      const int n = int(std::max<int64_t>(C, BG));
-      hipLaunchKernelGGL((gnb_finalize_kernel<T, P>), dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, chan,
+      const unsigned fblocks = unsigned((C + kWave - 1) / kWave + (BG + 255) / 256);
+      hipLaunchKernelGGL((gnb_finalize_kernel<T, P>), dim3(fblocks), dim3(256), 0, stream, chan,
                          gpart, static_cast<praw*>(dgamma), static_cast<praw*>(dbeta), static_cast<raw*>(dD), gm, BS,
                          int(C), BG, S, 1.0f / (float(L) * float(Cg)));
       const dim3 grid(unsigned((B * L + 3) / 4), unsigned((vpr + kWave - 1) / kWave));

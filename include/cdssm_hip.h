@@ -530,6 +530,20 @@ int cdssm_normalize_kq_qk_fwd(int dtype, const void* K, int64_t k_token_stride, 
                               int64_t D, hipStream_t stream);
 
 /*
+ * Backward of cdssm_normalize_kq_qk_fwd, for training through the block: given
+ * the gradients dK_out, dQ_out (B*L, H, D) dense of `dtype` and dqk (B*L, H)
+ * fp32 of its outputs, and its inputs K, Q (token strides as in the forward),
+ * writes dK, dQ (B*L, H, D) dense: per row g = dK_out + dqk Q^ (Q^ rounded as
+ * the forward rounds it), dK = (g - K^ <g, K^>) rsqrt(sum k^2 + 1e-6), the
+ * normalisation's rule of normalize_kq.cu (NormalizeKQFn, ops.py:84-97); dQ
+ * likewise.  Replaces NormalizeKQFn's backward together with the backward of
+ * torch's q.k product and sum (block.py:202).  Limits as the forward.
+ */
+int cdssm_normalize_kq_qk_bwd(int dtype, const void* K, int64_t k_token_stride, const void* Q, int64_t q_token_stride,
+                              const void* dK_out, const void* dQ_out, const float* dqk, void* dK, void* dQ, int64_t BL,
+                              int64_t H, int64_t D, hipStream_t stream);
+
+/*
  * The block's readout of per-token states for state_dim N > 2, where
  * SSDChunkwiseScan returns Y (block.py:208: einsum('blhsd,blhd->blhs', Y, Q)):
  * cdssm_state_readout_fwd writes r (n, N) = Y (n, N, D) . q (n, D) with fp32

@@ -1,9 +1,15 @@
-"""GPU parity of the block's GroupNorm + gate epilogue with gradients (GroupNormGateFn:
+"""GPU parity of the block's training ops on the HIP kernels with their backwards.
+
+The GroupNorm + gate epilogue (GroupNormGateFn:
 cdssm_group_norm_gate_fwd / cdssm_group_norm_gate_bwd) against autograd through the reference's op sequence
 (block.py:215-225): out = group_norm(y.float(), G, gamma.float(), beta.float(), eps).to(dtype) * silu(z)
 + D * x_conv, in fp64 on the CPU from the same (rounded) inputs.  z is a column slice of a wider tensor
 (a token stride, as the block's in_proj output gives it).  Tolerances: fp32 <= 1e-4, bf16 <= 2e-2 normwise
 for the output and every gradient (y, z, x_conv, gamma, beta, D).
+
+The K/Q normalisation with the current-token q.k (NormalizeKQQkFn: cdssm_normalize_kq_qk_fwd / _bwd) against
+fp64 autograd of NormalizeKQFn's rule (normalize_kq.cu:75-79) and q.k (block.py:191-192, 202), K a strided
+column slice as in the block: fp32 <= 1e-4, bf16 <= 2e-2.
 """
 
 import pytest
@@ -95,3 +101,40 @@ def test_group_norm_gate_backward_is_deterministic_and_matches_torch_bf16_ops():
     errs = [rel(g1, g2.grad) for g1, g2 in zip(grads[0], leaves)]
     log("   vs torch bf16 ops: " + "  ".join(f"{e:.1e}" for e in errs))
     assert max(errs) <= 2e-2
+
+
+KQ_CASES = [("fp32_D64", torch.float32, 64), ("fp32_D128", torch.float32, 128), ("bf16_D64", torch.bfloat16, 64),
+            ("bf16_D128", torch.bfloat16, 128)]
+
+
+@pytest.mark.parametrize("name,dtype,D", KQ_CASES, ids=[c[0] for c in KQ_CASES])
+def test_normalize_kq_qk_forward_and_backward(name, dtype, D):
+    from cdssm_hip.lm import NormalizeKQQkFn
+    B, L, H = 2, 300, 16
+    g = torch.Generator().manual_seed(3)
+    wide = torch.randn(B, L, 3 * H * D + 48, generator=g).to(dtype)   # K a column slice of it
+    Q = torch.randn(B, L, H, D, generator=g).to(dtype)
+    gK = torch.randn(B, L, H, D, generator=g).to(dtype)
+    gQ = torch.randn(B, L, H, D, generator=g).to(dtype)
+    gqk = torch.randn(B, L, H, generator=g)
+    off = H * D
+    # reference: fp64 on the CPU
+    wr = wide.double().requires_grad_(True)
+    qr = Q.double().requires_grad_(True)
+    Kr = wr[..., off:off + H * D].reshape(B, L, H, D)
+    Kn = Kr * torch.rsqrt((Kr * Kr).sum(-1, keepdim=True) + 1e-6)
+    Qn = qr * torch.rsqrt((qr * qr).sum(-1, keepdim=True) + 1e-6)
+    qk = (Kn * Qn).sum(-1)
+    torch.autograd.backward([Kn, Qn, qk], [gK.double(), gQ.double(), gqk.double()])
+    wg = wide.to(DEV).requires_grad_(True)
+    qg = Q.to(DEV).requires_grad_(True)
+    Kg = wg[..., off:off + H * D].reshape(B, L, H, D)
+    Ko, Qo, qko = NormalizeKQQkFn.apply(Kg, qg)
+    torch.autograd.backward([Ko, Qo, qko], [gK.to(DEV), gQ.to(DEV), gqk.to(DEV)])
+    torch.cuda.synchronize()
+    errs = {"K^": rel(Ko, Kn), "Q^": rel(Qo, Qn), "qk": rel(qko, qk), "dK": rel(wg.grad, wr.grad),
+            "dQ": rel(qg.grad, qr.grad)}
+    log(f"[normalize kq qk] {name}: " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    bad = {n: e for n, e in errs.items() if not e <= tol}
+    assert not bad, f"beyond {tol}: {bad}"
