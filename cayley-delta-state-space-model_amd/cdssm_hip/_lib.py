@@ -76,6 +76,8 @@ SIGNATURES = {
     "cdssm_state_readout_fwd": (_I32, [_I32] + [_P] * 3 + [_I64] * 3 + [_P]),
     "cdssm_state_readout_bwd": (_I32, [_I32] + [_P] * 5 + [_I64] * 3 + [_P]),
     "cdssm_group_norm_workspace_bytes": (_I64, [_I64, _I64, _I64]),
+    "cdssm_rms_norm_bwd_workspace_bytes": (_I64, [_I64, _I64]),
+    "cdssm_rms_norm_bwd": (_I32, [_I32, _P, _P, _P, _P, _P, _P, _I64, _I64, _F32, _P]),
     "cdssm_normalize_kq_qk_bwd": (_I32, [_I32, _P, _I64, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "cdssm_group_norm_gate_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "cdssm_group_norm_gate_bwd": (_I32, [_I32, _I32, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,

@@ -248,6 +248,46 @@ def rms_norm(x: Tensor, weight: Tensor, eps: float) -> Tensor:
     return y
 
 
+class RMSNormFn(torch.autograd.Function):
+    """RMSNorm with gradients on the HIP kernels (modules.py:49-53 under autograd): forward
+    ``cdssm_rms_norm_fwd``, backward ``cdssm_rms_norm_bwd`` (dx and the weight's gradient, with the
+    reference expression's rounding points; the weight's column sums in a fixed order), in place of
+    torch's cast, power, mean, rsqrt and products and their backwards.  ``usable`` says whether a call
+    qualifies (C a multiple of 64 16-byte vectors, at most 4 of them per lane)."""
+
+    @staticmethod
+    def usable(x: Tensor) -> bool:
+        if not (x.is_cuda and x.dtype in _lib.DTYPE_CODE):
+            return False
+        v = 64 * (16 // x.element_size())
+        return x.shape[-1] % v == 0 and x.shape[-1] // v <= 4
+
+    @staticmethod
+    def forward(ctx, x, weight, eps):
+        xc = x.contiguous()
+        w = weight.detach().to(x.dtype).contiguous()
+        y = rms_norm(xc, w, eps)
+        ctx.save_for_backward(xc, w)
+        ctx.meta = (float(eps), weight.dtype)
+        return y
+
+    @staticmethod
+    def backward(ctx, dout):
+        xc, w = ctx.saved_tensors
+        eps, wdt = ctx.meta
+        C = xc.shape[-1]
+        rows = xc.numel() // C
+        dout = dout.to(xc.dtype).contiguous()
+        lib = _lib.load()
+        ws = torch.empty(max(1, lib.cdssm_rms_norm_bwd_workspace_bytes(rows, C) // 4), dtype=torch.float32,
+                         device=xc.device)
+        dx, dw = torch.empty_like(xc), torch.empty_like(w)
+        st = lib.cdssm_rms_norm_bwd(_lib.DTYPE_CODE[xc.dtype], _lib.ptr(xc), _lib.ptr(w), _lib.ptr(dout), _lib.ptr(dx),
+                                    _lib.ptr(dw), _lib.ptr(ws), rows, C, eps, _lib.stream_of(xc.device))
+        _lib.check(st, "cdssm_rms_norm_bwd")
+        return dx, dw.to(wdt), None
+
+
 def _skinny_ok(x: Tensor, weight: Tensor) -> bool:
     """Whether cdssm_skinny_gemm serves x (M, K) @ weight (N, K)^T: bf16, M <= 64, K % 128 == 0,
     16-byte aligned rows."""
@@ -624,6 +664,9 @@ def group_norm_gate_step(y: Tensor, gsum: Tensor, gamma: Tensor, beta: Tensor, e
 class RMSNorm(nn.Module):
     """x * rsqrt(mean(x^2) + eps) in fp32, cast back, times weight (modules.py:38-53)."""
 
+    # training on the HIP forward and backward (RMSNormFn); False: the reference's torch expression
+    fused_backward: bool = True
+
     def __init__(self, d_model: int, eps: float = _BF16_EPS ** 2):
         super().__init__()
         self.eps = eps
@@ -631,6 +674,8 @@ class RMSNorm(nn.Module):
 
     def forward(self, x: Tensor) -> Tensor:
         if torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad):
+            if self.fused_backward and RMSNormFn.usable(x):
+                return RMSNormFn.apply(x, self.weight, self.eps)
             # training: the reference's expression (modules.py:49-53), differentiable through torch
             x32 = x.float()
             return (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + self.eps)).to(x.dtype) * self.weight

@@ -113,6 +113,95 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const typename T::raw* __
   }
 }
 
+// Backward of rms_norm_kernel (training; modules.py:49-53 under autograd), with
+// the forward's rounding points: xn = rnd(x r), r = rsqrt(mean(x^2) + eps),
+// out = rnd(xn w).  Given dout: dxn = rnd(dout w); dw = sum over rows of
+// rnd(dout xn); dx = rnd(dxn r - x r^3 (sum_j dxn_j x_j) / C).  A block of 4
+// waves takes kRmsRows rows (a wave every 4th), each lane KV 16-byte vectors
+// of channels (C = KV * 64 * vector width); the block's dw partial row is
+// written for rms_col_sum_kernel.
+constexpr int kRmsRows = 32;
+
+template <typename T, int KV>
+__global__ __launch_bounds__(256) void rms_norm_bwd_kernel(const typename T::raw* __restrict__ x,
+                                                           const typename T::raw* __restrict__ w,
+                                                           const typename T::raw* __restrict__ dout,
+                                                           typename T::raw* __restrict__ dx,
+                                                           float* __restrict__ wpart, int64_t rows, float eps) {
+  constexpr int N = Vec16<T>::N, C = KV * kWave * N;
+  __shared__ float red[4][kWave][KV * N];
+  const int lane = int(threadIdx.x) % kWave, wv = int(threadIdx.x) / kWave;
+  Vec16<T> wk[KV];
+#pragma unroll
+  for (int k = 0; k < KV; ++k) wk[k].load(w + (k * kWave + lane) * N);
+  float acc[KV][N];
+#pragma unroll
+  for (int k = 0; k < KV; ++k)
+#pragma unroll
+    for (int i = 0; i < N; ++i) acc[k][i] = 0.0f;
+  const int64_t r0 = int64_t(blockIdx.x) * kRmsRows;
+  for (int rr = wv; rr < kRmsRows; rr += 4) {
+    const int64_t row = r0 + rr;
+    if (row >= rows) break;  // uniform over the wave
+    Vec16<T> xv[KV], gv[KV];
+    float s2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+      xv[k].load(x + row * C + (k * kWave + lane) * N);
+      gv[k].load(dout + row * C + (k * kWave + lane) * N);
+#pragma unroll
+      for (int i = 0; i < N; ++i) s2 = fmaf(xv[k].v[i], xv[k].v[i], s2);
+    }
+    s2 = group_sum<kWave>(s2);
+    const float r = rsqrtf(s2 / float(C) + eps);
+    float sd = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KV; ++k)
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const float xn = rnd<T>(xv[k].v[i] * r);
+        acc[k][i] += rnd<T>(gv[k].v[i] * xn);
+        const float dxn = rnd<T>(gv[k].v[i] * wk[k].v[i]);
+        gv[k].v[i] = dxn;
+        sd = fmaf(dxn, xv[k].v[i], sd);
+      }
+    sd = group_sum<kWave>(sd);
+    const float c3 = r * r * r * sd / float(C);
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) gv[k].v[i] = gv[k].v[i] * r - xv[k].v[i] * c3;
+      gv[k].store(dx + row * C + (k * kWave + lane) * N);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < KV; ++k)
+#pragma unroll
+    for (int i = 0; i < N; ++i) red[wv][lane][k * N + i] = acc[k][i];
+  __syncthreads();
+  for (int e = int(threadIdx.x); e < C; e += 256) {
+    const int ln = (e / N) % kWave, k = e / (N * kWave), i = e % N;
+    const float v = ((red[0][ln][k * N + i] + red[1][ln][k * N + i]) + red[2][ln][k * N + i]) + red[3][ln][k * N + i];
+    wpart[int64_t(blockIdx.x) * C + e] = v;
+  }
+}
+
+// out[c] = sum over the partial rows of part (R, C), in a fixed order: 64
+// columns per block, the rows split over 4 thread rows.
+template <typename T>
+__global__ __launch_bounds__(256) void rms_col_sum_kernel(const float* __restrict__ part, int R, int C,
+                                                          typename T::raw* __restrict__ out) {
+  __shared__ float red[4][kWave];
+  const int tx = int(threadIdx.x) % kWave, ty = int(threadIdx.x) / kWave;
+  const int c = int(blockIdx.x) * kWave + tx;
+  float a = 0.0f;
+  if (c < C)
+    for (int r = ty; r < R; r += 4) a += part[int64_t(r) * C + c];
+  red[ty][tx] = a;
+  __syncthreads();
+  if (ty == 0 && c < C) T::store(out + c, ((red[0][tx] + red[1][tx]) + red[2][tx]) + red[3][tx]);
+}
+
 // ---------------------------------------------------------------------------
 // K/Q normalisation and q.k: LPR lanes per (token, head) row of D elements,
 // one 16-byte vector each (D = LPR * vector width).  K and Q rows are read
@@ -805,6 +894,46 @@ extern "C" int cdssm_normalize_kq_qk_fwd(int dtype, const void* K, int64_t k_tok
     else if (lpr == 8) go(std::integral_constant<int, 8>{});
     else if (lpr == 16) go(std::integral_constant<int, 16>{});
     else go(std::integral_constant<int, 32>{});
+    return cdssm_host::check_launch(op);
+  });
+}
+
+extern "C" int64_t cdssm_rms_norm_bwd_workspace_bytes(int64_t rows, int64_t C) {
+  if (rows <= 0 || C <= 0) return -1;
+  return (rows + kRmsRows - 1) / kRmsRows * C * int64_t(sizeof(float));
+}
+
+extern "C" int cdssm_rms_norm_bwd(int dtype, const void* x, const void* w, const void* dout, void* dx, void* dw,
+                                  float* workspace, int64_t rows, int64_t C, float eps, hipStream_t stream) {
+  const char* op = "cdssm_rms_norm_bwd";
+  return by_dtype(dtype, op, [&](auto t) -> int {
+    using T = decltype(t);
+    using raw = typename T::raw;
+    constexpr int N = Vec16<T>::N;
+    const int64_t kv = C / (int64_t(kWave) * N);
+    if (rows <= 0 || rows >= (int64_t(1) << 31) || C % (int64_t(kWave) * N) != 0 || kv < 1 || kv > 4) {
+      cdssm_host::set_error("%s: need C a multiple of %d up to %d (rows=%lld C=%lld)", op, kWave * N, 4 * kWave * N,
+                            (long long)rows, (long long)C);
+      return CDSSM_EINVAL;
+    }
+    if (!x || !w || !dout || !dx || !dw || !workspace || !aligned16(x) || !aligned16(w) || !aligned16(dout) ||
+        !aligned16(dx)) {
+      cdssm_host::set_error("%s: pointers must be non-null and 16-byte aligned", op);
+      return CDSSM_EINVAL;
+    }
+    const int nb = int((rows + kRmsRows - 1) / kRmsRows);
+    auto go = [&](auto kc) {
+      constexpr int KV = decltype(kc)::value;
+      hipLaunchKernelGGL((rms_norm_bwd_kernel<T, KV>), dim3(unsigned(nb)), dim3(256), 0, stream,
+                         static_cast<const raw*>(x), static_cast<const raw*>(w), static_cast<const raw*>(dout),
+                         static_cast<raw*>(dx), workspace, rows, eps);
+    };
+    if (kv == 1) go(std::integral_constant<int, 1>{});
+    else if (kv == 2) go(std::integral_constant<int, 2>{});
+    else if (kv == 3) go(std::integral_constant<int, 3>{});
+    else go(std::integral_constant<int, 4>{});
+    hipLaunchKernelGGL(rms_col_sum_kernel<T>, dim3(unsigned((C + kWave - 1) / kWave)), dim3(256), 0, stream,
+                       static_cast<const float*>(workspace), nb, int(C), static_cast<raw*>(dw));
     return cdssm_host::check_launch(op);
   });
 }

@@ -517,6 +517,21 @@ int cdssm_rms_norm_fwd(int dtype, const void* x, const void* weight, void* y, in
                        hipStream_t stream);
 
 /*
+ * Backward of cdssm_rms_norm_fwd, for training (modules.py:49-53 under
+ * autograd): given dout (rows, C) and the forward's x and weight (`dtype`),
+ * writes dx (rows, C) and dw (C), with the reference expression's rounding
+ * points (xn = (x r).to(dtype), out = xn w): dxn = dout w, dw = sum over rows
+ * of dout xn (fixed order), dx = dxn r - x r^3 (sum dxn x) / C in fp32,
+ * r = rsqrt(mean(x^2) + eps).  C a multiple of 64 16-byte vectors, at most 4
+ * per lane (bf16: 512 .. 2048; fp32: 256 .. 1024); 16-byte aligned.
+ * Workspace: cdssm_rms_norm_bwd_workspace_bytes (the per-block partial rows
+ * of dw).  Replaces the backward of torch's expression.
+ */
+int64_t cdssm_rms_norm_bwd_workspace_bytes(int64_t rows, int64_t C);
+int cdssm_rms_norm_bwd(int dtype, const void* x, const void* w, const void* dout, void* dx, void* dw, float* workspace,
+                       int64_t rows, int64_t C, float eps, hipStream_t stream);
+
+/*
  * Replaces the block's two NormalizeKQFn.forward calls (block.py:191-192 ->
  * normalize_kq.cu:75-79, x * rsqrt(sum x^2 + 1e-6) per (token, head)) and the
  * shortcut's q.k (block.py:202, einsum 'blhd,blhd->blh') in one pass.  K and Q

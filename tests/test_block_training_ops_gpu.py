@@ -10,6 +10,9 @@ for the output and every gradient (y, z, x_conv, gamma, beta, D).
 The K/Q normalisation with the current-token q.k (NormalizeKQQkFn: cdssm_normalize_kq_qk_fwd / _bwd) against
 fp64 autograd of NormalizeKQFn's rule (normalize_kq.cu:75-79) and q.k (block.py:191-192, 202), K a strided
 column slice as in the block: fp32 <= 1e-4, bf16 <= 2e-2.
+
+RMSNorm (RMSNormFn: cdssm_rms_norm_fwd / _bwd) against fp64 autograd of the reference expression
+(modules.py:49-53): fp32 <= 1e-4, bf16 <= 2e-2 for the output, dx and the weight's gradient.
 """
 
 import pytest
@@ -135,6 +138,37 @@ def test_normalize_kq_qk_forward_and_backward(name, dtype, D):
     errs = {"K^": rel(Ko, Kn), "Q^": rel(Qo, Qn), "qk": rel(qko, qk), "dK": rel(wg.grad, wr.grad),
             "dQ": rel(qg.grad, qr.grad)}
     log(f"[normalize kq qk] {name}: " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    bad = {n: e for n, e in errs.items() if not e <= tol}
+    assert not bad, f"beyond {tol}: {bad}"
+
+
+RMS_CASES = [("fp32_C1024", torch.float32, 1024), ("fp32_C512", torch.float32, 512),
+             ("bf16_C1024", torch.bfloat16, 1024), ("bf16_C2048", torch.bfloat16, 2048)]
+
+
+@pytest.mark.parametrize("name,dtype,C", RMS_CASES, ids=[c[0] for c in RMS_CASES])
+def test_rms_norm_forward_and_backward(name, dtype, C):
+    from cdssm_hip.lm import RMSNormFn
+    B, L, eps = 2, 301, 1e-5
+    g = torch.Generator().manual_seed(4)
+    x = (torch.randn(B, L, C, generator=g) * 2.0 + 0.5).to(dtype)
+    w = (1.0 + 0.3 * torch.randn(C, generator=g)).to(dtype)
+    dout = torch.randn(B, L, C, generator=g).to(dtype)
+    xr, wr = x.double().requires_grad_(True), w.double().requires_grad_(True)
+    yr = xr * torch.rsqrt(xr.pow(2).mean(-1, keepdim=True) + eps) * wr
+    yr.backward(dout.double())
+    assert RMSNormFn.usable(x.to(DEV))
+    grads = []
+    for _ in range(2):
+        xg, wg = x.to(DEV).requires_grad_(True), w.to(DEV).requires_grad_(True)
+        y = RMSNormFn.apply(xg, wg, eps)
+        y.backward(dout.to(DEV))
+        grads.append((xg.grad, wg.grad))
+    torch.cuda.synchronize()
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+    errs = {"y": rel(y, yr), "dx": rel(grads[0][0], xr.grad), "dw": rel(grads[0][1], wr.grad)}
+    log(f"[rms norm] {name}: " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
     tol = 1e-4 if dtype == torch.float32 else 2e-2
     bad = {n: e for n, e in errs.items() if not e <= tol}
     assert not bad, f"beyond {tol}: {bad}"
