@@ -40,6 +40,24 @@ __device__ __forceinline__ void rnd2(float& a, float& b) {
 // silu(u) = u sigmoid(u) with the hardware reciprocal (about 1 ulp)
 __device__ __forceinline__ float silu_fast(float u) { return u * __builtin_amdgcn_rcpf(1.0f + __expf(-u)); }
 
+// Column sum of a (R, W) fp32 matrix for a 256-thread block of 16 columns x
+// 16 thread rows (tx = threadIdx % 16 the column, ty the row group): every
+// thread adds rows ty, ty + 16, ...; the 16 row groups are joined in a fixed
+// order.  Returns the total to the ty == 0 threads.
+__device__ __forceinline__ float col_sum16(const float* __restrict__ part, int R, int W, int col) {
+  __shared__ float red[16][16];
+  const int tx = int(threadIdx.x) % 16, ty = int(threadIdx.x) / 16;
+  float a = 0.0f;
+  if (col < W)
+    for (int r = ty; r < R; r += 16) a += part[int64_t(r) * W + col];
+  red[ty][tx] = a;
+  __syncthreads();
+  float t = 0.0f;
+  if (ty == 0)
+    for (int u = 0; u < 16; ++u) t += red[u][tx];
+  return t;
+}
+
 // NV elements in registers: one 16-byte access (NV = 16 / element bytes, 8
 // bf16 or 4 fp32) or a single element (NV = 1).
 template <typename T, int NV = 16 / T::bytes>
@@ -186,20 +204,14 @@ __global__ __launch_bounds__(256) void rms_norm_bwd_kernel(const typename T::raw
   }
 }
 
-// out[c] = sum over the partial rows of part (R, C), in a fixed order: 64
-// columns per block, the rows split over 4 thread rows.
+// out[c] = sum over the partial rows of part (R, C), in a fixed order (16
+// columns per block).
 template <typename T>
 __global__ __launch_bounds__(256) void rms_col_sum_kernel(const float* __restrict__ part, int R, int C,
                                                           typename T::raw* __restrict__ out) {
-  __shared__ float red[4][kWave];
-  const int tx = int(threadIdx.x) % kWave, ty = int(threadIdx.x) / kWave;
-  const int c = int(blockIdx.x) * kWave + tx;
-  float a = 0.0f;
-  if (c < C)
-    for (int r = ty; r < R; r += 4) a += part[int64_t(r) * C + c];
-  red[ty][tx] = a;
-  __syncthreads();
-  if (ty == 0 && c < C) T::store(out + c, ((red[0][tx] + red[1][tx]) + red[2][tx]) + red[3][tx]);
+  const int c = int(blockIdx.x) * 16 + int(threadIdx.x) % 16;
+  const float v = col_sum16(part, R, C, c);
+  if (int(threadIdx.x) < 16 && c < C) T::store(out + c, v);
 }
 
 // ---------------------------------------------------------------------------
@@ -724,9 +736,8 @@ __global__ __launch_bounds__(256) void gnb_reduce_kernel(const typename T::raw* 
   }
 }
 
-// Blocks [0, ceil(C / 64)): 64 channels each, the partial rows split over 4
-// thread rows and joined in a fixed order; the blocks after: one (b, group)
-// per thread.
+// Blocks [0, ceil(3 C / 16)): column sums of the (BS, 3 C) partials (dgamma,
+// dbeta, dD side by side); the blocks after: one (b, group) per thread.
 template <typename T, typename P>
 __global__ __launch_bounds__(256) void gnb_finalize_kernel(const float* __restrict__ chan_part,
                                                            const float2* __restrict__ grp_part,
@@ -735,30 +746,18 @@ __global__ __launch_bounds__(256) void gnb_finalize_kernel(const float* __restri
                                                            typename T::raw* __restrict__ dD,
                                                            float2* __restrict__ gmeans, int BS, int C, int BG,
                                                            int S, float inv_n) {
-  __shared__ float red[4][kWave][3];
-  const int ncb = (C + kWave - 1) / kWave;
+  const int ncb = (3 * C + 15) / 16;
   if (int(blockIdx.x) < ncb) {
-    const int tx = int(threadIdx.x) % kWave, ty = int(threadIdx.x) / kWave;
-    const int c = int(blockIdx.x) * kWave + tx;
-    float a = 0.0f, bb = 0.0f, d = 0.0f;
-    if (c < C) {
-      for (int r = ty; r < BS; r += 4) {
-        a += chan_part[(int64_t(r) * 3 + 0) * C + c];
-        bb += chan_part[(int64_t(r) * 3 + 1) * C + c];
-        d += chan_part[(int64_t(r) * 3 + 2) * C + c];
-      }
-    }
-    red[ty][tx][0] = a;
-    red[ty][tx][1] = bb;
-    red[ty][tx][2] = d;
-    __syncthreads();
-    if (ty == 0 && c < C) {
-      float v[3];
-#pragma unroll
-      for (int k = 0; k < 3; ++k) v[k] = ((red[0][tx][k] + red[1][tx][k]) + red[2][tx][k]) + red[3][tx][k];
-      P::store(dgamma + c, v[0]);
-      P::store(dbeta + c, v[1]);
-      T::store(dD + c, v[2]);
+    const int col = int(blockIdx.x) * 16 + int(threadIdx.x) % 16;
+    const float v = col_sum16(chan_part, BS, 3 * C, col);
+    if (int(threadIdx.x) < 16 && col < 3 * C) {
+      const int k = col / C, c = col - k * C;
+      if (k == 0)
+        P::store(dgamma + c, v);
+      else if (k == 1)
+        P::store(dbeta + c, v);
+      else
+        T::store(dD + c, v);
     }
     return;
   }
@@ -932,7 +931,7 @@ extern "C" int cdssm_rms_norm_bwd(int dtype, const void* x, const void* w, const
     else if (kv == 2) go(std::integral_constant<int, 2>{});
     else if (kv == 3) go(std::integral_constant<int, 3>{});
     else go(std::integral_constant<int, 4>{});
-    hipLaunchKernelGGL(rms_col_sum_kernel<T>, dim3(unsigned((C + kWave - 1) / kWave)), dim3(256), 0, stream,
+    hipLaunchKernelGGL(rms_col_sum_kernel<T>, dim3(unsigned((C + 15) / 16)), dim3(256), 0, stream,
                        static_cast<const float*>(workspace), nb, int(C), static_cast<raw*>(dw));
     return cdssm_host::check_launch(op);
   });
@@ -1188,7 +1187,7 @@ extern "C" int cdssm_group_norm_gate_bwd(int dtype, int param_dtype, const void*
                          static_cast<const praw*>(beta), static_cast<const raw*>(z), z_token_stride,
                          static_cast<const raw*>(x_conv), static_cast<const raw*>(dout), chan, gpart, int(L), int(C),
                          int(G), S);
-      const unsigned fblocks = unsigned((C + kWave - 1) / kWave + (BG + 255) / 256);
+      const unsigned fblocks = unsigned((3 * C + 15) / 16 + (BG + 255) / 256);
       hipLaunchKernelGGL((gnb_finalize_kernel<T, P>), dim3(fblocks), dim3(256), 0, stream, chan,
                          gpart, static_cast<praw*>(dgamma), static_cast<praw*>(dbeta), static_cast<raw*>(dD), gm, BS,
                          int(C), BG, S, 1.0f / (float(L) * float(Cg)));
