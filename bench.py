@@ -662,20 +662,23 @@ def time_lm_forward(steps=5, warmup=2, state_dim=2):
 
 
 def time_lm_forward_state16(steps=3, warmup=1):
-    """time_lm_forward at the reference's default state_dim 16: the block's scan in the chunked MFMA form
-    (its default there) and, for comparison, through SSDChunkwiseScan's Y read out in torch."""
+    """time_lm_forward at the reference's default state_dim 16 with each route of the block's scan: the
+    chunked MFMA form (its default there), the sequential readout form over 8 state rows per head as
+    virtual heads, and SSDChunkwiseScan's Y read out in torch (the reference's op sequence)."""
     from cdssm_hip.lm import CDSSMBlock
-    prev = CDSSMBlock.chunked_scan
+    prev = CDSSMBlock.chunked_scan, CDSSMBlock.readout_scan
+    res = {}
     try:
-        CDSSMBlock.chunked_scan = True
-        chunked = time_lm_forward(steps, warmup, state_dim=16)
-        CDSSMBlock.chunked_scan = False
-        via_y = time_lm_forward(steps, warmup, state_dim=16)
+        for name, chunked, readout in (("chunked", True, True), ("rows", False, True), ("via_y", False, False)):
+            CDSSMBlock.chunked_scan, CDSSMBlock.readout_scan = chunked, readout
+            res[name] = time_lm_forward(steps, warmup, state_dim=16)
     finally:
-        CDSSMBlock.chunked_scan = prev
-    return {"workload": chunked["workload"], "chunked_ms_per_step": chunked["ms_per_step"],
-            "chunked_tokens_per_s": chunked["tokens_per_s"], "via_y_ms_per_step": via_y["ms_per_step"],
+        CDSSMBlock.chunked_scan, CDSSMBlock.readout_scan = prev
+    return {"workload": res["chunked"]["workload"], "chunked_ms_per_step": res["chunked"]["ms_per_step"],
+            "chunked_tokens_per_s": res["chunked"]["tokens_per_s"], "rows_ms_per_step": res["rows"]["ms_per_step"],
+            "via_y_ms_per_step": res["via_y"]["ms_per_step"],
             "note": "chunked: each block's scan, readout and shortcut in one cdssm_chunked_scan_fwd_abar call; "
+                    "rows: cdssm_fused_scan_fwd_abar with the 8 state rows of a head as virtual heads; "
                     "via_y: SSDChunkwiseScan's fused kernels write Y and torch reads it out"}
 
 

@@ -773,10 +773,12 @@ class CDSSMBlock(nn.Module):
         nn.init.normal_(self.out_proj.weight, std=std["out_proj"])
         nn.init.zeros_(self.D)
 
-    def forward(self, x: Tensor, v_first: Optional[Tensor] = None, cache: Optional[dict] = None):
+    def forward(self, x: Tensor, v_first: Optional[Tensor] = None, cache: Optional[dict] = None,
+                inplace_residual: bool = False):
         """x (B, L, d_model) -> (x + block(x), v_first).  With ``cache`` (a dict), also fills it with the
         state a decode step continues from: the conv window, the scan's decode state, the GroupNorm's
-        running sums and the position."""
+        running sums and the position.  ``inplace_residual`` (inference, a dense x the caller no longer
+        needs): the output is accumulated into x itself by the out_proj GEMM, with no copy of x."""
         cfg = self.config
         N, H, D, Di = cfg.state_dim, cfg.n_heads, cfg.head_dim, cfg.d_inner
         if N != 2 and cache is not None:
@@ -855,8 +857,11 @@ class CDSSMBlock(nn.Module):
                             self.ssm_norm.eps, z, x_conv, self.D, return_sums=cache is not None)
         if cache is not None:
             y, cache["gsum"] = y
-        # out_proj with the residual added in the GEMM epilogue
-        out = torch.addmm(residual.reshape(B * L, -1), y.reshape(B * L, Di), self.out_proj.weight.t())
+        # out_proj with the residual added in the GEMM epilogue (in place: no copy of the residual first)
+        if inplace_residual and residual.is_contiguous():
+            out = residual.view(B * L, -1).addmm_(y.reshape(B * L, Di), self.out_proj.weight.t())
+        else:
+            out = torch.addmm(residual.reshape(B * L, -1), y.reshape(B * L, Di), self.out_proj.weight.t())
         return out.reshape(residual.shape), v_first
 
     def _forward_autograd(self, x: Tensor, v_first: Optional[Tensor]):
@@ -1006,7 +1011,8 @@ class CDSSMLMHeadModel(nn.Module):
         x = self.embedding(input_ids)
         v_first = None
         for blk in self.blocks:
-            x, v_first = blk(x, v_first=v_first)
+            # the hidden state is this loop's own tensor: each block accumulates into it in place
+            x, v_first = blk(x, v_first=v_first, inplace_residual=True)
         return self.lm_head(self.final_norm(x))
 
     def prefill(self, input_ids: Tensor) -> tuple:
@@ -1018,7 +1024,7 @@ class CDSSMLMHeadModel(nn.Module):
         caches: List[dict] = []
         for blk in self.blocks:
             c: dict = {}
-            x, v_first = blk(x, v_first=v_first, cache=c)
+            x, v_first = blk(x, v_first=v_first, cache=c, inplace_residual=True)
             caches.append(c)
         return self.lm_head(self.final_norm(x[:, -1])), caches
 
