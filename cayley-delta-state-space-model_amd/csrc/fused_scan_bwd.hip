@@ -1730,37 +1730,46 @@ __global__ __launch_bounds__(256) void rows_sum_kernel(const float* __restrict__
                                                        typename T::raw* __restrict__ dq,
                                                        typename T::raw* __restrict__ dsel, int64_t n_rows,
                                                        int R, int P, int D) {
-  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;  // (token, head, 4 elements)
-  const int qd = D / 4;
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;  // (token, head, 8 elements)
+  const int qd = D / 8;
   if (i >= n_rows * qd) return;
   const int64_t row = i / qd;  // token * Hk + head
-  const int d0 = int(i - row * qd) * 4;
-  const auto sum4 = [&](const float* x, typename T::raw* o) {
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  const int d0 = int(i - row * qd) * 8;
+  const auto sum8 = [&](const float* x, typename T::raw* o) {
+    float a[8] = {};
     for (int j = 0; j < P; ++j) {
-      const float4 v = *reinterpret_cast<const float4*>(x + (row * P + j) * D + d0);
-      acc.x += v.x;
-      acc.y += v.y;
-      acc.z += v.z;
-      acc.w += v.w;
+      const float4* src = reinterpret_cast<const float4*>(x + (row * P + j) * D + d0);
+      const float4 v0 = src[0], v1 = src[1];
+      a[0] += v0.x;
+      a[1] += v0.y;
+      a[2] += v0.z;
+      a[3] += v0.w;
+      a[4] += v1.x;
+      a[5] += v1.y;
+      a[6] += v1.z;
+      a[7] += v1.w;
     }
-    o += row * D + d0;
-    T::store(o, acc.x);
-    T::store(o + 1, acc.y);
-    T::store(o + 2, acc.z);
-    T::store(o + 3, acc.w);
+    store_row<T, 8>(o + row * D + d0, a);
   };
-  sum4(dkp, dk);
-  if (dqp) sum4(dqp, dq);
+  sum8(dkp, dk);
+  if (dqp) sum8(dqp, dq);
   if (d0 == 0) {
-    float b = 0.0f;
-    for (int j = 0; j < R; ++j) b += dbp[row * R + j];
-    T::store(dbeta + row, b);
-    if (dsp) {
-      float g = 0.0f;
-      for (int j = 0; j < R; ++j) g += dsp[row * R + j];
-      T::store(dsel + row, g);
-    }
+    // the rows' partials of dbeta (and dsel) in order, four at a time where R allows
+    const auto sum_r = [&](const float* x) {
+      float b = 0.0f;
+      if (R % 4 == 0) {
+        const float4* src = reinterpret_cast<const float4*>(x + row * R);
+        for (int j = 0; j < R / 4; ++j) {
+          const float4 v = src[j];
+          b = (((b + v.x) + v.y) + v.z) + v.w;
+        }
+      } else {
+        for (int j = 0; j < R; ++j) b += x[row * R + j];
+      }
+      return b;
+    };
+    T::store(dbeta + row, sum_r(dbp));
+    if (dsp) T::store(dsel + row, sum_r(dsp));
   }
 }
 
@@ -1964,7 +1973,7 @@ int launch_fused_bwd(const void* q, const void* k, const void* v, const void* be
   if constexpr (GivenA<T>::value) {  // SSD and gate-level forms: no per-head dynamics parameters
     if (R > 1) {
       const int64_t n_rows = int64_t(B) * L * (H / R);
-      const int64_t threads = n_rows * (D / 4);
+      const int64_t threads = n_rows * (D / 8);
       hipLaunchKernelGGL(rows_sum_kernel<T>, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, stream,
                          (const float*)dkp, (const float*)dbp, (const float*)dqp, (const float*)dsp, (raw*)dk,
                          (raw*)dbeta, (raw*)dq, (raw*)dsel, n_rows, R, int(rows_partials_per_head(D, R)), D);
@@ -2086,6 +2095,12 @@ int fused_bwd_entry(int dtype, const void* q, const void* k, const void* v, cons
     if (reinterpret_cast<uintptr_t>(dt) % (dtype == 1 ? 4 : 8) != 0 ||
         reinterpret_cast<uintptr_t>(ddt) % (dtype == 1 ? 4 : 8) != 0) {
       cdssm_host::set_error("%s: A_bar and dA_bar must be aligned to their (re, im) pairs", op);
+      return CDSSM_EINVAL;
+    }
+    // q, k rows are read, and with state rows dq, dk written, as 16-byte vectors
+    const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (!a16(q) || !a16(k) || !a16(dq) || !a16(dk)) {
+      cdssm_host::set_error("%s: q, k, dq and dk must be 16-byte aligned", op);
       return CDSSM_EINVAL;
     }
     const int rr = int(R);
