@@ -87,6 +87,9 @@ SIGNATURES = {
     "cdssm_decode_init": (_I32, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "cdssm_decode_step": (_I32, [_I32] + [_P] * 9 + [_F32] + [_P] * 5 + [_I64] * 5 + [_P]),
     "cdssm_decode_step_abar": (_I32, [_I32] + [_P] * 12 + [_I64] * 5 + [_P]),
+    "cdssm_decode_block_tail": (_I32, [_I32, _I32, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _F32, _F32, _F32,
+                                        _F32, _F32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P,
+                                        _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _P]),
     "cdssm_decode_block_token": (_I32, [_I32, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P] + [_F32] * 5 +
                                  [_P] * 7 + [_I64] * 5 + [_P]),
     "cdssm_dynamics_fused_fwd_at": (_I32, [_I32, _P, _P, _P] + [_F32] * 5 + [_P] * 4 + [_I64] * 5 + [_P, _P]),

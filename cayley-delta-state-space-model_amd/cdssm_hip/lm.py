@@ -688,6 +688,9 @@ class CDSSMBlock(nn.Module):
     # decode steps take the one-launch token kernel (cdssm_decode_block_token) where its alignment holds;
     # False: the separate per-token kernels (the same values)
     fused_step: bool = True
+    # ... and, with it, the readout + GroupNorm + gate epilogue in the same launch (cdssm_decode_block_tail);
+    # False: the epilogue in a launch of its own
+    fused_tail: bool = True
     # training (and inference where the chunked form does not apply) takes the readout-form scan
     # (ChunkwiseDeltaScanAbarFn, no Y); False: SSDChunkwiseScan's Y read out in torch (the reference's op
     # sequence; the same gradients)
@@ -730,6 +733,18 @@ class CDSSMBlock(nn.Module):
         if hit is None or hit[0] != key:
             hit = (key, t.detach().float().contiguous())
             self._f32_cache[name] = hit
+        return hit[1]
+
+    def _param_as(self, name: str, t: Tensor, dtype: torch.dtype) -> Tensor:
+        """A contiguous copy of parameter ``t`` in ``dtype`` (``t`` itself where it already is one), kept while
+        the parameter's storage and version are unchanged, so a decode step launches no cast kernels."""
+        if t.dtype == dtype and t.is_contiguous():
+            return t.detach()
+        key = (t.data_ptr(), t._version, dtype, t.device)
+        hit = self._f32_cache.get(("as", name))
+        if hit is None or hit[0] != key:
+            hit = (key, t.detach().to(dtype).contiguous())
+            self._f32_cache[("as", name)] = hit
         return hit[1]
 
     def _stacked_gate_q(self) -> tuple:
@@ -806,7 +821,8 @@ class CDSSMBlock(nn.Module):
             if nk > 0:
                 win[:, Kc - nk:] = x_gate[:, L - nk:]
             cache["conv"] = win
-            cache["l"] = torch.full((1,), L, dtype=torch.int64, device=x.device)  # position of the next token
+            # the position of the next token, and an arrival count the fused decode tail uses to advance it
+            cache["l"] = torch.tensor([L, 0], dtype=torch.int64, device=x.device)
             # the step's parameter-derived constants, formed once (the weights are fixed while decoding)
             cache["lds"] = self.log_dt_scale.detach().float().contiguous()
             cache["rope"] = self.rope_freqs.detach().float().contiguous()
@@ -947,9 +963,38 @@ class CDSSMBlock(nn.Module):
         else:
             gq = torch.addmm(cache["b_gq"], x_conv, cache["w_gq"].t())
         es = x.element_size()
-        if (self.fused_step and D in (64, 128) and (gq.data_ptr() + GH * es) % 16 == 0 and (gq.stride(0) * es) % 16 == 0
-                and (proj.data_ptr() + 2 * Di * es) % 16 == 0 and (proj.stride(0) * es) % 16 == 0
-                and proj.stride(1) == 1 and gq.stride(1) == 1):
+        rows_ok = ((gq.data_ptr() + GH * es) % 16 == 0 and (gq.stride(0) * es) % 16 == 0
+                   and (proj.data_ptr() + 2 * Di * es) % 16 == 0 and (proj.stride(0) * es) % 16 == 0
+                   and proj.stride(1) == 1 and gq.stride(1) == 1)
+        if (self.fused_step and self.fused_tail and D in (64, 128) and rows_ok and cache["l"].numel() == 2
+                and x_conv.is_contiguous() and z.stride(1) == 1):
+            # the token step and the readout + GroupNorm + gate epilogue in one launch (cdssm_decode_block_tail)
+            st = cache["scan"]
+            v_used = torch.empty(B, H, N, dtype=x.dtype, device=x.device)
+            y = torch.empty(B, Di, dtype=x.dtype, device=x.device)
+            vf = None if v_first is None else v_first.contiguous()
+            gn = self.ssm_norm
+            pdt = gn.weight.dtype if gn.weight.dtype in _lib.DTYPE_CODE else torch.float32
+            gam_w = self._param_as("ssm_norm.weight", gn.weight, pdt)
+            bet_w = self._param_as("ssm_norm.bias", gn.bias, pdt)
+            Dp = self._param_as("D", self.D, x.dtype)
+            wr = self._param_as("readout_proj.weight", self.readout_proj.weight, x.dtype)
+            status = _lib.load().cdssm_decode_block_tail(
+                _lib.DTYPE_CODE[x.dtype], _lib.DTYPE_CODE[pdt], _lib.ptr(gq), gq.stride(0), _lib.ptr(proj),
+                proj.stride(0), 2 * Di, 3 * Di, _lib.ptr(vf), _lib.ptr(cache["vgate_h"]) if vf is not None else None,
+                _lib.ptr(cache["lds"]), _lib.ptr(cache["rope"]), float(cfg.gating_c), float(cfg.bf16_omega_thresh),
+                float(cfg.bf16_delta), float(cfg.bf16_smoothness), float(cfg.eps_adaptive_dt), _lib.ptr(cache["l"]),
+                _lib.ptr(cache["scale"]), _lib.ptr(st.state), _lib.ptr(st.gam), _lib.ptr(st.pos), _lib.ptr(v_used),
+                _lib.ptr(wr), _lib.ptr(cache["gsum"]), _lib.ptr(gam_w), _lib.ptr(bet_w), _lib.ptr(z), z.stride(0),
+                _lib.ptr(x_conv), _lib.ptr(Dp), _lib.ptr(y), B, H, D, N, st.chunk_size, Di, gn.num_groups,
+                float(gn.eps), _lib.stream_of(x.device))
+            _lib.check(status, "cdssm_decode_block_tail")
+            if v_first is None:
+                v_first = v_used
+            if _skinny_ok(y, self.out_proj.weight) and x.dtype == torch.bfloat16:
+                return skinny_linear(y, self.out_proj.weight, residual=x), v_first
+            return torch.addmm(x, y, self.out_proj.weight.t()), v_first
+        if self.fused_step and D in (64, 128) and rows_ok:
             # the token's dynamics, K/Q norm, value residual, scan step and shortcut in one launch
             st = cache["scan"]
             retrieved = torch.empty(B, H, N, dtype=x.dtype, device=x.device)

@@ -30,6 +30,7 @@
 // Work layout: one wave per (b, group of HPW heads), LPH lanes per head, each
 // lane DPL consecutive state elements (as the fused scan's main pass).
 #include "gate_math.hpp"
+#include "lm_common.hpp"
 
 namespace cdssm {
 
@@ -215,18 +216,18 @@ __device__ __forceinline__ float round_to(float x) {
     return x;
 }
 
+// The token step of one wave: batch row bi, heads hbase .. hbase + HPW - 1,
+// lane the lane in the wave.  The retrieved pair of each head goes to ret
+// (B, H, 2) or, with rs, to rs[2 h], rs[2 h + 1] (LDS; rounded as ret stores it).
 template <typename T, int D, int LPH>
-__global__ __launch_bounds__(kWave) void decode_token_kernel(
-    const typename T::raw* __restrict__ gq, const typename T::raw* __restrict__ proj,
+__device__ __forceinline__ void decode_token_wave(
+    int bi, int hbase, int lane, const typename T::raw* __restrict__ gq, const typename T::raw* __restrict__ proj,
     const typename T::raw* __restrict__ v_first, const typename T::raw* __restrict__ vgate,
     float* __restrict__ state, float2* __restrict__ gam, int* __restrict__ pos, typename T::raw* __restrict__ ret,
-    typename T::raw* __restrict__ v_out, DecodeTokenArgs a) {
-  constexpr int DPL = D / LPH, HPW = kWave / LPH, N = 2;
+    float* rs, typename T::raw* __restrict__ v_out, const DecodeTokenArgs& a) {
+  constexpr int DPL = D / LPH, N = 2;
   static_assert(DPL % 4 == 0, "state slices are whole float4s");
   const int H = a.H;
-  const int bi = int(blockIdx.x) / a.n_hg;
-  const int hbase = (int(blockIdx.x) % a.n_hg) * HPW;
-  const int lane = int(threadIdx.x);
   const int hh = lane / LPH, sub = lane % LPH;
   const int h = hbase + hh;
   const bool hok = h < H;
@@ -334,8 +335,13 @@ __global__ __launch_bounds__(kWave) void decode_token_kernel(
   if (sub == 0) {
     // the shortcut through the readout (shortcut_kernel's arithmetic)
     const float c = a.scale[0] * qkd * qkd * sc * tr.vp;
-    T::store(ret + 2 * bh, yr + c * v0);
-    T::store(ret + 2 * bh + 1, yi + c * v1);
+    if (rs) {
+      rs[2 * hl] = round_to<T>(yr + c * v0);
+      rs[2 * hl + 1] = round_to<T>(yi + c * v1);
+    } else {
+      T::store(ret + 2 * bh, yr + c * v0);
+      T::store(ret + 2 * bh + 1, yi + c * v1);
+    }
     T::store(v_out + 2 * bh, v0);
     T::store(v_out + 2 * bh + 1, v1);
   }
@@ -375,6 +381,69 @@ __global__ __launch_bounds__(kWave) void decode_token_kernel(
     gam[bh] = chunk_end ? make_float2(1.0f, 0.0f) : gn;
     pos[bh] = chunk_end ? 0 : jpos + 1;
   }
+}
+
+template <typename T, int D, int LPH>
+__global__ __launch_bounds__(kWave) void decode_token_kernel(
+    const typename T::raw* __restrict__ gq, const typename T::raw* __restrict__ proj,
+    const typename T::raw* __restrict__ v_first, const typename T::raw* __restrict__ vgate,
+    float* __restrict__ state, float2* __restrict__ gam, int* __restrict__ pos, typename T::raw* __restrict__ ret,
+    typename T::raw* __restrict__ v_out, DecodeTokenArgs a) {
+  constexpr int HPW = kWave / LPH;
+  decode_token_wave<T, D, LPH>(int(blockIdx.x) / a.n_hg, (int(blockIdx.x) % a.n_hg) * HPW, int(threadIdx.x), gq,
+                               proj, v_first, vgate, state, gam, pos, ret, nullptr, v_out, a);
+}
+
+// The block's decode tail in one launch (block.py:169-225 after the gate / Q
+// projection): one workgroup per batch row, a wave per group of HPW heads
+// running decode_token_wave into LDS, then the row's readout projection and
+// GroupNorm + gate step (lm::gn_row_step).  position[0] is the layer's decode
+// position and position[1] an arrival count: every workgroup arrives once it
+// has read the position, and the last to arrive advances it and clears the
+// count (so the next launch, and a replayed graph, find it zero).
+struct DecodeTailArgs {
+  const void* wr;  // readout_proj weight (C, 2 H)
+  float4* gsum;    // (B, G, 4) running GroupNorm sums
+  const void *gamma, *beta, *z, *xc, *Dp;
+  void* out;       // (B, C)
+  int64_t z_bs;
+  int C, G;
+  float eps;
+  unsigned long long* arrive;  // position + 1
+};
+
+template <typename T, int D, int LPH, typename P>
+__global__ __launch_bounds__(1024) void decode_tail_kernel(
+    const typename T::raw* __restrict__ gq, const typename T::raw* __restrict__ proj,
+    const typename T::raw* __restrict__ v_first, const typename T::raw* __restrict__ vgate,
+    float* __restrict__ state, float2* __restrict__ gam, int* __restrict__ pos, typename T::raw* __restrict__ v_out,
+    DecodeTokenArgs a, DecodeTailArgs t) {
+  using raw = typename T::raw;
+  constexpr int HPW = kWave / LPH;
+  extern __shared__ float tail_lds[];
+  const int kr = 2 * a.H;
+  float* rs = tail_lds;                                                  // the row's retrieved values (kr)
+  float2* gst = reinterpret_cast<float2*>(tail_lds + ((kr + 1) & ~1));  // (mean, rstd) per group
+  float* ys = reinterpret_cast<float*>(gst + t.G);                       // the row's y (C)
+  const int bi = int(blockIdx.x);
+  const int wv = int(threadIdx.x) / kWave;
+  // the first n_hg waves run the token step; the whole workgroup (at least 8 waves) the epilogue
+  if (wv < a.n_hg)
+    decode_token_wave<T, D, LPH>(bi, wv * HPW, int(threadIdx.x) % kWave, gq, proj, v_first, vgate, state, gam, pos,
+                                 nullptr, rs, v_out, a);
+  __syncthreads();  // every wave has read the position and written its heads' retrieved values
+  if (threadIdx.x == 0) {
+    const unsigned long long n = __hip_atomic_fetch_add(t.arrive, 1ull, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (n + 1 == gridDim.x) {
+      __hip_atomic_store(t.arrive, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      int64_t* position = const_cast<int64_t*>(a.l_dev);
+      position[0] += 1;
+    }
+  }
+  lm::gn_row_step<T, P>(bi, nullptr, rs, static_cast<const raw*>(t.wr), kr, t.gsum,
+                        static_cast<const typename P::raw*>(t.gamma), static_cast<const typename P::raw*>(t.beta),
+                        static_cast<const raw*>(t.z), t.z_bs, static_cast<const raw*>(t.xc),
+                        static_cast<const raw*>(t.Dp), static_cast<raw*>(t.out), t.C, t.G, t.eps, gst, ys);
 }
 
 // state = (0, h, h) per (b, h) (h = 0 if null), g = 1, j = 0: the decode state
@@ -563,6 +632,118 @@ extern "C" int cdssm_decode_block_token(int dtype, const void* gq, int64_t gq_st
       go(F32{}, I{}, std::integral_constant<int, 16>{});
     else
       go(F32{}, J{}, std::integral_constant<int, 32>{});
+  }
+  return cdssm_host::check_launch(op);
+}
+
+extern "C" int cdssm_decode_block_tail(int dtype, int param_dtype, const void* gq, int64_t gq_stride,
+                                       const void* proj, int64_t proj_stride, int64_t k_off, int64_t v_off,
+                                       const void* v_first, const void* vgate, const float* log_dt_scale,
+                                       const float* rope_freqs, float gating_c, float omega_thresh, float adt_delta,
+                                       float adt_smoothness, float adt_eps, int64_t* position,
+                                       const float* shortcut_scale, float* state, float* gam, int* pos, void* v_out,
+                                       const void* readout_weight, float* gsum, const void* gamma, const void* beta,
+                                       const void* z, int64_t z_batch_stride, const void* x_conv, const void* Dp,
+                                       void* out, int64_t B, int64_t H, int64_t D, int64_t N, int64_t chunk,
+                                       int64_t C, int64_t G, float eps, hipStream_t stream) {
+  const char* op = "cdssm_decode_block_tail";
+  if (dtype != 0 && dtype != 1) {
+    cdssm_host::set_error("%s: dtype must be 0 (fp32) or 1 (bf16), got %d", op, dtype);
+    return CDSSM_EINVAL;
+  }
+  if (param_dtype != 0 && param_dtype != 1) {
+    cdssm_host::set_error("%s: param_dtype must be 0 (fp32) or 1 (bf16), got %d", op, param_dtype);
+    return CDSSM_EINVAL;
+  }
+  if (B <= 0 || H <= 0 || B > 0x7fffffffLL || N != 2 || (D != 64 && D != 128) || chunk < 1 || chunk > 128 ||
+      gq_stride < 7 * H + H * D || k_off < 0 || v_off < 0 || proj_stride < k_off + H * D ||
+      proj_stride < v_off + 2 * H || proj_stride > (int64_t(1) << 40) || gq_stride > (int64_t(1) << 40)) {
+    cdssm_host::set_error("%s: need B, H > 0, N = 2, D in {64, 128}, 1 <= chunk <= 128 and the gate / Q and "
+                          "K / V columns inside their rows (B=%lld H=%lld D=%lld N=%lld chunk=%lld)",
+                          op, (long long)B, (long long)H, (long long)D, (long long)N, (long long)chunk);
+    return CDSSM_EINVAL;
+  }
+  const int64_t lph = D == 64 ? (dtype == 1 ? 8 : 16) : (dtype == 1 ? 16 : 32);
+  const int64_t waves = (H + kWave / lph - 1) / (kWave / lph);
+  if (waves > 16 || C <= 0 || G <= 0 || C % G != 0 || G > 8192 || C >= (int64_t(1) << 24) || z_batch_stride < C ||
+      ((2 * H + 1) / 2 * 2 + 2 * G + C) * int64_t(sizeof(float)) > 65536) {
+    cdssm_host::set_error("%s: need at most 16 head groups, C divisible by G <= 8192, a z row stride >= C and "
+                          "2 H + 2 G + C <= 16384 (H=%lld C=%lld G=%lld)", op, (long long)H, (long long)C,
+                          (long long)G);
+    return CDSSM_EINVAL;
+  }
+  if (!gq || !proj || (v_first && !vgate) || !log_dt_scale || !rope_freqs || !position || !shortcut_scale ||
+      !state || !gam || !pos || !v_out || !readout_weight || !gsum || !gamma || !beta || !z || !x_conv || !Dp ||
+      !out) {
+    cdssm_host::set_error("%s: null pointer argument", op);
+    return CDSSM_EINVAL;
+  }
+  if (!(adt_smoothness != 0.0f)) {
+    cdssm_host::set_error("%s: adt_smoothness must be nonzero", op);
+    return CDSSM_EINVAL;
+  }
+  const int64_t eb = dtype == 1 ? 2 : 4;
+  const int64_t qcol = 7 * H;  // Q's first column in gq
+  if ((reinterpret_cast<uintptr_t>(gq) + qcol * eb) % 16 || (gq_stride * eb) % 16 ||
+      (reinterpret_cast<uintptr_t>(proj) + k_off * eb) % 16 || (proj_stride * eb) % 16 ||
+      reinterpret_cast<uintptr_t>(position) % 8) {
+    cdssm_host::set_error("%s: the Q and K rows must start 16-byte aligned", op);
+    return CDSSM_EINVAL;
+  }
+  DecodeTokenArgs a;
+  a.gq_stride = gq_stride;
+  a.proj_stride = proj_stride;
+  a.k_off = int(k_off);
+  a.v_off = int(v_off);
+  a.lds = log_dt_scale;
+  a.rope = rope_freqs;
+  a.kc = gates::GateConsts{gating_c, omega_thresh, adt_delta, adt_smoothness, adt_eps};
+  a.l_dev = position;
+  a.scale = shortcut_scale;
+  a.H = int(H);
+  a.Q = int(chunk);
+  DecodeTailArgs t;
+  t.wr = readout_weight;
+  t.gsum = reinterpret_cast<float4*>(gsum);
+  t.gamma = gamma;
+  t.beta = beta;
+  t.z = z;
+  t.xc = x_conv;
+  t.Dp = Dp;
+  t.out = out;
+  t.z_bs = z_batch_stride;
+  t.C = int(C);
+  t.G = int(G);
+  t.eps = eps;
+  t.arrive = reinterpret_cast<unsigned long long*>(position + 1);
+  const size_t lds = size_t((2 * H + 1) / 2 * 2 + 2 * G + C) * sizeof(float);
+  auto go = [&](auto tt, auto pt, auto dc, auto lc) {
+    using T = decltype(tt);
+    using P = decltype(pt);
+    using raw = typename T::raw;
+    constexpr int DD = decltype(dc)::value, LP = decltype(lc)::value, HPW = kWave / LP;
+    a.n_hg = int((H + HPW - 1) / HPW);
+    const unsigned threads = unsigned(kWave * std::max(a.n_hg, 8));
+    hipLaunchKernelGGL((decode_tail_kernel<T, DD, LP, P>), dim3(unsigned(B)), dim3(threads), lds,
+                       stream, static_cast<const raw*>(gq), static_cast<const raw*>(proj),
+                       static_cast<const raw*>(v_first), static_cast<const raw*>(vgate), state,
+                       reinterpret_cast<float2*>(gam), pos, static_cast<raw*>(v_out), a, t);
+  };
+  using I = std::integral_constant<int, 64>;
+  using J = std::integral_constant<int, 128>;
+  using L8 = std::integral_constant<int, 8>;
+  using L16 = std::integral_constant<int, 16>;
+  using L32 = std::integral_constant<int, 32>;
+  if (dtype == 1) {
+    if (D == 64)
+      param_dtype == 1 ? go(BF16{}, BF16{}, I{}, L8{}) : go(BF16{}, F32{}, I{}, L8{});
+    else
+      param_dtype == 1 ? go(BF16{}, BF16{}, J{}, L16{}) : go(BF16{}, F32{}, J{}, L16{});
+  } else {
+    if (D == 64)
+      param_dtype == 1 ? go(F32{}, BF16{}, I{}, L16{}) : go(F32{}, F32{}, I{}, L16{});
+    else
+      param_dtype == 1 ? go(F32{}, BF16{}, J{}, L32{}) : go(F32{}, F32{}, J{}, L32{});
   }
   return cdssm_host::check_launch(op);
 }

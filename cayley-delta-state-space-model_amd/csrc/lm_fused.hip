@@ -13,32 +13,10 @@
 //                           + D x_conv                                        block.py:216-225
 // Roundings to the model dtype happen where the reference's torch ops round
 // (each op's output), so a bf16 model keeps the reference's rounding points.
-#include "common.hpp"
+#include "lm_common.hpp"
 
 namespace cdssm {
 namespace lm {
-
-// Round to the element type (identity for fp32).
-template <typename T>
-__device__ __forceinline__ float rnd(float x) {
-  if constexpr (T::bytes == 2)
-    return bf16_to_f32(f32_to_bf16(x));
-  else
-    return x;
-}
-
-// Round a pair to the element type with one packed conversion (identity for fp32).
-template <typename T>
-__device__ __forceinline__ void rnd2(float& a, float& b) {
-  if constexpr (T::bytes == 2) {
-    const uint32_t p = pack_bf16x2(a, b);
-    a = bf16_lo(p);
-    b = bf16_hi(p);
-  }
-}
-
-// silu(u) = u sigmoid(u) with the hardware reciprocal (about 1 ulp)
-__device__ __forceinline__ float silu_fast(float u) { return u * __builtin_amdgcn_rcpf(1.0f + __expf(-u)); }
 
 // Column sum of a (R, W) fp32 matrix for a 256-thread block of 16 columns x
 // 16 thread rows (tx = threadIdx % 16 the column, ty the row group): every
@@ -479,15 +457,8 @@ __global__ __launch_bounds__(256) void gn_gate_kernel(const typename T::raw* __r
   a.store(out + int64_t(tok) * C + c);  // the store rounds the sum
 }
 
-// ---------------------------------------------------------------------------
-// GroupNorm + gate for one decode token per batch row, with running
-// statistics: gsum (B, G, 4) fp32 = (shift K, sum (x - K), sum (x - K)^2,
-// count) over every position so far.  The new token's group sums are added in
-// a fixed order (one thread per group), the statistics formed from the
-// totals, and the token normalised, gated and skipped as gn_gate_kernel does.
-// With the prefix's sums this equals the GroupNorm of a forward over the
-// prefix plus the token, for that token.
-// ---------------------------------------------------------------------------
+// GroupNorm + gate for one decode token per batch row (gn_row_step): one
+// workgroup per row.
 template <typename T, typename P>
 __global__ __launch_bounds__(256) void gn_gate_step_kernel(const typename T::raw* __restrict__ y,
                                                            const typename T::raw* __restrict__ ret,
@@ -507,59 +478,12 @@ __global__ __launch_bounds__(256) void gn_gate_step_kernel(const typename T::raw
   // the layer's decode position advances with its last per-token kernel
   if (position && blockIdx.x == 0 && threadIdx.x == 0) position[0] += 1;
   const int b = blockIdx.x;
-  const int Cg = C / G;
-  const typename T::raw* yr = y + int64_t(b) * C;
   if (ret) {
-    // the readout projection of the row, rounded as the GEMM's output: y_c = rnd(sum_j ret_j W[c][j])
-    using raw = typename T::raw;
-    constexpr int E = 16 / int(sizeof(raw));  // elements per 16-byte load
-    const raw* rr = ret + int64_t(b) * kr;
+    const typename T::raw* rr = ret + int64_t(b) * kr;
     for (int j = threadIdx.x; j < kr; j += blockDim.x) rs[j] = T::load(rr + j);
     __syncthreads();
-    // W rows as 16-byte loads when every row starts on a 16-byte boundary
-    const bool vec = kr % E == 0 && (reinterpret_cast<uintptr_t>(wr) & 15u) == 0;
-    for (int c = threadIdx.x; c < C; c += blockDim.x) {
-      const raw* wc = wr + int64_t(c) * kr;
-      float a = 0.0f;
-      if (vec) {
-        for (int j = 0; j < kr; j += E) {
-          const uint4 v = *reinterpret_cast<const uint4*>(wc + j);
-          const raw* e = reinterpret_cast<const raw*>(&v);
-#pragma unroll
-          for (int u = 0; u < E; ++u) a = fmaf(rs[j + u], T::load(e + u), a);
-        }
-      } else {
-        for (int j = 0; j < kr; ++j) a = fmaf(rs[j], T::load(wc + j), a);
-      }
-      ys[c] = rnd<T>(a);
-    }
-    __syncthreads();
   }
-  auto yv = [&](int c) -> float { return ret ? ys[c] : T::load(yr + c); };
-  for (int g = threadIdx.x; g < G; g += blockDim.x) {
-    float4 a = gsum[int64_t(b) * G + g];
-    float s1 = 0.0f, s2 = 0.0f;
-    for (int c = 0; c < Cg; ++c) {
-      const float d = yv(g * Cg + c) - a.x;
-      s1 += d;
-      s2 = fmaf(d, d, s2);
-    }
-    a.y += s1;
-    a.z += s2;
-    a.w += float(Cg);
-    gsum[int64_t(b) * G + g] = a;
-    const float m = a.y / a.w;
-    gst[g] = make_float2(a.x + m, rsqrtf(fmaxf(a.z / a.w - m * m, 0.0f) + eps));
-  }
-  __syncthreads();
-  for (int c = threadIdx.x; c < C; c += blockDim.x) {
-    const float2 st = gst[c / Cg];
-    const float gn = rnd<T>(fmaf((yv(c) - st.x) * st.y, P::load(gamma + c), P::load(beta + c)));
-    const float s = rnd<T>(silu_fast(T::load(z + int64_t(b) * z_bs + c)));
-    const float p = rnd<T>(gn * s);
-    const float d = rnd<T>(T::load(Dp + c) * T::load(xc + int64_t(b) * C + c));
-    T::store(out + int64_t(b) * C + c, p + d);
-  }
+  gn_row_step<T, P>(b, y, ret ? rs : nullptr, wr, kr, gsum, gamma, beta, z, z_bs, xc, Dp, out, C, G, eps, gst, ys);
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

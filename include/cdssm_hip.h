@@ -745,6 +745,31 @@ int cdssm_decode_block_token(int dtype, const void* gq, int64_t gq_stride, const
                              void* v_out, int64_t B, int64_t H, int64_t D, int64_t N, int64_t chunk,
                              hipStream_t stream);
 
+/*
+ * cdssm_decode_block_token and the readout + GroupNorm + gate step after it
+ * (cdssm_readout_group_norm_gate_step) in one launch, for the model's decode
+ * step (block.py:169-225 between the gate / Q projection and out_proj): one
+ * workgroup per batch row whose waves run the token step of its heads into
+ * LDS, then the row's readout projection (readout_weight (C, 2 H)) and
+ * GroupNorm step with running sums gsum (B, G, 4), writing out (B, C).  The
+ * outputs equal the two separate calls'.  position points at two int64s: the
+ * layer's decode position and an arrival count, zero on entry (and left zero):
+ * every workgroup arrives after reading the position and the last advances it,
+ * as cdssm_readout_group_norm_gate_step does.  Arguments, shapes and limits as
+ * the two calls (v_out as cdssm_decode_block_token's); at most 16 head groups
+ * (H <= 128 in bf16 at D = 64), 2 H + 2 G + C <= 16384.  No reference
+ * counterpart: the reference re-forwards the sequence per token.
+ */
+int cdssm_decode_block_tail(int dtype, int param_dtype, const void* gq, int64_t gq_stride, const void* proj,
+                            int64_t proj_stride, int64_t k_off, int64_t v_off, const void* v_first, const void* vgate,
+                            const float* log_dt_scale, const float* rope_freqs, float gating_c, float omega_thresh,
+                            float adt_delta, float adt_smoothness, float adt_eps, int64_t* position,
+                            const float* shortcut_scale, float* state, float* gam, int* pos, void* v_out,
+                            const void* readout_weight, float* gsum, const void* gamma, const void* beta,
+                            const void* z, int64_t z_batch_stride, const void* x_conv, const void* D_skip, void* out,
+                            int64_t B, int64_t H, int64_t D, int64_t N, int64_t chunk, int64_t C, int64_t G,
+                            float eps, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -250,6 +250,38 @@ def test_fused_token_kernel_matches_separate_kernels(dtype):
         assert rel(ca[-1]["scan"].state, cb[-1]["scan"].state) <= (1e-5 if dtype == torch.float32 else 2e-2)
 
 
+@pytest.mark.parametrize("dtype,d_inner", [(torch.float32, 512), (torch.bfloat16, 1024)])
+def test_fused_tail_matches_token_kernel_and_separate_epilogue(dtype, d_inner):
+    """cdssm_decode_block_tail (token step + readout + GroupNorm step in one launch, one workgroup per batch
+    row) against cdssm_decode_block_token followed by cdssm_readout_group_norm_gate_step on the same caches:
+    the same arithmetic in the same order, so bit-identical logits, scan state, GroupNorm sums and position
+    (whose arrival count is back to zero after every step)."""
+    from cdssm_hip.lm import CDSSMBlock, _clone_cache
+    cfg, m = _cfg(dtype, n_layers=2, d_inner=d_inner)
+    B, L0, T = 5, 70, 3
+    log(f"[fused decode tail] {dtype} d_inner {d_inner} prompt {L0} steps {T}")
+    g = torch.Generator().manual_seed(19)
+    ids = torch.randint(0, cfg.vocab_size, (B, L0 + T), generator=g).to(DEV)
+    with torch.no_grad():
+        _, ca = m.prefill(ids[:, :L0])
+        cb = [_clone_cache(c) for c in ca]
+        try:
+            for t in range(L0, L0 + T):
+                CDSSMBlock.fused_tail = True
+                la = m.decode_step(ids[:, t], ca)
+                CDSSMBlock.fused_tail = False
+                lb = m.decode_step(ids[:, t], cb)
+                torch.cuda.synchronize()
+                log(f"   token {t}: fused tail vs separate {rel(la, lb):.2e}")
+                assert torch.equal(la, lb)
+        finally:
+            CDSSMBlock.fused_tail = True
+        for c1, c2 in zip(ca, cb):
+            assert torch.equal(c1["l"], c2["l"]) and int(c1["l"][1]) == 0 and int(c1["l"][0]) == L0 + T
+            assert torch.equal(c1["gsum"], c2["gsum"])
+            assert torch.equal(c1["scan"].state, c2["scan"].state)
+
+
 def test_config4_decode_24_layers_batch_64():
     """Config 4's decode: 24 layers, d_model 1024, 16 heads x 64, vocab 32000, bf16, B = 64 from a
     2048-token prefill.  Each step is finite; the graph-captured step equals the eager step on every
