@@ -684,13 +684,14 @@ def time_lm_forward_state16(steps=3, warmup=1):
                     "via_y: SSDChunkwiseScan's fused kernels write Y and torch reads it out"}
 
 
-def time_block_train(steps=5, warmup=2, B=8, L=2048):
+def time_block_train(steps=5, warmup=2, B=8, L=2048, state_dims=(2, 16), routes=("readout_scan", "ssd_y_readout")):
     """One training step through one CDSSMBlock at config 4's shape (d_model 1024, 16 heads x 64,
     d_inner 1024, bf16; B8 L2048): forward and backward of sum(out * g), the way the reference trains
     (block.py:140-229 under autograd, trainer.py:235-247; gradients cleared each step as
     zero_grad(set_to_none=True) does).  state_dim 2 and 16 (the reference's default), each with the
     readout-form scan (no (B,L,H,N,D) Y; at N = 16 the 8 complex state rows of a head run as virtual heads)
-    and with SSDChunkwiseScan's Y read out by the HIP readout (the reference's op sequence)."""
+    and with SSDChunkwiseScan's Y read out by the HIP readout (the reference's op sequence); ``state_dims`` and
+    ``routes`` select a subset (for a profile of one of them)."""
     import torch
     from cdssm_hip.lm import CDSSMBlock, CDSSMConfig
 
@@ -725,13 +726,15 @@ def time_block_train(steps=5, warmup=2, B=8, L=2048):
     res = {}
     prev = CDSSMBlock.readout_scan
     try:
-        for N in (2, 16):
+        for N in state_dims:
             torch.manual_seed(0)
             cfg = CDSSMConfig(d_model=1024, n_layers=24, context_length=2048, vocab_size=32000, state_dim=N,
                               d_inner=1024)
             blk = CDSSMBlock(cfg, 0).to(torch.bfloat16).to(dev).train()
             pre = "" if N == 2 else "state16_"
             for name, flag in (("readout_scan", True), ("ssd_y_readout", False)):
+                if name not in routes:
+                    continue
                 CDSSMBlock.readout_scan = flag
                 res[pre + name] = measure(blk)
             del blk
