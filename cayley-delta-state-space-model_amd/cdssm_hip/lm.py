@@ -321,6 +321,79 @@ def skinny_linear(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None, resi
     return y
 
 
+def _wgrad_slabs(T: int, O: int, I: int) -> int:
+    """Token slabs of a weight gradient dW = dY^T X over T tokens (O x I output).  One GEMM with an O x I
+    output of at most 1024 x 1024 and T = 16384 leaves most CUs idle (hipBLASLt: 64 x 64 tiles, no split
+    over the reduction; 0.1-0.3 PFLOP/s on MI355X); 8 slabs as one batched product with fp32 partials, summed
+    in fp32, ran 1.9-2.9x faster there (out_proj / Q_proj 111 -> 58 us, readout_proj 91 -> 33, gate_proj
+    98 -> 37 us, sum included).  Larger outputs (in_proj) keep the single product."""
+    return 8 if T >= 8192 and T % 8 == 0 and O * I <= (1 << 20) else 1
+
+
+def _weight_grad(gy: Tensor, x: Tensor) -> Tensor:
+    """dW = gy^T x for gy (T, O) and x (T, I), accumulated in fp32 (as one GEMM does), returned in fp32
+    when split over token slabs: a batched product of the slabs with fp32 outputs, then a fixed-order sum."""
+    T, O = gy.shape
+    I = x.shape[1]
+    S = _wgrad_slabs(T, O, I)
+    if S == 1:
+        return torch.mm(gy.t(), x)
+    a = gy.as_strided((S, T // S, O), (T // S * gy.stride(0), gy.stride(0), gy.stride(1))).transpose(1, 2)
+    b = x.as_strided((S, T // S, I), (T // S * x.stride(0), x.stride(0), x.stride(1)))
+    half = gy.dtype in (torch.bfloat16, torch.float16)
+    part = torch.bmm(a, b, out_dtype=torch.float32) if half else torch.bmm(a, b)
+    return part.sum(0)
+
+
+class TokenLinearFn(torch.autograd.Function):
+    """x @ weight^T (+ bias) (+ residual) over (..., in) token rows -- nn.Linear plus the block's residual
+    add (block.py:229) -- whose weight gradient is split over token slabs (``_weight_grad``).  The residual
+    enters the GEMM's epilogue (one rounding of the sum, as the inference forward's out_proj); its gradient
+    is the output's.  bias and residual are not both given."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, residual):
+        O = weight.shape[0]
+        x2 = x.reshape(-1, x.shape[-1])
+        if residual is not None:
+            y = torch.addmm(residual.reshape(-1, O), x2, weight.t())
+        elif bias is not None:
+            y = torch.addmm(bias, x2, weight.t())
+        else:
+            y = torch.mm(x2, weight.t())
+        ctx.save_for_backward(x2, weight)
+        ctx.xshape, ctx.has_bias = x.shape, bias is not None
+        return y.view(*x.shape[:-1], O)
+
+    @staticmethod
+    def backward(ctx, gy):
+        x2, w = ctx.saved_tensors
+        g2 = gy.reshape(-1, w.shape[0])
+        dx = dw = db = None
+        if ctx.needs_input_grad[0]:
+            dx = torch.mm(g2, w).view(ctx.xshape)
+        if ctx.needs_input_grad[1]:
+            dw = _weight_grad(g2, x2).to(w.dtype)
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            db = g2.sum(0)
+        return dx, dw, db, (gy if ctx.needs_input_grad[3] else None)
+
+
+def module_linear(lin: nn.Linear, x: Tensor, residual: Optional[Tensor] = None) -> Tensor:
+    """``lin(x)`` (+ ``residual``): the module and torch's add."""
+    y = lin(x)
+    return y if residual is None else residual + y
+
+
+def token_linear(lin: nn.Linear, x: Tensor, residual: Optional[Tensor] = None) -> Tensor:
+    """``lin(x)`` (+ ``residual``) through TokenLinearFn where it applies (a CUDA x of the weight's dtype, no
+    autocast; a residual only for a layer without bias), else ``module_linear``."""
+    if (x.is_cuda and x.dtype == lin.weight.dtype and not torch.is_autocast_enabled()
+            and (residual is None or (lin.bias is None and residual.dtype == x.dtype))):
+        return TokenLinearFn.apply(x, lin.weight, lin.bias, residual)
+    return module_linear(lin, x, residual)
+
+
 def _kq_rows(K: Tensor, Q: Tensor) -> tuple:
     """K, Q (B, L, H, D) as the fused normalisation reads them: in place where each token's (H, D) block is
     dense and 16-byte aligned with a uniform token stride, else dense copies; (K, Q, token strides)."""
@@ -701,6 +774,9 @@ class CDSSMBlock(nn.Module):
     # training runs the GroupNorm + gate epilogue on the HIP kernels with their backward (GroupNormGateFn);
     # False: torch's group_norm and elementwise ops (the reference's op sequence)
     fused_epilogue: bool = True
+    # training runs gate_proj, Q_proj, readout_proj and out_proj (with the residual add) through
+    # TokenLinearFn (weight gradients split over token slabs); False: nn.Linear and torch's add
+    token_linear: bool = True
 
     def __init__(self, config: CDSSMConfig, layer_idx: int = 0):
         super().__init__()
@@ -903,11 +979,12 @@ class CDSSMBlock(nn.Module):
         else:
             V = torch.lerp(v_first, V, torch.sigmoid(self.v_residual_gate)[None, None, :, None].to(V.dtype))
         x_conv = self.conv(x_gate)                                                    # block.py:177
-        gates = self.gate_proj(x_conv)
+        lin = token_linear if self.token_linear else module_linear
+        gates = lin(self.gate_proj, x_conv)
         A_bar, vp, beta, sel_C = DynamicsFusedFn.apply(
             gates, self.log_dt_scale.float(), self.rope_freqs, cfg.gating_c, cfg.bf16_omega_thresh,
             cfg.bf16_delta, cfg.bf16_smoothness, cfg.eps_adaptive_dt, H, N)           # block.py:184-188
-        Q = self.Q_proj(x_conv).reshape(B, L, H, D)
+        Q = lin(self.Q_proj, x_conv).reshape(B, L, H, D)
         if self.fused_epilogue and D // (16 // K.element_size()) in (4, 8, 16, 32) and D % (16 // K.element_size()) == 0:
             # block.py:191-192 and the q.k of :202 in one kernel each way
             K, Q, qk = NormalizeKQQkFn.apply(K, Q)
@@ -926,7 +1003,7 @@ class CDSSMBlock(nn.Module):
         else:
             Y = SSDChunkwiseScan(cfg.chunk_size, N)(A_bar, K, V_gated, beta)          # block.py:198
             retrieved = (StateReadoutFn.apply(Y, Q) + shortcut) * sel_C.unsqueeze(-1)     # block.py:208-211
-        y = self.readout_proj(retrieved.reshape(B, L, H * N))
+        y = lin(self.readout_proj, retrieved.reshape(B, L, H * N))
         G, gn = self.ssm_norm.num_groups, self.ssm_norm
         if self.fused_epilogue and GroupNormGateFn.usable(y, z, x_conv, G, (gn.weight, gn.bias, self.D)):
             # block.py:216-225 on the HIP kernels, forward and backward
@@ -935,7 +1012,7 @@ class CDSSMBlock(nn.Module):
             y = torch.nn.functional.group_norm(y.float().transpose(1, 2), G, gn.weight.float(), gn.bias.float(),
                                                gn.eps).to(y.dtype).transpose(1, 2)  # block.py:216-223
             y = y * torch.nn.functional.silu(z) + self.D * x_conv
-        return residual + self.out_proj(y.to(self.out_proj.weight.dtype)), v_first
+        return lin(self.out_proj, y.to(self.out_proj.weight.dtype), residual=residual), v_first
 
     def step(self, x: Tensor, v_first: Optional[Tensor], cache: dict):
         """One decode token: x (B, d_model) at position cache["l"] -> (x + block(x), v_first (B, H, N)),

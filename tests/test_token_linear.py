@@ -1,0 +1,86 @@
+"""TokenLinearFn: the block's training projections (nn.Linear, block.py:65-81, with out_proj's residual add,
+block.py:229) with the weight gradient dW = dY^T X split over token slabs, each slab's product in fp32 and the
+slabs summed in a fixed order.
+
+CPU (fp64): output, dx, dW, db and the residual's gradient against autograd through F.linear + add, at a
+token count that takes the split (T = 16384, small outputs) and one that does not; the split must equal the
+single product to fp64 rounding.  GPU: bf16 and fp32 at the block's shapes (T = B L = 16384; out_proj 1024 x
+1024, readout_proj 1024 x 256, gate_proj 336 x 1024 with bias) against fp64 autograd on the same rounded
+inputs: fp32 <= 1e-5, bf16 <= 1e-2 normwise (the bf16 rounding of each output), and bit-identical repeats.
+"""
+
+import pytest
+import torch
+
+from _gpu_util import DEV, log, rel
+
+
+def run_fn(x, w, b, r, g):
+    from cdssm_hip.lm import TokenLinearFn
+    x, w = x.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    b = b.clone().requires_grad_(True) if b is not None else None
+    r = r.clone().requires_grad_(True) if r is not None else None
+    y = TokenLinearFn.apply(x, w, b, r)
+    y.backward(g)
+    return y, x.grad, w.grad, (b.grad if b is not None else None), (r.grad if r is not None else None)
+
+
+def run_ref(x, w, b, r, g):
+    x, w = x.double().requires_grad_(True), w.double().requires_grad_(True)
+    b = b.double().requires_grad_(True) if b is not None else None
+    r = r.double().requires_grad_(True) if r is not None else None
+    y = torch.nn.functional.linear(x, w, b)
+    if r is not None:
+        y = y + r
+    y.backward(g.double())
+    return y, x.grad, w.grad, (b.grad if b is not None else None), (r.grad if r is not None else None)
+
+
+def draw(B, L, O, I, bias, residual, dtype, device, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    t = lambda *s: torch.randn(*s, generator=gen).to(dtype).to(device)  # noqa: E731
+    return (t(B, L, I), 0.05 * t(O, I), t(O) if bias else None, t(B, L, O) if residual else None, t(B, L, O))
+
+
+@pytest.mark.parametrize("B,L,O,I,bias,residual", [(8, 2048, 64, 32, True, False), (8, 2048, 48, 40, False, True),
+                                                    (2, 75, 7, 5, True, False)])
+def test_token_linear_matches_linear_fp64_cpu(B, L, O, I, bias, residual):
+    from cdssm_hip.lm import _wgrad_slabs
+    x, w, b, r, g = draw(B, L, O, I, bias, residual, torch.float64, "cpu")
+    got, want = run_fn(x, w, b, r, g), run_ref(x, w, b, r, g)
+    log(f"[token linear cpu] T{B * L} {O}x{I}: slabs {_wgrad_slabs(B * L, O, I)}")
+    for n, a, e in zip(("y", "dx", "dW", "db", "dres"), got, want):
+        assert (a is None) == (e is None), n
+        if a is not None:
+            assert rel(a, e) <= 1e-12, n
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,O,I,bias,residual,dtype", [
+    ("out_proj_bf16", 1024, 1024, False, True, torch.bfloat16),
+    ("readout_proj_bf16", 1024, 256, False, False, torch.bfloat16),
+    ("gate_proj_bf16", 336, 1024, True, False, torch.bfloat16),
+    ("out_proj_fp32", 1024, 1024, False, True, torch.float32),
+])
+def test_token_linear_gpu_matches_fp64(name, O, I, bias, residual, dtype):
+    from cdssm_hip.lm import _wgrad_slabs
+    B, L = 8, 2048
+    assert _wgrad_slabs(B * L, O, I) == 8
+    log(f"[token linear gpu] {name}: T{B * L} {O}x{I}")
+    x, w, b, r, g = draw(B, L, O, I, bias, residual, dtype, DEV, seed=1)
+    got = run_fn(x, w, b, r, g)
+    again = run_fn(x, w, b, r, g)
+    torch.cuda.synchronize()
+    want = run_ref(*[t.cpu() if t is not None else None for t in (x, w, b, r, g)])
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    errs = {}
+    for n, a, a2, e in zip(("y", "dx", "dW", "db", "dres"), got, again, want):
+        assert (a is None) == (e is None), n
+        if a is None:
+            continue
+        assert a.dtype == dtype, n
+        assert torch.equal(a, a2), n
+        errs[n] = rel(a, e)
+    log("   " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
+    bad = {n: e for n, e in errs.items() if not e <= tol}
+    assert not bad, f"beyond {tol}: {bad}"
