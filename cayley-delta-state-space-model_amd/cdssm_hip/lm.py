@@ -39,7 +39,8 @@ import torch.nn as nn
 from . import _lib
 from .ops import DynamicsFusedFn, NormalizeKQFn
 from .decode import DecodeState, decode_step_abar, prefill_abar
-from .scan import ChunkwiseDeltaScanAbarFn, chunked_scan_abar, chunkwise_delta_scan_abar
+from .scan import (ChunkwiseDeltaScanAbarFn, _abar_validate, chunked_scan_abar, chunkwise_delta_scan_abar,
+                   chunkwise_delta_scan_abar_bwd, chunkwise_delta_scan_abar_fwd)
 from .ssd import SSDChunkwiseScan
 
 Tensor = torch.Tensor
@@ -516,6 +517,71 @@ def shortcut_readout_(retrieved: Tensor, qk: Tensor, V: Tensor, vp: Tensor, sel_
     return retrieved
 
 
+def shortcut_readout_rows_(y: Tensor, qk: Tensor, V: Tensor, vp: Tensor, sel_C: Tensor, scale: Tensor) -> Tensor:
+    """In place: y += sel_C * scale * qk^2 * vp.repeat_interleave(2, -1) * V, in fp32 with one rounding
+    (block.py:194-211's shortcut through the readout, N/2 complex state rows per head;
+    cdssm_shortcut_readout_rows_fwd).  y, V (B, L, H, N) dense; vp (B, L, H, N/2); sel_C (B, L, H); qk fp32."""
+    dt = _check_gpu("shortcut_readout_rows", y, V, vp, sel_C)
+    B, L, H, N = y.shape
+    if tuple(V.shape) != (B, L, H, N) or tuple(vp.shape) != (B, L, H, N // 2) or tuple(sel_C.shape) != (B, L, H):
+        raise ValueError("y, V (B, L, H, N), vp (B, L, H, N/2), sel_C (B, L, H)")
+    if not y.is_contiguous():
+        raise ValueError("y must be contiguous")
+    qk32 = qk.to(torch.float32).contiguous()
+    sc = scale.detach().reshape(1).to(device=y.device, dtype=torch.float32).contiguous()
+    Vc, vpc, sc_ = V.contiguous(), vp.contiguous(), sel_C.contiguous()
+    st = _lib.load().cdssm_shortcut_readout_rows_fwd(_lib.DTYPE_CODE[dt], _lib.ptr(y), _lib.ptr(qk32), _lib.ptr(Vc),
+                                                     _lib.ptr(vpc), _lib.ptr(sc_), _lib.ptr(sc), B * L * H, N,
+                                                     _lib.stream_of(y.device))
+    _lib.check(st, "cdssm_shortcut_readout_rows_fwd")
+    return y
+
+
+class ScanShortcutFn(torch.autograd.Function):
+    """The block's retrieved vector for training, one autograd node: the readout-form scan
+    (ChunkwiseDeltaScanAbarFn's kernels: sel_C (Y.q) of SSDChunkwiseScan(A_bar, K, V vp, beta), never forming
+    Y) plus the current-token shortcut sel_C scale (q.k)^2 V vp (block.py:194-211), any even state_dim up to
+    32.  (q, k, v, beta, sel_C, A_bar, vp, qk, scale, chunk_size) -> retrieved (B,L,H,N); qk (B,L,H) fp32, scale
+    the one-element shortcut_scale.  The shortcut is added in fp32 with one rounding
+    (cdssm_shortcut_readout_rows_fwd); its backward adds its gradients to the scan's in place and returns
+    dL/d(q.k) in fp32 and dL/dscale from fixed-order partial sums (cdssm_shortcut_readout_rows_bwd)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, beta, sel_C, A_bar, vp, qk, scale, chunk_size):
+        B, L, H, D, N, Q, dtype = _abar_validate(q, k, v, beta, sel_C, A_bar, vp, None, chunk_size)
+        if qk.shape != (B, L, H):
+            raise ValueError(f"qk must be ({B}, {L}, {H}), got {tuple(qk.shape)}")
+        ins = [t.contiguous() for t in (q, k, v, beta, sel_C, A_bar, vp)]
+        qk32 = qk.detach().to(torch.float32).contiguous()
+        sc = scale.detach().reshape(1).to(device=q.device, dtype=torch.float32).contiguous()
+        y, _, ws = chunkwise_delta_scan_abar_fwd(*ins, None, Q, train=True)
+        st = _lib.load().cdssm_shortcut_readout_rows_fwd(_lib.DTYPE_CODE[dtype], _lib.ptr(y), _lib.ptr(qk32),
+                                                         _lib.ptr(ins[2]), _lib.ptr(ins[6]), _lib.ptr(ins[4]),
+                                                         _lib.ptr(sc), B * L * H, N, _lib.stream_of(q.device))
+        _lib.check(st, "cdssm_shortcut_readout_rows_fwd")
+        ctx.save_for_backward(*ins, qk32, sc, ws)
+        ctx.Q, ctx.qk_dtype, ctx.scale_dtype, ctx.scale_shape = Q, qk.dtype, scale.dtype, scale.shape
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        *ins, qk32, sc, ws = ctx.saved_tensors
+        dy = dy.to(ins[0].dtype).contiguous()
+        dq, dk, dv, dbeta, dsel, dA, dvp, _ = chunkwise_delta_scan_abar_bwd(dy, None, *ins, ws, False, ctx.Q)
+        B, L, H, N = dv.shape
+        lib = _lib.load()
+        n = B * L * H
+        dqk = torch.empty(B, L, H, dtype=torch.float32, device=dy.device)
+        part = torch.empty(lib.cdssm_shortcut_readout_rows_partials(n), dtype=torch.float32, device=dy.device)
+        st = lib.cdssm_shortcut_readout_rows_bwd(_lib.DTYPE_CODE[dy.dtype], _lib.ptr(dy), _lib.ptr(qk32),
+                                                 _lib.ptr(ins[2]), _lib.ptr(ins[6]), _lib.ptr(ins[4]), _lib.ptr(sc),
+                                                 _lib.ptr(dv), _lib.ptr(dvp), _lib.ptr(dsel), _lib.ptr(dqk),
+                                                 _lib.ptr(part), n, N, _lib.stream_of(dy.device))
+        _lib.check(st, "cdssm_shortcut_readout_rows_bwd")
+        dscale = part.sum().reshape(ctx.scale_shape).to(ctx.scale_dtype)
+        return dq, dk, dv, dbeta, dsel, dA, dvp, dqk.to(ctx.qk_dtype), dscale, None
+
+
 def group_norm_gate(y: Tensor, num_groups: int, gamma: Tensor, beta: Tensor, eps: float, z: Tensor,
                     x_conv: Tensor, D: Tensor, return_sums: bool = False):
     """GroupNorm over (channels of a group, all L) in fp32, cast to y's dtype, * silu(z) + D * x_conv
@@ -774,6 +840,9 @@ class CDSSMBlock(nn.Module):
     # training runs the GroupNorm + gate epilogue on the HIP kernels with their backward (GroupNormGateFn);
     # False: torch's group_norm and elementwise ops (the reference's op sequence)
     fused_epilogue: bool = True
+    # training with the readout-form scan adds the current-token shortcut in the scan's autograd node
+    # (ScanShortcutFn, HIP forward and backward); False: torch's elementwise ops for the shortcut
+    fused_shortcut: bool = True
     # training runs gate_proj, Q_proj, readout_proj and out_proj (with the residual add) through
     # TokenLinearFn (weight gradients split over token slabs); False: nn.Linear and torch's add
     token_linear: bool = True
@@ -924,10 +993,8 @@ class CDSSMBlock(nn.Module):
             # N/2 complex state rows per head: the fused scan with its readout, each row a virtual head
             # sharing k, q, beta and sel_C (block.py:194-211 with ssd.py:39-111), without forming Y; the
             # shortcut s (q.k)^2 V_gated (block.py:202-205) through the readout in fp32
-            ret, _ = chunkwise_delta_scan_abar(Q, K, V, beta, sel_C, A_bar, vp, chunk_size=cfg.chunk_size)
-            V_gated = V.float() * vp.float().repeat_interleave(2, dim=-1)
-            ret = ret.float() + (self._fp32("shortcut_scale") * (qk * qk) * sel_C.float()).unsqueeze(-1) * V_gated
-            retrieved = ret.to(x.dtype)
+            retrieved, _ = chunkwise_delta_scan_abar(Q, K, V, beta, sel_C, A_bar, vp, chunk_size=cfg.chunk_size)
+            shortcut_readout_rows_(retrieved, qk, V, vp, sel_C, self._fp32("shortcut_scale"))
         elif N != 2:
             # N/2 complex pairs per head (the reference default is 16): Y from SSDChunkwiseScan (its
             # fused kernels, each pair a virtual head sharing k; block.py:194-211 with ssd.py:39-111);
@@ -987,22 +1054,28 @@ class CDSSMBlock(nn.Module):
         Q = lin(self.Q_proj, x_conv).reshape(B, L, H, D)
         if self.fused_epilogue and D // (16 // K.element_size()) in (4, 8, 16, 32) and D % (16 // K.element_size()) == 0:
             # block.py:191-192 and the q.k of :202 in one kernel each way
-            K, Q, qk = NormalizeKQQkFn.apply(K, Q)
-            qk = qk.to(V.dtype)
+            K, Q, qk = NormalizeKQQkFn.apply(K, Q)                                    # qk in fp32
         else:
             K, Q = NormalizeKQFn.apply(K, Q)                                          # block.py:191-192
             qk = (Q * K).sum(-1)                                                      # block.py:202
-        V_gated = V * vp.repeat_interleave(2, dim=-1)                                 # block.py:194-195
-        shortcut = self.shortcut_scale * (qk * qk).unsqueeze(-1) * V_gated            # block.py:204-208
-        if self.readout_scan and D in (64, 128) and 1 <= cfg.chunk_size <= 128:
+        readout = self.readout_scan and D in (64, 128) and 1 <= cfg.chunk_size <= 128
+        if readout and self.fused_shortcut:
             # the fused scan with its readout, sel_C (Y.q) (block.py:198, 208-211), without forming the
-            # (B,L,H,N,D) Y: its backward rebuilds chunk states from the forward's records (N > 2: the
-            # head's N/2 complex state rows run as virtual heads sharing k, q, beta and sel_C)
-            y_scan, _ = ChunkwiseDeltaScanAbarFn.apply(Q, K, V, beta, sel_C, A_bar, vp, None, cfg.chunk_size)
-            retrieved = y_scan + shortcut * sel_C.unsqueeze(-1)
+            # (B,L,H,N,D) Y (its backward rebuilds chunk states from the forward's records; N > 2: the
+            # head's N/2 complex state rows run as virtual heads sharing k, q, beta and sel_C), and the
+            # current-token shortcut sel_C s (q.k)^2 V vp (block.py:194-195, 202-205) in the same node
+            retrieved = ScanShortcutFn.apply(Q, K, V, beta, sel_C, A_bar, vp, qk, self.shortcut_scale,
+                                             cfg.chunk_size)
         else:
-            Y = SSDChunkwiseScan(cfg.chunk_size, N)(A_bar, K, V_gated, beta)          # block.py:198
-            retrieved = (StateReadoutFn.apply(Y, Q) + shortcut) * sel_C.unsqueeze(-1)     # block.py:208-211
+            qk = qk.to(V.dtype)
+            V_gated = V * vp.repeat_interleave(2, dim=-1)                             # block.py:194-195
+            shortcut = self.shortcut_scale * (qk * qk).unsqueeze(-1) * V_gated        # block.py:204-208
+            if readout:
+                y_scan, _ = ChunkwiseDeltaScanAbarFn.apply(Q, K, V, beta, sel_C, A_bar, vp, None, cfg.chunk_size)
+                retrieved = y_scan + shortcut * sel_C.unsqueeze(-1)
+            else:
+                Y = SSDChunkwiseScan(cfg.chunk_size, N)(A_bar, K, V_gated, beta)      # block.py:198
+                retrieved = (StateReadoutFn.apply(Y, Q) + shortcut) * sel_C.unsqueeze(-1)  # block.py:208-211
         y = lin(self.readout_proj, retrieved.reshape(B, L, H * N))
         G, gn = self.ssm_norm.num_groups, self.ssm_norm
         if self.fused_epilogue and GroupNormGateFn.usable(y, z, x_conv, G, (gn.weight, gn.bias, self.D)):

@@ -316,6 +316,74 @@ __global__ __launch_bounds__(256) void shortcut_kernel(typename T::raw* __restri
 }
 
 // ---------------------------------------------------------------------------
+// The same shortcut over R = N/2 complex state rows per (token, head), with its
+// backward (the training step).  Per row i, c = scale (q.k)^2 sel_C:
+//   forward   y[j] += c vp[j/2] V[j]                       (j < N, one rounding)
+//   backward  (g = dL/dy; dV, dvp, dsel_C hold the scan's gradients and take
+//             the shortcut's added in fp32, one rounding each)
+//             dV[j] += c vp[j/2] g[j]
+//             dvp[p] += c (g[2p] V[2p] + g[2p+1] V[2p+1])
+//             u = sum_j g[j] vp[j/2] V[j];  dsel_C += scale (q.k)^2 u
+//             dqk = 2 scale (q.k) sel_C u  (fp32, written)
+//             dscale: each workgroup's sum of (q.k)^2 sel_C u over its rows, in a
+//             fixed tree order, to part[blockIdx.x] (the caller adds the partials).
+// ---------------------------------------------------------------------------
+constexpr int kShortcutThreads = 256;
+
+template <typename T>
+__global__ __launch_bounds__(kShortcutThreads) void shortcut_rows_fwd_kernel(
+    typename T::raw* __restrict__ y, const float* __restrict__ qk, const typename T::raw* __restrict__ v,
+    const typename T::raw* __restrict__ vp, const typename T::raw* __restrict__ sel,
+    const float* __restrict__ scale, int64_t n, int R) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float x = qk[i];
+  const float c = scale[0] * x * x * T::load(sel + i);
+  const int64_t o = i * 2 * R;
+  for (int p = 0; p < R; ++p) {
+    const float w = c * T::load(vp + i * R + p);
+    T::store(y + o + 2 * p, T::load(y + o + 2 * p) + w * T::load(v + o + 2 * p));
+    T::store(y + o + 2 * p + 1, T::load(y + o + 2 * p + 1) + w * T::load(v + o + 2 * p + 1));
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kShortcutThreads) void shortcut_rows_bwd_kernel(
+    const typename T::raw* __restrict__ g, const float* __restrict__ qk, const typename T::raw* __restrict__ v,
+    const typename T::raw* __restrict__ vp, const typename T::raw* __restrict__ sel,
+    const float* __restrict__ scale, typename T::raw* __restrict__ dv, typename T::raw* __restrict__ dvp,
+    typename T::raw* __restrict__ dsel, float* __restrict__ dqk, float* __restrict__ part, int64_t n, int R) {
+  __shared__ float red[kShortcutThreads];
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  float mine = 0.f;
+  if (i < n) {
+    const float x = qk[i], sc = scale[0], s = T::load(sel + i);
+    const float c = sc * x * x * s;
+    const int64_t o = i * 2 * R;
+    float u = 0.f;
+    for (int p = 0; p < R; ++p) {
+      const float a = T::load(vp + i * R + p);
+      const float g0 = T::load(g + o + 2 * p), g1 = T::load(g + o + 2 * p + 1);
+      const float gv = g0 * T::load(v + o + 2 * p) + g1 * T::load(v + o + 2 * p + 1);
+      T::store(dv + o + 2 * p, T::load(dv + o + 2 * p) + c * a * g0);
+      T::store(dv + o + 2 * p + 1, T::load(dv + o + 2 * p + 1) + c * a * g1);
+      T::store(dvp + i * R + p, T::load(dvp + i * R + p) + c * gv);
+      u += a * gv;
+    }
+    T::store(dsel + i, T::load(dsel + i) + sc * x * x * u);
+    dqk[i] = 2.f * sc * x * s * u;
+    mine = x * x * s * u;
+  }
+  red[threadIdx.x] = mine;
+  __syncthreads();
+  for (int w = kShortcutThreads / 2; w > 0; w >>= 1) {
+    if (int(threadIdx.x) < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) part[blockIdx.x] = red[0];
+}
+
+// ---------------------------------------------------------------------------
 // GroupNorm statistics over (L positions x Cg channels) per (b, g), Cg = C/G.
 // Sums of (x - K) and (x - K)^2 with a shift K = y[b, 0, g Cg] (the first
 // element of the group), which keeps the variance free of cancellation when
@@ -918,6 +986,61 @@ extern "C" int cdssm_shortcut_readout_fwd(int dtype, void* retrieved, const floa
     hipLaunchKernelGGL(shortcut_kernel<T>, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream,
                        static_cast<raw*>(retrieved), qk, static_cast<const raw*>(V), static_cast<const raw*>(vp),
                        static_cast<const raw*>(sel_c), scale, n);
+    return cdssm_host::check_launch(op);
+  });
+}
+
+namespace {
+int shortcut_rows_check(const char* op, int64_t n, int64_t N) {
+  if (n <= 0 || N <= 0 || N % 2 != 0 || N > 64 || n * N > (int64_t(1) << 38)) {
+    cdssm_host::set_error("%s: need n > 0 and an even N <= 64 (n=%lld N=%lld)", op, (long long)n, (long long)N);
+    return CDSSM_EINVAL;
+  }
+  return CDSSM_OK;
+}
+}  // namespace
+
+extern "C" int64_t cdssm_shortcut_readout_rows_partials(int64_t n) {
+  return n > 0 ? (n + kShortcutThreads - 1) / kShortcutThreads : -1;
+}
+
+extern "C" int cdssm_shortcut_readout_rows_fwd(int dtype, void* y, const float* qk, const void* V, const void* vp,
+                                               const void* sel_c, const float* scale, int64_t n, int64_t N,
+                                               hipStream_t stream) {
+  const char* op = "cdssm_shortcut_readout_rows_fwd";
+  return by_dtype(dtype, op, [&](auto t) -> int {
+    using T = decltype(t);
+    using raw = typename T::raw;
+    if (shortcut_rows_check(op, n, N) != CDSSM_OK) return CDSSM_EINVAL;
+    if (!y || !qk || !V || !vp || !sel_c || !scale) {
+      cdssm_host::set_error("%s: null pointer argument", op);
+      return CDSSM_EINVAL;
+    }
+    hipLaunchKernelGGL(shortcut_rows_fwd_kernel<T>, dim3(unsigned((n + kShortcutThreads - 1) / kShortcutThreads)),
+                       dim3(kShortcutThreads), 0, stream, static_cast<raw*>(y), qk, static_cast<const raw*>(V),
+                       static_cast<const raw*>(vp), static_cast<const raw*>(sel_c), scale, n, int(N / 2));
+    return cdssm_host::check_launch(op);
+  });
+}
+
+extern "C" int cdssm_shortcut_readout_rows_bwd(int dtype, const void* dy, const float* qk, const void* V,
+                                               const void* vp, const void* sel_c, const float* scale, void* dV,
+                                               void* dvp, void* dsel_c, float* dqk, float* dscale_partials,
+                                               int64_t n, int64_t N, hipStream_t stream) {
+  const char* op = "cdssm_shortcut_readout_rows_bwd";
+  return by_dtype(dtype, op, [&](auto t) -> int {
+    using T = decltype(t);
+    using raw = typename T::raw;
+    if (shortcut_rows_check(op, n, N) != CDSSM_OK) return CDSSM_EINVAL;
+    if (!dy || !qk || !V || !vp || !sel_c || !scale || !dV || !dvp || !dsel_c || !dqk || !dscale_partials) {
+      cdssm_host::set_error("%s: null pointer argument", op);
+      return CDSSM_EINVAL;
+    }
+    hipLaunchKernelGGL(shortcut_rows_bwd_kernel<T>, dim3(unsigned((n + kShortcutThreads - 1) / kShortcutThreads)),
+                       dim3(kShortcutThreads), 0, stream, static_cast<const raw*>(dy), qk,
+                       static_cast<const raw*>(V), static_cast<const raw*>(vp), static_cast<const raw*>(sel_c), scale,
+                       static_cast<raw*>(dV), static_cast<raw*>(dvp), static_cast<raw*>(dsel_c), dqk,
+                       dscale_partials, n, int(N / 2));
     return cdssm_host::check_launch(op);
   });
 }

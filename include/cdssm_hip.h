@@ -581,6 +581,27 @@ int cdssm_state_readout_bwd(int dtype, const void* Y, const void* q, const void*
 int cdssm_shortcut_readout_fwd(int dtype, void* retrieved, const float* qk, const void* V, const void* vp,
                                const void* sel_c, const float* scale, int64_t n, hipStream_t stream);
 
+/*
+ * The same shortcut with N/2 complex state rows per (token, head) (block.py:194-211 at any even
+ * state_dim N <= 64, the rows sharing q.k and sel_C), forward and backward, for the training step:
+ *   forward, in place:  y[i, j] += scale (q.k)_i^2 sel_C[i] vp[i, j/2] V[i, j],  one rounding;
+ *   backward (dy = dL/dy): adds the shortcut's gradients to the scan's, in place, in fp32 with one
+ *   rounding each -- dV[i, j] += c_i vp[i, j/2] dy[i, j], dvp[i, p] += c_i (dy V)[i, 2p] + c_i (dy V)[i, 2p+1],
+ *   dsel_c[i] += scale (q.k)_i^2 u_i with c_i = scale (q.k)_i^2 sel_C[i] and u_i = sum_j dy vp V;
+ *   writes dqk[i] = 2 scale (q.k)_i sel_C[i] u_i (fp32) and, per workgroup, the partial sum of
+ *   (q.k)^2 sel_C u over its rows to dscale_partials (cdssm_shortcut_readout_rows_partials(n) floats; their
+ *   sum, in any fixed order, is dL/dscale).
+ * y, dy, V, dV (n, N); vp, dvp (n, N/2); sel_c, dsel_c (n) in `dtype`, dense; qk, dqk (n) fp32; scale one
+ * fp32 on the device.  n = B*L*H.  The reference forms V_gated = V vp, scale (q.k)^2 V_gated and
+ * (Y.q + shortcut) sel_C with torch ops (block.py:194-211) and autograd's rules for them; no launcher.
+ */
+int64_t cdssm_shortcut_readout_rows_partials(int64_t n);
+int cdssm_shortcut_readout_rows_fwd(int dtype, void* y, const float* qk, const void* V, const void* vp,
+                                    const void* sel_c, const float* scale, int64_t n, int64_t N, hipStream_t stream);
+int cdssm_shortcut_readout_rows_bwd(int dtype, const void* dy, const float* qk, const void* V, const void* vp,
+                                    const void* sel_c, const float* scale, void* dV, void* dvp, void* dsel_c,
+                                    float* dqk, float* dscale_partials, int64_t n, int64_t N, hipStream_t stream);
+
 /* Bytes of the fp32 workspace cdssm_group_norm_gate_fwd needs (-1 if invalid).  No reference counterpart:
  * torch's group_norm allocates its statistics (block.py:216-223); this library never allocates. */
 int64_t cdssm_group_norm_workspace_bytes(int64_t B, int64_t G, int64_t L);

@@ -172,3 +172,57 @@ def test_abar_rows_rejects_odd_state_dim():
     g["A_bar"] = torch.randn(1, 64, 2, 5, device=DEV)
     with pytest.raises(ValueError):
         chunkwise_delta_scan_abar(*[g[n] for n in NAMES])
+
+
+SHORTCUT_CASES = [
+    ("fp32_N2", 2, 256, 4, 64, 2, torch.float32),
+    ("fp32_N16", 2, 200, 3, 64, 16, torch.float32),
+    ("bf16_N16", 2, 640, 4, 64, 16, torch.bfloat16),
+    ("bf16_N6_D128", 1, 300, 2, 128, 6, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("name,B,L,H,D,N,dtype", SHORTCUT_CASES, ids=[c[0] for c in SHORTCUT_CASES])
+def test_scan_shortcut_node_matches_scan_plus_torch_shortcut(name, B, L, H, D, N, dtype):
+    """ScanShortcutFn (the block's training node: the readout-form scan plus sel_C s (q.k)^2 V vp,
+    cdssm_shortcut_readout_rows_fwd / _bwd) against ChunkwiseDeltaScanAbarFn with the shortcut in fp64
+    torch on the same inputs (block.py:194-211): output and the gradients of q, k, v, beta, sel_C, A_bar, vp,
+    q.k and the scale.  The scan's kernels are the same in both, so fp32 agrees to 1e-5; bf16 to 1e-2 (the
+    rounding of each output).  A repeat is bit-identical (fixed-order partial sums for the scale)."""
+    from cdssm_hip import ChunkwiseDeltaScanAbarFn
+    from cdssm_hip.lm import ScanShortcutFn
+    log(f"[scan shortcut] {name}: B{B} L{L} H{H} D{D} N{N} {dtype}")
+    x = draw(B, L, H, D, N, dtype, seed=5)
+    gen = torch.Generator().manual_seed(11)
+    qk = (0.5 + 0.5 * torch.rand(B, L, H, generator=gen)).to(DEV)
+    scale = torch.tensor([0.3], device=DEV)
+    gy = torch.randn(B, L, H, N, generator=gen).to(dtype).to(DEV)
+
+    def fused():
+        ins = [x[n].to(DEV).clone().requires_grad_(True) for n in NAMES]
+        q2, s2 = qk.clone().requires_grad_(True), scale.clone().requires_grad_(True)
+        y = ScanShortcutFn.apply(*ins, q2, s2, None)
+        y.backward(gy)
+        return [y] + [t.grad for t in ins] + [q2.grad, s2.grad]
+
+    got, again = fused(), fused()
+    ins = [x[n].to(DEV).clone().requires_grad_(True) for n in NAMES]
+    y_scan, _ = ChunkwiseDeltaScanAbarFn.apply(*ins, None, None)
+    ys = y_scan.detach().double().requires_grad_(True)
+    q2, s2 = qk.double().requires_grad_(True), scale.double().requires_grad_(True)
+    v64, vp64, sel64 = (ins[i].detach().double().requires_grad_(True) for i in (2, 6, 4))
+    ref = ys + (s2 * q2 * q2 * sel64).unsqueeze(-1) * v64 * vp64.repeat_interleave(2, dim=-1)
+    ref.backward(gy.double())
+    y_scan.backward(ys.grad.to(dtype))
+    torch.cuda.synchronize()
+    want = [ref, ins[0].grad, ins[1].grad, ins[2].grad.double() + v64.grad, ins[3].grad,
+            ins[4].grad.double() + sel64.grad, ins[5].grad, ins[6].grad.double() + vp64.grad, q2.grad, s2.grad]
+    names = ("y",) + tuple("d" + n for n in NAMES) + ("dqk", "dscale")
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    errs = {}
+    for n, a, a2, e in zip(names, got, again, want):
+        assert torch.equal(a, a2), n
+        errs[n] = rel(a, e)
+    log("   " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
+    bad = {n: e for n, e in errs.items() if not e <= tol}
+    assert not bad, f"beyond {tol}: {bad}"
