@@ -73,7 +73,7 @@ SIGNATURES = {
     "cdssm_rms_norm_fwd": (_I32, [_I32, _P, _P, _P, _I64, _I64, _F32, _P]),
     "cdssm_normalize_kq_qk_fwd": (_I32, [_I32, _P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _P]),
     "cdssm_shortcut_readout_fwd": (_I32, [_I32] + [_P] * 6 + [_I64, _P]),
-    "cdssm_shortcut_readout_rows_partials": (_I64, [_I64]),
+    "cdssm_shortcut_readout_rows_partials": (_I64, [_I64, _I64]),
     "cdssm_shortcut_readout_rows_fwd": (_I32, [_I32] + [_P] * 6 + [_I64, _I64, _P]),
     "cdssm_shortcut_readout_rows_bwd": (_I32, [_I32] + [_P] * 11 + [_I64, _I64, _P]),
     "cdssm_state_readout_fwd": (_I32, [_I32] + [_P] * 3 + [_I64] * 3 + [_P]),

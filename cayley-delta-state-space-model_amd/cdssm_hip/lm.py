@@ -572,7 +572,7 @@ class ScanShortcutFn(torch.autograd.Function):
         lib = _lib.load()
         n = B * L * H
         dqk = torch.empty(B, L, H, dtype=torch.float32, device=dy.device)
-        part = torch.empty(lib.cdssm_shortcut_readout_rows_partials(n), dtype=torch.float32, device=dy.device)
+        part = torch.empty(lib.cdssm_shortcut_readout_rows_partials(n, N), dtype=torch.float32, device=dy.device)
         st = lib.cdssm_shortcut_readout_rows_bwd(_lib.DTYPE_CODE[dy.dtype], _lib.ptr(dy), _lib.ptr(qk32),
                                                  _lib.ptr(ins[2]), _lib.ptr(ins[6]), _lib.ptr(ins[4]), _lib.ptr(sc),
                                                  _lib.ptr(dv), _lib.ptr(dvp), _lib.ptr(dsel), _lib.ptr(dqk),

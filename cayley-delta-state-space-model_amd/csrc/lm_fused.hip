@@ -327,8 +327,66 @@ __global__ __launch_bounds__(256) void shortcut_kernel(typename T::raw* __restri
 //             dqk = 2 scale (q.k) sel_C u  (fp32, written)
 //             dscale: each workgroup's sum of (q.k)^2 sel_C u over its rows, in a
 //             fixed tree order, to part[blockIdx.x] (the caller adds the partials).
+// Where R is a power of two (N = 2, 4, 8, 16, 32, 64) a lane takes one complex
+// pair (consecutive lanes read consecutive pairs) and a row's R lanes, which
+// sit in one wave, add u with a fixed butterfly; otherwise a thread takes a row.
 // ---------------------------------------------------------------------------
 constexpr int kShortcutThreads = 256;
+
+template <typename T>
+__global__ __launch_bounds__(kShortcutThreads) void shortcut_pairs_fwd_kernel(
+    typename T::raw* __restrict__ y, const float* __restrict__ qk, const typename T::raw* __restrict__ v,
+    const typename T::raw* __restrict__ vp, const typename T::raw* __restrict__ sel,
+    const float* __restrict__ scale, int64_t n_pairs, int log2R) {
+  const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j >= n_pairs) return;
+  const int64_t i = j >> log2R;
+  const float x = qk[i];
+  const float w = scale[0] * x * x * T::load(sel + i) * T::load(vp + j);
+  store_pair<T>(y + 2 * j, T::load(y + 2 * j) + w * T::load(v + 2 * j),
+                T::load(y + 2 * j + 1) + w * T::load(v + 2 * j + 1));
+}
+
+template <typename T>
+__global__ __launch_bounds__(kShortcutThreads) void shortcut_pairs_bwd_kernel(
+    const typename T::raw* __restrict__ g, const float* __restrict__ qk, const typename T::raw* __restrict__ v,
+    const typename T::raw* __restrict__ vp, const typename T::raw* __restrict__ sel,
+    const float* __restrict__ scale, typename T::raw* __restrict__ dv, typename T::raw* __restrict__ dvp,
+    typename T::raw* __restrict__ dsel, float* __restrict__ dqk, float* __restrict__ part, int64_t n_pairs,
+    int log2R) {
+  __shared__ float red[kShortcutThreads];
+  const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const bool live = j < n_pairs;
+  const int64_t i = j >> log2R;
+  float x = 0.f, s = 0.f, t = 0.f;
+  const float sc = scale[0];
+  if (live) {
+    x = qk[i];
+    s = T::load(sel + i);
+    const float c = sc * x * x * s;
+    const float a = T::load(vp + j);
+    const float g0 = T::load(g + 2 * j), g1 = T::load(g + 2 * j + 1);
+    const float gv = g0 * T::load(v + 2 * j) + g1 * T::load(v + 2 * j + 1);
+    store_pair<T>(dv + 2 * j, T::load(dv + 2 * j) + c * a * g0, T::load(dv + 2 * j + 1) + c * a * g1);
+    T::store(dvp + j, T::load(dvp + j) + c * gv);
+    t = a * gv;
+  }
+  // u over the row's R consecutive lanes (a row never straddles a wave: 64 % R == 0)
+  for (int m = 1; m < (1 << log2R); m <<= 1) t += __shfl_xor(t, m, kWave);
+  float mine = 0.f;
+  if (live && (j & ((int64_t(1) << log2R) - 1)) == 0) {
+    T::store(dsel + i, T::load(dsel + i) + sc * x * x * t);
+    dqk[i] = 2.f * sc * x * s * t;
+    mine = x * x * s * t;
+  }
+  red[threadIdx.x] = mine;
+  __syncthreads();
+  for (int w = kShortcutThreads / 2; w > 0; w >>= 1) {
+    if (int(threadIdx.x) < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) part[blockIdx.x] = red[0];
+}
 
 template <typename T>
 __global__ __launch_bounds__(kShortcutThreads) void shortcut_rows_fwd_kernel(
@@ -998,10 +1056,25 @@ int shortcut_rows_check(const char* op, int64_t n, int64_t N) {
   }
   return CDSSM_OK;
 }
+
+// log2(N/2) where N/2 is a power of two (the lane-per-pair kernels), else -1
+int shortcut_log2_rows(int64_t N) {
+  const int64_t R = N / 2;
+  return (R & (R - 1)) == 0 ? __builtin_ctzll(uint64_t(R)) : -1;
+}
+
+// workgroups of a launch: one lane per pair, or per row
+int64_t shortcut_groups(int64_t n, int64_t N) {
+  const int64_t units = shortcut_log2_rows(N) >= 0 ? n * (N / 2) : n;
+  return (units + kShortcutThreads - 1) / kShortcutThreads;
+}
+
+// the pair stores need each (re, im) pair aligned to its size
+bool pair_aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % (2 * bytes)) == 0; }
 }  // namespace
 
-extern "C" int64_t cdssm_shortcut_readout_rows_partials(int64_t n) {
-  return n > 0 ? (n + kShortcutThreads - 1) / kShortcutThreads : -1;
+extern "C" int64_t cdssm_shortcut_readout_rows_partials(int64_t n, int64_t N) {
+  return n > 0 && N > 0 && N % 2 == 0 ? shortcut_groups(n, N) : -1;
 }
 
 extern "C" int cdssm_shortcut_readout_rows_fwd(int dtype, void* y, const float* qk, const void* V, const void* vp,
@@ -1016,9 +1089,19 @@ extern "C" int cdssm_shortcut_readout_rows_fwd(int dtype, void* y, const float* 
       cdssm_host::set_error("%s: null pointer argument", op);
       return CDSSM_EINVAL;
     }
-    hipLaunchKernelGGL(shortcut_rows_fwd_kernel<T>, dim3(unsigned((n + kShortcutThreads - 1) / kShortcutThreads)),
-                       dim3(kShortcutThreads), 0, stream, static_cast<raw*>(y), qk, static_cast<const raw*>(V),
-                       static_cast<const raw*>(vp), static_cast<const raw*>(sel_c), scale, n, int(N / 2));
+    if (!pair_aligned(y, T::bytes)) {
+      cdssm_host::set_error("%s: y must be aligned to a (re, im) pair (%d bytes)", op, 2 * T::bytes);
+      return CDSSM_EINVAL;
+    }
+    const int lr = shortcut_log2_rows(N);
+    if (lr >= 0)
+      hipLaunchKernelGGL(shortcut_pairs_fwd_kernel<T>, dim3(unsigned(shortcut_groups(n, N))), dim3(kShortcutThreads),
+                         0, stream, static_cast<raw*>(y), qk, static_cast<const raw*>(V), static_cast<const raw*>(vp),
+                         static_cast<const raw*>(sel_c), scale, n * (N / 2), lr);
+    else
+      hipLaunchKernelGGL(shortcut_rows_fwd_kernel<T>, dim3(unsigned(shortcut_groups(n, N))), dim3(kShortcutThreads),
+                         0, stream, static_cast<raw*>(y), qk, static_cast<const raw*>(V), static_cast<const raw*>(vp),
+                         static_cast<const raw*>(sel_c), scale, n, int(N / 2));
     return cdssm_host::check_launch(op);
   });
 }
@@ -1036,11 +1119,21 @@ extern "C" int cdssm_shortcut_readout_rows_bwd(int dtype, const void* dy, const 
       cdssm_host::set_error("%s: null pointer argument", op);
       return CDSSM_EINVAL;
     }
-    hipLaunchKernelGGL(shortcut_rows_bwd_kernel<T>, dim3(unsigned((n + kShortcutThreads - 1) / kShortcutThreads)),
-                       dim3(kShortcutThreads), 0, stream, static_cast<const raw*>(dy), qk,
-                       static_cast<const raw*>(V), static_cast<const raw*>(vp), static_cast<const raw*>(sel_c), scale,
-                       static_cast<raw*>(dV), static_cast<raw*>(dvp), static_cast<raw*>(dsel_c), dqk,
-                       dscale_partials, n, int(N / 2));
+    if (!pair_aligned(dV, T::bytes)) {
+      cdssm_host::set_error("%s: dV must be aligned to a (re, im) pair (%d bytes)", op, 2 * T::bytes);
+      return CDSSM_EINVAL;
+    }
+    const int lr = shortcut_log2_rows(N);
+    if (lr >= 0)
+      hipLaunchKernelGGL(shortcut_pairs_bwd_kernel<T>, dim3(unsigned(shortcut_groups(n, N))), dim3(kShortcutThreads),
+                         0, stream, static_cast<const raw*>(dy), qk, static_cast<const raw*>(V),
+                         static_cast<const raw*>(vp), static_cast<const raw*>(sel_c), scale, static_cast<raw*>(dV),
+                         static_cast<raw*>(dvp), static_cast<raw*>(dsel_c), dqk, dscale_partials, n * (N / 2), lr);
+    else
+      hipLaunchKernelGGL(shortcut_rows_bwd_kernel<T>, dim3(unsigned(shortcut_groups(n, N))), dim3(kShortcutThreads),
+                         0, stream, static_cast<const raw*>(dy), qk, static_cast<const raw*>(V),
+                         static_cast<const raw*>(vp), static_cast<const raw*>(sel_c), scale, static_cast<raw*>(dV),
+                         static_cast<raw*>(dvp), static_cast<raw*>(dsel_c), dqk, dscale_partials, n, int(N / 2));
     return cdssm_host::check_launch(op);
   });
 }

@@ -589,13 +589,13 @@ int cdssm_shortcut_readout_fwd(int dtype, void* retrieved, const float* qk, cons
  *   rounding each -- dV[i, j] += c_i vp[i, j/2] dy[i, j], dvp[i, p] += c_i (dy V)[i, 2p] + c_i (dy V)[i, 2p+1],
  *   dsel_c[i] += scale (q.k)_i^2 u_i with c_i = scale (q.k)_i^2 sel_C[i] and u_i = sum_j dy vp V;
  *   writes dqk[i] = 2 scale (q.k)_i sel_C[i] u_i (fp32) and, per workgroup, the partial sum of
- *   (q.k)^2 sel_C u over its rows to dscale_partials (cdssm_shortcut_readout_rows_partials(n) floats; their
- *   sum, in any fixed order, is dL/dscale).
- * y, dy, V, dV (n, N); vp, dvp (n, N/2); sel_c, dsel_c (n) in `dtype`, dense; qk, dqk (n) fp32; scale one
- * fp32 on the device.  n = B*L*H.  The reference forms V_gated = V vp, scale (q.k)^2 V_gated and
+ *   (q.k)^2 sel_C u over its rows to dscale_partials (cdssm_shortcut_readout_rows_partials(n, N) floats;
+ *   their sum, in any fixed order, is dL/dscale).
+ * y, dy, V, dV (n, N); vp, dvp (n, N/2); sel_c, dsel_c (n) in `dtype`, dense, y and dV aligned to a
+ * (re, im) pair; qk, dqk (n) fp32; scale one fp32 on the device.  n = B*L*H.  The reference forms V_gated = V vp, scale (q.k)^2 V_gated and
  * (Y.q + shortcut) sel_C with torch ops (block.py:194-211) and autograd's rules for them; no launcher.
  */
-int64_t cdssm_shortcut_readout_rows_partials(int64_t n);
+int64_t cdssm_shortcut_readout_rows_partials(int64_t n, int64_t N);
 int cdssm_shortcut_readout_rows_fwd(int dtype, void* y, const float* qk, const void* V, const void* vp,
                                     const void* sel_c, const float* scale, int64_t n, int64_t N, hipStream_t stream);
 int cdssm_shortcut_readout_rows_bwd(int dtype, const void* dy, const float* qk, const void* V, const void* vp,

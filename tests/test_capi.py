@@ -99,6 +99,33 @@ def test_skinny_gemm_rejects_invalid_arguments_without_launching(over, msg):
     assert msg in _lib.last_error()
 
 
+@pytest.mark.parametrize("over,msg", [
+    (dict(N=5), "even N <= 64"),
+    (dict(N=66), "even N <= 64"),
+    (dict(n=0), "n > 0"),
+    (dict(y=18), "aligned to a (re, im) pair"),
+    (dict(qk=None), "null pointer"),
+])
+def test_shortcut_rows_fwd_rejects_invalid_arguments_without_launching(over, msg):
+    lib = _lib.load()
+    args = dict(dtype=1, y=16, qk=16, V=16, vp=16, sel=16, scale=16, n=1024, N=16, stream=None)
+    args.update(over)
+    assert lib.cdssm_shortcut_readout_rows_fwd(*args.values()) == -1
+    assert msg in _lib.last_error()
+
+
+def test_shortcut_rows_bwd_rejects_a_misaligned_gradient_and_sizes_its_partials():
+    lib = _lib.load()
+    args = [1, 16, 16, 16, 16, 16, 16, 18, 16, 16, 16, 16, 1024, 16, None]
+    assert lib.cdssm_shortcut_readout_rows_bwd(*args) == -1
+    assert "dV must be aligned" in _lib.last_error()
+    # one partial per 256-lane workgroup: a lane per complex pair where N/2 is a power of two, else per row
+    assert lib.cdssm_shortcut_readout_rows_partials(1024, 16) == 1024 * 8 // 256
+    assert lib.cdssm_shortcut_readout_rows_partials(1000, 2) == 4
+    assert lib.cdssm_shortcut_readout_rows_partials(1024, 6) == 4
+    assert lib.cdssm_shortcut_readout_rows_partials(0, 16) == -1
+
+
 def test_fused_bwd_rejects_rows_beyond_32_bit_offsets_without_launching():
     lib = _lib.load()
     ptrs = [16] * 9
