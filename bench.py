@@ -684,7 +684,7 @@ def time_lm_forward_state16(steps=3, warmup=1):
                     "via_y: SSDChunkwiseScan's fused kernels write Y and torch reads it out"}
 
 
-def time_block_train(steps=5, warmup=2, B=8, L=2048, state_dims=(2, 16), routes=("readout_scan", "ssd_y_readout")):
+def time_block_train(steps=10, warmup=3, B=8, L=2048, state_dims=(2, 16), routes=("readout_scan", "ssd_y_readout")):
     """One training step through one CDSSMBlock at config 4's shape (d_model 1024, 16 heads x 64,
     d_inner 1024, bf16; B8 L2048): forward and backward of sum(out * g), the way the reference trains
     (block.py:140-229 under autograd, trainer.py:235-247; gradients cleared each step as

@@ -346,9 +346,30 @@ def _weight_grad(gy: Tensor, x: Tensor) -> Tensor:
     return part.sum(0)
 
 
+def column_sum(x: Tensor) -> Tensor:
+    """x (T, C) -> sum over T (C,) in x's dtype: fp32 accumulation in a fixed order, one rounding
+    (cdssm_col_sum) where the HIP kernel serves the layout (CUDA bf16 / fp32, unit column stride, C and the
+    row stride multiples of the 16-byte vector, 16-byte aligned); otherwise ``x.sum(0)``.  torch's reduction
+    over the token dimension of a narrow matrix is slow on MI355X (gate_proj's 16384 x 336 bias gradient:
+    19 us, against 4-5 us for the HIP kernel)."""
+    T_, C = x.shape
+    nv = 16 // x.element_size()
+    if not (x.is_cuda and x.dtype in (torch.bfloat16, torch.float32) and x.stride(1) == 1 and C % nv == 0
+            and x.stride(0) % nv == 0 and x.stride(0) >= C and x.data_ptr() % 16 == 0 and 0 < T_ < (1 << 22)):
+        return x.sum(0)
+    lib = _lib.load()
+    ws = torch.empty(lib.cdssm_col_sum_workspace_bytes(T_, C) // 4, dtype=torch.float32, device=x.device)
+    out = torch.empty(C, dtype=x.dtype, device=x.device)
+    st = lib.cdssm_col_sum(_lib.DTYPE_CODE[x.dtype], _lib.ptr(x), x.stride(0), T_, C, _lib.ptr(out), _lib.ptr(ws),
+                           _lib.stream_of(x.device))
+    _lib.check(st, "cdssm_col_sum")
+    return out
+
+
 class TokenLinearFn(torch.autograd.Function):
     """x @ weight^T (+ bias) (+ residual) over (..., in) token rows -- nn.Linear plus the block's residual
-    add (block.py:229) -- whose weight gradient is split over token slabs (``_weight_grad``).  The residual
+    add (block.py:229) -- whose weight gradient is split over token slabs (``_weight_grad``) and whose bias
+    gradient is ``column_sum``.  The residual
     enters the GEMM's epilogue (one rounding of the sum, as the inference forward's out_proj); its gradient
     is the output's.  bias and residual are not both given."""
 
@@ -376,7 +397,7 @@ class TokenLinearFn(torch.autograd.Function):
         if ctx.needs_input_grad[1]:
             dw = _weight_grad(g2, x2).to(w.dtype)
         if ctx.has_bias and ctx.needs_input_grad[2]:
-            db = g2.sum(0)
+            db = column_sum(g2)
         return dx, dw, db, (gy if ctx.needs_input_grad[3] else None)
 
 
@@ -843,8 +864,9 @@ class CDSSMBlock(nn.Module):
     # training with the readout-form scan adds the current-token shortcut in the scan's autograd node
     # (ScanShortcutFn, HIP forward and backward); False: torch's elementwise ops for the shortcut
     fused_shortcut: bool = True
-    # training runs gate_proj, Q_proj, readout_proj and out_proj (with the residual add) through
-    # TokenLinearFn (weight gradients split over token slabs); False: nn.Linear and torch's add
+    # training runs the five projections (out_proj with the residual add) through TokenLinearFn (weight
+    # gradients split over token slabs where that is faster, bias gradients by cdssm_col_sum); False:
+    # nn.Linear and torch's add
     token_linear: bool = True
 
     def __init__(self, config: CDSSMConfig, layer_idx: int = 0):
@@ -1037,7 +1059,8 @@ class CDSSMBlock(nn.Module):
         N, H, D, Di = cfg.state_dim, cfg.n_heads, cfg.head_dim, cfg.d_inner
         B, L, _ = x.shape
         residual = x
-        proj = self.in_proj(self.norm(x))
+        lin = token_linear if self.token_linear else module_linear
+        proj = lin(self.in_proj, self.norm(x))
         z, x_gate, K, V = proj.split([Di, Di, Di, H * N], dim=-1)                     # block.py:162-166
         K = K.reshape(B, L, H, D)
         V = V.reshape(B, L, H, N)
@@ -1046,7 +1069,6 @@ class CDSSMBlock(nn.Module):
         else:
             V = torch.lerp(v_first, V, torch.sigmoid(self.v_residual_gate)[None, None, :, None].to(V.dtype))
         x_conv = self.conv(x_gate)                                                    # block.py:177
-        lin = token_linear if self.token_linear else module_linear
         gates = lin(self.gate_proj, x_conv)
         A_bar, vp, beta, sel_C = DynamicsFusedFn.apply(
             gates, self.log_dt_scale.float(), self.rope_freqs, cfg.gating_c, cfg.bf16_omega_thresh,

@@ -193,6 +193,44 @@ __global__ __launch_bounds__(256) void rms_col_sum_kernel(const float* __restric
 }
 
 // ---------------------------------------------------------------------------
+// Column sums of a (rows, C) matrix read through a row stride (a linear layer's
+// bias gradient: the sum of dL/dy over tokens).  Stage one: a workgroup of 4
+// waves takes kColSlab rows of a 64-vector column tile (one 16-byte vector per
+// lane), the waves interleaving rows; the 4 waves' sums are joined in order
+// into part[slab][c].  Stage two: rms_col_sum_kernel adds the slabs in order.
+// ---------------------------------------------------------------------------
+constexpr int kColSlab = 64;
+
+template <typename T>
+__global__ __launch_bounds__(256) void col_part_kernel(const typename T::raw* __restrict__ x, int64_t ld,
+                                                       int64_t rows, int C, float* __restrict__ part) {
+  constexpr int N = Vec16<T>::N;
+  __shared__ float red[4][kWave * N];
+  const int lane = int(threadIdx.x) % kWave, wv = int(threadIdx.x) / kWave;
+  const int c0 = (int(blockIdx.x) * kWave + lane) * N;
+  const int64_t r0 = int64_t(blockIdx.y) * kColSlab;
+  float acc[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) acc[i] = 0.0f;
+  if (c0 < C) {
+    for (int rr = wv; rr < kColSlab && r0 + rr < rows; rr += 4) {
+      Vec16<T> v;
+      v.load(x + (r0 + rr) * ld + c0);
+#pragma unroll
+      for (int i = 0; i < N; ++i) acc[i] += v.v[i];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) red[wv][lane * N + i] = acc[i];
+  __syncthreads();
+  // threads 0..255 write the tile's kWave * N columns (N * 64 <= 512 = 2 per thread for bf16)
+  for (int j = int(threadIdx.x); j < kWave * N; j += 256) {
+    const int c = int(blockIdx.x) * kWave * N + j;
+    if (c < C) part[int64_t(blockIdx.y) * C + c] = ((red[0][j] + red[1][j]) + red[2][j]) + red[3][j];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // K/Q normalisation and q.k: LPR lanes per (token, head) row of D elements,
 // one 16-byte vector each (D = LPR * vector width).  K and Q rows are read
 // through a token stride (elements), so K may be a column slice of a wider
@@ -1022,6 +1060,43 @@ extern "C" int cdssm_normalize_kq_qk_bwd(int dtype, const void* K, int64_t k_tok
     else if (lpr == 8) go(std::integral_constant<int, 8>{});
     else if (lpr == 16) go(std::integral_constant<int, 16>{});
     else go(std::integral_constant<int, 32>{});
+    return cdssm_host::check_launch(op);
+  });
+}
+
+extern "C" int64_t cdssm_col_sum_workspace_bytes(int64_t rows, int64_t C) {
+  if (rows <= 0 || C <= 0) return -1;
+  return ((rows + kColSlab - 1) / kColSlab) * C * int64_t(sizeof(float));
+}
+
+extern "C" int cdssm_col_sum(int dtype, const void* x, int64_t ld, int64_t rows, int64_t C, void* out,
+                             float* workspace, hipStream_t stream) {
+  const char* op = "cdssm_col_sum";
+  return by_dtype(dtype, op, [&](auto t) -> int {
+    using T = decltype(t);
+    using raw = typename T::raw;
+    constexpr int N = Vec16<T>::N;
+    if (rows <= 0 || C <= 0 || C % N != 0 || ld < C || ld % N != 0 || rows >= (int64_t(1) << 31) ||
+        C >= (int64_t(1) << 24)) {
+      cdssm_host::set_error("%s: need rows > 0, C a positive multiple of %d and a row stride >= C, a multiple of "
+                            "%d (rows=%lld C=%lld ld=%lld)", op, N, N, (long long)rows, (long long)C, (long long)ld);
+      return CDSSM_EINVAL;
+    }
+    if (!x || !out || !workspace || (reinterpret_cast<uintptr_t>(x) & 15u) != 0) {
+      cdssm_host::set_error("%s: x, out and workspace must be non-null, x 16-byte aligned", op);
+      return CDSSM_EINVAL;
+    }
+    const int slabs = int((rows + kColSlab - 1) / kColSlab);
+    if (slabs > 65535) {
+      cdssm_host::set_error("%s: at most %d rows", op, 65535 * kColSlab);
+      return CDSSM_EINVAL;
+    }
+    hipLaunchKernelGGL(col_part_kernel<T>, dim3(unsigned((C + kWave * N - 1) / (kWave * N)), unsigned(slabs)),
+                       dim3(256), 0, stream, static_cast<const raw*>(x), ld, rows, int(C), workspace);
+    int st = cdssm_host::check_launch(op);
+    if (st) return st;
+    hipLaunchKernelGGL(rms_col_sum_kernel<T>, dim3(unsigned((C + 15) / 16)), dim3(256), 0, stream,
+                       static_cast<const float*>(workspace), slabs, int(C), static_cast<raw*>(out));
     return cdssm_host::check_launch(op);
   });
 }

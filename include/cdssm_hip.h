@@ -596,6 +596,17 @@ int cdssm_shortcut_readout_fwd(int dtype, void* retrieved, const float* qk, cons
  * (Y.q + shortcut) sel_C with torch ops (block.py:194-211) and autograd's rules for them; no launcher.
  */
 int64_t cdssm_shortcut_readout_rows_partials(int64_t n, int64_t N);
+
+/*
+ * Column sums out[c] = sum_r x[r, c] of a (rows, C) matrix read through a row stride ld (elements), fp32
+ * accumulation in a fixed order (slabs of 64 rows, then the slabs in order), rounded once to `dtype`:
+ * the bias gradient of a linear layer (the sum of dL/dy over tokens), which autograd forms for the
+ * reference's nn.Linear projections (block.py:65-81; no launcher).  C and ld multiples of the 16-byte
+ * vector (8 bf16, 4 fp32), x 16-byte aligned; workspace of cdssm_col_sum_workspace_bytes(rows, C).
+ */
+int64_t cdssm_col_sum_workspace_bytes(int64_t rows, int64_t C);
+int cdssm_col_sum(int dtype, const void* x, int64_t ld, int64_t rows, int64_t C, void* out, float* workspace,
+                  hipStream_t stream);
 int cdssm_shortcut_readout_rows_fwd(int dtype, void* y, const float* qk, const void* V, const void* vp,
                                     const void* sel_c, const float* scale, int64_t n, int64_t N, hipStream_t stream);
 int cdssm_shortcut_readout_rows_bwd(int dtype, const void* dy, const float* qk, const void* V, const void* vp,

@@ -126,6 +126,22 @@ def test_shortcut_rows_bwd_rejects_a_misaligned_gradient_and_sizes_its_partials(
     assert lib.cdssm_shortcut_readout_rows_partials(0, 16) == -1
 
 
+@pytest.mark.parametrize("over,msg", [
+    (dict(C=30, ld=30), "multiple of 8"),
+    (dict(ld=300), "row stride >= C"),
+    (dict(x=24), "16-byte aligned"),
+    (dict(ws=None), "non-null"),
+    (dict(rows=0), "rows > 0"),
+])
+def test_col_sum_rejects_invalid_arguments_without_launching(over, msg):
+    lib = _lib.load()
+    args = dict(dtype=1, x=16, ld=336, rows=1024, C=336, out=16, ws=16, stream=None)
+    args.update(over)
+    assert lib.cdssm_col_sum(*args.values()) == -1
+    assert msg in _lib.last_error()
+    assert lib.cdssm_col_sum_workspace_bytes(16384, 336) == 256 * 336 * 4
+
+
 def test_fused_bwd_rejects_rows_beyond_32_bit_offsets_without_launching():
     lib = _lib.load()
     ptrs = [16] * 9

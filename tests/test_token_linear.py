@@ -84,3 +84,29 @@ def test_token_linear_gpu_matches_fp64(name, O, I, bias, residual, dtype):
     log("   " + "  ".join(f"{n} {e:.1e}" for n, e in errs.items()))
     bad = {n: e for n, e in errs.items() if not e <= tol}
     assert not bad, f"beyond {tol}: {bad}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,T,C,ld,off,dtype", [
+    ("gate_bias_bf16", 16384, 336, 336, 0, torch.bfloat16),
+    ("in_proj_bias_bf16", 16384, 3328, 3328, 0, torch.bfloat16),
+    ("column_slice_bf16", 3000, 1024, 3104, 1024, torch.bfloat16),
+    ("ragged_fp32", 1000, 44, 52, 8, torch.float32),
+    ("fallback_bf16", 500, 30, 30, 0, torch.bfloat16),
+])
+def test_column_sum_matches_fp64(name, T, C, ld, off, dtype):
+    """column_sum (cdssm_col_sum: fixed-order slab sums in fp32, one rounding; torch's sum where the kernel
+    does not serve the layout) against the fp64 sum: one rounding of the result (bf16 <= 2^-8, fp32 <= 1e-6
+    of the largest column sum), bit-identical on a repeat."""
+    from cdssm_hip.lm import column_sum
+    log(f"[column sum] {name}: T{T} C{C} ld{ld}")
+    gen = torch.Generator().manual_seed(3)
+    full = (torch.randn(T, ld, generator=gen) + 0.2).to(dtype).to(DEV)
+    x = full[:, off:off + C]
+    a, b = column_sum(x), column_sum(x)
+    torch.cuda.synchronize()
+    assert a.dtype == dtype and a.shape == (C,)
+    assert torch.equal(a, b)
+    err = rel(a, x.double().sum(0))
+    log(f"   rel err {err:.1e}")
+    assert err <= (2.0 ** -8 if dtype == torch.bfloat16 else 1e-6)
