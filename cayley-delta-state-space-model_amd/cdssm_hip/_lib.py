@@ -75,6 +75,7 @@ SIGNATURES = {
     "cdssm_shortcut_readout_fwd": (_I32, [_I32] + [_P] * 6 + [_I64, _P]),
     "cdssm_shortcut_readout_rows_partials": (_I64, [_I64, _I64]),
     "cdssm_col_sum_workspace_bytes": (_I64, [_I64, _I64]),
+    "cdssm_slab_sum": (_I32, [_I32, _P, _I64, _I64, _P, _P]),
     "cdssm_col_sum": (_I32, [_I32, _P, _I64, _I64, _I64, _P, _P, _P]),
     "cdssm_shortcut_readout_rows_fwd": (_I32, [_I32] + [_P] * 6 + [_I64, _I64, _P]),
     "cdssm_shortcut_readout_rows_bwd": (_I32, [_I32] + [_P] * 11 + [_I64, _I64, _P]),

@@ -325,25 +325,32 @@ def skinny_linear(x: Tensor, weight: Tensor, bias: Optional[Tensor] = None, resi
 def _wgrad_slabs(T: int, O: int, I: int) -> int:
     """Token slabs of a weight gradient dW = dY^T X over T tokens (O x I output).  One GEMM with an O x I
     output of at most 1024 x 1024 and T = 16384 leaves most CUs idle (hipBLASLt: 64 x 64 tiles, no split
-    over the reduction; 0.1-0.3 PFLOP/s on MI355X); 8 slabs as one batched product with fp32 partials, summed
-    in fp32, ran 1.9-2.9x faster there (out_proj / Q_proj 111 -> 58 us, readout_proj 91 -> 33, gate_proj
-    98 -> 37 us, sum included).  Larger outputs (in_proj) keep the single product."""
-    return 8 if T >= 8192 and T % 8 == 0 and O * I <= (1 << 20) else 1
+    over the reduction; 0.1-0.3 PFLOP/s on MI355X); 8 slabs as one batched product with fp32 partials ran
+    2-3x faster there (out_proj / Q_proj 100-111 -> 39 us, readout_proj 91 -> 23, gate_proj 98 -> 29 us
+    before the slab sum); in_proj's 3328 x 1024 takes 2 slabs (185 -> 141 us before the sum)."""
+    if T < 8192 or T % 8:
+        return 1
+    return 8 if O * I <= (1 << 20) else 2
 
 
-def _weight_grad(gy: Tensor, x: Tensor) -> Tensor:
-    """dW = gy^T x for gy (T, O) and x (T, I), accumulated in fp32 (as one GEMM does), returned in fp32
-    when split over token slabs: a batched product of the slabs with fp32 outputs, then a fixed-order sum."""
+def _weight_grad(gy: Tensor, x: Tensor, dtype: torch.dtype) -> Tensor:
+    """dW = gy^T x in ``dtype`` for gy (T, O) and x (T, I), accumulated in fp32 as one GEMM does: split over
+    token slabs, a batched product of the slabs with fp32 outputs and their fixed-order sum rounded once
+    (cdssm_slab_sum) where the HIP kernel serves the dtype; otherwise one product."""
     T, O = gy.shape
     I = x.shape[1]
     S = _wgrad_slabs(T, O, I)
-    if S == 1:
-        return torch.mm(gy.t(), x)
+    if S == 1 or not gy.is_cuda or dtype not in _lib.DTYPE_CODE:
+        return torch.mm(gy.t(), x).to(dtype)
     a = gy.as_strided((S, T // S, O), (T // S * gy.stride(0), gy.stride(0), gy.stride(1))).transpose(1, 2)
     b = x.as_strided((S, T // S, I), (T // S * x.stride(0), x.stride(0), x.stride(1)))
     half = gy.dtype in (torch.bfloat16, torch.float16)
-    part = torch.bmm(a, b, out_dtype=torch.float32) if half else torch.bmm(a, b)
-    return part.sum(0)
+    part = (torch.bmm(a, b, out_dtype=torch.float32) if half else torch.bmm(a, b)).contiguous()
+    out = torch.empty(O, I, dtype=dtype, device=gy.device)
+    st = _lib.load().cdssm_slab_sum(_lib.DTYPE_CODE[dtype], _lib.ptr(part), S, O * I, _lib.ptr(out),
+                                    _lib.stream_of(gy.device))
+    _lib.check(st, "cdssm_slab_sum")
+    return out
 
 
 def column_sum(x: Tensor) -> Tensor:
@@ -395,7 +402,7 @@ class TokenLinearFn(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             dx = torch.mm(g2, w).view(ctx.xshape)
         if ctx.needs_input_grad[1]:
-            dw = _weight_grad(g2, x2).to(w.dtype)
+            dw = _weight_grad(g2, x2, w.dtype)
         if ctx.has_bias and ctx.needs_input_grad[2]:
             db = column_sum(g2)
         return dx, dw, db, (gy if ctx.needs_input_grad[3] else None)

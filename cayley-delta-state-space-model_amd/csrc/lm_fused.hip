@@ -231,6 +231,35 @@ __global__ __launch_bounds__(256) void col_part_kernel(const typename T::raw* __
 }
 
 // ---------------------------------------------------------------------------
+// Sum of S fp32 slabs of n elements, out[i] = sum_s part[s n + i] in slab
+// order, rounded once (the token-slab partials of a weight gradient).  Four
+// consecutive elements per thread where n % 4 == 0, else one.
+// ---------------------------------------------------------------------------
+template <typename T, int V>
+__global__ __launch_bounds__(256) void slab_sum_kernel(const float* __restrict__ part, int S, int64_t n,
+                                                       typename T::raw* __restrict__ out) {
+  const int64_t i = (int64_t(blockIdx.x) * 256 + threadIdx.x) * V;
+  if (i >= n) return;
+  float a[V] = {};
+  for (int s = 0; s < S; ++s) {
+    if constexpr (V == 4) {
+      const float4 v = *reinterpret_cast<const float4*>(part + int64_t(s) * n + i);
+      a[0] += v.x;
+      a[1] += v.y;
+      a[2] += v.z;
+      a[3] += v.w;
+    } else {
+      a[0] += part[int64_t(s) * n + i];
+    }
+  }
+  if constexpr (V == 4) {
+    store_row<T, 4>(out + i, a);
+  } else {
+    T::store(out + i, a[0]);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // K/Q normalisation and q.k: LPR lanes per (token, head) row of D elements,
 // one 16-byte vector each (D = LPR * vector width).  K and Q rows are read
 // through a token stride (elements), so K may be a column slice of a wider
@@ -1097,6 +1126,31 @@ extern "C" int cdssm_col_sum(int dtype, const void* x, int64_t ld, int64_t rows,
     if (st) return st;
     hipLaunchKernelGGL(rms_col_sum_kernel<T>, dim3(unsigned((C + 15) / 16)), dim3(256), 0, stream,
                        static_cast<const float*>(workspace), slabs, int(C), static_cast<raw*>(out));
+    return cdssm_host::check_launch(op);
+  });
+}
+
+extern "C" int cdssm_slab_sum(int dtype, const float* part, int64_t S, int64_t n, void* out, hipStream_t stream) {
+  const char* op = "cdssm_slab_sum";
+  return by_dtype(dtype, op, [&](auto t) -> int {
+    using T = decltype(t);
+    using raw = typename T::raw;
+    if (S <= 0 || S > 4096 || n <= 0 || n >= (int64_t(1) << 40)) {
+      cdssm_host::set_error("%s: need 0 < S <= 4096 and n > 0 (S=%lld n=%lld)", op, (long long)S, (long long)n);
+      return CDSSM_EINVAL;
+    }
+    if (!part || !out) {
+      cdssm_host::set_error("%s: null pointer argument", op);
+      return CDSSM_EINVAL;
+    }
+    const bool vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(part) & 15u) == 0 &&
+                     (reinterpret_cast<uintptr_t>(out) & uintptr_t(4 * T::bytes - 1)) == 0;
+    if (vec)
+      hipLaunchKernelGGL((slab_sum_kernel<T, 4>), dim3(unsigned((n / 4 + 255) / 256)), dim3(256), 0, stream, part,
+                         int(S), n, static_cast<raw*>(out));
+    else
+      hipLaunchKernelGGL((slab_sum_kernel<T, 1>), dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, part,
+                         int(S), n, static_cast<raw*>(out));
     return cdssm_host::check_launch(op);
   });
 }

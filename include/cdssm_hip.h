@@ -605,6 +605,13 @@ int64_t cdssm_shortcut_readout_rows_partials(int64_t n, int64_t N);
  * vector (8 bf16, 4 fp32), x 16-byte aligned; workspace of cdssm_col_sum_workspace_bytes(rows, C).
  */
 int64_t cdssm_col_sum_workspace_bytes(int64_t rows, int64_t C);
+
+/*
+ * out[i] = sum_s part[s n + i] over S fp32 slabs of n elements, in slab order, rounded once to `dtype`:
+ * the token-slab partials of a weight gradient dW = dY^T X (autograd's rule for the reference's
+ * nn.Linear projections, block.py:65-81; no launcher) joined into the weight's dtype.
+ */
+int cdssm_slab_sum(int dtype, const float* part, int64_t S, int64_t n, void* out, hipStream_t stream);
 int cdssm_col_sum(int dtype, const void* x, int64_t ld, int64_t rows, int64_t C, void* out, float* workspace,
                   hipStream_t stream);
 int cdssm_shortcut_readout_rows_fwd(int dtype, void* y, const float* qk, const void* V, const void* vp,

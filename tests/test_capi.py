@@ -142,6 +142,14 @@ def test_col_sum_rejects_invalid_arguments_without_launching(over, msg):
     assert lib.cdssm_col_sum_workspace_bytes(16384, 336) == 256 * 336 * 4
 
 
+def test_slab_sum_rejects_invalid_arguments_without_launching():
+    lib = _lib.load()
+    assert lib.cdssm_slab_sum(1, 16, 0, 1024, 16, None) == -1 and "0 < S" in _lib.last_error()
+    assert lib.cdssm_slab_sum(1, 16, 8, 0, 16, None) == -1 and "n > 0" in _lib.last_error()
+    assert lib.cdssm_slab_sum(1, None, 8, 1024, 16, None) == -1 and "null pointer" in _lib.last_error()
+    assert lib.cdssm_slab_sum(7, 16, 8, 1024, 16, None) == -1
+
+
 def test_fused_bwd_rejects_rows_beyond_32_bit_offsets_without_launching():
     lib = _lib.load()
     ptrs = [16] * 9

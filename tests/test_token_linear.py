@@ -1,12 +1,12 @@
 """TokenLinearFn: the block's training projections (nn.Linear, block.py:65-81, with out_proj's residual add,
-block.py:229) with the weight gradient dW = dY^T X split over token slabs, each slab's product in fp32 and the
-slabs summed in a fixed order.
+block.py:229) with the weight gradient dW = dY^T X split over token slabs on the GPU (each slab's product in
+fp32, the slabs summed in a fixed order by cdssm_slab_sum) and the bias gradient by cdssm_col_sum.
 
-CPU (fp64): output, dx, dW, db and the residual's gradient against autograd through F.linear + add, at a
-token count that takes the split (T = 16384, small outputs) and one that does not; the split must equal the
-single product to fp64 rounding.  GPU: bf16 and fp32 at the block's shapes (T = B L = 16384; out_proj 1024 x
-1024, readout_proj 1024 x 256, gate_proj 336 x 1024 with bias) against fp64 autograd on the same rounded
-inputs: fp32 <= 1e-5, bf16 <= 1e-2 normwise (the bf16 rounding of each output), and bit-identical repeats.
+CPU (fp64; one product for dW there): output, dx, dW, db and the residual's gradient against autograd
+through F.linear + add.  GPU: bf16 and fp32 at the block's shapes (T = B L = 16384; out_proj 1024 x 1024,
+readout_proj 1024 x 256, gate_proj 336 x 1024 with bias: 8 slabs; in_proj 3328 x 1024 with bias: 2 slabs)
+against fp64 autograd on the same rounded inputs: fp32 <= 1e-5, bf16 <= 1e-2 normwise (the bf16 rounding of
+each output), and bit-identical repeats.
 """
 
 import pytest
@@ -60,12 +60,13 @@ def test_token_linear_matches_linear_fp64_cpu(B, L, O, I, bias, residual):
     ("out_proj_bf16", 1024, 1024, False, True, torch.bfloat16),
     ("readout_proj_bf16", 1024, 256, False, False, torch.bfloat16),
     ("gate_proj_bf16", 336, 1024, True, False, torch.bfloat16),
+    ("in_proj_bf16", 3328, 1024, True, False, torch.bfloat16),
     ("out_proj_fp32", 1024, 1024, False, True, torch.float32),
 ])
 def test_token_linear_gpu_matches_fp64(name, O, I, bias, residual, dtype):
     from cdssm_hip.lm import _wgrad_slabs
     B, L = 8, 2048
-    assert _wgrad_slabs(B * L, O, I) == 8
+    assert _wgrad_slabs(B * L, O, I) == (8 if O * I <= 1 << 20 else 2)
     log(f"[token linear gpu] {name}: T{B * L} {O}x{I}")
     x, w, b, r, g = draw(B, L, O, I, bias, residual, dtype, DEV, seed=1)
     got = run_fn(x, w, b, r, g)
