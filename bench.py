@@ -84,8 +84,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="C1", choices=["C1", "C2", "C3"],
-                    help="forward workload (C1 is the metric's; C2 and C3 for profiling)")
+    ap.add_argument("--config", default="C1", choices=["C1", "C2", "C3", "C4scan"],
+                    help="forward workload (C1 is the metric's; C2, C3 and C4scan, the config-4 block's scan shape, for profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-batches", type=int, default=1)
     ap.add_argument("--no-fwd-bwd", action="store_true")

@@ -60,6 +60,9 @@ CONFIGS: Dict[str, ScanConfig] = {
     "C1": ScanConfig("C1", B=8, H=16, L=4096, D=64),
     "C2": ScanConfig("C2", B=4, H=24, L=8192, D=128, backward=True),
     "C3": ScanConfig("C3", B=1, H=32, L=65536, D=64, omega_std=3.0, h0_std=0.1),
+    # the scan inside one config-4 block (B8 L2048, 16 heads x 64), scan-level inputs: for the kernel's phase
+    # stamps at that shape (the block itself calls the gate-level form, the same kernel structure)
+    "C4scan": ScanConfig("C4scan", B=8, H=16, L=2048, D=64),
 }
 
 
