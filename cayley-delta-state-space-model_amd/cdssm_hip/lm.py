@@ -333,6 +333,31 @@ def _wgrad_slabs(T: int, O: int, I: int) -> int:
     return 8 if O * I <= (1 << 20) else 2
 
 
+def _padded_features(O: int) -> int:
+    """Output features a wide projection's forward GEMM is computed with: O rounded up to a multiple of 256
+    where O >= 2048 is not one.  hipBLASLt's kernel for (16384 x 1024) @ (1024 x O) on MI355X takes 159 us at
+    O = 3104 (in_proj at state_dim 2: 3 d_inner + 2 H) and 103 us at O = 3328 (0.65 against 1.09 PFLOP/s);
+    the extra features are zero rows of the weight, sliced off the output."""
+    return O if O < 2048 or O % 256 == 0 else (O + 255) // 256 * 256
+
+
+def padded_linear(x2: Tensor, weight: Tensor, bias: Optional[Tensor], padded: Optional[tuple] = None) -> Tensor:
+    """x2 (T, I) @ weight^T (+ bias) -> (T, O), computed with the output features padded as
+    ``_padded_features`` says (the result a column slice of the padded product, row stride O_pad).
+    ``padded``: the (weight, bias) already padded, else they are padded here."""
+    O = weight.shape[0]
+    Op = _padded_features(O)
+    if Op == O:
+        return torch.addmm(bias, x2, weight.t()) if bias is not None else torch.mm(x2, weight.t())
+    if padded is None:
+        w = torch.cat([weight, weight.new_zeros(Op - O, weight.shape[1])])
+        b = None if bias is None else torch.cat([bias, bias.new_zeros(Op - O)])
+    else:
+        w, b = padded
+    y = torch.addmm(b, x2, w.t()) if b is not None else torch.mm(x2, w.t())
+    return y[:, :O]
+
+
 def _weight_grad(gy: Tensor, x: Tensor, dtype: torch.dtype) -> Tensor:
     """dW = gy^T x in ``dtype`` for gy (T, O) and x (T, I), accumulated in fp32 as one GEMM does: split over
     token slabs, a batched product of the slabs with fp32 outputs and their fixed-order sum rounded once
@@ -386,10 +411,8 @@ class TokenLinearFn(torch.autograd.Function):
         x2 = x.reshape(-1, x.shape[-1])
         if residual is not None:
             y = torch.addmm(residual.reshape(-1, O), x2, weight.t())
-        elif bias is not None:
-            y = torch.addmm(bias, x2, weight.t())
         else:
-            y = torch.mm(x2, weight.t())
+            y = padded_linear(x2, weight, bias)
         ctx.save_for_backward(x2, weight)
         ctx.xshape, ctx.has_bias = x.shape, bias is not None
         return y.view(*x.shape[:-1], O)
@@ -921,6 +944,23 @@ class CDSSMBlock(nn.Module):
             self._f32_cache[("as", name)] = hit
         return hit[1]
 
+    def _padded_in_proj(self) -> Optional[tuple]:
+        """in_proj's weight and bias with zero rows up to ``_padded_features`` (None where no padding
+        applies), kept while the parameters' storage and versions are unchanged."""
+        w, b = self.in_proj.weight, self.in_proj.bias
+        O = w.shape[0]
+        Op = _padded_features(O)
+        if Op == O:
+            return None
+        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in (w, b))
+        hit = self._f32_cache.get("in_proj_pad")
+        if hit is None or hit[0] != key:
+            wp = torch.cat([w.detach(), w.new_zeros(Op - O, w.shape[1])]).contiguous()
+            bp = torch.cat([b.detach(), b.new_zeros(Op - O)]).contiguous()
+            hit = (key, (wp, bp))
+            self._f32_cache["in_proj_pad"] = hit
+        return hit[1]
+
     def _stacked_gate_q(self) -> tuple:
         """[gate_proj.weight; Q_proj.weight] and [gate_proj.bias; 0]: the decode step's two projections of
         x_conv (block.py:180, 190) as one GEMM (one launch fewer per layer; at the forward's B*L rows the
@@ -979,7 +1019,11 @@ class CDSSMBlock(nn.Module):
             return self._forward_autograd(x, v_first)
         B, L, _ = x.shape
         residual = x
-        proj = self.in_proj(self.norm(x))  # (B, L, 3 Di + H N); z, x_gate and K are read in place
+        # (B, L, 3 Di + H N), a column slice of the product with the features padded where that is faster;
+        # z, x_gate and K are read in place
+        xn = self.norm(x)
+        proj = padded_linear(xn.reshape(B * L, -1), self.in_proj.weight, self.in_proj.bias,
+                             self._padded_in_proj()).view(B, L, -1)
         z, x_gate, K, V = proj.split([Di, Di, Di, H * N], dim=-1)
         K = K.reshape(B, L, H, D)
         V = V.reshape(B, L, H, N)

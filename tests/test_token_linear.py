@@ -55,12 +55,28 @@ def test_token_linear_matches_linear_fp64_cpu(B, L, O, I, bias, residual):
             assert rel(a, e) <= 1e-12, n
 
 
+@pytest.mark.parametrize("O,bias", [(3104, True), (3104, False), (3328, True), (1040, True)])
+def test_padded_linear_matches_linear_fp64_cpu(O, bias):
+    """padded_linear: the product with the output features rounded up to a multiple of 256 (zero weight rows,
+    O >= 2048) and sliced back equals F.linear; the result is a column slice (row stride O_pad)."""
+    from cdssm_hip.lm import _padded_features, padded_linear
+    gen = torch.Generator().manual_seed(2)
+    x = torch.randn(70, 96, generator=gen, dtype=torch.float64)
+    w = torch.randn(O, 96, generator=gen, dtype=torch.float64)
+    b = torch.randn(O, generator=gen, dtype=torch.float64) if bias else None
+    y = padded_linear(x, w, b)
+    assert y.shape == (70, O) and y.stride(0) == _padded_features(O)
+    assert _padded_features(3104) == 3328 and _padded_features(3328) == 3328 and _padded_features(1040) == 1040
+    assert torch.equal(y, torch.nn.functional.linear(x, w, b))
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,O,I,bias,residual,dtype", [
     ("out_proj_bf16", 1024, 1024, False, True, torch.bfloat16),
     ("readout_proj_bf16", 1024, 256, False, False, torch.bfloat16),
     ("gate_proj_bf16", 336, 1024, True, False, torch.bfloat16),
     ("in_proj_bf16", 3328, 1024, True, False, torch.bfloat16),
+    ("in_proj_state2_padded_bf16", 3104, 1024, True, False, torch.bfloat16),
     ("out_proj_fp32", 1024, 1024, False, True, torch.float32),
 ])
 def test_token_linear_gpu_matches_fp64(name, O, I, bias, residual, dtype):
