@@ -944,6 +944,17 @@ class CDSSMBlock(nn.Module):
             self._f32_cache[("as", name)] = hit
         return hit[1]
 
+    def _value_gate(self, dtype: torch.dtype) -> Tensor:
+        """sigmoid(v_residual_gate) as (1, 1, H, 1) in ``dtype`` (block.py:169-174), kept while the parameter's
+        storage and version are unchanged, so an inference forward launches no kernel for it."""
+        g = self.v_residual_gate
+        key = (g.data_ptr(), g._version, dtype, g.device)
+        hit = self._f32_cache.get("vgate")
+        if hit is None or hit[0] != key:
+            hit = (key, torch.sigmoid(g.detach())[None, None, :, None].to(dtype))
+            self._f32_cache["vgate"] = hit
+        return hit[1]
+
     def _padded_in_proj(self) -> Optional[tuple]:
         """in_proj's weight and bias with zero rows up to ``_padded_features`` (None where no padding
         applies), kept while the parameters' storage and versions are unchanged."""
@@ -1030,7 +1041,7 @@ class CDSSMBlock(nn.Module):
         if v_first is None:
             v_first = V.detach()
         else:
-            V = torch.lerp(v_first, V, torch.sigmoid(self.v_residual_gate)[None, None, :, None].to(V.dtype))
+            V = torch.lerp(v_first, V, self._value_gate(V.dtype))
         x_conv = self.conv(x_gate)
         if cache is not None:
             Kc = self.conv.kernel_size - 1
