@@ -226,6 +226,120 @@ __global__ __launch_bounds__(256) void conv1d_silu_bwd_kernel(const typename T::
   pr[int64_t(K) * C] = gb;
 }
 
+// The same backward with VEC adjacent channels per thread (16-byte rows of x,
+// grad_out and grad_x; the caller checks C % VEC == 0, 16-byte aligned rows):
+// the thread walks its kConvBwdTB tokens plus the K-1 after them once, keeping
+// the last K inputs and the last K values of gu in registers; gu at token t is
+// formed when x[t] arrives, the weight / bias partials take it at once (owned
+// tokens), and gx[t-(K-1)] is complete when gu[t] is.  Every sum runs in the
+// order of the kernel above, so both give the same bits.
+template <typename T, int K, int VEC>
+__global__ __launch_bounds__(256) void conv1d_silu_bwd_vec_kernel(const typename T::raw* __restrict__ x, int64_t x_ts,
+                                                                  const typename T::raw* __restrict__ w,
+                                                                  const typename T::raw* __restrict__ bias,
+                                                                  const typename T::raw* __restrict__ gy,
+                                                                  typename T::raw* __restrict__ gx,
+                                                                  float* __restrict__ part, int L, int C, int ntb,
+                                                                  int n_threads) {
+  constexpr int TB = kConvBwdTB;
+  const int gid = int(blockIdx.x) * int(blockDim.x) + int(threadIdx.x);  // n_threads < 2^31 (host check)
+  if (gid >= n_threads) return;
+  const int ncv = C / VEC;
+  const int rest = gid / ncv;
+  const int c = (gid - rest * ncv) * VEC;
+  const int b = rest / ntb;
+  const int tb = rest - b * ntb;
+  const int t0 = tb * TB;
+  float wt[K][VEC], bs[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    bs[v] = T::load(bias + c + v);
+#pragma unroll
+    for (int j = 0; j < K; ++j) wt[j][v] = T::load(w + int64_t(c + v) * K + j);
+  }
+  const typename T::raw* xb = x + int64_t(b) * L * x_ts + c;
+  const typename T::raw* gyb = gy + int64_t(b) * L * C + c;
+  typename T::raw* gxb = gx + int64_t(b) * L * C + c;
+  // xw[j] = x[t - (K-1) + j] (zero outside [0, L)), gw_[j] = gu[t - (K-1) + j] at step t
+  float xw[K][VEC], gw_[K][VEC];
+#pragma unroll
+  for (int j = 0; j < K; ++j)
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      xw[j][v] = 0.0f;
+      gw_[j][v] = 0.0f;
+    }
+#pragma unroll
+  for (int j = 1; j < K; ++j) {
+    const int s = t0 - K + j;  // x[t0 - (K-1) + (j - 1)]
+    if (s >= 0 && s < L) load_vec<T, VEC>(xb + int64_t(s) * x_ts, xw[j]);
+  }
+  float gwt[K][VEC], gbs[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    gbs[v] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < K; ++j) gwt[j][v] = 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < TB + K - 1; ++i) {
+    const int t = t0 + i;
+    // shift the windows and bring in x[t] and grad_out[t]
+#pragma unroll
+    for (int j = 0; j < K - 1; ++j)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        xw[j][v] = xw[j + 1][v];
+        gw_[j][v] = gw_[j + 1][v];
+      }
+    float g[VEC];
+    if (t < L) {
+      load_vec<T, VEC>(xb + int64_t(t) * x_ts, xw[K - 1]);
+      load_vec<T, VEC>(gyb + int64_t(t) * C, g);
+    } else {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        xw[K - 1][v] = 0.0f;
+        g[v] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      float u = bs[v];
+#pragma unroll
+      for (int j = 0; j < K; ++j) u = fmaf(wt[j][v], xw[j][v], u);
+      const float sg = 1.0f / (1.0f + __expf(-u));
+      gw_[K - 1][v] = t < L ? g[v] * (sg * (1.0f + u * (1.0f - sg))) : 0.0f;
+    }
+    if (i < TB && t < L) {  // an owned token: the weight and bias partials
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+#pragma unroll
+        for (int j = 0; j < K; ++j) gwt[j][v] = fmaf(gw_[K - 1][v], xw[j][v], gwt[j][v]);
+        gbs[v] += gw_[K - 1][v];
+      }
+    }
+    const int so = t - (K - 1);  // gx[so] = sum_j w[j] gu[so + (K-1) - j] = sum_j w[j] gu[t - j]
+    if (i >= K - 1 && so < L) {
+      float a[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        a[v] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < K; ++j) a[v] = fmaf(wt[j][v], gw_[K - 1 - j][v], a[v]);
+      }
+      store_vec<T, VEC>(gxb + int64_t(so) * C, a);
+    }
+  }
+  float* pr = part + int64_t(b * ntb + tb) * (K + 1) * C + c;
+#pragma unroll
+  for (int j = 0; j < K; ++j)
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) pr[int64_t(j) * C + v] = gwt[j][v];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) pr[int64_t(K) * C + v] = gbs[v];
+}
+
 // grad_weight (C, K) and grad_bias (C), fp32: the partial rows added in order.
 // Sum of the partial rows: a workgroup of kRedWaves waves owns 64 adjacent
 // columns (j, c) of the (rows, K + 1, C) partials (one column per lane, so each
@@ -271,11 +385,22 @@ template <typename T, int K>
 int launch_conv_bwd(const void* x, int64_t x_ts, const void* w, const void* bias, const void* gy, void* gx,
                     float* gw, float* gb, float* ws, int64_t B, int64_t L, int64_t C, hipStream_t stream) {
   using raw = typename T::raw;
+  constexpr int VEC = 16 / T::bytes;
   const int ntb = int((L + kConvBwdTB - 1) / kConvBwdTB);
-  const int n = int(B * ntb * C);
-  hipLaunchKernelGGL((conv1d_silu_bwd_kernel<T, K>), dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream,
-                     static_cast<const raw*>(x), x_ts, static_cast<const raw*>(w), static_cast<const raw*>(bias),
-                     static_cast<const raw*>(gy), static_cast<raw*>(gx), ws, int(L), int(C), ntb, n);
+  const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  const bool vec = C % VEC == 0 && (x_ts * T::bytes) % 16 == 0 && a16(x) && a16(gy) && a16(gx);
+  if (vec) {
+    const int n = int(B * ntb * (C / VEC));
+    hipLaunchKernelGGL((conv1d_silu_bwd_vec_kernel<T, K, VEC>), dim3(unsigned((n + 255) / 256)), dim3(256), 0,
+                       stream, static_cast<const raw*>(x), x_ts, static_cast<const raw*>(w),
+                       static_cast<const raw*>(bias), static_cast<const raw*>(gy), static_cast<raw*>(gx), ws, int(L),
+                       int(C), ntb, n);
+  } else {
+    const int n = int(B * ntb * C);
+    hipLaunchKernelGGL((conv1d_silu_bwd_kernel<T, K>), dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<const raw*>(x), x_ts, static_cast<const raw*>(w), static_cast<const raw*>(bias),
+                       static_cast<const raw*>(gy), static_cast<raw*>(gx), ws, int(L), int(C), ntb, n);
+  }
   const int nr = int((K + 1) * C);
   hipLaunchKernelGGL(conv1d_silu_bwd_reduce_kernel, dim3(unsigned((nr + 63) / 64)), dim3(64 * kRedWaves), 0, stream,
                      ws, gw, gb, int(B * ntb), int(C), K);

@@ -153,7 +153,8 @@ def test_conv1d_silu_strided(dtype, B, L, C, K, pad):
 
 
 @pytest.mark.parametrize("dtype,B,L,C,K,pad", [(torch.float32, 2, 37, 24, 4, 0), (torch.float32, 1, 50, 16, 3, 5),
-                                               (torch.bfloat16, 2, 300, 256, 4, 64), (torch.float32, 1, 3, 8, 8, 0)])
+                                               (torch.bfloat16, 2, 300, 256, 4, 64), (torch.float32, 1, 3, 8, 8, 0),
+                                               (torch.bfloat16, 1, 70, 64, 4, 3)])
 def test_conv1d_silu_backward(dtype, B, L, C, K, pad):
     """Conv1dSiLU backward (cdssm_conv1d_silu_bwd) against autograd through the oracle's fp64 conv on the same
     rounded inputs; x read as a column slice when pad > 0."""
@@ -223,3 +224,28 @@ def test_lm_training_gradients_match_oracle(N):
     assert e_out <= 1e-3
     bad = {n: e for n, e in errs.items() if not e <= 1e-3}
     assert not bad, bad
+
+
+@pytest.mark.parametrize("dtype,K", [(torch.bfloat16, 4), (torch.float32, 4), (torch.bfloat16, 3)])
+def test_conv1d_silu_backward_vector_and_scalar_paths_agree_bitwise(dtype, K):
+    """cdssm_conv1d_silu_bwd takes 16-byte channel vectors where x, grad_out and grad_x rows are 16-byte
+    aligned and one channel per thread otherwise; both add every sum in the same order, so the same inputs
+    give the same bits (x read at an aligned and at a misaligned column offset)."""
+    from cdssm_hip.lm import conv1d_silu_bwd
+    B, L, C = 2, 531, 512
+    log(f"[conv1d_silu bwd paths] {dtype} K{K}")
+    g = torch.Generator().manual_seed(8)
+    f32 = dict(generator=g, dtype=torch.float32)
+    x = torch.randn(B, L, C, **f32).to(dtype)
+    w = (torch.randn(C, 1, K, **f32) / K ** 0.5).to(dtype).to(DEV)
+    b = torch.randn(C, **f32).to(dtype).to(DEV)
+    gy = torch.randn(B, L, C, **f32).to(dtype).to(DEV)
+    wide = torch.zeros(B, L, C + 16, dtype=dtype)
+    wide[..., 8:8 + C] = x        # 16-byte aligned rows (bf16: 16 bytes in; fp32: 32 bytes)
+    odd = torch.zeros(B, L, C + 16, dtype=dtype)
+    odd[..., 1:1 + C] = x         # misaligned: one channel per thread
+    ga = conv1d_silu_bwd(wide.to(DEV)[..., 8:8 + C], w, b, gy)
+    gb = conv1d_silu_bwd(odd.to(DEV)[..., 1:1 + C], w, b, gy)
+    torch.cuda.synchronize()
+    for a, c in zip(ga, gb):
+        assert torch.equal(a, c)
