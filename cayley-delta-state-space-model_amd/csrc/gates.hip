@@ -184,20 +184,36 @@ __global__ __launch_bounds__(256) void dynamics_bwd_kernel(
   glog_terms[o] = g_dts * sigmoid(log_scale);
 }
 
-// Fixed-order per-head sum of the per-token grad_log_dt_scale terms.
-__global__ __launch_bounds__(256) void head_sum_kernel(const float* __restrict__ terms,
-                                                       float* __restrict__ out, int64_t BL, int H) {
+// Fixed-order per-head sum of the per-token grad_log_dt_scale terms (BL, H):
+// the workgroup (h, slab) adds its slab of kHeadSlabs consecutive row ranges
+// (threads strided, then a fixed tree) into part[slab][h]; a second launch
+// adds the slabs in order per head.  H x kHeadSlabs workgroups keep the loads
+// in flight across the device (one workgroup per head left 240 CUs idle).
+constexpr int kHeadSlabs = 64;
+
+__global__ __launch_bounds__(256) void head_part_kernel(const float* __restrict__ terms,
+                                                        float* __restrict__ part, int64_t BL, int H) {
   __shared__ float sm[256];
-  const int h = blockIdx.x;
+  const int h = blockIdx.x, sl = blockIdx.y;
+  const int64_t r0 = BL * sl / kHeadSlabs, r1 = BL * (sl + 1) / kHeadSlabs;
   float a = 0.0f;
-  for (int64_t i = threadIdx.x; i < BL; i += 256) a += terms[i * H + h];
+  for (int64_t i = r0 + threadIdx.x; i < r1; i += 256) a += terms[i * H + h];
   sm[threadIdx.x] = a;
   __syncthreads();
   for (int s = 128; s > 0; s >>= 1) {
     if (int(threadIdx.x) < s) sm[threadIdx.x] += sm[threadIdx.x + s];
     __syncthreads();
   }
-  if (threadIdx.x == 0) out[h] = sm[0];
+  if (threadIdx.x == 0) part[int64_t(sl) * H + h] = sm[0];
+}
+
+__global__ __launch_bounds__(256) void head_sum_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                       int H) {
+  const int h = int(blockIdx.x) * 256 + int(threadIdx.x);
+  if (h >= H) return;
+  float a = 0.0f;
+  for (int sl = 0; sl < kHeadSlabs; ++sl) a += part[int64_t(sl) * H + h];
+  out[h] = a;
 }
 
 // ---------------------------------------------------------------------------
@@ -334,7 +350,7 @@ extern "C" int cdssm_dynamics_fused_fwd(int dtype, const void* gate_raw, const f
 
 extern "C" int64_t cdssm_dynamics_fused_bwd_workspace_bytes(int64_t B, int64_t L, int64_t H) {
   if (B <= 0 || L <= 0 || H <= 0) return -1;
-  return B * L * H * int64_t(sizeof(float));
+  return (B * L + kHeadSlabs) * H * int64_t(sizeof(float));  // the per-token terms, then the slab sums
 }
 
 extern "C" int cdssm_dynamics_fused_bwd(int dtype, const void* grad_A_bar, const void* grad_vp_scale,
@@ -373,8 +389,13 @@ extern "C" int cdssm_dynamics_fused_bwd(int dtype, const void* grad_A_bar, const
                        total);
   st = cdssm_host::check_launch(op);
   if (st) return st;
-  hipLaunchKernelGGL(head_sum_kernel, dim3(unsigned(H)), dim3(256), 0, stream, (const float*)workspace,
-                     grad_log_dt_scale, B * L, int(H));
+  float* part = workspace + B * L * H;
+  hipLaunchKernelGGL(head_part_kernel, dim3(unsigned(H), unsigned(kHeadSlabs)), dim3(256), 0, stream,
+                     (const float*)workspace, part, B * L, int(H));
+  st = cdssm_host::check_launch(op);
+  if (st) return st;
+  hipLaunchKernelGGL(head_sum_kernel, dim3(unsigned((H + 255) / 256)), dim3(256), 0, stream, (const float*)part,
+                     grad_log_dt_scale, int(H));
   return cdssm_host::check_launch(op);
 }
 
