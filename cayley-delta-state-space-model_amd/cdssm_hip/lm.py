@@ -415,6 +415,7 @@ class TokenLinearFn(torch.autograd.Function):
             y = padded_linear(x2, weight, bias)
         ctx.save_for_backward(x2, weight)
         ctx.xshape, ctx.has_bias = x.shape, bias is not None
+        ctx.bias_dtype = None if bias is None else bias.dtype
         return y.view(*x.shape[:-1], O)
 
     @staticmethod
@@ -427,7 +428,7 @@ class TokenLinearFn(torch.autograd.Function):
         if ctx.needs_input_grad[1]:
             dw = _weight_grad(g2, x2, w.dtype)
         if ctx.has_bias and ctx.needs_input_grad[2]:
-            db = column_sum(g2)
+            db = column_sum(g2).to(ctx.bias_dtype)
         return dx, dw, db, (gy if ctx.needs_input_grad[3] else None)
 
 
