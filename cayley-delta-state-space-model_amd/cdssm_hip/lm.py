@@ -407,6 +407,8 @@ class TokenLinearFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, weight, bias, residual):
+        if bias is not None and residual is not None:
+            raise ValueError("TokenLinearFn: a bias and a residual are not taken together")
         O = weight.shape[0]
         x2 = x.reshape(-1, x.shape[-1])
         if residual is not None:

@@ -179,6 +179,7 @@ SHORTCUT_CASES = [
     ("fp32_N16", 2, 200, 3, 64, 16, torch.float32),
     ("bf16_N16", 2, 640, 4, 64, 16, torch.bfloat16),
     ("bf16_N6_D128", 1, 300, 2, 128, 6, torch.bfloat16),
+    ("bf16_N16_ragged_L", 2, 333, 3, 64, 16, torch.bfloat16),
 ]
 
 

@@ -78,12 +78,14 @@ def test_padded_linear_matches_linear_fp64_cpu(O, bias):
     ("in_proj_bf16", 3328, 1024, True, False, torch.bfloat16),
     ("in_proj_state2_padded_bf16", 3104, 1024, True, False, torch.bfloat16),
     ("out_proj_fp32", 1024, 1024, False, True, torch.float32),
+    ("odd_tokens_single_product_bf16", 1024, 1024, True, False, torch.bfloat16),
 ])
 def test_token_linear_gpu_matches_fp64(name, O, I, bias, residual, dtype):
     from cdssm_hip.lm import _wgrad_slabs
-    B, L = 8, 2048
-    assert _wgrad_slabs(B * L, O, I) == (8 if O * I <= 1 << 20 else 2)
-    log(f"[token linear gpu] {name}: T{B * L} {O}x{I}")
+    B, L = (8, 2048) if not name.startswith("odd") else (3, 2731)  # 8193 tokens: one product, no slabs
+    want_slabs = 1 if name.startswith("odd") else (8 if O * I <= 1 << 20 else 2)
+    assert _wgrad_slabs(B * L, O, I) == want_slabs
+    log(f"[token linear gpu] {name}: T{B * L} {O}x{I} slabs {want_slabs}")
     x, w, b, r, g = draw(B, L, O, I, bias, residual, dtype, DEV, seed=1)
     got = run_fn(x, w, b, r, g)
     again = run_fn(x, w, b, r, g)
@@ -127,3 +129,10 @@ def test_column_sum_matches_fp64(name, T, C, ld, off, dtype):
     err = rel(a, x.double().sum(0))
     log(f"   rel err {err:.1e}")
     assert err <= (2.0 ** -8 if dtype == torch.bfloat16 else 1e-6)
+
+
+def test_token_linear_rejects_bias_with_residual():
+    from cdssm_hip.lm import TokenLinearFn
+    x, w = torch.randn(2, 3, 4, dtype=torch.float64), torch.randn(5, 4, dtype=torch.float64)
+    with pytest.raises(ValueError):
+        TokenLinearFn.apply(x, w, torch.zeros(5, dtype=torch.float64), torch.zeros(2, 3, 5, dtype=torch.float64))
