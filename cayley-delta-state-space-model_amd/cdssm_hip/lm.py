@@ -382,8 +382,8 @@ def column_sum(x: Tensor) -> Tensor:
     """x (T, C) -> sum over T (C,) in x's dtype: fp32 accumulation in a fixed order, one rounding
     (cdssm_col_sum) where the HIP kernel serves the layout (CUDA bf16 / fp32, unit column stride, C and the
     row stride multiples of the 16-byte vector, 16-byte aligned); otherwise ``x.sum(0)``.  torch's reduction
-    over the token dimension of a narrow matrix is slow on MI355X (gate_proj's 16384 x 336 bias gradient:
-    19 us, against 4-5 us for the HIP kernel)."""
+    over the token dimension is slow on MI355X for these shapes (gate_proj's 16384 x 336 bias gradient: 19 us,
+    in_proj's 16384 x 3328: 37 us; the two HIP launches: 13 and 24 us)."""
     T_, C = x.shape
     nv = 16 // x.element_size()
     if not (x.is_cuda and x.dtype in (torch.bfloat16, torch.float32) and x.stride(1) == 1 and C % nv == 0
@@ -401,9 +401,9 @@ def column_sum(x: Tensor) -> Tensor:
 class TokenLinearFn(torch.autograd.Function):
     """x @ weight^T (+ bias) (+ residual) over (..., in) token rows -- nn.Linear plus the block's residual
     add (block.py:229) -- whose weight gradient is split over token slabs (``_weight_grad``) and whose bias
-    gradient is ``column_sum``.  The residual
-    enters the GEMM's epilogue (one rounding of the sum, as the inference forward's out_proj); its gradient
-    is the output's.  bias and residual are not both given."""
+    gradient is ``column_sum``; wide outputs are computed with padded features (``padded_linear``).  The
+    residual enters the GEMM's epilogue (one rounding of the sum, as the inference forward's out_proj); its
+    gradient is the output's.  A bias and a residual are not taken together."""
 
     @staticmethod
     def forward(ctx, x, weight, bias, residual):
