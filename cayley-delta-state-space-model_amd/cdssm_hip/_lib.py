@@ -157,7 +157,16 @@ def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device: torch.device) -> int:
+    """The current HIP stream of ``device`` as an integer handle (torch's raw-stream query where this build
+    has it: 0.05 us against 1.9 us for current_stream(device).cuda_stream on the MI355X boxes' hosts, and a
+    training step makes some thirty of these calls)."""
+    if _raw_stream is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 
